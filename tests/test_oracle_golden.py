@@ -1,0 +1,118 @@
+"""Pins the CPU oracle against golden fixtures written from the reference (tests/golden/make_golden.py).
+
+Stage-wise: each stage of the oracle runs on the reference's own upstream tensors, so integer outputs (bucket ids,
+sorted orders, n-gram keys, their order, repeated flags, seen flags) must be bit-exact and floating-point ones must
+agree to rounding. Whole layer: forward and every gradient."""
+import pytest
+import torch
+
+from oracle import layer as O
+from tests import fixtures
+
+CASES = fixtures.names()
+
+
+def close(a, b, rel, what):
+    a, b = a.double(), b.double()
+    scale = b.abs().max().item() + 1e-6
+    err = (a - b).abs().max().item() if a.numel() else 0.0
+    assert err <= rel * scale, f'{what}: max err {err:.3g} vs scale {scale:.3g}'
+
+
+@pytest.mark.parametrize('name', CASES)
+def test_bucket_ids_and_order_bit_exact(name):
+    g, p, m = fixtures.load(name)
+    sh = fixtures.shape_of(p, m)
+    ids, order = O.bucket_rows(g['phi'], sh.T, sh.nb)
+    assert torch.equal(ids, g['ids'])
+    assert torch.equal(order, g['orden'])
+
+
+@pytest.mark.parametrize('name', CASES)
+def test_producers(name):
+    g, p, m = fixtures.load(name)
+    sh = fixtures.shape_of(p, m)
+    phi, V = O.phi_and_values(p, g['E'])
+    close(phi, g['phi'], 1e-6, 'phi')
+    close(V, g['V'], 1e-6, 'V')
+    Qc, Kc, beta, la = O.context(p, g['h'], sh, O.Prot())
+    for a, k in ((Qc, 'Qc'), (Kc, 'Kc'), (beta, 'beta'), (la, 'log_alfa')):
+        close(a, g[k], 1e-6, k)
+    assert beta.dtype == torch.float64
+
+
+@pytest.mark.parametrize('name', CASES)
+def test_candidate_stage_forward_and_gradients(name):
+    g, p, m = fixtures.load(name)
+    sh = fixtures.shape_of(p, m)
+    leaves = {k: g[k].clone().requires_grad_() for k in ('phi', 'V', 'Qc', 'Kc', 'Bt', 'log_alfa')}
+    w = p['w_sufijo'].clone().requires_grad_()
+    gam = p['gamma'].clone().requires_grad_()
+    salida, sen = O.candidates(leaves['phi'], leaves['V'], leaves['Qc'], leaves['Kc'], leaves['Bt'],
+                               leaves['log_alfa'], g['sig'], w, gam, sh)
+    acc = O.gate_signals(salida, sen, sh.T, sh.Tc)
+    for k in ('salida', 'pico'):
+        close(acc[k], g['acc.' + k], 1e-5, k)
+    for k in ('peso_total', 'peso_ctx'):
+        assert torch.equal(acc[k], g['acc.' + k]), k
+    close(acc['mejor'], g['acc.mejor'], 1e-5, 'mejor')
+    (salida * g['acc.gs']).sum().backward()
+    for k, t in leaves.items():
+        close(t.grad, g['acc.g_' + k], 1e-4, 'grad ' + k)
+    close(w.grad, g['acc.g_w_sufijo'], 1e-4, 'grad w_sufijo')
+    close(gam.grad, g['acc.g_gamma'], 1e-4, 'grad gamma')
+
+
+@pytest.mark.parametrize('name', CASES)
+def test_ngram_keys_order_and_flags_bit_exact(name):
+    g, p, m = fixtures.load(name)
+    sh = fixtures.shape_of(p, m)
+    keys = O.ngram_keys(g['sig'], p['c_vistos'], sh.n)
+    ref = g['claves']
+    assert torch.equal(torch.isnan(keys), torch.isnan(ref))
+    assert torch.equal(torch.nan_to_num(keys, nan=-7.0), torch.nan_to_num(ref, nan=-7.0))
+    order, rep = O.ngram_sort(keys)
+    assert torch.equal(order, g['orden_k'])
+    assert torch.equal(rep, g['repetido'].bool())
+
+
+@pytest.mark.parametrize('name', CASES)
+def test_repetition_stage_forward_and_gradients(name):
+    g, p, m = fixtures.load(name)
+    sh = fixtures.shape_of(p, m)
+    rl = {k: g[k].clone().requires_grad_() for k in ('beta', 'Bt', 'log_alfa')}
+    pp = dict(p)
+    pp['log_kappa'] = p['log_kappa'].clone().requires_grad_()
+    pp['log_kappa_racha'] = p['log_kappa_racha'].clone().requires_grad_()
+    r = O.repetition(pp, g['sig'], rl['beta'], rl['Bt'], rl['log_alfa'], sh, O.Prot())
+    assert torch.equal(r['vistos'], g['rep.vistos'])
+    if 'corrimiento' not in m['extra']:                          # with huge clock steps exp(-kappa dB) underflows
+        assert torch.equal(r['hawkes'] > 0, g['rep.vistos'] > 0)
+    close(r['hawkes'], g['rep.hawkes'], 1e-5, 'hawkes')
+    if m['extra'].get('kappa_r_zero'):
+        assert torch.equal(r['racha'], g['rep.racha'])            # integer run lengths: bit-exact
+    else:
+        close(r['racha'], g['rep.racha'], 1e-5, 'racha')
+    ((r['hawkes'] * g['rep.gh']).sum() + (r['racha'] * g['rep.gr']).sum()).backward()
+    for k, t in rl.items():
+        close(t.grad, g['rep.g_' + k], 1e-4, 'grad ' + k)
+    close(pp['log_kappa'].grad, g['rep.g_log_kappa'], 1e-4, 'grad log_kappa')
+    close(pp['log_kappa_racha'].grad, g['rep.g_log_kappa_racha'], 1e-4, 'grad log_kappa_racha')
+
+
+@pytest.mark.parametrize('name', CASES)
+def test_whole_layer_forward_and_gradients(name):
+    g, p, m = fixtures.load(name)
+    sh = fixtures.shape_of(p, m)
+    pp = {k: (v.clone().requires_grad_() if v.is_floating_point() and not k.startswith(('pot', 'c_vistos', 'r_firma'))
+              else v) for k, v in p.items()}
+    E, h = g['E'].clone().requires_grad_(), g['h'].clone().requires_grad_()
+    y = O.layer_forward(pp, E, h, g['x'], sh)
+    close(y, g['y'], 1e-5, 'y')
+    (y * g['gy']).sum().backward()
+    close(E.grad, g['gE'], 1e-4, 'grad E')
+    close(h.grad, g['gh'], 1e-4, 'grad h')
+    for k, t in pp.items():
+        if ('g.' + k) in g:
+            assert t.grad is not None, k
+            close(t.grad, g['g.' + k], 1e-4, 'grad ' + k)
