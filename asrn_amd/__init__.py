@@ -1,0 +1,14 @@
+"""asrn_amd: the ASRN layer's data-parallel hot path, MI355X-native (HIP kernels for gfx950 behind a C ABI).
+
+The public names mirror the reference package (KIROKOWA/ASRN, asrn/__init__.py:83-97) for the layer this build
+replaces: ASRNLayer / CapaASRNEstable, Protecciones / Protections, firmas_de_piezas and escaneo.
+"""
+from . import ops, synth
+from ._lib import ASRNHipError, LIB_PATH, load
+from .capa import ASRNLayer, CapaASRNEstable, Protecciones, Protections, firmas_de_piezas
+from .ops import escaneo
+
+__version__ = '0.1.0'
+
+__all__ = ['ASRNLayer', 'CapaASRNEstable', 'Protecciones', 'Protections', 'firmas_de_piezas', 'escaneo', 'ops',
+           'load', 'LIB_PATH', 'ASRNHipError', '__version__']

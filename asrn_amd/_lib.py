@@ -1,0 +1,80 @@
+"""Loads libasrn_hip.so (the C ABI declared in include/asrn_hip.h) and calls it with torch device tensors.
+
+torch is imported first so the HIP runtime the library links against is the one torch already loaded (both carry
+the soname libamdhip64.so.7): kernels and torch tensors then share one runtime, one device context and its streams.
+"""
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, 'libasrn_hip.so')
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_F32 = ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/asrn_hip.h
+SIGNATURES = {
+    'asrn_hip_last_error': (ctypes.c_char_p, []),
+    'asrn_hip_abi_version': (_I32, []),
+    'asrn_bucket_sort': (ctypes.c_int, [_P, _I64, _I64, _I32, _I32, _I64, _P, _P, _P, _P, _P]),
+    'asrn_candidates_fwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7 + [_F32, _F32] + [_P] * 4),
+    'asrn_candidate_lists': (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P]),
+    'asrn_candidates_bwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7 + [_F32, _F32] + [_P] * 11),
+    'asrn_clock_scan': (ctypes.c_int, [_P, _P, _I64, _I64, _I32, _P]),
+    'asrn_ngram_sort_workspace': (_I64, [_I64, _I64, _I32]),
+    'asrn_ngram_sort': (ctypes.c_int, [_P, _P, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _I64, _P]),
+    'asrn_scan_fwd': (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P]),
+    'asrn_scan_bwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _P]),
+    'asrn_hawkes_fwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P]),
+    'asrn_hawkes_bwd_workspace': (_I64, [_I64, _I64, _I32]),
+    'asrn_hawkes_bwd': (ctypes.c_int, [_P] * 8 + [_I64, _I64, _I32] + [_P] * 4 + [_I64, _P]),
+    'asrn_streak_fwd': (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I32, _P, _P]),
+    'asrn_streak_bwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P]),
+}
+
+_lib = None
+
+
+class ASRNHipError(RuntimeError):
+    pass
+
+
+def load(path=LIB_PATH):
+    """Opens the library once (raises if it is missing: the product has no CPU fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ASRNHipError(f'{path} is missing: build it with `python -m asrn_amd.build` (hipcc, gfx950)')
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def call(name, *args):
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        raise ASRNHipError(f'{name}: {lib.asrn_hip_last_error().decode(errors="replace")}')
+    return rc
+
+
+def query(name, *args):
+    return getattr(load(), name)(*args)

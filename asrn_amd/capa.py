@@ -1,0 +1,231 @@
+"""CapaASRNEstable on MI355X: the reference's stable ASRN layer with its hot path on HIP kernels.
+
+Same constructor arguments, parameter and buffer names, construction order (so the same seed gives the same weights)
+and forward contract as asrn.estable.CapaASRNEstable (asrn/estable.py:141-421, inheriting asrn/nucleo.py:574-886):
+forward(E (B, L, d), h (B, L, d), piezas (B, L) int64 | None) -> h' (B, L, d). The dense projections (hash MLPs, V,
+LayerNorm, Qc/Kc, the clock projection, the gate and W_o) stay PyTorch GEMMs; the bucket sort, the candidate
+attention forward and backward, the n-gram sort, the clock, Hawkes and streak scans run in libasrn_hip.so. There is
+no CPU path: CPU tensors or unsupported shapes raise.
+"""
+import dataclasses
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+
+PROHIBIDO = -1e9          # the "not allowed" score (asrn/nucleo.py:86)
+
+
+@dataclasses.dataclass(frozen=True)
+class Protecciones:
+    """Numerical protections (asrn/estable.py:57-77). Protecciones() = group A, the default of asrn.ASRNLayer."""
+    mascara_exacta: bool = True
+    reloj_64: bool = True
+    beta_max: float = 1e4
+    log_alfa_min: float = -30.0
+    mejor_max: float = 1e4
+    tope_puerta: float = None
+    kappa_min: float = None
+
+    @classmethod
+    def ninguna(cls):
+        return cls(mascara_exacta=False, reloj_64=False, beta_max=None, log_alfa_min=None, mejor_max=None)
+
+    @classmethod
+    def textos_largos(cls, largo_entrenamiento=1024):
+        return cls(tope_puerta=10.0, kappa_min=1.0 / (4 * largo_entrenamiento))
+
+
+Protections = Protecciones
+
+
+def firmas_de_piezas(piezas):
+    """Token signature = its id in fp32, exact for ids < 2**24 (asrn/nucleo.py:161-164)."""
+    return piezas.to(torch.float32)
+
+
+class CapaASRNEstable(nn.Module):
+    """The ASRN layer with group-A protections (asrn.ASRNLayer). See the module docstring."""
+
+    def __init__(self, d, protecciones=None, n_tablas=8, n_bits=14, afin_oculto=128, chunk=32, tablas_contexto=4,
+                 confirmar=16, sufijo=4, vistos=4, dropout=0.0, nodos_racha=16, racha_max=256):
+        super().__init__()
+        assert 0 < tablas_contexto < n_tablas and nodos_racha >= 2
+        self.n_tablas, self.n_bits, self.chunk = n_tablas, n_bits, chunk
+        self.tablas_contexto, self.confirmar, self.sufijo, self.vistos = tablas_contexto, confirmar, sufijo, vistos
+        # construction order = the reference's (asrn/nucleo.py:591-630): it fixes the weights a seed produces
+        mitad = max(8, afin_oculto // 2)
+        self.afin_palabra = nn.Sequential(nn.Linear(d, mitad), nn.GELU(),
+                                          nn.Linear(mitad, (n_tablas - tablas_contexto) * n_bits))
+        self.afin_contexto = nn.Sequential(nn.Linear(2 * d, mitad), nn.GELU(),
+                                           nn.Linear(mitad, tablas_contexto * n_bits))
+        self.v = nn.Linear(d, d, bias=False)
+        self.o = nn.Linear(d, d, bias=False)
+        self.g = nn.Linear(d, 1)
+        self.temperatura = (n_tablas * n_bits) ** 0.5
+        self.register_buffer('pot', 2 ** torch.arange(n_bits))
+        self.g_conf = nn.Linear(4, 1)
+        nn.init.zeros_(self.g_conf.weight)
+        nn.init.zeros_(self.g_conf.bias)
+        self.cq = nn.Linear(d, confirmar, bias=False)
+        nn.init.zeros_(self.cq.weight)
+        self.ck = nn.Linear(d, confirmar, bias=False)
+        self.ln_ctx = nn.LayerNorm(d)
+        self.w_vistos = nn.Parameter(torch.zeros(vistos))
+        g_v = torch.Generator().manual_seed(12345)
+        self.register_buffer('c_vistos', torch.rand(vistos, generator=g_v, dtype=torch.float64) + 0.5)
+        self.w_sufijo = nn.Parameter(torch.zeros(sufijo + 1))
+        self.register_buffer('r_firma', torch.randn(d))
+        self.drop = nn.Dropout(dropout)
+        self.w_reloj = nn.Parameter(torch.zeros(2, d))
+        self.b_reloj = nn.Parameter(torch.tensor([math.log(math.e - 1), 0.0]))
+        self.gamma = nn.Parameter(torch.zeros(n_tablas))
+        self.log_kappa = nn.Parameter(-torch.log(chunk * 4.0 ** torch.arange(vistos)))
+        self.log_kappa_racha = nn.Parameter(torch.tensor([-math.log(8.0 * chunk)]))
+        self.u_hawkes = nn.Parameter(torch.zeros(vistos))
+        self.racha_paso = math.log1p(racha_max) / (nodos_racha - 1)
+        self.d_racha = nn.Parameter(torch.zeros(nodos_racha))
+        self.protecciones = protecciones or Protecciones()
+
+    # --- checks -----------------------------------------------------------------------------------------------------
+
+    def _revisar(self, E):
+        p = self.protecciones
+        if not E.is_cuda:
+            raise RuntimeError('asrn_amd.ASRNLayer runs on the GPU only (HIP kernels for gfx950): move the layer and '
+                               'its inputs to a cuda device')
+        if not (p.mascara_exacta and p.reloj_64):
+            raise ValueError('asrn_amd.ASRNLayer implements the protected layer (exact mask and 64-bit clock); '
+                             'Protecciones.ninguna() is not supported')
+        if not 1 <= self.n_bits <= 14:
+            raise ValueError(f'n_bits={self.n_bits}: the HIP bucket sort supports 1..14 bits per table')
+        if not 1 <= self.chunk <= 64:
+            raise ValueError(f'chunk={self.chunk}: the HIP candidate kernels support 1..64 candidates per table')
+        d = E.shape[-1]
+        if d % 4 or d > 1024:
+            raise ValueError(f'd={d}: the HIP candidate kernels need d % 4 == 0 and d <= 1024')
+        if self.n_tablas * self.n_bits + self.confirmar > 256 or self.sufijo > 16 or self.n_tablas > 32:
+            raise ValueError('n_tablas*n_bits + confirmar must be <= 256, sufijo <= 16, n_tablas <= 32')
+
+    # --- producers (PyTorch GEMMs, asrn/nucleo.py:634-664 and asrn/estable.py:153-194) --------------------------------
+
+    def _firma(self, E):
+        with torch.autocast(device_type=E.device.type, enabled=False):
+            return E.float() @ self.r_firma.float()
+
+    def _phi(self, E):
+        llave = torch.cat([E, F.pad(E, (0, 0, 1, 0))[:, :E.shape[1]]], dim=-1)
+        return torch.cat([self.afin_palabra(E), self.afin_contexto(llave)], dim=-1)
+
+    def _phi_y_valores(self, E):
+        d, L = E.shape[-1], E.shape[1]
+        pal = self.afin_palabra
+        m = pal[0].out_features
+        E = _a_autocast(E)
+        y = F.linear(E, torch.cat([pal[0].weight, self.v.weight]), F.pad(pal[0].bias, (0, d)))
+        hp, v = y.split([m, d], dim=-1)
+        llave = torch.cat([E, F.pad(E, (0, 0, 1, 0))[:, :L]], dim=-1)
+        phi = torch.cat([pal[2](pal[1](hp)), self.afin_contexto(llave)], dim=-1)
+        return phi, F.pad(v, (0, 0, 0, 1))[:, 1:]
+
+    def _contexto(self, h):
+        """Qc, Kc (B, L, cf), beta (B, L) fp64 and log_alfa (B, L) (the GPU branch of asrn/estable.py:171-175: the
+        clock projection in true fp32, elementwise, immune to reduced-precision matmuls)."""
+        p = self.protecciones
+        hh32 = self.ln_ctx(h)
+        hh = _a_autocast(hh32)
+        cf = self.confirmar
+        y = F.linear(hh, torch.cat([self.cq.weight, self.ck.weight]))
+        x32 = hh32.float()
+        u = torch.stack([(x32 * self.w_reloj[i].float()).sum(-1) for i in range(2)], -1) + self.b_reloj.float()
+        beta = F.softplus(u[..., 0])
+        log_alfa = F.logsigmoid(u[..., 1]) + math.log(2)
+        if p.beta_max is not None:
+            beta = beta.clamp(max=p.beta_max)
+        if p.log_alfa_min is not None:
+            log_alfa = log_alfa.clamp(min=p.log_alfa_min)
+        return y[..., :cf], y[..., cf:2 * cf], beta.double(), log_alfa
+
+    def _kappas(self):
+        k, kr = self.log_kappa.exp(), self.log_kappa_racha.exp()
+        m = self.protecciones.kappa_min
+        return (k, kr) if m is None else (k.clamp(min=m), kr.clamp(min=m))
+
+    # --- hot path (HIP) ---------------------------------------------------------------------------------------------
+
+    def _acumular(self, E, Qc, Kc, Bt, log_alfa, sig):
+        """Candidate attention of all tables -> salida and the gate signals (asrn/estable.py:204-300)."""
+        T = self.n_tablas
+        phi, V = self._phi_y_valores(E)
+        _, order, ids_s, rank = ops.bucket_sort(phi.detach(), T, self.n_bits)
+        shape = dict(T=T, Tc=self.tablas_contexto, C=self.chunk, K=self.sufijo)
+        salida, sen = ops.Candidates.apply(phi, V, Qc, Kc, Bt, log_alfa, self.w_sufijo, self.gamma, sig, order,
+                                           ids_s, rank, shape)
+        return {'salida': salida, 'peso_total': sen[..., 0:1], 'mejor': sen[..., 1:2], 'pico': sen[..., 2:3],
+                'peso_ctx': sen[..., 3:4]}
+
+    def _repeticion(self, sig, beta, Bt, log_alfa):
+        """vistos, hawkes (B, L, n) and racha (B, L) (asrn/estable.py:304-321)."""
+        kappa, kappa_r = self._kappas()
+        with torch.no_grad():
+            _, order, rep, rank_k, vistos = ops.ngram_sort(sig, self.c_vistos, self.vistos)
+        hawkes = ops.Hawkes.apply(Bt, log_alfa, kappa, order, rep, rank_k)
+        racha = ops.Streak.apply(beta, kappa_r, vistos)
+        return {'vistos': vistos, 'hawkes': hawkes, 'racha': racha}
+
+    # --- gate (PyTorch, asrn/estable.py:376-403 and asrn/nucleo.py:865-878) ------------------------------------------
+
+    @property
+    def u_racha(self):
+        return self.d_racha.cumsum(0)
+
+    def _respuesta_racha(self, racha):
+        x = (torch.log1p(racha) / self.racha_paso).clamp(max=self.d_racha.shape[0] - 1)
+        i = torch.nan_to_num(x.detach(), nan=0.0).floor().long().clamp(0, self.d_racha.shape[0] - 2)
+        return self.u_racha[i] + (x - i) * self.d_racha[1:][i]
+
+    def _combinar(self, acc, h):
+        p = self.protecciones
+        salida, pt = acc['salida'], acc['peso_total'].detach()
+        salida = salida / acc['peso_total'].clamp(min=1)
+        mejor = torch.where(pt > 0, acc['mejor'], torch.zeros_like(pt))
+        if p.mejor_max is not None:
+            mejor = mejor.clamp(-p.mejor_max, p.mejor_max)
+        senales = torch.cat([pt / self.n_tablas, mejor, acc['pico'] / pt.clamp(min=1),
+                             acc['peso_ctx'].detach() / self.tablas_contexto], dim=-1)
+        with torch.autocast(device_type=h.device.type, enabled=False):
+            logit = F.linear(h, self.g.weight.to(h.dtype), self.g.bias.to(h.dtype))
+        logit = logit + self.g_conf(senales).to(logit.dtype)
+        logit = logit + (acc['vistos'].to(logit.dtype) * self.w_vistos.to(logit.dtype)).sum(-1, keepdim=True)
+        hawkes = torch.log1p(acc['hawkes']).to(logit.dtype)
+        logit = logit + (hawkes * self.u_hawkes.to(logit.dtype)).sum(-1, keepdim=True)
+        logit = logit + self._respuesta_racha(acc['racha']).unsqueeze(-1).to(logit.dtype)
+        if p.tope_puerta is not None:
+            logit = p.tope_puerta * torch.tanh(logit / p.tope_puerta)
+        aporte = self.o(salida)
+        return h + torch.sigmoid(logit).to(aporte.dtype) * self.drop(aporte)
+
+    # --- all together -----------------------------------------------------------------------------------------------
+
+    def forward(self, E, h, piezas=None):
+        """E (B, L, d), h (B, L, d), piezas (B, L) or None -> h' (B, L, d) (asrn/estable.py:407-421)."""
+        self._revisar(E)
+        sig = self._firma(E) if piezas is None else firmas_de_piezas(piezas)
+        Qc, Kc, beta, log_alfa = self._contexto(h)
+        Bt = ops.ClockScan.apply(beta)
+        acc = self._acumular(E, Qc, Kc, Bt, log_alfa, sig)
+        acc.update(self._repeticion(sig, beta, Bt, log_alfa))
+        return self._combinar(acc, h)
+
+
+def _a_autocast(x):
+    disp = x.device.type
+    if torch.is_autocast_enabled(disp) and x.is_floating_point():
+        return x.to(torch.get_autocast_dtype(disp))
+    return x
+
+
+ASRNLayer = CapaASRNEstable

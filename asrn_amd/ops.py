@@ -1,0 +1,255 @@
+"""torch.autograd wrappers around the HIP entry points (include/asrn_hip.h).
+
+Every op takes device tensors, allocates its outputs and workspaces with torch's caching allocator, and launches on
+torch's current stream. They replace the reference's fused-op layer: _CasillerosTriton (asrn/nucleo.py:461-515),
+_Escaneo / escaneo (asrn/nucleo.py:188-196, 518-537), the stable argsorts (asrn/estable.py:283, nucleo:693-701) and
+the clock cumsum (asrn/estable.py:418).
+"""
+import torch
+
+from . import _lib
+from ._lib import call, ptr, query, stream_of
+
+I32 = torch.int32
+
+
+def _dev(*ts):
+    for t in ts:
+        if not t.is_cuda:
+            raise RuntimeError('asrn_amd runs on the GPU only: got a CPU tensor (move the layer and inputs to cuda)')
+    return ts[0].device
+
+
+def _c(t, dtype=None):
+    if dtype is not None and t.dtype != dtype:
+        t = t.to(dtype)
+    return t.contiguous()
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a1 + a2
+# ---------------------------------------------------------------------------------------------------------------------
+
+def bucket_sort(phi, T, nb):
+    """phi (B, L, P) fp32 -> ids (B*T, L), order (B*T, L), ids_sorted (B*T, L), rank (B, L, T), all int32."""
+    dev = _dev(phi)
+    phi = _c(phi, torch.float32)
+    B, L, P = phi.shape
+    ids = torch.empty((B * T, L), dtype=I32, device=dev)
+    order = torch.zeros_like(ids)          # zero-filled: every index a later kernel reads is in range
+    ids_s = torch.zeros_like(ids)
+    rank = torch.zeros((B, L, T), dtype=I32, device=dev)
+    call('asrn_bucket_sort', ptr(phi), B, L, T, nb, P, ptr(ids), ptr(order), ptr(ids_s), ptr(rank), stream_of(dev))
+    return ids, order, ids_s, rank
+
+
+def candidate_lists(sig, order, ids_s, rank, C, K):
+    """The candidate windows the kernels walk: pos, ell (B, L, T, C) int32, -1 where a slot is empty."""
+    dev = _dev(sig)
+    B, L, T = rank.shape
+    pos = torch.empty((B, L, T, C), dtype=I32, device=dev)
+    ell = torch.empty_like(pos)
+    call('asrn_candidate_lists', ptr(_c(sig, torch.float32)), ptr(order), ptr(ids_s), ptr(rank), B, L, T, C, K,
+         ptr(pos), ptr(ell), stream_of(dev))
+    return pos, ell
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a10
+# ---------------------------------------------------------------------------------------------------------------------
+
+def ngram_sort(sig, coef, n):
+    """sig (B, L) fp32, coef (n,) fp64 -> keys (B, L, n) fp64, order (B, n, L) int32, repeated (B, n, L) uint8,
+    rank_k (B, n, L) int32, vistos (B, L, n) fp32."""
+    dev = _dev(sig)
+    sig = _c(sig, torch.float32)
+    coef = _c(coef, torch.float64)
+    B, L = sig.shape
+    keys = torch.empty((B, L, n), dtype=torch.float64, device=dev)
+    order = torch.empty((B, n, L), dtype=I32, device=dev)
+    rep = torch.empty((B, n, L), dtype=torch.uint8, device=dev)
+    rank_k = torch.zeros((B, n, L), dtype=I32, device=dev)   # zero-filled: every index read later is in range
+    vistos = torch.zeros((B, L, n), dtype=torch.float32, device=dev)
+    wsb = query('asrn_ngram_sort_workspace', B, L, n)
+    ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+    call('asrn_ngram_sort', ptr(sig), ptr(coef), B, L, n, ptr(keys), ptr(order), ptr(rep), ptr(rank_k), ptr(vistos),
+         ptr(ws), wsb, stream_of(dev))
+    return keys, order, rep, rank_k, vistos
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a9
+# ---------------------------------------------------------------------------------------------------------------------
+
+class ClockScan(torch.autograd.Function):
+    """Bt = cumsum(beta, 1) in fp64; the backward is the suffix sum."""
+
+    @staticmethod
+    def forward(ctx, beta):
+        dev = _dev(beta)
+        x = _c(beta, torch.float64)
+        y = torch.empty_like(x)
+        call('asrn_clock_scan', ptr(x), ptr(y), x.shape[0], x.shape[1], 0, stream_of(dev))
+        return y
+
+    @staticmethod
+    def backward(ctx, g):
+        g = _c(g, torch.float64)
+        out = torch.empty_like(g)
+        call('asrn_clock_scan', ptr(g), ptr(out), g.shape[0], g.shape[1], 1, stream_of(g.device))
+        return out
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a12
+# ---------------------------------------------------------------------------------------------------------------------
+
+class AffineScan(torch.autograd.Function):
+    """S_i = a_i S_{i-1} + b_i over the last axis in fp32 (the reference's escaneo, asrn/nucleo.py:188-196)."""
+
+    @staticmethod
+    def forward(ctx, a, b):
+        dev = _dev(a, b)
+        a, b = torch.broadcast_tensors(a, b)
+        shape = a.shape
+        N = shape[-1]
+        a2, b2 = _c(a, torch.float32).reshape(-1, N), _c(b, torch.float32).reshape(-1, N)
+        S = torch.empty_like(a2)
+        call('asrn_scan_fwd', ptr(a2), ptr(b2), ptr(S), a2.shape[0], N, stream_of(dev))
+        ctx.save_for_backward(a2, S)
+        ctx.shape = shape
+        return S.view(shape)
+
+    @staticmethod
+    def backward(ctx, g):
+        a2, S = ctx.saved_tensors
+        N = a2.shape[-1]
+        g2 = _c(g, torch.float32).reshape(-1, N)
+        ga, gb = torch.empty_like(g2), torch.empty_like(g2)
+        call('asrn_scan_bwd', ptr(a2), ptr(S), ptr(g2), ptr(ga), ptr(gb), a2.shape[0], N, stream_of(g.device))
+        return ga.view(ctx.shape), gb.view(ctx.shape)
+
+
+def escaneo(a, b):
+    return AffineScan.apply(a, b)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a11
+# ---------------------------------------------------------------------------------------------------------------------
+
+class Hawkes(torch.autograd.Function):
+    """hawkes (B, L, n) from the clock, log alfa and kappa (n,) along the n-gram key order (asrn/estable.py:313-318).
+    order/repeated/rank_k come from ngram_sort and carry no gradient."""
+
+    @staticmethod
+    def forward(ctx, Bt, log_alfa, kappa, order, rep, rank_k):
+        dev = _dev(Bt)
+        B, n, L = order.shape
+        Bt = _c(Bt, torch.float64)
+        la = _c(log_alfa, torch.float32)
+        kap = _c(kappa, torch.float32)
+        hawkes = torch.empty((B, L, n), dtype=torch.float32, device=dev)
+        S = torch.empty((B, n, L), dtype=torch.float32, device=dev)
+        call('asrn_hawkes_fwd', ptr(order), ptr(rep), ptr(Bt), ptr(la), ptr(kap), B, L, n, ptr(hawkes), ptr(S),
+             stream_of(dev))
+        ctx.save_for_backward(Bt, la, kap, order, rep, rank_k, S)
+        return hawkes
+
+    @staticmethod
+    def backward(ctx, g):
+        Bt, la, kap, order, rep, rank_k, S = ctx.saved_tensors
+        B, n, L = order.shape
+        dev = Bt.device
+        g = _c(g, torch.float32)
+        dBt = torch.empty((B, L), dtype=torch.float64, device=dev)
+        dla = torch.empty((B, L), dtype=torch.float32, device=dev)
+        dk = torch.empty((B, n), dtype=torch.float32, device=dev)
+        wsb = query('asrn_hawkes_bwd_workspace', B, L, n)
+        ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+        call('asrn_hawkes_bwd', ptr(order), ptr(rep), ptr(rank_k), ptr(Bt), ptr(la), ptr(kap), ptr(S), ptr(g), B, L,
+             n, ptr(dBt), ptr(dla), ptr(dk), ptr(ws), wsb, stream_of(dev))
+        return dBt, dla, dk.sum(0), None, None, None
+
+
+class Streak(torch.autograd.Function):
+    """racha (B, L) = scan(r exp(-kappa_r beta), r) with r = vistos[..., n-1] (asrn/estable.py:319-320)."""
+
+    @staticmethod
+    def forward(ctx, beta, kappa_r, vistos):
+        dev = _dev(beta)
+        B, L, n = vistos.shape
+        beta = _c(beta, torch.float64)
+        kr = _c(kappa_r, torch.float32)
+        vistos = _c(vistos, torch.float32)
+        racha = torch.empty((B, L), dtype=torch.float32, device=dev)
+        call('asrn_streak_fwd', ptr(vistos), ptr(beta), ptr(kr), B, L, n, ptr(racha), stream_of(dev))
+        ctx.save_for_backward(vistos, beta, kr, racha)
+        return racha
+
+    @staticmethod
+    def backward(ctx, g):
+        vistos, beta, kr, racha = ctx.saved_tensors
+        B, L, n = vistos.shape
+        dev = beta.device
+        g = _c(g, torch.float32)
+        dbeta = torch.empty((B, L), dtype=torch.float64, device=dev)
+        dkr = torch.empty((B,), dtype=torch.float32, device=dev)
+        call('asrn_streak_bwd', ptr(vistos), ptr(beta), ptr(kr), ptr(racha), ptr(g), B, L, n, ptr(dbeta), ptr(dkr),
+             stream_of(dev))
+        return dbeta, dkr.sum().reshape(1), None
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a3 - a8
+# ---------------------------------------------------------------------------------------------------------------------
+
+class Candidates(torch.autograd.Function):
+    """Candidate attention of all tables (the drop-in for _CasillerosTriton, asrn/nucleo.py:461-515). Returns salida
+    (B, L, d) and the gate signals (B, L, 4) = (peso_total, mejor, pico, peso_ctx), the latter without gradient.
+    Saves only its inputs and the per-(query, table) softmax statistics."""
+
+    @staticmethod
+    def forward(ctx, phi, V, Qc, Kc, Bt, log_alfa, w_suf, gamma, sig, order, ids_s, rank, shape):
+        T, Tc, C, K = shape['T'], shape['Tc'], shape['C'], shape['K']
+        dev = _dev(phi, V)
+        B, L, P = phi.shape
+        d, cf = V.shape[-1], Qc.shape[-1]
+        ins = dict(phi=_c(phi, torch.float32), V=_c(V, torch.float32), Qc=_c(Qc, torch.float32),
+                   Kc=_c(Kc, torch.float32), sig=_c(sig, torch.float32), Bt=_c(Bt, torch.float64),
+                   la=_c(log_alfa, torch.float32), w=_c(w_suf.detach(), torch.float32),
+                   g=_c(gamma.detach(), torch.float32))
+        salida = torch.empty((B, L, d), dtype=torch.float32, device=dev)
+        signals = torch.empty((B, L, 4), dtype=torch.float32, device=dev)
+        stats = torch.empty((B, L, T, 2), dtype=torch.float32, device=dev)
+        sp, sc = float(P) ** -0.5, float(cf) ** -0.5
+        call('asrn_candidates_fwd', ptr(ins['phi']), ptr(ins['V']), ptr(ins['Qc']), ptr(ins['Kc']), ptr(ins['sig']),
+             ptr(ins['Bt']), ptr(ins['la']), ptr(ins['w']), ptr(ins['g']), ptr(order), ptr(ids_s), ptr(rank), B, L, d,
+             P, cf, K, T, Tc, C, sp, sc, ptr(salida), ptr(signals), ptr(stats), stream_of(dev))
+        ctx.save_for_backward(*ins.values(), order, ids_s, rank, stats)
+        ctx.meta = (B, L, P, d, cf, K, T, Tc, C, sp, sc, V.dtype, phi.dtype, Qc.dtype, Kc.dtype, log_alfa.dtype)
+        ctx.mark_non_differentiable(signals)
+        return salida.to(V.dtype), signals
+
+    @staticmethod
+    def backward(ctx, dsal, _dsig):
+        phi, V, Qc, Kc, sig, Bt, la, w, g, order, ids_s, rank, stats = ctx.saved_tensors
+        B, L, P, d, cf, K, T, Tc, C, sp, sc, tv, tp, tq, tk, tl = ctx.meta
+        dev = phi.device
+        dsal = _c(dsal, torch.float32)
+        dphi = torch.empty_like(phi)
+        dV = torch.empty_like(V)
+        dQc = torch.empty_like(Qc)
+        dKc = torch.empty_like(Kc)
+        dBt = torch.empty_like(Bt)
+        dla = torch.empty_like(la)
+        qstats = torch.empty((B, L, T), dtype=torch.float32, device=dev)
+        partials = torch.empty((B * L, T + K + 1), dtype=torch.float32, device=dev)
+        call('asrn_candidates_bwd', ptr(phi), ptr(V), ptr(Qc), ptr(Kc), ptr(sig), ptr(Bt), ptr(la), ptr(w), ptr(g),
+             ptr(order), ptr(ids_s), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ptr(dsal), ptr(stats),
+             ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(qstats), ptr(partials), stream_of(dev))
+        part = partials.sum(0)
+        dgamma = part[:T] / C
+        dw = part[T:]
+        return (dphi.to(tp), dV.to(tv), dQc.to(tq), dKc.to(tk), dBt, dla.to(tl), dw, dgamma, None, None, None, None,
+                None)

@@ -1,0 +1,140 @@
+/* ASRN layer hot path on MI355X (gfx950): C ABI of libasrn_hip.so.
+ *
+ * Conventions for every entry point:
+ *   - device pointers are plain pointers; sizes are int64_t; `stream` is a hipStream_t passed as void*;
+ *   - the return value is 0 on success, nonzero on a rejected argument or a failed launch, with the message in
+ *     asrn_hip_last_error() (per calling thread);
+ *   - the caller owns every buffer (outputs and workspaces); the library never allocates, frees or synchronizes;
+ *   - work is stream-ordered and deterministic: no floating-point atomics, the same inputs give the same bits.
+ *
+ * Layout names: B batch rows, L positions, d width, T hash tables, nb bits per table, P = T*nb hash outputs,
+ * C candidates per table, cf confirmation width, K suffix length, n n-gram orders. A "row" of a per-table array
+ * is r = b*T + tau, as in the reference (estable:282).
+ */
+#ifndef ASRN_HIP_H
+#define ASRN_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Last error message of the calling thread ("" if none). */
+const char* asrn_hip_last_error(void);
+
+/* ABI version of this library (increments on any signature change). */
+int32_t asrn_hip_abi_version(void);
+
+/* ---- a1 + a2: sign hash and stable bucket sort ------------------------------------------------------------------
+ * Replaces CapaASRN._ids (asrn/nucleo.py:661-664), `ids.argsort(dim=-1, stable=True)` and `torch.gather(ids, 1,
+ * orden)` (asrn/estable.py:282-283, 288-291).
+ *   phi        (B, L, phi_stride) fp32; table tau reads columns [tau*nb, tau*nb + nb)
+ *   ids        (B*T, L) int32 out: bucket id of each position, text order
+ *   order      (B*T, L) int32 out: sorted rank -> text position (stable: ties keep text order)
+ *   ids_sorted (B*T, L) int32 out: ids[order]
+ *   rank       (B, L, T) int32 out: text position -> sorted rank, per table
+ * Requires 1 <= nb <= 14. */
+int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t T, int32_t nb, int64_t phi_stride,
+                     int32_t* ids, int32_t* order, int32_t* ids_sorted, int32_t* rank, void* stream);
+
+/* ---- a3 - a7: candidate attention, forward ---------------------------------------------------------------------
+ * Replaces _CasillerosTriton.forward / _casilleros_ida in ESTABLE mode (asrn/nucleo.py:359-382, 465-488) as called
+ * from CapaASRNEstable._acumular_triton (asrn/estable.py:274-292), with the table sum and the gate signals of
+ * _senales (asrn/estable.py:294-300) done in the kernel.
+ * For query t and table tau the candidates are the sorted ranks [s - C, s) of the same bucket (s = rank of t):
+ * its <= C most recent earlier bucket mates. Score = <phi_q, phi_k> * scale_phi + <Qc_q, Kc_k> * scale_c
+ * + w_suf[suffix match] + log_alfa_k + (gamma_tau / C) * fp32(Bt_k - Bt_q); exact masked softmax.
+ *   sig (B, L) fp32 token signatures; Bt (B, L) fp64 clock; log_alfa (B, L); w_suf (K+1); gamma (T)
+ *   salida  (B, L, d) out: sum over tables of sum_k att * V_k
+ *   signals (B, L, 4) out: peso_total, mejor, pico, peso_ctx
+ *   stats   (B, L, T, 2) out: per (query, table) the valid max score and the softmax denominator (for the backward)
+ * Requires d % 4 == 0, d <= 1024, 1 <= C <= 64, P + cf <= 256, K <= 16, T <= 32. */
+int asrn_candidates_fwd(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
+                        const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
+                        const int32_t* order, const int32_t* ids_sorted, const int32_t* rank, int64_t B, int64_t L,
+                        int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
+                        float scale_phi, float scale_c, float* salida, float* signals, float* stats, void* stream);
+
+/* The candidate lists the forward and backward walk, materialized for checking (a3, a4): for each (b, t, tau) the
+ * text positions of the <= C most recent earlier bucket mates in the C-slot window [s - C, s) of the sorted row
+ * (oldest first; the empty slots come first and hold -1), and their suffix-match lengths (asrn/nucleo.py:98-108,
+ * 313-320).
+ *   pos, ell (B, L, T, C) int32 out (-1 where the window slot holds no candidate). */
+int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* ids_sorted, const int32_t* rank,
+                         int64_t B, int64_t L, int32_t T, int32_t C, int32_t K, int32_t* pos, int32_t* ell,
+                         void* stream);
+
+/* ---- a8: candidate attention, backward -------------------------------------------------------------------------
+ * Replaces _CasillerosTriton.backward / _casilleros_vuelta (asrn/nucleo.py:384-451, 490-515). Two passes with one
+ * owner per output row, so no atomics and no per-slot buffers: a query pass (query-side gradients, the softmax
+ * correction D = sum att*dp per (query, table), and per-query partials of d gamma and d w_suf) and a key pass
+ * (key-side gradients; the queries that see key k in table tau are the next <= C same-bucket sorted ranks).
+ *   dsalida (B, L, d); stats from the forward
+ *   dphi (B, L, P), dV (B, L, d), dQc, dKc (B, L, cf), dBt (B, L) fp64, dlog_alfa (B, L) out (overwritten)
+ *   qstats   (B, L, T) fp32 workspace
+ *   partials (B*L, T + K + 1) fp32 out: per query, d gamma_tau then d w_suf[0..K]; the caller sums over rows. */
+int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
+                        const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
+                        const int32_t* order, const int32_t* ids_sorted, const int32_t* rank, int64_t B, int64_t L,
+                        int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
+                        float scale_phi, float scale_c, const float* dsalida, const float* stats, float* dphi,
+                        float* dV, float* dQc, float* dKc, double* dBt, float* dlog_alfa, float* qstats,
+                        float* partials, void* stream);
+
+/* ---- a9: clock --------------------------------------------------------------------------------------------------
+ * Bt = cumsum(beta) over L in fp64 (asrn/estable.py:418). reverse != 0 computes the suffix sums instead (the
+ * backward of the cumsum). */
+int asrn_clock_scan(const double* x, double* y, int64_t B, int64_t L, int32_t reverse, void* stream);
+
+/* ---- a10: n-gram keys, stable key sort, repeated and seen flags -------------------------------------------------
+ * Replaces _claves_de (asrn/nucleo.py:175-185), _ordenar_claves (asrn/nucleo.py:693-701) and the scatter of the seen
+ * flags (asrn/estable.py:310-312).
+ *   sig (B, L) fp32; coef (n) fp64 (the c_vistos buffer)
+ *   keys (B, L, n) fp64 out: k_j(t) = (((0 + s_t c_0) + s_{t-1} c_1) + ...) with separate roundings, NaN when the
+ *        group starts before the text
+ *   order (B, n, L) int32 out: stable sort of each (b, j) row by key, NaN last
+ *   repeated (B, n, L) uint8 out: key[order[i]] == key[order[i-1]]
+ *   rank_k (B, n, L) int32 out: text position -> sorted index
+ *   vistos (B, L, n) fp32 out: repeated scattered back to text order
+ *   workspace: asrn_ngram_sort_workspace(B, L, n) bytes. */
+int64_t asrn_ngram_sort_workspace(int64_t B, int64_t L, int32_t n);
+int asrn_ngram_sort(const float* sig, const double* coef, int64_t B, int64_t L, int32_t n, double* keys,
+                    int32_t* order, uint8_t* repeated, int32_t* rank_k, float* vistos, void* workspace,
+                    int64_t workspace_bytes, void* stream);
+
+/* ---- a12: affine scan S_i = a_i S_{i-1} + b_i over rows of N (asrn/nucleo.py:188-196, 214-257, 518-537) --------
+ * scan_bwd: l_i = g_i + a_{i+1} l_{i+1}; gb = l; ga_i = l_i S_{i-1}. */
+int asrn_scan_fwd(const float* a, const float* b, float* S, int64_t rows, int64_t N, void* stream);
+int asrn_scan_bwd(const float* a, const float* S, const float* g, float* ga, float* gb, int64_t rows, int64_t N,
+                  void* stream);
+
+/* ---- a11: Hawkes intensities in key order (asrn/estable.py:313-318) ---------------------------------------------
+ * Per (b, j) row in key order: dB_i = fp32(max(0, Bt[o_i] - Bt[o_{i-1}])), a_i = repeated_i exp(-kappa_j dB_i),
+ * lambda = scan(a, a * alfa_{i-1}) with alfa = exp(log_alfa); hawkes[b, o_i, j] = lambda_i.
+ *   hawkes (B, L, n) out; S_sorted (B, n, L) out (lambda in key order, kept for the backward)
+ * hawkes_bwd: from dhawkes (B, L, n) gives dBt (B, L) fp64 and dlog_alfa (B, L) (overwritten) and dkappa (B, n)
+ * per-row partials of d kappa_j. workspace: asrn_hawkes_bwd_workspace(B, L, n) bytes. */
+int asrn_hawkes_fwd(const int32_t* order, const uint8_t* repeated, const double* Bt, const float* log_alfa,
+                    const float* kappa, int64_t B, int64_t L, int32_t n, float* hawkes, float* S_sorted,
+                    void* stream);
+int64_t asrn_hawkes_bwd_workspace(int64_t B, int64_t L, int32_t n);
+int asrn_hawkes_bwd(const int32_t* order, const uint8_t* repeated, const int32_t* rank_k, const double* Bt,
+                    const float* log_alfa, const float* kappa, const float* S_sorted, const float* dhawkes,
+                    int64_t B, int64_t L, int32_t n, double* dBt, float* dlog_alfa, float* dkappa, void* workspace,
+                    int64_t workspace_bytes, void* stream);
+
+/* ---- a11: repetition streak (asrn/estable.py:319-320) ----------------------------------------------------------
+ * racha = scan(r exp(-kappa_r fp32(beta)), r) over the text with r = vistos[:, :, n-1].
+ * streak_bwd: dbeta (B, L) fp64 (overwritten) and dkappa_r (B) per-row partials of d kappa_r. */
+int asrn_streak_fwd(const float* vistos, const double* beta, const float* kappa_r, int64_t B, int64_t L, int32_t n,
+                    float* racha, void* stream);
+int asrn_streak_bwd(const float* vistos, const double* beta, const float* kappa_r, const float* racha,
+                    const float* dracha, int64_t B, int64_t L, int32_t n, double* dbeta, float* dkappa_r,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ASRN_HIP_H */

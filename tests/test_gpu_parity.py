@@ -1,0 +1,412 @@
+"""HIP kernels against the oracle and the reference's golden fixtures, on the GPU, through the C ABI.
+
+Bit-exact: bucket ids, sorted orders, candidate lists, suffix-match lengths, n-gram keys, their order, the repeated
+and seen flags, integer streaks. Within the north-star tolerance (1e-3 relative at fp32): outputs and gradients of
+the candidate attention, the Hawkes and streak scans, the clock, and the whole layer. Each test prints the case it
+runs before touching the device."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import asrn_amd
+from asrn_amd import ops, synth
+from asrn_amd.capa import CapaASRNEstable
+from oracle import layer as O
+from tests import fixtures
+
+pytestmark = pytest.mark.gpu
+DEV = 'cuda'
+TOL = 1e-3           # fp32 relative tolerance of the north star, on max |error| / max |reference|
+CASES = fixtures.names()
+
+
+def say(*a):
+    print('[case]', *a, flush=True)
+
+
+def rel_err(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    if a.numel() == 0:
+        return 0.0
+    return (a - b).abs().max().item() / (b.abs().max().item() + 1e-12)
+
+
+def assert_close(a, b, what, tol=TOL):
+    e = rel_err(a, b)
+    assert e <= tol, f'{what}: relative error {e:.3g} > {tol}'
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip('needs a GPU')
+    asrn_amd.load()
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a1 + a2: bucket ids and the stable sort
+# ---------------------------------------------------------------------------------------------------------------------
+
+def check_bucket_sort(phi, T, nb):
+    ids, order, ids_s, rank = ops.bucket_sort(phi.to(DEV), T, nb)
+    ref_ids, ref_order = O.bucket_rows(phi.cpu(), T, nb)
+    assert torch.equal(ids.cpu().long(), ref_ids.long())
+    assert torch.equal(order.cpu().long(), ref_order)
+    assert torch.equal(ids_s.cpu().long(), torch.gather(ref_ids.long(), 1, ref_order))
+    B, L = phi.shape[0], phi.shape[1]
+    inv = torch.empty_like(ref_order).scatter_(1, ref_order, torch.arange(L).expand(B * T, L))
+    assert torch.equal(rank.cpu().long().permute(0, 2, 1).reshape(B * T, L), inv)
+    return ids, order, ids_s, rank
+
+
+@pytest.mark.parametrize('name', CASES)
+def test_bucket_sort_golden(name):
+    say('bucket_sort golden', name)
+    g, p, m = fixtures.load(name)
+    sh = fixtures.shape_of(p, m)
+    ids, order, ids_s, rank = ops.bucket_sort(g['phi'].to(DEV), sh.T, sh.nb)
+    assert torch.equal(ids.cpu().long(), g['ids'].long())
+    assert torch.equal(order.cpu().long(), g['orden'])
+
+
+@pytest.mark.parametrize('B,L,T,nb,mode', [(8, 4096, 8, 14, 'randn'), (2, 5000, 8, 14, 'few'), (1, 1, 8, 14, 'randn'),
+                                           (3, 1023, 5, 3, 'randn'), (1, 2049, 8, 14, 'same'),
+                                           (1, 65536, 8, 14, 'few')])
+def test_bucket_sort_vs_numpy(B, L, T, nb, mode):
+    say('bucket_sort', B, L, T, nb, mode)
+    g = torch.Generator().manual_seed(L)
+    P = T * nb
+    if mode == 'randn':
+        phi = torch.randn(B, L, P, generator=g)
+    elif mode == 'few':                           # few distinct rows: long runs of ties in every bucket
+        phi = torch.randn(7, P, generator=g)[torch.randint(0, 7, (B, L), generator=g)]
+    else:                                         # one bucket for everything, with exact zeros (strict > 0)
+        phi = torch.zeros(B, L, P)
+    check_bucket_sort(phi, T, nb)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a3 + a4: candidate lists and suffix lengths
+# ---------------------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize('B,L,T,nb,C,K,V', [(2, 300, 8, 3, 16, 4, 5), (1, 200, 4, 2, 4, 4, 3), (2, 700, 8, 14, 32, 4, 6),
+                                            (1, 130, 3, 2, 64, 6, 4), (1, 50, 2, 1, 1, 1, 2)])
+def test_candidate_lists_bruteforce(B, L, T, nb, C, K, V):
+    say('candidate_lists', B, L, T, nb, C, K, V)
+    g = torch.Generator().manual_seed(B * 1000 + L)
+    x = torch.randint(0, V, (B, L), generator=g)
+    phi = torch.randn(V, T * nb, generator=g)[x]
+    sig = x.float()
+    ids, order, ids_s, rank = check_bucket_sort(phi, T, nb)
+    pos, ell = ops.candidate_lists(sig.to(DEV), order, ids_s, rank, C, K)
+    pos, ell = pos.cpu().long(), ell.cpu().long()
+    lists = O.candidate_lists_bruteforce(ids.cpu(), C)
+    want = torch.full((B, L, T, C), -1, dtype=torch.long)
+    for b in range(B):
+        for tau in range(T):
+            for t, lst in enumerate(lists[b * T + tau]):
+                if lst:
+                    want[b, t, tau, C - len(lst):] = torch.tensor(lst)
+    assert torch.equal(pos, want)
+    Pf = O.previous(sig, K)                                                   # (B, L, K)
+    valid = want >= 0
+    kk = want.clamp(min=0)
+    Pk = Pf.reshape(B * L, K)[(torch.arange(B).view(B, 1, 1, 1) * L + kk)]   # (B, L, T, C, K)
+    Pq = Pf[:, :, None, None, :].expand_as(Pk)
+    ref_ell = O.suffix_len(Pq, Pk)
+    assert torch.equal(ell[valid], ref_ell[valid])
+    assert bool((ell[~valid] == -1).all())
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a10: n-gram keys and their sort
+# ---------------------------------------------------------------------------------------------------------------------
+
+def check_ngram(sig, coef, n):
+    keys, order, rep, rank_k, vistos = ops.ngram_sort(sig.to(DEV), coef.to(DEV), n)
+    rk = O.ngram_keys(sig, coef, n)
+    k = keys.cpu()
+    assert torch.equal(torch.isnan(k), torch.isnan(rk))
+    assert torch.equal(k.nan_to_num(-5.0).view(torch.int64), rk.nan_to_num(-5.0).view(torch.int64))
+    ro, rr = O.ngram_sort(rk)
+    assert torch.equal(order.cpu().long(), ro)
+    assert torch.equal(rep.cpu().bool(), rr)
+    B, L = sig.shape
+    inv = torch.empty_like(ro).scatter_(-1, ro, torch.arange(L).expand_as(ro))
+    assert torch.equal(rank_k.cpu().long(), inv)
+    rv = torch.zeros_like(rr).scatter(-1, ro, rr).transpose(1, 2).float()
+    assert torch.equal(vistos.cpu(), rv)
+    return keys, order, rep, rank_k, vistos
+
+
+@pytest.mark.parametrize('name', CASES)
+def test_ngram_golden(name):
+    say('ngram golden', name)
+    g, p, m = fixtures.load(name)
+    keys, order, rep, rank_k, vistos = ops.ngram_sort(g['sig'].to(DEV), p['c_vistos'].to(DEV), 4)
+    k = keys.cpu()
+    assert torch.equal(torch.isnan(k), torch.isnan(g['claves']))
+    assert torch.equal(k.nan_to_num(-5.0), g['claves'].nan_to_num(-5.0))
+    assert torch.equal(order.cpu().long(), g['orden_k'])
+    assert torch.equal(rep.cpu().bool(), g['repetido'].bool())
+    assert torch.equal(vistos.cpu(), g['rep.vistos'])
+
+
+@pytest.mark.parametrize('B,L,V,zipf', [(8, 4096, 256, None), (2, 10000, 6, None), (1, 1, 5, None), (3, 3, 5, None),
+                                        (1, 65536, 32000, 1.1), (2, 333, 50304, 1.1)])
+def test_ngram_vs_oracle(B, L, V, zipf):
+    say('ngram', B, L, V, zipf)
+    x = synth.tokens(B, L, V, frac=0.3, span=(2, 8), zipf=zipf, seed=L)
+    coef = torch.rand(4, generator=torch.Generator().manual_seed(12345), dtype=torch.float64) + 0.5
+    check_ngram(x.float(), coef, 4)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a9, a11, a12: scans
+# ---------------------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize('N', [1, 2, 3, 7, 64, 1000, 4097, 10000])
+def test_affine_scan_vs_sequential(N):
+    say('scan', N)
+    g = torch.Generator().manual_seed(N)
+    a = torch.rand(3, 5, N, generator=g)
+    b = torch.randn(3, 5, N, generator=g)
+    a[..., ::7] = 0
+    w = torch.randn(3, 5, N, generator=g)
+    ar, br = a.clone().requires_grad_(), b.clone().requires_grad_()
+    (O.scan(ar, br) * w).sum().backward()
+    ad, bd = a.to(DEV).requires_grad_(), b.to(DEV).requires_grad_()
+    S = ops.escaneo(ad, bd)
+    (S * w.to(DEV)).sum().backward()
+    assert_close(S, O.scan(a, b), 'S', 1e-5)
+    assert_close(ad.grad, ar.grad, 'dL/da', 1e-5)
+    assert_close(bd.grad, br.grad, 'dL/db', 1e-5)
+
+
+@pytest.mark.parametrize('B,L', [(8, 4096), (4, 65536), (3, 1), (2, 5000)])
+def test_clock_scan(B, L):
+    say('clock', B, L)
+    beta = torch.rand(B, L, generator=torch.Generator().manual_seed(L), dtype=torch.float64) * 2
+    bd = beta.to(DEV).requires_grad_()
+    Bt = ops.ClockScan.apply(bd)
+    assert_close(Bt, beta.cumsum(1), 'Bt', 1e-12)
+    g = torch.randn(B, L, dtype=torch.float64)
+    Bt.backward(g.to(DEV))
+    assert_close(bd.grad, g.flip(1).cumsum(1).flip(1), 'dbeta', 1e-12)
+
+
+def run_repetition_stage(g, p, sh):
+    """HIP hawkes/streak on the fixture's stage inputs, with gradients."""
+    beta = g['beta'].to(DEV).requires_grad_()
+    Bt = g['Bt'].to(DEV).requires_grad_()
+    la = g['log_alfa'].to(DEV).requires_grad_()
+    lk = p['log_kappa'].to(DEV).requires_grad_()
+    lkr = p['log_kappa_racha'].to(DEV).requires_grad_()
+    _, order, rep, rank_k, vistos = ops.ngram_sort(g['sig'].to(DEV), p['c_vistos'].to(DEV), sh.n)
+    hawkes = ops.Hawkes.apply(Bt, la, lk.exp(), order, rep, rank_k)
+    racha = ops.Streak.apply(beta, lkr.exp(), vistos)
+    ((hawkes * g['rep.gh'].to(DEV)).sum() + (racha * g['rep.gr'].to(DEV)).sum()).backward()
+    return vistos, hawkes, racha, beta.grad, Bt.grad, la.grad, lk.grad, lkr.grad
+
+
+@pytest.mark.parametrize('name', CASES)
+def test_repetition_golden(name):
+    say('repetition golden', name)
+    g, p, m = fixtures.load(name)
+    sh = fixtures.shape_of(p, m)
+    vistos, hawkes, racha, gb, gB, gla, glk, glkr = run_repetition_stage(g, p, sh)
+    assert torch.equal(vistos.cpu(), g['rep.vistos'])
+    assert_close(hawkes, g['rep.hawkes'], 'hawkes')
+    if m['extra'].get('kappa_r_zero'):
+        assert torch.equal(racha.cpu(), g['rep.racha'])          # integer run lengths, bit-exact
+    else:
+        assert_close(racha, g['rep.racha'], 'racha')
+    assert_close(gb, g['rep.g_beta'], 'grad beta')
+    assert_close(gB, g['rep.g_Bt'], 'grad Bt')
+    assert_close(gla, g['rep.g_log_alfa'], 'grad log_alfa')
+    assert_close(glk, g['rep.g_log_kappa'], 'grad log_kappa')
+    assert_close(glkr, g['rep.g_log_kappa_racha'], 'grad log_kappa_racha')
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a3 - a8: candidate attention forward and backward
+# ---------------------------------------------------------------------------------------------------------------------
+
+def run_candidates(stage, sig, w_suf, gamma, sh, gs):
+    """HIP candidate stage on CPU-provided stage tensors; returns outputs and grads on the CPU."""
+    leaves = {k: stage[k].to(DEV).requires_grad_() for k in ('phi', 'V', 'Qc', 'Kc', 'Bt', 'log_alfa')}
+    w = w_suf.to(DEV).requires_grad_()
+    gam = gamma.to(DEV).requires_grad_()
+    _, order, ids_s, rank = ops.bucket_sort(leaves['phi'].detach(), sh.T, sh.nb)
+    shape = dict(T=sh.T, Tc=sh.Tc, C=sh.C, K=sh.K)
+    salida, sen = ops.Candidates.apply(leaves['phi'], leaves['V'], leaves['Qc'], leaves['Kc'], leaves['Bt'],
+                                       leaves['log_alfa'], w, gam, sig.to(DEV), order, ids_s, rank, shape)
+    (salida * gs.to(DEV)).sum().backward()
+    grads = {k: t.grad.cpu() for k, t in leaves.items()}
+    grads['w_sufijo'], grads['gamma'] = w.grad.cpu(), gam.grad.cpu()
+    return salida.detach().cpu(), sen.cpu(), grads
+
+
+def oracle_candidates(stage, sig, w_suf, gamma, sh, gs):
+    leaves = {k: stage[k].clone().requires_grad_() for k in ('phi', 'V', 'Qc', 'Kc', 'Bt', 'log_alfa')}
+    w, gam = w_suf.clone().requires_grad_(), gamma.clone().requires_grad_()
+    salida, sen = O.candidates(leaves['phi'], leaves['V'], leaves['Qc'], leaves['Kc'], leaves['Bt'],
+                               leaves['log_alfa'], sig, w, gam, sh)
+    acc = O.gate_signals(salida, sen, sh.T, sh.Tc)
+    (salida * gs).sum().backward()
+    grads = {k: t.grad for k, t in leaves.items()}
+    grads['w_sufijo'], grads['gamma'] = w.grad, gam.grad
+    return acc, grads
+
+
+def check_signals(sen, acc):
+    assert torch.equal(sen[..., 0:1], acc['peso_total'])
+    assert torch.equal(sen[..., 3:4], acc['peso_ctx'])
+    assert_close(sen[..., 1:2], acc['mejor'], 'mejor')
+    assert_close(sen[..., 2:3], acc['pico'], 'pico')
+
+
+@pytest.mark.parametrize('name', CASES)
+def test_candidates_golden(name):
+    say('candidates golden', name)
+    g, p, m = fixtures.load(name)
+    sh = fixtures.shape_of(p, m)
+    salida, sen, grads = run_candidates(g, g['sig'], p['w_sufijo'], p['gamma'], sh, g['acc.gs'])
+    assert_close(salida, g['acc.salida'], 'salida')
+    check_signals(sen, {k: g['acc.' + k] for k in ('peso_total', 'mejor', 'pico', 'peso_ctx')})
+    for k in ('phi', 'V', 'Qc', 'Kc', 'Bt', 'log_alfa', 'w_sufijo', 'gamma'):
+        assert_close(grads[k], g['acc.g_' + k], 'grad ' + k)
+
+
+def random_stage(B, L, d, V, nb=14, T=8, cf=16, K=4, seed=0, shift=0.0):
+    g = torch.Generator().manual_seed(seed)
+    x = synth.tokens(B, L, V, frac=0.3, span=(8, 64), seed=seed)
+    P = T * nb
+    emb = torch.randn(V, P, generator=g)
+    word = emb[x][..., :P // 2]
+    ctx = torch.randn(V, V, P - P // 2, generator=g) if V <= 64 else None
+    prev = torch.cat([x[:, :1], x[:, :-1]], 1)
+    ctxv = ctx[x, prev] if ctx is not None else (emb[x][..., P // 2:] + 0.7 * emb[prev][..., P // 2:])
+    phi = torch.cat([word, ctxv], -1).contiguous()
+    stage = dict(phi=phi, V=torch.randn(B, L, d, generator=g), Qc=torch.randn(B, L, cf, generator=g),
+                 Kc=torch.randn(B, L, cf, generator=g),
+                 Bt=(torch.rand(B, L, generator=g, dtype=torch.float64) * 1.5).cumsum(1) + shift,
+                 log_alfa=torch.randn(B, L, generator=g) * 0.3)
+    w_suf = torch.randn(K + 1, generator=g) * 0.5
+    gamma = torch.rand(T, generator=g) * 2
+    gs = torch.randn(B, L, d, generator=g)
+    return x.float(), stage, w_suf, gamma, gs
+
+
+@pytest.mark.parametrize('B,L,d,V,C,nb,shift', [(2, 1500, 256, 6, 32, 14, 0.0), (2, 777, 96, 40, 16, 4, 0.0),
+                                                (1, 600, 64, 5, 64, 6, 1e6), (2, 300, 1024, 8, 8, 3, 0.0),
+                                                (1, 2, 32, 3, 32, 14, 0.0)])
+def test_candidates_vs_oracle(B, L, d, V, C, nb, shift):
+    say('candidates', B, L, d, V, C, nb, shift)
+    sig, stage, w_suf, gamma, gs = random_stage(B, L, d, V, nb=nb, seed=L, shift=shift)
+    sh = O.Shape(d=d, nb=nb, C=C)
+    salida, sen, grads = run_candidates(stage, sig, w_suf, gamma, sh, gs)
+    acc, rg = oracle_candidates(stage, sig, w_suf, gamma, sh, gs)
+    assert_close(salida, acc['salida'], 'salida')
+    check_signals(sen, acc)
+    for k in rg:
+        assert_close(grads[k], rg[k], 'grad ' + k)
+
+
+def test_candidates_cfg2_full_size():
+    """BASELINE cfg2 (B 8, N 4096, d 256, fp32) on the synthetic generator, candidate stage vs the oracle."""
+    say('candidates cfg2 full size')
+    sig, stage, w_suf, gamma, gs = random_stage(8, 4096, 256, 256, seed=0)
+    sh = O.Shape(d=256)
+    salida, sen, grads = run_candidates(stage, sig, w_suf, gamma, sh, gs)
+    acc, rg = oracle_candidates(stage, sig, w_suf, gamma, sh, gs)
+    assert_close(salida, acc['salida'], 'salida')
+    check_signals(sen, acc)
+    for k in rg:
+        assert_close(grads[k], rg[k], 'grad ' + k)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# the whole layer
+# ---------------------------------------------------------------------------------------------------------------------
+
+def layer_from_fixture(p, m):
+    layer = CapaASRNEstable(m['d'], **m['kw'])
+    layer.load_state_dict(p)
+    return layer.to(DEV)
+
+
+def run_layer(layer, E, h, x, gy):
+    layer.zero_grad()
+    Ed, hd = E.to(DEV).requires_grad_(), h.to(DEV).requires_grad_()
+    y = layer(Ed, hd, x.to(DEV))
+    (y * gy.to(DEV)).sum().backward()
+    grads = {'E': Ed.grad.cpu(), 'h': hd.grad.cpu()}
+    grads.update({n: q.grad.cpu() for n, q in layer.named_parameters() if q.grad is not None})
+    return y.detach().cpu(), grads
+
+
+@pytest.mark.parametrize('name', CASES)
+def test_layer_golden(name):
+    say('layer golden', name)
+    g, p, m = fixtures.load(name)
+    sh = fixtures.shape_of(p, m)
+    layer = layer_from_fixture(p, m)
+    with torch.no_grad():
+        phi, _ = layer._phi_y_valores(g['E'].to(DEV))
+    ids, _ = O.bucket_rows(phi.cpu(), sh.T, sh.nb)
+    flips = (ids != g['ids']).sum().item()
+    if flips:
+        pytest.skip(f'{flips} bucket ids differ between the GPU GEMM and the CPU one (sign of phi near 0)')
+    y, grads = run_layer(layer, g['E'], g['h'], g['x'], g['gy'])
+    assert_close(y, g['y'], 'y')
+    assert_close(grads['E'], g['gE'], 'grad E')
+    assert_close(grads['h'], g['gh'], 'grad h')
+    for n in grads:
+        if ('g.' + n) in g:
+            assert_close(grads[n], g['g.' + n], 'grad ' + n)
+
+
+def test_layer_deterministic_and_causal():
+    say('layer determinism + causality')
+    torch.manual_seed(0)
+    layer = synth.move_params(CapaASRNEstable(64)).to(DEV)
+    x, E, h = synth.layer_inputs(2, 700, 64, 40, seed=3)
+    gy = torch.randn(2, 700, 64)
+    y1, g1 = run_layer(layer, E, h, x, gy)
+    y2, g2 = run_layer(layer, E, h, x, gy)
+    assert torch.equal(y1, y2)
+    for k in g1:
+        assert torch.equal(g1[k], g2[k]), k
+    cut = 400
+    x2, E2, h2 = x.clone(), E.clone(), h.clone()
+    x2[:, cut:] = torch.randint(0, 40, (2, 700 - cut))
+    E2[:, cut:] = torch.randn(2, 700 - cut, 64)
+    h2[:, cut:] = torch.randn(2, 700 - cut, 64)
+    with torch.no_grad():
+        ya = layer(E.to(DEV), h.to(DEV), x.to(DEV))[:, :cut]
+        yb = layer(E2.to(DEV), h2.to(DEV), x2.to(DEV))[:, :cut]
+    assert (ya - yb).abs().max().item() <= 1e-6 * ya.abs().max().item()
+
+
+def test_layer_exact_mask_no_leak_with_huge_gamma():
+    """gamma = 1e9: every valid score sinks below -1e9; the exact mask still gives no weight to invalid keys, so
+    the future never changes the past (asrn/estable.py:20-24, tests te:283-310)."""
+    say('layer gamma huge')
+    torch.manual_seed(0)
+    layer = CapaASRNEstable(32, chunk=16, n_bits=3).to(DEV)
+    with torch.no_grad():
+        layer.gamma.fill_(1e9)
+    L, cut = 96, 60
+    g = torch.Generator().manual_seed(0)
+    E, h, x = torch.randn(1, L, 32, generator=g), torch.randn(1, L, 32, generator=g), torch.randint(0, 7, (1, L), generator=g)
+    E2, h2, x2 = E.clone(), h.clone(), x.clone()
+    E2[:, cut:], h2[:, cut:] = torch.randn(1, L - cut, 32), torch.randn(1, L - cut, 32)
+    x2[:, cut:] = torch.randint(0, 7, (1, L - cut))
+    with torch.no_grad():
+        ya = layer(E.to(DEV), h.to(DEV), x.to(DEV))[:, :cut]
+        yb = layer(E2.to(DEV), h2.to(DEV), x2.to(DEV))[:, :cut]
+    assert torch.isfinite(ya).all()
+    assert (ya - yb).abs().max().item() <= 1e-6 * ya.abs().max().item()

@@ -1,0 +1,111 @@
+"""CPU-side checks of the product: the C-ABI library loads and exports every symbol include/asrn_hip.h declares, its
+argument checks reject bad sizes before any device work, the host layer mirrors the reference's parameters and
+construction order, and the product refuses CPU tensors instead of falling back."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import asrn_amd
+from asrn_amd import _lib
+from asrn_amd.capa import CapaASRNEstable
+from tests import fixtures
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, 'include', 'asrn_hip.h')
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'\b(asrn_\w+)\s*\(', text)))
+
+
+@pytest.fixture(scope='module')
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip('libasrn_hip.so not built (run `python -m asrn_amd.build`)')
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = declared()
+    assert len(names) >= 14, names
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f'{n} declared in the header but not bound in _lib.SIGNATURES'
+    assert set(_lib.SIGNATURES) == set(names)
+    assert lib.asrn_hip_abi_version() == 1
+
+
+def _err(lib):
+    return lib.asrn_hip_last_error().decode()
+
+
+def test_argument_checks_fail_before_any_device_work(lib):
+    N = None
+    # n_bits outside [1, 14]
+    assert lib.asrn_bucket_sort(N, 2, 16, 8, 15, 120, N, N, N, N, N) != 0
+    assert 'n_bits' in _err(lib)
+    # phi row stride shorter than T*nb
+    assert lib.asrn_bucket_sort(N, 2, 16, 8, 14, 100, N, N, N, N, N) != 0
+    assert 'stride' in _err(lib)
+    # empty inputs are a no-op
+    assert lib.asrn_bucket_sort(N, 0, 16, 8, 14, 112, N, N, N, N, N) == 0
+    args = [N] * 12 + [2, 16]
+    # d not a multiple of 4
+    assert lib.asrn_candidates_fwd(*args, 6, 112, 16, 4, 8, 4, 32, 0.1, 0.25, N, N, N, N) != 0
+    assert 'd=6' in _err(lib)
+    # chunk above 64
+    assert lib.asrn_candidates_fwd(*args, 64, 112, 16, 4, 8, 4, 65, 0.1, 0.25, N, N, N, N) != 0
+    assert 'chunk' in _err(lib)
+    # feature width above 256
+    assert lib.asrn_candidates_bwd(*args, 64, 250, 16, 4, 8, 4, 32, 0.1, 0.25, *([N] * 11)) != 0
+    assert 'P + cf' in _err(lib)
+    # workspace sizes are pure host arithmetic
+    assert lib.asrn_ngram_sort_workspace(8, 4096, 4) >= 2 * 8 * 4 * 4096 * 12
+    assert lib.asrn_ngram_sort(N, N, 8, 4096, 4, N, N, N, N, N, N, 16, N) != 0
+    assert 'workspace' in _err(lib)
+    assert lib.asrn_hawkes_bwd_workspace(8, 4096, 4) >= 2 * 8 * 4096 * 4 * 4
+
+
+def test_ops_refuse_cpu_tensors():
+    with pytest.raises(RuntimeError, match='GPU only'):
+        asrn_amd.ops.bucket_sort(torch.zeros(1, 4, 112), 8, 14)
+    layer = CapaASRNEstable(16)
+    with pytest.raises(RuntimeError, match='GPU only'):
+        layer(torch.zeros(1, 4, 16), torch.zeros(1, 4, 16), torch.zeros(1, 4, dtype=torch.long))
+
+
+@pytest.mark.parametrize('name', fixtures.names())
+def test_parameters_and_construction_order_match_the_reference(name):
+    """Same names, shapes, registration order and seeded values: building the layer with the fixture's seed and
+    moving the parameters exactly as tests/golden/make_golden.py did reproduces the reference's state_dict bit for
+    bit (asrn/nucleo.py:585-630)."""
+    g, p, m = fixtures.load(name)
+    torch.manual_seed(0)
+    layer = CapaASRNEstable(m['d'], **m['kw'])
+    with torch.no_grad():
+        gen = torch.Generator().manual_seed(1)
+        for n, par in layer.named_parameters():
+            par.add_(torch.randn(par.shape, generator=gen) * (0.5 if n in asrn_amd.synth.NUEVOS else 0.05))
+        layer.gamma.abs_()
+        if 'corrimiento' in m['extra']:
+            layer.b_reloj[0] += m['extra']['corrimiento']
+        if 'gamma_fill' in m['extra']:
+            layer.gamma.fill_(m['extra']['gamma_fill'])
+        if m['extra'].get('kappa_r_zero'):
+            layer.log_kappa_racha.fill_(-200.0)
+    sd = layer.state_dict()
+    assert sorted(sd) == sorted(p)              # (safetensors stores keys sorted)
+    for k in sd:
+        assert sd[k].dtype == p[k].dtype and torch.equal(sd[k], p[k]), k
+
+
+def test_unsupported_protections_and_shapes_raise_clearly():
+    if not torch.cuda.is_available():
+        layer = CapaASRNEstable(16, protecciones=asrn_amd.Protecciones.ninguna())
+        with pytest.raises(RuntimeError, match='GPU only'):
+            layer._revisar(torch.zeros(1, 2, 16))
