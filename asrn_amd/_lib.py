@@ -9,7 +9,7 @@ import os
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, 'libasrn_hip.so')
+LIB_PATH = os.environ.get('ASRN_HIP_LIB') or os.path.join(_HERE, 'libasrn_hip.so')   # override: another build
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -20,7 +20,7 @@ _F32 = ctypes.c_float
 SIGNATURES = {
     'asrn_hip_last_error': (ctypes.c_char_p, []),
     'asrn_hip_abi_version': (_I32, []),
-    'asrn_bucket_sort': (ctypes.c_int, [_P, _I64, _I64, _I32, _I32, _I64, _P, _P, _P, _P, _P]),
+    'asrn_bucket_sort': (ctypes.c_int, [_P, _I64, _I64, _I32, _I32, _I64, _I32, _P, _P, _P, _P, _P, _P]),
     'asrn_candidates_fwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7 + [_F32, _F32] + [_P] * 4),
     'asrn_candidate_lists': (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P]),
     'asrn_candidates_bwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7 + [_F32, _F32] + [_P] * 11),
@@ -68,9 +68,36 @@ def stream_of(device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+# entry point name -> list of (start, end) torch.cuda.Event pairs; filled only for the names being timed
+_TIMED = {}
+
+
+def time_calls(names):
+    """Starts timing the given entry points with device events recorded on torch's current stream (the stream the
+    library launches on). Returns the dict that collects (start, end) event pairs per name."""
+    _TIMED.clear()
+    for n in names:
+        _TIMED[n] = []
+    return _TIMED
+
+
+def stop_timing():
+    out = dict(_TIMED)
+    _TIMED.clear()
+    return out
+
+
 def call(name, *args):
     lib = load()
-    rc = getattr(lib, name)(*args)
+    ev = _TIMED.get(name)
+    if ev is not None:
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        rc = getattr(lib, name)(*args)
+        e.record()
+        ev.append((s, e))
+    else:
+        rc = getattr(lib, name)(*args)
     if rc != 0:
         raise ASRNHipError(f'{name}: {lib.asrn_hip_last_error().decode(errors="replace")}')
     return rc

@@ -16,8 +16,9 @@ CSRC = os.path.join(HERE, 'csrc')
 LIB = os.path.join(HERE, 'libasrn_hip.so')
 SOURCES = ['errors.hip', 'bucket_sort.hip', 'ngram.hip', 'scan.hip', 'candidates.hip']
 ARCH = os.environ.get('ASRN_OFFLOAD_ARCH', 'gfx950')
+INCLUDE = os.path.join(os.path.dirname(HERE), 'include')
 COMMON = ['-O3', '-fPIC', '-std=c++17', f'--offload-arch={ARCH}', '-Xclang', '-target-feature', '-Xclang',
-          '-packed-fp32-ops', '-Wno-unused-command-line-argument']
+          '-packed-fp32-ops', '-Wno-unused-command-line-argument', f'-I{INCLUDE}']
 PER_FILE = {'ngram.hip': ['-ffp-contract=off']}
 
 

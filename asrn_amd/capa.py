@@ -102,8 +102,9 @@ class CapaASRNEstable(nn.Module):
                              'Protecciones.ninguna() is not supported')
         if not 1 <= self.n_bits <= 14:
             raise ValueError(f'n_bits={self.n_bits}: the HIP bucket sort supports 1..14 bits per table')
-        if not 1 <= self.chunk <= 64:
-            raise ValueError(f'chunk={self.chunk}: the HIP candidate kernels support 1..64 candidates per table')
+        if not 1 <= self.chunk <= 64 or self.n_tablas * self.chunk > 256:
+            raise ValueError(f'chunk={self.chunk}, n_tablas={self.n_tablas}: the HIP candidate kernels support 1..64 '
+                             'candidates per table and n_tablas * chunk <= 256')
         d = E.shape[-1]
         if d % 4 or d > 1024:
             raise ValueError(f'd={d}: the HIP candidate kernels need d % 4 == 0 and d <= 1024')
@@ -160,10 +161,10 @@ class CapaASRNEstable(nn.Module):
         """Candidate attention of all tables -> salida and the gate signals (asrn/estable.py:204-300)."""
         T = self.n_tablas
         phi, V = self._phi_y_valores(E)
-        _, order, ids_s, rank = ops.bucket_sort(phi.detach(), T, self.n_bits)
+        _, order, _, rank, win = ops.bucket_sort(phi.detach(), T, self.n_bits, self.chunk)
         shape = dict(T=T, Tc=self.tablas_contexto, C=self.chunk, K=self.sufijo)
         salida, sen = ops.Candidates.apply(phi, V, Qc, Kc, Bt, log_alfa, self.w_sufijo, self.gamma, sig, order,
-                                           ids_s, rank, shape)
+                                           win, rank, shape)
         return {'salida': salida, 'peso_total': sen[..., 0:1], 'mejor': sen[..., 1:2], 'pico': sen[..., 2:3],
                 'peso_ctx': sen[..., 3:4]}
 
@@ -183,9 +184,10 @@ class CapaASRNEstable(nn.Module):
         return self.d_racha.cumsum(0)
 
     def _respuesta_racha(self, racha):
+        """Piecewise-linear response on log1p(racha), flat past the last node (asrn/nucleo.py:870-878)."""
         x = (torch.log1p(racha) / self.racha_paso).clamp(max=self.d_racha.shape[0] - 1)
         i = torch.nan_to_num(x.detach(), nan=0.0).floor().long().clamp(0, self.d_racha.shape[0] - 2)
-        return self.u_racha[i] + (x - i) * self.d_racha[1:][i]
+        return _Take.apply(i, self.u_racha) + (x - i) * _Take.apply(i, self.d_racha[1:])
 
     def _combinar(self, acc, h):
         p = self.protecciones
@@ -219,6 +221,25 @@ class CapaASRNEstable(nn.Module):
         acc = self._acumular(E, Qc, Kc, Bt, log_alfa, sig)
         acc.update(self._repeticion(sig, beta, Bt, log_alfa))
         return self._combinar(acc, h)
+
+
+class _Take(torch.autograd.Function):
+    """w[i] for a tiny w (the streak nodes) at every position. The backward sums the gradient of each entry with a
+    one-hot reduction instead of indexing's scatter-add (sorted atomics on the GPU), as the reference's _Tomar does
+    (asrn/nucleo.py:136-158): deterministic and a few small kernels."""
+
+    @staticmethod
+    def forward(ctx, i, w):
+        ctx.save_for_backward(i)
+        ctx.n = w.shape[0]
+        return w[i]
+
+    @staticmethod
+    def backward(ctx, g):
+        (i,) = ctx.saved_tensors
+        hot = i.reshape(-1, 1) == torch.arange(ctx.n, device=i.device)
+        gw = torch.where(hot, g.reshape(-1, 1).float(), 0.0).sum(0)
+        return None, gw.to(g.dtype)
 
 
 def _a_autocast(x):

@@ -48,11 +48,12 @@ __device__ void block_exclusive_scan(int* data, int n, int* wave_tot) {
 }
 
 __global__ __launch_bounds__(kSortThreads) void k_bucket_sort(const float* __restrict__ phi, int64_t L, int T, int nb,
-                                                              int64_t stride, int32_t* __restrict__ ids,
+                                                              int64_t stride, int C, int32_t* __restrict__ ids,
                                                               int32_t* __restrict__ order,
                                                               int32_t* __restrict__ ids_sorted,
-                                                              int32_t* __restrict__ rank) {
+                                                              int32_t* __restrict__ rank, int32_t* __restrict__ win) {
   __shared__ int cnt[1 << kMaxBits];
+  __shared__ int first[(1 << kMaxBits) + 1];     // bucket starts (cnt advances during the scatter)
   __shared__ int wave_tot[16];
   const int r = blockIdx.x;
   const int b = r / T, tau = r % T;
@@ -73,6 +74,9 @@ __global__ __launch_bounds__(kSortThreads) void k_bucket_sort(const float* __res
   }
   __syncthreads();
   block_exclusive_scan(cnt, nbins, wave_tot);
+  for (int i = tid; i < nbins; i += kSortThreads) first[i] = cnt[i];
+  if (tid == 0) first[nbins] = (int)L;
+  __syncthreads();
 
   int32_t* ordr = order + (int64_t)r * L;
   int32_t* idsr = ids_sorted + (int64_t)r * L;
@@ -96,7 +100,11 @@ __global__ __launch_bounds__(kSortThreads) void k_bucket_sort(const float* __res
     if (valid && dest >= 0 && dest < L) {       // always true for a correct sort; keeps a bug from faulting
       ordr[dest] = (int32_t)t;
       idsr[dest] = id;
-      rank[((int64_t)b * L + t) * T + tau] = dest;
+      const int64_t o = ((int64_t)b * L + t) * T + tau;
+      rank[o] = dest;
+      const int before = dest - first[id];               // earlier positions in the bucket
+      const int after = first[id + 1] - 1 - dest;          // later positions in the bucket
+      win[o] = min(before, C) | (min(after, C) << 8);
     }
   }
 }
@@ -104,7 +112,8 @@ __global__ __launch_bounds__(kSortThreads) void k_bucket_sort(const float* __res
 }  // namespace asrn
 
 extern "C" int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t T, int32_t nb, int64_t phi_stride,
-                                int32_t* ids, int32_t* order, int32_t* ids_sorted, int32_t* rank, void* stream) {
+                                int32_t C, int32_t* ids, int32_t* order, int32_t* ids_sorted, int32_t* rank,
+                                int32_t* win, void* stream) {
   ASRN_REQUIRE(nb >= 1 && nb <= asrn::kMaxBits, "asrn_bucket_sort: n_bits must be in [1, %d] (got %d)",
                asrn::kMaxBits, nb);
   ASRN_REQUIRE(B >= 0 && L >= 0 && T >= 1, "asrn_bucket_sort: bad sizes B=%lld L=%lld T=%d", (long long)B,
@@ -112,9 +121,11 @@ extern "C" int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t 
   ASRN_REQUIRE(L < (int64_t(1) << 31), "asrn_bucket_sort: L=%lld too long", (long long)L);
   ASRN_REQUIRE(phi_stride >= (int64_t)T * nb, "asrn_bucket_sort: phi row stride %lld < T*nb = %d",
                (long long)phi_stride, T * nb);
+  ASRN_REQUIRE(C >= 1 && C <= 255, "asrn_bucket_sort: window C=%d must be in [1, 255]", C);
   if (B == 0 || L == 0) return 0;
-  ASRN_REQUIRE(phi && ids && order && ids_sorted && rank, "asrn_bucket_sort: null pointer");
+  ASRN_REQUIRE(phi && ids && order && ids_sorted && rank && win, "asrn_bucket_sort: null pointer");
   hipLaunchKernelGGL(asrn::k_bucket_sort, dim3((unsigned)(B * T)), dim3(asrn::kSortThreads), 0,
-                     (hipStream_t)stream, phi, L, (int)T, (int)nb, phi_stride, ids, order, ids_sorted, rank);
+                     (hipStream_t)stream, phi, L, (int)T, (int)nb, phi_stride, (int)C, ids, order, ids_sorted, rank,
+                     win);
   return asrn::check_launch("asrn_bucket_sort");
 }

@@ -1,32 +1,38 @@
 // a3 - a8: candidate attention over the recent bucket mates, forward and backward.
 //
-// One wavefront per token. For table tau the query at sorted rank s sees the sorted ranks [s - C, s) of its own
-// bucket: the valid lanes of a C-lane window are always a suffix of it (sorted ids are non-decreasing), so the wave
-// only walks the valid candidates. Scores use coalesced feature loads: a 32-lane half-wave reads one candidate's
-// [phi ; Kc] row (consecutive lanes, consecutive floats) and reduces the products with the query's pre-scaled
-// [phi * scale_phi ; Qc * scale_c] row held in registers, so two candidates are scored per step. The copy-gather
-// reads each candidate's V row with all 64 lanes (float4 per lane) and accumulates the 8 tables in registers:
-// the table sum never leaves the kernel.
-//
-// The backward has one owner per output row and no atomics. The query pass recomputes the scores, gets
-// dp = <dO_q, V_k> per candidate, ds = att (dp - D) with D = sum att dp, and writes the query-side gradients, D per
-// (query, table) and per-query partials of d gamma and d w_suf. The key pass walks, for each key, the next <= C
-// same-bucket sorted ranks (exactly the queries whose window holds the key), rebuilds att from the forward's saved
-// (max, denominator), reloads dO_q once for both dp and dV, and adds the key-side gradients.
+// One wavefront per token, in phases that each keep many independent loads in flight and reduce across lanes with
+// DPP row rotations (no LDS round trips):
+//   gather  the recent-mates index gives, per table, the token's sorted rank s and how many bucket mates sit right
+//           before it (forward: the window [s - n, s)) or right after it (the backward's key pass: (s, s + n]); one
+//           round of `order` loads yields every table's candidates, packed into one list in LDS grouped by table,
+//           oldest first.
+//   dedupe  the tables mostly return the same positions (the word tables hash the same token), so each entry is
+//           matched against the earlier tables' segments and every distinct position gets one slot: the table-free
+//           part of the score, the suffix match and the row gathers are done once per position.
+//   score   a 32-lane half-wave reads one candidate's [phi ; Kc] row as one float4 per lane (512 B for P + cf = 128)
+//           and reduces it against the query's pre-scaled [phi * scale_phi ; Qc * scale_c] in registers, 16 rows in
+//           flight. Each table adds its own clock term; the exact masked softmax runs with one entry per lane.
+//   gather  each distinct candidate's V row is read once by the 64 lanes with the weights summed over the tables,
+//           8+ rows in flight: the table sum never leaves the kernel.
+// The backward has one owner per output row and no atomics: a query pass (query-side gradients, D = sum att*dp per
+// (query, table), per-query partials of d gamma and d w_suf) and a key pass (key-side gradients; att rebuilt from the
+// forward's saved max and denominator, each dO_q row loaded once for both dp and dV).
 #include "common.h"
 
 namespace asrn {
 
-constexpr int kMaxFPL = 8;   // features per half-wave lane: P + cf <= 256
-constexpr int kMaxDCH = 4;   // float4 chunks of 256 columns per lane: d <= 1024
 constexpr int kWavesPerBlock = 4;
+constexpr int kMaxSlots = 256;       // T * C
+constexpr int kCh = kMaxSlots / kWave;
+constexpr int kRows = 8;             // rows per half-wave in flight in the feature loops
 
 struct Cand {
   const float* phi; const float* V; const float* Qc; const float* Kc; const float* sig;
   const double* Bt; const float* la; const float* w_suf; const float* gamma;
-  const int32_t* order; const int32_t* ids_s; const int32_t* rank;
+  const int32_t* order; const int32_t* win; const int32_t* rank;
   int64_t B, L;
-  int d, P, cf, K, T, Tc, C, fpl, dch;
+  int d, P, cf, K, T, Tc, C;
+  int vec;            // P and cf multiples of 4: feature rows load as float4
   float sp, sc;
   // forward outputs
   float* salida; float* signals; float* stats;
@@ -35,172 +41,424 @@ struct Cand {
   float* dla; float* qstats; float* partials;
 };
 
-// feature f of a row: phi for f < P, then the confirmation vector (Qc for queries, Kc for keys)
-__device__ __forceinline__ float feat(const Cand& a, const float* conf, int64_t row, int f) {
-  if (f < a.P) return a.phi[row * a.P + f];
-  if (f < a.P + a.cf) return conf[row * a.cf + (f - a.P)];
-  return 0.f;
-}
+// per-wave LDS scratch: one token's candidate list (entries) and its distinct positions (uniques)
+struct Scratch {
+  int key[kMaxSlots];      // entry: (position << 5) | table
+  int uid[kMaxSlots];      // entry -> unique
+  int upos[kMaxSlots];     // unique: position
+  float ua[kMaxSlots];     // unique: base score, then (base + w_suf[ell]) + log_alfa_k
+  float ub[kMaxSlots];     // unique: fp32(Bt_k - Bt_q); the key side overwrites it with dp
+  float uc[kMaxSlots];     // unique: sum over tables of att (forward, key side) or dp (query side)
+  float ud[kMaxSlots];     // unique: sum over tables of ds
+  int uell[kMaxSlots];     // unique: suffix-match length (query side)
+  int off[40];             // entries of table tau: [off[tau], off[tau + 1])
+};
 
-// query features pre-scaled, lane layout f = (lane & 31) + 32 u
-__device__ __forceinline__ void query_feats(const Cand& a, int64_t row, float (&qf)[kMaxFPL]) {
-  const int hl = lane_id() & 31;
-#pragma unroll
-  for (int u = 0; u < kMaxFPL; ++u) {
-    const int f = hl + 32 * u;
-    float v = 0.f;
-    if (u < a.fpl) {
-      v = feat(a, a.Qc, row, f);
-      v *= f < a.P ? a.sp : a.sc;
-    }
-    qf[u] = v;
-  }
-}
-
-__device__ __forceinline__ void key_feats(const Cand& a, int64_t row, float (&kf)[kMaxFPL]) {
-  const int hl = lane_id() & 31;
-#pragma unroll
-  for (int u = 0; u < kMaxFPL; ++u) kf[u] = u < a.fpl ? feat(a, a.Kc, row, hl + 32 * u) : 0.f;
-}
-
-__device__ __forceinline__ float dot_feats(const float (&x)[kMaxFPL], const float (&y)[kMaxFPL], int fpl) {
-  float s = 0.f;
-#pragma unroll
-  for (int u = 0; u < kMaxFPL; ++u)
-    if (u < fpl) s += x[u] * y[u];
-  return s;
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float dot4(const float4& x, const float4& y) {
+  return x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
+}
+__device__ __forceinline__ void fma4(float4& acc, float w, const float4& v) {
+  acc.x += w * v.x; acc.y += w * v.y; acc.z += w * v.z; acc.w += w * v.w;
+}
+__device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
 
-// per-table candidate window of query (b, t): lane i < C holds candidate i of [s - C, s) if valid
-struct Window {
-  int64_t rowr;   // b*T + tau
-  int s;
-  bool valid;
-  int32_t k;      // text position of this lane's candidate (0 when invalid)
-  int nvalid, first;
+// Features 128 c + 4 (lane & 31) .. + 3 of a row: phi for x < P, then the confirmation vector (Qc for queries, Kc
+// for keys); queries pre-scaled by scale_phi / scale_c. One float4 load per chunk when P and cf are multiples of 4.
+template <int F4>
+__device__ __forceinline__ void feats(const Cand& a, const float* conf, int64_t row, bool scaled, float4 (&f)[F4]) {
+  const int x0 = 4 * (lane_id() & 31);
+  const int F = a.P + a.cf;
+#pragma unroll
+  for (int c = 0; c < F4; ++c) {
+    const int x = x0 + 128 * c;
+    float4 v = zero4();
+    if (a.vec) {
+      const float* p = x < a.P ? a.phi + row * a.P + x : conf + row * a.cf + (x - a.P);
+      if (x < F) v = ld4(p);
+      if (scaled) {
+        const float s = x < a.P ? a.sp : a.sc;
+        v.x *= s; v.y *= s; v.z *= s; v.w *= s;
+      }
+    } else {
+      float e[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int xi = x + i;
+        float w = 0.f;
+        if (xi < a.P) w = scaled ? a.phi[row * a.P + xi] * a.sp : a.phi[row * a.P + xi];
+        else if (xi < F) w = scaled ? conf[row * a.cf + (xi - a.P)] * a.sc : conf[row * a.cf + (xi - a.P)];
+        e[i] = w;
+      }
+      v = make_float4(e[0], e[1], e[2], e[3]);
+    }
+    f[c] = v;
+  }
+}
+
+template <int F4>
+__device__ __forceinline__ float dot_f(const float4 (&q)[F4], const float4 (&k)[F4]) {
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < F4; ++c) s += dot4(q[c], k[c]);
+  return s;
+}
+
+__device__ __forceinline__ float rate_of(const Cand& a, int tau) { return a.gamma[tau] / (float)a.C; }
+
+// The token's own previous signatures sig[self - 1 - j], j < K (uniform across the wave).
+__device__ __forceinline__ void own_suffix(const float* __restrict__ sigb, int64_t self_pos, int K, float (&mine)[16]) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) mine[j] = (j < K && self_pos - 1 - j >= 0) ? sigb[self_pos - 1 - j] : 0.f;
+}
+
+// Suffix match of `other` against the token's own previous signatures (K <= 16): the number of leading j with
+// sig[other - 1 - j] == sig[self - 1 - j], both in range; NaN never matches (reference nucleo:98-108, 313-320).
+__device__ __forceinline__ int suffix_vs(const float* __restrict__ sigb, const float (&mine)[16], int64_t self_pos,
+                                        int64_t other, int K) {
+  int ell = 0;
+  bool run = true;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    if (j < K) {
+      const int64_t io = other - 1 - j;
+      const float v = sigb[io >= 0 ? io : 0];
+      run = run && io >= 0 && self_pos - 1 - j >= 0 && v == mine[j];
+      ell += run ? 1 : 0;
+    }
+  }
+  return ell;
+}
+
+// Packs every table's window of token (b, t) into S.key and the table segments into S.off. query_window: the
+// `win & 255` sorted ranks before the token's; otherwise (the key pass) the `win >> 8` after it. Returns the count.
+__device__ __forceinline__ int gather(const Cand& a, int64_t b, int64_t t, bool query_window, Scratch& S) {
+  const int lane = lane_id();
+  int s = 0, n = 0;
+  if (lane < a.T) {
+    const int64_t o = (b * a.L + t) * a.T + lane;
+    s = a.rank[o];
+    const int w = a.win[o];
+    n = query_window ? (w & 255) : ((w >> 8) & 255);
+  }
+  const int slots = a.T * a.C;
+  int pos[kCh], tt[kCh];
+  bool ok[kCh];
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const int sl = c * kWave + lane;
+    const int tau = sl < slots ? sl / a.C : 0;
+    const int i = sl - tau * a.C;
+    const int st = __shfl(s, tau, 64), nt = __shfl(n, tau, 64);
+    // query window: slots [C - n, C) hold ranks s - n .. s - 1; key window: slots [0, n) hold s + 1 .. s + n
+    const bool v = sl < slots && (query_window ? i >= a.C - nt : i < nt);
+    const int64_t j = query_window ? (int64_t)st - a.C + i : (int64_t)st + 1 + i;
+    ok[c] = v && j >= 0 && j < a.L;
+    tt[c] = tau;
+    pos[c] = ok[c] ? a.order[(b * a.T + tau) * a.L + j] : 0;
+  }
+  int base = 0;
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const uint64_t bal = __ballot(ok[c]);
+    if (ok[c]) S.key[base + __popcll(bal & ((1ull << lane) - 1ull))] = (pos[c] << 5) | tt[c];
+    base += __popcll(bal);
+  }
+  wave_lds_sync();
+  if (lane <= a.T) {
+    int lo = 0, hi = base;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if ((S.key[mid] & 31) < lane) lo = mid + 1; else hi = mid;
+    }
+    S.off[lane] = lo;
+  }
+  wave_lds_sync();
+  return base;
+}
+
+// One slot per distinct position, in order of first appearance (table-major): S.uid[entry], S.upos[unique].
+// Deterministic: an entry is the first of its position when no earlier table's segment holds it.
+__device__ __forceinline__ int dedupe(const Cand& a, int M, Scratch& S) {
+  const int lane = lane_id();
+  int nu = 0;
+  for (int m0 = 0; m0 < M; m0 += kWave) {
+    const int m = m0 + lane;
+    const bool in = m < M;
+    int first = -1, pos = 0;
+    if (in) {
+      const int e = S.key[m];
+      pos = e >> 5;
+      const int tau = e & 31;
+      for (int tp = 0; tp < tau && first < 0; ++tp) {
+        int lo = S.off[tp], hi = S.off[tp + 1];
+        const int end = hi;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if ((S.key[mid] >> 5) < pos) lo = mid + 1; else hi = mid;
+        }
+        if (lo < end && (S.key[lo] >> 5) == pos) first = lo;
+      }
+    }
+    const bool prim = in && first < 0;
+    const uint64_t bal = __ballot(prim);
+    if (prim) {
+      const int u = nu + __popcll(bal & ((1ull << lane) - 1ull));
+      S.uid[m] = u;
+      S.upos[u] = pos;
+    }
+    nu += __popcll(bal);
+    wave_lds_sync();
+    if (in && first >= 0) S.uid[m] = S.uid[first];
+    wave_lds_sync();
+  }
+  return nu;
+}
+
+// (In these helpers self_pos is the token's own position inside batch row b: the row idle lanes read.)
+//
+// base scores <query, key> of every unique, 2*kRows rows in flight (kRows per half-wave). query side: fixed = the
+// query's scaled features and the rows are keys; key side: fixed = the key's raw features, rows = queries (scaled).
+// The product is always query * key and the reduction tree is the same, so both sides produce the same bits.
+template <int F4>
+__device__ __forceinline__ void unique_bases(const Cand& a, int64_t b, int64_t self_pos, int NU,
+                                             bool rows_are_queries, const float4 (&fixed)[F4], Scratch& S) {
+  const int lane = lane_id(), half = lane >> 5;
+  const float* conf = rows_are_queries ? a.Qc : a.Kc;
+  for (int u0 = 0; u0 < NU; u0 += 2 * kRows) {
+    float4 f[kRows][F4];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      const int u = u0 + 2 * r + half;
+      feats<F4>(a, conf, b * a.L + (u < NU ? S.upos[u] : self_pos), rows_are_queries, f[r]);
+    }
+    float p[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) p[r] = rows_are_queries ? dot_f(f[r], fixed) : dot_f(fixed, f[r]);
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      float h0, h1;
+      half_sums_u(p[r], &h0, &h1);
+      const int u = u0 + 2 * r;
+      if (lane == 0) {
+        if (u < NU) S.ua[u] = h0;
+        if (u + 1 < NU) S.ua[u + 1] = h1;
+      }
+    }
+  }
+  wave_lds_sync();
+}
+
+// sum_u w_u * row_u over the uniques' features (kRows rows per half-wave in flight), both halves combined.
+template <int F4>
+__device__ __forceinline__ void unique_feature_sum(const Cand& a, int64_t b, int64_t self_pos, int NU,
+                                                   bool rows_are_queries, const float* wts, Scratch& S,
+                                                   float4 (&g)[F4]) {
+  const int half = lane_id() >> 5;
+  const float* conf = rows_are_queries ? a.Qc : a.Kc;
+#pragma unroll
+  for (int c = 0; c < F4; ++c) g[c] = zero4();
+  for (int u0 = 0; u0 < NU; u0 += 2 * kRows) {
+    float4 f[kRows][F4];
+    float w[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      const int u = u0 + 2 * r + half;
+      const bool ok = u < NU;
+      feats<F4>(a, conf, b * a.L + (ok ? S.upos[u] : self_pos), rows_are_queries, f[r]);
+      w[r] = ok ? wts[u] : 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < kRows; ++r)
+#pragma unroll
+      for (int c = 0; c < F4; ++c) fma4(g[c], w[r], f[r][c]);
+  }
+#pragma unroll
+  for (int c = 0; c < F4; ++c) {
+    g[c].x += __shfl_xor(g[c].x, 32, 64);
+    g[c].y += __shfl_xor(g[c].y, 32, 64);
+    g[c].z += __shfl_xor(g[c].z, 32, 64);
+    g[c].w += __shfl_xor(g[c].w, 32, 64);
+  }
+}
+
+// <fixed, row_u> over the d columns for every unique (rows of batch row `rows`), R rows in flight, written to
+// out[u]; the key side (w_u != nullptr) also accumulates dV += w_u row_u from the same loads.
+template <int DCH>
+__device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows, int64_t self_pos, int NU,
+                                                const float4 (&fixed)[DCH], const float* w_u, float4 (&dv)[DCH],
+                                                Scratch& S, float* out) {
+  const int lane = lane_id();
+  constexpr int R = DCH >= 3 ? 2 : (DCH == 2 ? 4 : 8);
+  for (int u0 = 0; u0 < NU; u0 += R) {
+    float4 o[R][DCH];
+    float w[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int u = u0 + r;
+      const bool ok = u < NU;
+      const int64_t row = ok ? S.upos[u] : self_pos;
+      w[r] = (ok && w_u) ? w_u[u] : 0.f;
+#pragma unroll
+      for (int ch = 0; ch < DCH; ++ch) {
+        const int dd = ch * 256 + lane * 4;
+        o[r][ch] = dd < a.d ? ld4(rows + row * a.d + dd) : zero4();
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float p = 0.f;
+#pragma unroll
+      for (int ch = 0; ch < DCH; ++ch) {
+        p += dot4(o[r][ch], fixed[ch]);
+        if (w_u) fma4(dv[ch], w[r], o[r][ch]);
+      }
+      const float tot = wave_sum_u(p);
+      if (lane == 0 && u0 + r < NU) out[u0 + r] = tot;
+    }
+  }
+  wave_lds_sync();
+}
+
+// Entries of the candidate list held one per lane (entry c*64 + lane in chunk c).
+struct Entries {
+  int u[kCh];        // unique of the entry
+  int tau[kCh];      // table (-1 when the slot is empty)
+  float sc[kCh];     // score
 };
 
-__device__ __forceinline__ Window query_window(const Cand& a, int64_t b, int64_t t, int tau) {
-  Window w;
+__device__ __forceinline__ void load_entries(const Cand& a, int M, const Scratch& S, Entries& E) {
   const int lane = lane_id();
-  w.rowr = b * a.T + tau;
-  w.s = a.rank[(b * a.L + t) * a.T + tau];
-  const int32_t* ids = a.ids_s + w.rowr * a.L;
-  const int my = ids[w.s];
-  const int j = w.s - a.C + lane;
-  w.valid = lane < a.C && j >= 0 && ids[j] == my;
-  w.k = w.valid ? a.order[w.rowr * a.L + j] : 0;
-  w.nvalid = __popcll(__ballot(w.valid));
-  w.first = a.C - w.nvalid;
-  return w;
-}
-
-// score extras of lane candidate k against query q (text positions of batch row b):
-//   ((base + w_suf[ell]) + log_alfa_k) + rate * fp32(Bt_k - Bt_q)     (reference estable:249-258)
-__device__ __forceinline__ float score_of(const Cand& a, int64_t b, int64_t q, int64_t k, float base, float rate,
-                                          float* dt_out, int* ell_out) {
-  const float* sigb = a.sig + b * a.L;
-  const int ell = suffix_match(sigb, q, k, a.K);
-  const float dt = (float)(a.Bt[b * a.L + k] - a.Bt[b * a.L + q]);
-  if (dt_out) *dt_out = dt;
-  if (ell_out) *ell_out = ell;
-  return ((base + a.w_suf[ell]) + a.la[b * a.L + k]) + rate * dt;
-}
-
-// base scores <q, k_i> of the valid candidates of a window, two per step (one per half-wave)
-__device__ __forceinline__ float window_bases(const Cand& a, int64_t b, const Window& w, const float (&qf)[kMaxFPL]) {
-  const int lane = lane_id();
-  const int half = lane >> 5;
-  float mine = 0.f;
-  for (int c = 0; c < w.nvalid; c += 2) {
-    const int i0 = w.first + c, i1 = i0 + 1;
-    const int k0 = readlane_i(w.k, i0);
-    const int k1 = readlane_i(w.k, i1 < a.C ? i1 : i0);
-    const int64_t kk = half ? k1 : k0;
-    float kf[kMaxFPL];
-    key_feats(a, b * a.L + kk, kf);
-    const float tot = half_sum(dot_feats(qf, kf, a.fpl));
-    const float t0 = readlane_f(tot, 0), t1 = readlane_f(tot, 32);
-    if (lane == i0) mine = t0;
-    if (lane == i1) mine = t1;
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const int m = c * kWave + lane;
+    const bool in = m < M;
+    const int e = in ? S.key[m] : 0;
+    E.tau[c] = in ? (e & 31) : -1;
+    const int u = in ? S.uid[m] : 0;
+    E.u[c] = u;
+    E.sc[c] = in ? S.ua[u] + rate_of(a, e & 31) * S.ub[u] : -INFINITY;
   }
-  return mine;
+}
+
+// Exact masked softmax of every table over its entries: mx/den per entry's table and att per entry. The per-table
+// max and sum are DPP wave reductions restricted to the chunks the table's segment spans.
+struct TableStats {
+  float mx, den;
+};
+
+__device__ __forceinline__ TableStats table_softmax(const Entries& E, int tau, int lo, int hi) {
+  const int c0 = lo / kWave, c1 = (hi - 1) / kWave;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < kCh; ++c)
+    if (c >= c0 && c <= c1) mx = fmaxf(mx, wave_max_u(E.tau[c] == tau ? E.sc[c] : -INFINITY));
+  float den = 0.f;
+#pragma unroll
+  for (int c = 0; c < kCh; ++c)
+    if (c >= c0 && c <= c1) den += wave_sum_u(E.tau[c] == tau ? expf(E.sc[c] - mx) : 0.f);
+  return {mx, den};
+}
+
+// the two table segments' bounds for table tau, read from the lane-held copy of S.off
+__device__ __forceinline__ void segment(int offv, int tau, int* lo, int* hi) {
+  *lo = readlane_i(offv, tau);
+  *hi = readlane_i(offv, tau + 1);
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------------------------------------------------
+template <int F4, int DCH>
 __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_fwd(Cand a) {
+  __shared__ Scratch scratch[kWavesPerBlock];
+  Scratch& S = scratch[threadIdx.x >> 6];
   const int64_t tok = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   if (tok >= a.B * a.L) return;
   const int lane = lane_id();
   const int64_t b = tok / a.L, t = tok % a.L;
-  float qf[kMaxFPL];
-  query_feats(a, tok, qf);
-  float4 acc[kMaxDCH];
-#pragma unroll
-  for (int ch = 0; ch < kMaxDCH; ++ch) acc[ch] = make_float4(0.f, 0.f, 0.f, 0.f);
-  float pt = 0.f, best = -INFINITY, pico = 0.f, pctx = 0.f;
-  const float* Vb = a.V + b * a.L * a.d;
 
+  const int M = gather(a, b, t, true, S);
+  const int NU = dedupe(a, M, S);
+  float4 qf[F4];
+  feats<F4>(a, a.Qc, tok, true, qf);
+  unique_bases<F4>(a, b, t, NU, false, qf, S);
+  const float* sigb = a.sig + b * a.L;
+  float mine[16];
+  own_suffix(sigb, t, a.K, mine);
+  const double bq = a.Bt[tok];
+  for (int u = lane; u < NU; u += kWave) {
+    const int64_t k = S.upos[u];
+    const int ell = suffix_vs(sigb, mine, t, k, a.K);
+    S.ua[u] = (S.ua[u] + a.w_suf[ell]) + a.la[b * a.L + k];
+    S.ub[u] = (float)(a.Bt[b * a.L + k] - bq);
+    S.uc[u] = 0.f;
+  }
+  wave_lds_sync();
+
+  Entries E;
+  load_entries(a, M, S, E);
+  const int offv = lane <= a.T ? S.off[lane] : 0;
+  float pt = 0.f, best = -INFINITY, pico = 0.f, pctx = 0.f;
   for (int tau = 0; tau < a.T; ++tau) {
-    const Window w = query_window(a, b, t, tau);
-    const float rate = a.gamma[tau] / (float)a.C;
-    const float base = window_bases(a, b, w, qf);
-    const float sc = w.valid ? score_of(a, b, t, w.k, base, rate, nullptr, nullptr) : -INFINITY;
-    const bool hay = w.nvalid > 0;
-    const float m = wave_max(sc);
-    const float e = w.valid ? expf(sc - m) : 0.f;
-    const float den = wave_sum(e);
-    const float att = w.valid ? e / den : 0.f;
-    const float peak = wave_max(att);
+    int lo, hi;
+    segment(offv, tau, &lo, &hi);
+    float* st = a.stats + (tok * a.T + tau) * 2;
+    if (lo == hi) {
+      if (lane == 0) {
+        st[0] = 0.f;
+        st[1] = 1.f;
+      }
+      continue;
+    }
+    const TableStats ts = table_softmax(E, tau, lo, hi);
+#pragma unroll
+    for (int c = 0; c < kCh; ++c)
+      if (E.tau[c] == tau) S.uc[E.u[c]] += expf(E.sc[c] - ts.mx) / ts.den;   // uniques are distinct in a table
     if (lane == 0) {
-      float* st = a.stats + (tok * a.T + tau) * 2;
-      st[0] = hay ? m : 0.f;
-      st[1] = hay ? den : 1.f;
+      st[0] = ts.mx;
+      st[1] = ts.den;
     }
-    if (hay) {
-      pt += 1.f;
-      best = fmaxf(best, m);
-      pico += peak;
-      if (tau >= a.T - a.Tc) pctx += 1.f;
-    }
-    // copy-gather: sum_k att_k V_k, four candidate rows in flight
-    for (int c = 0; c < w.nvalid; c += 4) {
-      int kc[4];
-      float ac[4];
+    pt += 1.f;
+    best = fmaxf(best, ts.mx);
+    pico += 1.f / ts.den;            // the largest weight: exp(mx - mx) / den
+    if (tau >= a.T - a.Tc) pctx += 1.f;
+    wave_lds_sync();
+  }
+
+  // copy-gather over the distinct candidates: sum_u (sum_tau att) V_u, UNR rows in flight
+  constexpr int UNR = DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 16);
+  float4 acc[DCH];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const bool ok = c + u < w.nvalid;
-        const int ic = ok ? w.first + c + u : w.first;
-        kc[u] = readlane_i(w.k, ic);
-        const float av = readlane_f(att, ic);
-        ac[u] = ok ? av : 0.f;
-      }
+  for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
+  const float* Vb = a.V + b * a.L * a.d;
+  for (int u0 = 0; u0 < NU; u0 += UNR) {
+    float4 v[UNR][DCH];
+    float w[UNR];
 #pragma unroll
-      for (int ch = 0; ch < kMaxDCH; ++ch) {
-        if (ch >= a.dch) break;
+    for (int r = 0; r < UNR; ++r) {
+      const bool ok = u0 + r < NU;
+      const int64_t p = ok ? S.upos[u0 + r] : t;
+      w[r] = ok ? S.uc[u0 + r] : 0.f;
+#pragma unroll
+      for (int ch = 0; ch < DCH; ++ch) {
         const int dd = ch * 256 + lane * 4;
-        if (dd < a.d) {
-          float4 v[4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) v[u] = ld4(Vb + (int64_t)kc[u] * a.d + dd);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            acc[ch].x += ac[u] * v[u].x;
-            acc[ch].y += ac[u] * v[u].y;
-            acc[ch].z += ac[u] * v[u].z;
-            acc[ch].w += ac[u] * v[u].w;
-          }
-        }
+        v[r][ch] = dd < a.d ? ld4(Vb + p * a.d + dd) : zero4();
       }
     }
+#pragma unroll
+    for (int r = 0; r < UNR; ++r)
+#pragma unroll
+      for (int ch = 0; ch < DCH; ++ch) fma4(acc[ch], w[r], v[r][ch]);
   }
 #pragma unroll
-  for (int ch = 0; ch < kMaxDCH; ++ch) {
-    if (ch >= a.dch) break;
+  for (int ch = 0; ch < DCH; ++ch) {
     const int dd = ch * 256 + lane * 4;
     if (dd < a.d) *reinterpret_cast<float4*>(a.salida + tok * a.d + dd) = acc[ch];
   }
@@ -213,122 +471,119 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_fwd(Cand a) {
   }
 }
 
-// dot of a 64-lane float4 row chunk set with a register copy, two rows reduced together:
-// returns in every lane: lanes < 32 carry the sum for row 0, lanes >= 32 for row 1 (after half_sum)
-__device__ __forceinline__ float pair_reduce(float p0, float p1) {
-  const int lane = lane_id();
-  const float keep = lane < 32 ? p0 : p1;
-  const float give = lane < 32 ? p1 : p0;
-  return half_sum(keep + __shfl_xor(give, 32, 64));
-}
-
-__device__ __forceinline__ float dot4(const float4& x, const float4& y) {
-  return x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
-}
-
 // ---------------------------------------------------------------------------------------------------------------------
 // backward, query pass
 // ---------------------------------------------------------------------------------------------------------------------
+template <int F4, int DCH>
 __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
+  __shared__ Scratch scratch[kWavesPerBlock];
+  Scratch& S = scratch[threadIdx.x >> 6];
   const int64_t tok = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   if (tok >= a.B * a.L) return;
-  const int lane = lane_id();
-  const int half = lane >> 5;
+  const int lane = lane_id(), half = lane >> 5;
   const int64_t b = tok / a.L, t = tok % a.L;
-  float qf[kMaxFPL], gq[kMaxFPL];
-  query_feats(a, tok, qf);
-#pragma unroll
-  for (int u = 0; u < kMaxFPL; ++u) gq[u] = 0.f;
-  float4 dO[kMaxDCH];
-#pragma unroll
-  for (int ch = 0; ch < kMaxDCH; ++ch) {
-    const int dd = ch * 256 + lane * 4;
-    dO[ch] = (ch < a.dch && dd < a.d) ? ld4(a.dsal + tok * a.d + dd) : make_float4(0.f, 0.f, 0.f, 0.f);
+
+  const int M = gather(a, b, t, true, S);
+  const int NU = dedupe(a, M, S);
+  float4 qf[F4];
+  feats<F4>(a, a.Qc, tok, true, qf);
+  unique_bases<F4>(a, b, t, NU, false, qf, S);
+  const float* sigb = a.sig + b * a.L;
+  float mine[16];
+  own_suffix(sigb, t, a.K, mine);
+  const double bq = a.Bt[tok];
+  for (int u = lane; u < NU; u += kWave) {
+    const int64_t k = S.upos[u];
+    const int ell = suffix_vs(sigb, mine, t, k, a.K);
+    S.ua[u] = (S.ua[u] + a.w_suf[ell]) + a.la[b * a.L + k];
+    S.ub[u] = (float)(a.Bt[b * a.L + k] - bq);
+    S.ud[u] = 0.f;
+    S.uell[u] = ell;
   }
-  const float* Vb = a.V + b * a.L * a.d;
+  wave_lds_sync();
+
+  // dp_u = <dO_q, V_u>
+  float4 dO[DCH], unused[DCH];
+#pragma unroll
+  for (int ch = 0; ch < DCH; ++ch) {
+    const int dd = ch * 256 + lane * 4;
+    dO[ch] = dd < a.d ? ld4(a.dsal + tok * a.d + dd) : zero4();
+    unused[ch] = zero4();
+  }
+  unique_row_dots<DCH>(a, a.V + b * a.L * a.d, t, NU, dO, nullptr, unused, S, S.uc);
+
+  Entries E;
+  load_entries(a, M, S, E);
+  const int offv = lane <= a.T ? S.off[lane] : 0;
+  float* part = a.partials + tok * (a.T + a.K + 1);
   float dbq = 0.f;
   float dw[17];
 #pragma unroll
   for (int c = 0; c < 17; ++c) dw[c] = 0.f;
-  float* part = a.partials + tok * (a.T + a.K + 1);
-
   for (int tau = 0; tau < a.T; ++tau) {
-    const Window w = query_window(a, b, t, tau);
-    const float rate = a.gamma[tau] / (float)a.C;
-    const float base = window_bases(a, b, w, qf);
-    float dt = 0.f;
-    int ell = 0;
-    const float sc = w.valid ? score_of(a, b, t, w.k, base, rate, &dt, &ell) : -INFINITY;
-    const float m = wave_max(sc);
-    const float e = w.valid ? expf(sc - m) : 0.f;
-    const float den = wave_sum(e);
-    const float att = w.valid ? e / den : 0.f;
-    // dp_i = <dO_q, V_k_i>, two candidates per reduction
-    float dp = 0.f;
-    for (int c = 0; c < w.nvalid; c += 2) {
-      const int i0 = w.first + c;
-      const bool two = c + 1 < w.nvalid;
-      const int i1 = two ? i0 + 1 : i0;
-      const int k0 = readlane_i(w.k, i0);
-      const int k1 = readlane_i(w.k, i1);
-      float p0 = 0.f, p1 = 0.f;
-#pragma unroll
-      for (int ch = 0; ch < kMaxDCH; ++ch) {
-        const int dd = ch * 256 + lane * 4;
-        if (ch < a.dch && dd < a.d) {
-          p0 += dot4(dO[ch], ld4(Vb + (int64_t)k0 * a.d + dd));
-          if (two) p1 += dot4(dO[ch], ld4(Vb + (int64_t)k1 * a.d + dd));
-        }
+    int lo, hi;
+    segment(offv, tau, &lo, &hi);
+    if (lo == hi) {
+      if (lane == 0) {
+        a.qstats[tok * a.T + tau] = 0.f;
+        part[tau] = 0.f;
       }
-      const float r = pair_reduce(p0, p1);
-      const float r0 = readlane_f(r, 0), r1 = readlane_f(r, 32);
-      if (lane == i0) dp = r0;
-      if (two && lane == i1) dp = r1;
+      continue;
     }
-    const float D = wave_sum(att * dp);
-    const float ds = w.valid ? att * (dp - D) : 0.f;
-    if (lane == 0) a.qstats[tok * a.T + tau] = D;
-    const float sds = wave_sum(ds);
-    dbq += -rate * sds;
-    const float sdt = wave_sum(ds * dt);
-    if (lane == 0) part[tau] = sdt;
+    const TableStats ts = table_softmax(E, tau, lo, hi);
+    const int c0 = lo / kWave, c1 = (hi - 1) / kWave;
+    float att[kCh], dp[kCh];
+    float D = 0.f;
 #pragma unroll
-    for (int c = 0; c < 17; ++c)
-      if (c <= a.K && ell == c) dw[c] += ds;
-    // d phi_q, d Qc_q: sum_i ds_i [phi_k ; Kc_k], one candidate per half-wave
-    for (int c = 0; c < w.nvalid; c += 2) {
-      const int i0 = w.first + c;
-      const bool two = c + 1 < w.nvalid;
-      const int i1 = two ? i0 + 1 : i0;
-      const int k0 = readlane_i(w.k, i0);
-      const int k1 = readlane_i(w.k, i1);
-      const float s0 = readlane_f(ds, i0);
-      const float s1v = readlane_f(ds, i1);
-      const float s1 = two ? s1v : 0.f;
-      const int64_t kk = half ? k1 : k0;
-      const float sk = half ? s1 : s0;
-      float kf[kMaxFPL];
-      key_feats(a, b * a.L + kk, kf);
-#pragma unroll
-      for (int u = 0; u < kMaxFPL; ++u) gq[u] += sk * kf[u];
+    for (int c = 0; c < kCh; ++c) {
+      const bool in = E.tau[c] == tau;
+      att[c] = in ? expf(E.sc[c] - ts.mx) / ts.den : 0.f;
+      dp[c] = in ? S.uc[E.u[c]] : 0.f;
+      if (c >= c0 && c <= c1) D += wave_sum_u(att[c] * dp[c]);
     }
+    float sds = 0.f, sdt = 0.f;
+#pragma unroll
+    for (int c = 0; c < kCh; ++c) {
+      const bool in = E.tau[c] == tau;
+      const float ds = in ? att[c] * (dp[c] - D) : 0.f;
+      const float dt = in ? S.ub[E.u[c]] : 0.f;
+      const int ell = in ? S.uell[E.u[c]] : -1;
+      if (in) S.ud[E.u[c]] += ds;
+      if (c >= c0 && c <= c1) {
+        sds += wave_sum_u(ds);
+        sdt += wave_sum_u(ds * dt);
+      }
+#pragma unroll
+      for (int x = 0; x < 17; ++x)
+        if (ell == x) dw[x] += ds;
+    }
+    dbq += -rate_of(a, tau) * sds;
+    if (lane == 0) {
+      a.qstats[tok * a.T + tau] = D;
+      part[tau] = sdt;
+    }
+    wave_lds_sync();
   }
-  // combine the two halves and write the query-side gradients
-#pragma unroll
-  for (int u = 0; u < kMaxFPL; ++u) gq[u] += __shfl_xor(gq[u], 32, 64);
+
+  // d phi_q, d Qc_q = sum_u (sum_tau ds) [phi_u ; Kc_u]
+  float4 gq[F4];
+  unique_feature_sum<F4>(a, b, t, NU, false, S.ud, S, gq);
   if (half == 0) {
+    const int x0 = 4 * lane;
 #pragma unroll
-    for (int u = 0; u < kMaxFPL; ++u) {
-      const int f = lane + 32 * u;
-      if (u < a.fpl) {
-        if (f < a.P) a.dphi[tok * a.P + f] = gq[u] * a.sp;
-        else if (f < a.P + a.cf) a.dQc[tok * a.cf + (f - a.P)] = gq[u] * a.sc;
+    for (int c = 0; c < F4; ++c) {
+      const float g[4] = {gq[c].x, gq[c].y, gq[c].z, gq[c].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int f = x0 + 128 * c + i;
+        if (f < a.P) a.dphi[tok * a.P + f] = g[i] * a.sp;
+        else if (f < a.P + a.cf) a.dQc[tok * a.cf + (f - a.P)] = g[i] * a.sc;
       }
     }
   }
-  for (int c = 0; c <= a.K && c < 17; ++c) {
-    const float v = wave_sum(dw[c]);
-    if (lane == 0) part[a.T + c] = v;
+  for (int x = 0; x <= a.K && x < 17; ++x) {
+    const float v = wave_sum_u(dw[x]);
+    if (lane == 0) part[a.T + x] = v;
   }
   if (lane == 0) a.dBt[tok] = (double)dbq;
 }
@@ -336,176 +591,208 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
 // ---------------------------------------------------------------------------------------------------------------------
 // backward, key pass
 // ---------------------------------------------------------------------------------------------------------------------
+template <int F4, int DCH>
 __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_k(Cand a) {
+  __shared__ Scratch scratch[kWavesPerBlock];
+  Scratch& S = scratch[threadIdx.x >> 6];
   const int64_t tok = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   if (tok >= a.B * a.L) return;
-  const int lane = lane_id();
-  const int half = lane >> 5;
+  const int lane = lane_id(), half = lane >> 5;
   const int64_t b = tok / a.L, k = tok % a.L;
-  float kf[kMaxFPL], gk[kMaxFPL];
-  key_feats(a, tok, kf);
-#pragma unroll
-  for (int u = 0; u < kMaxFPL; ++u) gk[u] = 0.f;
-  float4 vk[kMaxDCH], dv[kMaxDCH];
-#pragma unroll
-  for (int ch = 0; ch < kMaxDCH; ++ch) {
-    const int dd = ch * 256 + lane * 4;
-    vk[ch] = (ch < a.dch && dd < a.d) ? ld4(a.V + tok * a.d + dd) : make_float4(0.f, 0.f, 0.f, 0.f);
-    dv[ch] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  const float* dOb = a.dsal + b * a.L * a.d;
-  float dla = 0.f, dbk = 0.f;
 
+  const int M = gather(a, b, k, false, S);
+  const int NU = dedupe(a, M, S);
+  float4 kf[F4];
+  feats<F4>(a, a.Kc, tok, false, kf);
+  unique_bases<F4>(a, b, k, NU, true, kf, S);
+  const float* sigb = a.sig + b * a.L;
+  float mine[16];
+  own_suffix(sigb, k, a.K, mine);
+  const double bk = a.Bt[tok];
+  const float lak = a.la[tok];
+  for (int u = lane; u < NU; u += kWave) {
+    const int64_t q = S.upos[u];
+    const int ell = suffix_vs(sigb, mine, k, q, a.K);
+    S.ua[u] = (S.ua[u] + a.w_suf[ell]) + lak;
+    S.ub[u] = (float)(bk - a.Bt[b * a.L + q]);
+    S.uc[u] = 0.f;
+    S.ud[u] = 0.f;
+  }
+  wave_lds_sync();
+
+  // att of every (query, table) from the forward's statistics; D of the query; sum over tables per query for dV
+  Entries E;
+  load_entries(a, M, S, E);
+  float att[kCh], Dq[kCh];
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    att[c] = 0.f;
+    Dq[c] = 0.f;
+    if (E.tau[c] >= 0) {
+      const int64_t o = (b * a.L + S.upos[E.u[c]]) * a.T + E.tau[c];
+      att[c] = expf(E.sc[c] - a.stats_in[o * 2]) / a.stats_in[o * 2 + 1];
+      Dq[c] = a.qstats[o];
+    }
+  }
+  const int offv = lane <= a.T ? S.off[lane] : 0;
   for (int tau = 0; tau < a.T; ++tau) {
-    const int64_t rowr = b * a.T + tau;
-    const int s = a.rank[tok * a.T + tau];
-    const int32_t* ids = a.ids_s + rowr * a.L;
-    const int my = ids[s];
-    const int64_t j = (int64_t)s + 1 + lane;
-    const bool valid = lane < a.C && j < a.L && ids[j] == my;
-    const int32_t q = valid ? a.order[rowr * a.L + j] : 0;
-    const int nvalid = __popcll(__ballot(valid));     // valid lanes are the prefix [0, nvalid)
-    if (nvalid == 0) continue;
-    const float rate = a.gamma[tau] / (float)a.C;
-    // base scores <q_i, k>: the query row is the one loaded per half-wave, pre-scaled as in the forward
-    float base = 0.f;
-    for (int c = 0; c < nvalid; c += 2) {
-      const int q0 = readlane_i(q, c);
-      const int q1 = readlane_i(q, c + 1 < a.C ? c + 1 : c);
-      const int64_t qq = half ? q1 : q0;
-      float qf[kMaxFPL];
-      query_feats(a, b * a.L + qq, qf);
-      const float tot = half_sum(dot_feats(qf, kf, a.fpl));
-      const float t0 = readlane_f(tot, 0), t1 = readlane_f(tot, 32);
-      if (lane == c) base = t0;
-      if (lane == c + 1) base = t1;
-    }
-    float att = 0.f, D = 0.f;
-    if (valid) {
-      const float sc = score_of(a, b, q, k, base, rate, nullptr, nullptr);
-      const float* st = a.stats_in + ((b * a.L + q) * a.T + tau) * 2;
-      att = expf(sc - st[0]) / st[1];
-      D = a.qstats[(b * a.L + q) * a.T + tau];
-    }
-    // dp_i = <dO_q_i, V_k> and dV_k += att_i dO_q_i from the same loads
-    float dp = 0.f;
-    for (int c = 0; c < nvalid; c += 2) {
-      const bool two = c + 1 < nvalid;
-      const int c1 = two ? c + 1 : c;
-      const int q0 = readlane_i(q, c);
-      const int q1 = readlane_i(q, c1);
-      const float a0 = readlane_f(att, c);
-      const float a1v = readlane_f(att, c1);
-      const float a1 = two ? a1v : 0.f;
-      float p0 = 0.f, p1 = 0.f;
+    int lo, hi;
+    segment(offv, tau, &lo, &hi);
+    if (lo == hi) continue;
 #pragma unroll
-      for (int ch = 0; ch < kMaxDCH; ++ch) {
-        const int dd = ch * 256 + lane * 4;
-        if (ch < a.dch && dd < a.d) {
-          const float4 o0 = ld4(dOb + (int64_t)q0 * a.d + dd);
-          p0 += dot4(o0, vk[ch]);
-          dv[ch].x += a0 * o0.x; dv[ch].y += a0 * o0.y; dv[ch].z += a0 * o0.z; dv[ch].w += a0 * o0.w;
-          if (two) {
-            const float4 o1 = ld4(dOb + (int64_t)q1 * a.d + dd);
-            p1 += dot4(o1, vk[ch]);
-            dv[ch].x += a1 * o1.x; dv[ch].y += a1 * o1.y; dv[ch].z += a1 * o1.z; dv[ch].w += a1 * o1.w;
-          }
-        }
-      }
-      const float r = pair_reduce(p0, p1);
-      const float r0 = readlane_f(r, 0), r1 = readlane_f(r, 32);
-      if (lane == c) dp = r0;
-      if (two && lane == c + 1) dp = r1;
-    }
-    const float ds = valid ? att * (dp - D) : 0.f;
-    dla += ds;
-    dbk += rate * ds;
-    // d phi_k, d Kc_k: sum_i ds_i [phi_q * scale_phi ; Qc_q * scale_c]
-    for (int c = 0; c < nvalid; c += 2) {
-      const bool two = c + 1 < nvalid;
-      const int c1 = two ? c + 1 : c;
-      const int q0 = readlane_i(q, c);
-      const int q1 = readlane_i(q, c1);
-      const float s0 = readlane_f(ds, c);
-      const float s1v = readlane_f(ds, c1);
-      const float s1 = two ? s1v : 0.f;
-      const int64_t qq = half ? q1 : q0;
-      const float sq = half ? s1 : s0;
-      float qf[kMaxFPL];
-      query_feats(a, b * a.L + qq, qf);
-#pragma unroll
-      for (int u = 0; u < kMaxFPL; ++u) gk[u] += sq * qf[u];
-    }
+    for (int c = 0; c < kCh; ++c)
+      if (E.tau[c] == tau) S.uc[E.u[c]] += att[c];
+    wave_lds_sync();
   }
+
+  // dp_u = <dO_q, V_k> and dV_k += (sum_tau att) dO_q from the same loads; dp overwrites ub
+  float4 vk[DCH], dv[DCH];
 #pragma unroll
-  for (int ch = 0; ch < kMaxDCH; ++ch) {
+  for (int ch = 0; ch < DCH; ++ch) {
     const int dd = ch * 256 + lane * 4;
-    if (ch < a.dch && dd < a.d) *reinterpret_cast<float4*>(a.dV + tok * a.d + dd) = dv[ch];
+    vk[ch] = dd < a.d ? ld4(a.V + tok * a.d + dd) : zero4();
+    dv[ch] = zero4();
   }
+  unique_row_dots<DCH>(a, a.dsal + b * a.L * a.d, k, NU, vk, S.uc, dv, S, S.ub);
+
+  float dla = 0.f, dbk = 0.f;
+  for (int tau = 0; tau < a.T; ++tau) {
+    int lo, hi;
+    segment(offv, tau, &lo, &hi);
+    if (lo == hi) continue;
+    const float rate = rate_of(a, tau);
 #pragma unroll
-  for (int u = 0; u < kMaxFPL; ++u) gk[u] += __shfl_xor(gk[u], 32, 64);
+    for (int c = 0; c < kCh; ++c) {
+      if (E.tau[c] == tau) {
+        const float ds = att[c] * (S.ub[E.u[c]] - Dq[c]);
+        S.ud[E.u[c]] += ds;
+        dla += ds;
+        dbk += rate * ds;
+      }
+    }
+    wave_lds_sync();
+  }
+
+  // d phi_k, d Kc_k = sum_u (sum_tau ds) [phi_q * scale_phi ; Qc_q * scale_c]
+  float4 gk[F4];
+  unique_feature_sum<F4>(a, b, k, NU, true, S.ud, S, gk);
+#pragma unroll
+  for (int ch = 0; ch < DCH; ++ch) {
+    const int dd = ch * 256 + lane * 4;
+    if (dd < a.d) *reinterpret_cast<float4*>(a.dV + tok * a.d + dd) = dv[ch];
+  }
   if (half == 0) {
+    const int x0 = 4 * lane;
 #pragma unroll
-    for (int u = 0; u < kMaxFPL; ++u) {
-      const int f = lane + 32 * u;
-      if (u < a.fpl) {
-        if (f < a.P) a.dphi[tok * a.P + f] += gk[u];
-        else if (f < a.P + a.cf) a.dKc[tok * a.cf + (f - a.P)] = gk[u];
+    for (int c = 0; c < F4; ++c) {
+      const float g[4] = {gk[c].x, gk[c].y, gk[c].z, gk[c].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int f = x0 + 128 * c + i;
+        if (f < a.P) a.dphi[tok * a.P + f] += g[i];
+        else if (f < a.P + a.cf) a.dKc[tok * a.cf + (f - a.P)] = g[i];
       }
     }
   }
-  const float sla = wave_sum(dla);
-  const float sbk = wave_sum(dbk);
+  const float sla = wave_sum_u(dla);
+  const float sbk = wave_sum_u(dbk);
   if (lane == 0) {
     a.dla[tok] = sla;
     a.dBt[tok] += (double)sbk;
   }
 }
 
-// the candidate lists the kernels walk, materialized: (B, L, T, C) text positions (-1 = none, oldest first) and
-// the suffix-match length of each against its query
+// the candidate lists the kernels walk, materialized: (B, L, T, C) text positions (-1 = empty slot; the valid
+// candidates fill the last slots, oldest first) and the suffix-match length of each against its query
 __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_lists(Cand a, int32_t* __restrict__ pos,
                                                                        int32_t* __restrict__ ell) {
+  __shared__ Scratch scratch[kWavesPerBlock];
+  Scratch& S = scratch[threadIdx.x >> 6];
   const int64_t tok = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   if (tok >= a.B * a.L) return;
   const int lane = lane_id();
   const int64_t b = tok / a.L, t = tok % a.L;
+  gather(a, b, t, true, S);
+  const float* sigb = a.sig + b * a.L;
+  float mine[16];
+  own_suffix(sigb, t, a.K, mine);
   for (int tau = 0; tau < a.T; ++tau) {
-    const Window w = query_window(a, b, t, tau);
+    const int lo = S.off[tau], n = S.off[tau + 1] - lo;
     if (lane < a.C) {
       const int64_t o = (tok * a.T + tau) * a.C + lane;
-      pos[o] = w.valid ? w.k : -1;
-      ell[o] = w.valid ? suffix_match(a.sig + b * a.L, t, w.k, a.K) : -1;
+      const int i = lane - (a.C - n);
+      const int64_t k = i >= 0 ? (S.key[lo + i] >> 5) : -1;
+      pos[o] = (int32_t)k;
+      ell[o] = i >= 0 ? suffix_vs(sigb, mine, t, k, a.K) : -1;
     }
   }
 }
 
 static int check_args(const Cand& a, const char* what) {
   ASRN_REQUIRE(a.B >= 0 && a.L >= 0, "%s: bad sizes", what);
-  ASRN_REQUIRE(a.L < (int64_t(1) << 31), "%s: L too long", what);
-  ASRN_REQUIRE(a.d >= 4 && a.d % 4 == 0 && a.d <= 256 * kMaxDCH, "%s: d=%d must be a multiple of 4 in [4, %d]",
-               what, a.d, 256 * kMaxDCH);
+  ASRN_REQUIRE(a.L < (int64_t(1) << 26), "%s: L=%lld too long (positions are packed in 26 bits)", what,
+               (long long)a.L);
+  ASRN_REQUIRE(a.d >= 4 && a.d % 4 == 0 && a.d <= 1024, "%s: d=%d must be a multiple of 4 in [4, 1024]", what, a.d);
   ASRN_REQUIRE(a.C >= 1 && a.C <= 64, "%s: chunk C=%d must be in [1, 64]", what, a.C);
-  ASRN_REQUIRE(a.P >= 1 && a.cf >= 1 && a.P + a.cf <= 32 * kMaxFPL, "%s: P + cf = %d must be <= %d", what,
-               a.P + a.cf, 32 * kMaxFPL);
+  ASRN_REQUIRE(a.T >= 1 && a.T <= 32 && a.T * a.C <= kMaxSlots && a.Tc >= 0 && a.Tc <= a.T,
+               "%s: T=%d, C=%d, Tc=%d: needs T <= 32 and T*C <= %d", what, a.T, a.C, a.Tc, kMaxSlots);
+  ASRN_REQUIRE(a.P >= 1 && a.cf >= 1 && a.P + a.cf <= 256, "%s: P + cf = %d must be <= 256", what, a.P + a.cf);
   ASRN_REQUIRE(a.K >= 0 && a.K <= 16, "%s: suffix K=%d must be in [0, 16]", what, a.K);
-  ASRN_REQUIRE(a.T >= 1 && a.T <= 32 && a.Tc >= 0 && a.Tc <= a.T, "%s: T=%d Tc=%d", what, a.T, a.Tc);
   return 0;
 }
 
 static Cand make(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                  const double* Bt, const float* la, const float* w_suf, const float* gamma, const int32_t* order,
-                 const int32_t* ids_s, const int32_t* rank, int64_t B, int64_t L, int d, int P, int cf, int K, int T,
+                 const int32_t* win, const int32_t* rank, int64_t B, int64_t L, int d, int P, int cf, int K, int T,
                  int Tc, int C, float sp, float sc) {
   Cand a = {};
   a.phi = phi; a.V = V; a.Qc = Qc; a.Kc = Kc; a.sig = sig; a.Bt = Bt; a.la = la; a.w_suf = w_suf;
-  a.gamma = gamma; a.order = order; a.ids_s = ids_s; a.rank = rank;
+  a.gamma = gamma; a.order = order; a.win = win; a.rank = rank;
   a.B = B; a.L = L; a.d = d; a.P = P; a.cf = cf; a.K = K; a.T = T; a.Tc = Tc; a.C = C;
-  a.fpl = (P + cf + 31) / 32;
-  a.dch = (d + 255) / 256;
+  a.vec = (P % 4 == 0 && cf % 4 == 0) ? 1 : 0;
   a.sp = sp; a.sc = sc;
   return a;
 }
+
+// launch a kernel template for the (float4 feature chunks per lane, d chunks) bucket of the arguments
+template <template <int, int> class Launcher>
+static int dispatch(const Cand& a, hipStream_t st) {
+  const int dch = (a.d + 255) / 256;
+  if (a.P + a.cf <= 128) {
+    switch (dch) {
+      case 1: return Launcher<1, 1>::run(a, st);
+      case 2: return Launcher<1, 2>::run(a, st);
+      case 3: return Launcher<1, 3>::run(a, st);
+      default: return Launcher<1, 4>::run(a, st);
+    }
+  }
+  switch (dch) {
+    case 1: return Launcher<2, 1>::run(a, st);
+    case 2: return Launcher<2, 2>::run(a, st);
+    case 3: return Launcher<2, 3>::run(a, st);
+    default: return Launcher<2, 4>::run(a, st);
+  }
+}
+
+static dim3 grid_of(const Cand& a) { return dim3((unsigned)((a.B * a.L + kWavesPerBlock - 1) / kWavesPerBlock)); }
+
+template <int F4, int DCH>
+struct LaunchFwd {
+  static int run(const Cand& a, hipStream_t st) {
+    hipLaunchKernelGGL((k_cand_fwd<F4, DCH>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
+    return check_launch("asrn_candidates_fwd");
+  }
+};
+
+template <int F4, int DCH>
+struct LaunchBwd {
+  static int run(const Cand& a, hipStream_t st) {
+    hipLaunchKernelGGL((k_cand_bwd_q<F4, DCH>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
+    if (check_launch("asrn_candidates_bwd/query")) return 1;
+    hipLaunchKernelGGL((k_cand_bwd_k<F4, DCH>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
+    return check_launch("asrn_candidates_bwd/key");
+  }
+};
 
 }  // namespace asrn
 
@@ -513,52 +800,44 @@ using namespace asrn;
 
 extern "C" int asrn_candidates_fwd(const float* phi, const float* V, const float* Qc, const float* Kc,
                                    const float* sig, const double* Bt, const float* log_alfa, const float* w_suf,
-                                   const float* gamma, const int32_t* order, const int32_t* ids_sorted,
-                                   const int32_t* rank, int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf,
-                                   int32_t K, int32_t T, int32_t Tc, int32_t C, float scale_phi, float scale_c,
-                                   float* salida, float* signals, float* stats, void* stream) {
-  Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, ids_sorted, rank, B, L, d, P, cf, K, T, Tc,
-                C, scale_phi, scale_c);
+                                   const float* gamma, const int32_t* order, const int32_t* win, const int32_t* rank,
+                                   int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
+                                   int32_t Tc, int32_t C, float scale_phi, float scale_c, float* salida,
+                                   float* signals, float* stats, void* stream) {
+  Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
+                scale_phi, scale_c);
   if (check_args(a, "asrn_candidates_fwd")) return 1;
   if (B == 0 || L == 0) return 0;
   a.salida = salida; a.signals = signals; a.stats = stats;
-  const int64_t blocks = (B * L + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipLaunchKernelGGL(k_cand_fwd, dim3((unsigned)blocks), dim3(kWave * kWavesPerBlock), 0, (hipStream_t)stream, a);
-  return check_launch("asrn_candidates_fwd");
+  return dispatch<LaunchFwd>(a, (hipStream_t)stream);
 }
 
 extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const float* Kc,
                                    const float* sig, const double* Bt, const float* log_alfa, const float* w_suf,
-                                   const float* gamma, const int32_t* order, const int32_t* ids_sorted,
-                                   const int32_t* rank, int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf,
-                                   int32_t K, int32_t T, int32_t Tc, int32_t C, float scale_phi, float scale_c,
-                                   const float* dsalida, const float* stats, float* dphi, float* dV, float* dQc,
-                                   float* dKc, double* dBt, float* dlog_alfa, float* qstats, float* partials,
-                                   void* stream) {
-  Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, ids_sorted, rank, B, L, d, P, cf, K, T, Tc,
-                C, scale_phi, scale_c);
+                                   const float* gamma, const int32_t* order, const int32_t* win, const int32_t* rank,
+                                   int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
+                                   int32_t Tc, int32_t C, float scale_phi, float scale_c, const float* dsalida,
+                                   const float* stats, float* dphi, float* dV, float* dQc, float* dKc, double* dBt,
+                                   float* dlog_alfa, float* qstats, float* partials, void* stream) {
+  Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
+                scale_phi, scale_c);
   if (check_args(a, "asrn_candidates_bwd")) return 1;
   if (B == 0 || L == 0) return 0;
   a.dsal = dsalida; a.stats_in = stats; a.dphi = dphi; a.dV = dV; a.dQc = dQc; a.dKc = dKc; a.dBt = dBt;
   a.dla = dlog_alfa; a.qstats = qstats; a.partials = partials;
-  const int64_t blocks = (B * L + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipLaunchKernelGGL(k_cand_bwd_q, dim3((unsigned)blocks), dim3(kWave * kWavesPerBlock), 0, (hipStream_t)stream, a);
-  if (check_launch("asrn_candidates_bwd/query")) return 1;
-  hipLaunchKernelGGL(k_cand_bwd_k, dim3((unsigned)blocks), dim3(kWave * kWavesPerBlock), 0, (hipStream_t)stream, a);
-  return check_launch("asrn_candidates_bwd/key");
+  return dispatch<LaunchBwd>(a, (hipStream_t)stream);
 }
 
-extern "C" int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* ids_sorted,
-                                    const int32_t* rank, int64_t B, int64_t L, int32_t T, int32_t C, int32_t K,
-                                    int32_t* pos, int32_t* ell, void* stream) {
-  ASRN_REQUIRE(B >= 0 && L >= 0 && T >= 1 && C >= 1 && C <= 64 && K >= 0 && K <= 16,
+extern "C" int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* win, const int32_t* rank,
+                                    int64_t B, int64_t L, int32_t T, int32_t C, int32_t K, int32_t* pos, int32_t* ell,
+                                    void* stream) {
+  ASRN_REQUIRE(B >= 0 && L >= 0 && L < (int64_t(1) << 26) && T >= 1 && T <= 32 && C >= 1 && C <= 64 &&
+                   T * C <= kMaxSlots && K >= 0 && K <= 16,
                "asrn_candidate_lists: bad sizes B=%lld L=%lld T=%d C=%d K=%d", (long long)B, (long long)L, T, C, K);
   if (B == 0 || L == 0) return 0;
   Cand a = {};
-  a.sig = sig; a.order = order; a.ids_s = ids_sorted; a.rank = rank;
+  a.sig = sig; a.order = order; a.win = win; a.rank = rank;
   a.B = B; a.L = L; a.T = T; a.C = C; a.K = K;
-  const int64_t blocks = (B * L + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipLaunchKernelGGL(k_cand_lists, dim3((unsigned)blocks), dim3(kWave * kWavesPerBlock), 0, (hipStream_t)stream, a,
-                     pos, ell);
+  hipLaunchKernelGGL(k_cand_lists, grid_of(a), dim3(kWave * kWavesPerBlock), 0, (hipStream_t)stream, a, pos, ell);
   return check_launch("asrn_candidate_lists");
 }

@@ -5,7 +5,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include "../../include/asrn_hip.h"
+#include "asrn_hip.h"
 
 namespace asrn {
 
@@ -43,6 +43,43 @@ __device__ __forceinline__ float half_sum(float v) {
 __device__ __forceinline__ int readlane_i(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 __device__ __forceinline__ float readlane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// ---- DPP reductions (no LDS traffic): rotate within each 16-lane row, then combine the four rows ---------------------
+// DPP control words of GFX9-family ISAs: row_ror:n = 0x120 + n.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// every lane of each 16-lane row ends with the row's sum / max
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp<0x128>(v);
+  v += dpp<0x124>(v);
+  v += dpp<0x122>(v);
+  v += dpp<0x121>(v);
+  return v;
+}
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, dpp<0x128>(v));
+  v = fmaxf(v, dpp<0x124>(v));
+  v = fmaxf(v, dpp<0x122>(v));
+  v = fmaxf(v, dpp<0x121>(v));
+  return v;
+}
+// wave-uniform totals, combined in a fixed order (deterministic)
+__device__ __forceinline__ float wave_sum_u(float v) {
+  v = row_sum16(v);
+  return ((readlane_f(v, 0) + readlane_f(v, 16)) + readlane_f(v, 32)) + readlane_f(v, 48);
+}
+__device__ __forceinline__ float wave_max_u(float v) {
+  v = row_max16(v);
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+// the two 32-lane halves' sums
+__device__ __forceinline__ void half_sums_u(float v, float* h0, float* h1) {
+  v = row_sum16(v);
+  *h0 = readlane_f(v, 0) + readlane_f(v, 16);
+  *h1 = readlane_f(v, 32) + readlane_f(v, 48);
 }
 
 // lanes of the wave that hold the same `nbits`-bit key as this lane (only meaningful for lanes with valid = true)

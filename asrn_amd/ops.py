@@ -30,8 +30,9 @@ def _c(t, dtype=None):
 # a1 + a2
 # ---------------------------------------------------------------------------------------------------------------------
 
-def bucket_sort(phi, T, nb):
-    """phi (B, L, P) fp32 -> ids (B*T, L), order (B*T, L), ids_sorted (B*T, L), rank (B, L, T), all int32."""
+def bucket_sort(phi, T, nb, C):
+    """phi (B, L, P) fp32 -> ids (B*T, L), order (B*T, L), ids_sorted (B*T, L), rank (B, L, T) and the recent-mates
+    index win (B, L, T) = min(C, mates before) | min(C, mates after) << 8, all int32."""
     dev = _dev(phi)
     phi = _c(phi, torch.float32)
     B, L, P = phi.shape
@@ -39,17 +40,19 @@ def bucket_sort(phi, T, nb):
     order = torch.zeros_like(ids)          # zero-filled: every index a later kernel reads is in range
     ids_s = torch.zeros_like(ids)
     rank = torch.zeros((B, L, T), dtype=I32, device=dev)
-    call('asrn_bucket_sort', ptr(phi), B, L, T, nb, P, ptr(ids), ptr(order), ptr(ids_s), ptr(rank), stream_of(dev))
-    return ids, order, ids_s, rank
+    win = torch.zeros((B, L, T), dtype=I32, device=dev)
+    call('asrn_bucket_sort', ptr(phi), B, L, T, nb, P, C, ptr(ids), ptr(order), ptr(ids_s), ptr(rank), ptr(win),
+         stream_of(dev))
+    return ids, order, ids_s, rank, win
 
 
-def candidate_lists(sig, order, ids_s, rank, C, K):
+def candidate_lists(sig, order, win, rank, C, K):
     """The candidate windows the kernels walk: pos, ell (B, L, T, C) int32, -1 where a slot is empty."""
     dev = _dev(sig)
     B, L, T = rank.shape
     pos = torch.empty((B, L, T, C), dtype=I32, device=dev)
     ell = torch.empty_like(pos)
-    call('asrn_candidate_lists', ptr(_c(sig, torch.float32)), ptr(order), ptr(ids_s), ptr(rank), B, L, T, C, K,
+    call('asrn_candidate_lists', ptr(_c(sig, torch.float32)), ptr(order), ptr(win), ptr(rank), B, L, T, C, K,
          ptr(pos), ptr(ell), stream_of(dev))
     return pos, ell
 
@@ -210,7 +213,7 @@ class Candidates(torch.autograd.Function):
     Saves only its inputs and the per-(query, table) softmax statistics."""
 
     @staticmethod
-    def forward(ctx, phi, V, Qc, Kc, Bt, log_alfa, w_suf, gamma, sig, order, ids_s, rank, shape):
+    def forward(ctx, phi, V, Qc, Kc, Bt, log_alfa, w_suf, gamma, sig, order, win, rank, shape):
         T, Tc, C, K = shape['T'], shape['Tc'], shape['C'], shape['K']
         dev = _dev(phi, V)
         B, L, P = phi.shape
@@ -224,16 +227,16 @@ class Candidates(torch.autograd.Function):
         stats = torch.empty((B, L, T, 2), dtype=torch.float32, device=dev)
         sp, sc = float(P) ** -0.5, float(cf) ** -0.5
         call('asrn_candidates_fwd', ptr(ins['phi']), ptr(ins['V']), ptr(ins['Qc']), ptr(ins['Kc']), ptr(ins['sig']),
-             ptr(ins['Bt']), ptr(ins['la']), ptr(ins['w']), ptr(ins['g']), ptr(order), ptr(ids_s), ptr(rank), B, L, d,
+             ptr(ins['Bt']), ptr(ins['la']), ptr(ins['w']), ptr(ins['g']), ptr(order), ptr(win), ptr(rank), B, L, d,
              P, cf, K, T, Tc, C, sp, sc, ptr(salida), ptr(signals), ptr(stats), stream_of(dev))
-        ctx.save_for_backward(*ins.values(), order, ids_s, rank, stats)
+        ctx.save_for_backward(*ins.values(), order, win, rank, stats)
         ctx.meta = (B, L, P, d, cf, K, T, Tc, C, sp, sc, V.dtype, phi.dtype, Qc.dtype, Kc.dtype, log_alfa.dtype)
         ctx.mark_non_differentiable(signals)
         return salida.to(V.dtype), signals
 
     @staticmethod
     def backward(ctx, dsal, _dsig):
-        phi, V, Qc, Kc, sig, Bt, la, w, g, order, ids_s, rank, stats = ctx.saved_tensors
+        phi, V, Qc, Kc, sig, Bt, la, w, g, order, win, rank, stats = ctx.saved_tensors
         B, L, P, d, cf, K, T, Tc, C, sp, sc, tv, tp, tq, tk, tl = ctx.meta
         dev = phi.device
         dsal = _c(dsal, torch.float32)
@@ -246,7 +249,7 @@ class Candidates(torch.autograd.Function):
         qstats = torch.empty((B, L, T), dtype=torch.float32, device=dev)
         partials = torch.empty((B * L, T + K + 1), dtype=torch.float32, device=dev)
         call('asrn_candidates_bwd', ptr(phi), ptr(V), ptr(Qc), ptr(Kc), ptr(sig), ptr(Bt), ptr(la), ptr(w), ptr(g),
-             ptr(order), ptr(ids_s), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ptr(dsal), ptr(stats),
+             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ptr(dsal), ptr(stats),
              ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(qstats), ptr(partials), stream_of(dev))
         part = partials.sum(0)
         dgamma = part[:T] / C

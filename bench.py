@@ -1,0 +1,161 @@
+"""Benchmark of the ASRN layer hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config cfg2] [--no-cpu-baseline]
+
+A step is one forward + backward of one ASRN layer (asrn.ASRNLayer, group-A protections) over one batch of
+synthetic tokens: BASELINE.json configs[1] = cfg2, B 8, N 4096, d 256, V 256, fp32, 30% copied spans. Inputs and
+weights are resident in HBM before the timed region. Prints one JSON line with the driver's keys plus:
+  roofline      the dominant HIP kernel: algorithmic bytes per launch / its mean launch time (device events recorded
+                on the stream it runs on), against MI355X's 8 TB/s
+  hip_aggregate BASELINE.md's headline: 7,776 B/token x tokens / (8 TB/s x the sum of the HIP kernels' time per step)
+  layer         whole-layer tokens/s and its HBM fraction at 25,876 B/token (the fp32 GEMMs stay PyTorch)
+  cpu_baseline  the CPU oracle (oracle/layer.py, PyTorch on the host cores) on the same workload
+"""
+import argparse
+import copy
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = 'ASRN layer fwd+bwd tokens/sec at N=4096 (1 GPU); % HBM roofline; decode tok/s'
+HBM_PEAK = 8.0e12
+
+# algorithmic bytes per token at cfg2 (fp32, T 8, P 112, cf 16, d 256): every tensor the kernel must touch, read
+# once and written once. The entry point timed below and its per-token figure.
+def algorithmic_bytes(d, P, cf, T):
+    a = 4
+    reads_fwd = P * a + 2 * cf * a + d * a + 8 + 8 + 4 + 2 * T * 4       # phi, Qc, Kc, V, x, Bt, log_alfa, order+ids
+    fwd = reads_fwd + d * a + 4 * 4                                     # + salida, 4 signals
+    bwd = reads_fwd + d * a + (P * a + 2 * cf * a + d * a + 8 + 4)      # + dsalida; dphi, dQc, dKc, dV, dBt, dlog_alfa
+    return {'asrn_candidates_fwd': fwd, 'asrn_candidates_bwd': bwd}
+
+
+HIP_BYTES_PER_TOKEN = 7776            # BASELINE.md / SURVEY 8(d): all HIP kernels of one fwd+bwd at cfg2
+LAYER_BYTES_PER_TOKEN = 25876         # whole layer at cfg2
+
+
+def cpu_baseline(layer_cpu, x, E, h, gy, reps=2):
+    """The CPU oracle's layer forward + backward on the same inputs (oracle/layer.py, PyTorch on all host cores)."""
+    import torch
+    from oracle import layer as O
+    torch.set_num_threads(os.cpu_count() or 1)
+    p = {k: (v.clone().requires_grad_() if v.is_floating_point() and k not in ('c_vistos', 'r_firma') else v.clone())
+         for k, v in layer_cpu.state_dict().items()}
+    sh = O.shape_from_params(p, E.shape[-1], n_bits=layer_cpu.n_bits, C=layer_cpu.chunk)
+    times = []
+    for i in range(reps + 1):
+        Ec, hc = E.clone().requires_grad_(), h.clone().requires_grad_()
+        t0 = time.perf_counter()
+        y = O.layer_forward(p, Ec, hc, x, sh)
+        (y * gy).sum().backward()
+        dt = time.perf_counter() - t0
+        if i:
+            times.append(dt)
+    t = statistics.median(times)
+    tokens = x.numel()
+    return {'value': round(tokens / t, 1), 'unit': 'tokens/s', 'cores': torch.get_num_threads(), 'kind': 'port',
+            'sample': f'full workload ({x.shape[0]}x{x.shape[1]} tokens), fp32, median of {reps} after 1 warm-up; '
+                      f'cpu_count={os.cpu_count()}',
+            'seconds_per_step': round(t, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=20)
+    ap.add_argument('--warmup', type=int, default=5)
+    ap.add_argument('--config', default='cfg2')
+    ap.add_argument('--seed', type=int, default=0)
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    args = ap.parse_args()
+    world = int(os.environ.get('WORLD_SIZE', '1'))
+    if args.gpus != 1 or world != 1:
+        print(f'bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): the ASRN hot path '
+              'shards over the batch with no exchange; see DESIGN.md for how it would scale.', file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import asrn_amd
+    from asrn_amd import _lib, synth
+
+    asrn_amd.load()
+    cfg = synth.CONFIGS[args.config]
+    B, N, d, V = cfg['B'], cfg['N'], cfg['d'], cfg['V']
+    dev = torch.device('cuda:0')
+    torch.manual_seed(args.seed)
+    layer_cpu = synth.move_params(asrn_amd.ASRNLayer(d), seed=args.seed)
+    layer = copy.deepcopy(layer_cpu).to(dev)
+    x, E, h = synth.layer_inputs(B, N, d, V, seed=args.seed, frac=cfg['frac'], span=cfg['span'], zipf=cfg['zipf'])
+    gy = torch.randn(B, N, d, generator=torch.Generator().manual_seed(args.seed + 1))
+    xd, Ed, hd, gyd = x.to(dev), E.to(dev).requires_grad_(), h.to(dev).requires_grad_(), gy.to(dev)
+
+    def step():
+        layer.zero_grad(set_to_none=True)
+        Ed.grad = None
+        hd.grad = None
+        y = layer(Ed, hd, xd)
+        (y * gyd).sum().backward()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # HIP-event timing of every library entry point over the timed region
+    names = [n for n in _lib.SIGNATURES if n not in ('asrn_hip_last_error', 'asrn_hip_abi_version')
+             and not n.endswith('_workspace')]
+    timed = _lib.time_calls(names)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    timed = _lib.stop_timing()
+
+    per_call = {}
+    for n, evs in timed.items():
+        if evs:
+            ms = [s.elapsed_time(e) for s, e in evs]
+            per_call[n] = {'launches': len(ms), 'mean_us': 1e3 * sum(ms) / len(ms), 'total_ms': sum(ms)}
+    wall = (t1 - t0) / args.steps
+    tokens = B * N
+    value = tokens * args.steps / (t1 - t0)
+
+    P, cf, T = layer.n_tablas * layer.n_bits, layer.confirmar, layer.n_tablas
+    algo = algorithmic_bytes(d, P, cf, T)
+    dom = max(algo, key=lambda n: per_call.get(n, {}).get('total_ms', 0.0))
+    dom_us = per_call[dom]['mean_us']
+    achieved = algo[dom] * tokens / (dom_us * 1e-6)
+    hip_ms_per_step = sum(v['total_ms'] for v in per_call.values()) / args.steps
+
+    out = {
+        'metric': METRIC, 'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps,
+        'warmup': args.warmup, 'ms_per_step': round(wall * 1e3, 4), 'higher_is_better': True, 'scaling': 'weak',
+        'vs_baseline': None, 'dtype': 'fp32', 'data': 'synthetic (seeded random bytes, 30% copied spans; random-init '
+        'layer moved off its neutral values)',
+        'config': {'workload': f'{args.config}: one ASRN layer fwd+bwd, B={B}, N={N}, d={d}, V={V}, T=8 tables x 14 '
+                               f'bits, C=32, fp32', 'global_batch': B, 'seq_len': N, 'parallelism': 'none (1 GPU)'},
+        'roofline': {'bound': 'hbm', 'kernel': dom, 'achieved': round(achieved / 1e9, 1), 'peak': HBM_PEAK / 1e9,
+                     'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK, 4), 'traffic': None,
+                     'bytes_per_token': algo[dom], 'mean_launch_us': round(dom_us, 2)},
+        'hip_aggregate': {'bytes_per_token': HIP_BYTES_PER_TOKEN, 'hip_ms_per_step': round(hip_ms_per_step, 4),
+                          'frac': round(HIP_BYTES_PER_TOKEN * tokens / (HBM_PEAK * hip_ms_per_step * 1e-3), 4)},
+        'layer': {'tokens_per_s': round(value, 1),
+                  'hbm_frac': round(LAYER_BYTES_PER_TOKEN * tokens / (HBM_PEAK * wall), 4)},
+        'kernels': {n: {k: round(v, 3) if isinstance(v, float) else v for k, v in s.items()}
+                    for n, s in sorted(per_call.items(), key=lambda kv: -kv[1]['total_ms'])},
+    }
+    if not args.no_cpu_baseline:
+        out['cpu_baseline'] = cpu_baseline(layer_cpu, x, E, h, gy)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == '__main__':
+    main()

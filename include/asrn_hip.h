@@ -34,16 +34,19 @@ int32_t asrn_hip_abi_version(void);
  *   order      (B*T, L) int32 out: sorted rank -> text position (stable: ties keep text order)
  *   ids_sorted (B*T, L) int32 out: ids[order]
  *   rank       (B, L, T) int32 out: text position -> sorted rank, per table
- * Requires 1 <= nb <= 14. */
-int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t T, int32_t nb, int64_t phi_stride,
-                     int32_t* ids, int32_t* order, int32_t* ids_sorted, int32_t* rank, void* stream);
+ *   win        (B, L, T) int32 out: the recent-mates index, min(C, earlier positions in the bucket) |
+ *              min(C, later positions in the bucket) << 8: the query window is the last `win & 255` sorted ranks
+ *              before `rank`, the key window the first `win >> 8` after it
+ * Requires 1 <= nb <= 14, 1 <= C <= 255. */
+int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t T, int32_t nb, int64_t phi_stride, int32_t C,
+                     int32_t* ids, int32_t* order, int32_t* ids_sorted, int32_t* rank, int32_t* win, void* stream);
 
 /* ---- a3 - a7: candidate attention, forward ---------------------------------------------------------------------
  * Replaces _CasillerosTriton.forward / _casilleros_ida in ESTABLE mode (asrn/nucleo.py:359-382, 465-488) as called
  * from CapaASRNEstable._acumular_triton (asrn/estable.py:274-292), with the table sum and the gate signals of
  * _senales (asrn/estable.py:294-300) done in the kernel.
- * For query t and table tau the candidates are the sorted ranks [s - C, s) of the same bucket (s = rank of t):
- * its <= C most recent earlier bucket mates. Score = <phi_q, phi_k> * scale_phi + <Qc_q, Kc_k> * scale_c
+ * For query t and table tau the candidates are the last (win & 255) sorted ranks before s = rank of t (both from
+ * asrn_bucket_sort): its <= C most recent earlier bucket mates. Score = <phi_q, phi_k> * scale_phi + <Qc_q, Kc_k> * scale_c
  * + w_suf[suffix match] + log_alfa_k + (gamma_tau / C) * fp32(Bt_k - Bt_q); exact masked softmax.
  *   sig (B, L) fp32 token signatures; Bt (B, L) fp64 clock; log_alfa (B, L); w_suf (K+1); gamma (T)
  *   salida  (B, L, d) out: sum over tables of sum_k att * V_k
@@ -52,7 +55,7 @@ int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t T, int32_t 
  * Requires d % 4 == 0, d <= 1024, 1 <= C <= 64, P + cf <= 256, K <= 16, T <= 32. */
 int asrn_candidates_fwd(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                         const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
-                        const int32_t* order, const int32_t* ids_sorted, const int32_t* rank, int64_t B, int64_t L,
+                        const int32_t* order, const int32_t* win, const int32_t* rank, int64_t B, int64_t L,
                         int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
                         float scale_phi, float scale_c, float* salida, float* signals, float* stats, void* stream);
 
@@ -61,7 +64,7 @@ int asrn_candidates_fwd(const float* phi, const float* V, const float* Qc, const
  * (oldest first; the empty slots come first and hold -1), and their suffix-match lengths (asrn/nucleo.py:98-108,
  * 313-320).
  *   pos, ell (B, L, T, C) int32 out (-1 where the window slot holds no candidate). */
-int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* ids_sorted, const int32_t* rank,
+int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* win, const int32_t* rank,
                          int64_t B, int64_t L, int32_t T, int32_t C, int32_t K, int32_t* pos, int32_t* ell,
                          void* stream);
 
@@ -76,7 +79,7 @@ int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* 
  *   partials (B*L, T + K + 1) fp32 out: per query, d gamma_tau then d w_suf[0..K]; the caller sums over rows. */
 int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                         const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
-                        const int32_t* order, const int32_t* ids_sorted, const int32_t* rank, int64_t B, int64_t L,
+                        const int32_t* order, const int32_t* win, const int32_t* rank, int64_t B, int64_t L,
                         int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
                         float scale_phi, float scale_c, const float* dsalida, const float* stats, float* dphi,
                         float* dV, float* dQc, float* dKc, double* dBt, float* dlog_alfa, float* qstats,

@@ -53,9 +53,7 @@ def shape_from_params(p, d, **kw):
     """Reads T, nb, Tc, cf, K, n and the streak nodes from the parameter shapes (nucleo:591-630)."""
     Tw_nb = p['afin_palabra.2.weight'].shape[0]
     Tc_nb = p['afin_contexto.2.weight'].shape[0]
-    nb = kw.pop('n_bits', None)
-    if nb is None:
-        nb = math.gcd(Tw_nb, Tc_nb)
+    nb = kw.pop('n_bits', 14)             # not recoverable from the shapes alone (T*nb is): the reference default
     T = (Tw_nb + Tc_nb) // nb
     return Shape(d=d, T=T, nb=nb, Tc=Tc_nb // nb, cf=p['cq.weight'].shape[0], K=p['w_sufijo'].shape[0] - 1,
                  n=p['w_vistos'].shape[0], nodos=p['d_racha'].shape[0], **kw)

@@ -50,7 +50,8 @@ def _need_gpu():
 # ---------------------------------------------------------------------------------------------------------------------
 
 def check_bucket_sort(phi, T, nb):
-    ids, order, ids_s, rank = ops.bucket_sort(phi.to(DEV), T, nb)
+    C = 32
+    ids, order, ids_s, rank, win = ops.bucket_sort(phi.to(DEV), T, nb, C)
     ref_ids, ref_order = O.bucket_rows(phi.cpu(), T, nb)
     assert torch.equal(ids.cpu().long(), ref_ids.long())
     assert torch.equal(order.cpu().long(), ref_order)
@@ -58,7 +59,21 @@ def check_bucket_sort(phi, T, nb):
     B, L = phi.shape[0], phi.shape[1]
     inv = torch.empty_like(ref_order).scatter_(1, ref_order, torch.arange(L).expand(B * T, L))
     assert torch.equal(rank.cpu().long().permute(0, 2, 1).reshape(B * T, L), inv)
-    return ids, order, ids_s, rank
+    # the recent-mates index: bucket mates before and after each position, clamped to C
+    ids_np = ref_ids.numpy()
+    before = np.zeros((B * T, L), dtype=np.int64)
+    total = np.zeros((B * T, L), dtype=np.int64)
+    for r in range(B * T):
+        _, inv_r, counts = np.unique(ids_np[r], return_inverse=True, return_counts=True)
+        seen = np.zeros(len(counts), dtype=np.int64)
+        for t, g in enumerate(inv_r):
+            before[r, t] = seen[g]
+            seen[g] += 1
+        total[r] = counts[inv_r]
+    after = total - 1 - before
+    want = torch.from_numpy(np.minimum(before, C) | (np.minimum(after, C) << 8))
+    assert torch.equal(win.cpu().long().permute(0, 2, 1).reshape(B * T, L), want)
+    return ids, order, ids_s, rank, win
 
 
 @pytest.mark.parametrize('name', CASES)
@@ -66,7 +81,7 @@ def test_bucket_sort_golden(name):
     say('bucket_sort golden', name)
     g, p, m = fixtures.load(name)
     sh = fixtures.shape_of(p, m)
-    ids, order, ids_s, rank = ops.bucket_sort(g['phi'].to(DEV), sh.T, sh.nb)
+    ids, order, ids_s, rank, win = ops.bucket_sort(g['phi'].to(DEV), sh.T, sh.nb, sh.C)
     assert torch.equal(ids.cpu().long(), g['ids'].long())
     assert torch.equal(order.cpu().long(), g['orden'])
 
@@ -99,8 +114,9 @@ def test_candidate_lists_bruteforce(B, L, T, nb, C, K, V):
     x = torch.randint(0, V, (B, L), generator=g)
     phi = torch.randn(V, T * nb, generator=g)[x]
     sig = x.float()
-    ids, order, ids_s, rank = check_bucket_sort(phi, T, nb)
-    pos, ell = ops.candidate_lists(sig.to(DEV), order, ids_s, rank, C, K)
+    ids, order, ids_s, rank, _ = check_bucket_sort(phi, T, nb)
+    _, order, ids_s, rank, win = ops.bucket_sort(phi.to(DEV), T, nb, C)
+    pos, ell = ops.candidate_lists(sig.to(DEV), order, win, rank, C, K)
     pos, ell = pos.cpu().long(), ell.cpu().long()
     lists = O.candidate_lists_bruteforce(ids.cpu(), C)
     want = torch.full((B, L, T, C), -1, dtype=torch.long)
@@ -239,10 +255,10 @@ def run_candidates(stage, sig, w_suf, gamma, sh, gs):
     leaves = {k: stage[k].to(DEV).requires_grad_() for k in ('phi', 'V', 'Qc', 'Kc', 'Bt', 'log_alfa')}
     w = w_suf.to(DEV).requires_grad_()
     gam = gamma.to(DEV).requires_grad_()
-    _, order, ids_s, rank = ops.bucket_sort(leaves['phi'].detach(), sh.T, sh.nb)
+    _, order, _, rank, win = ops.bucket_sort(leaves['phi'].detach(), sh.T, sh.nb, sh.C)
     shape = dict(T=sh.T, Tc=sh.Tc, C=sh.C, K=sh.K)
     salida, sen = ops.Candidates.apply(leaves['phi'], leaves['V'], leaves['Qc'], leaves['Kc'], leaves['Bt'],
-                                       leaves['log_alfa'], w, gam, sig.to(DEV), order, ids_s, rank, shape)
+                                       leaves['log_alfa'], w, gam, sig.to(DEV), order, win, rank, shape)
     (salida * gs.to(DEV)).sum().backward()
     grads = {k: t.grad.cpu() for k, t in leaves.items()}
     grads['w_sufijo'], grads['gamma'] = w.grad.cpu(), gam.grad.cpu()
@@ -300,13 +316,14 @@ def random_stage(B, L, d, V, nb=14, T=8, cf=16, K=4, seed=0, shift=0.0):
     return x.float(), stage, w_suf, gamma, gs
 
 
-@pytest.mark.parametrize('B,L,d,V,C,nb,shift', [(2, 1500, 256, 6, 32, 14, 0.0), (2, 777, 96, 40, 16, 4, 0.0),
-                                                (1, 600, 64, 5, 64, 6, 1e6), (2, 300, 1024, 8, 8, 3, 0.0),
-                                                (1, 2, 32, 3, 32, 14, 0.0)])
-def test_candidates_vs_oracle(B, L, d, V, C, nb, shift):
-    say('candidates', B, L, d, V, C, nb, shift)
-    sig, stage, w_suf, gamma, gs = random_stage(B, L, d, V, nb=nb, seed=L, shift=shift)
-    sh = O.Shape(d=d, nb=nb, C=C)
+@pytest.mark.parametrize('B,L,d,V,C,nb,T,shift', [(2, 1500, 256, 6, 32, 14, 8, 0.0), (2, 777, 96, 40, 16, 4, 8, 0.0),
+                                                  (1, 600, 64, 5, 64, 6, 4, 1e6), (2, 300, 1024, 8, 8, 3, 8, 0.0),
+                                                  (1, 2, 32, 3, 32, 14, 8, 0.0), (2, 900, 768, 7, 32, 14, 8, 0.0),
+                                                  (1, 500, 512, 9, 32, 14, 8, 0.0)])
+def test_candidates_vs_oracle(B, L, d, V, C, nb, T, shift):
+    say('candidates', B, L, d, V, C, nb, T, shift)
+    sig, stage, w_suf, gamma, gs = random_stage(B, L, d, V, nb=nb, T=T, seed=L, shift=shift)
+    sh = O.Shape(d=d, nb=nb, C=C, T=T, Tc=T // 2)
     salida, sen, grads = run_candidates(stage, sig, w_suf, gamma, sh, gs)
     acc, rg = oracle_candidates(stage, sig, w_suf, gamma, sh, gs)
     assert_close(salida, acc['salida'], 'salida')

@@ -47,13 +47,16 @@ def _err(lib):
 def test_argument_checks_fail_before_any_device_work(lib):
     N = None
     # n_bits outside [1, 14]
-    assert lib.asrn_bucket_sort(N, 2, 16, 8, 15, 120, N, N, N, N, N) != 0
+    assert lib.asrn_bucket_sort(N, 2, 16, 8, 15, 120, 32, N, N, N, N, N, N) != 0
     assert 'n_bits' in _err(lib)
     # phi row stride shorter than T*nb
-    assert lib.asrn_bucket_sort(N, 2, 16, 8, 14, 100, N, N, N, N, N) != 0
+    assert lib.asrn_bucket_sort(N, 2, 16, 8, 14, 100, 32, N, N, N, N, N, N) != 0
     assert 'stride' in _err(lib)
+    # window clamp outside [1, 255]
+    assert lib.asrn_bucket_sort(N, 2, 16, 8, 14, 112, 300, N, N, N, N, N, N) != 0
+    assert 'window' in _err(lib)
     # empty inputs are a no-op
-    assert lib.asrn_bucket_sort(N, 0, 16, 8, 14, 112, N, N, N, N, N) == 0
+    assert lib.asrn_bucket_sort(N, 0, 16, 8, 14, 112, 32, N, N, N, N, N, N) == 0
     args = [N] * 12 + [2, 16]
     # d not a multiple of 4
     assert lib.asrn_candidates_fwd(*args, 6, 112, 16, 4, 8, 4, 32, 0.1, 0.25, N, N, N, N) != 0
@@ -73,7 +76,7 @@ def test_argument_checks_fail_before_any_device_work(lib):
 
 def test_ops_refuse_cpu_tensors():
     with pytest.raises(RuntimeError, match='GPU only'):
-        asrn_amd.ops.bucket_sort(torch.zeros(1, 4, 112), 8, 14)
+        asrn_amd.ops.bucket_sort(torch.zeros(1, 4, 112), 8, 14, 32)
     layer = CapaASRNEstable(16)
     with pytest.raises(RuntimeError, match='GPU only'):
         layer(torch.zeros(1, 4, 16), torch.zeros(1, 4, 16), torch.zeros(1, 4, dtype=torch.long))
