@@ -6,9 +6,10 @@ replaces: ASRNLayer / CapaASRNEstable, Protecciones / Protections, firmas_de_pie
 from . import ops, synth
 from ._lib import ASRNHipError, LIB_PATH, load
 from .capa import ASRNLayer, CapaASRNEstable, Protecciones, Protections, firmas_de_piezas
+from .escritura import EscritorCapa, LayerWriter
 from .ops import escaneo
 
 __version__ = '0.1.0'
 
-__all__ = ['ASRNLayer', 'CapaASRNEstable', 'Protecciones', 'Protections', 'firmas_de_piezas', 'escaneo', 'ops',
+__all__ = ['ASRNLayer', 'CapaASRNEstable', 'EscritorCapa', 'LayerWriter', 'Protecciones', 'Protections', 'firmas_de_piezas', 'escaneo', 'ops',
            'load', 'LIB_PATH', 'ASRNHipError', '__version__']

@@ -2,8 +2,8 @@
 
     python -m asrn_amd.build            # or asrn_amd.build.build()
 
-Every source is compiled with packed-fp32 instructions disabled; ngram.hip also with -ffp-contract=off because the
-n-gram keys must round each fp64 multiply and add separately, exactly as the reference does.
+Every source is compiled with packed-fp32 instructions disabled; ngram.hip and decode.hip also with -ffp-contract=off
+because the n-gram keys must round each fp64 multiply and add separately, exactly as the reference does.
 """
 import os
 import shutil
@@ -14,12 +14,12 @@ import tempfile
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, 'csrc')
 LIB = os.path.join(HERE, 'libasrn_hip.so')
-SOURCES = ['errors.hip', 'bucket_sort.hip', 'ngram.hip', 'scan.hip', 'candidates.hip']
+SOURCES = ['errors.hip', 'bucket_sort.hip', 'ngram.hip', 'scan.hip', 'candidates.hip', 'decode.hip']
 ARCH = os.environ.get('ASRN_OFFLOAD_ARCH', 'gfx950')
 INCLUDE = os.path.join(os.path.dirname(HERE), 'include')
 COMMON = ['-O3', '-fPIC', '-std=c++17', f'--offload-arch={ARCH}', '-Xclang', '-target-feature', '-Xclang',
           '-packed-fp32-ops', '-Wno-unused-command-line-argument', f'-I{INCLUDE}']
-PER_FILE = {'ngram.hip': ['-ffp-contract=off']}
+PER_FILE = {'ngram.hip': ['-ffp-contract=off'], 'decode.hip': ['-ffp-contract=off']}
 
 
 def hipcc():

@@ -157,10 +157,12 @@ class CapaASRNEstable(nn.Module):
 
     # --- hot path (HIP) ---------------------------------------------------------------------------------------------
 
-    def _acumular(self, E, Qc, Kc, Bt, log_alfa, sig):
+    def _acumular(self, E, Qc, Kc, Bt, log_alfa, sig, partes=None):
         """Candidate attention of all tables -> salida and the gate signals (asrn/estable.py:204-300)."""
         T = self.n_tablas
         phi, V = self._phi_y_valores(E)
+        if partes is not None:
+            partes.update(phi=phi, V=V)
         _, order, _, rank, win = ops.bucket_sort(phi.detach(), T, self.n_bits, self.chunk)
         shape = dict(T=T, Tc=self.tablas_contexto, C=self.chunk, K=self.sufijo)
         salida, sen = ops.Candidates.apply(phi, V, Qc, Kc, Bt, log_alfa, self.w_sufijo, self.gamma, sig, order,
@@ -168,13 +170,15 @@ class CapaASRNEstable(nn.Module):
         return {'salida': salida, 'peso_total': sen[..., 0:1], 'mejor': sen[..., 1:2], 'pico': sen[..., 2:3],
                 'peso_ctx': sen[..., 3:4]}
 
-    def _repeticion(self, sig, beta, Bt, log_alfa):
+    def _repeticion(self, sig, beta, Bt, log_alfa, partes=None):
         """vistos, hawkes (B, L, n) and racha (B, L) (asrn/estable.py:304-321)."""
         kappa, kappa_r = self._kappas()
         with torch.no_grad():
-            _, order, rep, rank_k, vistos = ops.ngram_sort(sig, self.c_vistos, self.vistos)
+            claves, order, rep, rank_k, vistos = ops.ngram_sort(sig, self.c_vistos, self.vistos)
         hawkes = ops.Hawkes.apply(Bt, log_alfa, kappa, order, rep, rank_k)
         racha = ops.Streak.apply(beta, kappa_r, vistos)
+        if partes is not None:
+            partes.update(claves=claves, orden_k=order, repetido=rep)
         return {'vistos': vistos, 'hawkes': hawkes, 'racha': racha}
 
     # --- gate (PyTorch, asrn/estable.py:376-403 and asrn/nucleo.py:865-878) ------------------------------------------
@@ -214,12 +218,20 @@ class CapaASRNEstable(nn.Module):
 
     def forward(self, E, h, piezas=None):
         """E (B, L, d), h (B, L, d), piezas (B, L) or None -> h' (B, L, d) (asrn/estable.py:407-421)."""
+        return self._adelante(E, h, piezas)
+
+    def _adelante(self, E, h, piezas=None, partes=None):
+        """forward; with a dict `partes`, also keeps what the generation step starts from (the prompt's phi, V,
+        Qc, Kc, sig, beta, Bt, log_alfa, n-gram keys and their sort, hawkes and racha)."""
         self._revisar(E)
         sig = self._firma(E) if piezas is None else firmas_de_piezas(piezas)
         Qc, Kc, beta, log_alfa = self._contexto(h)
         Bt = ops.ClockScan.apply(beta)
-        acc = self._acumular(E, Qc, Kc, Bt, log_alfa, sig)
-        acc.update(self._repeticion(sig, beta, Bt, log_alfa))
+        acc = self._acumular(E, Qc, Kc, Bt, log_alfa, sig, partes)
+        acc.update(self._repeticion(sig, beta, Bt, log_alfa, partes))
+        if partes is not None:
+            partes.update(Qc=Qc, Kc=Kc, sig=sig, beta=beta, Bt=Bt, log_alfa=log_alfa, hawkes=acc['hawkes'],
+                          racha=acc['racha'])
         return self._combinar(acc, h)
 
 

@@ -39,6 +39,9 @@ struct Cand {
   // backward
   const float* dsal; const float* stats_in; float* dphi; float* dV; float* dQc; float* dKc; double* dBt;
   float* dla; float* qstats; float* partials;
+  // generation: per-bucket rings (B*T, 2^nb, C) of positions and their counts (B*T, 2^nb); the query position tq,
+  // its bucket ids (B, T) out, and whether tq then enters the rings
+  int32_t* rings; int32_t* counts; int32_t* ids_out; int nb; int64_t tq; int insert;
 };
 
 // per-wave LDS scratch: one token's candidate list (entries) and its distinct positions (uniques)
@@ -162,6 +165,55 @@ __device__ __forceinline__ int gather(const Cand& a, int64_t b, int64_t t, bool 
     ok[c] = v && j >= 0 && j < a.L;
     tt[c] = tau;
     pos[c] = ok[c] ? a.order[(b * a.T + tau) * a.L + j] : 0;
+  }
+  int base = 0;
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const uint64_t bal = __ballot(ok[c]);
+    if (ok[c]) S.key[base + __popcll(bal & ((1ull << lane) - 1ull))] = (pos[c] << 5) | tt[c];
+    base += __popcll(bal);
+  }
+  wave_lds_sync();
+  if (lane <= a.T) {
+    int lo = 0, hi = base;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if ((S.key[mid] & 31) < lane) lo = mid + 1; else hi = mid;
+    }
+    S.off[lane] = lo;
+  }
+  wave_lds_sync();
+  return base;
+}
+
+// Generation: the candidates of position t are the ring contents of its bucket in every table, oldest first. The
+// bucket ids come from the signs of the query's own hash outputs (written to ids_out for the ring insert).
+__device__ __forceinline__ int gather_rings(const Cand& a, int64_t b, int64_t t, Scratch& S) {
+  const int lane = lane_id();
+  int id = 0, cnt = 0;
+  if (lane < a.T) {
+    const float* ph = a.phi + (b * a.L + t) * a.P + lane * a.nb;
+    for (int j = 0; j < a.nb; ++j) id |= (ph[j] > 0.f ? 1 : 0) << j;     // strict > 0 (nucleo:663)
+    a.ids_out[b * a.T + lane] = id;
+    cnt = a.counts[(b * a.T + lane) * ((int64_t)1 << a.nb) + id];
+  }
+  const int slots = a.T * a.C;
+  int pos[kCh], tt[kCh];
+  bool ok[kCh];
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const int sl = c * kWave + lane;
+    const int tau = sl < slots ? sl / a.C : 0;
+    const int i = sl - tau * a.C;
+    const int idt = __shfl(id, tau, 64), ct = __shfl(cnt, tau, 64);
+    const int n = ct < a.C ? ct : a.C;              // filled slots
+    const int start = ct < a.C ? 0 : ct % a.C;     // the oldest entry
+    const bool v = sl < slots && i < n;
+    const int slot = (start + i) % a.C;
+    int p = v ? a.rings[((b * a.T + tau) * ((int64_t)1 << a.nb) + idt) * a.C + slot] : -1;
+    ok[c] = v && p >= 0 && p < t;
+    tt[c] = tau;
+    pos[c] = ok[c] ? p : 0;
   }
   int base = 0;
 #pragma unroll
@@ -375,16 +427,14 @@ __device__ __forceinline__ void segment(int offv, int tau, int* lo, int* hi) {
 // ---------------------------------------------------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------------------------------------------------
-template <int F4, int DCH>
-__global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_fwd(Cand a) {
-  __shared__ Scratch scratch[kWavesPerBlock];
-  Scratch& S = scratch[threadIdx.x >> 6];
-  const int64_t tok = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (tok >= a.B * a.L) return;
+// One query token's candidate attention: salida row (d), the 4 gate signals and, when `stats` is given, the per-table
+// (max, denominator). RING: candidates from the generation rings instead of the sorted windows.
+template <int F4, int DCH, bool RING>
+__device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t t, Scratch& S, float* salida_row,
+                                              float* signals_row, float* stats_rows) {
   const int lane = lane_id();
-  const int64_t b = tok / a.L, t = tok % a.L;
-
-  const int M = gather(a, b, t, true, S);
+  const int64_t tok = b * a.L + t;
+  const int M = RING ? gather_rings(a, b, t, S) : gather(a, b, t, true, S);
   const int NU = dedupe(a, M, S);
   float4 qf[F4];
   feats<F4>(a, a.Qc, tok, true, qf);
@@ -409,9 +459,9 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_fwd(Cand a) {
   for (int tau = 0; tau < a.T; ++tau) {
     int lo, hi;
     segment(offv, tau, &lo, &hi);
-    float* st = a.stats + (tok * a.T + tau) * 2;
+    float* st = stats_rows ? stats_rows + tau * 2 : nullptr;
     if (lo == hi) {
-      if (lane == 0) {
+      if (lane == 0 && st) {
         st[0] = 0.f;
         st[1] = 1.f;
       }
@@ -421,7 +471,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_fwd(Cand a) {
 #pragma unroll
     for (int c = 0; c < kCh; ++c)
       if (E.tau[c] == tau) S.uc[E.u[c]] += expf(E.sc[c] - ts.mx) / ts.den;   // uniques are distinct in a table
-    if (lane == 0) {
+    if (lane == 0 && st) {
       st[0] = ts.mx;
       st[1] = ts.den;
     }
@@ -460,14 +510,43 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_fwd(Cand a) {
 #pragma unroll
   for (int ch = 0; ch < DCH; ++ch) {
     const int dd = ch * 256 + lane * 4;
-    if (dd < a.d) *reinterpret_cast<float4*>(a.salida + tok * a.d + dd) = acc[ch];
+    if (dd < a.d) *reinterpret_cast<float4*>(salida_row + dd) = acc[ch];
   }
   if (lane == 0) {
-    float* sg = a.signals + tok * 4;
-    sg[0] = pt;
-    sg[1] = pt > 0.f ? fmaxf(best, -1e9f) : -1e9f;
-    sg[2] = pico;
-    sg[3] = pctx;
+    signals_row[0] = pt;
+    signals_row[1] = pt > 0.f ? fmaxf(best, -1e9f) : -1e9f;
+    signals_row[2] = pico;
+    signals_row[3] = pctx;
+  }
+}
+
+template <int F4, int DCH>
+__global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_fwd(Cand a) {
+  __shared__ Scratch scratch[kWavesPerBlock];
+  Scratch& S = scratch[threadIdx.x >> 6];
+  const int64_t tok = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (tok >= a.B * a.L) return;
+  forward_token<F4, DCH, false>(a, tok / a.L, tok % a.L, S, a.salida + tok * a.d, a.signals + tok * 4,
+                                a.stats + tok * a.T * 2);
+}
+
+// Generation step: one wave per batch row; the query is position a.tq of the caches (a.L = their capacity). With
+// a.insert, tq then enters its bucket's ring in every table at slot count % C, overwriting the oldest (reference
+// nucleo:1610-1618). Only this wave touches batch row b's rings, and its ring reads were consumed before.
+template <int F4, int DCH>
+__global__ __launch_bounds__(kWave * kWavesPerBlock) void k_decode_attend(Cand a) {
+  __shared__ Scratch scratch[kWavesPerBlock];
+  Scratch& S = scratch[threadIdx.x >> 6];
+  const int64_t b = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (b >= a.B) return;
+  forward_token<F4, DCH, true>(a, b, a.tq, S, a.salida + b * a.d, a.signals + b * 4, nullptr);
+  const int lane = lane_id();
+  if (a.insert && lane < a.T) {
+    const int id = a.ids_out[b * a.T + lane];
+    const int64_t bucket = (b * a.T + lane) * ((int64_t)1 << a.nb) + id;
+    const int c = a.counts[bucket];
+    a.rings[bucket * a.C + c % a.C] = (int32_t)a.tq;
+    a.counts[bucket] = c + 1;
   }
 }
 
@@ -785,6 +864,15 @@ struct LaunchFwd {
 };
 
 template <int F4, int DCH>
+struct LaunchDecode {
+  static int run(const Cand& a, hipStream_t st) {
+    hipLaunchKernelGGL((k_decode_attend<F4, DCH>), dim3((unsigned)((a.B + kWavesPerBlock - 1) / kWavesPerBlock)),
+                       dim3(kWave * kWavesPerBlock), 0, st, a);
+    return check_launch("asrn_decode_attend");
+  }
+};
+
+template <int F4, int DCH>
 struct LaunchBwd {
   static int run(const Cand& a, hipStream_t st) {
     hipLaunchKernelGGL((k_cand_bwd_q<F4, DCH>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
@@ -840,4 +928,23 @@ extern "C" int asrn_candidate_lists(const float* sig, const int32_t* order, cons
   a.B = B; a.L = L; a.T = T; a.C = C; a.K = K;
   hipLaunchKernelGGL(k_cand_lists, grid_of(a), dim3(kWave * kWavesPerBlock), 0, (hipStream_t)stream, a, pos, ell);
   return check_launch("asrn_candidate_lists");
+}
+
+// a14: the generation step's candidate attention over the per-bucket rings (see k_decode_attend)
+extern "C" int asrn_decode_attend(const float* phi, const float* V, const float* Qc, const float* Kc,
+                                  const float* sig, const double* Bt, const float* log_alfa, const float* w_suf,
+                                  const float* gamma, int32_t* rings, int32_t* counts, int64_t B, int64_t cap,
+                                  int64_t t, int32_t d, int32_t nb, int32_t cf, int32_t K, int32_t T, int32_t Tc,
+                                  int32_t C, float scale_phi, float scale_c, int32_t insert, float* salida,
+                                  float* signals, int32_t* ids, void* stream) {
+  Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, nullptr, nullptr, nullptr, B, cap, d, T * nb, cf,
+                K, T, Tc, C, scale_phi, scale_c);
+  if (check_args(a, "asrn_decode_attend")) return 1;
+  ASRN_REQUIRE(nb >= 1 && nb <= 14, "asrn_decode_attend: nb=%d must be in [1, 14]", nb);
+  ASRN_REQUIRE(t >= 0 && t < cap, "asrn_decode_attend: position t=%lld outside the caches (capacity %lld)",
+               (long long)t, (long long)cap);
+  if (B == 0) return 0;
+  a.rings = rings; a.counts = counts; a.ids_out = ids; a.nb = nb; a.tq = t; a.insert = insert ? 1 : 0;
+  a.salida = salida; a.signals = signals;
+  return dispatch<LaunchDecode>(a, (hipStream_t)stream);
 }

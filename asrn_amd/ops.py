@@ -256,3 +256,99 @@ class Candidates(torch.autograd.Function):
         dw = part[T:]
         return (dphi.to(tp), dV.to(tv), dQc.to(tq), dKc.to(tk), dBt, dla.to(tl), dw, dgamma, None, None, None, None,
                 None)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a14: the O(1) generation step's state
+# ---------------------------------------------------------------------------------------------------------------------
+
+def ring_build(phi_prefix, T, nb, C):
+    """Rings of the positions of phi_prefix (B, n, P): rings (B*T, 2^nb, C) int32 (-1 empty) and counts (B*T, 2^nb)
+    int32; the r-th position to enter a bucket sits in slot r % C (asrn/nucleo.py:1585-1607)."""
+    dev = _dev(phi_prefix)
+    B, n, _ = phi_prefix.shape
+    rings = torch.empty((B * T, 2 ** nb, C), dtype=I32, device=dev)
+    counts = torch.empty((B * T, 2 ** nb), dtype=I32, device=dev)
+    if n > 0:
+        _, order, ids_s, _, _ = bucket_sort(phi_prefix, T, nb, C)
+    else:
+        order = ids_s = None
+    call('asrn_ring_build', ptr(order), ptr(ids_s), B, n, T, nb, C, ptr(rings), ptr(counts), stream_of(dev))
+    return rings, counts
+
+
+def decode_attend(cache, t, rings, counts, w_suf, gamma, shape, insert):
+    """The step's candidate attention for position t of the caches (dict of (B, cap, .) tensors phi, V, Qc, Kc, sig,
+    Bt, log_alfa) over the rings; with insert, t then enters the rings. Returns salida (B, d), signals (B, 4) and
+    the bucket ids (B, T)."""
+    T, Tc, C, K, nb = shape['T'], shape['Tc'], shape['C'], shape['K'], shape['nb']
+    phi, V = cache['phi'], cache['V']
+    dev = _dev(phi)
+    B, cap, P = phi.shape
+    d, cf = V.shape[-1], cache['Qc'].shape[-1]
+    if P != T * nb:
+        raise ValueError(f'phi has {P} features, expected T * nb = {T * nb}')
+    salida = torch.empty((B, d), dtype=torch.float32, device=dev)
+    signals = torch.empty((B, 4), dtype=torch.float32, device=dev)
+    ids = torch.empty((B, T), dtype=I32, device=dev)
+    w = _c(w_suf.detach(), torch.float32)
+    g = _c(gamma.detach(), torch.float32)
+    call('asrn_decode_attend', ptr(phi), ptr(V), ptr(cache['Qc']), ptr(cache['Kc']), ptr(cache['sig']),
+         ptr(cache['Bt']), ptr(cache['log_alfa']), ptr(w), ptr(g), ptr(rings), ptr(counts), B, cap, t, d, nb, cf, K,
+         T, Tc, C, float(P) ** -0.5, float(cf) ** -0.5, 1 if insert else 0, ptr(salida), ptr(signals), ptr(ids),
+         stream_of(dev))
+    return salida, signals, ids
+
+
+def _pow2_at_least(x):
+    c = 1
+    while c < x:
+        c *= 2
+    return c
+
+
+class HawkesTable:
+    """Per (b, j) open-addressing tables of the Hawkes memory (asrn/nucleo.py:1634-1714): keys (B*n, cap) uint64
+    codes, Bu (B*n, cap) fp64, A (B*n, cap) fp32; cap a power of two kept >= 2x the keys a table can hold."""
+
+    def __init__(self, B, n, cap, dev):
+        self.B, self.n, self.cap = B, n, cap
+        self.keys = torch.empty((B * n, cap), dtype=torch.int64, device=dev)   # uint64 bits
+        self.Bu = torch.empty((B * n, cap), dtype=torch.float64, device=dev)
+        self.A = torch.empty((B * n, cap), dtype=torch.float32, device=dev)
+
+    @classmethod
+    def load(cls, keys, order, rep, hawkes, Bt, log_alfa, cap=None):
+        """The memory after a text of L: keys (B, L, n), order / rep (B, n, L) from ngram_sort, hawkes (B, L, n)."""
+        dev = _dev(keys)
+        B, L, n = keys.shape
+        tab = cls(B, n, _pow2_at_least(max(cap or 0, 2 * L, 2)), dev)
+        call('asrn_hawkes_table_load', ptr(_c(keys, torch.float64)), ptr(order), ptr(rep),
+             ptr(_c(hawkes, torch.float32)), ptr(_c(Bt, torch.float64)), ptr(_c(log_alfa, torch.float32)), B, L, n,
+             tab.cap, ptr(tab.keys), ptr(tab.Bu), ptr(tab.A), stream_of(dev))
+        return tab
+
+    def reserve(self, positions):
+        """Grows (rehashes) the tables so they can hold the keys of `positions` positions."""
+        if self.cap >= 2 * positions:
+            return
+        dev = self.keys.device
+        new = HawkesTable(self.B, self.n, _pow2_at_least(2 * positions), dev)
+        call('asrn_hawkes_table_grow', ptr(self.keys), ptr(self.Bu), ptr(self.A), self.B * self.n, self.cap,
+             ptr(new.keys), ptr(new.Bu), ptr(new.A), new.cap, stream_of(dev))
+        self.keys, self.Bu, self.A, self.cap = new.keys, new.Bu, new.A, new.cap
+
+    def step(self, cache, t, beta_t, coef, kappa, kappa_r, racha):
+        """Position t: Bt[:, t] = Bt[:, t-1] + beta_t (written into cache['Bt']), vistos and hawkes (B, n); racha (B)
+        is updated in place (asrn/nucleo.py:953-960, 1683-1714, 1826)."""
+        dev = _dev(racha)
+        self.reserve(t + 1)
+        sig, Bt, la = cache['sig'], cache['Bt'], cache['log_alfa']
+        B, stride = sig.shape
+        vistos = torch.empty((B, self.n), dtype=torch.float32, device=dev)
+        hawkes = torch.empty((B, self.n), dtype=torch.float32, device=dev)
+        call('asrn_repetition_step', ptr(sig), ptr(Bt), ptr(la), ptr(_c(beta_t, torch.float64)),
+             ptr(_c(coef, torch.float64)), ptr(_c(kappa.detach(), torch.float32)),
+             ptr(_c(kappa_r.detach(), torch.float32)), B, stride, t, self.n, self.cap, ptr(self.keys), ptr(self.Bu),
+             ptr(self.A), ptr(racha), ptr(vistos), ptr(hawkes), stream_of(dev))
+        return vistos, hawkes

@@ -136,6 +136,49 @@ int asrn_streak_bwd(const float* vistos, const double* beta, const float* kappa_
                     const float* dracha, int64_t B, int64_t L, int32_t n, double* dbeta, float* dkappa_r,
                     void* stream);
 
+/* ---- a14: the O(1) generation step (asrn/nucleo.py:1585-1854, asrn/estable.py:359-372) ------------------------
+ * Rings: rings (B*T, 2^nb, C) int32 positions (-1 empty), counts (B*T, 2^nb) int32. The r-th position to enter a
+ * bucket sits in slot r % C (the C most recent are kept).
+ *
+ * ring_build replaces _anillo_desde (asrn/nucleo.py:1585-1607): rings of positions 0..n-1 from their stable bucket
+ * sort (asrn_bucket_sort over those n positions: order and ids_sorted, rows of n). Fills and builds. */
+int asrn_ring_build(const int32_t* order, const int32_t* ids_sorted, int64_t B, int64_t n, int32_t T, int32_t nb,
+                    int32_t C, int32_t* rings, int32_t* counts, void* stream);
+
+/* decode_attend replaces _candidatos + _atender_cand + _acc_cand (asrn/nucleo.py:1621-1631, asrn/estable.py:359-372,
+ * asrn/nucleo.py:947-951), and with insert != 0 also _anillo_meter (asrn/nucleo.py:1610-1618) after the attention.
+ * The caches are (B, cap, .) rows: phi (P = T*nb), V (d), Qc, Kc (cf), sig, Bt (fp64), log_alfa; row t is the
+ * query (its phi, Qc, sig and Bt must be written), rows < t with a ring entry are the candidates (V[t-1] included).
+ * Out: salida (B, d) summed over tables, signals (B, 4) = (peso_total, mejor, pico, peso_ctx) as in
+ * asrn_candidates_fwd, ids (B, T) the query's bucket ids. */
+int asrn_decode_attend(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
+                       const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
+                       int32_t* rings, int32_t* counts, int64_t B, int64_t cap, int64_t t, int32_t d, int32_t nb,
+                       int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C, float scale_phi, float scale_c,
+                       int32_t insert, float* salida, float* signals, int32_t* ids, void* stream);
+
+/* Hawkes memory: per (b, j) group an open-addressing table of cap slots (a power of two, >= 2x the keys it can
+ * hold): tab_keys (B*n, cap) uint64 key codes, tab_Bu (B*n, cap) fp64 clock of the last occurrence, tab_A (B*n, cap)
+ * fp32 lambda + alfa there.
+ * hawkes_table_load replaces _MemoriaHawkes.cargar (asrn/nucleo.py:1656-1681): the state after a text of L from its
+ * asrn_ngram_sort outputs (keys, order, repeated) and asrn_hawkes_fwd's hawkes; cap >= 2 L.
+ * hawkes_table_grow replaces _MemoriaHawkes._ranuras' doubling (asrn/nucleo.py:1649-1654): rehash into new_cap. */
+int asrn_hawkes_table_load(const double* keys, const int32_t* order, const uint8_t* repeated, const float* hawkes,
+                           const double* Bt, const float* log_alfa, int64_t B, int64_t L, int32_t n, int64_t cap,
+                           uint64_t* tab_keys, double* tab_Bu, float* tab_A, void* stream);
+int asrn_hawkes_table_grow(const uint64_t* old_keys, const double* old_Bu, const float* old_A, int64_t groups,
+                           int64_t old_cap, uint64_t* new_keys, double* new_Bu, float* new_A, int64_t new_cap,
+                           void* stream);
+
+/* repetition_step replaces the clock advance (asrn/nucleo.py:1826), the step's n-gram keys (_claves_de,
+ * asrn/nucleo.py:175-186), _MemoriaHawkes.paso (asrn/nucleo.py:1683-1714) and _repeticion_o1
+ * (asrn/nucleo.py:953-960) for position t: Bt[:, t] = Bt[:, t-1] + beta_t (written), vistos and hawkes (B, n) out,
+ * racha (B) updated in place. sig, Bt, log_alfa are (B, stride) caches; cap >= 2 (t + 1). */
+int asrn_repetition_step(const float* sig, double* Bt, const float* log_alfa, const double* beta_t,
+                         const double* coef, const float* kappa, const float* kappa_r, int64_t B, int64_t stride,
+                         int64_t t, int32_t n, int64_t cap, uint64_t* tab_keys, double* tab_Bu, float* tab_A,
+                         float* racha, float* vistos, float* hawkes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,238 @@
+"""The O(1) generation step on the GPU, through the C ABI, against the oracle (oracle/generation.py) and against the
+whole-text layer.
+
+Bit-exact: ring contents slot by slot and counts (after the prompt and after every insert), the step's bucket ids,
+the Hawkes memory's seen flags. Within 1e-3 relative (fp32): the step's candidate attention output and gate
+signals, Hawkes intensities, streak, and the layer output written step by step. Each test prints its case first."""
+import numpy as np
+import pytest
+import torch
+
+import asrn_amd
+from asrn_amd import ops, synth
+from asrn_amd.capa import CapaASRNEstable
+from asrn_amd.escritura import EscritorCapa
+from oracle import generation as G
+from oracle import layer as O
+
+pytestmark = pytest.mark.gpu
+DEV = 'cuda'
+TOL = 1e-3
+
+
+def say(*a):
+    print('[case]', *a, flush=True)
+
+
+def rel_err(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    if a.numel() == 0:
+        return 0.0
+    return (a - b).abs().max().item() / (b.abs().max().item() + 1e-12)
+
+
+def assert_close(a, b, what, tol=TOL):
+    e = rel_err(a, b)
+    assert e <= tol, f'{what}: relative error {e:.3g} > {tol}'
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip('needs a GPU')
+    asrn_amd.load()
+
+
+def token_phi(B, L, V, T, nb, seed):
+    """phi whose word half depends on the token and context half on (token, previous token): buckets repeat."""
+    g = torch.Generator().manual_seed(seed)
+    x = synth.tokens(B, L, V, frac=0.3, span=(4, 16), seed=seed)
+    P = T * nb
+    emb = torch.randn(V, P, generator=g)
+    prev = torch.cat([x[:, :1], x[:, :-1]], 1)
+    phi = torch.cat([emb[x][..., :P // 2], emb[x][..., P // 2:] + 0.7 * emb[prev][..., P // 2:]], -1).contiguous()
+    return x, phi, g
+
+
+def gpu_rings_as_oracle(rings, counts, B, T):
+    nc, C = rings.shape[1], rings.shape[2]
+    return rings.cpu().numpy().reshape(B, T, nc, C), counts.cpu().numpy().reshape(B, T, nc).astype(np.int64)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# rings
+# ---------------------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize('B,n,T,nb,C,V', [(2, 300, 8, 14, 32, 6), (3, 200, 4, 2, 4, 5), (2, 0, 8, 3, 4, 5),
+                                          (1, 1, 8, 3, 4, 5), (16, 4096, 8, 14, 32, 40), (2, 5000, 8, 4, 64, 3)])
+def test_ring_build_vs_oracle(B, n, T, nb, C, V):
+    say('ring build', B, n, T, nb, C)
+    x, phi, _ = token_phi(B, max(n, 1), V, T, nb, seed=n)
+    phi = phi[:, :n]
+    rings, counts = ops.ring_build(phi.to(DEV), T, nb, C)
+    ids = O.bucket_ids(phi, T, nb).numpy() if n else np.zeros((B, 0, T), dtype=np.int32)
+    ring_ref, count_ref = G.ring_from(ids, n, C, 2 ** nb)
+    got_ring, got_count = gpu_rings_as_oracle(rings, counts, B, T)
+    assert np.array_equal(got_count, count_ref)
+    assert np.array_equal(got_ring, ring_ref)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# the step's candidate attention, with inserts
+# ---------------------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize('B,t0,steps,d,C,nb,T,V', [(2, 300, 24, 64, 32, 14, 8, 6), (3, 100, 40, 96, 4, 2, 4, 5),
+                                                   (2, 1, 30, 256, 16, 4, 8, 4), (1, 500, 8, 1024, 8, 3, 8, 7),
+                                                   (16, 2000, 4, 768, 32, 14, 8, 50)])
+def test_decode_attend_vs_oracle(B, t0, steps, d, C, nb, T, V):
+    say('decode attend', B, t0, steps, d, C, nb, T)
+    L = t0 + steps
+    cf, K, Tc = 16, 4, T // 2
+    x, phi, g = token_phi(B, L, V, T, nb, seed=t0 + d)
+    cache = dict(phi=phi, V=torch.randn(B, L, d, generator=g), Qc=torch.randn(B, L, cf, generator=g),
+                 Kc=torch.randn(B, L, cf, generator=g), sig=x.float(),
+                 Bt=(torch.rand(B, L, generator=g, dtype=torch.float64) * 1.5).cumsum(1),
+                 log_alfa=torch.randn(B, L, generator=g) * 0.3)
+    w_suf = torch.randn(K + 1, generator=g) * 0.5
+    gamma = torch.rand(T, generator=g) * 2
+    sh = O.Shape(d=d, T=T, nb=nb, C=C, Tc=Tc, cf=cf, K=K)
+    ids = O.bucket_ids(phi, T, nb).numpy()
+    ring, count = G.ring_from(ids, t0, C, 2 ** nb)
+    dcache = {k: v.to(DEV).contiguous() for k, v in cache.items()}
+    rings = torch.from_numpy(ring.reshape(B * T, 2 ** nb, C)).to(DEV)
+    counts = torch.from_numpy(count.reshape(B * T, 2 ** nb).astype(np.int32)).to(DEV)
+    shape = dict(T=T, Tc=Tc, C=C, K=K, nb=nb)
+    for t in range(t0, L):
+        sal, sen, got_ids = ops.decode_attend(dcache, t, rings, counts, w_suf.to(DEV), gamma.to(DEV), shape,
+                                              insert=True)
+        ref_sal, ref_sen = G.attend(G.ring_positions(ring, ids[:, t]), t, cache['phi'], cache['V'], cache['Qc'],
+                                    cache['Kc'], cache['sig'], cache['Bt'], cache['log_alfa'], w_suf, gamma, sh)
+        assert np.array_equal(got_ids.cpu().numpy(), ids[:, t]), t
+        assert_close(sal, ref_sal, f'salida t={t}')
+        assert torch.equal(sen[:, 0].cpu(), ref_sen[:, 0]), t                  # tables with candidates
+        assert torch.equal(sen[:, 3].cpu(), ref_sen[:, 3]), t
+        assert_close(sen[:, 1], ref_sen[:, 1], f'mejor t={t}')
+        assert_close(sen[:, 2], ref_sen[:, 2], f'pico t={t}')
+        G.ring_insert(ring, count, ids[:, t], t)
+        got_ring, got_count = gpu_rings_as_oracle(rings, counts, B, T)
+        assert np.array_equal(got_count, count) and np.array_equal(got_ring, ring), f'rings after insert t={t}'
+
+
+def test_decode_attend_without_insert_leaves_rings():
+    say('decode attend, no insert')
+    B, L, T, nb, C, d = 2, 80, 8, 3, 4, 64
+    x, phi, g = token_phi(B, L, 5, T, nb, seed=11)
+    cache = dict(phi=phi, V=torch.randn(B, L, d, generator=g), Qc=torch.randn(B, L, 16, generator=g),
+                 Kc=torch.randn(B, L, 16, generator=g), sig=x.float(),
+                 Bt=torch.rand(B, L, generator=g, dtype=torch.float64).cumsum(1), log_alfa=torch.zeros(B, L))
+    dcache = {k: v.to(DEV).contiguous() for k, v in cache.items()}
+    rings, counts = ops.ring_build(phi[:, :40].to(DEV), T, nb, C)
+    r0, c0 = rings.clone(), counts.clone()
+    for t in range(40, 60):
+        ops.decode_attend(dcache, t, rings, counts, torch.zeros(5, device=DEV), torch.ones(T, device=DEV),
+                          dict(T=T, Tc=4, C=C, K=4, nb=nb), insert=False)
+    assert torch.equal(rings, r0) and torch.equal(counts, c0)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# Hawkes memory and streak
+# ---------------------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize('B,L0,steps,V,n', [(3, 50, 150, 5, 4), (2, 1, 60, 3, 4), (4, 700, 40, 30, 4), (2, 20, 30, 4, 6)])
+def test_hawkes_table_vs_oracle(B, L0, steps, V, n):
+    say('hawkes table', B, L0, steps, V, n)
+    L = L0 + steps
+    g = torch.Generator().manual_seed(L0)
+    x = synth.tokens(B, L, V, frac=0.3, span=(3, 10), seed=L0)
+    sig = x.float()
+    beta = torch.rand(B, L, generator=g, dtype=torch.float64) * 2
+    Bt = beta.cumsum(1)
+    la = torch.randn(B, L, generator=g) * 0.5
+    coef = torch.rand(n, generator=torch.Generator().manual_seed(12345), dtype=torch.float64) + 0.5
+    kappa = torch.rand(n, generator=g) * 0.3 + 0.01
+    kappa_r = torch.rand(1, generator=g) * 0.1 + 0.01
+    keys, order, rep, rank_k, vistos = ops.ngram_sort(sig[:, :L0].to(DEV), coef.to(DEV), n)
+    hk = ops.Hawkes.apply(Bt[:, :L0].to(DEV), la[:, :L0].to(DEV), kappa.to(DEV), order, rep, rank_k)
+    tab = ops.HawkesTable.load(keys, order, rep, hk, Bt[:, :L0].to(DEV), la[:, :L0].to(DEV))
+    mem = G.HawkesMemory(B, n)
+    mem.load(keys.cpu(), hk.cpu(), Bt[:, :L0], la[:, :L0])
+    cache = dict(sig=sig.to(DEV).contiguous(), Bt=torch.zeros(B, L, dtype=torch.float64, device=DEV),
+                 log_alfa=la.to(DEV).contiguous())
+    cache['Bt'][:, :L0] = Bt[:, :L0].to(DEV)
+    racha = torch.rand(B, generator=g).to(DEV)
+    racha_ref = racha.cpu().clone()
+    all_keys = O.ngram_keys(sig, coef, n)
+    cap0 = tab.cap
+    for t in range(L0, L):
+        v, h = tab.step(cache, t, beta[:, t].to(DEV), coef.to(DEV), kappa.to(DEV), kappa_r.to(DEV), racha)
+        Bq = cache['Bt'][:, t].cpu()
+        assert torch.equal(Bq, Bt[:, t - 1] + beta[:, t]), t
+        v_ref, h_ref = mem.step(all_keys[:, t], Bq, la[:, t], kappa)
+        racha_ref = G.streak_step(v_ref, beta[:, t], racha_ref, kappa_r)
+        assert torch.equal(v.cpu(), v_ref), t
+        assert_close(h, h_ref, f'hawkes t={t}', 1e-5)
+        assert_close(racha, racha_ref, f'racha t={t}', 1e-5)
+    assert tab.cap > cap0 or 2 * L <= cap0                 # the tables grew when they had to
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# the layer written step by step
+# ---------------------------------------------------------------------------------------------------------------------
+
+def write(layer, E, h, x, L0, ajeno, capacidad):
+    esc = EscritorCapa(layer, memoria_de_lo_ajeno=ajeno)
+    Ed, hd, xd = E.to(DEV), h.to(DEV), x.to(DEV)
+    y0 = esc.inicio(Ed[:, :L0], hd[:, :L0], xd[:, :L0], capacidad=capacidad)
+    ys = [esc.paso(Ed[:, t], hd[:, t], xd[:, t]) for t in range(L0, E.shape[1])]
+    return y0, torch.stack(ys, 1), esc
+
+
+def ids_agree(layer, E, sh, ref=None):
+    """The step's phi (two-row GEMMs) and the whole text's (one fused GEMM) give the same bucket ids (and `ref`)."""
+    with torch.no_grad():
+        whole, _ = layer._phi_y_valores(E.to(DEV))
+        Ed = E.to(DEV)
+        step = torch.stack([layer._phi(Ed[:, max(0, t - 1):t + 1])[:, -1] for t in range(E.shape[1])], 1)
+    a, b = O.bucket_ids(whole.cpu(), sh.T, sh.nb), O.bucket_ids(step.cpu(), sh.T, sh.nb)
+    return torch.equal(a, b) and (ref is None or torch.equal(a, ref))
+
+
+SMALL = dict(chunk=4, n_bits=2, n_tablas=4, tablas_contexto=2)
+
+
+@pytest.mark.parametrize('B,L0,n,kw', [(2, 40, 50, SMALL), (1, 2, 30, SMALL), (3, 1, 20, SMALL), (2, 300, 60, {}),
+                                       (2, 64, 40, dict(chunk=16, n_bits=4))])
+def test_writer_equals_whole_text(B, L0, n, kw):
+    say('writer = whole text', B, L0, n, kw)
+    d = 64
+    torch.manual_seed(0)
+    layer = synth.move_params(CapaASRNEstable(d, **kw), 0).to(DEV)
+    x, E, h = synth.layer_inputs(B, L0 + n, d, 12, seed=L0, frac=0.4, span=(3, 8))
+    sh = O.shape_from_params({k: v.cpu() for k, v in layer.state_dict().items()}, d, n_bits=layer.n_bits,
+                             C=layer.chunk)
+    if not ids_agree(layer, E, sh):
+        pytest.skip('a bucket id differs between the step GEMM and the whole-text GEMM (sign of phi near 0)')
+    y0, ys, esc = write(layer, E, h, x, L0, ajeno=False, capacidad=L0 + 3)
+    with torch.no_grad():
+        y = layer(E.to(DEV), h.to(DEV), x.to(DEV))
+    assert_close(y0, y[:, :L0], 'prompt')
+    assert_close(ys, y[:, L0:], 'steps')
+    assert esc.cap >= L0 + n
+
+
+@pytest.mark.parametrize('ajeno', [True, False])
+@pytest.mark.parametrize('B,L0,n,kw', [(2, 40, 30, SMALL), (1, 2, 12, SMALL), (2, 100, 20, {})])
+def test_writer_vs_oracle(B, L0, n, kw, ajeno):
+    say('writer vs oracle', B, L0, n, kw, ajeno)
+    d = 32
+    torch.manual_seed(1)
+    layer = synth.move_params(CapaASRNEstable(d, **kw), 1).to(DEV)
+    p = {k: v.detach().cpu() for k, v in layer.state_dict().items()}
+    sh = O.shape_from_params(p, d, n_bits=layer.n_bits, C=layer.chunk)
+    x, E, h = synth.layer_inputs(B, L0 + n, d, 10, seed=5, frac=0.4, span=(3, 8))
+    phi_cpu = torch.stack([O.phi_and_values(p, E[:, max(0, t - 1):t + 1])[0][:, -1] for t in range(L0 + n)], 1)
+    if not ids_agree(layer, E, sh, O.bucket_ids(phi_cpu, sh.T, sh.nb)):
+        pytest.skip('a bucket id differs between the GPU GEMMs and the CPU one (sign of phi near 0)')
+    _, ys, _ = write(layer, E, h, x, L0, ajeno=ajeno, capacidad=0)
+    ref, _ = G.decode_layer(p, E, h, x, L0, sh, ajeno=ajeno)
+    assert_close(ys, ref, f'steps ajeno={ajeno}')
