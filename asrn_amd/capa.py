@@ -262,3 +262,25 @@ def _a_autocast(x):
 
 
 ASRNLayer = CapaASRNEstable
+
+
+def convertir(modelo, protecciones=None):
+    """Swaps, in place, every ASRN layer of a model (its `largos` ModuleList, as in the reference's ModeloASRN,
+    asrn/nucleo.py:1072) for this package's CapaASRNEstable with the same hyper-parameters, weights, device and
+    train/eval mode, and returns the model: the counterpart of asrn/estable.py:424-442 for the HIP layer."""
+    base = getattr(modelo, '_orig_mod', modelo)
+    for j, vieja in enumerate(base.largos):
+        d = vieja.v.weight.shape[1]
+        nodos = vieja.d_racha.shape[0]
+        racha_max = int(round(math.expm1(vieja.racha_paso * (nodos - 1))))
+        drop = vieja.drop.p if isinstance(vieja.drop, nn.Dropout) else 0.0
+        nueva = CapaASRNEstable(d, protecciones or getattr(vieja, 'protecciones', None), n_tablas=vieja.n_tablas,
+                                n_bits=vieja.n_bits, afin_oculto=2 * vieja.afin_palabra[0].out_features,
+                                chunk=vieja.chunk, tablas_contexto=vieja.tablas_contexto,
+                                confirmar=vieja.confirmar, sufijo=vieja.sufijo, vistos=vieja.vistos, dropout=drop,
+                                nodos_racha=nodos, racha_max=racha_max)
+        nueva = nueva.to(vieja.v.weight.device)
+        nueva.load_state_dict(vieja.state_dict())
+        nueva.train(vieja.training)
+        base.largos[j] = nueva
+    return modelo

@@ -57,6 +57,24 @@ struct Scratch {
   int off[40];             // entries of table tau: [off[tau], off[tau + 1])
 };
 
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup i runs on XCD i % 8), each with its own L2. Give
+// each XCD a contiguous range of tokens instead, so one XCD's L2 serves one stretch of a batch row (at B = 8, one
+// whole row) and candidates, which are earlier positions of the same row, hit there. The tail that does not divide
+// evenly keeps the identity mapping.
+#ifndef ASRN_XCD_MAP
+#define ASRN_XCD_MAP 1
+#endif
+constexpr int kXcds = 8;
+__device__ __forceinline__ int64_t token_of_wave() {
+  const int64_t n = gridDim.x, i = blockIdx.x;
+  int64_t blk = i;
+  if (ASRN_XCD_MAP) {
+    const int64_t per = n / kXcds;
+    if (i < per * kXcds) blk = (i % kXcds) * per + i / kXcds;
+  }
+  return blk * kWavesPerBlock + (threadIdx.x >> 6);
+}
+
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -524,7 +542,7 @@ template <int F4, int DCH>
 __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_fwd(Cand a) {
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
-  const int64_t tok = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t tok = token_of_wave();
   if (tok >= a.B * a.L) return;
   forward_token<F4, DCH, false>(a, tok / a.L, tok % a.L, S, a.salida + tok * a.d, a.signals + tok * 4,
                                 a.stats + tok * a.T * 2);
@@ -557,7 +575,7 @@ template <int F4, int DCH>
 __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
-  const int64_t tok = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t tok = token_of_wave();
   if (tok >= a.B * a.L) return;
   const int lane = lane_id(), half = lane >> 5;
   const int64_t b = tok / a.L, t = tok % a.L;
@@ -674,7 +692,7 @@ template <int F4, int DCH>
 __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_k(Cand a) {
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
-  const int64_t tok = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t tok = token_of_wave();
   if (tok >= a.B * a.L) return;
   const int lane = lane_id(), half = lane >> 5;
   const int64_t b = tok / a.L, k = tok % a.L;
@@ -787,7 +805,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_lists(Cand a, i
                                                                        int32_t* __restrict__ ell) {
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
-  const int64_t tok = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t tok = token_of_wave();
   if (tok >= a.B * a.L) return;
   const int lane = lane_id();
   const int64_t b = tok / a.L, t = tok % a.L;

@@ -79,6 +79,9 @@ class EscritorCapa:
         """One new token at position t: e_t, h_t (B, d) its embedding and layer input, pieza_t (B,) its id ->
         the layer's output (B, d) (the layer part of asrn/nucleo.py:1797-1854)."""
         capa = self.capa
+        # rows of a (B, L, d) text are strided views; the GEMMs below want dense (B, d) operands (a batch stride
+        # above 2^25 elements is outside what hipBLASLt accepts, and its fallback costs ~20 ms per call)
+        e_t, h_t = e_t.contiguous(), h_t.contiguous()
         if self.t >= self.cap:
             self._crecer()
         c, t = self.cache, self.t

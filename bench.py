@@ -1,14 +1,16 @@
 """Benchmark of the ASRN layer hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config cfg2] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config cfg2] [--no-cpu-baseline] [--no-decode]
 
 A step is one forward + backward of one ASRN layer (asrn.ASRNLayer, group-A protections) over one batch of
 synthetic tokens: BASELINE.json configs[1] = cfg2, B 8, N 4096, d 256, V 256, fp32, 30% copied spans. Inputs and
 weights are resident in HBM before the timed region. Prints one JSON line with the driver's keys plus:
   roofline      the dominant HIP kernel: algorithmic bytes per launch / its mean launch time (device events recorded
                 on the stream it runs on), against MI355X's 8 TB/s
-  hip_aggregate BASELINE.md's headline: 7,776 B/token x tokens / (8 TB/s x the sum of the HIP kernels' time per step)
+  hip_aggregate the headline: 7,776 B/token x tokens / (8 TB/s x the sum of the HIP kernels' time per step)
   layer         whole-layer tokens/s and its HBM fraction at 25,876 B/token (the fp32 GEMMs stay PyTorch)
+  decode        the O(1) generation step of one layer (BASELINE.json configs[4] at one layer): per-token latency
+                against the context, 1K to 64K, and its slope
   cpu_baseline  the CPU oracle (oracle/layer.py, PyTorch on the host cores) on the same workload
 """
 import argparse
@@ -36,8 +38,23 @@ def algorithmic_bytes(d, P, cf, T):
     return {'asrn_candidates_fwd': fwd, 'asrn_candidates_bwd': bwd}
 
 
-HIP_BYTES_PER_TOKEN = 7776            # BASELINE.md / SURVEY 8(d): all HIP kernels of one fwd+bwd at cfg2
-LAYER_BYTES_PER_TOKEN = 25876         # whole layer at cfg2
+# all HIP kernels of one fwd+bwd at cfg2, each distinct tensor read once and written once: hash + bucket sort 512,
+# clock 16 + 16, n-gram sort 28, Hawkes/streak scans 60 + 100, candidates 2,724 + 4,320 (fwd + bwd)
+HIP_BYTES_PER_TOKEN = 7776
+LAYER_BYTES_PER_TOKEN = 25876         # whole layer at cfg2: the above plus the GEMM-boundary tensors and their grads
+
+
+TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'cfg2_traffic.json')
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of an entry point from the committed counter passes (FETCH_SIZE and WRITE_SIZE, scaled
+    by a copy of known size), or None when they were not taken for this build."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)['bytes_per_launch'].get(kernel)
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def cpu_baseline(layer_cpu, x, E, h, gy, reps=2):
@@ -65,6 +82,69 @@ def cpu_baseline(layer_cpu, x, E, h, gy, reps=2):
             'seconds_per_step': round(t, 3)}
 
 
+DECODE = dict(B=16, d=768, V=50304, contexts=(1024, 4096, 16384, 32768, 65536), frac=0.2, span=(16, 256),
+              zipf=1.1)
+
+
+def decode_bench(dev, steps, warmup, seed=0, contexts=None):
+    """BASELINE.json configs[4], one layer: the O(1) generation step of one ASRN layer at d = 768, B = 16, after a
+    prefill of each context length. Per-token latency (wall clock over `steps` back-to-back steps, synchronized at
+    both ends) against the context, and the least-squares slope with its 95% interval (O(1): it includes 0)."""
+    import torch
+
+    import asrn_amd
+    from asrn_amd import _lib, synth
+
+    cfg = DECODE
+    B, d, V = cfg['B'], cfg['d'], cfg['V']
+    contexts = contexts or cfg['contexts']
+    torch.manual_seed(seed)
+    layer = synth.move_params(asrn_amd.ASRNLayer(d), seed=seed).to(dev)
+    g = torch.Generator(device=dev).manual_seed(seed + 7)
+    emb = torch.randn(V, d, generator=g, device=dev)
+    rows = []
+    kern = {}
+    for ctx in contexts:
+        x = synth.tokens(B, ctx + warmup + steps, V, frac=cfg['frac'], span=cfg['span'], zipf=cfg['zipf'],
+                         seed=seed + ctx).to(dev)
+        E = emb[x]
+        h = torch.randn(B, x.shape[1], d, generator=g, device=dev)
+        esc = asrn_amd.EscritorCapa(layer, memoria_de_lo_ajeno=False)     # every position a key: the rings update
+        esc.inicio(E[:, :ctx], h[:, :ctx], x[:, :ctx], capacidad=ctx + warmup + steps + 1)
+        for t in range(ctx, ctx + warmup):
+            esc.paso(E[:, t], h[:, t], x[:, t])
+        timed = _lib.time_calls(['asrn_decode_attend', 'asrn_repetition_step'])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for t in range(ctx + warmup, ctx + warmup + steps):
+            esc.paso(E[:, t], h[:, t], x[:, t])
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        timed = _lib.stop_timing()
+        for n, evs in timed.items():
+            kern.setdefault(n, []).extend(s.elapsed_time(e) for s, e in evs)
+        ms = 1e3 * (t1 - t0) / steps
+        rows.append({'context': ctx, 'ms_per_step': round(ms, 4), 'tokens_per_s': round(B * 1e3 / ms, 1)})
+        del esc, E, h, x
+        torch.cuda.empty_cache()
+    xs = [r['context'] for r in rows]
+    ys = [r['ms_per_step'] * 1e6 for r in rows]        # ns
+    n = len(xs)
+    mx, my = sum(xs) / n, sum(ys) / n
+    sxx = sum((a - mx) ** 2 for a in xs)
+    slope = sum((a - mx) * (b - my) for a, b in zip(xs, ys)) / sxx if sxx else 0.0
+    res = [b - (my + slope * (a - mx)) for a, b in zip(xs, ys)]
+    se = (sum(r * r for r in res) / max(n - 2, 1) / sxx) ** 0.5 if sxx else 0.0
+    t975 = {1: 12.71, 2: 4.30, 3: 3.18, 4: 2.78, 5: 2.57}.get(n - 2, 2.0)
+    return {'workload': f'configs[4], one layer: O(1) generation step of one ASRN layer, d={d}, B={B}, V={V}, '
+                        f'Zipf 1.1 with 20% copied spans, prefill of each context then {warmup} + {steps} steps',
+            'per_context': rows, 'tokens_per_s': rows[-1]['tokens_per_s'],
+            'slope_ns_per_context_token': round(slope, 4),
+            'slope_ci95': [round(slope - t975 * se, 4), round(slope + t975 * se, 4)],
+            'kernels': {k: {'launches': len(v), 'mean_us': round(1e3 * sum(v) / len(v), 3)} for k, v in kern.items()
+                        if v}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -73,17 +153,31 @@ def main():
     ap.add_argument('--config', default='cfg2')
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--no-decode', action='store_true')
+    ap.add_argument('--decode-steps', type=int, default=32)
+    ap.add_argument('--copy-calibration', type=int, default=0, metavar='BYTES',
+                    help='only run a plain device-to-device copy of BYTES, 3 times: the reference point that scales '
+                         'the FETCH_SIZE / WRITE_SIZE counters of a profiler run into bytes')
     args = ap.parse_args()
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
         print(f'bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): the ASRN hot path '
-              'shards over the batch with no exchange; see DESIGN.md for how it would scale.', file=sys.stderr)
+              'shards over the batch with no exchange between GPUs.', file=sys.stderr)
         sys.exit(2)
 
     import torch
 
     import asrn_amd
     from asrn_amd import _lib, synth
+
+    if args.copy_calibration:
+        src = torch.ones(args.copy_calibration // 4, dtype=torch.float32, device='cuda:0')
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({'copy_calibration_bytes': src.numel() * 4, 'launches': 3}), flush=True)
+        return
 
     asrn_amd.load()
     cfg = synth.CONFIGS[args.config]
@@ -143,7 +237,7 @@ def main():
         'config': {'workload': f'{args.config}: one ASRN layer fwd+bwd, B={B}, N={N}, d={d}, V={V}, T=8 tables x 14 '
                                f'bits, C=32, fp32', 'global_batch': B, 'seq_len': N, 'parallelism': 'none (1 GPU)'},
         'roofline': {'bound': 'hbm', 'kernel': dom, 'achieved': round(achieved / 1e9, 1), 'peak': HBM_PEAK / 1e9,
-                     'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK, 4), 'traffic': None,
+                     'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK, 4), 'traffic': measured_traffic(dom),
                      'bytes_per_token': algo[dom], 'mean_launch_us': round(dom_us, 2)},
         'hip_aggregate': {'bytes_per_token': HIP_BYTES_PER_TOKEN, 'hip_ms_per_step': round(hip_ms_per_step, 4),
                           'frac': round(HIP_BYTES_PER_TOKEN * tokens / (HBM_PEAK * hip_ms_per_step * 1e-3), 4)},
@@ -152,6 +246,8 @@ def main():
         'kernels': {n: {k: round(v, 3) if isinstance(v, float) else v for k, v in s.items()}
                     for n, s in sorted(per_call.items(), key=lambda kv: -kv[1]['total_ms'])},
     }
+    if not args.no_decode:
+        out['decode'] = decode_bench(dev, args.decode_steps, 5, seed=args.seed)
     if not args.no_cpu_baseline:
         out['cpu_baseline'] = cpu_baseline(layer_cpu, x, E, h, gy)
     print(json.dumps(out), flush=True)

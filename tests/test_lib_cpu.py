@@ -123,3 +123,23 @@ def test_unsupported_protections_and_shapes_raise_clearly():
         layer = CapaASRNEstable(16, protecciones=asrn_amd.Protecciones.ninguna())
         with pytest.raises(RuntimeError, match='GPU only'):
             layer._revisar(torch.zeros(1, 2, 16))
+
+
+def test_convertir_swaps_layers_keeping_weights():
+    """convertir (the counterpart of asrn/estable.py:424-442) rebuilds each layer with the same hyper-parameters and
+    weights; construction only, no device work."""
+    class Modelo(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.largos = torch.nn.ModuleList([CapaASRNEstable(16, chunk=8, n_bits=5, racha_max=100, nodos_racha=9),
+                                               CapaASRNEstable(16)])
+    m = Modelo()
+    before = [{k: v.clone() for k, v in c.state_dict().items()} for c in m.largos]
+    old = list(m.largos)
+    m.eval()
+    asrn_amd.convertir(m)
+    for c, o, sd in zip(m.largos, old, before):
+        assert c is not o and not c.training
+        assert (c.chunk, c.n_bits, c.racha_paso) == (o.chunk, o.n_bits, o.racha_paso)
+        for k, v in c.state_dict().items():
+            assert torch.equal(v, sd[k]), k
