@@ -14,9 +14,10 @@
 //           flight. Each table adds its own clock term; the exact masked softmax runs with one entry per lane.
 //   gather  each distinct candidate's V row is read once by the 64 lanes with the weights summed over the tables,
 //           8+ rows in flight: the table sum never leaves the kernel.
-// The backward has one owner per output row and no atomics: a query pass (query-side gradients, D = sum att*dp per
-// (query, table), per-query partials of d gamma and d w_suf) and a key pass (key-side gradients; att rebuilt from the
-// forward's saved max and denominator, each dO_q row loaded once for both dp and dV).
+// The forward also keeps every candidate's weight att at [query][table][distance - 1]. The backward has one owner per
+// output row, no atomics and no score recomputation: a query pass (ds = att (dp - D) with D = sum att*dp per (query,
+// table), written to the same slots; query-side gradients; per-query partials of d gamma and d w_suf) and a key pass
+// (key-side gradients: reads att and ds at the slots of the queries that see the key).
 #include "common.h"
 
 namespace asrn {
@@ -34,27 +35,39 @@ struct Cand {
   int d, P, cf, K, T, Tc, C;
   int vec;            // P and cf multiples of 4: feature rows load as float4
   float sp, sc;
-  // forward outputs
-  float* salida; float* signals; float* stats;
-  // backward
-  const float* dsal; const float* stats_in; float* dphi; float* dV; float* dQc; float* dKc; double* dBt;
-  float* dla; float* qstats; float* partials;
+  // forward outputs; att (B*L, T, C): the weight of the key at distance j + 1 before the query, at slot j
+  float* salida; float* signals; float* att;
+  // backward; ds (B*L, T, C) laid out like att, written by the query pass for the key pass
+  const float* dsal; const float* att_in; float* dphi; float* dV; float* dQc; float* dKc; double* dBt;
+  float* dla; float* ds; float* partials;
   // generation: per-bucket rings (B*T, 2^nb, C) of positions and their counts (B*T, 2^nb); the query position tq,
   // its bucket ids (B, T) out, and whether tq then enters the rings
   int32_t* rings; int32_t* counts; int32_t* ids_out; int nb; int64_t tq; int insert;
 };
 
 // per-wave LDS scratch: one token's candidate list (entries) and its distinct positions (uniques)
+constexpr int kHash = 2 * kMaxSlots;   // dedupe hash slots: at most kMaxSlots distinct positions, so probes end
+
 struct Scratch {
   int key[kMaxSlots];      // entry: (position << 5) | table
   int uid[kMaxSlots];      // entry -> unique
   int upos[kMaxSlots];     // unique: position
-  float ua[kMaxSlots];     // unique: base score, then (base + w_suf[ell]) + log_alfa_k
-  float ub[kMaxSlots];     // unique: fp32(Bt_k - Bt_q); the key side overwrites it with dp
-  float uc[kMaxSlots];     // unique: sum over tables of att (forward, key side) or dp (query side)
-  float ud[kMaxSlots];     // unique: sum over tables of ds
+  union {
+    struct {
+      float ua[kMaxSlots];   // unique: base score, then (base + w_suf[ell]) + log_alfa_k; per entry in the backward
+      float ub[kMaxSlots];   // unique: fp32(Bt_k - Bt_q)
+      float uc[kMaxSlots];   // unique: sum over tables of att (forward, key side) or dp (query side)
+      float ud[kMaxSlots];   // unique: sum over tables of ds
+    };
+    struct {                 // the dedupe's hash table, dead once the uniques are numbered
+      int hpos[kHash];       // position held by the slot (-1 empty)
+      int hfirst[kHash];     // the first entry (table-major) with that position
+    };
+  };
   int uell[kMaxSlots];     // unique: suffix-match length (query side)
   int off[40];             // entries of table tau: [off[tau], off[tau + 1])
+  int wrank[32], wlen[32]; // per table: the token's sorted rank and window length
+  float tsum[32];          // per-table sums (backward)
 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup i runs on XCD i % 8), each with its own L2. Give
@@ -158,7 +171,9 @@ __device__ __forceinline__ int suffix_vs(const float* __restrict__ sigb, const f
 }
 
 // Packs every table's window of token (b, t) into S.key and the table segments into S.off. query_window: the
-// `win & 255` sorted ranks before the token's; otherwise (the key pass) the `win >> 8` after it. Returns the count.
+// `win & 255` sorted ranks before the token's; otherwise (the key pass) the `win >> 8` after it. The segment offsets
+// are a prefix sum of the window lengths, so entry m finds its table by a binary search over T offsets and one round
+// of `order` loads fills the list, table-major and oldest first. Returns the count M.
 __device__ __forceinline__ int gather(const Cand& a, int64_t b, int64_t t, bool query_window, Scratch& S) {
   const int lane = lane_id();
   int s = 0, n = 0;
@@ -168,40 +183,37 @@ __device__ __forceinline__ int gather(const Cand& a, int64_t b, int64_t t, bool 
     const int w = a.win[o];
     n = query_window ? (w & 255) : ((w >> 8) & 255);
   }
-  const int slots = a.T * a.C;
-  int pos[kCh], tt[kCh];
-  bool ok[kCh];
-#pragma unroll
-  for (int c = 0; c < kCh; ++c) {
-    const int sl = c * kWave + lane;
-    const int tau = sl < slots ? sl / a.C : 0;
-    const int i = sl - tau * a.C;
-    const int st = __shfl(s, tau, 64), nt = __shfl(n, tau, 64);
-    // query window: slots [C - n, C) hold ranks s - n .. s - 1; key window: slots [0, n) hold s + 1 .. s + n
-    const bool v = sl < slots && (query_window ? i >= a.C - nt : i < nt);
-    const int64_t j = query_window ? (int64_t)st - a.C + i : (int64_t)st + 1 + i;
-    ok[c] = v && j >= 0 && j < a.L;
-    tt[c] = tau;
-    pos[c] = ok[c] ? a.order[(b * a.T + tau) * a.L + j] : 0;
+  int off = 0, M = 0;
+  for (int tt = 0; tt < a.T; ++tt) {
+    const int nt = readlane_i(n, tt);
+    if (lane == tt) off = M;
+    M += nt;
   }
-  int base = 0;
-#pragma unroll
-  for (int c = 0; c < kCh; ++c) {
-    const uint64_t bal = __ballot(ok[c]);
-    if (ok[c]) S.key[base + __popcll(bal & ((1ull << lane) - 1ull))] = (pos[c] << 5) | tt[c];
-    base += __popcll(bal);
+  if (lane < a.T) {
+    S.off[lane] = off;
+    S.wrank[lane] = s;
+    S.wlen[lane] = n;
   }
+  if (lane == 0) S.off[a.T] = M;
   wave_lds_sync();
-  if (lane <= a.T) {
-    int lo = 0, hi = base;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if ((S.key[mid] & 31) < lane) lo = mid + 1; else hi = mid;
+  for (int m0 = 0; m0 < M; m0 += kWave) {
+    const int m = m0 + lane;
+    if (m < M) {
+      int lo = 0, hi = a.T - 1;                  // the last table whose segment starts at or before m
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (S.off[mid] <= m) lo = mid; else hi = mid - 1;
+      }
+      const int i = m - S.off[lo];
+      // query window: ranks s - n .. s - 1; key window: s + 1 .. s + n (in range by construction; clamped so that
+      // inconsistent inputs cannot read out of bounds)
+      int64_t j = query_window ? (int64_t)S.wrank[lo] - S.wlen[lo] + i : (int64_t)S.wrank[lo] + 1 + i;
+      j = j < 0 ? 0 : (j >= a.L ? a.L - 1 : j);
+      S.key[m] = (a.order[(b * a.T + lo) * a.L + j] << 5) | lo;
     }
-    S.off[lane] = lo;
   }
   wave_lds_sync();
-  return base;
+  return M;
 }
 
 // Generation: the candidates of position t are the ring contents of its bucket in every table, oldest first. The
@@ -254,40 +266,60 @@ __device__ __forceinline__ int gather_rings(const Cand& a, int64_t b, int64_t t,
 }
 
 // One slot per distinct position, in order of first appearance (table-major): S.uid[entry], S.upos[unique].
-// Deterministic: an entry is the first of its position when no earlier table's segment holds it.
+// Every entry claims its position's slot in an LDS hash table (compare-and-swap, linear probing) and keeps the
+// smallest entry index there (atomic min, order-independent), so the numbering is deterministic.
+__device__ __forceinline__ uint32_t pos_hash(int pos) { return ((uint32_t)pos * 2654435761u) >> 23; }   // 9 bits
+
 __device__ __forceinline__ int dedupe(const Cand& a, int M, Scratch& S) {
+  static_assert(kHash == 512, "pos_hash yields 9 bits");
   const int lane = lane_id();
-  int nu = 0;
-  for (int m0 = 0; m0 < M; m0 += kWave) {
-    const int m = m0 + lane;
-    const bool in = m < M;
-    int first = -1, pos = 0;
-    if (in) {
-      const int e = S.key[m];
-      pos = e >> 5;
-      const int tau = e & 31;
-      for (int tp = 0; tp < tau && first < 0; ++tp) {
-        int lo = S.off[tp], hi = S.off[tp + 1];
-        const int end = hi;
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if ((S.key[mid] >> 5) < pos) lo = mid + 1; else hi = mid;
-        }
-        if (lo < end && (S.key[lo] >> 5) == pos) first = lo;
-      }
-    }
-    const bool prim = in && first < 0;
-    const uint64_t bal = __ballot(prim);
-    if (prim) {
-      const int u = nu + __popcll(bal & ((1ull << lane) - 1ull));
-      S.uid[m] = u;
-      S.upos[u] = pos;
-    }
-    nu += __popcll(bal);
-    wave_lds_sync();
-    if (in && first >= 0) S.uid[m] = S.uid[first];
-    wave_lds_sync();
+  for (int i = lane; i < kHash; i += kWave) {
+    S.hpos[i] = -1;
+    S.hfirst[i] = 0x7fffffff;
   }
+  wave_lds_sync();
+  int slot[kCh];
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    slot[c] = 0;
+    const int m = c * kWave + lane;
+    if (c * kWave < M && m < M) {
+      const int pos = S.key[m] >> 5;
+      uint32_t h = pos_hash(pos);
+      for (int probe = 0; probe < kHash; ++probe) {
+        const int old = atomicCAS(&S.hpos[h], -1, pos);
+        if (old == -1 || old == pos) break;
+        h = (h + 1) & (kHash - 1);
+      }
+      atomicMin(&S.hfirst[h], m);
+      slot[c] = (int)h;
+    }
+  }
+  wave_lds_sync();
+  int nu = 0;
+  bool prim[kCh];
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const int m = c * kWave + lane;
+    prim[c] = false;
+    if (c * kWave < M) {
+      prim[c] = m < M && S.hfirst[slot[c]] == m;
+      const uint64_t bal = __ballot(prim[c]);
+      if (prim[c]) {
+        const int u = nu + __popcll(bal & ((1ull << lane) - 1ull));
+        S.uid[m] = u;
+        S.upos[u] = S.key[m] >> 5;
+      }
+      nu += __popcll(bal);
+    }
+  }
+  wave_lds_sync();
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const int m = c * kWave + lane;
+    if (m < M && !prim[c]) S.uid[m] = S.uid[S.hfirst[slot[c]]];
+  }
+  wave_lds_sync();
   return nu;
 }
 
@@ -445,11 +477,12 @@ __device__ __forceinline__ void segment(int offv, int tau, int* lo, int* hi) {
 // ---------------------------------------------------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------------------------------------------------
-// One query token's candidate attention: salida row (d), the 4 gate signals and, when `stats` is given, the per-table
-// (max, denominator). RING: candidates from the generation rings instead of the sorted windows.
+// One query token's candidate attention: salida row (d), the 4 gate signals and, when `att_rows` is given, every
+// entry's weight at att_rows[tau * C + distance - 1]. RING: candidates from the generation rings instead of the
+// sorted windows.
 template <int F4, int DCH, bool RING>
 __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t t, Scratch& S, float* salida_row,
-                                              float* signals_row, float* stats_rows) {
+                                              float* signals_row, float* att_rows) {
   const int lane = lane_id();
   const int64_t tok = b * a.L + t;
   const int M = RING ? gather_rings(a, b, t, S) : gather(a, b, t, true, S);
@@ -477,22 +510,15 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
   for (int tau = 0; tau < a.T; ++tau) {
     int lo, hi;
     segment(offv, tau, &lo, &hi);
-    float* st = stats_rows ? stats_rows + tau * 2 : nullptr;
-    if (lo == hi) {
-      if (lane == 0 && st) {
-        st[0] = 0.f;
-        st[1] = 1.f;
-      }
-      continue;
-    }
+    if (lo == hi) continue;
     const TableStats ts = table_softmax(E, tau, lo, hi);
 #pragma unroll
     for (int c = 0; c < kCh; ++c)
-      if (E.tau[c] == tau) S.uc[E.u[c]] += expf(E.sc[c] - ts.mx) / ts.den;   // uniques are distinct in a table
-    if (lane == 0 && st) {
-      st[0] = ts.mx;
-      st[1] = ts.den;
-    }
+      if (E.tau[c] == tau) {
+        const float w = expf(E.sc[c] - ts.mx) / ts.den;
+        S.uc[E.u[c]] += w;                                   // uniques are distinct in a table
+        if (att_rows) att_rows[tau * a.C + (hi - 1 - (c * kWave + lane))] = w;   // entries ascend: distance hi - m
+      }
     pt += 1.f;
     best = fmaxf(best, ts.mx);
     pico += 1.f / ts.den;            // the largest weight: exp(mx - mx) / den
@@ -545,7 +571,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_fwd(Cand a) {
   const int64_t tok = token_of_wave();
   if (tok >= a.B * a.L) return;
   forward_token<F4, DCH, false>(a, tok / a.L, tok % a.L, S, a.salida + tok * a.d, a.signals + tok * 4,
-                                a.stats + tok * a.T * 2);
+                                a.att + tok * a.T * a.C);
 }
 
 // Generation step: one wave per batch row; the query is position a.tq of the caches (a.L = their capacity). With
@@ -569,7 +595,8 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_decode_attend(Cand a
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
-// backward, query pass
+// backward, query pass: needs no scores. att comes from the forward; per distinct key, dp = <dO_q, V_k>, the clock
+// difference and the suffix length; per table D = sum att dp, then ds = att (dp - D) per entry, kept for the key pass.
 // ---------------------------------------------------------------------------------------------------------------------
 template <int F4, int DCH>
 __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
@@ -582,24 +609,17 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
 
   const int M = gather(a, b, t, true, S);
   const int NU = dedupe(a, M, S);
-  float4 qf[F4];
-  feats<F4>(a, a.Qc, tok, true, qf);
-  unique_bases<F4>(a, b, t, NU, false, qf, S);
   const float* sigb = a.sig + b * a.L;
   float mine[16];
   own_suffix(sigb, t, a.K, mine);
   const double bq = a.Bt[tok];
   for (int u = lane; u < NU; u += kWave) {
     const int64_t k = S.upos[u];
-    const int ell = suffix_vs(sigb, mine, t, k, a.K);
-    S.ua[u] = (S.ua[u] + a.w_suf[ell]) + a.la[b * a.L + k];
+    S.uell[u] = suffix_vs(sigb, mine, t, k, a.K);
     S.ub[u] = (float)(a.Bt[b * a.L + k] - bq);
     S.ud[u] = 0.f;
-    S.uell[u] = ell;
   }
-  wave_lds_sync();
-
-  // dp_u = <dO_q, V_u>
+  // dp_u = <dO_q, V_u> (ends with a wave sync)
   float4 dO[DCH], unused[DCH];
 #pragma unroll
   for (int ch = 0; ch < DCH; ++ch) {
@@ -609,56 +629,65 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   }
   unique_row_dots<DCH>(a, a.V + b * a.L * a.d, t, NU, dO, nullptr, unused, S, S.uc);
 
-  Entries E;
-  load_entries(a, M, S, E);
-  const int offv = lane <= a.T ? S.off[lane] : 0;
-  float* part = a.partials + tok * (a.T + a.K + 1);
-  float dbq = 0.f;
+  // per entry: att from the forward and att * dp (S.ua is a per-entry buffer here)
+  const float* arow = a.att_in + tok * a.T * a.C;
+  float* dsrow = a.ds + tok * a.T * a.C;
+  float att[kCh], dp[kCh];
+  int tau[kCh], un[kCh], slot[kCh];
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const int m = c * kWave + lane;
+    const bool in = m < M;
+    const int e = in ? S.key[m] : 0;
+    tau[c] = in ? (e & 31) : -1;
+    un[c] = in ? S.uid[m] : 0;
+    slot[c] = in ? (e & 31) * a.C + (S.off[(e & 31) + 1] - 1 - m) : 0;
+    att[c] = in ? arow[slot[c]] : 0.f;
+    dp[c] = in ? S.uc[un[c]] : 0.f;
+    if (in) S.ua[m] = att[c] * dp[c];
+  }
+  wave_lds_sync();
+  if (lane < a.T) {                                     // D per table, summed in entry order
+    float D = 0.f;
+    for (int m = S.off[lane]; m < S.off[lane + 1]; ++m) D += S.ua[m];
+    S.tsum[lane] = D;
+  }
+  wave_lds_sync();
+  float ds[kCh];
   float dw[17];
 #pragma unroll
-  for (int c = 0; c < 17; ++c) dw[c] = 0.f;
-  for (int tau = 0; tau < a.T; ++tau) {
-    int lo, hi;
-    segment(offv, tau, &lo, &hi);
-    if (lo == hi) {
-      if (lane == 0) {
-        a.qstats[tok * a.T + tau] = 0.f;
-        part[tau] = 0.f;
-      }
-      continue;
-    }
-    const TableStats ts = table_softmax(E, tau, lo, hi);
-    const int c0 = lo / kWave, c1 = (hi - 1) / kWave;
-    float att[kCh], dp[kCh];
-    float D = 0.f;
+  for (int x = 0; x < 17; ++x) dw[x] = 0.f;
 #pragma unroll
-    for (int c = 0; c < kCh; ++c) {
-      const bool in = E.tau[c] == tau;
-      att[c] = in ? expf(E.sc[c] - ts.mx) / ts.den : 0.f;
-      dp[c] = in ? S.uc[E.u[c]] : 0.f;
-      if (c >= c0 && c <= c1) D += wave_sum_u(att[c] * dp[c]);
+  for (int c = 0; c < kCh; ++c) {
+    const int m = c * kWave + lane;
+    const bool in = tau[c] >= 0;
+    ds[c] = in ? att[c] * (dp[c] - S.tsum[tau[c]]) : 0.f;
+    if (in) {
+      dsrow[slot[c]] = ds[c];
+      S.ua[m] = ds[c];
     }
+    const int ell = in ? S.uell[un[c]] : -1;
+#pragma unroll
+    for (int x = 0; x < 17; ++x)
+      if (ell == x) dw[x] += ds[c];
+  }
+  wave_lds_sync();
+  float* part = a.partials + tok * (a.T + a.K + 1);
+  float dbq_t = 0.f;
+  if (lane < a.T) {                                     // per table: sum ds (clock) and sum ds * dt (d gamma)
     float sds = 0.f, sdt = 0.f;
-#pragma unroll
-    for (int c = 0; c < kCh; ++c) {
-      const bool in = E.tau[c] == tau;
-      const float ds = in ? att[c] * (dp[c] - D) : 0.f;
-      const float dt = in ? S.ub[E.u[c]] : 0.f;
-      const int ell = in ? S.uell[E.u[c]] : -1;
-      if (in) S.ud[E.u[c]] += ds;
-      if (c >= c0 && c <= c1) {
-        sds += wave_sum_u(ds);
-        sdt += wave_sum_u(ds * dt);
-      }
-#pragma unroll
-      for (int x = 0; x < 17; ++x)
-        if (ell == x) dw[x] += ds;
+    for (int m = S.off[lane]; m < S.off[lane + 1]; ++m) {
+      sds += S.ua[m];
+      sdt += S.ua[m] * S.ub[S.uid[m]];
     }
-    dbq += -rate_of(a, tau) * sds;
-    if (lane == 0) {
-      a.qstats[tok * a.T + tau] = D;
-      part[tau] = sdt;
-    }
+    part[lane] = sdt;
+    dbq_t = -rate_of(a, lane) * sds;
+  }
+  // per unique: sum over tables of ds, in table order
+  for (int tt = 0; tt < a.T; ++tt) {
+#pragma unroll
+    for (int c = 0; c < kCh; ++c)
+      if (tau[c] == tt) S.ud[un[c]] += ds[c];
     wave_lds_sync();
   }
 
@@ -682,11 +711,43 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
     const float v = wave_sum_u(dw[x]);
     if (lane == 0) part[a.T + x] = v;
   }
+  float dbq = 0.f;
+  for (int tt = 0; tt < a.T; ++tt) dbq += readlane_f(dbq_t, tt);
   if (lane == 0) a.dBt[tok] = (double)dbq;
 }
 
+// sum_u w_u row_u over the uniques' d-wide rows (rows of batch row b), UNR rows in flight
+template <int DCH>
+__device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows, int64_t self_pos, int NU,
+                                               const float* w_u, const Scratch& S, float4 (&acc)[DCH]) {
+  const int lane = lane_id();
+  constexpr int UNR = DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 16);
+#pragma unroll
+  for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
+  for (int u0 = 0; u0 < NU; u0 += UNR) {
+    float4 v[UNR][DCH];
+    float w[UNR];
+#pragma unroll
+    for (int r = 0; r < UNR; ++r) {
+      const bool ok = u0 + r < NU;
+      const int64_t p = ok ? S.upos[u0 + r] : self_pos;
+      w[r] = ok ? w_u[u0 + r] : 0.f;
+#pragma unroll
+      for (int ch = 0; ch < DCH; ++ch) {
+        const int dd = ch * 256 + lane * 4;
+        v[r][ch] = dd < a.d ? ld4(rows + p * a.d + dd) : zero4();
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < UNR; ++r)
+#pragma unroll
+      for (int ch = 0; ch < DCH; ++ch) fma4(acc[ch], w[r], v[r][ch]);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------------------------
-// backward, key pass
+// backward, key pass: no scores either. Every entry's att (forward) and ds (query pass) are read at the query's
+// slot for this key; per distinct query the table sums weight dO (-> dV) and [phi_q ; Qc_q] (-> d phi_k, d Kc_k).
 // ---------------------------------------------------------------------------------------------------------------------
 template <int F4, int DCH>
 __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_k(Cand a) {
@@ -699,77 +760,44 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_k(Cand a) {
 
   const int M = gather(a, b, k, false, S);
   const int NU = dedupe(a, M, S);
-  float4 kf[F4];
-  feats<F4>(a, a.Kc, tok, false, kf);
-  unique_bases<F4>(a, b, k, NU, true, kf, S);
-  const float* sigb = a.sig + b * a.L;
-  float mine[16];
-  own_suffix(sigb, k, a.K, mine);
-  const double bk = a.Bt[tok];
-  const float lak = a.la[tok];
   for (int u = lane; u < NU; u += kWave) {
-    const int64_t q = S.upos[u];
-    const int ell = suffix_vs(sigb, mine, k, q, a.K);
-    S.ua[u] = (S.ua[u] + a.w_suf[ell]) + lak;
-    S.ub[u] = (float)(bk - a.Bt[b * a.L + q]);
     S.uc[u] = 0.f;
     S.ud[u] = 0.f;
   }
-  wave_lds_sync();
-
-  // att of every (query, table) from the forward's statistics; D of the query; sum over tables per query for dV
-  Entries E;
-  load_entries(a, M, S, E);
-  float att[kCh], Dq[kCh];
+  float att[kCh], ds[kCh];
+  int tau[kCh], un[kCh];
+  float dla = 0.f, dbk = 0.f;
 #pragma unroll
   for (int c = 0; c < kCh; ++c) {
+    const int m = c * kWave + lane;
+    const bool in = m < M;
+    const int e = in ? S.key[m] : 0;
+    tau[c] = in ? (e & 31) : -1;
+    un[c] = in ? S.uid[m] : 0;
     att[c] = 0.f;
-    Dq[c] = 0.f;
-    if (E.tau[c] >= 0) {
-      const int64_t o = (b * a.L + S.upos[E.u[c]]) * a.T + E.tau[c];
-      att[c] = expf(E.sc[c] - a.stats_in[o * 2]) / a.stats_in[o * 2 + 1];
-      Dq[c] = a.qstats[o];
+    ds[c] = 0.f;
+    if (in) {   // the key sits at distance m - lo + 1 before query (e >> 5) in table tau
+      const int64_t o = ((b * a.L + (e >> 5)) * a.T + (e & 31)) * a.C + (m - S.off[e & 31]);
+      att[c] = a.att_in[o];
+      ds[c] = a.ds[o];
+      dla += ds[c];
+      dbk += rate_of(a, e & 31) * ds[c];
     }
   }
-  const int offv = lane <= a.T ? S.off[lane] : 0;
-  for (int tau = 0; tau < a.T; ++tau) {
-    int lo, hi;
-    segment(offv, tau, &lo, &hi);
-    if (lo == hi) continue;
+  wave_lds_sync();
+  for (int tt = 0; tt < a.T; ++tt) {
 #pragma unroll
     for (int c = 0; c < kCh; ++c)
-      if (E.tau[c] == tau) S.uc[E.u[c]] += att[c];
-    wave_lds_sync();
-  }
-
-  // dp_u = <dO_q, V_k> and dV_k += (sum_tau att) dO_q from the same loads; dp overwrites ub
-  float4 vk[DCH], dv[DCH];
-#pragma unroll
-  for (int ch = 0; ch < DCH; ++ch) {
-    const int dd = ch * 256 + lane * 4;
-    vk[ch] = dd < a.d ? ld4(a.V + tok * a.d + dd) : zero4();
-    dv[ch] = zero4();
-  }
-  unique_row_dots<DCH>(a, a.dsal + b * a.L * a.d, k, NU, vk, S.uc, dv, S, S.ub);
-
-  float dla = 0.f, dbk = 0.f;
-  for (int tau = 0; tau < a.T; ++tau) {
-    int lo, hi;
-    segment(offv, tau, &lo, &hi);
-    if (lo == hi) continue;
-    const float rate = rate_of(a, tau);
-#pragma unroll
-    for (int c = 0; c < kCh; ++c) {
-      if (E.tau[c] == tau) {
-        const float ds = att[c] * (S.ub[E.u[c]] - Dq[c]);
-        S.ud[E.u[c]] += ds;
-        dla += ds;
-        dbk += rate * ds;
+      if (tau[c] == tt) {
+        S.uc[un[c]] += att[c];
+        S.ud[un[c]] += ds[c];
       }
-    }
     wave_lds_sync();
   }
 
+  // dV_k = sum_u (sum_tau att) dO_u
+  float4 dv[DCH];
+  unique_row_sum<DCH>(a, a.dsal + b * a.L * a.d, k, NU, S.uc, S, dv);
   // d phi_k, d Kc_k = sum_u (sum_tau ds) [phi_q * scale_phi ; Qc_q * scale_c]
   float4 gk[F4];
   unique_feature_sum<F4>(a, b, k, NU, true, S.ud, S, gk);
@@ -909,12 +937,12 @@ extern "C" int asrn_candidates_fwd(const float* phi, const float* V, const float
                                    const float* gamma, const int32_t* order, const int32_t* win, const int32_t* rank,
                                    int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
                                    int32_t Tc, int32_t C, float scale_phi, float scale_c, float* salida,
-                                   float* signals, float* stats, void* stream) {
+                                   float* signals, float* att, void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
                 scale_phi, scale_c);
   if (check_args(a, "asrn_candidates_fwd")) return 1;
   if (B == 0 || L == 0) return 0;
-  a.salida = salida; a.signals = signals; a.stats = stats;
+  a.salida = salida; a.signals = signals; a.att = att;
   return dispatch<LaunchFwd>(a, (hipStream_t)stream);
 }
 
@@ -923,14 +951,14 @@ extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float
                                    const float* gamma, const int32_t* order, const int32_t* win, const int32_t* rank,
                                    int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
                                    int32_t Tc, int32_t C, float scale_phi, float scale_c, const float* dsalida,
-                                   const float* stats, float* dphi, float* dV, float* dQc, float* dKc, double* dBt,
-                                   float* dlog_alfa, float* qstats, float* partials, void* stream) {
+                                   const float* att, float* dphi, float* dV, float* dQc, float* dKc, double* dBt,
+                                   float* dlog_alfa, float* ds, float* partials, void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
                 scale_phi, scale_c);
   if (check_args(a, "asrn_candidates_bwd")) return 1;
   if (B == 0 || L == 0) return 0;
-  a.dsal = dsalida; a.stats_in = stats; a.dphi = dphi; a.dV = dV; a.dQc = dQc; a.dKc = dKc; a.dBt = dBt;
-  a.dla = dlog_alfa; a.qstats = qstats; a.partials = partials;
+  a.dsal = dsalida; a.att_in = att; a.dphi = dphi; a.dV = dV; a.dQc = dQc; a.dKc = dKc; a.dBt = dBt;
+  a.dla = dlog_alfa; a.ds = ds; a.partials = partials;
   return dispatch<LaunchBwd>(a, (hipStream_t)stream);
 }
 

@@ -210,7 +210,7 @@ class Streak(torch.autograd.Function):
 class Candidates(torch.autograd.Function):
     """Candidate attention of all tables (the drop-in for _CasillerosTriton, asrn/nucleo.py:461-515). Returns salida
     (B, L, d) and the gate signals (B, L, 4) = (peso_total, mejor, pico, peso_ctx), the latter without gradient.
-    Saves only its inputs and the per-(query, table) softmax statistics."""
+    Saves its inputs and the candidates' attention weights (B, L, T, C), so the backward recomputes no score."""
 
     @staticmethod
     def forward(ctx, phi, V, Qc, Kc, Bt, log_alfa, w_suf, gamma, sig, order, win, rank, shape):
@@ -224,19 +224,19 @@ class Candidates(torch.autograd.Function):
                    g=_c(gamma.detach(), torch.float32))
         salida = torch.empty((B, L, d), dtype=torch.float32, device=dev)
         signals = torch.empty((B, L, 4), dtype=torch.float32, device=dev)
-        stats = torch.empty((B, L, T, 2), dtype=torch.float32, device=dev)
+        att = torch.empty((B, L, T, C), dtype=torch.float32, device=dev)     # only the valid slots are written
         sp, sc = float(P) ** -0.5, float(cf) ** -0.5
         call('asrn_candidates_fwd', ptr(ins['phi']), ptr(ins['V']), ptr(ins['Qc']), ptr(ins['Kc']), ptr(ins['sig']),
              ptr(ins['Bt']), ptr(ins['la']), ptr(ins['w']), ptr(ins['g']), ptr(order), ptr(win), ptr(rank), B, L, d,
-             P, cf, K, T, Tc, C, sp, sc, ptr(salida), ptr(signals), ptr(stats), stream_of(dev))
-        ctx.save_for_backward(*ins.values(), order, win, rank, stats)
+             P, cf, K, T, Tc, C, sp, sc, ptr(salida), ptr(signals), ptr(att), stream_of(dev))
+        ctx.save_for_backward(*ins.values(), order, win, rank, att)
         ctx.meta = (B, L, P, d, cf, K, T, Tc, C, sp, sc, V.dtype, phi.dtype, Qc.dtype, Kc.dtype, log_alfa.dtype)
         ctx.mark_non_differentiable(signals)
         return salida.to(V.dtype), signals
 
     @staticmethod
     def backward(ctx, dsal, _dsig):
-        phi, V, Qc, Kc, sig, Bt, la, w, g, order, win, rank, stats = ctx.saved_tensors
+        phi, V, Qc, Kc, sig, Bt, la, w, g, order, win, rank, att = ctx.saved_tensors
         B, L, P, d, cf, K, T, Tc, C, sp, sc, tv, tp, tq, tk, tl = ctx.meta
         dev = phi.device
         dsal = _c(dsal, torch.float32)
@@ -246,11 +246,11 @@ class Candidates(torch.autograd.Function):
         dKc = torch.empty_like(Kc)
         dBt = torch.empty_like(Bt)
         dla = torch.empty_like(la)
-        qstats = torch.empty((B, L, T), dtype=torch.float32, device=dev)
+        ds = torch.empty((B, L, T, C), dtype=torch.float32, device=dev)
         partials = torch.empty((B * L, T + K + 1), dtype=torch.float32, device=dev)
         call('asrn_candidates_bwd', ptr(phi), ptr(V), ptr(Qc), ptr(Kc), ptr(sig), ptr(Bt), ptr(la), ptr(w), ptr(g),
-             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ptr(dsal), ptr(stats),
-             ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(qstats), ptr(partials), stream_of(dev))
+             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ptr(dsal), ptr(att),
+             ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(ds), ptr(partials), stream_of(dev))
         part = partials.sum(0)
         dgamma = part[:T] / C
         dw = part[T:]

@@ -51,7 +51,8 @@ int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t T, int32_t 
  *   sig (B, L) fp32 token signatures; Bt (B, L) fp64 clock; log_alfa (B, L); w_suf (K+1); gamma (T)
  *   salida  (B, L, d) out: sum over tables of sum_k att * V_k
  *   signals (B, L, 4) out: peso_total, mejor, pico, peso_ctx
- *   stats   (B, L, T, 2) out: per (query, table) the valid max score and the softmax denominator (for the backward)
+ *   att     (B, L, T, C) out: the weight of each candidate, at [query][tau][distance - 1] (distance in sorted
+ *           ranks, 1..n); slots beyond the table's n candidates are not written. Kept for the backward.
  * Requires d % 4 == 0, d <= 1024, 1 <= C <= 64, P + cf <= 256, K <= 16, T <= 32. */
 int asrn_candidates_fwd(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                         const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
@@ -70,12 +71,13 @@ int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* 
 
 /* ---- a8: candidate attention, backward -------------------------------------------------------------------------
  * Replaces _CasillerosTriton.backward / _casilleros_vuelta (asrn/nucleo.py:384-451, 490-515). Two passes with one
- * owner per output row, so no atomics and no per-slot buffers: a query pass (query-side gradients, the softmax
- * correction D = sum att*dp per (query, table), and per-query partials of d gamma and d w_suf) and a key pass
- * (key-side gradients; the queries that see key k in table tau are the next <= C same-bucket sorted ranks).
- *   dsalida (B, L, d); stats from the forward
+ * owner per output row, so no atomics, and neither recomputes a score: a query pass (from the forward's att:
+ * ds = att (dp - D) with D = sum att*dp per (query, table), query-side gradients, per-query partials of d gamma and
+ * d w_suf) and a key pass (key-side gradients from att and ds at the slots of the queries that see the key: the
+ * next <= C same-bucket sorted ranks).
+ *   dsalida (B, L, d); att from asrn_candidates_fwd
  *   dphi (B, L, P), dV (B, L, d), dQc, dKc (B, L, cf), dBt (B, L) fp64, dlog_alfa (B, L) out (overwritten)
- *   qstats   (B, L, T) fp32 workspace
+ *   ds       (B, L, T, C) fp32 workspace (laid out like att)
  *   partials (B*L, T + K + 1) fp32 out: per query, d gamma_tau then d w_suf[0..K]; the caller sums over rows. */
 int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                         const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
