@@ -33,7 +33,6 @@ struct Cand {
   const int32_t* order; const int32_t* win; const int32_t* rank;
   int64_t B, L;
   int d, P, cf, K, T, Tc, C;
-  int vec;            // P and cf multiples of 4: feature rows load as float4
   float sp, sc;
   // forward outputs; att (B*L, T, C): the weight of the key at distance j + 1 before the query, at slot j
   float* salida; float* signals; float* att;
@@ -67,8 +66,18 @@ struct Scratch {
   int uell[kMaxSlots];     // unique: suffix-match length (query side)
   int off[40];             // entries of table tau: [off[tau], off[tau + 1])
   int wrank[32], wlen[32]; // per table: the token's sorted rank and window length
-  float tsum[32];          // per-table sums (backward)
+  float tsum[32];          // per-table sums (backward); per-table max keys (forward)
+  float tinv[32];          // per-table 1 / softmax denominator (forward)
 };
+
+// order-preserving map of finite floats and -inf to unsigned keys, and back
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float from_order_key(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
 
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup i runs on XCD i % 8), each with its own L2. Give
 // each XCD a contiguous range of tokens instead, so one XCD's L2 serves one stretch of a batch row (at B = 8, one
@@ -103,35 +112,38 @@ __device__ __forceinline__ void fma4(float4& acc, float w, const float4& v) {
 }
 __device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
 
-// Features 128 c + 4 (lane & 31) .. + 3 of a row: phi for x < P, then the confirmation vector (Qc for queries, Kc
-// for keys); queries pre-scaled by scale_phi / scale_c. One float4 load per chunk when P and cf are multiples of 4.
+// The feature row a lane reads: float4 chunk c covers features x = 128 c + 4 (lane & 31) .. + 3 of [phi ; conf] (conf
+// = Qc for queries, Kc for keys), pre-scaled by scale_phi / scale_c for queries. P and cf are multiples of 4, so a
+// chunk never straddles the two. The per-lane base, stride and scale are fixed for a kernel: a row costs one 32-bit
+// multiply and one float4 load (offsets fit 31 bits; lanes past P + cf read column 0 and are zeroed by their scale).
 template <int F4>
-__device__ __forceinline__ void feats(const Cand& a, const float* conf, int64_t row, bool scaled, float4 (&f)[F4]) {
+struct FeatLanes {
+  const float* base[F4];
+  uint32_t stride[F4];
+  float scale[F4];
+};
+
+template <int F4>
+__device__ __forceinline__ FeatLanes<F4> feat_lanes(const Cand& a, const float* conf, bool scaled) {
+  FeatLanes<F4> fl;
   const int x0 = 4 * (lane_id() & 31);
-  const int F = a.P + a.cf;
 #pragma unroll
   for (int c = 0; c < F4; ++c) {
     const int x = x0 + 128 * c;
-    float4 v = zero4();
-    if (a.vec) {
-      const float* p = x < a.P ? a.phi + row * a.P + x : conf + row * a.cf + (x - a.P);
-      if (x < F) v = ld4(p);
-      if (scaled) {
-        const float s = x < a.P ? a.sp : a.sc;
-        v.x *= s; v.y *= s; v.z *= s; v.w *= s;
-      }
-    } else {
-      float e[4];
+    const bool in_phi = x < a.P, live = x < a.P + a.cf;
+    fl.base[c] = in_phi ? a.phi + x : (live ? conf + (x - a.P) : a.phi);
+    fl.stride[c] = in_phi || !live ? (uint32_t)a.P : (uint32_t)a.cf;
+    fl.scale[c] = !live ? 0.f : (scaled ? (in_phi ? a.sp : a.sc) : 1.f);
+  }
+  return fl;
+}
+
+template <int F4>
+__device__ __forceinline__ void feat_row(const FeatLanes<F4>& fl, uint32_t row, float4 (&f)[F4]) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int xi = x + i;
-        float w = 0.f;
-        if (xi < a.P) w = scaled ? a.phi[row * a.P + xi] * a.sp : a.phi[row * a.P + xi];
-        else if (xi < F) w = scaled ? conf[row * a.cf + (xi - a.P)] * a.sc : conf[row * a.cf + (xi - a.P)];
-        e[i] = w;
-      }
-      v = make_float4(e[0], e[1], e[2], e[3]);
-    }
+  for (int c = 0; c < F4; ++c) {
+    float4 v = ld4(fl.base[c] + row * fl.stride[c]);
+    v.x *= fl.scale[c]; v.y *= fl.scale[c]; v.z *= fl.scale[c]; v.w *= fl.scale[c];
     f[c] = v;
   }
 }
@@ -332,13 +344,14 @@ template <int F4>
 __device__ __forceinline__ void unique_bases(const Cand& a, int64_t b, int64_t self_pos, int NU,
                                              bool rows_are_queries, const float4 (&fixed)[F4], Scratch& S) {
   const int lane = lane_id(), half = lane >> 5;
-  const float* conf = rows_are_queries ? a.Qc : a.Kc;
+  const FeatLanes<F4> fl = feat_lanes<F4>(a, rows_are_queries ? a.Qc : a.Kc, rows_are_queries);
+  const uint32_t row0 = (uint32_t)(b * a.L);
   for (int u0 = 0; u0 < NU; u0 += 2 * kRows) {
     float4 f[kRows][F4];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
       const int u = u0 + 2 * r + half;
-      feats<F4>(a, conf, b * a.L + (u < NU ? S.upos[u] : self_pos), rows_are_queries, f[r]);
+      feat_row<F4>(fl, row0 + (uint32_t)(u < NU ? S.upos[u] : self_pos), f[r]);
     }
     float p[kRows];
 #pragma unroll
@@ -363,7 +376,8 @@ __device__ __forceinline__ void unique_feature_sum(const Cand& a, int64_t b, int
                                                    bool rows_are_queries, const float* wts, Scratch& S,
                                                    float4 (&g)[F4]) {
   const int half = lane_id() >> 5;
-  const float* conf = rows_are_queries ? a.Qc : a.Kc;
+  const FeatLanes<F4> fl = feat_lanes<F4>(a, rows_are_queries ? a.Qc : a.Kc, rows_are_queries);
+  const uint32_t row0 = (uint32_t)(b * a.L);
 #pragma unroll
   for (int c = 0; c < F4; ++c) g[c] = zero4();
   for (int u0 = 0; u0 < NU; u0 += 2 * kRows) {
@@ -373,7 +387,7 @@ __device__ __forceinline__ void unique_feature_sum(const Cand& a, int64_t b, int
     for (int r = 0; r < kRows; ++r) {
       const int u = u0 + 2 * r + half;
       const bool ok = u < NU;
-      feats<F4>(a, conf, b * a.L + (ok ? S.upos[u] : self_pos), rows_are_queries, f[r]);
+      feat_row<F4>(fl, row0 + (uint32_t)(ok ? S.upos[u] : self_pos), f[r]);
       w[r] = ok ? wts[u] : 0.f;
     }
 #pragma unroll
@@ -449,31 +463,6 @@ __device__ __forceinline__ void load_entries(const Cand& a, int M, const Scratch
   }
 }
 
-// Exact masked softmax of every table over its entries: mx/den per entry's table and att per entry. The per-table
-// max and sum are DPP wave reductions restricted to the chunks the table's segment spans.
-struct TableStats {
-  float mx, den;
-};
-
-__device__ __forceinline__ TableStats table_softmax(const Entries& E, int tau, int lo, int hi) {
-  const int c0 = lo / kWave, c1 = (hi - 1) / kWave;
-  float mx = -INFINITY;
-#pragma unroll
-  for (int c = 0; c < kCh; ++c)
-    if (c >= c0 && c <= c1) mx = fmaxf(mx, wave_max_u(E.tau[c] == tau ? E.sc[c] : -INFINITY));
-  float den = 0.f;
-#pragma unroll
-  for (int c = 0; c < kCh; ++c)
-    if (c >= c0 && c <= c1) den += wave_sum_u(E.tau[c] == tau ? expf(E.sc[c] - mx) : 0.f);
-  return {mx, den};
-}
-
-// the two table segments' bounds for table tau, read from the lane-held copy of S.off
-__device__ __forceinline__ void segment(int offv, int tau, int* lo, int* hi) {
-  *lo = readlane_i(offv, tau);
-  *hi = readlane_i(offv, tau + 1);
-}
-
 // ---------------------------------------------------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------------------------------------------------
@@ -488,7 +477,7 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
   const int M = RING ? gather_rings(a, b, t, S) : gather(a, b, t, true, S);
   const int NU = dedupe(a, M, S);
   float4 qf[F4];
-  feats<F4>(a, a.Qc, tok, true, qf);
+  feat_row<F4>(feat_lanes<F4>(a, a.Qc, true), (uint32_t)tok, qf);
   unique_bases<F4>(a, b, t, NU, false, qf, S);
   const float* sigb = a.sig + b * a.L;
   float mine[16];
@@ -503,28 +492,61 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
   }
   wave_lds_sync();
 
+  // Exact masked softmax of every table at once: the per-table max through an LDS atomic max on order-preserving
+  // integer keys (order-independent), one exp per entry, the per-table sum by one lane per table in entry order.
   Entries E;
   load_entries(a, M, S, E);
-  const int offv = lane <= a.T ? S.off[lane] : 0;
-  float pt = 0.f, best = -INFINITY, pico = 0.f, pctx = 0.f;
-  for (int tau = 0; tau < a.T; ++tau) {
-    int lo, hi;
-    segment(offv, tau, &lo, &hi);
-    if (lo == hi) continue;
-    const TableStats ts = table_softmax(E, tau, lo, hi);
+  uint32_t* tmax = reinterpret_cast<uint32_t*>(S.tsum);
+  if (lane < a.T) tmax[lane] = 0u;                       // below every key
+  wave_lds_sync();
+#pragma unroll
+  for (int c = 0; c < kCh; ++c)
+    if (c * kWave < M && E.tau[c] >= 0) atomicMax(&tmax[E.tau[c]], order_key(E.sc[c]));
+  wave_lds_sync();
+  float e[kCh];
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    e[c] = 0.f;
+    if (c * kWave < M && E.tau[c] >= 0) {
+      e[c] = __expf(E.sc[c] - from_order_key(tmax[E.tau[c]]));
+      S.ua[c * kWave + lane] = e[c];                     // per-entry now: the base scores are in E.sc
+    }
+  }
+  wave_lds_sync();
+  bool has = false;
+  float mx = -INFINITY, inv = 0.f;
+  if (lane < a.T) {
+    const int lo = S.off[lane], hi = S.off[lane + 1];
+    if (lo < hi) {
+      float den = 0.f;
+      for (int m = lo; m < hi; ++m) den += S.ua[m];
+      has = true;
+      mx = from_order_key(tmax[lane]);
+      inv = 1.f / den;
+    }
+    S.tinv[lane] = inv;
+  }
+  wave_lds_sync();
+  float w[kCh];
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    w[c] = 0.f;
+    const int m = c * kWave + lane;
+    if (c * kWave < M && E.tau[c] >= 0) {
+      w[c] = e[c] * S.tinv[E.tau[c]];
+      if (att_rows) att_rows[E.tau[c] * a.C + (S.off[E.tau[c] + 1] - 1 - m)] = w[c];   // entries ascend
+    }
+  }
+  for (int tt = 0; tt < a.T; ++tt) {                     // sum over tables per unique, in table order
 #pragma unroll
     for (int c = 0; c < kCh; ++c)
-      if (E.tau[c] == tau) {
-        const float w = expf(E.sc[c] - ts.mx) / ts.den;
-        S.uc[E.u[c]] += w;                                   // uniques are distinct in a table
-        if (att_rows) att_rows[tau * a.C + (hi - 1 - (c * kWave + lane))] = w;   // entries ascend: distance hi - m
-      }
-    pt += 1.f;
-    best = fmaxf(best, ts.mx);
-    pico += 1.f / ts.den;            // the largest weight: exp(mx - mx) / den
-    if (tau >= a.T - a.Tc) pctx += 1.f;
+      if (E.tau[c] == tt) S.uc[E.u[c]] += w[c];          // uniques are distinct within a table
     wave_lds_sync();
   }
+  const float pt = wave_sum_u(has ? 1.f : 0.f);
+  const float best = wave_max_u(mx);
+  const float pico = wave_sum_u(inv);                    // the largest weight of a table is exp(0) / den
+  const float pctx = wave_sum_u(has && lane >= a.T - a.Tc ? 1.f : 0.f);
 
   // copy-gather over the distinct candidates: sum_u (sum_tau att) V_u, UNR rows in flight
   constexpr int UNR = DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 16);
@@ -862,6 +884,13 @@ static int check_args(const Cand& a, const char* what) {
   ASRN_REQUIRE(a.T >= 1 && a.T <= 32 && a.T * a.C <= kMaxSlots && a.Tc >= 0 && a.Tc <= a.T,
                "%s: T=%d, C=%d, Tc=%d: needs T <= 32 and T*C <= %d", what, a.T, a.C, a.Tc, kMaxSlots);
   ASRN_REQUIRE(a.P >= 1 && a.cf >= 1 && a.P + a.cf <= 256, "%s: P + cf = %d must be <= 256", what, a.P + a.cf);
+  ASRN_REQUIRE(a.P % 4 == 0 && a.cf % 4 == 0, "%s: P=%d and cf=%d must be multiples of 4 (feature rows are read as "
+               "float4; pad the columns with zeros)", what, a.P, a.cf);
+  {
+    const int64_t widest = a.d > a.P ? (a.d > a.cf ? a.d : a.cf) : (a.P > a.cf ? a.P : a.cf);
+    ASRN_REQUIRE(a.B * a.L * widest < (int64_t(1) << 31), "%s: B*L*max(d, P) = %lld elements must stay below 2^31 "
+                 "(32-bit row offsets)", what, (long long)(a.B * a.L * widest));
+  }
   ASRN_REQUIRE(a.K >= 0 && a.K <= 16, "%s: suffix K=%d must be in [0, 16]", what, a.K);
   return 0;
 }
@@ -874,7 +903,6 @@ static Cand make(const float* phi, const float* V, const float* Qc, const float*
   a.phi = phi; a.V = V; a.Qc = Qc; a.Kc = Kc; a.sig = sig; a.Bt = Bt; a.la = la; a.w_suf = w_suf;
   a.gamma = gamma; a.order = order; a.win = win; a.rank = rank;
   a.B = B; a.L = L; a.d = d; a.P = P; a.cf = cf; a.K = K; a.T = T; a.Tc = Tc; a.C = C;
-  a.vec = (P % 4 == 0 && cf % 4 == 0) ? 1 : 0;
   a.sp = sp; a.sc = sc;
   return a;
 }

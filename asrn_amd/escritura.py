@@ -51,6 +51,9 @@ class EscritorCapa:
         B, L0 = piezas.shape
         if L0 < 1:
             raise ValueError('the prompt needs at least one token')
+        if (capa.n_tablas * capa.n_bits) % 4 or capa.confirmar % 4:
+            raise ValueError('the generation step reads its caches as float4 rows: n_tablas * n_bits and confirmar '
+                             'must be multiples of 4')
         partes = {}
         y = capa._adelante(E, h, piezas, partes)
         self.cap = max(L0 + 1, capacidad)

@@ -26,6 +26,13 @@ def _c(t, dtype=None):
     return t.contiguous()
 
 
+def _pad4(t):
+    """fp32, contiguous, last dimension zero-padded to a multiple of 4."""
+    t = _c(t, torch.float32)
+    extra = -t.shape[-1] % 4
+    return torch.nn.functional.pad(t, (0, extra)) if extra else t
+
+
 # ---------------------------------------------------------------------------------------------------------------------
 # a1 + a2
 # ---------------------------------------------------------------------------------------------------------------------
@@ -216,28 +223,31 @@ class Candidates(torch.autograd.Function):
     def forward(ctx, phi, V, Qc, Kc, Bt, log_alfa, w_suf, gamma, sig, order, win, rank, shape):
         T, Tc, C, K = shape['T'], shape['Tc'], shape['C'], shape['K']
         dev = _dev(phi, V)
-        B, L, P = phi.shape
-        d, cf = V.shape[-1], Qc.shape[-1]
-        ins = dict(phi=_c(phi, torch.float32), V=_c(V, torch.float32), Qc=_c(Qc, torch.float32),
-                   Kc=_c(Kc, torch.float32), sig=_c(sig, torch.float32), Bt=_c(Bt, torch.float64),
-                   la=_c(log_alfa, torch.float32), w=_c(w_suf.detach(), torch.float32),
+        B, L, P0 = phi.shape
+        d, cf0 = V.shape[-1], Qc.shape[-1]
+        sp, sc = float(P0) ** -0.5, float(cf0) ** -0.5
+        # the kernels read feature rows as float4: zero columns pad P and cf to multiples of 4 (dot products and the
+        # gradients of the real columns are unchanged)
+        ins = dict(phi=_pad4(phi), V=_c(V, torch.float32), Qc=_pad4(Qc), Kc=_pad4(Kc), sig=_c(sig, torch.float32),
+                   Bt=_c(Bt, torch.float64), la=_c(log_alfa, torch.float32), w=_c(w_suf.detach(), torch.float32),
                    g=_c(gamma.detach(), torch.float32))
+        P, cf = ins['phi'].shape[-1], ins['Qc'].shape[-1]
         salida = torch.empty((B, L, d), dtype=torch.float32, device=dev)
         signals = torch.empty((B, L, 4), dtype=torch.float32, device=dev)
         att = torch.empty((B, L, T, C), dtype=torch.float32, device=dev)     # only the valid slots are written
-        sp, sc = float(P) ** -0.5, float(cf) ** -0.5
         call('asrn_candidates_fwd', ptr(ins['phi']), ptr(ins['V']), ptr(ins['Qc']), ptr(ins['Kc']), ptr(ins['sig']),
              ptr(ins['Bt']), ptr(ins['la']), ptr(ins['w']), ptr(ins['g']), ptr(order), ptr(win), ptr(rank), B, L, d,
              P, cf, K, T, Tc, C, sp, sc, ptr(salida), ptr(signals), ptr(att), stream_of(dev))
         ctx.save_for_backward(*ins.values(), order, win, rank, att)
-        ctx.meta = (B, L, P, d, cf, K, T, Tc, C, sp, sc, V.dtype, phi.dtype, Qc.dtype, Kc.dtype, log_alfa.dtype)
+        ctx.meta = (B, L, P, d, cf, K, T, Tc, C, sp, sc, V.dtype, phi.dtype, Qc.dtype, Kc.dtype, log_alfa.dtype,
+                    P0, cf0)
         ctx.mark_non_differentiable(signals)
         return salida.to(V.dtype), signals
 
     @staticmethod
     def backward(ctx, dsal, _dsig):
         phi, V, Qc, Kc, sig, Bt, la, w, g, order, win, rank, att = ctx.saved_tensors
-        B, L, P, d, cf, K, T, Tc, C, sp, sc, tv, tp, tq, tk, tl = ctx.meta
+        B, L, P, d, cf, K, T, Tc, C, sp, sc, tv, tp, tq, tk, tl, P0, cf0 = ctx.meta
         dev = phi.device
         dsal = _c(dsal, torch.float32)
         dphi = torch.empty_like(phi)
@@ -254,8 +264,8 @@ class Candidates(torch.autograd.Function):
         part = partials.sum(0)
         dgamma = part[:T] / C
         dw = part[T:]
-        return (dphi.to(tp), dV.to(tv), dQc.to(tq), dKc.to(tk), dBt, dla.to(tl), dw, dgamma, None, None, None, None,
-                None)
+        return (dphi[..., :P0].to(tp), dV.to(tv), dQc[..., :cf0].to(tq), dKc[..., :cf0].to(tk), dBt, dla.to(tl), dw,
+                dgamma, None, None, None, None, None)
 
 
 # ---------------------------------------------------------------------------------------------------------------------

@@ -427,3 +427,36 @@ def test_layer_exact_mask_no_leak_with_huge_gamma():
         yb = layer(E2.to(DEV), h2.to(DEV), x2.to(DEV))[:, :cut]
     assert torch.isfinite(ya).all()
     assert (ya - yb).abs().max().item() <= 1e-6 * ya.abs().max().item()
+
+
+def test_layer_odd_feature_widths_vs_oracle():
+    """P = 15 and cf = 6 (not multiples of 4): the host pads the feature rows with zero columns for the float4 reads;
+    outputs and every gradient must still match the oracle."""
+    say('layer odd widths P=15 cf=6')
+    torch.manual_seed(2)
+    kw = dict(n_tablas=5, tablas_contexto=2, n_bits=3, confirmar=6, chunk=8)
+    layer = synth.move_params(CapaASRNEstable(32, **kw), 2)
+    p = {k: v.detach().clone() for k, v in layer.state_dict().items()}
+    sh = O.shape_from_params(p, 32, n_bits=3, C=8)
+    x, E, h = synth.layer_inputs(2, 300, 32, 7, seed=4)
+    gy = torch.randn(2, 300, 32, generator=torch.Generator().manual_seed(5))
+    layer = layer.to(DEV)
+    with torch.no_grad():
+        phi, _ = layer._phi_y_valores(E.to(DEV))
+    ids, _ = O.bucket_rows(phi.cpu(), sh.T, sh.nb)
+    ref_phi, _ = O.phi_and_values(p, E)
+    ref_ids, _ = O.bucket_rows(ref_phi, sh.T, sh.nb)
+    if not torch.equal(ids, ref_ids):
+        pytest.skip('a bucket id differs between the GPU GEMM and the CPU one (sign of phi near 0)')
+    y, grads = run_layer(layer, E, h, x, gy)
+    leaves = {k: (v.clone().requires_grad_() if v.is_floating_point() and k not in ('c_vistos', 'r_firma') else v)
+              for k, v in p.items()}
+    Ec, hc = E.clone().requires_grad_(), h.clone().requires_grad_()
+    yo = O.layer_forward(leaves, Ec, hc, x, sh)
+    (yo * gy).sum().backward()
+    assert_close(y, yo, 'y')
+    assert_close(grads['E'], Ec.grad, 'grad E')
+    assert_close(grads['h'], hc.grad, 'grad h')
+    for n, g in grads.items():
+        if n in leaves and leaves[n].grad is not None:
+            assert_close(g, leaves[n].grad, 'grad ' + n)

@@ -67,6 +67,9 @@ def test_argument_checks_fail_before_any_device_work(lib):
     # feature width above 256
     assert lib.asrn_candidates_bwd(*args, 64, 250, 16, 4, 8, 4, 32, 0.1, 0.25, *([N] * 11)) != 0
     assert 'P + cf' in _err(lib)
+    # feature widths are read as float4 (the host pads them)
+    assert lib.asrn_candidates_fwd(*args, 64, 110, 16, 4, 8, 4, 32, 0.1, 0.25, N, N, N, N) != 0
+    assert 'multiples of 4' in _err(lib)
     # workspace sizes are pure host arithmetic
     assert lib.asrn_ngram_sort_workspace(8, 4096, 4) >= 2 * 8 * 4 * 4096 * 12
     assert lib.asrn_ngram_sort(N, N, 8, 4096, 4, N, N, N, N, N, N, 16, N) != 0
