@@ -49,7 +49,7 @@ constexpr int kHash = 2 * kMaxSlots;   // dedupe hash slots: at most kMaxSlots d
 
 struct Scratch {
   int key[kMaxSlots];      // entry: (position << 5) | table
-  int uid[kMaxSlots];      // entry -> unique
+  uint16_t uid[kMaxSlots]; // entry -> unique
   int upos[kMaxSlots];     // unique: position
   union {
     struct {
@@ -63,7 +63,7 @@ struct Scratch {
       int hfirst[kHash];     // the first entry (table-major) with that position
     };
   };
-  int uell[kMaxSlots];     // unique: suffix-match length (query side)
+  uint8_t uell[kMaxSlots]; // unique: suffix-match length (query side)
   int off[40];             // entries of table tau: [off[tau], off[tau + 1])
   int wrank[32], wlen[32]; // per table: the token's sorted rank and window length
   float tsum[32];          // per-table sums (backward); per-table max keys (forward)
@@ -158,26 +158,37 @@ __device__ __forceinline__ float dot_f(const float4 (&q)[F4], const float4 (&k)[
 
 __device__ __forceinline__ float rate_of(const Cand& a, int tau) { return a.gamma[tau] / (float)a.C; }
 
-// The token's own previous signatures sig[self - 1 - j], j < K (uniform across the wave).
-__device__ __forceinline__ void own_suffix(const float* __restrict__ sigb, int64_t self_pos, int K, float (&mine)[16]) {
+// Suffix match of `other` against the token itself: the number of leading j < K with sig[other - 1 - j] ==
+// sig[self - 1 - j], both in range; NaN never matches (reference nucleo:98-108, 313-320). The reference's K = 4 keeps
+// the token's own four previous signatures in registers (`mine`, uniform across the wave); K up to 16 reads both sides.
+__device__ __forceinline__ void own_suffix_of(const float* __restrict__ sigb, int64_t self_pos, int K,
+                                              float (&mine)[4]) {
 #pragma unroll
-  for (int j = 0; j < 16; ++j) mine[j] = (j < K && self_pos - 1 - j >= 0) ? sigb[self_pos - 1 - j] : 0.f;
+  for (int j = 0; j < 4; ++j) mine[j] = (j < K && self_pos - 1 - j >= 0) ? sigb[self_pos - 1 - j] : 0.f;
 }
 
-// Suffix match of `other` against the token's own previous signatures (K <= 16): the number of leading j with
-// sig[other - 1 - j] == sig[self - 1 - j], both in range; NaN never matches (reference nucleo:98-108, 313-320).
-__device__ __forceinline__ int suffix_vs(const float* __restrict__ sigb, const float (&mine)[16], int64_t self_pos,
-                                        int64_t other, int K) {
+__device__ __forceinline__ int suffix_len_of(const float* __restrict__ sigb, const float (&mine)[4], int64_t self_pos,
+                                            int64_t other, int K) {
   int ell = 0;
   bool run = true;
+  if (K <= 4) {
+    float v[4];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    if (j < K) {
+    for (int j = 0; j < 4; ++j) {
       const int64_t io = other - 1 - j;
-      const float v = sigb[io >= 0 ? io : 0];
-      run = run && io >= 0 && self_pos - 1 - j >= 0 && v == mine[j];
+      v[j] = sigb[io >= 0 ? io : 0];               // every load in flight at once
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      run = run && j < K && other - 1 - j >= 0 && self_pos - 1 - j >= 0 && v[j] == mine[j];
       ell += run ? 1 : 0;
     }
+    return ell;
+  }
+  for (int j = 0; j < K && run; ++j) {
+    const int64_t io = other - 1 - j, is = self_pos - 1 - j;
+    run = io >= 0 && is >= 0 && sigb[io] == sigb[is];
+    ell += run ? 1 : 0;
   }
   return ell;
 }
@@ -319,7 +330,7 @@ __device__ __forceinline__ int dedupe(const Cand& a, int M, Scratch& S) {
       const uint64_t bal = __ballot(prim[c]);
       if (prim[c]) {
         const int u = nu + __popcll(bal & ((1ull << lane) - 1ull));
-        S.uid[m] = u;
+        S.uid[m] = (uint16_t)u;
         S.upos[u] = S.key[m] >> 5;
       }
       nu += __popcll(bal);
@@ -424,7 +435,7 @@ __device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows
 #pragma unroll
       for (int ch = 0; ch < DCH; ++ch) {
         const int dd = ch * 256 + lane * 4;
-        o[r][ch] = dd < a.d ? ld4(rows + row * a.d + dd) : zero4();
+        o[r][ch] = ld4(rows + ((uint32_t)row * (uint32_t)a.d + (uint32_t)(dd < a.d ? dd : a.d - 4)));
       }
     }
 #pragma unroll
@@ -480,12 +491,12 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
   feat_row<F4>(feat_lanes<F4>(a, a.Qc, true), (uint32_t)tok, qf);
   unique_bases<F4>(a, b, t, NU, false, qf, S);
   const float* sigb = a.sig + b * a.L;
-  float mine[16];
-  own_suffix(sigb, t, a.K, mine);
+  float mine[4];
+  own_suffix_of(sigb, t, a.K, mine);
   const double bq = a.Bt[tok];
   for (int u = lane; u < NU; u += kWave) {
     const int64_t k = S.upos[u];
-    const int ell = suffix_vs(sigb, mine, t, k, a.K);
+    const int ell = suffix_len_of(sigb, mine, t, k, a.K);
     S.ua[u] = (S.ua[u] + a.w_suf[ell]) + a.la[b * a.L + k];
     S.ub[u] = (float)(a.Bt[b * a.L + k] - bq);
     S.uc[u] = 0.f;
@@ -565,7 +576,7 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
 #pragma unroll
       for (int ch = 0; ch < DCH; ++ch) {
         const int dd = ch * 256 + lane * 4;
-        v[r][ch] = dd < a.d ? ld4(Vb + p * a.d + dd) : zero4();
+        v[r][ch] = ld4(Vb + ((uint32_t)p * (uint32_t)a.d + (uint32_t)(dd < a.d ? dd : a.d - 4)));
       }
     }
 #pragma unroll
@@ -632,12 +643,12 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   const int M = gather(a, b, t, true, S);
   const int NU = dedupe(a, M, S);
   const float* sigb = a.sig + b * a.L;
-  float mine[16];
-  own_suffix(sigb, t, a.K, mine);
+  float mine[4];
+  own_suffix_of(sigb, t, a.K, mine);
   const double bq = a.Bt[tok];
   for (int u = lane; u < NU; u += kWave) {
     const int64_t k = S.upos[u];
-    S.uell[u] = suffix_vs(sigb, mine, t, k, a.K);
+    S.uell[u] = (uint8_t)suffix_len_of(sigb, mine, t, k, a.K);
     S.ub[u] = (float)(a.Bt[b * a.L + k] - bq);
     S.ud[u] = 0.f;
   }
@@ -757,7 +768,7 @@ __device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows,
 #pragma unroll
       for (int ch = 0; ch < DCH; ++ch) {
         const int dd = ch * 256 + lane * 4;
-        v[r][ch] = dd < a.d ? ld4(rows + p * a.d + dd) : zero4();
+        v[r][ch] = ld4(rows + ((uint32_t)p * (uint32_t)a.d + (uint32_t)(dd < a.d ? dd : a.d - 4)));
       }
     }
 #pragma unroll
@@ -772,7 +783,7 @@ __device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows,
 // slot for this key; per distinct query the table sums weight dO (-> dV) and [phi_q ; Qc_q] (-> d phi_k, d Kc_k).
 // ---------------------------------------------------------------------------------------------------------------------
 template <int F4, int DCH>
-__global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_k(Cand a) {
+__global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH != 3) ? 5 : 1) void k_cand_bwd_k(Cand a) {
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
   const int64_t tok = token_of_wave();
@@ -861,8 +872,8 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_lists(Cand a, i
   const int64_t b = tok / a.L, t = tok % a.L;
   gather(a, b, t, true, S);
   const float* sigb = a.sig + b * a.L;
-  float mine[16];
-  own_suffix(sigb, t, a.K, mine);
+  float mine[4];
+  own_suffix_of(sigb, t, a.K, mine);
   for (int tau = 0; tau < a.T; ++tau) {
     const int lo = S.off[tau], n = S.off[tau + 1] - lo;
     if (lane < a.C) {
@@ -870,7 +881,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_lists(Cand a, i
       const int i = lane - (a.C - n);
       const int64_t k = i >= 0 ? (S.key[lo + i] >> 5) : -1;
       pos[o] = (int32_t)k;
-      ell[o] = i >= 0 ? suffix_vs(sigb, mine, t, k, a.K) : -1;
+      ell[o] = i >= 0 ? suffix_len_of(sigb, mine, t, k, a.K) : -1;
     }
   }
 }

@@ -58,7 +58,7 @@ int asrn_candidates_fwd(const float* phi, const float* V, const float* Qc, const
                         const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
                         const int32_t* order, const int32_t* win, const int32_t* rank, int64_t B, int64_t L,
                         int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
-                        float scale_phi, float scale_c, float* salida, float* signals, float* stats, void* stream);
+                        float scale_phi, float scale_c, float* salida, float* signals, float* att, void* stream);
 
 /* The candidate lists the forward and backward walk, materialized for checking (a3, a4): for each (b, t, tau) the
  * text positions of the <= C most recent earlier bucket mates in the C-slot window [s - C, s) of the sorted row
@@ -83,8 +83,8 @@ int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const
                         const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
                         const int32_t* order, const int32_t* win, const int32_t* rank, int64_t B, int64_t L,
                         int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
-                        float scale_phi, float scale_c, const float* dsalida, const float* stats, float* dphi,
-                        float* dV, float* dQc, float* dKc, double* dBt, float* dlog_alfa, float* qstats,
+                        float scale_phi, float scale_c, const float* dsalida, const float* att, float* dphi,
+                        float* dV, float* dQc, float* dKc, double* dBt, float* dlog_alfa, float* ds,
                         float* partials, void* stream);
 
 /* ---- a9: clock --------------------------------------------------------------------------------------------------
