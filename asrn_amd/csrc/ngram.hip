@@ -3,14 +3,14 @@
 // Keys are fp64 and must round exactly as the reference's separate multiply and add (asrn/nucleo.py:182-184): the
 // kernel uses __dmul_rn / __dadd_rn and this file builds with -ffp-contract=off. The sort orders (key, position)
 // pairs, with the key mapped to an order-preserving uint64 (-0 -> +0, every NaN -> the largest code so NaN sorts
-// last and stays in text order, as torch.argsort(stable=True) does). Tiles of up to 4096 pairs are bitonic-sorted
-// in LDS; longer rows are finished by merge passes in which every element finds its output slot by a binary search
-// in the other run.
-#include "common.h"
+// last and stays in text order, as torch.argsort(stable=True) does). Tiles of up to 1024 pairs are bitonic-sorted
+// in registers, lane exchanges and LDS (block_sort.h); longer rows are finished by merge passes in which every
+// element finds its output slot by a binary search in the other run.
+#include "block_sort.h"
 
 namespace asrn {
 
-constexpr int kTile = 4096;
+constexpr int kTile = 1024;          // pairs per sorted tile (more workgroups; merges finish longer rows)
 constexpr uint64_t kNanCode = ~0ull;
 constexpr uint32_t kPadIdx = 0xFFFFFFFFu;
 
@@ -54,40 +54,23 @@ __global__ void k_ngram_keys(const float* __restrict__ sig, const double* __rest
   }
 }
 
-// bitonic sort of each tile of `tile` pairs (tile is a power of two <= 4096)
-__global__ __launch_bounds__(1024) void k_tile_sort(uint64_t* __restrict__ code, uint32_t* __restrict__ idx,
-                                                    int64_t Lp, int tile) {
-  __shared__ uint64_t sk[kTile];
-  __shared__ uint32_t si[kTile];
+// each tile of `tile` (code, position) pairs sorted by one workgroup of tile / 4 threads (block_sort.h)
+__global__ __launch_bounds__(kTile / 4) void k_tile_sort(uint64_t* __restrict__ code, uint32_t* __restrict__ idx,
+                                                         int64_t Lp, int tile) {
+  __shared__ SortKI lds[kTile];
   const int64_t base = (int64_t)blockIdx.y * Lp + (int64_t)blockIdx.x * tile;
-  for (int i = threadIdx.x; i < tile; i += blockDim.x) {
-    sk[i] = code[base + i];
-    si[i] = idx[base + i];
+  SortKI x[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int64_t e = base + 4 * threadIdx.x + q;
+    x[q] = SortKI{code[e], idx[e]};
   }
-  __syncthreads();
-  const int half = tile >> 1;
-  for (int k = 2; k <= tile; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int p = threadIdx.x; p < half; p += blockDim.x) {
-        const int i = 2 * j * (p / j) + (p % j);
-        const int l = i + j;
-        const bool asc = (i & k) == 0;
-        const uint64_t ka = sk[i], kb = sk[l];
-        const uint32_t ia = si[i], ib = si[l];
-        const bool gt = pair_less(kb, ib, ka, ia);
-        if (gt == asc) {
-          sk[i] = kb;
-          sk[l] = ka;
-          si[i] = ib;
-          si[l] = ia;
-        }
-      }
-      __syncthreads();
-    }
-  }
-  for (int i = threadIdx.x; i < tile; i += blockDim.x) {
-    code[base + i] = sk[i];
-    idx[base + i] = si[i];
+  block_bitonic_sort(x, lds, tile);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int64_t e = base + 4 * threadIdx.x + q;
+    code[e] = x[q].k;
+    idx[e] = x[q].i;
   }
 }
 
@@ -142,6 +125,7 @@ __global__ void k_ngram_finish(const uint64_t* __restrict__ code, const uint32_t
 static void ngram_dims(int64_t B, int64_t L, int n, NgramDims* g) {
   int tile = 2;
   while (tile < L && tile < kTile) tile <<= 1;
+  if (tile < 4) tile = 4;
   int64_t tiles = 1;
   while (tiles * tile < L) tiles <<= 1;
   g->B = B;
@@ -184,8 +168,7 @@ extern "C" int asrn_ngram_sort(const float* sig, const double* coef, int64_t B, 
   hipLaunchKernelGGL(k_ngram_keys, dim3((unsigned)((B * g.Lp + threads - 1) / threads)), dim3(threads), 0, st, sig,
                      coef, g, keys, code0, idx0);
   if (check_launch("asrn_ngram_sort/keys")) return 1;
-  const int sort_threads = g.tile / 2 < 64 ? 64 : (g.tile / 2 > 1024 ? 1024 : g.tile / 2);
-  hipLaunchKernelGGL(k_tile_sort, dim3((unsigned)(g.Lp / g.tile), (unsigned)rows), dim3(sort_threads), 0, st, code0,
+  hipLaunchKernelGGL(k_tile_sort, dim3((unsigned)(g.Lp / g.tile), (unsigned)rows), dim3(g.tile / 4), 0, st, code0,
                      idx0, g.Lp, g.tile);
   if (check_launch("asrn_ngram_sort/tile")) return 1;
   uint64_t* kc = code0;
