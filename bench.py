@@ -30,8 +30,7 @@ HBM_PEAK = 8.0e12
 
 # algorithmic bytes per token at cfg2 (fp32, T 8, P 112, cf 16, d 256): every tensor the kernel must touch, read
 # once and written once. The entry point timed below and its per-token figure.
-def algorithmic_bytes(d, P, cf, T):
-    a = 4
+def algorithmic_bytes(d, P, cf, T, a=4):
     reads_fwd = P * a + 2 * cf * a + d * a + 8 + 8 + 4 + 2 * T * 4       # phi, Qc, Kc, V, x, Bt, log_alfa, order+ids
     fwd = reads_fwd + d * a + 4 * 4                                     # + salida, 4 signals
     bwd = reads_fwd + d * a + (P * a + 2 * cf * a + d * a + 8 + 4)      # + dsalida; dphi, dQc, dKc, dV, dBt, dlog_alfa
@@ -40,8 +39,9 @@ def algorithmic_bytes(d, P, cf, T):
 
 # all HIP kernels of one fwd+bwd at cfg2, each distinct tensor read once and written once: hash + bucket sort 512,
 # clock 16 + 16, n-gram sort 28, Hawkes/streak scans 60 + 100, candidates 2,724 + 4,320 (fwd + bwd)
-HIP_BYTES_PER_TOKEN = 7776
-LAYER_BYTES_PER_TOKEN = 25876         # whole layer at cfg2: the above plus the GEMM-boundary tensors and their grads
+HIP_BYTES_PER_TOKEN = {'fp32': 7776, 'bf16': 6688}    # bf16: the activation tensors at 2 bytes
+# whole layer: the above plus the GEMM-boundary tensors and their gradients (cfg2 fp32; cfg3 bf16)
+LAYER_BYTES_PER_TOKEN = {'fp32': 25876, 'bf16': 24436}
 
 
 TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'cfg2_traffic.json')
@@ -190,12 +190,16 @@ def main():
     gy = torch.randn(B, N, d, generator=torch.Generator().manual_seed(args.seed + 1))
     xd, Ed, hd, gyd = x.to(dev), E.to(dev).requires_grad_(), h.to(dev).requires_grad_(), gy.to(dev)
 
+    bf16 = args.config == 'cfg3'           # configs[2]: bf16 activations, fp32 scan state (autocast)
+    dtype = 'bf16' if bf16 else 'fp32'
+
     def step():
         layer.zero_grad(set_to_none=True)
         Ed.grad = None
         hd.grad = None
-        y = layer(Ed, hd, xd)
-        (y * gyd).sum().backward()
+        with torch.autocast('cuda', dtype=torch.bfloat16, enabled=bf16):
+            y = layer(Ed, hd, xd)
+        (y.float() * gyd).sum().backward()
 
     for _ in range(args.warmup):
         step()
@@ -223,7 +227,7 @@ def main():
     value = tokens * args.steps / (t1 - t0)
 
     P, cf, T = layer.n_tablas * layer.n_bits, layer.confirmar, layer.n_tablas
-    algo = algorithmic_bytes(d, P, cf, T)
+    algo = algorithmic_bytes(d, P, cf, T, a=2 if bf16 else 4)
     dom = max(algo, key=lambda n: per_call.get(n, {}).get('total_ms', 0.0))
     dom_us = per_call[dom]['mean_us']
     achieved = algo[dom] * tokens / (dom_us * 1e-6)
@@ -232,17 +236,17 @@ def main():
     out = {
         'metric': METRIC, 'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps,
         'warmup': args.warmup, 'ms_per_step': round(wall * 1e3, 4), 'higher_is_better': True, 'scaling': 'weak',
-        'vs_baseline': None, 'dtype': 'fp32', 'data': 'synthetic (seeded random bytes, 30% copied spans; random-init '
-        'layer moved off its neutral values)',
+        'vs_baseline': None, 'dtype': dtype, 'data': f'synthetic (seeded tokens, {int(cfg["frac"] * 100)}% copied '
+        'spans; random-init layer moved off its neutral values)',
         'config': {'workload': f'{args.config}: one ASRN layer fwd+bwd, B={B}, N={N}, d={d}, V={V}, T=8 tables x 14 '
-                               f'bits, C=32, fp32', 'global_batch': B, 'seq_len': N, 'parallelism': 'none (1 GPU)'},
+                               f'bits, C=32, {dtype}', 'global_batch': B, 'seq_len': N, 'parallelism': 'none (1 GPU)'},
         'roofline': {'bound': 'hbm', 'kernel': dom, 'achieved': round(achieved / 1e9, 1), 'peak': HBM_PEAK / 1e9,
-                     'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK, 4), 'traffic': measured_traffic(dom),
+                     'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK, 4), 'traffic': measured_traffic(dom) if args.config == 'cfg2' else None,
                      'bytes_per_token': algo[dom], 'mean_launch_us': round(dom_us, 2)},
-        'hip_aggregate': {'bytes_per_token': HIP_BYTES_PER_TOKEN, 'hip_ms_per_step': round(hip_ms_per_step, 4),
-                          'frac': round(HIP_BYTES_PER_TOKEN * tokens / (HBM_PEAK * hip_ms_per_step * 1e-3), 4)},
+        'hip_aggregate': {'bytes_per_token': HIP_BYTES_PER_TOKEN[dtype], 'hip_ms_per_step': round(hip_ms_per_step, 4),
+                          'frac': round(HIP_BYTES_PER_TOKEN[dtype] * tokens / (HBM_PEAK * hip_ms_per_step * 1e-3), 4)},
         'layer': {'tokens_per_s': round(value, 1),
-                  'hbm_frac': round(LAYER_BYTES_PER_TOKEN * tokens / (HBM_PEAK * wall), 4)},
+                  'hbm_frac': round(LAYER_BYTES_PER_TOKEN[dtype] * tokens / (HBM_PEAK * wall), 4)},
         'kernels': {n: {k: round(v, 3) if isinstance(v, float) else v for k, v in s.items()}
                     for n, s in sorted(per_call.items(), key=lambda kv: -kv[1]['total_ms'])},
     }

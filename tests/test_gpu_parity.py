@@ -460,3 +460,27 @@ def test_layer_odd_feature_widths_vs_oracle():
     for n, g in grads.items():
         if n in leaves and leaves[n].grad is not None:
             assert_close(g, leaves[n].grad, 'grad ' + n)
+
+
+def test_layer_bf16_autocast_close_to_fp32():
+    """cfg3's mode at a smaller size: bf16 autocast activations (the GEMMs run in bf16, the kernels read the bf16
+    producers upcast to fp32 and keep fp32 scan state and an fp64 clock). The output and the gradient of h stay within
+    the bf16 tolerance, 2e-2, of the fp32 layer in relative Frobenius norm (a sign flip of a bf16 hash output can move
+    a position to another bucket, so a max-norm comparison would not be meaningful). The gradient of E passes through
+    the bf16 hash MLPs' backward and is looser: the CPU oracle's own bf16-autocast-vs-fp32 gap on this input is 9.0%
+    (0.9% for grad h, 1.9% for y), so it is held to 15%."""
+    say('layer bf16 autocast vs fp32')
+    torch.manual_seed(3)
+    layer = synth.move_params(CapaASRNEstable(64), 3).to(DEV)
+    x, E, h = synth.layer_inputs(2, 2048, 64, 300, seed=8, frac=0.2, span=(16, 64), zipf=1.1)
+    gy = torch.randn(2, 2048, 64, generator=torch.Generator().manual_seed(9))
+    y32, g32 = run_layer(layer, E, h, x, gy)
+    with torch.autocast('cuda', dtype=torch.bfloat16):
+        y16, g16 = run_layer(layer, E, h, x, gy)
+    def fro(a, b):
+        a, b = a.double(), b.double()
+        return ((a - b).norm() / b.norm()).item()
+    assert torch.isfinite(y16).all()
+    assert fro(y16, y32) <= 2e-2, fro(y16, y32)
+    assert fro(g16['E'], g32['E']) <= 0.15, fro(g16['E'], g32['E'])
+    assert fro(g16['h'], g32['h']) <= 2e-2, fro(g16['h'], g32['h'])
