@@ -16,8 +16,8 @@
 //           8+ rows in flight: the table sum never leaves the kernel.
 // The forward also keeps every candidate's weight att at [query][table][distance - 1]. The backward has one owner per
 // output row, no atomics and no score recomputation: a query pass (ds = att (dp - D) with D = sum att*dp per (query,
-// table), written to the same slots; query-side gradients; per-query partials of d gamma and d w_suf) and a key pass
-// (key-side gradients: reads att and ds at the slots of the queries that see the key).
+// table), written next to att; query-side gradients; per-query partials of d gamma and d w_suf) and a key pass
+// (key-side gradients: reads each (att, ds) pair with one 8-byte load at the slots of the queries that see the key).
 #include "common.h"
 
 namespace asrn {
@@ -34,11 +34,13 @@ struct Cand {
   int64_t B, L;
   int d, P, cf, K, T, Tc, C;
   float sp, sc;
-  // forward outputs; att (B*L, T, C): the weight of the key at distance j + 1 before the query, at slot j
-  float* salida; float* signals; float* att;
-  // backward; ds (B*L, T, C) laid out like att, written by the query pass for the key pass
-  const float* dsal; const float* att_in; float* dphi; float* dV; float* dQc; float* dKc; double* dBt;
-  float* dla; float* ds; float* partials;
+  // per-entry weights (B*L, T, C, 2): for the key at distance j + 1 before the query in a table, at slot j, its
+  // attention weight (the forward writes it) and its ds (the backward's query pass writes it for the key pass)
+  float* ent;
+  // forward outputs
+  float* salida; float* signals;
+  // backward
+  const float* dsal; float* dphi; float* dV; float* dQc; float* dKc; double* dBt; float* dla; float* partials;
   // generation: per-bucket rings (B*T, 2^nb, C) of positions and their counts (B*T, 2^nb); the query position tq,
   // its bucket ids (B, T) out, and whether tq then enters the rings
   int32_t* rings; int32_t* counts; int32_t* ids_out; int nb; int64_t tq; int insert;
@@ -477,12 +479,12 @@ __device__ __forceinline__ void load_entries(const Cand& a, int M, const Scratch
 // ---------------------------------------------------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------------------------------------------------
-// One query token's candidate attention: salida row (d), the 4 gate signals and, when `att_rows` is given, every
-// entry's weight at att_rows[tau * C + distance - 1]. RING: candidates from the generation rings instead of the
+// One query token's candidate attention: salida row (d), the 4 gate signals and, when `ent_rows` is given, every
+// entry's weight at ent_rows[2 (tau * C + distance - 1)]. RING: candidates from the generation rings instead of the
 // sorted windows.
 template <int F4, int DCH, bool RING>
 __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t t, Scratch& S, float* salida_row,
-                                              float* signals_row, float* att_rows) {
+                                              float* signals_row, float* ent_rows) {
   const int lane = lane_id();
   const int64_t tok = b * a.L + t;
   const int M = RING ? gather_rings(a, b, t, S) : gather(a, b, t, true, S);
@@ -545,7 +547,7 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
     const int m = c * kWave + lane;
     if (c * kWave < M && E.tau[c] >= 0) {
       w[c] = e[c] * S.tinv[E.tau[c]];
-      if (att_rows) att_rows[E.tau[c] * a.C + (S.off[E.tau[c] + 1] - 1 - m)] = w[c];   // entries ascend
+      if (ent_rows) ent_rows[2 * (E.tau[c] * a.C + (S.off[E.tau[c] + 1] - 1 - m))] = w[c];   // entries ascend
     }
   }
   for (int tt = 0; tt < a.T; ++tt) {                     // sum over tables per unique, in table order
@@ -604,7 +606,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_fwd(Cand a) {
   const int64_t tok = token_of_wave();
   if (tok >= a.B * a.L) return;
   forward_token<F4, DCH, false>(a, tok / a.L, tok % a.L, S, a.salida + tok * a.d, a.signals + tok * 4,
-                                a.att + tok * a.T * a.C);
+                                a.ent + tok * a.T * a.C * 2);
 }
 
 // Generation step: one wave per batch row; the query is position a.tq of the caches (a.L = their capacity). With
@@ -663,8 +665,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   unique_row_dots<DCH>(a, a.V + b * a.L * a.d, t, NU, dO, nullptr, unused, S, S.uc);
 
   // per entry: att from the forward and att * dp (S.ua is a per-entry buffer here)
-  const float* arow = a.att_in + tok * a.T * a.C;
-  float* dsrow = a.ds + tok * a.T * a.C;
+  float* erow = a.ent + tok * a.T * a.C * 2;
   float att[kCh], dp[kCh];
   int tau[kCh], un[kCh], slot[kCh];
 #pragma unroll
@@ -675,7 +676,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
     tau[c] = in ? (e & 31) : -1;
     un[c] = in ? S.uid[m] : 0;
     slot[c] = in ? (e & 31) * a.C + (S.off[(e & 31) + 1] - 1 - m) : 0;
-    att[c] = in ? arow[slot[c]] : 0.f;
+    att[c] = in ? erow[2 * slot[c]] : 0.f;
     dp[c] = in ? S.uc[un[c]] : 0.f;
     if (in) S.ua[m] = att[c] * dp[c];
   }
@@ -696,7 +697,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
     const bool in = tau[c] >= 0;
     ds[c] = in ? att[c] * (dp[c] - S.tsum[tau[c]]) : 0.f;
     if (in) {
-      dsrow[slot[c]] = ds[c];
+      erow[2 * slot[c] + 1] = ds[c];
       S.ua[m] = ds[c];
     }
     const int ell = in ? S.uell[un[c]] : -1;
@@ -811,8 +812,9 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH != 3) ? 5 :
     ds[c] = 0.f;
     if (in) {   // the key sits at distance m - lo + 1 before query (e >> 5) in table tau
       const int64_t o = ((b * a.L + (e >> 5)) * a.T + (e & 31)) * a.C + (m - S.off[e & 31]);
-      att[c] = a.att_in[o];
-      ds[c] = a.ds[o];
+      const float2 w2 = *reinterpret_cast<const float2*>(a.ent + 2 * o);
+      att[c] = w2.x;
+      ds[c] = w2.y;
       dla += ds[c];
       dbk += rate_of(a, e & 31) * ds[c];
     }
@@ -976,12 +978,12 @@ extern "C" int asrn_candidates_fwd(const float* phi, const float* V, const float
                                    const float* gamma, const int32_t* order, const int32_t* win, const int32_t* rank,
                                    int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
                                    int32_t Tc, int32_t C, float scale_phi, float scale_c, float* salida,
-                                   float* signals, float* att, void* stream) {
+                                   float* signals, float* entries, void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
                 scale_phi, scale_c);
   if (check_args(a, "asrn_candidates_fwd")) return 1;
   if (B == 0 || L == 0) return 0;
-  a.salida = salida; a.signals = signals; a.att = att;
+  a.salida = salida; a.signals = signals; a.ent = entries;
   return dispatch<LaunchFwd>(a, (hipStream_t)stream);
 }
 
@@ -990,14 +992,14 @@ extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float
                                    const float* gamma, const int32_t* order, const int32_t* win, const int32_t* rank,
                                    int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
                                    int32_t Tc, int32_t C, float scale_phi, float scale_c, const float* dsalida,
-                                   const float* att, float* dphi, float* dV, float* dQc, float* dKc, double* dBt,
-                                   float* dlog_alfa, float* ds, float* partials, void* stream) {
+                                   float* entries, float* dphi, float* dV, float* dQc, float* dKc, double* dBt,
+                                   float* dlog_alfa, float* partials, void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
                 scale_phi, scale_c);
   if (check_args(a, "asrn_candidates_bwd")) return 1;
   if (B == 0 || L == 0) return 0;
-  a.dsal = dsalida; a.att_in = att; a.dphi = dphi; a.dV = dV; a.dQc = dQc; a.dKc = dKc; a.dBt = dBt;
-  a.dla = dlog_alfa; a.ds = ds; a.partials = partials;
+  a.dsal = dsalida; a.ent = entries; a.dphi = dphi; a.dV = dV; a.dQc = dQc; a.dKc = dKc; a.dBt = dBt;
+  a.dla = dlog_alfa; a.partials = partials;
   return dispatch<LaunchBwd>(a, (hipStream_t)stream);
 }
 

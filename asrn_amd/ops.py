@@ -217,7 +217,8 @@ class Streak(torch.autograd.Function):
 class Candidates(torch.autograd.Function):
     """Candidate attention of all tables (the drop-in for _CasillerosTriton, asrn/nucleo.py:461-515). Returns salida
     (B, L, d) and the gate signals (B, L, 4) = (peso_total, mejor, pico, peso_ctx), the latter without gradient.
-    Saves its inputs and the candidates' attention weights (B, L, T, C), so the backward recomputes no score."""
+    Saves its inputs and the candidates' attention weights (B, L, T, C, 2 with room for ds), so the backward
+    recomputes no score."""
 
     @staticmethod
     def forward(ctx, phi, V, Qc, Kc, Bt, log_alfa, w_suf, gamma, sig, order, win, rank, shape):
@@ -234,11 +235,11 @@ class Candidates(torch.autograd.Function):
         P, cf = ins['phi'].shape[-1], ins['Qc'].shape[-1]
         salida = torch.empty((B, L, d), dtype=torch.float32, device=dev)
         signals = torch.empty((B, L, 4), dtype=torch.float32, device=dev)
-        att = torch.empty((B, L, T, C), dtype=torch.float32, device=dev)     # only the valid slots are written
+        ent = torch.empty((B, L, T, C, 2), dtype=torch.float32, device=dev)  # only the valid slots are written
         call('asrn_candidates_fwd', ptr(ins['phi']), ptr(ins['V']), ptr(ins['Qc']), ptr(ins['Kc']), ptr(ins['sig']),
              ptr(ins['Bt']), ptr(ins['la']), ptr(ins['w']), ptr(ins['g']), ptr(order), ptr(win), ptr(rank), B, L, d,
-             P, cf, K, T, Tc, C, sp, sc, ptr(salida), ptr(signals), ptr(att), stream_of(dev))
-        ctx.save_for_backward(*ins.values(), order, win, rank, att)
+             P, cf, K, T, Tc, C, sp, sc, ptr(salida), ptr(signals), ptr(ent), stream_of(dev))
+        ctx.save_for_backward(*ins.values(), order, win, rank, ent)
         ctx.meta = (B, L, P, d, cf, K, T, Tc, C, sp, sc, V.dtype, phi.dtype, Qc.dtype, Kc.dtype, log_alfa.dtype,
                     P0, cf0)
         ctx.mark_non_differentiable(signals)
@@ -246,7 +247,7 @@ class Candidates(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dsal, _dsig):
-        phi, V, Qc, Kc, sig, Bt, la, w, g, order, win, rank, att = ctx.saved_tensors
+        phi, V, Qc, Kc, sig, Bt, la, w, g, order, win, rank, ent = ctx.saved_tensors
         B, L, P, d, cf, K, T, Tc, C, sp, sc, tv, tp, tq, tk, tl, P0, cf0 = ctx.meta
         dev = phi.device
         dsal = _c(dsal, torch.float32)
@@ -256,11 +257,10 @@ class Candidates(torch.autograd.Function):
         dKc = torch.empty_like(Kc)
         dBt = torch.empty_like(Bt)
         dla = torch.empty_like(la)
-        ds = torch.empty((B, L, T, C), dtype=torch.float32, device=dev)
         partials = torch.empty((B * L, T + K + 1), dtype=torch.float32, device=dev)
         call('asrn_candidates_bwd', ptr(phi), ptr(V), ptr(Qc), ptr(Kc), ptr(sig), ptr(Bt), ptr(la), ptr(w), ptr(g),
-             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ptr(dsal), ptr(att),
-             ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(ds), ptr(partials), stream_of(dev))
+             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ptr(dsal), ptr(ent),
+             ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(partials), stream_of(dev))
         part = partials.sum(0)
         dgamma = part[:T] / C
         dw = part[T:]

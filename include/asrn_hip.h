@@ -51,14 +51,16 @@ int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t T, int32_t 
  *   sig (B, L) fp32 token signatures; Bt (B, L) fp64 clock; log_alfa (B, L); w_suf (K+1); gamma (T)
  *   salida  (B, L, d) out: sum over tables of sum_k att * V_k
  *   signals (B, L, 4) out: peso_total, mejor, pico, peso_ctx
- *   att     (B, L, T, C) out: the weight of each candidate, at [query][tau][distance - 1] (distance in sorted
- *           ranks, 1..n); slots beyond the table's n candidates are not written. Kept for the backward.
+ *   entries (B, L, T, C, 2) out: [..., 0] the weight of each candidate, at [query][tau][distance - 1] (distance
+ *           in sorted ranks, 1..n; slots beyond the table's n candidates are not written); [..., 1] is filled by the
+ *           backward. Kept for the backward.
  * Requires d % 4 == 0, d <= 1024, 1 <= C <= 64, P + cf <= 256, K <= 16, T <= 32. */
 int asrn_candidates_fwd(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                         const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
                         const int32_t* order, const int32_t* win, const int32_t* rank, int64_t B, int64_t L,
                         int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
-                        float scale_phi, float scale_c, float* salida, float* signals, float* att, void* stream);
+                        float scale_phi, float scale_c, float* salida, float* signals, float* entries,
+                        void* stream);
 
 /* The candidate lists the forward and backward walk, materialized for checking (a3, a4): for each (b, t, tau) the
  * text positions of the <= C most recent earlier bucket mates in the C-slot window [s - C, s) of the sorted row
@@ -75,17 +77,16 @@ int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* 
  * ds = att (dp - D) with D = sum att*dp per (query, table), query-side gradients, per-query partials of d gamma and
  * d w_suf) and a key pass (key-side gradients from att and ds at the slots of the queries that see the key: the
  * next <= C same-bucket sorted ranks).
- *   dsalida (B, L, d); att from asrn_candidates_fwd
+ *   dsalida (B, L, d); entries from asrn_candidates_fwd (its [..., 1] receives ds, read back by the key pass)
  *   dphi (B, L, P), dV (B, L, d), dQc, dKc (B, L, cf), dBt (B, L) fp64, dlog_alfa (B, L) out (overwritten)
- *   ds       (B, L, T, C) fp32 workspace (laid out like att)
  *   partials (B*L, T + K + 1) fp32 out: per query, d gamma_tau then d w_suf[0..K]; the caller sums over rows. */
 int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                         const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
                         const int32_t* order, const int32_t* win, const int32_t* rank, int64_t B, int64_t L,
                         int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
-                        float scale_phi, float scale_c, const float* dsalida, const float* att, float* dphi,
-                        float* dV, float* dQc, float* dKc, double* dBt, float* dlog_alfa, float* ds,
-                        float* partials, void* stream);
+                        float scale_phi, float scale_c, const float* dsalida, float* entries, float* dphi,
+                        float* dV, float* dQc, float* dKc, double* dBt, float* dlog_alfa, float* partials,
+                        void* stream);
 
 /* ---- a9: clock --------------------------------------------------------------------------------------------------
  * Bt = cumsum(beta) over L in fp64 (asrn/estable.py:418). reverse != 0 computes the suffix sums instead (the

@@ -65,7 +65,7 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert lib.asrn_candidates_fwd(*args, 64, 112, 16, 4, 8, 4, 65, 0.1, 0.25, N, N, N, N) != 0
     assert 'chunk' in _err(lib)
     # feature width above 256
-    assert lib.asrn_candidates_bwd(*args, 64, 250, 16, 4, 8, 4, 32, 0.1, 0.25, *([N] * 11)) != 0
+    assert lib.asrn_candidates_bwd(*args, 64, 250, 16, 4, 8, 4, 32, 0.1, 0.25, *([N] * 10)) != 0
     assert 'P + cf' in _err(lib)
     # feature widths are read as float4 (the host pads them)
     assert lib.asrn_candidates_fwd(*args, 64, 110, 16, 4, 8, 4, 32, 0.1, 0.25, N, N, N, N) != 0
