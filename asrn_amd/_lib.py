@@ -24,16 +24,17 @@ SIGNATURES = {
     'asrn_candidates_fwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7 + [_F32, _F32] + [_P] * 4),
     'asrn_candidate_lists': (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P]),
     'asrn_candidates_bwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7 + [_F32, _F32] + [_P] * 10),
-    'asrn_clock_scan': (ctypes.c_int, [_P, _P, _I64, _I64, _I32, _P]),
+    'asrn_scan_workspace': (_I64, [_I64, _I64]),
+    'asrn_clock_scan': (ctypes.c_int, [_P, _P, _I64, _I64, _I32, _P, _I64, _P]),
     'asrn_ngram_sort_workspace': (_I64, [_I64, _I64, _I32]),
     'asrn_ngram_sort': (ctypes.c_int, [_P, _P, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _I64, _P]),
-    'asrn_scan_fwd': (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P]),
-    'asrn_scan_bwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _P]),
-    'asrn_hawkes_fwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P]),
+    'asrn_scan_fwd': (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _I64, _P]),
+    'asrn_scan_bwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _P, _I64, _P]),
+    'asrn_hawkes_fwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P, _I64, _P]),
     'asrn_hawkes_bwd_workspace': (_I64, [_I64, _I64, _I32]),
     'asrn_hawkes_bwd': (ctypes.c_int, [_P] * 8 + [_I64, _I64, _I32] + [_P] * 4 + [_I64, _P]),
-    'asrn_streak_fwd': (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I32, _P, _P]),
-    'asrn_streak_bwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P]),
+    'asrn_streak_fwd': (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I32, _P, _P, _I64, _P]),
+    'asrn_streak_bwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P, _I64, _P]),
     'asrn_ring_build': (ctypes.c_int, [_P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P]),
     'asrn_decode_attend': (ctypes.c_int, [_P] * 11 + [_I64, _I64, _I64] + [_I32] * 7 + [_F32, _F32, _I32] + [_P] * 4),
     'asrn_hawkes_table_load': (ctypes.c_int, [_P] * 6 + [_I64, _I64, _I32, _I64] + [_P] * 4),

@@ -91,6 +91,14 @@ def ngram_sort(sig, coef, n):
 # a9
 # ---------------------------------------------------------------------------------------------------------------------
 
+def _scan_workspace(rows, N, dev):
+    """Chunk totals for the scans (asrn_scan_workspace): None for rows that fit one chunk."""
+    wsb = query('asrn_scan_workspace', rows, N)
+    if wsb < 0:
+        raise RuntimeError(f'scan of {rows} rows x {N}: too many chunks')
+    return (torch.empty((wsb,), dtype=torch.uint8, device=dev) if wsb else None), wsb
+
+
 class ClockScan(torch.autograd.Function):
     """Bt = cumsum(beta, 1) in fp64; the backward is the suffix sum."""
 
@@ -99,14 +107,16 @@ class ClockScan(torch.autograd.Function):
         dev = _dev(beta)
         x = _c(beta, torch.float64)
         y = torch.empty_like(x)
-        call('asrn_clock_scan', ptr(x), ptr(y), x.shape[0], x.shape[1], 0, stream_of(dev))
+        ws, wsb = _scan_workspace(x.shape[0], x.shape[1], dev)
+        call('asrn_clock_scan', ptr(x), ptr(y), x.shape[0], x.shape[1], 0, ptr(ws), wsb, stream_of(dev))
         return y
 
     @staticmethod
     def backward(ctx, g):
         g = _c(g, torch.float64)
         out = torch.empty_like(g)
-        call('asrn_clock_scan', ptr(g), ptr(out), g.shape[0], g.shape[1], 1, stream_of(g.device))
+        ws, wsb = _scan_workspace(g.shape[0], g.shape[1], g.device)
+        call('asrn_clock_scan', ptr(g), ptr(out), g.shape[0], g.shape[1], 1, ptr(ws), wsb, stream_of(g.device))
         return out
 
 
@@ -125,7 +135,8 @@ class AffineScan(torch.autograd.Function):
         N = shape[-1]
         a2, b2 = _c(a, torch.float32).reshape(-1, N), _c(b, torch.float32).reshape(-1, N)
         S = torch.empty_like(a2)
-        call('asrn_scan_fwd', ptr(a2), ptr(b2), ptr(S), a2.shape[0], N, stream_of(dev))
+        ws, wsb = _scan_workspace(a2.shape[0], N, dev)
+        call('asrn_scan_fwd', ptr(a2), ptr(b2), ptr(S), a2.shape[0], N, ptr(ws), wsb, stream_of(dev))
         ctx.save_for_backward(a2, S)
         ctx.shape = shape
         return S.view(shape)
@@ -136,7 +147,9 @@ class AffineScan(torch.autograd.Function):
         N = a2.shape[-1]
         g2 = _c(g, torch.float32).reshape(-1, N)
         ga, gb = torch.empty_like(g2), torch.empty_like(g2)
-        call('asrn_scan_bwd', ptr(a2), ptr(S), ptr(g2), ptr(ga), ptr(gb), a2.shape[0], N, stream_of(g.device))
+        ws, wsb = _scan_workspace(a2.shape[0], N, g.device)
+        call('asrn_scan_bwd', ptr(a2), ptr(S), ptr(g2), ptr(ga), ptr(gb), a2.shape[0], N, ptr(ws), wsb,
+             stream_of(g.device))
         return ga.view(ctx.shape), gb.view(ctx.shape)
 
 
@@ -161,8 +174,9 @@ class Hawkes(torch.autograd.Function):
         kap = _c(kappa, torch.float32)
         hawkes = torch.empty((B, L, n), dtype=torch.float32, device=dev)
         S = torch.empty((B, n, L), dtype=torch.float32, device=dev)
+        ws, wsb = _scan_workspace(B * n, L, dev)
         call('asrn_hawkes_fwd', ptr(order), ptr(rep), ptr(Bt), ptr(la), ptr(kap), B, L, n, ptr(hawkes), ptr(S),
-             stream_of(dev))
+             ptr(ws), wsb, stream_of(dev))
         ctx.save_for_backward(Bt, la, kap, order, rep, rank_k, S)
         return hawkes
 
@@ -193,7 +207,8 @@ class Streak(torch.autograd.Function):
         kr = _c(kappa_r, torch.float32)
         vistos = _c(vistos, torch.float32)
         racha = torch.empty((B, L), dtype=torch.float32, device=dev)
-        call('asrn_streak_fwd', ptr(vistos), ptr(beta), ptr(kr), B, L, n, ptr(racha), stream_of(dev))
+        ws, wsb = _scan_workspace(B, L, dev)
+        call('asrn_streak_fwd', ptr(vistos), ptr(beta), ptr(kr), B, L, n, ptr(racha), ptr(ws), wsb, stream_of(dev))
         ctx.save_for_backward(vistos, beta, kr, racha)
         return racha
 
@@ -205,8 +220,9 @@ class Streak(torch.autograd.Function):
         g = _c(g, torch.float32)
         dbeta = torch.empty((B, L), dtype=torch.float64, device=dev)
         dkr = torch.empty((B,), dtype=torch.float32, device=dev)
+        ws, wsb = _scan_workspace(B, L, dev)
         call('asrn_streak_bwd', ptr(vistos), ptr(beta), ptr(kr), ptr(racha), ptr(g), B, L, n, ptr(dbeta), ptr(dkr),
-             stream_of(dev))
+             ptr(ws), wsb, stream_of(dev))
         return dbeta, dkr.sum().reshape(1), None
 
 

@@ -88,10 +88,18 @@ int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const
                         float* dV, float* dQc, float* dKc, double* dBt, float* dlog_alfa, float* partials,
                         void* stream);
 
+/* ---- scan workspace -------------------------------------------------------------------------------------------
+ * No counterpart in the reference (PyTorch allocates for it). Every scan below cuts its rows into chunks spread over
+ * the CUs; rows longer than 1024 elements need a device workspace of asrn_scan_workspace(rows, N) bytes for the chunk
+ * totals (0 for shorter rows, where the workspace pointer may be null; -1 when rows x chunks would reach 2^31). The
+ * contents need no clearing and are dead after the call. */
+int64_t asrn_scan_workspace(int64_t rows, int64_t N);
+
 /* ---- a9: clock --------------------------------------------------------------------------------------------------
  * Bt = cumsum(beta) over L in fp64 (asrn/estable.py:418). reverse != 0 computes the suffix sums instead (the
- * backward of the cumsum). */
-int asrn_clock_scan(const double* x, double* y, int64_t B, int64_t L, int32_t reverse, void* stream);
+ * backward of the cumsum). workspace: asrn_scan_workspace(B, L) bytes. */
+int asrn_clock_scan(const double* x, double* y, int64_t B, int64_t L, int32_t reverse, void* workspace,
+                    int64_t workspace_bytes, void* stream);
 
 /* ---- a10: n-gram keys, stable key sort, repeated and seen flags -------------------------------------------------
  * Replaces _claves_de (asrn/nucleo.py:175-185), _ordenar_claves (asrn/nucleo.py:693-701) and the scatter of the seen
@@ -110,20 +118,22 @@ int asrn_ngram_sort(const float* sig, const double* coef, int64_t B, int64_t L, 
                     int64_t workspace_bytes, void* stream);
 
 /* ---- a12: affine scan S_i = a_i S_{i-1} + b_i over rows of N (asrn/nucleo.py:188-196, 214-257, 518-537) --------
- * scan_bwd: l_i = g_i + a_{i+1} l_{i+1}; gb = l; ga_i = l_i S_{i-1}. */
-int asrn_scan_fwd(const float* a, const float* b, float* S, int64_t rows, int64_t N, void* stream);
+ * scan_bwd: l_i = g_i + a_{i+1} l_{i+1}; gb = l; ga_i = l_i S_{i-1}. workspace: asrn_scan_workspace(rows, N) bytes. */
+int asrn_scan_fwd(const float* a, const float* b, float* S, int64_t rows, int64_t N, void* workspace,
+                  int64_t workspace_bytes, void* stream);
 int asrn_scan_bwd(const float* a, const float* S, const float* g, float* ga, float* gb, int64_t rows, int64_t N,
-                  void* stream);
+                  void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- a11: Hawkes intensities in key order (asrn/estable.py:313-318) ---------------------------------------------
  * Per (b, j) row in key order: dB_i = fp32(max(0, Bt[o_i] - Bt[o_{i-1}])), a_i = repeated_i exp(-kappa_j dB_i),
  * lambda = scan(a, a * alfa_{i-1}) with alfa = exp(log_alfa); hawkes[b, o_i, j] = lambda_i.
  *   hawkes (B, L, n) out; S_sorted (B, n, L) out (lambda in key order, kept for the backward)
  * hawkes_bwd: from dhawkes (B, L, n) gives dBt (B, L) fp64 and dlog_alfa (B, L) (overwritten) and dkappa (B, n)
- * per-row partials of d kappa_j. workspace: asrn_hawkes_bwd_workspace(B, L, n) bytes. */
+ * per-row partials of d kappa_j. Workspaces: asrn_scan_workspace(B * n, L) bytes for hawkes_fwd,
+ * asrn_hawkes_bwd_workspace(B, L, n) for hawkes_bwd. */
 int asrn_hawkes_fwd(const int32_t* order, const uint8_t* repeated, const double* Bt, const float* log_alfa,
                     const float* kappa, int64_t B, int64_t L, int32_t n, float* hawkes, float* S_sorted,
-                    void* stream);
+                    void* workspace, int64_t workspace_bytes, void* stream);
 int64_t asrn_hawkes_bwd_workspace(int64_t B, int64_t L, int32_t n);
 int asrn_hawkes_bwd(const int32_t* order, const uint8_t* repeated, const int32_t* rank_k, const double* Bt,
                     const float* log_alfa, const float* kappa, const float* S_sorted, const float* dhawkes,
@@ -132,12 +142,13 @@ int asrn_hawkes_bwd(const int32_t* order, const uint8_t* repeated, const int32_t
 
 /* ---- a11: repetition streak (asrn/estable.py:319-320) ----------------------------------------------------------
  * racha = scan(r exp(-kappa_r fp32(beta)), r) over the text with r = vistos[:, :, n-1].
- * streak_bwd: dbeta (B, L) fp64 (overwritten) and dkappa_r (B) per-row partials of d kappa_r. */
+ * streak_bwd: dbeta (B, L) fp64 (overwritten) and dkappa_r (B) per-row partials of d kappa_r.
+ * workspace: asrn_scan_workspace(B, L) bytes. */
 int asrn_streak_fwd(const float* vistos, const double* beta, const float* kappa_r, int64_t B, int64_t L, int32_t n,
-                    float* racha, void* stream);
+                    float* racha, void* workspace, int64_t workspace_bytes, void* stream);
 int asrn_streak_bwd(const float* vistos, const double* beta, const float* kappa_r, const float* racha,
                     const float* dracha, int64_t B, int64_t L, int32_t n, double* dbeta, float* dkappa_r,
-                    void* stream);
+                    void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- a14: the O(1) generation step (asrn/nucleo.py:1585-1854, asrn/estable.py:359-372) ------------------------
  * Rings: rings (B*T, 2^nb, C) int32 positions (-1 empty), counts (B*T, 2^nb) int32. The r-th position to enter a

@@ -183,7 +183,7 @@ def test_ngram_vs_oracle(B, L, V, zipf):
 # a9, a11, a12: scans
 # ---------------------------------------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize('N', [1, 2, 3, 7, 64, 1000, 4097, 10000])
+@pytest.mark.parametrize('N', [1, 2, 3, 7, 64, 1000, 1025, 4097, 10000, 70000])
 def test_affine_scan_vs_sequential(N):
     say('scan', N)
     g = torch.Generator().manual_seed(N)
@@ -244,6 +244,38 @@ def test_repetition_golden(name):
     assert_close(gla, g['rep.g_log_alfa'], 'grad log_alfa')
     assert_close(glk, g['rep.g_log_kappa'], 'grad log_kappa')
     assert_close(glkr, g['rep.g_log_kappa_racha'], 'grad log_kappa_racha')
+
+
+@pytest.mark.parametrize('B,L,n,V', [(2, 1025, 4, 3), (2, 5000, 4, 5), (1, 70000, 3, 8)])
+def test_repetition_vs_oracle_long_rows(B, L, n, V):
+    """Hawkes and streak scans over rows that span many chunks (the carry between chunks and the chunk-summed d kappa)
+    against the oracle's sequential scans, outputs and every gradient."""
+    say('repetition long rows', B, L, n, V)
+    g = torch.Generator().manual_seed(L)
+    x = torch.randint(0, V, (B, L), generator=g)
+    sig = O.firmas(x)
+    beta = (torch.rand(B, L, generator=g, dtype=torch.float64) * 0.2).requires_grad_()
+    Bt = (torch.rand(B, L, generator=g, dtype=torch.float64) * 0.2).cumsum(1).requires_grad_()
+    la = (torch.randn(B, L, generator=g) * 0.3).requires_grad_()
+    lk = (torch.randn(n, generator=g) * 0.5 - 1.0).requires_grad_()
+    lkr = torch.tensor([-2.0]).requires_grad_()
+    c = torch.rand(n, generator=g, dtype=torch.float64) + 0.5                  # the c_vistos buffer's law
+    gh = torch.randn(B, L, n, generator=g)
+    gr = torch.randn(B, L, generator=g)
+    p = {'log_kappa': lk, 'log_kappa_racha': lkr, 'c_vistos': c}
+    ref = O.repetition(p, sig, beta, Bt, la, O.Shape(d=32, n=n), O.Prot())
+    ((ref['hawkes'] * gh).sum() + (ref['racha'] * gr).sum()).backward()
+    leaves = [t.detach().to(DEV).requires_grad_() for t in (beta, Bt, la, lk, lkr)]
+    _, order, rep, rank_k, vistos = ops.ngram_sort(sig.to(DEV), c.to(DEV), n)
+    hawkes = ops.Hawkes.apply(leaves[1], leaves[2], leaves[3].exp(), order, rep, rank_k)
+    racha = ops.Streak.apply(leaves[0], leaves[4].exp(), vistos)
+    ((hawkes * gh.to(DEV)).sum() + (racha * gr.to(DEV)).sum()).backward()
+    assert torch.equal(vistos.cpu(), ref['vistos'])
+    assert_close(hawkes, ref['hawkes'], 'hawkes')
+    assert_close(racha, ref['racha'], 'racha')
+    for name, mine, want in zip(('beta', 'Bt', 'log_alfa', 'log_kappa', 'log_kappa_racha'), leaves,
+                                (beta, Bt, la, lk, lkr)):
+        assert_close(mine.grad, want.grad, 'grad ' + name)
 
 
 # ---------------------------------------------------------------------------------------------------------------------

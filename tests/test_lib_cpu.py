@@ -75,6 +75,15 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert lib.asrn_ngram_sort(N, N, 8, 4096, 4, N, N, N, N, N, N, 16, N) != 0
     assert 'workspace' in _err(lib)
     assert lib.asrn_hawkes_bwd_workspace(8, 4096, 4) >= 2 * 8 * 4096 * 4 * 4
+    # scans: rows of one chunk need none; longer rows hold 12 bytes per chunk of 256
+    assert lib.asrn_scan_workspace(8, 1024) == 0
+    assert lib.asrn_scan_workspace(32, 4096) >= 32 * 16 * 12
+    assert lib.asrn_scan_workspace(1 << 20, 1 << 20) == -1
+    assert lib.asrn_hawkes_bwd_workspace(8, 4096, 4) >= 2 * 8 * 4096 * 4 * 4 + lib.asrn_scan_workspace(32, 4096)
+    assert lib.asrn_scan_fwd(N, N, N, 2, 4096, N, 0, N) != 0
+    assert 'workspace' in _err(lib)
+    assert lib.asrn_streak_bwd(*([N] * 5), 2, 2048, 4, N, N, N, 1 << 20, N) != 0
+    assert 'workspace' in _err(lib)
     # generation: ring sizes, the decode position inside the caches, table capacities
     assert lib.asrn_ring_build(N, N, 2, 10, 8, 15, 32, N, N, N) != 0
     assert 'asrn_ring_build' in _err(lib)
