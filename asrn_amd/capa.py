@@ -3,9 +3,10 @@
 Same constructor arguments, parameter and buffer names, construction order (so the same seed gives the same weights)
 and forward contract as asrn.estable.CapaASRNEstable (asrn/estable.py:141-421, inheriting asrn/nucleo.py:574-886):
 forward(E (B, L, d), h (B, L, d), piezas (B, L) int64 | None) -> h' (B, L, d). The dense projections (hash MLPs, V,
-LayerNorm, Qc/Kc, the clock projection, the gate and W_o) stay PyTorch GEMMs; the bucket sort, the candidate
-attention forward and backward, the n-gram sort, the clock, Hawkes and streak scans run in libasrn_hip.so. There is
-no CPU path: CPU tensors or unsupported shapes raise.
+LayerNorm, Qc/Kc, the clock projection, the gate and W_o) stay hipBLASLt GEMMs, with their weight gradients split
+over slabs of tokens (asrn_amd.lineal); the bucket sort, the candidate attention forward and backward, the n-gram
+sort, the clock, Hawkes and streak scans run in libasrn_hip.so. There is no CPU path: CPU tensors or unsupported
+shapes raise.
 """
 import dataclasses
 import math
@@ -15,6 +16,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
+from .lineal import lineal
 
 PROHIBIDO = -1e9          # the "not allowed" score (asrn/nucleo.py:86)
 
@@ -126,10 +128,12 @@ class CapaASRNEstable(nn.Module):
         pal = self.afin_palabra
         m = pal[0].out_features
         E = _a_autocast(E)
-        y = F.linear(E, torch.cat([pal[0].weight, self.v.weight]), F.pad(pal[0].bias, (0, d)))
+        y = lineal(E, torch.cat([pal[0].weight, self.v.weight]), F.pad(pal[0].bias, (0, d)))
         hp, v = y.split([m, d], dim=-1)
         llave = torch.cat([E, F.pad(E, (0, 0, 1, 0))[:, :L]], dim=-1)
-        phi = torch.cat([pal[2](pal[1](hp)), self.afin_contexto(llave)], dim=-1)
+        ctx = self.afin_contexto
+        phi = torch.cat([lineal(pal[1](hp), pal[2].weight, pal[2].bias),
+                         lineal(ctx[1](lineal(llave, ctx[0].weight, ctx[0].bias)), ctx[2].weight, ctx[2].bias)], dim=-1)
         return phi, F.pad(v, (0, 0, 0, 1))[:, 1:]
 
     def _contexto(self, h):
@@ -139,9 +143,9 @@ class CapaASRNEstable(nn.Module):
         hh32 = self.ln_ctx(h)
         hh = _a_autocast(hh32)
         cf = self.confirmar
-        y = F.linear(hh, torch.cat([self.cq.weight, self.ck.weight]))
-        x32 = hh32.float()
-        u = torch.stack([(x32 * self.w_reloj[i].float()).sum(-1) for i in range(2)], -1) + self.b_reloj.float()
+        y = lineal(hh, torch.cat([self.cq.weight, self.ck.weight]))
+        with torch.autocast(device_type=h.device.type, enabled=False):
+            u = lineal(hh32.float(), self.w_reloj.float(), self.b_reloj.float())
         beta = F.softplus(u[..., 0])
         log_alfa = F.logsigmoid(u[..., 1]) + math.log(2)
         if p.beta_max is not None:
@@ -203,15 +207,15 @@ class CapaASRNEstable(nn.Module):
         senales = torch.cat([pt / self.n_tablas, mejor, acc['pico'] / pt.clamp(min=1),
                              acc['peso_ctx'].detach() / self.tablas_contexto], dim=-1)
         with torch.autocast(device_type=h.device.type, enabled=False):
-            logit = F.linear(h, self.g.weight.to(h.dtype), self.g.bias.to(h.dtype))
-        logit = logit + self.g_conf(senales).to(logit.dtype)
+            logit = lineal(h, self.g.weight, self.g.bias)
+        logit = logit + lineal(senales, self.g_conf.weight, self.g_conf.bias).to(logit.dtype)
         logit = logit + (acc['vistos'].to(logit.dtype) * self.w_vistos.to(logit.dtype)).sum(-1, keepdim=True)
         hawkes = torch.log1p(acc['hawkes']).to(logit.dtype)
         logit = logit + (hawkes * self.u_hawkes.to(logit.dtype)).sum(-1, keepdim=True)
         logit = logit + self._respuesta_racha(acc['racha']).unsqueeze(-1).to(logit.dtype)
         if p.tope_puerta is not None:
             logit = p.tope_puerta * torch.tanh(logit / p.tope_puerta)
-        aporte = self.o(salida)
+        aporte = lineal(salida, self.o.weight)
         return h + torch.sigmoid(logit).to(aporte.dtype) * self.drop(aporte)
 
     # --- all together -----------------------------------------------------------------------------------------------
