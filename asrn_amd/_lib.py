@@ -35,6 +35,10 @@ SIGNATURES = {
     'asrn_hawkes_bwd': (ctypes.c_int, [_P] * 8 + [_I64, _I64, _I32] + [_P] * 4 + [_I64, _P]),
     'asrn_streak_fwd': (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I32, _P, _P, _I64, _P]),
     'asrn_streak_bwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P, _I64, _P]),
+    'asrn_gate_fwd': (ctypes.c_int, [_P, _P, _I32] + [_P] * 11 + [_I64] + [_I32] * 5 + [_F32] * 3 + [_P] * 3),
+    'asrn_gate_bwd_workspace': (_I64, [_I64, _I32]),
+    'asrn_gate_bwd': (ctypes.c_int, [_P, _P, _I32] + [_P] * 11 + [_I64] + [_I32] * 5 + [_F32] * 3 + [_P] * 8
+                      + [_I64, _P]),
     'asrn_ring_build': (ctypes.c_int, [_P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P]),
     'asrn_decode_attend': (ctypes.c_int, [_P] * 11 + [_I64, _I64, _I64] + [_I32] * 7 + [_F32, _F32, _I32] + [_P] * 4),
     'asrn_hawkes_table_load': (ctypes.c_int, [_P] * 6 + [_I64, _I64, _I32, _I64] + [_P] * 4),

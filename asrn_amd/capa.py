@@ -171,8 +171,7 @@ class CapaASRNEstable(nn.Module):
         shape = dict(T=T, Tc=self.tablas_contexto, C=self.chunk, K=self.sufijo)
         salida, sen = ops.Candidates.apply(phi, V, Qc, Kc, Bt, log_alfa, self.w_sufijo, self.gamma, sig, order,
                                            win, rank, shape)
-        return {'salida': salida, 'peso_total': sen[..., 0:1], 'mejor': sen[..., 1:2], 'pico': sen[..., 2:3],
-                'peso_ctx': sen[..., 3:4]}
+        return {'salida': salida, 'senales': sen}
 
     def _repeticion(self, sig, beta, Bt, log_alfa, partes=None):
         """vistos, hawkes (B, L, n) and racha (B, L) (asrn/estable.py:304-321)."""
@@ -185,38 +184,18 @@ class CapaASRNEstable(nn.Module):
             partes.update(claves=claves, orden_k=order, repetido=rep)
         return {'vistos': vistos, 'hawkes': hawkes, 'racha': racha}
 
-    # --- gate (PyTorch, asrn/estable.py:376-403 and asrn/nucleo.py:865-878) ------------------------------------------
-
-    @property
-    def u_racha(self):
-        return self.d_racha.cumsum(0)
-
-    def _respuesta_racha(self, racha):
-        """Piecewise-linear response on log1p(racha), flat past the last node (asrn/nucleo.py:870-878)."""
-        x = (torch.log1p(racha) / self.racha_paso).clamp(max=self.d_racha.shape[0] - 1)
-        i = torch.nan_to_num(x.detach(), nan=0.0).floor().long().clamp(0, self.d_racha.shape[0] - 2)
-        return _Take.apply(i, self.u_racha) + (x - i) * _Take.apply(i, self.d_racha[1:])
+    # --- gate (asrn/estable.py:376-403 and asrn/nucleo.py:865-878) ---------------------------------------------------
 
     def _combinar(self, acc, h):
+        """h' = h + sigmoid(logit) W_o (salida / max(1, peso_total)): W_o on hipBLASLt, the rest fused in asrn_gate_*
+        (the division by the table count is applied after W_o, per token)."""
         p = self.protecciones
-        salida, pt = acc['salida'], acc['peso_total'].detach()
-        salida = salida / acc['peso_total'].clamp(min=1)
-        mejor = torch.where(pt > 0, acc['mejor'], torch.zeros_like(pt))
-        if p.mejor_max is not None:
-            mejor = mejor.clamp(-p.mejor_max, p.mejor_max)
-        senales = torch.cat([pt / self.n_tablas, mejor, acc['pico'] / pt.clamp(min=1),
-                             acc['peso_ctx'].detach() / self.tablas_contexto], dim=-1)
-        with torch.autocast(device_type=h.device.type, enabled=False):
-            logit = lineal(h, self.g.weight, self.g.bias)
-        logit = logit + lineal(senales, self.g_conf.weight, self.g_conf.bias).to(logit.dtype)
-        logit = logit + (acc['vistos'].to(logit.dtype) * self.w_vistos.to(logit.dtype)).sum(-1, keepdim=True)
-        hawkes = torch.log1p(acc['hawkes']).to(logit.dtype)
-        logit = logit + (hawkes * self.u_hawkes.to(logit.dtype)).sum(-1, keepdim=True)
-        logit = logit + self._respuesta_racha(acc['racha']).unsqueeze(-1).to(logit.dtype)
-        if p.tope_puerta is not None:
-            logit = p.tope_puerta * torch.tanh(logit / p.tope_puerta)
-        aporte = lineal(salida, self.o.weight)
-        return h + torch.sigmoid(logit).to(aporte.dtype) * self.drop(aporte)
+        aporte = self.drop(lineal(acc['salida'], self.o.weight))
+        meta = (self.n_tablas, self.tablas_contexto, self.racha_paso,
+                -1.0 if p.mejor_max is None else float(p.mejor_max), 0.0 if p.tope_puerta is None else float(p.tope_puerta))
+        return ops.Gate.apply(h, aporte, acc['senales'], acc['vistos'], acc['hawkes'], acc['racha'], self.g.weight,
+                               self.g.bias, self.g_conf.weight, self.g_conf.bias, self.w_vistos, self.u_hawkes,
+                               self.d_racha, meta)
 
     # --- all together -----------------------------------------------------------------------------------------------
 
@@ -237,25 +216,6 @@ class CapaASRNEstable(nn.Module):
             partes.update(Qc=Qc, Kc=Kc, sig=sig, beta=beta, Bt=Bt, log_alfa=log_alfa, hawkes=acc['hawkes'],
                           racha=acc['racha'])
         return self._combinar(acc, h)
-
-
-class _Take(torch.autograd.Function):
-    """w[i] for a tiny w (the streak nodes) at every position. The backward sums the gradient of each entry with a
-    one-hot reduction instead of indexing's scatter-add (sorted atomics on the GPU), as the reference's _Tomar does
-    (asrn/nucleo.py:136-158): deterministic and a few small kernels."""
-
-    @staticmethod
-    def forward(ctx, i, w):
-        ctx.save_for_backward(i)
-        ctx.n = w.shape[0]
-        return w[i]
-
-    @staticmethod
-    def backward(ctx, g):
-        (i,) = ctx.saved_tensors
-        hot = i.reshape(-1, 1) == torch.arange(ctx.n, device=i.device)
-        gw = torch.where(hot, g.reshape(-1, 1).float(), 0.0).sum(0)
-        return None, gw.to(g.dtype)
 
 
 def _a_autocast(x):

@@ -97,8 +97,7 @@ class EscritorCapa:
         vistos, hawkes = self.hawkes.step(c, t, beta[:, 0], capa.c_vistos, kappa, kappa_r, self.racha)
         salida, sen, _ = ops.decode_attend(c, t, self.anillos, self.cuentas, capa.w_sufijo, capa.gamma, self._forma(),
                                            insert=not self.ajeno)
-        acc = {'salida': salida.unsqueeze(1).to(e_t.dtype), 'peso_total': sen[:, None, 0:1],
-               'mejor': sen[:, None, 1:2], 'pico': sen[:, None, 2:3], 'peso_ctx': sen[:, None, 3:4],
+        acc = {'salida': salida.unsqueeze(1).to(e_t.dtype), 'senales': sen[:, None],
                'vistos': vistos.unsqueeze(1), 'hawkes': hawkes.unsqueeze(1), 'racha': self.racha.unsqueeze(1).clone()}
         y = capa._combinar(acc, h_t.unsqueeze(1))[:, 0]
         self.e_ult = e_t

@@ -227,6 +227,61 @@ class Streak(torch.autograd.Function):
 
 
 # ---------------------------------------------------------------------------------------------------------------------
+# a13
+# ---------------------------------------------------------------------------------------------------------------------
+
+GATE_COLS = 64        # the small parameters' block of asrn_gate_bwd's dparams
+
+
+class Gate(torch.autograd.Function):
+    """h' = h + sigmoid(cap(logit)) A / max(1, peso_total), A = W_o salida, with the logit of _combinar
+    (asrn/estable.py:376-403) and the streak response (asrn/nucleo.py:865-878), fused in asrn_gate_fwd/bwd.
+    meta = (T, Tc, racha_paso, mejor_max or -1, tope or 0). signals and vistos carry no gradient."""
+
+    @staticmethod
+    def forward(ctx, h, A, signals, vistos, hawkes, racha, wg, bg, wc, bc, wv, uh, dr, meta):
+        T, Tc, paso, mejor_max, tope = meta
+        dev = _dev(h, A)
+        B, L, d = h.shape
+        n, nodes = vistos.shape[-1], dr.shape[0]
+        h32 = _c(h, torch.float32)
+        bf = A.dtype == torch.bfloat16
+        A = A.contiguous() if bf else _c(A, torch.float32)
+        sig, vis, haw, ra = (_c(t, torch.float32) for t in (signals, vistos, hawkes, racha))
+        params = [_c(p, torch.float32).reshape(-1) for p in (wg, bg, wc, bc, wv, uh, dr)]
+        logit = torch.empty((B, L), dtype=torch.float32, device=dev)
+        out = torch.empty_like(h32)
+        call('asrn_gate_fwd', ptr(h32), ptr(A), int(bf), ptr(sig), ptr(vis), ptr(haw), ptr(ra),
+             *[ptr(p) for p in params], B * L, d, n, nodes, T, Tc, paso, mejor_max, tope, ptr(logit), ptr(out),
+             stream_of(dev))
+        ctx.save_for_backward(h32, A, sig, vis, haw, ra, *params, logit)
+        ctx.meta = (B, L, d, n, nodes, T, Tc, paso, mejor_max, tope, h.dtype,
+                    [p.shape for p in (wg, bg, wc, bc, wv, uh, dr)])
+        return out.to(torch.promote_types(h.dtype, A.dtype))
+
+    @staticmethod
+    def backward(ctx, g):
+        h32, A, sig, vis, haw, ra, *rest = ctx.saved_tensors
+        params, logit = rest[:7], rest[7]
+        B, L, d, n, nodes, T, Tc, paso, mejor_max, tope, hdt, shapes = ctx.meta
+        dev = h32.device
+        g = _c(g, torch.float32)
+        dh = torch.empty_like(h32)
+        dA = torch.empty_like(A)
+        dhaw = torch.empty_like(haw)
+        dra = torch.empty_like(ra)
+        dp = torch.empty((d + GATE_COLS,), dtype=torch.float32, device=dev)
+        wsb = query('asrn_gate_bwd_workspace', B * L, d)
+        ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+        call('asrn_gate_bwd', ptr(h32), ptr(A), int(A.dtype == torch.bfloat16), ptr(sig), ptr(vis), ptr(haw),
+             ptr(ra), *[ptr(p) for p in params], B * L, d, n, nodes, T, Tc, paso, mejor_max, tope, ptr(logit),
+             ptr(g), ptr(dh), ptr(dA), ptr(dhaw), ptr(dra), ptr(dp), ptr(ws), wsb, stream_of(dev))
+        sizes = [d, 1, 4, 1, n, n, nodes]
+        grads = [t.view(s) for t, s in zip(torch.split(dp[:sum(sizes)], sizes), shapes)]
+        return (dh.to(hdt), dA, None, None, dhaw, dra, *grads, None)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
 # a3 - a8
 # ---------------------------------------------------------------------------------------------------------------------
 

@@ -150,6 +150,33 @@ int asrn_streak_bwd(const float* vistos, const double* beta, const float* kappa_
                     const float* dracha, int64_t B, int64_t L, int32_t n, double* dbeta, float* dkappa_r,
                     void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- a13: the gate consumer (asrn/estable.py:376-403, asrn/nucleo.py:865-878) -------------------------------
+ * Replaces the PyTorch ops of _combinar after W_o: with A = W_o salida (B*L, d) (fp32, or bf16 when aporte_bf16),
+ * r = 1 / max(1, peso_total) and
+ *   logit = (h . w_g + b_g) + (sen . w_conf + b_conf) + vistos . w_vistos + log1p(hawkes) . u_hawkes + f(racha),
+ *   sen = [peso_total / T, clip(mejor, +-mejor_max) or 0 without candidates, pico / max(1, peso_total), peso_ctx / Tc],
+ *   f(racha) = cumsum(d_racha)[i] + (x - i) d_racha[i + 1], x = min(log1p(racha) / racha_paso, nodes - 1),
+ *   i = clamp(floor(x), 0, nodes - 2),
+ * gives out = h + sigmoid(cap(logit)) r A (cap(l) = tope tanh(l / tope) when tope > 0; mejor_max < 0: no clip) and
+ * the logit (B*L) kept for the backward. h, out fp32 (B*L, d); signals (B*L, 4) from asrn_candidates_fwd; vistos,
+ * hawkes (B*L, n); racha (B*L); w_g (d), b_g (1), w_conf (4), b_conf (1), w_vistos (n), u_hawkes (n), d_racha (nodes).
+ * d % 4 == 0, d <= 1024, 6 + 2 n + nodes <= 64.
+ * gate_bwd: from dout gives dh (fp32), daporte (A's dtype), dhawkes (B*L, n), dracha (B*L) and dparams (d + 64) =
+ * the gradients of [w_g | b_g | w_conf | b_conf | w_vistos | u_hawkes | d_racha | unused], summed over tokens in a
+ * fixed order. workspace: asrn_gate_bwd_workspace(B*L, d) bytes. */
+int asrn_gate_fwd(const float* h, const void* aporte, int32_t aporte_bf16, const float* signals, const float* vistos,
+                  const float* hawkes, const float* racha, const float* w_g, const float* b_g, const float* w_conf,
+                  const float* b_conf, const float* w_vistos, const float* u_hawkes, const float* d_racha, int64_t BL,
+                  int32_t d, int32_t n, int32_t nodes, int32_t T, int32_t Tc, float racha_paso, float mejor_max,
+                  float tope, float* logit, float* out, void* stream);
+int64_t asrn_gate_bwd_workspace(int64_t BL, int32_t d);
+int asrn_gate_bwd(const float* h, const void* aporte, int32_t aporte_bf16, const float* signals, const float* vistos,
+                  const float* hawkes, const float* racha, const float* w_g, const float* b_g, const float* w_conf,
+                  const float* b_conf, const float* w_vistos, const float* u_hawkes, const float* d_racha, int64_t BL,
+                  int32_t d, int32_t n, int32_t nodes, int32_t T, int32_t Tc, float racha_paso, float mejor_max,
+                  float tope, const float* logit, const float* dout, float* dh, void* daporte, float* dhawkes,
+                  float* dracha, float* dparams, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---- a14: the O(1) generation step (asrn/nucleo.py:1585-1854, asrn/estable.py:359-372) ------------------------
  * Rings: rings (B*T, 2^nb, C) int32 positions (-1 empty), counts (B*T, 2^nb) int32. The r-th position to enter a
  * bucket sits in slot r % C (the C most recent are kept).

@@ -13,6 +13,7 @@ import torch
 import asrn_amd
 from asrn_amd import ops, synth
 from asrn_amd.capa import CapaASRNEstable
+from asrn_amd.lineal import lineal
 from oracle import layer as O
 from tests import fixtures
 
@@ -376,6 +377,61 @@ def test_candidates_cfg2_full_size():
     for k in rg:
         assert_close(grads[k], rg[k], 'grad ' + k)
 
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a13: the gate
+# ---------------------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize('tope,bf16', [(None, False), (10.0, False), (None, True)])
+def test_gate_vs_oracle(tope, bf16):
+    """The fused gate (asrn_gate_fwd/bwd, with W_o on hipBLASLt) against the oracle's combine: rows without any
+    candidate (peso_total 0, mejor -1e9), mejor beyond the clip, streaks past the last response node, and the optional
+    tanh cap; output and the gradients of h, salida, hawkes, racha and every gate parameter. bf16: W_o under bf16
+    autocast, within the bf16 tolerance."""
+    say('gate', tope, bf16)
+    B, L, d, n, T, Tc = 2, 333, 64, 4, 8, 4
+    sh = O.Shape(d=d, T=T, Tc=Tc, n=n)
+    prot = O.Prot(tope_puerta=tope)
+    g = torch.Generator().manual_seed(7 + int(bf16) + (0 if tope is None else 1))
+    p = {'g.weight': torch.randn(1, d, generator=g) * 0.1, 'g.bias': torch.randn(1, generator=g),
+         'g_conf.weight': torch.randn(1, 4, generator=g) * 0.5, 'g_conf.bias': torch.randn(1, generator=g),
+         'w_vistos': torch.randn(n, generator=g), 'u_hawkes': torch.randn(n, generator=g),
+         'd_racha': torch.randn(sh.nodos, generator=g) * 0.3, 'o.weight': torch.randn(d, d, generator=g) * 0.1}
+    pt = torch.randint(0, T + 1, (B, L, 1), generator=g).float()
+    mejor = torch.randn(B, L, 1, generator=g) * 3
+    mejor[:, ::17] = 2e4                                                   # beyond the clip at 1e4
+    mejor = torch.where(pt > 0, mejor, torch.full_like(mejor, -1e9))
+    pico = torch.rand(B, L, 1, generator=g) * pt
+    ctx = torch.minimum(pt, torch.randint(0, Tc + 1, (B, L, 1), generator=g).float())
+    top = math.log1p(sh.racha_max) * 1.3
+    leaves = {'h': torch.randn(B, L, d, generator=g), 'salida': torch.randn(B, L, d, generator=g) * 2,
+              'hawkes': torch.rand(B, L, n, generator=g) * 5,
+              'racha': torch.expm1(torch.rand(B, L, generator=g) * top)}
+    vistos = (torch.rand(B, L, n, generator=g) < 0.5).float()
+    gy = torch.randn(B, L, d, generator=g)
+    ref = {k: v.clone().requires_grad_() for k, v in leaves.items()}
+    pr = {k: v.clone().requires_grad_() for k, v in p.items()}
+    acc = {'salida': ref['salida'], 'peso_total': pt, 'mejor': mejor, 'pico': pico, 'peso_ctx': ctx,
+           'vistos': vistos, 'hawkes': ref['hawkes'], 'racha': ref['racha']}
+    yo = O.combine(pr, acc, ref['h'], sh, prot)
+    (yo * gy).sum().backward()
+    mine = {k: v.to(DEV).requires_grad_() for k, v in leaves.items()}
+    pm = {k: v.to(DEV).requires_grad_() for k, v in p.items()}
+    sen = torch.cat([pt, mejor, pico, ctx], -1).to(DEV)
+    meta = (T, Tc, sh.racha_paso, float(prot.mejor_max), 0.0 if tope is None else tope)
+    with torch.autocast('cuda', dtype=torch.bfloat16, enabled=bf16):
+        A = lineal(mine['salida'], pm['o.weight'])
+    y = ops.Gate.apply(mine['h'], A, sen, vistos.to(DEV), mine['hawkes'], mine['racha'], pm['g.weight'],
+                       pm['g.bias'], pm['g_conf.weight'], pm['g_conf.bias'], pm['w_vistos'], pm['u_hawkes'],
+                       pm['d_racha'], meta)
+    (y * gy.to(DEV)).sum().backward()
+    tol = 2e-2 if bf16 else TOL
+    assert y.dtype == torch.float32
+    assert_close(y, yo, 'out', tol)
+    for k in leaves:
+        assert_close(mine[k].grad, ref[k].grad, 'grad ' + k, tol)
+    for k in p:
+        assert_close(pm[k].grad, pr[k].grad, 'grad ' + k, tol)
 
 # ---------------------------------------------------------------------------------------------------------------------
 # the whole layer

@@ -84,6 +84,15 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert 'workspace' in _err(lib)
     assert lib.asrn_streak_bwd(*([N] * 5), 2, 2048, 4, N, N, N, 1 << 20, N) != 0
     assert 'workspace' in _err(lib)
+    # gate: row width, the small parameters' block, the workspace
+    gate = [N, N, 0] + [N] * 11
+    assert lib.asrn_gate_fwd(*gate, 10, 6, 4, 16, 8, 4, 0.4, 1e4, 0.0, N, N, N) != 0
+    assert 'd=6' in _err(lib)
+    assert lib.asrn_gate_fwd(*gate, 10, 256, 16, 40, 8, 4, 0.4, 1e4, 0.0, N, N, N) != 0
+    assert 'nodes' in _err(lib)
+    assert lib.asrn_gate_bwd(*gate, 10, 256, 4, 16, 8, 4, 0.4, 1e4, 0.0, *([N] * 8), 16, N) != 0
+    assert 'workspace' in _err(lib)
+    assert lib.asrn_gate_bwd_workspace(32768, 256) >= 320 * 4
     # generation: ring sizes, the decode position inside the caches, table capacities
     assert lib.asrn_ring_build(N, N, 2, 10, 8, 15, 32, N, N, N) != 0
     assert 'asrn_ring_build' in _err(lib)
