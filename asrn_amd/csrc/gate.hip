@@ -10,7 +10,9 @@
 //   h' = h + sigmoid(cap(logit)) r A,        cap(l) = tope tanh(l / tope) when a cap is set
 // (W_o (salida r) = r (W_o salida): the division by the table count is folded into the per-token factor.)
 //
-// One wavefront per token (grid-stride), the d-rows read as float4 per lane: h, A and h' stream through HBM once.
+// A workgroup takes 32 tokens: their small inputs (signals, seen flags, Hawkes, streak) are turned into features by one
+// thread per token, then each wave runs 8 tokens' d-rows, as float4 per lane, loading 4 tokens' rows at a time so the
+// loads overlap: h, A and h' stream through HBM once.
 // The backward gives dh, dA, dhawkes, dracha per token and the parameter gradients as per-workgroup partials summed
 // in a fixed order by a second launch (deterministic, no atomics).
 #include "common.h"
@@ -19,7 +21,6 @@ namespace asrn {
 
 constexpr int kGateThreads = 256;
 constexpr int kGateWaves = kGateThreads / kWave;
-constexpr int kGateMaxBlocks = 512;
 constexpr int kGateMaxD4 = 4;    // d <= 1024
 constexpr int kGateCols = 64;    // lanes that carry the small parameters' gradients: 6 + 2 n + nodes <= 64
 
@@ -55,181 +56,238 @@ __device__ __forceinline__ void store_a4(void* p, int bf16, int64_t q, float4 v)
   ((uint2*)p)[q] = make_uint2(bf16_bits(v.x) | (bf16_bits(v.y) << 16), bf16_bits(v.z) | (bf16_bits(v.w) << 16));
 }
 
-// The per-token inputs of the logit other than h, and the streak response's position.
-struct Small {
-  float r, sen[4], x, frac, sum;   // sum: every logit term but h . w_g + b_g
-  int i;
-  bool xpass;                      // the clamp of x passes the gradient
+// The small part of the logit is linear in the packed small parameters P = [b_g | w_conf (4) | b_conf | w_vistos (n)
+// | u_hawkes (n) | d_racha (nodes)]: logit = h . w_g + sum_c P_c f_c(t), with the features
+//   f = [1 | sen (4) | 1 | vistos (n) | log1p(hawkes) (n) | [m <= i] + (x - i) [m == i + 1] for m < nodes]
+// (the streak response cumsum(d_racha)[i] + (x - i) d_racha[i + 1] written per node). Phase 1 of each workgroup
+// computes f for its tokens, one thread per token, into LDS; the d-row work then runs a wave per token.
+constexpr int kGateTok = 32;             // tokens per workgroup
+constexpr int kGateTokPerWave = kGateTok / kGateWaves;
+constexpr int kGateBatch = 4;            // tokens whose rows a wave loads together
+constexpr int kFeatStride = kGateCols + 1;
+
+struct TokenInfo {
+  float r;       // 1 / max(1, peso_total)
+  float small;   // sum_c P_c f_c
+  float dxdr;    // d x / d racha where the clamp passes, else 0
+  int i;         // streak segment
 };
 
-__device__ __forceinline__ Small small_terms(const GateArgs& a, int64_t t) {
-  Small s;
+__device__ __forceinline__ float small_param(const GateArgs& a, int c) {
+  const int n = a.n;
+  if (c == 0) return a.bg[0];
+  if (c <= 4) return a.wc[c - 1];
+  if (c == 5) return a.bc[0];
+  if (c < 6 + n) return a.wv[c - 6];
+  if (c < 6 + 2 * n) return a.uh[c - 6 - n];
+  return a.dr[c - 6 - 2 * n];
+}
+
+// phase 1: token t's features into f (LDS row), its info into ti
+__device__ void token_features(const GateArgs& a, int64_t t, float* f, TokenInfo* ti) {
+  const int n = a.n, S = 6 + 2 * n + a.nodes;
   const float4 g = ((const float4*)a.sig)[t];     // peso_total, mejor, pico, peso_ctx
   const float pt = g.x;
-  s.r = 1.f / fmaxf(pt, 1.f);
   float mejor = pt > 0.f ? g.y : 0.f;
   if (a.mejor_max >= 0.f) mejor = fminf(fmaxf(mejor, -a.mejor_max), a.mejor_max);
-  s.sen[0] = pt / (float)a.T;
-  s.sen[1] = mejor;
-  s.sen[2] = g.z / fmaxf(pt, 1.f);
-  s.sen[3] = g.w / (float)a.Tc;
-  float conf = 0.f;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) conf += s.sen[k] * a.wc[k];
-  conf += a.bc[0];
-  float vis = 0.f, haw = 0.f;
-  for (int j = 0; j < a.n; ++j) {
-    vis += a.vistos[t * a.n + j] * a.wv[j];
-    haw += log1pf(a.hawkes[t * a.n + j]) * a.uh[j];
+  f[0] = 1.f;
+  f[1] = pt / (float)a.T;
+  f[2] = mejor;
+  f[3] = g.z / fmaxf(pt, 1.f);
+  f[4] = g.w / (float)a.Tc;
+  f[5] = 1.f;
+  for (int j = 0; j < n; ++j) {
+    f[6 + j] = a.vistos[t * n + j];
+    f[6 + n + j] = log1pf(a.hawkes[t * n + j]);
   }
   const float top = (float)(a.nodes - 1);
-  const float xr = log1pf(a.racha[t]) / a.paso;
-  s.xpass = xr <= top;
-  s.x = fminf(xr, top);
-  float fi = s.x != s.x ? 0.f : floorf(s.x);
+  const float ra = a.racha[t];
+  const float xr = log1pf(ra) / a.paso;
+  const float x = fminf(xr, top);
+  float fi = x != x ? 0.f : floorf(x);
   fi = fminf(fmaxf(fi, 0.f), (float)(a.nodes - 2));
-  s.i = (int)fi;
-  s.frac = s.x - fi;
-  float cum = 0.f;
-  for (int k = 0; k <= s.i; ++k) cum += a.dr[k];
-  const float resp = cum + s.frac * a.dr[s.i + 1];
-  s.sum = conf + vis + haw + resp;
-  return s;
+  const int i = (int)fi;
+  for (int m = 0; m < a.nodes; ++m) f[6 + 2 * n + m] = (m <= i ? 1.f : 0.f) + (m == i + 1 ? x - fi : 0.f);
+  float small = 0.f;
+  for (int c = 0; c < S; ++c) small += small_param(a, c) * f[c];
+  ti->r = 1.f / fmaxf(pt, 1.f);
+  ti->small = small;
+  ti->dxdr = xr <= top ? 1.f / ((1.f + ra) * a.paso) : 0.f;
+  ti->i = i;
 }
 
 __device__ __forceinline__ float capped(float l, float tope) { return tope > 0.f ? tope * tanhf(l / tope) : l; }
 
 template <int D4>
 __global__ __launch_bounds__(kGateThreads) void k_gate_fwd(GateArgs a) {
-  const int lane = threadIdx.x & (kWave - 1);
+  __shared__ float feat[kGateTok][kFeatStride];
+  __shared__ TokenInfo info[kGateTok];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int d4 = a.d >> 2;
-  const int64_t stride = (int64_t)gridDim.x * kGateWaves;
-  for (int64_t t = (int64_t)blockIdx.x * kGateWaves + (threadIdx.x >> 6); t < a.BL; t += stride) {
-    const float4* h4 = (const float4*)(a.h + t * a.d);
-    float4 hv[D4], av[D4];
-    float dot = 0.f;
+  const int64_t t0 = (int64_t)blockIdx.x * kGateTok;
+  if (threadIdx.x < kGateTok && t0 + threadIdx.x < a.BL)
+    token_features(a, t0 + threadIdx.x, feat[threadIdx.x], &info[threadIdx.x]);
+  __syncthreads();
+  for (int b = 0; b < kGateTokPerWave; b += kGateBatch) {
+    float4 hv[kGateBatch][D4], av[kGateBatch][D4];
+    float dot[kGateBatch];
 #pragma unroll
-    for (int k = 0; k < D4; ++k) {
-      const int q = lane + kWave * k;
-      if (q < d4) {
-        hv[k] = h4[q];
-        av[k] = load_a4(a.A, a.a_bf16, t * d4 + q);
-        const float4 w = ((const float4*)a.wg)[q];
-        dot += hv[k].x * w.x + hv[k].y * w.y + hv[k].z * w.z + hv[k].w * w.w;
+    for (int u = 0; u < kGateBatch; ++u) {
+      const int64_t t = t0 + wave * kGateTokPerWave + b + u;
+      dot[u] = 0.f;
+#pragma unroll
+      for (int k = 0; k < D4; ++k) {
+        const int q = lane + kWave * k;
+        if (t < a.BL && q < d4) {
+          hv[u][k] = ((const float4*)(a.h + t * a.d))[q];
+          av[u][k] = load_a4(a.A, a.a_bf16, t * d4 + q);
+          const float4 w = ((const float4*)a.wg)[q];
+          dot[u] += hv[u][k].x * w.x + hv[u][k].y * w.y + hv[u][k].z * w.z + hv[u][k].w * w.w;
+        }
       }
     }
-    const Small s = small_terms(a, t);
-    const float logit = (wave_sum_u(dot) + a.bg[0]) + s.sum;
-    if (lane == 0) a.logit[t] = logit;
-    const float sr = s.r / (1.f + expf(-capped(logit, a.tope)));
-    float4* o4 = (float4*)(a.out + t * a.d);
 #pragma unroll
-    for (int k = 0; k < D4; ++k) {
-      const int q = lane + kWave * k;
-      if (q < d4)
-        o4[q] = make_float4(hv[k].x + sr * av[k].x, hv[k].y + sr * av[k].y, hv[k].z + sr * av[k].z,
-                            hv[k].w + sr * av[k].w);
+    for (int u = 0; u < kGateBatch; ++u) {
+      const int tl = wave * kGateTokPerWave + b + u;
+      const int64_t t = t0 + tl;
+      if (t >= a.BL) break;
+      const float logit = wave_sum_u(dot[u]) + info[tl].small;
+      if (lane == 0) a.logit[t] = logit;
+      const float sr = info[tl].r / (1.f + expf(-capped(logit, a.tope)));
+      float4* o4 = (float4*)(a.out + t * a.d);
+#pragma unroll
+      for (int k = 0; k < D4; ++k) {
+        const int q = lane + kWave * k;
+        if (q < d4)
+          o4[q] = make_float4(hv[u][k].x + sr * av[u][k].x, hv[u][k].y + sr * av[u][k].y,
+                              hv[u][k].z + sr * av[u][k].z, hv[u][k].w + sr * av[u][k].w);
+      }
     }
   }
 }
 
 template <int D4>
 __global__ __launch_bounds__(kGateThreads) void k_gate_bwd(GateArgs a) {
-  __shared__ float red[kGateWaves][4 * D4 * kWave + kGateCols];
+  __shared__ float feat[kGateTok][kFeatStride];
+  __shared__ TokenInfo info[kGateTok];
+  __shared__ float dl[kGateTok];
+  __shared__ float red[kGateWaves][4 * D4 * kWave];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int d4 = a.d >> 2;
-  const int n = a.n, base_v = 6, base_u = 6 + n, base_r = 6 + 2 * n;
-  const int64_t stride = (int64_t)gridDim.x * kGateWaves;
+  const int n = a.n, S = 6 + 2 * n + a.nodes;
+  const int64_t t0 = (int64_t)blockIdx.x * kGateTok;
+  if (threadIdx.x < kGateTok) {
+    dl[threadIdx.x] = 0.f;
+    if (t0 + threadIdx.x < a.BL) token_features(a, t0 + threadIdx.x, feat[threadIdx.x], &info[threadIdx.x]);
+  }
+  __syncthreads();
   float4 gw[D4];
 #pragma unroll
   for (int k = 0; k < D4; ++k) gw[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-  float gs = 0.f;   // this lane's small parameter (column d + lane)
-  for (int64_t t = (int64_t)blockIdx.x * kGateWaves + wave; t < a.BL; t += stride) {
-    const float4* g4 = (const float4*)(a.dout + t * a.d);
-    const float4* h4 = (const float4*)(a.h + t * a.d);
-    float4 gv[D4], hv[D4], av[D4];
-    float ga = 0.f;
+  for (int b = 0; b < kGateTokPerWave; b += kGateBatch) {
+    float4 gv[kGateBatch][D4], hv[kGateBatch][D4], av[kGateBatch][D4];
+    float ga[kGateBatch], lg[kGateBatch];
 #pragma unroll
-    for (int k = 0; k < D4; ++k) {
-      const int q = lane + kWave * k;
-      if (q < d4) {
-        gv[k] = g4[q];
-        hv[k] = h4[q];
-        av[k] = load_a4(a.A, a.a_bf16, t * d4 + q);
-        ga += gv[k].x * av[k].x + gv[k].y * av[k].y + gv[k].z * av[k].z + gv[k].w * av[k].w;
+    for (int u = 0; u < kGateBatch; ++u) {
+      const int64_t t = t0 + wave * kGateTokPerWave + b + u;
+      ga[u] = 0.f;
+      lg[u] = t < a.BL ? a.logit[t] : 0.f;
+#pragma unroll
+      for (int k = 0; k < D4; ++k) {
+        const int q = lane + kWave * k;
+        if (t < a.BL && q < d4) {
+          gv[u][k] = ((const float4*)(a.dout + t * a.d))[q];
+          hv[u][k] = ((const float4*)(a.h + t * a.d))[q];
+          av[u][k] = load_a4(a.A, a.a_bf16, t * d4 + q);
+          ga[u] += gv[u][k].x * av[u][k].x + gv[u][k].y * av[u][k].y + gv[u][k].z * av[u][k].z +
+                   gv[u][k].w * av[u][k].w;
+        }
       }
     }
-    const Small s = small_terms(a, t);
-    const float l = a.logit[t];
-    float dcap = 1.f;
-    float lc = l;
-    if (a.tope > 0.f) {
-      const float th = tanhf(l / a.tope);
-      lc = a.tope * th;
-      dcap = 1.f - th * th;
-    }
-    const float sg = 1.f / (1.f + expf(-lc));
-    const float dlogit = wave_sum_u(ga) * s.r * (sg * (1.f - sg)) * dcap;
-    const float sr = sg * s.r;
-    float4* dh4 = (float4*)(a.dh + t * a.d);
 #pragma unroll
-    for (int k = 0; k < D4; ++k) {
-      const int q = lane + kWave * k;
-      if (q < d4) {
-        const float4 w = ((const float4*)a.wg)[q];
-        dh4[q] = make_float4(gv[k].x + dlogit * w.x, gv[k].y + dlogit * w.y, gv[k].z + dlogit * w.z,
-                             gv[k].w + dlogit * w.w);
-        store_a4(a.dA, a.a_bf16, t * d4 + q, make_float4(gv[k].x * sr, gv[k].y * sr, gv[k].z * sr, gv[k].w * sr));
-        gw[k].x += dlogit * hv[k].x;
-        gw[k].y += dlogit * hv[k].y;
-        gw[k].z += dlogit * hv[k].z;
-        gw[k].w += dlogit * hv[k].w;
+    for (int u = 0; u < kGateBatch; ++u) {
+      const int tl = wave * kGateTokPerWave + b + u;
+      const int64_t t = t0 + tl;
+      if (t >= a.BL) break;
+      float dcap = 1.f, lc = lg[u];
+      if (a.tope > 0.f) {
+        const float th = tanhf(lg[u] / a.tope);
+        lc = a.tope * th;
+        dcap = 1.f - th * th;
+      }
+      const float sg = 1.f / (1.f + expf(-lc));
+      const float r = info[tl].r;
+      const float dlogit = wave_sum_u(ga[u]) * r * (sg * (1.f - sg)) * dcap;
+      if (lane == 0) dl[tl] = dlogit;
+      const float sr = sg * r;
+#pragma unroll
+      for (int k = 0; k < D4; ++k) {
+        const int q = lane + kWave * k;
+        if (q < d4) {
+          const float4 w = ((const float4*)a.wg)[q];
+          ((float4*)(a.dh + t * a.d))[q] = make_float4(gv[u][k].x + dlogit * w.x, gv[u][k].y + dlogit * w.y,
+                                                       gv[u][k].z + dlogit * w.z, gv[u][k].w + dlogit * w.w);
+          store_a4(a.dA, a.a_bf16, t * d4 + q,
+                   make_float4(gv[u][k].x * sr, gv[u][k].y * sr, gv[u][k].z * sr, gv[u][k].w * sr));
+          gw[k].x += dlogit * hv[u][k].x;
+          gw[k].y += dlogit * hv[u][k].y;
+          gw[k].z += dlogit * hv[u][k].z;
+          gw[k].w += dlogit * hv[u][k].w;
+        }
       }
     }
-    // small parameters: one lane each
-    float f = 0.f;
-    if (lane == 0 || lane == 5) f = 1.f;
-    else if (lane <= 4) f = lane == 1 ? s.sen[0] : lane == 2 ? s.sen[1] : lane == 3 ? s.sen[2] : s.sen[3];
-    else if (lane < base_u) f = a.vistos[t * n + lane - base_v];
-    else if (lane < base_r) f = log1pf(a.hawkes[t * n + lane - base_u]);
-    else if (lane < base_r + a.nodes) {
-      const int m = lane - base_r;
-      f = (m <= s.i ? 1.f : 0.f) + (m == s.i + 1 ? s.frac : 0.f);
-    }
-    gs += dlogit * f;
-    if (lane < n) a.dhawkes[t * n + lane] = dlogit * a.uh[lane] / (1.f + a.hawkes[t * n + lane]);
-    if (lane == 0)
-      a.dracha[t] = s.xpass ? dlogit * a.dr[s.i + 1] / ((1.f + a.racha[t]) * a.paso) : 0.f;
   }
-  // workgroup partial: the waves' sums in wave order
-  float* mine = red[wave];
 #pragma unroll
   for (int k = 0; k < D4; ++k) {
     const int q = lane + kWave * k;
-    mine[4 * q + 0] = gw[k].x;
-    mine[4 * q + 1] = gw[k].y;
-    mine[4 * q + 2] = gw[k].z;
-    mine[4 * q + 3] = gw[k].w;
+    red[wave][4 * q + 0] = gw[k].x;
+    red[wave][4 * q + 1] = gw[k].y;
+    red[wave][4 * q + 2] = gw[k].z;
+    red[wave][4 * q + 3] = gw[k].w;
   }
-  mine[4 * D4 * kWave + lane] = gs;
   __syncthreads();
   const int cols = a.d + kGateCols;
-  for (int c = threadIdx.x; c < cols; c += kGateThreads) {
-    const int src = c < a.d ? c : 4 * D4 * kWave + (c - a.d);
+  float* prow = a.partial + (int64_t)blockIdx.x * cols;
+  for (int c = threadIdx.x; c < a.d; c += kGateThreads) {
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < kGateWaves; ++w) v += red[w][src];
-    a.partial[(int64_t)blockIdx.x * cols + c] = v;
+    for (int w = 0; w < kGateWaves; ++w) v += red[w][c];
+    prow[c] = v;
+  }
+  const int tid = threadIdx.x;
+  if (tid < kGateCols) {                 // the small parameters: tokens in order
+    const int64_t left = a.BL - t0;
+    const int ntok = left < kGateTok ? (int)left : kGateTok;
+    float v = 0.f;
+    if (tid < S)
+      for (int tl = 0; tl < ntok; ++tl) v += dl[tl] * feat[tl][tid];
+    prow[a.d + tid] = v;
+  } else if (tid >= 128 && tid < 128 + kGateTok && t0 + (tid - 128) < a.BL) {   // per-token gradients
+    const int tl = tid - 128;
+    const int64_t t = t0 + tl;
+    const float g = dl[tl];
+    for (int j = 0; j < n; ++j) a.dhawkes[t * n + j] = g * a.uh[j] / (1.f + a.hawkes[t * n + j]);
+    a.dracha[t] = g * a.dr[info[tl].i + 1] * info[tl].dxdr;
   }
 }
 
-// dparams[c] = sum over workgroups g of partial[g][c], in workgroup order
-__global__ void k_gate_params(const float* __restrict__ partial, int groups, int cols, float* __restrict__ dparams) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
+// dparams[c] = sum over workgroups g of partial[g][c]: one workgroup per column (thread-strided runs, then the
+// waves' sums in order)
+__global__ __launch_bounds__(kGateThreads) void k_gate_params(const float* __restrict__ partial, int groups,
+                                                               int cols, float* __restrict__ dparams) {
+  __shared__ float ws[kGateWaves];
+  const int c = blockIdx.x, lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   float v = 0.f;
-  for (int g = 0; g < groups; ++g) v += partial[(int64_t)g * cols + c];
-  dparams[c] = v;
+  for (int g = threadIdx.x; g < groups; g += kGateThreads) v += partial[(int64_t)g * cols + c];
+  v = wave_sum_u(v);
+  if (lane == 0) ws[wave] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kGateWaves; ++w) s += ws[w];
+    dparams[c] = s;
+  }
 }
 
 static int gate_check(const GateArgs& a, const char* what) {
@@ -242,10 +300,8 @@ static int gate_check(const GateArgs& a, const char* what) {
   return 0;
 }
 
-static int gate_groups(int64_t BL) {
-  const int64_t g = (BL + kGateWaves - 1) / kGateWaves;
-  return (int)(g < kGateMaxBlocks ? (g > 0 ? g : 1) : kGateMaxBlocks);
-}
+// one workgroup per kGateTok tokens (the backward writes a row of parameter partials per workgroup)
+static int64_t gate_groups(int64_t BL) { return BL > 0 ? (BL + kGateTok - 1) / kGateTok : 1; }
 
 }  // namespace asrn
 
@@ -264,7 +320,8 @@ extern "C" int asrn_gate_fwd(const float* h, const void* aporte, int32_t aporte_
   a.mejor_max = mejor_max; a.tope = tope; a.logit = logit; a.out = out;
   if (gate_check(a, "asrn_gate_fwd")) return 1;
   if (BL == 0) return 0;
-  const dim3 grid(gate_groups(BL)), block(kGateThreads);
+  ASRN_REQUIRE(gate_groups(BL) < (int64_t(1) << 31), "asrn_gate_fwd: too many tokens");
+  const dim3 grid((unsigned)gate_groups(BL)), block(kGateThreads);
   hipStream_t st = (hipStream_t)stream;
   switch ((d + 4 * kWave - 1) / (4 * kWave)) {
     case 1: hipLaunchKernelGGL(k_gate_fwd<1>, grid, block, 0, st, a); break;
@@ -276,7 +333,7 @@ extern "C" int asrn_gate_fwd(const float* h, const void* aporte, int32_t aporte_
 }
 
 extern "C" int64_t asrn_gate_bwd_workspace(int64_t BL, int32_t d) {
-  return (int64_t)gate_groups(BL) * (d + kGateCols) * (int64_t)sizeof(float);
+  return gate_groups(BL) * (d + kGateCols) * (int64_t)sizeof(float);
 }
 
 extern "C" int asrn_gate_bwd(const float* h, const void* aporte, int32_t aporte_bf16, const float* signals,
@@ -295,7 +352,8 @@ extern "C" int asrn_gate_bwd(const float* h, const void* aporte, int32_t aporte_
   if (gate_check(a, "asrn_gate_bwd")) return 1;
   ASRN_REQUIRE(workspace != nullptr && workspace_bytes >= asrn_gate_bwd_workspace(BL, d),
                "asrn_gate_bwd: workspace too small");
-  const int groups = gate_groups(BL);
+  ASRN_REQUIRE(gate_groups(BL) < (int64_t(1) << 31), "asrn_gate_bwd: too many tokens");
+  const int groups = (int)gate_groups(BL);
   const int cols = d + kGateCols;
   hipStream_t st = (hipStream_t)stream;
   switch ((d + 4 * kWave - 1) / (4 * kWave)) {
@@ -305,7 +363,7 @@ extern "C" int asrn_gate_bwd(const float* h, const void* aporte, int32_t aporte_
     default: hipLaunchKernelGGL(k_gate_bwd<4>, dim3(groups), dim3(kGateThreads), 0, st, a); break;
   }
   if (check_launch("asrn_gate_bwd")) return 1;
-  hipLaunchKernelGGL(k_gate_params, dim3((cols + 255) / 256), dim3(256), 0, st, (const float*)workspace, groups,
-                     cols, dparams);
+  hipLaunchKernelGGL(k_gate_params, dim3(cols), dim3(kGateThreads), 0, st, (const float*)workspace, groups, cols,
+                     dparams);
   return check_launch("asrn_gate_bwd/params");
 }

@@ -52,6 +52,23 @@ def weight_grad(g2, x2):
     return torch.bmm(_slab(g2, s).transpose(1, 2), _slab(x2, s)).sum(0, dtype=_acc_dtype(g2))
 
 
+_ONES = {}
+
+
+def column_sums(g2):
+    """Sum over the rows of g2 (N, k), in fp32 (fp64 for fp64): per-slab products with a ones vector on the matrix
+    cores, then the slab sum. (A plain sum over N is a multi-workgroup reduction, whose semaphores are cleared with a
+    memset before every call.)"""
+    s = slabs_for(g2.shape[0])
+    if s == 1:
+        return g2.sum(0, dtype=_acc_dtype(g2))
+    key = (s, g2.shape[0] // s, g2.dtype, g2.device)
+    ones = _ONES.get(key)
+    if ones is None:
+        ones = _ONES[key] = torch.ones((s, 1, key[1]), dtype=g2.dtype, device=g2.device)
+    return torch.bmm(ones, _slab(g2, s)).sum(0, dtype=_acc_dtype(g2)).reshape(-1)
+
+
 class _Lineal(torch.autograd.Function):
 
     @staticmethod
@@ -77,7 +94,7 @@ class _Lineal(torch.autograd.Function):
             if ctx.needs_input_grad[1]:
                 gw = weight_grad(g2, _rows(xc)).to(wdt)
             if bdt is not None and ctx.needs_input_grad[2]:
-                gb = g2.sum(0, dtype=_acc_dtype(g2)).to(bdt)
+                gb = column_sums(g2).to(bdt)
         return gx, gw, gb, None
 
 

@@ -199,7 +199,7 @@ def main():
         hd.grad = None
         with torch.autocast('cuda', dtype=torch.bfloat16, enabled=bf16):
             y = layer(Ed, hd, xd)
-        (y.float() * gyd).sum().backward()
+        y.backward(gyd.to(y.dtype))                     # the gradient of sum(y * gy)
 
     for _ in range(args.warmup):
         step()
