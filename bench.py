@@ -4,7 +4,10 @@
 
 A step is one forward + backward of one ASRN layer (asrn.ASRNLayer, group-A protections) over one batch of
 synthetic tokens: BASELINE.json configs[1] = cfg2, B 8, N 4096, d 256, V 256, fp32, 30% copied spans. Inputs and
-weights are resident in HBM before the timed region. Prints one JSON line with the driver's keys plus:
+weights are resident in HBM before the timed region. The step is captured once into a HIP graph and the timed steps
+are its replays (the same kernels, launched without the host's per-op overhead); --eager times Python-launched steps
+instead. The per-kernel device events (roofline, hip_aggregate, kernels) come from an eager pass of the same number of
+steps, since events recorded while capturing are not replayed. Prints one JSON line with the driver's keys plus:
   roofline      the dominant HIP kernel: algorithmic bytes per launch / its mean launch time (device events recorded
                 on the stream it runs on), against MI355X's 8 TB/s
   hip_aggregate the headline: 7,776 B/token x tokens / (8 TB/s x the sum of the HIP kernels' time per step)
@@ -155,6 +158,7 @@ def main():
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-decode', action='store_true')
     ap.add_argument('--decode-steps', type=int, default=32)
+    ap.add_argument('--eager', action='store_true', help='time Python-launched steps instead of HIP graph replays')
     ap.add_argument('--copy-calibration', type=int, default=0, metavar='BYTES',
                     help='only run a plain device-to-device copy of BYTES, 3 times: the reference point that scales '
                          'the FETCH_SIZE / WRITE_SIZE counters of a profiler run into bytes')
@@ -193,19 +197,22 @@ def main():
     bf16 = args.config == 'cfg3'           # configs[2]: bf16 activations, fp32 scan state (autocast)
     dtype = 'bf16' if bf16 else 'fp32'
 
+    def fwd_bwd():
+        with torch.autocast('cuda', dtype=torch.bfloat16, enabled=bf16):
+            y = layer(Ed, hd, xd)
+        y.backward(gyd.to(y.dtype))                     # the gradient of sum(y * gy)
+
     def step():
         layer.zero_grad(set_to_none=True)
         Ed.grad = None
         hd.grad = None
-        with torch.autocast('cuda', dtype=torch.bfloat16, enabled=bf16):
-            y = layer(Ed, hd, xd)
-        y.backward(gyd.to(y.dtype))                     # the gradient of sum(y * gy)
+        fwd_bwd()
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
 
-    # HIP-event timing of every library entry point over the timed region
+    # eager pass with HIP-event timing of every library entry point (on the stream each one launches on)
     names = [n for n in _lib.SIGNATURES if n not in ('asrn_hip_last_error', 'asrn_hip_abi_version')
              and not n.endswith('_workspace')]
     timed = _lib.time_calls(names)
@@ -216,6 +223,32 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     timed = _lib.stop_timing()
+    eager_wall = (t1 - t0) / args.steps
+
+    graph = None
+    if not args.eager:
+        # capture one step; the gradients are written into the graph's buffers on every replay
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        layer.zero_grad(set_to_none=True)
+        Ed.grad = None
+        hd.grad = None
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fwd_bwd()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
 
     per_call = {}
     for n, evs in timed.items():
@@ -239,7 +272,9 @@ def main():
         'vs_baseline': None, 'dtype': dtype, 'data': f'synthetic (seeded tokens, {int(cfg["frac"] * 100)}% copied '
         'spans; random-init layer moved off its neutral values)',
         'config': {'workload': f'{args.config}: one ASRN layer fwd+bwd, B={B}, N={N}, d={d}, V={V}, T=8 tables x 14 '
-                               f'bits, C=32, {dtype}', 'global_batch': B, 'seq_len': N, 'parallelism': 'none (1 GPU)'},
+                               f'bits, C=32, {dtype}', 'global_batch': B, 'seq_len': N, 'parallelism': 'none (1 GPU)',
+                   'launch': 'eager' if graph is None else 'hip graph replay'},
+        'eager_ms_per_step': round(eager_wall * 1e3, 4),
         'roofline': {'bound': 'hbm', 'kernel': dom, 'achieved': round(achieved / 1e9, 1), 'peak': HBM_PEAK / 1e9,
                      'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK, 4), 'traffic': measured_traffic(dom) if args.config == 'cfg2' else None,
                      'bytes_per_token': algo[dom], 'mean_launch_us': round(dom_us, 2)},
