@@ -9,6 +9,7 @@ import torch
 
 from . import _lib
 from ._lib import call, ptr, query, stream_of
+from .lineal import column_sums
 
 I32 = torch.int32
 
@@ -332,7 +333,7 @@ class Candidates(torch.autograd.Function):
         call('asrn_candidates_bwd', ptr(phi), ptr(V), ptr(Qc), ptr(Kc), ptr(sig), ptr(Bt), ptr(la), ptr(w), ptr(g),
              ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ptr(dsal), ptr(ent),
              ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(partials), stream_of(dev))
-        part = partials.sum(0)
+        part = column_sums(partials)          # per-query partials summed over the tokens (no memset-cleared reduction)
         dgamma = part[:T] / C
         dw = part[T:]
         return (dphi[..., :P0].to(tp), dV.to(tv), dQc[..., :cf0].to(tq), dKc[..., :cf0].to(tk), dBt, dla.to(tl), dw,

@@ -10,7 +10,7 @@ instead. The per-kernel device events (roofline, hip_aggregate, kernels) come fr
 steps, since events recorded while capturing are not replayed. Prints one JSON line with the driver's keys plus:
   roofline      the dominant HIP kernel: algorithmic bytes per launch / its mean launch time (device events recorded
                 on the stream it runs on), against MI355X's 8 TB/s
-  hip_aggregate the headline: 7,776 B/token x tokens / (8 TB/s x the sum of the HIP kernels' time per step)
+  hip_aggregate all HIP kernels: 16,100 B/token (cfg2) x tokens / (8 TB/s x their summed time per step)
   layer         whole-layer tokens/s and its HBM fraction at 25,876 B/token (the fp32 GEMMs stay PyTorch)
   decode        the O(1) generation step of one layer (BASELINE.json configs[4] at one layer): per-token latency
                 against the context, 1K to 64K, and its slope
@@ -40,9 +40,23 @@ def algorithmic_bytes(d, P, cf, T, a=4):
     return {'asrn_candidates_fwd': fwd, 'asrn_candidates_bwd': bwd}
 
 
-# all HIP kernels of one fwd+bwd at cfg2, each distinct tensor read once and written once: hash + bucket sort 512,
-# clock 16 + 16, n-gram sort 28, Hawkes/streak scans 60 + 100, candidates 2,724 + 4,320 (fwd + bwd)
-HIP_BYTES_PER_TOKEN = {'fp32': 7776, 'bf16': 6688}    # bf16: the activation tensors at 2 bytes
+def gate_bytes(d, n, a=4):
+    """The fused gate (asrn_gate_fwd/bwd): h, A (W_o salida, a bytes), signals, seen flags, Hawkes, streak, logit in;
+    h' out; the backward also reads dh' and writes dh, dA, dHawkes, dstreak."""
+    small = 16 + 8 * n + 4 + 4
+    fwd = 4 * d + a * d + small + 4 * d
+    bwd = 4 * d + 4 * d + a * d + small + 4 * d + a * d + 4 * n + 4
+    return fwd, bwd
+
+
+def hip_bytes_per_token(d, P, cf, T, n=4, a=4):
+    """All HIP kernels of one fwd+bwd, each distinct tensor read once and written once: hash + bucket sort (phi in, ids
+    and order out), clock 16 + 16, n-gram sort 28, Hawkes/streak scans 60 + 100, candidates, gate. cfg2 fp32:
+    512 + 32 + 28 + 160 + 7,044 + 8,324 = 16,100."""
+    cand = algorithmic_bytes(d, P, cf, T, a)
+    return P * a + 8 * T + 32 + 28 + 160 + sum(cand.values()) + sum(gate_bytes(d, n, a))
+
+
 # whole layer: the above plus the GEMM-boundary tensors and their gradients (cfg2 fp32; cfg3 bf16)
 LAYER_BYTES_PER_TOKEN = {'fp32': 25876, 'bf16': 24436}
 
@@ -265,6 +279,7 @@ def main():
     dom_us = per_call[dom]['mean_us']
     achieved = algo[dom] * tokens / (dom_us * 1e-6)
     hip_ms_per_step = sum(v['total_ms'] for v in per_call.values()) / args.steps
+    hip_b = hip_bytes_per_token(d, P, cf, T, layer.vistos, a=2 if bf16 else 4)
 
     out = {
         'metric': METRIC, 'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps,
@@ -278,8 +293,8 @@ def main():
         'roofline': {'bound': 'hbm', 'kernel': dom, 'achieved': round(achieved / 1e9, 1), 'peak': HBM_PEAK / 1e9,
                      'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK, 4), 'traffic': measured_traffic(dom) if args.config == 'cfg2' else None,
                      'bytes_per_token': algo[dom], 'mean_launch_us': round(dom_us, 2)},
-        'hip_aggregate': {'bytes_per_token': HIP_BYTES_PER_TOKEN[dtype], 'hip_ms_per_step': round(hip_ms_per_step, 4),
-                          'frac': round(HIP_BYTES_PER_TOKEN[dtype] * tokens / (HBM_PEAK * hip_ms_per_step * 1e-3), 4)},
+        'hip_aggregate': {'bytes_per_token': hip_b, 'hip_ms_per_step': round(hip_ms_per_step, 4),
+                          'frac': round(hip_b * tokens / (HBM_PEAK * hip_ms_per_step * 1e-3), 4)},
         'layer': {'tokens_per_s': round(value, 1),
                   'hbm_frac': round(LAYER_BYTES_PER_TOKEN[dtype] * tokens / (HBM_PEAK * wall), 4)},
         'kernels': {n: {k: round(v, 3) if isinstance(v, float) else v for k, v in s.items()}
