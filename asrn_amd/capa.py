@@ -137,22 +137,17 @@ class CapaASRNEstable(nn.Module):
         return phi, F.pad(v, (0, 0, 0, 1))[:, 1:]
 
     def _contexto(self, h):
-        """Qc, Kc (B, L, cf), beta (B, L) fp64 and log_alfa (B, L) (the GPU branch of asrn/estable.py:171-175: the
-        clock projection in true fp32, elementwise, immune to reduced-precision matmuls)."""
+        """Qc, Kc (B, L, cf), beta (B, L) fp64 and log_alfa (B, L) (asrn/estable.py:153-194 with the GPU branch's clock
+        projection in true fp32, estable:171-175): LayerNorm, the clock projection and its softplus / logsigmoid /
+        clamps fused in asrn_context_fwd/bwd; Qc, Kc on hipBLASLt."""
         p = self.protecciones
-        hh32 = self.ln_ctx(h)
-        hh = _a_autocast(hh32)
+        meta = (float(self.ln_ctx.eps), -1.0 if p.beta_max is None else float(p.beta_max),
+                -math.inf if p.log_alfa_min is None else float(p.log_alfa_min))
+        hh32, beta, log_alfa = ops.Context.apply(h, self.ln_ctx.weight, self.ln_ctx.bias, self.w_reloj, self.b_reloj,
+                                                 meta)
         cf = self.confirmar
-        y = lineal(hh, torch.cat([self.cq.weight, self.ck.weight]))
-        with torch.autocast(device_type=h.device.type, enabled=False):
-            u = lineal(hh32.float(), self.w_reloj.float(), self.b_reloj.float())
-        beta = F.softplus(u[..., 0])
-        log_alfa = F.logsigmoid(u[..., 1]) + math.log(2)
-        if p.beta_max is not None:
-            beta = beta.clamp(max=p.beta_max)
-        if p.log_alfa_min is not None:
-            log_alfa = log_alfa.clamp(min=p.log_alfa_min)
-        return y[..., :cf], y[..., cf:2 * cf], beta.double(), log_alfa
+        y = lineal(_a_autocast(hh32), torch.cat([self.cq.weight, self.ck.weight]))
+        return y[..., :cf], y[..., cf:2 * cf], beta, log_alfa
 
     def _kappas(self):
         k, kr = self.log_kappa.exp(), self.log_kappa_racha.exp()

@@ -89,6 +89,55 @@ def ngram_sort(sig, coef, n):
 
 
 # ---------------------------------------------------------------------------------------------------------------------
+# a0 (the context producer's LayerNorm and clock projection)
+# ---------------------------------------------------------------------------------------------------------------------
+
+class Context(torch.autograd.Function):
+    """hh = LayerNorm(h), beta = min(softplus(u_0), beta_max) fp64, log_alfa = max(logsigmoid(u_1) + log 2, min) with
+    u = w_reloj hh + b_reloj in fp32 (asrn/estable.py:153-194), fused in asrn_context_fwd/bwd. hh feeds the Qc/Kc GEMM.
+    meta = (eps, beta_max or -1, log_alfa_min or -inf)."""
+
+    @staticmethod
+    def forward(ctx, h, ln_w, ln_b, w_reloj, b_reloj, meta):
+        eps, beta_max, la_min = meta
+        dev = _dev(h)
+        d = h.shape[-1]
+        lead = h.shape[:-1]
+        h32 = _c(h, torch.float32).reshape(-1, d)
+        BL = h32.shape[0]
+        params = [_c(p, torch.float32) for p in (ln_w, ln_b, w_reloj, b_reloj)]
+        hh = torch.empty_like(h32)
+        stats = torch.empty((BL, 4), dtype=torch.float32, device=dev)
+        beta = torch.empty((BL,), dtype=torch.float64, device=dev)
+        la = torch.empty((BL,), dtype=torch.float32, device=dev)
+        call('asrn_context_fwd', ptr(h32), *[ptr(p) for p in params], BL, d, eps, beta_max, la_min, ptr(hh),
+             ptr(stats), ptr(beta), ptr(la), stream_of(dev))
+        ctx.save_for_backward(h32, *params[:3], stats)
+        ctx.meta = (beta_max, la_min, h.dtype, lead, [p.shape for p in (ln_w, ln_b, w_reloj, b_reloj)])
+        return hh.view(*lead, d), beta.view(lead), la.view(lead)
+
+    @staticmethod
+    def backward(ctx, dhh, dbeta, dla):
+        h32, lnw, lnb, wr, stats = ctx.saved_tensors
+        beta_max, la_min, hdt, lead, shapes = ctx.meta
+        BL, d = h32.shape
+        dev = h32.device
+        dhh = torch.zeros_like(h32) if dhh is None else _c(dhh, torch.float32).reshape(BL, d)
+        dbeta = (torch.zeros((BL,), dtype=torch.float64, device=dev) if dbeta is None
+                 else _c(dbeta, torch.float64).reshape(BL))
+        dla = torch.zeros((BL,), dtype=torch.float32, device=dev) if dla is None else _c(dla, torch.float32).reshape(BL)
+        dh = torch.empty_like(h32)
+        dp = torch.empty((4 * d + 2,), dtype=torch.float32, device=dev)
+        wsb = query('asrn_context_bwd_workspace', BL, d)
+        ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+        call('asrn_context_bwd', ptr(h32), ptr(lnw), ptr(lnb), ptr(wr), ptr(stats), BL, d, beta_max, la_min,
+             ptr(dhh), ptr(dbeta), ptr(dla), ptr(dh), ptr(dp), ptr(ws), wsb, stream_of(dev))
+        sizes = [d, d, 2 * d, 2]
+        grads = [t.view(s) for t, s in zip(torch.split(dp, sizes), shapes)]
+        return (dh.view(*lead, d).to(hdt), *grads, None)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
 # a9
 # ---------------------------------------------------------------------------------------------------------------------
 

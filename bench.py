@@ -10,7 +10,7 @@ instead. The per-kernel device events (roofline, hip_aggregate, kernels) come fr
 steps, since events recorded while capturing are not replayed. Prints one JSON line with the driver's keys plus:
   roofline      the dominant HIP kernel: algorithmic bytes per launch / its mean launch time (device events recorded
                 on the stream it runs on), against MI355X's 8 TB/s
-  hip_aggregate all HIP kernels: 16,100 B/token (cfg2) x tokens / (8 TB/s x their summed time per step)
+  hip_aggregate all HIP kernels: 21,276 B/token (cfg2) x tokens / (8 TB/s x their summed time per step)
   layer         whole-layer tokens/s and its HBM fraction at 25,876 B/token (the fp32 GEMMs stay PyTorch)
   decode        the O(1) generation step of one layer (BASELINE.json configs[4] at one layer): per-token latency
                 against the context, 1K to 64K, and its slope
@@ -49,12 +49,19 @@ def gate_bytes(d, n, a=4):
     return fwd, bwd
 
 
+def context_bytes(d):
+    """The fused LayerNorm + clock projection (asrn_context_fwd/bwd), fp32: h in, hh, (mean, rstd, u) and beta (fp64),
+    log_alfa out; the backward reads h, dhh, the stats, dbeta, dlog_alfa and writes dh."""
+    return 4 * d + 4 * d + 16 + 8 + 4, 4 * d + 4 * d + 16 + 8 + 4 + 4 * d
+
+
 def hip_bytes_per_token(d, P, cf, T, n=4, a=4):
     """All HIP kernels of one fwd+bwd, each distinct tensor read once and written once: hash + bucket sort (phi in, ids
-    and order out), clock 16 + 16, n-gram sort 28, Hawkes/streak scans 60 + 100, candidates, gate. cfg2 fp32:
-    512 + 32 + 28 + 160 + 7,044 + 8,324 = 16,100."""
+    and order out), clock 16 + 16, n-gram sort 28, Hawkes/streak scans 60 + 100, candidates, gate, context producer.
+    cfg2 fp32: 512 + 32 + 28 + 160 + 7,044 + 8,324 + 5,176 = 21,276."""
     cand = algorithmic_bytes(d, P, cf, T, a)
-    return P * a + 8 * T + 32 + 28 + 160 + sum(cand.values()) + sum(gate_bytes(d, n, a))
+    return (P * a + 8 * T + 32 + 28 + 160 + sum(cand.values()) + sum(gate_bytes(d, n, a))
+            + sum(context_bytes(d)))
 
 
 # whole layer: the above plus the GEMM-boundary tensors and their gradients (cfg2 fp32; cfg3 bf16)

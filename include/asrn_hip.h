@@ -95,6 +95,24 @@ int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const
  * contents need no clearing and are dead after the call. */
 int64_t asrn_scan_workspace(int64_t rows, int64_t N);
 
+/* ---- a0 (part): the context producer's LayerNorm and clock projection (asrn/estable.py:153-194) ----------------
+ * Replaces ln_ctx, the fp32 clock projection and its softplus / logsigmoid / clamps of _contexto. Per token of h
+ * (BL, d) fp32: hh = LayerNorm(h) (biased variance, eps) * ln_w + ln_b (BL, d) fp32 out, the input of the Qc/Kc GEMM;
+ * u_k = hh . w_reloj[k] + b_reloj[k] (w_reloj (2, d)); beta = min(softplus(u_0), beta_max) (BL) fp64 out (beta_max < 0:
+ * no clamp); log_alfa = max(logsigmoid(u_1) + log 2, log_alfa_min) (BL) fp32 out (-inf: no clamp); stats (BL, 4) =
+ * (mean, rstd, u_0, u_1) kept for the backward. d % 4 == 0, d <= 1024.
+ * context_bwd: from dhh (BL, d) (the Qc/Kc GEMM's input gradient), dbeta (BL) fp64 and dlog_alfa (BL) gives dh (BL, d)
+ * (overwritten) and dparams (4 d + 2) = the gradients of [ln_w | ln_b | w_reloj (2 d) | b_reloj (2)], summed over
+ * tokens in a fixed order. workspace: asrn_context_bwd_workspace(BL, d) bytes. */
+int asrn_context_fwd(const float* h, const float* ln_w, const float* ln_b, const float* w_reloj, const float* b_reloj,
+                     int64_t BL, int32_t d, float eps, float beta_max, float log_alfa_min, float* hh, float* stats,
+                     double* beta, float* log_alfa, void* stream);
+int64_t asrn_context_bwd_workspace(int64_t BL, int32_t d);
+int asrn_context_bwd(const float* h, const float* ln_w, const float* ln_b, const float* w_reloj, const float* stats,
+                     int64_t BL, int32_t d, float beta_max, float log_alfa_min, const float* dhh, const double* dbeta,
+                     const float* dlog_alfa, float* dh, float* dparams, void* workspace, int64_t workspace_bytes,
+                     void* stream);
+
 /* ---- a9: clock --------------------------------------------------------------------------------------------------
  * Bt = cumsum(beta) over L in fp64 (asrn/estable.py:418). reverse != 0 computes the suffix sums instead (the
  * backward of the cumsum). workspace: asrn_scan_workspace(B, L) bytes. */

@@ -379,6 +379,56 @@ def test_candidates_cfg2_full_size():
 
 
 # ---------------------------------------------------------------------------------------------------------------------
+# a0: the context producer
+# ---------------------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize('case', ['plain', 'clamped', 'bf16'])
+def test_context_vs_oracle(case):
+    """LayerNorm + Qc/Kc + the fp32 clock projection with softplus / logsigmoid and the group-A clamps (the fused
+    asrn_context_fwd/bwd and the Qc/Kc GEMM) against the oracle's context: outputs and the gradients of h and every
+    parameter. 'clamped' drives some tokens past beta_max and below log_alfa_min; 'bf16' runs under bf16 autocast
+    (the Qc/Kc GEMM in bf16, the clock in fp32), within the bf16 tolerance."""
+    say('context', case)
+    B, L, d, cf = 2, 777, 96, 16
+    g = torch.Generator().manual_seed(11)
+    sh = O.Shape(d=d, cf=cf)
+    prot = O.Prot()
+    p = {'ln_ctx.weight': 1 + 0.1 * torch.randn(d, generator=g), 'ln_ctx.bias': 0.1 * torch.randn(d, generator=g),
+         'cq.weight': 0.1 * torch.randn(cf, d, generator=g), 'ck.weight': 0.1 * torch.randn(cf, d, generator=g),
+         'w_reloj': 0.3 * torch.randn(2, d, generator=g), 'b_reloj': torch.tensor([0.5, -0.2])}
+    h = torch.randn(B, L, d, generator=g) * 2 + 0.5
+    if case == 'clamped':                 # large |u|: softplus past 1e4 and logsigmoid below -30 on some tokens
+        p['w_reloj'] = p['w_reloj'] * 4000
+    gQ, gK = torch.randn(B, L, cf, generator=g), torch.randn(B, L, cf, generator=g)
+    gb, gl = torch.randn(B, L, generator=g, dtype=torch.float64), torch.randn(B, L, generator=g)
+    hr = h.clone().requires_grad_()
+    pr = {k: v.clone().requires_grad_() for k, v in p.items()}
+    Qr, Kr, br, lr = O.context(pr, hr, sh, prot)
+    ((Qr * gQ).sum() + (Kr * gK).sum() + (br * gb).sum() + (lr * gl).sum()).backward()
+    if case == 'clamped':
+        assert (br == prot.beta_max).any() and (lr == prot.log_alfa_min).any()
+    layer = CapaASRNEstable(d, confirmar=cf).to(DEV)
+    with torch.no_grad():
+        for k, v in p.items():
+            dict(layer.named_parameters())[k].copy_(v)
+    hd = h.to(DEV).requires_grad_()
+    with torch.autocast('cuda', dtype=torch.bfloat16, enabled=case == 'bf16'):
+        Q, K, be, la = layer._contexto(hd)
+    assert be.dtype == torch.float64 and la.dtype == torch.float32
+    ((Q.float() * gQ.to(DEV)).sum() + (K.float() * gK.to(DEV)).sum() + (be * gb.to(DEV)).sum()
+     + (la * gl.to(DEV)).sum()).backward()
+    tol = 2e-2 if case == 'bf16' else TOL
+    assert_close(Q, Qr, 'Qc', tol)
+    assert_close(K, Kr, 'Kc', tol)
+    assert_close(be, br, 'beta', TOL)                  # the clock stays fp32 under autocast
+    assert_close(la, lr, 'log_alfa', TOL)
+    assert_close(hd.grad, hr.grad, 'grad h', tol)
+    named = dict(layer.named_parameters())
+    for k in p:
+        assert_close(named[k].grad, pr[k].grad, 'grad ' + k, tol)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
 # a13: the gate
 # ---------------------------------------------------------------------------------------------------------------------
 
