@@ -124,17 +124,21 @@ class CapaASRNEstable(nn.Module):
         return torch.cat([self.afin_palabra(E), self.afin_contexto(llave)], dim=-1)
 
     def _phi_y_valores(self, E):
+        """phi (B, L, P) and v (B, L, d) = W_v E at every position (asrn/nucleo.py:644-659; the layer's V[t] is v[t+1],
+        which the candidate kernels read in place). One GEMM over E gives the word MLP's first layer, v, and the
+        context MLP's first layer split by linearity: W [E_t; E_{t-1}] = W_a E_t + W_b E_{t-1}, so the key
+        [E_t; E_{t-1}] is never materialized (its second half is the W_b product shifted one position)."""
         d, L = E.shape[-1], E.shape[1]
-        pal = self.afin_palabra
-        m = pal[0].out_features
+        pal, ctx = self.afin_palabra, self.afin_contexto
+        m, mc = pal[0].out_features, ctx[0].out_features
         E = _a_autocast(E)
-        y = lineal(E, torch.cat([pal[0].weight, self.v.weight]), F.pad(pal[0].bias, (0, d)))
-        hp, v = y.split([m, d], dim=-1)
-        llave = torch.cat([E, F.pad(E, (0, 0, 1, 0))[:, :L]], dim=-1)
-        ctx = self.afin_contexto
+        W = torch.cat([pal[0].weight, self.v.weight, ctx[0].weight[:, :d], ctx[0].weight[:, d:]])
+        y = lineal(E, W, F.pad(pal[0].bias, (0, d + 2 * mc)))
+        hp, v, za, zb = y.split([m, d, mc, mc], dim=-1)
+        pre = za + F.pad(zb, (0, 0, 1, 0))[:, :L] + ctx[0].bias
         phi = torch.cat([lineal(pal[1](hp), pal[2].weight, pal[2].bias),
-                         lineal(ctx[1](lineal(llave, ctx[0].weight, ctx[0].bias)), ctx[2].weight, ctx[2].bias)], dim=-1)
-        return phi, F.pad(v, (0, 0, 0, 1))[:, 1:]
+                         lineal(ctx[1](pre), ctx[2].weight, ctx[2].bias)], dim=-1)
+        return phi, v
 
     def _contexto(self, h):
         """Qc, Kc (B, L, cf), beta (B, L) fp64 and log_alfa (B, L) (asrn/estable.py:153-194 with the GPU branch's clock
@@ -159,12 +163,12 @@ class CapaASRNEstable(nn.Module):
     def _acumular(self, E, Qc, Kc, Bt, log_alfa, sig, partes=None):
         """Candidate attention of all tables -> salida and the gate signals (asrn/estable.py:204-300)."""
         T = self.n_tablas
-        phi, V = self._phi_y_valores(E)
+        phi, v = self._phi_y_valores(E)
         if partes is not None:
-            partes.update(phi=phi, V=V)
+            partes.update(phi=phi, V=F.pad(v, (0, 0, 0, 1))[:, 1:])         # V[t] = W_v E[t+1], 0 at the end
         _, order, _, rank, win = ops.bucket_sort(phi.detach(), T, self.n_bits, self.chunk)
-        shape = dict(T=T, Tc=self.tablas_contexto, C=self.chunk, K=self.sufijo)
-        salida, sen = ops.Candidates.apply(phi, V, Qc, Kc, Bt, log_alfa, self.w_sufijo, self.gamma, sig, order,
+        shape = dict(T=T, Tc=self.tablas_contexto, C=self.chunk, K=self.sufijo, v_shift=1)
+        salida, sen = ops.Candidates.apply(phi, v, Qc, Kc, Bt, log_alfa, self.w_sufijo, self.gamma, sig, order,
                                            win, rank, shape)
         return {'salida': salida, 'senales': sen}
 

@@ -29,6 +29,9 @@ constexpr int kRows = 8;             // rows per half-wave in flight in the feat
 
 struct Cand {
   const float* phi; const float* V; const float* Qc; const float* Kc; const float* sig;
+  // V rows: position p of batch row b at V + (b * L + p + vshift) * ldv (vshift 1: the layer's V[p] = W_v E[p + 1] read
+  // straight from the projection of every position; the backward then writes dV at p + 1, and zeros at 0)
+  int64_t ldv; int vshift;
   const double* Bt; const float* la; const float* w_suf; const float* gamma;
   const int32_t* order; const int32_t* win; const int32_t* rank;
   int64_t B, L;
@@ -420,9 +423,9 @@ __device__ __forceinline__ void unique_feature_sum(const Cand& a, int64_t b, int
 // <fixed, row_u> over the d columns for every unique (rows of batch row `rows`), R rows in flight, written to
 // out[u]; the key side (w_u != nullptr) also accumulates dV += w_u row_u from the same loads.
 template <int DCH>
-__device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows, int64_t self_pos, int NU,
-                                                const float4 (&fixed)[DCH], const float* w_u, float4 (&dv)[DCH],
-                                                Scratch& S, float* out) {
+__device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows, int64_t ld, int64_t self_pos,
+                                                int NU, const float4 (&fixed)[DCH], const float* w_u,
+                                                float4 (&dv)[DCH], Scratch& S, float* out) {
   const int lane = lane_id();
   constexpr int R = DCH >= 3 ? 2 : (DCH == 2 ? 4 : 8);
   for (int u0 = 0; u0 < NU; u0 += R) {
@@ -437,7 +440,7 @@ __device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows
 #pragma unroll
       for (int ch = 0; ch < DCH; ++ch) {
         const int dd = ch * 256 + lane * 4;
-        o[r][ch] = ld4(rows + ((uint32_t)row * (uint32_t)a.d + (uint32_t)(dd < a.d ? dd : a.d - 4)));
+        o[r][ch] = ld4(rows + ((uint32_t)row * (uint32_t)ld + (uint32_t)(dd < a.d ? dd : a.d - 4)));
       }
     }
 #pragma unroll
@@ -566,19 +569,19 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
   float4 acc[DCH];
 #pragma unroll
   for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
-  const float* Vb = a.V + b * a.L * a.d;
+  const float* Vb = a.V + (b * a.L + a.vshift) * a.ldv;
   for (int u0 = 0; u0 < NU; u0 += UNR) {
     float4 v[UNR][DCH];
     float w[UNR];
 #pragma unroll
     for (int r = 0; r < UNR; ++r) {
       const bool ok = u0 + r < NU;
-      const int64_t p = ok ? S.upos[u0 + r] : t;
+      const int64_t p = ok ? S.upos[u0 + r] : 0;   // idle lanes read position 0 (always a V row, weight 0)
       w[r] = ok ? S.uc[u0 + r] : 0.f;
 #pragma unroll
       for (int ch = 0; ch < DCH; ++ch) {
         const int dd = ch * 256 + lane * 4;
-        v[r][ch] = ld4(Vb + ((uint32_t)p * (uint32_t)a.d + (uint32_t)(dd < a.d ? dd : a.d - 4)));
+        v[r][ch] = ld4(Vb + ((uint32_t)p * (uint32_t)a.ldv + (uint32_t)(dd < a.d ? dd : a.d - 4)));
       }
     }
 #pragma unroll
@@ -662,7 +665,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
     dO[ch] = dd < a.d ? ld4(a.dsal + tok * a.d + dd) : zero4();
     unused[ch] = zero4();
   }
-  unique_row_dots<DCH>(a, a.V + b * a.L * a.d, t, NU, dO, nullptr, unused, S, S.uc);
+  unique_row_dots<DCH>(a, a.V + (b * a.L + a.vshift) * a.ldv, a.ldv, 0, NU, dO, nullptr, unused, S, S.uc);
 
   // per entry: att from the forward and att * dp (S.ua is a per-entry buffer here)
   float* erow = a.ent + tok * a.T * a.C * 2;
@@ -830,7 +833,9 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH != 3) ? 5 :
     wave_lds_sync();
   }
 
-  // dV_k = sum_u (sum_tau att) dO_u
+  // dV_k = sum_u (sum_tau att) dO_u. With vshift, V[k] is the projection of k + 1: its gradient goes to row k + 1, and
+  // the last position (which no query sees, so dv is 0) clears row 0, the projection no V reads.
+  const int64_t dv_row = a.vshift ? b * a.L + (k + 1 < a.L ? k + 1 : 0) : tok;
   float4 dv[DCH];
   unique_row_sum<DCH>(a, a.dsal + b * a.L * a.d, k, NU, S.uc, S, dv);
   // d phi_k, d Kc_k = sum_u (sum_tau ds) [phi_q * scale_phi ; Qc_q * scale_c]
@@ -839,7 +844,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH != 3) ? 5 :
 #pragma unroll
   for (int ch = 0; ch < DCH; ++ch) {
     const int dd = ch * 256 + lane * 4;
-    if (dd < a.d) *reinterpret_cast<float4*>(a.dV + tok * a.d + dd) = dv[ch];
+    if (dd < a.d) *reinterpret_cast<float4*>(a.dV + dv_row * a.d + dd) = dv[ch];
   }
   if (half == 0) {
     const int x0 = 4 * lane;
@@ -905,6 +910,9 @@ static int check_args(const Cand& a, const char* what) {
                  "(32-bit row offsets)", what, (long long)(a.B * a.L * widest));
   }
   ASRN_REQUIRE(a.K >= 0 && a.K <= 16, "%s: suffix K=%d must be in [0, 16]", what, a.K);
+  ASRN_REQUIRE(a.ldv >= a.d && a.ldv % 4 == 0 && ((uintptr_t)a.V & 15) == 0 && (a.vshift == 0 || a.vshift == 1),
+               "%s: V rows need a stride ldv >= d, a multiple of 4, a 16-byte aligned V and v_shift 0 or 1", what);
+  ASRN_REQUIRE(a.L * a.ldv < (int64_t(1) << 31), "%s: L*ldv must stay below 2^31 (32-bit row offsets)", what);
   return 0;
 }
 
@@ -915,6 +923,7 @@ static Cand make(const float* phi, const float* V, const float* Qc, const float*
   Cand a = {};
   a.phi = phi; a.V = V; a.Qc = Qc; a.Kc = Kc; a.sig = sig; a.Bt = Bt; a.la = la; a.w_suf = w_suf;
   a.gamma = gamma; a.order = order; a.win = win; a.rank = rank;
+  a.ldv = d; a.vshift = 0;
   a.B = B; a.L = L; a.d = d; a.P = P; a.cf = cf; a.K = K; a.T = T; a.Tc = Tc; a.C = C;
   a.sp = sp; a.sc = sc;
   return a;
@@ -977,10 +986,12 @@ extern "C" int asrn_candidates_fwd(const float* phi, const float* V, const float
                                    const float* sig, const double* Bt, const float* log_alfa, const float* w_suf,
                                    const float* gamma, const int32_t* order, const int32_t* win, const int32_t* rank,
                                    int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
-                                   int32_t Tc, int32_t C, float scale_phi, float scale_c, float* salida,
-                                   float* signals, float* entries, void* stream) {
+                                   int32_t Tc, int32_t C, float scale_phi, float scale_c, int64_t ldv,
+                                   int32_t v_shift, float* salida, float* signals, float* entries, void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
                 scale_phi, scale_c);
+  a.ldv = ldv;
+  a.vshift = v_shift;
   if (check_args(a, "asrn_candidates_fwd")) return 1;
   if (B == 0 || L == 0) return 0;
   a.salida = salida; a.signals = signals; a.ent = entries;
@@ -991,11 +1002,14 @@ extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float
                                    const float* sig, const double* Bt, const float* log_alfa, const float* w_suf,
                                    const float* gamma, const int32_t* order, const int32_t* win, const int32_t* rank,
                                    int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
-                                   int32_t Tc, int32_t C, float scale_phi, float scale_c, const float* dsalida,
-                                   float* entries, float* dphi, float* dV, float* dQc, float* dKc, double* dBt,
-                                   float* dlog_alfa, float* partials, void* stream) {
+                                   int32_t Tc, int32_t C, float scale_phi, float scale_c, int64_t ldv,
+                                   int32_t v_shift, const float* dsalida, float* entries, float* dphi, float* dV,
+                                   float* dQc, float* dKc, double* dBt, float* dlog_alfa, float* partials,
+                                   void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
                 scale_phi, scale_c);
+  a.ldv = ldv;
+  a.vshift = v_shift;
   if (check_args(a, "asrn_candidates_bwd")) return 1;
   if (B == 0 || L == 0) return 0;
   a.dsal = dsalida; a.ent = entries; a.dphi = dphi; a.dV = dV; a.dQc = dQc; a.dKc = dKc; a.dBt = dBt;

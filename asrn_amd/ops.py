@@ -27,6 +27,13 @@ def _c(t, dtype=None):
     return t.contiguous()
 
 
+def _rows_in_place(V):
+    """True when V (B, L, d) fp32 can be read in place: unit column stride, rows evenly strided across the batch (a
+    column block of a (B, L, n) tensor), a row stride that keeps float4 loads aligned."""
+    return (V.dtype == torch.float32 and V.dim() == 3 and V.stride(2) == 1 and V.stride(1) % 4 == 0
+            and V.stride(1) >= V.shape[2] and V.stride(0) == V.shape[1] * V.stride(1) and V.data_ptr() % 16 == 0)
+
+
 def _pad4(t):
     """fp32, contiguous, last dimension zero-padded to a multiple of 4."""
     t = _c(t, torch.float32)
@@ -339,7 +346,9 @@ class Candidates(torch.autograd.Function):
     """Candidate attention of all tables (the drop-in for _CasillerosTriton, asrn/nucleo.py:461-515). Returns salida
     (B, L, d) and the gate signals (B, L, 4) = (peso_total, mejor, pico, peso_ctx), the latter without gradient.
     Saves its inputs and the candidates' attention weights (B, L, T, C, 2 with room for ds), so the backward
-    recomputes no score."""
+    recomputes no score. shape['v_shift'] = 1 takes V as the value projection of every position (the kernels read
+    position s + 1 for candidate s, the reference's V[s] = W_v E[s+1]); a column block of a wider fp32 GEMM output is
+    read in place through its row stride."""
 
     @staticmethod
     def forward(ctx, phi, V, Qc, Kc, Bt, log_alfa, w_suf, gamma, sig, order, win, rank, shape):
@@ -350,7 +359,9 @@ class Candidates(torch.autograd.Function):
         sp, sc = float(P0) ** -0.5, float(cf0) ** -0.5
         # the kernels read feature rows as float4: zero columns pad P and cf to multiples of 4 (dot products and the
         # gradients of the real columns are unchanged)
-        ins = dict(phi=_pad4(phi), V=_c(V, torch.float32), Qc=_pad4(Qc), Kc=_pad4(Kc), sig=_c(sig, torch.float32),
+        vs = int(shape.get('v_shift', 0))
+        Vk = V if _rows_in_place(V) else _c(V, torch.float32)
+        ins = dict(phi=_pad4(phi), V=Vk, Qc=_pad4(Qc), Kc=_pad4(Kc), sig=_c(sig, torch.float32),
                    Bt=_c(Bt, torch.float64), la=_c(log_alfa, torch.float32), w=_c(w_suf.detach(), torch.float32),
                    g=_c(gamma.detach(), torch.float32))
         P, cf = ins['phi'].shape[-1], ins['Qc'].shape[-1]
@@ -359,28 +370,28 @@ class Candidates(torch.autograd.Function):
         ent = torch.empty((B, L, T, C, 2), dtype=torch.float32, device=dev)  # only the valid slots are written
         call('asrn_candidates_fwd', ptr(ins['phi']), ptr(ins['V']), ptr(ins['Qc']), ptr(ins['Kc']), ptr(ins['sig']),
              ptr(ins['Bt']), ptr(ins['la']), ptr(ins['w']), ptr(ins['g']), ptr(order), ptr(win), ptr(rank), B, L, d,
-             P, cf, K, T, Tc, C, sp, sc, ptr(salida), ptr(signals), ptr(ent), stream_of(dev))
+             P, cf, K, T, Tc, C, sp, sc, Vk.stride(1), vs, ptr(salida), ptr(signals), ptr(ent), stream_of(dev))
         ctx.save_for_backward(*ins.values(), order, win, rank, ent)
         ctx.meta = (B, L, P, d, cf, K, T, Tc, C, sp, sc, V.dtype, phi.dtype, Qc.dtype, Kc.dtype, log_alfa.dtype,
-                    P0, cf0)
+                    P0, cf0, vs)
         ctx.mark_non_differentiable(signals)
         return salida.to(V.dtype), signals
 
     @staticmethod
     def backward(ctx, dsal, _dsig):
         phi, V, Qc, Kc, sig, Bt, la, w, g, order, win, rank, ent = ctx.saved_tensors
-        B, L, P, d, cf, K, T, Tc, C, sp, sc, tv, tp, tq, tk, tl, P0, cf0 = ctx.meta
+        B, L, P, d, cf, K, T, Tc, C, sp, sc, tv, tp, tq, tk, tl, P0, cf0, vs = ctx.meta
         dev = phi.device
         dsal = _c(dsal, torch.float32)
         dphi = torch.empty_like(phi)
-        dV = torch.empty_like(V)
+        dV = torch.empty((B, L, d), dtype=torch.float32, device=dev)
         dQc = torch.empty_like(Qc)
         dKc = torch.empty_like(Kc)
         dBt = torch.empty_like(Bt)
         dla = torch.empty_like(la)
         partials = torch.empty((B * L, T + K + 1), dtype=torch.float32, device=dev)
         call('asrn_candidates_bwd', ptr(phi), ptr(V), ptr(Qc), ptr(Kc), ptr(sig), ptr(Bt), ptr(la), ptr(w), ptr(g),
-             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ptr(dsal), ptr(ent),
+             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, V.stride(1), vs, ptr(dsal), ptr(ent),
              ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(partials), stream_of(dev))
         part = column_sums(partials)          # per-query partials summed over the tokens (no memset-cleared reduction)
         dgamma = part[:T] / C

@@ -378,6 +378,38 @@ def test_candidates_cfg2_full_size():
         assert_close(grads[k], rg[k], 'grad ' + k)
 
 
+def test_candidates_v_shift_in_place():
+    """v_shift = 1 with v a column block of a wider fp32 tensor (read in place through its row stride) against
+    v_shift = 0 with the reference's shifted, contiguous V[t] = v[t+1]: the same outputs bit for bit, and dv = dV
+    moved one row down with row 0 zero."""
+    say('candidates v_shift')
+    B, L, d, P, cf, T, nb, C = 2, 900, 96, 56, 16, 4, 6, 16
+    g = torch.Generator().manual_seed(21)
+    wide = torch.randn(B, L, 40 + d + 12, generator=g).to(DEV)
+    v = wide[..., 40:40 + d]
+    V = torch.cat([v[:, 1:], torch.zeros_like(v[:, :1])], 1).contiguous()
+    phi = torch.randn(B, L, P, generator=g).to(DEV)
+    Qc, Kc = torch.randn(B, L, cf, generator=g).to(DEV), torch.randn(B, L, cf, generator=g).to(DEV)
+    Bt = (torch.rand(B, L, generator=g, dtype=torch.float64) * 0.1).cumsum(1).to(DEV)
+    la = (torch.randn(B, L, generator=g) * 0.3).to(DEV)
+    sig = torch.randint(0, 7, (B, L), generator=g).float().to(DEV)
+    w, gam = torch.randn(5, generator=g).to(DEV), torch.rand(T, generator=g).to(DEV)
+    _, order, _, rank, win = ops.bucket_sort(phi, T, nb, C)
+    gs = torch.randn(B, L, d, generator=g).to(DEV)
+    outs = []
+    for vv, shift in ((V, 0), (v, 1)):
+        leaf = vv.detach().clone() if shift == 0 else wide.detach().clone().requires_grad_()
+        vin = leaf.requires_grad_() if shift == 0 else leaf[..., 40:40 + d]
+        shape = dict(T=T, Tc=2, C=C, K=4, v_shift=shift)
+        sal, sen = ops.Candidates.apply(phi, vin, Qc, Kc, Bt, la, w, gam, sig, order, win, rank, shape)
+        (sal * gs).sum().backward()
+        outs.append((sal.detach(), sen, leaf.grad if shift == 0 else leaf.grad[..., 40:40 + d]))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    dV, dv = outs[0][2], outs[1][2]
+    assert torch.equal(dv[:, 1:], dV[:, :-1]) and torch.equal(dv[:, 0], torch.zeros_like(dv[:, 0]))
+    assert torch.equal(dV[:, -1], torch.zeros_like(dV[:, -1]))
+
+
 # ---------------------------------------------------------------------------------------------------------------------
 # a0: the context producer
 # ---------------------------------------------------------------------------------------------------------------------
