@@ -136,8 +136,10 @@ class CapaASRNEstable(nn.Module):
         y = lineal(E, W, F.pad(pal[0].bias, (0, d + 2 * mc)))
         hp, v, za, zb = y.split([m, d, mc, mc], dim=-1)
         pre = za + F.pad(zb, (0, 0, 1, 0))[:, :L] + ctx[0].bias
-        phi = torch.cat([lineal(pal[1](hp), pal[2].weight, pal[2].bias),
-                         lineal(ctx[1](pre), ctx[2].weight, ctx[2].bias)], dim=-1)
+        # both second layers as one GEMM with a block-diagonal weight: phi comes out whole
+        w2p, w2c = pal[2].weight, ctx[2].weight
+        W2 = torch.cat([F.pad(w2p, (0, mc)), F.pad(w2c, (m, 0))])
+        phi = lineal(F.gelu(torch.cat([hp, pre], dim=-1)), W2, torch.cat([pal[2].bias, ctx[2].bias]))
         return phi, v
 
     def _contexto(self, h):
