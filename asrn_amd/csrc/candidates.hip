@@ -731,17 +731,16 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   // d phi_q, d Qc_q = sum_u (sum_tau ds) [phi_u ; Kc_u]
   float4 gq[F4];
   unique_feature_sum<F4>(a, b, t, NU, false, S.ud, S, gq);
-  if (half == 0) {
-    const int x0 = 4 * lane;
+  if (half == 0) {   // P and cf are multiples of 4: a lane's 4 features lie in one of the two rows
 #pragma unroll
     for (int c = 0; c < F4; ++c) {
-      const float g[4] = {gq[c].x, gq[c].y, gq[c].z, gq[c].w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int f = x0 + 128 * c + i;
-        if (f < a.P) a.dphi[tok * a.P + f] = g[i] * a.sp;
-        else if (f < a.P + a.cf) a.dQc[tok * a.cf + (f - a.P)] = g[i] * a.sc;
-      }
+      const int f0 = 4 * lane + 128 * c;
+      if (f0 < a.P)
+        *reinterpret_cast<float4*>(a.dphi + tok * a.P + f0) =
+            make_float4(gq[c].x * a.sp, gq[c].y * a.sp, gq[c].z * a.sp, gq[c].w * a.sp);
+      else if (f0 < a.P + a.cf)
+        *reinterpret_cast<float4*>(a.dQc + tok * a.cf + (f0 - a.P)) =
+            make_float4(gq[c].x * a.sc, gq[c].y * a.sc, gq[c].z * a.sc, gq[c].w * a.sc);
     }
   }
   for (int x = 0; x <= a.K && x < 17; ++x) {
@@ -758,7 +757,7 @@ template <int DCH>
 __device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows, int64_t self_pos, int NU,
                                                const float* w_u, const Scratch& S, float4 (&acc)[DCH]) {
   const int lane = lane_id();
-  constexpr int UNR = DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 16);
+  constexpr int UNR = DCH >= 4 ? 3 : (DCH >= 2 ? 6 : 12);   // fits the key pass's 5-waves register budget
 #pragma unroll
   for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
   for (int u0 = 0; u0 < NU; u0 += UNR) {
@@ -794,12 +793,26 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH != 3) ? 5 :
   if (tok >= a.B * a.L) return;
   const int lane = lane_id(), half = lane >> 5;
   const int64_t b = tok / a.L, k = tok % a.L;
+  // the query pass's d phi and dBt of this token, loaded now so their latency hides behind the gathers
+  float4 dphi_q[F4];
+#pragma unroll
+  for (int c = 0; c < F4; ++c) {
+    const int f0 = 4 * lane + 128 * c;
+    dphi_q[c] = half == 0 && f0 < a.P ? ld4(a.dphi + tok * a.P + f0) : zero4();
+  }
+  const double dbt_q = a.dBt[tok];   // wave-uniform
 
   const int M = gather(a, b, k, false, S);
   const int NU = dedupe(a, M, S);
   for (int u = lane; u < NU; u += kWave) {
     S.uc[u] = 0.f;
     S.ud[u] = 0.f;
+  }
+  // park the prefetched d phi in LDS (S.ua is free once the dedupe hash is done) to keep registers for the gathers
+#pragma unroll
+  for (int c = 0; c < F4; ++c) {
+    const int f0 = 4 * lane + 128 * c;
+    if (half == 0 && f0 < a.P) *reinterpret_cast<float4*>(S.ua + f0) = dphi_q[c];
   }
   float att[kCh], ds[kCh];
   int tau[kCh], un[kCh];
@@ -833,37 +846,36 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH != 3) ? 5 :
     wave_lds_sync();
   }
 
-  // dV_k = sum_u (sum_tau att) dO_u. With vshift, V[k] is the projection of k + 1: its gradient goes to row k + 1, and
-  // the last position (which no query sees, so dv is 0) clears row 0, the projection no V reads.
-  const int64_t dv_row = a.vshift ? b * a.L + (k + 1 < a.L ? k + 1 : 0) : tok;
+  // dV_k = sum_u (sum_tau att) dO_u
   float4 dv[DCH];
   unique_row_sum<DCH>(a, a.dsal + b * a.L * a.d, k, NU, S.uc, S, dv);
   // d phi_k, d Kc_k = sum_u (sum_tau ds) [phi_q * scale_phi ; Qc_q * scale_c]
   float4 gk[F4];
   unique_feature_sum<F4>(a, b, k, NU, true, S.ud, S, gk);
+  // with vshift, V[k] is the projection of k + 1: its gradient goes to row k + 1, and the last position (which no
+  // query sees, so dv is 0) clears row 0, the projection no V reads
+  const int64_t dv_row = a.vshift ? b * a.L + (k + 1 < a.L ? k + 1 : 0) : tok;
 #pragma unroll
   for (int ch = 0; ch < DCH; ++ch) {
     const int dd = ch * 256 + lane * 4;
     if (dd < a.d) *reinterpret_cast<float4*>(a.dV + dv_row * a.d + dd) = dv[ch];
   }
-  if (half == 0) {
-    const int x0 = 4 * lane;
+  if (half == 0) {   // P and cf are multiples of 4: a lane's 4 features lie in one of the two rows
 #pragma unroll
     for (int c = 0; c < F4; ++c) {
-      const float g[4] = {gk[c].x, gk[c].y, gk[c].z, gk[c].w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int f = x0 + 128 * c + i;
-        if (f < a.P) a.dphi[tok * a.P + f] += g[i];
-        else if (f < a.P + a.cf) a.dKc[tok * a.cf + (f - a.P)] = g[i];
-      }
+      const int f0 = 4 * lane + 128 * c;
+      if (f0 < a.P)
+        *reinterpret_cast<float4*>(a.dphi + tok * a.P + f0) =
+            make_float4(S.ua[f0] + gk[c].x, S.ua[f0 + 1] + gk[c].y, S.ua[f0 + 2] + gk[c].z, S.ua[f0 + 3] + gk[c].w);
+      else if (f0 < a.P + a.cf)
+        *reinterpret_cast<float4*>(a.dKc + tok * a.cf + (f0 - a.P)) = gk[c];
     }
   }
   const float sla = wave_sum_u(dla);
   const float sbk = wave_sum_u(dbk);
   if (lane == 0) {
     a.dla[tok] = sla;
-    a.dBt[tok] += (double)sbk;
+    a.dBt[tok] = dbt_q + (double)sbk;
   }
 }
 
