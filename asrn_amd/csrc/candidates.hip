@@ -163,6 +163,25 @@ __device__ __forceinline__ float dot_f(const float4 (&q)[F4], const float4 (&k)[
 
 __device__ __forceinline__ float rate_of(const Cand& a, int tau) { return a.gamma[tau] / (float)a.C; }
 
+// Per-table sums over the candidate entries, which are grouped by table (entries [off[tau], off[tau+1]) of table tau):
+// each table gets G = 64 / (T rounded up to a power of two) lanes, which stride through its entries and then add up
+// in a fixed butterfly. Deterministic, and no lane walks a whole table alone. Every lane of table tau's group (lanes
+// tau*G .. tau*G + G - 1) returns its sum.
+__device__ __forceinline__ int lanes_per_table(int T) {
+  int tp = 1;
+  while (tp < T) tp <<= 1;
+  return kWave / tp;
+}
+template <class F>
+__device__ __forceinline__ float table_sum(const Scratch& S, int T, int G, F val) {
+  const int lane = lane_id(), tau = lane / G;
+  float s = 0.f;
+  if (tau < T)
+    for (int m = S.off[tau] + lane % G; m < S.off[tau + 1]; m += G) s += val(m);
+  for (int x = G >> 1; x > 0; x >>= 1) s += __shfl_xor(s, x, kWave);
+  return s;
+}
+
 // Suffix match of `other` against the token itself: the number of leading j < K with sig[other - 1 - j] ==
 // sig[self - 1 - j], both in range; NaN never matches (reference nucleo:98-108, 313-320). The reference's K = 4 keeps
 // the token's own four previous signatures in registers (`mine`, uniform across the wave); K up to 16 reads both sides.
@@ -509,7 +528,7 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
   wave_lds_sync();
 
   // Exact masked softmax of every table at once: the per-table max through an LDS atomic max on order-preserving
-  // integer keys (order-independent), one exp per entry, the per-table sum by one lane per table in entry order.
+  // integer keys (order-independent), one exp per entry, the per-table sums by lane groups (table_sum).
   Entries E;
   load_entries(a, M, S, E);
   uint32_t* tmax = reinterpret_cast<uint32_t*>(S.tsum);
@@ -529,18 +548,19 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
     }
   }
   wave_lds_sync();
+  // one lead lane per table (lane tau * G) carries the table's softmax denominator, max and peak
+  const int G = lanes_per_table(a.T), tg = lane / G;
+  const bool lead = lane % G == 0 && tg < a.T;
+  const float den = table_sum(S, a.T, G, [&](int m) { return S.ua[m]; });
   bool has = false;
   float mx = -INFINITY, inv = 0.f;
-  if (lane < a.T) {
-    const int lo = S.off[lane], hi = S.off[lane + 1];
-    if (lo < hi) {
-      float den = 0.f;
-      for (int m = lo; m < hi; ++m) den += S.ua[m];
+  if (lead) {
+    if (S.off[tg] < S.off[tg + 1]) {
       has = true;
-      mx = from_order_key(tmax[lane]);
+      mx = from_order_key(tmax[tg]);
       inv = 1.f / den;
     }
-    S.tinv[lane] = inv;
+    S.tinv[tg] = inv;
   }
   wave_lds_sync();
   float w[kCh];
@@ -562,7 +582,7 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
   const float pt = wave_sum_u(has ? 1.f : 0.f);
   const float best = wave_max_u(mx);
   const float pico = wave_sum_u(inv);                    // the largest weight of a table is exp(0) / den
-  const float pctx = wave_sum_u(has && lane >= a.T - a.Tc ? 1.f : 0.f);
+  const float pctx = wave_sum_u(has && tg >= a.T - a.Tc ? 1.f : 0.f);
 
   // copy-gather over the distinct candidates: sum_u (sum_tau att) V_u, UNR rows in flight
   constexpr int UNR = DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 16);
@@ -684,10 +704,11 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
     if (in) S.ua[m] = att[c] * dp[c];
   }
   wave_lds_sync();
-  if (lane < a.T) {                                     // D per table, summed in entry order
-    float D = 0.f;
-    for (int m = S.off[lane]; m < S.off[lane + 1]; ++m) D += S.ua[m];
-    S.tsum[lane] = D;
+  const int G = lanes_per_table(a.T), tg = lane / G;
+  const bool lead = lane % G == 0 && tg < a.T;
+  {                                                     // D per table
+    const float D = table_sum(S, a.T, G, [&](int m) { return S.ua[m]; });
+    if (lead) S.tsum[tg] = D;
   }
   wave_lds_sync();
   float ds[kCh];
@@ -711,14 +732,13 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   wave_lds_sync();
   float* part = a.partials + tok * (a.T + a.K + 1);
   float dbq_t = 0.f;
-  if (lane < a.T) {                                     // per table: sum ds (clock) and sum ds * dt (d gamma)
-    float sds = 0.f, sdt = 0.f;
-    for (int m = S.off[lane]; m < S.off[lane + 1]; ++m) {
-      sds += S.ua[m];
-      sdt += S.ua[m] * S.ub[S.uid[m]];
+  {                                                     // per table: sum ds (clock) and sum ds * dt (d gamma)
+    const float sds = table_sum(S, a.T, G, [&](int m) { return S.ua[m]; });
+    const float sdt = table_sum(S, a.T, G, [&](int m) { return S.ua[m] * S.ub[S.uid[m]]; });
+    if (lead) {
+      part[tg] = sdt;
+      dbq_t = -rate_of(a, tg) * sds;
     }
-    part[lane] = sdt;
-    dbq_t = -rate_of(a, lane) * sds;
   }
   // per unique: sum over tables of ds, in table order
   for (int tt = 0; tt < a.T; ++tt) {
@@ -748,7 +768,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
     if (lane == 0) part[a.T + x] = v;
   }
   float dbq = 0.f;
-  for (int tt = 0; tt < a.T; ++tt) dbq += readlane_f(dbq_t, tt);
+  for (int tt = 0; tt < a.T; ++tt) dbq += readlane_f(dbq_t, tt * G);
   if (lane == 0) a.dBt[tok] = (double)dbq;
 }
 
