@@ -21,10 +21,10 @@ SIGNATURES = {
     'asrn_hip_last_error': (ctypes.c_char_p, []),
     'asrn_hip_abi_version': (_I32, []),
     'asrn_bucket_sort': (ctypes.c_int, [_P, _I64, _I64, _I32, _I32, _I64, _I32, _P, _P, _P, _P, _P, _P]),
-    'asrn_candidates_fwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7 + [_F32, _F32, _I64, _I32]
+    'asrn_candidates_fwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7 + [_F32, _F32, _I64, _I32, _I64]
                             + [_P] * 4),
     'asrn_candidate_lists': (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P]),
-    'asrn_candidates_bwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7 + [_F32, _F32, _I64, _I32]
+    'asrn_candidates_bwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7 + [_F32, _F32, _I64, _I32, _I64]
                             + [_P] * 10),
     'asrn_scan_workspace': (_I64, [_I64, _I64]),
     'asrn_clock_scan': (ctypes.c_int, [_P, _P, _I64, _I64, _I32, _P, _I64, _P]),

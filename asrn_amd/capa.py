@@ -16,7 +16,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
-from .lineal import lineal
+from .lineal import column_sums, lineal
 
 PROHIBIDO = -1e9          # the "not allowed" score (asrn/nucleo.py:86)
 
@@ -132,13 +132,13 @@ class CapaASRNEstable(nn.Module):
         pal, ctx = self.afin_palabra, self.afin_contexto
         m, mc = pal[0].out_features, ctx[0].out_features
         E = _a_autocast(E)
-        W = torch.cat([pal[0].weight, self.v.weight, ctx[0].weight[:, :d], ctx[0].weight[:, d:]])
+        wab = ctx[0].weight.view(mc, 2, d).transpose(0, 1).reshape(2 * mc, d)      # [W_a; W_b]
+        W = torch.cat([pal[0].weight, self.v.weight, wab])
         y = lineal(E, W, F.pad(pal[0].bias, (0, d + 2 * mc)))
         hp, v, za, zb = y.split([m, d, mc, mc], dim=-1)
-        pre = za + F.pad(zb, (0, 0, 1, 0))[:, :L] + ctx[0].bias
+        pre = _ShiftAdd.apply(za, zb, ctx[0].bias)
         # both second layers as one GEMM with a block-diagonal weight: phi comes out whole
-        w2p, w2c = pal[2].weight, ctx[2].weight
-        W2 = torch.cat([F.pad(w2p, (0, mc)), F.pad(w2c, (m, 0))])
+        W2 = torch.block_diag(pal[2].weight, ctx[2].weight)
         phi = lineal(F.gelu(torch.cat([hp, pre], dim=-1)), W2, torch.cat([pal[2].bias, ctx[2].bias]))
         return phi, v
 
@@ -153,7 +153,8 @@ class CapaASRNEstable(nn.Module):
                                                  meta)
         cf = self.confirmar
         y = lineal(_a_autocast(hh32), torch.cat([self.cq.weight, self.ck.weight]))
-        return y[..., :cf], y[..., cf:2 * cf], beta, log_alfa
+        Qc, Kc = _Split2.apply(y, cf)
+        return Qc, Kc, beta, log_alfa
 
     def _kappas(self):
         k, kr = self.log_kappa.exp(), self.log_kappa_racha.exp()
@@ -217,6 +218,45 @@ class CapaASRNEstable(nn.Module):
             partes.update(Qc=Qc, Kc=Kc, sig=sig, beta=beta, Bt=Bt, log_alfa=log_alfa, hawkes=acc['hawkes'],
                           racha=acc['racha'])
         return self._combinar(acc, h)
+
+
+class _ShiftAdd(torch.autograd.Function):
+    """out[:, t] = za[:, t] + zb[:, t - 1] + bias (zb's term absent at t = 0): the context MLP's first layer on the key
+    [E_t; E_{t-1}], from the two halves' products. No zero-padded copies in either direction."""
+
+    @staticmethod
+    def forward(ctx, za, zb, bias):
+        out = za + bias
+        out[:, 1:] += zb[:, :-1]
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        dzb = torch.empty_like(g)
+        dzb[:, :-1] = g[:, 1:]
+        dzb[:, -1] = 0
+        return g, dzb, column_sums(g.reshape(-1, g.shape[-1]))
+
+
+class _Split2(torch.autograd.Function):
+    """y[..., :k] and y[..., k:] as views (the candidate kernels read both in place through their row stride). The
+    backward joins the two gradients with one concatenation; slicing's own backward would zero-fill a copy of y per
+    part and add them."""
+
+    @staticmethod
+    def forward(ctx, y, k):
+        ctx.k, ctx.shape, ctx.dtype = k, y.shape, y.dtype
+        return y[..., :k], y[..., k:]
+
+    @staticmethod
+    def backward(ctx, ga, gb):
+        k, n = ctx.k, ctx.shape[-1]
+        ref = ga if ga is not None else gb
+        if ga is None:
+            ga = torch.zeros(ctx.shape[:-1] + (k,), dtype=ref.dtype, device=ref.device)
+        if gb is None:
+            gb = torch.zeros(ctx.shape[:-1] + (n - k,), dtype=ref.dtype, device=ref.device)
+        return torch.cat([ga, gb], dim=-1), None
 
 
 def _a_autocast(x):

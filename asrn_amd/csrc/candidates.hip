@@ -32,6 +32,7 @@ struct Cand {
   // V rows: position p of batch row b at V + (b * L + p + vshift) * ldv (vshift 1: the layer's V[p] = W_v E[p + 1] read
   // straight from the projection of every position; the backward then writes dV at p + 1, and zeros at 0)
   int64_t ldv; int vshift;
+  int64_t ldq;   // row stride of Qc and Kc (cf for dense rows; more when both are column blocks of one projection)
   const double* Bt; const float* la; const float* w_suf; const float* gamma;
   const int32_t* order; const int32_t* win; const int32_t* rank;
   int64_t B, L;
@@ -137,7 +138,7 @@ __device__ __forceinline__ FeatLanes<F4> feat_lanes(const Cand& a, const float* 
     const int x = x0 + 128 * c;
     const bool in_phi = x < a.P, live = x < a.P + a.cf;
     fl.base[c] = in_phi ? a.phi + x : (live ? conf + (x - a.P) : a.phi);
-    fl.stride[c] = in_phi || !live ? (uint32_t)a.P : (uint32_t)a.cf;
+    fl.stride[c] = in_phi || !live ? (uint32_t)a.P : (uint32_t)a.ldq;
     fl.scale[c] = !live ? 0.f : (scaled ? (in_phi ? a.sp : a.sc) : 1.f);
   }
   return fl;
@@ -945,6 +946,9 @@ static int check_args(const Cand& a, const char* what) {
   ASRN_REQUIRE(a.ldv >= a.d && a.ldv % 4 == 0 && ((uintptr_t)a.V & 15) == 0 && (a.vshift == 0 || a.vshift == 1),
                "%s: V rows need a stride ldv >= d, a multiple of 4, a 16-byte aligned V and v_shift 0 or 1", what);
   ASRN_REQUIRE(a.L * a.ldv < (int64_t(1) << 31), "%s: L*ldv must stay below 2^31 (32-bit row offsets)", what);
+  ASRN_REQUIRE(a.ldq >= a.cf && a.ldq % 4 == 0 && ((uintptr_t)a.Qc & 15) == 0 && ((uintptr_t)a.Kc & 15) == 0 &&
+                   a.B * a.L * a.ldq < (int64_t(1) << 31),
+               "%s: Qc/Kc rows need a stride ldq >= cf, a multiple of 4, 16-byte aligned rows, B*L*ldq < 2^31", what);
   return 0;
 }
 
@@ -955,7 +959,7 @@ static Cand make(const float* phi, const float* V, const float* Qc, const float*
   Cand a = {};
   a.phi = phi; a.V = V; a.Qc = Qc; a.Kc = Kc; a.sig = sig; a.Bt = Bt; a.la = la; a.w_suf = w_suf;
   a.gamma = gamma; a.order = order; a.win = win; a.rank = rank;
-  a.ldv = d; a.vshift = 0;
+  a.ldv = d; a.vshift = 0; a.ldq = cf;
   a.B = B; a.L = L; a.d = d; a.P = P; a.cf = cf; a.K = K; a.T = T; a.Tc = Tc; a.C = C;
   a.sp = sp; a.sc = sc;
   return a;
@@ -1019,11 +1023,13 @@ extern "C" int asrn_candidates_fwd(const float* phi, const float* V, const float
                                    const float* gamma, const int32_t* order, const int32_t* win, const int32_t* rank,
                                    int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
                                    int32_t Tc, int32_t C, float scale_phi, float scale_c, int64_t ldv,
-                                   int32_t v_shift, float* salida, float* signals, float* entries, void* stream) {
+                                   int32_t v_shift, int64_t ldq, float* salida, float* signals, float* entries,
+                                   void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
                 scale_phi, scale_c);
   a.ldv = ldv;
   a.vshift = v_shift;
+  a.ldq = ldq;
   if (check_args(a, "asrn_candidates_fwd")) return 1;
   if (B == 0 || L == 0) return 0;
   a.salida = salida; a.signals = signals; a.ent = entries;
@@ -1035,13 +1041,14 @@ extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float
                                    const float* gamma, const int32_t* order, const int32_t* win, const int32_t* rank,
                                    int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
                                    int32_t Tc, int32_t C, float scale_phi, float scale_c, int64_t ldv,
-                                   int32_t v_shift, const float* dsalida, float* entries, float* dphi, float* dV,
-                                   float* dQc, float* dKc, double* dBt, float* dlog_alfa, float* partials,
+                                   int32_t v_shift, int64_t ldq, const float* dsalida, float* entries, float* dphi,
+                                   float* dV, float* dQc, float* dKc, double* dBt, float* dlog_alfa, float* partials,
                                    void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
                 scale_phi, scale_c);
   a.ldv = ldv;
   a.vshift = v_shift;
+  a.ldq = ldq;
   if (check_args(a, "asrn_candidates_bwd")) return 1;
   if (B == 0 || L == 0) return 0;
   a.dsal = dsalida; a.ent = entries; a.dphi = dphi; a.dV = dV; a.dQc = dQc; a.dKc = dKc; a.dBt = dBt;

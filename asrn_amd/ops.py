@@ -361,7 +361,11 @@ class Candidates(torch.autograd.Function):
         # gradients of the real columns are unchanged)
         vs = int(shape.get('v_shift', 0))
         Vk = V if _rows_in_place(V) else _c(V, torch.float32)
-        ins = dict(phi=_pad4(phi), V=Vk, Qc=_pad4(Qc), Kc=_pad4(Kc), sig=_c(sig, torch.float32),
+        if _rows_in_place(Qc) and _rows_in_place(Kc) and Qc.stride(1) == Kc.stride(1) and Qc.shape[-1] % 4 == 0:
+            Qk, Kk = Qc, Kc                        # column blocks of one projection, read through their row stride
+        else:
+            Qk, Kk = _pad4(Qc), _pad4(Kc)
+        ins = dict(phi=_pad4(phi), V=Vk, Qc=Qk, Kc=Kk, sig=_c(sig, torch.float32),
                    Bt=_c(Bt, torch.float64), la=_c(log_alfa, torch.float32), w=_c(w_suf.detach(), torch.float32),
                    g=_c(gamma.detach(), torch.float32))
         P, cf = ins['phi'].shape[-1], ins['Qc'].shape[-1]
@@ -370,7 +374,8 @@ class Candidates(torch.autograd.Function):
         ent = torch.empty((B, L, T, C, 2), dtype=torch.float32, device=dev)  # only the valid slots are written
         call('asrn_candidates_fwd', ptr(ins['phi']), ptr(ins['V']), ptr(ins['Qc']), ptr(ins['Kc']), ptr(ins['sig']),
              ptr(ins['Bt']), ptr(ins['la']), ptr(ins['w']), ptr(ins['g']), ptr(order), ptr(win), ptr(rank), B, L, d,
-             P, cf, K, T, Tc, C, sp, sc, Vk.stride(1), vs, ptr(salida), ptr(signals), ptr(ent), stream_of(dev))
+             P, cf, K, T, Tc, C, sp, sc, Vk.stride(1), vs, Qk.stride(1), ptr(salida), ptr(signals), ptr(ent),
+             stream_of(dev))
         ctx.save_for_backward(*ins.values(), order, win, rank, ent)
         ctx.meta = (B, L, P, d, cf, K, T, Tc, C, sp, sc, V.dtype, phi.dtype, Qc.dtype, Kc.dtype, log_alfa.dtype,
                     P0, cf0, vs)
@@ -385,13 +390,14 @@ class Candidates(torch.autograd.Function):
         dsal = _c(dsal, torch.float32)
         dphi = torch.empty_like(phi)
         dV = torch.empty((B, L, d), dtype=torch.float32, device=dev)
-        dQc = torch.empty_like(Qc)
-        dKc = torch.empty_like(Kc)
+        dQc = torch.empty((B, L, cf), dtype=torch.float32, device=dev)
+        dKc = torch.empty((B, L, cf), dtype=torch.float32, device=dev)
         dBt = torch.empty_like(Bt)
         dla = torch.empty_like(la)
         partials = torch.empty((B * L, T + K + 1), dtype=torch.float32, device=dev)
         call('asrn_candidates_bwd', ptr(phi), ptr(V), ptr(Qc), ptr(Kc), ptr(sig), ptr(Bt), ptr(la), ptr(w), ptr(g),
-             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, V.stride(1), vs, ptr(dsal), ptr(ent),
+             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, V.stride(1), vs, Qc.stride(1),
+             ptr(dsal), ptr(ent),
              ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(partials), stream_of(dev))
         part = column_sums(partials)          # per-query partials summed over the tokens (no memset-cleared reduction)
         dgamma = part[:T] / C

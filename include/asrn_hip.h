@@ -58,12 +58,14 @@ int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t T, int32_t 
  *           aligned). v_shift = 0: V as the reference passes it (V[p] = W_v E[p+1], nucleo:659, the last row 0);
  *           v_shift = 1: V is the projection W_v E of every position (e.g. a column block of a wider GEMM output,
  *           ldv its row stride), and the kernels read the next position's row themselves.
+ *   Qc, Kc rows: row t at Qc + t * ldq (and Kc + t * ldq): ldq = cf for dense rows, or the row stride when both are
+ *           column blocks of one projection (ldq >= cf, a multiple of 4, rows 16-byte aligned).
  * Requires d % 4 == 0, d <= 1024, 1 <= C <= 64, P + cf <= 256, K <= 16, T <= 32, L * ldv < 2^31. */
 int asrn_candidates_fwd(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                         const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
                         const int32_t* order, const int32_t* win, const int32_t* rank, int64_t B, int64_t L,
                         int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
-                        float scale_phi, float scale_c, int64_t ldv, int32_t v_shift, float* salida,
+                        float scale_phi, float scale_c, int64_t ldv, int32_t v_shift, int64_t ldq, float* salida,
                         float* signals, float* entries, void* stream);
 
 /* The candidate lists the forward and backward walk, materialized for checking (a3, a4): for each (b, t, tau) the
@@ -82,16 +84,16 @@ int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* 
  * d w_suf) and a key pass (key-side gradients from att and ds at the slots of the queries that see the key: the
  * next <= C same-bucket sorted ranks).
  *   dsalida (B, L, d); entries from asrn_candidates_fwd (its [..., 1] receives ds, read back by the key pass)
- *   dphi (B, L, P), dV (B, L, d), dQc, dKc (B, L, cf), dBt (B, L) fp64, dlog_alfa (B, L) out (overwritten); dV is
+ *   dphi (B, L, P), dV (B, L, d), dQc, dKc (B, L, cf) dense, dBt (B, L) fp64, dlog_alfa (B, L) out (overwritten); dV is
  *   contiguous and, with v_shift = 1, the gradient of the per-position projection (row 0 of each batch row is 0)
  *   partials (B*L, T + K + 1) fp32 out: per query, d gamma_tau then d w_suf[0..K]; the caller sums over rows. */
 int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                         const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
                         const int32_t* order, const int32_t* win, const int32_t* rank, int64_t B, int64_t L,
                         int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
-                        float scale_phi, float scale_c, int64_t ldv, int32_t v_shift, const float* dsalida,
-                        float* entries, float* dphi, float* dV, float* dQc, float* dKc, double* dBt,
-                        float* dlog_alfa, float* partials, void* stream);
+                        float scale_phi, float scale_c, int64_t ldv, int32_t v_shift, int64_t ldq,
+                        const float* dsalida, float* entries, float* dphi, float* dV, float* dQc, float* dKc,
+                        double* dBt, float* dlog_alfa, float* partials, void* stream);
 
 /* ---- scan workspace -------------------------------------------------------------------------------------------
  * No counterpart in the reference (PyTorch allocates for it). Every scan below cuts its rows into chunks spread over
