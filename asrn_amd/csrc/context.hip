@@ -10,7 +10,7 @@
 //   g = dhh + du_0 w_reloj[0] + du_1 w_reloj[1],  dxhat = g ln_w
 //   dh = rstd (dxhat - mean(dxhat) - xhat mean(dxhat xhat))
 //   d ln_w = sum_t g xhat, d ln_b = sum_t g, d w_reloj[k] = sum_t du_k hh, d b_reloj[k] = sum_t du_k
-// A workgroup takes 32 tokens, each wave 8 of them, loading 4 tokens' rows (float4 per lane) at a time; the parameter
+// A workgroup takes 32 tokens, each wave 8 of them, loading 2 tokens' rows (float4 per lane) at a time; the parameter
 // gradients are per-workgroup partials summed in order by a second launch (deterministic, no atomics).
 #include "common.h"
 
@@ -20,7 +20,7 @@ constexpr int kCtxThreads = 256;
 constexpr int kCtxWaves = kCtxThreads / kWave;
 constexpr int kCtxTok = 32;
 constexpr int kCtxTokPerWave = kCtxTok / kCtxWaves;
-constexpr int kCtxBatch = 4;
+constexpr int kCtxBatch = 2;
 constexpr int kCtxMaxD4 = 4;    // d <= 1024
 
 struct CtxArgs {
