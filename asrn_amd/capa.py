@@ -125,21 +125,26 @@ class CapaASRNEstable(nn.Module):
 
     def _phi_y_valores(self, E):
         """phi (B, L, P) and v (B, L, d) = W_v E at every position (asrn/nucleo.py:644-659; the layer's V[t] is v[t+1],
-        which the candidate kernels read in place). One GEMM over E gives the word MLP's first layer, v, and the
-        context MLP's first layer split by linearity: W [E_t; E_{t-1}] = W_a E_t + W_b E_{t-1}, so the key
-        [E_t; E_{t-1}] is never materialized (its second half is the W_b product shifted one position)."""
-        d, L = E.shape[-1], E.shape[1]
+        which the candidate kernels read in place). One GEMM over E gives the word MLP's first layer, the context
+        MLP's first layer split by linearity (W [E_t; E_{t-1}] = W_a E_t + W_b E_{t-1}: the key [E_t; E_{t-1}] is
+        never materialized) and v. In fp32, the biases, the shift of the W_b product and the GELU are one kernel
+        (ops.Producer); under autocast they are PyTorch ops on the GEMM's output."""
+        d = E.shape[-1]
         pal, ctx = self.afin_palabra, self.afin_contexto
         m, mc = pal[0].out_features, ctx[0].out_features
-        E = _a_autocast(E)
         wab = ctx[0].weight.view(mc, 2, d).transpose(0, 1).reshape(2 * mc, d)      # [W_a; W_b]
-        W = torch.cat([pal[0].weight, self.v.weight, wab])
-        y = lineal(E, W, F.pad(pal[0].bias, (0, d + 2 * mc)))
-        hp, v, za, zb = y.split([m, d, mc, mc], dim=-1)
-        pre = _ShiftAdd.apply(za, zb, ctx[0].bias)
+        if (E.dtype == torch.float32 and not torch.is_autocast_enabled(E.device.type) and m % 4 == 0
+                and mc % 4 == 0 and pal[0].weight.dtype == torch.float32):
+            g, v = ops.Producer.apply(E, torch.cat([pal[0].weight, wab, self.v.weight]), pal[0].bias, ctx[0].bias,
+                                      m, mc)
+        else:
+            y = lineal(_a_autocast(E), torch.cat([pal[0].weight, wab, self.v.weight]),
+                       F.pad(pal[0].bias, (0, 2 * mc + d)))
+            hp, za, zb, v = y.split([m, mc, mc, d], dim=-1)
+            g = F.gelu(torch.cat([hp, _ShiftAdd.apply(za, zb, ctx[0].bias)], dim=-1))
         # both second layers as one GEMM with a block-diagonal weight: phi comes out whole
         W2 = torch.block_diag(pal[2].weight, ctx[2].weight)
-        phi = lineal(F.gelu(torch.cat([hp, pre], dim=-1)), W2, torch.cat([pal[2].bias, ctx[2].bias]))
+        phi = lineal(g, W2, torch.cat([pal[2].bias, ctx[2].bias]))
         return phi, v
 
     def _contexto(self, h):

@@ -30,7 +30,8 @@ constexpr int kRows = 8;             // rows per half-wave in flight in the feat
 struct Cand {
   const float* phi; const float* V; const float* Qc; const float* Kc; const float* sig;
   // V rows: position p of batch row b at V + (b * L + p + vshift) * ldv (vshift 1: the layer's V[p] = W_v E[p + 1] read
-  // straight from the projection of every position; the backward then writes dV at p + 1, and zeros at 0)
+  // straight from the projection of every position; the backward then writes dV at p + 1, and zeros at 0). dV has
+  // V's layout: the same row stride ldv.
   int64_t ldv; int vshift;
   int64_t ldq;   // row stride of Qc and Kc (cf for dense rows; more when both are column blocks of one projection)
   const double* Bt; const float* la; const float* w_suf; const float* gamma;
@@ -879,7 +880,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH != 3) ? 5 :
 #pragma unroll
   for (int ch = 0; ch < DCH; ++ch) {
     const int dd = ch * 256 + lane * 4;
-    if (dd < a.d) *reinterpret_cast<float4*>(a.dV + dv_row * a.d + dd) = dv[ch];
+    if (dd < a.d) *reinterpret_cast<float4*>(a.dV + dv_row * a.ldv + dd) = dv[ch];
   }
   if (half == 0) {   // P and cf are multiples of 4: a lane's 4 features lie in one of the two rows
 #pragma unroll
@@ -1050,6 +1051,7 @@ extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float
   a.vshift = v_shift;
   a.ldq = ldq;
   if (check_args(a, "asrn_candidates_bwd")) return 1;
+  ASRN_REQUIRE(((uintptr_t)dV & 15) == 0, "asrn_candidates_bwd: dV must be 16-byte aligned (rows of stride ldv)");
   if (B == 0 || L == 0) return 0;
   a.dsal = dsalida; a.ent = entries; a.dphi = dphi; a.dV = dV; a.dQc = dQc; a.dKc = dKc; a.dBt = dBt;
   a.dla = dlog_alfa; a.partials = partials;

@@ -6,9 +6,15 @@ shape) into a small (out, in) matrix. As one GEMM it has only (out / tile) x (in
 they took a third of the step. Here the token axis is cut into S slabs: one batched GEMM forms the S partial products
 (S times the tiles) and they are added in fp32, in slab order. The forward and the input gradient are the usual
 GEMMs. Under autocast the operands are cast as autocast casts F.linear's, and the products run in that dtype.
+
+On the GPU, the sums (the slab partials, and the bias gradients' column sums) run in the library's asrn_column_sums
+(fp32 accumulation in a fixed order, no memset-cleared semaphores, safe to capture in a HIP graph). fp64 operands,
+and CPU tensors (the math checked on the CPU), use torch's sums.
 """
 import torch
 import torch.nn.functional as F
+
+from . import _lib
 
 MIN_SLAB = 1024            # tokens per slab: below this the batched GEMM's own overhead dominates
 
@@ -43,30 +49,43 @@ def _acc_dtype(t):
     return torch.float64 if t.dtype == torch.float64 else torch.float32
 
 
+def _hip_sums(x, rows, cols, ld):
+    """fp32 column sums of the (rows, cols) matrix at x (row stride ld) through asrn_column_sums."""
+    out = torch.empty((cols,), dtype=torch.float32, device=x.device)
+    wsb = _lib.query('asrn_column_sums_workspace', rows, cols)
+    ws = torch.empty((wsb,), dtype=torch.uint8, device=x.device) if wsb > 0 else None
+    _lib.call('asrn_column_sums', _lib.ptr(x), int(x.dtype == torch.bfloat16), rows, cols, ld, _lib.ptr(out),
+              _lib.ptr(ws), wsb, _lib.stream_of(x.device))
+    return out
+
+
+def _on_hip(t):
+    return t.is_cuda and t.dtype in (torch.float32, torch.bfloat16)
+
+
+def sum_rows(t):
+    """t (S, ...) summed over its first axis in fp32 (fp64 for fp64), in order."""
+    if _on_hip(t):
+        t = t.contiguous()
+        n = t[0].numel() if t.shape[0] else 0
+        return _hip_sums(t, t.shape[0], n, max(n, 1)).view(t.shape[1:])
+    return t.sum(0, dtype=_acc_dtype(t))
+
+
 def weight_grad(g2, x2):
     """dW = g2^T x2, summed in fp32 (fp64 for fp64 operands): g2 (N, out), x2 (N, in), both with unit last stride."""
     s = slabs_for(g2.shape[0])
     if s == 1:
         return g2.t().mm(x2).to(_acc_dtype(g2))
     # left operand: the transposed slab of g2; right operand: x2's slab as stored (never a transposed view)
-    return torch.bmm(_slab(g2, s).transpose(1, 2), _slab(x2, s)).sum(0, dtype=_acc_dtype(g2))
-
-
-_ONES = {}
+    return sum_rows(torch.bmm(_slab(g2, s).transpose(1, 2), _slab(x2, s)))
 
 
 def column_sums(g2):
-    """Sum over the rows of g2 (N, k), in fp32 (fp64 for fp64): per-slab products with a ones vector on the matrix
-    cores, then the slab sum. (A plain sum over N is a multi-workgroup reduction, whose semaphores are cleared with a
-    memset before every call.)"""
-    s = slabs_for(g2.shape[0])
-    if s == 1:
-        return g2.sum(0, dtype=_acc_dtype(g2))
-    key = (s, g2.shape[0] // s, g2.dtype, g2.device)
-    ones = _ONES.get(key)
-    if ones is None:
-        ones = _ONES[key] = torch.ones((s, 1, key[1]), dtype=g2.dtype, device=g2.device)
-    return torch.bmm(ones, _slab(g2, s)).sum(0, dtype=_acc_dtype(g2)).reshape(-1)
+    """Sum over the rows of g2 (N, k) with unit last stride, in fp32 (fp64 for fp64)."""
+    if _on_hip(g2):
+        return _hip_sums(g2, g2.shape[0], g2.shape[1], max(g2.stride(0), g2.shape[1], 1))
+    return g2.sum(0, dtype=_acc_dtype(g2))
 
 
 class _Lineal(torch.autograd.Function):

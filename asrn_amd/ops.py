@@ -9,7 +9,7 @@ import torch
 
 from . import _lib
 from ._lib import call, ptr, query, stream_of
-from .lineal import column_sums
+from .lineal import column_sums, weight_grad
 
 I32 = torch.int32
 
@@ -142,6 +142,66 @@ class Context(torch.autograd.Function):
         sizes = [d, d, 2 * d, 2]
         grads = [t.view(s) for t, s in zip(torch.split(dp, sizes), shapes)]
         return (dh.view(*lead, d).to(hdt), *grads, None)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# a0 (the hash MLPs' first layers and the value projection)
+# ---------------------------------------------------------------------------------------------------------------------
+
+class Producer(torch.autograd.Function):
+    """y = E W^T by one bias-free GEMM, W's rows [W_p (m) | W_a (mc) | W_b (mc) | W_v (d)]; returns the hash MLPs'
+    hidden units g (B, L, m + mc) = [gelu(W_p E_t + b_word) | gelu(W_a E_t + W_b E_{t-1} + b_ctx)] (asrn_hidden_fwd;
+    asrn/nucleo.py:644-652) and v = W_v E, a column block of y read in place by the candidate kernels.
+
+    Backward: the candidate backward writes dv as the same column block of a (B, L, n) buffer; asrn_hidden_bwd fills
+    the buffer's other columns from dg, and the buffer is dy, with no concatenation. (dv in any other layout is copied
+    into a fresh dy.) dE = dy W, dW by token slabs, and the biases' gradients are the column sums of dy's first m + mc
+    columns. fp32 only."""
+
+    @staticmethod
+    def forward(ctx, E, W, b_word, b_ctx, m, mc):
+        dev = _dev(E, W)
+        B, L, d = E.shape
+        n = W.shape[0]
+        E = _c(E, torch.float32)
+        bw, bc = _c(b_word, torch.float32), _c(b_ctx, torch.float32)
+        y = torch.nn.functional.linear(E, W)
+        g = torch.empty((B, L, m + mc), dtype=torch.float32, device=dev)
+        call('asrn_hidden_fwd', ptr(y), n, ptr(bw), ptr(bc), B, L, m, mc, ptr(g), stream_of(dev))
+        ctx.save_for_backward(E, W, y, bw, bc)
+        ctx.meta = (m, mc)
+        return g, y[..., m + 2 * mc:]
+
+    @staticmethod
+    def backward(ctx, dg, dv):
+        E, W, y, bw, bc = ctx.saved_tensors
+        m, mc = ctx.meta
+        B, L, n = y.shape
+        d0 = m + 2 * mc
+        dev = y.device
+        dy = None
+        if (dv is not None and dv.dtype == torch.float32 and dv.stride() == (L * n, n, 1)
+                and dv.storage_offset() >= d0
+                and dv.untyped_storage().nbytes() >= 4 * (dv.storage_offset() - d0 + B * L * n)):
+            dy = dv.as_strided((B, L, n), (L * n, n, 1), dv.storage_offset() - d0)   # the buffer dv lives in
+        if dy is None:
+            dy = torch.empty((B, L, n), dtype=torch.float32, device=dev)
+            if dv is None:
+                dy[..., d0:].zero_()
+            else:
+                dy[..., d0:].copy_(dv)
+        dg = torch.zeros((B, L, m + mc), dtype=torch.float32, device=dev) if dg is None else _c(dg, torch.float32)
+        call('asrn_hidden_bwd', ptr(y), n, ptr(bw), ptr(bc), B, L, m, mc, ptr(dg), ptr(dy), n, stream_of(dev))
+        dy2 = dy.view(B * L, n)
+        dE = dW = dbw = dbc = None
+        if ctx.needs_input_grad[0]:
+            dE = dy2.mm(W).view(B, L, -1)
+        if ctx.needs_input_grad[1]:
+            dW = weight_grad(dy2, E.view(B * L, -1))
+        if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:
+            db = column_sums(dy2[:, :m + mc])
+            dbw, dbc = db[:m], db[m:]
+        return dE, dW, dbw, dbc, None, None
 
 
 # ---------------------------------------------------------------------------------------------------------------------
@@ -389,14 +449,19 @@ class Candidates(torch.autograd.Function):
         dev = phi.device
         dsal = _c(dsal, torch.float32)
         dphi = torch.empty_like(phi)
-        dV = torch.empty((B, L, d), dtype=torch.float32, device=dev)
+        # dV takes V's layout: when V is a column block read in place, the same block of a (B, L, ldv) buffer, so the
+        # producer whose output V is can take the buffer as its own output gradient without a copy
+        ldv = V.stride(1)
+        col = V.storage_offset() % ldv
+        col = col if col + d <= ldv else 0
+        dV = torch.empty((B, L, ldv), dtype=torch.float32, device=dev)[..., col:col + d]
         dQc = torch.empty((B, L, cf), dtype=torch.float32, device=dev)
         dKc = torch.empty((B, L, cf), dtype=torch.float32, device=dev)
         dBt = torch.empty_like(Bt)
         dla = torch.empty_like(la)
         partials = torch.empty((B * L, T + K + 1), dtype=torch.float32, device=dev)
         call('asrn_candidates_bwd', ptr(phi), ptr(V), ptr(Qc), ptr(Kc), ptr(sig), ptr(Bt), ptr(la), ptr(w), ptr(g),
-             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, V.stride(1), vs, Qc.stride(1),
+             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ldv, vs, Qc.stride(1),
              ptr(dsal), ptr(ent),
              ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(partials), stream_of(dev))
         part = column_sums(partials)          # per-query partials summed over the tokens (no memset-cleared reduction)

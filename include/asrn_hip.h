@@ -84,8 +84,9 @@ int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* 
  * d w_suf) and a key pass (key-side gradients from att and ds at the slots of the queries that see the key: the
  * next <= C same-bucket sorted ranks).
  *   dsalida (B, L, d); entries from asrn_candidates_fwd (its [..., 1] receives ds, read back by the key pass)
- *   dphi (B, L, P), dV (B, L, d), dQc, dKc (B, L, cf) dense, dBt (B, L) fp64, dlog_alfa (B, L) out (overwritten); dV is
- *   contiguous and, with v_shift = 1, the gradient of the per-position projection (row 0 of each batch row is 0)
+ *   dphi (B, L, P), dQc, dKc (B, L, cf) dense, dBt (B, L) fp64, dlog_alfa (B, L) out (overwritten); dV has V's
+ *   layout (row stride ldv, 16-byte aligned) and, with v_shift = 1, is the gradient of the per-position projection
+ *   (row 0 of each batch row is 0): its d columns of every row are written, the rest of a row is left alone
  *   partials (B*L, T + K + 1) fp32 out: per query, d gamma_tau then d w_suf[0..K]; the caller sums over rows. */
 int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                         const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
@@ -119,6 +120,29 @@ int asrn_context_bwd(const float* h, const float* ln_w, const float* ln_b, const
                      int64_t BL, int32_t d, float beta_max, float log_alfa_min, const float* dhh, const double* dbeta,
                      const float* dlog_alfa, float* dh, float* dparams, void* workspace, int64_t workspace_bytes,
                      void* stream);
+
+/* ---- a0 (part): the hash MLPs' hidden layer (asrn/nucleo.py:644-659) -------------------------------------------
+ * Replaces the GELU of afin_palabra and afin_contexto between their two Linear layers, with the context MLP's first
+ * layer on the key [E_t; E_{t-1}] (nucleo:649-652) split by linearity. y (B*L, ldy) fp32 holds, per token, the bias-free
+ * products hp = W_p E_t at columns [0, m), za = W_a E_t at [m, m + mc) and zb = W_b E_t at [m + mc, m + 2 mc), where
+ * [W_a | W_b] = afin_contexto[0].weight. hidden_fwd writes g (B*L, m + mc) = [gelu(hp + b_word) | gelu(za + zb[t-1] +
+ * b_ctx)] (no zb term at t = 0; gelu in the exact erf form). hidden_bwd, from dg (B*L, m + mc), writes columns
+ * [0, m + 2 mc) of dy (B*L, ldd): the gradients of hp, za and zb (zb's at t is the context pre-activation's gradient
+ * at t + 1, 0 at a row's last position); the biases' gradients are then the column sums of dy's first m + mc
+ * columns. m and mc multiples of 4; rows, g, dg and the biases 16-byte aligned. */
+int asrn_hidden_fwd(const float* y, int64_t ldy, const float* b_word, const float* b_ctx, int64_t B, int64_t L,
+                    int32_t m, int32_t mc, float* g, void* stream);
+int asrn_hidden_bwd(const float* y, int64_t ldy, const float* b_word, const float* b_ctx, int64_t B, int64_t L,
+                    int32_t m, int32_t mc, const float* dg, float* dy, int64_t ldd, void* stream);
+
+/* ---- column sums -----------------------------------------------------------------------------------------------
+ * No counterpart in the reference's FFI: the reductions PyTorch's autograd runs for it (the bias gradients of its
+ * nn.Linear projections, asrn/nucleo.py:591-630, and the parameter sums of the candidate backward, nucleo:465-515).
+ * out (cols) fp32 = the sum over the rows of x (rows, cols) with row stride ld, fp32 or bf16 (bf16 != 0), summed in
+ * fp32 in a fixed order. workspace: asrn_column_sums_workspace(rows, cols) bytes (0: none needed). */
+int64_t asrn_column_sums_workspace(int64_t rows, int64_t cols);
+int asrn_column_sums(const void* x, int32_t bf16, int64_t rows, int64_t cols, int64_t ld, float* out,
+                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- a9: clock --------------------------------------------------------------------------------------------------
  * Bt = cumsum(beta) over L in fp64 (asrn/estable.py:418). reverse != 0 computes the suffix sums instead (the

@@ -411,6 +411,79 @@ def test_candidates_v_shift_in_place():
 
 
 # ---------------------------------------------------------------------------------------------------------------------
+# a0: the hash producer (one GEMM, the fused hidden layer) and the column sums of the parameter gradients
+# ---------------------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize('rows,cols,ld,off,bf16', [(32768, 13, 13, 0, False), (32768, 112, 448, 192, False),
+                                                   (16, 114688, 114688, 0, False), (4096, 7, 9, 1, False),
+                                                   (1, 5, 5, 0, False), (0, 6, 6, 0, False), (5000, 64, 64, 0, True),
+                                                   (20000, 448, 448, 0, True), (300, 1024, 1030, 2, True)])
+def test_column_sums_exact(rows, cols, ld, off, bf16):
+    """asrn_column_sums on small integers, whose fp32 sums are exact in any order: every column must equal the integer
+    sum bit for bit (one slab or two passes, float4 or scalar loads, strided and offset rows, bf16 input)."""
+    say('column sums', rows, cols, ld, off, bf16)
+    from asrn_amd.lineal import _hip_sums
+    g = torch.Generator().manual_seed(rows + cols)
+    flat = torch.randint(-8, 9, (rows * ld + off + 8,), generator=g)
+    ref = flat[off:off + rows * ld].view(rows, ld)[:, :cols].sum(0) if rows else torch.zeros(cols, dtype=torch.int64)
+    x = flat.to(torch.bfloat16 if bf16 else torch.float32).to(DEV)
+    xv = x.as_strided((rows, cols), (ld, 1), off)
+    out = _hip_sums(xv, rows, cols, ld)
+    assert torch.equal(out.cpu().double(), ref.double())
+
+
+class _GradAsBlock(torch.autograd.Function):
+    """Identity whose backward hands back the gradient as a column block of a wider buffer, the layout the candidate
+    backward gives dv (its dV takes V's layout)."""
+
+    @staticmethod
+    def forward(ctx, v):
+        ctx.n, ctx.col = v.stride(1), v.storage_offset() % v.stride(1)
+        return v.view_as(v)
+
+    @staticmethod
+    def backward(ctx, g):
+        B, L, d = g.shape
+        buf = torch.full((B, L, ctx.n), float('nan'), device=g.device)
+        buf[..., ctx.col:ctx.col + d] = g
+        return buf[..., ctx.col:ctx.col + d]
+
+
+@pytest.mark.parametrize('B,L,d,block', [(2, 777, 96, True), (2, 777, 96, False), (3, 1, 64, True),
+                                         (1, 2048, 256, True)])
+def test_hash_producer_vs_oracle(B, L, d, block):
+    """phi and v from the fused producer (one GEMM, asrn_hidden_fwd/bwd, column sums for the biases) against the
+    oracle's word and context MLPs on the materialized key [E_t; E_{t-1}] (fp64 on the CPU): outputs, the gradient of
+    E and of every producer parameter. block: dv arrives as a column block of a (B, L, n) buffer (the in-place
+    backward); otherwise dense (copied into the output gradient)."""
+    say('hash producer', B, L, d, block)
+    layer = synth.move_params(CapaASRNEstable(d), seed=B + d)
+    p = {k: v.detach().clone() for k, v in layer.state_dict().items()}
+    g = torch.Generator().manual_seed(L)
+    E = torch.randn(B, L, d, generator=g)
+    gphi = torch.randn(B, L, layer.n_tablas * layer.n_bits, generator=g)
+    gv = torch.randn(B, L, d, generator=g)
+    gv[:, 0] = 0                     # v[0] is no V row: the oracle's V[t] = v[t + 1]
+    names = [k for k in p if k.startswith(('afin_palabra', 'afin_contexto', 'v.'))]
+    leaves = {k: (v.double().requires_grad_() if k in names else v) for k, v in p.items()}
+    Ec = E.double().requires_grad_()
+    phi_r, V_r = O.phi_and_values(leaves, Ec)
+    ((phi_r * gphi.double()).sum() + (V_r[:, :-1] * gv[:, 1:].double()).sum()).backward()
+    layer = layer.to(DEV)
+    Ed = E.to(DEV).requires_grad_()
+    phi, v = layer._phi_y_valores(Ed)
+    assert v.stride(1) != d               # v is read in place from the GEMM output
+    vv = _GradAsBlock.apply(v) if block else v
+    ((phi * gphi.to(DEV)).sum() + (vv * gv.to(DEV)).sum()).backward()
+    assert_close(phi, phi_r, 'phi')
+    assert_close(v[:, 1:], V_r[:, :-1], 'v')
+    assert_close(Ed.grad, Ec.grad, 'grad E')
+    named = dict(layer.named_parameters())
+    for k in names:
+        assert_close(named[k].grad, leaves[k].grad, 'grad ' + k)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
 # a0: the context producer
 # ---------------------------------------------------------------------------------------------------------------------
 

@@ -96,6 +96,19 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert lib.asrn_gate_bwd(*gate, 10, 256, 4, 16, 8, 4, 0.4, 1e4, 0.0, *([N] * 8), 16, N) != 0
     assert 'workspace' in _err(lib)
     assert lib.asrn_gate_bwd_workspace(32768, 256) >= 320 * 4
+    # hidden layer: widths in float4 groups, the row strides
+    assert lib.asrn_hidden_fwd(N, 200, N, N, 2, 16, 6, 64, N, N) != 0
+    assert 'm=6' in _err(lib)
+    assert lib.asrn_hidden_bwd(N, 100, N, N, 2, 16, 64, 64, N, N, 448, N) != 0
+    assert 'row stride' in _err(lib)
+    # column sums: a stride below the width; long columns need the slab workspace, short ones none
+    assert lib.asrn_column_sums(N, 0, 16, 13, 12, N, N, 0, N) != 0
+    assert 'bad sizes' in _err(lib)
+    assert lib.asrn_column_sums_workspace(16, 448 * 256) == 0
+    assert lib.asrn_column_sums_workspace(0, 6) == 0 and lib.asrn_column_sums_workspace(1, 0) == 0
+    assert lib.asrn_column_sums_workspace(32768, 13) >= 2 * 13 * 4
+    assert lib.asrn_column_sums(N, 0, 32768, 13, 13, N, N, 0, N) != 0
+    assert 'workspace' in _err(lib)
     # generation: ring sizes, the decode position inside the caches, table capacities
     assert lib.asrn_ring_build(N, N, 2, 10, 8, 15, 32, N, N, N) != 0
     assert 'asrn_ring_build' in _err(lib)
