@@ -39,11 +39,12 @@ SIGNATURES = {
     'asrn_streak_bwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P, _I64, _P]),
     'asrn_context_fwd': (ctypes.c_int, [_P] * 5 + [_I64, _I32] + [_F32] * 3 + [_P] * 5),
     'asrn_context_bwd_workspace': (_I64, [_I64, _I32]),
-    'asrn_context_bwd': (ctypes.c_int, [_P] * 5 + [_I64, _I32] + [_F32] * 2 + [_P] * 6 + [_I64, _P]),
+    'asrn_context_bwd': (ctypes.c_int, [_P] * 5 + [_I64, _I32] + [_F32] * 2 + [_P] * 7 + [_I64, _P]),
     'asrn_hidden_fwd': (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I64, _I32, _I32, _P, _P]),
     'asrn_hidden_bwd': (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I64, _I32, _I32, _P, _P, _I64, _P]),
     'asrn_column_sums_workspace': (_I64, [_I64, _I64]),
     'asrn_column_sums': (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _P, _P, _I64, _P]),
+    'asrn_small_gemm': (ctypes.c_int, [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I32, _I32, _I32, _P]),
     'asrn_gate_fwd': (ctypes.c_int, [_P, _P, _I32] + [_P] * 11 + [_I64] + [_I32] * 5 + [_F32] * 3 + [_P] * 3),
     'asrn_gate_bwd_workspace': (_I64, [_I64, _I32]),
     'asrn_gate_bwd': (ctypes.c_int, [_P, _P, _I32] + [_P] * 11 + [_I64] + [_I32] * 5 + [_F32] * 3 + [_P] * 8

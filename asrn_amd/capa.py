@@ -124,42 +124,46 @@ class CapaASRNEstable(nn.Module):
         return torch.cat([self.afin_palabra(E), self.afin_contexto(llave)], dim=-1)
 
     def _phi_y_valores(self, E):
-        """phi (B, L, P) and v (B, L, d) = W_v E at every position (asrn/nucleo.py:644-659; the layer's V[t] is v[t+1],
-        which the candidate kernels read in place). One GEMM over E gives the word MLP's first layer, the context
-        MLP's first layer split by linearity (W [E_t; E_{t-1}] = W_a E_t + W_b E_{t-1}: the key [E_t; E_{t-1}] is
-        never materialized) and v. In fp32, the biases, the shift of the W_b product and the GELU are one kernel
-        (ops.Producer); under autocast they are PyTorch ops on the GEMM's output."""
+        """phi (B, L, P) and the rows the candidate kernels gather for the values (asrn/nucleo.py:644-659).
+
+        The reference's values are V[s] = W_v E[s+1] and the layer adds W_o (sum over tables of att V). Both maps are
+        linear, so the kernels gather E[s+1] itself (read in place, shifted) and the layer applies W_o W_v once to the
+        gathered sum (_combinar): the same result up to fp32 reassociation, without the W_v projection of every
+        position in the forward and its two GEMMs in the backward. One GEMM over E gives the word MLP's first layer
+        and the context MLP's first layer split by linearity (W [E_t; E_{t-1}] = W_a E_t + W_b E_{t-1}: the key
+        [E_t; E_{t-1}] is never materialized). In fp32 the biases, the shift of the W_b product and the GELU are one
+        kernel (ops.Producer); under autocast they are PyTorch ops on the GEMM's output."""
         d = E.shape[-1]
         pal, ctx = self.afin_palabra, self.afin_contexto
         m, mc = pal[0].out_features, ctx[0].out_features
-        wab = ctx[0].weight.view(mc, 2, d).transpose(0, 1).reshape(2 * mc, d)      # [W_a; W_b]
+        W = torch.cat([pal[0].weight, ctx[0].weight.view(mc, 2, d).transpose(0, 1).reshape(2 * mc, d)])
         if (E.dtype == torch.float32 and not torch.is_autocast_enabled(E.device.type) and m % 4 == 0
-                and mc % 4 == 0 and pal[0].weight.dtype == torch.float32):
-            g, v = ops.Producer.apply(E, torch.cat([pal[0].weight, wab, self.v.weight]), pal[0].bias, ctx[0].bias,
-                                      m, mc)
+                and mc % 4 == 0 and W.dtype == torch.float32):
+            g, filas = ops.Producer.apply(E, W, pal[0].bias, ctx[0].bias, m, mc)
         else:
-            y = lineal(_a_autocast(E), torch.cat([pal[0].weight, wab, self.v.weight]),
-                       F.pad(pal[0].bias, (0, 2 * mc + d)))
-            hp, za, zb, v = y.split([m, mc, mc, d], dim=-1)
+            y = lineal(_a_autocast(E), W, F.pad(pal[0].bias, (0, 2 * mc)))
+            hp, za, zb = y.split([m, mc, mc], dim=-1)
             g = F.gelu(torch.cat([hp, _ShiftAdd.apply(za, zb, ctx[0].bias)], dim=-1))
+            filas = _a_autocast(E)
         # both second layers as one GEMM with a block-diagonal weight: phi comes out whole
         W2 = torch.block_diag(pal[2].weight, ctx[2].weight)
         phi = lineal(g, W2, torch.cat([pal[2].bias, ctx[2].bias]))
-        return phi, v
+        return phi, filas
 
-    def _contexto(self, h):
+    def _contexto(self, h, con_h=False):
         """Qc, Kc (B, L, cf), beta (B, L) fp64 and log_alfa (B, L) (asrn/estable.py:153-194 with the GPU branch's clock
         projection in true fp32, estable:171-175): LayerNorm, the clock projection and its softplus / logsigmoid /
-        clamps fused in asrn_context_fwd/bwd; Qc, Kc on hipBLASLt."""
+        clamps fused in asrn_context_fwd/bwd; Qc, Kc on hipBLASLt. con_h: also h as the gate should take it (an
+        alias whose gradient the context backward adds to its own)."""
         p = self.protecciones
         meta = (float(self.ln_ctx.eps), -1.0 if p.beta_max is None else float(p.beta_max),
                 -math.inf if p.log_alfa_min is None else float(p.log_alfa_min))
-        hh32, beta, log_alfa = ops.Context.apply(h, self.ln_ctx.weight, self.ln_ctx.bias, self.w_reloj, self.b_reloj,
-                                                 meta)
+        hh32, beta, log_alfa, h_puerta = ops.Context.apply(h, self.ln_ctx.weight, self.ln_ctx.bias, self.w_reloj,
+                                                           self.b_reloj, meta)
         cf = self.confirmar
         y = lineal(_a_autocast(hh32), torch.cat([self.cq.weight, self.ck.weight]))
         Qc, Kc = _Split2.apply(y, cf)
-        return Qc, Kc, beta, log_alfa
+        return (Qc, Kc, beta, log_alfa, h_puerta) if con_h else (Qc, Kc, beta, log_alfa)
 
     def _kappas(self):
         k, kr = self.log_kappa.exp(), self.log_kappa_racha.exp()
@@ -171,14 +175,16 @@ class CapaASRNEstable(nn.Module):
     def _acumular(self, E, Qc, Kc, Bt, log_alfa, sig, partes=None):
         """Candidate attention of all tables -> salida and the gate signals (asrn/estable.py:204-300)."""
         T = self.n_tablas
-        phi, v = self._phi_y_valores(E)
-        if partes is not None:
+        phi, filas = self._phi_y_valores(E)
+        if partes is not None:                                              # the generation step's value cache
+            v = F.linear(_a_autocast(E), self.v.weight)
             partes.update(phi=phi, V=F.pad(v, (0, 0, 0, 1))[:, 1:])         # V[t] = W_v E[t+1], 0 at the end
         _, order, _, rank, win = ops.bucket_sort(phi.detach(), T, self.n_bits, self.chunk)
         shape = dict(T=T, Tc=self.tablas_contexto, C=self.chunk, K=self.sufijo, v_shift=1)
-        salida, sen = ops.Candidates.apply(phi, v, Qc, Kc, Bt, log_alfa, self.w_sufijo, self.gamma, sig, order,
-                                           win, rank, shape)
-        return {'salida': salida, 'senales': sen}
+        suma, sen = ops.Candidates.apply(phi, filas, Qc, Kc, Bt, log_alfa, self.w_sufijo, self.gamma, sig, order,
+                                         win, rank, shape)
+        # sum over tables of att E[s+1]: W_v and W_o are applied together after it (see _phi_y_valores)
+        return {'salida': suma, 'senales': sen, 'w_salida': ops.SmallMatmul.apply(self.o.weight, self.v.weight)}
 
     def _repeticion(self, sig, beta, Bt, log_alfa, partes=None):
         """vistos, hawkes (B, L, n) and racha (B, L) (asrn/estable.py:304-321)."""
@@ -195,9 +201,10 @@ class CapaASRNEstable(nn.Module):
 
     def _combinar(self, acc, h):
         """h' = h + sigmoid(logit) W_o (salida / max(1, peso_total)): W_o on hipBLASLt, the rest fused in asrn_gate_*
-        (the division by the table count is applied after W_o, per token)."""
+        (the division by the table count is applied after W_o, per token). acc['w_salida'], when present, replaces W_o
+        (the whole-text path passes W_o W_v with the gathered sum of E rows)."""
         p = self.protecciones
-        aporte = self.drop(lineal(acc['salida'], self.o.weight))
+        aporte = self.drop(lineal(acc['salida'], acc.get('w_salida', self.o.weight)))
         meta = (self.n_tablas, self.tablas_contexto, self.racha_paso,
                 -1.0 if p.mejor_max is None else float(p.mejor_max), 0.0 if p.tope_puerta is None else float(p.tope_puerta))
         return ops.Gate.apply(h, aporte, acc['senales'], acc['vistos'], acc['hawkes'], acc['racha'], self.g.weight,
@@ -215,7 +222,7 @@ class CapaASRNEstable(nn.Module):
         Qc, Kc, sig, beta, Bt, log_alfa, n-gram keys and their sort, hawkes and racha)."""
         self._revisar(E)
         sig = self._firma(E) if piezas is None else firmas_de_piezas(piezas)
-        Qc, Kc, beta, log_alfa = self._contexto(h)
+        Qc, Kc, beta, log_alfa, h = self._contexto(h, con_h=True)
         Bt = ops.ClockScan.apply(beta)
         acc = self._acumular(E, Qc, Kc, Bt, log_alfa, sig, partes)
         acc.update(self._repeticion(sig, beta, Bt, log_alfa, partes))

@@ -8,7 +8,7 @@
 // Backward, from dhh (the Qc/Kc GEMM's input gradient), dbeta and dlog_alfa:
 //   du_0 = dbeta softplus'(u_0) [softplus(u_0) <= beta_max],  du_1 = dlog_alfa sigmoid(-u_1) [not clamped below]
 //   g = dhh + du_0 w_reloj[0] + du_1 w_reloj[1],  dxhat = g ln_w
-//   dh = rstd (dxhat - mean(dxhat) - xhat mean(dxhat xhat))
+//   dh = rstd (dxhat - mean(dxhat) - xhat mean(dxhat xhat)) [+ dh_add: h's gradient through the layer's other use]
 //   d ln_w = sum_t g xhat, d ln_b = sum_t g, d w_reloj[k] = sum_t du_k hh, d b_reloj[k] = sum_t du_k
 // A workgroup takes 32 tokens, each wave 8 of them, loading 2 tokens' rows (float4 per lane) at a time; the parameter
 // gradients are per-workgroup partials summed in order by a second launch (deterministic, no atomics).
@@ -28,6 +28,7 @@ struct CtxArgs {
   int64_t BL; int d; float eps; float beta_max; float la_min;
   float* hh; float4* stats; double* beta; float* la;                      // forward
   const float* dhh; const double* dbeta; const float* dla; float* dh; float* partial;   // backward
+  const float* dh_add;   // backward, optional: a gradient of h from elsewhere, added to dh
 };
 
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
   for (int k = 0; k < D4; ++k) gw[k] = gb[k] = gr0[k] = gr1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
   float gbr0 = 0.f, gbr1 = 0.f;
   for (int b = 0; b < kCtxTokPerWave; b += kCtxBatch) {
-    float4 hv[kCtxBatch][D4], gv[kCtxBatch][D4];
+    float4 hv[kCtxBatch][D4], gv[kCtxBatch][D4], av[kCtxBatch][D4];
     float4 st[kCtxBatch];
     float db[kCtxBatch], dl[kCtxBatch];
 #pragma unroll
@@ -127,6 +128,7 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
         if (ok && q < d4) {
           hv[u][k] = ((const float4*)(a.h + t * a.d))[q];
           gv[u][k] = ((const float4*)(a.dhh + t * a.d))[q];
+          av[u][k] = a.dh_add ? ((const float4*)(a.dh_add + t * a.d))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
       }
     }
@@ -173,9 +175,10 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
         const int q = lane + kWave * k;
         if (q < d4) {
           const float4 w = ((const float4*)a.lnw)[q];
-          ((float4*)(a.dh + t * a.d))[q] =
-              make_float4(rstd * (g[k].x * w.x - m1 - xh[k].x * m2), rstd * (g[k].y * w.y - m1 - xh[k].y * m2),
-                          rstd * (g[k].z * w.z - m1 - xh[k].z * m2), rstd * (g[k].w * w.w - m1 - xh[k].w * m2));
+          ((float4*)(a.dh + t * a.d))[q] = make_float4(rstd * (g[k].x * w.x - m1 - xh[k].x * m2) + av[u][k].x,
+                                                       rstd * (g[k].y * w.y - m1 - xh[k].y * m2) + av[u][k].y,
+                                                       rstd * (g[k].z * w.z - m1 - xh[k].z * m2) + av[u][k].z,
+                                                       rstd * (g[k].w * w.w - m1 - xh[k].w * m2) + av[u][k].w);
         }
       }
       gbr0 += du0;
@@ -274,12 +277,12 @@ extern "C" int64_t asrn_context_bwd_workspace(int64_t BL, int32_t d) {
 
 extern "C" int asrn_context_bwd(const float* h, const float* ln_w, const float* ln_b, const float* w_reloj,
                                 const float* stats, int64_t BL, int32_t d, float beta_max, float log_alfa_min,
-                                const float* dhh, const double* dbeta, const float* dlog_alfa, float* dh,
-                                float* dparams, void* workspace, int64_t workspace_bytes, void* stream) {
+                                const float* dhh, const double* dbeta, const float* dlog_alfa, const float* dh_add,
+                                float* dh, float* dparams, void* workspace, int64_t workspace_bytes, void* stream) {
   CtxArgs a{};
   a.h = h; a.lnw = ln_w; a.lnb = ln_b; a.wr = w_reloj; a.BL = BL; a.d = d; a.eps = 1.f; a.beta_max = beta_max;
   a.la_min = log_alfa_min; a.stats = (float4*)stats; a.dhh = dhh; a.dbeta = dbeta; a.dla = dlog_alfa; a.dh = dh;
-  a.partial = (float*)workspace;
+  a.dh_add = dh_add; a.partial = (float*)workspace;
   if (ctx_check(a, "asrn_context_bwd")) return 1;
   ASRN_REQUIRE(workspace != nullptr && workspace_bytes >= asrn_context_bwd_workspace(BL, d),
                "asrn_context_bwd: workspace too small");

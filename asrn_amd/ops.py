@@ -102,6 +102,8 @@ def ngram_sort(sig, coef, n):
 class Context(torch.autograd.Function):
     """hh = LayerNorm(h), beta = min(softplus(u_0), beta_max) fp64, log_alfa = max(logsigmoid(u_1) + log 2, min) with
     u = w_reloj hh + b_reloj in fp32 (asrn/estable.py:153-194), fused in asrn_context_fwd/bwd. hh feeds the Qc/Kc GEMM.
+    The fourth output is h itself (fp32, an alias) for the layer's other use of h (the gate): its gradient is added
+    to dh inside asrn_context_bwd, so the two paths to h need no separate addition.
     meta = (eps, beta_max or -1, log_alfa_min or -inf)."""
 
     @staticmethod
@@ -121,10 +123,10 @@ class Context(torch.autograd.Function):
              ptr(stats), ptr(beta), ptr(la), stream_of(dev))
         ctx.save_for_backward(h32, *params[:3], stats)
         ctx.meta = (beta_max, la_min, h.dtype, lead, [p.shape for p in (ln_w, ln_b, w_reloj, b_reloj)])
-        return hh.view(*lead, d), beta.view(lead), la.view(lead)
+        return hh.view(*lead, d), beta.view(lead), la.view(lead), h32.view(*lead, d)
 
     @staticmethod
-    def backward(ctx, dhh, dbeta, dla):
+    def backward(ctx, dhh, dbeta, dla, dh_add):
         h32, lnw, lnb, wr, stats = ctx.saved_tensors
         beta_max, la_min, hdt, lead, shapes = ctx.meta
         BL, d = h32.shape
@@ -133,36 +135,39 @@ class Context(torch.autograd.Function):
         dbeta = (torch.zeros((BL,), dtype=torch.float64, device=dev) if dbeta is None
                  else _c(dbeta, torch.float64).reshape(BL))
         dla = torch.zeros((BL,), dtype=torch.float32, device=dev) if dla is None else _c(dla, torch.float32).reshape(BL)
+        if dh_add is not None:
+            dh_add = _c(dh_add, torch.float32).reshape(BL, d)
         dh = torch.empty_like(h32)
         dp = torch.empty((4 * d + 2,), dtype=torch.float32, device=dev)
         wsb = query('asrn_context_bwd_workspace', BL, d)
         ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
         call('asrn_context_bwd', ptr(h32), ptr(lnw), ptr(lnb), ptr(wr), ptr(stats), BL, d, beta_max, la_min,
-             ptr(dhh), ptr(dbeta), ptr(dla), ptr(dh), ptr(dp), ptr(ws), wsb, stream_of(dev))
+             ptr(dhh), ptr(dbeta), ptr(dla), ptr(dh_add), ptr(dh), ptr(dp), ptr(ws), wsb, stream_of(dev))
         sizes = [d, d, 2 * d, 2]
         grads = [t.view(s) for t, s in zip(torch.split(dp, sizes), shapes)]
         return (dh.view(*lead, d).to(hdt), *grads, None)
 
 
 # ---------------------------------------------------------------------------------------------------------------------
-# a0 (the hash MLPs' first layers and the value projection)
+# a0 (the hash MLPs' first layers)
 # ---------------------------------------------------------------------------------------------------------------------
 
 class Producer(torch.autograd.Function):
-    """y = E W^T by one bias-free GEMM, W's rows [W_p (m) | W_a (mc) | W_b (mc) | W_v (d)]; returns the hash MLPs'
-    hidden units g (B, L, m + mc) = [gelu(W_p E_t + b_word) | gelu(W_a E_t + W_b E_{t-1} + b_ctx)] (asrn_hidden_fwd;
-    asrn/nucleo.py:644-652) and v = W_v E, a column block of y read in place by the candidate kernels.
+    """y = E W^T by one bias-free GEMM, W's rows [W_p (m) | W_a (mc) | W_b (mc)]; returns the hash MLPs' hidden units
+    g (B, L, m + mc) = [gelu(W_p E_t + b_word) | gelu(W_a E_t + W_b E_{t-1} + b_ctx)] (asrn_hidden_fwd;
+    asrn/nucleo.py:644-652) and E itself (fp32, an alias) as the rows the candidate kernels gather.
 
-    Backward: the candidate backward writes dv as the same column block of a (B, L, n) buffer; asrn_hidden_bwd fills
-    the buffer's other columns from dg, and the buffer is dy, with no concatenation. (dv in any other layout is copied
-    into a fresh dy.) dE = dy W, dW by token slabs, and the biases' gradients are the column sums of dy's first m + mc
-    columns. fp32 only."""
+    Backward: asrn_hidden_bwd turns dg into dy; the alias's gradient (from the candidate backward) is the buffer the
+    input gradient accumulates into, dE = dE_rows + dy W in one GEMM with beta = 1, so the two paths to E need no
+    separate addition. dW by token slabs; the biases' gradients are the column sums of dy. fp32 only."""
 
     @staticmethod
     def forward(ctx, E, W, b_word, b_ctx, m, mc):
         dev = _dev(E, W)
         B, L, d = E.shape
         n = W.shape[0]
+        if n != m + 2 * mc:
+            raise ValueError(f'Producer: W has {n} rows, expected m + 2 mc = {m + 2 * mc}')
         E = _c(E, torch.float32)
         bw, bc = _c(b_word, torch.float32), _c(b_ctx, torch.float32)
         y = torch.nn.functional.linear(E, W)
@@ -170,38 +175,72 @@ class Producer(torch.autograd.Function):
         call('asrn_hidden_fwd', ptr(y), n, ptr(bw), ptr(bc), B, L, m, mc, ptr(g), stream_of(dev))
         ctx.save_for_backward(E, W, y, bw, bc)
         ctx.meta = (m, mc)
-        return g, y[..., m + 2 * mc:]
+        return g, E.view_as(E)
 
     @staticmethod
-    def backward(ctx, dg, dv):
+    def backward(ctx, dg, drows):
         E, W, y, bw, bc = ctx.saved_tensors
         m, mc = ctx.meta
         B, L, n = y.shape
-        d0 = m + 2 * mc
+        d = E.shape[-1]
         dev = y.device
-        dy = None
-        if (dv is not None and dv.dtype == torch.float32 and dv.stride() == (L * n, n, 1)
-                and dv.storage_offset() >= d0
-                and dv.untyped_storage().nbytes() >= 4 * (dv.storage_offset() - d0 + B * L * n)):
-            dy = dv.as_strided((B, L, n), (L * n, n, 1), dv.storage_offset() - d0)   # the buffer dv lives in
-        if dy is None:
-            dy = torch.empty((B, L, n), dtype=torch.float32, device=dev)
-            if dv is None:
-                dy[..., d0:].zero_()
-            else:
-                dy[..., d0:].copy_(dv)
-        dg = torch.zeros((B, L, m + mc), dtype=torch.float32, device=dev) if dg is None else _c(dg, torch.float32)
+        dE = dW = dbw = dbc = None
+        if dg is None:
+            if ctx.needs_input_grad[0] and drows is not None:
+                dE = drows
+            return dE, None, None, None, None, None
+        dg = _c(dg, torch.float32)
+        dy = torch.empty((B, L, n), dtype=torch.float32, device=dev)
         call('asrn_hidden_bwd', ptr(y), n, ptr(bw), ptr(bc), B, L, m, mc, ptr(dg), ptr(dy), n, stream_of(dev))
         dy2 = dy.view(B * L, n)
-        dE = dW = dbw = dbc = None
         if ctx.needs_input_grad[0]:
-            dE = dy2.mm(W).view(B, L, -1)
+            if drows is None:
+                dE = dy2.mm(W).view(B, L, d)
+            else:
+                # the rows' gradient is a fresh buffer of the candidate backward: accumulate the GEMM into it
+                dE = _c(drows, torch.float32) if drows.dtype != torch.float32 or not drows.is_contiguous() else drows
+                dE.view(B * L, d).addmm_(dy2, W)
         if ctx.needs_input_grad[1]:
-            dW = weight_grad(dy2, E.view(B * L, -1))
+            dW = weight_grad(dy2, E.view(B * L, d))
         if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:
             db = column_sums(dy2[:, :m + mc])
             dbw, dbc = db[:m], db[m:]
         return dE, dW, dbw, dbc, None, None
+
+
+class SmallMatmul(torch.autograd.Function):
+    """A @ B for small fp32 matrices (asrn_small_gemm: one workgroup per 16 x 16 tile of the result): the layer's
+    W_o W_v. The backward's dA = dC B^T and dB = A^T dC run on the same kernel."""
+
+    @staticmethod
+    def forward(ctx, A, B):
+        dev = _dev(A, B)
+        A32, B32 = _c(A, torch.float32), _c(B, torch.float32)
+        (M, K), (K2, N) = A32.shape, B32.shape
+        if K != K2:
+            raise ValueError(f'SmallMatmul: shapes {tuple(A.shape)} and {tuple(B.shape)} do not chain')
+        C = torch.empty((M, N), dtype=torch.float32, device=dev)
+        call('asrn_small_gemm', ptr(A32), K, 0, ptr(B32), N, 0, ptr(C), N, M, N, K, stream_of(dev))
+        ctx.save_for_backward(A32, B32)
+        ctx.dts = (A.dtype, B.dtype)
+        return C
+
+    @staticmethod
+    def backward(ctx, dC):
+        A, B = ctx.saved_tensors
+        (M, K), N = A.shape, B.shape[1]
+        dev = A.device
+        dC = _c(dC, torch.float32)
+        dA = dB = None
+        if ctx.needs_input_grad[0]:                # (M, K) = dC (M, N) B^T
+            dA = torch.empty((M, K), dtype=torch.float32, device=dev)
+            call('asrn_small_gemm', ptr(dC), N, 0, ptr(B), N, 1, ptr(dA), K, M, K, N, stream_of(dev))
+            dA = dA.to(ctx.dts[0])
+        if ctx.needs_input_grad[1]:                # (K, N) = A^T (K, M) dC (M, N)
+            dB = torch.empty((K, N), dtype=torch.float32, device=dev)
+            call('asrn_small_gemm', ptr(A), K, 1, ptr(dC), N, 0, ptr(dB), N, K, N, M, stream_of(dev))
+            dB = dB.to(ctx.dts[1])
+        return dA, dB
 
 
 # ---------------------------------------------------------------------------------------------------------------------

@@ -110,7 +110,7 @@ int64_t asrn_scan_workspace(int64_t rows, int64_t N);
  * no clamp); log_alfa = max(logsigmoid(u_1) + log 2, log_alfa_min) (BL) fp32 out (-inf: no clamp); stats (BL, 4) =
  * (mean, rstd, u_0, u_1) kept for the backward. d % 4 == 0, d <= 1024.
  * context_bwd: from dhh (BL, d) (the Qc/Kc GEMM's input gradient), dbeta (BL) fp64 and dlog_alfa (BL) gives dh (BL, d)
- * (overwritten) and dparams (4 d + 2) = the gradients of [ln_w | ln_b | w_reloj (2 d) | b_reloj (2)], summed over
+ * (overwritten; plus dh_add (BL, d) when not null: the gradient of h through the gate) and dparams (4 d + 2) = the gradients of [ln_w | ln_b | w_reloj (2 d) | b_reloj (2)], summed over
  * tokens in a fixed order. workspace: asrn_context_bwd_workspace(BL, d) bytes. */
 int asrn_context_fwd(const float* h, const float* ln_w, const float* ln_b, const float* w_reloj, const float* b_reloj,
                      int64_t BL, int32_t d, float eps, float beta_max, float log_alfa_min, float* hh, float* stats,
@@ -118,8 +118,8 @@ int asrn_context_fwd(const float* h, const float* ln_w, const float* ln_b, const
 int64_t asrn_context_bwd_workspace(int64_t BL, int32_t d);
 int asrn_context_bwd(const float* h, const float* ln_w, const float* ln_b, const float* w_reloj, const float* stats,
                      int64_t BL, int32_t d, float beta_max, float log_alfa_min, const float* dhh, const double* dbeta,
-                     const float* dlog_alfa, float* dh, float* dparams, void* workspace, int64_t workspace_bytes,
-                     void* stream);
+                     const float* dlog_alfa, const float* dh_add, float* dh, float* dparams, void* workspace,
+                     int64_t workspace_bytes, void* stream);
 
 /* ---- a0 (part): the hash MLPs' hidden layer (asrn/nucleo.py:644-659) -------------------------------------------
  * Replaces the GELU of afin_palabra and afin_contexto between their two Linear layers, with the context MLP's first
@@ -143,6 +143,14 @@ int asrn_hidden_bwd(const float* y, int64_t ldy, const float* b_word, const floa
 int64_t asrn_column_sums_workspace(int64_t rows, int64_t cols);
 int asrn_column_sums(const void* x, int32_t bf16, int64_t rows, int64_t cols, int64_t ld, float* out,
                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- products of small matrices ---------------------------------------------------------------------------------
+ * No counterpart in the reference's FFI. The layer applies W_o W_v to the gathered sum of embedding rows (the two
+ * linear maps the reference applies one after the other, V = v(E shifted) at asrn/nucleo.py:683 and aporte =
+ * o(salida) at asrn/estable.py:402); this forms W_o W_v and the two products of its backward. C (M, N) = op(A) op(B) in fp32, op(X) = X or X^T (trans != 0), row-major with leading
+ * dimensions lda, ldb, ldc; each element sums over k in order. M, N, K <= 8192. */
+int asrn_small_gemm(const float* A, int64_t lda, int32_t trans_a, const float* B, int64_t ldb, int32_t trans_b,
+                    float* C, int64_t ldc, int32_t M, int32_t N, int32_t K, void* stream);
 
 /* ---- a9: clock --------------------------------------------------------------------------------------------------
  * Bt = cumsum(beta) over L in fp64 (asrn/estable.py:418). reverse != 0 computes the suffix sums instead (the

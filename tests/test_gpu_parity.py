@@ -432,51 +432,48 @@ def test_column_sums_exact(rows, cols, ld, off, bf16):
     assert torch.equal(out.cpu().double(), ref.double())
 
 
-class _GradAsBlock(torch.autograd.Function):
-    """Identity whose backward hands back the gradient as a column block of a wider buffer, the layout the candidate
-    backward gives dv (its dV takes V's layout)."""
+@pytest.mark.parametrize('M,N,K', [(256, 256, 256), (33, 70, 129), (1, 17, 5), (512, 96, 768)])
+def test_small_matmul_vs_fp64(M, N, K):
+    """asrn_small_gemm through ops.SmallMatmul (the layer's W_o W_v): the product and both gradients against fp64
+    on the CPU, including sizes that leave partial 16 x 16 tiles."""
+    say('small matmul', M, N, K)
+    g = torch.Generator().manual_seed(M * N + K)
+    A, B, gC = torch.randn(M, K, generator=g), torch.randn(K, N, generator=g), torch.randn(M, N, generator=g)
+    Ar, Br = A.double().requires_grad_(), B.double().requires_grad_()
+    (Ar @ Br * gC.double()).sum().backward()
+    Ad, Bd = A.to(DEV).requires_grad_(), B.to(DEV).requires_grad_()
+    C = ops.SmallMatmul.apply(Ad, Bd)
+    (C * gC.to(DEV)).sum().backward()
+    assert_close(C, Ar @ Br, 'C', 1e-5)
+    assert_close(Ad.grad, Ar.grad, 'dA', 1e-5)
+    assert_close(Bd.grad, Br.grad, 'dB', 1e-5)
 
-    @staticmethod
-    def forward(ctx, v):
-        ctx.n, ctx.col = v.stride(1), v.storage_offset() % v.stride(1)
-        return v.view_as(v)
 
-    @staticmethod
-    def backward(ctx, g):
-        B, L, d = g.shape
-        buf = torch.full((B, L, ctx.n), float('nan'), device=g.device)
-        buf[..., ctx.col:ctx.col + d] = g
-        return buf[..., ctx.col:ctx.col + d]
-
-
-@pytest.mark.parametrize('B,L,d,block', [(2, 777, 96, True), (2, 777, 96, False), (3, 1, 64, True),
-                                         (1, 2048, 256, True)])
-def test_hash_producer_vs_oracle(B, L, d, block):
-    """phi and v from the fused producer (one GEMM, asrn_hidden_fwd/bwd, column sums for the biases) against the
-    oracle's word and context MLPs on the materialized key [E_t; E_{t-1}] (fp64 on the CPU): outputs, the gradient of
-    E and of every producer parameter. block: dv arrives as a column block of a (B, L, n) buffer (the in-place
-    backward); otherwise dense (copied into the output gradient)."""
-    say('hash producer', B, L, d, block)
+@pytest.mark.parametrize('B,L,d,rows_grad', [(2, 777, 96, True), (2, 777, 96, False), (3, 1, 64, True),
+                                             (1, 2048, 256, True)])
+def test_hash_producer_vs_oracle(B, L, d, rows_grad):
+    """phi from the fused producer (one GEMM, asrn_hidden_fwd/bwd, column sums for the biases) against the oracle's
+    word and context MLPs on the materialized key [E_t; E_{t-1}] (fp64 on the CPU): phi, the gradient of E and of
+    every MLP parameter. rows_grad: the E rows the producer hands on (the candidate kernels' values) also receive a
+    gradient, which the producer's input-gradient GEMM accumulates into."""
+    say('hash producer', B, L, d, rows_grad)
     layer = synth.move_params(CapaASRNEstable(d), seed=B + d)
     p = {k: v.detach().clone() for k, v in layer.state_dict().items()}
     g = torch.Generator().manual_seed(L)
     E = torch.randn(B, L, d, generator=g)
     gphi = torch.randn(B, L, layer.n_tablas * layer.n_bits, generator=g)
-    gv = torch.randn(B, L, d, generator=g)
-    gv[:, 0] = 0                     # v[0] is no V row: the oracle's V[t] = v[t + 1]
-    names = [k for k in p if k.startswith(('afin_palabra', 'afin_contexto', 'v.'))]
+    gr = torch.randn(B, L, d, generator=g)
+    names = [k for k in p if k.startswith(('afin_palabra', 'afin_contexto'))]
     leaves = {k: (v.double().requires_grad_() if k in names else v) for k, v in p.items()}
     Ec = E.double().requires_grad_()
-    phi_r, V_r = O.phi_and_values(leaves, Ec)
-    ((phi_r * gphi.double()).sum() + (V_r[:, :-1] * gv[:, 1:].double()).sum()).backward()
+    phi_r, _ = O.phi_and_values(leaves, Ec)
+    ((phi_r * gphi.double()).sum() + ((Ec * gr.double()).sum() if rows_grad else 0)).backward()
     layer = layer.to(DEV)
     Ed = E.to(DEV).requires_grad_()
-    phi, v = layer._phi_y_valores(Ed)
-    assert v.stride(1) != d               # v is read in place from the GEMM output
-    vv = _GradAsBlock.apply(v) if block else v
-    ((phi * gphi.to(DEV)).sum() + (vv * gv.to(DEV)).sum()).backward()
+    phi, filas = layer._phi_y_valores(Ed)
+    assert filas.data_ptr() == Ed.data_ptr()          # the values are E's own rows, read in place
+    ((phi * gphi.to(DEV)).sum() + ((filas * gr.to(DEV)).sum() if rows_grad else 0)).backward()
     assert_close(phi, phi_r, 'phi')
-    assert_close(v[:, 1:], V_r[:, :-1], 'v')
     assert_close(Ed.grad, Ec.grad, 'grad E')
     named = dict(layer.named_parameters())
     for k in names:

@@ -109,6 +109,11 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert lib.asrn_column_sums_workspace(32768, 13) >= 2 * 13 * 4
     assert lib.asrn_column_sums(N, 0, 32768, 13, 13, N, N, 0, N) != 0
     assert 'workspace' in _err(lib)
+    # small products: sizes and leading dimensions
+    assert lib.asrn_small_gemm(N, 16, 0, N, 16, 0, N, 16, 16, 16, 10000, N) != 0
+    assert 'K=10000' in _err(lib)
+    assert lib.asrn_small_gemm(N, 8, 0, N, 16, 0, N, 16, 16, 16, 16, N) != 0
+    assert 'leading' in _err(lib)
     # generation: ring sizes, the decode position inside the caches, table capacities
     assert lib.asrn_ring_build(N, N, 2, 10, 8, 15, 32, N, N, N) != 0
     assert 'asrn_ring_build' in _err(lib)
