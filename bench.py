@@ -180,6 +180,8 @@ def main():
     ap.add_argument('--no-decode', action='store_true')
     ap.add_argument('--decode-steps', type=int, default=32)
     ap.add_argument('--eager', action='store_true', help='time Python-launched steps instead of HIP graph replays')
+    ap.add_argument('--default-gemms', action='store_true',
+                    help="leave the GEMMs on the libraries' default picks instead of the shipped MI355X picks")
     ap.add_argument('--copy-calibration', type=int, default=0, metavar='BYTES',
                     help='only run a plain device-to-device copy of BYTES, 3 times: the reference point that scales '
                          'the FETCH_SIZE / WRITE_SIZE counters of a profiler run into bytes')
@@ -205,6 +207,11 @@ def main():
         return
 
     asrn_amd.load()
+    gemm_picks = 'library defaults'
+    if not args.default_gemms:
+        from asrn_amd import tuning
+        if tuning.use_tuned_gemms():
+            gemm_picks = 'TunableOp picks, asrn_amd/data/gemm_picks_mi355x.csv'
     cfg = synth.CONFIGS[args.config]
     B, N, d, V = cfg['B'], cfg['N'], cfg['d'], cfg['V']
     dev = torch.device('cuda:0')
@@ -295,7 +302,7 @@ def main():
         'spans; random-init layer moved off its neutral values)',
         'config': {'workload': f'{args.config}: one ASRN layer fwd+bwd, B={B}, N={N}, d={d}, V={V}, T=8 tables x 14 '
                                f'bits, C=32, {dtype}', 'global_batch': B, 'seq_len': N, 'parallelism': 'none (1 GPU)',
-                   'launch': 'eager' if graph is None else 'hip graph replay'},
+                   'launch': 'eager' if graph is None else 'hip graph replay', 'gemms': gemm_picks},
         'eager_ms_per_step': round(eager_wall * 1e3, 4),
         'roofline': {'bound': 'hbm', 'kernel': dom, 'achieved': round(achieved / 1e9, 1), 'peak': HBM_PEAK / 1e9,
                      'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK, 4), 'traffic': measured_traffic(dom) if args.config == 'cfg2' else None,
