@@ -123,7 +123,17 @@ class CapaASRNEstable(nn.Module):
         llave = torch.cat([E, F.pad(E, (0, 0, 1, 0))[:, :E.shape[1]]], dim=-1)
         return torch.cat([self.afin_palabra(E), self.afin_contexto(llave)], dim=-1)
 
-    def _phi_y_valores(self, E):
+    def _pesos(self):
+        """The fused GEMMs' weights (W, W2, b2, Wq) assembled in one launch (_Pesos), or None when a parameter is not
+        fp32 (the methods below then assemble them with PyTorch ops)."""
+        pal, ctx = self.afin_palabra, self.afin_contexto
+        ps = (pal[0].weight, ctx[0].weight, pal[2].weight, ctx[2].weight, pal[2].bias, ctx[2].bias, self.cq.weight,
+              self.ck.weight)
+        if not all(p.dtype == torch.float32 and p.is_cuda and p.is_contiguous() for p in ps):
+            return None
+        return _Pesos.apply(*ps)
+
+    def _phi_y_valores(self, E, pesos=None):
         """phi (B, L, P) and the rows the candidate kernels gather for the values (asrn/nucleo.py:644-659).
 
         The reference's values are V[s] = W_v E[s+1] and the layer adds W_o (sum over tables of att V). Both maps are
@@ -136,7 +146,12 @@ class CapaASRNEstable(nn.Module):
         d = E.shape[-1]
         pal, ctx = self.afin_palabra, self.afin_contexto
         m, mc = pal[0].out_features, ctx[0].out_features
-        W = torch.cat([pal[0].weight, ctx[0].weight.view(mc, 2, d).transpose(0, 1).reshape(2 * mc, d)])
+        if pesos is None:
+            W = torch.cat([pal[0].weight, ctx[0].weight.view(mc, 2, d).transpose(0, 1).reshape(2 * mc, d)])
+            W2 = torch.block_diag(pal[2].weight, ctx[2].weight)    # both second layers as one GEMM: phi comes whole
+            b2 = torch.cat([pal[2].bias, ctx[2].bias])
+        else:
+            W, W2, b2 = pesos[:3]
         if (E.dtype == torch.float32 and not torch.is_autocast_enabled(E.device.type) and m % 4 == 0
                 and mc % 4 == 0 and W.dtype == torch.float32):
             g, filas = ops.Producer.apply(E, W, pal[0].bias, ctx[0].bias, m, mc)
@@ -145,12 +160,10 @@ class CapaASRNEstable(nn.Module):
             hp, za, zb = y.split([m, mc, mc], dim=-1)
             g = F.gelu(torch.cat([hp, _ShiftAdd.apply(za, zb, ctx[0].bias)], dim=-1))
             filas = _a_autocast(E)
-        # both second layers as one GEMM with a block-diagonal weight: phi comes out whole
-        W2 = torch.block_diag(pal[2].weight, ctx[2].weight)
-        phi = lineal(g, W2, torch.cat([pal[2].bias, ctx[2].bias]))
+        phi = lineal(g, W2, b2)
         return phi, filas
 
-    def _contexto(self, h, con_h=False):
+    def _contexto(self, h, con_h=False, pesos=None):
         """Qc, Kc (B, L, cf), beta (B, L) fp64 and log_alfa (B, L) (asrn/estable.py:153-194 with the GPU branch's clock
         projection in true fp32, estable:171-175): LayerNorm, the clock projection and its softplus / logsigmoid /
         clamps fused in asrn_context_fwd/bwd; Qc, Kc on hipBLASLt. con_h: also h as the gate should take it (an
@@ -161,7 +174,8 @@ class CapaASRNEstable(nn.Module):
         hh32, beta, log_alfa, h_puerta = ops.Context.apply(h, self.ln_ctx.weight, self.ln_ctx.bias, self.w_reloj,
                                                            self.b_reloj, meta)
         cf = self.confirmar
-        y = lineal(_a_autocast(hh32), torch.cat([self.cq.weight, self.ck.weight]))
+        Wq = torch.cat([self.cq.weight, self.ck.weight]) if pesos is None else pesos[3]
+        y = lineal(_a_autocast(hh32), Wq)
         Qc, Kc = _Split2.apply(y, cf)
         return (Qc, Kc, beta, log_alfa, h_puerta) if con_h else (Qc, Kc, beta, log_alfa)
 
@@ -172,10 +186,10 @@ class CapaASRNEstable(nn.Module):
 
     # --- hot path (HIP) ---------------------------------------------------------------------------------------------
 
-    def _acumular(self, E, Qc, Kc, Bt, log_alfa, sig, partes=None):
+    def _acumular(self, E, Qc, Kc, Bt, log_alfa, sig, partes=None, pesos=None):
         """Candidate attention of all tables -> salida and the gate signals (asrn/estable.py:204-300)."""
         T = self.n_tablas
-        phi, filas = self._phi_y_valores(E)
+        phi, filas = self._phi_y_valores(E, pesos)
         if partes is not None:                                              # the generation step's value cache
             v = F.linear(_a_autocast(E), self.v.weight)
             partes.update(phi=phi, V=F.pad(v, (0, 0, 0, 1))[:, 1:])         # V[t] = W_v E[t+1], 0 at the end
@@ -186,11 +200,14 @@ class CapaASRNEstable(nn.Module):
         # sum over tables of att E[s+1]: W_v and W_o are applied together after it (see _phi_y_valores)
         return {'salida': suma, 'senales': sen, 'w_salida': ops.SmallMatmul.apply(self.o.weight, self.v.weight)}
 
-    def _repeticion(self, sig, beta, Bt, log_alfa, partes=None):
-        """vistos, hawkes (B, L, n) and racha (B, L) (asrn/estable.py:304-321)."""
+    def _repeticion(self, sig, beta, Bt, log_alfa, partes=None, ngram=None):
+        """vistos, hawkes (B, L, n) and racha (B, L) (asrn/estable.py:304-321); ngram: ops.ngram_sort(sig, ...) when
+        it already ran."""
         kappa, kappa_r = self._kappas()
-        with torch.no_grad():
-            claves, order, rep, rank_k, vistos = ops.ngram_sort(sig, self.c_vistos, self.vistos)
+        if ngram is None:
+            with torch.no_grad():
+                ngram = ops.ngram_sort(sig, self.c_vistos, self.vistos)
+        claves, order, rep, rank_k, vistos = ngram
         hawkes = ops.Hawkes.apply(Bt, log_alfa, kappa, order, rep, rank_k)
         racha = ops.Streak.apply(beta, kappa_r, vistos)
         if partes is not None:
@@ -222,14 +239,43 @@ class CapaASRNEstable(nn.Module):
         Qc, Kc, sig, beta, Bt, log_alfa, n-gram keys and their sort, hawkes and racha)."""
         self._revisar(E)
         sig = self._firma(E) if piezas is None else firmas_de_piezas(piezas)
-        Qc, Kc, beta, log_alfa, h = self._contexto(h, con_h=True)
+        # The repetition branch (n-gram sort, Hawkes and streak scans: small, latency-bound kernels) runs on a second
+        # stream beside the producers and the candidate attention; autograd runs their backward on that stream too.
+        principal, lado = torch.cuda.current_stream(E.device), _lateral(E.device)
+        lado.wait_stream(principal)
+        with torch.cuda.stream(lado), torch.no_grad():
+            ngram = ops.ngram_sort(sig, self.c_vistos, self.vistos)
+        pesos = self._pesos()
+        Qc, Kc, beta, log_alfa, h = self._contexto(h, con_h=True, pesos=pesos)
         Bt = ops.ClockScan.apply(beta)
-        acc = self._acumular(E, Qc, Kc, Bt, log_alfa, sig, partes)
-        acc.update(self._repeticion(sig, beta, Bt, log_alfa, partes))
+        lado.wait_stream(principal)
+        with torch.cuda.stream(lado):
+            rep = self._repeticion(sig, beta, Bt, log_alfa, partes, ngram)
+        for t in (sig, beta, Bt, log_alfa):          # used on both streams: not reused before both are done
+            t.record_stream(lado)
+        acc = self._acumular(E, Qc, Kc, Bt, log_alfa, sig, partes, pesos)
+        principal.wait_stream(lado)
+        for t in list(rep.values()) + list(ngram):
+            t.record_stream(principal)
+        acc.update(rep)
         if partes is not None:
             partes.update(Qc=Qc, Kc=Kc, sig=sig, beta=beta, Bt=Bt, log_alfa=log_alfa, hawkes=acc['hawkes'],
                           racha=acc['racha'])
         return self._combinar(acc, h)
+
+
+_LATERAL = {}
+
+
+def _lateral(device):
+    """The second stream of a device (default priority), made once."""
+    i = torch.device(device).index
+    if i is None:
+        i = torch.cuda.current_device()
+    s = _LATERAL.get(i)
+    if s is None:
+        s = _LATERAL[i] = torch.cuda.Stream(device=i)
+    return s
 
 
 class _ShiftAdd(torch.autograd.Function):
@@ -250,10 +296,58 @@ class _ShiftAdd(torch.autograd.Function):
         return g, dzb, column_sums(g.reshape(-1, g.shape[-1]))
 
 
+class _Pesos(torch.autograd.Function):
+    """The fused GEMMs' weights, assembled from the parameters in one launch (ops.copy_blocks):
+    W = [W_p; W_a; W_b] (the word MLP's first layer and the context MLP's split into its E_t and E_{t-1} halves),
+    W2 = blockdiag(word second layer, context second layer) with b2 = [b_word2; b_ctx2], and Wq = [cq; ck]. The
+    backward scatters the four gradients back to the eight parameters in one launch. fp32 parameters only."""
+
+    @staticmethod
+    def forward(ctx, p0w, c0w, p2w, c2w, p2b, c2b, cqw, ckw):
+        (m, d), mc = p0w.shape, c0w.shape[0]
+        (o1, h1), (o2, h2), cf = p2w.shape, c2w.shape, cqw.shape[0]
+        dev = p0w.device
+        W = torch.empty((m + 2 * mc, d), dtype=torch.float32, device=dev)
+        W2 = torch.empty((o1 + o2, h1 + h2), dtype=torch.float32, device=dev)
+        b2 = torch.empty((1, o1 + o2), dtype=torch.float32, device=dev)
+        Wq = torch.empty((2 * cf, d), dtype=torch.float32, device=dev)
+        ops.copy_blocks(_Pesos.bloques(W, W2, b2, Wq, (p0w, c0w, p2w, c2w, p2b.view(1, -1), c2b.view(1, -1), cqw,
+                                                       ckw), ida=True))
+        ctx.meta = [t.shape for t in (p0w, c0w, p2w, c2w, p2b, c2b, cqw, ckw)]
+        return W, W2, b2.view(-1), Wq
+
+    @staticmethod
+    def bloques(W, W2, b2, Wq, params, ida):
+        """(source, destination) pairs: parameters -> assembled weights (ida), or the reverse for the gradients."""
+        p0w, c0w, p2w, c2w, p2b, c2b, cqw, ckw = params
+        m, d, mc = p0w.shape[0], p0w.shape[1], c0w.shape[0]
+        o1, h1, cf = p2w.shape[0], p2w.shape[1], cqw.shape[0]
+        pares = [(p0w, W[:m]), (c0w[:, :d], W[m:m + mc]), (c0w[:, d:], W[m + mc:]), (p2w, W2[:o1, :h1]),
+                 (c2w, W2[o1:, h1:]), (p2b, b2[:, :o1]), (c2b, b2[:, o1:]), (cqw, Wq[:cf]), (ckw, Wq[cf:])]
+        if ida:
+            return pares + [(None, W2[:o1, h1:]), (None, W2[o1:, :h1])]
+        return [(b, a) for a, b in pares]
+
+    @staticmethod
+    def backward(ctx, dW, dW2, db2, dWq):
+        shapes = ctx.meta
+        dev = next(g for g in (dW, dW2, db2, dWq) if g is not None).device
+        (m, d), mc = shapes[0], shapes[1][0]
+        (o1, h1), (o2, h2), cf = shapes[2], shapes[3], shapes[6][0]
+        formas = [(m + 2 * mc, d), (o1 + o2, h1 + h2), (o1 + o2,), (2 * cf, d)]
+        gs = [torch.zeros(f, dtype=torch.float32, device=dev) if g is None else g.to(torch.float32).contiguous()
+              for g, f in zip((dW, dW2, db2, dWq), formas)]
+        grads = [torch.empty(sh, dtype=torch.float32, device=dev) for sh in shapes]
+        destinos = grads[:4] + [grads[4].view(1, -1), grads[5].view(1, -1)] + grads[6:]
+        ops.copy_blocks(_Pesos.bloques(gs[0], gs[1], gs[2].view(1, -1), gs[3], destinos, ida=False))
+        return tuple(grads)
+
+
 class _Split2(torch.autograd.Function):
     """y[..., :k] and y[..., k:] as views (the candidate kernels read both in place through their row stride). The
-    backward joins the two gradients with one concatenation; slicing's own backward would zero-fill a copy of y per
-    part and add them."""
+    backward hands on the buffer both gradients live in when they arrive as its two column blocks (the candidate
+    backward writes them so), and otherwise joins them with one concatenation; slicing's own backward would zero-fill
+    a copy of y per part and add them."""
 
     @staticmethod
     def forward(ctx, y, k):
@@ -263,6 +357,12 @@ class _Split2(torch.autograd.Function):
     @staticmethod
     def backward(ctx, ga, gb):
         k, n = ctx.k, ctx.shape[-1]
+        if (ga is not None and gb is not None and ga.dim() == 3 and ga.dtype == gb.dtype and ga.stride() == gb.stride()
+                and ga.stride(-1) == 1 and ga.stride(1) == n and ga.stride(0) == ga.shape[1] * n
+                and gb.storage_offset() == ga.storage_offset() + k and ga.untyped_storage().data_ptr()
+                == gb.untyped_storage().data_ptr()
+                and ga.untyped_storage().nbytes() >= ga.element_size() * (ga.storage_offset() + ga.shape[0] * ga.stride(0))):
+            return ga.as_strided(ctx.shape, (ga.stride(0), n, 1), ga.storage_offset()), None
         ref = ga if ga is not None else gb
         if ga is None:
             ga = torch.zeros(ctx.shape[:-1] + (k,), dtype=ref.dtype, device=ref.device)

@@ -33,7 +33,8 @@ struct Cand {
   // straight from the projection of every position; the backward then writes dV at p + 1, and zeros at 0). dV has
   // V's layout: the same row stride ldv.
   int64_t ldv; int vshift;
-  int64_t ldq;   // row stride of Qc and Kc (cf for dense rows; more when both are column blocks of one projection)
+  int64_t ldq;   // row stride of Qc and Kc (cf for dense rows; more when both are column blocks of one projection),
+                 // and of dQc and dKc
   const double* Bt; const float* la; const float* w_suf; const float* gamma;
   const int32_t* order; const int32_t* win; const int32_t* rank;
   int64_t B, L;
@@ -738,7 +739,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
     const float sds = table_sum(S, a.T, G, [&](int m) { return S.ua[m]; });
     const float sdt = table_sum(S, a.T, G, [&](int m) { return S.ua[m] * S.ub[S.uid[m]]; });
     if (lead) {
-      part[tg] = sdt;
+      part[tg] = sdt / (float)a.C;                     // d gamma_tau: the rate is gamma / C
       dbq_t = -rate_of(a, tg) * sds;
     }
   }
@@ -761,7 +762,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
         *reinterpret_cast<float4*>(a.dphi + tok * a.P + f0) =
             make_float4(gq[c].x * a.sp, gq[c].y * a.sp, gq[c].z * a.sp, gq[c].w * a.sp);
       else if (f0 < a.P + a.cf)
-        *reinterpret_cast<float4*>(a.dQc + tok * a.cf + (f0 - a.P)) =
+        *reinterpret_cast<float4*>(a.dQc + tok * a.ldq + (f0 - a.P)) =
             make_float4(gq[c].x * a.sc, gq[c].y * a.sc, gq[c].z * a.sc, gq[c].w * a.sc);
     }
   }
@@ -890,7 +891,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH != 3) ? 5 :
         *reinterpret_cast<float4*>(a.dphi + tok * a.P + f0) =
             make_float4(S.ua[f0] + gk[c].x, S.ua[f0 + 1] + gk[c].y, S.ua[f0 + 2] + gk[c].z, S.ua[f0 + 3] + gk[c].w);
       else if (f0 < a.P + a.cf)
-        *reinterpret_cast<float4*>(a.dKc + tok * a.cf + (f0 - a.P)) = gk[c];
+        *reinterpret_cast<float4*>(a.dKc + tok * a.ldq + (f0 - a.P)) = gk[c];
     }
   }
   const float sla = wave_sum_u(dla);
@@ -1051,7 +1052,8 @@ extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float
   a.vshift = v_shift;
   a.ldq = ldq;
   if (check_args(a, "asrn_candidates_bwd")) return 1;
-  ASRN_REQUIRE(((uintptr_t)dV & 15) == 0, "asrn_candidates_bwd: dV must be 16-byte aligned (rows of stride ldv)");
+  ASRN_REQUIRE(((uintptr_t)dV & 15) == 0 && ((uintptr_t)dQc & 15) == 0 && ((uintptr_t)dKc & 15) == 0,
+               "asrn_candidates_bwd: dV, dQc and dKc must be 16-byte aligned (rows of stride ldv, ldq)");
   if (B == 0 || L == 0) return 0;
   a.dsal = dsalida; a.ent = entries; a.dphi = dphi; a.dV = dV; a.dQc = dQc; a.dKc = dKc; a.dBt = dBt;
   a.dla = dlog_alfa; a.partials = partials;

@@ -5,6 +5,8 @@ torch's current stream. They replace the reference's fused-op layer: _Casilleros
 _Escaneo / escaneo (asrn/nucleo.py:188-196, 518-537), the stable argsorts (asrn/estable.py:283, nucleo:693-701) and
 the clock cumsum (asrn/estable.py:418).
 """
+import ctypes
+
 import torch
 
 from . import _lib
@@ -52,10 +54,11 @@ def bucket_sort(phi, T, nb, C):
     phi = _c(phi, torch.float32)
     B, L, P = phi.shape
     ids = torch.empty((B * T, L), dtype=I32, device=dev)
-    order = torch.zeros_like(ids)          # zero-filled: every index a later kernel reads is in range
-    ids_s = torch.zeros_like(ids)
-    rank = torch.zeros((B, L, T), dtype=I32, device=dev)
-    win = torch.zeros((B, L, T), dtype=I32, device=dev)
+    # order, ids_sorted, rank and win share one zero-filled buffer (one fill): every index a later kernel reads is
+    # in range even if a sort were wrong; a correct sort overwrites all of it
+    buf = torch.zeros((4, B * T * L), dtype=I32, device=dev)
+    order, ids_s = buf[0].view(B * T, L), buf[1].view(B * T, L)
+    rank, win = buf[2].view(B, L, T), buf[3].view(B, L, T)
     call('asrn_bucket_sort', ptr(phi), B, L, T, nb, P, C, ptr(ids), ptr(order), ptr(ids_s), ptr(rank), ptr(win),
          stream_of(dev))
     return ids, order, ids_s, rank, win
@@ -86,8 +89,9 @@ def ngram_sort(sig, coef, n):
     keys = torch.empty((B, L, n), dtype=torch.float64, device=dev)
     order = torch.empty((B, n, L), dtype=I32, device=dev)
     rep = torch.empty((B, n, L), dtype=torch.uint8, device=dev)
-    rank_k = torch.zeros((B, n, L), dtype=I32, device=dev)   # zero-filled: every index read later is in range
-    vistos = torch.zeros((B, L, n), dtype=torch.float32, device=dev)
+    buf = torch.zeros((2, B * n * L), dtype=I32, device=dev)   # one fill: every index read later is in range
+    rank_k = buf[0].view(B, n, L)
+    vistos = buf[1].view(torch.float32).view(B, L, n)              # int32 zeros are fp32 zeros
     wsb = query('asrn_ngram_sort_workspace', B, L, n)
     ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
     call('asrn_ngram_sort', ptr(sig), ptr(coef), B, L, n, ptr(keys), ptr(order), ptr(rep), ptr(rank_k), ptr(vistos),
@@ -206,6 +210,25 @@ class Producer(torch.autograd.Function):
             db = column_sums(dy2[:, :m + mc])
             dbw, dbc = db[:m], db[m:]
         return dE, dW, dbw, dbc, None, None
+
+
+def copy_blocks(blocks):
+    """One launch of asrn_copy_blocks: blocks is a list of (src, dst) 2-D fp32 device views of equal shape with unit
+    column stride (src None: dst is filled with zeros)."""
+    n = len(blocks)
+    if n == 0:
+        return
+    dev = _dev(blocks[0][1])
+    for src, dst in blocks:
+        if dst.dim() != 2 or dst.dtype != torch.float32 or dst.stride(1) != 1 or (
+                src is not None and (src.shape != dst.shape or src.dtype != torch.float32 or src.stride(1) != 1)):
+            raise ValueError('copy_blocks: blocks are 2-D fp32 views of one shape with unit column stride')
+    arr = lambda ty, xs: (ty * n)(*xs)
+    call('asrn_copy_blocks', n, arr(ctypes.c_void_p, [None if s is None else s.data_ptr() for s, _ in blocks]),
+         arr(ctypes.c_void_p, [d.data_ptr() for _, d in blocks]),
+         arr(ctypes.c_int64, [d.shape[1] if s is None else s.stride(0) for s, d in blocks]),
+         arr(ctypes.c_int64, [d.stride(0) for _, d in blocks]), arr(ctypes.c_int64, [d.shape[0] for _, d in blocks]),
+         arr(ctypes.c_int64, [d.shape[1] for _, d in blocks]), stream_of(dev))
 
 
 class SmallMatmul(torch.autograd.Function):
@@ -494,8 +517,16 @@ class Candidates(torch.autograd.Function):
         col = V.storage_offset() % ldv
         col = col if col + d <= ldv else 0
         dV = torch.empty((B, L, ldv), dtype=torch.float32, device=dev)[..., col:col + d]
-        dQc = torch.empty((B, L, cf), dtype=torch.float32, device=dev)
-        dKc = torch.empty((B, L, cf), dtype=torch.float32, device=dev)
+        # dQc and dKc take the layout of Qc and Kc: when both are column blocks of one projection (row stride ldq),
+        # the same blocks of one (B, L, ldq) buffer, which _Split2's backward hands on whole
+        ldq = Qc.stride(1)
+        qo, ko = Qc.storage_offset() % ldq, Kc.storage_offset() % ldq
+        if Qc.data_ptr() != Kc.data_ptr() and qo + cf <= ldq and ko + cf <= ldq and (qo + cf <= ko or ko + cf <= qo):
+            dq = torch.empty((B, L, ldq), dtype=torch.float32, device=dev)
+            dQc, dKc = dq[..., qo:qo + cf], dq[..., ko:ko + cf]
+        else:
+            dQc = torch.empty((B, L, ldq), dtype=torch.float32, device=dev)[..., :cf]
+            dKc = torch.empty((B, L, ldq), dtype=torch.float32, device=dev)[..., :cf]
         dBt = torch.empty_like(Bt)
         dla = torch.empty_like(la)
         partials = torch.empty((B * L, T + K + 1), dtype=torch.float32, device=dev)
@@ -504,7 +535,7 @@ class Candidates(torch.autograd.Function):
              ptr(dsal), ptr(ent),
              ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(partials), stream_of(dev))
         part = column_sums(partials)          # per-query partials summed over the tokens (no memset-cleared reduction)
-        dgamma = part[:T] / C
+        dgamma = part[:T]
         dw = part[T:]
         return (dphi[..., :P0].to(tp), dV.to(tv), dQc[..., :cf0].to(tq), dKc[..., :cf0].to(tk), dBt, dla.to(tl), dw,
                 dgamma, None, None, None, None, None)

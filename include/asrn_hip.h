@@ -84,9 +84,10 @@ int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* 
  * d w_suf) and a key pass (key-side gradients from att and ds at the slots of the queries that see the key: the
  * next <= C same-bucket sorted ranks).
  *   dsalida (B, L, d); entries from asrn_candidates_fwd (its [..., 1] receives ds, read back by the key pass)
- *   dphi (B, L, P), dQc, dKc (B, L, cf) dense, dBt (B, L) fp64, dlog_alfa (B, L) out (overwritten); dV has V's
- *   layout (row stride ldv, 16-byte aligned) and, with v_shift = 1, is the gradient of the per-position projection
- *   (row 0 of each batch row is 0): its d columns of every row are written, the rest of a row is left alone
+ *   dphi (B, L, P) dense, dBt (B, L) fp64, dlog_alfa (B, L) out (overwritten); dV, dQc and dKc have the layout of
+ *   V, Qc and Kc (row strides ldv and ldq, 16-byte aligned): their d (cf) columns of every row are written, the rest
+ *   of a row is left alone; with v_shift = 1, dV is the gradient of the per-position rows (row 0 of each batch row
+ *   is 0)
  *   partials (B*L, T + K + 1) fp32 out: per query, d gamma_tau then d w_suf[0..K]; the caller sums over rows. */
 int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                         const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
@@ -151,6 +152,14 @@ int asrn_column_sums(const void* x, int32_t bf16, int64_t rows, int64_t cols, in
  * dimensions lda, ldb, ldc; each element sums over k in order. M, N, K <= 8192. */
 int asrn_small_gemm(const float* A, int64_t lda, int32_t trans_a, const float* B, int64_t ldb, int32_t trans_b,
                     float* C, int64_t ldc, int32_t M, int32_t N, int32_t K, void* stream);
+
+/* ---- batched block copies -------------------------------------------------------------------------------------
+ * No counterpart in the reference's FFI: the layer assembles its fused GEMMs' weights from the parameters (the
+ * torch.cat / block_diag calls it would make every step) and scatters their gradients back, each in one launch.
+ * n <= 16 blocks, given as host arrays: block i copies rows[i] x cols[i] fp32 from src[i] (row stride sld[i]) to
+ * dst[i] (row stride dld[i]), or writes zeros when src[i] is null. */
+int asrn_copy_blocks(int32_t n, const float* const* src, float* const* dst, const int64_t* sld, const int64_t* dld,
+                     const int64_t* rows, const int64_t* cols, void* stream);
 
 /* ---- a9: clock --------------------------------------------------------------------------------------------------
  * Bt = cumsum(beta) over L in fp64 (asrn/estable.py:418). reverse != 0 computes the suffix sums instead (the

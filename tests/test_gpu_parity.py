@@ -432,6 +432,31 @@ def test_column_sums_exact(rows, cols, ld, off, bf16):
     assert torch.equal(out.cpu().double(), ref.double())
 
 
+@pytest.mark.parametrize('d,kw', [(256, {}), (32, dict(n_tablas=5, tablas_contexto=2, n_bits=3, confirmar=6))])
+def test_weight_assembly_is_exact(d, kw):
+    """The one-launch assembly of the fused GEMMs' weights (asrn_copy_blocks) equals torch.cat / block_diag of the
+    parameters bit for bit, and its backward hands each parameter exactly its block of the gradients."""
+    say('weight assembly', d, kw)
+    from asrn_amd.capa import _Pesos
+    layer = synth.move_params(CapaASRNEstable(d, **kw), seed=7).to(DEV)
+    pal, ctx = layer.afin_palabra, layer.afin_contexto
+    mc = ctx[0].out_features
+    ref = [torch.cat([pal[0].weight, ctx[0].weight.view(mc, 2, d).transpose(0, 1).reshape(2 * mc, d)]),
+           torch.block_diag(pal[2].weight, ctx[2].weight), torch.cat([pal[2].bias, ctx[2].bias]),
+           torch.cat([layer.cq.weight, layer.ck.weight])]
+    got = layer._pesos()
+    g = torch.Generator().manual_seed(d)
+    gs = [torch.randn(r.shape, generator=g).to(DEV) for r in ref]
+    params = [pal[0].weight, ctx[0].weight, pal[2].weight, ctx[2].weight, pal[2].bias, ctx[2].bias, layer.cq.weight,
+              layer.ck.weight]
+    want = torch.autograd.grad(sum((r * x).sum() for r, x in zip(ref, gs)), params)
+    have = torch.autograd.grad(sum((r * x).sum() for r, x in zip(got, gs)), params)
+    for r, x in zip(ref, got):
+        assert torch.equal(r, x)
+    for a, b in zip(want, have):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize('M,N,K', [(256, 256, 256), (33, 70, 129), (1, 17, 5), (512, 96, 768)])
 def test_small_matmul_vs_fp64(M, N, K):
     """asrn_small_gemm through ops.SmallMatmul (the layer's W_o W_v): the product and both gradients against fp64
