@@ -186,8 +186,10 @@ class CapaASRNEstable(nn.Module):
 
     # --- hot path (HIP) ---------------------------------------------------------------------------------------------
 
-    def _acumular(self, E, Qc, Kc, Bt, log_alfa, sig, partes=None, pesos=None):
-        """Candidate attention of all tables -> salida and the gate signals (asrn/estable.py:204-300)."""
+    def _acumular(self, E, Qc, Kc, Bt, log_alfa, sig, partes=None, pesos=None, esperar=None):
+        """Candidate attention of all tables -> salida and the gate signals (asrn/estable.py:204-300). esperar: called
+        before the candidate kernels, after the producers and the bucket sort (the point where the context inputs
+        must be ready)."""
         T = self.n_tablas
         phi, filas = self._phi_y_valores(E, pesos)
         if partes is not None:                                              # the generation step's value cache
@@ -195,6 +197,8 @@ class CapaASRNEstable(nn.Module):
             partes.update(phi=phi, V=F.pad(v, (0, 0, 0, 1))[:, 1:])         # V[t] = W_v E[t+1], 0 at the end
         _, order, _, rank, win = ops.bucket_sort(phi.detach(), T, self.n_bits, self.chunk)
         shape = dict(T=T, Tc=self.tablas_contexto, C=self.chunk, K=self.sufijo, v_shift=1)
+        if esperar is not None:
+            esperar()
         suma, sen = ops.Candidates.apply(phi, filas, Qc, Kc, Bt, log_alfa, self.w_sufijo, self.gamma, sig, order,
                                          win, rank, shape)
         # sum over tables of att E[s+1]: W_v and W_o are applied together after it (see _phi_y_valores)
@@ -239,23 +243,27 @@ class CapaASRNEstable(nn.Module):
         Qc, Kc, sig, beta, Bt, log_alfa, n-gram keys and their sort, hawkes and racha)."""
         self._revisar(E)
         sig = self._firma(E) if piezas is None else firmas_de_piezas(piezas)
-        # The repetition branch (n-gram sort, Hawkes and streak scans: small, latency-bound kernels) runs on a second
-        # stream beside the producers and the candidate attention; autograd runs their backward on that stream too.
+        # Two streams: the context producer (LayerNorm, Qc/Kc, the clock) and the repetition branch (n-gram sort,
+        # Hawkes and streak scans: small, latency-bound kernels) run on the second one, beside the hash producers and
+        # the bucket sort; the candidate attention waits for the context only. Autograd runs each op's backward on
+        # the stream of its forward, so the backward overlaps the same way.
         principal, lado = torch.cuda.current_stream(E.device), _lateral(E.device)
-        lado.wait_stream(principal)
-        with torch.cuda.stream(lado), torch.no_grad():
-            ngram = ops.ngram_sort(sig, self.c_vistos, self.vistos)
         pesos = self._pesos()
-        Qc, Kc, beta, log_alfa, h = self._contexto(h, con_h=True, pesos=pesos)
-        Bt = ops.ClockScan.apply(beta)
         lado.wait_stream(principal)
         with torch.cuda.stream(lado):
+            Qc, Kc, beta, log_alfa, h = self._contexto(h, con_h=True, pesos=pesos)
+            Bt = ops.ClockScan.apply(beta)
+            contexto_listo = torch.cuda.Event()
+            contexto_listo.record(lado)
+            with torch.no_grad():
+                ngram = ops.ngram_sort(sig, self.c_vistos, self.vistos)
             rep = self._repeticion(sig, beta, Bt, log_alfa, partes, ngram)
-        for t in (sig, beta, Bt, log_alfa):          # used on both streams: not reused before both are done
-            t.record_stream(lado)
-        acc = self._acumular(E, Qc, Kc, Bt, log_alfa, sig, partes, pesos)
+        for t in [sig] + ([pesos[3]] if pesos is not None else []):
+            t.record_stream(lado)                      # made here, used there: not reused before both are done
+        acc = self._acumular(E, Qc, Kc, Bt, log_alfa, sig, partes, pesos,
+                             esperar=lambda: principal.wait_event(contexto_listo))
         principal.wait_stream(lado)
-        for t in list(rep.values()) + list(ngram):
+        for t in [Qc, Kc, beta, Bt, log_alfa, h] + list(rep.values()) + list(ngram):
             t.record_stream(principal)
         acc.update(rep)
         if partes is not None:
