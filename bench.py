@@ -10,8 +10,9 @@ instead. The per-kernel device events (roofline, hip_aggregate, kernels) come fr
 steps, since events recorded while capturing are not replayed. Prints one JSON line with the driver's keys plus:
   roofline      the dominant HIP kernel: algorithmic bytes per launch / its mean launch time (device events recorded
                 on the stream it runs on), against MI355X's 8 TB/s
-  hip_aggregate all HIP kernels: 21,276 B/token (cfg2) x tokens / (8 TB/s x their summed time per step)
-  layer         whole-layer tokens/s and its HBM fraction at 25,876 B/token (the fp32 GEMMs stay PyTorch)
+  hip_aggregate all HIP kernels: 26,640 B/token (cfg2) x tokens / (8 TB/s x their summed time per step)
+  layer         whole-layer tokens/s and its HBM fraction at 45,520 B/token (the HIP kernels' bytes plus the GEMMs'
+                operands and results, 18,880 B/token at cfg2)
   decode        the O(1) generation step of one layer (BASELINE.json configs[4] at one layer): per-token latency
                 against the context, 1K to 64K, and its slope
   cpu_baseline  the CPU oracle (oracle/layer.py, PyTorch on the host cores) on the same workload
@@ -51,21 +52,37 @@ def gate_bytes(d, n, a=4):
 
 def context_bytes(d):
     """The fused LayerNorm + clock projection (asrn_context_fwd/bwd), fp32: h in, hh, (mean, rstd, u) and beta (fp64),
-    log_alfa out; the backward reads h, dhh, the stats, dbeta, dlog_alfa and writes dh."""
-    return 4 * d + 4 * d + 16 + 8 + 4, 4 * d + 4 * d + 16 + 8 + 4 + 4 * d
+    log_alfa out; the backward reads h, dhh, the gate's dh, the stats, dbeta, dlog_alfa and writes dh."""
+    return 4 * d + 4 * d + 16 + 8 + 4, 4 * d + 4 * d + 4 * d + 16 + 8 + 4 + 4 * d
 
 
-def hip_bytes_per_token(d, P, cf, T, n=4, a=4):
+def hidden_bytes(m=64, mc=64):
+    """The hash MLPs' hidden layer (asrn_hidden_fwd/bwd), fp32: the forward reads the three first-layer blocks and
+    writes g; the backward reads them and dg and writes their gradients."""
+    return 4 * (m + 2 * mc) + 4 * (m + mc), 4 * (m + 2 * mc) + 4 * (m + mc) + 4 * (m + 2 * mc)
+
+
+def hip_bytes_per_token(d, P, cf, T, n=4, a=4, m=64, mc=64, K=4):
     """All HIP kernels of one fwd+bwd, each distinct tensor read once and written once: hash + bucket sort (phi in, ids
-    and order out), clock 16 + 16, n-gram sort 28, Hawkes/streak scans 60 + 100, candidates, gate, context producer.
-    cfg2 fp32: 512 + 32 + 28 + 160 + 7,044 + 8,324 + 5,176 = 21,276."""
+    and order out), clock 16 + 16, n-gram sort 28, Hawkes/streak scans 60 + 100, candidates, gate, context producer,
+    hidden layer, and the column sums of the bias gradients and the candidates' per-token partials (the weight
+    gradients' slab sums scale with the weights, not the tokens, and are left out).
+    cfg2 fp32: 512 + 32 + 28 + 160 + 7,044 + 8,324 + 6,200 + 3,328 + 1,012 = 26,640."""
     cand = algorithmic_bytes(d, P, cf, T, a)
+    colsums = 4 * (m + mc) + 4 * P + 4 * (T + K + 1)
     return (P * a + 8 * T + 32 + 28 + 160 + sum(cand.values()) + sum(gate_bytes(d, n, a))
-            + sum(context_bytes(d)))
+            + sum(context_bytes(d)) + sum(hidden_bytes(m, mc)) + colsums)
 
 
-# whole layer: the above plus the GEMM-boundary tensors and their gradients (cfg2 fp32; cfg3 bf16)
-LAYER_BYTES_PER_TOKEN = {'fp32': 25876, 'bf16': 24436}
+def gemm_bytes_per_token(d, P, cf, a=4, m=64, mc=64):
+    """Operands and results of the layer's GEMMs per token, each read or written once (activations in a bytes;
+    weights are per step, not per token): forward E -> [hp|za|zb], g -> phi, hh -> [Qc|Kc], sum -> W_o W_v sum;
+    backward the input gradients (the E one accumulating into the candidates' dE) and the weight gradients (both
+    operands read). cfg2 fp32: 5,952 + 12,928 = 18,880."""
+    h, q = m + 2 * mc, 2 * cf
+    fwd = (d + h) + ((m + mc) + P) + (d + q) + (d + d)
+    bwd = (d + d) + 2 * d + (P + m + mc) + (P + m + mc) + (q + d) + (q + d) + (h + 2 * d) + (h + d)
+    return a * (fwd + bwd)
 
 
 TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'cfg2_traffic.json')
@@ -293,7 +310,8 @@ def main():
     dom_us = per_call[dom]['mean_us']
     achieved = algo[dom] * tokens / (dom_us * 1e-6)
     hip_ms_per_step = sum(v['total_ms'] for v in per_call.values()) / args.steps
-    hip_b = hip_bytes_per_token(d, P, cf, T, layer.vistos, a=2 if bf16 else 4)
+    hip_b = hip_bytes_per_token(d, P, cf, T, layer.vistos, a=2 if bf16 else 4, K=layer.sufijo)
+    layer_b = hip_b + gemm_bytes_per_token(d, P, cf, a=2 if bf16 else 4)
 
     out = {
         'metric': METRIC, 'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps,
@@ -310,7 +328,7 @@ def main():
         'hip_aggregate': {'bytes_per_token': hip_b, 'hip_ms_per_step': round(hip_ms_per_step, 4),
                           'frac': round(hip_b * tokens / (HBM_PEAK * hip_ms_per_step * 1e-3), 4)},
         'layer': {'tokens_per_s': round(value, 1),
-                  'hbm_frac': round(LAYER_BYTES_PER_TOKEN[dtype] * tokens / (HBM_PEAK * wall), 4)},
+                  'bytes_per_token': layer_b, 'hbm_frac': round(layer_b * tokens / (HBM_PEAK * wall), 4)},
         'kernels': {n: {k: round(v, 3) if isinstance(v, float) else v for k, v in s.items()}
                     for n, s in sorted(per_call.items(), key=lambda kv: -kv[1]['total_ms'])},
     }
