@@ -43,6 +43,9 @@ struct Cand {
   // per-entry weights (B*L, T, C, 2): for the key at distance j + 1 before the query in a table, at slot j, its
   // attention weight (the forward writes it) and its ds (the backward's query pass writes it for the key pass)
   float* ent;
+  // the query's deduplicated candidate list, one record per token (see RecLayout): written by the forward when not
+  // null, read by the backward's query pass instead of its own gather and dedupe
+  uint8_t* lists; int64_t rec;
   // forward outputs
   float* salida; float* signals;
   // backward
@@ -501,6 +504,70 @@ __device__ __forceinline__ void load_entries(const Cand& a, int M, const Scratch
   }
 }
 
+// A query's candidate list as the forward leaves it for the backward's query pass, at lists + token * rec (bytes):
+//   header  (T + 2) u16: the table offsets off[0..T] (entries of table tau are [off[tau], off[tau + 1])), then NU
+//   e16     per entry m < M = off[T]: its unique | table << 8
+//   upos    per unique u < NU: the candidate's position (int32)
+//   ub      per unique: fp32(Bt_k - Bt_q)
+//   uell    per unique: the suffix-match length (u8)
+// Every region is sized for T * C (the most entries and uniques a query can have); 16-byte aligned.
+struct RecLayout { int64_t e16, upos, ub, uell, size; };
+__host__ __device__ inline RecLayout rec_layout(int T, int C) {
+  const int64_t tc = (int64_t)T * C;
+  RecLayout r;
+  r.e16 = 128;                                    // (T + 2) u16 <= 68 bytes
+  r.upos = (r.e16 + 2 * tc + 15) / 16 * 16;
+  r.ub = r.upos + 4 * tc;
+  r.uell = r.ub + 4 * tc;
+  r.size = (r.uell + tc + 15) / 16 * 16;
+  return r;
+}
+
+// The query pass's view of a record: S.off, S.key (the table of each entry; the position part is not needed there),
+// S.uid, S.upos, S.ub, S.uell, and S.ud cleared. The first 64 entries and uniques are loaded with the header in one
+// round (most queries have no more); loads past M or NU stay inside the record and are ignored.
+__device__ __forceinline__ void load_record(const Cand& a, const uint8_t* rec, Scratch& S, int& M, int& NU) {
+  const int lane = lane_id();
+  const RecLayout R = rec_layout(a.T, a.C);
+  const int tc = a.T * a.C;
+  const uint16_t* hdr = reinterpret_cast<const uint16_t*>(rec);
+  const uint16_t* e16 = reinterpret_cast<const uint16_t*>(rec + R.e16);
+  const int32_t* upos = reinterpret_cast<const int32_t*>(rec + R.upos);
+  const float* ub = reinterpret_cast<const float*>(rec + R.ub);
+  const uint8_t* uell = rec + R.uell;
+  const int i0 = lane < tc ? lane : 0;
+  const int h = lane <= a.T + 1 ? (int)hdr[lane] : 0;
+  const int e0 = e16[i0];
+  const int p0 = upos[i0];
+  const float b0 = ub[i0];
+  const int l0 = uell[i0];
+  M = readlane_i(h, a.T);
+  NU = readlane_i(h, a.T + 1);
+  if (lane <= a.T) S.off[lane] = h;
+  if (lane < M) {
+    S.key[lane] = e0 >> 8;
+    S.uid[lane] = (uint16_t)(e0 & 255);
+  }
+  for (int m = kWave + lane; m < M; m += kWave) {
+    const int e = e16[m];
+    S.key[m] = e >> 8;
+    S.uid[m] = (uint16_t)(e & 255);
+  }
+  if (lane < NU) {
+    S.upos[lane] = p0;
+    S.ub[lane] = b0;
+    S.uell[lane] = (uint8_t)l0;
+    S.ud[lane] = 0.f;
+  }
+  for (int u = kWave + lane; u < NU; u += kWave) {
+    S.upos[u] = upos[u];
+    S.ub[u] = ub[u];
+    S.uell[u] = uell[u];
+    S.ud[u] = 0.f;
+  }
+  wave_lds_sync();
+}
+
 // ---------------------------------------------------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------------------------------------------------
@@ -514,6 +581,15 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
   const int64_t tok = b * a.L + t;
   const int M = RING ? gather_rings(a, b, t, S) : gather(a, b, t, true, S);
   const int NU = dedupe(a, M, S);
+  uint8_t* rec = (!RING && a.lists) ? a.lists + tok * a.rec : nullptr;
+  const RecLayout R = rec_layout(a.T, a.C);
+  if (rec) {
+    uint16_t* hdr = reinterpret_cast<uint16_t*>(rec);
+    uint16_t* e16 = reinterpret_cast<uint16_t*>(rec + R.e16);
+    if (lane <= a.T) hdr[lane] = (uint16_t)S.off[lane];
+    if (lane == a.T + 1) hdr[lane] = (uint16_t)NU;
+    for (int m = lane; m < M; m += kWave) e16[m] = (uint16_t)(((S.key[m] & 31) << 8) | S.uid[m]);
+  }
   float4 qf[F4];
   feat_row<F4>(feat_lanes<F4>(a, a.Qc, true), (uint32_t)tok, qf);
   unique_bases<F4>(a, b, t, NU, false, qf, S);
@@ -524,9 +600,15 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
   for (int u = lane; u < NU; u += kWave) {
     const int64_t k = S.upos[u];
     const int ell = suffix_len_of(sigb, mine, t, k, a.K);
+    const float db = (float)(a.Bt[b * a.L + k] - bq);
     S.ua[u] = (S.ua[u] + a.w_suf[ell]) + a.la[b * a.L + k];
-    S.ub[u] = (float)(a.Bt[b * a.L + k] - bq);
+    S.ub[u] = db;
     S.uc[u] = 0.f;
+    if (rec) {
+      reinterpret_cast<int32_t*>(rec + R.upos)[u] = (int32_t)k;
+      reinterpret_cast<float*>(rec + R.ub)[u] = db;
+      rec[R.uell + u] = (uint8_t)ell;
+    }
   }
   wave_lds_sync();
 
@@ -668,17 +750,22 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   const int lane = lane_id(), half = lane >> 5;
   const int64_t b = tok / a.L, t = tok % a.L;
 
-  const int M = gather(a, b, t, true, S);
-  const int NU = dedupe(a, M, S);
-  const float* sigb = a.sig + b * a.L;
-  float mine[4];
-  own_suffix_of(sigb, t, a.K, mine);
-  const double bq = a.Bt[tok];
-  for (int u = lane; u < NU; u += kWave) {
-    const int64_t k = S.upos[u];
-    S.uell[u] = (uint8_t)suffix_len_of(sigb, mine, t, k, a.K);
-    S.ub[u] = (float)(a.Bt[b * a.L + k] - bq);
-    S.ud[u] = 0.f;
+  int M, NU;
+  if (a.lists) {             // the forward's list: no gather, dedupe or per-candidate clock and suffix loads
+    load_record(a, a.lists + tok * a.rec, S, M, NU);
+  } else {
+    M = gather(a, b, t, true, S);
+    NU = dedupe(a, M, S);
+    const float* sigb = a.sig + b * a.L;
+    float mine[4];
+    own_suffix_of(sigb, t, a.K, mine);
+    const double bq = a.Bt[tok];
+    for (int u = lane; u < NU; u += kWave) {
+      const int64_t k = S.upos[u];
+      S.uell[u] = (uint8_t)suffix_len_of(sigb, mine, t, k, a.K);
+      S.ub[u] = (float)(a.Bt[b * a.L + k] - bq);
+      S.ud[u] = 0.f;
+    }
   }
   // dp_u = <dO_q, V_u> (ends with a wave sync)
   float4 dO[DCH], unused[DCH];
@@ -1026,7 +1113,7 @@ extern "C" int asrn_candidates_fwd(const float* phi, const float* V, const float
                                    int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
                                    int32_t Tc, int32_t C, float scale_phi, float scale_c, int64_t ldv,
                                    int32_t v_shift, int64_t ldq, float* salida, float* signals, float* entries,
-                                   void* stream) {
+                                   uint8_t* lists, void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
                 scale_phi, scale_c);
   a.ldv = ldv;
@@ -1035,6 +1122,8 @@ extern "C" int asrn_candidates_fwd(const float* phi, const float* V, const float
   if (check_args(a, "asrn_candidates_fwd")) return 1;
   if (B == 0 || L == 0) return 0;
   a.salida = salida; a.signals = signals; a.ent = entries;
+  a.lists = lists; a.rec = rec_layout(T, C).size;
+  ASRN_REQUIRE(((uintptr_t)lists & 15) == 0, "asrn_candidates_fwd: lists must be 16-byte aligned");
   return dispatch<LaunchFwd>(a, (hipStream_t)stream);
 }
 
@@ -1043,7 +1132,8 @@ extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float
                                    const float* gamma, const int32_t* order, const int32_t* win, const int32_t* rank,
                                    int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
                                    int32_t Tc, int32_t C, float scale_phi, float scale_c, int64_t ldv,
-                                   int32_t v_shift, int64_t ldq, const float* dsalida, float* entries, float* dphi,
+                                   int32_t v_shift, int64_t ldq, const float* dsalida, float* entries,
+                                   const uint8_t* lists, float* dphi,
                                    float* dV, float* dQc, float* dKc, double* dBt, float* dlog_alfa, float* partials,
                                    void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
@@ -1055,9 +1145,16 @@ extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float
   ASRN_REQUIRE(((uintptr_t)dV & 15) == 0 && ((uintptr_t)dQc & 15) == 0 && ((uintptr_t)dKc & 15) == 0,
                "asrn_candidates_bwd: dV, dQc and dKc must be 16-byte aligned (rows of stride ldv, ldq)");
   if (B == 0 || L == 0) return 0;
+  a.lists = const_cast<uint8_t*>(lists); a.rec = rec_layout(T, C).size;
+  ASRN_REQUIRE(((uintptr_t)lists & 15) == 0, "asrn_candidates_bwd: lists must be 16-byte aligned");
   a.dsal = dsalida; a.ent = entries; a.dphi = dphi; a.dV = dV; a.dQc = dQc; a.dKc = dKc; a.dBt = dBt;
   a.dla = dlog_alfa; a.partials = partials;
   return dispatch<LaunchBwd>(a, (hipStream_t)stream);
+}
+
+extern "C" int64_t asrn_candidates_record_bytes(int32_t T, int32_t C) {
+  if (T < 1 || C < 1) return -1;
+  return rec_layout(T, C).size;
 }
 
 extern "C" int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* win, const int32_t* rank,

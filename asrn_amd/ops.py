@@ -494,11 +494,14 @@ class Candidates(torch.autograd.Function):
         salida = torch.empty((B, L, d), dtype=torch.float32, device=dev)
         signals = torch.empty((B, L, 4), dtype=torch.float32, device=dev)
         ent = torch.empty((B, L, T, C, 2), dtype=torch.float32, device=dev)  # only the valid slots are written
+        # each query's deduplicated candidate list, for the backward's query pass (shape['listas'] = False: none)
+        listas = (torch.empty((B, L, query('asrn_candidates_record_bytes', T, C)), dtype=torch.uint8, device=dev)
+                  if shape.get('listas', True) else None)
         call('asrn_candidates_fwd', ptr(ins['phi']), ptr(ins['V']), ptr(ins['Qc']), ptr(ins['Kc']), ptr(ins['sig']),
              ptr(ins['Bt']), ptr(ins['la']), ptr(ins['w']), ptr(ins['g']), ptr(order), ptr(win), ptr(rank), B, L, d,
              P, cf, K, T, Tc, C, sp, sc, Vk.stride(1), vs, Qk.stride(1), ptr(salida), ptr(signals), ptr(ent),
-             stream_of(dev))
-        ctx.save_for_backward(*ins.values(), order, win, rank, ent)
+             ptr(listas), stream_of(dev))
+        ctx.save_for_backward(*ins.values(), order, win, rank, ent, listas)
         ctx.meta = (B, L, P, d, cf, K, T, Tc, C, sp, sc, V.dtype, phi.dtype, Qc.dtype, Kc.dtype, log_alfa.dtype,
                     P0, cf0, vs)
         ctx.mark_non_differentiable(signals)
@@ -506,7 +509,7 @@ class Candidates(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dsal, _dsig):
-        phi, V, Qc, Kc, sig, Bt, la, w, g, order, win, rank, ent = ctx.saved_tensors
+        phi, V, Qc, Kc, sig, Bt, la, w, g, order, win, rank, ent, listas = ctx.saved_tensors
         B, L, P, d, cf, K, T, Tc, C, sp, sc, tv, tp, tq, tk, tl, P0, cf0, vs = ctx.meta
         dev = phi.device
         dsal = _c(dsal, torch.float32)
@@ -532,7 +535,7 @@ class Candidates(torch.autograd.Function):
         partials = torch.empty((B * L, T + K + 1), dtype=torch.float32, device=dev)
         call('asrn_candidates_bwd', ptr(phi), ptr(V), ptr(Qc), ptr(Kc), ptr(sig), ptr(Bt), ptr(la), ptr(w), ptr(g),
              ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ldv, vs, Qc.stride(1),
-             ptr(dsal), ptr(ent),
+             ptr(dsal), ptr(ent), ptr(listas),
              ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(partials), stream_of(dev))
         part = column_sums(partials)          # per-query partials summed over the tokens (no memset-cleared reduction)
         dgamma = part[:T]

@@ -54,6 +54,8 @@ int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t T, int32_t 
  *   entries (B, L, T, C, 2) out: [..., 0] the weight of each candidate, at [query][tau][distance - 1] (distance
  *           in sorted ranks, 1..n; slots beyond the table's n candidates are not written); [..., 1] is filled by the
  *           backward. Kept for the backward.
+ *   lists   (B*L, asrn_candidates_record_bytes(T, C)) bytes out, or null: each query's deduplicated candidate list,
+ *           which the backward's query pass then reads instead of gathering and deduplicating again.
  *   V rows: position p of batch row b is read at V + (b*L + p + v_shift) * ldv (ldv >= d, a multiple of 4, V 16-byte
  *           aligned). v_shift = 0: V as the reference passes it (V[p] = W_v E[p+1], nucleo:659, the last row 0);
  *           v_shift = 1: V is the projection W_v E of every position (e.g. a column block of a wider GEMM output,
@@ -66,7 +68,12 @@ int asrn_candidates_fwd(const float* phi, const float* V, const float* Qc, const
                         const int32_t* order, const int32_t* win, const int32_t* rank, int64_t B, int64_t L,
                         int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
                         float scale_phi, float scale_c, int64_t ldv, int32_t v_shift, int64_t ldq, float* salida,
-                        float* signals, float* entries, void* stream);
+                        float* signals, float* entries, uint8_t* lists, void* stream);
+
+/* Bytes of one token's record in the `lists` buffer (B*L records, 16-byte aligned): the query's deduplicated candidate
+ * list (table offsets, each entry's distinct candidate, the candidates' positions, clock differences and suffix
+ * lengths) as the forward builds it. */
+int64_t asrn_candidates_record_bytes(int32_t T, int32_t C);
 
 /* The candidate lists the forward and backward walk, materialized for checking (a3, a4): for each (b, t, tau) the
  * text positions of the <= C most recent earlier bucket mates in the C-slot window [s - C, s) of the sorted row
@@ -84,6 +91,7 @@ int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* 
  * d w_suf) and a key pass (key-side gradients from att and ds at the slots of the queries that see the key: the
  * next <= C same-bucket sorted ranks).
  *   dsalida (B, L, d); entries from asrn_candidates_fwd (its [..., 1] receives ds, read back by the key pass)
+ *   lists   the forward's candidate lists (same inputs), or null to gather and deduplicate again
  *   dphi (B, L, P) dense, dBt (B, L) fp64, dlog_alfa (B, L) out (overwritten); dV, dQc and dKc have the layout of
  *   V, Qc and Kc (row strides ldv and ldq, 16-byte aligned): their d (cf) columns of every row are written, the rest
  *   of a row is left alone; with v_shift = 1, dV is the gradient of the per-position rows (row 0 of each batch row
@@ -94,8 +102,8 @@ int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const
                         const int32_t* order, const int32_t* win, const int32_t* rank, int64_t B, int64_t L,
                         int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
                         float scale_phi, float scale_c, int64_t ldv, int32_t v_shift, int64_t ldq,
-                        const float* dsalida, float* entries, float* dphi, float* dV, float* dQc, float* dKc,
-                        double* dBt, float* dlog_alfa, float* partials, void* stream);
+                        const float* dsalida, float* entries, const uint8_t* lists, float* dphi, float* dV,
+                        float* dQc, float* dKc, double* dBt, float* dlog_alfa, float* partials, void* stream);
 
 /* ---- scan workspace -------------------------------------------------------------------------------------------
  * No counterpart in the reference (PyTorch allocates for it). Every scan below cuts its rows into chunks spread over

@@ -378,6 +378,34 @@ def test_candidates_cfg2_full_size():
         assert_close(grads[k], rg[k], 'grad ' + k)
 
 
+@pytest.mark.parametrize('B,L,d,T,nb,C', [(2, 900, 96, 4, 6, 16), (2, 1500, 64, 8, 3, 32), (1, 1, 64, 8, 14, 32),
+                                         (3, 700, 256, 8, 2, 8)])
+def test_candidates_lists_match_regather(B, L, d, T, nb, C):
+    """The backward's query pass reading the forward's candidate lists gives the same outputs and gradients, bit for
+    bit, as gathering and deduplicating again (few bits per table: many queries have more than 64 candidates)."""
+    say('candidate lists', B, L, d, T, nb, C)
+    P, cf = T * nb + (-(T * nb)) % 4, 16
+    g = torch.Generator().manual_seed(L + nb)
+    phi = torch.randn(B, L, P, generator=g).to(DEV)
+    V = torch.randn(B, L, d, generator=g).to(DEV)
+    Qc, Kc = torch.randn(B, L, cf, generator=g).to(DEV), torch.randn(B, L, cf, generator=g).to(DEV)
+    Bt = (torch.rand(B, L, generator=g, dtype=torch.float64) * 0.1).cumsum(1).to(DEV)
+    la = (torch.randn(B, L, generator=g) * 0.3).to(DEV)
+    sig = torch.randint(0, 7, (B, L), generator=g).float().to(DEV)
+    w, gam = torch.randn(5, generator=g).to(DEV), torch.rand(T, generator=g).to(DEV)
+    _, order, _, rank, win = ops.bucket_sort(phi[..., :T * nb].contiguous(), T, nb, C)
+    gs = torch.randn(B, L, d, generator=g).to(DEV)
+    outs = []
+    for listas in (True, False):
+        leaves = [t.detach().clone().requires_grad_() for t in (phi, V, Qc, Kc, Bt, la, w, gam)]
+        shape = dict(T=T, Tc=T // 2, C=C, K=4, listas=listas)
+        sal, sen = ops.Candidates.apply(*leaves[:6], leaves[6], leaves[7], sig, order, win, rank, shape)
+        (sal * gs).sum().backward()
+        outs.append([sal.detach(), sen] + [t.grad for t in leaves])
+    for i, (a, b) in enumerate(zip(outs[0], outs[1])):
+        assert torch.equal(a, b), f'output {i} differs'
+
+
 def test_candidates_v_shift_in_place():
     """v_shift = 1 with v a column block of a wider fp32 tensor (read in place through its row stride) against
     v_shift = 0 with the reference's shifted, contiguous V[t] = v[t+1]: the same outputs bit for bit, and dv = dV
