@@ -767,17 +767,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
       S.ud[u] = 0.f;
     }
   }
-  // dp_u = <dO_q, V_u> (ends with a wave sync)
-  float4 dO[DCH], unused[DCH];
-#pragma unroll
-  for (int ch = 0; ch < DCH; ++ch) {
-    const int dd = ch * 256 + lane * 4;
-    dO[ch] = dd < a.d ? ld4(a.dsal + tok * a.d + dd) : zero4();
-    unused[ch] = zero4();
-  }
-  unique_row_dots<DCH>(a, a.V + (b * a.L + a.vshift) * a.ldv, a.ldv, 0, NU, dO, nullptr, unused, S, S.uc);
-
-  // per entry: att from the forward and att * dp (S.ua is a per-entry buffer here)
+  // every entry's att from the forward, loaded now so that it arrives with the value rows below
   float* erow = a.ent + tok * a.T * a.C * 2;
   float att[kCh], dp[kCh];
   int tau[kCh], un[kCh], slot[kCh];
@@ -790,6 +780,22 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
     un[c] = in ? S.uid[m] : 0;
     slot[c] = in ? (e & 31) * a.C + (S.off[(e & 31) + 1] - 1 - m) : 0;
     att[c] = in ? erow[2 * slot[c]] : 0.f;
+  }
+  // dp_u = <dO_q, V_u> (ends with a wave sync)
+  float4 dO[DCH], unused[DCH];
+#pragma unroll
+  for (int ch = 0; ch < DCH; ++ch) {
+    const int dd = ch * 256 + lane * 4;
+    dO[ch] = dd < a.d ? ld4(a.dsal + tok * a.d + dd) : zero4();
+    unused[ch] = zero4();
+  }
+  unique_row_dots<DCH>(a, a.V + (b * a.L + a.vshift) * a.ldv, a.ldv, 0, NU, dO, nullptr, unused, S, S.uc);
+
+  // per entry: att * dp (S.ua is a per-entry buffer here)
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const int m = c * kWave + lane;
+    const bool in = tau[c] >= 0;
     dp[c] = in ? S.uc[un[c]] : 0.f;
     if (in) S.ua[m] = att[c] * dp[c];
   }
