@@ -123,15 +123,29 @@ class CapaASRNEstable(nn.Module):
         llave = torch.cat([E, F.pad(E, (0, 0, 1, 0))[:, :E.shape[1]]], dim=-1)
         return torch.cat([self.afin_palabra(E), self.afin_contexto(llave)], dim=-1)
 
-    def _pesos(self):
-        """The fused GEMMs' weights (W, W2, b2, Wq) assembled in one launch (_Pesos), or None when a parameter is not
-        fp32 (the methods below then assemble them with PyTorch ops)."""
+    def _hash_fusionado(self, E):
+        """Whether phi comes from the fused hash kernels (ops.HashProducer): fp32 outside autocast and the widths
+        asrn_hash_fwd supports; otherwise the first layers' GEMM, the hidden-layer kernel or PyTorch ops, and one
+        block-diagonal GEMM."""
         pal, ctx = self.afin_palabra, self.afin_contexto
-        ps = (pal[0].weight, ctx[0].weight, pal[2].weight, ctx[2].weight, pal[2].bias, ctx[2].bias, self.cq.weight,
-              self.ck.weight)
+        m, mc = pal[0].out_features, ctx[0].out_features
+        pw, pc = pal[2].out_features, ctx[2].out_features
+        return (E.dtype == torch.float32 and not torch.is_autocast_enabled(E.device.type) and m % 4 == 0
+                and mc % 4 == 0 and 4 <= m <= 64 and 4 <= mc <= 64 and 256 % ((m + mc) // 4) == 0
+                and 1 <= pw <= 64 and 1 <= pc <= 64 and pal[0].weight.dtype == torch.float32)
+
+    def _pesos(self, E):
+        """The fused GEMMs' weights assembled in one launch (_Pesos): a dict with W and Wq, and W2, b2 unless the hash
+        kernels take the second layers' parameters directly; None when a parameter is not fp32 (the methods below
+        then assemble them with PyTorch ops)."""
+        pal, ctx = self.afin_palabra, self.afin_contexto
+        ps = [pal[0].weight, ctx[0].weight, self.cq.weight, self.ck.weight]
+        if not self._hash_fusionado(E):
+            ps += [pal[2].weight, ctx[2].weight, pal[2].bias, ctx[2].bias]
         if not all(p.dtype == torch.float32 and p.is_cuda and p.is_contiguous() for p in ps):
             return None
-        return _Pesos.apply(*ps)
+        out = _Pesos.apply(*ps)
+        return dict(zip(('W', 'Wq', 'W2', 'b2'), out))
 
     def _phi_y_valores(self, E, pesos=None):
         """phi (B, L, P) and the rows the candidate kernels gather for the values (asrn/nucleo.py:644-659).
@@ -146,12 +160,16 @@ class CapaASRNEstable(nn.Module):
         d = E.shape[-1]
         pal, ctx = self.afin_palabra, self.afin_contexto
         m, mc = pal[0].out_features, ctx[0].out_features
-        if pesos is None:
-            W = torch.cat([pal[0].weight, ctx[0].weight.view(mc, 2, d).transpose(0, 1).reshape(2 * mc, d)])
+        W = (torch.cat([pal[0].weight, ctx[0].weight.view(mc, 2, d).transpose(0, 1).reshape(2 * mc, d)])
+             if pesos is None else pesos['W'])
+        if self._hash_fusionado(E):
+            return ops.HashProducer.apply(E, W, pal[0].bias, ctx[0].bias, pal[2].weight, pal[2].bias, ctx[2].weight,
+                                          ctx[2].bias, m, mc)
+        if pesos is None or 'W2' not in pesos:
             W2 = torch.block_diag(pal[2].weight, ctx[2].weight)    # both second layers as one GEMM: phi comes whole
             b2 = torch.cat([pal[2].bias, ctx[2].bias])
         else:
-            W, W2, b2 = pesos[:3]
+            W2, b2 = pesos['W2'], pesos['b2']
         if (E.dtype == torch.float32 and not torch.is_autocast_enabled(E.device.type) and m % 4 == 0
                 and mc % 4 == 0 and W.dtype == torch.float32):
             g, filas = ops.Producer.apply(E, W, pal[0].bias, ctx[0].bias, m, mc)
@@ -174,7 +192,7 @@ class CapaASRNEstable(nn.Module):
         hh32, beta, log_alfa, h_puerta = ops.Context.apply(h, self.ln_ctx.weight, self.ln_ctx.bias, self.w_reloj,
                                                            self.b_reloj, meta)
         cf = self.confirmar
-        Wq = torch.cat([self.cq.weight, self.ck.weight]) if pesos is None else pesos[3]
+        Wq = torch.cat([self.cq.weight, self.ck.weight]) if pesos is None else pesos['Wq']
         y = lineal(_a_autocast(hh32), Wq)
         Qc, Kc = _Split2.apply(y, cf)
         return (Qc, Kc, beta, log_alfa, h_puerta) if con_h else (Qc, Kc, beta, log_alfa)
@@ -186,17 +204,22 @@ class CapaASRNEstable(nn.Module):
 
     # --- hot path (HIP) ---------------------------------------------------------------------------------------------
 
-    def _acumular(self, E, Qc, Kc, Bt, log_alfa, sig, partes=None, pesos=None, esperar=None):
-        """Candidate attention of all tables -> salida and the gate signals (asrn/estable.py:204-300). esperar: called
-        before the candidate kernels, after the producers and the bucket sort (the point where the context inputs
-        must be ready)."""
-        T = self.n_tablas
+    def _cubetas(self, E, partes=None, pesos=None):
+        """The hash producers and the bucket sort (asrn/estable.py:204-236): phi, the rows the values gather, and the
+        sorted order, windows and ranks of every table."""
         phi, filas = self._phi_y_valores(E, pesos)
         if partes is not None:                                              # the generation step's value cache
             v = F.linear(_a_autocast(E), self.v.weight)
             partes.update(phi=phi, V=F.pad(v, (0, 0, 0, 1))[:, 1:])         # V[t] = W_v E[t+1], 0 at the end
-        _, order, _, rank, win = ops.bucket_sort(phi.detach(), T, self.n_bits, self.chunk)
-        shape = dict(T=T, Tc=self.tablas_contexto, C=self.chunk, K=self.sufijo, v_shift=1)
+        _, order, _, rank, win = ops.bucket_sort(phi.detach(), self.n_tablas, self.n_bits, self.chunk)
+        return phi, filas, order, win, rank
+
+    def _acumular(self, E, Qc, Kc, Bt, log_alfa, sig, partes=None, pesos=None, esperar=None, cubetas=None):
+        """Candidate attention of all tables -> salida and the gate signals (asrn/estable.py:204-300). esperar: called
+        before the candidate kernels, after the producers and the bucket sort (the point where the context inputs
+        must be ready); cubetas: what _cubetas returned, when it already ran."""
+        phi, filas, order, win, rank = self._cubetas(E, partes, pesos) if cubetas is None else cubetas
+        shape = dict(T=self.n_tablas, Tc=self.tablas_contexto, C=self.chunk, K=self.sufijo, v_shift=1)
         if esperar is not None:
             esperar()
         suma, sen = ops.Candidates.apply(phi, filas, Qc, Kc, Bt, log_alfa, self.w_sufijo, self.gamma, sig, order,
@@ -248,7 +271,7 @@ class CapaASRNEstable(nn.Module):
         # the bucket sort; the candidate attention waits for the context only. Autograd runs each op's backward on
         # the stream of its forward, so the backward overlaps the same way.
         principal, lado = torch.cuda.current_stream(E.device), _lateral(E.device)
-        pesos = self._pesos()
+        pesos = self._pesos(E)
         lado.wait_stream(principal)
         with torch.cuda.stream(lado):
             Qc, Kc, beta, log_alfa, h = self._contexto(h, con_h=True, pesos=pesos)
@@ -258,7 +281,7 @@ class CapaASRNEstable(nn.Module):
             with torch.no_grad():
                 ngram = ops.ngram_sort(sig, self.c_vistos, self.vistos)
             rep = self._repeticion(sig, beta, Bt, log_alfa, partes, ngram)
-        for t in [sig] + ([pesos[3]] if pesos is not None else []):
+        for t in [sig] + ([pesos['Wq']] if pesos is not None else []):
             t.record_stream(lado)                      # made here, used there: not reused before both are done
         acc = self._acumular(E, Qc, Kc, Bt, log_alfa, sig, partes, pesos,
                              esperar=lambda: principal.wait_event(contexto_listo))
@@ -306,49 +329,60 @@ class _ShiftAdd(torch.autograd.Function):
 
 class _Pesos(torch.autograd.Function):
     """The fused GEMMs' weights, assembled from the parameters in one launch (ops.copy_blocks):
-    W = [W_p; W_a; W_b] (the word MLP's first layer and the context MLP's split into its E_t and E_{t-1} halves),
-    W2 = blockdiag(word second layer, context second layer) with b2 = [b_word2; b_ctx2], and Wq = [cq; ck]. The
-    backward scatters the four gradients back to the eight parameters in one launch. fp32 parameters only."""
+    W = [W_p; W_a; W_b] (the word MLP's first layer and the context MLP's split into its E_t and E_{t-1} halves) and
+    Wq = [cq; ck]; with the second layers given, also W2 = blockdiag(word second layer, context second layer) and
+    b2 = [b_word2; b_ctx2]. The backward scatters the gradients back to the parameters in one launch. fp32 only."""
 
     @staticmethod
-    def forward(ctx, p0w, c0w, p2w, c2w, p2b, c2b, cqw, ckw):
-        (m, d), mc = p0w.shape, c0w.shape[0]
-        (o1, h1), (o2, h2), cf = p2w.shape, c2w.shape, cqw.shape[0]
+    def forward(ctx, p0w, c0w, cqw, ckw, p2w=None, c2w=None, p2b=None, c2b=None):
+        (m, d), mc, cf = p0w.shape, c0w.shape[0], cqw.shape[0]
         dev = p0w.device
+        con2 = p2w is not None
         W = torch.empty((m + 2 * mc, d), dtype=torch.float32, device=dev)
-        W2 = torch.empty((o1 + o2, h1 + h2), dtype=torch.float32, device=dev)
-        b2 = torch.empty((1, o1 + o2), dtype=torch.float32, device=dev)
         Wq = torch.empty((2 * cf, d), dtype=torch.float32, device=dev)
-        ops.copy_blocks(_Pesos.bloques(W, W2, b2, Wq, (p0w, c0w, p2w, c2w, p2b.view(1, -1), c2b.view(1, -1), cqw,
-                                                       ckw), ida=True))
-        ctx.meta = [t.shape for t in (p0w, c0w, p2w, c2w, p2b, c2b, cqw, ckw)]
-        return W, W2, b2.view(-1), Wq
+        W2 = b2 = None
+        params = [p0w, c0w, cqw, ckw]
+        if con2:
+            (o1, h1), (o2, h2) = p2w.shape, c2w.shape
+            W2 = torch.empty((o1 + o2, h1 + h2), dtype=torch.float32, device=dev)
+            b2 = torch.empty((1, o1 + o2), dtype=torch.float32, device=dev)
+            params += [p2w, c2w, p2b.view(1, -1), c2b.view(1, -1)]
+        ops.copy_blocks(_Pesos.bloques(W, Wq, W2, b2, params, ida=True))
+        ctx.meta = [t.shape for t in (p0w, c0w, cqw, ckw)] + ([t.shape for t in (p2w, c2w, p2b, c2b)] if con2 else [])
+        ctx.set_materialize_grads(False)
+        return (W, Wq, W2, b2.view(-1)) if con2 else (W, Wq)
 
     @staticmethod
-    def bloques(W, W2, b2, Wq, params, ida):
+    def bloques(W, Wq, W2, b2, params, ida):
         """(source, destination) pairs: parameters -> assembled weights (ida), or the reverse for the gradients."""
-        p0w, c0w, p2w, c2w, p2b, c2b, cqw, ckw = params
-        m, d, mc = p0w.shape[0], p0w.shape[1], c0w.shape[0]
-        o1, h1, cf = p2w.shape[0], p2w.shape[1], cqw.shape[0]
-        pares = [(p0w, W[:m]), (c0w[:, :d], W[m:m + mc]), (c0w[:, d:], W[m + mc:]), (p2w, W2[:o1, :h1]),
-                 (c2w, W2[o1:, h1:]), (p2b, b2[:, :o1]), (c2b, b2[:, o1:]), (cqw, Wq[:cf]), (ckw, Wq[cf:])]
-        if ida:
-            return pares + [(None, W2[:o1, h1:]), (None, W2[o1:, :h1])]
-        return [(b, a) for a, b in pares]
+        p0w, c0w, cqw, ckw = params[:4]
+        m, d, mc, cf = p0w.shape[0], p0w.shape[1], c0w.shape[0], cqw.shape[0]
+        pares = [(p0w, W[:m]), (c0w[:, :d], W[m:m + mc]), (c0w[:, d:], W[m + mc:]), (cqw, Wq[:cf]), (ckw, Wq[cf:])]
+        ceros = []
+        if W2 is not None:
+            p2w, c2w, p2b, c2b = params[4:]
+            o1, h1 = p2w.shape
+            pares += [(p2w, W2[:o1, :h1]), (c2w, W2[o1:, h1:]), (p2b, b2[:, :o1]), (c2b, b2[:, o1:])]
+            ceros = [(None, W2[:o1, h1:]), (None, W2[o1:, :h1])]
+        return pares + ceros if ida else [(b, a) for a, b in pares]
 
     @staticmethod
-    def backward(ctx, dW, dW2, db2, dWq):
+    def backward(ctx, dW, dWq, dW2=None, db2=None):
         shapes = ctx.meta
-        dev = next(g for g in (dW, dW2, db2, dWq) if g is not None).device
-        (m, d), mc = shapes[0], shapes[1][0]
-        (o1, h1), (o2, h2), cf = shapes[2], shapes[3], shapes[6][0]
-        formas = [(m + 2 * mc, d), (o1 + o2, h1 + h2), (o1 + o2,), (2 * cf, d)]
+        con2 = len(shapes) == 8
+        dev = next(g for g in (dW, dWq, dW2, db2) if g is not None).device
+        (m, d), mc, cf = shapes[0], shapes[1][0], shapes[2][0]
+        formas = [(m + 2 * mc, d), (2 * cf, d)]
+        if con2:
+            (o1, h1), (o2, h2) = shapes[4], shapes[5]
+            formas += [(o1 + o2, h1 + h2), (o1 + o2,)]
         gs = [torch.zeros(f, dtype=torch.float32, device=dev) if g is None else g.to(torch.float32).contiguous()
-              for g, f in zip((dW, dW2, db2, dWq), formas)]
+              for g, f in zip((dW, dWq, dW2, db2), formas)]
         grads = [torch.empty(sh, dtype=torch.float32, device=dev) for sh in shapes]
-        destinos = grads[:4] + [grads[4].view(1, -1), grads[5].view(1, -1)] + grads[6:]
-        ops.copy_blocks(_Pesos.bloques(gs[0], gs[1], gs[2].view(1, -1), gs[3], destinos, ida=False))
-        return tuple(grads)
+        destinos = grads[:4] + ([grads[4], grads[5], grads[6].view(1, -1), grads[7].view(1, -1)] if con2 else [])
+        ops.copy_blocks(_Pesos.bloques(gs[0], gs[1], gs[2] if con2 else None,
+                                       gs[3].view(1, -1) if con2 else None, destinos, ida=False))
+        return tuple(grads) + ((None,) * 4 if not con2 else ())
 
 
 class _Split2(torch.autograd.Function):

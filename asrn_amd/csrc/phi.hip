@@ -1,0 +1,439 @@
+// a0 (part): the hash MLPs from their first layers' products to phi (asrn/nucleo.py:644-659), fused.
+//
+// The first GEMM gives, per token t, y[t] = [W_p E_t | W_a E_t | W_b E_t] (bias-free). Then, per tile of 64 tokens:
+//   forward   g = [gelu(hp + b_p) | gelu(za + zb[t-1] + b_c)] into LDS (exact erf GELU; no zb term at a row's first
+//             position), and phi = [g_word W2w^T + b2w | g_ctx W2c^T + b2c] on the matrix cores
+//             (v_mfma_f32_16x16x4_f32), the two second layers as the two diagonal blocks they are.
+//   backward  dg = [dphi_word W2w | dphi_ctx W2c] on the matrix cores; the pre-activations recomputed from y; dp =
+//             dg gelu'(x) written into the first GEMM's output gradient dy (the word block, the W_a block, and the
+//             W_b block one position earlier, 0 at a row's last position: each element written once); and this
+//             workgroup's share of every parameter gradient: dW2w = dphi_word^T g_word and dW2c = dphi_ctx^T g_ctx
+//             (matrix cores again), db2 = sum dphi, and the first-layer biases' sum dp. The per-workgroup rows are
+//             summed in order by asrn_column_sums.
+// v_mfma_f32_16x16x4_f32 lane layout (checked on gfx950): lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16]
+// and receives D[(l / 16) * 4 + q][l % 16], q = 0..3.
+#include "common.h"
+
+namespace asrn {
+
+constexpr int kPhiTok = 64;          // tokens per workgroup
+constexpr int kPhiThreads = 256;     // 4 waves: wave w owns tokens 16w .. 16w + 15 of the tile
+constexpr int kPhiMax = 64;          // the most hidden units or outputs per MLP
+constexpr int kGld = 2 * kPhiMax + 1;   // LDS row stride of the g / dg tiles (odd: conflict-free column reads)
+constexpr int kWld = kPhiMax + 1;       // LDS row stride of a weight block or a dphi tile
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+struct PhiArgs {
+  const float* y; int64_t ldy;         // (N, ldy): hp at [0, m), za at [m, m + mc), zb at [m + mc, m + 2 mc)
+  const float* bp; const float* bc;    // first-layer biases: word (m), context (mc)
+  const float* Ww; const float* bw;    // word second layer (Pw, m) and its bias (Pw)
+  const float* Wc; const float* bc2;   // context second layer (Pc, mc) and its bias (Pc)
+  float* phi;                          // (N, Pw + Pc)
+  const float* dphi;                   // (N, Pw + Pc)
+  float* dy; int64_t ldd;              // (N, ldd): columns [0, m + 2 mc) written
+  float* part;                         // per workgroup: [dW2w | dW2c | db2w | db2c | db_word | db_ctx]
+  int64_t B, L;
+  int m, mc, Pw, Pc;
+};
+
+__device__ __forceinline__ float gelu_e(float x) { return 0.5f * x * (1.f + erff(x * 0.70710678118654752f)); }
+__device__ __forceinline__ float gelu_d(float x) {
+  return 0.5f * (1.f + erff(x * 0.70710678118654752f)) + x * 0.39894228040143268f * __expf(-0.5f * x * x);
+}
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// a weight block (rows x cols, row-major) into LDS as ws[r][c] (stride kWld), zero beyond it up to kPhiMax x kPhiMax;
+// every thread's 16 loads are issued before any is stored
+__device__ __forceinline__ void stage_block(const float* __restrict__ W, int rows, int cols, float* ws) {
+  constexpr int kPer = kPhiMax * kPhiMax / kPhiThreads;
+  float v[kPer];
+#pragma unroll
+  for (int x = 0; x < kPer; ++x) {
+    const int e = threadIdx.x + x * kPhiThreads, r = e / kPhiMax, c = e % kPhiMax;
+    const bool ok = r < rows && c < cols;
+    v[x] = W[ok ? r * cols + c : 0];
+    v[x] = ok ? v[x] : 0.f;
+  }
+#pragma unroll
+  for (int x = 0; x < kPer; ++x) {
+    const int e = threadIdx.x + x * kPhiThreads;
+    ws[(e / kPhiMax) * kWld + e % kPhiMax] = v[x];
+  }
+}
+
+// The hidden layer's inputs for kHidPer float4 groups of the tile per thread (group e = tid + x * 256: token e / h4,
+// columns 4 (e % h4) ..): y at those columns (hp for word columns, za for context ones: both at y[row][j]), the
+// previous token's zb for context columns (0 at a row's first position) and the bias. All loads issued together.
+constexpr int kHidPer = kPhiTok * 2 * kPhiMax / 4 / kPhiThreads;   // 8 float4 groups per thread at most
+template <int NG>
+struct HidInN {
+  float4 ya[NG], yb[NG], bb[NG];
+};
+using HidIn = HidInN<kHidPer>;
+// groups first .. first + NG - 1 of this thread
+template <int NG>
+__device__ __forceinline__ void load_hidden(const PhiArgs& a, int64_t t0, int64_t N, int h4, HidInN<NG>& in,
+                                            int first = 0) {
+#pragma unroll
+  for (int x = 0; x < NG; ++x) {
+    const int e = threadIdx.x + (first + x) * kPhiThreads;
+    const int tk = e / h4, j = (e - tk * h4) * 4;
+    const int64_t row = t0 + tk;
+    const bool ok = tk < kPhiTok && row < N;
+    const bool ctx = j >= a.m;
+    const bool prev = ok && ctx && row % a.L > 0;
+    const int64_t r0 = ok ? row : 0;
+    in.ya[x] = *reinterpret_cast<const float4*>(a.y + r0 * a.ldy + (ok ? j : 0));
+    in.yb[x] = *reinterpret_cast<const float4*>(a.y + (prev ? (r0 - 1) * a.ldy + a.mc + j : 0));
+    in.bb[x] = *reinterpret_cast<const float4*>(ctx ? a.bc + (j - a.m) : a.bp + (ok ? j : 0));
+    if (!prev) in.yb[x] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+template <int NG>
+__device__ __forceinline__ float4 pre_of(const HidInN<NG>& in, int x) {
+  return make_float4((in.ya[x].x + in.bb[x].x) + in.yb[x].x, (in.ya[x].y + in.bb[x].y) + in.yb[x].y,
+                     (in.ya[x].z + in.bb[x].z) + in.yb[x].z, (in.ya[x].w + in.bb[x].w) + in.yb[x].w);
+}
+
+__global__ __launch_bounds__(kPhiThreads) void k_phi_fwd(PhiArgs a) {
+  __shared__ float gs[kPhiTok * kGld];
+  __shared__ float wsw[kPhiMax * kWld];
+  __shared__ float wsc[kPhiMax * kWld];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t N = a.B * a.L, t0 = (int64_t)blockIdx.x * kPhiTok;
+  const int h = a.m + a.mc, h4 = h / 4, P = a.Pw + a.Pc;
+  float bias[8];                                   // the second layers' biases of this lane's output columns
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int cw = nt * 16 + (lane & 15);
+    bias[nt] = a.bw[cw < a.Pw ? cw : 0];
+    bias[4 + nt] = a.bc2[cw < a.Pc ? cw : 0];
+  }
+  {
+    HidIn in;
+    load_hidden(a, t0, N, h4, in);
+    stage_block(a.Ww, a.Pw, a.m, wsw);
+    stage_block(a.Wc, a.Pc, a.mc, wsc);
+#pragma unroll
+    for (int x = 0; x < kHidPer; ++x) {
+      const int e = tid + x * kPhiThreads;
+      const int tk = e / h4, j = (e - tk * h4) * 4;
+      if (tk >= kPhiTok) continue;
+      float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (t0 + tk < N) {
+        const float4 v = pre_of(in, x);
+        g = make_float4(gelu_e(v.x), gelu_e(v.y), gelu_e(v.z), gelu_e(v.w));
+      }
+      float* o = gs + tk * kGld + j;
+      o[0] = g.x; o[1] = g.y; o[2] = g.z; o[3] = g.w;
+    }
+  }
+  __syncthreads();
+  // phi tile: wave w, tokens 16w + ..; 4 n-tiles of 16 outputs per MLP and 16 k-steps per MLP, all fixed (the weight
+  // blocks are zero beyond Pw x m and Pc x mc, so the padding adds nothing); every operand of an MLP is read from LDS
+  // before its 64 MFMAs issue
+  const int r16 = lane & 15, k4 = lane >> 4;
+  const float* ga = gs + (wave * 16 + r16) * kGld;
+  floatx4 acc[2][4];
+#pragma unroll
+  for (int part = 0; part < 2; ++part) {
+    const float* wsp = part ? wsc : wsw;
+    const int koff = part ? a.m : 0, kn = part ? a.mc : a.m;
+    float av[kPhiMax / 4], bv[kPhiMax / 4][4];
+#pragma unroll
+    for (int ks = 0; ks < kPhiMax / 4; ++ks) {
+      av[ks] = ks * 4 + k4 < kn ? ga[koff + ks * 4 + k4] : 0.f;   // the tile's other columns are not this MLP's
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) bv[ks][nt] = wsp[(nt * 16 + r16) * kWld + ks * 4 + k4];
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[part][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < kPhiMax / 4; ++ks)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) acc[part][nt] = mfma4(av[ks], bv[ks][nt], acc[part][nt]);
+  }
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int cw = nt * 16 + r16;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t row = t0 + wave * 16 + k4 * 4 + q;
+      if (row >= N) continue;
+      if (cw < a.Pw) a.phi[row * P + cw] = acc[0][nt][q] + bias[nt];
+      if (cw < a.Pc) a.phi[row * P + a.Pw + cw] = acc[1][nt][q] + bias[4 + nt];
+    }
+  }
+}
+
+// One workgroup per CU, looping over tiles of 64 tokens (blockIdx.x, + gridDim.x, ...): the weight blocks are staged
+// once, and the parameter gradients accumulate across the workgroup's tiles (the dW MFMA accumulators stay in
+// registers), so each workgroup writes one partial row.
+__global__ __launch_bounds__(kPhiThreads) void k_phi_bwd(PhiArgs a) {
+  __shared__ float ws[2 * kPhiMax * kWld];        // the two weight blocks (outputs x hidden, zero-padded to 64 x 64)
+  __shared__ float dps[kPhiTok * 2 * kWld];       // the dphi tile: word at [0, kWld), context at [kWld, 2 kWld)
+  __shared__ float dgs[kPhiTok * kGld];           // dg, in the tile's token rows
+  __shared__ float gs[kPhiTok * kGld];            // g = gelu(x), in the tile's token rows
+  __shared__ float red[kPhiThreads];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, k4 = lane >> 4;
+  const int64_t N = a.B * a.L, ntiles = (N + kPhiTok - 1) / kPhiTok;
+  const int h = a.m + a.mc, h4 = h / 4, P = a.Pw + a.Pc;
+  float* wsw = ws;
+  float* wsc = ws + kPhiMax * kWld;
+  stage_block(a.Ww, a.Pw, a.m, wsw);
+  stage_block(a.Wc, a.Pc, a.mc, wsc);
+  floatx4 dWacc[2][4];                            // this wave's output rows 16w .. 16w + 15 of both dW2 blocks
+#pragma unroll
+  for (int part = 0; part < 2; ++part)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) dWacc[part][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float4 bsum = make_float4(0.f, 0.f, 0.f, 0.f);  // first-layer biases: this thread's column group
+  float b2sum = 0.f;                              // second-layer biases: output column tid (tid < 128)
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t t0 = tile * kPhiTok;
+    constexpr int kDPer = kPhiTok * 2 * kPhiMax / kPhiThreads / 4;   // four rounds of 8 loads per thread
+#pragma unroll
+    for (int half = 0; half < 4; ++half) {
+      float v[kDPer];
+#pragma unroll
+      for (int x = 0; x < kDPer; ++x) {
+        const int e = tid + (half * kDPer + x) * kPhiThreads;
+        const int tk = e / (2 * kPhiMax), c = e - tk * 2 * kPhiMax;
+        const int64_t row = t0 + tk;
+        const bool ctx = c >= kPhiMax;
+        const int cc = ctx ? c - kPhiMax : c;
+        const bool ok = row < N && cc < (ctx ? a.Pc : a.Pw);
+        v[x] = a.dphi[ok ? row * P + (ctx ? a.Pw : 0) + cc : 0];
+        v[x] = ok ? v[x] : 0.f;
+      }
+#pragma unroll
+      for (int x = 0; x < kDPer; ++x) {
+        const int e = tid + (half * kDPer + x) * kPhiThreads;
+        const int tk = e / (2 * kPhiMax), c = e - tk * 2 * kPhiMax;
+        dps[tk * 2 * kWld + (c >= kPhiMax ? kWld + c - kPhiMax : c)] = v[x];
+      }
+    }
+    __syncthreads();
+    // dg = dphi W2 per block: A = dphi tile (tokens x outputs), B = the block (outputs x hidden), K = the 64 padded
+    // outputs (zero past Pw / Pc in both operands); all operands of a block read before its 64 MFMAs
+    {
+      const float* da = dps + (wave * 16 + r16) * 2 * kWld;
+#pragma unroll
+      for (int part = 0; part < 2; ++part) {
+        const float* wsp = part ? wsc : wsw;
+        floatx4 acc[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {     // 8 k-steps at a time: their operands read, then 32 MFMAs
+          float av[8], bv[8][4];
+#pragma unroll
+          for (int ks = 0; ks < 8; ++ks) {
+            const int k = (half * 8 + ks) * 4 + k4;
+            av[ks] = da[(part ? kWld : 0) + k];
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) bv[ks][nt] = wsp[k * kWld + nt * 16 + r16];
+          }
+#pragma unroll
+          for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma4(av[ks], bv[ks][nt], acc[nt]);
+        }
+        const int kn = part ? a.mc : a.m, off = part ? a.m : 0;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          const int col = nt * 16 + r16;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (col < kn) dgs[(wave * 16 + k4 * 4 + q) * kGld + off + col] = acc[nt][q];
+        }
+      }
+    }
+    __syncthreads();
+    // the hidden layer's backward, one float4 of one token per thread: dp = dg gelu'(x) into dy; g = gelu(x) into
+    // LDS; each thread keeps one column group (h4 divides 256), summing dp for the first-layer biases
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {              // two rounds of 4 groups (register pressure)
+    HidInN<kHidPer / 2> in;
+    load_hidden(a, t0, N, h4, in, hf * (kHidPer / 2));
+#pragma unroll
+    for (int xi = 0; xi < kHidPer / 2; ++xi) {
+      const int xg = hf * (kHidPer / 2) + xi;
+      const int e = tid + xg * kPhiThreads;
+      const int tk = e / h4, j = (e - tk * h4) * 4;
+      if (tk >= kPhiTok) continue;
+      const int64_t row = t0 + tk;
+      float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (row < N) {
+        const int64_t t = row % a.L;
+        const float4 x = pre_of(in, xi);
+        const float* d = dgs + tk * kGld + j;
+        const float4 dp = make_float4(d[0] * gelu_d(x.x), d[1] * gelu_d(x.y), d[2] * gelu_d(x.z),
+                                      d[3] * gelu_d(x.w));
+        g = make_float4(gelu_e(x.x), gelu_e(x.y), gelu_e(x.z), gelu_e(x.w));
+        *reinterpret_cast<float4*>(a.dy + row * a.ldd + j) = dp;
+        if (j >= a.m) {
+          const int c = j - a.m;
+          if (t > 0) *reinterpret_cast<float4*>(a.dy + (row - 1) * a.ldd + a.m + a.mc + c) = dp;
+          if (t == a.L - 1)
+            *reinterpret_cast<float4*>(a.dy + row * a.ldd + a.m + a.mc + c) = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        bsum.x += dp.x; bsum.y += dp.y; bsum.z += dp.z; bsum.w += dp.w;
+      }
+      float* o = gs + tk * kGld + j;
+      o[0] = g.x; o[1] = g.y; o[2] = g.z; o[3] = g.w;
+    }
+    }
+    __syncthreads();
+    // dW2w += dphi_word^T g_word, dW2c += dphi_ctx^T g_ctx: A = dphi^T (outputs x tokens), B = g (tokens x hidden),
+    // K = the tile's 64 tokens; wave w takes output rows 16w .. 16w + 15 of both blocks
+    {
+      const int orow = wave * 16 + r16;
+#pragma unroll
+      for (int quarter = 0; quarter < 4; ++quarter) {   // 4 token steps at a time: their operands read, then 32 MFMAs
+        float aw[4], ac[4], bw_[4][4], bc_[4][4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const int tk = (quarter * 4 + ks) * 4 + k4;
+          aw[ks] = dps[tk * 2 * kWld + orow];
+          ac[ks] = dps[tk * 2 * kWld + kWld + orow];
+          const float* gr = gs + tk * kGld;
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) {
+            const int col = nt * 16 + r16;
+            bw_[ks][nt] = col < a.m ? gr[col] : 0.f;
+            bc_[ks][nt] = col < a.mc ? gr[a.m + col] : 0.f;
+          }
+        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) {
+            dWacc[0][nt] = mfma4(aw[ks], bw_[ks][nt], dWacc[0][nt]);
+            dWacc[1][nt] = mfma4(ac[ks], bc_[ks][nt], dWacc[1][nt]);
+          }
+      }
+    }
+    // db2: output column tid's sum over the tile's tokens, in order
+    if (tid < 2 * kPhiMax) {
+      const float* col = dps + (tid >= kPhiMax ? kWld + tid - kPhiMax : tid);
+      float s = 0.f;
+      for (int tk = 0; tk < kPhiTok; ++tk) s += col[tk * 2 * kWld];
+      b2sum += s;
+    }
+    __syncthreads();                              // the next tile overwrites dps, dgs and gs
+  }
+  float* prow = a.part + (int64_t)blockIdx.x * (a.Pw * a.m + a.Pc * a.mc + a.Pw + a.Pc + h);
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int col = nt * 16 + r16;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int o = wave * 16 + k4 * 4 + q;
+      if (o < a.Pw && col < a.m) prow[o * a.m + col] = dWacc[0][nt][q];
+      if (o < a.Pc && col < a.mc) prow[a.Pw * a.m + o * a.mc + col] = dWacc[1][nt][q];
+    }
+  }
+  float* pb = prow + a.Pw * a.m + a.Pc * a.mc;
+  if (tid < 2 * kPhiMax) {
+    const bool ctx = tid >= kPhiMax;
+    const int c = ctx ? tid - kPhiMax : tid;
+    if (c < (ctx ? a.Pc : a.Pw)) pb[(ctx ? a.Pw : 0) + c] = b2sum;
+  }
+  // first-layer biases: threads with the same column group (tid mod h4) combine in order of tid
+  float* pdb = pb + a.Pw + a.Pc;
+  for (int comp = 0; comp < 4; ++comp) {
+    red[tid] = comp == 0 ? bsum.x : (comp == 1 ? bsum.y : (comp == 2 ? bsum.z : bsum.w));
+    __syncthreads();
+    if (tid < h4) {
+      float s = 0.f;
+      for (int r = tid; r < kPhiThreads; r += h4) s += red[r];
+      pdb[tid * 4 + comp] = s;
+    }
+    __syncthreads();
+  }
+}
+
+static int phi_check(const PhiArgs& a, const char* what) {
+  ASRN_REQUIRE(a.B >= 0 && a.L >= 0 && a.m >= 4 && a.mc >= 4 && a.m <= kPhiMax && a.mc <= kPhiMax && a.m % 4 == 0 &&
+                   a.mc % 4 == 0 && a.Pw >= 1 && a.Pc >= 1 && a.Pw <= kPhiMax && a.Pc <= kPhiMax,
+               "%s: m=%d, mc=%d (multiples of 4 in [4, %d]) and Pw=%d, Pc=%d (in [1, %d]) out of range", what, a.m,
+               a.mc, kPhiMax, a.Pw, a.Pc, kPhiMax);
+  ASRN_REQUIRE(kPhiThreads % ((a.m + a.mc) / 4) == 0, "%s: (m + mc) / 4 = %d must divide %d", what,
+               (a.m + a.mc) / 4, kPhiThreads);
+  ASRN_REQUIRE(a.ldy >= a.m + 2 * a.mc && a.ldy % 4 == 0 && ((uintptr_t)a.y & 15) == 0 && ((uintptr_t)a.bp & 15) == 0 &&
+                   ((uintptr_t)a.bc & 15) == 0,
+               "%s: y needs a row stride >= m + 2 mc (a multiple of 4); y and the first-layer biases 16-byte aligned",
+               what);
+  return 0;
+}
+
+}  // namespace asrn
+
+using namespace asrn;
+
+extern "C" int asrn_hash_fwd(const float* y, int64_t ldy, const float* b_word, const float* b_ctx,
+                             const float* w2_word, const float* b2_word, const float* w2_ctx, const float* b2_ctx,
+                             int64_t B, int64_t L, int32_t m, int32_t mc, int32_t p_word, int32_t p_ctx, float* phi,
+                             void* stream) {
+  PhiArgs a = {};
+  a.y = y; a.ldy = ldy; a.bp = b_word; a.bc = b_ctx; a.Ww = w2_word; a.bw = b2_word; a.Wc = w2_ctx; a.bc2 = b2_ctx;
+  a.phi = phi; a.B = B; a.L = L; a.m = m; a.mc = mc; a.Pw = p_word; a.Pc = p_ctx;
+  if (phi_check(a, "asrn_hash_fwd")) return 1;
+  const int64_t n = B * L;
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_phi_fwd, dim3((unsigned)((n + kPhiTok - 1) / kPhiTok)), dim3(kPhiThreads), 0,
+                     (hipStream_t)stream, a);
+  return check_launch("asrn_hash_fwd");
+}
+
+// the backward's workgroups: at most 128, one per CU on half of the 256, fewer for short inputs. The layer runs the
+// context producer's backward on a second stream beside this kernel; a grid over every CU (one 133 KB-LDS workgroup
+// each) keeps that work off the machine until it ends, and the step measured 2% slower with 256 than with 128.
+static int64_t phi_bwd_groups(int64_t n) {
+  const int64_t tiles = (n + kPhiTok - 1) / kPhiTok;
+  return tiles < 128 ? tiles : 128;
+}
+
+extern "C" int64_t asrn_hash_bwd_workspace(int64_t B, int64_t L, int32_t m, int32_t mc, int32_t p_word,
+                                           int32_t p_ctx) {
+  if (B < 0 || L < 0 || m < 0 || mc < 0 || p_word < 0 || p_ctx < 0) return -1;
+  const int64_t groups = phi_bwd_groups(B * L);
+  const int64_t cols = (int64_t)p_word * m + (int64_t)p_ctx * mc + p_word + p_ctx + m + mc;
+  const int64_t part = (groups * cols * 4 + 255) / 256 * 256;
+  const int64_t sums = asrn_column_sums_workspace(groups, cols);
+  return sums < 0 ? -1 : part + sums;
+}
+
+extern "C" int asrn_hash_bwd(const float* y, int64_t ldy, const float* b_word, const float* b_ctx,
+                             const float* w2_word, const float* w2_ctx, int64_t B, int64_t L, int32_t m, int32_t mc,
+                             int32_t p_word, int32_t p_ctx, const float* dphi, float* dy, int64_t ldd, float* dparams,
+                             void* workspace, int64_t workspace_bytes, void* stream) {
+  PhiArgs a = {};
+  a.y = y; a.ldy = ldy; a.bp = b_word; a.bc = b_ctx; a.Ww = w2_word; a.Wc = w2_ctx; a.dphi = dphi; a.dy = dy;
+  a.ldd = ldd; a.B = B; a.L = L; a.m = m; a.mc = mc; a.Pw = p_word; a.Pc = p_ctx;
+  if (phi_check(a, "asrn_hash_bwd")) return 1;
+  ASRN_REQUIRE(ldd >= m + 2 * mc && ldd % 4 == 0 && ((uintptr_t)dy & 15) == 0,
+               "asrn_hash_bwd: dy needs a row stride >= m + 2 mc (a multiple of 4) and 16-byte aligned rows");
+  const int64_t need = asrn_hash_bwd_workspace(B, L, m, mc, p_word, p_ctx);
+  ASRN_REQUIRE(need >= 0 && workspace_bytes >= need && (need == 0 || workspace != nullptr) &&
+                   ((uintptr_t)workspace % 256) == 0,
+               "asrn_hash_bwd: needs a 256-byte aligned workspace of %lld bytes", (long long)need);
+  const int64_t n = B * L;
+  const int64_t groups = phi_bwd_groups(n);
+  const int64_t cols = (int64_t)p_word * m + (int64_t)p_ctx * mc + p_word + p_ctx + m + mc;
+  if (n == 0) {   // no tokens: every gradient is 0 (column sums over no rows)
+    return asrn_column_sums(nullptr, 0, 0, cols, cols, dparams, nullptr, 0, stream);
+  }
+  a.part = (float*)workspace;
+  hipLaunchKernelGGL(k_phi_bwd, dim3((unsigned)groups), dim3(kPhiThreads), 0, (hipStream_t)stream, a);
+  if (check_launch("asrn_hash_bwd")) return 1;
+  const int64_t part_bytes = (groups * cols * 4 + 255) / 256 * 256;
+  return asrn_column_sums(a.part, 0, groups, cols, cols, dparams, (char*)workspace + part_bytes, need - part_bytes,
+                          stream);
+}

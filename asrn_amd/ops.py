@@ -231,6 +231,61 @@ def copy_blocks(blocks):
          arr(ctypes.c_int64, [d.shape[1] for _, d in blocks]), stream_of(dev))
 
 
+class HashProducer(torch.autograd.Function):
+    """phi (B, L, Pw + Pc) from E through both hash MLPs (asrn/nucleo.py:644-659): y = E W^T by one bias-free GEMM
+    (W's rows [W_p (m) | W_a (mc) | W_b (mc)]), then the hidden layer and both second layers in asrn_hash_fwd (the
+    second layers on the matrix cores as the two diagonal blocks they are). Also returns E itself (fp32, an alias) as
+    the rows the candidate kernels gather. Backward: asrn_hash_bwd writes dy and every second-layer and bias gradient;
+    dE = dE_rows + dy W in one GEMM with beta = 1; dW by token slabs. fp32 only."""
+
+    @staticmethod
+    def forward(ctx, E, W, b_word, b_ctx, W2w, b2w, W2c, b2c, m, mc):
+        dev = _dev(E, W)
+        B, L, d = E.shape
+        n = W.shape[0]
+        Pw, Pc = W2w.shape[0], W2c.shape[0]
+        if n != m + 2 * mc or W2w.shape[1] != m or W2c.shape[1] != mc:
+            raise ValueError('HashProducer: W must be (m + 2 mc, d), W2w (Pw, m) and W2c (Pc, mc)')
+        E = _c(E, torch.float32)
+        ps = [_c(t, torch.float32) for t in (b_word, b_ctx, W2w, b2w, W2c, b2c)]
+        y = torch.nn.functional.linear(E, W)
+        phi = torch.empty((B, L, Pw + Pc), dtype=torch.float32, device=dev)
+        call('asrn_hash_fwd', ptr(y), n, *[ptr(t) for t in ps], B, L, m, mc, Pw, Pc, ptr(phi), stream_of(dev))
+        ctx.save_for_backward(E, W, y, ps[0], ps[1], ps[2], ps[4])
+        ctx.meta = (m, mc, Pw, Pc)
+        ctx.set_materialize_grads(False)
+        return phi, E.view_as(E)
+
+    @staticmethod
+    def backward(ctx, dphi, drows):
+        E, W, y, bw, bc, W2w, W2c = ctx.saved_tensors
+        m, mc, Pw, Pc = ctx.meta
+        B, L, n = y.shape
+        d = E.shape[-1]
+        dev = y.device
+        if dphi is None:
+            dphi = torch.zeros((B, L, Pw + Pc), dtype=torch.float32, device=dev)
+        dphi = _c(dphi, torch.float32)
+        dy = torch.empty((B, L, n), dtype=torch.float32, device=dev)
+        dp = torch.empty((Pw * m + Pc * mc + Pw + Pc + m + mc,), dtype=torch.float32, device=dev)
+        wsb = query('asrn_hash_bwd_workspace', B, L, m, mc, Pw, Pc)
+        ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+        call('asrn_hash_bwd', ptr(y), n, ptr(bw), ptr(bc), ptr(W2w), ptr(W2c), B, L, m, mc, Pw, Pc, ptr(dphi),
+             ptr(dy), n, ptr(dp), ptr(ws), wsb, stream_of(dev))
+        dW2w, dW2c, db2w, db2c, dbw, dbc = torch.split(dp, [Pw * m, Pc * mc, Pw, Pc, m, mc])
+        dy2 = dy.view(B * L, n)
+        dE = None
+        if ctx.needs_input_grad[0]:
+            if drows is None:
+                dE = dy2.mm(W).view(B, L, d)
+            else:
+                # the rows' gradient is a fresh buffer of the candidate backward: accumulate the GEMM into it
+                dE = _c(drows, torch.float32) if drows.dtype != torch.float32 or not drows.is_contiguous() else drows
+                dE.view(B * L, d).addmm_(dy2, W)
+        dW = weight_grad(dy2, E.view(B * L, d)) if ctx.needs_input_grad[1] else None
+        return (dE, dW, dbw, dbc, dW2w.view(Pw, m), db2w, dW2c.view(Pc, mc), db2c, None, None)
+
+
 class SmallMatmul(torch.autograd.Function):
     """A @ B for small fp32 matrices (asrn_small_gemm: one workgroup per 16 x 16 tile of the result): the layer's
     W_o W_v. The backward's dA = dC B^T and dB = A^T dC run on the same kernel."""

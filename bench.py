@@ -57,31 +57,40 @@ def context_bytes(d):
 
 
 def hidden_bytes(m=64, mc=64):
-    """The hash MLPs' hidden layer (asrn_hidden_fwd/bwd), fp32: the forward reads the three first-layer blocks and
-    writes g; the backward reads them and dg and writes their gradients."""
+    """The hash MLPs' hidden layer (asrn_hidden_fwd/bwd, the path under autocast), fp32: the forward reads the three
+    first-layer blocks and writes g; the backward reads them and dg and writes their gradients."""
     return 4 * (m + 2 * mc) + 4 * (m + mc), 4 * (m + 2 * mc) + 4 * (m + mc) + 4 * (m + 2 * mc)
 
 
-def hip_bytes_per_token(d, P, cf, T, n=4, a=4, m=64, mc=64, K=4):
+def hash_bytes(P, m=64, mc=64):
+    """The fused hash MLPs (asrn_hash_fwd/bwd, the fp32 path): the forward reads the three first-layer blocks and
+    writes phi; the backward reads them and dphi and writes the blocks' gradients (g, dg and the second layer's
+    GEMM operands stay on chip; the parameter gradients are per-workgroup partials, not per token)."""
+    return 4 * (m + 2 * mc) + 4 * P, 4 * (m + 2 * mc) + 4 * P + 4 * (m + 2 * mc)
+
+
+def hip_bytes_per_token(d, P, cf, T, n=4, a=4, m=64, mc=64, K=4, fused=True):
     """All HIP kernels of one fwd+bwd, each distinct tensor read once and written once: hash + bucket sort (phi in, ids
     and order out), clock 16 + 16, n-gram sort 28, Hawkes/streak scans 60 + 100, candidates, gate, context producer,
-    hidden layer, and the column sums of the bias gradients and the candidates' per-token partials (the weight
-    gradients' slab sums scale with the weights, not the tokens, and are left out).
-    cfg2 fp32: 512 + 32 + 28 + 160 + 7,044 + 8,324 + 6,200 + 3,328 + 1,012 = 26,640."""
+    the hash MLPs (fused: hash_bytes; else the hidden layer and its bias column sums), and the column sums of the
+    candidates' per-token partials (the weight gradients' slab sums scale with the weights, not the tokens, and are
+    left out).
+    cfg2 fp32 (fused): 512 + 32 + 28 + 160 + 7,044 + 8,324 + 6,200 + 3,200 + 52 = 25,552."""
     cand = algorithmic_bytes(d, P, cf, T, a)
-    colsums = 4 * (m + mc) + 4 * P + 4 * (T + K + 1)
+    colsums = 4 * (T + K + 1) + (0 if fused else 4 * (m + mc) + 4 * P)
+    mlp = sum(hash_bytes(P, m, mc)) if fused else sum(hidden_bytes(m, mc))
     return (P * a + 8 * T + 32 + 28 + 160 + sum(cand.values()) + sum(gate_bytes(d, n, a))
-            + sum(context_bytes(d)) + sum(hidden_bytes(m, mc)) + colsums)
+            + sum(context_bytes(d)) + mlp + colsums)
 
 
-def gemm_bytes_per_token(d, P, cf, a=4, m=64, mc=64):
+def gemm_bytes_per_token(d, P, cf, a=4, m=64, mc=64, fused=True):
     """Operands and results of the layer's GEMMs per token, each read or written once (activations in a bytes;
-    weights are per step, not per token): forward E -> [hp|za|zb], g -> phi, hh -> [Qc|Kc], sum -> W_o W_v sum;
-    backward the input gradients (the E one accumulating into the candidates' dE) and the weight gradients (both
-    operands read). cfg2 fp32: 5,952 + 12,928 = 18,880."""
+    weights are per step, not per token): forward E -> [hp|za|zb], hh -> [Qc|Kc], sum -> W_o W_v sum and, unfused,
+    g -> phi; backward the input gradients (the E one accumulating into the candidates' dE) and the weight gradients
+    (both operands read). cfg2 fp32 (fused): 4,992 + 11,008 = 16,000."""
     h, q = m + 2 * mc, 2 * cf
-    fwd = (d + h) + ((m + mc) + P) + (d + q) + (d + d)
-    bwd = (d + d) + 2 * d + (P + m + mc) + (P + m + mc) + (q + d) + (q + d) + (h + 2 * d) + (h + d)
+    fwd = (d + h) + (d + q) + (d + d) + (0 if fused else (m + mc) + P)
+    bwd = (d + d) + 2 * d + (q + d) + (q + d) + (h + 2 * d) + (h + d) + (0 if fused else 2 * (P + m + mc))
     return a * (fwd + bwd)
 
 
@@ -310,8 +319,9 @@ def main():
     dom_us = per_call[dom]['mean_us']
     achieved = algo[dom] * tokens / (dom_us * 1e-6)
     hip_ms_per_step = sum(v['total_ms'] for v in per_call.values()) / args.steps
-    hip_b = hip_bytes_per_token(d, P, cf, T, layer.vistos, a=2 if bf16 else 4, K=layer.sufijo)
-    layer_b = hip_b + gemm_bytes_per_token(d, P, cf, a=2 if bf16 else 4)
+    fused = not bf16                    # the fused hash kernels run in fp32 outside autocast
+    hip_b = hip_bytes_per_token(d, P, cf, T, layer.vistos, a=2 if bf16 else 4, K=layer.sufijo, fused=fused)
+    layer_b = hip_b + gemm_bytes_per_token(d, P, cf, a=2 if bf16 else 4, fused=fused)
 
     out = {
         'metric': METRIC, 'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps,

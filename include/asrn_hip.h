@@ -144,6 +144,24 @@ int asrn_hidden_fwd(const float* y, int64_t ldy, const float* b_word, const floa
 int asrn_hidden_bwd(const float* y, int64_t ldy, const float* b_word, const float* b_ctx, int64_t B, int64_t L,
                     int32_t m, int32_t mc, const float* dg, float* dy, int64_t ldd, void* stream);
 
+/* ---- a0 (part): the hash MLPs from their first layers to phi, fused (asrn/nucleo.py:644-659) ---------------------
+ * Replaces the GELU and both second layers of afin_palabra and afin_contexto (and the block-diagonal GEMM they would
+ * be): with y as for asrn_hidden_fwd, hash_fwd writes phi (B*L, Pw + Pc) = [gelu(hp + b_word) W2w^T + b2w |
+ * gelu(za + zb[t-1] + b_ctx) W2c^T + b2c], W2w (Pw, m) = afin_palabra[2].weight, W2c (Pc, mc) = afin_contexto[2].weight.
+ * hash_bwd, from dphi (B*L, Pw + Pc), writes columns [0, m + 2 mc) of dy (B*L, ldd) as asrn_hidden_bwd does, and
+ * dparams = [dW2w (Pw*m) | dW2c (Pc*mc) | db2w (Pw) | db2c (Pc) | db_word (m) | db_ctx (mc)], summed over the tokens
+ * in a fixed order. The second layers run on the matrix cores. m, mc multiples of 4 in [4, 64] with (m + mc) / 4
+ * dividing 256; Pw, Pc in [1, 64]; y, dy rows and the first-layer biases 16-byte aligned.
+ * workspace: asrn_hash_bwd_workspace(...) bytes, 256-byte aligned. */
+int asrn_hash_fwd(const float* y, int64_t ldy, const float* b_word, const float* b_ctx, const float* w2_word,
+                  const float* b2_word, const float* w2_ctx, const float* b2_ctx, int64_t B, int64_t L, int32_t m,
+                  int32_t mc, int32_t p_word, int32_t p_ctx, float* phi, void* stream);
+int64_t asrn_hash_bwd_workspace(int64_t B, int64_t L, int32_t m, int32_t mc, int32_t p_word, int32_t p_ctx);
+int asrn_hash_bwd(const float* y, int64_t ldy, const float* b_word, const float* b_ctx, const float* w2_word,
+                  const float* w2_ctx, int64_t B, int64_t L, int32_t m, int32_t mc, int32_t p_word, int32_t p_ctx,
+                  const float* dphi, float* dy, int64_t ldd, float* dparams, void* workspace, int64_t workspace_bytes,
+                  void* stream);
+
 /* ---- column sums -----------------------------------------------------------------------------------------------
  * No counterpart in the reference's FFI: the reductions PyTorch's autograd runs for it (the bias gradients of its
  * nn.Linear projections, asrn/nucleo.py:591-630, and the parameter sums of the candidate backward, nucleo:465-515).

@@ -470,19 +470,21 @@ def test_weight_assembly_is_exact(d, kw):
     pal, ctx = layer.afin_palabra, layer.afin_contexto
     mc = ctx[0].out_features
     ref = [torch.cat([pal[0].weight, ctx[0].weight.view(mc, 2, d).transpose(0, 1).reshape(2 * mc, d)]),
-           torch.block_diag(pal[2].weight, ctx[2].weight), torch.cat([pal[2].bias, ctx[2].bias]),
-           torch.cat([layer.cq.weight, layer.ck.weight])]
-    got = layer._pesos()
+           torch.cat([layer.cq.weight, layer.ck.weight]), torch.block_diag(pal[2].weight, ctx[2].weight),
+           torch.cat([pal[2].bias, ctx[2].bias])]
+    params = [pal[0].weight, ctx[0].weight, layer.cq.weight, layer.ck.weight, pal[2].weight, ctx[2].weight,
+              pal[2].bias, ctx[2].bias]
     g = torch.Generator().manual_seed(d)
     gs = [torch.randn(r.shape, generator=g).to(DEV) for r in ref]
-    params = [pal[0].weight, ctx[0].weight, pal[2].weight, ctx[2].weight, pal[2].bias, ctx[2].bias, layer.cq.weight,
-              layer.ck.weight]
-    want = torch.autograd.grad(sum((r * x).sum() for r, x in zip(ref, gs)), params)
-    have = torch.autograd.grad(sum((r * x).sum() for r, x in zip(got, gs)), params)
-    for r, x in zip(ref, got):
-        assert torch.equal(r, x)
-    for a, b in zip(want, have):
-        assert torch.equal(a, b)
+    for k in (8, 4):             # with the second layers' blocks, and without (the fused hash kernels' path)
+        got = _Pesos.apply(*params[:k])
+        assert len(got) == k // 2
+        want = torch.autograd.grad(sum((r * x).sum() for r, x in zip(ref[:k // 2], gs)), params[:k])
+        have = torch.autograd.grad(sum((r * x).sum() for r, x in zip(got, gs)), params[:k])
+        for r, x in zip(ref, got):
+            assert torch.equal(r, x)
+        for a, b in zip(want, have):
+            assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize('M,N,K', [(256, 256, 256), (33, 70, 129), (1, 17, 5), (512, 96, 768)])
@@ -502,15 +504,20 @@ def test_small_matmul_vs_fp64(M, N, K):
     assert_close(Bd.grad, Br.grad, 'dB', 1e-5)
 
 
-@pytest.mark.parametrize('B,L,d,rows_grad', [(2, 777, 96, True), (2, 777, 96, False), (3, 1, 64, True),
-                                             (1, 2048, 256, True)])
-def test_hash_producer_vs_oracle(B, L, d, rows_grad):
-    """phi from the fused producer (one GEMM, asrn_hidden_fwd/bwd, column sums for the biases) against the oracle's
-    word and context MLPs on the materialized key [E_t; E_{t-1}] (fp64 on the CPU): phi, the gradient of E and of
-    every MLP parameter. rows_grad: the E rows the producer hands on (the candidate kernels' values) also receive a
-    gradient, which the producer's input-gradient GEMM accumulates into."""
-    say('hash producer', B, L, d, rows_grad)
-    layer = synth.move_params(CapaASRNEstable(d), seed=B + d)
+@pytest.mark.parametrize('B,L,d,kw,rows_grad', [(2, 777, 96, {}, True), (2, 777, 96, {}, False), (3, 1, 64, {}, True),
+                                                (1, 2048, 256, {}, True), (2, 300, 32, dict(n_tablas=5, tablas_contexto=2,
+                                                                                          n_bits=3), True),
+                                                (2, 300, 32, dict(afin_oculto=16), True),
+                                                (2, 300, 32, dict(afin_oculto=160), True)])
+def test_hash_producer_vs_oracle(B, L, d, kw, rows_grad):
+    """phi from the fused hash producer (one GEMM, then asrn_hash_fwd/bwd: the hidden layer and both second layers
+    on the matrix cores, every parameter gradient summed in order) against the oracle's word and context MLPs on the
+    materialized key [E_t; E_{t-1}] (fp64 on the CPU): phi, the gradient of E and of every MLP parameter. Odd output
+    widths (9 and 6) and 8 hidden units take the same kernels; 80 hidden units take the unfused path (the first
+    layers' GEMM, asrn_hidden_fwd/bwd, a block-diagonal GEMM). rows_grad: the E rows the producer hands on (the
+    candidate kernels' values) also receive a gradient, which the producer's input-gradient GEMM accumulates into."""
+    say('hash producer', B, L, d, kw, rows_grad)
+    layer = synth.move_params(CapaASRNEstable(d, **kw), seed=B + d)
     p = {k: v.detach().clone() for k, v in layer.state_dict().items()}
     g = torch.Generator().manual_seed(L)
     E = torch.randn(B, L, d, generator=g)
