@@ -16,7 +16,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
-from .lineal import column_sums, lineal
+from .lineal import _rows, column_sums, lineal, weight_grad
 
 PROHIBIDO = -1e9          # the "not allowed" score (asrn/nucleo.py:86)
 
@@ -225,7 +225,7 @@ class CapaASRNEstable(nn.Module):
         suma, sen = ops.Candidates.apply(phi, filas, Qc, Kc, Bt, log_alfa, self.w_sufijo, self.gamma, sig, order,
                                          win, rank, shape)
         # sum over tables of att E[s+1]: W_v and W_o are applied together after it (see _phi_y_valores)
-        return {'salida': suma, 'senales': sen, 'w_salida': ops.SmallMatmul.apply(self.o.weight, self.v.weight)}
+        return {'salida': suma, 'senales': sen}
 
     def _repeticion(self, sig, beta, Bt, log_alfa, partes=None, ngram=None):
         """vistos, hawkes (B, L, n) and racha (B, L) (asrn/estable.py:304-321); ngram: ops.ngram_sort(sig, ...) when
@@ -246,9 +246,16 @@ class CapaASRNEstable(nn.Module):
     def _combinar(self, acc, h):
         """h' = h + sigmoid(logit) W_o (salida / max(1, peso_total)): W_o on hipBLASLt, the rest fused in asrn_gate_*
         (the division by the table count is applied after W_o, per token). acc['w_salida'], when present, replaces W_o
-        (the whole-text path passes W_o W_v with the gathered sum of E rows)."""
+        (the whole-text path passes W_o W_v with the gathered sum of E rows); acc['gemelo'], when present, takes the
+        projection's weight gradient (_Gemelo), and the GEMM here computes only the input gradient."""
         p = self.protecciones
-        aporte = self.drop(lineal(acc['salida'], acc.get('w_salida', self.o.weight)))
+        w = acc.get('w_salida', self.o.weight)
+        gemelo = acc.get('gemelo')
+        if gemelo is None:
+            aporte = lineal(acc['salida'], w)
+        else:
+            aporte = _ConPeso.apply(lineal(acc['salida'], w.detach()), gemelo)
+        aporte = self.drop(aporte)
         meta = (self.n_tablas, self.tablas_contexto, self.racha_paso,
                 -1.0 if p.mejor_max is None else float(p.mejor_max), 0.0 if p.tope_puerta is None else float(p.tope_puerta))
         return ops.Gate.apply(h, aporte, acc['senales'], acc['vistos'], acc['hawkes'], acc['racha'], self.g.weight,
@@ -265,15 +272,17 @@ class CapaASRNEstable(nn.Module):
         """forward; with a dict `partes`, also keeps what the generation step starts from (the prompt's phi, V,
         Qc, Kc, sig, beta, Bt, log_alfa, n-gram keys and their sort, hawkes and racha)."""
         self._revisar(E)
-        sig = self._firma(E) if piezas is None else firmas_de_piezas(piezas)
-        # Two streams: the context producer (LayerNorm, Qc/Kc, the clock) and the repetition branch (n-gram sort,
-        # Hawkes and streak scans: small, latency-bound kernels) run on the second one, beside the hash producers and
-        # the bucket sort; the candidate attention waits for the context only. Autograd runs each op's backward on
-        # the stream of its forward, so the backward overlaps the same way.
+        # Two streams: the context producer (LayerNorm, Qc/Kc, the clock), the token signatures, W_o W_v and the
+        # repetition branch (n-gram sort, Hawkes and streak scans: small, latency-bound kernels) run on the second
+        # one, beside the hash producers and the bucket sort; the candidate attention waits for the context only.
+        # Autograd runs each op's backward on the stream of its forward, so the backward overlaps the same way, and
+        # the W_o W_v projection's weight gradient (_Gemelo) runs there too.
         principal, lado = torch.cuda.current_stream(E.device), _lateral(E.device)
         pesos = self._pesos(E)
         lado.wait_stream(principal)
         with torch.cuda.stream(lado):
+            sig = self._firma(E) if piezas is None else firmas_de_piezas(piezas)
+            w_salida = ops.SmallMatmul.apply(self.o.weight, self.v.weight)
             Qc, Kc, beta, log_alfa, h = self._contexto(h, con_h=True, pesos=pesos)
             Bt = ops.ClockScan.apply(beta)
             contexto_listo = torch.cuda.Event()
@@ -281,14 +290,16 @@ class CapaASRNEstable(nn.Module):
             with torch.no_grad():
                 ngram = ops.ngram_sort(sig, self.c_vistos, self.vistos)
             rep = self._repeticion(sig, beta, Bt, log_alfa, partes, ngram)
-        for t in [sig] + ([pesos['Wq']] if pesos is not None else []):
-            t.record_stream(lado)                      # made here, used there: not reused before both are done
+        if pesos is not None:
+            pesos['Wq'].record_stream(lado)            # made here, used there: not reused before both are done
         acc = self._acumular(E, Qc, Kc, Bt, log_alfa, sig, partes, pesos,
                              esperar=lambda: principal.wait_event(contexto_listo))
+        with torch.cuda.stream(lado):
+            gemelo = _Gemelo.apply(acc['salida'], w_salida)    # launches nothing
         principal.wait_stream(lado)
-        for t in [Qc, Kc, beta, Bt, log_alfa, h] + list(rep.values()) + list(ngram):
+        for t in [Qc, Kc, beta, Bt, log_alfa, h, sig, w_salida] + list(rep.values()) + list(ngram):
             t.record_stream(principal)
-        acc.update(rep)
+        acc.update(rep, w_salida=w_salida, gemelo=gemelo)
         if partes is not None:
             partes.update(Qc=Qc, Kc=Kc, sig=sig, beta=beta, Bt=Bt, log_alfa=log_alfa, hawkes=acc['hawkes'],
                           racha=acc['racha'])
@@ -307,6 +318,44 @@ def _lateral(device):
     if s is None:
         s = _LATERAL[i] = torch.cuda.Stream(device=i)
     return s
+
+
+class _Gemelo(torch.autograd.Function):
+    """Stands in for the projection A = x W^T in W's part of the autograd graph: no value and no memory (a stride-0
+    view of an uninitialized scalar), and it reads nothing in the forward. Its backward receives dA (from _ConPeso)
+    and returns dW = dA^T x, cast and summed over token slabs as lineal's own backward does, on the stream the forward
+    was called on: the weight gradient's GEMM runs there, beside the input gradient's."""
+
+    @staticmethod
+    def forward(ctx, x, w):
+        dev = x.device.type
+        ctx.dt = torch.get_autocast_dtype(dev) if torch.is_autocast_enabled(dev) else x.dtype
+        ctx.wdt = w.dtype
+        ctx.save_for_backward(x)
+        return torch.empty((), dtype=ctx.dt, device=x.device).expand(*x.shape[:-1], w.shape[0])   # A's dtype
+
+    @staticmethod
+    def backward(ctx, g):
+        x, = ctx.saved_tensors
+        s = torch.cuda.current_stream(g.device)
+        g.record_stream(s)                             # both made on the other stream and read here
+        x.record_stream(s)
+        with torch.autocast(device_type=g.device.type, enabled=False):
+            gw = weight_grad(_rows(g.to(ctx.dt)), _rows(x.to(ctx.dt)))
+        return None, gw.to(ctx.wdt)
+
+
+class _ConPeso(torch.autograd.Function):
+    """A itself (an alias); the backward hands dA to A's producer and to the _Gemelo that takes its weight
+    gradient."""
+
+    @staticmethod
+    def forward(ctx, a, gemelo):
+        return a.view_as(a)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g, g
 
 
 class _ShiftAdd(torch.autograd.Function):
