@@ -281,7 +281,9 @@ class CapaASRNEstable(nn.Module):
         pesos = self._pesos(E)
         lado.wait_stream(principal)
         with torch.cuda.stream(lado):
-            sig = self._firma(E) if piezas is None else firmas_de_piezas(piezas)
+            # signatures carry no gradient (they are only compared); a detached E keeps E's gradient accumulation
+            # on the main stream, where its gradient is made
+            sig = self._firma(E.detach()) if piezas is None else firmas_de_piezas(piezas)
             w_salida = ops.SmallMatmul.apply(self.o.weight, self.v.weight)
             Qc, Kc, beta, log_alfa, h = self._contexto(h, con_h=True, pesos=pesos)
             Bt = ops.ClockScan.apply(beta)

@@ -658,7 +658,7 @@ def layer_from_fixture(p, m):
 def run_layer(layer, E, h, x, gy):
     layer.zero_grad()
     Ed, hd = E.to(DEV).requires_grad_(), h.to(DEV).requires_grad_()
-    y = layer(Ed, hd, x.to(DEV))
+    y = layer(Ed, hd, None if x is None else x.to(DEV))
     (y * gy.to(DEV)).sum().backward()
     grads = {'E': Ed.grad.cpu(), 'h': hd.grad.cpu()}
     grads.update({n: q.grad.cpu() for n, q in layer.named_parameters() if q.grad is not None})
@@ -753,6 +753,43 @@ def test_layer_odd_feature_widths_vs_oracle():
               for k, v in p.items()}
     Ec, hc = E.clone().requires_grad_(), h.clone().requires_grad_()
     yo = O.layer_forward(leaves, Ec, hc, x, sh)
+    (yo * gy).sum().backward()
+    assert_close(y, yo, 'y')
+    assert_close(grads['E'], Ec.grad, 'grad E')
+    assert_close(grads['h'], hc.grad, 'grad h')
+    for n, g in grads.items():
+        if n in leaves and leaves[n].grad is not None:
+            assert_close(g, leaves[n].grad, 'grad ' + n)
+
+
+def test_layer_signatures_from_E_vs_oracle():
+    """No token ids: the signatures are E r_firma (asrn/nucleo.py:161-164), computed on the layer's second stream.
+    Outputs and every gradient match the oracle, and E's gradient is accumulated without a stream-mismatch warning
+    (the signatures take no gradient, so the second stream holds no edge to E)."""
+    say('layer signatures from E')
+    torch.manual_seed(6)
+    kw = dict(n_tablas=5, tablas_contexto=2, n_bits=4, confirmar=8, chunk=8)
+    layer = synth.move_params(CapaASRNEstable(32, **kw), 6)
+    p = {k: v.detach().clone() for k, v in layer.state_dict().items()}
+    sh = O.shape_from_params(p, 32, n_bits=4, C=8)
+    _, E, h = synth.layer_inputs(2, 400, 32, 9, seed=7)
+    gy = torch.randn(2, 400, 32, generator=torch.Generator().manual_seed(8))
+    layer = layer.to(DEV)
+    with torch.no_grad():
+        phi, _ = layer._phi_y_valores(E.to(DEV))
+    ids, _ = O.bucket_rows(phi.cpu(), sh.T, sh.nb)
+    ref_ids, _ = O.bucket_rows(O.phi_and_values(p, E)[0], sh.T, sh.nb)
+    if not torch.equal(ids, ref_ids):
+        pytest.skip('a bucket id differs between the GPU GEMM and the CPU one (sign of phi near 0)')
+    import warnings
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter('always')
+        y, grads = run_layer(layer, E, h, None, gy)
+    assert not [w for w in caught if 'AccumulateGrad' in str(w.message)]
+    leaves = {k: (v.clone().requires_grad_() if v.is_floating_point() and k not in ('c_vistos', 'r_firma') else v)
+              for k, v in p.items()}
+    Ec, hc = E.clone().requires_grad_(), h.clone().requires_grad_()
+    yo = O.layer_forward(leaves, Ec, hc, None, sh)
     (yo * gy).sum().backward()
     assert_close(y, yo, 'y')
     assert_close(grads['E'], Ec.grad, 'grad E')
