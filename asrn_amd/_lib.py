@@ -55,10 +55,11 @@ SIGNATURES = {
     'asrn_gate_bwd': (ctypes.c_int, [_P, _P, _I32] + [_P] * 11 + [_I64] + [_I32] * 5 + [_F32] * 3 + [_P] * 8
                       + [_I64, _P]),
     'asrn_ring_build': (ctypes.c_int, [_P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P]),
-    'asrn_decode_attend': (ctypes.c_int, [_P] * 11 + [_I64, _I64, _I64] + [_I32] * 7 + [_F32, _F32, _I32] + [_P] * 4),
+    'asrn_decode_attend': (ctypes.c_int, [_P] * 11 + [_I64, _I64, _I64, _P] + [_I32] * 7 + [_F32, _F32, _I32]
+                           + [_P] * 4),
     'asrn_hawkes_table_load': (ctypes.c_int, [_P] * 6 + [_I64, _I64, _I32, _I64] + [_P] * 4),
     'asrn_hawkes_table_grow': (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _P, _P, _I64, _P]),
-    'asrn_repetition_step': (ctypes.c_int, [_P] * 7 + [_I64, _I64, _I64, _I32, _I64] + [_P] * 7),
+    'asrn_repetition_step': (ctypes.c_int, [_P] * 7 + [_I64, _I64, _I64, _P, _I32, _I64] + [_P] * 7),
 }
 
 _lib = None

@@ -53,6 +53,7 @@ struct Cand {
   // generation: per-bucket rings (B*T, 2^nb, C) of positions and their counts (B*T, 2^nb); the query position tq,
   // its bucket ids (B, T) out, and whether tq then enters the rings
   int32_t* rings; int32_t* counts; int32_t* ids_out; int nb; int64_t tq; int insert;
+  const int64_t* tq_dev;   // generation, optional: the query position read from device memory instead of tq
 };
 
 // per-wave LDS scratch: one token's candidate list (entries) and its distinct positions (uniques)
@@ -717,22 +718,24 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_fwd(Cand a) {
                                 a.ent + tok * a.T * a.C * 2);
 }
 
-// Generation step: one wave per batch row; the query is position a.tq of the caches (a.L = their capacity). With
-// a.insert, tq then enters its bucket's ring in every table at slot count % C, overwriting the oldest (reference
-// nucleo:1610-1618). Only this wave touches batch row b's rings, and its ring reads were consumed before.
+// Generation step: one wave per batch row; the query is position tq = a.tq (or *a.tq_dev) of the caches (a.L = their
+// capacity; a position outside them writes nothing). With a.insert, tq then enters its bucket's ring in every table
+// at slot count % C, overwriting the oldest (reference nucleo:1610-1618). Only this wave touches batch row b's rings,
+// and its ring reads were consumed before.
 template <int F4, int DCH>
 __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_decode_attend(Cand a) {
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
   const int64_t b = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (b >= a.B) return;
-  forward_token<F4, DCH, true>(a, b, a.tq, S, a.salida + b * a.d, a.signals + b * 4, nullptr);
+  const int64_t tq = a.tq_dev ? *a.tq_dev : a.tq;
+  if (b >= a.B || tq < 0 || tq >= a.L) return;
+  forward_token<F4, DCH, true>(a, b, tq, S, a.salida + b * a.d, a.signals + b * 4, nullptr);
   const int lane = lane_id();
   if (a.insert && lane < a.T) {
     const int id = a.ids_out[b * a.T + lane];
     const int64_t bucket = (b * a.T + lane) * ((int64_t)1 << a.nb) + id;
     const int c = a.counts[bucket];
-    a.rings[bucket * a.C + c % a.C] = (int32_t)a.tq;
+    a.rings[bucket * a.C + c % a.C] = (int32_t)tq;
     a.counts[bucket] = c + 1;
   }
 }
@@ -1181,7 +1184,8 @@ extern "C" int asrn_candidate_lists(const float* sig, const int32_t* order, cons
 extern "C" int asrn_decode_attend(const float* phi, const float* V, const float* Qc, const float* Kc,
                                   const float* sig, const double* Bt, const float* log_alfa, const float* w_suf,
                                   const float* gamma, int32_t* rings, int32_t* counts, int64_t B, int64_t cap,
-                                  int64_t t, int32_t d, int32_t nb, int32_t cf, int32_t K, int32_t T, int32_t Tc,
+                                  int64_t t, const int64_t* t_dev, int32_t d, int32_t nb, int32_t cf, int32_t K,
+                                  int32_t T, int32_t Tc,
                                   int32_t C, float scale_phi, float scale_c, int32_t insert, float* salida,
                                   float* signals, int32_t* ids, void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, nullptr, nullptr, nullptr, B, cap, d, T * nb, cf,
@@ -1191,7 +1195,8 @@ extern "C" int asrn_decode_attend(const float* phi, const float* V, const float*
   ASRN_REQUIRE(t >= 0 && t < cap, "asrn_decode_attend: position t=%lld outside the caches (capacity %lld)",
                (long long)t, (long long)cap);
   if (B == 0) return 0;
-  a.rings = rings; a.counts = counts; a.ids_out = ids; a.nb = nb; a.tq = t; a.insert = insert ? 1 : 0;
+  a.rings = rings; a.counts = counts; a.ids_out = ids; a.nb = nb; a.tq = t; a.tq_dev = t_dev;
+  a.insert = insert ? 1 : 0;
   a.salida = salida; a.signals = signals;
   return dispatch<LaunchDecode>(a, (hipStream_t)stream);
 }

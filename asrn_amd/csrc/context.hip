@@ -10,8 +10,9 @@
 //   g = dhh + du_0 w_reloj[0] + du_1 w_reloj[1],  dxhat = g ln_w
 //   dh = rstd (dxhat - mean(dxhat) - xhat mean(dxhat xhat)) [+ dh_add: h's gradient through the layer's other use]
 //   d ln_w = sum_t g xhat, d ln_b = sum_t g, d w_reloj[k] = sum_t du_k hh, d b_reloj[k] = sum_t du_k
-// A workgroup takes 32 tokens, each wave 8 of them, loading 2 tokens' rows (float4 per lane) at a time; the parameter
-// gradients are per-workgroup partials summed in order by a second launch (deterministic, no atomics).
+// Forward: a workgroup takes 8 tokens, each wave 2 of them with both rows (float4 per lane) loaded at once. Backward:
+// a workgroup takes 32 tokens, each wave 8 of them, loading 2 tokens' rows at a time; the parameter gradients are
+// per-workgroup partials summed in order by a second launch (deterministic, no atomics).
 #include "common.h"
 
 namespace asrn {
@@ -21,6 +22,8 @@ constexpr int kCtxWaves = kCtxThreads / kWave;
 constexpr int kCtxTok = 32;
 constexpr int kCtxTokPerWave = kCtxTok / kCtxWaves;
 constexpr int kCtxBatch = 2;
+constexpr int kCtxFwdTok = 8;              // forward: tokens per workgroup, one round of loads per wave
+constexpr int kCtxFwdPerWave = kCtxFwdTok / kCtxWaves;
 constexpr int kCtxMaxD4 = 4;    // d <= 1024
 
 struct CtxArgs {
@@ -41,8 +44,8 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_fwd(CtxArgs a) {
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int d4 = a.d >> 2;
   const float inv_d = 1.f / (float)a.d;
-  const int64_t tw = (int64_t)blockIdx.x * kCtxTok + wave * kCtxTokPerWave;
-  for (int b = 0; b < kCtxTokPerWave; b += kCtxBatch) {
+  const int64_t tw = (int64_t)blockIdx.x * kCtxFwdTok + wave * kCtxFwdPerWave;
+  for (int b = 0; b < kCtxFwdPerWave; b += kCtxBatch) {
     float4 hv[kCtxBatch][D4];
     float s[kCtxBatch];
 #pragma unroll
@@ -111,12 +114,13 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
 #pragma unroll
   for (int k = 0; k < D4; ++k) gw[k] = gb[k] = gr0[k] = gr1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
   float gbr0 = 0.f, gbr1 = 0.f;
-  for (int b = 0; b < kCtxTokPerWave; b += kCtxBatch) {
-    float4 hv[kCtxBatch][D4], gv[kCtxBatch][D4], av[kCtxBatch][D4];
-    float4 st[kCtxBatch];
-    float db[kCtxBatch], dl[kCtxBatch];
+  constexpr int BB = kCtxBatch;                  // tokens whose rows are loaded together
+  for (int b = 0; b < kCtxTokPerWave; b += BB) {
+    float4 hv[BB][D4], gv[BB][D4], av[BB][D4];
+    float4 st[BB];
+    float db[BB], dl[BB];
 #pragma unroll
-    for (int u = 0; u < kCtxBatch; ++u) {
+    for (int u = 0; u < BB; ++u) {
       const int64_t t = tw + b + u;
       const bool ok = t < a.BL;
       st[u] = ok ? a.stats[t] : make_float4(0.f, 1.f, 0.f, 0.f);
@@ -133,7 +137,7 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
       }
     }
 #pragma unroll
-    for (int u = 0; u < kCtxBatch; ++u) {
+    for (int u = 0; u < BB; ++u) {
       const int64_t t = tw + b + u;
       if (t >= a.BL) break;
       const float mean = st[u].x, rstd = st[u].y, u0 = st[u].z, u1 = st[u].w;
@@ -237,6 +241,7 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_params(const float* __restr
 }
 
 static int64_t ctx_groups(int64_t BL) { return BL > 0 ? (BL + kCtxTok - 1) / kCtxTok : 1; }
+static int64_t ctx_fwd_groups(int64_t BL) { return (BL + kCtxFwdTok - 1) / kCtxFwdTok; }
 
 static int ctx_check(const CtxArgs& a, const char* what) {
   ASRN_REQUIRE(a.BL >= 0, "%s: bad sizes", what);
@@ -260,7 +265,8 @@ extern "C" int asrn_context_fwd(const float* h, const float* ln_w, const float* 
   a.beta_max = beta_max; a.la_min = log_alfa_min; a.hh = hh; a.stats = (float4*)stats; a.beta = beta; a.la = log_alfa;
   if (ctx_check(a, "asrn_context_fwd")) return 1;
   if (BL == 0) return 0;
-  const dim3 grid((unsigned)ctx_groups(BL)), block(kCtxThreads);
+  ASRN_REQUIRE(ctx_fwd_groups(BL) < (int64_t(1) << 31), "asrn_context_fwd: too many tokens");
+  const dim3 grid((unsigned)ctx_fwd_groups(BL)), block(kCtxThreads);
   hipStream_t st = (hipStream_t)stream;
   switch ((d + 4 * kWave - 1) / (4 * kWave)) {
     case 1: hipLaunchKernelGGL(k_ctx_fwd<1>, grid, block, 0, st, a); break;

@@ -155,6 +155,7 @@ struct Step {
   const float* sig; double* Bt; const float* la; const double* beta_t; const double* coef; const float* kappa;
   const float* kappa_r; int64_t B, stride, t; int n;
   float* racha; float* vistos; float* hawkes;
+  const int64_t* t_dev;    // optional: the position read from device memory instead of t
 };
 
 __global__ void k_repetition_step(Step a, Table tb) {
@@ -162,7 +163,8 @@ __global__ void k_repetition_step(Step a, Table tb) {
   if (e >= a.B * a.n) return;
   const int64_t b = e / a.n;
   const int j = (int)(e % a.n);
-  const int64_t t = a.t;
+  const int64_t t = a.t_dev ? *a.t_dev : a.t;
+  if (t < 0 || t >= a.stride) return;                            // outside the caches: nothing written
   const double* Btb = a.Bt + b * a.stride;
   const double Bq = (t > 0 ? Btb[t - 1] : 0.0) + a.beta_t[b];     // the clock advances (nucleo:1826)
   if (j == 0) a.Bt[b * a.stride + t] = Bq;
@@ -260,7 +262,8 @@ extern "C" int asrn_hawkes_table_grow(const uint64_t* old_keys, const double* ol
 
 extern "C" int asrn_repetition_step(const float* sig, double* Bt, const float* log_alfa, const double* beta_t,
                                     const double* coef, const float* kappa, const float* kappa_r, int64_t B,
-                                    int64_t stride, int64_t t, int32_t n, int64_t cap, uint64_t* tab_keys,
+                                    int64_t stride, int64_t t, const int64_t* t_dev, int32_t n, int64_t cap,
+                                    uint64_t* tab_keys,
                                     double* tab_Bu, float* tab_A, float* racha, float* vistos, float* hawkes,
                                     void* stream) {
   ASRN_REQUIRE(B >= 0 && n >= 1 && n <= 16 && t >= 0 && t < stride,
@@ -270,7 +273,7 @@ extern "C" int asrn_repetition_step(const float* sig, double* Bt, const float* l
                "asrn_repetition_step: table capacity %lld must be a power of two >= 2 (t + 1) = %lld: grow it first",
                (long long)cap, (long long)(2 * (t + 1)));
   if (B == 0) return 0;
-  Step a = {sig, Bt, log_alfa, beta_t, coef, kappa, kappa_r, B, stride, t, n, racha, vistos, hawkes};
+  Step a = {sig, Bt, log_alfa, beta_t, coef, kappa, kappa_r, B, stride, t, n, racha, vistos, hawkes, t_dev};
   Table tb = {tab_keys, tab_Bu, tab_A, cap};
   hipLaunchKernelGGL(k_repetition_step, dim3((unsigned)((B * n + kThreads - 1) / kThreads)), dim3(kThreads), 0,
                      (hipStream_t)stream, a, tb);

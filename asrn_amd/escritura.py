@@ -17,6 +17,12 @@ as in the whole-text layer. Every step reads a fixed amount, T*C candidates, wha
 memoria_de_lo_ajeno=True (the reference default): the keys are only prompt positions k with k + 1 < L0 (their V rows
 are values of prompt tokens), so the rings hold positions 0..L0-2 and never change. False: every earlier position is
 a key, and the step equals the whole-text layer position by position.
+
+grafo=True: the step is captured once in a HIP graph and replayed, since launching its ~30 small kernels from Python
+costs several times their GPU time. The position then lives in a device counter that the two HIP kernels read and the
+graph advances; the first step runs eagerly (it initializes the GEMM libraries' handles), the second is captured, and
+a capacity doubling (new cache tensors) captures again. The graph holds the layer's parameters and this writer's
+state by address: replacing a parameter tensor (rather than updating it in place) needs a new writer.
 """
 import torch
 
@@ -32,8 +38,9 @@ def _reservar(x, cap):
 class EscritorCapa:
     """Step-by-step writer for one CapaASRNEstable (see the module docstring)."""
 
-    def __init__(self, capa, memoria_de_lo_ajeno=True):
-        self.capa, self.ajeno = capa, memoria_de_lo_ajeno
+    def __init__(self, capa, memoria_de_lo_ajeno=True, grafo=False):
+        self.capa, self.ajeno, self.grafo = capa, memoria_de_lo_ajeno, grafo
+        self._g = None
 
     def _forma(self):
         c = self.capa
@@ -71,38 +78,84 @@ class EscritorCapa:
         self.racha = partes['racha'][:, -1].to(f32).contiguous().clone()
         self.e_ult = E[:, -1]
         self.t = L0
+        self._g = None
+        self._calentado = False
         return y
 
     def _crecer(self):
         self.cap *= 2
         self.cache = {k: _reservar(v, self.cap) for k, v in self.cache.items()}
 
+    def _escribir(self, nombre, pos, valor):
+        """valor (B, ...) into row pos of cache[nombre]: pos an int, or a one-element device tensor."""
+        c = self.cache[nombre]
+        if torch.is_tensor(pos):
+            c.index_copy_(1, pos, valor.unsqueeze(1).to(c.dtype))
+        else:
+            c[:, pos] = valor
+
+    def _cuerpo(self, e_t, e_ult, h_t, pieza_t, pos, t_max=None):
+        """One step's work at position pos (an int, or a device counter holding it with t_max its largest value) ->
+        the layer's output (B, d) (the layer part of asrn/nucleo.py:1797-1854)."""
+        capa = self.capa
+        c = self.cache
+        self._escribir('sig', pos, pieza_t.to(torch.float32))
+        self._escribir('V', pos - 1, capa.v(e_t))                          # V[t-1] = W_v e_t
+        self._escribir('phi', pos, capa._phi(torch.stack([e_ult, e_t], 1))[:, -1])
+        Qc, Kc, beta, log_alfa = capa._contexto(h_t.unsqueeze(1))
+        self._escribir('Qc', pos, Qc[:, 0])
+        self._escribir('Kc', pos, Kc[:, 0])
+        self._escribir('log_alfa', pos, log_alfa[:, 0])
+        kappa, kappa_r = capa._kappas()
+        vistos, hawkes = self.hawkes.step(c, pos, beta[:, 0], capa.c_vistos, kappa, kappa_r, self.racha, t_max=t_max)
+        salida, sen, _ = ops.decode_attend(c, pos, self.anillos, self.cuentas, capa.w_sufijo, capa.gamma,
+                                           self._forma(), insert=not self.ajeno, t_max=t_max)
+        acc = {'salida': salida.unsqueeze(1).to(e_t.dtype), 'senales': sen[:, None],
+               'vistos': vistos.unsqueeze(1), 'hawkes': hawkes.unsqueeze(1), 'racha': self.racha.unsqueeze(1).clone()}
+        return capa._combinar(acc, h_t.unsqueeze(1))[:, 0]
+
     @torch.no_grad()
     def paso(self, e_t, h_t, pieza_t):
         """One new token at position t: e_t, h_t (B, d) its embedding and layer input, pieza_t (B,) its id ->
         the layer's output (B, d) (the layer part of asrn/nucleo.py:1797-1854)."""
-        capa = self.capa
         # rows of a (B, L, d) text are strided views; the GEMMs below want dense (B, d) operands (a batch stride
         # above 2^25 elements is outside what hipBLASLt accepts, and its fallback costs ~20 ms per call)
         e_t, h_t = e_t.contiguous(), h_t.contiguous()
         if self.t >= self.cap:
             self._crecer()
-        c, t = self.cache, self.t
-        c['sig'][:, t] = pieza_t.to(torch.float32)
-        c['V'][:, t - 1] = capa.v(e_t)                                        # V[t-1] = W_v e_t
-        c['phi'][:, t] = capa._phi(torch.stack([self.e_ult, e_t], 1))[:, -1]
-        Qc, Kc, beta, log_alfa = capa._contexto(h_t.unsqueeze(1))
-        c['Qc'][:, t], c['Kc'][:, t], c['log_alfa'][:, t] = Qc[:, 0], Kc[:, 0], log_alfa[:, 0]
-        kappa, kappa_r = capa._kappas()
-        vistos, hawkes = self.hawkes.step(c, t, beta[:, 0], capa.c_vistos, kappa, kappa_r, self.racha)
-        salida, sen, _ = ops.decode_attend(c, t, self.anillos, self.cuentas, capa.w_sufijo, capa.gamma, self._forma(),
-                                           insert=not self.ajeno)
-        acc = {'salida': salida.unsqueeze(1).to(e_t.dtype), 'senales': sen[:, None],
-               'vistos': vistos.unsqueeze(1), 'hawkes': hawkes.unsqueeze(1), 'racha': self.racha.unsqueeze(1).clone()}
-        y = capa._combinar(acc, h_t.unsqueeze(1))[:, 0]
+            self._g = None
+        if self.grafo and self._calentado:
+            return self._paso_grafo(e_t, h_t, pieza_t)
+        y = self._cuerpo(e_t, self.e_ult, h_t, pieza_t, self.t)
         self.e_ult = e_t
         self.t += 1
+        self._calentado = True
         return y
+
+    def _paso_grafo(self, e_t, h_t, pieza_t):
+        if self._g is None:
+            self._capturar(e_t, h_t, pieza_t)
+        self._e.copy_(e_t)
+        self._h.copy_(h_t)
+        self._p.copy_(pieza_t)
+        self._g.replay()
+        self.t += 1
+        self.e_ult = self._e_ult
+        return self._y.clone()
+
+    def _capturar(self, e_t, h_t, pieza_t):
+        """Captures one step whose position is the device counter _pos (valid for positions < cap, the caches'
+        capacity): the step, then e_ult <- e_t and _pos += 1."""
+        self.hawkes.reserve(self.cap)          # tables sized for every position the graph will see: no growth inside
+        self._e, self._h, self._p = torch.empty_like(e_t), torch.empty_like(h_t), torch.empty_like(pieza_t)
+        self._e_ult = self.e_ult.clone()
+        self._pos = torch.full((1,), self.t, dtype=torch.int64, device=e_t.device)
+        torch.cuda.current_stream(e_t.device).synchronize()
+        self._g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self._g):
+            self._y = self._cuerpo(self._e, self._e_ult, self._h, self._p, self._pos, t_max=self.cap - 1)
+            self._e_ult.copy_(self._e)
+            self._pos.add_(1)
 
 
 LayerWriter = EscritorCapa

@@ -618,10 +618,22 @@ def ring_build(phi_prefix, T, nb, C):
     return rings, counts
 
 
-def decode_attend(cache, t, rings, counts, w_suf, gamma, shape, insert):
+def _posicion(t, t_max):
+    """The position for the generation entry points: (host int, device pointer). t an int: (t, None); t a one-element
+    int64 device tensor (the position as a step captured in a graph reads it): (t_max, its pointer), t_max being the
+    largest position it will hold, which the host checks against the capacities."""
+    if torch.is_tensor(t):
+        if t.dtype != torch.int64 or t.numel() != 1 or not t.is_cuda or t_max is None:
+            raise ValueError('a device position is a one-element int64 cuda tensor, with t_max given')
+        return int(t_max), ptr(t)
+    return int(t), None
+
+
+def decode_attend(cache, t, rings, counts, w_suf, gamma, shape, insert, t_max=None):
     """The step's candidate attention for position t of the caches (dict of (B, cap, .) tensors phi, V, Qc, Kc, sig,
     Bt, log_alfa) over the rings; with insert, t then enters the rings. Returns salida (B, d), signals (B, 4) and
-    the bucket ids (B, T)."""
+    the bucket ids (B, T). t: an int, or a one-element int64 device tensor holding it (then t_max: the largest
+    position it will hold)."""
     T, Tc, C, K, nb = shape['T'], shape['Tc'], shape['C'], shape['K'], shape['nb']
     phi, V = cache['phi'], cache['V']
     dev = _dev(phi)
@@ -634,10 +646,11 @@ def decode_attend(cache, t, rings, counts, w_suf, gamma, shape, insert):
     ids = torch.empty((B, T), dtype=I32, device=dev)
     w = _c(w_suf.detach(), torch.float32)
     g = _c(gamma.detach(), torch.float32)
+    th, tdev = _posicion(t, t_max)
     call('asrn_decode_attend', ptr(phi), ptr(V), ptr(cache['Qc']), ptr(cache['Kc']), ptr(cache['sig']),
-         ptr(cache['Bt']), ptr(cache['log_alfa']), ptr(w), ptr(g), ptr(rings), ptr(counts), B, cap, t, d, nb, cf, K,
-         T, Tc, C, float(P) ** -0.5, float(cf) ** -0.5, 1 if insert else 0, ptr(salida), ptr(signals), ptr(ids),
-         stream_of(dev))
+         ptr(cache['Bt']), ptr(cache['log_alfa']), ptr(w), ptr(g), ptr(rings), ptr(counts), B, cap, th, tdev, d, nb,
+         cf, K, T, Tc, C, float(P) ** -0.5, float(cf) ** -0.5, 1 if insert else 0, ptr(salida), ptr(signals),
+         ptr(ids), stream_of(dev))
     return salida, signals, ids
 
 
@@ -679,17 +692,19 @@ class HawkesTable:
              ptr(new.keys), ptr(new.Bu), ptr(new.A), new.cap, stream_of(dev))
         self.keys, self.Bu, self.A, self.cap = new.keys, new.Bu, new.A, new.cap
 
-    def step(self, cache, t, beta_t, coef, kappa, kappa_r, racha):
+    def step(self, cache, t, beta_t, coef, kappa, kappa_r, racha, t_max=None):
         """Position t: Bt[:, t] = Bt[:, t-1] + beta_t (written into cache['Bt']), vistos and hawkes (B, n); racha (B)
-        is updated in place (asrn/nucleo.py:953-960, 1683-1714, 1826)."""
+        is updated in place (asrn/nucleo.py:953-960, 1683-1714, 1826). t: an int, or a one-element int64 device
+        tensor holding it (then t_max: the largest position it will hold)."""
         dev = _dev(racha)
-        self.reserve(t + 1)
+        th, tdev = _posicion(t, t_max)
+        self.reserve(th + 1)
         sig, Bt, la = cache['sig'], cache['Bt'], cache['log_alfa']
         B, stride = sig.shape
         vistos = torch.empty((B, self.n), dtype=torch.float32, device=dev)
         hawkes = torch.empty((B, self.n), dtype=torch.float32, device=dev)
         call('asrn_repetition_step', ptr(sig), ptr(Bt), ptr(la), ptr(_c(beta_t, torch.float64)),
              ptr(_c(coef, torch.float64)), ptr(_c(kappa.detach(), torch.float32)),
-             ptr(_c(kappa_r.detach(), torch.float32)), B, stride, t, self.n, self.cap, ptr(self.keys), ptr(self.Bu),
-             ptr(self.A), ptr(racha), ptr(vistos), ptr(hawkes), stream_of(dev))
+             ptr(_c(kappa_r.detach(), torch.float32)), B, stride, th, tdev, self.n, self.cap, ptr(self.keys),
+             ptr(self.Bu), ptr(self.A), ptr(racha), ptr(vistos), ptr(hawkes), stream_of(dev))
         return vistos, hawkes

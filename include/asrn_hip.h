@@ -283,12 +283,16 @@ int asrn_ring_build(const int32_t* order, const int32_t* ids_sorted, int64_t B, 
  * The caches are (B, cap, .) rows: phi (P = T*nb), V (d), Qc, Kc (cf), sig, Bt (fp64), log_alfa; row t is the
  * query (its phi, Qc, sig and Bt must be written), rows < t with a ring entry are the candidates (V[t-1] included).
  * Out: salida (B, d) summed over tables, signals (B, 4) = (peso_total, mejor, pico, peso_ctx) as in
- * asrn_candidates_fwd, ids (B, T) the query's bucket ids. */
+ * asrn_candidates_fwd, ids (B, T) the query's bucket ids.
+ * t_dev: null, or a device int64 holding the position, which the kernel then reads (a step captured once in a HIP
+ * graph and replayed as the position advances); t is then checked as the largest position it will hold, and a
+ * position outside [0, cap) writes nothing. */
 int asrn_decode_attend(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                        const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
-                       int32_t* rings, int32_t* counts, int64_t B, int64_t cap, int64_t t, int32_t d, int32_t nb,
-                       int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C, float scale_phi, float scale_c,
-                       int32_t insert, float* salida, float* signals, int32_t* ids, void* stream);
+                       int32_t* rings, int32_t* counts, int64_t B, int64_t cap, int64_t t, const int64_t* t_dev,
+                       int32_t d, int32_t nb, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
+                       float scale_phi, float scale_c, int32_t insert, float* salida, float* signals, int32_t* ids,
+                       void* stream);
 
 /* Hawkes memory: per (b, j) group an open-addressing table of cap slots (a power of two, >= 2x the keys it can
  * hold): tab_keys (B*n, cap) uint64 key codes, tab_Bu (B*n, cap) fp64 clock of the last occurrence, tab_A (B*n, cap)
@@ -306,11 +310,12 @@ int asrn_hawkes_table_grow(const uint64_t* old_keys, const double* old_Bu, const
 /* repetition_step replaces the clock advance (asrn/nucleo.py:1826), the step's n-gram keys (_claves_de,
  * asrn/nucleo.py:175-186), _MemoriaHawkes.paso (asrn/nucleo.py:1683-1714) and _repeticion_o1
  * (asrn/nucleo.py:953-960) for position t: Bt[:, t] = Bt[:, t-1] + beta_t (written), vistos and hawkes (B, n) out,
- * racha (B) updated in place. sig, Bt, log_alfa are (B, stride) caches; cap >= 2 (t + 1). */
+ * racha (B) updated in place. sig, Bt, log_alfa are (B, stride) caches; cap >= 2 (t + 1). t_dev: as for
+ * asrn_decode_attend (a position outside [0, stride) writes nothing). */
 int asrn_repetition_step(const float* sig, double* Bt, const float* log_alfa, const double* beta_t,
                          const double* coef, const float* kappa, const float* kappa_r, int64_t B, int64_t stride,
-                         int64_t t, int32_t n, int64_t cap, uint64_t* tab_keys, double* tab_Bu, float* tab_A,
-                         float* racha, float* vistos, float* hawkes, void* stream);
+                         int64_t t, const int64_t* t_dev, int32_t n, int64_t cap, uint64_t* tab_keys, double* tab_Bu,
+                         float* tab_A, float* racha, float* vistos, float* hawkes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -236,3 +236,31 @@ def test_writer_vs_oracle(B, L0, n, kw, ajeno):
     _, ys, _ = write(layer, E, h, x, L0, ajeno=ajeno, capacidad=0)
     ref, _ = G.decode_layer(p, E, h, x, L0, sh, ajeno=ajeno)
     assert_close(ys, ref, f'steps ajeno={ajeno}')
+
+
+@pytest.mark.parametrize('ajeno', [True, False])
+@pytest.mark.parametrize('B,L0,n,cap,kw', [(2, 40, 30, 45, SMALL), (3, 300, 24, 0, {}), (1, 2, 20, 4, SMALL)])
+def test_writer_graph_equals_eager(B, L0, n, cap, kw, ajeno):
+    """The step captured in a HIP graph and replayed (the position in a device counter that the kernels read and the
+    graph advances; a capacity doubling captures again) writes the same outputs, caches, rings, counts and streak as
+    the step launched op by op, bit for bit, step after step."""
+    say('writer graph = eager', B, L0, n, cap, kw, ajeno)
+    d = 32
+    torch.manual_seed(2)
+    layer = synth.move_params(CapaASRNEstable(d, **kw), 2).to(DEV)
+    x, E, h = synth.layer_inputs(B, L0 + n, d, 9, seed=7, frac=0.4, span=(3, 8))
+    Ed, hd, xd = E.to(DEV), h.to(DEV), x.to(DEV)
+    outs = []
+    for grafo in (False, True):
+        esc = EscritorCapa(layer, memoria_de_lo_ajeno=ajeno, grafo=grafo)
+        esc.inicio(Ed[:, :L0], hd[:, :L0], xd[:, :L0], capacidad=cap)
+        ys = [esc.paso(Ed[:, t], hd[:, t], xd[:, t]) for t in range(L0, L0 + n)]
+        torch.cuda.synchronize()
+        outs.append((torch.stack(ys, 1), esc))
+    (ye, ee), (yg, eg) = outs
+    assert eg._g is not None and eg.t == ee.t == L0 + n and eg.cap == ee.cap
+    assert torch.equal(yg, ye)
+    for k in ee.cache:
+        assert torch.equal(eg.cache[k][:, :L0 + n], ee.cache[k][:, :L0 + n]), k
+    assert torch.equal(eg.anillos, ee.anillos) and torch.equal(eg.cuentas, ee.cuentas)
+    assert torch.equal(eg.racha, ee.racha)

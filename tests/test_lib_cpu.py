@@ -131,11 +131,12 @@ def test_argument_checks_fail_before_any_device_work(lib):
     # generation: ring sizes, the decode position inside the caches, table capacities
     assert lib.asrn_ring_build(N, N, 2, 10, 8, 15, 32, N, N, N) != 0
     assert 'asrn_ring_build' in _err(lib)
-    assert lib.asrn_decode_attend(*([N] * 11), 2, 100, 100, 64, 14, 16, 4, 8, 4, 32, 0.1, 0.25, 1, N, N, N, N) != 0
+    assert lib.asrn_decode_attend(*([N] * 11), 2, 100, 100, N, 64, 14, 16, 4, 8, 4, 32, 0.1, 0.25, 1, N, N, N,
+                                  N) != 0
     assert 'outside the caches' in _err(lib)
     assert lib.asrn_hawkes_table_load(*([N] * 6), 2, 100, 4, 96, N, N, N, N) != 0
     assert 'power of two' in _err(lib)
-    assert lib.asrn_repetition_step(*([N] * 7), 2, 1000, 100, 4, 128, *([N] * 7)) != 0
+    assert lib.asrn_repetition_step(*([N] * 7), 2, 1000, 100, N, 4, 128, *([N] * 7)) != 0
     assert 'grow it first' in _err(lib)
     assert lib.asrn_hawkes_table_grow(N, N, N, 8, 256, N, N, N, 128, N) != 0
     assert 'growing' in _err(lib)
