@@ -384,11 +384,12 @@ __device__ __forceinline__ int dedupe(const Cand& a, int M, Scratch& S) {
 // The product is always query * key and the reduction tree is the same, so both sides produce the same bits.
 template <int F4>
 __device__ __forceinline__ void unique_bases(const Cand& a, int64_t b, int64_t self_pos, int NU,
-                                             bool rows_are_queries, const float4 (&fixed)[F4], Scratch& S) {
+                                             bool rows_are_queries, const float4 (&fixed)[F4], Scratch& S,
+                                             int first = 0, int step = 2 * kRows) {
   const int lane = lane_id(), half = lane >> 5;
   const FeatLanes<F4> fl = feat_lanes<F4>(a, rows_are_queries ? a.Qc : a.Kc, rows_are_queries);
   const uint32_t row0 = (uint32_t)(b * a.L);
-  for (int u0 = 0; u0 < NU; u0 += 2 * kRows) {
+  for (int u0 = first; u0 < NU; u0 += step) {   // chunks of 2 kRows uniques
     float4 f[kRows][F4];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
@@ -572,33 +573,73 @@ __device__ __forceinline__ void load_record(const Cand& a, const uint8_t* rec, S
 // ---------------------------------------------------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------------------------------------------------
-// One query token's candidate attention: salida row (d), the 4 gate signals and, when `ent_rows` is given, every
-// entry's weight at ent_rows[2 (tau * C + distance - 1)]. RING: candidates from the generation rings instead of the
-// sorted windows.
-template <int F4, int DCH, bool RING>
-__device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t t, Scratch& S, float* salida_row,
-                                              float* signals_row, float* ent_rows) {
+// The copy-gather's rows: acc += sum over uniques u of (sum over tables of att) V_u, for u in chunks of UNR
+// consecutive uniques starting at `first`, one chunk every `step` (UNR rows in flight per chunk).
+template <int DCH>
+__device__ __forceinline__ void gather_values(const Cand& a, int64_t b, const Scratch& S, int NU, int first, int step,
+                                              float4 (&acc)[DCH]) {
+  constexpr int UNR = DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 16);
   const int lane = lane_id();
-  const int64_t tok = b * a.L + t;
+  const float* Vb = a.V + (b * a.L + a.vshift) * a.ldv;
+  for (int u0 = first; u0 < NU; u0 += step) {
+    float4 v[UNR][DCH];
+    float w[UNR];
+#pragma unroll
+    for (int r = 0; r < UNR; ++r) {
+      const bool ok = u0 + r < NU;
+      const int64_t p = ok ? S.upos[u0 + r] : 0;   // idle lanes read position 0 (always a V row, weight 0)
+      w[r] = ok ? S.uc[u0 + r] : 0.f;
+#pragma unroll
+      for (int ch = 0; ch < DCH; ++ch) {
+        const int dd = ch * 256 + lane * 4;
+        v[r][ch] = ld4(Vb + ((uint32_t)p * (uint32_t)a.ldv + (uint32_t)(dd < a.d ? dd : a.d - 4)));
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < UNR; ++r)
+#pragma unroll
+      for (int ch = 0; ch < DCH; ++ch) fma4(acc[ch], w[r], v[r][ch]);
+  }
+}
+template <int DCH>
+constexpr int gather_rows_in_flight() { return DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 16); }
+
+// A query token's candidate list (gather and dedupe; the record's header and entries when it is kept): returns the
+// entry count M, and the unique count NU in *nu.
+template <bool RING>
+__device__ __forceinline__ int token_list(const Cand& a, int64_t b, int64_t t, Scratch& S, uint8_t* rec, int* nu) {
+  const int lane = lane_id();
   const int M = RING ? gather_rings(a, b, t, S) : gather(a, b, t, true, S);
   const int NU = dedupe(a, M, S);
-  uint8_t* rec = (!RING && a.lists) ? a.lists + tok * a.rec : nullptr;
-  const RecLayout R = rec_layout(a.T, a.C);
   if (rec) {
+    const RecLayout R = rec_layout(a.T, a.C);
     uint16_t* hdr = reinterpret_cast<uint16_t*>(rec);
     uint16_t* e16 = reinterpret_cast<uint16_t*>(rec + R.e16);
     if (lane <= a.T) hdr[lane] = (uint16_t)S.off[lane];
     if (lane == a.T + 1) hdr[lane] = (uint16_t)NU;
     for (int m = lane; m < M; m += kWave) e16[m] = (uint16_t)(((S.key[m] & 31) << 8) | S.uid[m]);
   }
+  *nu = NU;
+  return M;
+}
+
+// The uniques' score terms: S.ua = base + w_suf[ell] + log_alfa_k, S.ub = fp32(Bt_k - Bt_q), S.uc = 0 (and the
+// record's per-unique fields). NW = 1: the whole wave does every unique. NW > 1: wave `wave` of NW does the chunks of
+// 2 kRows uniques wave, wave + NW, ... (its bases and then their other terms, so no other wave's results are read).
+template <int F4, int NW>
+__device__ __forceinline__ void unique_terms(const Cand& a, int64_t b, int64_t t, int NU, Scratch& S, uint8_t* rec,
+                                             int wave) {
+  const int lane = lane_id();
+  const int64_t tok = b * a.L + t;
+  const RecLayout R = rec_layout(a.T, a.C);
   float4 qf[F4];
   feat_row<F4>(feat_lanes<F4>(a, a.Qc, true), (uint32_t)tok, qf);
-  unique_bases<F4>(a, b, t, NU, false, qf, S);
+  unique_bases<F4>(a, b, t, NU, false, qf, S, wave * 2 * kRows, NW * 2 * kRows);
   const float* sigb = a.sig + b * a.L;
   float mine[4];
   own_suffix_of(sigb, t, a.K, mine);
   const double bq = a.Bt[tok];
-  for (int u = lane; u < NU; u += kWave) {
+  auto one = [&](int u) {
     const int64_t k = S.upos[u];
     const int ell = suffix_len_of(sigb, mine, t, k, a.K);
     const float db = (float)(a.Bt[b * a.L + k] - bq);
@@ -610,8 +651,41 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
       reinterpret_cast<float*>(rec + R.ub)[u] = db;
       rec[R.uell + u] = (uint8_t)ell;
     }
+  };
+  if constexpr (NW == 1) {
+    for (int u = lane; u < NU; u += kWave) one(u);
+  } else {
+    for (int c0 = wave * 2 * kRows; c0 < NU; c0 += NW * 2 * kRows)
+      if (lane < 2 * kRows && c0 + lane < NU) one(c0 + lane);
   }
   wave_lds_sync();
+}
+
+template <int DCH, bool VALUES>
+__device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, int NU, Scratch& S, float* salida_row,
+                                              float* signals_row, float* ent_rows);
+
+// One query token's candidate attention: salida row (d), the 4 gate signals and, when `ent_rows` is given, every
+// entry's weight at ent_rows[2 (tau * C + distance - 1)]. RING: candidates from the generation rings instead of the
+// sorted windows.
+template <int F4, int DCH, bool RING>
+__device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t t, Scratch& S, float* salida_row,
+                                              float* signals_row, float* ent_rows) {
+  const int64_t tok = b * a.L + t;
+  uint8_t* rec = (!RING && a.lists) ? a.lists + tok * a.rec : nullptr;
+  int NU;
+  const int M = token_list<RING>(a, b, t, S, rec, &NU);
+  unique_terms<F4, 1>(a, b, t, NU, S, rec, 0);
+  token_weights<DCH, true>(a, b, M, NU, S, salida_row, signals_row, ent_rows);
+}
+
+// The rest of a query's attention once its list and unique terms are in S: the exact masked softmax, the entries'
+// weights (into ent_rows when given), the 4 gate signals and, with VALUES, the copy-gather into salida_row (without
+// it, S.uc holds each unique's summed weight for the caller).
+template <int DCH, bool VALUES>
+__device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, int NU, Scratch& S, float* salida_row,
+                                              float* signals_row, float* ent_rows) {
+  const int lane = lane_id();
 
   // Exact masked softmax of every table at once: the per-table max through an LDS atomic max on order-preserving
   // integer keys (order-independent), one exp per entry, the per-table sums by lane groups (table_sum).
@@ -670,41 +744,23 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
   const float pico = wave_sum_u(inv);                    // the largest weight of a table is exp(0) / den
   const float pctx = wave_sum_u(has && tg >= a.T - a.Tc ? 1.f : 0.f);
 
-  // copy-gather over the distinct candidates: sum_u (sum_tau att) V_u, UNR rows in flight
-  constexpr int UNR = DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 16);
-  float4 acc[DCH];
-#pragma unroll
-  for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
-  const float* Vb = a.V + (b * a.L + a.vshift) * a.ldv;
-  for (int u0 = 0; u0 < NU; u0 += UNR) {
-    float4 v[UNR][DCH];
-    float w[UNR];
-#pragma unroll
-    for (int r = 0; r < UNR; ++r) {
-      const bool ok = u0 + r < NU;
-      const int64_t p = ok ? S.upos[u0 + r] : 0;   // idle lanes read position 0 (always a V row, weight 0)
-      w[r] = ok ? S.uc[u0 + r] : 0.f;
-#pragma unroll
-      for (int ch = 0; ch < DCH; ++ch) {
-        const int dd = ch * 256 + lane * 4;
-        v[r][ch] = ld4(Vb + ((uint32_t)p * (uint32_t)a.ldv + (uint32_t)(dd < a.d ? dd : a.d - 4)));
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < UNR; ++r)
-#pragma unroll
-      for (int ch = 0; ch < DCH; ++ch) fma4(acc[ch], w[r], v[r][ch]);
-  }
-#pragma unroll
-  for (int ch = 0; ch < DCH; ++ch) {
-    const int dd = ch * 256 + lane * 4;
-    if (dd < a.d) *reinterpret_cast<float4*>(salida_row + dd) = acc[ch];
-  }
   if (lane == 0) {
     signals_row[0] = pt;
     signals_row[1] = pt > 0.f ? fmaxf(best, -1e9f) : -1e9f;
     signals_row[2] = pico;
     signals_row[3] = pctx;
+  }
+  if constexpr (VALUES) {
+    // copy-gather over the distinct candidates: sum_u (sum_tau att) V_u
+    float4 acc[DCH];
+#pragma unroll
+    for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
+    gather_values<DCH>(a, b, S, NU, 0, gather_rows_in_flight<DCH>(), acc);
+#pragma unroll
+    for (int ch = 0; ch < DCH; ++ch) {
+      const int dd = ch * 256 + lane * 4;
+      if (dd < a.d) *reinterpret_cast<float4*>(salida_row + dd) = acc[ch];
+    }
   }
 }
 
@@ -718,19 +774,58 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_fwd(Cand a) {
                                 a.ent + tok * a.T * a.C * 2);
 }
 
-// Generation step: one wave per batch row; the query is position tq = a.tq (or *a.tq_dev) of the caches (a.L = their
-// capacity; a position outside them writes nothing). With a.insert, tq then enters its bucket's ring in every table
-// at slot count % C, overwriting the oldest (reference nucleo:1610-1618). Only this wave touches batch row b's rings,
-// and its ring reads were consumed before.
+// Generation step: one workgroup of kDecodeWaves waves per batch row; the query is position tq = a.tq (or *a.tq_dev)
+// of the caches (a.L = their capacity; a position outside them writes nothing). Wave 0 gathers the ring candidates
+// and dedupes them; every wave forms the score terms of its share of the distinct candidates; wave 0 normalizes;
+// then every wave sums the value rows of its share (chunks of consecutive uniques, one chunk in kDecodeWaves per
+// wave), and wave 0 adds the waves' sums in wave order.
+// With a.insert, tq then enters its bucket's ring in every table at slot count % C, overwriting the oldest (reference
+// nucleo:1610-1618): only wave 0 touches batch row b's rings, and its ring reads were consumed before.
+constexpr int kDecodeWaves = 8;
+
 template <int F4, int DCH>
-__global__ __launch_bounds__(kWave * kWavesPerBlock) void k_decode_attend(Cand a) {
-  __shared__ Scratch scratch[kWavesPerBlock];
-  Scratch& S = scratch[threadIdx.x >> 6];
-  const int64_t b = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+__global__ __launch_bounds__(kWave * kDecodeWaves) void k_decode_attend(Cand a) {
+  __shared__ Scratch S;
+  __shared__ float4 part[kDecodeWaves][DCH][kWave];
+  __shared__ int nu_shared;
+  const int64_t b = blockIdx.x;
   const int64_t tq = a.tq_dev ? *a.tq_dev : a.tq;
-  if (b >= a.B || tq < 0 || tq >= a.L) return;
-  forward_token<F4, DCH, true>(a, b, tq, S, a.salida + b * a.d, a.signals + b * 4, nullptr);
-  const int lane = lane_id();
+  if (b >= a.B || tq < 0 || tq >= a.L) return;            // the same for every wave of the workgroup
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  __shared__ int m_shared;
+  if (wave == 0) {
+    int nu;
+    const int m = token_list<true>(a, b, tq, S, nullptr, &nu);
+    if (lane == 0) {
+      nu_shared = nu;
+      m_shared = m;
+    }
+  }
+  __syncthreads();
+  const int NU = nu_shared;
+  unique_terms<F4, kDecodeWaves>(a, b, tq, NU, S, nullptr, wave);
+  __syncthreads();
+  if (wave == 0) token_weights<DCH, false>(a, b, m_shared, NU, S, nullptr, a.signals + b * 4, nullptr);
+  __syncthreads();
+  constexpr int UNR = gather_rows_in_flight<DCH>();
+  float4 acc[DCH];
+#pragma unroll
+  for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
+  gather_values<DCH>(a, b, S, NU, wave * UNR, kDecodeWaves * UNR, acc);
+#pragma unroll
+  for (int ch = 0; ch < DCH; ++ch) part[wave][ch][lane] = acc[ch];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int ch = 0; ch < DCH; ++ch) {
+    float4 s = part[0][ch][lane];
+    for (int w = 1; w < kDecodeWaves; ++w) {
+      const float4 q = part[w][ch][lane];
+      s.x += q.x; s.y += q.y; s.z += q.z; s.w += q.w;
+    }
+    const int dd = ch * 256 + lane * 4;
+    if (dd < a.d) *reinterpret_cast<float4*>(a.salida + b * a.d + dd) = s;
+  }
   if (a.insert && lane < a.T) {
     const int id = a.ids_out[b * a.T + lane];
     const int64_t bucket = (b * a.T + lane) * ((int64_t)1 << a.nb) + id;
@@ -1096,8 +1191,7 @@ struct LaunchFwd {
 template <int F4, int DCH>
 struct LaunchDecode {
   static int run(const Cand& a, hipStream_t st) {
-    hipLaunchKernelGGL((k_decode_attend<F4, DCH>), dim3((unsigned)((a.B + kWavesPerBlock - 1) / kWavesPerBlock)),
-                       dim3(kWave * kWavesPerBlock), 0, st, a);
+    hipLaunchKernelGGL((k_decode_attend<F4, DCH>), dim3((unsigned)a.B), dim3(kWave * kDecodeWaves), 0, st, a);
     return check_launch("asrn_decode_attend");
   }
 };
