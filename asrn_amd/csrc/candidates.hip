@@ -57,7 +57,7 @@ struct Cand {
 };
 
 // per-wave LDS scratch: one token's candidate list (entries) and its distinct positions (uniques)
-constexpr int kHash = 2 * kMaxSlots;   // dedupe hash slots: at most kMaxSlots distinct positions, so probes end
+constexpr int kHash = 3 * kMaxSlots / 2;   // dedupe hash slots: at most kMaxSlots distinct positions (load <= 2/3)
 
 struct Scratch {
   int key[kMaxSlots];      // entry: (position << 5) | table
@@ -68,7 +68,6 @@ struct Scratch {
       float ua[kMaxSlots];   // unique: base score, then (base + w_suf[ell]) + log_alfa_k; per entry in the backward
       float ub[kMaxSlots];   // unique: fp32(Bt_k - Bt_q)
       float uc[kMaxSlots];   // unique: sum over tables of att (forward, key side) or dp (query side)
-      float ud[kMaxSlots];   // unique: sum over tables of ds
     };
     struct {                 // the dedupe's hash table, dead once the uniques are numbered
       int hpos[kHash];       // position held by the slot (-1 empty)
@@ -81,6 +80,8 @@ struct Scratch {
   float tsum[32];          // per-table sums (backward); per-table max keys (forward)
   float tinv[32];          // per-table 1 / softmax denominator (forward)
 };
+// 6.4 KB of LDS per wave: 6 waves per SIMD. The backward's per-unique sums of ds reuse a per-unique array its pass no
+// longer needs (uc in the query pass once dp is in registers, ub in the key pass, which has no clock differences).
 
 // order-preserving map of finite floats and -inf to unsigned keys, and back
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -322,10 +323,12 @@ __device__ __forceinline__ int gather_rings(const Cand& a, int64_t b, int64_t t,
 // One slot per distinct position, in order of first appearance (table-major): S.uid[entry], S.upos[unique].
 // Every entry claims its position's slot in an LDS hash table (compare-and-swap, linear probing) and keeps the
 // smallest entry index there (atomic min, order-independent), so the numbering is deterministic.
-__device__ __forceinline__ uint32_t pos_hash(int pos) { return ((uint32_t)pos * 2654435761u) >> 23; }   // 9 bits
+// a slot in [0, kHash): the high part of (Knuth's multiplicative hash) * kHash
+__device__ __forceinline__ uint32_t pos_hash(int pos) {
+  return (uint32_t)(((uint64_t)((uint32_t)pos * 2654435761u) * (uint64_t)kHash) >> 32);
+}
 
 __device__ __forceinline__ int dedupe(const Cand& a, int M, Scratch& S) {
-  static_assert(kHash == 512, "pos_hash yields 9 bits");
   const int lane = lane_id();
   for (int i = lane; i < kHash; i += kWave) {
     S.hpos[i] = -1;
@@ -343,7 +346,7 @@ __device__ __forceinline__ int dedupe(const Cand& a, int M, Scratch& S) {
       for (int probe = 0; probe < kHash; ++probe) {
         const int old = atomicCAS(&S.hpos[h], -1, pos);
         if (old == -1 || old == pos) break;
-        h = (h + 1) & (kHash - 1);
+        h = h + 1 == (uint32_t)kHash ? 0u : h + 1;
       }
       atomicMin(&S.hfirst[h], m);
       slot[c] = (int)h;
@@ -526,7 +529,7 @@ __host__ __device__ inline RecLayout rec_layout(int T, int C) {
 }
 
 // The query pass's view of a record: S.off, S.key (the table of each entry; the position part is not needed there),
-// S.uid, S.upos, S.ub, S.uell, and S.ud cleared. The first 64 entries and uniques are loaded with the header in one
+// S.uid, S.upos, S.ub and S.uell. The first 64 entries and uniques are loaded with the header in one
 // round (most queries have no more); loads past M or NU stay inside the record and are ignored.
 __device__ __forceinline__ void load_record(const Cand& a, const uint8_t* rec, Scratch& S, int& M, int& NU) {
   const int lane = lane_id();
@@ -559,13 +562,11 @@ __device__ __forceinline__ void load_record(const Cand& a, const uint8_t* rec, S
     S.upos[lane] = p0;
     S.ub[lane] = b0;
     S.uell[lane] = (uint8_t)l0;
-    S.ud[lane] = 0.f;
   }
   for (int u = kWave + lane; u < NU; u += kWave) {
     S.upos[u] = upos[u];
     S.ub[u] = ub[u];
     S.uell[u] = uell[u];
-    S.ud[u] = 0.f;
   }
   wave_lds_sync();
 }
@@ -573,12 +574,16 @@ __device__ __forceinline__ void load_record(const Cand& a, const uint8_t* rec, S
 // ---------------------------------------------------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------------------------------------------------
+// value rows in flight per wave in the copy-gather (the loads of one chunk)
+template <int DCH>
+constexpr int gather_rows_in_flight() { return DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 12); }
+
 // The copy-gather's rows: acc += sum over uniques u of (sum over tables of att) V_u, for u in chunks of UNR
 // consecutive uniques starting at `first`, one chunk every `step` (UNR rows in flight per chunk).
 template <int DCH>
 __device__ __forceinline__ void gather_values(const Cand& a, int64_t b, const Scratch& S, int NU, int first, int step,
                                               float4 (&acc)[DCH]) {
-  constexpr int UNR = DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 16);
+  constexpr int UNR = gather_rows_in_flight<DCH>();
   const int lane = lane_id();
   const float* Vb = a.V + (b * a.L + a.vshift) * a.ldv;
   for (int u0 = first; u0 < NU; u0 += step) {
@@ -601,8 +606,6 @@ __device__ __forceinline__ void gather_values(const Cand& a, int64_t b, const Sc
       for (int ch = 0; ch < DCH; ++ch) fma4(acc[ch], w[r], v[r][ch]);
   }
 }
-template <int DCH>
-constexpr int gather_rows_in_flight() { return DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 16); }
 
 // A query token's candidate list (gather and dedupe; the record's header and entries when it is kept): returns the
 // entry count M, and the unique count NU in *nu.
@@ -765,7 +768,7 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
 }
 
 template <int F4, int DCH>
-__global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_fwd(Cand a) {
+__global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 6 : 1) void k_cand_fwd(Cand a) {   // 6 waves per SIMD when narrow
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
   const int64_t tok = token_of_wave();
@@ -862,7 +865,6 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
       const int64_t k = S.upos[u];
       S.uell[u] = (uint8_t)suffix_len_of(sigb, mine, t, k, a.K);
       S.ub[u] = (float)(a.Bt[b * a.L + k] - bq);
-      S.ud[u] = 0.f;
     }
   }
   // every entry's att from the forward, loaded now so that it arrives with the value rows below
@@ -898,6 +900,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
     if (in) S.ua[m] = att[c] * dp[c];
   }
   wave_lds_sync();
+  for (int u = lane; u < NU; u += kWave) S.uc[u] = 0.f;   // dp is in registers: uc now sums ds per unique
   const int G = lanes_per_table(a.T), tg = lane / G;
   const bool lead = lane % G == 0 && tg < a.T;
   {                                                     // D per table
@@ -938,13 +941,13 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   for (int tt = 0; tt < a.T; ++tt) {
 #pragma unroll
     for (int c = 0; c < kCh; ++c)
-      if (tau[c] == tt) S.ud[un[c]] += ds[c];
+      if (tau[c] == tt) S.uc[un[c]] += ds[c];
     wave_lds_sync();
   }
 
   // d phi_q, d Qc_q = sum_u (sum_tau ds) [phi_u ; Kc_u]
   float4 gq[F4];
-  unique_feature_sum<F4>(a, b, t, NU, false, S.ud, S, gq);
+  unique_feature_sum<F4>(a, b, t, NU, false, S.uc, S, gq);
   if (half == 0) {   // P and cf are multiples of 4: a lane's 4 features lie in one of the two rows
 #pragma unroll
     for (int c = 0; c < F4; ++c) {
@@ -971,7 +974,7 @@ template <int DCH>
 __device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows, int64_t self_pos, int NU,
                                                const float* w_u, const Scratch& S, float4 (&acc)[DCH]) {
   const int lane = lane_id();
-  constexpr int UNR = DCH >= 4 ? 3 : (DCH >= 2 ? 6 : 12);   // fits the key pass's 5-waves register budget
+  constexpr int UNR = DCH >= 4 ? 3 : (DCH >= 2 ? 6 : 8);   // fits the key pass's register budget (6 waves at DCH 1)
 #pragma unroll
   for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
   for (int u0 = 0; u0 < NU; u0 += UNR) {
@@ -1000,7 +1003,8 @@ __device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows,
 // slot for this key; per distinct query the table sums weight dO (-> dV) and [phi_q ; Qc_q] (-> d phi_k, d Kc_k).
 // ---------------------------------------------------------------------------------------------------------------------
 template <int F4, int DCH>
-__global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH != 3) ? 5 : 1) void k_cand_bwd_k(Cand a) {
+__global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 6 : ((F4 == 1 && DCH != 3) ? 5 : 1))
+void k_cand_bwd_k(Cand a) {
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
   const int64_t tok = token_of_wave();
@@ -1018,9 +1022,9 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH != 3) ? 5 :
 
   const int M = gather(a, b, k, false, S);
   const int NU = dedupe(a, M, S);
-  for (int u = lane; u < NU; u += kWave) {
+  for (int u = lane; u < NU; u += kWave) {   // per unique: uc sums att, ub (free in this pass) sums ds
     S.uc[u] = 0.f;
-    S.ud[u] = 0.f;
+    S.ub[u] = 0.f;
   }
   // park the prefetched d phi in LDS (S.ua is free once the dedupe hash is done) to keep registers for the gathers
 #pragma unroll
@@ -1055,7 +1059,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH != 3) ? 5 :
     for (int c = 0; c < kCh; ++c)
       if (tau[c] == tt) {
         S.uc[un[c]] += att[c];
-        S.ud[un[c]] += ds[c];
+        S.ub[un[c]] += ds[c];
       }
     wave_lds_sync();
   }
@@ -1065,7 +1069,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH != 3) ? 5 :
   unique_row_sum<DCH>(a, a.dsal + b * a.L * a.d, k, NU, S.uc, S, dv);
   // d phi_k, d Kc_k = sum_u (sum_tau ds) [phi_q * scale_phi ; Qc_q * scale_c]
   float4 gk[F4];
-  unique_feature_sum<F4>(a, b, k, NU, true, S.ud, S, gk);
+  unique_feature_sum<F4>(a, b, k, NU, true, S.ub, S, gk);
   // with vshift, V[k] is the projection of k + 1: its gradient goes to row k + 1, and the last position (which no
   // query sees, so dv is 0) clears row 0, the projection no V reads
   const int64_t dv_row = a.vshift ? b * a.L + (k + 1 < a.L ? k + 1 : 0) : tok;
