@@ -1,6 +1,6 @@
 """Benchmark of the ASRN layer hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config cfg2] [--no-cpu-baseline] [--no-decode]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--config cfg2] [--no-cpu-baseline] [--no-decode]
 
 A step is one forward + backward of one ASRN layer (asrn.ASRNLayer, group-A protections) over one batch of
 synthetic tokens: BASELINE.json configs[1] = cfg2, B 8, N 4096, d 256, V 256, fp32, 30% copied spans. Inputs and
@@ -10,9 +10,9 @@ instead. The per-kernel device events (roofline, hip_aggregate, kernels) come fr
 steps, since events recorded while capturing are not replayed. Prints one JSON line with the driver's keys plus:
   roofline      the dominant HIP kernel: algorithmic bytes per launch / its mean launch time (device events recorded
                 on the stream it runs on), against MI355X's 8 TB/s
-  hip_aggregate all HIP kernels: 26,640 B/token (cfg2) x tokens / (8 TB/s x their summed time per step)
-  layer         whole-layer tokens/s and its HBM fraction at 45,520 B/token (the HIP kernels' bytes plus the GEMMs'
-                operands and results, 18,880 B/token at cfg2)
+  hip_aggregate all HIP kernels: 25,552 B/token (cfg2) x tokens / (8 TB/s x their summed time per step)
+  layer         whole-layer tokens/s and its HBM fraction at 41,552 B/token (the HIP kernels' bytes plus the GEMMs'
+                operands and results, 16,000 B/token at cfg2)
   decode        the O(1) generation step of one layer (BASELINE.json configs[4] at one layer): per-token latency
                 against the context, 1K to 64K, and its slope
   cpu_baseline  the CPU oracle (oracle/layer.py, PyTorch on the host cores) on the same workload
@@ -205,8 +205,9 @@ def decode_bench(dev, steps, warmup, seed=0, contexts=None):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--steps', type=int, default=20)
-    ap.add_argument('--warmup', type=int, default=5)
+    # 200 replays (about 0.17 s) measure the steady state: 20 read about 3% slower, the clocks still settling
+    ap.add_argument('--steps', type=int, default=200)
+    ap.add_argument('--warmup', type=int, default=20)
     ap.add_argument('--config', default='cfg2')
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--no-cpu-baseline', action='store_true')
