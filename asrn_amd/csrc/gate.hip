@@ -12,7 +12,8 @@
 //
 // A workgroup takes 32 tokens: their small inputs (signals, seen flags, Hawkes, streak) are turned into features by one
 // thread per token, then each wave runs 8 tokens' d-rows, as float4 per lane, loading 4 tokens' rows at a time so the
-// loads overlap: h, A and h' stream through HBM once.
+// loads overlap: h, A and h' stream through HBM once. In the forward wave w takes tokens w, w + 4, ... of the
+// workgroup, so a short input (the generation step's B tokens) still spreads over all four waves.
 // The backward gives dh, dA, dhawkes, dracha per token and the parameter gradients as per-workgroup partials summed
 // in a fixed order by a second launch (deterministic, no atomics).
 #include "common.h"
@@ -133,7 +134,7 @@ __global__ __launch_bounds__(kGateThreads) void k_gate_fwd(GateArgs a) {
     float dot[kGateBatch];
 #pragma unroll
     for (int u = 0; u < kGateBatch; ++u) {
-      const int64_t t = t0 + wave * kGateTokPerWave + b + u;
+      const int64_t t = t0 + wave + kGateWaves * (b + u);
       dot[u] = 0.f;
 #pragma unroll
       for (int k = 0; k < D4; ++k) {
@@ -148,7 +149,7 @@ __global__ __launch_bounds__(kGateThreads) void k_gate_fwd(GateArgs a) {
     }
 #pragma unroll
     for (int u = 0; u < kGateBatch; ++u) {
-      const int tl = wave * kGateTokPerWave + b + u;
+      const int tl = wave + kGateWaves * (b + u);
       const int64_t t = t0 + tl;
       if (t >= a.BL) break;
       const float logit = wave_sum_u(dot[u]) + info[tl].small;

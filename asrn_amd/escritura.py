@@ -101,7 +101,9 @@ class EscritorCapa:
         c = self.cache
         self._escribir('sig', pos, pieza_t.to(torch.float32))
         self._escribir('V', pos - 1, capa.v(e_t))                          # V[t-1] = W_v e_t
-        self._escribir('phi', pos, capa._phi(torch.stack([e_ult, e_t], 1))[:, -1])
+        # the token's phi from its own row and the previous one (the context MLP's key), by the whole-text
+        # producer (in fp32 the fused hash kernels: one GEMM and one kernel)
+        self._escribir('phi', pos, capa._phi_y_valores(torch.stack([e_ult, e_t], 1))[0][:, -1])
         Qc, Kc, beta, log_alfa = capa._contexto(h_t.unsqueeze(1))
         self._escribir('Qc', pos, Qc[:, 0])
         self._escribir('Kc', pos, Kc[:, 0])

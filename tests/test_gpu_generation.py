@@ -188,11 +188,12 @@ def write(layer, E, h, x, L0, ajeno, capacidad):
 
 
 def ids_agree(layer, E, sh, ref=None):
-    """The step's phi (two-row GEMMs) and the whole text's (one fused GEMM) give the same bucket ids (and `ref`)."""
+    """The step's phi (the producer over two rows) and the whole text's give the same bucket ids (and `ref`)."""
     with torch.no_grad():
         whole, _ = layer._phi_y_valores(E.to(DEV))
         Ed = E.to(DEV)
-        step = torch.stack([layer._phi(Ed[:, max(0, t - 1):t + 1])[:, -1] for t in range(E.shape[1])], 1)
+        step = torch.stack([layer._phi_y_valores(Ed[:, max(0, t - 1):t + 1])[0][:, -1] for t in range(E.shape[1])],
+                           1)
     a, b = O.bucket_ids(whole.cpu(), sh.T, sh.nb), O.bucket_ids(step.cpu(), sh.T, sh.nb)
     return torch.equal(a, b) and (ref is None or torch.equal(a, ref))
 
