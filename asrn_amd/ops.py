@@ -248,7 +248,12 @@ class HashProducer(torch.autograd.Function):
             raise ValueError('HashProducer: W must be (m + 2 mc, d), W2w (Pw, m) and W2c (Pc, mc)')
         E = _c(E, torch.float32)
         ps = [_c(t, torch.float32) for t in (b_word, b_ctx, W2w, b2w, W2c, b2c)]
-        y = torch.nn.functional.linear(E, W)
+        if B * L <= 256:        # a few tokens (the generation step): one small tile per workgroup beats the library
+            W32 = _c(W, torch.float32)
+            y = torch.empty((B, L, n), dtype=torch.float32, device=dev)
+            call('asrn_small_gemm', ptr(E), d, 0, ptr(W32), d, 1, ptr(y), n, B * L, n, d, stream_of(dev))
+        else:
+            y = torch.nn.functional.linear(E, W)
         phi = torch.empty((B, L, Pw + Pc), dtype=torch.float32, device=dev)
         call('asrn_hash_fwd', ptr(y), n, *[ptr(t) for t in ps], B, L, m, mc, Pw, Pc, ptr(phi), stream_of(dev))
         ctx.save_for_backward(E, W, y, ps[0], ps[1], ps[2], ps[4])
