@@ -565,10 +565,13 @@ class Candidates(torch.autograd.Function):
         ctx.meta = (B, L, P, d, cf, K, T, Tc, C, sp, sc, V.dtype, phi.dtype, Qc.dtype, Kc.dtype, log_alfa.dtype,
                     P0, cf0, vs)
         ctx.mark_non_differentiable(signals)
+        ctx.set_materialize_grads(False)       # no zero-filled gradient for the signals (none flows back through them)
         return salida.to(V.dtype), signals
 
     @staticmethod
     def backward(ctx, dsal, _dsig):
+        if dsal is None:
+            return (None,) * 13
         phi, V, Qc, Kc, sig, Bt, la, w, g, order, win, rank, ent, listas = ctx.saved_tensors
         B, L, P, d, cf, K, T, Tc, C, sp, sc, tv, tp, tq, tk, tl, P0, cf0, vs = ctx.meta
         dev = phi.device
