@@ -1,0 +1,267 @@
+// a14 (part): the generation step's per-token producers, fused (reference asrn/nucleo.py:1797-1826, the producers of
+// asrn/nucleo.py:644-659, 683 and asrn/estable.py:153-194 applied to one new token).
+//
+// For each of the B texts, the new token at position t (e_t its embedding, e_prev the previous one, h_t its layer
+// input, its id) gives the rows the step's attention reads, written straight into the caches (B, cap, .):
+//   V[t-1]  = W_v e_t                                            (the value of the previous position)
+//   phi[t]  = [W2w gelu(W_p e_t + b_p) + b2w | W2c gelu((W_a e_t + b_c) + W_b e_prev) + b2c]
+//   Qc[t], Kc[t] = cq hh, ck hh with hh = LayerNorm(h_t) (biased variance, two passes)
+//   log_alfa[t] = max(logsigmoid(u_1) + log 2, log_alfa_min), and beta = min(softplus(u_0), beta_max) returned in fp64
+//              for the repetition step, u_k = hh . w_reloj[k] + b_reloj[k]
+//   sig[t]  = the token id in fp32
+// The context MLP's first layer is read in place as its (mc, 2 d) weight: a row's first d columns act on e_t (W_a) and
+// its last d on e_prev (W_b).
+//
+// Two launches. The first splits the weight rows into blocks of 16 (W_v, W_p, W_a, W_b, cq, ck); a workgroup stages
+// 16 tokens' input vectors in LDS (e_t, e_prev, or hh with the LayerNorm done there) and each wave dots 4 rows with
+// them, so every weight row is read once per 16 tokens. The second takes one token per workgroup: the hidden units,
+// both second layers and the clock. Every sum runs in a fixed order. The position is t, or *t_dev (a step replayed
+// from a graph); a position outside [1, cap) writes nothing.
+#include "common.h"
+
+namespace asrn {
+
+constexpr int kProdThreads = 256;
+constexpr int kProdWaves = kProdThreads / kWave;
+constexpr int kProdRows = 16;          // weight rows per workgroup of the first launch
+constexpr int kProdTok = 16;           // tokens per workgroup of the first launch
+constexpr int kProdMaxD4 = 4;          // d <= 1024
+constexpr int kProdMax = 64;           // hidden units, outputs per hash MLP, and cf, at most
+
+struct ProdArgs {
+  const float* e; const float* e_prev; const float* h; const int64_t* pieza; int64_t B; int d;
+  const float* wv; const float* ww; const float* wc;        // W_v (d, d), W_p (m, d), the context first layer (mc, 2d)
+  const float* bw; const float* bc;                         // first-layer biases (m), (mc)
+  const float* w2w; const float* b2w; const float* w2c; const float* b2c;
+  const float* lnw; const float* lnb; float eps;
+  const float* wr; const float* br; float beta_max; float la_min;
+  const float* wq; const float* wk;                         // cq (cf, d), ck (cf, d)
+  int m, mc, Pw, Pc, cf;
+  float* phi; float* V; float* Qc; float* Kc; float* sig; float* la; int64_t cap; int64_t t; const int64_t* t_dev;
+  double* beta; float* y;                                   // beta (B); y (B, m + 2 mc): the first layers' products
+};
+
+__device__ __forceinline__ int64_t prod_pos(const ProdArgs& a) { return a.t_dev ? *a.t_dev : a.t; }
+
+__device__ __forceinline__ float dot4(float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
+
+// rows of kind k: 0 W_v (on e), 1 W_p (on e), 2 W_a (on e), 3 W_b (on e_prev), 4 cq (on hh), 5 ck (on hh)
+__device__ __forceinline__ int kind_rows(const ProdArgs& a, int k) {
+  return k == 0 ? a.d : (k == 1 ? a.m : (k <= 3 ? a.mc : a.cf));
+}
+
+// LayerNorm of the staged rows x[tok][.] (d4 float4 each) in place: wave w takes tokens w, w + 4, ...
+__device__ __forceinline__ void layer_norm_rows(const ProdArgs& a, float4* xs, int ntok, int d4) {
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const float inv_d = 1.f / (float)a.d;
+  for (int j = wave; j < ntok; j += kProdWaves) {
+    float4* x = xs + j * d4;
+    float s = 0.f;
+    for (int q = lane; q < d4; q += kWave) s += (x[q].x + x[q].y) + (x[q].z + x[q].w);
+    const float mean = wave_sum_u(s) * inv_d;
+    float v = 0.f;
+    for (int q = lane; q < d4; q += kWave) {
+      const float4 c = make_float4(x[q].x - mean, x[q].y - mean, x[q].z - mean, x[q].w - mean);
+      v += dot4(c, c);
+    }
+    const float rstd = rsqrtf(wave_sum_u(v) * inv_d + a.eps);
+    for (int q = lane; q < d4; q += kWave) {
+      const float4 w = ((const float4*)a.lnw)[q], b = ((const float4*)a.lnb)[q];
+      x[q] = make_float4((x[q].x - mean) * rstd * w.x + b.x, (x[q].y - mean) * rstd * w.y + b.y,
+                         (x[q].z - mean) * rstd * w.z + b.z, (x[q].w - mean) * rstd * w.w + b.w);
+    }
+  }
+}
+
+template <int D4>
+__global__ __launch_bounds__(kProdThreads) void k_produce_rows(ProdArgs a) {
+  __shared__ float4 xs[kProdTok * kProdMaxD4 * kWave];
+  const int64_t t = prod_pos(a);
+  if (t < 1 || t >= a.cap) return;                          // the same for the whole grid
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const int d4 = a.d >> 2;
+  // which kind and block
+  int k = 0, blk = blockIdx.x;
+  for (; k < 5; ++k) {
+    const int nb = (kind_rows(a, k) + kProdRows - 1) / kProdRows;
+    if (blk < nb) break;
+    blk -= nb;
+  }
+  const int nrows = kind_rows(a, k);
+  const int64_t b0 = (int64_t)blockIdx.y * kProdTok;
+  const int ntok = a.B - b0 < kProdTok ? (int)(a.B - b0) : kProdTok;
+  // stage the input vectors
+  const float* src = k == 3 ? a.e_prev : (k >= 4 ? a.h : a.e);
+  for (int i = threadIdx.x; i < ntok * d4; i += kProdThreads) {
+    const int j = i / d4, q = i - j * d4;
+    xs[j * d4 + q] = ((const float4*)(src + (b0 + j) * a.d))[q];
+  }
+  __syncthreads();
+  if (k >= 4) {
+    layer_norm_rows(a, xs, ntok, d4);
+    __syncthreads();
+  }
+  // wave w dots rows 4w .. 4w + 3 of the block with every token
+  const int r0 = blk * kProdRows + wave * 4;
+  float4 w[4][D4];
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int r = r0 + rr;
+    const float* row = k == 0 ? a.wv + (int64_t)r * a.d
+                     : (k == 1 ? a.ww + (int64_t)r * a.d
+                     : (k == 2 ? a.wc + (int64_t)r * 2 * a.d
+                     : (k == 3 ? a.wc + (int64_t)r * 2 * a.d + a.d
+                     : (k == 4 ? a.wq + (int64_t)r * a.d : a.wk + (int64_t)r * a.d))));
+#pragma unroll
+    for (int kk = 0; kk < D4; ++kk) {
+      const int q = lane + kWave * kk;
+      w[rr][kk] = r < nrows && q < d4 ? ((const float4*)row)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  for (int j = 0; j < ntok; ++j) {
+    const int64_t b = b0 + j;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      float p = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < D4; ++kk) {
+        const int q = lane + kWave * kk;
+        if (q < d4) p += dot4(w[rr][kk], xs[j * d4 + q]);
+      }
+      const float s = wave_sum_u(p);
+      const int r = r0 + rr;
+      if (lane == 0 && r < nrows) {
+        const int n1 = a.m + 2 * a.mc;
+        if (k == 0) a.V[(b * a.cap + t - 1) * a.d + r] = s;
+        else if (k == 1) a.y[b * n1 + r] = s;
+        else if (k == 2) a.y[b * n1 + a.m + r] = s;
+        else if (k == 3) a.y[b * n1 + a.m + a.mc + r] = s;
+        else if (k == 4) a.Qc[(b * a.cap + t) * a.cf + r] = s;
+        else a.Kc[(b * a.cap + t) * a.cf + r] = s;
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ float gelu_exact(float x) { return 0.5f * x * (1.f + erff(x * 0.70710678118654752f)); }
+__device__ __forceinline__ float softplus_p(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float logsigmoid_p(float x) { return fminf(x, 0.f) - log1pf(expf(-fabsf(x))); }
+
+// one token per workgroup: hidden units, both second layers, the clock, the token id
+__global__ __launch_bounds__(kProdThreads) void k_produce_token(ProdArgs a) {
+  __shared__ float g[2 * kProdMax];
+  const int64_t t = prod_pos(a);
+  if (t < 1 || t >= a.cap) return;
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  const int n1 = a.m + 2 * a.mc;
+  const float* yb = a.y + b * n1;
+  if (tid < a.m) g[tid] = gelu_exact(yb[tid] + a.bw[tid]);
+  else if (tid < a.m + a.mc) {
+    const int j = tid - a.m;
+    g[tid] = gelu_exact((yb[a.m + j] + a.bc[j]) + yb[a.m + a.mc + j]);
+  }
+  __syncthreads();
+  const int P = a.Pw + a.Pc;
+  if (tid < a.Pw) {
+    float s = 0.f;
+    for (int j = 0; j < a.m; ++j) s += a.w2w[tid * a.m + j] * g[j];
+    a.phi[(b * a.cap + t) * P + tid] = s + a.b2w[tid];
+  } else if (tid < P) {
+    const int o = tid - a.Pw;
+    float s = 0.f;
+    for (int j = 0; j < a.mc; ++j) s += a.w2c[o * a.mc + j] * g[a.m + j];
+    a.phi[(b * a.cap + t) * P + tid] = s + a.b2c[o];
+  }
+  if (wave == kProdWaves - 1) {                             // the clock: LayerNorm of h_t and its two projections
+    const int d4 = a.d >> 2;
+    const float inv_d = 1.f / (float)a.d;
+    const float4* x = (const float4*)(a.h + b * a.d);
+    float s = 0.f;
+    for (int q = lane; q < d4; q += kWave) s += (x[q].x + x[q].y) + (x[q].z + x[q].w);
+    const float mean = wave_sum_u(s) * inv_d;
+    float v = 0.f;
+    for (int q = lane; q < d4; q += kWave) {
+      const float4 c = make_float4(x[q].x - mean, x[q].y - mean, x[q].z - mean, x[q].w - mean);
+      v += dot4(c, c);
+    }
+    const float rstd = rsqrtf(wave_sum_u(v) * inv_d + a.eps);
+    float u0 = 0.f, u1 = 0.f;
+    for (int q = lane; q < d4; q += kWave) {
+      const float4 w = ((const float4*)a.lnw)[q], bb = ((const float4*)a.lnb)[q];
+      const float4 yv = make_float4((x[q].x - mean) * rstd * w.x + bb.x, (x[q].y - mean) * rstd * w.y + bb.y,
+                                    (x[q].z - mean) * rstd * w.z + bb.z, (x[q].w - mean) * rstd * w.w + bb.w);
+      u0 += dot4(yv, ((const float4*)a.wr)[q]);
+      u1 += dot4(yv, ((const float4*)(a.wr + a.d))[q]);
+    }
+    u0 = wave_sum_u(u0) + a.br[0];
+    u1 = wave_sum_u(u1) + a.br[1];
+    if (lane == 0) {
+      float be = softplus_p(u0);
+      if (a.beta_max >= 0.f) be = fminf(be, a.beta_max);
+      a.beta[b] = (double)be;
+      a.la[b * a.cap + t] = fmaxf(logsigmoid_p(u1) + 0.69314718055994530942f, a.la_min);
+      a.sig[b * a.cap + t] = (float)a.pieza[b];
+    }
+  }
+}
+
+static int kind_rows_host(int d, int m, int mc, int cf, int k) {
+  return k == 0 ? d : (k == 1 ? m : (k <= 3 ? mc : cf));
+}
+
+}  // namespace asrn
+
+using namespace asrn;
+
+extern "C" int64_t asrn_decode_produce_workspace(int64_t B, int32_t m, int32_t mc) {
+  if (B < 0 || m < 0 || mc < 0) return -1;
+  return B * (int64_t)(m + 2 * mc) * (int64_t)sizeof(float);
+}
+
+extern "C" int asrn_decode_produce(const float* e, const float* e_prev, const float* h, const int64_t* pieza,
+                                   int64_t B, int32_t d, const float* w_v, const float* w_word, const float* w_ctx,
+                                   const float* b_word, const float* b_ctx, const float* w2_word,
+                                   const float* b2_word, const float* w2_ctx, const float* b2_ctx, int32_t m,
+                                   int32_t mc, int32_t p_word, int32_t p_ctx, const float* ln_w, const float* ln_b,
+                                   float eps, const float* w_reloj, const float* b_reloj, float beta_max,
+                                   float log_alfa_min, const float* w_cq, const float* w_ck, int32_t cf, float* phi,
+                                   float* V, float* Qc, float* Kc, float* sig, float* log_alfa, int64_t cap,
+                                   int64_t t, const int64_t* t_dev, double* beta, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
+  ASRN_REQUIRE(B >= 0 && d > 0 && d % 4 == 0 && d <= 4 * kProdMaxD4 * kWave,
+               "asrn_decode_produce: d=%d must be a positive multiple of 4, <= %d", d, 4 * kProdMaxD4 * kWave);
+  ASRN_REQUIRE(m >= 1 && mc >= 1 && m <= kProdMax && mc <= kProdMax && p_word >= 1 && p_ctx >= 1 &&
+                   p_word + p_ctx <= kProdThreads && cf >= 1 && cf <= kProdMax,
+               "asrn_decode_produce: m=%d, mc=%d, cf=%d must be in [1, %d], Pw + Pc=%d in [2, %d]", m, mc, cf, kProdMax,
+               p_word + p_ctx, kProdThreads);
+  ASRN_REQUIRE(eps > 0.f, "asrn_decode_produce: eps must be positive");
+  ASRN_REQUIRE(t >= 1 && t < cap, "asrn_decode_produce: position t=%lld outside [1, capacity %lld)", (long long)t,
+               (long long)cap);
+  const int64_t need = asrn_decode_produce_workspace(B, m, mc);
+  ASRN_REQUIRE(workspace != nullptr || need == 0, "asrn_decode_produce: needs a workspace of %lld bytes",
+               (long long)need);
+  ASRN_REQUIRE(workspace_bytes >= need, "asrn_decode_produce: workspace of %lld bytes, needs %lld",
+               (long long)workspace_bytes, (long long)need);
+  for (const void* p : {(const void*)e, (const void*)e_prev, (const void*)h, (const void*)w_v, (const void*)w_word,
+                        (const void*)w_ctx, (const void*)ln_w, (const void*)ln_b, (const void*)w_reloj,
+                        (const void*)w_cq, (const void*)w_ck})
+    ASRN_REQUIRE(((uintptr_t)p & 15) == 0, "asrn_decode_produce: the rows are read as float4: 16-byte alignment");
+  if (B == 0) return 0;
+  ProdArgs a = {e, e_prev, h, pieza, B, d, w_v, w_word, w_ctx, b_word, b_ctx, w2_word, b2_word, w2_ctx, b2_ctx, ln_w,
+                ln_b, eps, w_reloj, b_reloj, beta_max, log_alfa_min, w_cq, w_ck, m, mc, p_word, p_ctx, cf, phi, V, Qc,
+                Kc, sig, log_alfa, cap, t, t_dev, beta, (float*)workspace};
+  int blocks = 0;
+  for (int k = 0; k < 6; ++k) blocks += (kind_rows_host(d, m, mc, cf, k) + kProdRows - 1) / kProdRows;
+  const dim3 grid((unsigned)blocks, (unsigned)((B + kProdTok - 1) / kProdTok));
+  hipStream_t st = (hipStream_t)stream;
+  switch ((d + 4 * kWave - 1) / (4 * kWave)) {
+    case 1: hipLaunchKernelGGL(k_produce_rows<1>, grid, dim3(kProdThreads), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(k_produce_rows<2>, grid, dim3(kProdThreads), 0, st, a); break;
+    case 3: hipLaunchKernelGGL(k_produce_rows<3>, grid, dim3(kProdThreads), 0, st, a); break;
+    default: hipLaunchKernelGGL(k_produce_rows<4>, grid, dim3(kProdThreads), 0, st, a); break;
+  }
+  if (check_launch("asrn_decode_produce/rows")) return 1;
+  hipLaunchKernelGGL(k_produce_token, dim3((unsigned)B), dim3(kProdThreads), 0, st, a);
+  return check_launch("asrn_decode_produce/token");
+}

@@ -99,17 +99,22 @@ class EscritorCapa:
         the layer's output (B, d) (the layer part of asrn/nucleo.py:1797-1854)."""
         capa = self.capa
         c = self.cache
-        self._escribir('sig', pos, pieza_t.to(torch.float32))
-        self._escribir('V', pos - 1, capa.v(e_t))                          # V[t-1] = W_v e_t
-        # the token's phi from its own row and the previous one (the context MLP's key), by the whole-text
-        # producer (in fp32 the fused hash kernels: one GEMM and one kernel)
-        self._escribir('phi', pos, capa._phi_y_valores(torch.stack([e_ult, e_t], 1))[0][:, -1])
-        Qc, Kc, beta, log_alfa = capa._contexto(h_t.unsqueeze(1))
-        self._escribir('Qc', pos, Qc[:, 0])
-        self._escribir('Kc', pos, Kc[:, 0])
-        self._escribir('log_alfa', pos, log_alfa[:, 0])
+        if ops.decode_produce_ok(capa, e_t):
+            # fp32: the token's V, phi, Qc, Kc, log_alfa and id rows in two kernels (asrn_decode_produce)
+            beta_t = ops.decode_produce(capa, c, e_t, e_ult, h_t, pieza_t, pos, t_max=t_max)
+        else:
+            self._escribir('sig', pos, pieza_t.to(torch.float32))
+            self._escribir('V', pos - 1, capa.v(e_t))                      # V[t-1] = W_v e_t
+            # the token's phi from its own row and the previous one (the context MLP's key), by the whole-text
+            # producer
+            self._escribir('phi', pos, capa._phi_y_valores(torch.stack([e_ult, e_t], 1))[0][:, -1])
+            Qc, Kc, beta, log_alfa = capa._contexto(h_t.unsqueeze(1))
+            self._escribir('Qc', pos, Qc[:, 0])
+            self._escribir('Kc', pos, Kc[:, 0])
+            self._escribir('log_alfa', pos, log_alfa[:, 0])
+            beta_t = beta[:, 0]
         kappa, kappa_r = capa._kappas()
-        vistos, hawkes = self.hawkes.step(c, pos, beta[:, 0], capa.c_vistos, kappa, kappa_r, self.racha, t_max=t_max)
+        vistos, hawkes = self.hawkes.step(c, pos, beta_t, capa.c_vistos, kappa, kappa_r, self.racha, t_max=t_max)
         salida, sen, _ = ops.decode_attend(c, pos, self.anillos, self.cuentas, capa.w_sufijo, capa.gamma,
                                            self._forma(), insert=not self.ajeno, t_max=t_max)
         acc = {'salida': salida.unsqueeze(1).to(e_t.dtype), 'senales': sen[:, None],

@@ -6,6 +6,7 @@ _Escaneo / escaneo (asrn/nucleo.py:188-196, 518-537), the stable argsorts (asrn/
 the clock cumsum (asrn/estable.py:418).
 """
 import ctypes
+import math
 
 import torch
 
@@ -70,8 +71,9 @@ def candidate_lists(sig, order, win, rank, C, K):
     B, L, T = rank.shape
     pos = torch.empty((B, L, T, C), dtype=I32, device=dev)
     ell = torch.empty_like(pos)
-    call('asrn_candidate_lists', ptr(_c(sig, torch.float32)), ptr(order), ptr(win), ptr(rank), B, L, T, C, K,
-         ptr(pos), ptr(ell), stream_of(dev))
+    sig32 = _c(sig, torch.float32)            # held until the launch: a converted copy must outlive its pointer
+    call('asrn_candidate_lists', ptr(sig32), ptr(order), ptr(win), ptr(rank), B, L, T, C, K, ptr(pos), ptr(ell),
+         stream_of(dev))
     return pos, ell
 
 
@@ -662,6 +664,49 @@ def decode_attend(cache, t, rings, counts, w_suf, gamma, shape, insert, t_max=No
     return salida, signals, ids
 
 
+def decode_produce_ok(capa, e):
+    """Whether asrn_decode_produce covers this layer and input: fp32 (no autocast) and the widths it takes."""
+    pal, ctx = capa.afin_palabra, capa.afin_contexto
+    ps = [capa.v.weight, pal[0].weight, ctx[0].weight, pal[0].bias, ctx[0].bias, pal[2].weight, pal[2].bias,
+          ctx[2].weight, ctx[2].bias, capa.ln_ctx.weight, capa.ln_ctx.bias, capa.w_reloj, capa.b_reloj, capa.cq.weight,
+          capa.ck.weight]
+    d = e.shape[-1]
+    m, mc, cf = pal[0].out_features, ctx[0].out_features, capa.confirmar
+    return (e.is_cuda and e.dtype == torch.float32 and not torch.is_autocast_enabled(e.device.type)
+            and all(p.dtype == torch.float32 and p.is_cuda and p.is_contiguous() for p in ps)
+            and d % 4 == 0 and d <= 1024 and 1 <= m <= 64 and 1 <= mc <= 64 and 1 <= cf <= 64
+            and pal[2].out_features + ctx[2].out_features <= 256)
+
+
+def decode_produce(capa, cache, e, e_prev, h, pieza, t, t_max=None):
+    """The generation step's producers for the new tokens at position t (asrn_decode_produce): V[t-1], phi[t], Qc[t],
+    Kc[t], log_alfa[t] and sig[t] written into the caches; returns beta (B,) fp64. t: an int, or a one-element int64
+    device tensor holding it (then t_max: the largest position it will hold)."""
+    dev = _dev(e)
+    B, d = e.shape
+    pal, ctx = capa.afin_palabra, capa.afin_contexto
+    m, mc = pal[0].out_features, ctx[0].out_features
+    Pw, Pc, cf = pal[2].out_features, ctx[2].out_features, capa.confirmar
+    cap = cache['phi'].shape[1]
+    p = capa.protecciones
+    beta_max = -1.0 if p.beta_max is None else float(p.beta_max)
+    la_min = -math.inf if p.log_alfa_min is None else float(p.log_alfa_min)
+    beta = torch.empty((B,), dtype=torch.float64, device=dev)
+    wsb = query('asrn_decode_produce_workspace', B, m, mc)
+    ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+    th, tdev = _posicion(t, t_max)
+    # the converted inputs are held until the launch (a freed copy's memory could be reused by the next one)
+    ins = [_c(e, torch.float32), _c(e_prev, torch.float32), _c(h, torch.float32), _c(pieza, torch.int64)]
+    call('asrn_decode_produce', ptr(ins[0]), ptr(ins[1]), ptr(ins[2]),
+         ptr(ins[3]), B, d, ptr(capa.v.weight), ptr(pal[0].weight), ptr(ctx[0].weight),
+         ptr(pal[0].bias), ptr(ctx[0].bias), ptr(pal[2].weight), ptr(pal[2].bias), ptr(ctx[2].weight),
+         ptr(ctx[2].bias), m, mc, Pw, Pc, ptr(capa.ln_ctx.weight), ptr(capa.ln_ctx.bias), float(capa.ln_ctx.eps),
+         ptr(capa.w_reloj), ptr(capa.b_reloj), beta_max, la_min, ptr(capa.cq.weight), ptr(capa.ck.weight), cf,
+         ptr(cache['phi']), ptr(cache['V']), ptr(cache['Qc']), ptr(cache['Kc']), ptr(cache['sig']),
+         ptr(cache['log_alfa']), cap, th, tdev, ptr(beta), ptr(ws), wsb, stream_of(dev))
+    return beta
+
+
 def _pow2_at_least(x):
     c = 1
     while c < x:
@@ -685,9 +730,10 @@ class HawkesTable:
         dev = _dev(keys)
         B, L, n = keys.shape
         tab = cls(B, n, _pow2_at_least(max(cap or 0, 2 * L, 2)), dev)
-        call('asrn_hawkes_table_load', ptr(_c(keys, torch.float64)), ptr(order), ptr(rep),
-             ptr(_c(hawkes, torch.float32)), ptr(_c(Bt, torch.float64)), ptr(_c(log_alfa, torch.float32)), B, L, n,
-             tab.cap, ptr(tab.keys), ptr(tab.Bu), ptr(tab.A), stream_of(dev))
+        # the converted inputs are held until the launch (a freed copy's memory could be reused by the next one)
+        ins = [_c(keys, torch.float64), _c(hawkes, torch.float32), _c(Bt, torch.float64), _c(log_alfa, torch.float32)]
+        call('asrn_hawkes_table_load', ptr(ins[0]), ptr(order), ptr(rep), ptr(ins[1]), ptr(ins[2]), ptr(ins[3]), B, L,
+             n, tab.cap, ptr(tab.keys), ptr(tab.Bu), ptr(tab.A), stream_of(dev))
         return tab
 
     def reserve(self, positions):
@@ -711,8 +757,10 @@ class HawkesTable:
         B, stride = sig.shape
         vistos = torch.empty((B, self.n), dtype=torch.float32, device=dev)
         hawkes = torch.empty((B, self.n), dtype=torch.float32, device=dev)
-        call('asrn_repetition_step', ptr(sig), ptr(Bt), ptr(la), ptr(_c(beta_t, torch.float64)),
-             ptr(_c(coef, torch.float64)), ptr(_c(kappa.detach(), torch.float32)),
-             ptr(_c(kappa_r.detach(), torch.float32)), B, stride, th, tdev, self.n, self.cap, ptr(self.keys),
-             ptr(self.Bu), ptr(self.A), ptr(racha), ptr(vistos), ptr(hawkes), stream_of(dev))
+        # the converted inputs are held until the launch (a freed copy's memory could be reused by the next one)
+        ins = [_c(beta_t, torch.float64), _c(coef, torch.float64), _c(kappa.detach(), torch.float32),
+               _c(kappa_r.detach(), torch.float32)]
+        call('asrn_repetition_step', ptr(sig), ptr(Bt), ptr(la), ptr(ins[0]), ptr(ins[1]), ptr(ins[2]), ptr(ins[3]),
+             B, stride, th, tdev, self.n, self.cap, ptr(self.keys), ptr(self.Bu), ptr(self.A), ptr(racha),
+             ptr(vistos), ptr(hawkes), stream_of(dev))
         return vistos, hawkes

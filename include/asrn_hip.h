@@ -317,6 +317,23 @@ int asrn_repetition_step(const float* sig, double* Bt, const float* log_alfa, co
                          int64_t t, const int64_t* t_dev, int32_t n, int64_t cap, uint64_t* tab_keys, double* tab_Bu,
                          float* tab_A, float* racha, float* vistos, float* hawkes, void* stream);
 
+/* decode_produce replaces the per-token producers of _Escritor.paso (asrn/nucleo.py:1797-1826): for the B new tokens
+ * at position t (or *t_dev, as asrn_decode_attend), e, e_prev, h (B, d) fp32, pieza (B) int64, it writes into the
+ * (B, cap, .) caches V[t-1] = W_v e (asrn/nucleo.py:683), phi[t] = the hash MLPs on [e; e_prev] (asrn/nucleo.py:644-659),
+ * Qc[t], Kc[t] = cq hh, ck hh and log_alfa[t] with hh = LayerNorm(h) and the clock projection (asrn/estable.py:153-194),
+ * sig[t] = pieza; beta (B) fp64 out. w_word (m, d) and w_ctx (mc, 2 d) are the MLPs' first layers as nn.Linear holds
+ * them (w_ctx's first d columns act on e, its last d on e_prev); w_cq, w_ck (cf, d). d a multiple of 4, <= 1024;
+ * m, mc, cf <= 64; the float4-read rows 16-byte aligned. workspace: asrn_decode_produce_workspace(B, m, mc) bytes. */
+int64_t asrn_decode_produce_workspace(int64_t B, int32_t m, int32_t mc);
+int asrn_decode_produce(const float* e, const float* e_prev, const float* h, const int64_t* pieza, int64_t B, int32_t d,
+                        const float* w_v, const float* w_word, const float* w_ctx, const float* b_word,
+                        const float* b_ctx, const float* w2_word, const float* b2_word, const float* w2_ctx,
+                        const float* b2_ctx, int32_t m, int32_t mc, int32_t p_word, int32_t p_ctx, const float* ln_w,
+                        const float* ln_b, float eps, const float* w_reloj, const float* b_reloj, float beta_max,
+                        float log_alfa_min, const float* w_cq, const float* w_ck, int32_t cf, float* phi, float* V,
+                        float* Qc, float* Kc, float* sig, float* log_alfa, int64_t cap, int64_t t,
+                        const int64_t* t_dev, double* beta, void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -265,3 +265,41 @@ def test_writer_graph_equals_eager(B, L0, n, cap, kw, ajeno):
         assert torch.equal(eg.cache[k][:, :L0 + n], ee.cache[k][:, :L0 + n]), k
     assert torch.equal(eg.anillos, ee.anillos) and torch.equal(eg.cuentas, ee.cuentas)
     assert torch.equal(eg.racha, ee.racha)
+
+
+@pytest.mark.parametrize('B,d,kw', [(16, 768, {}), (3, 64, SMALL), (2, 32, dict(confirmar=8, n_tablas=5, n_bits=4))])
+def test_decode_produce_matches_the_ops(B, d, kw):
+    """asrn_decode_produce (the step's V, phi, Qc, Kc, log_alfa, id rows and beta in two kernels) against the same rows
+    from the layer's own ops (the hash producer, the context producer, W_v), within 1e-5 relative: the same products
+    summed in another order. Also through a device-held position, and from strided views of the text (the wrapper's
+    contiguous copies held until the launch: freed early, the next copy reused their memory)."""
+    say('decode produce = ops', B, d, kw)
+    torch.manual_seed(4)
+    layer = synth.move_params(CapaASRNEstable(d, **kw), 4).to(DEV)
+    x, E, h = synth.layer_inputs(B, 40, d, 9, seed=3)
+    Ed, hd, xd = E.to(DEV), h.to(DEV), x.to(DEV)
+    esc = EscritorCapa(layer, memoria_de_lo_ajeno=False)
+    esc.inicio(Ed[:, :30], hd[:, :30], xd[:, :30], capacidad=40)
+    t = 30
+    e_t, e_prev, h_t = Ed[:, t].contiguous(), Ed[:, t - 1].contiguous(), hd[:, t].contiguous()
+    assert ops.decode_produce_ok(layer, e_t)
+    with torch.no_grad():
+        v = layer.v(e_t)
+        phi = layer._phi_y_valores(torch.stack([e_prev, e_t], 1))[0][:, -1]
+        Qc, Kc, beta, la = layer._contexto(h_t.unsqueeze(1))
+    strided = (Ed[:, t], Ed[:, t - 1], hd[:, t])             # views: the wrapper's converted copies must live on
+    for pos, ins in ((t, (e_t, e_prev, h_t)), (torch.full((1,), t, dtype=torch.int64, device=DEV), strided),
+                     (t, strided)):
+        cache = {k: v_.clone() for k, v_ in esc.cache.items()}
+        got_beta = ops.decode_produce(layer, cache, *ins, xd[:, t], pos, t_max=t)
+        assert_close(cache['V'][:, t - 1], v, 'V', 1e-5)
+        assert_close(cache['phi'][:, t], phi, 'phi', 1e-5)
+        assert_close(cache['Qc'][:, t], Qc[:, 0], 'Qc', 1e-5)
+        assert_close(cache['Kc'][:, t], Kc[:, 0], 'Kc', 1e-5)
+        assert_close(cache['log_alfa'][:, t], la[:, 0], 'log_alfa', 1e-5)
+        assert_close(got_beta, beta[:, 0], 'beta', 1e-5)
+        assert torch.equal(cache['sig'][:, t], xd[:, t].float())
+        for k in cache:                                    # nothing else written
+            rows = [t - 1, t] if k == 'V' else [t]
+            keep = [i for i in range(cache[k].shape[1]) if i not in rows]
+            assert torch.equal(cache[k][:, keep], esc.cache[k][:, keep]), k

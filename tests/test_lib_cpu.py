@@ -140,6 +140,19 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert 'grow it first' in _err(lib)
     assert lib.asrn_hawkes_table_grow(N, N, N, 8, 256, N, N, N, 128, N) != 0
     assert 'growing' in _err(lib)
+    # the step's producers: width, position, workspace
+    prod = [N] * 4
+    w = [N] * 9
+    assert lib.asrn_decode_produce(*prod, 16, 6, *w, 64, 64, 56, 56, N, N, 1e-5, N, N, 1e4, -30.0, N, N, 16,
+                                   *([N] * 6), 100, 50, N, N, N, 0, N) != 0
+    assert 'd=6' in _err(lib)
+    assert lib.asrn_decode_produce(*prod, 16, 768, *w, 64, 64, 56, 56, N, N, 1e-5, N, N, 1e4, -30.0, N, N, 16,
+                                   *([N] * 6), 100, 100, N, N, N, 0, N) != 0
+    assert 'outside' in _err(lib)
+    assert lib.asrn_decode_produce_workspace(16, 64, 64) == 16 * 192 * 4
+    assert lib.asrn_decode_produce(*prod, 16, 768, *w, 64, 64, 56, 56, N, N, 1e-5, N, N, 1e4, -30.0, N, N, 16,
+                                   *([N] * 6), 100, 50, N, N, N, 0, N) != 0
+    assert 'workspace' in _err(lib)
 
 
 def test_ops_refuse_cpu_tensors():
