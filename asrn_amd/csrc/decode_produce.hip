@@ -12,9 +12,10 @@
 // The context MLP's first layer is read in place as its (mc, 2 d) weight: a row's first d columns act on e_t (W_a) and
 // its last d on e_prev (W_b).
 //
-// Two launches. The first splits the weight rows into blocks of 16 (W_v, W_p, W_a, W_b, cq, ck); a workgroup stages
-// 16 tokens' input vectors in LDS (e_t, e_prev, or hh with the LayerNorm done there) and each wave dots 4 rows with
-// them, so every weight row is read once per 16 tokens. The second takes one token per workgroup: the hidden units,
+// Two launches. The first splits the weight rows into blocks of 4 (W_v, W_p, W_a, W_b, cq, ck); a workgroup stages
+// 16 tokens' input vectors in LDS (e_t, e_prev, or hh with the LayerNorm done there) and each wave dots one row with
+// them, so every weight row is read once per 16 tokens. One row per wave keeps each wave's chain of dot products
+// short and spreads the launch over the whole chip (d = 768: about 270 workgroups). The second takes one token per workgroup: the hidden units,
 // both second layers and the clock. Every sum runs in a fixed order. The position is t, or *t_dev (a step replayed
 // from a graph); a position outside [1, cap) writes nothing.
 #include "common.h"
@@ -23,7 +24,7 @@ namespace asrn {
 
 constexpr int kProdThreads = 256;
 constexpr int kProdWaves = kProdThreads / kWave;
-constexpr int kProdRows = 16;          // weight rows per workgroup of the first launch
+constexpr int kProdRows = kProdWaves; // weight rows per workgroup of the first launch: one per wave
 constexpr int kProdTok = 16;           // tokens per workgroup of the first launch
 constexpr int kProdMaxD4 = 4;          // d <= 1024
 constexpr int kProdMax = 64;           // hidden units, outputs per hash MLP, and cf, at most
@@ -101,12 +102,10 @@ __global__ __launch_bounds__(kProdThreads) void k_produce_rows(ProdArgs a) {
     layer_norm_rows(a, xs, ntok, d4);
     __syncthreads();
   }
-  // wave w dots rows 4w .. 4w + 3 of the block with every token
-  const int r0 = blk * kProdRows + wave * 4;
-  float4 w[4][D4];
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int r = r0 + rr;
+  // wave w dots row w of the block with every token
+  const int r = blk * kProdRows + wave;
+  float4 w[D4];
+  {
     const float* row = k == 0 ? a.wv + (int64_t)r * a.d
                      : (k == 1 ? a.ww + (int64_t)r * a.d
                      : (k == 2 ? a.wc + (int64_t)r * 2 * a.d
@@ -115,21 +114,19 @@ __global__ __launch_bounds__(kProdThreads) void k_produce_rows(ProdArgs a) {
 #pragma unroll
     for (int kk = 0; kk < D4; ++kk) {
       const int q = lane + kWave * kk;
-      w[rr][kk] = r < nrows && q < d4 ? ((const float4*)row)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      w[kk] = r < nrows && q < d4 ? ((const float4*)row)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
   for (int j = 0; j < ntok; ++j) {
     const int64_t b = b0 + j;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
+    {
       float p = 0.f;
 #pragma unroll
       for (int kk = 0; kk < D4; ++kk) {
         const int q = lane + kWave * kk;
-        if (q < d4) p += dot4(w[rr][kk], xs[j * d4 + q]);
+        if (q < d4) p += dot4(w[kk], xs[j * d4 + q]);
       }
       const float s = wave_sum_u(p);
-      const int r = r0 + rr;
       if (lane == 0 && r < nrows) {
         const int n1 = a.m + 2 * a.mc;
         if (k == 0) a.V[(b * a.cap + t - 1) * a.d + r] = s;
