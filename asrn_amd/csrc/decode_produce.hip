@@ -13,9 +13,10 @@
 // its last d on e_prev (W_b).
 //
 // Two launches. The first splits the weight rows into blocks of 4 (W_v, W_p, W_a, W_b, cq, ck); a workgroup stages
-// 16 tokens' input vectors in LDS (e_t, e_prev, or hh with the LayerNorm done there) and each wave dots one row with
-// them, so every weight row is read once per 16 tokens. One row per wave keeps each wave's chain of dot products
-// short and spreads the launch over the whole chip (d = 768: about 270 workgroups). The second takes one token per workgroup: the hidden units,
+// 4 tokens' input vectors in LDS (e_t, e_prev, or hh with the LayerNorm done there) and each wave dots one row with
+// them, so every weight row is read once per 4 tokens. The step is latency-bound, not bandwidth-bound: one row and
+// 4 tokens per wave keep each wave's chain of dot products short and spread the launch over the whole chip (d = 768,
+// B = 16: about 1080 workgroups; 16 tokens and 16 rows per workgroup took 31 us, this 8). The second takes one token per workgroup: the hidden units,
 // both second layers and the clock. Every sum runs in a fixed order. The position is t, or *t_dev (a step replayed
 // from a graph); a position outside [1, cap) writes nothing.
 #include "common.h"
@@ -25,7 +26,7 @@ namespace asrn {
 constexpr int kProdThreads = 256;
 constexpr int kProdWaves = kProdThreads / kWave;
 constexpr int kProdRows = kProdWaves; // weight rows per workgroup of the first launch: one per wave
-constexpr int kProdTok = 16;           // tokens per workgroup of the first launch
+constexpr int kProdTok = 4;            // tokens per workgroup of the first launch
 constexpr int kProdMaxD4 = 4;          // d <= 1024
 constexpr int kProdMax = 64;           // hidden units, outputs per hash MLP, and cf, at most
 
