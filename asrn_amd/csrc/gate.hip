@@ -84,8 +84,27 @@ __device__ __forceinline__ float small_param(const GateArgs& a, int c) {
   return a.dr[c - 6 - 2 * n];
 }
 
-// phase 1: token t's features into f (LDS row), its info into ti
-__device__ void token_features(const GateArgs& a, int64_t t, float* f, TokenInfo* ti) {
+// the packed small parameters into LDS, one thread each, so that phase 1's sum reads them without a chain of global
+// loads (a short input, the generation step's few tokens, waits on that chain alone); S <= kGateCols
+__device__ __forceinline__ void stage_small_params(const GateArgs& a, float* P) {
+  if (threadIdx.x < 6 + 2 * a.n + a.nodes) P[threadIdx.x] = small_param(a, threadIdx.x);
+}
+
+constexpr int kGateMaxN = (kGateCols - 8) / 2;   // tables, at most (6 + 2 n + nodes <= kGateCols, nodes >= 2)
+
+// the workgroup's seen flags and Hawkes intensities (n per token, rows in token order) into LDS, all threads loading
+__device__ __forceinline__ void stage_token_rows(const GateArgs& a, int64_t t0, float* vis, float* haw) {
+  const int64_t nt = a.BL - t0 < kGateTok ? a.BL - t0 : kGateTok;
+  for (int64_t i = threadIdx.x; i < nt * a.n; i += kGateThreads) {
+    vis[i] = a.vistos[t0 * a.n + i];
+    haw[i] = a.hawkes[t0 * a.n + i];
+  }
+}
+
+// phase 1: token t's features into f (LDS row), its info into ti; P the staged small parameters, vis and haw the
+// token's staged rows
+__device__ void token_features(const GateArgs& a, int64_t t, const float* P, const float* vis, const float* haw,
+                               float* f, TokenInfo* ti) {
   const int n = a.n, S = 6 + 2 * n + a.nodes;
   const float4 g = ((const float4*)a.sig)[t];     // peso_total, mejor, pico, peso_ctx
   const float pt = g.x;
@@ -98,8 +117,8 @@ __device__ void token_features(const GateArgs& a, int64_t t, float* f, TokenInfo
   f[4] = g.w / (float)a.Tc;
   f[5] = 1.f;
   for (int j = 0; j < n; ++j) {
-    f[6 + j] = a.vistos[t * n + j];
-    f[6 + n + j] = log1pf(a.hawkes[t * n + j]);
+    f[6 + j] = vis[j];
+    f[6 + n + j] = log1pf(haw[j]);
   }
   const float top = (float)(a.nodes - 1);
   const float ra = a.racha[t];
@@ -110,7 +129,7 @@ __device__ void token_features(const GateArgs& a, int64_t t, float* f, TokenInfo
   const int i = (int)fi;
   for (int m = 0; m < a.nodes; ++m) f[6 + 2 * n + m] = (m <= i ? 1.f : 0.f) + (m == i + 1 ? x - fi : 0.f);
   float small = 0.f;
-  for (int c = 0; c < S; ++c) small += small_param(a, c) * f[c];
+  for (int c = 0; c < S; ++c) small += P[c] * f[c];
   ti->r = 1.f / fmaxf(pt, 1.f);
   ti->small = small;
   ti->dxdr = xr <= top ? 1.f / ((1.f + ra) * a.paso) : 0.f;
@@ -123,11 +142,17 @@ template <int D4>
 __global__ __launch_bounds__(kGateThreads) void k_gate_fwd(GateArgs a) {
   __shared__ float feat[kGateTok][kFeatStride];
   __shared__ TokenInfo info[kGateTok];
+  __shared__ float P[kGateCols];
+  __shared__ float vh[2][kGateTok * kGateMaxN];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int d4 = a.d >> 2;
   const int64_t t0 = (int64_t)blockIdx.x * kGateTok;
+  stage_small_params(a, P);
+  stage_token_rows(a, t0, vh[0], vh[1]);
+  __syncthreads();
   if (threadIdx.x < kGateTok && t0 + threadIdx.x < a.BL)
-    token_features(a, t0 + threadIdx.x, feat[threadIdx.x], &info[threadIdx.x]);
+    token_features(a, t0 + threadIdx.x, P, vh[0] + threadIdx.x * a.n, vh[1] + threadIdx.x * a.n, feat[threadIdx.x],
+                   &info[threadIdx.x]);
   __syncthreads();
   for (int b = 0; b < kGateTokPerWave; b += kGateBatch) {
     float4 hv[kGateBatch][D4], av[kGateBatch][D4];
@@ -177,9 +202,16 @@ __global__ __launch_bounds__(kGateThreads) void k_gate_bwd(GateArgs a) {
   const int d4 = a.d >> 2;
   const int n = a.n, S = 6 + 2 * n + a.nodes;
   const int64_t t0 = (int64_t)blockIdx.x * kGateTok;
+  __shared__ float P[kGateCols];
+  __shared__ float vh[2][kGateTok * kGateMaxN];
+  stage_small_params(a, P);
+  stage_token_rows(a, t0, vh[0], vh[1]);
+  __syncthreads();
   if (threadIdx.x < kGateTok) {
     dl[threadIdx.x] = 0.f;
-    if (t0 + threadIdx.x < a.BL) token_features(a, t0 + threadIdx.x, feat[threadIdx.x], &info[threadIdx.x]);
+    if (t0 + threadIdx.x < a.BL)
+      token_features(a, t0 + threadIdx.x, P, vh[0] + threadIdx.x * n, vh[1] + threadIdx.x * n, feat[threadIdx.x],
+                     &info[threadIdx.x]);
   }
   __syncthreads();
   float4 gw[D4];
