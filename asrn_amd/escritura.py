@@ -118,21 +118,21 @@ class EscritorCapa:
         salida, sen, _ = ops.decode_attend(c, pos, self.anillos, self.cuentas, capa.w_sufijo, capa.gamma,
                                            self._forma(), insert=not self.ajeno, t_max=t_max)
         acc = {'salida': salida.unsqueeze(1).to(e_t.dtype), 'senales': sen[:, None],
-               'vistos': vistos.unsqueeze(1), 'hawkes': hawkes.unsqueeze(1), 'racha': self.racha.unsqueeze(1).clone()}
+               'vistos': vistos.unsqueeze(1), 'hawkes': hawkes.unsqueeze(1), 'racha': self.racha.unsqueeze(1)}
         return capa._combinar(acc, h_t.unsqueeze(1))[:, 0]
 
     @torch.no_grad()
     def paso(self, e_t, h_t, pieza_t):
         """One new token at position t: e_t, h_t (B, d) its embedding and layer input, pieza_t (B,) its id ->
         the layer's output (B, d) (the layer part of asrn/nucleo.py:1797-1854)."""
-        # rows of a (B, L, d) text are strided views; the GEMMs below want dense (B, d) operands (a batch stride
-        # above 2^25 elements is outside what hipBLASLt accepts, and its fallback costs ~20 ms per call)
-        e_t, h_t = e_t.contiguous(), h_t.contiguous()
         if self.t >= self.cap:
             self._crecer()
             self._g = None
         if self.grafo and self._calentado:
-            return self._paso_grafo(e_t, h_t, pieza_t)
+            return self._paso_grafo(e_t, h_t, pieza_t)     # its dense input buffers take strided rows in one copy
+        # rows of a (B, L, d) text are strided views; the GEMMs below want dense (B, d) operands (a batch stride
+        # above 2^25 elements is outside what hipBLASLt accepts, and its fallback costs ~20 ms per call)
+        e_t, h_t = e_t.contiguous(), h_t.contiguous()
         y = self._cuerpo(e_t, self.e_ult, h_t, pieza_t, self.t)
         self.e_ult = e_t
         self.t += 1
@@ -154,7 +154,7 @@ class EscritorCapa:
         """Captures one step whose position is the device counter _pos (valid for positions < cap, the caches'
         capacity): the step, then e_ult <- e_t and _pos += 1."""
         self.hawkes.reserve(self.cap)          # tables sized for every position the graph will see: no growth inside
-        self._e, self._h, self._p = torch.empty_like(e_t), torch.empty_like(h_t), torch.empty_like(pieza_t)
+        self._e, self._h, self._p = (torch.empty(v.shape, dtype=v.dtype, device=v.device) for v in (e_t, h_t, pieza_t))
         self._e_ult = self.e_ult.clone()
         self._pos = torch.full((1,), self.t, dtype=torch.int64, device=e_t.device)
         torch.cuda.current_stream(e_t.device).synchronize()
