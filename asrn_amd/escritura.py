@@ -113,7 +113,10 @@ class EscritorCapa:
             self._escribir('Kc', pos, Kc[:, 0])
             self._escribir('log_alfa', pos, log_alfa[:, 0])
             beta_t = beta[:, 0]
-        kappa, kappa_r = capa._kappas()
+        # both decay rates in one launch (capa._kappas' values, without autograd)
+        kappa, kappa_r = torch._foreach_exp([capa.log_kappa, capa.log_kappa_racha])
+        if capa.protecciones.kappa_min is not None:
+            kappa, kappa_r = kappa.clamp(min=capa.protecciones.kappa_min), kappa_r.clamp(min=capa.protecciones.kappa_min)
         vistos, hawkes = self.hawkes.step(c, pos, beta_t, capa.c_vistos, kappa, kappa_r, self.racha, t_max=t_max)
         salida, sen, _ = ops.decode_attend(c, pos, self.anillos, self.cuentas, capa.w_sufijo, capa.gamma,
                                            self._forma(), insert=not self.ajeno, t_max=t_max)
