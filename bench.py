@@ -213,6 +213,8 @@ def main():
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-decode', action='store_true')
     ap.add_argument('--decode-steps', type=int, default=32)
+    ap.add_argument('--decode-only', action='store_true',
+                    help='only the generation-step leg (configs[4], one layer); prints its JSON object')
     ap.add_argument('--eager', action='store_true', help='time Python-launched steps instead of HIP graph replays')
     ap.add_argument('--default-gemms', action='store_true',
                     help="leave the GEMMs on the libraries' default picks instead of the shipped MI355X picks")
@@ -246,6 +248,10 @@ def main():
         from asrn_amd import tuning
         if tuning.use_tuned_gemms():
             gemm_picks = 'TunableOp picks, asrn_amd/data/gemm_picks_mi355x.csv'
+    if args.decode_only:
+        print(json.dumps({'decode': decode_bench(torch.device('cuda:0'), args.decode_steps, 5, seed=args.seed),
+                          'gemm_picks': gemm_picks}), flush=True)
+        return
     cfg = synth.CONFIGS[args.config]
     B, N, d, V = cfg['B'], cfg['N'], cfg['d'], cfg['V']
     dev = torch.device('cuda:0')
