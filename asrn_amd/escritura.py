@@ -145,27 +145,36 @@ class EscritorCapa:
     def _paso_grafo(self, e_t, h_t, pieza_t):
         if self._g is None:
             self._capturar(e_t, h_t, pieza_t)
-        self._e.copy_(e_t)
+        k = self._k
+        self._eb[k].copy_(e_t)
         self._h.copy_(h_t)
         self._p.copy_(pieza_t)
-        self._g.replay()
+        self._g[k].replay()
         self.t += 1
-        self.e_ult = self._e_ult
-        return self._y.clone()
+        self.e_ult = self._eb[k]
+        self._k = 1 - k
+        return self._y[k].clone()
 
     def _capturar(self, e_t, h_t, pieza_t):
-        """Captures one step whose position is the device counter _pos (valid for positions < cap, the caches'
-        capacity): the step, then e_ult <- e_t and _pos += 1."""
+        """Captures the step twice, with the two embedding buffers in swapped roles: graph k reads the token's
+        embedding from buffer k and the previous one from buffer 1 - k, so consecutive steps alternate and no copy
+        carries e_t over. Its position is the device counter _pos (valid for positions < cap, the caches' capacity):
+        the step, then _pos += 1."""
         self.hawkes.reserve(self.cap)          # tables sized for every position the graph will see: no growth inside
-        self._e, self._h, self._p = (torch.empty(v.shape, dtype=v.dtype, device=v.device) for v in (e_t, h_t, pieza_t))
-        self._e_ult = self.e_ult.clone()
+        self._eb = [torch.empty(e_t.shape, dtype=e_t.dtype, device=e_t.device) for _ in range(2)]
+        self._h, self._p = (torch.empty(v.shape, dtype=v.dtype, device=v.device) for v in (h_t, pieza_t))
+        self._eb[1].copy_(self.e_ult)
+        self._k = 0
         self._pos = torch.full((1,), self.t, dtype=torch.int64, device=e_t.device)
         torch.cuda.current_stream(e_t.device).synchronize()
-        self._g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self._g):
-            self._y = self._cuerpo(self._e, self._e_ult, self._h, self._p, self._pos, t_max=self.cap - 1)
-            self._e_ult.copy_(self._e)
-            self._pos.add_(1)
+        self._g, self._y = [], []
+        for k in range(2):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._y.append(self._cuerpo(self._eb[k], self._eb[1 - k], self._h, self._p, self._pos,
+                                            t_max=self.cap - 1))
+                self._pos.add_(1)
+            self._g.append(g)
 
 
 LayerWriter = EscritorCapa
