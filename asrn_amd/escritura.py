@@ -146,9 +146,18 @@ class EscritorCapa:
         if self._g is None:
             self._capturar(e_t, h_t, pieza_t)
         k = self._k
-        self._eb[k].copy_(e_t)
-        self._h.copy_(h_t)
-        self._p.copy_(pieza_t)
+        dev = self._h.device
+        if (all(v.device == dev for v in (e_t, h_t, pieza_t)) and e_t.dtype == h_t.dtype == torch.float32
+                and pieza_t.dtype == torch.int64 and e_t.shape == self._eb[k].shape and h_t.shape == self._h.shape
+                and pieza_t.shape == self._p.shape and e_t.stride(1) == 1 and h_t.stride(1) == 1
+                and e_t.stride(0) >= e_t.shape[1] and h_t.stride(0) >= h_t.shape[1] and pieza_t.stride(0) >= 1):
+            # the three inputs into the graph's buffers in one launch (the ids as pairs of 32-bit words, moved as bits)
+            ops.copy_blocks([(e_t, self._eb[k]), (h_t, self._h),
+                             (pieza_t.unsqueeze(1).view(torch.float32), self._p.view(torch.float32).view(-1, 2))])
+        else:
+            self._eb[k].copy_(e_t)
+            self._h.copy_(h_t)
+            self._p.copy_(pieza_t)
         self._g[k].replay()
         self.t += 1
         self.e_ult = self._eb[k]
