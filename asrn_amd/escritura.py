@@ -151,13 +151,17 @@ class EscritorCapa:
                 and pieza_t.dtype == torch.int64 and e_t.shape == self._eb[k].shape and h_t.shape == self._h.shape
                 and pieza_t.shape == self._p.shape and e_t.stride(1) == 1 and h_t.stride(1) == 1
                 and e_t.stride(0) >= e_t.shape[1] and h_t.stride(0) >= h_t.shape[1] and pieza_t.stride(0) >= 1):
-            # the three inputs into the graph's buffers in one launch (the ids as pairs of 32-bit words, moved as bits)
+            # the three inputs and the position into the graph's buffers in one launch (the int64 ids and position
+            # as pairs of 32-bit words, moved as bits)
             ops.copy_blocks([(e_t, self._eb[k]), (h_t, self._h),
-                             (pieza_t.unsqueeze(1).view(torch.float32), self._p.view(torch.float32).view(-1, 2))])
+                             (pieza_t.unsqueeze(1).view(torch.float32), self._p.view(torch.float32).view(-1, 2)),
+                             (self._posiciones[self.t:self.t + 1].unsqueeze(1).view(torch.float32),
+                              self._pos.view(torch.float32).view(1, 2))])
         else:
             self._eb[k].copy_(e_t)
             self._h.copy_(h_t)
             self._p.copy_(pieza_t)
+            self._pos.copy_(self._posiciones[self.t:self.t + 1])
         self._g[k].replay()
         self.t += 1
         self.e_ult = self._eb[k]
@@ -167,13 +171,14 @@ class EscritorCapa:
     def _capturar(self, e_t, h_t, pieza_t):
         """Captures the step twice, with the two embedding buffers in swapped roles: graph k reads the token's
         embedding from buffer k and the previous one from buffer 1 - k, so consecutive steps alternate and no copy
-        carries e_t over. Its position is the device counter _pos (valid for positions < cap, the caches' capacity):
-        the step, then _pos += 1."""
+        carries e_t over. Its position is the device scalar _pos (valid for positions < cap, the caches' capacity),
+        set before each replay from the device table _posiciones = 0, 1, ..., cap - 1."""
         self.hawkes.reserve(self.cap)          # tables sized for every position the graph will see: no growth inside
         self._eb = [torch.empty(e_t.shape, dtype=e_t.dtype, device=e_t.device) for _ in range(2)]
         self._h, self._p = (torch.empty(v.shape, dtype=v.dtype, device=v.device) for v in (h_t, pieza_t))
         self._eb[1].copy_(self.e_ult)
         self._k = 0
+        self._posiciones = torch.arange(self.cap, dtype=torch.int64, device=e_t.device)
         self._pos = torch.full((1,), self.t, dtype=torch.int64, device=e_t.device)
         torch.cuda.current_stream(e_t.device).synchronize()
         self._g, self._y = [], []
@@ -182,7 +187,6 @@ class EscritorCapa:
             with torch.cuda.graph(g):
                 self._y.append(self._cuerpo(self._eb[k], self._eb[1 - k], self._h, self._p, self._pos,
                                             t_max=self.cap - 1))
-                self._pos.add_(1)
             self._g.append(g)
 
 

@@ -212,7 +212,7 @@ def main():
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-decode', action='store_true')
-    ap.add_argument('--decode-steps', type=int, default=32)
+    ap.add_argument('--decode-steps', type=int, default=256)
     ap.add_argument('--decode-only', action='store_true',
                     help='only the generation-step leg (configs[4], one layer); prints its JSON object')
     ap.add_argument('--eager', action='store_true', help='time Python-launched steps instead of HIP graph replays')
@@ -249,7 +249,7 @@ def main():
         if tuning.use_tuned_gemms():
             gemm_picks = 'TunableOp picks, asrn_amd/data/gemm_picks_mi355x.csv'
     if args.decode_only:
-        print(json.dumps({'decode': decode_bench(torch.device('cuda:0'), args.decode_steps, 5, seed=args.seed),
+        print(json.dumps({'decode': decode_bench(torch.device('cuda:0'), args.decode_steps, 20, seed=args.seed),
                           'gemm_picks': gemm_picks}), flush=True)
         return
     cfg = synth.CONFIGS[args.config]
@@ -357,7 +357,7 @@ def main():
                     for n, s in sorted(per_call.items(), key=lambda kv: -kv[1]['total_ms'])},
     }
     if not args.no_decode:
-        out['decode'] = decode_bench(dev, args.decode_steps, 5, seed=args.seed)
+        out['decode'] = decode_bench(dev, args.decode_steps, 20, seed=args.seed)
     if not args.no_cpu_baseline:
         out['cpu_baseline'] = cpu_baseline(layer_cpu, x, E, h, gy)
     print(json.dumps(out), flush=True)
