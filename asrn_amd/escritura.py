@@ -8,21 +8,25 @@ EscritorCapa(capa, memoria_de_lo_ajeno) keeps, per layer:
               (asrn/nucleo.py:1585-1618), built from the prompt's stable bucket sort;
   Hawkes      per (text, group) open-addressing tables of (key code, Bu, A) (asrn/nucleo.py:1634-1714);
   racha       (B,) the streak.
-inicio() runs the layer over the prompt (its ordinary forward) and builds that state; paso() processes one new token
-with two HIP kernels: asrn_repetition_step (clock advance, n-gram keys, Hawkes lookup/update, streak) and
-asrn_decode_attend (the T*C ring candidates: score, exact softmax, copy-gather, and the ring insert when every
-position may become a key). The per-token producers (hash MLPs, V, context projections) and the gate stay PyTorch,
-as in the whole-text layer. Every step reads a fixed amount, T*C candidates, whatever the text length.
+inicio() runs the layer over the prompt (its ordinary forward) and builds that state; paso() processes one new token:
+asrn_decode_produce writes the token's V, phi, Qc, Kc, log_alfa and signature rows into the caches and returns its
+beta (fp32 layers within its widths; otherwise the layer's own producers, PyTorch GEMMs, write those rows);
+asrn_repetition_step advances the clock and does the n-gram keys, the Hawkes lookup/update and the streak;
+asrn_decode_attend scores the T*C ring candidates (exact softmax, copy-gather) and inserts the token into the rings
+when every position may become a key; the gate is the layer's fused gate kernel after the W_o GEMM. Every step reads
+a fixed amount, T*C candidates, whatever the text length.
 
 memoria_de_lo_ajeno=True (the reference default): the keys are only prompt positions k with k + 1 < L0 (their V rows
 are values of prompt tokens), so the rings hold positions 0..L0-2 and never change. False: every earlier position is
 a key, and the step equals the whole-text layer position by position.
 
-grafo=True: the step is captured once in a HIP graph and replayed, since launching its ~30 small kernels from Python
-costs several times their GPU time. The position then lives in a device counter that the two HIP kernels read and the
-graph advances; the first step runs eagerly (it initializes the GEMM libraries' handles), the second is captured, and
-a capacity doubling (new cache tensors) captures again. The graph holds the layer's parameters and this writer's
-state by address: replacing a parameter tensor (rather than updating it in place) needs a new writer.
+grafo=True: the step is captured once in a HIP graph and replayed, since launching its small kernels from Python
+costs several times their GPU time. The position then lives in a one-element device buffer that the kernels read: one
+asrn_copy_blocks launch before each replay copies the token's inputs into the graph's input buffers and the position
+from a device table of positions (0, 1, ..., cap - 1) into that buffer, so nothing inside the graph advances it. The
+first step runs eagerly (it initializes the GEMM libraries' handles), the second is captured, and a capacity doubling
+(new cache tensors) captures again. The graph holds the layer's parameters and this writer's state by address:
+replacing a parameter tensor (rather than updating it in place) needs a new writer.
 """
 import torch
 
@@ -47,7 +51,8 @@ class EscritorCapa:
         return dict(T=c.n_tablas, Tc=c.tablas_contexto, C=c.chunk, K=c.sufijo, nb=c.n_bits)
 
     def bytes_anillos(self, B):
-        """Device bytes of the rings and counts (asrn/nucleo.py:1747-1748 sizes them the same way)."""
+        """Device bytes of the rings and counts: (B*T, 2^nb) buckets of C int32 slots and an int32 count. The
+        reference sizes its rings as B*T*2^nb*(4*chunk + 8) bytes (int32 slots, int64 counts; asrn/nucleo.py:1747)."""
         c = self.capa
         return B * c.n_tablas * 2 ** c.n_bits * (4 * c.chunk + 4)
 
@@ -95,7 +100,7 @@ class EscritorCapa:
             c[:, pos] = valor
 
     def _cuerpo(self, e_t, e_ult, h_t, pieza_t, pos, t_max=None):
-        """One step's work at position pos (an int, or a device counter holding it with t_max its largest value) ->
+        """One step's work at position pos (an int, or a one-element device buffer holding it, t_max its largest value) ->
         the layer's output (B, d) (the layer part of asrn/nucleo.py:1797-1854)."""
         capa = self.capa
         c = self.cache

@@ -117,15 +117,19 @@ class HawkesMemory:
         """keys (B, L, n) fp64, hawkes (B, L, n), Bt (B, L) fp64, log_alfa (B, L): every key's last occurrence
         (nucleo:1656-1681)."""
         B, L, n = keys.shape
+        A_all = (hawkes + log_alfa.exp().unsqueeze(-1)).float()              # A = lambda + alfa, per position
         for b in range(B):
+            Bb = Bt[b].tolist()
             for j in range(n):
                 m = self.maps[b * n + j] = {}
+                ks, As = keys[b, :, j].tolist(), A_all[b, :, j]
                 for t in range(L):
-                    k = float(keys[b, t, j])
+                    k = ks[t]
                     if k != k:
                         continue
-                    A = (hawkes[b, t, j] + log_alfa[b, t].exp()).float()
-                    m[k] = [Bt[b, t].item(), A]
+                    m[k] = [Bb[t], t]
+                for v in m.values():                        # the last occurrence's A, as a 0-d fp32 tensor
+                    v[1] = As[v[1]].clone()
 
     def step(self, keys_t, B_t, log_alfa_t, kappa):
         """keys_t (B, n) fp64, B_t (B,) fp64, log_alfa_t (B,), kappa (n,) -> vistos, hawkes (B, n) fp32

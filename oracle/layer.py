@@ -89,9 +89,18 @@ def suffix_len(a, b):
 # producers (they stay PyTorch GEMMs in the product as well)
 # ----------------------------------------------------------------------------------------------------------------
 
+def _autocast(x):
+    """x in autocast's 16-bit type when CPU autocast is on, else x (nucleo:565-571)."""
+    if torch.is_autocast_enabled('cpu') and x.is_floating_point():
+        return x.to(torch.get_autocast_dtype('cpu'))
+    return x
+
+
 def phi_and_values(p, E):
     """phi (B, L, P) = [word hash(E_t) ; context hash(E_t, E_{t-1})] and V[t] = W_v E[t+1] with V[L-1] = 0.
-    The first word-hash layer and W_v share one GEMM, as in nucleo:644-659."""
+    The first word-hash layer and W_v share one GEMM, as in nucleo:644-659; under autocast E is converted once and
+    the key [E_t; E_{t-1}] is built from the 16-bit E (nucleo:653)."""
+    E = _autocast(E)
     B, L, d = E.shape
     W0, b0 = p['afin_palabra.0.weight'], p['afin_palabra.0.bias']
     m = W0.shape[0]
@@ -105,12 +114,23 @@ def phi_and_values(p, E):
 
 
 def context(p, h, sh, prot):
-    """Qc, Kc (B, L, cf), beta (B, L) fp64, log_alfa (B, L) fp32 (estable:153-194, the CPU no-autocast branch:
-    one GEMM for cq, ck and the clock projection)."""
+    """Qc, Kc (B, L, cf), beta (B, L) fp64, log_alfa (B, L) fp32 (estable:153-194, its CPU branches). Without
+    autocast: one GEMM for cq, ck and the clock projection (estable:181-185). Under autocast: Qc, Kc from the 16-bit
+    LayerNorm output, the clock projection apart in fp32 with autocast off (estable:176-180)."""
     cf = sh.cf
-    hh = F.layer_norm(h, (h.shape[-1],), p['ln_ctx.weight'], p['ln_ctx.bias'])
+    hh32 = F.layer_norm(h, (h.shape[-1],), p['ln_ctx.weight'], p['ln_ctx.bias'])
+    hh = _autocast(hh32)
+    if hh.dtype != hh32.dtype:
+        y = F.linear(hh, torch.cat([p['cq.weight'], p['ck.weight']]))
+        with torch.autocast(device_type='cpu', enabled=False):
+            u = F.linear(hh32.float(), p['w_reloj'].float(), p['b_reloj'].float())
+        return _clock(y, u, cf, prot)
     y = F.linear(hh, torch.cat([p['cq.weight'], p['ck.weight'], p['w_reloj']]), F.pad(p['b_reloj'], (2 * cf, 0)))
-    u = y[..., 2 * cf:].float()
+    return _clock(y, y[..., 2 * cf:].float(), cf, prot)
+
+
+def _clock(y, u, cf, prot):
+    """beta = min(softplus(u_0), beta_max) in fp64 and log_alfa = max(logsigmoid(u_1) + log 2, min) (estable:186-193)."""
     beta = F.softplus(u[..., 0])
     log_alfa = F.logsigmoid(u[..., 1]) + math.log(2)
     if prot.beta_max is not None:
@@ -232,6 +252,54 @@ def candidates(phi, V, Qc, Kc, Bt, log_alfa, sig, w_suf, gamma, sh):
     sen = torch.cat([hay.float(), torch.where(hay, mx, torch.full_like(mx, PROHIBIDO)).float(),
                      att.detach().amax(-1, keepdim=True).float()], dim=-1)
     sen = sen.reshape(-1, 3).index_select(0, row_of).view(B, T, L, 3)
+    return salida, sen
+
+
+def candidates_at(phi, V, Qc, Kc, Bt, log_alfa, sig, w_suf, gamma, sh, ids, queries):
+    """The candidate attention of selected queries only, one query at a time (estable:204-272 restated per query, for
+    shapes where the sorted-window form above would not fit in memory). ids (B, L, T): the bucket ids; queries
+    (nq, 2) int64: (b, t) pairs. A query's candidates in table tau are the <= C most recent earlier positions with
+    its bucket (the set the sorted window nucleo:809-812 keeps), found from a stable sort of each (b, tau) row.
+    Returns salida (nq, d) summed over tables and the per-table signals (nq, T, 3) = (hay, valid max, max weight);
+    autograd reaches every input through the gathers."""
+    B, L, P = phi.shape
+    T, C, cf, K = sh.T, sh.C, sh.cf, sh.K
+    ids = np.asarray(ids)
+    qb, qt = queries[:, 0].numpy(), queries[:, 1].numpy()
+    nq = len(qb)
+    pos = np.zeros((nq, T, C), dtype=np.int64)
+    valid = np.zeros((nq, T, C), dtype=bool)
+    for b in np.unique(qb):
+        sel = np.nonzero(qb == b)[0]
+        for tau in range(T):
+            row = ids[b, :, tau]
+            order = np.argsort(row, kind='stable')
+            rank = np.empty(L, dtype=np.int64)
+            rank[order] = np.arange(L)
+            s = rank[qt[sel]]
+            idx = s[:, None] - np.arange(1, C + 1)[None, :]              # the C sorted ranks before the query's
+            ok = (idx >= 0) & (row[order[np.clip(idx, 0, L - 1)]] == row[qt[sel]][:, None])
+            pos[sel, tau] = np.where(ok, order[np.clip(idx, 0, L - 1)], 0)
+            valid[sel, tau] = ok
+    bq = torch.from_numpy(qb)
+    tq = torch.from_numpy(qt)
+    pk = torch.from_numpy(pos)
+    vk = torch.from_numpy(valid)
+    bk = bq.view(nq, 1, 1).expand_as(pk)
+    Pf = previous(sig, K)
+    sc = (phi[bq, tq].unsqueeze(1).unsqueeze(1) * phi[bk, pk]).sum(-1) / math.sqrt(P)
+    sc = sc + (Qc[bq, tq].unsqueeze(1).unsqueeze(1) * Kc[bk, pk]).sum(-1) * cf ** -0.5
+    ell = suffix_len(Pf[bq, tq].unsqueeze(1).unsqueeze(1), Pf[bk, pk])
+    sc = sc + w_suf[ell]
+    dt = (Bt[bk, pk] - Bt[bq, tq].view(nq, 1, 1)).to(torch.float32)
+    sc = sc + log_alfa[bk, pk] + dt * (gamma / C).view(1, T, 1)
+    hay = vk.any(-1, keepdim=True)
+    mx = sc.detach().masked_fill(~vk, float('-inf')).amax(-1, keepdim=True)
+    ref = torch.where(hay, mx, torch.zeros_like(mx))
+    att = torch.softmax((sc - ref).masked_fill(~vk, PROHIBIDO), dim=-1) * hay
+    salida = (att.unsqueeze(-1) * V[bk, pk]).sum(2).sum(1)
+    sen = torch.cat([hay.float(), torch.where(hay, mx, torch.full_like(mx, PROHIBIDO)).float(),
+                     att.detach().amax(-1, keepdim=True).float()], dim=-1)
     return salida, sen
 
 
@@ -365,14 +433,16 @@ def combine(p, acc, h, sh, prot):
     if prot.mejor_max is not None:
         mejor = mejor.clamp(-prot.mejor_max, prot.mejor_max)
     sen = torch.cat([pt / sh.T, mejor, acc['pico'] / pt.clamp(min=1), acc['peso_ctx'].detach() / sh.Tc], dim=-1)
-    logit = F.linear(h, p['g.weight'], p['g.bias'])
-    logit = logit + F.linear(sen, p['g_conf.weight'], p['g_conf.bias'])
+    with torch.autocast(device_type='cpu', enabled=False):
+        logit = F.linear(h, p['g.weight'].to(h.dtype), p['g.bias'].to(h.dtype))
+    logit = logit + F.linear(sen, p['g_conf.weight'], p['g_conf.bias']).to(logit.dtype)
     logit = logit + (acc['vistos'] * p['w_vistos']).sum(-1, keepdim=True)
     logit = logit + (torch.log1p(acc['hawkes']) * p['u_hawkes']).sum(-1, keepdim=True)
     logit = logit + streak_response(p, acc['racha'], sh).unsqueeze(-1)
     if prot.tope_puerta is not None:
         logit = prot.tope_puerta * torch.tanh(logit / prot.tope_puerta)
-    return h + torch.sigmoid(logit) * F.linear(salida, p['o.weight'])
+    aporte = F.linear(salida, p['o.weight'])
+    return h + torch.sigmoid(logit).to(aporte.dtype) * aporte
 
 
 def layer_forward(p, E, h, x, sh, prot=Prot()):

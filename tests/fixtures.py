@@ -8,8 +8,15 @@ from safetensors import safe_open
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden')
 
 
-def names():
-    return sorted(os.path.basename(f)[:-len('.safetensors')] for f in glob.glob(os.path.join(GOLDEN, '*.safetensors')))
+def names(autocast=None):
+    """Fixture names; autocast=None: all, False: the fp32 ones, 'bf16': those written under bf16 autocast."""
+    out = []
+    for f in sorted(glob.glob(os.path.join(GOLDEN, '*.safetensors'))):
+        with safe_open(f, framework='pt') as fh:
+            mode = json.loads(fh.metadata()['extra']).get('autocast', False)
+        if autocast is None or mode == autocast:
+            out.append(os.path.basename(f)[:-len('.safetensors')])
+    return out
 
 
 def load(name):
@@ -30,3 +37,29 @@ def shape_of(params, meta):
     if 'chunk' in kw:
         extra['C'] = kw['chunk']
     return shape_from_params(params, meta['d'], n_bits=kw.get('n_bits', 14), **extra)
+
+
+def prot(meta):
+    """The oracle's protections for a fixture: group A, plus group B (estable:72-77) for a 'textos_largos' case."""
+    from oracle.layer import Prot
+    if meta['extra'].get('prot') == 'textos_largos':
+        return Prot(tope_puerta=10.0, kappa_min=1.0 / (4 * meta['extra']['largo']))
+    return Prot()
+
+
+def protecciones(meta):
+    """The HIP layer's Protecciones for a fixture (the same choice as prot)."""
+    from asrn_amd.capa import Protecciones
+    if meta['extra'].get('prot') == 'textos_largos':
+        return Protecciones.textos_largos(meta['extra']['largo'])
+    return Protecciones()
+
+
+def cpu_autocast(meta):
+    """torch.autocast('cpu', bfloat16) for a fixture written under it, else a no-op context."""
+    import contextlib
+
+    import torch
+    if meta['extra'].get('autocast') == 'bf16':
+        return torch.autocast('cpu', dtype=torch.bfloat16)
+    return contextlib.nullcontext()

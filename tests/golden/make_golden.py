@@ -7,7 +7,7 @@ repetition stage (estable:304-321) with the reference's own rounding order. Each
 inputs, the layer's state_dict, every intermediate the hot path produces and the gradients. Nothing from the
 reference itself is stored.
 
-Run from the repository root:  python tests/golden/make_golden.py /root/reference
+Run from the repository root:  python tests/golden/make_golden.py /root/reference [case names...]
 """
 import json
 import os
@@ -29,17 +29,29 @@ CASES = [
     ('f_gamma_huge', dict(chunk=16, n_bits=3), 32, 1, 96, 7, {'gamma_fill': 1e9}),
     ('g_default_V6_L300', dict(), 32, 2, 300, 6, {}),
     ('h_streak_exact', dict(chunk=16, n_bits=4), 32, 2, 120, 5, {'kappa_r_zero': True}),
+    # group-B protections (estable:72-77): the gate's tanh cap (logits pushed well past it) and the kappa floor
+    # (two Hawkes rates and the streak rate pushed below it)
+    ('i_textos_largos', dict(chunk=16, n_bits=4), 32, 2, 120, 12, {'prot': 'textos_largos', 'largo': 1024}),
+    # bf16 autocast on the CPU (the reference's own bf16 case, tests/test_nucleo.py:476: d 64, default tables,
+    # B 2, L 160): the layer and its stages under torch.autocast('cpu', bfloat16), and the fp32 layer beside it
+    ('j_bf16_d64_L160', dict(), 64, 2, 160, 12, {'autocast': 'bf16'}),
 ]
 
 
-def build(ref_root):
+def build(ref_root, only=()):
     sys.path.insert(0, ref_root)
+    os.environ['ASRN_TRITON'] = '0'             # the reference's PyTorch path (the CPU has no Triton kernels anyway)
+    import contextlib
+
     import asrn.estable as est
     import asrn.nucleo as v89
 
     for name, kw, d, B, L, V, extra in CASES:
+        if only and name not in only:
+            continue
         torch.manual_seed(0)
-        capa = est.CapaASRNEstable(d, **kw)
+        prot = est.Protecciones.textos_largos(extra['largo']) if extra.get('prot') == 'textos_largos' else None
+        capa = est.CapaASRNEstable(d, protecciones=prot, **kw)
         with torch.no_grad():
             g = torch.Generator().manual_seed(1)
             for n, p in capa.named_parameters():
@@ -51,6 +63,12 @@ def build(ref_root):
                 capa.gamma.fill_(extra['gamma_fill'])
             if extra.get('kappa_r_zero'):
                 capa.log_kappa_racha.fill_(-200.0)
+            if extra.get('prot') == 'textos_largos':
+                capa.g.weight.mul_(100.0)
+                capa.log_kappa[2:] = -12.0
+                capa.log_kappa_racha.fill_(-12.0)
+        bf16 = extra.get('autocast') == 'bf16'
+        autocast = (lambda: torch.autocast('cpu', dtype=torch.bfloat16)) if bf16 else contextlib.nullcontext
         gx = torch.Generator().manual_seed(2)
         x = torch.randint(0, V, (B, L), generator=gx)
         x[:, L // 2:L // 2 + L // 4] = x[:, :L // 4].clone()
@@ -61,20 +79,22 @@ def build(ref_root):
         for k, v in capa.state_dict().items():
             out['p.' + k] = v.clone()
 
-        # whole layer forward + backward
-        E, h = E0.clone().requires_grad_(), h0.clone().requires_grad_()
-        capa.zero_grad()
-        y = capa(E, h, x)
-        (y * gy).sum().backward()
-        out['y'] = y.detach()
-        out['gE'] = E.grad
-        out['gh'] = h.grad
-        for n, p in capa.named_parameters():
-            if p.grad is not None:
-                out['g.' + n] = p.grad.clone()
+        # whole layer forward + backward (under autocast for a bf16 case, and then also in fp32 with suffix 32)
+        for suffix, ctx in (('', autocast),) + ((('32', contextlib.nullcontext),) if bf16 else ()):
+            E, h = E0.clone().requires_grad_(), h0.clone().requires_grad_()
+            capa.zero_grad()
+            with ctx():
+                y = capa(E, h, x)
+            (y.float() * gy).sum().backward()
+            out['y' + suffix] = y.detach().float()
+            out['gE' + suffix] = E.grad
+            out['gh' + suffix] = h.grad
+            for n, p in capa.named_parameters():
+                if p.grad is not None:
+                    out['g' + suffix + '.' + n] = p.grad.clone()
 
         # stage outputs, forward only
-        with torch.no_grad():
+        with torch.no_grad(), autocast():
             sig = v89.firmas_de_piezas(x)
             Qc, Kc, beta, la = capa._contexto(h0)
             Bt = beta.cumsum(1)
@@ -93,10 +113,11 @@ def build(ref_root):
         orig = capa._phi_y_valores
         capa._phi_y_valores = lambda _E: (leaves['phi'], leaves['V'])
         capa.zero_grad()
-        acc = capa._acumular(E0, leaves['Qc'], leaves['Kc'], leaves['Bt'], leaves['log_alfa'], sig)
+        with autocast():
+            acc = capa._acumular(E0, leaves['Qc'], leaves['Kc'], leaves['Bt'], leaves['log_alfa'], sig)
         capa._phi_y_valores = orig
         gs = torch.randn(B, L, d, generator=torch.Generator().manual_seed(4))
-        (acc['salida'] * gs).sum().backward()
+        (acc['salida'].float() * gs).sum().backward()
         out['acc.gs'] = gs
         for k in ('salida', 'peso_total', 'mejor', 'pico', 'peso_ctx'):
             out['acc.' + k] = acc[k].detach()
@@ -128,4 +149,4 @@ def build(ref_root):
 
 
 if __name__ == '__main__':
-    build(sys.argv[1] if len(sys.argv) > 1 else '/root/reference')
+    build(sys.argv[1] if len(sys.argv) > 1 else '/root/reference', tuple(sys.argv[2:]))

@@ -221,13 +221,19 @@ def test_writer_equals_whole_text(B, L0, n, kw):
     assert esc.cap >= L0 + n
 
 
+# the generation step's fallback branch (not asrn_decode_produce): widths past the fused producer's limits
+FALLBACK = [dict(confirmar=80), dict(afin_oculto=256)]
+
+
 @pytest.mark.parametrize('ajeno', [True, False])
-@pytest.mark.parametrize('B,L0,n,kw', [(2, 40, 30, SMALL), (1, 2, 12, SMALL), (2, 100, 20, {})])
+@pytest.mark.parametrize('B,L0,n,kw', [(2, 40, 30, SMALL), (1, 2, 12, SMALL), (2, 100, 20, {}),
+                                       (2, 60, 16, FALLBACK[0]), (2, 60, 16, FALLBACK[1])])
 def test_writer_vs_oracle(B, L0, n, kw, ajeno):
     say('writer vs oracle', B, L0, n, kw, ajeno)
     d = 32
     torch.manual_seed(1)
     layer = synth.move_params(CapaASRNEstable(d, **kw), 1).to(DEV)
+    assert ops.decode_produce_ok(layer, torch.zeros(B, d, device=DEV)) == (kw not in FALLBACK)
     p = {k: v.detach().cpu() for k, v in layer.state_dict().items()}
     sh = O.shape_from_params(p, d, n_bits=layer.n_bits, C=layer.chunk)
     x, E, h = synth.layer_inputs(B, L0 + n, d, 10, seed=5, frac=0.4, span=(3, 8))
@@ -240,22 +246,30 @@ def test_writer_vs_oracle(B, L0, n, kw, ajeno):
 
 
 @pytest.mark.parametrize('ajeno', [True, False])
-@pytest.mark.parametrize('B,L0,n,cap,kw', [(2, 40, 30, 45, SMALL), (3, 300, 24, 0, {}), (1, 2, 20, 4, SMALL)])
-def test_writer_graph_equals_eager(B, L0, n, cap, kw, ajeno):
-    """The step captured in a HIP graph and replayed (the position in a device counter that the kernels read and the
-    graph advances; a capacity doubling captures again) writes the same outputs, caches, rings, counts and streak as
-    the step launched op by op, bit for bit, step after step."""
-    say('writer graph = eager', B, L0, n, cap, kw, ajeno)
+@pytest.mark.parametrize('B,L0,n,cap,kw,bf16', [(2, 40, 30, 45, SMALL, False), (3, 300, 24, 0, {}, False),
+                                                (1, 2, 20, 4, SMALL, False), (2, 60, 20, 70, FALLBACK[0], False),
+                                                (2, 60, 20, 0, FALLBACK[1], False), (2, 60, 20, 70, {}, True)])
+def test_writer_graph_equals_eager(B, L0, n, cap, kw, bf16, ajeno):
+    """The step captured in a HIP graph and replayed (its position copied before each replay, with its inputs, from
+    a device table of positions into the buffer the kernels read; a capacity doubling captures again) writes the
+    same outputs, caches, rings, counts and streak as the step launched op by op, bit for bit, step after step. The
+    FALLBACK widths and bf16 autocast take the step's PyTorch-producer branch, whose cache rows are written with
+    index_copy_ at the device-held position."""
+    say('writer graph = eager', B, L0, n, cap, kw, bf16, ajeno)
     d = 32
     torch.manual_seed(2)
     layer = synth.move_params(CapaASRNEstable(d, **kw), 2).to(DEV)
     x, E, h = synth.layer_inputs(B, L0 + n, d, 9, seed=7, frac=0.4, span=(3, 8))
     Ed, hd, xd = E.to(DEV), h.to(DEV), x.to(DEV)
+    with torch.autocast('cuda', dtype=torch.bfloat16, enabled=bf16):
+        ok = ops.decode_produce_ok(layer, Ed[:, 0])
+    assert ok == (kw not in FALLBACK and not bf16)
     outs = []
     for grafo in (False, True):
         esc = EscritorCapa(layer, memoria_de_lo_ajeno=ajeno, grafo=grafo)
-        esc.inicio(Ed[:, :L0], hd[:, :L0], xd[:, :L0], capacidad=cap)
-        ys = [esc.paso(Ed[:, t], hd[:, t], xd[:, t]) for t in range(L0, L0 + n)]
+        with torch.autocast('cuda', dtype=torch.bfloat16, enabled=bf16):
+            esc.inicio(Ed[:, :L0], hd[:, :L0], xd[:, :L0], capacidad=cap)
+            ys = [esc.paso(Ed[:, t], hd[:, t], xd[:, t]) for t in range(L0, L0 + n)]
         torch.cuda.synchronize()
         outs.append((torch.stack(ys, 1), esc))
     (ye, ee), (yg, eg) = outs

@@ -182,6 +182,10 @@ def test_parameters_and_construction_order_match_the_reference(name):
             layer.gamma.fill_(m['extra']['gamma_fill'])
         if m['extra'].get('kappa_r_zero'):
             layer.log_kappa_racha.fill_(-200.0)
+        if m['extra'].get('prot') == 'textos_largos':
+            layer.g.weight.mul_(100.0)
+            layer.log_kappa[2:] = -12.0
+            layer.log_kappa_racha.fill_(-12.0)
     sd = layer.state_dict()
     assert sorted(sd) == sorted(p)              # (safetensors stores keys sorted)
     for k in sd:

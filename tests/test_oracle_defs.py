@@ -1,0 +1,180 @@
+"""Pins the oracle's per-query candidate restatement (oracle.layer.candidates_at) against the golden fixtures and
+against the sorted-window form (oracle.layer.candidates), which the fixtures pin, forward and gradients; a planted
+mistake (one candidate too many per table) must fail."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import layer as O
+from tests import fixtures
+
+
+def all_queries(B, L):
+    return torch.stack(torch.meshgrid(torch.arange(B), torch.arange(L), indexing='ij'), -1).reshape(-1, 2)
+
+
+@pytest.mark.parametrize('name', fixtures.names(False))
+def test_candidates_at_equals_golden(name):
+    g, p, m = fixtures.load(name)
+    sh = fixtures.shape_of(p, m)
+    B, L = g['x'].shape
+    ids = O.bucket_ids(g['phi'], sh.T, sh.nb).numpy()
+    salida, sen = O.candidates_at(g['phi'], g['V'], g['Qc'], g['Kc'], g['Bt'], g['log_alfa'], g['sig'],
+                                  p['w_sufijo'], p['gamma'], sh, ids, all_queries(B, L))
+    ref = g['acc.salida'].reshape(B * L, -1)
+    assert (salida - ref).abs().max() <= 1e-5 * (ref.abs().max() + 1e-6)
+    assert torch.equal(sen[:, :, 0].sum(1).view(B, L, 1), g['acc.peso_total'])
+
+
+@pytest.mark.parametrize('B,L,T,nb,C,V', [(2, 300, 8, 3, 16, 5), (1, 200, 4, 2, 4, 3), (3, 97, 8, 14, 32, 4)])
+def test_candidates_at_equals_sorted_windows(B, L, T, nb, C, V):
+    gen = torch.Generator().manual_seed(L)
+    sh = O.Shape(d=24, T=T, nb=nb, C=C, Tc=T // 2, cf=8, K=4)
+    x = torch.randint(0, V, (B, L), generator=gen)
+    st = dict(phi=torch.randn(B, L, sh.P, generator=gen), V=torch.randn(B, L, sh.d, generator=gen),
+              Qc=torch.randn(B, L, sh.cf, generator=gen), Kc=torch.randn(B, L, sh.cf, generator=gen),
+              Bt=(torch.rand(B, L, generator=gen, dtype=torch.float64) * 2).cumsum(1),
+              log_alfa=torch.randn(B, L, generator=gen) * 0.3)
+    w = torch.randn(sh.K + 1, generator=gen)
+    gam = torch.rand(T, generator=gen) * 3
+    gs = torch.randn(B, L, sh.d, generator=gen)
+    sig = x.float()
+    ids = O.bucket_ids(st['phi'], T, nb).numpy()
+
+    def run(fn):
+        lv = {k: v.clone().requires_grad_() for k, v in st.items()}
+        wl, gl = w.clone().requires_grad_(), gam.clone().requires_grad_()
+        if fn == 'windows':
+            sal, sen = O.candidates(lv['phi'], lv['V'], lv['Qc'], lv['Kc'], lv['Bt'], lv['log_alfa'], sig, wl, gl, sh)
+            sen = sen.permute(0, 2, 1, 3).reshape(B * L, T, 3)
+        else:
+            sal, sen = O.candidates_at(lv['phi'], lv['V'], lv['Qc'], lv['Kc'], lv['Bt'], lv['log_alfa'], sig, wl, gl,
+                                       sh, ids, all_queries(B, L))
+        sal = sal.reshape(B, L, -1)
+        (sal * gs).sum().backward()
+        return sal.detach(), sen, {**{k: t.grad for k, t in lv.items()}, 'w': wl.grad, 'gamma': gl.grad}
+
+    a, b = run('windows'), run('per query')
+    assert (a[0] - b[0]).abs().max() <= 1e-5 * a[0].abs().max()
+    assert torch.equal(a[1][..., 0], b[1][..., 0])
+    assert (a[1] - b[1]).abs().max() <= 1e-5 * a[1].abs().max()
+    for k in a[2]:
+        assert (a[2][k] - b[2][k]).abs().max() <= 1e-4 * (a[2][k].abs().max() + 1e-6), k
+
+
+def test_candidates_at_planted_extra_candidate_fails():
+    """C + 1 candidates per table instead of C changes the output: the comparisons above can see a window off by
+    one."""
+    gen = torch.Generator().manual_seed(0)
+    B, L = 1, 200
+    sh = O.Shape(d=16, T=4, nb=1, C=4, Tc=2, cf=4, K=2)
+    wide = O.Shape(d=16, T=4, nb=1, C=5, Tc=2, cf=4, K=2)
+    st = [torch.randn(B, L, sh.P, generator=gen), torch.randn(B, L, 16, generator=gen),
+          torch.randn(B, L, 4, generator=gen), torch.randn(B, L, 4, generator=gen),
+          torch.arange(L, dtype=torch.float64).view(1, L), torch.zeros(B, L)]
+    sig = torch.randint(0, 3, (B, L), generator=gen).float()
+    w, gam = torch.zeros(3), torch.zeros(4)
+    ids = O.bucket_ids(st[0], 4, 1).numpy()
+    q = all_queries(B, L)
+    a, _ = O.candidates_at(*st, sig, w, gam, sh, ids, q)
+    b, _ = O.candidates_at(*st, sig, w, gam, wide, ids, q)
+    ref, _ = O.candidates(*st, sig, w, gam, sh)
+    assert (a - ref.reshape(B * L, -1)).abs().max() <= 1e-5
+    assert (b - ref.reshape(B * L, -1)).abs().max() > 1e-2
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# definitions that pin the small pieces of the oracle
+# ---------------------------------------------------------------------------------------------------------------------
+
+def test_ngram_keys_equal_python_float_loop():
+    """k_j = (((0 + s_t c_0) + s_{t-1} c_1) + ...) with every multiply and add rounded on its own (nucleo:175-185):
+    Python floats round each operation, so a plain loop is the definition. A single rounding of the exact sum
+    (fractions) differs for some keys, so the comparison can tell the two apart."""
+    from fractions import Fraction
+    gen = torch.Generator().manual_seed(0)
+    B, L, n, V = 2, 400, 4, 50304
+    sig = torch.randint(0, V, (B, L), generator=gen).float()
+    c = torch.rand(n, generator=torch.Generator().manual_seed(12345), dtype=torch.float64) + 0.5
+    keys = O.ngram_keys(sig, c, n)
+    cl = c.tolist()
+    once_rounded_differs = 0
+    for b in range(B):
+        s = sig[b].tolist()
+        for t in range(L):
+            k = 0.0
+            exact = Fraction(0)
+            for j in range(n):
+                if t - j < 0:
+                    assert all(np.isnan(keys[b, t, jj].item()) for jj in range(j, n))
+                    break
+                k = k + s[t - j] * cl[j]
+                exact += Fraction(s[t - j]) * Fraction(cl[j])
+                assert keys[b, t, j].item() == k, (b, t, j)
+                once_rounded_differs += float(exact) != k
+    assert once_rounded_differs > 0
+
+
+def test_hawkes_equals_quadratic_sum_and_streak_recurrence():
+    """lambda at an occurrence of a key = sum over its earlier occurrences u of alfa_u exp(-kappa (B_t - B_u)) (the
+    O(N^2) sum the scan telescopes, tests/test_nucleo.py:287-306); the streak rho_t = v_t (exp(-kappa_r beta_t)
+    rho_{t-1} + 1) with v the seen flag of the longest group (tests/test_nucleo.py:307-312)."""
+    gen = torch.Generator().manual_seed(1)
+    B, L, n = 2, 150, 4
+    sh = O.Shape(d=8, n=n)
+    x = torch.randint(0, 4, (B, L), generator=gen)
+    sig = x.float()
+    beta = (torch.rand(B, L, generator=gen, dtype=torch.float64) * 0.5)
+    Bt = beta.cumsum(1)
+    la = torch.randn(B, L, generator=gen) * 0.3
+    p = {'log_kappa': torch.log(torch.tensor([0.3, 0.1, 0.05, 0.02])), 'log_kappa_racha': torch.log(torch.tensor([0.2])),
+         'c_vistos': torch.rand(n, generator=torch.Generator().manual_seed(12345), dtype=torch.float64) + 0.5}
+    r = O.repetition(p, sig, beta, Bt, la, sh, O.Prot())
+    keys = O.ngram_keys(sig, p['c_vistos'], n)
+    kappa = p['log_kappa'].exp().double()
+    for b in range(B):
+        for j in range(n):
+            for t in range(L):
+                kt = keys[b, t, j].item()
+                earlier = [u for u in range(t) if keys[b, u, j].item() == kt]
+                ref = sum(math.exp(la[b, u].item()) * math.exp(-kappa[j].item() * (Bt[b, t] - Bt[b, u]).item())
+                          for u in earlier)
+                assert abs(r['hawkes'][b, t, j].item() - ref) <= 1e-5 * max(1.0, ref), (b, j, t)
+                assert r['vistos'][b, t, j].item() == float(bool(earlier))
+        rho = 0.0
+        kr = p['log_kappa_racha'].exp().item()
+        for t in range(L):
+            v = r['vistos'][b, t, n - 1].item()
+            rho = v * (math.exp(-kr * beta[b, t].item()) * rho + 1.0)
+            assert abs(r['racha'][b, t].item() - rho) <= 1e-5 * max(1.0, rho)
+
+
+def test_scan_equals_loop_with_gradients():
+    """S_i = a_i S_{i-1} + b_i and its gradients against autograd through a plain loop (nucleo:188-196)."""
+    gen = torch.Generator().manual_seed(2)
+    a = torch.rand(3, 77, generator=gen)
+    b = torch.randn(3, 77, generator=gen)
+    g = torch.randn(3, 77, generator=gen)
+    a1, b1 = a.clone().requires_grad_(), b.clone().requires_grad_()
+    S = O.scan(a1, b1)
+    (S * g).sum().backward()
+    a2, b2 = a.double().requires_grad_(), b.double().requires_grad_()
+    acc, outs = torch.zeros(3, dtype=torch.float64), []
+    for i in range(77):
+        acc = a2[:, i] * acc + b2[:, i]
+        outs.append(acc)
+    S2 = torch.stack(outs, 1)
+    (S2 * g.double()).sum().backward()
+    assert (S.double() - S2).abs().max() <= 1e-5 * S2.abs().max()
+    assert (a1.grad.double() - a2.grad).abs().max() <= 1e-5 * a2.grad.abs().max()
+    assert (b1.grad.double() - b2.grad).abs().max() <= 1e-5 * b2.grad.abs().max()
+
+
+def test_suffix_len_definition():
+    """Leading run of equal entries; NaN never matches (nucleo:98-108)."""
+    nan = float('nan')
+    a = torch.tensor([[1., 2., 3., 4.], [1., 2., 3., 4.], [nan, 2., 3., 4.], [1., 2., nan, 4.], [5., 2., 3., 4.]])
+    b = torch.tensor([[1., 2., 3., 4.], [1., 2., 9., 4.], [nan, 2., 3., 4.], [1., 2., nan, 4.], [1., 2., 3., 4.]])
+    assert O.suffix_len(a, b).tolist() == [4, 2, 0, 2, 0]

@@ -30,12 +30,18 @@ def test_bucket_ids_and_order_bit_exact(name):
 
 @pytest.mark.parametrize('name', CASES)
 def test_producers(name):
+    """phi, V, Qc, Kc, beta and log_alfa; a bf16 fixture runs the oracle under CPU autocast, where Qc/Kc come from
+    the 16-bit LayerNorm output and the clock projection stays fp32 (estable:176-180): every output keeps the
+    reference's dtype."""
     g, p, m = fixtures.load(name)
     sh = fixtures.shape_of(p, m)
-    phi, V = O.phi_and_values(p, g['E'])
+    with fixtures.cpu_autocast(m):
+        phi, V = O.phi_and_values(p, g['E'])
+        Qc, Kc, beta, la = O.context(p, g['h'], sh, fixtures.prot(m))
     close(phi, g['phi'], 1e-6, 'phi')
     close(V, g['V'], 1e-6, 'V')
-    Qc, Kc, beta, la = O.context(p, g['h'], sh, O.Prot())
+    for a, k in ((phi, 'phi'), (V, 'V'), (Qc, 'Qc'), (Kc, 'Kc'), (beta, 'beta'), (la, 'log_alfa')):
+        assert a.dtype == g[k].dtype, (k, a.dtype, g[k].dtype)
     for a, k in ((Qc, 'Qc'), (Kc, 'Kc'), (beta, 'beta'), (la, 'log_alfa')):
         close(a, g[k], 1e-6, k)
     assert beta.dtype == torch.float64
@@ -48,15 +54,17 @@ def test_candidate_stage_forward_and_gradients(name):
     leaves = {k: g[k].clone().requires_grad_() for k in ('phi', 'V', 'Qc', 'Kc', 'Bt', 'log_alfa')}
     w = p['w_sufijo'].clone().requires_grad_()
     gam = p['gamma'].clone().requires_grad_()
-    salida, sen = O.candidates(leaves['phi'], leaves['V'], leaves['Qc'], leaves['Kc'], leaves['Bt'],
-                               leaves['log_alfa'], g['sig'], w, gam, sh)
-    acc = O.gate_signals(salida, sen, sh.T, sh.Tc)
+    with fixtures.cpu_autocast(m):
+        salida, sen = O.candidates(leaves['phi'], leaves['V'], leaves['Qc'], leaves['Kc'], leaves['Bt'],
+                                   leaves['log_alfa'], g['sig'], w, gam, sh)
+        acc = O.gate_signals(salida, sen, sh.T, sh.Tc)
+    assert salida.dtype == g['acc.salida'].dtype
     for k in ('salida', 'pico'):
         close(acc[k], g['acc.' + k], 1e-5, k)
     for k in ('peso_total', 'peso_ctx'):
         assert torch.equal(acc[k], g['acc.' + k]), k
     close(acc['mejor'], g['acc.mejor'], 1e-5, 'mejor')
-    (salida * g['acc.gs']).sum().backward()
+    (salida.float() * g['acc.gs']).sum().backward()
     for k, t in leaves.items():
         close(t.grad, g['acc.g_' + k], 1e-4, 'grad ' + k)
     close(w.grad, g['acc.g_w_sufijo'], 1e-4, 'grad w_sufijo')
@@ -84,7 +92,7 @@ def test_repetition_stage_forward_and_gradients(name):
     pp = dict(p)
     pp['log_kappa'] = p['log_kappa'].clone().requires_grad_()
     pp['log_kappa_racha'] = p['log_kappa_racha'].clone().requires_grad_()
-    r = O.repetition(pp, g['sig'], rl['beta'], rl['Bt'], rl['log_alfa'], sh, O.Prot())
+    r = O.repetition(pp, g['sig'], rl['beta'], rl['Bt'], rl['log_alfa'], sh, fixtures.prot(m))
     assert torch.equal(r['vistos'], g['rep.vistos'])
     if 'corrimiento' not in m['extra']:                          # with huge clock steps exp(-kappa dB) underflows
         assert torch.equal(r['hawkes'] > 0, g['rep.vistos'] > 0)
@@ -107,7 +115,9 @@ def test_whole_layer_forward_and_gradients(name):
     pp = {k: (v.clone().requires_grad_() if v.is_floating_point() and not k.startswith(('pot', 'c_vistos', 'r_firma'))
               else v) for k, v in p.items()}
     E, h = g['E'].clone().requires_grad_(), g['h'].clone().requires_grad_()
-    y = O.layer_forward(pp, E, h, g['x'], sh)
+    with fixtures.cpu_autocast(m):
+        y = O.layer_forward(pp, E, h, g['x'], sh, fixtures.prot(m))
+    assert y.dtype == torch.float32
     close(y, g['y'], 1e-5, 'y')
     (y * g['gy']).sum().backward()
     close(E.grad, g['gE'], 1e-4, 'grad E')
