@@ -173,11 +173,21 @@ class CapaASRNEstable(nn.Module):
         if (E.dtype == torch.float32 and not torch.is_autocast_enabled(E.device.type) and m % 4 == 0
                 and mc % 4 == 0 and W.dtype == torch.float32):
             g, filas = ops.Producer.apply(E, W, pal[0].bias, ctx[0].bias, m, mc)
+        elif torch.is_autocast_enabled(E.device.type):
+            # 16-bit: the reference's own products (nucleo:644-659): the word MLP's first layer on E, and the context
+            # MLP's on the key [E_t; E_{t-1}] built from the 16-bit E, each rounded once. Split by linearity, the
+            # context layer would round W_a E_t and W_b E_{t-1} apart: one 16-bit rounding more, which moves phi
+            # values near 0 to the other sign and their positions to other buckets than the reference's
+            E16 = _a_autocast(E)
+            llave = torch.cat([E16, F.pad(E16, (0, 0, 1, 0))[:, :E16.shape[1]]], dim=-1)
+            g = F.gelu(torch.cat([lineal(E16, pal[0].weight, pal[0].bias), lineal(llave, ctx[0].weight, ctx[0].bias)],
+                                 dim=-1))
+            filas = E16
         else:
-            y = lineal(_a_autocast(E), W, F.pad(pal[0].bias, (0, 2 * mc)))
+            y = lineal(E, W, F.pad(pal[0].bias, (0, 2 * mc)))
             hp, za, zb = y.split([m, mc, mc], dim=-1)
             g = F.gelu(torch.cat([hp, _ShiftAdd.apply(za, zb, ctx[0].bias)], dim=-1))
-            filas = _a_autocast(E)
+            filas = E
         phi = lineal(g, W2, b2)
         return phi, filas
 
