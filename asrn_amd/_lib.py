@@ -33,6 +33,8 @@ SIGNATURES = {
     'asrn_ngram_sort': (ctypes.c_int, [_P, _P, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _I64, _P]),
     'asrn_scan_fwd': (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _I64, _P]),
     'asrn_scan_bwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _P, _I64, _P]),
+    'asrn_scan_static_scratch_bytes': (_I64, []),
+    'asrn_scan_fwd_static': (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P]),
     'asrn_hawkes_fwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P, _I64, _P]),
     'asrn_hawkes_bwd_workspace': (_I64, [_I64, _I64, _I32]),
     'asrn_hawkes_bwd': (ctypes.c_int, [_P] * 8 + [_I64, _I64, _I32] + [_P] * 4 + [_I64, _P]),

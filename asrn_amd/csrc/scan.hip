@@ -12,6 +12,8 @@
 // The backward recurrence l_i = g_i + a_{i+1} l_{i+1} is the same scan run from the right. A per-row reduction the
 // functor feeds (d kappa) is summed per chunk, and a third launch adds the chunk sums in a fixed order (deterministic;
 // no fences or atomics between workgroups, whose agent-scope release would write back and invalidate the L2).
+#include <mutex>
+
 #include "common.h"
 
 namespace asrn {
@@ -360,6 +362,8 @@ struct ClockOp {
 // ---- launch ---------------------------------------------------------------------------------------------------------
 constexpr int64_t kOneChunk = (int64_t)kScanThreads * 4;   // rows up to this length take one chunk and no workspace
 constexpr int64_t kAlign = 256;
+constexpr int64_t kScanStaticScratchBytes = int64_t(4) << 20;   // asrn_scan_fwd_static's chunk totals
+constexpr int kMaxScratchDevices = 64;
 
 static int64_t round_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
@@ -429,6 +433,50 @@ extern "C" int asrn_scan_fwd(const float* a, const float* b, float* S, int64_t r
   ASRN_REQUIRE(rows >= 0 && N >= 0, "asrn_scan_fwd: bad sizes");
   PlainFwd op{a, b, S, N};
   return launch_scan(op, rows, N, workspace, workspace_bytes, stream, "asrn_scan_fwd");
+}
+
+// ---- the affine scan without a caller workspace ------------------------------------------------------------------
+// The chunk totals go to a file-scope device array instead of a caller's workspace; every GPU the library runs on
+// holds its own copy until the process ends. On the host the array's name is only a stand-in: the device address
+// comes from hipGetSymbolAddress, taken once per device with that device current, and only that address is passed
+// to kernels. Every call on one GPU shares the array, so calls that overlap on one GPU (on different streams) race.
+static __device__ __align__(256) char scratch[kScanStaticScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_addr[kMaxScratchDevices] = {};
+
+static int scratch_address(void** out, const char* what) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail("%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  ASRN_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "%s: device %d beyond the %d the library tracks", what, dev,
+               kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev, hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return 0;
+}
+
+extern "C" int64_t asrn_scan_static_scratch_bytes(void) { return kScanStaticScratchBytes; }
+
+extern "C" int asrn_scan_fwd_static(const float* a, const float* b, float* S, int64_t rows, int64_t N, void* stream) {
+  const char* what = "asrn_scan_fwd_static";
+  ASRN_REQUIRE(rows >= 0 && N >= 0, "%s: bad sizes", what);
+  const int64_t need = asrn_scan_workspace(rows, N);
+  ASRN_REQUIRE(need >= 0 && need <= kScanStaticScratchBytes,
+               "%s: rows=%lld, N=%lld need %lld bytes of chunk totals, beyond the library's %lld-byte static scratch "
+               "(call asrn_scan_fwd with a workspace instead)", what, (long long)rows, (long long)N, (long long)need,
+               (long long)kScanStaticScratchBytes);
+  void* ws = nullptr;
+  if (need > 0 && scratch_address(&ws, what)) return 1;
+  PlainFwd op{a, b, S, N};
+  return launch_scan(op, rows, N, ws, need, stream, what);
 }
 
 extern "C" int asrn_scan_bwd(const float* a, const float* S, const float* g, float* ga, float* gb, int64_t rows,

@@ -216,6 +216,15 @@ int asrn_scan_fwd(const float* a, const float* b, float* S, int64_t rows, int64_
 int asrn_scan_bwd(const float* a, const float* S, const float* g, float* ga, float* gb, int64_t rows, int64_t N,
                   void* workspace, int64_t workspace_bytes, void* stream);
 
+/* asrn_scan_fwd with no workspace argument and no allocation: no counterpart in the reference. It is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The chunk totals live in a static device array of asrn_scan_static_scratch_bytes() bytes (4 MiB) per GPU, held
+ * until the process ends; sizes whose asrn_scan_workspace(rows, N) exceeds it are rejected with an error. Same
+ * kernels and results as asrn_scan_fwd. Every call on one GPU shares that array: calls that overlap on one GPU race
+ * (order them on one stream). */
+int64_t asrn_scan_static_scratch_bytes(void);
+int asrn_scan_fwd_static(const float* a, const float* b, float* S, int64_t rows, int64_t N, void* stream);
+
 /* ---- a11: Hawkes intensities in key order (asrn/estable.py:313-318) ---------------------------------------------
  * Per (b, j) row in key order: dB_i = fp32(max(0, Bt[o_i] - Bt[o_{i-1}])), a_i = repeated_i exp(-kappa_j dB_i),
  * lambda = scan(a, a * alfa_{i-1}) with alfa = exp(log_alfa); hawkes[b, o_i, j] = lambda_i.

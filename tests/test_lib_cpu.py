@@ -88,6 +88,10 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert lib.asrn_hawkes_bwd_workspace(8, 4096, 4) >= 2 * 8 * 4096 * 4 * 4 + lib.asrn_scan_workspace(32, 4096)
     assert lib.asrn_scan_fwd(N, N, N, 2, 4096, N, 0, N) != 0
     assert 'workspace' in _err(lib)
+    # the scan without a workspace: its static scratch is 4 MiB; larger scans are refused before any device work
+    assert lib.asrn_scan_static_scratch_bytes() == 4 << 20
+    assert lib.asrn_scan_fwd_static(N, N, N, 4096, 1 << 20, N) != 0
+    assert 'static scratch' in _err(lib)
     assert lib.asrn_streak_bwd(*([N] * 5), 2, 2048, 4, N, N, N, 1 << 20, N) != 0
     assert 'workspace' in _err(lib)
     # gate: row width, the small parameters' block, the workspace
