@@ -274,14 +274,23 @@ class CapaASRNEstable(nn.Module):
 
     # --- all together -----------------------------------------------------------------------------------------------
 
-    def forward(self, E, h, piezas=None):
-        """E (B, L, d), h (B, L, d), piezas (B, L) or None -> h' (B, L, d) (asrn/estable.py:407-421)."""
-        return self._adelante(E, h, piezas)
+    def forward(self, E, h, piezas=None, ngramas=None):
+        """E (B, L, d), h (B, L, d), piezas (B, L) or None -> h' (B, L, d) (asrn/estable.py:407-421).
 
-    def _adelante(self, E, h, piezas=None, partes=None):
+        ngramas: what `ngramas(piezas, capa)` returned for these token ids, to share one n-gram sort between every ASRN
+        layer of a model (it depends on the tokens only; the reference sorts again in each layer, nucleo:688-701).
+        Without it the layer sorts itself."""
+        return self._adelante(E, h, piezas, ngramas=ngramas)
+
+    def _adelante(self, E, h, piezas=None, partes=None, ngramas=None):
         """forward; with a dict `partes`, also keeps what the generation step starts from (the prompt's phi, V,
         Qc, Kc, sig, beta, Bt, log_alfa, n-gram keys and their sort, hawkes and racha)."""
         self._revisar(E)
+        if ngramas is not None:
+            if piezas is None:
+                raise ValueError('ngramas: the shared n-gram sort is for token ids (piezas); without them the '
+                                 'signatures come from E and differ per layer')
+            _revisar_ngramas(ngramas, piezas, self)
         # Two streams: the context producer (LayerNorm, Qc/Kc, the clock), the token signatures, W_o W_v and the
         # repetition branch (n-gram sort, Hawkes and streak scans: small, latency-bound kernels) run on the second
         # one, beside the hash producers and the bucket sort; the candidate attention waits for the context only.
@@ -299,8 +308,11 @@ class CapaASRNEstable(nn.Module):
             Bt = ops.ClockScan.apply(beta)
             contexto_listo = torch.cuda.Event()
             contexto_listo.record(lado)
-            with torch.no_grad():
-                ngram = ops.ngram_sort(sig, self.c_vistos, self.vistos)
+            if ngramas is None:
+                with torch.no_grad():
+                    ngram = ops.ngram_sort(sig, self.c_vistos, self.vistos)
+            else:
+                ngram = ngramas[1:]
             rep = self._repeticion(sig, beta, Bt, log_alfa, partes, ngram)
         if pesos is not None:
             pesos['Wq'].record_stream(lado)            # made here, used there: not reused before both are done
@@ -482,6 +494,26 @@ def _a_autocast(x):
 
 
 ASRNLayer = CapaASRNEstable
+
+
+@torch.no_grad()
+def ngramas(piezas, capa):
+    """The n-gram keys of token ids `piezas` (B, L), their stable sort per (b, j) row, the repeated flags, the ranks
+    and the seen flags, for every ASRN layer of a model at once: they depend on the tokens, on the buffer c_vistos
+    (the same constants in every layer, drawn from a fixed generator, nucleo:609-610) and on the group count n only.
+    Pass the result to each layer's forward(..., ngramas=...). Launched on the current stream."""
+    if not piezas.is_cuda:
+        raise RuntimeError('asrn_amd.ngramas runs on the GPU only')
+    return (piezas,) + tuple(ops.ngram_sort(firmas_de_piezas(piezas), capa.c_vistos, capa.vistos))
+
+
+def _revisar_ngramas(ng, piezas, capa):
+    """Checks that a shared n-gram sort was made for these tokens and this layer's group count and constants."""
+    src, claves = ng[0], ng[1]
+    if src is not piezas and not (src.shape == piezas.shape and src.data_ptr() == piezas.data_ptr()):
+        raise ValueError('ngramas: computed for other token ids than this call\'s piezas')
+    if claves.shape[-1] != capa.vistos:
+        raise ValueError(f'ngramas: {claves.shape[-1]} groups, this layer has vistos={capa.vistos}')
 
 
 def convertir(modelo, protecciones=None):

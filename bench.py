@@ -1,21 +1,25 @@
 """Benchmark of the ASRN layer hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--config cfg2] [--no-cpu-baseline] [--no-decode]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--config cfg2|cfg3] [--no-cpu-baseline] [--no-decode]
+                    [--decode-steps 1024] [--decode-layers 6] [--decode-only]
 
 A step is one forward + backward of one ASRN layer (asrn.ASRNLayer, group-A protections) over one batch of
-synthetic tokens: BASELINE.json configs[1] = cfg2, B 8, N 4096, d 256, V 256, fp32, 30% copied spans. Inputs and
+synthetic tokens: BASELINE.json configs[1] = cfg2, B 8, N 4096, d 256, V 256, fp32, 30% copied spans (--config cfg3:
+configs[2], B 4, N 65,536, d 512, V 32,000, Zipf tokens, bf16 autocast; run it with --no-decode). Inputs and
 weights are resident in HBM before the timed region. The step is captured once into a HIP graph and the timed steps
 are its replays (the same kernels, launched without the host's per-op overhead); --eager times Python-launched steps
 instead. The per-kernel device events (roofline, hip_aggregate, kernels) come from an eager pass of the same number of
 steps, since events recorded while capturing are not replayed. Prints one JSON line with the driver's keys plus:
   roofline      the dominant HIP kernel: algorithmic bytes per launch / its mean launch time (device events recorded
                 on the stream it runs on), against MI355X's 8 TB/s
-  hip_aggregate all HIP kernels: 25,552 B/token (cfg2) x tokens / (8 TB/s x their summed time per step)
+  hip_aggregate all HIP kernels: 25,552 B/token (cfg2) x tokens / (8 TB/s x their summed time per step), the time
+                from the committed rocprofv3 kernel trace (profiles/cfg2_kernel_times.json) where there is one
   layer         whole-layer tokens/s and its HBM fraction at 41,552 B/token (the HIP kernels' bytes plus the GEMMs'
                 operands and results, 16,000 B/token at cfg2)
-  decode        the O(1) generation step of one layer (BASELINE.json configs[4] at one layer): per-token latency
-                against the context, 1K to 64K, and its slope
-  cpu_baseline  the CPU oracle (oracle/layer.py, PyTorch on the host cores) on the same workload
+  decode        the O(1) generation step of configs[4]'s 6 ASRN layers (d 768, B 16): per-token latency over 1,024
+                steps against the context, 1K to 64K, and its slope
+  cpu_baseline  the CPU oracle (oracle/layer.py, PyTorch fp32 on the host cores) on the same workload (a bounded
+                sample of it for cfg3)
 """
 import argparse
 import copy
@@ -107,11 +111,31 @@ def measured_traffic(kernel):
         return None
 
 
-def cpu_baseline(layer_cpu, x, E, h, gy, reps=2):
-    """The CPU oracle's layer forward + backward on the same inputs (oracle/layer.py, PyTorch on all host cores)."""
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or '' where it cannot be read."""
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return ''
+
+
+def cpu_baseline(layer_cpu, x, E, h, gy, reps=3, max_tokens=32768):
+    """The CPU oracle's layer forward + backward (oracle/layer.py, PyTorch fp32 on all host cores), median of `reps`
+    after 1 warm-up, on the same inputs; workloads over `max_tokens` tokens are timed on a bounded sample (the first
+    rows, cut to at most max_tokens tokens in all) so that the run stays within about half a minute."""
     import torch
     from oracle import layer as O
     torch.set_num_threads(os.cpu_count() or 1)
+    B, N = x.shape
+    full = B * N <= max_tokens
+    if not full:
+        rows = max(1, max_tokens // N)
+        n = min(N, max_tokens // rows)
+        x, E, h, gy = x[:rows, :n], E[:rows, :n], h[:rows, :n], gy[:rows, :n]
     p = {k: (v.clone().requires_grad_() if v.is_floating_point() and k not in ('c_vistos', 'r_firma') else v.clone())
          for k, v in layer_cpu.state_dict().items()}
     sh = O.shape_from_params(p, E.shape[-1], n_bits=layer_cpu.n_bits, C=layer_cpu.chunk)
@@ -126,22 +150,41 @@ def cpu_baseline(layer_cpu, x, E, h, gy, reps=2):
             times.append(dt)
     t = statistics.median(times)
     tokens = x.numel()
+    what = (f'full workload ({x.shape[0]}x{x.shape[1]} tokens)' if full else
+            f'bounded sample: the first {x.shape[0]}x{x.shape[1]} tokens of the {B}x{N} workload')
     return {'value': round(tokens / t, 1), 'unit': 'tokens/s', 'cores': torch.get_num_threads(), 'kind': 'port',
-            'sample': f'full workload ({x.shape[0]}x{x.shape[1]} tokens), fp32, median of {reps} after 1 warm-up; '
-                      f'cpu_count={os.cpu_count()}',
-            'seconds_per_step': round(t, 3)}
+            'sample': f'{what}, fp32, median of {reps} after 1 warm-up; cpu_count={os.cpu_count()}',
+            'cpu_model': cpu_model(), 'seconds_per_step': round(t, 3)}
 
 
-DECODE = dict(B=16, d=768, V=50304, contexts=(1024, 4096, 16384, 32768, 65536), frac=0.2, span=(16, 256),
+KERNEL_TIMES_FILE = os.path.join(ROOT, 'profiles', 'cfg2_kernel_times.json')
+
+
+def profiled_hip_us(config):
+    """The HIP kernels' summed time per step from the committed rocprofv3 kernel trace of this configuration
+    (profiles/cfg2_kernel_times.json), or None when there is none."""
+    if config != 'cfg2':
+        return None
+    try:
+        with open(KERNEL_TIMES_FILE) as f:
+            return json.load(f)['hip_us_per_step']
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+DECODE = dict(B=16, d=768, V=50304, layers=6, contexts=(1024, 4096, 16384, 32768, 65536), frac=0.2, span=(16, 256),
               zipf=1.1)
 
 
-def decode_bench(dev, steps, warmup, seed=0, contexts=None):
-    """BASELINE.json configs[4], one layer: the O(1) generation step of one ASRN layer at d = 768, B = 16, after a
-    prefill of each context length. Per-token latency (wall clock over `steps` back-to-back steps, synchronized at
-    both ends) against the context, and the least-squares slope with its 95% interval (O(1): it includes 0). The
-    step is the writer's HIP graph replay (EscritorCapa(grafo=True)); its first step runs op by op, and there the two
-    HIP kernels are timed with events (a replay makes no library call to time); the second captures the graph."""
+def decode_bench(dev, steps, warmup, seed=0, contexts=None, layers=None):
+    """BASELINE.json configs[4]'s decode over its ASRN layers: the O(1) generation step of a stack of `layers` ASRN
+    layers (6, as the d = 768 model has) at d = 768, B = 16, after a prefill of each context length, one
+    EscritorCapa per layer, each layer's output the next one's input h and E the token embeddings for all of them
+    (asrn/nucleo.py:1751-1854 per layer). The model's local blocks, embedding and head are not part of this build
+    and are not timed. Per-token latency (wall clock over `steps` back-to-back steps, synchronized at both ends)
+    against the context, and the least-squares slope with its 95% interval (O(1): it includes 0). Each layer's step
+    is its writer's HIP graph replay (EscritorCapa(grafo=True)); their first step runs op by op, and there the HIP
+    kernels are timed with events (a replay makes no library call to time); the second captures the graphs."""
     import torch
 
     import asrn_amd
@@ -149,57 +192,82 @@ def decode_bench(dev, steps, warmup, seed=0, contexts=None):
 
     cfg = DECODE
     B, d, V = cfg['B'], cfg['d'], cfg['V']
+    nl = layers or cfg['layers']
     contexts = contexts or cfg['contexts']
     torch.manual_seed(seed)
-    layer = synth.move_params(asrn_amd.ASRNLayer(d), seed=seed).to(dev)
+    capas = [synth.move_params(asrn_amd.ASRNLayer(d), seed=seed + j).to(dev) for j in range(nl)]
     g = torch.Generator(device=dev).manual_seed(seed + 7)
     emb = torch.randn(V, d, generator=g, device=dev)
     rows = []
     kern = {}
+    w = max(warmup, 2)
     for ctx in contexts:
-        x = synth.tokens(B, ctx + max(warmup, 2) + steps, V, frac=cfg['frac'], span=cfg['span'], zipf=cfg['zipf'],
-                         seed=seed + ctx).to(dev)
+        n = ctx + w + steps
+        x = synth.tokens(B, n, V, frac=cfg['frac'], span=cfg['span'], zipf=cfg['zipf'], seed=seed + ctx).to(dev)
         E = emb[x]
-        h = torch.randn(B, x.shape[1], d, generator=g, device=dev)
-        # every position a key (the rings update); the step replayed from a HIP graph
-        esc = asrn_amd.EscritorCapa(layer, memoria_de_lo_ajeno=False, grafo=True)
-        esc.inicio(E[:, :ctx], h[:, :ctx], x[:, :ctx], capacidad=ctx + max(warmup, 2) + steps + 1)
-        timed = _lib.time_calls(['asrn_decode_attend', 'asrn_repetition_step'])
-        esc.paso(E[:, ctx], h[:, ctx], x[:, ctx])                        # op by op: its kernels timed
+        h = torch.randn(B, n, d, generator=g, device=dev)
+        # every position a key (the rings update); each layer's step replayed from a HIP graph
+        escs = [asrn_amd.EscritorCapa(c, memoria_de_lo_ajeno=False, grafo=True) for c in capas]
+        hj = h[:, :ctx]
+        for esc in escs:
+            hj = esc.inicio(E[:, :ctx], hj, x[:, :ctx], capacidad=n + 1)
+        del hj
+
+        def paso(t):
+            y = h[:, t]
+            for esc in escs:
+                y = esc.paso(E[:, t], y, x[:, t])
+            return y
+
+        timed = _lib.time_calls(['asrn_decode_attend', 'asrn_repetition_step', 'asrn_decode_produce', 'asrn_gate_fwd'])
+        paso(ctx)                                                  # op by op: its kernels timed
         timed = _lib.stop_timing()
-        for t in range(ctx + 1, ctx + max(warmup, 2)):                    # the first of these captures the graph
-            esc.paso(E[:, t], h[:, t], x[:, t])
-        w = max(warmup, 2)
+        for t in range(ctx + 1, ctx + w):                          # the first of these captures the graphs
+            paso(t)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for t in range(ctx + w, ctx + w + steps):
-            esc.paso(E[:, t], h[:, t], x[:, t])
+            paso(t)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        for n, evs in timed.items():
-            kern.setdefault(n, []).extend(s.elapsed_time(e) for s, e in evs)
+        for name, evs in timed.items():
+            kern.setdefault(name, []).extend(s.elapsed_time(e) for s, e in evs)
         ms = 1e3 * (t1 - t0) / steps
         rows.append({'context': ctx, 'ms_per_step': round(ms, 4), 'tokens_per_s': round(B * 1e3 / ms, 1),
-                     'kernel_us': {n: round(1e3 * sum(s.elapsed_time(e) for s, e in evs) / len(evs), 2)
-                                   for n, evs in timed.items() if evs}})
-        del esc, E, h, x
+                     'kernel_us_per_step': {name: round(1e3 * sum(s.elapsed_time(e) for s, e in evs), 2)
+                                            for name, evs in timed.items() if evs}})
+        del escs, E, h, x
         torch.cuda.empty_cache()
     xs = [r['context'] for r in rows]
     ys = [r['ms_per_step'] * 1e6 for r in rows]        # ns
-    n = len(xs)
-    mx, my = sum(xs) / n, sum(ys) / n
+    k = len(xs)
+    mx, my = sum(xs) / k, sum(ys) / k
     sxx = sum((a - mx) ** 2 for a in xs)
     slope = sum((a - mx) * (b - my) for a, b in zip(xs, ys)) / sxx if sxx else 0.0
     res = [b - (my + slope * (a - mx)) for a, b in zip(xs, ys)]
-    se = (sum(r * r for r in res) / max(n - 2, 1) / sxx) ** 0.5 if sxx else 0.0
-    t975 = {1: 12.71, 2: 4.30, 3: 3.18, 4: 2.78, 5: 2.57}.get(n - 2, 2.0)
-    return {'workload': f'configs[4], one layer: O(1) generation step of one ASRN layer, d={d}, B={B}, V={V}, '
-                        f'Zipf 1.1 with 20% copied spans, prefill of each context then {warmup} + {steps} steps',
-            'launch': 'hip graph replay of the step', 'per_context': rows, 'tokens_per_s': rows[-1]['tokens_per_s'],
+    se = (sum(r * r for r in res) / max(k - 2, 1) / sxx) ** 0.5 if sxx else 0.0
+    t975 = {1: 12.71, 2: 4.30, 3: 3.18, 4: 2.78, 5: 2.57}.get(k - 2, 2.0)
+    return {'workload': f'configs[4] decode over {nl} ASRN layers: d={d}, B={B}, V={V}, Zipf 1.1 with 20% copied '
+                        f'spans, prefill of each context then {w} + {steps} greedy-position steps (the tokens of the '
+                        'synthetic stream); local blocks, embedding and head not included',
+            'layers': nl, 'launch': 'hip graph replay of each layer\'s step', 'per_context': rows,
+            'tokens_per_s': rows[-1]['tokens_per_s'],
             'slope_ns_per_context_token': round(slope, 4),
             'slope_ci95': [round(slope - t975 * se, 4), round(slope + t975 * se, 4)],
-            'kernels': {k: {'launches': len(v), 'mean_us': round(1e3 * sum(v) / len(v), 3)} for k, v in kern.items()
-                        if v}}
+            'kernels_op_by_op_step': {name: {'launches': len(v), 'mean_us': round(1e3 * sum(v) / len(v), 3)}
+                                      for name, v in kern.items() if v}}
+
+
+def hip_aggregate(hip_b, tokens, eager_ms, prof_us):
+    """All HIP kernels' algorithmic bytes over their summed time per step: from the committed rocprofv3 kernel trace
+    when there is one (the eager pass's event times include the host's launch gaps of a host-bound step), else from
+    those events."""
+    if prof_us:
+        return {'bytes_per_token': hip_b, 'hip_us_per_step': prof_us, 'source': 'rocprofv3 kernel trace, '
+                'profiles/cfg2_kernel_times.json', 'frac': round(hip_b * tokens / (HBM_PEAK * prof_us * 1e-6), 4)}
+    return {'bytes_per_token': hip_b, 'hip_us_per_step': round(eager_ms * 1e3, 1),
+            'source': 'device events around each library call in the eager pass (include launch gaps)',
+            'frac': round(hip_b * tokens / (HBM_PEAK * eager_ms * 1e-3), 4)}
 
 
 def main():
@@ -212,7 +280,9 @@ def main():
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-decode', action='store_true')
-    ap.add_argument('--decode-steps', type=int, default=256)
+    ap.add_argument('--decode-steps', type=int, default=1024)
+    ap.add_argument('--decode-layers', type=int, default=DECODE['layers'])
+    ap.add_argument('--decode-contexts', default=None, help='comma-separated prefill lengths (default 1K,4K,16K,32K,64K)')
     ap.add_argument('--decode-only', action='store_true',
                     help='only the generation-step leg (configs[4], one layer); prints its JSON object')
     ap.add_argument('--eager', action='store_true', help='time Python-launched steps instead of HIP graph replays')
@@ -248,8 +318,10 @@ def main():
         from asrn_amd import tuning
         if tuning.use_tuned_gemms():
             gemm_picks = 'TunableOp picks, asrn_amd/data/gemm_picks_mi355x.csv'
+    contexts = [int(c) for c in args.decode_contexts.split(',')] if args.decode_contexts else None
     if args.decode_only:
-        print(json.dumps({'decode': decode_bench(torch.device('cuda:0'), args.decode_steps, 20, seed=args.seed),
+        print(json.dumps({'decode': decode_bench(torch.device('cuda:0'), args.decode_steps, 20, seed=args.seed,
+                                                  contexts=contexts, layers=args.decode_layers),
                           'gemm_picks': gemm_picks}), flush=True)
         return
     cfg = synth.CONFIGS[args.config]
@@ -349,15 +421,15 @@ def main():
         'roofline': {'bound': 'hbm', 'kernel': dom, 'achieved': round(achieved / 1e9, 1), 'peak': HBM_PEAK / 1e9,
                      'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK, 4), 'traffic': measured_traffic(dom) if args.config == 'cfg2' else None,
                      'bytes_per_token': algo[dom], 'mean_launch_us': round(dom_us, 2)},
-        'hip_aggregate': {'bytes_per_token': hip_b, 'hip_ms_per_step': round(hip_ms_per_step, 4),
-                          'frac': round(hip_b * tokens / (HBM_PEAK * hip_ms_per_step * 1e-3), 4)},
+        'hip_aggregate': hip_aggregate(hip_b, tokens, hip_ms_per_step, profiled_hip_us(args.config)),
         'layer': {'tokens_per_s': round(value, 1),
                   'bytes_per_token': layer_b, 'hbm_frac': round(layer_b * tokens / (HBM_PEAK * wall), 4)},
         'kernels': {n: {k: round(v, 3) if isinstance(v, float) else v for k, v in s.items()}
                     for n, s in sorted(per_call.items(), key=lambda kv: -kv[1]['total_ms'])},
     }
     if not args.no_decode:
-        out['decode'] = decode_bench(dev, args.decode_steps, 20, seed=args.seed)
+        out['decode'] = decode_bench(dev, args.decode_steps, 20, seed=args.seed, contexts=contexts,
+                                     layers=args.decode_layers)
     if not args.no_cpu_baseline:
         out['cpu_baseline'] = cpu_baseline(layer_cpu, x, E, h, gy)
     print(json.dumps(out), flush=True)

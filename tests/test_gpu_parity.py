@@ -386,11 +386,14 @@ def test_candidates_cfg2_full_size():
                                          (3, 700, 256, 8, 2, 8)])
 def test_candidates_lists_match_regather(B, L, d, T, nb, C):
     """The backward's query pass reading the forward's candidate lists gives the same outputs and gradients, bit for
-    bit, as gathering and deduplicating again (few bits per table: many queries have more than 64 candidates)."""
+    bit, as gathering and deduplicating again (few bits per table: many queries have more than 64 candidates); both
+    match the oracle."""
     say('candidate lists', B, L, d, T, nb, C)
     P, cf = T * nb + (-(T * nb)) % 4, 16
     g = torch.Generator().manual_seed(L + nb)
-    phi = torch.randn(B, L, P, generator=g).to(DEV)
+    phi = torch.randn(B, L, P, generator=g)
+    phi[..., T * nb:] = 0                              # the float4 padding columns
+    phi = phi.to(DEV)
     V = torch.randn(B, L, d, generator=g).to(DEV)
     Qc, Kc = torch.randn(B, L, cf, generator=g).to(DEV), torch.randn(B, L, cf, generator=g).to(DEV)
     Bt = (torch.rand(B, L, generator=g, dtype=torch.float64) * 0.1).cumsum(1).to(DEV)
@@ -408,6 +411,15 @@ def test_candidates_lists_match_regather(B, L, d, T, nb, C):
         outs.append([sal.detach(), sen] + [t.grad for t in leaves])
     for i, (a, b) in enumerate(zip(outs[0], outs[1])):
         assert torch.equal(a, b), f'output {i} differs'
+    sh = O.Shape(d=d, T=T, nb=nb, C=C, Tc=T // 2, cf=cf, K=4)
+    stage = {k: v.detach().cpu() for k, v in zip(('phi', 'V', 'Qc', 'Kc', 'Bt', 'log_alfa'), (phi, V, Qc, Kc, Bt, la))}
+    stage['phi'] = stage['phi'][..., :T * nb]
+    acc, rg = oracle_candidates(stage, sig.cpu(), w.cpu(), gam.cpu(), sh, gs.cpu())
+    assert_close(outs[1][0], acc['salida'], 'salida vs oracle')
+    check_signals(outs[1][1].cpu(), acc)
+    for i, k in enumerate(('phi', 'V', 'Qc', 'Kc', 'Bt', 'log_alfa', 'w_sufijo', 'gamma')):
+        got = outs[1][2 + i]
+        assert_close(got[..., :T * nb] if k == 'phi' else got, rg[k], 'grad ' + k + ' vs oracle')
 
 
 def test_candidates_v_shift_in_place():
@@ -805,3 +817,33 @@ def test_layer_signatures_from_E_vs_oracle():
     for n, g in grads.items():
         if n in leaves and leaves[n].grad is not None:
             assert_close(g, leaves[n].grad, 'grad ' + n)
+
+
+def test_shared_ngram_sort_across_layers_is_bit_identical():
+    """One n-gram sort for a stack of 6 layers (asrn_amd.ngramas, handed to every layer's forward) gives the same
+    outputs and gradients, bit for bit, as each layer sorting the same tokens itself; a sort made for other tokens
+    is refused."""
+    say('shared n-gram sort, 6 layers')
+    d, B, L = 64, 2, 700
+    torch.manual_seed(5)
+    capas = [synth.move_params(CapaASRNEstable(d), 10 + j).to(DEV) for j in range(6)]
+    x, E, h = synth.layer_inputs(B, L, d, 40, seed=9)
+    gy = torch.randn(B, L, d, generator=torch.Generator().manual_seed(2)).to(DEV)
+    xd = x.to(DEV)
+    outs = []
+    for shared in (False, True):
+        for c in capas:
+            c.zero_grad()
+        Ed, hd = E.to(DEV).requires_grad_(), h.to(DEV).requires_grad_()
+        ng = asrn_amd.ngramas(xd, capas[0]) if shared else None
+        y = hd
+        for c in capas:
+            y = c(Ed, y, xd, ngramas=ng)
+        (y * gy).sum().backward()
+        outs.append([y.detach(), Ed.grad, hd.grad] + [p.grad.clone() for c in capas for p in c.parameters()
+                                                       if p.grad is not None])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    other = xd.clone()
+    with pytest.raises(ValueError, match='other token ids'):
+        capas[0](E.to(DEV), h.to(DEV), xd, ngramas=asrn_amd.ngramas(other, capas[0]))
