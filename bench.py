@@ -1,7 +1,8 @@
 """Benchmark of the ASRN layer hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--config cfg2|cfg3] [--no-cpu-baseline] [--no-decode]
-                    [--decode-steps 1024] [--decode-layers 6] [--decode-only]
+                    [--decode-steps 1024] [--decode-layers 6] [--decode-only] [--no-model] [--model-only]
+                    [--model-steps 20]
 
 A step is one forward + backward of one ASRN layer (asrn.ASRNLayer, group-A protections) over one batch of
 synthetic tokens: BASELINE.json configs[1] = cfg2, B 8, N 4096, d 256, V 256, fp32, 30% copied spans (--config cfg3:
@@ -18,6 +19,9 @@ steps, since events recorded while capturing are not replayed. Prints one JSON l
                 operands and results, 16,000 B/token at cfg2)
   decode        the O(1) generation step of configs[4]'s 6 ASRN layers (d 768, B 16): per-token latency over 1,024
                 steps against the context, 1K to 64K, and its slope
+  modelo        the whole model's training step as PasoGrafado replays it: configs[3] (V 50,304, d 768, 12 local
+                blocks, 6 ASRN layers, B 8, N 2,048, bf16 autocast, AdamW) and configs[0] (the quick-start model,
+                fp32, 8 x 256 tokens)
   cpu_baseline  the CPU oracle (oracle/layer.py, PyTorch fp32 on the host cores) on the same workload (a bounded
                 sample of it for cfg3)
 """
@@ -258,6 +262,66 @@ def decode_bench(dev, steps, warmup, seed=0, contexts=None, layers=None):
                                       for name, v in kern.items() if v}}
 
 
+# BASELINE.json configs[3] (the d = 768 LM training step) and configs[0] (the quick-start model's step)
+MODELOS = {
+    'cfg4': dict(kw=dict(V=50304, d=768, n_capas=12, largo_cada=2), B=8, N=2048, precision='bf16', frac=0.15,
+                 span=(8, 128), zipf=1.1),
+    'cfg1': dict(kw=dict(V=256, d=64, n_capas=4), B=8, N=256, precision='fp32', frac=0.3, span=(8, 64), zipf=None),
+}
+
+
+def modelo_bench(dev, nombre, steps, warmup, seed=0, eager_steps=5):
+    """One whole training step of ModeloASRN (forward, fp32 cross-entropy, backward, clipping at 1.0, fused AdamW)
+    as PasoGrafado replays it: the step captured once into a HIP graph, new batches copied into its inputs each
+    step. Weights random-init from the seed (create_model(..., semilla=seed)), synthetic tokens of the config's
+    distribution, all resident in HBM. Also the same step launched op by op (eager_steps of them), for the host
+    overhead the graph removes."""
+    import torch
+
+    import asrn_amd
+    from asrn_amd import synth
+
+    cfg = MODELOS[nombre]
+    B, N = cfg['B'], cfg['N']
+    m = asrn_amd.crear_modelo(**cfg['kw'], semilla=seed).to(dev).train()
+    opt = asrn_amd.crear_optimizador(m, lr=1e-3, capturable=True)
+    nb = 4
+    w = synth.tokens(B * nb, N + 1, cfg['kw']['V'], frac=cfg['frac'], span=cfg['span'], zipf=cfg['zipf'],
+                     seed=seed + 11).to(dev)
+    lotes = [(w[B * i:B * i + B, :-1].contiguous(), w[B * i:B * i + B, 1:].contiguous()) for i in range(nb)]
+
+    def correr(paso, n, desde):
+        ultimo = None
+        for i in range(n):
+            x, y = lotes[(desde + i) % nb]
+            ultimo = paso(x, y, lr=1e-3)
+        return ultimo
+
+    eager = asrn_amd.PasoGrafado(m, opt, B, N, precision=cfg['precision'], grabar=False)
+    correr(eager, 2, 0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    correr(eager, eager_steps, 0)
+    torch.cuda.synchronize()
+    eager_ms = 1e3 * (time.perf_counter() - t0) / eager_steps
+    del eager
+    grafo = asrn_amd.PasoGrafado(m, opt, B, N, precision=cfg['precision'], calentar=2)
+    correr(grafo, max(warmup, 3), 0)                              # 2 side-stream steps, then capture and replays
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    perdida, norma, salto = correr(grafo, steps, 0)
+    torch.cuda.synchronize()
+    ms = 1e3 * (time.perf_counter() - t0) / steps
+    return {'workload': f"configs[{'3' if nombre == 'cfg4' else '0'}]: ModeloASRN training step, "
+                        f"V={cfg['kw']['V']}, d={cfg['kw']['d']}, {cfg['kw']['n_capas']} local blocks, "
+                        f"{len(m.largos)} ASRN layers, B={B}, N={N}, {cfg['precision']} autocast, fp32 weights, "
+                        'AdamW (fused, capturable), clip 1.0; synthetic tokens, random-init weights',
+            'parameters': m.num_parametros(), 'tokens_per_s': round(B * N * 1e3 / ms, 1), 'ms_per_step': round(ms, 3),
+            'steps': steps, 'launch': 'PasoGrafado: hip graph replay of the whole step',
+            'eager_ms_per_step': round(eager_ms, 3), 'last_loss': round(float(perdida), 5),
+            'skipped_last': float(salto)}
+
+
 def hip_aggregate(hip_b, tokens, eager_ms, prof_us):
     """All HIP kernels' algorithmic bytes over their summed time per step: from the committed rocprofv3 kernel trace
     when there is one (the eager pass's event times include the host's launch gaps of a host-bound step), else from
@@ -286,6 +350,10 @@ def main():
     ap.add_argument('--decode-only', action='store_true',
                     help='only the generation-step leg (configs[4], one layer); prints its JSON object')
     ap.add_argument('--eager', action='store_true', help='time Python-launched steps instead of HIP graph replays')
+    ap.add_argument('--no-model', action='store_true', help='skip the whole-model training-step legs')
+    ap.add_argument('--model-only', action='store_true',
+                    help='only the whole-model training-step legs (configs[3] and configs[0]); prints their JSON')
+    ap.add_argument('--model-steps', type=int, default=20)
     ap.add_argument('--default-gemms', action='store_true',
                     help="leave the GEMMs on the libraries' default picks instead of the shipped MI355X picks")
     ap.add_argument('--copy-calibration', type=int, default=0, metavar='BYTES',
@@ -312,7 +380,11 @@ def main():
         print(json.dumps({'copy_calibration_bytes': src.numel() * 4, 'launches': 3}), flush=True)
         return
 
-    asrn_amd.load()
+    asrn_amd.cargar_biblioteca()
+    if args.model_only:
+        print(json.dumps({'modelo': {n: modelo_bench(torch.device('cuda:0'), n, args.model_steps, 5, seed=args.seed)
+                                     for n in MODELOS}}), flush=True)
+        return
     gemm_picks = 'library defaults'
     if not args.default_gemms:
         from asrn_amd import tuning
@@ -430,6 +502,8 @@ def main():
     if not args.no_decode:
         out['decode'] = decode_bench(dev, args.decode_steps, 20, seed=args.seed, contexts=contexts,
                                      layers=args.decode_layers)
+    if not args.no_model:
+        out['modelo'] = {n: modelo_bench(dev, n, args.model_steps, 5, seed=args.seed) for n in MODELOS}
     if not args.no_cpu_baseline:
         out['cpu_baseline'] = cpu_baseline(layer_cpu, x, E, h, gy)
     print(json.dumps(out), flush=True)

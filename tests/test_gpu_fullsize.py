@@ -41,7 +41,7 @@ def say(*a):
 def _need_gpu():
     if not torch.cuda.is_available():
         pytest.skip('needs a GPU')
-    asrn_amd.load()
+    asrn_amd.cargar_biblioteca()
 
 
 def leaves_of(layer_cpu):

@@ -40,7 +40,7 @@ def assert_close(a, b, what, tol=TOL):
 def _need_gpu():
     if not torch.cuda.is_available():
         pytest.skip('needs a GPU')
-    asrn_amd.load()
+    asrn_amd.cargar_biblioteca()
 
 
 def token_phi(B, L, V, T, nb, seed):

@@ -17,7 +17,7 @@ DEV = 'cuda'
 def _need_gpu():
     if not torch.cuda.is_available():
         pytest.skip('needs a GPU')
-    asrn_amd.load()
+    asrn_amd.cargar_biblioteca()
 
 
 @pytest.mark.parametrize('B,L,d,bf16', [(2, 1500, 64, False), (2, 2048, 128, True)])

@@ -16,7 +16,7 @@ DEV = 'cuda'
 def _need_gpu():
     if not torch.cuda.is_available():
         pytest.skip('needs a GPU')
-    asrn_amd.load()
+    asrn_amd.cargar_biblioteca()
 
 
 def scan_with_workspace(a, b):
