@@ -7,7 +7,8 @@ The public names mirror the reference package (KIROKOWA/ASRN, asrn/__init__.py:4
     crear_modelo / create_model, crear_desde_config / create_from_config;
   - training: crear_optimizador, tasa_aprendizaje, PasoGrafado, entrenar / train, evaluar / evaluate;
   - files: guardar / save, cargar / load (the reference's format, v83 on);
-  - generation: EscritorCapa / LayerWriter, the layer's O(1) step;
+  - generation: escribir / generate (the loop on the device), EscritorModelo / ModelWriter (the model's O(1) step),
+    EscritorCapa / LayerWriter (one layer's);
   - ngramas, one n-gram sort shared by every layer of a model.
 cargar_biblioteca() opens the HIP library (the product has no CPU fallback).
 """
@@ -19,6 +20,7 @@ from .capa import ASRNLayer, CapaASRNEstable, Protecciones, Protections, convert
 from .entrenamiento import (MULT_SUFIJO_Y_PUERTA, PESOS_SUFIJO_Y_PUERTA, PasoGrafado, crear_optimizador, entrenar,
                             evaluar, tasa_aprendizaje)
 from .escritura import EscritorCapa, LayerWriter
+from .generacion import EscritorModelo, escribir
 from .modelo import TALLAS, BloqueLocal, ConfigASRN, ModeloASRN, crear_desde_config, crear_modelo
 from .ops import escaneo
 
@@ -26,12 +28,13 @@ __version__ = '0.2.0'
 
 ASRNModel, ASRNConfig, LocalBlock = ModeloASRN, ConfigASRN, BloqueLocal
 create_model, create_from_config, convert = crear_modelo, crear_desde_config, convertir
-train, evaluate, save, load = entrenar, evaluar, guardar, cargar
+train, evaluate, save, load, generate = entrenar, evaluar, guardar, cargar, escribir
+ModelWriter = EscritorModelo
 load_library = cargar_biblioteca
 
 __all__ = ['ASRNLayer', 'CapaASRNEstable', 'Protecciones', 'Protections', 'convertir', 'convert', 'firmas_de_piezas',
            'ngramas', 'escaneo', 'ModeloASRN', 'ASRNModel', 'BloqueLocal', 'LocalBlock', 'ConfigASRN', 'ASRNConfig',
            'TALLAS', 'crear_modelo', 'create_model', 'crear_desde_config', 'create_from_config', 'crear_optimizador',
            'tasa_aprendizaje', 'PasoGrafado', 'entrenar', 'train', 'evaluar', 'evaluate', 'guardar', 'save',
-           'cargar', 'load', 'EscritorCapa', 'LayerWriter', 'MULT_SUFIJO_Y_PUERTA', 'PESOS_SUFIJO_Y_PUERTA', 'ops',
-           'cargar_biblioteca', 'load_library', 'LIB_PATH', 'ASRNHipError', '__version__']
+           'cargar', 'load', 'escribir', 'generate', 'EscritorModelo', 'ModelWriter', 'EscritorCapa', 'LayerWriter',
+           'MULT_SUFIJO_Y_PUERTA', 'PESOS_SUFIJO_Y_PUERTA', 'ops', 'cargar_biblioteca', 'load_library', 'LIB_PATH', 'ASRNHipError', '__version__']

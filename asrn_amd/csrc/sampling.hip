@@ -1,0 +1,521 @@
+// Token choice for the generation loop, on the device, and the n-gram sets it consults.
+//
+// n-gram sets: per text row, an open-addressing table of 64-bit keys; a key packs the n token ids of an n-gram, w bits
+// apiece, the oldest token in the lowest bits. w is asrn_sample_bits(V), the smallest width whose all-ones field is
+// above every token id, so no key is the all-ones word that marks an empty slot. Inserting is then one 64-bit
+// compare-and-swap that claims and publishes the key at once: concurrent inserts of one n-gram meet in one slot, and
+// no thread ever waits on another. Tables hold at most half their slots, so probes stay short, and every probe loop
+// ends within `cap` steps.
+//
+// asrn_sample: one workgroup per text row makes the reference's whole per-token decision of escribir
+// (asrn/nucleo.py:2017-2036) with no host round trip:
+//   the repetition penalty over the last `window` tokens and the n-gram bans (_frenar, nucleo:1909-1918), with the
+//   fallback to the plain logits when the bans leave nothing (nucleo:2020-2021); the quote mask (_Ngramas.siguientes,
+//   nucleo:1877-1889); temperature, top-k and top-p (_muestrear, nucleo:1946-1962: the k-th largest logit and the
+//   top-p cut are found by radix selection over the values' bits, counts and fixed-point masses in LDS, instead of a
+//   sort); the softmax and the quote-mass correction (_conservar_cita, nucleo:1933-1943); one draw by inverse CDF
+//   with a counter-based uniform (seed, row, position); the stop token (nucleo:2026-2028); then the token is written
+//   into the text and its n-grams into the sets (_Ngramas.agregar, nucleo:1872-1875).
+// Every reduction runs in a fixed order: the same inputs and seed give the same token.
+#include "common.h"
+
+namespace asrn {
+namespace {
+
+constexpr unsigned long long kEmptySlot = ~0ull;
+constexpr int kSampleThreads = 1024;
+constexpr int kSampleWaves = kSampleThreads / kWave;
+constexpr double kMassScale = 1099511627776.0;   // 2^40: fixed-point probability masses (sums stay below 2^63)
+
+// SplitMix64's output function (G. Steele, D. Lea, C. Flood, "Fast splittable pseudorandom number generators",
+// OOPSLA 2014): a bijective 64-bit mixer, used for slot hashes and for the counter-based uniforms.
+__device__ __forceinline__ uint64_t mix64(uint64_t x) {
+  x ^= x >> 30;
+  x *= 0xbf58476d1ce4e5b9ull;
+  x ^= x >> 27;
+  x *= 0x94d049bb133111ebull;
+  x ^= x >> 31;
+  return x;
+}
+
+struct TupleSet {
+  unsigned long long* slots;   // (rows, cap); nullptr: the set is not used
+  int64_t cap;                 // power of two
+  int32_t n;                   // tokens per key
+};
+
+__device__ __forceinline__ bool set_has(const TupleSet& s, int64_t row, uint64_t key) {
+  const unsigned long long* t = s.slots + row * s.cap;
+  const uint64_t m = (uint64_t)s.cap - 1;
+  uint64_t i = mix64(key) & m;
+  for (int64_t p = 0; p < s.cap; ++p) {
+    const unsigned long long v = t[i];
+    if (v == key) return true;
+    if (v == kEmptySlot) return false;
+    i = (i + 1) & m;
+  }
+  return false;
+}
+
+__device__ __forceinline__ void set_add(const TupleSet& s, int64_t row, uint64_t key) {
+  unsigned long long* t = s.slots + row * s.cap;
+  const uint64_t m = (uint64_t)s.cap - 1;
+  uint64_t i = mix64(key) & m;
+  for (int64_t p = 0; p < s.cap; ++p) {
+    const unsigned long long prev = atomicCAS(t + i, kEmptySlot, (unsigned long long)key);
+    if (prev == kEmptySlot || prev == key) return;
+    i = (i + 1) & m;
+  }
+}
+
+// tokens x[0..n-1] packed w bits apiece, x[0] lowest
+__device__ __forceinline__ uint64_t pack(const int64_t* x, int n, int w) {
+  uint64_t k = 0;
+  for (int j = 0; j < n; ++j) k |= (uint64_t)x[j] << (w * j);
+  return k;
+}
+
+__global__ void k_set_build(const int64_t* __restrict__ x, int64_t ldx, int64_t rows, int64_t L, TupleSet s, int w) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * L) return;
+  const int64_t b = i / L, t = i - b * L;
+  if (t < s.n - 1) return;
+  set_add(s, b, pack(x + b * ldx + t - (s.n - 1), s.n, w));
+}
+
+// ---- block reductions over the 1024 threads (fixed order: deterministic) ----------------------------------------
+
+struct Red {
+  float f[kSampleWaves];
+  unsigned long long u[kSampleWaves];
+};
+
+__device__ __forceinline__ float block_sum(float v, Red& r) {
+  v = wave_sum_u(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if (lane_id() == 0) r.f[w] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kSampleWaves; ++i) s += r.f[i];
+  return s;
+}
+
+__device__ __forceinline__ float block_max(float v, Red& r) {
+  v = wave_max_u(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if (lane_id() == 0) r.f[w] = v;
+  __syncthreads();
+  float s = r.f[0];
+#pragma unroll
+  for (int i = 1; i < kSampleWaves; ++i) s = fmaxf(s, r.f[i]);
+  return s;
+}
+
+__device__ __forceinline__ unsigned long long block_sum_u(unsigned long long v, Red& r) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if (lane_id() == 0) r.u[w] = v;
+  __syncthreads();
+  unsigned long long s = 0;
+#pragma unroll
+  for (int i = 0; i < kSampleWaves; ++i) s += r.u[i];
+  return s;
+}
+
+// float -> unsigned key with the same order (NaN above +inf)
+__device__ __forceinline__ uint32_t ordered(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float from_ordered(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+struct SampleArgs {
+  const float* lg;
+  int64_t ldl;
+  float* work;                 // (B, V): the logits after penalty and bans
+  uint32_t* quote_bits;        // (B, ceil(V / 32))
+  float* prob_out;             // (B, V) or nullptr: the final probabilities
+  float* logits_out;           // (B, steps, V) or nullptr: the logits as they came, at step pos - L0
+  int64_t steps;
+  int64_t* text;
+  int64_t ld_text;
+  const int64_t* pos_dev;
+  int64_t pos_max;
+  int64_t L0;
+  int64_t* tokens;
+  uint8_t* done;
+  int32_t* stop_step;
+  TupleSet quote, ban;
+  int32_t w;
+  int64_t V;
+  float temperature, top_p, penalty;
+  int32_t top_k, window;
+  int64_t stop_token;
+  uint64_t seed;
+};
+
+__global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
+  __shared__ Red red;
+  __shared__ unsigned int hist_n[256];
+  __shared__ unsigned long long hist_m[256];
+  __shared__ uint32_t sel[4];          // radix results: [0] prefix, [1] flag
+  __shared__ float scan[kSampleThreads];
+  __shared__ int pick[2];
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  const int64_t pos = *a.pos_dev;
+  if (pos < 0 || pos > a.pos_max) return;                       // outside the text buffer: nothing is touched
+  const int64_t V = a.V;
+  const float* lg = a.lg + b * a.ldl;
+  float* work = a.work + b * V;
+  int64_t* text = a.text + b * a.ld_text;
+  const int64_t step = pos - a.L0;
+  const float ninf = -INFINITY;
+
+  // penalty (_frenar): the logits as they came, then the tokens of the window penalized from those same values
+  float* lout = (a.logits_out && step >= 0 && step < a.steps) ? a.logits_out + (b * a.steps + step) * V : nullptr;
+  for (int64_t v = tid; v < V; v += kSampleThreads) {
+    const float l = lg[v];
+    work[v] = l;
+    if (lout) lout[v] = l;
+  }
+  __syncthreads();
+  if (a.penalty != 1.f) {
+    for (int j = tid; j < a.window; j += kSampleThreads) {
+      const int64_t p = pos - a.window + j;
+      if (p < 0) continue;
+      const int64_t v = text[p];
+      const float l = lg[v];
+      work[v] = l > 0.f ? l / a.penalty : l * a.penalty;       // duplicates write the same value
+    }
+  }
+  __syncthreads();
+  // bans: tokens that would close an n-gram already generated (only generated tokens count)
+  const int nb = a.ban.n;
+  if (a.ban.slots && pos - a.L0 >= nb) {
+    const uint64_t base = pack(text + pos - (nb - 1), nb - 1, a.w);
+    const int sh = a.w * (nb - 1);
+    for (int64_t v = tid; v < V; v += kSampleThreads)
+      if (set_has(a.ban, b, base | ((uint64_t)v << sh))) work[v] = ninf;
+  }
+  __syncthreads();
+  {
+    float finite = 0.f;
+    for (int64_t v = tid; v < V; v += kSampleThreads) finite += (work[v] == ninf) ? 0.f : 1.f;
+    if (block_sum(finite, red) == 0.f) {                        // nothing left: the plain logits (no penalty either)
+      __syncthreads();
+      for (int64_t v = tid; v < V; v += kSampleThreads) work[v] = lg[v];
+    }
+  }
+  __syncthreads();
+
+  // quote mask and its mass at temperature 1 (_conservar_cita's p1)
+  const int nq = a.quote.n;
+  const bool quote = a.quote.slots && pos >= nq;
+  uint32_t* qbits = a.quote_bits + b * ((V + 31) / 32);
+  float mass_p = 0.f;
+  if (quote) {
+    const uint64_t base = pack(text + pos - (nq - 1), nq - 1, a.w);
+    const int sh = a.w * (nq - 1);
+    for (int64_t wd = tid; wd < (V + 31) / 32; wd += kSampleThreads) {
+      uint32_t bits = 0;
+      for (int i = 0; i < 32; ++i) {
+        const int64_t v = wd * 32 + i;
+        if (v < V && set_has(a.quote, b, base | ((uint64_t)v << sh))) bits |= 1u << i;
+      }
+      qbits[wd] = bits;
+    }
+    __syncthreads();
+    float m = ninf;
+    for (int64_t v = tid; v < V; v += kSampleThreads) m = fmaxf(m, work[v]);
+    const float m1 = block_max(m, red);
+    float s = 0.f, c = 0.f;
+    for (int64_t v = tid; v < V; v += kSampleThreads) {
+      const float e = expf(work[v] - m1);
+      s += e;
+      if ((qbits[v >> 5] >> (v & 31)) & 1u) c += e;
+    }
+    const float S1 = block_sum(s, red);
+    mass_p = block_sum(c, red) / S1;
+  }
+  auto in_quote = [&](int64_t v) { return quote && ((qbits[v >> 5] >> (v & 31)) & 1u); };
+
+  // temperature and top-k: keep the logits >= the k-th largest
+  const float tinv_den = fmaxf(a.temperature, 1e-6f);
+  auto l3 = [&](int64_t v) { return work[v] / tinv_den; };
+  float corte = ninf;
+  if (a.top_k > 0 && (int64_t)a.top_k < V) {
+    uint32_t prefix = 0, mask = 0, rest = (uint32_t)a.top_k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int i = tid; i < 256; i += kSampleThreads) hist_n[i] = 0;
+      __syncthreads();
+      for (int64_t v = tid; v < V; v += kSampleThreads) {
+        const uint32_t k = ordered(l3(v));
+        if ((k & mask) == prefix) atomicAdd(&hist_n[(k >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        uint32_t cum = 0, d = 0;
+        for (int i = 255; i >= 0; --i) {
+          if (cum + hist_n[i] >= rest) { d = (uint32_t)i; break; }
+          cum += hist_n[i];
+        }
+        sel[0] = d;
+        sel[1] = rest - cum;
+      }
+      __syncthreads();
+      prefix |= sel[0] << shift;
+      mask |= 255u << shift;
+      rest = sel[1];
+      __syncthreads();
+    }
+    corte = from_ordered(prefix);
+  }
+  auto kept_k = [&](float x) { return !(x < corte); };
+
+  // the kept logits' max (the row's max is always kept) and top-p over their softmax
+  float mloc = ninf;
+  for (int64_t v = tid; v < V; v += kSampleThreads) {
+    const float x = l3(v);
+    if (kept_k(x)) mloc = fmaxf(mloc, x);
+  }
+  const float m3 = block_max(mloc, red);
+  float tau = -1.f;                                              // keep probabilities >= tau (all when < 0)
+  float S3 = 1.f;
+  if (a.top_p < 1.f) {
+    float s = 0.f;
+    for (int64_t v = tid; v < V; v += kSampleThreads) {
+      const float x = l3(v);
+      if (kept_k(x)) s += expf(x - m3);
+    }
+    S3 = block_sum(s, red);
+    const double target = ceil((double)a.top_p * kMassScale);
+    uint32_t prefix = 0, mask = 0;
+    unsigned long long acc = 0;
+    bool found = true;
+    for (int shift = 24; shift >= 0 && found; shift -= 8) {
+      for (int i = tid; i < 256; i += kSampleThreads) {
+        hist_n[i] = 0;
+        hist_m[i] = 0;
+      }
+      __syncthreads();
+      for (int64_t v = tid; v < V; v += kSampleThreads) {
+        const float x = l3(v);
+        if (!kept_k(x)) continue;
+        const float p = expf(x - m3) / S3;
+        const uint32_t k = __float_as_uint(p);
+        if ((k & mask) == prefix) {
+          atomicAdd(&hist_n[(k >> shift) & 255u], 1u);
+          atomicAdd(&hist_m[(k >> shift) & 255u], (unsigned long long)rint((double)p * kMassScale));
+        }
+      }
+      __syncthreads();
+      if (tid == 0) {
+        // from the largest values down: the bin where the mass of everything at or above it first reaches top_p
+        int d = -1;
+        for (int i = 255; i >= 0; --i) {
+          if (hist_n[i] == 0) continue;
+          if ((double)(acc + hist_m[i]) >= target) { d = i; break; }
+          acc += hist_m[i];
+        }
+        sel[0] = d < 0 ? 0u : (uint32_t)d;
+        sel[1] = d < 0 ? 0u : 1u;
+      }
+      __syncthreads();
+      found = sel[1] != 0;
+      prefix |= sel[0] << shift;
+      mask |= 255u << shift;
+      __syncthreads();
+    }
+    if (found) tau = __uint_as_float(prefix);
+  }
+
+  // final probabilities: softmax over what is kept, then the quote-mass correction
+  auto keep = [&](int64_t v, float* e) {
+    const float x = l3(v);
+    if (!kept_k(x)) return false;
+    *e = expf(x - m3);
+    return tau < 0.f || (*e / S3) >= tau;
+  };
+  float S4;
+  {
+    float s = 0.f;
+    for (int64_t v = tid; v < V; v += kSampleThreads) {
+      float e;
+      if (keep(v, &e)) s += e;
+    }
+    S4 = block_sum(s, red);
+  }
+  float sc_q = 1.f, sc_n = 1.f;
+  if (quote) {
+    float c = 0.f;
+    for (int64_t v = tid; v < V; v += kSampleThreads) {
+      float e;
+      if (keep(v, &e) && in_quote(v)) c += e / S4;
+    }
+    const float mass_q = block_sum(c, red);
+    if (mass_q > 0.f && mass_q < 1.f) {
+      sc_q = mass_p / fmaxf(mass_q, 1e-30f);
+      sc_n = (1.f - mass_p) / fmaxf(1.f - mass_q, 1e-30f);
+    }
+  }
+  auto prob = [&](int64_t v) {
+    float e;
+    if (!keep(v, &e)) return 0.f;
+    const float p = e / S4;
+    return quote ? p * (in_quote(v) ? sc_q : sc_n) : p;
+  };
+  if (a.prob_out) {
+    for (int64_t v = tid; v < V; v += kSampleThreads) a.prob_out[b * V + v] = prob(v);
+  }
+
+  // the draw: inverse CDF over the tokens in index order, each thread a contiguous segment
+  const int64_t seg = (V + kSampleThreads - 1) / kSampleThreads;
+  const int64_t v0 = (int64_t)tid * seg, v1 = v0 + seg < V ? v0 + seg : V;
+  float local = 0.f;
+  int64_t last_pos = -1;
+  for (int64_t v = v0; v < v1; ++v) {
+    const float p = prob(v);
+    local += p;
+    if (p > 0.f) last_pos = v;
+  }
+  scan[tid] = local;
+  if (tid < 2) pick[tid] = tid == 0 ? 0x7fffffff : -1;
+  __syncthreads();
+  for (int off = 1; off < kSampleThreads; off <<= 1) {        // inclusive scan (Hillis-Steele), fixed order
+    const float add = tid >= off ? scan[tid - off] : 0.f;
+    __syncthreads();
+    scan[tid] += add;
+    __syncthreads();
+  }
+  // thread t owns [scan[t - 1], scan[t]): neighbouring bounds are the same numbers, so the segments tile [0, total)
+  const float total = scan[kSampleThreads - 1];
+  const float before = tid > 0 ? scan[tid - 1] : 0.f;
+  const float after = scan[tid];
+  const uint64_t r = mix64(a.seed ^ mix64((uint64_t)pos * 0x9e3779b97f4a7c15ull + (uint64_t)b));
+  const float u = (float)(r >> 40) * (1.f / 16777216.f);      // 24 random bits: [0, 1)
+  const float target = u * total;
+  if (local > 0.f && target >= before && target < after) {
+    const float inside = target - before;
+    float acc = 0.f;                                             // summed from 0 in `local`'s order
+    int64_t chosen = -1;
+    for (int64_t v = v0; v < v1; ++v) {
+      const float p = prob(v);
+      acc += p;
+      if (p > 0.f && acc > inside) { chosen = v; break; }
+    }
+    if (chosen < 0) chosen = last_pos;
+    if (chosen >= 0) atomicMin(&pick[0], (int)chosen);
+  }
+  if (last_pos >= 0) atomicMax(&pick[1], (int)last_pos);
+  __syncthreads();
+
+  if (tid == 0) {
+    int64_t tok = pick[0] != 0x7fffffff ? pick[0] : (pick[1] >= 0 ? pick[1] : 0);
+    if (a.stop_token >= 0) {
+      if (a.done[b]) {
+        tok = a.stop_token;
+      } else if (tok == a.stop_token) {
+        a.done[b] = 1;
+        a.stop_step[b] = (int32_t)step;
+      }
+    }
+    text[pos] = tok;
+    a.tokens[b] = tok;
+    if (a.quote.slots && pos + 1 >= nq) set_add(a.quote, b, pack(text + pos - (nq - 1), nq, a.w));
+    if (a.ban.slots && pos + 1 - a.L0 >= nb) set_add(a.ban, b, pack(text + pos - (nb - 1), nb, a.w));
+  }
+}
+
+int check_set(const char* what, const unsigned long long* slots, int64_t cap, int32_t n, int32_t w) {
+  if (!slots) return 0;
+  ASRN_REQUIRE(cap >= 2 && (cap & (cap - 1)) == 0, "%s: the set's capacity %lld must be a power of two", what,
+               (long long)cap);
+  ASRN_REQUIRE(n >= 1 && (int64_t)n * w <= 64, "%s: n=%d tokens of %d bits do not fit a 64-bit key", what, n, w);
+  return 0;
+}
+
+}  // namespace
+}  // namespace asrn
+
+using namespace asrn;
+
+extern "C" int32_t asrn_sample_bits(int64_t V) {
+  // bits per token such that the largest id, V - 1, is below 2^w - 1: the all-ones key then never occurs
+  int32_t w = 1;
+  while (w < 62 && ((int64_t(1) << w) - 1) <= V - 1) ++w;
+  return w;
+}
+
+extern "C" int asrn_ngram_set_build(const int64_t* x, int64_t ldx, int64_t rows, int64_t L, int32_t n, int32_t w,
+                                    uint64_t* slots, int64_t cap, void* stream) {
+  ASRN_REQUIRE(rows >= 0 && L >= 0 && ldx >= L, "asrn_ngram_set_build: bad sizes rows=%lld L=%lld ldx=%lld",
+               (long long)rows, (long long)L, (long long)ldx);
+  ASRN_REQUIRE(slots != nullptr, "asrn_ngram_set_build: null table");
+  if (int rc = check_set("asrn_ngram_set_build", (const unsigned long long*)slots, cap, n, w)) return rc;
+  ASRN_REQUIRE(L <= cap / 2, "asrn_ngram_set_build: %lld n-grams per row need a capacity of at least %lld (got %lld)",
+               (long long)L, (long long)(2 * L), (long long)cap);
+  const int64_t total = rows * L;
+  if (total == 0) return 0;
+  TupleSet s{(unsigned long long*)slots, cap, n};
+  const int threads = 256;
+  hipLaunchKernelGGL(k_set_build, dim3((unsigned)((total + threads - 1) / threads)), dim3(threads), 0,
+                     (hipStream_t)stream, x, ldx, rows, L, s, w);
+  return check_launch("asrn_ngram_set_build");
+}
+
+extern "C" int asrn_sample(const float* lg, int64_t ldl, float* work, uint32_t* quote_bits, float* prob_out,
+                           float* logits_out, int64_t steps, int64_t* text, int64_t ld_text, const int64_t* pos_dev,
+                           int64_t pos_max, int64_t L0, int64_t* tokens, uint8_t* done, int32_t* stop_step,
+                           uint64_t* quote_slots, int64_t quote_cap, int32_t quote_n, uint64_t* ban_slots,
+                           int64_t ban_cap, int32_t ban_n, int32_t w, int64_t B, int64_t V, float temperature,
+                           int32_t top_k, float top_p, float penalty, int32_t window, int64_t stop_token, uint64_t seed,
+                           void* stream) {
+  ASRN_REQUIRE(B >= 1 && V >= 1 && V <= (int64_t(1) << 31) && ldl >= V, "asrn_sample: bad sizes B=%lld V=%lld",
+               (long long)B, (long long)V);
+  ASRN_REQUIRE(B <= (int64_t(1) << 20), "asrn_sample: at most 2^20 rows");
+  ASRN_REQUIRE(lg && work && quote_bits && text && pos_dev && tokens && done && stop_step, "asrn_sample: null pointer");
+  ASRN_REQUIRE(pos_max >= 0 && pos_max < ld_text && L0 >= 0, "asrn_sample: positions up to %lld do not fit a text "
+               "row of %lld", (long long)pos_max, (long long)ld_text);
+  ASRN_REQUIRE(window >= 0 && top_k >= 0 && penalty > 0.f, "asrn_sample: window, top_k >= 0 and penalty > 0");
+  ASRN_REQUIRE(w == asrn_sample_bits(V), "asrn_sample: w=%d must be asrn_sample_bits(V)=%d", w, asrn_sample_bits(V));
+  ASRN_REQUIRE(logits_out == nullptr || steps >= 1, "asrn_sample: logits_out needs steps >= 1");
+  if (int rc = check_set("asrn_sample (quote)", (const unsigned long long*)quote_slots, quote_cap, quote_n, w)) return rc;
+  if (int rc = check_set("asrn_sample (bans)", (const unsigned long long*)ban_slots, ban_cap, ban_n, w)) return rc;
+  SampleArgs a{};
+  a.lg = lg;
+  a.ldl = ldl;
+  a.work = work;
+  a.quote_bits = quote_bits;
+  a.prob_out = prob_out;
+  a.logits_out = logits_out;
+  a.steps = steps;
+  a.text = text;
+  a.ld_text = ld_text;
+  a.pos_dev = pos_dev;
+  a.pos_max = pos_max;
+  a.L0 = L0;
+  a.tokens = tokens;
+  a.done = done;
+  a.stop_step = stop_step;
+  a.quote = TupleSet{(unsigned long long*)quote_slots, quote_cap, quote_n};
+  a.ban = TupleSet{(unsigned long long*)ban_slots, ban_cap, ban_n};
+  a.w = w;
+  a.V = V;
+  a.temperature = temperature;
+  a.top_p = top_p;
+  a.penalty = penalty;
+  a.top_k = top_k;
+  a.window = window;
+  a.stop_token = stop_token;
+  a.seed = seed;
+  hipLaunchKernelGGL(k_sample, dim3((unsigned)B), dim3(kSampleThreads), 0, (hipStream_t)stream, a);
+  return check_launch("asrn_sample");
+}

@@ -764,3 +764,76 @@ class HawkesTable:
              B, stride, th, tdev, self.n, self.cap, ptr(self.keys), ptr(self.Bu), ptr(self.A), ptr(racha),
              ptr(vistos), ptr(hawkes), stream_of(dev))
         return vistos, hawkes
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# generation: n-gram sets and the device sampler
+# ---------------------------------------------------------------------------------------------------------------------
+
+def bits_por_pieza(V):
+    """Bits per token id in a packed n-gram key: the smallest width whose all-ones field exceeds V - 1."""
+    return int(query('asrn_sample_bits', int(V)))
+
+
+class ConjuntoNgramas:
+    """Per text row, a device hash set of the n-grams seen (n token ids packed into one 64-bit key): the device side
+    of the reference's _Ngramas (asrn/nucleo.py:1857-1889). Sized for `capacidad` n-grams per row (at most half the
+    slots in use); n * bits_por_pieza(V) must be <= 64."""
+
+    def __init__(self, filas, n, V, capacidad, dev):
+        w = bits_por_pieza(V)
+        if n < 1 or n * w > 64:
+            raise ValueError(f'n-gram sets pack n={n} token ids of {w} bits (V={V}) into 64 bits: n * {w} must be '
+                             '<= 64')
+        self.n, self.w, self.V = n, w, V
+        self.cap = _pow2_at_least(max(2 * int(capacidad), 2))
+        self.slots = torch.full((filas, self.cap), -1, dtype=torch.int64, device=dev)     # all ones: empty
+
+    def agregar_texto(self, x):
+        """Every n-gram of the rows of x (filas, L) int64."""
+        dev = _dev(x)
+        if x.dim() != 2 or x.dtype != torch.int64 or x.shape[0] != self.slots.shape[0]:
+            raise ValueError('agregar_texto: x is (rows, L) int64 with one row per set')
+        x = x if x.stride(1) == 1 else x.contiguous()
+        if x.shape[1] > self.cap // 2:
+            raise ValueError(f'agregar_texto: {x.shape[1]} n-grams per row exceed the sets\' capacity')
+        call('asrn_ngram_set_build', ptr(x), x.stride(0), x.shape[0], x.shape[1], self.n, self.w, ptr(self.slots),
+             self.cap, stream_of(dev))
+
+
+def muestrear(lg, texto, pos, pos_max, L0, piezas, terminado, paso_fin, trabajo, bits_cita, temperatura, top_k,
+              top_p, pena, ventana, semilla, cita=None, prohibidas=None, parar_en=None, logits=None, prob=None):
+    """One token per row by asrn_sample: lg (B, V) fp32 logits (rows unit-strided), texto (B, cap) int64 (the token
+    is written at position pos: a one-element int64 device tensor, at most pos_max), piezas (B,) int64 out,
+    terminado (B,) uint8 and paso_fin (B,) int32 (stop flags and the step each row stopped at), trabajo (B, V) fp32 and
+    bits_cita (B, ceil(V/32)) int32 scratch; cita / prohibidas: ConjuntoNgramas or None; logits: (B, steps, V) fp32
+    receiving lg at step pos - L0; prob: (B, V) fp32 receiving the final probabilities."""
+    dev = _dev(lg, texto, pos)
+    B, V = lg.shape
+    if lg.dtype != torch.float32 or lg.stride(1) != 1 or texto.dtype != torch.int64 or texto.stride(1) != 1:
+        raise ValueError('muestrear: lg fp32 and texto int64, both with unit column stride')
+    if pos.dtype != torch.int64 or pos.numel() != 1:
+        raise ValueError('muestrear: pos is a one-element int64 device tensor')
+    if parar_en is not None and not 0 <= int(parar_en) < V:
+        raise ValueError(f'parar_en={parar_en}: a token id in [0, {V})')
+    for t, forma, tipo in ((piezas, (B,), torch.int64), (terminado, (B,), torch.uint8), (paso_fin, (B,), torch.int32),
+                           (trabajo, (B, V), torch.float32), (bits_cita, (B, (V + 31) // 32), torch.int32)):
+        if tuple(t.shape) != forma or t.dtype != tipo or not t.is_contiguous():
+            raise ValueError(f'muestrear: a buffer must be contiguous {tipo} of shape {forma}')
+    if logits is not None and (logits.dim() != 3 or logits.shape[0] != B or logits.shape[2] != V
+                               or logits.dtype != torch.float32 or not logits.is_contiguous()):
+        raise ValueError('muestrear: logits is a contiguous (B, steps, V) fp32 tensor')
+    if prob is not None and (tuple(prob.shape) != (B, V) or prob.dtype != torch.float32 or not prob.is_contiguous()):
+        raise ValueError('muestrear: prob is a contiguous (B, V) fp32 tensor')
+    w = bits_por_pieza(V)
+    for s in (cita, prohibidas):
+        if s is not None and (s.w != w or s.slots.shape[0] != B):
+            raise ValueError('muestrear: an n-gram set made for another vocabulary or batch')
+    semilla = int(semilla) & 0xFFFFFFFFFFFFFFFF
+    call('asrn_sample', ptr(lg), lg.stride(0), ptr(trabajo), ptr(bits_cita), ptr(prob), ptr(logits),
+         logits.shape[1] if logits is not None else 0, ptr(texto), texto.stride(0), ptr(pos), int(pos_max), int(L0),
+         ptr(piezas), ptr(terminado), ptr(paso_fin),
+         ptr(cita.slots) if cita else None, cita.cap if cita else 0, cita.n if cita else 0,
+         ptr(prohibidas.slots) if prohibidas else None, prohibidas.cap if prohibidas else 0,
+         prohibidas.n if prohibidas else 0, w, B, V, float(temperatura), int(top_k), float(top_p), float(pena),
+         int(ventana), -1 if parar_en is None else int(parar_en), ctypes.c_uint64(semilla), stream_of(dev))

@@ -13,7 +13,6 @@ import hashlib
 import json
 import os
 import sys
-import tempfile
 
 import torch
 from safetensors.torch import save_file
@@ -122,7 +121,7 @@ def build(ref_root):
     torch.manual_seed(0)
     m = asrn.crear_modelo(**CKPT)
     mover(m, v89._NUEVOS_V87, 9)
-    with tempfile.TemporaryDirectory() as tmp:
+    if True:
         p89 = os.path.join(HERE, 'ckpt_v89.pt')
         asrn.guardar(m, p89)
         r = torch.load(p89, map_location='cpu', weights_only=True)
@@ -149,8 +148,43 @@ def build(ref_root):
                        'ajustes': est['ajustes'], 'n_estado_opt': len(est['optimizador']['state']),
                        'grupos': [{k: v for k, v in g.items() if k != 'params'} | {'params': g['params']}
                                   for g in est['optimizador']['param_groups']]}, f, indent=1, sort_keys=True)
+    escritura(asrn, v89)
     for fn in sorted(os.listdir(HERE)):
         print(fn, os.path.getsize(os.path.join(HERE, fn)) // 1024, 'KiB')
+
+
+ESCRITURA = dict(V=60, d=32, n_capas=3, largo_cada=1, semilla=1, chunk=8, n_bits=3)
+
+
+def escritura(asrn, v89):
+    """The reference's O(1) writer (asrn/nucleo.py:1717-1854) on a teacher-forced text, with and without
+    memoria_de_lo_ajeno, the whole-text logits beside it, and one greedy escribir() (top_k=1, nucleo:1965-2043):
+    its tokens and the logits of every step."""
+    torch.manual_seed(0)
+    m = asrn.crear_modelo(**ESCRITURA)
+    mover(m, v89._NUEVOS_V87, 7)
+    m.eval()
+    B, L0, n = 2, 40, 24
+    g = torch.Generator().manual_seed(0)
+    x = torch.randint(0, ESCRITURA['V'], (B, L0 + n), generator=g)
+    x[:, 20:36] = x[:, 2:18].clone()
+    out = {'x': x}
+    with torch.no_grad():
+        for ajeno in (True, False):
+            esc = v89._Escritor(m, memoria_de_lo_ajeno=ajeno, o1=True)
+            lgs = [esc.inicio(x[:, :L0], capacidad=L0 + 3)] + [esc.paso(x[:, t]) for t in range(L0, L0 + n - 1)]
+            out['paso_ajeno' if ajeno else 'paso_todo'] = torch.stack(lgs, 1)
+        out['entero'] = m(x[:, :L0 + n - 1])[:, L0 - 1:].contiguous()
+        sec, pasos = asrn.escribir(m, x[:, :L0], n_nuevos=n, top_k=1, semilla=0)
+    out['greedy'] = sec
+    out['greedy_logits'] = pasos
+    save_file({k: v.contiguous() for k, v in out.items()}, os.path.join(HERE, 'escritura.safetensors'),
+              metadata={'kw': json.dumps(ESCRITURA), 'L0': str(L0), 'n': str(n)})
+    torch.manual_seed(0)
+    m2 = asrn.crear_modelo(**ESCRITURA)
+    mover(m2, v89._NUEVOS_V87, 7)
+    for k, v in m2.state_dict().items():
+        assert torch.equal(v, m.state_dict()[k])
 
 
 if __name__ == '__main__':

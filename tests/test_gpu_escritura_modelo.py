@@ -1,0 +1,279 @@
+"""Generation with the whole model on the GPU: the device sampler against the oracle's restatement of the reference's
+per-token choice, the model's O(1) step against the reference's writer (tests/golden/make_golden_modelo.py), and
+escribir against the reference's own tests of it (tests/test_nucleo.py:86-140, 632-639, 1237-1257).
+
+- ops.muestrear (asrn_sample): the final probability row equals oracle.muestreo's (penalty, bans with their fallback,
+  quote mask, temperature, top-k, top-p, the quote-mass correction) within fp32 rounding, with the same support;
+  the token lies in that support and is written into the text; the n-gram sets take the new n-grams (checked by a
+  second step against the oracle on the longer text); draws follow the distribution (chi-square) and repeat for a
+  seed.
+- EscritorModelo: teacher-forced logits equal the reference's O(1) writer's, with and without memoria_de_lo_ajeno, to
+  the reference's tolerance (1e-4); with every position a key they equal the whole-text model.
+- escribir: the logits of every step equal the whole-text model on the written text (tests/test_nucleo.py:105-115);
+  greedy tokens equal the reference's greedy run; the graphed loop equals the eagerly launched one; conservar_cita
+  changes nothing at temperature 1; edge cases and errors as the reference's.
+Each test prints its case first."""
+import json
+import os
+
+import pytest
+import torch
+from safetensors import safe_open
+
+import asrn_amd
+from asrn_amd import ops
+from oracle import muestreo as M
+
+pytestmark = pytest.mark.gpu
+DEV = 'cuda'
+AQUI = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden', 'modelo')
+TOL = 1e-4
+
+
+def say(*a):
+    print('[case]', *a, flush=True)
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip('needs a GPU')
+    asrn_amd.cargar_biblioteca()
+
+
+def _mover(m, seed):
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for n, p in m.named_parameters():
+            nuevo = n.rsplit('.', 1)[-1] in asrn_amd.archivo.NUEVOS_V87
+            p.add_(torch.randn(p.shape, generator=g) * (0.5 if nuevo else 0.05))
+        for c in m.largos:
+            c.gamma.abs_()
+    return m
+
+
+def _fixture():
+    with safe_open(os.path.join(AQUI, 'escritura.safetensors'), framework='pt') as f:
+        t = {k: f.get_tensor(k) for k in f.keys()}
+        meta = f.metadata()
+    kw = json.loads(meta['kw'])
+    torch.manual_seed(0)
+    m = _mover(asrn_amd.crear_modelo(**kw), 7).to(DEV).eval()
+    return t, m, int(meta['L0']), int(meta['n'])
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# the sampler kernel
+# ---------------------------------------------------------------------------------------------------------------------
+
+def _texto(B, L, V, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randint(0, V, (B, L), generator=g)
+    x[:, L // 2:L // 2 + L // 4] = x[:, :L // 4].clone()
+    return x
+
+
+class _Estado:
+    def __init__(self, B, V, total):
+        self.piezas = torch.zeros(B, dtype=torch.int64, device=DEV)
+        self.terminado = torch.zeros(B, dtype=torch.uint8, device=DEV)
+        self.paso_fin = torch.full((B,), -1, dtype=torch.int32, device=DEV)
+        self.trabajo = torch.empty((B, V), dtype=torch.float32, device=DEV)
+        self.bits = torch.empty((B, (V + 31) // 32), dtype=torch.int32, device=DEV)
+        self.prob = torch.empty((B, V), dtype=torch.float32, device=DEV)
+
+
+SAMPLER_CASES = [
+    dict(V=300, T=0.8, k=40, p=1.0, pena=1.0, ventana=64, nb=0, nq=0),
+    dict(V=300, T=1.0, k=0, p=0.9, pena=1.0, ventana=64, nb=0, nq=0),
+    dict(V=300, T=0.7, k=0, p=1.0, pena=1.3, ventana=16, nb=0, nq=0),
+    dict(V=300, T=0.9, k=50, p=0.95, pena=1.0, ventana=64, nb=2, nq=0),
+    dict(V=40, T=0.6, k=0, p=1.0, pena=1.0, ventana=64, nb=0, nq=4),
+    dict(V=40, T=0.5, k=10, p=0.8, pena=1.2, ventana=8, nb=3, nq=4),
+    dict(V=2, T=1.0, k=0, p=1.0, pena=1.0, ventana=64, nb=1, nq=0),
+    dict(V=50304, T=0.8, k=40, p=0.9, pena=1.1, ventana=64, nb=3, nq=4),
+    dict(V=1000, T=1.0, k=1, p=1.0, pena=1.0, ventana=64, nb=0, nq=4),
+    dict(V=1000, T=0.8, k=0, p=0.0, pena=1.0, ventana=64, nb=0, nq=0),
+]
+
+
+@pytest.mark.parametrize('c', SAMPLER_CASES, ids=lambda c: '-'.join(f'{k}{v}' for k, v in c.items()))
+def test_sampler_matches_oracle(c):
+    say('sampler', c)
+    B, L0, gen = 3, 50, 12
+    V = c['V']
+    pos = L0 + gen
+    x = _texto(B, pos + 2, V, 1 + V)
+    if V <= 2:
+        x[:, L0:] = torch.arange(x.shape[1] - L0) % 2          # every generated unigram seen: all banned
+    texto = x.to(DEV).contiguous()
+    g = torch.Generator().manual_seed(V)
+    est = _Estado(B, V, pos + 2)
+    cita = prohibidas = None
+    if c['nq']:
+        cita = ops.ConjuntoNgramas(B, c['nq'], V, pos + 2, DEV)
+        cita.agregar_texto(texto[:, :pos].contiguous())
+    if c['nb']:
+        prohibidas = ops.ConjuntoNgramas(B, c['nb'], V, pos + 2, DEV)
+        prohibidas.agregar_texto(texto[:, L0:pos].contiguous())
+    for paso in range(2):                                      # the second step sees the n-grams the first added
+        p_now = pos + paso
+        lg = (torch.randn(B, V, generator=g) * 3).to(DEV)
+        pdev = torch.tensor([p_now], dtype=torch.int64, device=DEV)
+        ops.muestrear(lg, texto, pdev, pos + 1, L0, est.piezas, est.terminado, est.paso_fin, est.trabajo, est.bits,
+                      c['T'], c['k'], c['p'], c['pena'], c['ventana'], 1234 + paso, cita=cita, prohibidas=prohibidas,
+                      prob=est.prob)
+        torch.cuda.synchronize()
+        prob = est.prob.cpu().double()
+        texto_cpu = texto.cpu()
+        for b in range(B):
+            t_b = texto_cpu[b, :p_now].tolist()
+            lgr = M.frenar(lg[b].cpu().double(), t_b, L0, c['pena'], c['ventana'], c['nb'])
+            q = M.probabilidades(lgr, c['T'], c['k'], c['p'], M.ngramas_siguientes(t_b, c['nq']) if c['nq'] else None)
+            assert set(torch.nonzero(prob[b] > 0).view(-1).tolist()) == set(torch.nonzero(q > 0).view(-1).tolist()), b
+            assert torch.allclose(prob[b], q, rtol=1e-4, atol=2e-6), (b, (prob[b] - q).abs().max())
+            tok = int(est.piezas[b])
+            assert q[tok] > 0 and int(texto_cpu[b, p_now]) == tok
+
+
+def test_sampler_distribution_and_seed():
+    say('sampler chi-square')
+    B, V = 512, 12
+    lg0 = torch.linspace(-2, 2, V)
+    lg = lg0.expand(B, V).contiguous().to(DEV)
+    esperado = torch.softmax(lg0.double() / 0.9, -1)
+    texto = torch.zeros((B, 4), dtype=torch.int64, device=DEV)
+    est = _Estado(B, V, 4)
+    pdev = torch.tensor([1], dtype=torch.int64, device=DEV)
+    cuentas = torch.zeros(V, dtype=torch.float64)
+    for s in range(20):
+        ops.muestrear(lg, texto, pdev, 2, 1, est.piezas, est.terminado, est.paso_fin, est.trabajo, est.bits, 0.9, 0,
+                      1.0, 1.0, 64, s)
+        cuentas += torch.bincount(est.piezas.cpu(), minlength=V).double()
+    n = cuentas.sum()
+    chi2 = float(((cuentas - n * esperado) ** 2 / (n * esperado)).sum())
+    print('chi2', chi2, 'draws', int(n), flush=True)
+    assert chi2 < 45.0                               # 11 degrees of freedom: p < 1e-5 above 45
+    a = est.piezas.clone()
+    ops.muestrear(lg, texto, pdev, 2, 1, est.piezas, est.terminado, est.paso_fin, est.trabajo, est.bits, 0.9, 0, 1.0,
+                  1.0, 64, 19)
+    assert torch.equal(a, est.piezas)
+    ops.muestrear(lg, texto, pdev, 2, 1, est.piezas, est.terminado, est.paso_fin, est.trabajo, est.bits, 0.9, 0, 1.0,
+                  1.0, 64, 20)
+    assert not torch.equal(a, est.piezas)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# the model's step and escribir
+# ---------------------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize('ajeno', [True, False])
+def test_model_writer_matches_reference_writer(ajeno):
+    say('EscritorModelo teacher-forced, ajeno', ajeno)
+    t, m, L0, n = _fixture()
+    x = t['x'].to(DEV)
+    esc = asrn_amd.EscritorModelo(m, memoria_de_lo_ajeno=ajeno)
+    with torch.no_grad():
+        lgs = [esc.inicio(x[:, :L0], capacidad=L0 + 3)] + [esc.paso(x[:, k]) for k in range(L0, L0 + n - 1)]
+    got = torch.stack(lgs, 1).cpu()
+    ref = t['paso_ajeno' if ajeno else 'paso_todo']
+    err = (got - ref).abs().max().item()
+    print('max |hip - reference writer|', err, flush=True)
+    assert err < TOL
+    if not ajeno:
+        assert (got - t['entero']).abs().max().item() < TOL
+
+
+@pytest.mark.parametrize('mezcla', ['conv', 'memoria'])
+def test_escribir_equals_whole_text(mezcla):
+    """tests/test_nucleo.py:105-115: the logits of every step equal the model on the whole written text."""
+    say('escribir vs whole text', mezcla)
+    torch.manual_seed(1)
+    kw = dict(mezcla=mezcla, memoria_max=64) if mezcla == 'memoria' else {}
+    m = _mover(asrn_amd.crear_modelo(60, d=32, n_capas=3, largo_cada=1, semilla=1, chunk=8, n_bits=3, **kw), 3)
+    m = m.to(DEV).eval()
+    x0 = _texto(2, 40, 60, 0).to(DEV)
+    for grafo in (True, False):
+        sec, pasos = asrn_amd.escribir(m, x0, n_nuevos=60, memoria_de_lo_ajeno=False, top_k=0, grafo=grafo)
+        with torch.no_grad():
+            entero = m(sec[:, :-1].to(DEV))[:, 40 - 1:].cpu()
+        err = (entero - pasos).abs().max().item()
+        print('grafo', grafo, 'max |step - whole text|', err, flush=True)
+        assert sec.shape == (2, 100) and pasos.shape == (2, 60, 60)
+        assert err < TOL
+
+
+def test_greedy_tokens_match_reference():
+    say('greedy vs reference')
+    t, m, L0, n = _fixture()
+    sec, pasos = asrn_amd.escribir(m, t['x'][:, :L0], n_nuevos=n, top_k=1, semilla=0)
+    print(sec[:, L0:].tolist(), flush=True)
+    assert torch.equal(sec, t['greedy'])
+    assert (pasos - t['greedy_logits']).abs().max().item() < TOL
+
+
+def test_graph_loop_equals_eager_loop():
+    say('escribir graph vs eager, every option on')
+    t, m, L0, n = _fixture()
+    kw = dict(n_nuevos=48, temperatura=0.8, top_k=20, top_p=0.9, semilla=3, pena_repeticion=1.2, ventana_pena=16,
+              no_repetir_ngramas=3, conservar_cita=True)
+    a, la = asrn_amd.escribir(m, t['x'][:, :L0], grafo=True, **kw)
+    b, lb = asrn_amd.escribir(m, t['x'][:, :L0], grafo=False, **kw)
+    assert torch.equal(a, b) and torch.equal(la, lb)
+    # no 3-gram of the generated part repeats
+    for fila in a[:, L0:].tolist():
+        grupos = [tuple(fila[i:i + 3]) for i in range(len(fila) - 2)]
+        assert len(grupos) == len(set(grupos))
+
+
+def test_quote_correction_changes_nothing_at_temperature_one():
+    """tests/test_nucleo.py:632-639."""
+    say('conservar_cita at T=1')
+    t, m, L0, n = _fixture()
+    a, _ = asrn_amd.escribir(m, t['x'][:, :L0], n_nuevos=30, temperatura=1.0, top_k=0, semilla=5, conservar_cita=True)
+    b, _ = asrn_amd.escribir(m, t['x'][:, :L0], n_nuevos=30, temperatura=1.0, top_k=0, semilla=5, conservar_cita=False)
+    assert torch.equal(a, b)
+
+
+def test_stop_token():
+    say('parar_en')
+    t, m, L0, n = _fixture()
+    x0 = t['x'][:, :L0]
+    libre, _ = asrn_amd.escribir(m, x0, n_nuevos=40, temperatura=1.5, top_k=0, semilla=2)
+    parar = int(libre[0, L0 + 3])                      # a token the first row writes early
+    sec, pasos = asrn_amd.escribir(m, x0, n_nuevos=40, temperatura=1.5, top_k=0, semilla=2, parar_en=parar)
+    gen = sec[:, L0:]
+    primeros = []
+    for fila in gen.tolist():
+        i = fila.index(parar) if parar in fila else None
+        primeros.append(i)
+        if i is not None:
+            assert all(v == parar for v in fila[i:])
+    assert primeros[0] is not None and primeros[0] <= 3
+    if all(i is not None for i in primeros):
+        assert gen.shape[1] == max(primeros) + 1 and pasos.shape[1] == gen.shape[1]
+    else:
+        assert gen.shape[1] == 40
+
+
+def test_escribir_edge_cases():
+    """tests/test_nucleo.py:86-103, 1237-1257."""
+    say('escribir edge cases')
+    m = asrn_amd.crear_modelo(2, d=16, n_capas=2, semilla=0).to(DEV)
+    m.train()
+    s, _ = asrn_amd.escribir(m, torch.tensor([[1]]), n_nuevos=12, no_repetir_ngramas=1)
+    assert s.shape == (1, 13) and m.training
+    s, _ = asrn_amd.escribir(m, torch.tensor([[1, 0]]), n_nuevos=4, top_p=0.0)
+    assert s.shape == (1, 6)
+    s, lg = asrn_amd.escribir(m, torch.tensor([1, 0, 1]), n_nuevos=0)
+    assert s.shape == (1, 3) and lg.shape == (1, 0, 2)
+    s, lg = asrn_amd.escribir(m, torch.tensor([[1, 0]]), n_nuevos=3, devolver_logits=False)
+    assert s.shape == (1, 5) and lg is None
+    with pytest.raises(ValueError, match=r'outside \[0, 2\)'):
+        asrn_amd.escribir(m, torch.tensor([[5]]), n_nuevos=2)
+    with pytest.raises(AssertionError):
+        asrn_amd.escribir(m, torch.zeros(1, 0, dtype=torch.long), n_nuevos=5)
+    assert m.training
+    m16 = asrn_amd.crear_modelo(30, d=16, n_capas=2, semilla=0).to(DEV).to(torch.bfloat16)
+    with pytest.raises(ValueError, match='autocast'):
+        asrn_amd.escribir(m16, torch.tensor([[1, 2]]), n_nuevos=2)
