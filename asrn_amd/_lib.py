@@ -63,10 +63,11 @@ SIGNATURES = {
     'asrn_hawkes_table_grow': (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _P, _P, _I64, _P]),
     'asrn_repetition_step': (ctypes.c_int, [_P] * 7 + [_I64, _I64, _I64, _P, _I32, _I64] + [_P] * 7),
     'asrn_sample_bits': (_I32, [_I64]),
-    'asrn_ngram_set_build': (ctypes.c_int, [_P, _I64, _I64, _I64, _I32, _I32, _P, _I64, _P]),
-    'asrn_sample': (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _P, _P, _P, _P, _I64, _I32,
-                                   _P, _I64, _I32, _I32, _I64, _I64, _F32, _I32, _F32, _F32, _I32, _I64,
-                                   ctypes.c_uint64, _P]),
+    'asrn_ngram_set_successors': (_I32, []),
+    'asrn_ngram_set_build': (ctypes.c_int, [_P, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _P, _I64, _P]),
+    'asrn_sample': (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _P, _P, _P]
+                    + [_P, _P, _P, _P, _I64, _I32] * 2
+                    + [_I32, _I64, _I64, _F32, _I32, _F32, _F32, _I32, _I64, ctypes.c_uint64, _P]),
     'asrn_decode_produce_workspace': (ctypes.c_int64, [_I64, _I32, _I32]),
     'asrn_decode_produce': (ctypes.c_int, [_P] * 4 + [_I64, _I32] + [_P] * 9 + [_I32] * 4 + [_P, _P, _F32, _P, _P, _F32,
                                                                                               _F32, _P, _P, _I32]

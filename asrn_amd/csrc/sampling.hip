@@ -4,18 +4,22 @@
 // apiece, the oldest token in the lowest bits. w is asrn_sample_bits(V), the smallest width whose all-ones field is
 // above every token id, so no key is the all-ones word that marks an empty slot. Inserting is then one 64-bit
 // compare-and-swap that claims and publishes the key at once: concurrent inserts of one n-gram meet in one slot, and
-// no thread ever waits on another. Tables hold at most half their slots, so probes stay short, and every probe loop
-// ends within `cap` steps.
+// no thread ever waits on another. Beside it, a table of contexts (the n-gram minus its last token) holds each
+// context's distinct successors, up to kSucc of them inline with a count: a successor is appended only by the insert
+// that added its n-gram, so the list has no repeats, and a context whose count passes kSucc is answered by probing
+// every token instead. Tables hold at most half their slots, so probes stay short, and every probe loop ends within
+// `cap` steps.
 //
 // asrn_sample: one workgroup per text row makes the reference's whole per-token decision of escribir
 // (asrn/nucleo.py:2017-2036) with no host round trip:
 //   the repetition penalty over the last `window` tokens and the n-gram bans (_frenar, nucleo:1909-1918), with the
 //   fallback to the plain logits when the bans leave nothing (nucleo:2020-2021); the quote mask (_Ngramas.siguientes,
 //   nucleo:1877-1889); temperature, top-k and top-p (_muestrear, nucleo:1946-1962: the k-th largest logit and the
-//   top-p cut are found by radix selection over the values' bits, counts and fixed-point masses in LDS, instead of a
-//   sort); the softmax and the quote-mass correction (_conservar_cita, nucleo:1933-1943); one draw by inverse CDF
-//   with a counter-based uniform (seed, row, position); the stop token (nucleo:2026-2028); then the token is written
-//   into the text and its n-grams into the sets (_Ngramas.agregar, nucleo:1872-1875).
+//   top-p cut are found by radix selection over the values' bits, with counts and fixed-point masses in LDS, each
+//   wavefront adding once per distinct bin, instead of a sort); the softmax and the quote-mass correction
+//   (_conservar_cita, nucleo:1933-1943); one draw by inverse CDF with a counter-based uniform (seed, row, position);
+//   the stop token (nucleo:2026-2028); then the token is written into the text and its n-grams into the sets
+//   (_Ngramas.agregar, nucleo:1872-1875).
 // Every reduction runs in a fixed order: the same inputs and seed give the same token.
 #include "common.h"
 
@@ -25,6 +29,7 @@ namespace {
 constexpr unsigned long long kEmptySlot = ~0ull;
 constexpr int kSampleThreads = 1024;
 constexpr int kSampleWaves = kSampleThreads / kWave;
+constexpr int kSucc = 8;                         // successors held inline per context
 constexpr double kMassScale = 1099511627776.0;   // 2^40: fixed-point probability masses (sums stay below 2^63)
 
 // SplitMix64's output function (G. Steele, D. Lea, C. Flood, "Fast splittable pseudorandom number generators",
@@ -39,33 +44,44 @@ __device__ __forceinline__ uint64_t mix64(uint64_t x) {
 }
 
 struct TupleSet {
-  unsigned long long* slots;   // (rows, cap); nullptr: the set is not used
+  unsigned long long* slots;   // (rows, cap) n-gram keys; nullptr: the set is not used
+  unsigned long long* ctx;     // (rows, cap) context keys
+  int32_t* count;              // (rows, cap) distinct successors per context
+  int32_t* succ;               // (rows, cap, kSucc) the first kSucc of them
   int64_t cap;                 // power of two
-  int32_t n;                   // tokens per key
+  int32_t n;                   // tokens per n-gram
 };
 
-__device__ __forceinline__ bool set_has(const TupleSet& s, int64_t row, uint64_t key) {
-  const unsigned long long* t = s.slots + row * s.cap;
-  const uint64_t m = (uint64_t)s.cap - 1;
+__device__ __forceinline__ int64_t slot_of(const unsigned long long* t, int64_t cap, uint64_t key) {
+  const uint64_t m = (uint64_t)cap - 1;
   uint64_t i = mix64(key) & m;
-  for (int64_t p = 0; p < s.cap; ++p) {
+  for (int64_t p = 0; p < cap; ++p) {
     const unsigned long long v = t[i];
-    if (v == key) return true;
-    if (v == kEmptySlot) return false;
+    if (v == key) return (int64_t)i;
+    if (v == kEmptySlot) return -1;
     i = (i + 1) & m;
   }
-  return false;
+  return -1;
 }
 
-__device__ __forceinline__ void set_add(const TupleSet& s, int64_t row, uint64_t key) {
-  unsigned long long* t = s.slots + row * s.cap;
-  const uint64_t m = (uint64_t)s.cap - 1;
+// the slot holding `key` after the call, and whether this call put it there (-1: the table is full)
+__device__ __forceinline__ int64_t slot_add(unsigned long long* t, int64_t cap, uint64_t key, bool* nuevo) {
+  const uint64_t m = (uint64_t)cap - 1;
   uint64_t i = mix64(key) & m;
-  for (int64_t p = 0; p < s.cap; ++p) {
+  for (int64_t p = 0; p < cap; ++p) {
     const unsigned long long prev = atomicCAS(t + i, kEmptySlot, (unsigned long long)key);
-    if (prev == kEmptySlot || prev == key) return;
+    if (prev == kEmptySlot || prev == key) {
+      *nuevo = prev == kEmptySlot;
+      return (int64_t)i;
+    }
     i = (i + 1) & m;
   }
+  *nuevo = false;
+  return -1;
+}
+
+__device__ __forceinline__ bool set_has(const TupleSet& s, int64_t row, uint64_t key) {
+  return slot_of(s.slots + row * s.cap, s.cap, key) >= 0;
 }
 
 // tokens x[0..n-1] packed w bits apiece, x[0] lowest
@@ -75,19 +91,31 @@ __device__ __forceinline__ uint64_t pack(const int64_t* x, int n, int w) {
   return k;
 }
 
+// the n-gram x[0..n-1] into row `row`'s set and, when new, its last token into its context's successors
+__device__ __forceinline__ void ngram_add(const TupleSet& s, int64_t row, const int64_t* x, int w) {
+  const uint64_t ctx = pack(x, s.n - 1, w);
+  const uint64_t key = ctx | ((uint64_t)x[s.n - 1] << (w * (s.n - 1)));
+  bool nuevo;
+  if (slot_add(s.slots + row * s.cap, s.cap, key, &nuevo) < 0 || !nuevo) return;
+  const int64_t c = slot_add(s.ctx + row * s.cap, s.cap, ctx, &nuevo);
+  if (c < 0) return;
+  const int64_t e = row * s.cap + c;
+  const int k = atomicAdd(s.count + e, 1);
+  if (k < kSucc) s.succ[e * kSucc + k] = (int32_t)x[s.n - 1];
+}
+
 __global__ void k_set_build(const int64_t* __restrict__ x, int64_t ldx, int64_t rows, int64_t L, TupleSet s, int w) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= rows * L) return;
   const int64_t b = i / L, t = i - b * L;
   if (t < s.n - 1) return;
-  set_add(s, b, pack(x + b * ldx + t - (s.n - 1), s.n, w));
+  ngram_add(s, b, x + b * ldx + t - (s.n - 1), w);
 }
 
 // ---- block reductions over the 1024 threads (fixed order: deterministic) ----------------------------------------
 
 struct Red {
   float f[kSampleWaves];
-  unsigned long long u[kSampleWaves];
 };
 
 __device__ __forceinline__ float block_sum(float v, Red& r) {
@@ -114,17 +142,35 @@ __device__ __forceinline__ float block_max(float v, Red& r) {
   return s;
 }
 
-__device__ __forceinline__ unsigned long long block_sum_u(unsigned long long v, Red& r) {
+// histogram adds aggregated over the wavefront: one LDS atomic per distinct bin among the valid lanes (every lane of
+// the wavefront must call it together)
+__device__ __forceinline__ void hist_count(unsigned int* h, uint32_t bin, bool valid) {
+  uint64_t todo = __ballot(valid);
+  while (todo) {
+    const int leader = __ffsll((unsigned long long)todo) - 1;
+    const uint32_t lb = (uint32_t)__builtin_amdgcn_readlane((int)bin, leader);
+    const uint64_t same = __ballot(valid && bin == lb) & todo;
+    if (lane_id() == leader) atomicAdd(h + lb, (unsigned int)__popcll(same));
+    todo &= ~same;
+  }
+}
+
+__device__ __forceinline__ void hist_mass(unsigned int* h, unsigned long long* hm, uint32_t bin, bool valid,
+                                          unsigned long long q) {
+  uint64_t todo = __ballot(valid);
+  while (todo) {
+    const int leader = __ffsll((unsigned long long)todo) - 1;
+    const uint32_t lb = (uint32_t)__builtin_amdgcn_readlane((int)bin, leader);
+    const uint64_t same = __ballot(valid && bin == lb) & todo;
+    unsigned long long part = ((same >> lane_id()) & 1ull) ? q : 0ull;
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  const int w = threadIdx.x / kWave;
-  __syncthreads();
-  if (lane_id() == 0) r.u[w] = v;
-  __syncthreads();
-  unsigned long long s = 0;
-#pragma unroll
-  for (int i = 0; i < kSampleWaves; ++i) s += r.u[i];
-  return s;
+    for (int m = 32; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
+    if (lane_id() == leader) {
+      atomicAdd(h + lb, (unsigned int)__popcll(same));
+      atomicAdd(hm + lb, part);
+    }
+    todo &= ~same;
+  }
 }
 
 // float -> unsigned key with the same order (NaN above +inf)
@@ -140,7 +186,7 @@ struct SampleArgs {
   const float* lg;
   int64_t ldl;
   float* work;                 // (B, V): the logits after penalty and bans
-  uint32_t* quote_bits;        // (B, ceil(V / 32))
+  uint32_t* quote_bits;        // (B, ceil(V / 32)), used when a context has more than kSucc successors
   float* prob_out;             // (B, V) or nullptr: the final probabilities
   float* logits_out;           // (B, steps, V) or nullptr: the logits as they came, at step pos - L0
   int64_t steps;
@@ -161,13 +207,35 @@ struct SampleArgs {
   uint64_t seed;
 };
 
+// The successors of the context text[pos - n + 1 .. pos - 1] in row b's set: *n_list < 0 when the context has more
+// than kSucc of them (then the caller probes every token); list[0 .. *n_list) otherwise. One thread calls it.
+__device__ __forceinline__ void successors(const TupleSet& s, int64_t b, const int64_t* text, int64_t pos, int w,
+                                           int* list, int* n_list) {
+  const uint64_t ctx = pack(text + pos - (s.n - 1), s.n - 1, w);
+  const int64_t c = slot_of(s.ctx + b * s.cap, s.cap, ctx);
+  if (c < 0) {
+    *n_list = 0;
+    return;
+  }
+  const int64_t e = b * s.cap + c;
+  const int k = s.count[e];
+  if (k > kSucc) {
+    *n_list = -1;
+    return;
+  }
+  for (int i = 0; i < k; ++i) list[i] = s.succ[e * kSucc + i];
+  *n_list = k;
+}
+
 __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   __shared__ Red red;
   __shared__ unsigned int hist_n[256];
   __shared__ unsigned long long hist_m[256];
-  __shared__ uint32_t sel[4];          // radix results: [0] prefix, [1] flag
+  __shared__ uint32_t sel[2];          // radix results: [0] digit, [1] rank left / found
   __shared__ float scan[kSampleThreads];
   __shared__ int pick[2];
+  __shared__ int qlist[kSucc], blist[kSucc];
+  __shared__ int nq_list, nb_list;
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.x;
   const int64_t pos = *a.pos_dev;
@@ -178,6 +246,14 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   int64_t* text = a.text + b * a.ld_text;
   const int64_t step = pos - a.L0;
   const float ninf = -INFINITY;
+  const int nq = a.quote.n, nb = a.ban.n;
+  const bool quote = a.quote.slots && pos >= nq;
+  const bool bans = a.ban.slots && pos - a.L0 >= nb;
+  if (tid == 0) {
+    nq_list = nb_list = 0;
+    if (quote) successors(a.quote, b, text, pos, a.w, qlist, &nq_list);
+    if (bans) successors(a.ban, b, text, pos, a.w, blist, &nb_list);
+  }
 
   // penalty (_frenar): the logits as they came, then the tokens of the window penalized from those same values
   float* lout = (a.logits_out && step >= 0 && step < a.steps) ? a.logits_out + (b * a.steps + step) * V : nullptr;
@@ -198,12 +274,15 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   }
   __syncthreads();
   // bans: tokens that would close an n-gram already generated (only generated tokens count)
-  const int nb = a.ban.n;
-  if (a.ban.slots && pos - a.L0 >= nb) {
-    const uint64_t base = pack(text + pos - (nb - 1), nb - 1, a.w);
-    const int sh = a.w * (nb - 1);
-    for (int64_t v = tid; v < V; v += kSampleThreads)
-      if (set_has(a.ban, b, base | ((uint64_t)v << sh))) work[v] = ninf;
+  if (bans) {
+    if (nb_list >= 0) {
+      if (tid < nb_list) work[blist[tid]] = ninf;
+    } else {
+      const uint64_t base = pack(text + pos - (nb - 1), nb - 1, a.w);
+      const int sh = a.w * (nb - 1);
+      for (int64_t v = tid; v < V; v += kSampleThreads)
+        if (set_has(a.ban, b, base | ((uint64_t)v << sh))) work[v] = ninf;
+    }
   }
   __syncthreads();
   {
@@ -217,11 +296,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   __syncthreads();
 
   // quote mask and its mass at temperature 1 (_conservar_cita's p1)
-  const int nq = a.quote.n;
-  const bool quote = a.quote.slots && pos >= nq;
   uint32_t* qbits = a.quote_bits + b * ((V + 31) / 32);
-  float mass_p = 0.f;
-  if (quote) {
+  const bool qprobe = quote && nq_list < 0;
+  if (qprobe) {
     const uint64_t base = pack(text + pos - (nq - 1), nq - 1, a.w);
     const int sh = a.w * (nq - 1);
     for (int64_t wd = tid; wd < (V + 31) / 32; wd += kSampleThreads) {
@@ -233,6 +310,17 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
       qbits[wd] = bits;
     }
     __syncthreads();
+  }
+  const int nql = quote && !qprobe ? nq_list : 0;
+  auto in_quote = [&](int64_t v) {
+    if (!quote) return false;
+    if (qprobe) return ((qbits[v >> 5] >> (v & 31)) & 1u) != 0u;
+    for (int i = 0; i < nql; ++i)
+      if (qlist[i] == v) return true;
+    return false;
+  };
+  float mass_p = 0.f;
+  if (quote && (qprobe || nql > 0)) {
     float m = ninf;
     for (int64_t v = tid; v < V; v += kSampleThreads) m = fmaxf(m, work[v]);
     const float m1 = block_max(m, red);
@@ -240,25 +328,26 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     for (int64_t v = tid; v < V; v += kSampleThreads) {
       const float e = expf(work[v] - m1);
       s += e;
-      if ((qbits[v >> 5] >> (v & 31)) & 1u) c += e;
+      if (qprobe && in_quote(v)) c += e;
     }
+    if (!qprobe && tid < nql) c = expf(work[qlist[tid]] - m1);
     const float S1 = block_sum(s, red);
     mass_p = block_sum(c, red) / S1;
   }
-  auto in_quote = [&](int64_t v) { return quote && ((qbits[v >> 5] >> (v & 31)) & 1u); };
 
   // temperature and top-k: keep the logits >= the k-th largest
-  const float tinv_den = fmaxf(a.temperature, 1e-6f);
-  auto l3 = [&](int64_t v) { return work[v] / tinv_den; };
+  const float tden = fmaxf(a.temperature, 1e-6f);
+  auto l3 = [&](int64_t v) { return work[v] / tden; };
   float corte = ninf;
   if (a.top_k > 0 && (int64_t)a.top_k < V) {
     uint32_t prefix = 0, mask = 0, rest = (uint32_t)a.top_k;
     for (int shift = 24; shift >= 0; shift -= 8) {
       for (int i = tid; i < 256; i += kSampleThreads) hist_n[i] = 0;
       __syncthreads();
-      for (int64_t v = tid; v < V; v += kSampleThreads) {
-        const uint32_t k = ordered(l3(v));
-        if ((k & mask) == prefix) atomicAdd(&hist_n[(k >> shift) & 255u], 1u);
+      for (int64_t base = 0; base < V; base += kSampleThreads) {
+        const int64_t v = base + tid;
+        const uint32_t k = v < V ? ordered(l3(v)) : 0u;
+        hist_count(hist_n, (k >> shift) & 255u, v < V && (k & mask) == prefix);
       }
       __syncthreads();
       if (tid == 0) {
@@ -306,15 +395,18 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
         hist_m[i] = 0;
       }
       __syncthreads();
-      for (int64_t v = tid; v < V; v += kSampleThreads) {
-        const float x = l3(v);
-        if (!kept_k(x)) continue;
-        const float p = expf(x - m3) / S3;
-        const uint32_t k = __float_as_uint(p);
-        if ((k & mask) == prefix) {
-          atomicAdd(&hist_n[(k >> shift) & 255u], 1u);
-          atomicAdd(&hist_m[(k >> shift) & 255u], (unsigned long long)rint((double)p * kMassScale));
+      for (int64_t base = 0; base < V; base += kSampleThreads) {
+        const int64_t v = base + tid;
+        float p = 0.f;
+        bool in = false;
+        if (v < V) {
+          const float x = l3(v);
+          in = kept_k(x);
+          if (in) p = expf(x - m3) / S3;
         }
+        const uint32_t k = __float_as_uint(p);
+        hist_mass(hist_n, hist_m, (k >> shift) & 255u, in && (k & mask) == prefix,
+                  (unsigned long long)rint((double)p * kMassScale));
       }
       __syncthreads();
       if (tid == 0) {
@@ -354,11 +446,13 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     S4 = block_sum(s, red);
   }
   float sc_q = 1.f, sc_n = 1.f;
-  if (quote) {
-    float c = 0.f;
-    for (int64_t v = tid; v < V; v += kSampleThreads) {
-      float e;
-      if (keep(v, &e) && in_quote(v)) c += e / S4;
+  if (quote && (qprobe || nql > 0)) {
+    float c = 0.f, e;
+    if (qprobe) {
+      for (int64_t v = tid; v < V; v += kSampleThreads)
+        if (in_quote(v) && keep(v, &e)) c += e / S4;
+    } else if (tid < nql && keep(qlist[tid], &e)) {
+      c = e / S4;
     }
     const float mass_q = block_sum(c, red);
     if (mass_q > 0.f && mass_q < 1.f) {
@@ -366,11 +460,12 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
       sc_n = (1.f - mass_p) / fmaxf(1.f - mass_q, 1e-30f);
     }
   }
+  const bool scaled = sc_q != 1.f || sc_n != 1.f;
   auto prob = [&](int64_t v) {
     float e;
     if (!keep(v, &e)) return 0.f;
     const float p = e / S4;
-    return quote ? p * (in_quote(v) ? sc_q : sc_n) : p;
+    return scaled ? p * (in_quote(v) ? sc_q : sc_n) : p;
   };
   if (a.prob_out) {
     for (int64_t v = tid; v < V; v += kSampleThreads) a.prob_out[b * V + v] = prob(v);
@@ -378,7 +473,8 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
 
   // the draw: inverse CDF over the tokens in index order, each thread a contiguous segment
   const int64_t seg = (V + kSampleThreads - 1) / kSampleThreads;
-  const int64_t v0 = (int64_t)tid * seg, v1 = v0 + seg < V ? v0 + seg : V;
+  const int64_t v0 = (int64_t)tid * seg < V ? (int64_t)tid * seg : V;
+  const int64_t v1 = v0 + seg < V ? v0 + seg : V;
   float local = 0.f;
   int64_t last_pos = -1;
   for (int64_t v = v0; v < v1; ++v) {
@@ -429,16 +525,18 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     }
     text[pos] = tok;
     a.tokens[b] = tok;
-    if (a.quote.slots && pos + 1 >= nq) set_add(a.quote, b, pack(text + pos - (nq - 1), nq, a.w));
-    if (a.ban.slots && pos + 1 - a.L0 >= nb) set_add(a.ban, b, pack(text + pos - (nb - 1), nb, a.w));
+    if (a.quote.slots && pos + 1 >= nq) ngram_add(a.quote, b, text + pos - (nq - 1), a.w);
+    if (a.ban.slots && pos + 1 - a.L0 >= nb) ngram_add(a.ban, b, text + pos - (nb - 1), a.w);
   }
 }
 
-int check_set(const char* what, const unsigned long long* slots, int64_t cap, int32_t n, int32_t w) {
-  if (!slots) return 0;
-  ASRN_REQUIRE(cap >= 2 && (cap & (cap - 1)) == 0, "%s: the set's capacity %lld must be a power of two", what,
-               (long long)cap);
-  ASRN_REQUIRE(n >= 1 && (int64_t)n * w <= 64, "%s: n=%d tokens of %d bits do not fit a 64-bit key", what, n, w);
+int check_set(const char* what, const TupleSet& s, int32_t w) {
+  if (!s.slots) return 0;
+  ASRN_REQUIRE(s.ctx && s.count && s.succ, "%s: a set needs its context, count and successor tables", what);
+  ASRN_REQUIRE(s.cap >= 2 && (s.cap & (s.cap - 1)) == 0, "%s: the set's capacity %lld must be a power of two", what,
+               (long long)s.cap);
+  ASRN_REQUIRE(s.n >= 1 && (int64_t)s.n * w <= 64, "%s: n=%d tokens of %d bits do not fit a 64-bit key", what, s.n,
+               w);
   return 0;
 }
 
@@ -454,17 +552,20 @@ extern "C" int32_t asrn_sample_bits(int64_t V) {
   return w;
 }
 
+extern "C" int32_t asrn_ngram_set_successors(void) { return kSucc; }
+
 extern "C" int asrn_ngram_set_build(const int64_t* x, int64_t ldx, int64_t rows, int64_t L, int32_t n, int32_t w,
-                                    uint64_t* slots, int64_t cap, void* stream) {
+                                    uint64_t* slots, uint64_t* ctx, int32_t* count, int32_t* succ, int64_t cap,
+                                    void* stream) {
   ASRN_REQUIRE(rows >= 0 && L >= 0 && ldx >= L, "asrn_ngram_set_build: bad sizes rows=%lld L=%lld ldx=%lld",
                (long long)rows, (long long)L, (long long)ldx);
   ASRN_REQUIRE(slots != nullptr, "asrn_ngram_set_build: null table");
-  if (int rc = check_set("asrn_ngram_set_build", (const unsigned long long*)slots, cap, n, w)) return rc;
+  TupleSet s{(unsigned long long*)slots, (unsigned long long*)ctx, count, succ, cap, n};
+  if (int rc = check_set("asrn_ngram_set_build", s, w)) return rc;
   ASRN_REQUIRE(L <= cap / 2, "asrn_ngram_set_build: %lld n-grams per row need a capacity of at least %lld (got %lld)",
                (long long)L, (long long)(2 * L), (long long)cap);
   const int64_t total = rows * L;
   if (total == 0) return 0;
-  TupleSet s{(unsigned long long*)slots, cap, n};
   const int threads = 256;
   hipLaunchKernelGGL(k_set_build, dim3((unsigned)((total + threads - 1) / threads)), dim3(threads), 0,
                      (hipStream_t)stream, x, ldx, rows, L, s, w);
@@ -474,10 +575,11 @@ extern "C" int asrn_ngram_set_build(const int64_t* x, int64_t ldx, int64_t rows,
 extern "C" int asrn_sample(const float* lg, int64_t ldl, float* work, uint32_t* quote_bits, float* prob_out,
                            float* logits_out, int64_t steps, int64_t* text, int64_t ld_text, const int64_t* pos_dev,
                            int64_t pos_max, int64_t L0, int64_t* tokens, uint8_t* done, int32_t* stop_step,
-                           uint64_t* quote_slots, int64_t quote_cap, int32_t quote_n, uint64_t* ban_slots,
-                           int64_t ban_cap, int32_t ban_n, int32_t w, int64_t B, int64_t V, float temperature,
-                           int32_t top_k, float top_p, float penalty, int32_t window, int64_t stop_token, uint64_t seed,
-                           void* stream) {
+                           uint64_t* quote_slots, uint64_t* quote_ctx, int32_t* quote_count, int32_t* quote_succ,
+                           int64_t quote_cap, int32_t quote_n, uint64_t* ban_slots, uint64_t* ban_ctx,
+                           int32_t* ban_count, int32_t* ban_succ, int64_t ban_cap, int32_t ban_n, int32_t w, int64_t B,
+                           int64_t V, float temperature, int32_t top_k, float top_p, float penalty, int32_t window,
+                           int64_t stop_token, uint64_t seed, void* stream) {
   ASRN_REQUIRE(B >= 1 && V >= 1 && V <= (int64_t(1) << 31) && ldl >= V, "asrn_sample: bad sizes B=%lld V=%lld",
                (long long)B, (long long)V);
   ASRN_REQUIRE(B <= (int64_t(1) << 20), "asrn_sample: at most 2^20 rows");
@@ -487,9 +589,12 @@ extern "C" int asrn_sample(const float* lg, int64_t ldl, float* work, uint32_t* 
   ASRN_REQUIRE(window >= 0 && top_k >= 0 && penalty > 0.f, "asrn_sample: window, top_k >= 0 and penalty > 0");
   ASRN_REQUIRE(w == asrn_sample_bits(V), "asrn_sample: w=%d must be asrn_sample_bits(V)=%d", w, asrn_sample_bits(V));
   ASRN_REQUIRE(logits_out == nullptr || steps >= 1, "asrn_sample: logits_out needs steps >= 1");
-  if (int rc = check_set("asrn_sample (quote)", (const unsigned long long*)quote_slots, quote_cap, quote_n, w)) return rc;
-  if (int rc = check_set("asrn_sample (bans)", (const unsigned long long*)ban_slots, ban_cap, ban_n, w)) return rc;
   SampleArgs a{};
+  a.quote = TupleSet{(unsigned long long*)quote_slots, (unsigned long long*)quote_ctx, quote_count, quote_succ,
+                     quote_cap, quote_n};
+  a.ban = TupleSet{(unsigned long long*)ban_slots, (unsigned long long*)ban_ctx, ban_count, ban_succ, ban_cap, ban_n};
+  if (int rc = check_set("asrn_sample (quote)", a.quote, w)) return rc;
+  if (int rc = check_set("asrn_sample (bans)", a.ban, w)) return rc;
   a.lg = lg;
   a.ldl = ldl;
   a.work = work;
@@ -505,8 +610,6 @@ extern "C" int asrn_sample(const float* lg, int64_t ldl, float* work, uint32_t* 
   a.tokens = tokens;
   a.done = done;
   a.stop_step = stop_step;
-  a.quote = TupleSet{(unsigned long long*)quote_slots, quote_cap, quote_n};
-  a.ban = TupleSet{(unsigned long long*)ban_slots, ban_cap, ban_n};
   a.w = w;
   a.V = V;
   a.temperature = temperature;

@@ -776,9 +776,10 @@ def bits_por_pieza(V):
 
 
 class ConjuntoNgramas:
-    """Per text row, a device hash set of the n-grams seen (n token ids packed into one 64-bit key): the device side
-    of the reference's _Ngramas (asrn/nucleo.py:1857-1889). Sized for `capacidad` n-grams per row (at most half the
-    slots in use); n * bits_por_pieza(V) must be <= 64."""
+    """Per text row, a device hash set of the n-grams seen (n token ids packed into one 64-bit key) and a table of
+    their contexts' distinct successors (the first asrn_ngram_set_successors() inline): the device side of the
+    reference's _Ngramas (asrn/nucleo.py:1857-1889). Sized for `capacidad` n-grams per row (at most half the slots in
+    use); n * bits_por_pieza(V) must be <= 64."""
 
     def __init__(self, filas, n, V, capacidad, dev):
         w = bits_por_pieza(V)
@@ -788,6 +789,13 @@ class ConjuntoNgramas:
         self.n, self.w, self.V = n, w, V
         self.cap = _pow2_at_least(max(2 * int(capacidad), 2))
         self.slots = torch.full((filas, self.cap), -1, dtype=torch.int64, device=dev)     # all ones: empty
+        self.ctx = torch.full((filas, self.cap), -1, dtype=torch.int64, device=dev)
+        self.count = torch.zeros((filas, self.cap), dtype=torch.int32, device=dev)
+        self.succ = torch.empty((filas, self.cap, int(query('asrn_ngram_set_successors'))), dtype=torch.int32,
+                                device=dev)
+
+    def punteros(self):
+        return [ptr(self.slots), ptr(self.ctx), ptr(self.count), ptr(self.succ), self.cap, self.n]
 
     def agregar_texto(self, x):
         """Every n-gram of the rows of x (filas, L) int64."""
@@ -798,7 +806,7 @@ class ConjuntoNgramas:
         if x.shape[1] > self.cap // 2:
             raise ValueError(f'agregar_texto: {x.shape[1]} n-grams per row exceed the sets\' capacity')
         call('asrn_ngram_set_build', ptr(x), x.stride(0), x.shape[0], x.shape[1], self.n, self.w, ptr(self.slots),
-             self.cap, stream_of(dev))
+             ptr(self.ctx), ptr(self.count), ptr(self.succ), self.cap, stream_of(dev))
 
 
 def muestrear(lg, texto, pos, pos_max, L0, piezas, terminado, paso_fin, trabajo, bits_cita, temperatura, top_k,
@@ -833,7 +841,6 @@ def muestrear(lg, texto, pos, pos_max, L0, piezas, terminado, paso_fin, trabajo,
     call('asrn_sample', ptr(lg), lg.stride(0), ptr(trabajo), ptr(bits_cita), ptr(prob), ptr(logits),
          logits.shape[1] if logits is not None else 0, ptr(texto), texto.stride(0), ptr(pos), int(pos_max), int(L0),
          ptr(piezas), ptr(terminado), ptr(paso_fin),
-         ptr(cita.slots) if cita else None, cita.cap if cita else 0, cita.n if cita else 0,
-         ptr(prohibidas.slots) if prohibidas else None, prohibidas.cap if prohibidas else 0,
-         prohibidas.n if prohibidas else 0, w, B, V, float(temperatura), int(top_k), float(top_p), float(pena),
+         *(cita.punteros() if cita else [None, None, None, None, 0, 0]),
+         *(prohibidas.punteros() if prohibidas else [None, None, None, None, 0, 0]), w, B, V, float(temperatura), int(top_k), float(top_p), float(pena),
          int(ventana), -1 if parar_en is None else int(parar_en), ctypes.c_uint64(semilla), stream_of(dev))

@@ -1,7 +1,7 @@
 """Benchmark of the ASRN layer hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--config cfg2|cfg3] [--no-cpu-baseline] [--no-decode]
-                    [--decode-steps 1024] [--decode-layers 6] [--decode-only] [--no-model] [--model-only]
+                    [--decode-steps 1024] [--decode-only] [--no-model] [--model-only]
                     [--model-steps 20]
 
 A step is one forward + backward of one ASRN layer (asrn.ASRNLayer, group-A protections) over one batch of
@@ -17,7 +17,7 @@ steps, since events recorded while capturing are not replayed. Prints one JSON l
                 from the committed rocprofv3 kernel trace (profiles/cfg2_kernel_times.json) where there is one
   layer         whole-layer tokens/s and its HBM fraction at 41,552 B/token (the HIP kernels' bytes plus the GEMMs'
                 operands and results, 16,000 B/token at cfg2)
-  decode        the O(1) generation step of configs[4]'s 6 ASRN layers (d 768, B 16): per-token latency over 1,024
+  decode        configs[4]'s greedy generation with the whole d = 768 model (B 16): per-token latency over 1,024
                 steps against the context, 1K to 64K, and its slope
   modelo        the whole model's training step as PasoGrafado replays it: configs[3] (V 50,304, d 768, 12 local
                 blocks, 6 ASRN layers, B 8, N 2,048, bf16 autocast, AdamW) and configs[0] (the quick-start model,
@@ -176,72 +176,60 @@ def profiled_hip_us(config):
         return None
 
 
-DECODE = dict(B=16, d=768, V=50304, layers=6, contexts=(1024, 4096, 16384, 32768, 65536), frac=0.2, span=(16, 256),
-              zipf=1.1)
+DECODE = dict(B=16, V=50304, d=768, n_capas=12, contexts=(1024, 4096, 16384, 32768, 65536), frac=0.2,
+              span=(16, 256), zipf=1.1)
 
 
-def decode_bench(dev, steps, warmup, seed=0, contexts=None, layers=None):
-    """BASELINE.json configs[4]'s decode over its ASRN layers: the O(1) generation step of a stack of `layers` ASRN
-    layers (6, as the d = 768 model has) at d = 768, B = 16, after a prefill of each context length, one
-    EscritorCapa per layer, each layer's output the next one's input h and E the token embeddings for all of them
-    (asrn/nucleo.py:1751-1854 per layer). The model's local blocks, embedding and head are not part of this build
-    and are not timed. Per-token latency (wall clock over `steps` back-to-back steps, synchronized at both ends)
-    against the context, and the least-squares slope with its 95% interval (O(1): it includes 0). Each layer's step
-    is its writer's HIP graph replay (EscritorCapa(grafo=True)); their first step runs op by op, and there the HIP
-    kernels are timed with events (a replay makes no library call to time); the second captures the graphs."""
+def decode_bench(dev, steps, warmup, seed=0, contexts=None):
+    """greedy generation (top_k=1, memoria_de_lo_ajeno=False, so every new position enters
+    the rings; the quote correction on, the reference's default) with the whole d = 768 model of configs[3] (12 local
+    blocks, 6 ASRN layers, tied head; random-init weights from the seed, fp32), B = 16, after a prefill of each context
+    length, 1K to 64K. A step is escribir's loop step: the token choice (asrn_sample) and the model's O(1) step, one HIP
+    graph replay. Per-token latency is wall clock over `steps` back-to-back steps (synchronized at both ends); the
+    least-squares slope against the context, with its 95% interval, is the O(1) check. The first step runs op by op,
+    and there each HIP entry point is timed with device events (a replay makes no library call to time)."""
     import torch
 
     import asrn_amd
     from asrn_amd import _lib, synth
+    from asrn_amd.generacion import EscritorModelo, _Bucle
 
     cfg = DECODE
-    B, d, V = cfg['B'], cfg['d'], cfg['V']
-    nl = layers or cfg['layers']
+    B, V = cfg['B'], cfg['V']
     contexts = contexts or cfg['contexts']
-    torch.manual_seed(seed)
-    capas = [synth.move_params(asrn_amd.ASRNLayer(d), seed=seed + j).to(dev) for j in range(nl)]
-    g = torch.Generator(device=dev).manual_seed(seed + 7)
-    emb = torch.randn(V, d, generator=g, device=dev)
-    rows = []
-    kern = {}
+    m = asrn_amd.crear_modelo(V, d=cfg['d'], n_capas=cfg['n_capas'], largo_cada=2, semilla=seed).to(dev).eval()
+    rows, kern = [], {}
     w = max(warmup, 2)
-    for ctx in contexts:
-        n = ctx + w + steps
-        x = synth.tokens(B, n, V, frac=cfg['frac'], span=cfg['span'], zipf=cfg['zipf'], seed=seed + ctx).to(dev)
-        E = emb[x]
-        h = torch.randn(B, n, d, generator=g, device=dev)
-        # every position a key (the rings update); each layer's step replayed from a HIP graph
-        escs = [asrn_amd.EscritorCapa(c, memoria_de_lo_ajeno=False, grafo=True) for c in capas]
-        hj = h[:, :ctx]
-        for esc in escs:
-            hj = esc.inicio(E[:, :ctx], hj, x[:, :ctx], capacidad=n + 1)
-        del hj
-
-        def paso(t):
-            y = h[:, t]
-            for esc in escs:
-                y = esc.paso(E[:, t], y, x[:, t])
-            return y
-
-        timed = _lib.time_calls(['asrn_decode_attend', 'asrn_repetition_step', 'asrn_decode_produce', 'asrn_gate_fwd'])
-        paso(ctx)                                                  # op by op: its kernels timed
-        timed = _lib.stop_timing()
-        for t in range(ctx + 1, ctx + w):                          # the first of these captures the graphs
-            paso(t)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for t in range(ctx + w, ctx + w + steps):
-            paso(t)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        for name, evs in timed.items():
-            kern.setdefault(name, []).extend(s.elapsed_time(e) for s, e in evs)
-        ms = 1e3 * (t1 - t0) / steps
-        rows.append({'context': ctx, 'ms_per_step': round(ms, 4), 'tokens_per_s': round(B * 1e3 / ms, 1),
-                     'kernel_us_per_step': {name: round(1e3 * sum(s.elapsed_time(e) for s, e in evs), 2)
-                                            for name, evs in timed.items() if evs}})
-        del escs, E, h, x
-        torch.cuda.empty_cache()
+    nombres = ['asrn_sample', 'asrn_decode_produce', 'asrn_repetition_step', 'asrn_decode_attend', 'asrn_gate_fwd']
+    with torch.no_grad():
+        for ctx in contexts:
+            x = synth.tokens(B, ctx, V, frac=cfg['frac'], span=cfg['span'], zipf=cfg['zipf'], seed=seed + ctx).to(dev)
+            n = w + steps + 1
+            esc = EscritorModelo(m, memoria_de_lo_ajeno=False)
+            lg = esc.inicio(x, capacidad=ctx + n)
+            esc.reservar(ctx + n)
+            bucle = _Bucle(esc, x, n, 1.0, 1, seed, 1.0, 64, 0, None, 1.0, False, True, True)
+            bucle.lg.copy_(lg)
+            del lg
+            timed = _lib.time_calls(nombres)
+            bucle.paso(0)                                          # op by op: its kernels timed
+            timed = _lib.stop_timing()
+            for k in range(1, w):                                  # the first of these captures the step
+                bucle.paso(k)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for k in range(w, w + steps):
+                bucle.paso(k)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            for name, evs in timed.items():
+                kern.setdefault(name, []).extend(s.elapsed_time(e) for s, e in evs)
+            ms = 1e3 * (t1 - t0) / steps
+            rows.append({'context': ctx, 'ms_per_step': round(ms, 4), 'tokens_per_s': round(B * 1e3 / ms, 1),
+                         'kernel_us_first_step': {name: round(1e3 * sum(s.elapsed_time(e) for s, e in evs), 2)
+                                                  for name, evs in timed.items() if evs}})
+            del bucle, esc, x
+            torch.cuda.empty_cache()
     xs = [r['context'] for r in rows]
     ys = [r['ms_per_step'] * 1e6 for r in rows]        # ns
     k = len(xs)
@@ -251,11 +239,12 @@ def decode_bench(dev, steps, warmup, seed=0, contexts=None, layers=None):
     res = [b - (my + slope * (a - mx)) for a, b in zip(xs, ys)]
     se = (sum(r * r for r in res) / max(k - 2, 1) / sxx) ** 0.5 if sxx else 0.0
     t975 = {1: 12.71, 2: 4.30, 3: 3.18, 4: 2.78, 5: 2.57}.get(k - 2, 2.0)
-    return {'workload': f'configs[4] decode over {nl} ASRN layers: d={d}, B={B}, V={V}, Zipf 1.1 with 20% copied '
-                        f'spans, prefill of each context then {w} + {steps} greedy-position steps (the tokens of the '
-                        'synthetic stream); local blocks, embedding and head not included',
-            'layers': nl, 'launch': 'hip graph replay of each layer\'s step', 'per_context': rows,
-            'tokens_per_s': rows[-1]['tokens_per_s'],
+    return {'workload': f"configs[4]: greedy generation with the whole configs[3] model (V={V}, d={cfg['d']}, "
+                        f"{cfg['n_capas']} local blocks, {len(m.largos)} ASRN layers, random-init fp32), B={B}, Zipf 1.1 "
+                        f'tokens with 20% copied spans, prefill of each context then {w} + {steps} steps, every '
+                        'position a key, quote correction on',
+            'parameters': m.num_parametros(), 'launch': 'hip graph replay of the whole loop step (choice + model)',
+            'per_context': rows, 'tokens_per_s': rows[-1]['tokens_per_s'],
             'slope_ns_per_context_token': round(slope, 4),
             'slope_ci95': [round(slope - t975 * se, 4), round(slope + t975 * se, 4)],
             'kernels_op_by_op_step': {name: {'launches': len(v), 'mean_us': round(1e3 * sum(v) / len(v), 3)}
@@ -345,10 +334,9 @@ def main():
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-decode', action='store_true')
     ap.add_argument('--decode-steps', type=int, default=1024)
-    ap.add_argument('--decode-layers', type=int, default=DECODE['layers'])
     ap.add_argument('--decode-contexts', default=None, help='comma-separated prefill lengths (default 1K,4K,16K,32K,64K)')
     ap.add_argument('--decode-only', action='store_true',
-                    help='only the generation-step leg (configs[4], one layer); prints its JSON object')
+                    help='only the generation leg (configs[4], the whole model); prints its JSON object')
     ap.add_argument('--eager', action='store_true', help='time Python-launched steps instead of HIP graph replays')
     ap.add_argument('--no-model', action='store_true', help='skip the whole-model training-step legs')
     ap.add_argument('--model-only', action='store_true',
@@ -393,7 +381,7 @@ def main():
     contexts = [int(c) for c in args.decode_contexts.split(',')] if args.decode_contexts else None
     if args.decode_only:
         print(json.dumps({'decode': decode_bench(torch.device('cuda:0'), args.decode_steps, 20, seed=args.seed,
-                                                  contexts=contexts, layers=args.decode_layers),
+                                                  contexts=contexts),
                           'gemm_picks': gemm_picks}), flush=True)
         return
     cfg = synth.CONFIGS[args.config]
@@ -500,8 +488,7 @@ def main():
                     for n, s in sorted(per_call.items(), key=lambda kv: -kv[1]['total_ms'])},
     }
     if not args.no_decode:
-        out['decode'] = decode_bench(dev, args.decode_steps, 20, seed=args.seed, contexts=contexts,
-                                     layers=args.decode_layers)
+        out['decode'] = decode_bench(dev, args.decode_steps, 20, seed=args.seed, contexts=contexts)
     if not args.no_model:
         out['modelo'] = {n: modelo_bench(dev, n, args.model_steps, 5, seed=args.seed) for n in MODELOS}
     if not args.no_cpu_baseline:

@@ -346,13 +346,17 @@ int asrn_decode_produce(const float* e, const float* e_prev, const float* h, con
 /* ---- generation loop: n-gram sets and the per-token choice ------------------------------------------------------
  * The host side of escribir (asrn/nucleo.py:1965-2043) moved onto the device. The n-gram sets replace _Ngramas
  * (asrn/nucleo.py:1857-1889: Python dicts of token tuples, updated on the host after every token): per text row, an
- * open-addressing table of `cap` (a power of two) uint64 slots, all ones when empty, each key the n token ids of an
- * n-gram packed w = asrn_sample_bits(V) bits apiece (n * w <= 64), the oldest lowest.
+ * open-addressing table `slots` of `cap` (a power of two) uint64 keys, all ones when empty, each key the n token ids of
+ * an n-gram packed w = asrn_sample_bits(V) bits apiece (n * w <= 64), the oldest lowest; and a table of its contexts
+ * (the first n - 1 ids, packed the same way): `ctx` (rows, cap) uint64, all ones when empty, `count` (rows, cap) int32,
+ * zero to start, the number of distinct successors, and `succ` (rows, cap, asrn_ngram_set_successors()) int32, the
+ * first of them.
  * asrn_sample_bits: the smallest w with 2^w - 1 > V - 1.
- * asrn_ngram_set_build: every n-gram of x (rows, L), row stride ldx, into row r's table; L <= cap / 2. */
+ * asrn_ngram_set_build: every n-gram of x (rows, L), row stride ldx, into row r's tables; L <= cap / 2. */
 int32_t asrn_sample_bits(int64_t V);
+int32_t asrn_ngram_set_successors(void);
 int asrn_ngram_set_build(const int64_t* x, int64_t ldx, int64_t rows, int64_t L, int32_t n, int32_t w, uint64_t* slots,
-                         int64_t cap, void* stream);
+                         uint64_t* ctx, int32_t* count, int32_t* succ, int64_t cap, void* stream);
 
 /* asrn_sample replaces _frenar + _muestrear + _conservar_cita and the stop-token and bookkeeping lines of the
  * generation loop (asrn/nucleo.py:1909-1962, 2017-2036; there: a CPU multinomial and a .cpu() sync per token). Row b
@@ -367,10 +371,11 @@ int asrn_ngram_set_build(const int64_t* x, int64_t ldx, int64_t rows, int64_t L,
  * the final probabilities and logits_out (B, steps, V) the logits row at step pos - L0, when not NULL. */
 int asrn_sample(const float* lg, int64_t ldl, float* work, uint32_t* quote_bits, float* prob_out, float* logits_out,
                 int64_t steps, int64_t* text, int64_t ld_text, const int64_t* pos_dev, int64_t pos_max, int64_t L0,
-                int64_t* tokens, uint8_t* done, int32_t* stop_step, uint64_t* quote_slots, int64_t quote_cap,
-                int32_t quote_n, uint64_t* ban_slots, int64_t ban_cap, int32_t ban_n, int32_t w, int64_t B, int64_t V,
-                float temperature, int32_t top_k, float top_p, float penalty, int32_t window, int64_t stop_token,
-                uint64_t seed, void* stream);
+                int64_t* tokens, uint8_t* done, int32_t* stop_step, uint64_t* quote_slots, uint64_t* quote_ctx,
+                int32_t* quote_count, int32_t* quote_succ, int64_t quote_cap, int32_t quote_n, uint64_t* ban_slots,
+                uint64_t* ban_ctx, int32_t* ban_count, int32_t* ban_succ, int64_t ban_cap, int32_t ban_n, int32_t w,
+                int64_t B, int64_t V, float temperature, int32_t top_k, float top_p, float penalty, int32_t window,
+                int64_t stop_token, uint64_t seed, void* stream);
 
 #ifdef __cplusplus
 }
