@@ -30,6 +30,7 @@ constexpr unsigned long long kEmptySlot = ~0ull;
 constexpr int kSampleThreads = 1024;
 constexpr int kSampleWaves = kSampleThreads / kWave;
 constexpr int kSucc = 8;                         // successors held inline per context
+constexpr int kMaxCand = 4096;                   // tokens past the top-k cut handled in LDS
 constexpr double kMassScale = 1099511627776.0;   // 2^40: fixed-point probability masses (sums stay below 2^63)
 
 // SplitMix64's output function (G. Steele, D. Lea, C. Flood, "Fast splittable pseudorandom number generators",
@@ -227,6 +228,56 @@ __device__ __forceinline__ void successors(const TupleSet& s, int64_t b, const i
   *n_list = k;
 }
 
+// f(v, x) for this thread's strided share of a row (v = tid + k * 1024, x = row[v]), eight loads in flight
+template <class F>
+__device__ __forceinline__ void each(const float* row, int64_t V, F&& f) {
+  for (int64_t base = threadIdx.x; base < V; base += 8 * (int64_t)kSampleThreads) {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t v = base + (int64_t)j * kSampleThreads;
+      t[j] = v < V ? row[v] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t v = base + (int64_t)j * kSampleThreads;
+      if (v < V) f(v, t[j]);
+    }
+  }
+}
+
+// the same with every lane of the wavefront calling f(v, x, valid) the same number of times (for passes that use
+// wavefront-wide operations)
+template <class F>
+__device__ __forceinline__ void each_all(const float* row, int64_t V, F&& f) {
+  for (int64_t base = 0; base < V; base += 8 * (int64_t)kSampleThreads) {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t v = base + (int64_t)j * kSampleThreads + threadIdx.x;
+      t[j] = v < V ? row[v] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t v = base + (int64_t)j * kSampleThreads + threadIdx.x;
+      f(v, t[j], v < V);
+    }
+  }
+}
+
+// f(v, x) over the contiguous range [v0, v1) of a row, in order, eight loads in flight; f returns false to stop
+template <class F>
+__device__ __forceinline__ void each_range(const float* row, int64_t v0, int64_t v1, F&& f) {
+  for (int64_t vb = v0; vb < v1; vb += 8) {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = vb + j < v1 ? row[vb + j] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (vb + j < v1 && !f(vb + j, t[j])) return;
+  }
+}
+
 __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   __shared__ Red red;
   __shared__ unsigned int hist_n[256];
@@ -236,6 +287,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   __shared__ int pick[2];
   __shared__ int qlist[kSucc], blist[kSucc];
   __shared__ int nq_list, nb_list;
+  __shared__ int ctok[kMaxCand];
+  __shared__ float cval[kMaxCand];
+  __shared__ int cscan[kSampleThreads];
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.x;
   const int64_t pos = *a.pos_dev;
@@ -257,11 +311,10 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
 
   // penalty (_frenar): the logits as they came, then the tokens of the window penalized from those same values
   float* lout = (a.logits_out && step >= 0 && step < a.steps) ? a.logits_out + (b * a.steps + step) * V : nullptr;
-  for (int64_t v = tid; v < V; v += kSampleThreads) {
-    const float l = lg[v];
+  each(lg, V, [&](int64_t v, float l) {
     work[v] = l;
     if (lout) lout[v] = l;
-  }
+  });
   __syncthreads();
   if (a.penalty != 1.f) {
     for (int j = tid; j < a.window; j += kSampleThreads) {
@@ -287,10 +340,10 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   __syncthreads();
   {
     float finite = 0.f;
-    for (int64_t v = tid; v < V; v += kSampleThreads) finite += (work[v] == ninf) ? 0.f : 1.f;
+    each(work, V, [&](int64_t, float x) { finite += (x == ninf) ? 0.f : 1.f; });
     if (block_sum(finite, red) == 0.f) {                        // nothing left: the plain logits (no penalty either)
       __syncthreads();
-      for (int64_t v = tid; v < V; v += kSampleThreads) work[v] = lg[v];
+      each(lg, V, [&](int64_t v, float l) { work[v] = l; });
     }
   }
   __syncthreads();
@@ -322,14 +375,14 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   float mass_p = 0.f;
   if (quote && (qprobe || nql > 0)) {
     float m = ninf;
-    for (int64_t v = tid; v < V; v += kSampleThreads) m = fmaxf(m, work[v]);
+    each(work, V, [&](int64_t, float x) { m = fmaxf(m, x); });
     const float m1 = block_max(m, red);
     float s = 0.f, c = 0.f;
-    for (int64_t v = tid; v < V; v += kSampleThreads) {
-      const float e = expf(work[v] - m1);
+    each(work, V, [&](int64_t v, float x) {
+      const float e = expf(x - m1);
       s += e;
       if (qprobe && in_quote(v)) c += e;
-    }
+    });
     if (!qprobe && tid < nql) c = expf(work[qlist[tid]] - m1);
     const float S1 = block_sum(s, red);
     mass_p = block_sum(c, red) / S1;
@@ -337,18 +390,20 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
 
   // temperature and top-k: keep the logits >= the k-th largest
   const float tden = fmaxf(a.temperature, 1e-6f);
-  auto l3 = [&](int64_t v) { return work[v] / tden; };
   float corte = ninf;
-  if (a.top_k > 0 && (int64_t)a.top_k < V) {
+  if (a.top_k == 1 && V > 1) {                                   // the k-th largest is the maximum: one pass
+    float m = ninf;
+    each(work, V, [&](int64_t, float x) { m = fmaxf(m, x / tden); });
+    corte = block_max(m, red);
+  } else if (a.top_k > 0 && (int64_t)a.top_k < V) {
     uint32_t prefix = 0, mask = 0, rest = (uint32_t)a.top_k;
     for (int shift = 24; shift >= 0; shift -= 8) {
       for (int i = tid; i < 256; i += kSampleThreads) hist_n[i] = 0;
       __syncthreads();
-      for (int64_t base = 0; base < V; base += kSampleThreads) {
-        const int64_t v = base + tid;
-        const uint32_t k = v < V ? ordered(l3(v)) : 0u;
-        hist_count(hist_n, (k >> shift) & 255u, v < V && (k & mask) == prefix);
-      }
+      each_all(work, V, [&](int64_t, float x, bool ok) {
+        const uint32_t k = ok ? ordered(x / tden) : 0u;
+        hist_count(hist_n, (k >> shift) & 255u, ok && (k & mask) == prefix);
+      });
       __syncthreads();
       if (tid == 0) {
         uint32_t cum = 0, d = 0;
@@ -367,50 +422,539 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     }
     corte = from_ordered(prefix);
   }
-  auto kept_k = [&](float x) { return !(x < corte); };
+  auto kept_k = [&](float l) { return !(l < corte); };
 
-  // the kept logits' max (the row's max is always kept) and top-p over their softmax
-  float mloc = ninf;
-  for (int64_t v = tid; v < V; v += kSampleThreads) {
-    const float x = l3(v);
-    if (kept_k(x)) mloc = fmaxf(mloc, x);
+  // Few tokens past the top-k cut: they are gathered into LDS in a fixed order (thread, then stride) and the rest of
+  // the decision (top-p, the softmax, the quote-mass correction, the draw) runs on them alone. More than kMaxCand
+  // (ties at the cut): the full-row passes below.
+  bool lista = false;
+  int ncand = 0;
+  if (a.top_k > 0 && (int64_t)a.top_k < V) {
+    int cnt = 0;
+    each(work, V, [&](int64_t, float x) { cnt += kept_k(x / tden) ? 1 : 0; });
+    __syncthreads();
+    cscan[tid] = cnt;
+    __syncthreads();
+    for (int off = 1; off < kSampleThreads; off <<= 1) {
+      const int add = tid >= off ? cscan[tid - off] : 0;
+      __syncthreads();
+      cscan[tid] += add;
+      __syncthreads();
+    }
+    ncand = cscan[kSampleThreads - 1];
+    lista = ncand <= kMaxCand;
+    if (lista) {
+      int o = cscan[tid] - cnt;
+      each(work, V, [&](int64_t v, float x) {
+        const float l = x / tden;
+        if (kept_k(l)) {
+          ctok[o] = (int)v;
+          cval[o] = l;
+          ++o;
+        }
+      });
+      __syncthreads();
+    }
   }
+  if (lista) {
+    float m = ninf;
+    for (int i = tid; i < ncand; i += kSampleThreads) m = fmaxf(m, cval[i]);
+    const float m3 = block_max(m, red);
+    float tau = -1.f, S3 = 1.f;
+    if (a.top_p < 1.f) {
+      float s = 0.f;
+      for (int i = tid; i < ncand; i += kSampleThreads) s += expf(cval[i] - m3);
+      S3 = block_sum(s, red);
+      const double target = ceil((double)a.top_p * kMassScale);
+      uint32_t prefix = 0, mask = 0;
+      unsigned long long acc = 0;
+      bool found = true;
+      for (int shift = 24; shift >= 0 && found; shift -= 8) {
+        for (int i = tid; i < 256; i += kSampleThreads) {
+          hist_n[i] = 0;
+          hist_m[i] = 0;
+        }
+        __syncthreads();
+        for (int base = 0; base < ncand; base += kSampleThreads) {
+          const int i = base + tid;
+          const bool ok = i < ncand;
+          const float p = ok ? expf(cval[i] - m3) / S3 : 0.f;
+          const uint32_t k = __float_as_uint(p);
+          hist_mass(hist_n, hist_m, (k >> shift) & 255u, ok && (k & mask) == prefix,
+                    (unsigned long long)rint((double)p * kMassScale));
+        }
+        __syncthreads();
+        if (tid == 0) {
+          int d = -1;
+          for (int i = 255; i >= 0; --i) {
+            if (hist_n[i] == 0) continue;
+            if ((double)(acc + hist_m[i]) >= target) { d = i; break; }
+            acc += hist_m[i];
+          }
+          sel[0] = d < 0 ? 0u : (uint32_t)d;
+          sel[1] = d < 0 ? 0u : 1u;
+        }
+        __syncthreads();
+        found = sel[1] != 0;
+        prefix |= sel[0] << shift;
+        mask |= 255u << shift;
+        __syncthreads();
+      }
+      if (found) tau = __uint_as_float(prefix);
+    }
+    auto keep_i = [&](int i, float* e) {
+      *e = expf(cval[i] - m3);
+      return tau < 0.f || (*e / S3) >= tau;
+    };
+    float s4 = 0.f;
+    for (int i = tid; i < ncand; i += kSampleThreads) {
+      float e;
+      if (keep_i(i, &e)) s4 += e;
+    }
+    const float S4 = block_sum(s4, red);
+    float sc_q = 1.f, sc_n = 1.f;
+    if (quote && (qprobe || nql > 0)) {
+      float c = 0.f;
+      for (int i = tid; i < ncand; i += kSampleThreads) {
+        float e;
+        if (in_quote(ctok[i]) && keep_i(i, &e)) c += e / S4;
+      }
+      const float mass_q = block_sum(c, red);
+      if (mass_q > 0.f && mass_q < 1.f) {
+        sc_q = mass_p / fmaxf(mass_q, 1e-30f);
+        sc_n = (1.f - mass_p) / fmaxf(1.f - mass_q, 1e-30f);
+      }
+    }
+    const bool scaled = sc_q != 1.f || sc_n != 1.f;
+    auto prob_i = [&](int i) {
+      float e;
+      if (!keep_i(i, &e)) return 0.f;
+      const float p = e / S4;
+      return scaled ? p * (in_quote(ctok[i]) ? sc_q : sc_n) : p;
+    };
+    if (a.prob_out) {
+      each(work, V, [&](int64_t v, float) { a.prob_out[b * V + v] = 0.f; });
+      __syncthreads();
+      for (int i = tid; i < ncand; i += kSampleThreads) a.prob_out[b * V + ctok[i]] = prob_i(i);
+    }
+    // the draw over the list, each thread a contiguous segment of it
+    const int seg = (ncand + kSampleThreads - 1) / kSampleThreads;
+    const int i0 = tid * seg < ncand ? tid * seg : ncand, i1 = i0 + seg < ncand ? i0 + seg : ncand;
+    float local = 0.f;
+    int last = -1;
+    for (int i = i0; i < i1; ++i) {
+      const float p = prob_i(i);
+      local += p;
+      if (p > 0.f) last = i;
+    }
+    __syncthreads();
+    scan[tid] = local;
+    if (tid < 2) pick[tid] = tid == 0 ? 0x7fffffff : -1;
+    __syncthreads();
+    for (int off = 1; off < kSampleThreads; off <<= 1) {
+      const float add = tid >= off ? scan[tid - off] : 0.f;
+      __syncthreads();
+      scan[tid] += add;
+      __syncthreads();
+    }
+    const float total = scan[kSampleThreads - 1];
+    const float before = tid > 0 ? scan[tid - 1] : 0.f;
+    const float after = scan[tid];
+    const uint64_t r = mix64(a.seed ^ mix64((uint64_t)pos * 0x9e3779b97f4a7c15ull + (uint64_t)b));
+    const float u = (float)(r >> 40) * (1.f / 16777216.f);
+    const float target = u * total;
+    if (local > 0.f && target >= before && target < after) {
+      const float inside = target - before;
+      float acc = 0.f;
+      int chosen = -1;
+      for (int i = i0; i < i1; ++i) {
+        const float p = prob_i(i);
+        acc += p;
+        if (p > 0.f && acc > inside) {
+          chosen = i;
+          break;
+        }
+      }
+      if (chosen < 0) chosen = last;
+      if (chosen >= 0) atomicMin(&pick[0], chosen);
+    }
+    if (last >= 0) atomicMax(&pick[1], last);
+    __syncthreads();
+    if (tid == 0) {                                              // list positions -> token ids
+      const int o = pick[0] != 0x7fffffff ? pick[0] : pick[1];
+      pick[0] = o >= 0 ? ctok[o] : 0x7fffffff;
+      pick[1] = -1;
+    }
+    __syncthreads();
+  } else {
+    // the kept logits' max (the row's max is always kept) and top-p over their softmax
+    float mloc = ninf;
+    each(work, V, [&](int64_t, float x) {
+      const float l = x / tden;
+      if (kept_k(l)) mloc = fmaxf(mloc, l);
+    });
+    const float m3 = block_max(mloc, red);
+    float tau = -1.f;                                              // keep probabilities >= tau (all when < 0)
+    float S3 = 1.f;
+    if (a.top_p < 1.f) {
+      float s = 0.f;
+      each(work, V, [&](int64_t, float x) {
+        const float l = x / tden;
+        if (kept_k(l)) s += expf(l - m3);
+      });
+      S3 = block_sum(s, red);
+      const double target = ceil((double)a.top_p * kMassScale);
+      uint32_t prefix = 0, mask = 0;
+      unsigned long long acc = 0;
+      bool found = true;
+      for (int shift = 24; shift >= 0 && found; shift -= 8) {
+        for (int i = tid; i < 256; i += kSampleThreads) {
+          hist_n[i] = 0;
+          hist_m[i] = 0;
+        }
+        __syncthreads();
+        each_all(work, V, [&](int64_t, float x, bool ok) {
+          const float l = x / tden;
+          const bool in = ok && kept_k(l);
+          const float p = in ? expf(l - m3) / S3 : 0.f;
+          const uint32_t k = __float_as_uint(p);
+          hist_mass(hist_n, hist_m, (k >> shift) & 255u, in && (k & mask) == prefix,
+                    (unsigned long long)rint((double)p * kMassScale));
+        });
+        __syncthreads();
+        if (tid == 0) {
+          // from the largest values down: the bin where the mass of everything at or above it first reaches top_p
+          int d = -1;
+          for (int i = 255; i >= 0; --i) {
+            if (hist_n[i] == 0) continue;
+            if ((double)(acc + hist_m[i]) >= target) { d = i; break; }
+            acc += hist_m[i];
+          }
+          sel[0] = d < 0 ? 0u : (uint32_t)d;
+          sel[1] = d < 0 ? 0u : 1u;
+        }
+        __syncthreads();
+        found = sel[1] != 0;
+        prefix |= sel[0] << shift;
+        mask |= 255u << shift;
+        __syncthreads();
+      }
+      if (found) tau = __uint_as_float(prefix);
+    }
+
+    // final probabilities: softmax over what is kept, then the quote-mass correction
+    auto keep = [&](float x, float* e) {
+      const float l = x / tden;
+      if (!kept_k(l)) return false;
+      *e = expf(l - m3);
+      return tau < 0.f || (*e / S3) >= tau;
+    };
+    float S4;
+    {
+      float s = 0.f;
+      each(work, V, [&](int64_t, float x) {
+        float e;
+        if (keep(x, &e)) s += e;
+      });
+      S4 = block_sum(s, red);
+    }
+    float sc_q = 1.f, sc_n = 1.f;
+    if (quote && (qprobe || nql > 0)) {
+      float c = 0.f, e;
+      if (qprobe) {
+        each(work, V, [&](int64_t v, float x) {
+          float ee;
+          if (in_quote(v) && keep(x, &ee)) c += ee / S4;
+        });
+      } else if (tid < nql && keep(work[qlist[tid]], &e)) {
+        c = e / S4;
+      }
+      const float mass_q = block_sum(c, red);
+      if (mass_q > 0.f && mass_q < 1.f) {
+        sc_q = mass_p / fmaxf(mass_q, 1e-30f);
+        sc_n = (1.f - mass_p) / fmaxf(1.f - mass_q, 1e-30f);
+      }
+    }
+    const bool scaled = sc_q != 1.f || sc_n != 1.f;
+    auto prob = [&](int64_t v, float x) {
+      float e;
+      if (!keep(x, &e)) return 0.f;
+      const float p = e / S4;
+      return scaled ? p * (in_quote(v) ? sc_q : sc_n) : p;
+    };
+    if (a.prob_out) each(work, V, [&](int64_t v, float x) { a.prob_out[b * V + v] = prob(v, x); });
+
+    // the draw: inverse CDF over the tokens in index order, each thread a contiguous segment
+    const int64_t seg = (V + kSampleThreads - 1) / kSampleThreads;
+    const int64_t v0 = (int64_t)tid * seg < V ? (int64_t)tid * seg : V;
+    const int64_t v1 = v0 + seg < V ? v0 + seg : V;
+    float local = 0.f;
+    int64_t last_pos = -1;
+    each_range(work, v0, v1, [&](int64_t v, float x) {
+      const float p = prob(v, x);
+      local += p;
+      if (p > 0.f) last_pos = v;
+      return true;
+    });
+    scan[tid] = local;
+    if (tid < 2) pick[tid] = tid == 0 ? 0x7fffffff : -1;
+    __syncthreads();
+    for (int off = 1; off < kSampleThreads; off <<= 1) {        // inclusive scan (Hillis-Steele), fixed order
+      const float add = tid >= off ? scan[tid - off] : 0.f;
+      __syncthreads();
+      scan[tid] += add;
+      __syncthreads();
+    }
+    // thread t owns [scan[t - 1], scan[t]): neighbouring bounds are the same numbers, so the segments tile [0, total)
+    const float total = scan[kSampleThreads - 1];
+    const float before = tid > 0 ? scan[tid - 1] : 0.f;
+    const float after = scan[tid];
+    const uint64_t r = mix64(a.seed ^ mix64((uint64_t)pos * 0x9e3779b97f4a7c15ull + (uint64_t)b));
+    const float u = (float)(r >> 40) * (1.f / 16777216.f);      // 24 random bits: [0, 1)
+    const float target = u * total;
+    if (local > 0.f && target >= before && target < after) {
+      const float inside = target - before;
+      float acc = 0.f;                                             // summed from 0 in `local`'s order
+      int64_t chosen = -1;
+      each_range(work, v0, v1, [&](int64_t v, float x) {
+        const float p = prob(v, x);
+        acc += p;
+        if (p > 0.f && acc > inside) {
+          chosen = v;
+          return false;
+        }
+        return true;
+      });
+      if (chosen < 0) chosen = last_pos;
+      if (chosen >= 0) atomicMin(&pick[0], (int)chosen);
+    }
+    if (last_pos >= 0) atomicMax(&pick[1], (int)last_pos);
+    __syncthreads();
+  }
+
+  if (tid == 0) {
+    int64_t tok = pick[0] != 0x7fffffff ? pick[0] : (pick[1] >= 0 ? pick[1] : 0);
+    if (a.stop_token >= 0) {
+      if (a.done[b]) {
+        tok = a.stop_token;
+      } else if (tok == a.stop_token) {
+        a.done[b] = 1;
+        a.stop_step[b] = (int32_t)step;
+      }
+    }
+    text[pos] = tok;
+    a.tokens[b] = tok;
+    if (a.quote.slots && pos + 1 >= nq) ngram_add(a.quote, b, text + pos - (nq - 1), a.w);
+    if (a.ban.slots && pos + 1 - a.L0 >= nb) ngram_add(a.ban, b, text + pos - (nb - 1), a.w);
+  }
+}
+
+// The same decision with the row held in registers: thread t owns tokens t, t + 1024, ..., t + (R - 1) * 1024, loaded
+// once, so every pass after the first is arithmetic on registers (the global-memory kernel above reads the row from
+// the cache in each pass, eight loads in flight per thread). Tokens the thread does not own are reached through LDS lists (window, bans, quotes). The
+// draw walks the tokens in thread-major order (thread 0's R tokens, then thread 1's, ...): a fixed order, so the
+// inverse CDF draws from the same distribution, with other tokens for a given uniform than the index order would.
+template <int R>
+__global__ __launch_bounds__(kSampleThreads) void k_sample_reg(SampleArgs a) {
+  __shared__ Red red;
+  __shared__ unsigned int hist_n[256];
+  __shared__ unsigned long long hist_m[256];
+  __shared__ uint32_t sel[2];
+  __shared__ float scan[kSampleThreads];
+  __shared__ int pick[2];
+  __shared__ int qlist[kSucc], blist[kSucc];
+  __shared__ int nq_list, nb_list;
+  __shared__ int wtok[kSampleThreads];
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  const int64_t pos = *a.pos_dev;
+  if (pos < 0 || pos > a.pos_max) return;                       // outside the text buffer: nothing is touched
+  const int64_t V = a.V;
+  const float* lg = a.lg + b * a.ldl;
+  int64_t* text = a.text + b * a.ld_text;
+  const int64_t step = pos - a.L0;
+  const float ninf = -INFINITY;
+  const int nq = a.quote.n, nb = a.ban.n;
+  const bool quote = a.quote.slots && pos >= nq;
+  const bool bans = a.ban.slots && pos - a.L0 >= nb;
+  if (tid == 0) {
+    nq_list = nb_list = 0;
+    if (quote) successors(a.quote, b, text, pos, a.w, qlist, &nq_list);
+    if (bans) successors(a.ban, b, text, pos, a.w, blist, &nb_list);
+  }
+  auto tok_of = [&](int r) { return (int64_t)r * kSampleThreads + tid; };
+  // the slot of token v when this thread owns it
+  auto owned = [&](int64_t v, int* r) {
+    if (v < 0 || (v & (kSampleThreads - 1)) != tid) return false;
+    *r = (int)(v >> 10);
+    return *r < R;
+  };
+
+  float x[R];
+  float* lout = (a.logits_out && step >= 0 && step < a.steps) ? a.logits_out + (b * a.steps + step) * V : nullptr;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t v = tok_of(r);
+    x[r] = v < V ? lg[v] : ninf;
+    if (lout && v < V) lout[v] = x[r];
+  }
+  // penalty over the window's tokens, each penalized once from its own logit
+  if (a.penalty != 1.f) {
+    uint64_t hecho = 0;
+    for (int base = 0; base < a.window; base += kSampleThreads) {
+      const int j = base + tid;
+      const int64_t p = pos - a.window + j;
+      __syncthreads();
+      wtok[tid] = (j < a.window && p >= 0) ? (int)text[p] : -1;
+      __syncthreads();
+      const int cnt = a.window - base < kSampleThreads ? a.window - base : kSampleThreads;
+      for (int k = 0; k < cnt; ++k) {
+        int rr;
+        if (owned(wtok[k], &rr) && !((hecho >> rr) & 1ull)) {
+          hecho |= 1ull << rr;
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+            if (r == rr) x[r] = x[r] > 0.f ? x[r] / a.penalty : x[r] * a.penalty;
+        }
+      }
+    }
+  }
+  __syncthreads();                                              // the successor lists are visible from here
+  if (bans) {
+    if (nb_list >= 0) {
+      for (int k = 0; k < nb_list; ++k) {
+        int rr;
+        if (owned(blist[k], &rr)) {
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+            if (r == rr) x[r] = ninf;
+        }
+      }
+    } else {
+      const uint64_t base = pack(text + pos - (nb - 1), nb - 1, a.w);
+      const int sh = a.w * (nb - 1);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int64_t v = tok_of(r);
+        if (v < V && set_has(a.ban, b, base | ((uint64_t)v << sh))) x[r] = ninf;
+      }
+    }
+  }
+  {
+    float finite = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) finite += (tok_of(r) < V && x[r] != ninf) ? 1.f : 0.f;
+    if (block_sum(finite, red) == 0.f) {                        // nothing left: the plain logits (no penalty either)
+#pragma unroll
+      for (int r = 0; r < R; ++r) x[r] = tok_of(r) < V ? lg[tok_of(r)] : ninf;
+    }
+  }
+
+  // quote flags (bit r: token tok_of(r) closes an n-gram of the text) and the quote mass at temperature 1
+  uint64_t qmask = 0;
+  if (quote) {
+    if (nq_list >= 0) {
+      for (int k = 0; k < nq_list; ++k) {
+        int rr;
+        if (owned(qlist[k], &rr)) qmask |= 1ull << rr;
+      }
+    } else {
+      const uint64_t base = pack(text + pos - (nq - 1), nq - 1, a.w);
+      const int sh = a.w * (nq - 1);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int64_t v = tok_of(r);
+        if (v < V && set_has(a.quote, b, base | ((uint64_t)v << sh))) qmask |= 1ull << r;
+      }
+    }
+  }
+  const bool hay_cita = quote && (nq_list != 0);
+  float mass_p = 0.f;
+  if (hay_cita) {
+    float m = ninf;
+#pragma unroll
+    for (int r = 0; r < R; ++r) m = fmaxf(m, x[r]);
+    const float m1 = block_max(m, red);
+    float s = 0.f, c = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float e = tok_of(r) < V ? expf(x[r] - m1) : 0.f;
+      s += e;
+      if ((qmask >> r) & 1ull) c += e;
+    }
+    const float S1 = block_sum(s, red);
+    mass_p = block_sum(c, red) / S1;
+  }
+
+  // temperature, then top-k by radix selection over the values' ordered bits
+  const float tden = fmaxf(a.temperature, 1e-6f);
+#pragma unroll
+  for (int r = 0; r < R; ++r) x[r] = x[r] / tden;
+  float corte = ninf;
+  if (a.top_k > 0 && (int64_t)a.top_k < V) {
+    uint32_t prefix = 0, mask = 0, rest = (uint32_t)a.top_k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      __syncthreads();
+      for (int i = tid; i < 256; i += kSampleThreads) hist_n[i] = 0;
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t k = ordered(x[r]);
+        hist_count(hist_n, (k >> shift) & 255u, tok_of(r) < V && (k & mask) == prefix);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        uint32_t cum = 0, d = 0;
+        for (int i = 255; i >= 0; --i) {
+          if (cum + hist_n[i] >= rest) { d = (uint32_t)i; break; }
+          cum += hist_n[i];
+        }
+        sel[0] = d;
+        sel[1] = rest - cum;
+      }
+      __syncthreads();
+      prefix |= sel[0] << shift;
+      mask |= 255u << shift;
+      rest = sel[1];
+    }
+    corte = from_ordered(prefix);
+  }
+  // from here x[r] is the kept logit or -inf
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (x[r] < corte) x[r] = ninf;
+  float mloc = ninf;
+#pragma unroll
+  for (int r = 0; r < R; ++r) mloc = fmaxf(mloc, x[r]);
   const float m3 = block_max(mloc, red);
-  float tau = -1.f;                                              // keep probabilities >= tau (all when < 0)
+  float tau = -1.f;
   float S3 = 1.f;
   if (a.top_p < 1.f) {
     float s = 0.f;
-    for (int64_t v = tid; v < V; v += kSampleThreads) {
-      const float x = l3(v);
-      if (kept_k(x)) s += expf(x - m3);
-    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) s += expf(x[r] - m3);
     S3 = block_sum(s, red);
     const double target = ceil((double)a.top_p * kMassScale);
     uint32_t prefix = 0, mask = 0;
     unsigned long long acc = 0;
     bool found = true;
     for (int shift = 24; shift >= 0 && found; shift -= 8) {
+      __syncthreads();
       for (int i = tid; i < 256; i += kSampleThreads) {
         hist_n[i] = 0;
         hist_m[i] = 0;
       }
       __syncthreads();
-      for (int64_t base = 0; base < V; base += kSampleThreads) {
-        const int64_t v = base + tid;
-        float p = 0.f;
-        bool in = false;
-        if (v < V) {
-          const float x = l3(v);
-          in = kept_k(x);
-          if (in) p = expf(x - m3) / S3;
-        }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const bool in = x[r] != ninf;
+        const float p = in ? expf(x[r] - m3) / S3 : 0.f;
         const uint32_t k = __float_as_uint(p);
         hist_mass(hist_n, hist_m, (k >> shift) & 255u, in && (k & mask) == prefix,
                   (unsigned long long)rint((double)p * kMassScale));
       }
       __syncthreads();
       if (tid == 0) {
-        // from the largest values down: the bin where the mass of everything at or above it first reaches top_p
         int d = -1;
         for (int i = 255; i >= 0; --i) {
           if (hist_n[i] == 0) continue;
@@ -424,97 +968,85 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
       found = sel[1] != 0;
       prefix |= sel[0] << shift;
       mask |= 255u << shift;
-      __syncthreads();
     }
     if (found) tau = __uint_as_float(prefix);
+    if (tau >= 0.f) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (x[r] != ninf && !(expf(x[r] - m3) / S3 >= tau)) x[r] = ninf;
+    }
   }
 
-  // final probabilities: softmax over what is kept, then the quote-mass correction
-  auto keep = [&](int64_t v, float* e) {
-    const float x = l3(v);
-    if (!kept_k(x)) return false;
-    *e = expf(x - m3);
-    return tau < 0.f || (*e / S3) >= tau;
-  };
-  float S4;
-  {
-    float s = 0.f;
-    for (int64_t v = tid; v < V; v += kSampleThreads) {
-      float e;
-      if (keep(v, &e)) s += e;
-    }
-    S4 = block_sum(s, red);
+  // final probabilities in place: softmax over what is kept, then the quote-mass correction
+  float s4 = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    x[r] = expf(x[r] - m3);
+    s4 += x[r];
   }
-  float sc_q = 1.f, sc_n = 1.f;
-  if (quote && (qprobe || nql > 0)) {
-    float c = 0.f, e;
-    if (qprobe) {
-      for (int64_t v = tid; v < V; v += kSampleThreads)
-        if (in_quote(v) && keep(v, &e)) c += e / S4;
-    } else if (tid < nql && keep(qlist[tid], &e)) {
-      c = e / S4;
-    }
+  const float S4 = block_sum(s4, red);
+#pragma unroll
+  for (int r = 0; r < R; ++r) x[r] = x[r] / S4;
+  if (hay_cita) {
+    float c = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if ((qmask >> r) & 1ull) c += x[r];
     const float mass_q = block_sum(c, red);
     if (mass_q > 0.f && mass_q < 1.f) {
-      sc_q = mass_p / fmaxf(mass_q, 1e-30f);
-      sc_n = (1.f - mass_p) / fmaxf(1.f - mass_q, 1e-30f);
+      const float sc_q = mass_p / fmaxf(mass_q, 1e-30f), sc_n = (1.f - mass_p) / fmaxf(1.f - mass_q, 1e-30f);
+#pragma unroll
+      for (int r = 0; r < R; ++r) x[r] = x[r] * (((qmask >> r) & 1ull) ? sc_q : sc_n);
     }
   }
-  const bool scaled = sc_q != 1.f || sc_n != 1.f;
-  auto prob = [&](int64_t v) {
-    float e;
-    if (!keep(v, &e)) return 0.f;
-    const float p = e / S4;
-    return scaled ? p * (in_quote(v) ? sc_q : sc_n) : p;
-  };
   if (a.prob_out) {
-    for (int64_t v = tid; v < V; v += kSampleThreads) a.prob_out[b * V + v] = prob(v);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (tok_of(r) < V) a.prob_out[b * V + tok_of(r)] = x[r];
   }
 
-  // the draw: inverse CDF over the tokens in index order, each thread a contiguous segment
-  const int64_t seg = (V + kSampleThreads - 1) / kSampleThreads;
-  const int64_t v0 = (int64_t)tid * seg < V ? (int64_t)tid * seg : V;
-  const int64_t v1 = v0 + seg < V ? v0 + seg : V;
+  // the draw: inverse CDF in thread-major order
   float local = 0.f;
-  int64_t last_pos = -1;
-  for (int64_t v = v0; v < v1; ++v) {
-    const float p = prob(v);
-    local += p;
-    if (p > 0.f) last_pos = v;
+  int last = -1;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    local += x[r];
+    if (x[r] > 0.f) last = r;
   }
+  __syncthreads();
   scan[tid] = local;
   if (tid < 2) pick[tid] = tid == 0 ? 0x7fffffff : -1;
   __syncthreads();
-  for (int off = 1; off < kSampleThreads; off <<= 1) {        // inclusive scan (Hillis-Steele), fixed order
+  for (int off = 1; off < kSampleThreads; off <<= 1) {
     const float add = tid >= off ? scan[tid - off] : 0.f;
     __syncthreads();
     scan[tid] += add;
     __syncthreads();
   }
-  // thread t owns [scan[t - 1], scan[t]): neighbouring bounds are the same numbers, so the segments tile [0, total)
   const float total = scan[kSampleThreads - 1];
   const float before = tid > 0 ? scan[tid - 1] : 0.f;
   const float after = scan[tid];
-  const uint64_t r = mix64(a.seed ^ mix64((uint64_t)pos * 0x9e3779b97f4a7c15ull + (uint64_t)b));
-  const float u = (float)(r >> 40) * (1.f / 16777216.f);      // 24 random bits: [0, 1)
+  const uint64_t rnd = mix64(a.seed ^ mix64((uint64_t)pos * 0x9e3779b97f4a7c15ull + (uint64_t)b));
+  const float u = (float)(rnd >> 40) * (1.f / 16777216.f);
   const float target = u * total;
   if (local > 0.f && target >= before && target < after) {
     const float inside = target - before;
-    float acc = 0.f;                                             // summed from 0 in `local`'s order
-    int64_t chosen = -1;
-    for (int64_t v = v0; v < v1; ++v) {
-      const float p = prob(v);
-      acc += p;
-      if (p > 0.f && acc > inside) { chosen = v; break; }
+    float acc = 0.f;
+    int chosen = -1;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      acc += x[r];
+      if (chosen < 0 && x[r] > 0.f && acc > inside) chosen = r;
     }
-    if (chosen < 0) chosen = last_pos;
-    if (chosen >= 0) atomicMin(&pick[0], (int)chosen);
+    if (chosen < 0) chosen = last;
+    if (chosen >= 0) atomicMin(&pick[0], tid * R + chosen);     // the position in thread-major order
   }
-  if (last_pos >= 0) atomicMax(&pick[1], (int)last_pos);
+  if (last >= 0) atomicMax(&pick[1], tid * R + last);
   __syncthreads();
 
   if (tid == 0) {
-    int64_t tok = pick[0] != 0x7fffffff ? pick[0] : (pick[1] >= 0 ? pick[1] : 0);
+    const int o = pick[0] != 0x7fffffff ? pick[0] : pick[1];
+    int64_t tok = o >= 0 ? (int64_t)(o % R) * kSampleThreads + o / R : 0;
     if (a.stop_token >= 0) {
       if (a.done[b]) {
         tok = a.stop_token;
@@ -619,6 +1151,15 @@ extern "C" int asrn_sample(const float* lg, int64_t ldl, float* work, uint32_t* 
   a.window = window;
   a.stop_token = stop_token;
   a.seed = seed;
-  hipLaunchKernelGGL(k_sample, dim3((unsigned)B), dim3(kSampleThreads), 0, (hipStream_t)stream, a);
+  const dim3 grid((unsigned)B), block(kSampleThreads);
+  const hipStream_t st = (hipStream_t)stream;
+  // rows up to 16 Ki tokens in registers (R tokens per thread: R = 16 is what fits 128 VGPRs, the budget of a
+  // 1,024-thread workgroup), longer rows from global memory
+  if (V <= 4 * kSampleThreads)
+    hipLaunchKernelGGL(k_sample_reg<4>, grid, block, 0, st, a);
+  else if (V <= 16 * kSampleThreads)
+    hipLaunchKernelGGL(k_sample_reg<16>, grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL(k_sample, grid, block, 0, st, a);
   return check_launch("asrn_sample");
 }

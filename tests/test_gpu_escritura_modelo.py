@@ -4,7 +4,8 @@ escribir against the reference's own tests of it (tests/test_nucleo.py:86-140, 6
 
 - ops.muestrear (asrn_sample): the final probability row equals oracle.muestreo's (penalty, bans with their fallback,
   quote mask, temperature, top-k, top-p, the quote-mass correction) within fp32 rounding, with the same support, both
-  where the n-gram contexts' successor lists answer and where a context overflows them and every token is probed;
+  where the n-gram contexts' successor lists answer and where a context overflows them and every token is probed,
+  with the row in registers (V up to 16,384) and read from memory (larger V);
   the token lies in that support and is written into the text; the n-gram sets take the new n-grams (checked by a
   second step against the oracle on the longer text); draws follow the distribution (chi-square) and repeat for a
   seed.
@@ -95,6 +96,8 @@ SAMPLER_CASES = [
     dict(V=50304, T=0.8, k=40, p=0.9, pena=1.1, ventana=64, nb=3, nq=4),
     dict(V=1000, T=1.0, k=1, p=1.0, pena=1.0, ventana=64, nb=0, nq=4),
     dict(V=1000, T=0.8, k=0, p=0.0, pena=1.0, ventana=64, nb=0, nq=0),
+    dict(V=10000, T=0.9, k=100, p=0.95, pena=1.2, ventana=32, nb=2, nq=3),
+    dict(V=70000, T=0.9, k=100, p=0.95, pena=1.2, ventana=32, nb=2, nq=3),
     # contexts with more distinct successors than the inline lists hold: the bans and the quote mask probe every token
     dict(V=20, T=0.7, k=0, p=1.0, pena=1.0, ventana=64, nb=1, nq=2),
     dict(V=50, T=1.0, k=5, p=0.9, pena=1.0, ventana=64, nb=1, nq=2),
