@@ -3,8 +3,9 @@ reference's _Escritor (model part) and escribir (asrn/nucleo.py:1717-1854, 1965-
 
 EscritorModelo keeps, besides each ASRN layer's EscritorCapa state, each local block's last k - 1 LayerNorm rows (the
 causal convolution's window) and, for mezcla='memoria', its per-channel memory, so one new token costs the same work
-whatever the text length. (The reference's step leaves the 'memoria' blocks' memory out, nucleo:1811-1814; here the
-step equals the whole-text model for both block kinds.)
+whatever the text length. A 'conv' block's step in fp32 is three fused kernels (asrn_block_step) that stream its
+three weight matrices once for all rows, its window a ring indexed by the position. (The reference's step leaves the
+'memoria' blocks' memory out, nucleo:1811-1814; here the step equals the whole-text model for both block kinds.)
 
 escribir keeps the text, the n-gram sets behind the quote mask and the no-repeat bans, and the stop flags on the
 device, and makes each token's choice with one kernel (ops.muestrear: penalty, bans, quote mask, temperature, top-k,
@@ -48,11 +49,24 @@ class EscritorModelo:
         self.cap = max(L0 + 1, capacidad)
         E = m.emb(x0)
         h = E
-        self.ventanas, self.memorias = [], []
+        self.ventanas, self.memorias, self.anillos, self.fusion = [], [], [], []
+        if hasattr(self, 'espacio'):
+            del self.espacio
         capas = iter(self.capas)
         for i, blq in enumerate(m.bloques):
             z = blq.ln1(h)
-            self.ventanas.append(_ventana_inicial(z, blq.k))
+            ventana = _ventana_inicial(z, blq.k)
+            # the fused step keeps the window as a ring: position t at slot t mod (k - 1)
+            fusion = ops.paso_bloque_ok(blq, h[:, -1])
+            anillo = None
+            if fusion and blq.k > 1:
+                anillo = torch.empty_like(ventana)
+                anillo[:, :, (L0 + torch.arange(blq.k - 1, device=x0.device)) % (blq.k - 1)] = ventana
+            self.ventanas.append(None if fusion else ventana)
+            self.anillos.append(anillo)
+            self.fusion.append(fusion)
+            if fusion and not hasattr(self, 'espacio'):
+                self.espacio = ops.espacio_bloque(B, blq.ln1.weight.shape[0], blq.ff[0].weight.shape[0], x0.device)
             if blq.mezcla == 'memoria':
                 u, f = blq.mem(z).float().chunk(2, dim=-1)
                 f = torch.sigmoid(f) * blq.f_max
@@ -66,8 +80,14 @@ class EscritorModelo:
         self.pos = torch.full((1,), L0, dtype=torch.int64, device=x0.device)
         return m.head(m.ln_f(h[:, -1]))
 
-    def _bloque(self, i, blq, h, mem_i):
-        """Block i's step on the new token's state h (B, d): the window shifts by one row."""
+    def _bloque(self, i, blq, h, mem_i, pos):
+        """Block i's step on the new token's state h (B, d) at position pos: three fused kernels for 'conv' blocks in
+        fp32 (asrn_block_step, the window a ring), else PyTorch ops on a window that shifts by one row."""
+        if self.fusion[i]:
+            if not ops.paso_bloque_ok(blq, h):
+                raise ValueError('EscritorModelo: the prompt ran the fused block step (fp32, no autocast); every step '
+                                 'must run the same way')
+            return ops.paso_bloque(blq, h, self.anillos[i], pos, self.espacio)
         z = blq.ln1(h)
         ventana = torch.cat([self.ventanas[i], z.unsqueeze(-1)], dim=-1)            # (B, d, k)
         if blq.mezcla == 'conv':
@@ -93,7 +113,7 @@ class EscritorModelo:
         capas = iter(self.capas)
         k = 0
         for i, blq in enumerate(m.bloques):
-            h = self._bloque(i, blq, h, k)
+            h = self._bloque(i, blq, h, k, pos)
             k += blq.mezcla == 'memoria'
             if i in m.pos_largo:
                 h = next(capas)._cuerpo(e_t, self.e_ult, h, pieza, pos, t_max=t_max)

@@ -844,3 +844,43 @@ def muestrear(lg, texto, pos, pos_max, L0, piezas, terminado, paso_fin, trabajo,
          *(cita.punteros() if cita else [None, None, None, None, 0, 0]),
          *(prohibidas.punteros() if prohibidas else [None, None, None, None, 0, 0]), w, B, V, float(temperatura), int(top_k), float(top_p), float(pena),
          int(ventana), -1 if parar_en is None else int(parar_en), ctypes.c_uint64(semilla), stream_of(dev))
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# the model's local block, generation step
+# ---------------------------------------------------------------------------------------------------------------------
+
+def paso_bloque_ok(blq, h):
+    """Whether asrn_block_step takes this block and state: mezcla 'conv', fp32 parameters and state, no autocast,
+    one LayerNorm epsilon, the block's usual feed-forward layout."""
+    dev = h.device.type
+    ps = [blq.ln1.weight, blq.ln1.bias, blq.conv.weight, blq.conv.bias, blq.ln2.weight, blq.ln2.bias, blq.ff[0].weight,
+          blq.ff[0].bias, blq.ff[2].weight, blq.ff[2].bias]
+    return (blq.mezcla == 'conv' and h.is_cuda and h.dtype == torch.float32 and h.dim() == 2 and h.stride(1) == 1
+            and not torch.is_autocast_enabled(dev) and all(p is not None and p.dtype == torch.float32 for p in ps)
+            and blq.ln1.eps == blq.ln2.eps and blq.conv.groups == 1)
+
+
+def espacio_bloque(B, d, ff, dev):
+    """The workspace of paso_bloque at these sizes (the products' partial sums); one serves every block of a writer
+    whose blocks share d and ff."""
+    return torch.empty(int(query('asrn_block_step_workspace', B, d, ff)), dtype=torch.uint8, device=dev)
+
+
+def paso_bloque(blq, h, anillo, pos, espacio):
+    """The block's step for rows h (B, d) at position pos (a one-element int64 device tensor): returns (B, d); the ring
+    anillo (B, d, k - 1) of LayerNorm1 rows (position t at slot t mod (k - 1)) takes this position's row."""
+    dev = _dev(h)
+    B, d = h.shape
+    k = blq.k
+    ff = blq.ff[0].weight.shape[0]
+    if k > 1 and (anillo is None or tuple(anillo.shape) != (B, d, k - 1) or not anillo.is_contiguous()):
+        raise ValueError('paso_bloque: the ring is a contiguous (B, d, k - 1) fp32 tensor')
+    ws = [_c(p.detach()) for p in (blq.ln1.weight, blq.ln1.bias, blq.conv.weight, blq.conv.bias, blq.ln2.weight,
+                                   blq.ln2.bias, blq.ff[0].weight, blq.ff[0].bias, blq.ff[2].weight, blq.ff[2].bias)]
+    z, h1, x2, out = (torch.empty((B, d), dtype=torch.float32, device=dev) for _ in range(4))
+    x1 = torch.empty((B, d * k), dtype=torch.float32, device=dev)
+    call('asrn_block_step', ptr(h), h.stride(0), ptr(anillo), ptr(pos), B, d, k, ff, *[ptr(w) for w in ws],
+         float(blq.ln1.eps), ptr(z), ptr(x1), ptr(h1), ptr(x2), ptr(out), ptr(espacio), espacio.numel(),
+         stream_of(dev))
+    return out

@@ -377,6 +377,23 @@ int asrn_sample(const float* lg, int64_t ldl, float* work, uint32_t* quote_bits,
                 int64_t B, int64_t V, float temperature, int32_t top_k, float top_p, float penalty, int32_t window,
                 int64_t stop_token, uint64_t seed, void* stream);
 
+/* ---- the model's local block, generation step -----------------------------------------------------------------
+ * Replaces the local block's part of _Escritor.paso (asrn/nucleo.py:1811-1814: LayerNorm, the window cat, conv1d,
+ * GELU, the adds, LayerNorm and the feed-forward layer, about a dozen launches per block) for mezcla 'conv' blocks
+ * (BloqueLocal, nucleo:969-1014): out = h1 + W2 GELU(W1 LN2(h1) + b1) + b2 with h1 = h + GELU(conv([ring; LN1(h)])
+ * + conv_b), for B rows h (stride ldh), fp32, in six launches (three products on the matrix cores in depth splits,
+ * three row-wise kernels that prepare their operands and sum the splits in a fixed order). conv_w (d, d * k) is
+ * nn.Conv1d's weight (d, d, k); w1 (ff, d), w2 (d, ff). ring (B, d, k - 1) holds LayerNorm1 of the k - 1 previous
+ * positions, position t at slot t mod (k - 1); the step reads taps (pos + j) mod (k - 1) and writes LN1(h) at slot
+ * pos mod (k - 1) (pos read from *pos at run time). z, h1, x2 (B, d) and x1 (B, d * k) are scratch outputs; out
+ * (B, d). workspace: asrn_block_step_workspace(B, d, ff) bytes (the products' partial sums). */
+int64_t asrn_block_step_workspace(int64_t B, int32_t d, int32_t ff);
+int asrn_block_step(const float* h, int64_t ldh, float* ring, const int64_t* pos, int64_t B, int32_t d, int32_t k,
+                    int32_t ff, const float* ln1_w, const float* ln1_b, const float* conv_w, const float* conv_b,
+                    const float* ln2_w, const float* ln2_b, const float* w1, const float* b1, const float* w2,
+                    const float* b2, float eps, float* z, float* x1, float* h1, float* x2, float* out,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

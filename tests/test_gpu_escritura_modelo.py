@@ -191,6 +191,39 @@ def test_model_writer_matches_reference_writer(ajeno):
         assert (got - t['entero']).abs().max().item() < TOL
 
 
+@pytest.mark.parametrize('B,d,k,ff,L', [(16, 768, 4, 1536, 9), (20, 96, 3, 40, 5), (3, 64, 1, 128, 4),
+                                          (2, 32, 4, 64, 2)])
+def test_block_step_equals_whole_text_block(B, d, k, ff, L):
+    """asrn_block_step against BloqueLocal.forward at the last position of a short text: the ring built from the
+    earlier positions' LayerNorm rows (slot t mod (k - 1)), then the step at position L - 1; 20 rows span two row
+    tiles, k = 1 has no ring, L < k starts with zeros."""
+    say('block step', B, d, k, ff, L)
+    torch.manual_seed(B + d)
+    blq = asrn_amd.BloqueLocal(d, k, ff).to(DEV)
+    with torch.no_grad():
+        for p in blq.parameters():
+            p.add_(torch.randn_like(p) * 0.1)
+        h = torch.randn(B, L, d, device=DEV)
+        todo = blq(h)[:, -1]
+        anillo = None
+        if k > 1:
+            z = blq.ln1(h[:, :-1])
+            ventana = torch.nn.functional.pad(z, (0, 0, k - 1, 0))[:, z.shape[1]:].transpose(1, 2).contiguous()
+            anillo = torch.empty_like(ventana)
+            anillo[:, :, (L - 1 + torch.arange(k - 1, device=DEV)) % (k - 1)] = ventana
+        pos = torch.tensor([L - 1], dtype=torch.int64, device=DEV)
+        espacio = ops.espacio_bloque(B, d, ff, DEV)
+        anillo0 = anillo.clone() if anillo is not None else None
+        out = ops.paso_bloque(blq, h[:, -1], anillo, pos, espacio)
+        out2 = ops.paso_bloque(blq, h[:, -1], anillo0, pos, espacio)
+        assert torch.equal(out, out2)                           # deterministic, the workspace reused
+        err = ((out - todo).abs().max() / todo.abs().max()).item()
+        print('max relative difference', err, flush=True)
+        assert err < 1e-5
+        if k > 1:                                               # the ring took LayerNorm1 of position L - 1
+            assert torch.allclose(anillo[:, :, (L - 1) % (k - 1)], blq.ln1(h[:, -1]), atol=1e-5)
+
+
 @pytest.mark.parametrize('mezcla', ['conv', 'memoria'])
 def test_escribir_equals_whole_text(mezcla):
     """tests/test_nucleo.py:105-115: the logits of every step equal the model on the whole written text."""
