@@ -1,68 +1,33 @@
 // a1 + a2 + a3: sign hash, stable bucket sort and the recent-mates index, for every row r = b*T + tau.
 //
-//   k_bucket_ids     the sign hash: one thread per position computes every table's id from its phi row.
-//   k_bucket_tile    one workgroup per tile of up to 4096 positions of a row: a stable LSD radix sort of the ids in
-//                    LDS (7 bits per pass, ranks by wave ballots), so ties keep text order and the result equals
-//                    torch.argsort(stable=True) bit for bit (reference asrn/estable.py:283); a row that is one tile
-//                    also gets its ranks and windows there, from the sorted ids in LDS.
+//   k_bucket_rows    one workgroup of 1024 threads per tile of up to 4096 positions of a row: the sign hash of its
+//                    positions (their phi columns of table tau, read 4 rows x 16 columns per load instruction and
+//                    turned into ids by ballots), then a stable LSD radix sort of the ids in LDS, 7 bits per pass:
+//                    each wave owns 256 consecutive positions, ranks equal digits among its lanes by ballots and
+//                    across its 4 rounds by a per-wave count in LDS, and one exclusive scan of the (digit, wave)
+//                    counts places every group, so ties keep text order and the result equals
+//                    torch.argsort(stable=True) bit for bit (reference asrn/estable.py:283). A row that is one tile
+//                    also gets its ranks and windows there: the bucket start and end of every sorted index from a
+//                    forward max scan and a backward min scan of the run boundaries.
 //   k_bucket_merge   rows longer than a tile: merge passes of sorted runs (each element finds its place in the
 //                    partner run by a binary search), ping-ponging between the output buffers.
 //   k_bucket_finish  (longer rows) per sorted index: the rank of its position and win = min(C, mates before) |
 //                    min(C, mates after) << 8, read off the sorted ids within C places on either side.
+#include <limits.h>
+
 #include "common.h"
 
 namespace asrn {
 
 constexpr int kMaxBits = 14;
-constexpr int kTileMax = 4096;
-
-// Tile length for rows of L: a power of two, at most kTileMax, at least 4. Shorter tiles mean more workgroups and
-// more merge passes.
-static int bucket_tile(int64_t L) {
-  int tile = 4;
-  while (tile < L && tile < kTileMax) tile <<= 1;
-  return tile;
-}
-
-// The sign hash for kIdTokens positions per workgroup: their phi rows (T*nb floats each) are read with consecutive
-// threads on consecutive floats and kept as sign bytes in LDS; then one thread per (table, position) assembles the
-// id, positions fastest, so the ids rows are written contiguously.
-constexpr int kIdTokens = 16;
-constexpr int kIdThreads = 256;
-
-__global__ __launch_bounds__(kIdThreads) void k_bucket_ids(const float* __restrict__ phi, int64_t B, int64_t L, int T,
-                                                           int nb, int64_t stride, int32_t* __restrict__ ids) {
-  __shared__ uint8_t sgn[kIdTokens * 32 * kMaxBits];
-  const int tnb = T * nb;
-  const int64_t e0 = (int64_t)blockIdx.x * kIdTokens, n = B * L;
-  constexpr int U = 8;                             // loads in flight per thread
-  for (int k0 = 0; k0 < kIdTokens * tnb; k0 += kIdThreads * U) {
-    float v[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = k0 + u * kIdThreads + threadIdx.x;
-      const int row = k / tnb, col = k - row * tnb;
-      const int64_t e = e0 + row;
-      v[u] = (k < kIdTokens * tnb && e < n) ? phi[e * stride + col] : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = k0 + u * kIdThreads + threadIdx.x;
-      if (k < kIdTokens * tnb) sgn[k] = v[u] > 0.f ? 1 : 0;        // strict > 0 (nucleo:663)
-    }
-  }
-  __syncthreads();
-  for (int p = threadIdx.x; p < kIdTokens * T; p += kIdThreads) {
-    const int tau = p / kIdTokens, row = p - tau * kIdTokens;
-    const int64_t e = e0 + row;
-    if (e < n) {
-      uint32_t id = 0;
-      for (int j = 0; j < nb; ++j) id |= (uint32_t)sgn[row * tnb + tau * nb + j] << j;
-      const int64_t b = e / L, t = e % L;
-      ids[(b * T + tau) * L + t] = (int32_t)id;
-    }
-  }
-}
+constexpr int kTile = 4096;                        // positions per workgroup
+constexpr int kPosBits = 12;                       // a position in the tile
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kSeg = kTile / kWaves;               // 256 consecutive positions per wave, 4 rounds of 64
+constexpr int kRadixBits = 7;
+constexpr int kBins = 1 << kRadixBits;
+static_assert(kBins * kWaves == 2 * kThreads, "two (digit, wave) counts per thread in the scan");
 
 // before / after of sorted index i among n sorted ids: same-bucket neighbours within C places on either side
 template <class Ids>
@@ -94,100 +59,218 @@ struct GlobalIds {
   __device__ __forceinline__ int operator[](int64_t i) const { return p[i]; }
 };
 
-// One tile of a row (up to 4096 positions, 1024 threads): a stable LSD radix sort of the ids in LDS, 7 bits per pass.
-// A pass visits the tile in 4 rounds of 1024 consecutive positions; inside a round each wave ranks its lanes with
-// equal digits by ballots (match_key), and an exclusive scan of the (digit, round, wave) group sizes gives every group
-// its output start, so equal digits keep their order and the result equals torch.argsort(stable=True). When the tile
-// is the whole row (`whole`), also the rank and window of every position, from the sorted ids in LDS.
-constexpr int kRadixBits = 7;
-constexpr int kRadixBins = 1 << kRadixBits;
-constexpr int kTileThreads = 1024;
-constexpr int kRounds = kTileMax / kTileThreads;
-constexpr int kTileWaves = kTileThreads / kWave;
-constexpr int kGroups = kRadixBins * kRounds * kTileWaves;   // 8192 (digit, round, wave) groups
-constexpr int kPerThread = kGroups / kTileThreads;
+// LDS reads and writes of one wavefront take effect in program order; the fence keeps the compiler from moving them
+__device__ __forceinline__ void wave_lds_order() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
-struct LdsPacked {                                 // (id << 16 | position in the tile) -> id
-  const uint32_t* p;
-  __device__ __forceinline__ int operator[](int64_t i) const { return (int)(p[i] >> 16); }
-};
+// exclusive scans over the workgroup's threads (every thread calls them; wt: kWaves ints of LDS)
+__device__ __forceinline__ int block_excl_sum(int a, int* wt) {
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  int inc = a;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int u = __shfl_up(inc, off, kWave);
+    if (lane >= off) inc += u;
+  }
+  if (lane == kWave - 1) wt[wave] = inc;
+  __syncthreads();
+  int pre = 0;
+  for (int w = 0; w < wave; ++w) pre += wt[w];
+  __syncthreads();
+  return pre + inc - a;
+}
+__device__ __forceinline__ int block_excl_max(int a, int* wt) {      // over the threads before this one
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  int inc = a;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int u = __shfl_up(inc, off, kWave);
+    if (lane >= off) inc = max(inc, u);
+  }
+  if (lane == kWave - 1) wt[wave] = inc;
+  __syncthreads();
+  int pre = INT_MIN;
+  for (int w = 0; w < wave; ++w) pre = max(pre, wt[w]);
+  int ex = __shfl_up(inc, 1, kWave);
+  if (lane == 0) ex = INT_MIN;
+  __syncthreads();
+  return max(pre, ex);
+}
+__device__ __forceinline__ int block_excl_min_rev(int a, int* wt) {  // over the threads after this one
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  int inc = a;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int u = __shfl_down(inc, off, kWave);
+    if (lane + off < kWave) inc = min(inc, u);
+  }
+  if (lane == 0) wt[wave] = inc;
+  __syncthreads();
+  int post = INT_MAX;
+  for (int w = wave + 1; w < kWaves; ++w) post = min(post, wt[w]);
+  int ex = __shfl_down(inc, 1, kWave);
+  if (lane == kWave - 1) ex = INT_MAX;
+  __syncthreads();
+  return min(post, ex);
+}
 
-__global__ __launch_bounds__(kTileThreads) void k_bucket_tile(const int32_t* __restrict__ ids, int64_t L, int T,
-                                                              int nb, int tile, int C, bool whole,
-                                                              int32_t* __restrict__ key_out,
-                                                              int32_t* __restrict__ pos_out,
-                                                              int32_t* __restrict__ rank, int32_t* __restrict__ win) {
-  __shared__ uint32_t kbuf[2][kTileMax];
-  __shared__ int cnt[kGroups];
-  __shared__ int wave_tot[kTileWaves];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t r = blockIdx.y;
-  const int64_t t0 = (int64_t)blockIdx.x * tile;
-  const int n = (int)(L - t0 < tile ? L - t0 : tile);
-  for (int e = tid; e < kTileMax; e += kTileThreads)   // padding takes the largest id and sorts last, in order
-    kbuf[0][e] = e < n ? ((uint32_t)ids[r * L + t0 + e] << 16) | (uint32_t)e : (0xFFFFu << 16) | (uint32_t)e;
+// Grid (tiles, B * T), kThreads threads. Workgroup y takes table tau = y / B of batch row b = y % B, so with B a
+// multiple of 8 every table of one batch row runs on one XCD and its phi rows are read into that XCD's L2 once.
+// whole: the tile is the row, so rank and win are written here; otherwise the sorted tile's (id, position) pairs go
+// to key_out / pos_out (the merge passes finish them).
+__global__ __launch_bounds__(kThreads) void k_bucket_rows(const float* __restrict__ phi, int64_t B, int64_t L, int T,
+                                                          int nb, int64_t stride, int C, bool whole,
+                                                          int32_t* __restrict__ ids, int32_t* __restrict__ key_out,
+                                                          int32_t* __restrict__ pos_out, int32_t* __restrict__ rank,
+                                                          int32_t* __restrict__ win) {
+  __shared__ uint32_t kb[2][kTile];                // (id << kPosBits | position in the tile)
+  __shared__ int hist[kBins * kWaves];             // (digit, wave) counts, digit-major
+  __shared__ int wt[kWaves];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int64_t b = blockIdx.y % B, tau = blockIdx.y / B;
+  const int64_t r = b * T + tau;
+  const int64_t t0 = (int64_t)blockIdx.x * kTile;
+  const int n = (int)(L - t0 < kTile ? L - t0 : kTile);
+  const int seg = kSeg * wave;                     // element (round q, lane) of this wave: position seg + 64 q + lane
+
+  // sign hash: load u of round q reads position seg + 64 q + 4 u + (lane >> 4), column lane & 15; its ballot holds
+  // the ids of 4 positions, one per 16-lane group; lane l keeps load l >> 2's group l & 3
+  uint32_t k[4];
+  {
+    const float* base = phi + (b * L + t0) * stride + tau * nb;
+    const int g = lane >> 4, c = lane & 15;
+    // 32 loads of the wave in flight at a time: unconditional loads from clamped addresses (a load under a branch is
+    // waited for before the branch joins), the out-of-range ones masked afterwards
+    const int cc = c < nb ? c : nb - 1;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float v[32];
+      if (seg + kSeg <= n) {                         // the wave's positions are all in the row
+        const float* p0 = base + (int64_t)(seg + 128 * h + g) * stride + cc;
+#pragma unroll
+        for (int u = 0; u < 32; ++u) v[u] = p0[(int64_t)(4 * u) * stride];
+      } else {
+#pragma unroll
+        for (int u = 0; u < 32; ++u) {
+          const int e = seg + 128 * h + 4 * u + g;
+          v[u] = base[(int64_t)(e < n ? e : n - 1) * stride + cc];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 32; ++u)
+        if (!(c < nb && seg + 128 * h + 4 * u + g < n)) v[u] = 0.f;
+#pragma unroll
+      for (int qq = 0; qq < 2; ++qq) {
+        const int q = 2 * h + qq;
+        uint32_t id = 0;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const uint64_t m = __ballot(v[16 * qq + u] > 0.f);       // strict > 0 (nucleo:663)
+          if ((lane >> 2) == u) id = (uint32_t)(m >> (16 * (lane & 3))) & 0xFFFFu;
+        }
+        const int e = seg + 64 * q + lane;
+        if (e < n) ids[r * L + t0 + e] = (int32_t)id;
+        // padding takes the largest id and sorts after every real position, in order
+        k[q] = ((e < n ? id : (1u << nb) - 1u) << kPosBits) | (uint32_t)e;
+      }
+    }
+  }
+
+  // radix passes over the ids, least significant digit first
   int cur = 0;
   const int passes = (nb + kRadixBits - 1) / kRadixBits;
   for (int pass = 0; pass < passes; ++pass) {
-    const int shift = 16 + pass * kRadixBits;
+    const int shift = kPosBits + pass * kRadixBits;
     const int bits = nb - pass * kRadixBits < kRadixBits ? nb - pass * kRadixBits : kRadixBits;
+    hist[lane * kWaves + wave] = 0;
+    hist[(lane + kWave) * kWaves + wave] = 0;
+    wave_lds_order();
+    int rk[4], dg[4];
 #pragma unroll
-    for (int i = 0; i < kPerThread; ++i) cnt[tid * kPerThread + i] = 0;
-    __syncthreads();                               // kbuf[cur] written, counts cleared
-    uint32_t v[kRounds];
-    int dig[kRounds], below[kRounds];
-#pragma unroll
-    for (int q = 0; q < kRounds; ++q) {
-      v[q] = kbuf[cur][q * kTileThreads + tid];
-      dig[q] = (int)((v[q] >> shift) & ((1u << bits) - 1u));
-      const uint64_t peers = match_key(dig[q], bits, true);
-      below[q] = __popcll(peers & ((1ull << lane) - 1ull));
-      if ((peers >> lane) == 1ull) cnt[(dig[q] * kRounds + q) * kTileWaves + wave] = __popcll(peers);
+    for (int q = 0; q < 4; ++q) {
+      const int d = (int)((k[q] >> shift) & ((1u << bits) - 1u));
+      const uint64_t peers = match_key(d, bits, true);
+      const int base = hist[d * kWaves + wave];                    // this digit in the wave's earlier rounds
+      rk[q] = base + __popcll(peers & ((1ull << lane) - 1ull));
+      dg[q] = d;
+      wave_lds_order();
+      if (lane == __ffsll((unsigned long long)peers) - 1) hist[d * kWaves + wave] = base + __popcll(peers);
+      wave_lds_order();
     }
     __syncthreads();
-    // exclusive scan of the 8192 group sizes: kPerThread consecutive per thread, then across threads
-    int local[kPerThread];
-    int sum = 0;
-#pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
-      local[i] = cnt[tid * kPerThread + i];
-      sum += local[i];
-    }
-    int incl = sum;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const int u = __shfl_up(incl, off, kWave);
-      if (lane >= off) incl += u;
-    }
-    if (lane == kWave - 1) wave_tot[wave] = incl;
-    __syncthreads();
-    int wave_base = 0;
-    for (int w = 0; w < wave; ++w) wave_base += wave_tot[w];
-    int run = wave_base + incl - sum;
-#pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
-      cnt[tid * kPerThread + i] = run;
-      run += local[i];
-    }
+    const int h0 = hist[2 * tid], h1 = hist[2 * tid + 1];
+    const int ex = block_excl_sum(h0 + h1, wt);
+    hist[2 * tid] = ex;
+    hist[2 * tid + 1] = ex + h0;
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < kRounds; ++q)
-      kbuf[cur ^ 1][cnt[(dig[q] * kRounds + q) * kTileWaves + wave] + below[q]] = v[q];
-    cur ^= 1;
-    __syncthreads();                               // before the next pass clears the counts
+    for (int q = 0; q < 4; ++q) kb[cur][hist[dg[q] * kWaves + wave] + rk[q]] = k[q];
+    __syncthreads();
+    if (pass + 1 < passes) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) k[q] = kb[cur][seg + 64 * q + lane];
+      cur ^= 1;
+    }
   }
-  for (int i = tid; i < n; i += kTileThreads) {    // the sorted tile has its real elements first
-    const uint32_t x = kbuf[cur][i];
-    key_out[r * L + t0 + i] = (int32_t)(x >> 16);
-    pos_out[r * L + t0 + i] = (int32_t)(t0 + (x & 0xFFFFu));
+  const uint32_t* srt = kb[cur];                   // the sorted tile; real positions first
+
+  // outputs per sorted index i = 4 tid + q
+  const int i0 = 4 * tid;
+  uint32_t s4[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) s4[q] = srt[i0 + q];
+  if (!whole) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (i0 + q < n) {
+        key_out[r * L + t0 + i0 + q] = (int32_t)(s4[q] >> kPosBits);
+        pos_out[r * L + t0 + i0 + q] = (int32_t)(t0 + (s4[q] & ((1u << kPosBits) - 1u)));
+      }
+    }
+    return;
   }
-  if (!whole) return;
-  const int64_t b = r / T, tau = r % T;
-  for (int i = tid; i < n; i += kTileThreads) {
-    const int64_t t = (int64_t)(kbuf[cur][i] & 0xFFFFu);
+  // bucket runs: start(i) = the last run start at or before i, end(i) = one past the last index of i's run
+  const uint32_t prev = i0 > 0 ? srt[i0 - 1] >> kPosBits : 0u;
+  const uint32_t next = i0 + 4 < kTile ? srt[i0 + 4] >> kPosBits : 0u;
+  int ls[4], le[4];
+  int run = INT_MIN;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = i0 + q;
+    const uint32_t id = s4[q] >> kPosBits, pid = q ? s4[q - 1] >> kPosBits : prev;
+    if (i == 0 || id != pid) run = i;
+    ls[q] = run;
+  }
+  const int pre = block_excl_max(run, wt);
+  int runb = INT_MAX;
+#pragma unroll
+  for (int q = 3; q >= 0; --q) {
+    const int i = i0 + q;
+    const uint32_t id = s4[q] >> kPosBits, nid = q < 3 ? s4[q + 1] >> kPosBits : next;
+    if (i == n - 1 || (i < n - 1 && id != nid)) runb = i + 1;
+    le[q] = runb;
+  }
+  const int post = block_excl_min_rev(runb, wt);
+  uint32_t* by_pos = kb[cur ^ 1];                  // free: rank | win << kPosBits per position in the tile
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = i0 + q;
+    if (i >= n) continue;
+    const int start = max(pre, ls[q]), end = min(post, le[q]);
+    const int before = min(C, i - start), after = min(C, end - 1 - i);
+    key_out[r * L + i] = (int32_t)(s4[q] >> kPosBits);
+    pos_out[r * L + i] = (int32_t)(s4[q] & ((1u << kPosBits) - 1u));
+    by_pos[s4[q] & ((1u << kPosBits) - 1u)] = (uint32_t)i | ((uint32_t)(before | (after << 8)) << kPosBits);
+  }
+  __syncthreads();
+  // consecutive lanes take consecutive positions: T-strided, not scattered, writes
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int t = q * kThreads + tid;
+    if (t >= n) continue;
+    const uint32_t x = by_pos[t];
     const int64_t o = (b * L + t) * T + tau;
-    rank[o] = i;
-    win[o] = window_of(LdsPacked{kbuf[cur]}, i, n, C);
+    rank[o] = (int32_t)(x & ((1u << kPosBits) - 1u));
+    win[o] = (int32_t)(x >> kPosBits);
   }
 }
 
@@ -249,29 +332,26 @@ extern "C" int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t 
   ASRN_REQUIRE(phi && ids && order && ids_sorted && rank && win, "asrn_bucket_sort: null pointer");
   hipStream_t st = (hipStream_t)stream;
   const int64_t rows = B * T;
-  const int tile = bucket_tile(L);
-  const int64_t tiles = (L + tile - 1) / tile;
+  const int64_t tiles = (L + kTile - 1) / kTile;
   int passes = 0;
-  for (int64_t w = tile; w < L; w <<= 1) ++passes;
+  for (int64_t w = kTile; w < L; w <<= 1) ++passes;
   // the merge passes ping-pong between (ids_sorted, order) and (rank, win), which the finish overwrites last: start
   // in the buffer that makes the final pass land in (ids_sorted, order)
   int32_t* bufk[2] = {ids_sorted, rank};
   int32_t* bufp[2] = {order, win};
   int cur = passes % 2;
+  hipLaunchKernelGGL(k_bucket_rows, dim3((unsigned)tiles, (unsigned)rows), dim3(kThreads), 0, st, phi, B, L, (int)T,
+                     (int)nb, phi_stride, (int)C, tiles == 1, ids, bufk[cur], bufp[cur], rank, win);
+  if (check_launch("asrn_bucket_sort/rows")) return 1;
   const int threads = 256;
   const unsigned blocks = (unsigned)((rows * L + threads - 1) / threads);
-  hipLaunchKernelGGL(k_bucket_ids, dim3((unsigned)((B * L + kIdTokens - 1) / kIdTokens)), dim3(kIdThreads), 0, st, phi,
-                     B, L, (int)T, (int)nb, phi_stride, ids);
-  hipLaunchKernelGGL(k_bucket_tile, dim3((unsigned)tiles, (unsigned)rows), dim3(kTileThreads), 0, st, ids, L, (int)T,
-                     (int)nb, tile, (int)C, tiles == 1, bufk[cur], bufp[cur], rank, win);
-  if (check_launch("asrn_bucket_sort/tile")) return 1;
-  for (int64_t w = tile; w < L; w <<= 1) {
+  for (int64_t w = kTile; w < L; w <<= 1) {
     hipLaunchKernelGGL(k_bucket_merge, dim3(blocks), dim3(threads), 0, st, bufk[cur], bufp[cur], bufk[cur ^ 1],
                        bufp[cur ^ 1], rows, L, w);
     if (check_launch("asrn_bucket_sort/merge")) return 1;
     cur ^= 1;
   }
-  if (tiles == 1) return 0;                        // the tile kernel wrote rank and win
+  if (tiles == 1) return 0;                        // the row kernel wrote rank and win
   hipLaunchKernelGGL(k_bucket_finish, dim3(blocks), dim3(threads), 0, st, ids_sorted, order, rows, L, (int)T, (int)C,
                      rank, win);
   return check_launch("asrn_bucket_sort/finish");

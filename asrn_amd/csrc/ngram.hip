@@ -1,18 +1,26 @@
 // a10: n-gram keys, their stable sort per (b, j) row, the repeated flags and the seen flags.
 //
 // Keys are fp64 and must round exactly as the reference's separate multiply and add (asrn/nucleo.py:182-184): the
-// kernel uses __dmul_rn / __dadd_rn and this file builds with -ffp-contract=off. The sort orders (key, position)
+// kernels use __dmul_rn / __dadd_rn and this file builds with -ffp-contract=off. The sort orders (key, position)
 // pairs, with the key mapped to an order-preserving uint64 (-0 -> +0, every NaN -> the largest code so NaN sorts
-// last and stays in text order, as torch.argsort(stable=True) does). Tiles of up to 1024 pairs are bitonic-sorted
-// in registers, lane exchanges and LDS (block_sort.h); longer rows are finished by merge passes in which every
-// element finds its output slot by a binary search in the other run.
-#include "block_sort.h"
+// last and stays in text order, as torch.argsort(stable=True) does). The pairs are unique, so any correct sort of
+// them is the stable sort.
+//
+//   k_ngram_rows   one workgroup per tile of up to 4096 positions of a (b, j) row: the keys of its positions, a sort
+//                  of the tile in LDS (4 pairs per thread sorted in registers, then merge levels of doubling runs in
+//                  which every thread finds its 4 output slots' split point by a merge-path search and merges them),
+//                  and, when the tile is the whole row, the outputs (order, repeated, rank, seen) from the sorted
+//                  pairs in LDS: one launch for rows of up to 4096 positions.
+//   k_merge_pass   longer rows: merge passes over the sorted tiles (every element finds its output slot by a binary
+//                  search in the partner run), ping-ponging in the workspace.
+//   k_ngram_finish longer rows: the outputs from the merged pairs.
+#include "common.h"
 
 namespace asrn {
 
-constexpr int kTile = 1024;          // pairs per sorted tile (more workgroups; merges finish longer rows)
+constexpr int kRowTile = 4096;                   // pairs sorted per workgroup
+constexpr int kRowThreads = kRowTile / 4;
 constexpr uint64_t kNanCode = ~0ull;
-constexpr uint32_t kPadIdx = 0xFFFFFFFFu;
 
 __device__ __forceinline__ uint64_t key_code(double x) {
   if (x != x) return kNanCode;
@@ -30,47 +38,141 @@ struct NgramDims {
   int n, tile;
 };
 
-// keys (B, L, n) and the (code, position) pairs of every (b, j) row, padded to Lp with sentinels
-__global__ void k_ngram_keys(const float* __restrict__ sig, const double* __restrict__ coef, NgramDims g,
-                             double* __restrict__ keys, uint64_t* __restrict__ code, uint32_t* __restrict__ idx) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = g.B * g.Lp;
-  if (e >= total) return;
-  const int64_t b = e / g.Lp, t = e % g.Lp;
-  if (t >= g.L) {
-    for (int j = 0; j < g.n; ++j) {
-      code[(b * g.n + j) * g.Lp + t] = kNanCode;
-      idx[(b * g.n + j) * g.Lp + t] = kPadIdx;
+// the n-gram key of length j + 1 ending at t: sum over i <= j of sig[t - i] * coef[i], each product and sum rounded
+// separately, in the reference's order (NaN before the text's start)
+__device__ __forceinline__ double ngram_key(const float* __restrict__ sigb, const double* __restrict__ coef,
+                                            int64_t t, int j) {
+  double key = 0.0;
+  for (int i = 0; i <= j; ++i) {
+    const float x = sigb[t - i >= 0 ? t - i : 0];              // unconditional load, masked after
+    const double s = (t - i >= 0) ? (double)x : __longlong_as_double(0x7ff8000000000000ll);
+    key = __dadd_rn(key, __dmul_rn(s, coef[i]));
+  }
+  return key;
+}
+
+template <class T>
+__device__ __forceinline__ void swap_if(bool c, T& a, T& b) {
+  const T x = c ? b : a, y = c ? a : b;
+  a = x;
+  b = y;
+}
+
+__device__ __forceinline__ void sort_pair(uint64_t (&k)[4], uint32_t (&p)[4], int a, int b) {
+  const bool c = pair_less(k[b], p[b], k[a], p[a]);
+  swap_if(c, k[a], k[b]);
+  swap_if(c, p[a], p[b]);
+}
+
+// Grid (Lp / tile, B * n), tile / 4 threads. whole: the tile is the row (Lp == tile), so the outputs are written
+// here; otherwise the sorted (code, position) pairs of the tile go to code_out / idx_out at row * Lp + tile start.
+__global__ __launch_bounds__(kRowThreads) void k_ngram_rows(const float* __restrict__ sig,
+                                                            const double* __restrict__ coef, NgramDims g, bool whole,
+                                                            double* __restrict__ keys, int32_t* __restrict__ order,
+                                                            uint8_t* __restrict__ repeated,
+                                                            int32_t* __restrict__ rank_k, float* __restrict__ vistos,
+                                                            uint64_t* __restrict__ code_out,
+                                                            uint32_t* __restrict__ idx_out) {
+  __shared__ uint64_t ck[2][kRowTile];
+  __shared__ uint16_t cp[2][kRowTile];             // position within the tile
+  const int tid = threadIdx.x, tile = g.tile;
+  const int64_t row = blockIdx.y, b = row / g.n;
+  const int j = (int)(row % g.n);
+  const int64_t t0 = (int64_t)blockIdx.x * tile;
+  const float* sigb = sig + b * g.L;
+
+  uint64_t k[4];
+  uint32_t p[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int e = 4 * tid + r;
+    const int64_t t = t0 + e;
+    p[r] = (uint32_t)e;
+    k[r] = kNanCode;                                // padding past the row: after every real pair
+    if (t < g.L) {
+      const double key = ngram_key(sigb, coef, t, j);
+      keys[(b * g.L + t) * g.n + j] = key;
+      k[r] = key_code(key);
+    }
+  }
+  sort_pair(k, p, 0, 1);
+  sort_pair(k, p, 2, 3);
+  sort_pair(k, p, 0, 2);
+  sort_pair(k, p, 1, 3);
+  sort_pair(k, p, 1, 2);
+
+  // merge levels: runs of w sorted pairs become runs of 2w. Run [s, s + w) holds exactly the tile positions
+  // [s, s + w), so a merge that takes A's pair on equal codes keeps text order: the search and the merge compare
+  // codes only. Thread tid owns output slots 4 tid .. 4 tid + 3 of its pair of runs A = [s, s + w), B = [s + w,
+  // s + 2w); the split (i, d - i) of diagonal d = 4 tid - s is the number of A's pairs among the first d of the merge.
+  int cur = 0;
+  for (int w = 4; w < tile; w <<= 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ck[cur][4 * tid + r] = k[r];
+      cp[cur][4 * tid + r] = (uint16_t)p[r];
+    }
+    __syncthreads();
+    const int s = (4 * tid) & ~(2 * w - 1), d = 4 * tid - s;
+    const uint64_t* ak = ck[cur] + s;
+    const uint16_t* ap = cp[cur] + s;
+    const uint64_t* bk = ak + w;
+    const uint16_t* bp = ap + w;
+    int lo = d > w ? d - w : 0, hi = d < w ? d : w;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (ak[mid] <= bk[d - 1 - mid]) lo = mid + 1; else hi = mid;
+    }
+    int ia = lo, ib = d - lo;
+    uint64_t ka = ia < w ? ak[ia] : 0, kb = ib < w ? bk[ib] : 0;
+    uint32_t pa = ia < w ? ap[ia] : 0, pb = ib < w ? bp[ib] : 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool take_a = ia < w && (ib >= w || ka <= kb);
+      k[r] = take_a ? ka : kb;
+      p[r] = take_a ? pa : pb;
+      if (take_a) {
+        ++ia;
+        ka = ia < w ? ak[ia] : 0;
+        pa = ia < w ? ap[ia] : 0;
+      } else {
+        ++ib;
+        kb = ib < w ? bk[ib] : 0;
+        pb = ib < w ? bp[ib] : 0;
+      }
+    }
+    cur ^= 1;
+  }
+
+  if (!whole) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t o = row * g.Lp + t0 + 4 * tid + r;
+      code_out[o] = k[r];
+      idx_out[o] = (uint32_t)(t0 + p[r]);
     }
     return;
   }
-  double key = 0.0;
-  for (int j = 0; j < g.n; ++j) {
-    const double s = (t - j >= 0) ? (double)sig[b * g.L + t - j] : __longlong_as_double(0x7ff8000000000000ll);
-    key = __dadd_rn(key, __dmul_rn(s, coef[j]));
-    keys[(b * g.L + t) * g.n + j] = key;
-    code[(b * g.n + j) * g.Lp + t] = key_code(key);
-    idx[(b * g.n + j) * g.Lp + t] = (uint32_t)t;
-  }
-}
-
-// each tile of `tile` (code, position) pairs sorted by one workgroup of tile / 4 threads (block_sort.h)
-__global__ __launch_bounds__(kTile / 4) void k_tile_sort(uint64_t* __restrict__ code, uint32_t* __restrict__ idx,
-                                                         int64_t Lp, int tile) {
-  __shared__ SortKI lds[kTile];
-  const int64_t base = (int64_t)blockIdx.y * Lp + (int64_t)blockIdx.x * tile;
-  SortKI x[4];
+  // outputs: order and repeated per sorted slot here; rank and seen per position through LDS (sorted slot | repeated
+  // << 15 by position), so that both are written in position order
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int64_t e = base + 4 * threadIdx.x + q;
-    x[q] = SortKI{code[e], idx[e]};
-  }
-  block_bitonic_sort(x, lds, tile);
+  for (int r = 0; r < 4; ++r) ck[cur][4 * tid + r] = k[r];
+  __syncthreads();
+  uint16_t* by_pos = cp[cur];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int64_t e = base + 4 * threadIdx.x + q;
-    code[e] = x[q].k;
-    idx[e] = x[q].i;
+  for (int r = 0; r < 4; ++r) {
+    const int i = 4 * tid + r;
+    if (i >= g.L) continue;                         // padding sorts last
+    const bool rep = i > 0 && k[r] != kNanCode && ck[cur][i - 1] == k[r];
+    order[row * g.L + i] = (int32_t)p[r];
+    repeated[row * g.L + i] = rep ? 1 : 0;
+    by_pos[p[r]] = (uint16_t)(i | (rep ? 0x8000 : 0));
+  }
+  __syncthreads();
+  for (int t = tid; t < g.L; t += blockDim.x) {
+    const uint32_t x = by_pos[t];
+    rank_k[row * g.L + t] = (int32_t)(x & 0x7FFFu);
+    vistos[(b * g.L + t) * g.n + j] = (x & 0x8000u) ? 1.f : 0.f;
   }
 }
 
@@ -122,10 +224,10 @@ __global__ void k_ngram_finish(const uint64_t* __restrict__ code, const uint32_t
   }
 }
 
+// tile: a power of two, 4 <= tile <= kRowTile; Lp: the row padded to a power-of-two number of tiles
 static void ngram_dims(int64_t B, int64_t L, int n, NgramDims* g) {
-  int tile = 2;
-  while (tile < L && tile < kTile) tile <<= 1;
-  if (tile < 4) tile = 4;
+  int tile = 4;
+  while (tile < L && tile < kRowTile) tile <<= 1;
   int64_t tiles = 1;
   while (tiles * tile < L) tiles <<= 1;
   g->B = B;
@@ -163,14 +265,13 @@ extern "C" int asrn_ngram_sort(const float* sig, const double* coef, int64_t B, 
   uint32_t* idx0 = (uint32_t*)(code1 + elems);
   uint32_t* idx1 = idx0 + elems;
   hipStream_t st = (hipStream_t)stream;
+  const bool whole = g.Lp == g.tile;
 
+  hipLaunchKernelGGL(k_ngram_rows, dim3((unsigned)(g.Lp / g.tile), (unsigned)rows), dim3(g.tile / 4), 0, st, sig,
+                     coef, g, whole, keys, order, repeated, rank_k, vistos, code0, idx0);
+  if (check_launch("asrn_ngram_sort/rows")) return 1;
+  if (whole) return 0;
   const int threads = 256;
-  hipLaunchKernelGGL(k_ngram_keys, dim3((unsigned)((B * g.Lp + threads - 1) / threads)), dim3(threads), 0, st, sig,
-                     coef, g, keys, code0, idx0);
-  if (check_launch("asrn_ngram_sort/keys")) return 1;
-  hipLaunchKernelGGL(k_tile_sort, dim3((unsigned)(g.Lp / g.tile), (unsigned)rows), dim3(g.tile / 4), 0, st, code0,
-                     idx0, g.Lp, g.tile);
-  if (check_launch("asrn_ngram_sort/tile")) return 1;
   uint64_t* kc = code0;
   uint32_t* ic = idx0;
   uint64_t* ko = code1;

@@ -89,7 +89,8 @@ def test_bucket_sort_golden(name):
 
 @pytest.mark.parametrize('B,L,T,nb,mode', [(8, 4096, 8, 14, 'randn'), (2, 5000, 8, 14, 'few'), (1, 1, 8, 14, 'randn'),
                                            (3, 1023, 5, 3, 'randn'), (1, 2049, 8, 14, 'same'),
-                                           (1, 65536, 8, 14, 'few')])
+                                           (1, 65536, 8, 14, 'few'), (1, 4097, 8, 14, 'randn'),
+                                           (4, 4096, 8, 14, 'few'), (5, 3, 3, 2, 'randn'), (3, 8200, 2, 1, 'randn')])
 def test_bucket_sort_vs_numpy(B, L, T, nb, mode):
     say('bucket_sort', B, L, T, nb, mode)
     g = torch.Generator().manual_seed(L)
@@ -172,7 +173,8 @@ def test_ngram_golden(name):
 
 
 @pytest.mark.parametrize('B,L,V,zipf', [(8, 4096, 256, None), (2, 10000, 6, None), (1, 1, 5, None), (3, 3, 5, None),
-                                        (1, 65536, 32000, 1.1), (2, 333, 50304, 1.1)])
+                                        (1, 65536, 32000, 1.1), (2, 333, 50304, 1.1), (1, 4097, 3, None),
+                                        (3, 4095, 2, None), (2, 12289, 40, 1.1)])
 def test_ngram_vs_oracle(B, L, V, zipf):
     say('ngram', B, L, V, zipf)
     x = synth.tokens(B, L, V, frac=0.3, span=(2, 8), zipf=zipf, seed=L)
