@@ -59,6 +59,18 @@ struct GlobalIds {
   __device__ __forceinline__ int operator[](int64_t i) const { return p[i]; }
 };
 
+// the lanes whose 7-bit digit equals this lane's (every lane of the wavefront calls it)
+__device__ __forceinline__ uint64_t match7(int d) {
+  uint64_t m = __ballot(1);
+#pragma unroll
+  for (int j = 0; j < kRadixBits; ++j) {
+    const bool bit = (d >> j) & 1;
+    const uint64_t bj = __ballot(bit);
+    m &= bit ? bj : ~bj;
+  }
+  return m;
+}
+
 // LDS reads and writes of one wavefront take effect in program order; the fence keeps the compiler from moving them
 __device__ __forceinline__ void wave_lds_order() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
@@ -188,7 +200,7 @@ __global__ __launch_bounds__(kThreads) void k_bucket_rows(const float* __restric
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int d = (int)((k[q] >> shift) & ((1u << bits) - 1u));
-      const uint64_t peers = match_key(d, bits, true);
+      const uint64_t peers = match7(d);
       const int base = hist[d * kWaves + wave];                    // this digit in the wave's earlier rounds
       rk[q] = base + __popcll(peers & ((1ull << lane) - 1ull));
       dg[q] = d;

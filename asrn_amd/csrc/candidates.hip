@@ -264,7 +264,9 @@ __device__ __forceinline__ int gather(const Cand& a, int64_t b, int64_t t, bool 
       // inconsistent inputs cannot read out of bounds)
       int64_t j = query_window ? (int64_t)S.wrank[lo] - S.wlen[lo] + i : (int64_t)S.wrank[lo] + 1 + i;
       j = j < 0 ? 0 : (j >= a.L ? a.L - 1 : j);
-      S.key[m] = (a.order[(b * a.T + lo) * a.L + j] << 5) | lo;
+      int pos = a.order[(b * a.T + lo) * a.L + j];
+      pos = pos < 0 ? 0 : (pos >= a.L ? (int)a.L - 1 : pos);          // a position whatever the sort left
+      S.key[m] = (pos << 5) | lo;
     }
   }
   wave_lds_sync();

@@ -55,9 +55,9 @@ def bucket_sort(phi, T, nb, C):
     phi = _c(phi, torch.float32)
     B, L, P = phi.shape
     ids = torch.empty((B * T, L), dtype=I32, device=dev)
-    # order, ids_sorted, rank and win share one zero-filled buffer (one fill): every index a later kernel reads is
-    # in range even if a sort were wrong; a correct sort overwrites all of it
-    buf = torch.zeros((4, B * T * L), dtype=I32, device=dev)
+    # every entry of order, ids_sorted, rank and win is written by the sort (no fill); the candidate kernels clamp
+    # the positions they read from order
+    buf = torch.empty((4, B * T * L), dtype=I32, device=dev)
     order, ids_s = buf[0].view(B * T, L), buf[1].view(B * T, L)
     rank, win = buf[2].view(B, L, T), buf[3].view(B, L, T)
     call('asrn_bucket_sort', ptr(phi), B, L, T, nb, P, C, ptr(ids), ptr(order), ptr(ids_s), ptr(rank), ptr(win),
