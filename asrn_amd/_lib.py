@@ -21,12 +21,12 @@ SIGNATURES = {
     'asrn_hip_last_error': (ctypes.c_char_p, []),
     'asrn_hip_abi_version': (_I32, []),
     'asrn_bucket_sort': (ctypes.c_int, [_P, _I64, _I64, _I32, _I32, _I64, _I32, _P, _P, _P, _P, _P, _P]),
-    'asrn_candidates_fwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7 + [_F32, _F32, _I64, _I32, _I64]
-                            + [_P] * 5),
+    'asrn_candidates_fwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7
+                            + [_F32, _F32, _I64, _I32, _I64, _I32] + [_P] * 5),
     'asrn_candidates_record_bytes': (_I64, [_I32, _I32]),
     'asrn_candidate_lists': (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P]),
-    'asrn_candidates_bwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7 + [_F32, _F32, _I64, _I32, _I64]
-                            + [_P] * 11),
+    'asrn_candidates_bwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7
+                            + [_F32, _F32, _I64, _I32, _I64, _I32] + [_P] * 11),
     'asrn_scan_workspace': (_I64, [_I64, _I64]),
     'asrn_clock_scan': (ctypes.c_int, [_P, _P, _I64, _I64, _I32, _P, _I64, _P]),
     'asrn_ngram_sort_workspace': (_I64, [_I64, _I64, _I32]),

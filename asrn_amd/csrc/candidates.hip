@@ -117,6 +117,23 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+// value-side rows (V, dO) stored as fp32 or as bf16 (B16): `base` points at element 0 of a row block, offsets count
+// elements; a bf16 row's 4 elements load as 8 bytes and widen exactly (bf16 -> fp32 shifts the bits)
+template <bool B16>
+__device__ __forceinline__ const float* rows_at(const float* base, int64_t elems) {
+  if constexpr (B16) return reinterpret_cast<const float*>(reinterpret_cast<const uint16_t*>(base) + elems);
+  else return base + elems;
+}
+template <bool B16>
+__device__ __forceinline__ float4 ld4r(const float* base, uint32_t off) {
+  if constexpr (B16) {
+    const uint2 u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(base) + off);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xffff0000u));
+  } else {
+    return ld4(base + off);
+  }
+}
 __device__ __forceinline__ float dot4(const float4& x, const float4& y) {
   return x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
 }
@@ -454,7 +471,7 @@ __device__ __forceinline__ void unique_feature_sum(const Cand& a, int64_t b, int
 
 // <fixed, row_u> over the d columns for every unique (rows of batch row `rows`), R rows in flight, written to
 // out[u]; the key side (w_u != nullptr) also accumulates dV += w_u row_u from the same loads.
-template <int DCH>
+template <int DCH, bool B16 = false>
 __device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows, int64_t ld, int64_t self_pos,
                                                 int NU, const float4 (&fixed)[DCH], const float* w_u,
                                                 float4 (&dv)[DCH], Scratch& S, float* out) {
@@ -472,7 +489,7 @@ __device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows
 #pragma unroll
       for (int ch = 0; ch < DCH; ++ch) {
         const int dd = ch * 256 + lane * 4;
-        o[r][ch] = ld4(rows + ((uint32_t)row * (uint32_t)ld + (uint32_t)(dd < a.d ? dd : a.d - 4)));
+        o[r][ch] = ld4r<B16>(rows, (uint32_t)row * (uint32_t)ld + (uint32_t)(dd < a.d ? dd : a.d - 4));
       }
     }
 #pragma unroll
@@ -582,12 +599,12 @@ constexpr int gather_rows_in_flight() { return DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 12
 
 // The copy-gather's rows: acc += sum over uniques u of (sum over tables of att) V_u, for u in chunks of UNR
 // consecutive uniques starting at `first`, one chunk every `step` (UNR rows in flight per chunk).
-template <int DCH>
+template <int DCH, bool B16 = false>
 __device__ __forceinline__ void gather_values(const Cand& a, int64_t b, const Scratch& S, int NU, int first, int step,
                                               float4 (&acc)[DCH]) {
   constexpr int UNR = gather_rows_in_flight<DCH>();
   const int lane = lane_id();
-  const float* Vb = a.V + (b * a.L + a.vshift) * a.ldv;
+  const float* Vb = rows_at<B16>(a.V, (b * a.L + a.vshift) * a.ldv);
   for (int u0 = first; u0 < NU; u0 += step) {
     float4 v[UNR][DCH];
     float w[UNR];
@@ -599,7 +616,7 @@ __device__ __forceinline__ void gather_values(const Cand& a, int64_t b, const Sc
 #pragma unroll
       for (int ch = 0; ch < DCH; ++ch) {
         const int dd = ch * 256 + lane * 4;
-        v[r][ch] = ld4(Vb + ((uint32_t)p * (uint32_t)a.ldv + (uint32_t)(dd < a.d ? dd : a.d - 4)));
+        v[r][ch] = ld4r<B16>(Vb, (uint32_t)p * (uint32_t)a.ldv + (uint32_t)(dd < a.d ? dd : a.d - 4));
       }
     }
 #pragma unroll
@@ -666,14 +683,14 @@ __device__ __forceinline__ void unique_terms(const Cand& a, int64_t b, int64_t t
   wave_lds_sync();
 }
 
-template <int DCH, bool VALUES>
+template <int DCH, bool VALUES, bool B16 = false>
 __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, int NU, Scratch& S, float* salida_row,
                                               float* signals_row, float* ent_rows);
 
 // One query token's candidate attention: salida row (d), the 4 gate signals and, when `ent_rows` is given, every
 // entry's weight at ent_rows[2 (tau * C + distance - 1)]. RING: candidates from the generation rings instead of the
 // sorted windows.
-template <int F4, int DCH, bool RING>
+template <int F4, int DCH, bool RING, bool B16 = false>
 __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t t, Scratch& S, float* salida_row,
                                               float* signals_row, float* ent_rows) {
   const int64_t tok = b * a.L + t;
@@ -681,13 +698,13 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
   int NU;
   const int M = token_list<RING>(a, b, t, S, rec, &NU);
   unique_terms<F4, 1>(a, b, t, NU, S, rec, 0);
-  token_weights<DCH, true>(a, b, M, NU, S, salida_row, signals_row, ent_rows);
+  token_weights<DCH, true, B16>(a, b, M, NU, S, salida_row, signals_row, ent_rows);
 }
 
 // The rest of a query's attention once its list and unique terms are in S: the exact masked softmax, the entries'
 // weights (into ent_rows when given), the 4 gate signals and, with VALUES, the copy-gather into salida_row (without
 // it, S.uc holds each unique's summed weight for the caller).
-template <int DCH, bool VALUES>
+template <int DCH, bool VALUES, bool B16>
 __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, int NU, Scratch& S, float* salida_row,
                                               float* signals_row, float* ent_rows) {
   const int lane = lane_id();
@@ -760,7 +777,7 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
     float4 acc[DCH];
 #pragma unroll
     for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
-    gather_values<DCH>(a, b, S, NU, 0, gather_rows_in_flight<DCH>(), acc);
+    gather_values<DCH, B16>(a, b, S, NU, 0, gather_rows_in_flight<DCH>(), acc);
 #pragma unroll
     for (int ch = 0; ch < DCH; ++ch) {
       const int dd = ch * 256 + lane * 4;
@@ -769,13 +786,13 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
   }
 }
 
-template <int F4, int DCH>
+template <int F4, int DCH, bool B16>
 __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 6 : 1) void k_cand_fwd(Cand a) {   // 6 waves per SIMD when narrow
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
   const int64_t tok = token_of_wave();
   if (tok >= a.B * a.L) return;
-  forward_token<F4, DCH, false>(a, tok / a.L, tok % a.L, S, a.salida + tok * a.d, a.signals + tok * 4,
+  forward_token<F4, DCH, false, B16>(a, tok / a.L, tok % a.L, S, a.salida + tok * a.d, a.signals + tok * 4,
                                 a.ent + tok * a.T * a.C * 2);
 }
 
@@ -844,7 +861,7 @@ __global__ __launch_bounds__(kWave * kDecodeWaves) void k_decode_attend(Cand a) 
 // backward, query pass: needs no scores. att comes from the forward; per distinct key, dp = <dO_q, V_k>, the clock
 // difference and the suffix length; per table D = sum att dp, then ds = att (dp - D) per entry, kept for the key pass.
 // ---------------------------------------------------------------------------------------------------------------------
-template <int F4, int DCH>
+template <int F4, int DCH, bool B16>
 __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
@@ -888,10 +905,11 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
 #pragma unroll
   for (int ch = 0; ch < DCH; ++ch) {
     const int dd = ch * 256 + lane * 4;
-    dO[ch] = dd < a.d ? ld4(a.dsal + tok * a.d + dd) : zero4();
+    dO[ch] = dd < a.d ? ld4r<B16>(rows_at<B16>(a.dsal, tok * a.d), (uint32_t)dd) : zero4();
     unused[ch] = zero4();
   }
-  unique_row_dots<DCH>(a, a.V + (b * a.L + a.vshift) * a.ldv, a.ldv, 0, NU, dO, nullptr, unused, S, S.uc);
+  unique_row_dots<DCH, B16>(a, rows_at<B16>(a.V, (b * a.L + a.vshift) * a.ldv), a.ldv, 0, NU, dO, nullptr, unused, S,
+                            S.uc);
 
   // per entry: att * dp (S.ua is a per-entry buffer here)
 #pragma unroll
@@ -972,7 +990,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
 }
 
 // sum_u w_u row_u over the uniques' d-wide rows (rows of batch row b), UNR rows in flight
-template <int DCH>
+template <int DCH, bool B16 = false>
 __device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows, int64_t self_pos, int NU,
                                                const float* w_u, const Scratch& S, float4 (&acc)[DCH]) {
   const int lane = lane_id();
@@ -990,7 +1008,7 @@ __device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows,
 #pragma unroll
       for (int ch = 0; ch < DCH; ++ch) {
         const int dd = ch * 256 + lane * 4;
-        v[r][ch] = ld4(rows + ((uint32_t)p * (uint32_t)a.d + (uint32_t)(dd < a.d ? dd : a.d - 4)));
+        v[r][ch] = ld4r<B16>(rows, (uint32_t)p * (uint32_t)a.d + (uint32_t)(dd < a.d ? dd : a.d - 4));
       }
     }
 #pragma unroll
@@ -1004,7 +1022,7 @@ __device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows,
 // backward, key pass: no scores either. Every entry's att (forward) and ds (query pass) are read at the query's
 // slot for this key; per distinct query the table sums weight dO (-> dV) and [phi_q ; Qc_q] (-> d phi_k, d Kc_k).
 // ---------------------------------------------------------------------------------------------------------------------
-template <int F4, int DCH>
+template <int F4, int DCH, bool B16>
 __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 6 : ((F4 == 1 && DCH != 3) ? 5 : 1))
 void k_cand_bwd_k(Cand a) {
   __shared__ Scratch scratch[kWavesPerBlock];
@@ -1068,7 +1086,7 @@ void k_cand_bwd_k(Cand a) {
 
   // dV_k = sum_u (sum_tau att) dO_u
   float4 dv[DCH];
-  unique_row_sum<DCH>(a, a.dsal + b * a.L * a.d, k, NU, S.uc, S, dv);
+  unique_row_sum<DCH, B16>(a, rows_at<B16>(a.dsal, b * a.L * a.d), k, NU, S.uc, S, dv);
   // d phi_k, d Kc_k = sum_u (sum_tau ds) [phi_q * scale_phi ; Qc_q * scale_c]
   float4 gk[F4];
   unique_feature_sum<F4>(a, b, k, NU, true, S.ub, S, gk);
@@ -1165,49 +1183,55 @@ static Cand make(const float* phi, const float* V, const float* Qc, const float*
 }
 
 // launch a kernel template for the (float4 feature chunks per lane, d chunks) bucket of the arguments
-template <template <int, int> class Launcher>
-static int dispatch(const Cand& a, hipStream_t st) {
+template <template <int, int, bool> class Launcher, bool B16>
+static int dispatch_rows(const Cand& a, hipStream_t st) {
   const int dch = (a.d + 255) / 256;
   if (a.P + a.cf <= 128) {
     switch (dch) {
-      case 1: return Launcher<1, 1>::run(a, st);
-      case 2: return Launcher<1, 2>::run(a, st);
-      case 3: return Launcher<1, 3>::run(a, st);
-      default: return Launcher<1, 4>::run(a, st);
+      case 1: return Launcher<1, 1, B16>::run(a, st);
+      case 2: return Launcher<1, 2, B16>::run(a, st);
+      case 3: return Launcher<1, 3, B16>::run(a, st);
+      default: return Launcher<1, 4, B16>::run(a, st);
     }
   }
   switch (dch) {
-    case 1: return Launcher<2, 1>::run(a, st);
-    case 2: return Launcher<2, 2>::run(a, st);
-    case 3: return Launcher<2, 3>::run(a, st);
-    default: return Launcher<2, 4>::run(a, st);
+    case 1: return Launcher<2, 1, B16>::run(a, st);
+    case 2: return Launcher<2, 2, B16>::run(a, st);
+    case 3: return Launcher<2, 3, B16>::run(a, st);
+    default: return Launcher<2, 4, B16>::run(a, st);
   }
+}
+// rows_bf16: V (and the backward's dO) stored as bf16
+template <template <int, int, bool> class Launcher>
+static int dispatch(const Cand& a, hipStream_t st, bool rows_bf16 = false) {
+  return rows_bf16 ? dispatch_rows<Launcher, true>(a, st) : dispatch_rows<Launcher, false>(a, st);
 }
 
 static dim3 grid_of(const Cand& a) { return dim3((unsigned)((a.B * a.L + kWavesPerBlock - 1) / kWavesPerBlock)); }
 
-template <int F4, int DCH>
+template <int F4, int DCH, bool B16>
 struct LaunchFwd {
   static int run(const Cand& a, hipStream_t st) {
-    hipLaunchKernelGGL((k_cand_fwd<F4, DCH>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
+    hipLaunchKernelGGL((k_cand_fwd<F4, DCH, B16>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
     return check_launch("asrn_candidates_fwd");
   }
 };
 
-template <int F4, int DCH>
-struct LaunchDecode {
+template <int F4, int DCH, bool B16>
+struct LaunchDecode {                              // the generation caches are fp32 (B16 is never dispatched)
   static int run(const Cand& a, hipStream_t st) {
+    if constexpr (B16) return fail("asrn_decode_attend: fp32 caches only");
     hipLaunchKernelGGL((k_decode_attend<F4, DCH>), dim3((unsigned)a.B), dim3(kWave * kDecodeWaves), 0, st, a);
     return check_launch("asrn_decode_attend");
   }
 };
 
-template <int F4, int DCH>
+template <int F4, int DCH, bool B16>
 struct LaunchBwd {
   static int run(const Cand& a, hipStream_t st) {
-    hipLaunchKernelGGL((k_cand_bwd_q<F4, DCH>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
+    hipLaunchKernelGGL((k_cand_bwd_q<F4, DCH, B16>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
     if (check_launch("asrn_candidates_bwd/query")) return 1;
-    hipLaunchKernelGGL((k_cand_bwd_k<F4, DCH>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
+    hipLaunchKernelGGL((k_cand_bwd_k<F4, DCH, B16>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
     return check_launch("asrn_candidates_bwd/key");
   }
 };
@@ -1221,8 +1245,8 @@ extern "C" int asrn_candidates_fwd(const float* phi, const float* V, const float
                                    const float* gamma, const int32_t* order, const int32_t* win, const int32_t* rank,
                                    int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
                                    int32_t Tc, int32_t C, float scale_phi, float scale_c, int64_t ldv,
-                                   int32_t v_shift, int64_t ldq, float* salida, float* signals, float* entries,
-                                   uint8_t* lists, void* stream) {
+                                   int32_t v_shift, int64_t ldq, int32_t rows_bf16, float* salida, float* signals,
+                                   float* entries, uint8_t* lists, void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
                 scale_phi, scale_c);
   a.ldv = ldv;
@@ -1233,7 +1257,8 @@ extern "C" int asrn_candidates_fwd(const float* phi, const float* V, const float
   a.salida = salida; a.signals = signals; a.ent = entries;
   a.lists = lists; a.rec = rec_layout(T, C).size;
   ASRN_REQUIRE(((uintptr_t)lists & 15) == 0, "asrn_candidates_fwd: lists must be 16-byte aligned");
-  return dispatch<LaunchFwd>(a, (hipStream_t)stream);
+  ASRN_REQUIRE(rows_bf16 == 0 || rows_bf16 == 1, "asrn_candidates_fwd: rows_bf16 must be 0 or 1");
+  return dispatch<LaunchFwd>(a, (hipStream_t)stream, rows_bf16 != 0);
 }
 
 extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const float* Kc,
@@ -1241,8 +1266,8 @@ extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float
                                    const float* gamma, const int32_t* order, const int32_t* win, const int32_t* rank,
                                    int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
                                    int32_t Tc, int32_t C, float scale_phi, float scale_c, int64_t ldv,
-                                   int32_t v_shift, int64_t ldq, const float* dsalida, float* entries,
-                                   const uint8_t* lists, float* dphi,
+                                   int32_t v_shift, int64_t ldq, int32_t rows_bf16, const float* dsalida,
+                                   float* entries, const uint8_t* lists, float* dphi,
                                    float* dV, float* dQc, float* dKc, double* dBt, float* dlog_alfa, float* partials,
                                    void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
@@ -1258,7 +1283,9 @@ extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float
   ASRN_REQUIRE(((uintptr_t)lists & 15) == 0, "asrn_candidates_bwd: lists must be 16-byte aligned");
   a.dsal = dsalida; a.ent = entries; a.dphi = dphi; a.dV = dV; a.dQc = dQc; a.dKc = dKc; a.dBt = dBt;
   a.dla = dlog_alfa; a.partials = partials;
-  return dispatch<LaunchBwd>(a, (hipStream_t)stream);
+  ASRN_REQUIRE(rows_bf16 == 0 || rows_bf16 == 1, "asrn_candidates_bwd: rows_bf16 must be 0 or 1");
+  ASRN_REQUIRE(((uintptr_t)dsalida & 15) == 0, "asrn_candidates_bwd: dsalida must be 16-byte aligned");
+  return dispatch<LaunchBwd>(a, (hipStream_t)stream, rows_bf16 != 0);
 }
 
 extern "C" int64_t asrn_candidates_record_bytes(int32_t T, int32_t C) {

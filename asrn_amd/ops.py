@@ -30,10 +30,10 @@ def _c(t, dtype=None):
     return t.contiguous()
 
 
-def _rows_in_place(V):
-    """True when V (B, L, d) fp32 can be read in place: unit column stride, rows evenly strided across the batch (a
-    column block of a (B, L, n) tensor), a row stride that keeps float4 loads aligned."""
-    return (V.dtype == torch.float32 and V.dim() == 3 and V.stride(2) == 1 and V.stride(1) % 4 == 0
+def _rows_in_place(V, dtype=torch.float32):
+    """True when V (B, L, d) of `dtype` can be read in place: unit column stride, rows evenly strided across the batch
+    (a column block of a (B, L, n) tensor), a row stride that keeps the 4-element row loads aligned."""
+    return (V.dtype == dtype and V.dim() == 3 and V.stride(2) == 1 and V.stride(1) % 4 == 0
             and V.stride(1) >= V.shape[2] and V.stride(0) == V.shape[1] * V.stride(1) and V.data_ptr() % 16 == 0)
 
 
@@ -544,7 +544,12 @@ class Candidates(torch.autograd.Function):
         # the kernels read feature rows as float4: zero columns pad P and cf to multiples of 4 (dot products and the
         # gradients of the real columns are unchanged)
         vs = int(shape.get('v_shift', 0))
-        Vk = V if _rows_in_place(V) else _c(V, torch.float32)
+        # bf16 value rows (autocast) are read as they are: the kernels widen each element exactly
+        rows16 = V.dtype == torch.bfloat16 and d % 4 == 0
+        if rows16:
+            Vk = V if _rows_in_place(V, torch.bfloat16) else _c(V)
+        else:
+            Vk = V if _rows_in_place(V) else _c(V, torch.float32)
         if _rows_in_place(Qc) and _rows_in_place(Kc) and Qc.stride(1) == Kc.stride(1) and Qc.shape[-1] % 4 == 0:
             Qk, Kk = Qc, Kc                        # column blocks of one projection, read through their row stride
         else:
@@ -561,8 +566,8 @@ class Candidates(torch.autograd.Function):
                   if shape.get('listas', True) else None)
         call('asrn_candidates_fwd', ptr(ins['phi']), ptr(ins['V']), ptr(ins['Qc']), ptr(ins['Kc']), ptr(ins['sig']),
              ptr(ins['Bt']), ptr(ins['la']), ptr(ins['w']), ptr(ins['g']), ptr(order), ptr(win), ptr(rank), B, L, d,
-             P, cf, K, T, Tc, C, sp, sc, Vk.stride(1), vs, Qk.stride(1), ptr(salida), ptr(signals), ptr(ent),
-             ptr(listas), stream_of(dev))
+             P, cf, K, T, Tc, C, sp, sc, Vk.stride(1), vs, Qk.stride(1), int(rows16), ptr(salida), ptr(signals),
+             ptr(ent), ptr(listas), stream_of(dev))
         ctx.save_for_backward(*ins.values(), order, win, rank, ent, listas)
         ctx.meta = (B, L, P, d, cf, K, T, Tc, C, sp, sc, V.dtype, phi.dtype, Qc.dtype, Kc.dtype, log_alfa.dtype,
                     P0, cf0, vs)
@@ -577,7 +582,10 @@ class Candidates(torch.autograd.Function):
         phi, V, Qc, Kc, sig, Bt, la, w, g, order, win, rank, ent, listas = ctx.saved_tensors
         B, L, P, d, cf, K, T, Tc, C, sp, sc, tv, tp, tq, tk, tl, P0, cf0, vs = ctx.meta
         dev = phi.device
-        dsal = _c(dsal, torch.float32)
+        rows16 = V.dtype == torch.bfloat16 and dsal.dtype == torch.bfloat16
+        if V.dtype == torch.bfloat16 and not rows16:                  # an fp32 gradient: the fp32 path throughout
+            V = V.float()
+        dsal = _c(dsal) if rows16 else _c(dsal, torch.float32)
         dphi = torch.empty_like(phi)
         # dV takes V's layout: when V is a column block read in place, the same block of a (B, L, ldv) buffer, so the
         # producer whose output V is can take the buffer as its own output gradient without a copy
@@ -599,7 +607,7 @@ class Candidates(torch.autograd.Function):
         dla = torch.empty_like(la)
         partials = torch.empty((B * L, T + K + 1), dtype=torch.float32, device=dev)
         call('asrn_candidates_bwd', ptr(phi), ptr(V), ptr(Qc), ptr(Kc), ptr(sig), ptr(Bt), ptr(la), ptr(w), ptr(g),
-             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ldv, vs, Qc.stride(1),
+             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ldv, vs, Qc.stride(1), int(rows16),
              ptr(dsal), ptr(ent), ptr(listas),
              ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(partials), stream_of(dev))
         part = column_sums(partials)          # per-query partials summed over the tokens (no memset-cleared reduction)

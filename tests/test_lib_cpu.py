@@ -59,19 +59,19 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert lib.asrn_bucket_sort(N, 0, 16, 8, 14, 112, 32, N, N, N, N, N, N) == 0
     args = [N] * 12 + [2, 16]
     # d not a multiple of 4
-    assert lib.asrn_candidates_fwd(*args, 6, 112, 16, 4, 8, 4, 32, 0.1, 0.25, 6, 0, 16, N, N, N, N, N) != 0
+    assert lib.asrn_candidates_fwd(*args, 6, 112, 16, 4, 8, 4, 32, 0.1, 0.25, 6, 0, 16, 0, N, N, N, N, N) != 0
     assert 'd=6' in _err(lib)
     # chunk above 64
-    assert lib.asrn_candidates_fwd(*args, 64, 112, 16, 4, 8, 4, 65, 0.1, 0.25, 64, 0, 16, N, N, N, N, N) != 0
+    assert lib.asrn_candidates_fwd(*args, 64, 112, 16, 4, 8, 4, 65, 0.1, 0.25, 64, 0, 16, 0, N, N, N, N, N) != 0
     assert 'chunk' in _err(lib)
     # feature width above 256
-    assert lib.asrn_candidates_bwd(*args, 64, 250, 16, 4, 8, 4, 32, 0.1, 0.25, 64, 0, 16, *([N] * 11)) != 0
+    assert lib.asrn_candidates_bwd(*args, 64, 250, 16, 4, 8, 4, 32, 0.1, 0.25, 64, 0, 16, 0, *([N] * 11)) != 0
     assert 'P + cf' in _err(lib)
     # feature widths are read as float4 (the host pads them)
-    assert lib.asrn_candidates_fwd(*args, 64, 110, 16, 4, 8, 4, 32, 0.1, 0.25, 64, 0, 16, N, N, N, N, N) != 0
+    assert lib.asrn_candidates_fwd(*args, 64, 110, 16, 4, 8, 4, 32, 0.1, 0.25, 64, 0, 16, 0, N, N, N, N, N) != 0
     assert 'multiples of 4' in _err(lib)
     # V row stride below d
-    assert lib.asrn_candidates_fwd(*args, 64, 112, 16, 4, 8, 4, 32, 0.1, 0.25, 60, 1, 16, N, N, N, N, N) != 0
+    assert lib.asrn_candidates_fwd(*args, 64, 112, 16, 4, 8, 4, 32, 0.1, 0.25, 60, 1, 16, 0, N, N, N, N, N) != 0
     assert 'ldv' in _err(lib)
     # the candidate-list records: 16-byte multiples, sized for T * C entries and uniques
     assert lib.asrn_candidates_record_bytes(8, 32) % 16 == 0 and lib.asrn_candidates_record_bytes(8, 32) >= 11 * 256
