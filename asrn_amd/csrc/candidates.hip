@@ -117,8 +117,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
-// value-side rows (V, dO) stored as fp32 or as bf16 (B16): `base` points at element 0 of a row block, offsets count
-// elements; a bf16 row's 4 elements load as 8 bytes and widen exactly (bf16 -> fp32 shifts the bits)
+// rows stored as fp32 or as bf16 (B16; the value rows V and dO, and the feature rows phi, Qc, Kc): `base` points at
+// element 0 of a row block, offsets count elements; a bf16 row's 4 elements load as 8 bytes and widen exactly (bf16 ->
+// fp32 shifts the bits), so the results equal those from fp32 copies
 template <bool B16>
 __device__ __forceinline__ const float* rows_at(const float* base, int64_t elems) {
   if constexpr (B16) return reinterpret_cast<const float*>(reinterpret_cast<const uint16_t*>(base) + elems);
@@ -153,7 +154,7 @@ struct FeatLanes {
   float scale[F4];
 };
 
-template <int F4>
+template <int F4, bool FB16 = false>
 __device__ __forceinline__ FeatLanes<F4> feat_lanes(const Cand& a, const float* conf, bool scaled) {
   FeatLanes<F4> fl;
   const int x0 = 4 * (lane_id() & 31);
@@ -161,18 +162,18 @@ __device__ __forceinline__ FeatLanes<F4> feat_lanes(const Cand& a, const float* 
   for (int c = 0; c < F4; ++c) {
     const int x = x0 + 128 * c;
     const bool in_phi = x < a.P, live = x < a.P + a.cf;
-    fl.base[c] = in_phi ? a.phi + x : (live ? conf + (x - a.P) : a.phi);
+    fl.base[c] = in_phi ? rows_at<FB16>(a.phi, x) : (live ? rows_at<FB16>(conf, x - a.P) : a.phi);
     fl.stride[c] = in_phi || !live ? (uint32_t)a.P : (uint32_t)a.ldq;
     fl.scale[c] = !live ? 0.f : (scaled ? (in_phi ? a.sp : a.sc) : 1.f);
   }
   return fl;
 }
 
-template <int F4>
+template <int F4, bool FB16 = false>
 __device__ __forceinline__ void feat_row(const FeatLanes<F4>& fl, uint32_t row, float4 (&f)[F4]) {
 #pragma unroll
   for (int c = 0; c < F4; ++c) {
-    float4 v = ld4(fl.base[c] + row * fl.stride[c]);
+    float4 v = ld4r<FB16>(fl.base[c], row * fl.stride[c]);
     v.x *= fl.scale[c]; v.y *= fl.scale[c]; v.z *= fl.scale[c]; v.w *= fl.scale[c];
     f[c] = v;
   }
@@ -404,19 +405,19 @@ __device__ __forceinline__ int dedupe(const Cand& a, int M, Scratch& S) {
 // base scores <query, key> of every unique, 2*kRows rows in flight (kRows per half-wave). query side: fixed = the
 // query's scaled features and the rows are keys; key side: fixed = the key's raw features, rows = queries (scaled).
 // The product is always query * key and the reduction tree is the same, so both sides produce the same bits.
-template <int F4>
+template <int F4, bool FB16 = false>
 __device__ __forceinline__ void unique_bases(const Cand& a, int64_t b, int64_t self_pos, int NU,
                                              bool rows_are_queries, const float4 (&fixed)[F4], Scratch& S,
                                              int first = 0, int step = 2 * kRows) {
   const int lane = lane_id(), half = lane >> 5;
-  const FeatLanes<F4> fl = feat_lanes<F4>(a, rows_are_queries ? a.Qc : a.Kc, rows_are_queries);
+  const FeatLanes<F4> fl = feat_lanes<F4, FB16>(a, rows_are_queries ? a.Qc : a.Kc, rows_are_queries);
   const uint32_t row0 = (uint32_t)(b * a.L);
   for (int u0 = first; u0 < NU; u0 += step) {   // chunks of 2 kRows uniques
     float4 f[kRows][F4];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
       const int u = u0 + 2 * r + half;
-      feat_row<F4>(fl, row0 + (uint32_t)(u < NU ? S.upos[u] : self_pos), f[r]);
+      feat_row<F4, FB16>(fl, row0 + (uint32_t)(u < NU ? S.upos[u] : self_pos), f[r]);
     }
     float p[kRows];
 #pragma unroll
@@ -436,12 +437,12 @@ __device__ __forceinline__ void unique_bases(const Cand& a, int64_t b, int64_t s
 }
 
 // sum_u w_u * row_u over the uniques' features (kRows rows per half-wave in flight), both halves combined.
-template <int F4>
+template <int F4, bool FB16 = false>
 __device__ __forceinline__ void unique_feature_sum(const Cand& a, int64_t b, int64_t self_pos, int NU,
                                                    bool rows_are_queries, const float* wts, Scratch& S,
                                                    float4 (&g)[F4]) {
   const int half = lane_id() >> 5;
-  const FeatLanes<F4> fl = feat_lanes<F4>(a, rows_are_queries ? a.Qc : a.Kc, rows_are_queries);
+  const FeatLanes<F4> fl = feat_lanes<F4, FB16>(a, rows_are_queries ? a.Qc : a.Kc, rows_are_queries);
   const uint32_t row0 = (uint32_t)(b * a.L);
 #pragma unroll
   for (int c = 0; c < F4; ++c) g[c] = zero4();
@@ -452,7 +453,7 @@ __device__ __forceinline__ void unique_feature_sum(const Cand& a, int64_t b, int
     for (int r = 0; r < kRows; ++r) {
       const int u = u0 + 2 * r + half;
       const bool ok = u < NU;
-      feat_row<F4>(fl, row0 + (uint32_t)(ok ? S.upos[u] : self_pos), f[r]);
+      feat_row<F4, FB16>(fl, row0 + (uint32_t)(ok ? S.upos[u] : self_pos), f[r]);
       w[r] = ok ? wts[u] : 0.f;
     }
 #pragma unroll
@@ -648,15 +649,15 @@ __device__ __forceinline__ int token_list(const Cand& a, int64_t b, int64_t t, S
 // The uniques' score terms: S.ua = base + w_suf[ell] + log_alfa_k, S.ub = fp32(Bt_k - Bt_q), S.uc = 0 (and the
 // record's per-unique fields). NW = 1: the whole wave does every unique. NW > 1: wave `wave` of NW does the chunks of
 // 2 kRows uniques wave, wave + NW, ... (its bases and then their other terms, so no other wave's results are read).
-template <int F4, int NW>
+template <int F4, int NW, bool FB16 = false>
 __device__ __forceinline__ void unique_terms(const Cand& a, int64_t b, int64_t t, int NU, Scratch& S, uint8_t* rec,
                                              int wave) {
   const int lane = lane_id();
   const int64_t tok = b * a.L + t;
   const RecLayout R = rec_layout(a.T, a.C);
   float4 qf[F4];
-  feat_row<F4>(feat_lanes<F4>(a, a.Qc, true), (uint32_t)tok, qf);
-  unique_bases<F4>(a, b, t, NU, false, qf, S, wave * 2 * kRows, NW * 2 * kRows);
+  feat_row<F4, FB16>(feat_lanes<F4, FB16>(a, a.Qc, true), (uint32_t)tok, qf);
+  unique_bases<F4, FB16>(a, b, t, NU, false, qf, S, wave * 2 * kRows, NW * 2 * kRows);
   const float* sigb = a.sig + b * a.L;
   float mine[4];
   own_suffix_of(sigb, t, a.K, mine);
@@ -690,15 +691,15 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
 // One query token's candidate attention: salida row (d), the 4 gate signals and, when `ent_rows` is given, every
 // entry's weight at ent_rows[2 (tau * C + distance - 1)]. RING: candidates from the generation rings instead of the
 // sorted windows.
-template <int F4, int DCH, bool RING, bool B16 = false>
+template <int F4, int DCH, bool RING, int RB = 0>
 __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t t, Scratch& S, float* salida_row,
                                               float* signals_row, float* ent_rows) {
   const int64_t tok = b * a.L + t;
   uint8_t* rec = (!RING && a.lists) ? a.lists + tok * a.rec : nullptr;
   int NU;
   const int M = token_list<RING>(a, b, t, S, rec, &NU);
-  unique_terms<F4, 1>(a, b, t, NU, S, rec, 0);
-  token_weights<DCH, true, B16>(a, b, M, NU, S, salida_row, signals_row, ent_rows);
+  unique_terms<F4, 1, RB == 2>(a, b, t, NU, S, rec, 0);
+  token_weights<DCH, true, RB >= 1>(a, b, M, NU, S, salida_row, signals_row, ent_rows);
 }
 
 // The rest of a query's attention once its list and unique terms are in S: the exact masked softmax, the entries'
@@ -786,13 +787,14 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
   }
 }
 
-template <int F4, int DCH, bool B16>
+// RB: how V (and the backward's dO) and the features [phi ; Qc ; Kc] are stored: 0 fp32; 1 V and dO bf16; 2 all bf16
+template <int F4, int DCH, int RB>
 __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 6 : 1) void k_cand_fwd(Cand a) {   // 6 waves per SIMD when narrow
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
   const int64_t tok = token_of_wave();
   if (tok >= a.B * a.L) return;
-  forward_token<F4, DCH, false, B16>(a, tok / a.L, tok % a.L, S, a.salida + tok * a.d, a.signals + tok * 4,
+  forward_token<F4, DCH, false, RB>(a, tok / a.L, tok % a.L, S, a.salida + tok * a.d, a.signals + tok * 4,
                                 a.ent + tok * a.T * a.C * 2);
 }
 
@@ -861,8 +863,9 @@ __global__ __launch_bounds__(kWave * kDecodeWaves) void k_decode_attend(Cand a) 
 // backward, query pass: needs no scores. att comes from the forward; per distinct key, dp = <dO_q, V_k>, the clock
 // difference and the suffix length; per table D = sum att dp, then ds = att (dp - D) per entry, kept for the key pass.
 // ---------------------------------------------------------------------------------------------------------------------
-template <int F4, int DCH, bool B16>
+template <int F4, int DCH, int RB>
 __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
+  constexpr bool B16 = RB >= 1, FB16 = RB == 2;
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
   const int64_t tok = token_of_wave();
@@ -967,7 +970,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
 
   // d phi_q, d Qc_q = sum_u (sum_tau ds) [phi_u ; Kc_u]
   float4 gq[F4];
-  unique_feature_sum<F4>(a, b, t, NU, false, S.uc, S, gq);
+  unique_feature_sum<F4, FB16>(a, b, t, NU, false, S.uc, S, gq);
   if (half == 0) {   // P and cf are multiples of 4: a lane's 4 features lie in one of the two rows
 #pragma unroll
     for (int c = 0; c < F4; ++c) {
@@ -1022,9 +1025,10 @@ __device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows,
 // backward, key pass: no scores either. Every entry's att (forward) and ds (query pass) are read at the query's
 // slot for this key; per distinct query the table sums weight dO (-> dV) and [phi_q ; Qc_q] (-> d phi_k, d Kc_k).
 // ---------------------------------------------------------------------------------------------------------------------
-template <int F4, int DCH, bool B16>
+template <int F4, int DCH, int RB>
 __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 6 : ((F4 == 1 && DCH != 3) ? 5 : 1))
 void k_cand_bwd_k(Cand a) {
+  constexpr bool B16 = RB >= 1, FB16 = RB == 2;
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
   const int64_t tok = token_of_wave();
@@ -1089,7 +1093,7 @@ void k_cand_bwd_k(Cand a) {
   unique_row_sum<DCH, B16>(a, rows_at<B16>(a.dsal, b * a.L * a.d), k, NU, S.uc, S, dv);
   // d phi_k, d Kc_k = sum_u (sum_tau ds) [phi_q * scale_phi ; Qc_q * scale_c]
   float4 gk[F4];
-  unique_feature_sum<F4>(a, b, k, NU, true, S.ub, S, gk);
+  unique_feature_sum<F4, FB16>(a, b, k, NU, true, S.ub, S, gk);
   // with vshift, V[k] is the projection of k + 1: its gradient goes to row k + 1, and the last position (which no
   // query sees, so dv is 0) clears row 0, the projection no V reads
   const int64_t dv_row = a.vshift ? b * a.L + (k + 1 < a.L ? k + 1 : 0) : tok;
@@ -1183,55 +1187,59 @@ static Cand make(const float* phi, const float* V, const float* Qc, const float*
 }
 
 // launch a kernel template for the (float4 feature chunks per lane, d chunks) bucket of the arguments
-template <template <int, int, bool> class Launcher, bool B16>
+template <template <int, int, int> class Launcher, int RB>
 static int dispatch_rows(const Cand& a, hipStream_t st) {
   const int dch = (a.d + 255) / 256;
   if (a.P + a.cf <= 128) {
     switch (dch) {
-      case 1: return Launcher<1, 1, B16>::run(a, st);
-      case 2: return Launcher<1, 2, B16>::run(a, st);
-      case 3: return Launcher<1, 3, B16>::run(a, st);
-      default: return Launcher<1, 4, B16>::run(a, st);
+      case 1: return Launcher<1, 1, RB>::run(a, st);
+      case 2: return Launcher<1, 2, RB>::run(a, st);
+      case 3: return Launcher<1, 3, RB>::run(a, st);
+      default: return Launcher<1, 4, RB>::run(a, st);
     }
   }
   switch (dch) {
-    case 1: return Launcher<2, 1, B16>::run(a, st);
-    case 2: return Launcher<2, 2, B16>::run(a, st);
-    case 3: return Launcher<2, 3, B16>::run(a, st);
-    default: return Launcher<2, 4, B16>::run(a, st);
+    case 1: return Launcher<2, 1, RB>::run(a, st);
+    case 2: return Launcher<2, 2, RB>::run(a, st);
+    case 3: return Launcher<2, 3, RB>::run(a, st);
+    default: return Launcher<2, 4, RB>::run(a, st);
   }
 }
-// rows_bf16: V (and the backward's dO) stored as bf16
-template <template <int, int, bool> class Launcher>
-static int dispatch(const Cand& a, hipStream_t st, bool rows_bf16 = false) {
-  return rows_bf16 ? dispatch_rows<Launcher, true>(a, st) : dispatch_rows<Launcher, false>(a, st);
+// rows_bf16: 0 fp32 rows; 1 V (and the backward's dO) bf16; 2 V, dO and the features bf16
+template <template <int, int, int> class Launcher>
+static int dispatch(const Cand& a, hipStream_t st, int rows_bf16 = 0) {
+  if (rows_bf16 == 2) return dispatch_rows<Launcher, 2>(a, st);
+  return rows_bf16 == 1 ? dispatch_rows<Launcher, 1>(a, st) : dispatch_rows<Launcher, 0>(a, st);
 }
 
 static dim3 grid_of(const Cand& a) { return dim3((unsigned)((a.B * a.L + kWavesPerBlock - 1) / kWavesPerBlock)); }
 
-template <int F4, int DCH, bool B16>
+template <int F4, int DCH, int RB>
 struct LaunchFwd {
   static int run(const Cand& a, hipStream_t st) {
-    hipLaunchKernelGGL((k_cand_fwd<F4, DCH, B16>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
+    hipLaunchKernelGGL((k_cand_fwd<F4, DCH, RB>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
     return check_launch("asrn_candidates_fwd");
   }
 };
 
-template <int F4, int DCH, bool B16>
-struct LaunchDecode {                              // the generation caches are fp32 (B16 is never dispatched)
+template <int F4, int DCH, int RB>
+struct LaunchDecode {                              // the generation caches are fp32 (RB > 0 is never dispatched)
   static int run(const Cand& a, hipStream_t st) {
-    if constexpr (B16) return fail("asrn_decode_attend: fp32 caches only");
-    hipLaunchKernelGGL((k_decode_attend<F4, DCH>), dim3((unsigned)a.B), dim3(kWave * kDecodeWaves), 0, st, a);
-    return check_launch("asrn_decode_attend");
+    if constexpr (RB != 0) {
+      return fail("asrn_decode_attend: fp32 caches only");
+    } else {
+      hipLaunchKernelGGL((k_decode_attend<F4, DCH>), dim3((unsigned)a.B), dim3(kWave * kDecodeWaves), 0, st, a);
+      return check_launch("asrn_decode_attend");
+    }
   }
 };
 
-template <int F4, int DCH, bool B16>
+template <int F4, int DCH, int RB>
 struct LaunchBwd {
   static int run(const Cand& a, hipStream_t st) {
-    hipLaunchKernelGGL((k_cand_bwd_q<F4, DCH, B16>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
+    hipLaunchKernelGGL((k_cand_bwd_q<F4, DCH, RB>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
     if (check_launch("asrn_candidates_bwd/query")) return 1;
-    hipLaunchKernelGGL((k_cand_bwd_k<F4, DCH, B16>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
+    hipLaunchKernelGGL((k_cand_bwd_k<F4, DCH, RB>), grid_of(a), dim3(kWave * kWavesPerBlock), 0, st, a);
     return check_launch("asrn_candidates_bwd/key");
   }
 };
@@ -1257,8 +1265,8 @@ extern "C" int asrn_candidates_fwd(const float* phi, const float* V, const float
   a.salida = salida; a.signals = signals; a.ent = entries;
   a.lists = lists; a.rec = rec_layout(T, C).size;
   ASRN_REQUIRE(((uintptr_t)lists & 15) == 0, "asrn_candidates_fwd: lists must be 16-byte aligned");
-  ASRN_REQUIRE(rows_bf16 == 0 || rows_bf16 == 1, "asrn_candidates_fwd: rows_bf16 must be 0 or 1");
-  return dispatch<LaunchFwd>(a, (hipStream_t)stream, rows_bf16 != 0);
+  ASRN_REQUIRE(rows_bf16 >= 0 && rows_bf16 <= 2, "asrn_candidates_fwd: rows_bf16 must be 0, 1 or 2");
+  return dispatch<LaunchFwd>(a, (hipStream_t)stream, rows_bf16);
 }
 
 extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float* Qc, const float* Kc,
@@ -1283,9 +1291,9 @@ extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float
   ASRN_REQUIRE(((uintptr_t)lists & 15) == 0, "asrn_candidates_bwd: lists must be 16-byte aligned");
   a.dsal = dsalida; a.ent = entries; a.dphi = dphi; a.dV = dV; a.dQc = dQc; a.dKc = dKc; a.dBt = dBt;
   a.dla = dlog_alfa; a.partials = partials;
-  ASRN_REQUIRE(rows_bf16 == 0 || rows_bf16 == 1, "asrn_candidates_bwd: rows_bf16 must be 0 or 1");
+  ASRN_REQUIRE(rows_bf16 >= 0 && rows_bf16 <= 2, "asrn_candidates_bwd: rows_bf16 must be 0, 1 or 2");
   ASRN_REQUIRE(((uintptr_t)dsalida & 15) == 0, "asrn_candidates_bwd: dsalida must be 16-byte aligned");
-  return dispatch<LaunchBwd>(a, (hipStream_t)stream, rows_bf16 != 0);
+  return dispatch<LaunchBwd>(a, (hipStream_t)stream, rows_bf16);
 }
 
 extern "C" int64_t asrn_candidates_record_bytes(int32_t T, int32_t C) {

@@ -544,17 +544,26 @@ class Candidates(torch.autograd.Function):
         # the kernels read feature rows as float4: zero columns pad P and cf to multiples of 4 (dot products and the
         # gradients of the real columns are unchanged)
         vs = int(shape.get('v_shift', 0))
-        # bf16 value rows (autocast) are read as they are: the kernels widen each element exactly
-        rows16 = V.dtype == torch.bfloat16 and d % 4 == 0
+        # bf16 rows (autocast) are read as they are, the kernels widening each element exactly: the value rows
+        # (mode 1), and the feature rows too when phi, Qc and Kc are all bf16 with widths that need no padding (mode 2)
+        bf = torch.bfloat16
+        rows16 = V.dtype == bf and d % 4 == 0
+        feat16 = (rows16 and phi.dtype == bf and Qc.dtype == bf and Kc.dtype == bf and P0 % 4 == 0
+                  and cf0 % 4 == 0)
         if rows16:
-            Vk = V if _rows_in_place(V, torch.bfloat16) else _c(V)
+            Vk = V if _rows_in_place(V, bf) else _c(V)
         else:
             Vk = V if _rows_in_place(V) else _c(V, torch.float32)
-        if _rows_in_place(Qc) and _rows_in_place(Kc) and Qc.stride(1) == Kc.stride(1) and Qc.shape[-1] % 4 == 0:
+        ft = bf if feat16 else torch.float32
+        if (_rows_in_place(Qc, ft) and _rows_in_place(Kc, ft) and Qc.stride(1) == Kc.stride(1)
+                and Qc.shape[-1] % 4 == 0):
             Qk, Kk = Qc, Kc                        # column blocks of one projection, read through their row stride
+        elif feat16:
+            Qk, Kk = _c(Qc), _c(Kc)
         else:
             Qk, Kk = _pad4(Qc), _pad4(Kc)
-        ins = dict(phi=_pad4(phi), V=Vk, Qc=Qk, Kc=Kk, sig=_c(sig, torch.float32),
+        mode = 2 if feat16 else int(rows16)
+        ins = dict(phi=_c(phi) if feat16 else _pad4(phi), V=Vk, Qc=Qk, Kc=Kk, sig=_c(sig, torch.float32),
                    Bt=_c(Bt, torch.float64), la=_c(log_alfa, torch.float32), w=_c(w_suf.detach(), torch.float32),
                    g=_c(gamma.detach(), torch.float32))
         P, cf = ins['phi'].shape[-1], ins['Qc'].shape[-1]
@@ -566,7 +575,7 @@ class Candidates(torch.autograd.Function):
                   if shape.get('listas', True) else None)
         call('asrn_candidates_fwd', ptr(ins['phi']), ptr(ins['V']), ptr(ins['Qc']), ptr(ins['Kc']), ptr(ins['sig']),
              ptr(ins['Bt']), ptr(ins['la']), ptr(ins['w']), ptr(ins['g']), ptr(order), ptr(win), ptr(rank), B, L, d,
-             P, cf, K, T, Tc, C, sp, sc, Vk.stride(1), vs, Qk.stride(1), int(rows16), ptr(salida), ptr(signals),
+             P, cf, K, T, Tc, C, sp, sc, Vk.stride(1), vs, Qk.stride(1), mode, ptr(salida), ptr(signals),
              ptr(ent), ptr(listas), stream_of(dev))
         ctx.save_for_backward(*ins.values(), order, win, rank, ent, listas)
         ctx.meta = (B, L, P, d, cf, K, T, Tc, C, sp, sc, V.dtype, phi.dtype, Qc.dtype, Kc.dtype, log_alfa.dtype,
@@ -582,11 +591,15 @@ class Candidates(torch.autograd.Function):
         phi, V, Qc, Kc, sig, Bt, la, w, g, order, win, rank, ent, listas = ctx.saved_tensors
         B, L, P, d, cf, K, T, Tc, C, sp, sc, tv, tp, tq, tk, tl, P0, cf0, vs = ctx.meta
         dev = phi.device
-        rows16 = V.dtype == torch.bfloat16 and dsal.dtype == torch.bfloat16
-        if V.dtype == torch.bfloat16 and not rows16:                  # an fp32 gradient: the fp32 path throughout
-            V = V.float()
-        dsal = _c(dsal) if rows16 else _c(dsal, torch.float32)
-        dphi = torch.empty_like(phi)
+        bf = torch.bfloat16
+        mode = (2 if phi.dtype == bf else 1) if V.dtype == bf else 0
+        if mode and dsal.dtype != bf:             # an fp32 gradient: the fp32 path throughout
+            mode = 0
+            V, phi = V.float(), phi.float()
+            if Qc.dtype == bf:
+                Qc, Kc = Qc.float(), Kc.float()
+        dsal = _c(dsal) if mode else _c(dsal, torch.float32)
+        dphi = torch.empty(phi.shape, dtype=torch.float32, device=dev)
         # dV takes V's layout: when V is a column block read in place, the same block of a (B, L, ldv) buffer, so the
         # producer whose output V is can take the buffer as its own output gradient without a copy
         ldv = V.stride(1)
@@ -607,7 +620,7 @@ class Candidates(torch.autograd.Function):
         dla = torch.empty_like(la)
         partials = torch.empty((B * L, T + K + 1), dtype=torch.float32, device=dev)
         call('asrn_candidates_bwd', ptr(phi), ptr(V), ptr(Qc), ptr(Kc), ptr(sig), ptr(Bt), ptr(la), ptr(w), ptr(g),
-             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ldv, vs, Qc.stride(1), int(rows16),
+             ptr(order), ptr(win), ptr(rank), B, L, d, P, cf, K, T, Tc, C, sp, sc, ldv, vs, Qc.stride(1), mode,
              ptr(dsal), ptr(ent), ptr(listas),
              ptr(dphi), ptr(dV), ptr(dQc), ptr(dKc), ptr(dBt), ptr(dla), ptr(partials), stream_of(dev))
         part = column_sums(partials)          # per-query partials summed over the tokens (no memset-cleared reduction)

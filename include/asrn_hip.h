@@ -60,8 +60,9 @@ int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t T, int32_t 
  *           aligned). v_shift = 0: V as the reference passes it (V[p] = W_v E[p+1], nucleo:659, the last row 0);
  *           v_shift = 1: V is the projection W_v E of every position (e.g. a column block of a wider GEMM output,
  *           ldv its row stride), and the kernels read the next position's row themselves.
- *   rows_bf16: 1 when V holds bf16 values (the same layout in 2-byte elements; the reference's V under bf16
- *           autocast): the kernels widen each element exactly, so the results equal those from an fp32 copy of V.
+ *   rows_bf16: 0 fp32 rows; 1 V holds bf16 values (the same layout in 2-byte elements; the reference's V under
+ *           bf16 autocast); 2 phi, Qc and Kc are bf16 too. The kernels widen each element exactly, so the results
+ *           equal those from fp32 copies.
  *   Qc, Kc rows: row t at Qc + t * ldq (and Kc + t * ldq): ldq = cf for dense rows, or the row stride when both are
  *           column blocks of one projection (ldq >= cf, a multiple of 4, rows 16-byte aligned).
  * Requires d % 4 == 0, d <= 1024, 1 <= C <= 64, P + cf <= 256, K <= 16, T <= 32, L * ldv < 2^31. */
@@ -92,7 +93,7 @@ int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* 
  * ds = att (dp - D) with D = sum att*dp per (query, table), query-side gradients, per-query partials of d gamma and
  * d w_suf) and a key pass (key-side gradients from att and ds at the slots of the queries that see the key: the
  * next <= C same-bucket sorted ranks).
- *   dsalida (B, L, d), 16-byte aligned: bf16 with V when rows_bf16 = 1; entries from asrn_candidates_fwd (its
+ *   dsalida (B, L, d), 16-byte aligned: bf16 with V when rows_bf16 > 0; entries from asrn_candidates_fwd (its
  *   [..., 1] receives ds, read back by the key pass)
  *   lists   the forward's candidate lists (same inputs), or null to gather and deduplicate again
  *   dphi (B, L, P) dense, dBt (B, L) fp64, dlog_alfa (B, L) out (overwritten); dV, dQc and dKc have the layout of
