@@ -135,6 +135,21 @@ __device__ __forceinline__ float4 ld4r(const float* base, uint32_t off) {
     return ld4(base + off);
   }
 }
+// 4 values stored at element `off` of an fp32 or bf16 (B16: rounded to nearest even, as a cast to bfloat16 does) row
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+  const uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;        // NaN stays a (quiet) NaN
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+template <bool B16>
+__device__ __forceinline__ void st4r(float* base, int64_t off, const float4& v) {
+  if constexpr (B16) {
+    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(base) + off) =
+        make_uint2(bf16_bits(v.x) | (bf16_bits(v.y) << 16), bf16_bits(v.z) | (bf16_bits(v.w) << 16));
+  } else {
+    *reinterpret_cast<float4*>(base + off) = v;
+  }
+}
 __device__ __forceinline__ float dot4(const float4& x, const float4& y) {
   return x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
 }
@@ -782,7 +797,7 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
 #pragma unroll
     for (int ch = 0; ch < DCH; ++ch) {
       const int dd = ch * 256 + lane * 4;
-      if (dd < a.d) *reinterpret_cast<float4*>(salida_row + dd) = acc[ch];
+      if (dd < a.d) st4r<B16>(salida_row, dd, acc[ch]);
     }
   }
 }
@@ -794,8 +809,9 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 6 :
   Scratch& S = scratch[threadIdx.x >> 6];
   const int64_t tok = token_of_wave();
   if (tok >= a.B * a.L) return;
-  forward_token<F4, DCH, false, RB>(a, tok / a.L, tok % a.L, S, a.salida + tok * a.d, a.signals + tok * 4,
-                                a.ent + tok * a.T * a.C * 2);
+  float* salida_row = const_cast<float*>(rows_at<RB >= 1>(a.salida, tok * a.d));   // bf16 with the value rows
+  forward_token<F4, DCH, false, RB>(a, tok / a.L, tok % a.L, S, salida_row, a.signals + tok * 4,
+                                    a.ent + tok * a.T * a.C * 2);
 }
 
 // Generation step: one workgroup of kDecodeWaves waves per batch row; the query is position tq = a.tq (or *a.tq_dev)
@@ -1100,7 +1116,7 @@ void k_cand_bwd_k(Cand a) {
 #pragma unroll
   for (int ch = 0; ch < DCH; ++ch) {
     const int dd = ch * 256 + lane * 4;
-    if (dd < a.d) *reinterpret_cast<float4*>(a.dV + dv_row * a.ldv + dd) = dv[ch];
+    if (dd < a.d) st4r<B16>(a.dV, dv_row * a.ldv + dd, dv[ch]);
   }
   if (half == 0) {   // P and cf are multiples of 4: a lane's 4 features lie in one of the two rows
 #pragma unroll

@@ -567,7 +567,8 @@ class Candidates(torch.autograd.Function):
                    Bt=_c(Bt, torch.float64), la=_c(log_alfa, torch.float32), w=_c(w_suf.detach(), torch.float32),
                    g=_c(gamma.detach(), torch.float32))
         P, cf = ins['phi'].shape[-1], ins['Qc'].shape[-1]
-        salida = torch.empty((B, L, d), dtype=torch.float32, device=dev)
+        # bf16 value rows: salida written in bf16 by the kernel (each fp32 sum rounded once, as a cast would)
+        salida = torch.empty((B, L, d), dtype=bf if mode else torch.float32, device=dev)
         signals = torch.empty((B, L, 4), dtype=torch.float32, device=dev)
         ent = torch.empty((B, L, T, C, 2), dtype=torch.float32, device=dev)  # only the valid slots are written
         # each query's deduplicated candidate list, for the backward's query pass (shape['listas'] = False: none)
@@ -605,7 +606,7 @@ class Candidates(torch.autograd.Function):
         ldv = V.stride(1)
         col = V.storage_offset() % ldv
         col = col if col + d <= ldv else 0
-        dV = torch.empty((B, L, ldv), dtype=torch.float32, device=dev)[..., col:col + d]
+        dV = torch.empty((B, L, ldv), dtype=bf if mode else torch.float32, device=dev)[..., col:col + d]
         # dQc and dKc take the layout of Qc and Kc: when both are column blocks of one projection (row stride ldq),
         # the same blocks of one (B, L, ldq) buffer, which _Split2's backward hands on whole
         ldq = Qc.stride(1)

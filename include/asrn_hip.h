@@ -49,7 +49,7 @@ int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t T, int32_t 
  * asrn_bucket_sort): its <= C most recent earlier bucket mates. Score = <phi_q, phi_k> * scale_phi + <Qc_q, Kc_k> * scale_c
  * + w_suf[suffix match] + log_alfa_k + (gamma_tau / C) * fp32(Bt_k - Bt_q); exact masked softmax.
  *   sig (B, L) fp32 token signatures; Bt (B, L) fp64 clock; log_alfa (B, L); w_suf (K+1); gamma (T)
- *   salida  (B, L, d) out: sum over tables of sum_k att * V_k
+ *   salida  (B, L, d) out: sum over tables of sum_k att * V_k (bf16, rounded to nearest even, when rows_bf16 > 0)
  *   signals (B, L, 4) out: peso_total, mejor, pico, peso_ctx
  *   entries (B, L, T, C, 2) out: [..., 0] the weight of each candidate, at [query][tau][distance - 1] (distance
  *           in sorted ranks, 1..n; slots beyond the table's n candidates are not written); [..., 1] is filled by the
@@ -96,7 +96,8 @@ int asrn_candidate_lists(const float* sig, const int32_t* order, const int32_t* 
  *   dsalida (B, L, d), 16-byte aligned: bf16 with V when rows_bf16 > 0; entries from asrn_candidates_fwd (its
  *   [..., 1] receives ds, read back by the key pass)
  *   lists   the forward's candidate lists (same inputs), or null to gather and deduplicate again
- *   dphi (B, L, P) dense, dBt (B, L) fp64, dlog_alfa (B, L) out (overwritten); dV, dQc and dKc have the layout of
+ *   dphi (B, L, P) dense, dBt (B, L) fp64, dlog_alfa (B, L) out (overwritten); dV (bf16 when rows_bf16 > 0), dQc
+ *   and dKc (fp32) have the layout of
  *   V, Qc and Kc (row strides ldv and ldq, 16-byte aligned): their d (cf) columns of every row are written, the rest
  *   of a row is left alone; with v_shift = 1, dV is the gradient of the per-position rows (row 0 of each batch row
  *   is 0)
