@@ -38,8 +38,11 @@ struct PhiArgs {
 };
 
 __device__ __forceinline__ float gelu_e(float x) { return 0.5f * x * (1.f + erff(x * 0.70710678118654752f)); }
-__device__ __forceinline__ float gelu_d(float x) {
-  return 0.5f * (1.f + erff(x * 0.70710678118654752f)) + x * 0.39894228040143268f * __expf(-0.5f * x * x);
+// gelu(x) and gelu'(x) from one erf: cdf = Phi(x), gelu = x cdf, gelu' = cdf + x pdf(x)
+__device__ __forceinline__ void gelu_both(float x, float* g, float* gd) {
+  const float cdf = 0.5f * (1.f + erff(x * 0.70710678118654752f));
+  *g = x * cdf;
+  *gd = cdf + x * 0.39894228040143268f * __expf(-0.5f * x * x);
 }
 
 __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
@@ -273,9 +276,12 @@ __global__ __launch_bounds__(kPhiThreads) void k_phi_bwd(PhiArgs a) {
         const int64_t t = row % a.L;
         const float4 x = pre_of(in, xi);
         const float* d = dgs + tk * kGld + j;
-        const float4 dp = make_float4(d[0] * gelu_d(x.x), d[1] * gelu_d(x.y), d[2] * gelu_d(x.z),
-                                      d[3] * gelu_d(x.w));
-        g = make_float4(gelu_e(x.x), gelu_e(x.y), gelu_e(x.z), gelu_e(x.w));
+        float4 gd;
+        gelu_both(x.x, &g.x, &gd.x);
+        gelu_both(x.y, &g.y, &gd.y);
+        gelu_both(x.z, &g.z, &gd.z);
+        gelu_both(x.w, &g.w, &gd.w);
+        const float4 dp = make_float4(d[0] * gd.x, d[1] * gd.y, d[2] * gd.z, d[3] * gd.w);
         *reinterpret_cast<float4*>(a.dy + row * a.ldd + j) = dp;
         if (j >= a.m) {
           const int c = j - a.m;
