@@ -14,9 +14,8 @@ import time
 import warnings
 
 import torch
-import torch.nn.functional as F
 
-from . import archivo
+from . import archivo, ops
 from .modelo import _base
 
 # the suffix and gate parameters of each ASRN layer learn this many times faster (asrn/nucleo.py:2188-2189)
@@ -96,8 +95,9 @@ def autocast(precision, disp, cache=True):
 
 
 def entropia(logits, y, reduccion='mean'):
-    """fp32 cross-entropy of logits (..., V) against y (...)."""
-    return F.cross_entropy(logits.float().flatten(0, -2), y.flatten(), reduction=reduccion)
+    """fp32 cross-entropy of logits (..., V) against y (...) (asrn/nucleo.py:2301): on the GPU by ops.cross_entropy,
+    which reads bf16 logits as they are."""
+    return ops.cross_entropy(logits, y, reduction=reduccion)
 
 
 class PasoGrafado:

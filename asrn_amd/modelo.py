@@ -16,6 +16,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .capa import CapaASRNEstable, ngramas
+from . import ops
 from .ops import escaneo
 
 MEZCLAS = ('conv', 'memoria')
@@ -197,7 +198,7 @@ class ModeloASRN(nn.Module):
     def perdida(self, x, y, ignorar=-100):
         """Mean fp32 cross-entropy of predicting y from x, both (B, L) (asrn/nucleo.py:1122-1125)."""
         logits = self(x)
-        return F.cross_entropy(logits.float().flatten(0, -2), y.flatten(), ignore_index=ignorar)
+        return ops.cross_entropy(logits, y, ignore_index=ignorar)
 
     def num_parametros(self):
         return sum(p.numel() for p in self.parameters())

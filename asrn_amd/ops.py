@@ -906,3 +906,71 @@ def paso_bloque(blq, h, anillo, pos, espacio):
          float(blq.ln1.eps), ptr(z), ptr(x1), ptr(h1), ptr(x2), ptr(out), ptr(espacio), espacio.numel(),
          stream_of(dev))
     return out
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# the model's loss
+# ---------------------------------------------------------------------------------------------------------------------
+
+class CrossEntropy(torch.autograd.Function):
+    """F.cross_entropy(logits.float().reshape(-1, V), target.reshape(-1), ignore_index, reduction) for 'mean' and
+    'sum' (asrn/nucleo.py:1108): asrn_cross_entropy_fwd/bwd compute it in fp32 from fp32 or bf16 logits as they are
+    (no fp32 copy), and the gradient comes back in the logits' dtype. The rows are reduced here: the mean divides the
+    summed row losses by the count of rows not ignored (NaN when there is none, as PyTorch gives)."""
+
+    @staticmethod
+    def forward(ctx, logits, target, ignore_index, reduction):
+        dev = _dev(logits)
+        V = logits.shape[-1]
+        x = logits.reshape(-1, V)
+        if x.dtype not in (torch.float32, torch.bfloat16):
+            x = x.float()
+        bf16 = x.dtype == torch.bfloat16
+        step = 8 if bf16 else 4                      # elements per 16 bytes: rows must start 16-byte aligned
+        if x.stride(-1) != 1 or x.stride(0) % step or x.data_ptr() % 16:
+            if V % step:
+                xp = torch.empty((x.shape[0], V + (-V % step)), dtype=x.dtype, device=dev)
+                xp[:, :V] = x
+                x = xp[:, :V]
+            else:
+                x = x.contiguous()
+        rows, ld = x.shape[0], x.stride(0)
+        t = target.reshape(-1).to(torch.int64).contiguous()
+        if t.numel() != rows:
+            raise ValueError(f'cross_entropy: {rows} rows of logits against {t.numel()} targets')
+        lse = torch.empty((rows,), dtype=torch.float32, device=dev)
+        per = torch.empty((rows,), dtype=torch.float32, device=dev)
+        call('asrn_cross_entropy_fwd', ptr(x), int(bf16), ld, ptr(t), rows, V, int(ignore_index), ptr(lse), ptr(per),
+             stream_of(dev))
+        total = per.sum()
+        if reduction == 'mean':
+            count = (t != ignore_index).sum().to(torch.float32)
+            out = total / count
+        else:
+            count = None
+            out = total
+        ctx.save_for_backward(x, t, lse, count if count is not None else total)
+        ctx.meta = (int(ignore_index), reduction, logits.shape, logits.dtype, bf16)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        x, t, lse, count = ctx.saved_tensors
+        ignore_index, reduction, shape, dtype, bf16 = ctx.meta
+        rows, V = x.shape
+        dev = x.device
+        scale = (g.float() / count) if reduction == 'mean' else g.float().reshape(())
+        scale = scale.reshape(1).contiguous()
+        ld = V + (-V % (8 if bf16 else 4))
+        dx = torch.empty((rows, ld), dtype=x.dtype, device=dev)
+        call('asrn_cross_entropy_bwd', ptr(x), int(bf16), x.stride(0), ptr(t), ptr(lse), rows, V, ignore_index,
+             ptr(scale), ptr(dx), ld, stream_of(dev))
+        return dx[:, :V].reshape(shape).to(dtype), None, None, None
+
+
+def cross_entropy(logits, target, ignore_index=-100, reduction='mean'):
+    """The model's loss on the GPU (CrossEntropy); 'none' and CPU tensors take F.cross_entropy on the fp32 logits."""
+    if logits.is_cuda and reduction in ('mean', 'sum'):
+        return CrossEntropy.apply(logits, target, ignore_index, reduction)
+    return torch.nn.functional.cross_entropy(logits.float().reshape(-1, logits.shape[-1]), target.reshape(-1),
+                                             ignore_index=ignore_index, reduction=reduction)

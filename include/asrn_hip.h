@@ -399,6 +399,20 @@ int asrn_block_step(const float* h, int64_t ldh, float* ring, const int64_t* pos
                     const float* b2, float eps, float* z, float* x1, float* h1, float* x2, float* out,
                     void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- the model's loss: cross-entropy ---------------------------------------------------------------------------
+ * Replaces F.cross_entropy(logits.float().reshape(-1, V), y.reshape(-1), ignore_index) of ModeloASRN.perdida and the
+ * training loop (asrn/nucleo.py:1108, 2301): the same fp32 arithmetic on fp32 or bf16 logits (logits_bf16), without
+ * the fp32 copy of the logits. logits (rows, V) with row stride ld (16-byte aligned rows), target (rows) int64.
+ * fwd: lse (rows) = logsumexp of the row, loss (rows) = lse - logits[target] (0 where target == ignore_index, NaN
+ * for a target outside [0, V)); the caller reduces the rows (mean over the rows not ignored, or sum).
+ * bwd: dlogits (rows, V), row stride ldd, in the logits' dtype = (softmax - onehot(target)) * *scale (scale a device
+ * float: d loss / count for the mean), 0 for ignored rows; bf16 rounded to nearest even. */
+int asrn_cross_entropy_fwd(const void* logits, int32_t logits_bf16, int64_t ld, const int64_t* target, int64_t rows,
+                           int64_t V, int64_t ignore_index, float* lse, float* loss, void* stream);
+int asrn_cross_entropy_bwd(const void* logits, int32_t logits_bf16, int64_t ld, const int64_t* target,
+                           const float* lse, int64_t rows, int64_t V, int64_t ignore_index, const float* scale,
+                           void* dlogits, int64_t ldd, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,42 @@ def _grads(m, x, y, checkpoint='no'):
     return float(perdida.detach()), float(norma), {n: p.grad.detach().cpu() for n, p in m.named_parameters()}
 
 
+@pytest.mark.parametrize('dtype,V,rows,reduction', [(torch.bfloat16, 50304, 300, 'mean'),
+                                                     (torch.float32, 50304, 300, 'mean'),
+                                                     (torch.bfloat16, 1001, 257, 'sum'),
+                                                     (torch.float32, 6, 5, 'mean'),
+                                                     (torch.bfloat16, 7, 33, 'mean')])
+def test_cross_entropy_matches_torch(dtype, V, rows, reduction):
+    """asrn_cross_entropy_fwd/bwd (the model's loss) against F.cross_entropy(logits.float(), y, ignore_index) as the
+    reference computes it: the loss to 2e-6 relative and the gradient (in the logits' dtype, after PyTorch's cast back)
+    to one bf16 rounding step or 1e-6 in fp32; ignored targets; odd V (a padded row stride); a row of +-inf and huge
+    logits; a NaN row makes the loss NaN."""
+    say('cross_entropy', dtype, V, rows, reduction)
+    g = torch.Generator().manual_seed(V + rows)
+    x = (torch.randn(rows, V, generator=g) * 4).to(dtype).to(DEV)
+    x[1, :3] = float('-inf')
+    x[2, 0] = 1e4 if dtype == torch.float32 else 3e38
+    y = torch.randint(0, V, (rows,), generator=g).to(DEV)
+    y[::7] = -100
+    y[1] = 4 if V > 4 else V - 1
+    a = x.clone().requires_grad_()
+    b = x.clone().requires_grad_()
+    la = asrn_amd.ops.cross_entropy(a, y, ignore_index=-100, reduction=reduction)
+    lb = torch.nn.functional.cross_entropy(b.float(), y, ignore_index=-100, reduction=reduction)
+    assert abs(float(la) - float(lb)) <= 2e-6 * abs(float(lb)), (float(la), float(lb))
+    la.backward()
+    lb.backward()
+    assert a.grad.dtype == dtype
+    d = (a.grad.float() - b.grad.float()).abs()
+    if dtype == torch.bfloat16:
+        assert bool((d <= b.grad.float().abs() * 2 ** -7 + 1e-12).all()), float(d.max())
+    else:
+        assert float(d.max()) <= 1e-6 * float(b.grad.abs().max()), float(d.max())
+    xn = x.clone()
+    xn[3, 3] = float('nan')                         # row 3 counts (row 0 is ignored, as in PyTorch)
+    assert torch.isnan(asrn_amd.ops.cross_entropy(xn, y)).item()
+
+
 @pytest.mark.parametrize('nombre', ['paso_cfg0', 'paso_memoria'])
 def test_training_step_matches_reference(nombre):
     t, kw = _fixture(nombre)
