@@ -44,9 +44,14 @@ def conv_causal(z, peso, sesgo):
     weight layout (d_out, d_in, k) over the left-padded sequence, as one GEMM of (B L, k d_in) by (k d_in, d_out).
     z (B, L, d_in) -> (B, L, d_out)."""
     k = peso.shape[-1]
-    zp = F.pad(z, (0, 0, k - 1, 0))
-    cols = zp.unfold(1, k, 1)                        # (B, L, d_in, k): [b, t, c, j] = zp[b, t + j, c]
-    cols = cols.reshape(z.shape[0], z.shape[1], -1)  # (B, L, d_in * k), column c * k + j (one copy)
+    if z.is_cuda and z.dtype == torch.float32 and 1 <= k <= 16:
+        # the columns written once, in the dtype the GEMM computes in (ops.VentanaCausal)
+        dt = torch.get_autocast_dtype('cuda') if torch.is_autocast_enabled('cuda') else torch.float32
+        cols = ops.ventana_causal(z, k, dt if dt in (torch.float32, torch.bfloat16) else torch.float32)
+    else:
+        zp = F.pad(z, (0, 0, k - 1, 0))
+        cols = zp.unfold(1, k, 1)                        # (B, L, d_in, k): [b, t, c, j] = zp[b, t + j, c]
+        cols = cols.reshape(z.shape[0], z.shape[1], -1)  # (B, L, d_in * k), column c * k + j (one copy)
     return F.linear(cols, peso.reshape(peso.shape[0], -1), sesgo)
 
 

@@ -974,3 +974,39 @@ def cross_entropy(logits, target, ignore_index=-100, reduction='mean'):
         return CrossEntropy.apply(logits, target, ignore_index, reduction)
     return torch.nn.functional.cross_entropy(logits.float().reshape(-1, logits.shape[-1]), target.reshape(-1),
                                              ignore_index=ignore_index, reduction=reduction)
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# the local block's convolution window
+# ---------------------------------------------------------------------------------------------------------------------
+
+class VentanaCausal(torch.autograd.Function):
+    """The columns of a 'conv' local block's causal convolution, cols[b, t, c k + j] = z[b, t + j - (k - 1), c] (zeros
+    before a row's start): what pad + unfold + reshape build (asrn/nucleo.py:969-1014), written by asrn_conv_window_fwd
+    straight in the dtype the GEMM takes (bf16 under autocast: the same rounding as the cast); the backward folds the
+    columns' gradient back (asrn_conv_window_bwd) into an fp32 z gradient. z fp32 (B, L, d)."""
+
+    @staticmethod
+    def forward(ctx, z, k, dtype):
+        dev = _dev(z)
+        B, L, d = z.shape
+        zc = z if z.stride(-1) == 1 and z.stride(0) == L * z.stride(1) else z.contiguous()
+        cols = torch.empty((B, L, d * k), dtype=dtype, device=dev)
+        call('asrn_conv_window_fwd', ptr(zc), zc.stride(1), B, L, d, k, int(dtype == torch.bfloat16), ptr(cols),
+             stream_of(dev))
+        ctx.meta = (B, L, d, k)
+        return cols
+
+    @staticmethod
+    def backward(ctx, dcols):
+        B, L, d, k = ctx.meta
+        dev = dcols.device
+        bf16 = dcols.dtype == torch.bfloat16
+        dc = _c(dcols) if bf16 else _c(dcols, torch.float32)
+        dz = torch.empty((B, L, d), dtype=torch.float32, device=dev)
+        call('asrn_conv_window_bwd', ptr(dc), int(bf16), B, L, d, k, ptr(dz), d, stream_of(dev))
+        return dz, None, None
+
+
+def ventana_causal(z, k, dtype):
+    return VentanaCausal.apply(z, k, dtype)

@@ -413,6 +413,18 @@ int asrn_cross_entropy_bwd(const void* logits, int32_t logits_bf16, int64_t ld, 
                            const float* lse, int64_t rows, int64_t V, int64_t ignore_index, const float* scale,
                            void* dlogits, int64_t ldd, void* stream);
 
+/* ---- the model's local block: the causal convolution's columns ----------------------------------------------
+ * Replaces F.pad + unfold + reshape of the 'conv' BloqueLocal's convolution (asrn/nucleo.py:969-1014, nn.Conv1d over
+ * the left-padded sequence) and the cast of those columns to the autocast dtype. fwd: z (B, L, d) fp32, row stride
+ * ldz -> cols (B, L, d * k) with cols[b, t, c * k + j] = z[b, t + j - (k - 1), c] (0 before the row's start), in
+ * fp32 or bf16 (cols_bf16, rounded to nearest even), 16-byte aligned. bwd: dcols (B, L, d * k) of that dtype ->
+ * dz (B, L, d) fp32, row stride lddz: dz[b, s, c] = sum over j (ascending) of dcols[b, s + k - 1 - j, c * k + j]
+ * (windows inside the row). 1 <= k <= 16. */
+int asrn_conv_window_fwd(const float* z, int64_t ldz, int64_t B, int64_t L, int32_t d, int32_t k, int32_t cols_bf16,
+                         void* cols, void* stream);
+int asrn_conv_window_bwd(const void* dcols, int32_t cols_bf16, int64_t B, int64_t L, int32_t d, int32_t k, float* dz,
+                         int64_t lddz, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

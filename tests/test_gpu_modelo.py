@@ -89,6 +89,26 @@ def test_cross_entropy_matches_torch(dtype, V, rows, reduction):
     assert torch.isnan(asrn_amd.ops.cross_entropy(xn, y)).item()
 
 
+@pytest.mark.parametrize('dtype,B,L,d,k', [(torch.bfloat16, 3, 517, 96, 4), (torch.float32, 2, 300, 64, 4),
+                                            (torch.bfloat16, 2, 40, 10, 3), (torch.float32, 1, 5, 8, 7)])
+def test_conv_window_matches_unfold(dtype, B, L, d, k):
+    """asrn_conv_window_fwd/bwd (the 'conv' block's convolution columns) against pad + unfold + reshape and the cast to
+    the GEMM's dtype: the columns bit-identical, the z gradient to fp32 rounding (the fold sums k terms in another
+    order); k = 4 takes the vectorized kernels, 3 and 7 the general ones, and rows shorter than k are covered."""
+    say('conv window', dtype, B, L, d, k)
+    g = torch.Generator().manual_seed(L + k)
+    z = torch.randn(B, L, d, generator=g).to(DEV)
+    gc = torch.randn(B, L, d * k, generator=g).to(DEV).to(dtype)
+    a = z.clone().requires_grad_()
+    b = z.clone().requires_grad_()
+    ca = asrn_amd.ops.ventana_causal(a, k, dtype)
+    cb = torch.nn.functional.pad(b, (0, 0, k - 1, 0)).unfold(1, k, 1).reshape(B, L, -1).to(dtype)
+    assert ca.dtype == dtype and torch.equal(ca, cb)
+    (ca.float() * gc.float()).sum().backward()
+    (cb.float() * gc.float()).sum().backward()
+    assert torch.allclose(a.grad, b.grad, rtol=1e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize('nombre', ['paso_cfg0', 'paso_memoria'])
 def test_training_step_matches_reference(nombre):
     t, kw = _fixture(nombre)
