@@ -1,11 +1,12 @@
-"""GEMM solution picks for the layer's projections on MI355X.
+"""GEMM solution picks for the layer's and the model's dense products on MI355X.
 
-The layer's dense products run on hipBLASLt / rocBLAS through torch. Their default heuristics pick kernels that leave
-a few percent on the table at the layer benchmark's shapes (32768 tokens, d = 256), so the package ships the picks
-torch's TunableOp measured on MI355X for those shapes (data/gemm_picks_mi355x.csv: one line per GEMM shape, the
-solution and its time, headed by the torch / HIP / hipBLASLt / rocBLAS versions and the GPU arch they are valid for).
-use_tuned_gemms() loads them with tuning off: shapes in the file run the measured solution, every other shape the
-library default, and a version mismatch makes TunableOp ignore the file. Nothing is tuned at run time.
+They run on hipBLASLt / rocBLAS through torch, whose default heuristics leave time on the table at the benchmarks'
+shapes (the layer: 32768 tokens, d = 256, fp32; the d = 768 model's bf16 training step: 16384 tokens, its blocks,
+layers and the 50,304-row head; the quick-start model). The package ships the picks torch's TunableOp measured on
+MI355X for those shapes (data/gemm_picks_mi355x.csv: one line per GEMM shape, the solution and its time, headed by the
+torch / HIP / hipBLASLt / rocBLAS versions and the GPU arch they are valid for). use_tuned_gemms() loads them with
+tuning off: shapes in the file run the measured solution, every other shape the library default, and a version
+mismatch makes TunableOp ignore the file. Nothing is tuned at run time.
 """
 import os
 import tempfile

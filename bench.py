@@ -369,15 +369,15 @@ def main():
         return
 
     asrn_amd.cargar_biblioteca()
-    if args.model_only:
-        print(json.dumps({'modelo': {n: modelo_bench(torch.device('cuda:0'), n, args.model_steps, 5, seed=args.seed)
-                                     for n in MODELOS}}), flush=True)
-        return
     gemm_picks = 'library defaults'
     if not args.default_gemms:
         from asrn_amd import tuning
         if tuning.use_tuned_gemms():
             gemm_picks = 'TunableOp picks, asrn_amd/data/gemm_picks_mi355x.csv'
+    if args.model_only:
+        print(json.dumps({'modelo': {n: modelo_bench(torch.device('cuda:0'), n, args.model_steps, 5, seed=args.seed)
+                                     for n in MODELOS}, 'gemm_picks': gemm_picks}), flush=True)
+        return
     contexts = [int(c) for c in args.decode_contexts.split(',')] if args.decode_contexts else None
     if args.decode_only:
         print(json.dumps({'decode': decode_bench(torch.device('cuda:0'), args.decode_steps, 20, seed=args.seed,
