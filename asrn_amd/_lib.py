@@ -20,7 +20,8 @@ _F32 = ctypes.c_float
 SIGNATURES = {
     'asrn_hip_last_error': (ctypes.c_char_p, []),
     'asrn_hip_abi_version': (_I32, []),
-    'asrn_bucket_sort': (ctypes.c_int, [_P, _I64, _I64, _I32, _I32, _I64, _I32, _P, _P, _P, _P, _P, _P]),
+    'asrn_bucket_sort_workspace': (_I64, [_I64, _I64, _I32]),
+    'asrn_bucket_sort': (ctypes.c_int, [_P, _I64, _I64, _I32, _I32, _I64, _I32, _P, _P, _P, _P, _P, _P, _I64, _P]),
     'asrn_candidates_fwd': (ctypes.c_int, [_P] * 12 + [_I64, _I64] + [_I32] * 7
                             + [_F32, _F32, _I64, _I32, _I64, _I32] + [_P] * 5),
     'asrn_candidates_record_bytes': (_I64, [_I32, _I32]),

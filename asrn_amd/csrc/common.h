@@ -45,6 +45,21 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// ---- workgroup placement ----------------------------------------------------------------------------------------------
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup i runs on XCD i % 8), each with its own L2. For a
+// 1-D grid of xcd_grid(rows, chunks) workgroups, the (chunk, row) of this workgroup such that every chunk of a row runs
+// on XCD row % 8: a later kernel with the same map reads what an earlier one wrote for the row from that XCD's L2.
+// The rows past `rows` in the last group of 8 come out >= rows; their workgroups have nothing to do.
+constexpr int kXcdCount = 8;
+inline unsigned xcd_grid(int64_t rows, int chunks) {
+  return (unsigned)((rows + kXcdCount - 1) / kXcdCount * kXcdCount * chunks);
+}
+__device__ __forceinline__ void xcd_chunk_row(int chunks, int* chunk, int64_t* row) {
+  const int64_t i = blockIdx.x, rest = i / kXcdCount;
+  *chunk = (int)(rest % chunks);
+  *row = i % kXcdCount + kXcdCount * (rest / chunks);
+}
+
 // ---- DPP reductions (no LDS traffic): rotate within each 16-lane row, then combine the four rows ---------------------
 // DPP control words of GFX9-family ISAs: row_ror:n = 0x120 + n.
 template <int CTRL>

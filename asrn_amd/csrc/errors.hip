@@ -22,4 +22,4 @@ int check_launch(const char* what) {
 }  // namespace asrn
 
 extern "C" const char* asrn_hip_last_error(void) { return asrn::g_msg; }
-extern "C" int32_t asrn_hip_abi_version(void) { return 1; }
+extern "C" int32_t asrn_hip_abi_version(void) { return 2; }

@@ -6,20 +6,32 @@
 // last and stays in text order, as torch.argsort(stable=True) does). The pairs are unique, so any correct sort of
 // them is the stable sort.
 //
-//   k_ngram_rows   one workgroup per tile of up to 4096 positions of a (b, j) row: the keys of its positions, a sort
-//                  of the tile in LDS (4 pairs per thread sorted in registers, then merge levels of doubling runs in
-//                  which every thread finds its 4 output slots' split point by a merge-path search and merges them),
-//                  and, when the tile is the whole row, the outputs (order, repeated, rank, seen) from the sorted
-//                  pairs in LDS: one launch for rows of up to 4096 positions.
-//   k_merge_pass   longer rows: merge passes over the sorted tiles (every element finds its output slot by a binary
-//                  search in the partner run), ping-ponging in the workspace.
-//   k_ngram_finish longer rows: the outputs from the merged pairs.
+//   k_ngram_rows   one workgroup per tile of a (b, j) row (a row of up to 1024 positions, or a tile of 4096 of a
+//                  longer row): the keys of its positions, a sort of the tile in LDS (4 pairs per thread sorted in
+//                  registers, then merge levels of doubling runs in which every thread finds its 4 output slots'
+//                  split point by a merge-path search and merges them), and, when the tile is the whole row, the
+//                  outputs (order, repeated, rank, seen) from the sorted pairs in LDS: one launch.
+//   k_ngram_chunk  rows of 1025 to 4096 positions: a workgroup of 1024 threads per chunk of 1024 (so a row spreads
+//                  over up to 4 CUs) computes the chunk's keys and sorts its pairs in LDS, one pair per thread: at
+//                  each of the 10 merge levels a pair's new index is its index in its run plus the count of the
+//                  partner run's codes below its own (the right run's pairs count the left run's codes up to their
+//                  own, so ties keep text order), a fixed-length search in LDS.
+//   k_ngram_place  then every sorted pair finds its place in the row: with the row's sorted chunk codes in LDS,
+//                  searches count, in each chunk, the codes below its own and up to its own; earlier chunks' equal
+//                  codes go first (they hold earlier positions), so its sorted index is its index in its chunk plus
+//                  those counts, and it repeats its predecessor exactly when codes equal to its own precede it.
+//   k_merge_pass   rows longer than 4096: merge passes over the sorted tiles (every element finds its output slot by
+//                  a binary search in the partner run), ping-ponging in the workspace.
+//   k_ngram_finish those rows: the outputs from the merged pairs.
 #include "common.h"
 
 namespace asrn {
 
 constexpr int kRowTile = 4096;                   // pairs sorted per workgroup
 constexpr int kRowThreads = kRowTile / 4;
+constexpr int kChunk = 1024;                     // the chunks of rows of kChunk < L <= kRowTile (k_ngram_place)
+constexpr int kPlaceChunks = kRowTile / kChunk;
+constexpr int kPlaceThreads = kChunk;
 constexpr uint64_t kNanCode = ~0ull;
 
 __device__ __forceinline__ uint64_t key_code(double x) {
@@ -36,6 +48,7 @@ __device__ __forceinline__ bool pair_less(uint64_t ka, uint32_t ia, uint64_t kb,
 struct NgramDims {
   int64_t B, L, Lp;
   int n, tile;
+  bool place;                                    // chunks of kChunk placed by k_ngram_place
 };
 
 // the n-gram key of length j + 1 ending at t: sum over i <= j of sig[t - i] * coef[i], each product and sum rounded
@@ -224,7 +237,140 @@ __global__ void k_ngram_finish(const uint64_t* __restrict__ code, const uint32_t
   }
 }
 
-// tile: a power of two, 4 <= tile <= kRowTile; Lp: the row padded to a power-of-two number of tiles
+// For each of the kPlaceChunks sorted runs of kChunk codes at s + q kChunk: lb[q] = its codes below x, ub[q] = up to
+// x. Branch-free lower bounds with a fixed trip count (the interval halves whatever the data): the lanes never
+// diverge and every step's 2 kPlaceChunks LDS reads are in flight together.
+__device__ __forceinline__ void count_below_all(const uint64_t* s, uint64_t x, int (&lb)[kPlaceChunks],
+                                                int (&ub)[kPlaceChunks]) {
+#pragma unroll
+  for (int q = 0; q < kPlaceChunks; ++q) lb[q] = ub[q] = q * kChunk;
+#pragma unroll
+  for (int len = kChunk; len > 1; len -= len >> 1) {
+    const int h = len >> 1;
+    uint64_t vl[kPlaceChunks], vu[kPlaceChunks];
+#pragma unroll
+    for (int q = 0; q < kPlaceChunks; ++q) {
+      vl[q] = s[lb[q] + h];
+      vu[q] = s[ub[q] + h];
+    }
+#pragma unroll
+    for (int q = 0; q < kPlaceChunks; ++q) {
+      lb[q] += vl[q] < x ? h : 0;
+      ub[q] += vu[q] <= x ? h : 0;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kPlaceChunks; ++q) {
+    lb[q] += (s[lb[q]] < x ? 1 : 0) - q * kChunk;
+    ub[q] += (s[ub[q]] <= x ? 1 : 0) - q * kChunk;
+  }
+}
+
+// Grid xcd_grid(B * n, chunks), kPlaceThreads threads: thread e starts with position t0 + e of the chunk and follows
+// that pair through the merge levels; the sorted chunk goes to code_out / idx_out at row * Lp + t0. (k_ngram_place,
+// on the same map, finds a row's sorted chunks in its XCD's L2.)
+__global__ __launch_bounds__(kPlaceThreads) void k_ngram_chunk(const float* __restrict__ sig,
+                                                               const double* __restrict__ coef, NgramDims g,
+                                                               double* __restrict__ keys,
+                                                               uint64_t* __restrict__ code_out,
+                                                               uint32_t* __restrict__ idx_out, int chunks) {
+  __shared__ uint64_t ck[2][kChunk];
+  const int e0 = threadIdx.x;
+  int c;
+  int64_t row;
+  xcd_chunk_row(chunks, &c, &row);
+  if (row >= g.B * g.n) return;
+  const int64_t b = row / g.n;
+  const int j = (int)(row % g.n);
+  const int64_t t0 = (int64_t)c * kChunk, t = t0 + e0;
+  uint64_t k = kNanCode;                           // padding past the row: after every real pair, in order
+  if (t < g.L) {
+    const double key = ngram_key(sig + b * g.L, coef, t, j);
+    keys[(b * g.L + t) * g.n + j] = key;
+    k = key_code(key);
+  }
+  int e = e0;                                      // the pair's index in the chunk: sorted runs of w after level w
+  int cur = 0;
+  ck[0][e] = k;
+  __syncthreads();
+  for (int w = 1; w < kChunk; w <<= 1) {
+    const bool left = (e & w) == 0;                // run A (earlier positions) or B of the pair of runs
+    const uint64_t* part = ck[cur] + ((e ^ w) & ~(w - 1));   // the partner run
+    // count of the partner's codes below k (A) or up to k (B): branch-free lower bound, log2 w + 1 reads
+    int base = 0;
+    for (int len = w; len > 1; len -= len >> 1) {
+      const uint64_t v = part[base + (len >> 1)];
+      base += (left ? v < k : v <= k) ? (len >> 1) : 0;
+    }
+    const uint64_t v = part[base];
+    base += (left ? v < k : v <= k) ? 1 : 0;
+    e = (e & ~(2 * w - 1)) + (e & (w - 1)) + base;
+    ck[cur ^ 1][e] = k;
+    __syncthreads();
+    cur ^= 1;
+  }
+  // thread e0's pair ends at sorted index e; the pairs are unique, so the chunk's sorted codes and positions are
+  // written from their owners (positions) and from LDS (codes, coalesced)
+  code_out[row * g.Lp + t0 + e0] = ck[cur][e0];
+  idx_out[row * g.Lp + t0 + e] = (uint32_t)t;
+}
+
+// Grid xcd_grid(B * n, chunks), kPlaceThreads threads; the row's chunks sorted by k_ngram_chunk into code / idx (row
+// at row * Lp). Thread e takes sorted pair e of chunk c.
+__global__ __launch_bounds__(kPlaceThreads) void k_ngram_place(const uint64_t* __restrict__ code,
+                                                               const uint32_t* __restrict__ idx, NgramDims g,
+                                                               int chunks, int32_t* __restrict__ order,
+                                                               uint8_t* __restrict__ repeated,
+                                                               int32_t* __restrict__ rank_k,
+                                                               float* __restrict__ vistos) {
+  __shared__ uint64_t ks[kPlaceChunks * kChunk];  // the row's sorted chunk codes
+  __shared__ uint16_t by_pos[kChunk];             // sorted index | repeated << 15 per position of the chunk
+  const int tid = threadIdx.x;
+  int c;
+  int64_t row;
+  xcd_chunk_row(chunks, &c, &row);
+  if (row >= g.B * g.n) return;
+  const int64_t b = row / g.n;
+  const int j = (int)(row % g.n);
+  const uint64_t* rc = code + row * g.Lp;
+#pragma unroll
+  for (int q = 0; q < kPlaceChunks; ++q) ks[q * kChunk + tid] = q < chunks ? rc[q * kChunk + tid] : kNanCode;
+  const uint32_t t = idx[row * g.Lp + (int64_t)c * kChunk + tid];
+  __syncthreads();
+  const int nc = (int)(g.L - (int64_t)c * kChunk < kChunk ? g.L - (int64_t)c * kChunk : kChunk);
+  const bool real = tid < nc;                     // not padding (sorted after the chunk's real pairs)
+  const uint64_t x = ks[c * kChunk + tid];
+  // per chunk q: lb = its codes below x, ub = up to x. Padding and the slots past the row's chunks hold the NaN
+  // code, which is never below x; ub is used only of the full chunks before this one. Unconditional, so that the
+  // 2 kPlaceChunks searches share one unrolled loop and their LDS reads overlap.
+  int lb[kPlaceChunks], ub[kPlaceChunks];
+  count_below_all(ks, x, lb, ub);
+  int i = tid, start = 0;
+#pragma unroll
+  for (int q = 0; q < kPlaceChunks; ++q) {
+    start += lb[q];
+    i += q < c ? ub[q] : (q > c ? lb[q] : 0);
+  }
+  const bool rep = x != kNanCode && i > start;
+  const int64_t p = (int64_t)t - (int64_t)c * kChunk;   // in [0, nc) for a correct sort
+  if (real) {
+    order[row * g.L + i] = (int32_t)t;
+    repeated[row * g.L + i] = rep ? 1 : 0;
+    if (p >= 0 && p < nc) by_pos[p] = (uint16_t)(i | (rep ? 0x8000 : 0));
+  }
+  __syncthreads();
+  // rank and seen in position order
+  if (real) {
+    const uint32_t y = by_pos[tid];
+    const int64_t tt = (int64_t)c * kChunk + tid;
+    rank_k[row * g.L + tt] = (int32_t)(y & 0x7FFFu);
+    vistos[(b * g.L + tt) * g.n + j] = (y & 0x8000u) ? 1.f : 0.f;
+  }
+}
+
+// Rows of up to kChunk: one tile, a power of two >= L (at least 4). Rows of kChunk < L <= kRowTile: tiles of kChunk,
+// Lp = the chunks' span (place). Longer rows: tiles of kRowTile, Lp = the row padded to a power-of-two number of
+// tiles (merge passes).
 static void ngram_dims(int64_t B, int64_t L, int n, NgramDims* g) {
   int tile = 4;
   while (tile < L && tile < kRowTile) tile <<= 1;
@@ -235,6 +381,11 @@ static void ngram_dims(int64_t B, int64_t L, int n, NgramDims* g) {
   g->n = n;
   g->tile = tile;
   g->Lp = tiles * tile;
+  g->place = L > kChunk && L <= kRowTile;
+  if (g->place) {
+    g->tile = kChunk;
+    g->Lp = (L + kChunk - 1) / kChunk * kChunk;
+  }
 }
 
 }  // namespace asrn
@@ -265,8 +416,16 @@ extern "C" int asrn_ngram_sort(const float* sig, const double* coef, int64_t B, 
   uint32_t* idx0 = (uint32_t*)(code1 + elems);
   uint32_t* idx1 = idx0 + elems;
   hipStream_t st = (hipStream_t)stream;
+  if (g.place) {
+    const int chunks = (int)(g.Lp / kChunk);
+    hipLaunchKernelGGL(k_ngram_chunk, dim3(xcd_grid(rows, chunks)), dim3(kPlaceThreads), 0, st, sig, coef, g, keys,
+                       code0, idx0, chunks);
+    if (check_launch("asrn_ngram_sort/chunks")) return 1;
+    hipLaunchKernelGGL(k_ngram_place, dim3(xcd_grid(rows, chunks)), dim3(kPlaceThreads), 0, st, code0,
+                       idx0, g, chunks, order, repeated, rank_k, vistos);
+    return check_launch("asrn_ngram_sort/place");
+  }
   const bool whole = g.Lp == g.tile;
-
   hipLaunchKernelGGL(k_ngram_rows, dim3((unsigned)(g.Lp / g.tile), (unsigned)rows), dim3(g.tile / 4), 0, st, sig,
                      coef, g, whole, keys, order, repeated, rank_k, vistos, code0, idx0);
   if (check_launch("asrn_ngram_sort/rows")) return 1;

@@ -60,8 +60,10 @@ def bucket_sort(phi, T, nb, C):
     buf = torch.empty((4, B * T * L), dtype=I32, device=dev)
     order, ids_s = buf[0].view(B * T, L), buf[1].view(B * T, L)
     rank, win = buf[2].view(B, L, T), buf[3].view(B, L, T)
+    wsb = query('asrn_bucket_sort_workspace', B, L, T)
+    ws = torch.empty((wsb,), dtype=torch.uint8, device=dev) if wsb else None
     call('asrn_bucket_sort', ptr(phi), B, L, T, nb, P, C, ptr(ids), ptr(order), ptr(ids_s), ptr(rank), ptr(win),
-         stream_of(dev))
+         ptr(ws), wsb, stream_of(dev))
     return ids, order, ids_s, rank, win
 
 

@@ -37,9 +37,12 @@ int32_t asrn_hip_abi_version(void);
  *   win        (B, L, T) int32 out: the recent-mates index, min(C, earlier positions in the bucket) |
  *              min(C, later positions in the bucket) << 8: the query window is the last `win & 255` sorted ranks
  *              before `rank`, the key window the first `win >> 8` after it
+ *   workspace  asrn_bucket_sort_workspace(B, L, T) bytes (0, and workspace may be null, unless 1024 < L <= 4096)
  * Requires 1 <= nb <= 14, 1 <= C <= 255. */
+int64_t asrn_bucket_sort_workspace(int64_t B, int64_t L, int32_t T);
 int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t T, int32_t nb, int64_t phi_stride, int32_t C,
-                     int32_t* ids, int32_t* order, int32_t* ids_sorted, int32_t* rank, int32_t* win, void* stream);
+                     int32_t* ids, int32_t* order, int32_t* ids_sorted, int32_t* rank, int32_t* win, void* workspace,
+                     int64_t workspace_bytes, void* stream);
 
 /* ---- a3 - a7: candidate attention, forward ---------------------------------------------------------------------
  * Replaces _CasillerosTriton.forward / _casilleros_ida in ESTABLE mode (asrn/nucleo.py:359-382, 465-488) as called

@@ -37,7 +37,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
         assert hasattr(lib, n), n
         assert n in _lib.SIGNATURES, f'{n} declared in the header but not bound in _lib.SIGNATURES'
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.asrn_hip_abi_version() == 1
+    assert lib.asrn_hip_abi_version() == 2
 
 
 def _err(lib):
@@ -47,16 +47,21 @@ def _err(lib):
 def test_argument_checks_fail_before_any_device_work(lib):
     N = None
     # n_bits outside [1, 14]
-    assert lib.asrn_bucket_sort(N, 2, 16, 8, 15, 120, 32, N, N, N, N, N, N) != 0
+    assert lib.asrn_bucket_sort(N, 2, 16, 8, 15, 120, 32, N, N, N, N, N, N, 0, N) != 0
     assert 'n_bits' in _err(lib)
     # phi row stride shorter than T*nb
-    assert lib.asrn_bucket_sort(N, 2, 16, 8, 14, 100, 32, N, N, N, N, N, N) != 0
+    assert lib.asrn_bucket_sort(N, 2, 16, 8, 14, 100, 32, N, N, N, N, N, N, 0, N) != 0
     assert 'stride' in _err(lib)
     # window clamp outside [1, 255]
-    assert lib.asrn_bucket_sort(N, 2, 16, 8, 14, 112, 300, N, N, N, N, N, N) != 0
+    assert lib.asrn_bucket_sort(N, 2, 16, 8, 14, 112, 300, N, N, N, N, N, N, 0, N) != 0
     assert 'window' in _err(lib)
     # empty inputs are a no-op
-    assert lib.asrn_bucket_sort(N, 0, 16, 8, 14, 112, 32, N, N, N, N, N, N) == 0
+    assert lib.asrn_bucket_sort(N, 0, 16, 8, 14, 112, 32, N, N, N, N, N, N, 0, N) == 0
+    # rows of 1025 to 4096 positions need the chunks' workspace: 4 chunks of 1024 int32 per (batch row, table)
+    assert lib.asrn_bucket_sort_workspace(2, 1024, 8) == 0 and lib.asrn_bucket_sort_workspace(2, 8192, 8) == 0
+    assert lib.asrn_bucket_sort_workspace(2, 3000, 8) == 2 * 8 * 3 * 1024 * 4
+    assert lib.asrn_bucket_sort(1, 2, 3000, 8, 14, 112, 32, 1, 1, 1, 1, 1, N, 100, N) != 0
+    assert 'workspace' in _err(lib)
     args = [N] * 12 + [2, 16]
     # d not a multiple of 4
     assert lib.asrn_candidates_fwd(*args, 6, 112, 16, 4, 8, 4, 32, 0.1, 0.25, 6, 0, 16, 0, N, N, N, N, N) != 0
