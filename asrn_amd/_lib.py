@@ -43,7 +43,8 @@ SIGNATURES = {
     'asrn_streak_bwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P, _I64, _P]),
     'asrn_context_fwd': (ctypes.c_int, [_P] * 5 + [_I64, _I32] + [_F32] * 3 + [_P] * 5),
     'asrn_context_bwd_workspace': (_I64, [_I64, _I32]),
-    'asrn_context_bwd': (ctypes.c_int, [_P] * 5 + [_I64, _I32] + [_F32] * 2 + [_P] * 7 + [_I64, _P]),
+    'asrn_context_bwd': (ctypes.c_int, [_P] * 5 + [_I64, _I32] + [_F32] * 2 + [_P] * 2 + [_I64, _I32] + [_P] * 7
+                         + [_I64, _P]),
     'asrn_hidden_fwd': (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I64, _I32, _I32, _P, _P]),
     'asrn_hidden_bwd': (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I64, _I32, _I32, _P, _P, _I64, _P]),
     'asrn_hash_fwd': (ctypes.c_int, [_P, _I64] + [_P] * 6 + [_I64, _I64] + [_I32] * 4 + [_P, _P]),

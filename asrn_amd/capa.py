@@ -199,11 +199,16 @@ class CapaASRNEstable(nn.Module):
         p = self.protecciones
         meta = (float(self.ln_ctx.eps), -1.0 if p.beta_max is None else float(p.beta_max),
                 -math.inf if p.log_alfa_min is None else float(p.log_alfa_min))
-        hh32, beta, log_alfa, h_puerta = ops.Context.apply(h, self.ln_ctx.weight, self.ln_ctx.bias, self.w_reloj,
-                                                           self.b_reloj, meta)
         cf = self.confirmar
         Wq = torch.cat([self.cq.weight, self.ck.weight]) if pesos is None else pesos['Wq']
-        y = lineal(_a_autocast(hh32), Wq)
+        if not torch.is_autocast_enabled(h.device.type) and h.shape[-1] <= 512 and 2 * cf <= 64:
+            # fp32: the projection's input gradient formed inside the context backward (no GEMM, no dhh buffer)
+            y, beta, log_alfa, h_puerta = ops.ContextProj.apply(h, self.ln_ctx.weight, self.ln_ctx.bias,
+                                                                self.w_reloj, self.b_reloj, Wq, meta)
+        else:
+            hh32, beta, log_alfa, h_puerta = ops.Context.apply(h, self.ln_ctx.weight, self.ln_ctx.bias,
+                                                               self.w_reloj, self.b_reloj, meta)
+            y = lineal(_a_autocast(hh32), Wq)
         Qc, Kc = _Split2.apply(y, cf)
         return (Qc, Kc, beta, log_alfa, h_puerta) if con_h else (Qc, Kc, beta, log_alfa)
 

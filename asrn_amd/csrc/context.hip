@@ -5,7 +5,9 @@
 //   u_k = hh . w_reloj[k] + b_reloj[k]           (k = 0, 1; fp32, as the reference's IEEE branch)
 //   beta = min(softplus(u_0), beta_max) -> fp64, log_alfa = max(logsigmoid(u_1) + log 2, log_alfa_min)
 // hh feeds the Qc/Kc GEMM (hipBLASLt). Kept per token for the backward: (mean, rstd, u_0, u_1).
-// Backward, from dhh (the Qc/Kc GEMM's input gradient), dbeta and dlog_alfa:
+// Backward, from dhh (the Qc/Kc GEMM's input gradient) or from that GEMM's output gradient dy (ny per token) and its
+// weight Wq (ny, d), as dhh = dy Wq formed here (each wave first forms its tokens' rows: one Wq load per output column
+// serves all of them), and from dbeta and dlog_alfa:
 //   du_0 = dbeta softplus'(u_0) [softplus(u_0) <= beta_max],  du_1 = dlog_alfa sigmoid(-u_1) [not clamped below]
 //   g = dhh + du_0 w_reloj[0] + du_1 w_reloj[1],  dxhat = g ln_w
 //   dh = rstd (dxhat - mean(dxhat) - xhat mean(dxhat xhat)) [+ dh_add: h's gradient through the layer's other use]
@@ -32,6 +34,7 @@ struct CtxArgs {
   float* hh; float4* stats; double* beta; float* la;                      // forward
   const float* dhh; const double* dbeta; const float* dla; float* dh; float* partial;   // backward
   const float* dh_add;   // backward, optional: a gradient of h from elsewhere, added to dh
+  const float* dy; int64_t ldy; int ny; const float* wq;   // backward, instead of dhh: dhh = dy Wq
 };
 
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
@@ -103,7 +106,9 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_fwd(CtxArgs a) {
   }
 }
 
-template <int D4>
+// PROJ: dhh = dy Wq for the wave's kCtxTokPerWave tokens, formed before the loop (one Wq row load per output column
+// for all of them, each token's dy value broadcast from the lane that loaded it; in output column order)
+template <int D4, bool PROJ>
 __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
   __shared__ float red[kCtxWaves][4 * 4 * D4 * kWave + 2];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
@@ -114,7 +119,36 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
 #pragma unroll
   for (int k = 0; k < D4; ++k) gw[k] = gb[k] = gr0[k] = gr1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
   float gbr0 = 0.f, gbr1 = 0.f;
+  float4 pj[PROJ ? kCtxTokPerWave : 1][D4];
+  if constexpr (PROJ) {
+    float dyv[kCtxTokPerWave];
+#pragma unroll
+    for (int u = 0; u < kCtxTokPerWave; ++u) {
+      const int64_t t = tw + u;
+      dyv[u] = (t < a.BL && lane < a.ny) ? a.dy[t * a.ldy + lane] : 0.f;
+#pragma unroll
+      for (int k = 0; k < D4; ++k) pj[u][k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    for (int o = 0; o < a.ny; ++o) {
+      float4 w[D4];
+#pragma unroll
+      for (int k = 0; k < D4; ++k) {
+        const int q = lane + kWave * k;
+        w[k] = q < d4 ? ((const float4*)(a.wq + (int64_t)o * a.d))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < kCtxTokPerWave; ++u) {
+        const float c = readlane_f(dyv[u], o);
+#pragma unroll
+        for (int k = 0; k < D4; ++k) {
+          pj[u][k].x += c * w[k].x; pj[u][k].y += c * w[k].y; pj[u][k].z += c * w[k].z; pj[u][k].w += c * w[k].w;
+        }
+      }
+    }
+  }
   constexpr int BB = kCtxBatch;                  // tokens whose rows are loaded together
+  constexpr int kUnroll = PROJ ? kCtxTokPerWave / BB : 1;   // PROJ: pj's indices must be constants
+#pragma unroll kUnroll
   for (int b = 0; b < kCtxTokPerWave; b += BB) {
     float4 hv[BB][D4], gv[BB][D4], av[BB][D4];
     float4 st[BB];
@@ -131,7 +165,8 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
         const int q = lane + kWave * k;
         if (ok && q < d4) {
           hv[u][k] = ((const float4*)(a.h + t * a.d))[q];
-          gv[u][k] = ((const float4*)(a.dhh + t * a.d))[q];
+          if constexpr (PROJ) gv[u][k] = pj[b + u][k];
+          else gv[u][k] = ((const float4*)(a.dhh + t * a.d))[q];
           av[u][k] = a.dh_add ? ((const float4*)(a.dh_add + t * a.d))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
       }
@@ -283,23 +318,35 @@ extern "C" int64_t asrn_context_bwd_workspace(int64_t BL, int32_t d) {
 
 extern "C" int asrn_context_bwd(const float* h, const float* ln_w, const float* ln_b, const float* w_reloj,
                                 const float* stats, int64_t BL, int32_t d, float beta_max, float log_alfa_min,
-                                const float* dhh, const double* dbeta, const float* dlog_alfa, const float* dh_add,
-                                float* dh, float* dparams, void* workspace, int64_t workspace_bytes, void* stream) {
+                                const float* dhh, const float* dy, int64_t ldy, int32_t ny, const float* wq,
+                                const double* dbeta, const float* dlog_alfa, const float* dh_add, float* dh,
+                                float* dparams, void* workspace, int64_t workspace_bytes, void* stream) {
   CtxArgs a{};
   a.h = h; a.lnw = ln_w; a.lnb = ln_b; a.wr = w_reloj; a.BL = BL; a.d = d; a.eps = 1.f; a.beta_max = beta_max;
   a.la_min = log_alfa_min; a.stats = (float4*)stats; a.dhh = dhh; a.dbeta = dbeta; a.dla = dlog_alfa; a.dh = dh;
   a.dh_add = dh_add; a.partial = (float*)workspace;
+  a.dy = dy; a.ldy = ldy; a.ny = ny; a.wq = wq;
   if (ctx_check(a, "asrn_context_bwd")) return 1;
+  ASRN_REQUIRE((dhh == nullptr) != (dy == nullptr), "asrn_context_bwd: give exactly one of dhh and dy");
+  ASRN_REQUIRE(dy == nullptr || (wq != nullptr && ny >= 1 && ny <= kWave && ldy >= ny && d <= 2 * 4 * kWave),
+               "asrn_context_bwd: dy needs Wq, 1 <= ny=%d <= %d, ldy=%lld >= ny and d=%d <= %d", ny, kWave,
+               (long long)ldy, d, 2 * 4 * kWave);
   ASRN_REQUIRE(workspace != nullptr && workspace_bytes >= asrn_context_bwd_workspace(BL, d),
                "asrn_context_bwd: workspace too small");
   const int groups = (int)ctx_groups(BL);
   const int cols = 4 * d + 2;
   hipStream_t st = (hipStream_t)stream;
-  switch ((d + 4 * kWave - 1) / (4 * kWave)) {
-    case 1: hipLaunchKernelGGL(k_ctx_bwd<1>, dim3(groups), dim3(kCtxThreads), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(k_ctx_bwd<2>, dim3(groups), dim3(kCtxThreads), 0, st, a); break;
-    case 3: hipLaunchKernelGGL(k_ctx_bwd<3>, dim3(groups), dim3(kCtxThreads), 0, st, a); break;
-    default: hipLaunchKernelGGL(k_ctx_bwd<4>, dim3(groups), dim3(kCtxThreads), 0, st, a); break;
+  const int d4c = (d + 4 * kWave - 1) / (4 * kWave);
+  if (dy) {
+    if (d4c == 1) hipLaunchKernelGGL((k_ctx_bwd<1, true>), dim3(groups), dim3(kCtxThreads), 0, st, a);
+    else hipLaunchKernelGGL((k_ctx_bwd<2, true>), dim3(groups), dim3(kCtxThreads), 0, st, a);
+  } else {
+    switch (d4c) {
+      case 1: hipLaunchKernelGGL((k_ctx_bwd<1, false>), dim3(groups), dim3(kCtxThreads), 0, st, a); break;
+      case 2: hipLaunchKernelGGL((k_ctx_bwd<2, false>), dim3(groups), dim3(kCtxThreads), 0, st, a); break;
+      case 3: hipLaunchKernelGGL((k_ctx_bwd<3, false>), dim3(groups), dim3(kCtxThreads), 0, st, a); break;
+      default: hipLaunchKernelGGL((k_ctx_bwd<4, false>), dim3(groups), dim3(kCtxThreads), 0, st, a); break;
+    }
   }
   if (check_launch("asrn_context_bwd")) return 1;
   hipLaunchKernelGGL(k_ctx_params, dim3(cols), dim3(kCtxThreads), 0, st, (const float*)workspace, groups, cols,

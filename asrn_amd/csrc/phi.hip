@@ -21,6 +21,7 @@ constexpr int kPhiThreads = 256;     // 4 waves: wave w owns tokens 16w .. 16w +
 constexpr int kPhiMax = 64;          // the most hidden units or outputs per MLP
 constexpr int kGld = 2 * kPhiMax + 1;   // LDS row stride of the g / dg tiles (odd: conflict-free column reads)
 constexpr int kWld = kPhiMax + 1;       // LDS row stride of a weight block or a dphi tile
+static_assert(kPhiThreads == 2 * (2 * kPhiMax), "k_phi_bwd: thread tid loads dphi column tid % 128, even or odd tokens");
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -196,7 +197,9 @@ __global__ __launch_bounds__(kPhiThreads) void k_phi_bwd(PhiArgs a) {
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) dWacc[part][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float4 bsum = make_float4(0.f, 0.f, 0.f, 0.f);  // first-layer biases: this thread's column group
-  float b2sum = 0.f;                              // second-layer biases: output column tid (tid < 128)
+  // second-layer biases: every dphi load of thread tid is output column tid % 128 (of [word | context]), at the
+  // tile's even tokens for tid < 128 and its odd ones above, so the thread sums them as it loads them
+  float b2sum = 0.f;
   for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int64_t t0 = tile * kPhiTok;
     constexpr int kDPer = kPhiTok * 2 * kPhiMax / kPhiThreads / 4;   // four rounds of 8 loads per thread
@@ -219,6 +222,7 @@ __global__ __launch_bounds__(kPhiThreads) void k_phi_bwd(PhiArgs a) {
         const int e = tid + (half * kDPer + x) * kPhiThreads;
         const int tk = e / (2 * kPhiMax), c = e - tk * 2 * kPhiMax;
         dps[tk * 2 * kWld + (c >= kPhiMax ? kWld + c - kPhiMax : c)] = v[x];
+        b2sum += v[x];
       }
     }
     __syncthreads();
@@ -325,13 +329,6 @@ __global__ __launch_bounds__(kPhiThreads) void k_phi_bwd(PhiArgs a) {
           }
       }
     }
-    // db2: output column tid's sum over the tile's tokens, in order
-    if (tid < 2 * kPhiMax) {
-      const float* col = dps + (tid >= kPhiMax ? kWld + tid - kPhiMax : tid);
-      float s = 0.f;
-      for (int tk = 0; tk < kPhiTok; ++tk) s += col[tk * 2 * kWld];
-      b2sum += s;
-    }
     __syncthreads();                              // the next tile overwrites dps, dgs and gs
   }
   float* prow = a.part + (int64_t)blockIdx.x * (a.Pw * a.m + a.Pc * a.mc + a.Pw + a.Pc + h);
@@ -346,11 +343,14 @@ __global__ __launch_bounds__(kPhiThreads) void k_phi_bwd(PhiArgs a) {
     }
   }
   float* pb = prow + a.Pw * a.m + a.Pc * a.mc;
-  if (tid < 2 * kPhiMax) {
+  red[tid] = b2sum;
+  __syncthreads();
+  if (tid < 2 * kPhiMax) {                         // even tokens' sum + odd tokens' sum
     const bool ctx = tid >= kPhiMax;
     const int c = ctx ? tid - kPhiMax : tid;
-    if (c < (ctx ? a.Pc : a.Pw)) pb[(ctx ? a.Pw : 0) + c] = b2sum;
+    if (c < (ctx ? a.Pc : a.Pw)) pb[(ctx ? a.Pw : 0) + c] = red[tid] + red[tid + 2 * kPhiMax];
   }
+  __syncthreads();
   // first-layer biases: threads with the same column group (tid mod h4) combine in order of tid
   float* pdb = pb + a.Pw + a.Pc;
   for (int comp = 0; comp < 4; ++comp) {

@@ -9,6 +9,7 @@ import ctypes
 import math
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib
 from ._lib import call, ptr, query, stream_of
@@ -107,6 +108,44 @@ def ngram_sort(sig, coef, n):
 # a0 (the context producer's LayerNorm and clock projection)
 # ---------------------------------------------------------------------------------------------------------------------
 
+def _context_fwd(h, ln_w, ln_b, w_reloj, b_reloj, meta):
+    """asrn_context_fwd: (h32 (BL, d), the fp32 parameters, hh, stats, beta, la)."""
+    eps, beta_max, la_min = meta
+    dev = _dev(h)
+    d = h.shape[-1]
+    h32 = _c(h, torch.float32).reshape(-1, d)
+    BL = h32.shape[0]
+    params = [_c(p, torch.float32) for p in (ln_w, ln_b, w_reloj, b_reloj)]
+    hh = torch.empty_like(h32)
+    stats = torch.empty((BL, 4), dtype=torch.float32, device=dev)
+    beta = torch.empty((BL,), dtype=torch.float64, device=dev)
+    la = torch.empty((BL,), dtype=torch.float32, device=dev)
+    call('asrn_context_fwd', ptr(h32), *[ptr(p) for p in params], BL, d, eps, beta_max, la_min, ptr(hh),
+         ptr(stats), ptr(beta), ptr(la), stream_of(dev))
+    return h32, params, hh, stats, beta, la
+
+
+def _context_bwd(h32, lnw, lnb, wr, stats, beta_max, la_min, dhh, dy, wq, dbeta, dla, dh_add):
+    """asrn_context_bwd from dhh (BL, d) or from dy (BL, ny) and wq (ny, d): dh (BL, d) and the 4 d + 2 parameter
+    gradients [ln_w | ln_b | w_reloj | b_reloj]."""
+    BL, d = h32.shape
+    dev = h32.device
+    dbeta = (torch.zeros((BL,), dtype=torch.float64, device=dev) if dbeta is None
+             else _c(dbeta, torch.float64).reshape(BL))
+    dla = torch.zeros((BL,), dtype=torch.float32, device=dev) if dla is None else _c(dla, torch.float32).reshape(BL)
+    if dh_add is not None:
+        dh_add = _c(dh_add, torch.float32).reshape(BL, d)
+    dh = torch.empty_like(h32)
+    dp = torch.empty((4 * d + 2,), dtype=torch.float32, device=dev)
+    wsb = query('asrn_context_bwd_workspace', BL, d)
+    ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+    ny = 0 if dy is None else dy.shape[1]
+    call('asrn_context_bwd', ptr(h32), ptr(lnw), ptr(lnb), ptr(wr), ptr(stats), BL, d, beta_max, la_min,
+         ptr(dhh), ptr(dy), max(ny, 1), ny, ptr(wq), ptr(dbeta), ptr(dla), ptr(dh_add), ptr(dh), ptr(dp), ptr(ws),
+         wsb, stream_of(dev))
+    return dh, dp
+
+
 class Context(torch.autograd.Function):
     """hh = LayerNorm(h), beta = min(softplus(u_0), beta_max) fp64, log_alfa = max(logsigmoid(u_1) + log 2, min) with
     u = w_reloj hh + b_reloj in fp32 (asrn/estable.py:153-194), fused in asrn_context_fwd/bwd. hh feeds the Qc/Kc GEMM.
@@ -116,19 +155,9 @@ class Context(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, h, ln_w, ln_b, w_reloj, b_reloj, meta):
-        eps, beta_max, la_min = meta
-        dev = _dev(h)
-        d = h.shape[-1]
-        lead = h.shape[:-1]
-        h32 = _c(h, torch.float32).reshape(-1, d)
-        BL = h32.shape[0]
-        params = [_c(p, torch.float32) for p in (ln_w, ln_b, w_reloj, b_reloj)]
-        hh = torch.empty_like(h32)
-        stats = torch.empty((BL, 4), dtype=torch.float32, device=dev)
-        beta = torch.empty((BL,), dtype=torch.float64, device=dev)
-        la = torch.empty((BL,), dtype=torch.float32, device=dev)
-        call('asrn_context_fwd', ptr(h32), *[ptr(p) for p in params], BL, d, eps, beta_max, la_min, ptr(hh),
-             ptr(stats), ptr(beta), ptr(la), stream_of(dev))
+        _, beta_max, la_min = meta
+        d, lead = h.shape[-1], h.shape[:-1]
+        h32, params, hh, stats, beta, la = _context_fwd(h, ln_w, ln_b, w_reloj, b_reloj, meta)
         ctx.save_for_backward(h32, *params[:3], stats)
         ctx.meta = (beta_max, la_min, h.dtype, lead, [p.shape for p in (ln_w, ln_b, w_reloj, b_reloj)])
         return hh.view(*lead, d), beta.view(lead), la.view(lead), h32.view(*lead, d)
@@ -138,22 +167,42 @@ class Context(torch.autograd.Function):
         h32, lnw, lnb, wr, stats = ctx.saved_tensors
         beta_max, la_min, hdt, lead, shapes = ctx.meta
         BL, d = h32.shape
-        dev = h32.device
         dhh = torch.zeros_like(h32) if dhh is None else _c(dhh, torch.float32).reshape(BL, d)
-        dbeta = (torch.zeros((BL,), dtype=torch.float64, device=dev) if dbeta is None
-                 else _c(dbeta, torch.float64).reshape(BL))
-        dla = torch.zeros((BL,), dtype=torch.float32, device=dev) if dla is None else _c(dla, torch.float32).reshape(BL)
-        if dh_add is not None:
-            dh_add = _c(dh_add, torch.float32).reshape(BL, d)
-        dh = torch.empty_like(h32)
-        dp = torch.empty((4 * d + 2,), dtype=torch.float32, device=dev)
-        wsb = query('asrn_context_bwd_workspace', BL, d)
-        ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
-        call('asrn_context_bwd', ptr(h32), ptr(lnw), ptr(lnb), ptr(wr), ptr(stats), BL, d, beta_max, la_min,
-             ptr(dhh), ptr(dbeta), ptr(dla), ptr(dh_add), ptr(dh), ptr(dp), ptr(ws), wsb, stream_of(dev))
-        sizes = [d, d, 2 * d, 2]
-        grads = [t.view(s) for t, s in zip(torch.split(dp, sizes), shapes)]
+        dh, dp = _context_bwd(h32, lnw, lnb, wr, stats, beta_max, la_min, dhh, None, None, dbeta, dla, dh_add)
+        grads = [t.view(s) for t, s in zip(torch.split(dp, [d, d, 2 * d, 2]), shapes)]
         return (dh.view(*lead, d).to(hdt), *grads, None)
+
+
+class ContextProj(torch.autograd.Function):
+    """Context followed by the Qc/Kc projection y = hh Wq^T, fp32 (asrn/estable.py:153-194): the first output is y
+    (.., ny) instead of hh. The backward forms the projection's input gradient dhh = dy Wq inside asrn_context_bwd
+    (no GEMM and no dhh buffer: dy is ny <= 64 values a token) and Wq's gradient dy^T hh by token slabs, as lineal
+    does. For fp32 layers with d <= 512."""
+
+    @staticmethod
+    def forward(ctx, h, ln_w, ln_b, w_reloj, b_reloj, Wq, meta):
+        _, beta_max, la_min = meta
+        d, lead = h.shape[-1], h.shape[:-1]
+        h32, params, hh, stats, beta, la = _context_fwd(h, ln_w, ln_b, w_reloj, b_reloj, meta)
+        wq = _c(Wq, torch.float32)
+        with torch.autocast(device_type=h.device.type, enabled=False):
+            y = F.linear(hh, wq)
+        ctx.save_for_backward(h32, *params[:3], stats, hh, wq)
+        ctx.meta = (beta_max, la_min, h.dtype, lead, [p.shape for p in (ln_w, ln_b, w_reloj, b_reloj)], Wq.dtype)
+        return y.view(*lead, wq.shape[0]), beta.view(lead), la.view(lead), h32.view(*lead, d)
+
+    @staticmethod
+    def backward(ctx, dy, dbeta, dla, dh_add):
+        h32, lnw, lnb, wr, stats, hh, wq = ctx.saved_tensors
+        beta_max, la_min, hdt, lead, shapes, wdt = ctx.meta
+        BL, d = h32.shape
+        ny = wq.shape[0]
+        dy = (torch.zeros((BL, ny), dtype=torch.float32, device=h32.device) if dy is None
+              else _c(dy, torch.float32).reshape(BL, ny))
+        dwq = weight_grad(dy, hh).to(wdt) if ctx.needs_input_grad[5] else None
+        dh, dp = _context_bwd(h32, lnw, lnb, wr, stats, beta_max, la_min, None, dy, wq, dbeta, dla, dh_add)
+        grads = [t.view(s) for t, s in zip(torch.split(dp, [d, d, 2 * d, 2]), shapes)]
+        return (dh.view(*lead, d).to(hdt), *grads, dwq, None)
 
 
 # ---------------------------------------------------------------------------------------------------------------------

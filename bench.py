@@ -58,10 +58,12 @@ def gate_bytes(d, n, a=4):
     return fwd, bwd
 
 
-def context_bytes(d):
+def context_bytes(d, cf=16, proj=True):
     """The fused LayerNorm + clock projection (asrn_context_fwd/bwd), fp32: h in, hh, (mean, rstd, u) and beta (fp64),
-    log_alfa out; the backward reads h, dhh, the gate's dh, the stats, dbeta, dlog_alfa and writes dh."""
-    return 4 * d + 4 * d + 16 + 8 + 4, 4 * d + 4 * d + 4 * d + 16 + 8 + 4 + 4 * d
+    log_alfa out; the backward reads h, the Qc/Kc gradient (proj: the 2 cf values of dy, from which it forms dhh;
+    else the GEMM's dhh), the gate's dh, the stats, dbeta, dlog_alfa and writes dh."""
+    dq = 4 * 2 * cf if proj else 4 * d
+    return 4 * d + 4 * d + 16 + 8 + 4, 4 * d + dq + 4 * d + 16 + 8 + 4 + 4 * d
 
 
 def hidden_bytes(m=64, mc=64):
@@ -83,22 +85,23 @@ def hip_bytes_per_token(d, P, cf, T, n=4, a=4, m=64, mc=64, K=4, fused=True):
     the hash MLPs (fused: hash_bytes; else the hidden layer and its bias column sums), and the column sums of the
     candidates' per-token partials (the weight gradients' slab sums scale with the weights, not the tokens, and are
     left out).
-    cfg2 fp32 (fused): 512 + 32 + 28 + 160 + 7,044 + 8,324 + 6,200 + 3,200 + 52 = 25,552."""
+    cfg2 fp32 (fused): 512 + 32 + 28 + 160 + 7,044 + 8,324 + 5,304 + 3,200 + 52 = 24,656."""
     cand = algorithmic_bytes(d, P, cf, T, a)
     colsums = 4 * (T + K + 1) + (0 if fused else 4 * (m + mc) + 4 * P)
     mlp = sum(hash_bytes(P, m, mc)) if fused else sum(hidden_bytes(m, mc))
     return (P * a + 8 * T + 32 + 28 + 160 + sum(cand.values()) + sum(gate_bytes(d, n, a))
-            + sum(context_bytes(d)) + mlp + colsums)
+            + sum(context_bytes(d, cf, proj=fused)) + mlp + colsums)
 
 
 def gemm_bytes_per_token(d, P, cf, a=4, m=64, mc=64, fused=True):
     """Operands and results of the layer's GEMMs per token, each read or written once (activations in a bytes;
     weights are per step, not per token): forward E -> [hp|za|zb], hh -> [Qc|Kc], sum -> W_o W_v sum and, unfused,
-    g -> phi; backward the input gradients (the E one accumulating into the candidates' dE) and the weight gradients
-    (both operands read). cfg2 fp32 (fused): 4,992 + 11,008 = 16,000."""
+    g -> phi; backward the input gradients (the E one accumulating into the candidates' dE; fused, the [Qc|Kc] one is
+    formed inside the context backward instead) and the weight gradients (both operands read).
+    cfg2 fp32 (fused): 4,992 + 9,856 = 14,848."""
     h, q = m + 2 * mc, 2 * cf
     fwd = (d + h) + (d + q) + (d + d) + (0 if fused else (m + mc) + P)
-    bwd = (d + d) + 2 * d + (q + d) + (q + d) + (h + 2 * d) + (h + d) + (0 if fused else 2 * (P + m + mc))
+    bwd = (d + d) + 2 * d + (0 if fused else (q + d)) + (q + d) + (h + 2 * d) + (h + d) + (0 if fused else 2 * (P + m + mc))
     return a * (fwd + bwd)
 
 

@@ -126,17 +126,21 @@ int64_t asrn_scan_workspace(int64_t rows, int64_t N);
  * u_k = hh . w_reloj[k] + b_reloj[k] (w_reloj (2, d)); beta = min(softplus(u_0), beta_max) (BL) fp64 out (beta_max < 0:
  * no clamp); log_alfa = max(logsigmoid(u_1) + log 2, log_alfa_min) (BL) fp32 out (-inf: no clamp); stats (BL, 4) =
  * (mean, rstd, u_0, u_1) kept for the backward. d % 4 == 0, d <= 1024.
- * context_bwd: from dhh (BL, d) (the Qc/Kc GEMM's input gradient), dbeta (BL) fp64 and dlog_alfa (BL) gives dh (BL, d)
- * (overwritten; plus dh_add (BL, d) when not null: the gradient of h through the gate) and dparams (4 d + 2) = the gradients of [ln_w | ln_b | w_reloj (2 d) | b_reloj (2)], summed over
- * tokens in a fixed order. workspace: asrn_context_bwd_workspace(BL, d) bytes. */
+ * context_bwd: from dhh (BL, d) (the Qc/Kc GEMM's input gradient), or instead from that GEMM's output gradient dy
+ * (BL rows of ny <= 64, row stride ldy) and its weight wq (ny, d) with d <= 512, as dhh = dy wq formed in the kernel
+ * (replacing the GEMM `grad @ weight` of the Linear's backward), and from dbeta (BL) fp64 and dlog_alfa (BL): gives
+ * dh (BL, d) (overwritten; plus dh_add (BL, d) when not null: the gradient of h through the gate) and dparams
+ * (4 d + 2) = the gradients of [ln_w | ln_b | w_reloj (2 d) | b_reloj (2)], summed over tokens in a fixed order.
+ * Exactly one of dhh and dy is given. workspace: asrn_context_bwd_workspace(BL, d) bytes. */
 int asrn_context_fwd(const float* h, const float* ln_w, const float* ln_b, const float* w_reloj, const float* b_reloj,
                      int64_t BL, int32_t d, float eps, float beta_max, float log_alfa_min, float* hh, float* stats,
                      double* beta, float* log_alfa, void* stream);
 int64_t asrn_context_bwd_workspace(int64_t BL, int32_t d);
 int asrn_context_bwd(const float* h, const float* ln_w, const float* ln_b, const float* w_reloj, const float* stats,
-                     int64_t BL, int32_t d, float beta_max, float log_alfa_min, const float* dhh, const double* dbeta,
-                     const float* dlog_alfa, const float* dh_add, float* dh, float* dparams, void* workspace,
-                     int64_t workspace_bytes, void* stream);
+                     int64_t BL, int32_t d, float beta_max, float log_alfa_min, const float* dhh, const float* dy,
+                     int64_t ldy, int32_t ny, const float* wq, const double* dbeta, const float* dlog_alfa,
+                     const float* dh_add, float* dh, float* dparams, void* workspace, int64_t workspace_bytes,
+                     void* stream);
 
 /* ---- a0 (part): the hash MLPs' hidden layer (asrn/nucleo.py:644-659) -------------------------------------------
  * Replaces the GELU of afin_palabra and afin_contexto between their two Linear layers, with the context MLP's first
