@@ -201,7 +201,7 @@ class CapaASRNEstable(nn.Module):
                 -math.inf if p.log_alfa_min is None else float(p.log_alfa_min))
         cf = self.confirmar
         Wq = torch.cat([self.cq.weight, self.ck.weight]) if pesos is None else pesos['Wq']
-        if not torch.is_autocast_enabled(h.device.type) and h.shape[-1] <= 512 and 2 * cf <= 64:
+        if not torch.is_autocast_enabled(h.device.type) and h.shape[-1] <= 512 and 2 * cf <= 32:
             # fp32: the projection's input gradient formed inside the context backward (no GEMM, no dhh buffer)
             y, beta, log_alfa, h_puerta = ops.ContextProj.apply(h, self.ln_ctx.weight, self.ln_ctx.bias,
                                                                 self.w_reloj, self.b_reloj, Wq, meta)

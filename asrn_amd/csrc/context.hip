@@ -106,11 +106,17 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_fwd(CtxArgs a) {
   }
 }
 
-// PROJ: dhh = dy Wq for the wave's kCtxTokPerWave tokens, formed before the loop (one Wq row load per output column
-// for all of them, each token's dy value broadcast from the lane that loaded it; in output column order)
+// PROJ: dhh = dy Wq for the wave's kCtxTokPerWave tokens, formed before the loop: Wq (ny <= 32 rows) staged in LDS
+// once per workgroup, one float4 of a row per lane and output column for all of the wave's tokens, each token's dy
+// value broadcast from the lane that loaded it; in output column order. The stage shares its LDS with the end's
+// partial rows.
+constexpr int kProjRows = 32;
 template <int D4, bool PROJ>
 __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
-  __shared__ float red[kCtxWaves][4 * 4 * D4 * kWave + 2];
+  constexpr int kRed = kCtxWaves * (4 * 4 * D4 * kWave + 2);
+  constexpr int kStage = PROJ ? kProjRows * 4 * D4 * kWave : 0;
+  __shared__ float lds[kRed > kStage ? kRed : kStage];
+  float (*red)[4 * 4 * D4 * kWave + 2] = reinterpret_cast<float (*)[4 * 4 * D4 * kWave + 2]>(lds);
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int d4 = a.d >> 2;
   const float inv_d = 1.f / (float)a.d;
@@ -121,6 +127,12 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
   float gbr0 = 0.f, gbr1 = 0.f;
   float4 pj[PROJ ? kCtxTokPerWave : 1][D4];
   if constexpr (PROJ) {
+    float4* wq4 = reinterpret_cast<float4*>(lds);  // row o, float4 q at wq4[o * D4 * kWave + q]
+    for (int i = threadIdx.x; i < a.ny * D4 * kWave; i += kCtxThreads) {
+      const int o = i / (D4 * kWave), q = i - o * (D4 * kWave);
+      wq4[i] = q < d4 ? ((const float4*)(a.wq + (int64_t)o * a.d))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __syncthreads();
     float dyv[kCtxTokPerWave];
 #pragma unroll
     for (int u = 0; u < kCtxTokPerWave; ++u) {
@@ -132,10 +144,7 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
     for (int o = 0; o < a.ny; ++o) {
       float4 w[D4];
 #pragma unroll
-      for (int k = 0; k < D4; ++k) {
-        const int q = lane + kWave * k;
-        w[k] = q < d4 ? ((const float4*)(a.wq + (int64_t)o * a.d))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      for (int k = 0; k < D4; ++k) w[k] = wq4[o * D4 * kWave + lane + kWave * k];
 #pragma unroll
       for (int u = 0; u < kCtxTokPerWave; ++u) {
         const float c = readlane_f(dyv[u], o);
@@ -225,6 +234,7 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
     }
   }
   // workgroup partial row: [d ln_w | d ln_b | d w_reloj[0] | d w_reloj[1] | d b_reloj (2)], the waves in order
+  if constexpr (PROJ) __syncthreads();           // every wave is past the stage before the partial rows reuse it
   float* mine = red[wave];
 #pragma unroll
   for (int k = 0; k < D4; ++k) {
@@ -328,8 +338,8 @@ extern "C" int asrn_context_bwd(const float* h, const float* ln_w, const float* 
   a.dy = dy; a.ldy = ldy; a.ny = ny; a.wq = wq;
   if (ctx_check(a, "asrn_context_bwd")) return 1;
   ASRN_REQUIRE((dhh == nullptr) != (dy == nullptr), "asrn_context_bwd: give exactly one of dhh and dy");
-  ASRN_REQUIRE(dy == nullptr || (wq != nullptr && ny >= 1 && ny <= kWave && ldy >= ny && d <= 2 * 4 * kWave),
-               "asrn_context_bwd: dy needs Wq, 1 <= ny=%d <= %d, ldy=%lld >= ny and d=%d <= %d", ny, kWave,
+  ASRN_REQUIRE(dy == nullptr || (wq != nullptr && ny >= 1 && ny <= kProjRows && ldy >= ny && d <= 2 * 4 * kWave),
+               "asrn_context_bwd: dy needs Wq, 1 <= ny=%d <= %d, ldy=%lld >= ny and d=%d <= %d", ny, kProjRows,
                (long long)ldy, d, 2 * 4 * kWave);
   ASRN_REQUIRE(workspace != nullptr && workspace_bytes >= asrn_context_bwd_workspace(BL, d),
                "asrn_context_bwd: workspace too small");

@@ -79,7 +79,7 @@ struct HidInN {
 };
 using HidIn = HidInN<kHidPer>;
 // groups first .. first + NG - 1 of this thread
-template <int NG>
+template <int NG, int TOK = kPhiTok>
 __device__ __forceinline__ void load_hidden(const PhiArgs& a, int64_t t0, int64_t N, int h4, HidInN<NG>& in,
                                             int first = 0) {
 #pragma unroll
@@ -87,7 +87,7 @@ __device__ __forceinline__ void load_hidden(const PhiArgs& a, int64_t t0, int64_
     const int e = threadIdx.x + (first + x) * kPhiThreads;
     const int tk = e / h4, j = (e - tk * h4) * 4;
     const int64_t row = t0 + tk;
-    const bool ok = tk < kPhiTok && row < N;
+    const bool ok = tk < TOK && row < N;
     const bool ctx = j >= a.m;
     const bool prev = ok && ctx && row % a.L > 0;
     const int64_t r0 = ok ? row : 0;
@@ -97,6 +97,28 @@ __device__ __forceinline__ void load_hidden(const PhiArgs& a, int64_t t0, int64_
     if (!prev) in.yb[x] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
 }
+// the backward's tile inputs: y and the previous token's zb only (a thread's groups all share one column group, whose
+// bias the kernel loads once)
+template <int NG>
+struct HidYN {
+  float4 ya[NG], yb[NG];
+};
+template <int NG, int TOK>
+__device__ __forceinline__ void load_hidden_y(const PhiArgs& a, int64_t t0, int64_t N, int h4, HidYN<NG>& in) {
+#pragma unroll
+  for (int x = 0; x < NG; ++x) {
+    const int e = threadIdx.x + x * kPhiThreads;
+    const int tk = e / h4, j = (e - tk * h4) * 4;
+    const int64_t row = t0 + tk;
+    const bool ok = tk < TOK && row < N;
+    const bool prev = ok && j >= a.m && row % a.L > 0;
+    const int64_t r0 = ok ? row : 0;
+    in.ya[x] = *reinterpret_cast<const float4*>(a.y + r0 * a.ldy + (ok ? j : 0));
+    in.yb[x] = *reinterpret_cast<const float4*>(a.y + (prev ? (r0 - 1) * a.ldy + a.mc + j : 0));
+    if (!prev) in.yb[x] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
 template <int NG>
 __device__ __forceinline__ float4 pre_of(const HidInN<NG>& in, int x) {
   return make_float4((in.ya[x].x + in.bb[x].x) + in.yb[x].x, (in.ya[x].y + in.bb[x].y) + in.yb[x].y,
@@ -174,18 +196,24 @@ __global__ __launch_bounds__(kPhiThreads) void k_phi_fwd(PhiArgs a) {
   }
 }
 
-// One workgroup per CU, looping over tiles of 64 tokens (blockIdx.x, + gridDim.x, ...): the weight blocks are staged
-// once, and the parameter gradients accumulate across the workgroup's tiles (the dW MFMA accumulators stay in
-// registers), so each workgroup writes one partial row.
-__global__ __launch_bounds__(kPhiThreads) void k_phi_bwd(PhiArgs a) {
+// The backward loops over tiles of kBwdTok = 32 tokens (blockIdx.x, + gridDim.x, ...) in workgroups of 67 KB of LDS,
+// two per CU, so that one workgroup's loads, MFMA and GELU phases overlap another's: the weight blocks are staged once,
+// dg turns into g in place, the tile's hidden inputs are loaded with its dphi (their latency under the dg products),
+// and the parameter gradients accumulate across the workgroup's tiles (the dW MFMA accumulators stay in registers), so
+// each workgroup writes one partial row.
+constexpr int kBwdTok = 32;
+constexpr int kBwdHid = kBwdTok * 2 * kPhiMax / 4 / kPhiThreads;     // hidden float4 groups per thread: 4
+constexpr int kBwdD = kBwdTok * 2 * kPhiMax / kPhiThreads;           // dphi loads per thread: 16
+static_assert(kBwdTok == 2 * 16, "k_phi_bwd: two 16-token MFMA row blocks per tile");
+
+__global__ __launch_bounds__(kPhiThreads, 2) void k_phi_bwd(PhiArgs a) {
   __shared__ float ws[2 * kPhiMax * kWld];        // the two weight blocks (outputs x hidden, zero-padded to 64 x 64)
-  __shared__ float dps[kPhiTok * 2 * kWld];       // the dphi tile: word at [0, kWld), context at [kWld, 2 kWld)
-  __shared__ float dgs[kPhiTok * kGld];           // dg, in the tile's token rows
-  __shared__ float gs[kPhiTok * kGld];            // g = gelu(x), in the tile's token rows
+  __shared__ float dps[kBwdTok * 2 * kWld];       // the dphi tile: word at [0, kWld), context at [kWld, 2 kWld)
+  __shared__ float gs[kBwdTok * kGld];            // dg, then g = gelu(x) in place, in the tile's token rows
   __shared__ float red[kPhiThreads];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, k4 = lane >> 4;
-  const int64_t N = a.B * a.L, ntiles = (N + kPhiTok - 1) / kPhiTok;
+  const int64_t N = a.B * a.L, ntiles = (N + kBwdTok - 1) / kBwdTok;
   const int h = a.m + a.mc, h4 = h / 4, P = a.Pw + a.Pc;
   float* wsw = ws;
   float* wsc = ws + kPhiMax * kWld;
@@ -197,94 +225,95 @@ __global__ __launch_bounds__(kPhiThreads) void k_phi_bwd(PhiArgs a) {
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) dWacc[part][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float4 bsum = make_float4(0.f, 0.f, 0.f, 0.f);  // first-layer biases: this thread's column group
+  // every hidden group of thread tid is column group tid % h4 (h4 divides 256): its first-layer bias
+  const int jb = (tid % h4) * 4;
+  const float4 bias = *reinterpret_cast<const float4*>(jb >= a.m ? a.bc + (jb - a.m) : a.bp + jb);
   // second-layer biases: every dphi load of thread tid is output column tid % 128 (of [word | context]), at the
   // tile's even tokens for tid < 128 and its odd ones above, so the thread sums them as it loads them
   float b2sum = 0.f;
   for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int64_t t0 = tile * kPhiTok;
-    constexpr int kDPer = kPhiTok * 2 * kPhiMax / kPhiThreads / 4;   // four rounds of 8 loads per thread
-#pragma unroll
-    for (int half = 0; half < 4; ++half) {
-      float v[kDPer];
-#pragma unroll
-      for (int x = 0; x < kDPer; ++x) {
-        const int e = tid + (half * kDPer + x) * kPhiThreads;
-        const int tk = e / (2 * kPhiMax), c = e - tk * 2 * kPhiMax;
-        const int64_t row = t0 + tk;
-        const bool ctx = c >= kPhiMax;
-        const int cc = ctx ? c - kPhiMax : c;
-        const bool ok = row < N && cc < (ctx ? a.Pc : a.Pw);
-        v[x] = a.dphi[ok ? row * P + (ctx ? a.Pw : 0) + cc : 0];
-        v[x] = ok ? v[x] : 0.f;
-      }
-#pragma unroll
-      for (int x = 0; x < kDPer; ++x) {
-        const int e = tid + (half * kDPer + x) * kPhiThreads;
-        const int tk = e / (2 * kPhiMax), c = e - tk * 2 * kPhiMax;
-        dps[tk * 2 * kWld + (c >= kPhiMax ? kWld + c - kPhiMax : c)] = v[x];
-        b2sum += v[x];
-      }
-    }
-    __syncthreads();
-    // dg = dphi W2 per block: A = dphi tile (tokens x outputs), B = the block (outputs x hidden), K = the 64 padded
-    // outputs (zero past Pw / Pc in both operands); all operands of a block read before its 64 MFMAs
+    const int64_t t0 = tile * kBwdTok;
+    HidYN<kBwdHid> in;                            // the tile's hidden inputs, in flight with its dphi
+    load_hidden_y<kBwdHid, kBwdTok>(a, t0, N, h4, in);
     {
-      const float* da = dps + (wave * 16 + r16) * 2 * kWld;
+      // thread tid reads column c = tid % 128 of tokens tid / 128 + 2 x: one 32-bit offset, stepped by 2 rows
+      const int c = tid & (2 * kPhiMax - 1), tk0 = tid / (2 * kPhiMax);
+      const bool ctx = c >= kPhiMax;
+      const int cc = ctx ? c - kPhiMax : c;
+      const bool col_ok = cc < (ctx ? a.Pc : a.Pw);
+      const float* src = a.dphi + t0 * P + (ctx ? a.Pw : 0) + (col_ok ? cc : 0);
+      float* dst = dps + tk0 * 2 * kWld + (ctx ? kWld + cc : cc);
 #pragma unroll
-      for (int part = 0; part < 2; ++part) {
-        const float* wsp = part ? wsc : wsw;
-        floatx4 acc[4];
+      for (int r = 0; r < kBwdD / 4; ++r) {
+        float v[4];
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) acc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {     // 8 k-steps at a time: their operands read, then 32 MFMAs
-          float av[8], bv[8][4];
-#pragma unroll
-          for (int ks = 0; ks < 8; ++ks) {
-            const int k = (half * 8 + ks) * 4 + k4;
-            av[ks] = da[(part ? kWld : 0) + k];
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt) bv[ks][nt] = wsp[k * kWld + nt * 16 + r16];
-          }
-#pragma unroll
-          for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma4(av[ks], bv[ks][nt], acc[nt]);
+        for (int x = 0; x < 4; ++x) {
+          const int tk = tk0 + 2 * (4 * r + x);
+          const bool ok = col_ok && t0 + tk < N;
+          v[x] = src[ok ? (uint32_t)(tk * P) : 0u];
+          v[x] = ok ? v[x] : 0.f;
         }
-        const int kn = part ? a.mc : a.m, off = part ? a.m : 0;
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const int col = nt * 16 + r16;
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (col < kn) dgs[(wave * 16 + k4 * 4 + q) * kGld + off + col] = acc[nt][q];
+        for (int x = 0; x < 4; ++x) {
+          dst[2 * (4 * r + x) * 2 * kWld] = v[x];
+          b2sum += v[x];
         }
       }
     }
     __syncthreads();
-    // the hidden layer's backward, one float4 of one token per thread: dp = dg gelu'(x) into dy; g = gelu(x) into
-    // LDS; each thread keeps one column group (h4 divides 256), summing dp for the first-layer biases
+    // dg = dphi W2 per block: wave w takes token rows 16 (w & 1) .. + 15 of block w >> 1; A = dphi tile (tokens x
+    // outputs), B = the block (outputs x hidden), K = the 64 padded outputs (zero past Pw / Pc in both operands)
+    {
+      const int tb = wave & 1, part = wave >> 1;
+      const float* da = dps + (tb * 16 + r16) * 2 * kWld + (part ? kWld : 0);
+      const float* wsp = part ? wsc : wsw;
+      floatx4 acc[4];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {              // two rounds of 4 groups (register pressure)
-    HidInN<kHidPer / 2> in;
-    load_hidden(a, t0, N, h4, in, hf * (kHidPer / 2));
+      for (int nt = 0; nt < 4; ++nt) acc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int xi = 0; xi < kHidPer / 2; ++xi) {
-      const int xg = hf * (kHidPer / 2) + xi;
-      const int e = tid + xg * kPhiThreads;
+      for (int quarter = 0; quarter < 4; ++quarter) {   // 4 k-steps at a time: their operands read, then 16 MFMAs
+        float av[4], bv[4][4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const int k = (quarter * 4 + ks) * 4 + k4;
+          av[ks] = da[k];
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) bv[ks][nt] = wsp[k * kWld + nt * 16 + r16];
+        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma4(av[ks], bv[ks][nt], acc[nt]);
+      }
+      const int kn = part ? a.mc : a.m, off = part ? a.m : 0;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int col = nt * 16 + r16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (col < kn) gs[(tb * 16 + k4 * 4 + q) * kGld + off + col] = acc[nt][q];
+      }
+    }
+    __syncthreads();
+    // the hidden layer's backward, one float4 of one token per thread: dp = dg gelu'(x) into dy; g = gelu(x) over dg
+    // in LDS; each thread keeps one column group (h4 divides 256), summing dp for the first-layer biases
+#pragma unroll
+    for (int x = 0; x < kBwdHid; ++x) {
+      const int e = tid + x * kPhiThreads;
       const int tk = e / h4, j = (e - tk * h4) * 4;
-      if (tk >= kPhiTok) continue;
+      if (tk >= kBwdTok) continue;
       const int64_t row = t0 + tk;
+      float* d = gs + tk * kGld + j;
       float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
       if (row < N) {
         const int64_t t = row % a.L;
-        const float4 x = pre_of(in, xi);
-        const float* d = dgs + tk * kGld + j;
+        const float4 xv = make_float4((in.ya[x].x + bias.x) + in.yb[x].x, (in.ya[x].y + bias.y) + in.yb[x].y,
+                                      (in.ya[x].z + bias.z) + in.yb[x].z, (in.ya[x].w + bias.w) + in.yb[x].w);
         float4 gd;
-        gelu_both(x.x, &g.x, &gd.x);
-        gelu_both(x.y, &g.y, &gd.y);
-        gelu_both(x.z, &g.z, &gd.z);
-        gelu_both(x.w, &g.w, &gd.w);
+        gelu_both(xv.x, &g.x, &gd.x);
+        gelu_both(xv.y, &g.y, &gd.y);
+        gelu_both(xv.z, &g.z, &gd.z);
+        gelu_both(xv.w, &g.w, &gd.w);
         const float4 dp = make_float4(d[0] * gd.x, d[1] * gd.y, d[2] * gd.z, d[3] * gd.w);
         *reinterpret_cast<float4*>(a.dy + row * a.ldd + j) = dp;
         if (j >= a.m) {
@@ -295,17 +324,15 @@ __global__ __launch_bounds__(kPhiThreads) void k_phi_bwd(PhiArgs a) {
         }
         bsum.x += dp.x; bsum.y += dp.y; bsum.z += dp.z; bsum.w += dp.w;
       }
-      float* o = gs + tk * kGld + j;
-      o[0] = g.x; o[1] = g.y; o[2] = g.z; o[3] = g.w;
-    }
+      d[0] = g.x; d[1] = g.y; d[2] = g.z; d[3] = g.w;
     }
     __syncthreads();
     // dW2w += dphi_word^T g_word, dW2c += dphi_ctx^T g_ctx: A = dphi^T (outputs x tokens), B = g (tokens x hidden),
-    // K = the tile's 64 tokens; wave w takes output rows 16w .. 16w + 15 of both blocks
+    // K = the tile's 32 tokens; wave w takes output rows 16w .. 16w + 15 of both blocks
     {
       const int orow = wave * 16 + r16;
 #pragma unroll
-      for (int quarter = 0; quarter < 4; ++quarter) {   // 4 token steps at a time: their operands read, then 32 MFMAs
+      for (int quarter = 0; quarter < 2; ++quarter) {   // 4 token steps at a time: their operands read, then 32 MFMAs
         float aw[4], ac[4], bw_[4][4], bc_[4][4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
@@ -329,7 +356,7 @@ __global__ __launch_bounds__(kPhiThreads) void k_phi_bwd(PhiArgs a) {
           }
       }
     }
-    __syncthreads();                              // the next tile overwrites dps, dgs and gs
+    __syncthreads();                              // the next tile overwrites dps and gs
   }
   float* prow = a.part + (int64_t)blockIdx.x * (a.Pw * a.m + a.Pc * a.mc + a.Pw + a.Pc + h);
 #pragma unroll
@@ -398,12 +425,14 @@ extern "C" int asrn_hash_fwd(const float* y, int64_t ldy, const float* b_word, c
   return check_launch("asrn_hash_fwd");
 }
 
-// the backward's workgroups: at most 128, one per CU on half of the 256, fewer for short inputs. The layer runs the
-// context producer's backward on a second stream beside this kernel; a grid over every CU (one 133 KB-LDS workgroup
-// each) keeps that work off the machine until it ends, and the step measured 2% slower with 256 than with 128.
+// the backward's workgroups: at most kBwdGroups (two of 67 KB LDS fit a CU), fewer for short inputs
+#ifndef ASRN_PHI_BWD_GROUPS
+#define ASRN_PHI_BWD_GROUPS 512
+#endif
+constexpr int64_t kBwdGroups = ASRN_PHI_BWD_GROUPS;
 static int64_t phi_bwd_groups(int64_t n) {
-  const int64_t tiles = (n + kPhiTok - 1) / kPhiTok;
-  return tiles < 128 ? tiles : 128;
+  const int64_t tiles = (n + kBwdTok - 1) / kBwdTok;
+  return tiles < kBwdGroups ? tiles : kBwdGroups;
 }
 
 extern "C" int64_t asrn_hash_bwd_workspace(int64_t B, int64_t L, int32_t m, int32_t mc, int32_t p_word,

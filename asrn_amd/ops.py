@@ -176,8 +176,8 @@ class Context(torch.autograd.Function):
 class ContextProj(torch.autograd.Function):
     """Context followed by the Qc/Kc projection y = hh Wq^T, fp32 (asrn/estable.py:153-194): the first output is y
     (.., ny) instead of hh. The backward forms the projection's input gradient dhh = dy Wq inside asrn_context_bwd
-    (no GEMM and no dhh buffer: dy is ny <= 64 values a token) and Wq's gradient dy^T hh by token slabs, as lineal
-    does. For fp32 layers with d <= 512."""
+    (no GEMM and no dhh buffer: dy is ny <= 32 values a token) and Wq's gradient dy^T hh by token slabs, as lineal
+    does. For fp32 layers with d <= 512 and 2 cf <= 32."""
 
     @staticmethod
     def forward(ctx, h, ln_w, ln_b, w_reloj, b_reloj, Wq, meta):

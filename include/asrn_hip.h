@@ -127,7 +127,7 @@ int64_t asrn_scan_workspace(int64_t rows, int64_t N);
  * no clamp); log_alfa = max(logsigmoid(u_1) + log 2, log_alfa_min) (BL) fp32 out (-inf: no clamp); stats (BL, 4) =
  * (mean, rstd, u_0, u_1) kept for the backward. d % 4 == 0, d <= 1024.
  * context_bwd: from dhh (BL, d) (the Qc/Kc GEMM's input gradient), or instead from that GEMM's output gradient dy
- * (BL rows of ny <= 64, row stride ldy) and its weight wq (ny, d) with d <= 512, as dhh = dy wq formed in the kernel
+ * (BL rows of ny <= 32, row stride ldy) and its weight wq (ny, d) with d <= 512, as dhh = dy wq formed in the kernel
  * (replacing the GEMM `grad @ weight` of the Linear's backward), and from dbeta (BL) fp64 and dlog_alfa (BL): gives
  * dh (BL, d) (overwritten; plus dh_add (BL, d) when not null: the gradient of h through the gate) and dparams
  * (4 d + 2) = the gradients of [ln_w | ln_b | w_reloj (2 d) | b_reloj (2)], summed over tokens in a fixed order.
