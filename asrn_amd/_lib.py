@@ -74,6 +74,9 @@ SIGNATURES = {
     'asrn_cross_entropy_bwd': (ctypes.c_int, [_P, _I32, _I64, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P]),
     'asrn_conv_window_fwd': (ctypes.c_int, [_P, _I64, _I64, _I64, _I32, _I32, _I32, _P, _P]),
     'asrn_conv_window_bwd': (ctypes.c_int, [_P, _I32, _I64, _I64, _I32, _I32, _P, _I64, _P]),
+    'asrn_layer_norm_fwd': (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I32, _F32, _I32, _P, _I64, _P, _P]),
+    'asrn_layer_norm_bwd_workspace': (_I64, [_I64, _I32]),
+    'asrn_layer_norm_bwd': (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I32, _P, _I32, _I64, _P, _P, _P, _P, _I64, _P]),
     'asrn_block_step_workspace': (_I64, [_I64, _I32, _I32]),
     'asrn_block_step': (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I32, _I32, _I32] + [_P] * 10 + [_F32] + [_P] * 6
                         + [_I64, _P]),

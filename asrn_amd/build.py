@@ -16,7 +16,8 @@ CSRC = os.path.join(HERE, 'csrc')
 LIB = os.path.join(HERE, 'libasrn_hip.so')
 SOURCES = ['errors.hip', 'bucket_sort.hip', 'ngram.hip', 'scan.hip', 'candidates.hip', 'decode.hip',
            'decode_produce.hip', 'gate.hip', 'context.hip', 'hidden.hip', 'reduce.hip', 'small_gemm.hip', 'blocks.hip',
-           'phi.hip', 'sampling.hip', 'block_step.hip', 'cross_entropy.hip', 'conv_window.hip']
+           'phi.hip', 'sampling.hip', 'block_step.hip', 'cross_entropy.hip', 'conv_window.hip',
+           'layernorm.hip']
 ARCH = os.environ.get('ASRN_OFFLOAD_ARCH', 'gfx950')
 INCLUDE = os.path.join(os.path.dirname(HERE), 'include')
 COMMON = ['-O3', '-fPIC', '-std=c++17', f'--offload-arch={ARCH}', '-Xclang', '-target-feature', '-Xclang',

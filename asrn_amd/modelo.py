@@ -67,6 +67,12 @@ def conv_canal_causal(z, peso, sesgo):
     return out + sesgo.to(z.dtype)
 
 
+def _dtype_producto(x):
+    """The dtype the next product takes x in: autocast's on x's device when enabled, else x's own."""
+    dev = x.device.type
+    return torch.get_autocast_dtype(dev) if torch.is_autocast_enabled(dev) else x.dtype
+
+
 class BloqueLocal(nn.Module):
     """Causal local context (asrn/nucleo.py:969-1014): h += GELU(causal conv of LayerNorm(h) over the current and
     k - 1 previous tokens); h += FF(LayerNorm(h)). mezcla='memoria': the convolution is per channel, plus a forgetting
@@ -104,7 +110,9 @@ class BloqueLocal(nn.Module):
         return self.mem_o(m.transpose(1, 2).to(z.dtype))
 
     def forward(self, h):
-        z = self.ln1(h)
+        # the LayerNorms run fused (ops.norma_residual): ln2's output comes out in the feed-forward's dtype, and the
+        # residual path's gradient joins each LayerNorm's backward
+        z, h = ops.norma_residual(self.ln1, h, torch.float32)
         if self.mezcla == 'conv':
             c = conv_causal(z, self.conv.weight, self.conv.bias)
         else:
@@ -113,7 +121,8 @@ class BloqueLocal(nn.Module):
         if self.mezcla == 'memoria':
             c = c + self._memoria(z)
         h = h + self.drop(c)
-        return h + self.drop(self.ff(self.ln2(h)))
+        y, h = ops.norma_residual(self.ln2, h, _dtype_producto(h))
+        return h + self.drop(self.ff(y))
 
 
 @torch.no_grad()
@@ -198,7 +207,9 @@ class ModeloASRN(nn.Module):
         return h
 
     def forward(self, x):
-        return self.head(self.ln_f(self.estado(x)))
+        h = self.estado(x)
+        y, _ = ops.norma_residual(self.ln_f, h, _dtype_producto(h))
+        return self.head(y)
 
     def perdida(self, x, y, ignorar=-100):
         """Mean fp32 cross-entropy of predicting y from x, both (B, L) (asrn/nucleo.py:1122-1125)."""

@@ -1061,3 +1061,56 @@ class VentanaCausal(torch.autograd.Function):
 
 def ventana_causal(z, k, dtype):
     return VentanaCausal.apply(z, k, dtype)
+
+
+class NormaResidual(torch.autograd.Function):
+    """A local block's or the model's LayerNorm (asrn/nucleo.py:969-1014, 1047-1125) as torch.nn.LayerNorm computes it
+    in fp32, written by asrn_layer_norm_fwd straight in the dtype the next product takes (bf16 under autocast: the same
+    rounding as the cast), with (mean, rstd) kept per row. The second output is x itself (fp32, an alias) for the
+    residual path: its gradient is added to dx inside asrn_layer_norm_bwd, so autograd adds nothing. x fp32
+    (..., d), d a multiple of 4 and at most 1024."""
+
+    @staticmethod
+    def forward(ctx, x, gamma, beta, eps, dtype):
+        dev = _dev(x)
+        d, lead = x.shape[-1], x.shape[:-1]
+        x2 = _c(x, torch.float32).reshape(-1, d)
+        rows = x2.shape[0]
+        g, b = _c(gamma, torch.float32), _c(beta, torch.float32)
+        y = torch.empty((rows, d), dtype=dtype, device=dev)
+        stats = torch.empty((rows, 2), dtype=torch.float32, device=dev)
+        call('asrn_layer_norm_fwd', ptr(x2), d, ptr(g), ptr(b), rows, d, float(eps), int(dtype == torch.bfloat16),
+             ptr(y), d, ptr(stats), stream_of(dev))
+        ctx.save_for_backward(x2, g, stats)
+        ctx.meta = (x.dtype, lead, gamma.shape, beta.shape)
+        return y.view(*lead, d), x2.view(*lead, d)
+
+    @staticmethod
+    def backward(ctx, dy, dres):
+        x2, g, stats = ctx.saved_tensors
+        xdt, lead, gshape, bshape = ctx.meta
+        rows, d = x2.shape
+        dev = x2.device
+        if dy is None:
+            dy = torch.zeros((rows, d), dtype=torch.float32, device=dev)
+        bf16 = dy.dtype == torch.bfloat16
+        dyc = (_c(dy) if bf16 else _c(dy, torch.float32)).reshape(rows, d)
+        dr = None if dres is None else _c(dres, torch.float32).reshape(rows, d)
+        dx = torch.empty_like(x2)
+        dp = torch.empty((2 * d,), dtype=torch.float32, device=dev)
+        wsb = query('asrn_layer_norm_bwd_workspace', rows, d)
+        ws = torch.empty((wsb,), dtype=torch.uint8, device=dev)
+        call('asrn_layer_norm_bwd', ptr(x2), d, ptr(g), ptr(stats), rows, d, ptr(dyc), int(bf16), d, ptr(dr), ptr(dx),
+             ptr(dp), ptr(ws), wsb, stream_of(dev))
+        return dx.view(*lead, d).to(xdt), dp[:d].view(gshape), dp[d:].view(bshape), None, None
+
+
+def norma_residual(ln, x, dtype):
+    """(LayerNorm ln of x in `dtype`, x for the residual path): the library's fused LayerNorm for fp32 x on the GPU
+    with d a multiple of 4 up to 1024, else ln(x) (cast to dtype) and x itself."""
+    d = x.shape[-1]
+    if x.is_cuda and x.dtype == torch.float32 and dtype in (torch.float32, torch.bfloat16) and d % 4 == 0 and \
+            d <= 1024 and ln.elementwise_affine and ln.bias is not None and tuple(ln.normalized_shape) == (d,):
+        return NormaResidual.apply(x, ln.weight, ln.bias, ln.eps, dtype)
+    y = ln(x)
+    return (y if y.dtype == dtype else y.to(dtype)), x

@@ -432,6 +432,22 @@ int asrn_conv_window_fwd(const float* z, int64_t ldz, int64_t B, int64_t L, int3
 int asrn_conv_window_bwd(const void* dcols, int32_t cols_bf16, int64_t B, int64_t L, int32_t d, int32_t k, float* dz,
                          int64_t lddz, void* stream);
 
+/* ---- the model's LayerNorms ------------------------------------------------------------------------------------
+ * Replaces torch.nn.LayerNorm of the local blocks (ln1, ln2) and the final ln_f (asrn/nucleo.py:969-1014,
+ * 1047-1125) as it runs in fp32 under autocast, with the cast of its output to bf16 for the next product, and, in the
+ * backward, the residual path's gradient addition. fwd: x (rows, d) fp32, row stride ldx -> y = (x - mean) rstd gamma
+ * + beta (biased variance, rstd = 1 / sqrt(var + eps)) in fp32 or bf16 (out_bf16, rounded to nearest even), row
+ * stride ldy, and stats (rows, 2) = (mean, rstd). bwd: from dy (fp32 or bf16, row stride lddy) -> dx (rows, d) fp32,
+ * row stride ldx (overwritten; plus dres (rows, d), row stride ldx, when not null), and dparams (2 d) = [d gamma |
+ * d beta] summed over rows in a fixed order. d a multiple of 4, <= 1024; rows 16-byte aligned (8 for bf16).
+ * workspace: asrn_layer_norm_bwd_workspace(rows, d) bytes, 256-byte aligned. */
+int asrn_layer_norm_fwd(const float* x, int64_t ldx, const float* gamma, const float* beta, int64_t rows, int32_t d,
+                        float eps, int32_t out_bf16, void* y, int64_t ldy, float* stats, void* stream);
+int64_t asrn_layer_norm_bwd_workspace(int64_t rows, int32_t d);
+int asrn_layer_norm_bwd(const float* x, int64_t ldx, const float* gamma, const float* stats, int64_t rows, int32_t d,
+                        const void* dy, int32_t dy_bf16, int64_t lddy, const float* dres, float* dx, float* dparams,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

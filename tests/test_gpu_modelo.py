@@ -109,6 +109,41 @@ def test_conv_window_matches_unfold(dtype, B, L, d, k):
     assert torch.allclose(a.grad, b.grad, rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize('dtype,rows,d,res', [(torch.float32, 1000, 768, True), (torch.bfloat16, 4099, 768, True),
+                                              (torch.bfloat16, 33, 64, False), (torch.float32, 7, 1024, True),
+                                              (torch.float32, 70, 12, False)])
+def test_layer_norm_matches_torch(dtype, rows, d, res):
+    """asrn_layer_norm_fwd/bwd (ops.NormaResidual) against torch.nn.LayerNorm in fp32 followed by the cast to the
+    product's dtype: the output within one bf16 rounding (fp32: 2e-6), the gradients of x (with the residual path's
+    gradient added in the kernel) and of gamma and beta to fp32 rounding; rows that leave partial workgroups (1000,
+    4099, 33, 7, 70) and widths of 1 to 4 float4 columns a lane."""
+    say('layer norm', dtype, rows, d, res)
+    g = torch.Generator().manual_seed(rows + d)
+    x = (torch.randn(rows, d, generator=g) * 3 + 1).to(DEV)
+    ln = torch.nn.LayerNorm(d).to(DEV)
+    with torch.no_grad():
+        ln.weight.copy_(1 + 0.2 * torch.randn(d, generator=g))
+        ln.bias.copy_(0.2 * torch.randn(d, generator=g))
+    gy = torch.randn(rows, d, generator=g).to(DEV).to(dtype)
+    gr = torch.randn(rows, d, generator=g).to(DEV)
+    a = x.clone().requires_grad_()
+    b = x.clone().requires_grad_()
+    ya, ra = asrn_amd.ops.norma_residual(ln, a, dtype)
+    assert ya.dtype == dtype
+    ((ya.float() * gy.float()).sum() + ((ra * gr).sum() if res else 0)).backward()
+    wa, ba = ln.weight.grad.clone(), ln.bias.grad.clone()
+    ln.weight.grad = ln.bias.grad = None
+    yb = ln(b)
+    ((yb.to(dtype).float() * gy.float()).sum() + ((b * gr).sum() if res else 0)).backward()
+    if dtype == torch.bfloat16:     # one rounding apart at most: the fp32 values differ in the last bits
+        assert torch.allclose(ya.float(), yb.to(dtype).float(), rtol=8e-3, atol=1e-2)
+    else:
+        assert torch.allclose(ya, yb, rtol=2e-6, atol=2e-6)
+    assert torch.allclose(a.grad, b.grad, rtol=1e-4, atol=1e-4)
+    assert torch.allclose(wa, ln.weight.grad, rtol=1e-4, atol=1e-3)
+    assert torch.allclose(ba, ln.bias.grad, rtol=1e-4, atol=1e-3)
+
+
 @pytest.mark.parametrize('nombre', ['paso_cfg0', 'paso_memoria'])
 def test_training_step_matches_reference(nombre):
     t, kw = _fixture(nombre)
