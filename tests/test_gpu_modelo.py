@@ -90,11 +90,13 @@ def test_cross_entropy_matches_torch(dtype, V, rows, reduction):
 
 
 @pytest.mark.parametrize('dtype,B,L,d,k', [(torch.bfloat16, 3, 517, 96, 4), (torch.float32, 2, 300, 64, 4),
-                                            (torch.bfloat16, 2, 40, 10, 3), (torch.float32, 1, 5, 8, 7)])
+                                            (torch.bfloat16, 2, 40, 10, 3), (torch.float32, 1, 5, 8, 7),
+                                            (torch.bfloat16, 2, 2048, 768, 4), (torch.bfloat16, 3, 8, 12, 4)])
 def test_conv_window_matches_unfold(dtype, B, L, d, k):
     """asrn_conv_window_fwd/bwd (the 'conv' block's convolution columns) against pad + unfold + reshape and the cast to
     the GEMM's dtype: the columns bit-identical, the z gradient to fp32 rounding (the fold sums k terms in another
-    order); k = 4 takes the vectorized kernels, 3 and 7 the general ones, and rows shorter than k are covered."""
+    order); k = 4 takes the vectorized kernels (4 tokens a thread when L is a multiple of 4: 300, 2048, 8), 3 and 7
+    the general ones, and rows shorter than k are covered."""
     say('conv window', dtype, B, L, d, k)
     g = torch.Generator().manual_seed(L + k)
     z = torch.randn(B, L, d, generator=g).to(DEV)
