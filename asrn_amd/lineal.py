@@ -17,10 +17,15 @@ import torch.nn.functional as F
 from . import _lib
 
 MIN_SLAB = 1024            # tokens per slab: below this the batched GEMM's own overhead dominates
+MAX_SLAB_WEIGHT = 1 << 20  # weights with this many elements or more keep one GEMM: enough output tiles already, and
+                           # S partial copies of them would cost more traffic than they save
 
 
-def slabs_for(n):
-    """Slab count for a token axis of n: 16 (or fewer) slabs of at least MIN_SLAB tokens that divide n exactly."""
+def slabs_for(n, weight_elems=0):
+    """Slab count for a token axis of n: 16 (or fewer) slabs of at least MIN_SLAB tokens that divide n exactly; 1 for
+    weights of MAX_SLAB_WEIGHT elements or more."""
+    if weight_elems >= MAX_SLAB_WEIGHT:
+        return 1
     for s in (16, 8, 4, 2):
         if n % s == 0 and n // s >= MIN_SLAB:
             return s
@@ -74,7 +79,7 @@ def sum_rows(t):
 
 def weight_grad(g2, x2):
     """dW = g2^T x2, summed in fp32 (fp64 for fp64 operands): g2 (N, out), x2 (N, in), both with unit last stride."""
-    s = slabs_for(g2.shape[0])
+    s = slabs_for(g2.shape[0], g2.shape[1] * x2.shape[1])
     if s == 1:
         return g2.t().mm(x2).to(_acc_dtype(g2))
     # left operand: the transposed slab of g2; right operand: x2's slab as stored (never a transposed view)

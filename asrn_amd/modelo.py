@@ -18,6 +18,7 @@ import torch.nn.functional as F
 from .capa import CapaASRNEstable, ngramas
 from . import ops
 from .ops import escaneo
+from .lineal import lineal
 
 MEZCLAS = ('conv', 'memoria')
 OPCIONES_CAPA = ('n_tablas', 'n_bits', 'afin_oculto', 'chunk', 'tablas_contexto', 'confirmar', 'sufijo', 'vistos',
@@ -52,7 +53,7 @@ def conv_causal(z, peso, sesgo):
         zp = F.pad(z, (0, 0, k - 1, 0))
         cols = zp.unfold(1, k, 1)                        # (B, L, d_in, k): [b, t, c, j] = zp[b, t + j, c]
         cols = cols.reshape(z.shape[0], z.shape[1], -1)  # (B, L, d_in * k), column c * k + j (one copy)
-    return F.linear(cols, peso.reshape(peso.shape[0], -1), sesgo)
+    return lineal(cols, peso.reshape(peso.shape[0], -1), sesgo)
 
 
 def conv_canal_causal(z, peso, sesgo):
@@ -122,7 +123,12 @@ class BloqueLocal(nn.Module):
             c = c + self._memoria(z)
         h = h + self.drop(c)
         y, h = ops.norma_residual(self.ln2, h, _dtype_producto(h))
-        return h + self.drop(self.ff(y))
+        return h + self.drop(self._ff(y))
+
+    def _ff(self, y):
+        """self.ff on the library's Linear (lineal: the bias gradients as the library's fixed-order column sums)."""
+        f0, act, f2 = self.ff
+        return lineal(act(lineal(y, f0.weight, f0.bias)), f2.weight, f2.bias)
 
 
 @torch.no_grad()
