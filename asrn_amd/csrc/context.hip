@@ -5,9 +5,9 @@
 //   u_k = hh . w_reloj[k] + b_reloj[k]           (k = 0, 1; fp32, as the reference's IEEE branch)
 //   beta = min(softplus(u_0), beta_max) -> fp64, log_alfa = max(logsigmoid(u_1) + log 2, log_alfa_min)
 // hh feeds the Qc/Kc GEMM (hipBLASLt). Kept per token for the backward: (mean, rstd, u_0, u_1).
-// Backward, from dhh (the Qc/Kc GEMM's input gradient) or from that GEMM's output gradient dy (ny per token) and its
-// weight Wq (ny, d), as dhh = dy Wq formed here (each wave first forms its tokens' rows: one Wq load per output column
-// serves all of them), and from dbeta and dlog_alfa:
+// Backward, from dhh (the Qc/Kc GEMM's input gradient) or from that GEMM's output gradient dy (ny <= 32 per token)
+// and its weight Wq (ny, d), as dhh = dy Wq formed here on the matrix cores (v_mfma_f32_16x16x4_f32: lane l supplies
+// A[l % 16][l / 16] and B[l / 16][l % 16] and receives D[(l / 16) * 4 + q][l % 16]), and from dbeta and dlog_alfa:
 //   du_0 = dbeta softplus'(u_0) [softplus(u_0) <= beta_max],  du_1 = dlog_alfa sigmoid(-u_1) [not clamped below]
 //   g = dhh + du_0 w_reloj[0] + du_1 w_reloj[1],  dxhat = g ln_w
 //   dh = rstd (dxhat - mean(dxhat) - xhat mean(dxhat xhat)) [+ dh_add: h's gradient through the layer's other use]
@@ -106,16 +106,23 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_fwd(CtxArgs a) {
   }
 }
 
-// PROJ: dhh = dy Wq for the wave's kCtxTokPerWave tokens, formed before the loop: Wq (ny <= 32 rows) staged in LDS
-// once per workgroup, one float4 of a row per lane and output column for all of the wave's tokens, each token's dy
-// value broadcast from the lane that loaded it; in output column order. The stage shares its LDS with the end's
-// partial rows.
+// PROJ: dhh = dy Wq for the workgroup's kCtxTok tokens, formed before the loop as a (32 x 32) by (32 x 4 D4 kWave)
+// product on the matrix cores: Wq (ny <= 32 rows, zero-padded to 32 rows and 4 D4 kWave columns) and the tokens' dy
+// rows staged in LDS, wave w taking the column blocks w, w + 4, ... for both 16-token blocks (K = 8 steps of 4), and
+// the dhh tile written back over the stage for the token loop. The stage shares its LDS with the end's partial rows.
 constexpr int kProjRows = 32;
+typedef float ctx_floatx4 __attribute__((ext_vector_type(4)));
 template <int D4, bool PROJ>
-__global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
+__global__ __launch_bounds__(kCtxThreads, (PROJ && D4 == 1) ? 4 : 1) void k_ctx_bwd(CtxArgs a) {   // PROJ, d <= 256: 4 waves per SIMD
+  constexpr int kW = 4 * D4 * kWave;             // padded row width of Wq and the dhh tile
+  // LDS row strides chosen so that a wave's 64 lanes fall in distinct banks: the B reads (4 rows x 16 columns), the
+  // A reads (16 rows x 4 columns) and the output writes (4 rows x 16 columns, rows 4 apart)
+  constexpr int kWs = kW + 16, kDs = kProjRows + 4, kTs = kW + 4;
   constexpr int kRed = kCtxWaves * (4 * 4 * D4 * kWave + 2);
-  constexpr int kStage = PROJ ? kProjRows * 4 * D4 * kWave : 0;
-  __shared__ float lds[kRed > kStage ? kRed : kStage];
+  constexpr int kStage = PROJ ? kProjRows * kWs + kCtxTok * kDs : 0;
+  constexpr int kTile = PROJ ? kCtxTok * kTs : 0;
+  constexpr int kLds = kRed > kStage ? (kRed > kTile ? kRed : kTile) : (kStage > kTile ? kStage : kTile);
+  __shared__ float lds[kLds];
   float (*red)[4 * 4 * D4 * kWave + 2] = reinterpret_cast<float (*)[4 * 4 * D4 * kWave + 2]>(lds);
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int d4 = a.d >> 2;
@@ -125,39 +132,47 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
 #pragma unroll
   for (int k = 0; k < D4; ++k) gw[k] = gb[k] = gr0[k] = gr1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
   float gbr0 = 0.f, gbr1 = 0.f;
-  float4 pj[PROJ ? kCtxTokPerWave : 1][D4];
   if constexpr (PROJ) {
-    float4* wq4 = reinterpret_cast<float4*>(lds);  // row o, float4 q at wq4[o * D4 * kWave + q]
-    for (int i = threadIdx.x; i < a.ny * D4 * kWave; i += kCtxThreads) {
-      const int o = i / (D4 * kWave), q = i - o * (D4 * kWave);
-      wq4[i] = q < d4 ? ((const float4*)(a.wq + (int64_t)o * a.d))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float* wqs = lds;                              // Wq: row o at o * kWs
+    float* dys = lds + kProjRows * kWs;            // dy: token row at tk * kDs
+    for (int i = threadIdx.x; i < kProjRows * (kW / 4); i += kCtxThreads) {
+      const int o = i / (kW / 4), q = i - o * (kW / 4);
+      reinterpret_cast<float4*>(wqs + o * kWs)[q] = (o < a.ny && q < d4) ? ((const float4*)(a.wq + (int64_t)o * a.d))[q]
+                                                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    for (int i = threadIdx.x; i < kCtxTok * kProjRows; i += kCtxThreads) {
+      const int tk = i / kProjRows, o = i - tk * kProjRows;
+      const int64_t t = (int64_t)blockIdx.x * kCtxTok + tk;
+      dys[tk * kDs + o] = (t < a.BL && o < a.ny) ? a.dy[t * a.ldy + o] : 0.f;
     }
     __syncthreads();
-    float dyv[kCtxTokPerWave];
+    constexpr int kNb = kW / 16 / kCtxWaves;       // column blocks of 16 per wave
+    const int r16 = lane & 15, k4 = lane >> 4;
+    ctx_floatx4 acc[2][kNb];
 #pragma unroll
-    for (int u = 0; u < kCtxTokPerWave; ++u) {
-      const int64_t t = tw + u;
-      dyv[u] = (t < a.BL && lane < a.ny) ? a.dy[t * a.ldy + lane] : 0.f;
+    for (int j = 0; j < kNb; ++j) acc[0][j] = acc[1][j] = ctx_floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int k = 0; k < D4; ++k) pj[u][k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    for (int o = 0; o < a.ny; ++o) {
-      float4 w[D4];
+    for (int ks = 0; ks < kProjRows / 4; ++ks) {
+      const int k = ks * 4 + k4;
+      const float a0 = dys[r16 * kDs + k], a1 = dys[(16 + r16) * kDs + k];
 #pragma unroll
-      for (int k = 0; k < D4; ++k) w[k] = wq4[o * D4 * kWave + lane + kWave * k];
-#pragma unroll
-      for (int u = 0; u < kCtxTokPerWave; ++u) {
-        const float c = readlane_f(dyv[u], o);
-#pragma unroll
-        for (int k = 0; k < D4; ++k) {
-          pj[u][k].x += c * w[k].x; pj[u][k].y += c * w[k].y; pj[u][k].z += c * w[k].z; pj[u][k].w += c * w[k].w;
-        }
+      for (int j = 0; j < kNb; ++j) {
+        const float b = wqs[k * kWs + (wave + kCtxWaves * j) * 16 + r16];
+        acc[0][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b, acc[0][j], 0, 0, 0);
+        acc[1][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b, acc[1][j], 0, 0, 0);
       }
     }
+    __syncthreads();                               // every wave has read the stage
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int j = 0; j < kNb; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          lds[(mb * 16 + k4 * 4 + q) * kTs + (wave + kCtxWaves * j) * 16 + r16] = acc[mb][j][q];
+    __syncthreads();
   }
   constexpr int BB = kCtxBatch;                  // tokens whose rows are loaded together
-  constexpr int kUnroll = PROJ ? kCtxTokPerWave / BB : 1;   // PROJ: pj's indices must be constants
-#pragma unroll kUnroll
   for (int b = 0; b < kCtxTokPerWave; b += BB) {
     float4 hv[BB][D4], gv[BB][D4], av[BB][D4];
     float4 st[BB];
@@ -174,7 +189,7 @@ __global__ __launch_bounds__(kCtxThreads) void k_ctx_bwd(CtxArgs a) {
         const int q = lane + kWave * k;
         if (ok && q < d4) {
           hv[u][k] = ((const float4*)(a.h + t * a.d))[q];
-          if constexpr (PROJ) gv[u][k] = pj[b + u][k];
+          if constexpr (PROJ) gv[u][k] = reinterpret_cast<const float4*>(lds + (wave * kCtxTokPerWave + b + u) * kTs)[q];
           else gv[u][k] = ((const float4*)(a.dhh + t * a.d))[q];
           av[u][k] = a.dh_add ? ((const float4*)(a.dh_add + t * a.d))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
