@@ -1,6 +1,6 @@
 // a0 (part): the hash MLPs from their first layers' products to phi (asrn/nucleo.py:644-659), fused.
 //
-// The first GEMM gives, per token t, y[t] = [W_p E_t | W_a E_t | W_b E_t] (bias-free). Then, per tile of 64 tokens:
+// The first GEMM gives, per token t, y[t] = [W_p E_t | W_a E_t | W_b E_t] (bias-free). Then, per tile of 32 tokens:
 //   forward   g = [gelu(hp + b_p) | gelu(za + zb[t-1] + b_c)] into LDS (exact erf GELU; no zb term at a row's first
 //             position), and phi = [g_word W2w^T + b2w | g_ctx W2c^T + b2c] on the matrix cores
 //             (v_mfma_f32_16x16x4_f32), the two second layers as the two diagonal blocks they are.
@@ -16,8 +16,7 @@
 
 namespace asrn {
 
-constexpr int kPhiTok = 64;          // tokens per workgroup
-constexpr int kPhiThreads = 256;     // 4 waves: wave w owns tokens 16w .. 16w + 15 of the tile
+constexpr int kPhiThreads = 256;     // 4 waves
 constexpr int kPhiMax = 64;          // the most hidden units or outputs per MLP
 constexpr int kGld = 2 * kPhiMax + 1;   // LDS row stride of the g / dg tiles (odd: conflict-free column reads)
 constexpr int kWld = kPhiMax + 1;       // LDS row stride of a weight block or a dphi tile
@@ -69,36 +68,10 @@ __device__ __forceinline__ void stage_block(const float* __restrict__ W, int row
   }
 }
 
-// The hidden layer's inputs for kHidPer float4 groups of the tile per thread (group e = tid + x * 256: token e / h4,
-// columns 4 (e % h4) ..): y at those columns (hp for word columns, za for context ones: both at y[row][j]), the
-// previous token's zb for context columns (0 at a row's first position) and the bias. All loads issued together.
-constexpr int kHidPer = kPhiTok * 2 * kPhiMax / 4 / kPhiThreads;   // 8 float4 groups per thread at most
-template <int NG>
-struct HidInN {
-  float4 ya[NG], yb[NG], bb[NG];
-};
-using HidIn = HidInN<kHidPer>;
-// groups first .. first + NG - 1 of this thread
-template <int NG, int TOK = kPhiTok>
-__device__ __forceinline__ void load_hidden(const PhiArgs& a, int64_t t0, int64_t N, int h4, HidInN<NG>& in,
-                                            int first = 0) {
-#pragma unroll
-  for (int x = 0; x < NG; ++x) {
-    const int e = threadIdx.x + (first + x) * kPhiThreads;
-    const int tk = e / h4, j = (e - tk * h4) * 4;
-    const int64_t row = t0 + tk;
-    const bool ok = tk < TOK && row < N;
-    const bool ctx = j >= a.m;
-    const bool prev = ok && ctx && row % a.L > 0;
-    const int64_t r0 = ok ? row : 0;
-    in.ya[x] = *reinterpret_cast<const float4*>(a.y + r0 * a.ldy + (ok ? j : 0));
-    in.yb[x] = *reinterpret_cast<const float4*>(a.y + (prev ? (r0 - 1) * a.ldy + a.mc + j : 0));
-    in.bb[x] = *reinterpret_cast<const float4*>(ctx ? a.bc + (j - a.m) : a.bp + (ok ? j : 0));
-    if (!prev) in.yb[x] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-}
-// the backward's tile inputs: y and the previous token's zb only (a thread's groups all share one column group, whose
-// bias the kernel loads once)
+// A tile's hidden-layer inputs for NG float4 groups per thread (group e = tid + x * 256: token e / h4, columns
+// 4 (e % h4) ..): y at those columns (hp for word columns, za for context ones: both at y[row][j]) and the previous
+// token's zb for context columns (0 at a row's first position). All loads issued together. A thread's groups all
+// share one column group, whose bias the kernels load once.
 template <int NG>
 struct HidYN {
   float4 ya[NG], yb[NG];
@@ -119,39 +92,46 @@ __device__ __forceinline__ void load_hidden_y(const PhiArgs& a, int64_t t0, int6
   }
 }
 
-template <int NG>
-__device__ __forceinline__ float4 pre_of(const HidInN<NG>& in, int x) {
-  return make_float4((in.ya[x].x + in.bb[x].x) + in.yb[x].x, (in.ya[x].y + in.bb[x].y) + in.yb[x].y,
-                     (in.ya[x].z + in.bb[x].z) + in.yb[x].z, (in.ya[x].w + in.bb[x].w) + in.yb[x].w);
-}
+
+// The forward takes tiles of kFwdTok = 32 tokens per workgroup of 50 KB of LDS (three per CU): the tile's hidden inputs
+// (4 float4 groups a thread, its column group's bias loaded once), g = gelu into LDS, then wave w forms the 16-token
+// block w & 1 of MLP w >> 1 on the matrix cores (64 MFMAs, operands read 4 k-steps at a time).
+constexpr int kFwdTok = 32;
+constexpr int kFwdHid = kFwdTok * 2 * kPhiMax / 4 / kPhiThreads;     // hidden float4 groups per thread: 4
 
 __global__ __launch_bounds__(kPhiThreads) void k_phi_fwd(PhiArgs a) {
-  __shared__ float gs[kPhiTok * kGld];
+  __shared__ float gs[kFwdTok * kGld];
   __shared__ float wsw[kPhiMax * kWld];
   __shared__ float wsc[kPhiMax * kWld];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t N = a.B * a.L, t0 = (int64_t)blockIdx.x * kPhiTok;
+  const int64_t N = a.B * a.L, t0 = (int64_t)blockIdx.x * kFwdTok;
   const int h = a.m + a.mc, h4 = h / 4, P = a.Pw + a.Pc;
-  float bias[8];                                   // the second layers' biases of this lane's output columns
+  const int r16 = lane & 15, k4 = lane >> 4;
+  const int tb = wave & 1, part = wave >> 1;
+  const int kn = part ? a.mc : a.m, koff = part ? a.m : 0, pn = part ? a.Pc : a.Pw;
+  float bias[4];                                   // the second layer's biases of this lane's output columns
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
-    const int cw = nt * 16 + (lane & 15);
-    bias[nt] = a.bw[cw < a.Pw ? cw : 0];
-    bias[4 + nt] = a.bc2[cw < a.Pc ? cw : 0];
+    const int cw = nt * 16 + r16;
+    bias[nt] = cw < pn ? (part ? a.bc2 : a.bw)[cw] : 0.f;
   }
   {
-    HidIn in;
-    load_hidden(a, t0, N, h4, in);
+    HidYN<kFwdHid> in;
+    load_hidden_y<kFwdHid, kFwdTok>(a, t0, N, h4, in);
+    // every hidden group of thread tid is column group tid % h4 (h4 divides 256): its first-layer bias
+    const int jb = (tid % h4) * 4;
+    const float4 b1 = *reinterpret_cast<const float4*>(jb >= a.m ? a.bc + (jb - a.m) : a.bp + jb);
     stage_block(a.Ww, a.Pw, a.m, wsw);
     stage_block(a.Wc, a.Pc, a.mc, wsc);
 #pragma unroll
-    for (int x = 0; x < kHidPer; ++x) {
+    for (int x = 0; x < kFwdHid; ++x) {
       const int e = tid + x * kPhiThreads;
       const int tk = e / h4, j = (e - tk * h4) * 4;
-      if (tk >= kPhiTok) continue;
+      if (tk >= kFwdTok) continue;
       float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
       if (t0 + tk < N) {
-        const float4 v = pre_of(in, x);
+        const float4 v = make_float4((in.ya[x].x + b1.x) + in.yb[x].x, (in.ya[x].y + b1.y) + in.yb[x].y,
+                                     (in.ya[x].z + b1.z) + in.yb[x].z, (in.ya[x].w + b1.w) + in.yb[x].w);
         g = make_float4(gelu_e(v.x), gelu_e(v.y), gelu_e(v.z), gelu_e(v.w));
       }
       float* o = gs + tk * kGld + j;
@@ -159,39 +139,35 @@ __global__ __launch_bounds__(kPhiThreads) void k_phi_fwd(PhiArgs a) {
     }
   }
   __syncthreads();
-  // phi tile: wave w, tokens 16w + ..; 4 n-tiles of 16 outputs per MLP and 16 k-steps per MLP, all fixed (the weight
-  // blocks are zero beyond Pw x m and Pc x mc, so the padding adds nothing); every operand of an MLP is read from LDS
-  // before its 64 MFMAs issue
-  const int r16 = lane & 15, k4 = lane >> 4;
-  const float* ga = gs + (wave * 16 + r16) * kGld;
-  floatx4 acc[2][4];
+  // phi tile of this wave: tokens 16 tb + .., the 4 n-tiles of 16 outputs of MLP `part` over its 16 k-steps (the
+  // weight blocks are zero beyond Pw x m and Pc x mc, so the padding adds nothing)
+  const float* ga = gs + (tb * 16 + r16) * kGld + koff;
+  const float* wsp = part ? wsc : wsw;
+  floatx4 acc[4];
 #pragma unroll
-  for (int part = 0; part < 2; ++part) {
-    const float* wsp = part ? wsc : wsw;
-    const int koff = part ? a.m : 0, kn = part ? a.mc : a.m;
-    float av[kPhiMax / 4], bv[kPhiMax / 4][4];
+  for (int nt = 0; nt < 4; ++nt) acc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < kPhiMax / 4; ++ks) {
-      av[ks] = ks * 4 + k4 < kn ? ga[koff + ks * 4 + k4] : 0.f;   // the tile's other columns are not this MLP's
+  for (int quarter = 0; quarter < 4; ++quarter) {  // 4 k-steps at a time: their operands read, then 16 MFMAs
+    float av[4], bv[4][4];
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) bv[ks][nt] = wsp[(nt * 16 + r16) * kWld + ks * 4 + k4];
+    for (int ks = 0; ks < 4; ++ks) {
+      const int k = (quarter * 4 + ks) * 4 + k4;
+      av[ks] = k < kn ? ga[k] : 0.f;                // the tile's other columns are not this MLP's
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) bv[ks][nt] = wsp[(nt * 16 + r16) * kWld + k];
     }
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) acc[part][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-    for (int ks = 0; ks < kPhiMax / 4; ++ks)
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) acc[part][nt] = mfma4(av[ks], bv[ks][nt], acc[part][nt]);
+      for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma4(av[ks], bv[ks][nt], acc[nt]);
   }
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
     const int cw = nt * 16 + r16;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int64_t row = t0 + wave * 16 + k4 * 4 + q;
-      if (row >= N) continue;
-      if (cw < a.Pw) a.phi[row * P + cw] = acc[0][nt][q] + bias[nt];
-      if (cw < a.Pc) a.phi[row * P + a.Pw + cw] = acc[1][nt][q] + bias[4 + nt];
+      const int64_t row = t0 + tb * 16 + k4 * 4 + q;
+      if (row < N && cw < pn) a.phi[row * P + (part ? a.Pw : 0) + cw] = acc[nt][q] + bias[nt];
     }
   }
 }
@@ -420,7 +396,7 @@ extern "C" int asrn_hash_fwd(const float* y, int64_t ldy, const float* b_word, c
   if (phi_check(a, "asrn_hash_fwd")) return 1;
   const int64_t n = B * L;
   if (n == 0) return 0;
-  hipLaunchKernelGGL(k_phi_fwd, dim3((unsigned)((n + kPhiTok - 1) / kPhiTok)), dim3(kPhiThreads), 0,
+  hipLaunchKernelGGL(k_phi_fwd, dim3((unsigned)((n + kFwdTok - 1) / kFwdTok)), dim3(kPhiThreads), 0,
                      (hipStream_t)stream, a);
   return check_launch("asrn_hash_fwd");
 }
