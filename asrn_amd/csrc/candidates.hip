@@ -22,7 +22,8 @@
 
 namespace asrn {
 
-constexpr int kWavesPerBlock = 4;
+constexpr int kWavesPerBlock = 1;   // a wave's slot frees when its own query ends, and 5.9 KB of LDS a workgroup
+                                    // fits 27 per CU (a 4-wave workgroup's 23.6 KB fits 6: 24 waves)
 constexpr int kMaxSlots = 256;       // T * C
 constexpr int kCh = kMaxSlots / kWave;
 constexpr int kRows = 8;             // rows per half-wave in flight in the feature loops
@@ -61,7 +62,7 @@ constexpr int kHash = 3 * kMaxSlots / 2;   // dedupe hash slots: at most kMaxSlo
 
 struct Scratch {
   int key[kMaxSlots];      // entry: (position << 5) | table
-  uint16_t uid[kMaxSlots]; // entry -> unique
+  uint8_t uid[kMaxSlots];  // entry -> unique (fewer than kMaxSlots = 256)
   int upos[kMaxSlots];     // unique: position
   union {
     struct {
@@ -75,12 +76,15 @@ struct Scratch {
     };
   };
   uint8_t uell[kMaxSlots]; // unique: suffix-match length (query side)
-  int off[40];             // entries of table tau: [off[tau], off[tau + 1])
-  int wrank[32], wlen[32]; // per table: the token's sorted rank and window length
+  int off[36];             // entries of table tau: [off[tau], off[tau + 1]) (T <= 32); table tau's window length
+                           // is off[tau + 1] - off[tau]
+  union {
+    int wrank[32];         // per table: the token's sorted rank (the gather)
+    float tinv[32];        // per table: 1 / softmax denominator (the forward's weights, after the gather)
+  };
   float tsum[32];          // per-table sums (backward); per-table max keys (forward)
-  float tinv[32];          // per-table 1 / softmax denominator (forward)
 };
-// 6.4 KB of LDS per wave: 6 waves per SIMD. The backward's per-unique sums of ds reuse a per-unique array its pass no
+// 5.9 KB of LDS per wave. The backward's per-unique sums of ds reuse a per-unique array its pass no
 // longer needs (uc in the query pass once dp is in registers, ub in the key pass, which has no clock differences).
 
 // order-preserving map of finite floats and -inf to unsigned keys, and back
@@ -280,7 +284,6 @@ __device__ __forceinline__ int gather(const Cand& a, int64_t b, int64_t t, bool 
   if (lane < a.T) {
     S.off[lane] = off;
     S.wrank[lane] = s;
-    S.wlen[lane] = n;
   }
   if (lane == 0) S.off[a.T] = M;
   wave_lds_sync();
@@ -295,7 +298,7 @@ __device__ __forceinline__ int gather(const Cand& a, int64_t b, int64_t t, bool 
       const int i = m - S.off[lo];
       // query window: ranks s - n .. s - 1; key window: s + 1 .. s + n (in range by construction; clamped so that
       // inconsistent inputs cannot read out of bounds)
-      int64_t j = query_window ? (int64_t)S.wrank[lo] - S.wlen[lo] + i : (int64_t)S.wrank[lo] + 1 + i;
+      int64_t j = query_window ? (int64_t)S.wrank[lo] - (S.off[lo + 1] - S.off[lo]) + i : (int64_t)S.wrank[lo] + 1 + i;
       j = j < 0 ? 0 : (j >= a.L ? a.L - 1 : j);
       int pos = a.order[(b * a.T + lo) * a.L + j];
       pos = pos < 0 ? 0 : (pos >= a.L ? (int)a.L - 1 : pos);          // a position whatever the sort left
@@ -399,7 +402,7 @@ __device__ __forceinline__ int dedupe(const Cand& a, int M, Scratch& S) {
       const uint64_t bal = __ballot(prim[c]);
       if (prim[c]) {
         const int u = nu + __popcll(bal & ((1ull << lane) - 1ull));
-        S.uid[m] = (uint16_t)u;
+        S.uid[m] = (uint8_t)u;
         S.upos[u] = S.key[m] >> 5;
       }
       nu += __popcll(bal);
@@ -586,12 +589,12 @@ __device__ __forceinline__ void load_record(const Cand& a, const uint8_t* rec, S
   if (lane <= a.T) S.off[lane] = h;
   if (lane < M) {
     S.key[lane] = e0 >> 8;
-    S.uid[lane] = (uint16_t)(e0 & 255);
+    S.uid[lane] = (uint8_t)(e0 & 255);
   }
   for (int m = kWave + lane; m < M; m += kWave) {
     const int e = e16[m];
     S.key[m] = e >> 8;
-    S.uid[m] = (uint16_t)(e & 255);
+    S.uid[m] = (uint8_t)(e & 255);
   }
   if (lane < NU) {
     S.upos[lane] = p0;
