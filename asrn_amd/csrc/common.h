@@ -14,6 +14,9 @@ constexpr int kWave = 64;
 // ---- error reporting (thread-local last message; every entry point returns 0 on success) -------------------------
 int fail(const char* fmt, ...);
 int check_launch(const char* what);
+// out[c] = sum over g of partial[g * cols + c] (per-workgroup partial rows of parameter gradients), in a fixed order,
+// one launch on `stream`
+int group_sums(const float* partial, int groups, int cols, float* out, hipStream_t stream);
 
 #define ASRN_REQUIRE(cond, ...)            \
   do {                                     \

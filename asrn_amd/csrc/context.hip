@@ -14,7 +14,7 @@
 //   d ln_w = sum_t g xhat, d ln_b = sum_t g, d w_reloj[k] = sum_t du_k hh, d b_reloj[k] = sum_t du_k
 // Forward: a workgroup takes 8 tokens, each wave 2 of them with both rows (float4 per lane) loaded at once. Backward:
 // a workgroup takes 32 tokens, each wave 8 of them, loading 2 tokens' rows at a time; the parameter gradients are
-// per-workgroup partials summed in order by a second launch (deterministic, no atomics).
+// per-workgroup partials summed in a fixed order by a second launch (deterministic, no atomics).
 #include "common.h"
 
 namespace asrn {
@@ -281,25 +281,6 @@ __global__ __launch_bounds__(kCtxThreads, (PROJ && D4 == 1) ? 4 : 1) void k_ctx_
   }
 }
 
-// dparams[c] = sum over workgroups g of partial[g][c]: one workgroup per column (thread-strided runs, then the waves'
-// sums in order)
-__global__ __launch_bounds__(kCtxThreads) void k_ctx_params(const float* __restrict__ partial, int groups, int cols,
-                                                            float* __restrict__ dparams) {
-  __shared__ float ws[kCtxWaves];
-  const int c = blockIdx.x, lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
-  float v = 0.f;
-  for (int g = threadIdx.x; g < groups; g += kCtxThreads) v += partial[(int64_t)g * cols + c];
-  v = wave_sum_u(v);
-  if (lane == 0) ws[wave] = v;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float s = 0.f;
-#pragma unroll
-    for (int w = 0; w < kCtxWaves; ++w) s += ws[w];
-    dparams[c] = s;
-  }
-}
-
 static int64_t ctx_groups(int64_t BL) { return BL > 0 ? (BL + kCtxTok - 1) / kCtxTok : 1; }
 static int64_t ctx_fwd_groups(int64_t BL) { return (BL + kCtxFwdTok - 1) / kCtxFwdTok; }
 
@@ -374,7 +355,5 @@ extern "C" int asrn_context_bwd(const float* h, const float* ln_w, const float* 
     }
   }
   if (check_launch("asrn_context_bwd")) return 1;
-  hipLaunchKernelGGL(k_ctx_params, dim3(cols), dim3(kCtxThreads), 0, st, (const float*)workspace, groups, cols,
-                     dparams);
-  return check_launch("asrn_context_bwd/params");
+  return group_sums((const float*)workspace, groups, cols, dparams, st);
 }

@@ -304,25 +304,6 @@ __global__ __launch_bounds__(kGateThreads) void k_gate_bwd(GateArgs a) {
   }
 }
 
-// dparams[c] = sum over workgroups g of partial[g][c]: one workgroup per column (thread-strided runs, then the
-// waves' sums in order)
-__global__ __launch_bounds__(kGateThreads) void k_gate_params(const float* __restrict__ partial, int groups,
-                                                               int cols, float* __restrict__ dparams) {
-  __shared__ float ws[kGateWaves];
-  const int c = blockIdx.x, lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
-  float v = 0.f;
-  for (int g = threadIdx.x; g < groups; g += kGateThreads) v += partial[(int64_t)g * cols + c];
-  v = wave_sum_u(v);
-  if (lane == 0) ws[wave] = v;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float s = 0.f;
-#pragma unroll
-    for (int w = 0; w < kGateWaves; ++w) s += ws[w];
-    dparams[c] = s;
-  }
-}
-
 static int gate_check(const GateArgs& a, const char* what) {
   ASRN_REQUIRE(a.BL >= 0, "%s: bad sizes", what);
   ASRN_REQUIRE(a.d > 0 && a.d % 4 == 0 && a.d <= 4 * kGateMaxD4 * kWave, "%s: d=%d must be a multiple of 4, <= %d",
@@ -396,7 +377,5 @@ extern "C" int asrn_gate_bwd(const float* h, const void* aporte, int32_t aporte_
     default: hipLaunchKernelGGL(k_gate_bwd<4>, dim3(groups), dim3(kGateThreads), 0, st, a); break;
   }
   if (check_launch("asrn_gate_bwd")) return 1;
-  hipLaunchKernelGGL(k_gate_params, dim3(cols), dim3(kGateThreads), 0, st, (const float*)workspace, groups, cols,
-                     dparams);
-  return check_launch("asrn_gate_bwd/params");
+  return group_sums((const float*)workspace, groups, cols, dparams, st);
 }

@@ -12,6 +12,45 @@ namespace asrn {
 
 constexpr int kColThreads = 256;
 
+// Parameter gradients from per-workgroup partial rows (groups x cols, row-major), one launch: a workgroup of 1024
+// threads takes 64 adjacent columns by 16 row lanes, so each wave reads 256 contiguous bytes of one row. Row lane r
+// sums rows r, r + 16, ... in increasing order, 32 loads in flight, then the row lanes combine in order in LDS.
+constexpr int kGsCols = 64, kGsLanes = 16, kGsBatch = 32;
+__global__ __launch_bounds__(kGsCols * kGsLanes) void k_group_sums(const float* __restrict__ partial, int groups,
+                                                                   int cols, float* __restrict__ out) {
+  __shared__ float red[kGsLanes][kGsCols];
+  const int cl = threadIdx.x % kGsCols, rl = threadIdx.x / kGsCols;
+  const int c = blockIdx.x * kGsCols + cl;
+  float acc = 0.f;
+  if (c < cols) {
+    for (int g0 = rl; g0 < groups; g0 += kGsLanes * kGsBatch) {
+      float v[kGsBatch];
+#pragma unroll
+      for (int j = 0; j < kGsBatch; ++j) {
+        const int g = g0 + j * kGsLanes;
+        v[j] = g < groups ? partial[(int64_t)g * cols + c] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < kGsBatch; ++j) acc += v[j];
+    }
+  }
+  red[rl][cl] = acc;
+  __syncthreads();
+  if (rl == 0 && c < cols) {
+    float s = 0.f;
+#pragma unroll
+    for (int r = 0; r < kGsLanes; ++r) s += red[r][cl];
+    out[c] = s;
+  }
+}
+
+int group_sums(const float* partial, int groups, int cols, float* out, hipStream_t stream) {
+  if (cols <= 0) return 0;
+  hipLaunchKernelGGL(k_group_sums, dim3((unsigned)((cols + kGsCols - 1) / kGsCols)), dim3(kGsCols * kGsLanes), 0,
+                     stream, partial, groups, cols, out);
+  return check_launch("group_sums");
+}
+
 __device__ __forceinline__ float bf16_to_f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
 template <int VEC>
