@@ -7,7 +7,10 @@
 //   1. k_scan_totals: each chunk but the last composes its elements into one total;
 //   2. k_scan_chunks: each chunk composes the totals of the chunks before it (its carry: a wave-parallel fold in a fixed
 //      order), reloads its elements, scans them across the workgroup and stores through the functor.
-// A row that fits one chunk needs only the second launch. Loads and stores go through small functors, so the Hawkes
+// A row that fits one chunk needs only the second launch. So does a row of up to 4,096 elements of the scans whose
+// loads are plain (kOneLaunch: the clock and the affine scan), as one chunk of a 1,024-thread workgroup with 4
+// elements a thread; the Hawkes and streak scans, whose loads are dependent gathers, measured slower that way (8 to 32
+// workgroups cannot hide them: 24 -> 32 us for each backward at cfg2) and keep their 256-element chunks. Loads and stores go through small functors, so the Hawkes
 // and streak scans gather their inputs (key order, clock differences, exp) and scatter their outputs in the same pass.
 // The backward recurrence l_i = g_i + a_{i+1} l_{i+1} is the same scan run from the right. A per-row reduction the
 // functor feeds (d kappa) is summed per chunk, and a third launch adds the chunk sums in a fixed order (deterministic;
@@ -43,9 +46,11 @@ struct Sum64 {
 __device__ __forceinline__ Sum64 cat(const Sum64& x, const Sum64& y) { return {x.s + y.s}; }
 __device__ __forceinline__ Sum64 shfl_up(const Sum64& x, int d) { return {__shfl_up(x.s, d, kWave)}; }
 
-// Exclusive prefix (in thread order) of each thread's element t across the workgroup, and the workgroup's total.
-template <class M>
+// Exclusive prefix (in thread order) of each thread's element t across a workgroup of Threads, and the workgroup's
+// total.
+template <class M, int Threads = kScanThreads>
 __device__ __forceinline__ void block_scan(const M& t, M& excl, M& total, M* lds) {
+  constexpr int kWaves = Threads / kWave;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   M inc = t;
 #pragma unroll
@@ -57,7 +62,7 @@ __device__ __forceinline__ void block_scan(const M& t, M& excl, M& total, M* lds
   __syncthreads();
   M before = M::id(), all = M::id();
 #pragma unroll
-  for (int w = 0; w < kScanWaves; ++w) {
+  for (int w = 0; w < kWaves; ++w) {
     const M x = lds[w];
     if (w < wave) before = cat(before, x);
     all = cat(all, x);
@@ -104,17 +109,19 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_totals(Op op, int64_t N, 
 }
 
 // 2. every chunk of every row (grid: rows x nc): carry from the totals before it, local scan, stores. All loads, the
-// ones the stores need included (the functor's Aux), are issued before the scan's barrier.
-template <class Op, int Items>
-__global__ __launch_bounds__(kScanThreads) void k_scan_chunks(Op op, int64_t N, int nc, const typename Op::M* totals,
-                                                              float* partial) {
+// ones the stores need included (the functor's Aux), are issued before the scan's barrier. With Threads = kRowThreads
+// a chunk is a whole row (nc = 1): the scan's only launch.
+template <class Op, int Items, int Threads = kScanThreads>
+__global__ __launch_bounds__(Threads) void k_scan_chunks(Op op, int64_t N, int nc, const typename Op::M* totals,
+                                                         float* partial) {
   using M = typename Op::M;
-  __shared__ M lds[kScanWaves];
+  constexpr int kWaves = Threads / kWave;
+  __shared__ M lds[kWaves];
   __shared__ M carry_s;
-  __shared__ float red[kScanWaves];
+  __shared__ float red[kWaves];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int row = blockIdx.x / nc, c = blockIdx.x % nc;
-  const int64_t base = ((int64_t)c * kScanThreads + tid) * Items;
+  const int64_t base = ((int64_t)c * Threads + tid) * Items;
   M e[Items];
   typename Op::Aux aux[Items];
   M t = M::id();
@@ -128,7 +135,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_chunks(Op op, int64_t N, 
     if (lane == kWave - 1) carry_s = x;
   }
   M excl, total;
-  block_scan(t, excl, total, lds);   // its barrier also publishes carry_s
+  block_scan<M, Threads>(t, excl, total, lds);   // its barrier also publishes carry_s
   M s = cat(carry_s, excl);
   float acc = 0.f;   // per-thread accumulator for the reduction the functor feeds (d kappa)
 #pragma unroll
@@ -143,7 +150,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_chunks(Op op, int64_t N, 
     if (tid == 0) {
       float sum = 0.f;
 #pragma unroll
-      for (int w = 0; w < kScanWaves; ++w) sum += red[w];
+      for (int w = 0; w < kWaves; ++w) sum += red[w];
       if (nc == 1) op.reduce(row, sum);
       else partial[blockIdx.x] = sum;
     }
@@ -167,6 +174,7 @@ struct NoAux {};
 // ---- plain affine scan ----------------------------------------------------------------------------------------------
 struct PlainFwd {
   static constexpr bool kReduce = false;
+  static constexpr bool kOneLaunch = true;
   using M = Affine;
   using Aux = NoAux;
   const float* a; const float* b; float* S; int64_t N;
@@ -177,6 +185,7 @@ struct PlainFwd {
 
 struct PlainBwd {
   static constexpr bool kReduce = false;
+  static constexpr bool kOneLaunch = true;
   using M = Affine;
   struct Aux { float Sprev; };
   const float* a; const float* Sf; const float* g; float* ga; float* gb; int64_t N;
@@ -208,6 +217,7 @@ struct HawkesCommon {
 
 struct HawkesFwd : HawkesCommon {
   static constexpr bool kReduce = false;
+  static constexpr bool kOneLaunch = false;
   using M = Affine;
   struct Aux { int32_t t; };
   float* hawkes; float* S_sorted;
@@ -238,6 +248,7 @@ struct HawkesFwd : HawkesCommon {
 
 struct HawkesBwd : HawkesCommon {
   static constexpr bool kReduce = true;
+  static constexpr bool kOneLaunch = false;
   using M = Affine;
   struct Aux { float a, dB, Sprev, alfa; bool pass; };
   const float* S_sorted; const float* dh; float* gdB; float* wa; float* dkappa;
@@ -316,6 +327,7 @@ struct StreakCommon {
 
 struct StreakFwd : StreakCommon {
   static constexpr bool kReduce = false;
+  static constexpr bool kOneLaunch = false;
   using M = Affine;
   using Aux = NoAux;
   float* racha;
@@ -326,6 +338,7 @@ struct StreakFwd : StreakCommon {
 
 struct StreakBwd : StreakCommon {
   static constexpr bool kReduce = true;
+  static constexpr bool kOneLaunch = false;
   using M = Affine;
   struct Aux { float a, rprev, beta; };
   const float* racha; const float* dr; double* dbeta; float* dkr;
@@ -349,6 +362,7 @@ struct StreakBwd : StreakCommon {
 // ---- clock: fp64 prefix (or suffix) sums -----------------------------------------------------------------------------
 struct ClockOp {
   static constexpr bool kReduce = false;
+  static constexpr bool kOneLaunch = true;
   using M = Sum64;
   using Aux = NoAux;
   const double* x; double* y; int64_t L; int reverse;
@@ -361,6 +375,8 @@ struct ClockOp {
 
 // ---- launch ---------------------------------------------------------------------------------------------------------
 constexpr int64_t kOneChunk = (int64_t)kScanThreads * 4;   // rows up to this length take one chunk and no workspace
+constexpr int kRowThreads = 1024;
+constexpr int64_t kOneRow = (int64_t)kRowThreads * 4;      // longer rows up to this: one 1024-thread workgroup a row
 constexpr int64_t kAlign = 256;
 constexpr int64_t kScanStaticScratchBytes = int64_t(4) << 20;   // asrn_scan_fwd_static's chunk totals
 constexpr int kMaxScratchDevices = 64;
@@ -368,8 +384,8 @@ constexpr int kMaxScratchDevices = 64;
 static int64_t round_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 // Items per thread: one chunk for a short row; otherwise as many elements per thread as still leaves ~1000 chunks.
-// (One chunk per row of up to 4096 with 16 per thread measured slower than two launches over 256-element chunks: the
-// per-thread chain of gathers, not the launch, is what costs.)
+// (One 256-thread chunk per row of up to 4096, 16 per thread, measured slower than two launches over 256-element
+// chunks: the per-thread chain of gathers, not the launch, is what costs.)
 static int items_for(int64_t rows, int64_t N) {
   if (N <= kOneChunk) return N <= kScanThreads ? 1 : (N <= 2 * kScanThreads ? 2 : 4);
   const int64_t total = rows * N;
@@ -402,8 +418,13 @@ static int launch_scan(const Op& op, int64_t rows, int64_t N, void* ws, int64_t 
   ASRN_REQUIRE(need >= 0, "%s: rows x chunks must stay below 2^31", what);
   ASRN_REQUIRE(need == 0 || (ws != nullptr && wsb >= need), "%s: workspace too small (%lld bytes needed)", what,
                (long long)need);
-  const int items = items_for(rows, N);
   hipStream_t st = (hipStream_t)stream;
+  if (Op::kOneLaunch && N > kOneChunk && N <= kOneRow) {   // one launch: a workgroup per row, 4 elements a thread
+    hipLaunchKernelGGL((k_scan_chunks<Op, 4, kRowThreads>), dim3((unsigned)rows), dim3(kRowThreads), 0, st, op, N, 1,
+                       (const typename Op::M*)nullptr, (float*)nullptr);
+    return check_launch(what);
+  }
+  const int items = items_for(rows, N);
   if (items == 1) launch_items<1>(op, rows, N, (char*)ws, st);
   else if (items == 2) launch_items<2>(op, rows, N, (char*)ws, st);
   else launch_items<4>(op, rows, N, (char*)ws, st);

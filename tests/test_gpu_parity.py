@@ -186,7 +186,7 @@ def test_ngram_vs_oracle(B, L, V, zipf):
 # a9, a11, a12: scans
 # ---------------------------------------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize('N', [1, 2, 3, 7, 64, 1000, 1025, 4097, 10000, 70000])
+@pytest.mark.parametrize('N', [1, 2, 3, 7, 64, 1000, 1025, 4096, 4097, 10000, 70000])
 def test_affine_scan_vs_sequential(N):
     say('scan', N)
     g = torch.Generator().manual_seed(N)
@@ -253,7 +253,7 @@ def test_repetition_golden(name):
     assert_close(glkr, g['rep.g_log_kappa_racha'], 'grad log_kappa_racha')
 
 
-@pytest.mark.parametrize('B,L,n,V', [(2, 1025, 4, 3), (2, 5000, 4, 5), (1, 70000, 3, 8)])
+@pytest.mark.parametrize('B,L,n,V', [(2, 1025, 4, 3), (3, 4096, 4, 4), (2, 5000, 4, 5), (1, 70000, 3, 8)])
 def test_repetition_vs_oracle_long_rows(B, L, n, V):
     """Hawkes and streak scans over rows that span many chunks (the carry between chunks and the chunk-summed d kappa)
     against the oracle's sequential scans, outputs and every gradient."""
