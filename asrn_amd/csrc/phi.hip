@@ -51,19 +51,20 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
 
 // a weight block (rows x cols, row-major) into LDS as ws[r][c] (stride kWld), zero beyond it up to kPhiMax x kPhiMax;
 // every thread's 16 loads are issued before any is stored
+template <int THREADS = kPhiThreads>
 __device__ __forceinline__ void stage_block(const float* __restrict__ W, int rows, int cols, float* ws) {
-  constexpr int kPer = kPhiMax * kPhiMax / kPhiThreads;
+  constexpr int kPer = kPhiMax * kPhiMax / THREADS;
   float v[kPer];
 #pragma unroll
   for (int x = 0; x < kPer; ++x) {
-    const int e = threadIdx.x + x * kPhiThreads, r = e / kPhiMax, c = e % kPhiMax;
+    const int e = threadIdx.x + x * THREADS, r = e / kPhiMax, c = e % kPhiMax;
     const bool ok = r < rows && c < cols;
     v[x] = W[ok ? r * cols + c : 0];
     v[x] = ok ? v[x] : 0.f;
   }
 #pragma unroll
   for (int x = 0; x < kPer; ++x) {
-    const int e = threadIdx.x + x * kPhiThreads;
+    const int e = threadIdx.x + x * THREADS;
     ws[(e / kPhiMax) * kWld + e % kPhiMax] = v[x];
   }
 }
@@ -76,11 +77,11 @@ template <int NG>
 struct HidYN {
   float4 ya[NG], yb[NG];
 };
-template <int NG, int TOK>
+template <int NG, int TOK, int THREADS = kPhiThreads>
 __device__ __forceinline__ void load_hidden_y(const PhiArgs& a, int64_t t0, int64_t N, int h4, HidYN<NG>& in) {
 #pragma unroll
   for (int x = 0; x < NG; ++x) {
-    const int e = threadIdx.x + x * kPhiThreads;
+    const int e = threadIdx.x + x * THREADS;
     const int tk = e / h4, j = (e - tk * h4) * 4;
     const int64_t row = t0 + tk;
     const bool ok = tk < TOK && row < N;
@@ -93,13 +94,15 @@ __device__ __forceinline__ void load_hidden_y(const PhiArgs& a, int64_t t0, int6
 }
 
 
-// The forward takes tiles of kFwdTok = 32 tokens per workgroup of 50 KB of LDS (three per CU): the tile's hidden inputs
-// (4 float4 groups a thread, its column group's bias loaded once), g = gelu into LDS, then wave w forms the 16-token
-// block w & 1 of MLP w >> 1 on the matrix cores (64 MFMAs, operands read 4 k-steps at a time).
-constexpr int kFwdTok = 32;
-constexpr int kFwdHid = kFwdTok * 2 * kPhiMax / 4 / kPhiThreads;     // hidden float4 groups per thread: 4
+// The forward takes tiles of kFwdTok = 64 tokens per workgroup of 8 waves and 66 KB of LDS (two per CU, so that 512
+// tiles, 32,768 tokens, are one round; 32-token tiles at three per CU left a third-full second round): the tile's
+// hidden inputs (4 float4 groups a thread, its column group's bias loaded once), g = gelu into LDS, then wave w forms
+// the 16-token block w & 3 of MLP w >> 2 on the matrix cores (64 MFMAs, operands read 4 k-steps at a time).
+constexpr int kFwdTok = 64;
+constexpr int kFwdThreads = 512;
+constexpr int kFwdHid = kFwdTok * 2 * kPhiMax / 4 / kFwdThreads;     // hidden float4 groups per thread: 4
 
-__global__ __launch_bounds__(kPhiThreads) void k_phi_fwd(PhiArgs a) {
+__global__ __launch_bounds__(kFwdThreads) void k_phi_fwd(PhiArgs a) {
   __shared__ float gs[kFwdTok * kGld];
   __shared__ float wsw[kPhiMax * kWld];
   __shared__ float wsc[kPhiMax * kWld];
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(kPhiThreads) void k_phi_fwd(PhiArgs a) {
   const int64_t N = a.B * a.L, t0 = (int64_t)blockIdx.x * kFwdTok;
   const int h = a.m + a.mc, h4 = h / 4, P = a.Pw + a.Pc;
   const int r16 = lane & 15, k4 = lane >> 4;
-  const int tb = wave & 1, part = wave >> 1;
+  const int tb = wave & 3, part = wave >> 2;
   const int kn = part ? a.mc : a.m, koff = part ? a.m : 0, pn = part ? a.Pc : a.Pw;
   float bias[4];                                   // the second layer's biases of this lane's output columns
 #pragma unroll
@@ -117,15 +120,15 @@ __global__ __launch_bounds__(kPhiThreads) void k_phi_fwd(PhiArgs a) {
   }
   {
     HidYN<kFwdHid> in;
-    load_hidden_y<kFwdHid, kFwdTok>(a, t0, N, h4, in);
+    load_hidden_y<kFwdHid, kFwdTok, kFwdThreads>(a, t0, N, h4, in);
     // every hidden group of thread tid is column group tid % h4 (h4 divides 256): its first-layer bias
     const int jb = (tid % h4) * 4;
     const float4 b1 = *reinterpret_cast<const float4*>(jb >= a.m ? a.bc + (jb - a.m) : a.bp + jb);
-    stage_block(a.Ww, a.Pw, a.m, wsw);
-    stage_block(a.Wc, a.Pc, a.mc, wsc);
+    stage_block<kFwdThreads>(a.Ww, a.Pw, a.m, wsw);
+    stage_block<kFwdThreads>(a.Wc, a.Pc, a.mc, wsc);
 #pragma unroll
     for (int x = 0; x < kFwdHid; ++x) {
-      const int e = tid + x * kPhiThreads;
+      const int e = tid + x * kFwdThreads;
       const int tk = e / h4, j = (e - tk * h4) * 4;
       if (tk >= kFwdTok) continue;
       float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -396,7 +399,7 @@ extern "C" int asrn_hash_fwd(const float* y, int64_t ldy, const float* b_word, c
   if (phi_check(a, "asrn_hash_fwd")) return 1;
   const int64_t n = B * L;
   if (n == 0) return 0;
-  hipLaunchKernelGGL(k_phi_fwd, dim3((unsigned)((n + kFwdTok - 1) / kFwdTok)), dim3(kPhiThreads), 0,
+  hipLaunchKernelGGL(k_phi_fwd, dim3((unsigned)((n + kFwdTok - 1) / kFwdTok)), dim3(kFwdThreads), 0,
                      (hipStream_t)stream, a);
   return check_launch("asrn_hash_fwd");
 }
