@@ -344,9 +344,21 @@ class HashProducer(torch.autograd.Function):
         return (dE, dW, dbw, dbc, dW2w.view(Pw, m), db2w, dW2c.view(Pc, mc), db2c, None, None)
 
 
+# products of more multiply-adds than this go to the library GEMM: the one-tile-per-workgroup kernel wins only while
+# the launch, not the arithmetic, is the cost (d = 256: 7 us; d = 768: 70-105 us against about 10 us in the library)
+SMALL_GEMM_MAX_MACS = 256 ** 3
+
+
+def _mm32(A, B):
+    """fp32 A @ B on the library GEMM, outside any autocast region (operands may be transposed views)."""
+    with torch.autocast(device_type=A.device.type, enabled=False):
+        return A.mm(B)
+
+
 class SmallMatmul(torch.autograd.Function):
     """A @ B for small fp32 matrices (asrn_small_gemm: one workgroup per 16 x 16 tile of the result): the layer's
-    W_o W_v. The backward's dA = dC B^T and dB = A^T dC run on the same kernel."""
+    W_o W_v. The backward's dA = dC B^T and dB = A^T dC run on the same kernel. Products beyond SMALL_GEMM_MAX_MACS
+    multiply-adds (d > 256) run on the library's fp32 GEMM instead, in both directions."""
 
     @staticmethod
     def forward(ctx, A, B):
@@ -355,8 +367,11 @@ class SmallMatmul(torch.autograd.Function):
         (M, K), (K2, N) = A32.shape, B32.shape
         if K != K2:
             raise ValueError(f'SmallMatmul: shapes {tuple(A.shape)} and {tuple(B.shape)} do not chain')
-        C = torch.empty((M, N), dtype=torch.float32, device=dev)
-        call('asrn_small_gemm', ptr(A32), K, 0, ptr(B32), N, 0, ptr(C), N, M, N, K, stream_of(dev))
+        if M * N * K > SMALL_GEMM_MAX_MACS:
+            C = _mm32(A32, B32)
+        else:
+            C = torch.empty((M, N), dtype=torch.float32, device=dev)
+            call('asrn_small_gemm', ptr(A32), K, 0, ptr(B32), N, 0, ptr(C), N, M, N, K, stream_of(dev))
         ctx.save_for_backward(A32, B32)
         ctx.dts = (A.dtype, B.dtype)
         return C
@@ -368,6 +383,12 @@ class SmallMatmul(torch.autograd.Function):
         dev = A.device
         dC = _c(dC, torch.float32)
         dA = dB = None
+        if M * N * K > SMALL_GEMM_MAX_MACS:
+            if ctx.needs_input_grad[0]:
+                dA = _mm32(dC, B.t()).to(ctx.dts[0])
+            if ctx.needs_input_grad[1]:
+                dB = _mm32(A.t(), dC).to(ctx.dts[1])
+            return dA, dB
         if ctx.needs_input_grad[0]:                # (M, K) = dC (M, N) B^T
             dA = torch.empty((M, K), dtype=torch.float32, device=dev)
             call('asrn_small_gemm', ptr(dC), N, 0, ptr(B), N, 1, ptr(dA), K, M, K, N, stream_of(dev))

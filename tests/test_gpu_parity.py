@@ -505,18 +505,22 @@ def test_weight_assembly_is_exact(d, kw):
             assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize('M,N,K', [(256, 256, 256), (33, 70, 129), (1, 17, 5), (512, 96, 768)])
-def test_small_matmul_vs_fp64(M, N, K):
-    """asrn_small_gemm through ops.SmallMatmul (the layer's W_o W_v): the product and both gradients against fp64
-    on the CPU, including sizes that leave partial 16 x 16 tiles."""
-    say('small matmul', M, N, K)
+@pytest.mark.parametrize('M,N,K,autocast', [(256, 256, 256, False), (33, 70, 129, False), (1, 17, 5, False),
+                                            (512, 96, 768, False), (768, 768, 768, False), (768, 768, 768, True)])
+def test_small_matmul_vs_fp64(M, N, K, autocast):
+    """ops.SmallMatmul (the layer's W_o W_v; asrn_small_gemm up to 256^3 multiply-adds, the library's fp32 GEMM beyond):
+    the product and both gradients against fp64 on the CPU, including sizes that leave partial 16 x 16 tiles, and
+    fp32 also when called under bf16 autocast."""
+    say('small matmul', M, N, K, autocast)
     g = torch.Generator().manual_seed(M * N + K)
     A, B, gC = torch.randn(M, K, generator=g), torch.randn(K, N, generator=g), torch.randn(M, N, generator=g)
     Ar, Br = A.double().requires_grad_(), B.double().requires_grad_()
     (Ar @ Br * gC.double()).sum().backward()
     Ad, Bd = A.to(DEV).requires_grad_(), B.to(DEV).requires_grad_()
-    C = ops.SmallMatmul.apply(Ad, Bd)
-    (C * gC.to(DEV)).sum().backward()
+    with torch.autocast(device_type='cuda', dtype=torch.bfloat16, enabled=autocast):
+        C = ops.SmallMatmul.apply(Ad, Bd)
+        (C * gC.to(DEV)).sum().backward()
+    assert C.dtype == torch.float32
     assert_close(C, Ar @ Br, 'C', 1e-5)
     assert_close(Ad.grad, Ar.grad, 'dA', 1e-5)
     assert_close(Bd.grad, Br.grad, 'dB', 1e-5)
