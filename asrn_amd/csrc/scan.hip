@@ -9,9 +9,10 @@
 //      order), reloads its elements, scans them across the workgroup and stores through the functor.
 // A row that fits one chunk needs only the second launch. So does a row of up to 4,096 elements of the scans whose
 // loads are plain (kOneLaunch: the clock and the affine scan), as one chunk of a 1,024-thread workgroup with 4
-// elements a thread; the Hawkes and streak scans, whose loads are dependent gathers, measured slower that way (8 to 32
-// workgroups cannot hide them: 24 -> 32 us for each backward at cfg2) and keep their 256-element chunks. Loads and stores go through small functors, so the Hawkes
-// and streak scans gather their inputs (key order, clock differences, exp) and scatter their outputs in the same pass.
+// elements a thread; the Hawkes and streak scans, whose loads are dependent gathers, measured slower that way (8 to
+// 32 workgroups cannot hide them: 24 -> 32 us for each backward at cfg2) and keep their 256-element chunks. Loads
+// and stores go through small functors, so the Hawkes and streak scans gather their inputs (key order, clock
+// differences, exp) and scatter their outputs in the same pass.
 // The backward recurrence l_i = g_i + a_{i+1} l_{i+1} is the same scan run from the right. A per-row reduction the
 // functor feeds (d kappa) is summed per chunk, and a third launch adds the chunk sums in a fixed order (deterministic;
 // no fences or atomics between workgroups, whose agent-scope release would write back and invalidate the L2).
