@@ -570,16 +570,17 @@ def test_hash_producer_vs_oracle(B, L, d, kw, rows_grad):
 # a0: the context producer
 # ---------------------------------------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize('case', ['plain', 'clamped', 'bf16', 'wide', 'wide20'])
+@pytest.mark.parametrize('case', ['plain', 'clamped', 'bf16', 'wide', 'wide20', 'many'])
 def test_context_vs_oracle(case):
     """LayerNorm + Qc/Kc + the fp32 clock projection with softplus / logsigmoid and the group-A clamps (the fused
     asrn_context_fwd/bwd and the Qc/Kc GEMM, whose input gradient the fp32 backward forms in the kernel) against the
     oracle's context: outputs and the gradients of h and every parameter. 'clamped' drives some tokens past beta_max
     and below log_alfa_min; 'bf16' runs under bf16 autocast (the Qc/Kc GEMM in bf16 with its own backward, the clock
     in fp32), within the bf16 tolerance; 'wide' takes d = 384 (two float4 columns a lane) and 16 + 16 outputs, 'wide20'
-    20 + 20 outputs (more than the kernel forms: the projection's own backward)."""
+    20 + 20 outputs (more than the kernel forms: the projection's own backward); 'many' takes 30,035 tokens, 939
+    per-workgroup partial rows of the parameter gradients (a full and a ragged batch of the fixed-order sum)."""
     say('context', case)
-    B, L, d, cf = {'wide': (3, 301, 384, 16), 'wide20': (3, 301, 384, 20)}.get(case, (2, 777, 96, 16))
+    B, L, d, cf = {'wide': (3, 301, 384, 16), 'wide20': (3, 301, 384, 20), 'many': (5, 6007, 96, 16)}.get(case, (2, 777, 96, 16))
     g = torch.Generator().manual_seed(11)
     sh = O.Shape(d=d, cf=cf)
     prot = O.Prot()
