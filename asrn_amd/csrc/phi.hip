@@ -51,7 +51,7 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
 
 // a weight block (rows x cols, row-major) into LDS as ws[r][c] (stride kWld), zero beyond it up to kPhiMax x kPhiMax;
 // every thread's 16 loads are issued before any is stored
-template <int THREADS = kPhiThreads>
+template <int THREADS = kPhiThreads, int LD = kWld>
 __device__ __forceinline__ void stage_block(const float* __restrict__ W, int rows, int cols, float* ws) {
   constexpr int kPer = kPhiMax * kPhiMax / THREADS;
   float v[kPer];
@@ -65,7 +65,7 @@ __device__ __forceinline__ void stage_block(const float* __restrict__ W, int row
 #pragma unroll
   for (int x = 0; x < kPer; ++x) {
     const int e = threadIdx.x + x * THREADS;
-    ws[(e / kPhiMax) * kWld + e % kPhiMax] = v[x];
+    ws[(e / kPhiMax) * LD + e % kPhiMax] = v[x];
   }
 }
 
@@ -94,18 +94,43 @@ __device__ __forceinline__ void load_hidden_y(const PhiArgs& a, int64_t t0, int6
 }
 
 
-// The forward takes tiles of kFwdTok = 64 tokens per workgroup of 8 waves and 66 KB of LDS (two per CU, so that 512
+// The forward takes tiles of kFwdTok = 64 tokens per workgroup of 8 waves and 67 KB of LDS (two per CU, so that 512
 // tiles, 32,768 tokens, are one round; 32-token tiles at three per CU left a third-full second round): the tile's
 // hidden inputs (4 float4 groups a thread, its column group's bias loaded once), g = gelu into LDS, then wave w forms
 // the 16-token block w & 3 of MLP w >> 2 on the matrix cores (64 MFMAs, operands read 4 k-steps at a time).
 constexpr int kFwdTok = 64;
 constexpr int kFwdThreads = 512;
 constexpr int kFwdHid = kFwdTok * 2 * kPhiMax / 4 / kFwdThreads;     // hidden float4 groups per thread: 4
+// LDS row strides. A wave's 32-bit LDS reads are served 32 lanes at a time over 32 banks (measured: the conflict
+// counter follows that model). The forward's matrix-core loop reads row r16 = lane % 16 at column k4 = lane / 16 of
+// the g tile and of a weight block, so a stride of 2 mod 32 words puts each 32 lanes in distinct banks (the odd
+// strides 129 / 65 gave 1.86 conflict cycles per LDS instruction, these 0.24; the kernel's time did not move).
+#ifndef ASRN_PHI_FWD_GLD
+#define ASRN_PHI_FWD_GLD 130
+#endif
+#ifndef ASRN_PHI_FWD_WLD
+#define ASRN_PHI_FWD_WLD 66
+#endif
+// The backward's matrix-core loops read a weight block and the g / dg tile at row k4 = lane / 16, column r16 = lane %
+// 16, so those rows take a stride of 16 mod 32 words (2.06 -> 0.27 conflict cycles per LDS instruction; 37.0 -> 36.6
+// us at cfg2). The dphi tile keeps kWld: it is read both ways.
+#ifndef ASRN_PHI_BWD_GLD
+#define ASRN_PHI_BWD_GLD 144
+#endif
+#ifndef ASRN_PHI_BWD_WLD
+#define ASRN_PHI_BWD_WLD 80
+#endif
+constexpr int kGldB = ASRN_PHI_BWD_GLD;
+constexpr int kWldW = ASRN_PHI_BWD_WLD;
+static_assert(kGldB >= 2 * kPhiMax && kWldW >= kPhiMax, "rows hold a tile");
+constexpr int kGldF = ASRN_PHI_FWD_GLD;
+constexpr int kWldF = ASRN_PHI_FWD_WLD;
+static_assert(kGldF >= 2 * kPhiMax && kWldF >= kPhiMax, "rows hold a tile");
 
 __global__ __launch_bounds__(kFwdThreads) void k_phi_fwd(PhiArgs a) {
-  __shared__ float gs[kFwdTok * kGld];
-  __shared__ float wsw[kPhiMax * kWld];
-  __shared__ float wsc[kPhiMax * kWld];
+  __shared__ __align__(16) float gs[kFwdTok * kGldF];
+  __shared__ float wsw[kPhiMax * kWldF];
+  __shared__ float wsc[kPhiMax * kWldF];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t N = a.B * a.L, t0 = (int64_t)blockIdx.x * kFwdTok;
   const int h = a.m + a.mc, h4 = h / 4, P = a.Pw + a.Pc;
@@ -124,8 +149,8 @@ __global__ __launch_bounds__(kFwdThreads) void k_phi_fwd(PhiArgs a) {
     // every hidden group of thread tid is column group tid % h4 (h4 divides 256): its first-layer bias
     const int jb = (tid % h4) * 4;
     const float4 b1 = *reinterpret_cast<const float4*>(jb >= a.m ? a.bc + (jb - a.m) : a.bp + jb);
-    stage_block<kFwdThreads>(a.Ww, a.Pw, a.m, wsw);
-    stage_block<kFwdThreads>(a.Wc, a.Pc, a.mc, wsc);
+    stage_block<kFwdThreads, kWldF>(a.Ww, a.Pw, a.m, wsw);
+    stage_block<kFwdThreads, kWldF>(a.Wc, a.Pc, a.mc, wsc);
 #pragma unroll
     for (int x = 0; x < kFwdHid; ++x) {
       const int e = tid + x * kFwdThreads;
@@ -137,14 +162,18 @@ __global__ __launch_bounds__(kFwdThreads) void k_phi_fwd(PhiArgs a) {
                                      (in.ya[x].z + b1.z) + in.yb[x].z, (in.ya[x].w + b1.w) + in.yb[x].w);
         g = make_float4(gelu_e(v.x), gelu_e(v.y), gelu_e(v.z), gelu_e(v.w));
       }
-      float* o = gs + tk * kGld + j;
-      o[0] = g.x; o[1] = g.y; o[2] = g.z; o[3] = g.w;
+      float* o = gs + tk * kGldF + j;
+      if constexpr (kGldF % 4 == 0) {
+        *reinterpret_cast<float4*>(o) = g;
+      } else {
+        o[0] = g.x; o[1] = g.y; o[2] = g.z; o[3] = g.w;
+      }
     }
   }
   __syncthreads();
   // phi tile of this wave: tokens 16 tb + .., the 4 n-tiles of 16 outputs of MLP `part` over its 16 k-steps (the
   // weight blocks are zero beyond Pw x m and Pc x mc, so the padding adds nothing)
-  const float* ga = gs + (tb * 16 + r16) * kGld + koff;
+  const float* ga = gs + (tb * 16 + r16) * kGldF + koff;
   const float* wsp = part ? wsc : wsw;
   floatx4 acc[4];
 #pragma unroll
@@ -157,7 +186,7 @@ __global__ __launch_bounds__(kFwdThreads) void k_phi_fwd(PhiArgs a) {
       const int k = (quarter * 4 + ks) * 4 + k4;
       av[ks] = k < kn ? ga[k] : 0.f;                // the tile's other columns are not this MLP's
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) bv[ks][nt] = wsp[(nt * 16 + r16) * kWld + k];
+      for (int nt = 0; nt < 4; ++nt) bv[ks][nt] = wsp[(nt * 16 + r16) * kWldF + k];
     }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
@@ -175,7 +204,7 @@ __global__ __launch_bounds__(kFwdThreads) void k_phi_fwd(PhiArgs a) {
   }
 }
 
-// The backward loops over tiles of kBwdTok = 32 tokens (blockIdx.x, + gridDim.x, ...) in workgroups of 67 KB of LDS,
+// The backward loops over tiles of kBwdTok = 32 tokens (blockIdx.x, + gridDim.x, ...) in workgroups of 75 KB of LDS,
 // two per CU, so that one workgroup's loads, MFMA and GELU phases overlap another's: the weight blocks are staged once,
 // dg turns into g in place, the tile's hidden inputs are loaded with its dphi (their latency under the dg products),
 // and the parameter gradients accumulate across the workgroup's tiles (the dW MFMA accumulators stay in registers), so
@@ -186,18 +215,18 @@ constexpr int kBwdD = kBwdTok * 2 * kPhiMax / kPhiThreads;           // dphi loa
 static_assert(kBwdTok == 2 * 16, "k_phi_bwd: two 16-token MFMA row blocks per tile");
 
 __global__ __launch_bounds__(kPhiThreads, 2) void k_phi_bwd(PhiArgs a) {
-  __shared__ float ws[2 * kPhiMax * kWld];        // the two weight blocks (outputs x hidden, zero-padded to 64 x 64)
+  __shared__ float ws[2 * kPhiMax * kWldW];        // the two weight blocks (outputs x hidden, zero-padded to 64 x 64)
   __shared__ float dps[kBwdTok * 2 * kWld];       // the dphi tile: word at [0, kWld), context at [kWld, 2 kWld)
-  __shared__ float gs[kBwdTok * kGld];            // dg, then g = gelu(x) in place, in the tile's token rows
+  __shared__ float gs[kBwdTok * kGldB];            // dg, then g = gelu(x) in place, in the tile's token rows
   __shared__ float red[kPhiThreads];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, k4 = lane >> 4;
   const int64_t N = a.B * a.L, ntiles = (N + kBwdTok - 1) / kBwdTok;
   const int h = a.m + a.mc, h4 = h / 4, P = a.Pw + a.Pc;
   float* wsw = ws;
-  float* wsc = ws + kPhiMax * kWld;
-  stage_block(a.Ww, a.Pw, a.m, wsw);
-  stage_block(a.Wc, a.Pc, a.mc, wsc);
+  float* wsc = ws + kPhiMax * kWldW;
+  stage_block<kPhiThreads, kWldW>(a.Ww, a.Pw, a.m, wsw);
+  stage_block<kPhiThreads, kWldW>(a.Wc, a.Pc, a.mc, wsc);
   floatx4 dWacc[2][4];                            // this wave's output rows 16w .. 16w + 15 of both dW2 blocks
 #pragma unroll
   for (int part = 0; part < 2; ++part)
@@ -257,7 +286,7 @@ __global__ __launch_bounds__(kPhiThreads, 2) void k_phi_bwd(PhiArgs a) {
           const int k = (quarter * 4 + ks) * 4 + k4;
           av[ks] = da[k];
 #pragma unroll
-          for (int nt = 0; nt < 4; ++nt) bv[ks][nt] = wsp[k * kWld + nt * 16 + r16];
+          for (int nt = 0; nt < 4; ++nt) bv[ks][nt] = wsp[k * kWldW + nt * 16 + r16];
         }
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
@@ -270,7 +299,7 @@ __global__ __launch_bounds__(kPhiThreads, 2) void k_phi_bwd(PhiArgs a) {
         const int col = nt * 16 + r16;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          if (col < kn) gs[(tb * 16 + k4 * 4 + q) * kGld + off + col] = acc[nt][q];
+          if (col < kn) gs[(tb * 16 + k4 * 4 + q) * kGldB + off + col] = acc[nt][q];
       }
     }
     __syncthreads();
@@ -282,7 +311,7 @@ __global__ __launch_bounds__(kPhiThreads, 2) void k_phi_bwd(PhiArgs a) {
       const int tk = e / h4, j = (e - tk * h4) * 4;
       if (tk >= kBwdTok) continue;
       const int64_t row = t0 + tk;
-      float* d = gs + tk * kGld + j;
+      float* d = gs + tk * kGldB + j;
       float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
       if (row < N) {
         const int64_t t = row % a.L;
@@ -318,7 +347,7 @@ __global__ __launch_bounds__(kPhiThreads, 2) void k_phi_bwd(PhiArgs a) {
           const int tk = (quarter * 4 + ks) * 4 + k4;
           aw[ks] = dps[tk * 2 * kWld + orow];
           ac[ks] = dps[tk * 2 * kWld + kWld + orow];
-          const float* gr = gs + tk * kGld;
+          const float* gr = gs + tk * kGldB;
 #pragma unroll
           for (int nt = 0; nt < 4; ++nt) {
             const int col = nt * 16 + r16;
@@ -404,7 +433,7 @@ extern "C" int asrn_hash_fwd(const float* y, int64_t ldy, const float* b_word, c
   return check_launch("asrn_hash_fwd");
 }
 
-// the backward's workgroups: at most kBwdGroups (two of 67 KB LDS fit a CU), fewer for short inputs
+// the backward's workgroups: at most kBwdGroups (two of 75 KB LDS fit a CU), fewer for short inputs
 #ifndef ASRN_PHI_BWD_GROUPS
 #define ASRN_PHI_BWD_GROUPS 512
 #endif
