@@ -114,6 +114,18 @@ __device__ __forceinline__ int64_t token_of_wave() {
   return blk * kWavesPerBlock + (threadIdx.x >> 6);
 }
 
+// The whole-text kernels take their tokens in one table's sorted order (table ASRN_SORTED_TABLE, the last one when
+// negative): the waves that run together on an XCD are then mostly mates of a few buckets, whose candidate lists
+// overlap, instead of a stretch of positions whose candidates spread over the whole row, so L2 keeps their rows.
+#ifndef ASRN_SORTED_MAP
+#define ASRN_SORTED_MAP 1
+#endif
+#ifndef ASRN_SORTED_TABLE
+#define ASRN_SORTED_TABLE 0
+#endif
+struct Cand;
+__device__ __forceinline__ int64_t sorted_token_of_wave(const Cand& a);
+
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -810,7 +822,7 @@ template <int F4, int DCH, int RB>
 __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 6 : 1) void k_cand_fwd(Cand a) {   // 6 waves per SIMD when narrow
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
-  const int64_t tok = token_of_wave();
+  const int64_t tok = sorted_token_of_wave(a);
   if (tok >= a.B * a.L) return;
   float* salida_row = const_cast<float*>(rows_at<RB >= 1>(a.salida, tok * a.d));   // bf16 with the value rows
   forward_token<F4, DCH, false, RB>(a, tok / a.L, tok % a.L, S, salida_row, a.signals + tok * 4,
@@ -887,7 +899,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   constexpr bool B16 = RB >= 1, FB16 = RB == 2;
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
-  const int64_t tok = token_of_wave();
+  const int64_t tok = sorted_token_of_wave(a);
   if (tok >= a.B * a.L) return;
   const int lane = lane_id(), half = lane >> 5;
   const int64_t b = tok / a.L, t = tok % a.L;
@@ -1050,7 +1062,7 @@ void k_cand_bwd_k(Cand a) {
   constexpr bool B16 = RB >= 1, FB16 = RB == 2;
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
-  const int64_t tok = token_of_wave();
+  const int64_t tok = sorted_token_of_wave(a);
   if (tok >= a.B * a.L) return;
   const int lane = lane_id(), half = lane >> 5;
   const int64_t b = tok / a.L, k = tok % a.L;
@@ -1164,6 +1176,16 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_lists(Cand a, i
       ell[o] = i >= 0 ? suffix_len_of(sigb, mine, t, k, a.K) : -1;
     }
   }
+}
+
+__device__ __forceinline__ int64_t sorted_token_of_wave(const Cand& a) {
+  const int64_t i = token_of_wave();
+  if (!ASRN_SORTED_MAP || i >= a.B * a.L) return i;
+  const int64_t b = i / a.L, r = i - b * a.L;
+  const int tab = ASRN_SORTED_TABLE < 0 ? a.T - 1 : (ASRN_SORTED_TABLE < a.T ? ASRN_SORTED_TABLE : 0);
+  int p = a.order[(b * a.T + tab) * a.L + r];            // a permutation of the row's positions (the bucket sort's)
+  p = p < 0 ? 0 : (p >= a.L ? (int)a.L - 1 : p);        // clamped so that inconsistent inputs stay in bounds
+  return b * a.L + p;
 }
 
 static int check_args(const Cand& a, const char* what) {
