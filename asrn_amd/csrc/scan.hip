@@ -412,10 +412,18 @@ static void launch_items(const Op& op, int64_t rows, int64_t N, char* ws, hipStr
                        (const float*)partial);
 }
 
+// The chunk totals a scan of this op and size needs: none where it runs as one launch (a short row, or a row of up
+// to kOneRow for the ops whose loads are plain), else asrn_scan_workspace's bound.
+template <typename Op>
+static int64_t scan_need(int64_t rows, int64_t N) {
+  if (Op::kOneLaunch && N > kOneChunk && N <= kOneRow) return 0;
+  return asrn_scan_workspace(rows, N);
+}
+
 template <typename Op>
 static int launch_scan(const Op& op, int64_t rows, int64_t N, void* ws, int64_t wsb, void* stream, const char* what) {
   if (rows == 0 || N == 0) return 0;
-  const int64_t need = asrn_scan_workspace(rows, N);
+  const int64_t need = scan_need<Op>(rows, N);
   ASRN_REQUIRE(need >= 0, "%s: rows x chunks must stay below 2^31", what);
   ASRN_REQUIRE(need == 0 || (ws != nullptr && wsb >= need), "%s: workspace too small (%lld bytes needed)", what,
                (long long)need);
@@ -490,7 +498,7 @@ extern "C" int64_t asrn_scan_static_scratch_bytes(void) { return kScanStaticScra
 extern "C" int asrn_scan_fwd_static(const float* a, const float* b, float* S, int64_t rows, int64_t N, void* stream) {
   const char* what = "asrn_scan_fwd_static";
   ASRN_REQUIRE(rows >= 0 && N >= 0, "%s: bad sizes", what);
-  const int64_t need = asrn_scan_workspace(rows, N);
+  const int64_t need = scan_need<PlainFwd>(rows, N);    // 0 where the scan runs as one launch
   ASRN_REQUIRE(need >= 0 && need <= kScanStaticScratchBytes,
                "%s: rows=%lld, N=%lld need %lld bytes of chunk totals, beyond the library's %lld-byte static scratch "
                "(call asrn_scan_fwd with a workspace instead)", what, (long long)rows, (long long)N, (long long)need,

@@ -41,12 +41,19 @@ class Shape:
 
 @dataclasses.dataclass(frozen=True)
 class Prot:
-    """Group-A protections (estable:57-66) plus the optional group-B ones."""
+    """Group-A protections (estable:57-66) plus the optional group-B ones. ninguna(): none of them, the core layer's
+    v89 numerics (estable:68-71; nucleo.CapaASRN computes the same, asrn/__init__.py:84)."""
     beta_max: float = 1e4
     log_alfa_min: float = -30.0
     mejor_max: float = 1e4
     tope_puerta: float = None
     kappa_min: float = None
+    mascara_exacta: bool = True
+    reloj_64: bool = True
+
+    @classmethod
+    def ninguna(cls):
+        return cls(beta_max=None, log_alfa_min=None, mejor_max=None, mascara_exacta=False, reloj_64=False)
 
 
 def shape_from_params(p, d, **kw):
@@ -114,13 +121,14 @@ def phi_and_values(p, E):
 
 
 def context(p, h, sh, prot):
-    """Qc, Kc (B, L, cf), beta (B, L) fp64, log_alfa (B, L) fp32 (estable:153-194, its CPU branches). Without
-    autocast: one GEMM for cq, ck and the clock projection (estable:181-185). Under autocast: Qc, Kc from the 16-bit
-    LayerNorm output, the clock projection apart in fp32 with autocast off (estable:176-180)."""
+    """Qc, Kc (B, L, cf), beta (B, L) fp64 (fp32 without reloj_64), log_alfa (B, L) fp32 (estable:153-194, its CPU
+    branches). Without autocast: one GEMM for cq, ck and the clock projection (estable:181-185). Under autocast: Qc, Kc
+    from the 16-bit LayerNorm output, the clock projection apart in fp32 with autocast off (estable:176-180); without
+    reloj_64 the one GEMM in 16 bits, the clock projection rounded to 16 bits too (estable:181-185, nucleo:702-706)."""
     cf = sh.cf
     hh32 = F.layer_norm(h, (h.shape[-1],), p['ln_ctx.weight'], p['ln_ctx.bias'])
     hh = _autocast(hh32)
-    if hh.dtype != hh32.dtype:
+    if hh.dtype != hh32.dtype and prot.reloj_64:
         y = F.linear(hh, torch.cat([p['cq.weight'], p['ck.weight']]))
         with torch.autocast(device_type='cpu', enabled=False):
             u = F.linear(hh32.float(), p['w_reloj'].float(), p['b_reloj'].float())
@@ -130,14 +138,15 @@ def context(p, h, sh, prot):
 
 
 def _clock(y, u, cf, prot):
-    """beta = min(softplus(u_0), beta_max) in fp64 and log_alfa = max(logsigmoid(u_1) + log 2, min) (estable:186-193)."""
+    """beta = min(softplus(u_0), beta_max) and log_alfa = max(logsigmoid(u_1) + log 2, min) (estable:186-193); beta
+    in fp64 with reloj_64, else fp32 (its cumsum then gives the fp32 clock)."""
     beta = F.softplus(u[..., 0])
     log_alfa = F.logsigmoid(u[..., 1]) + math.log(2)
     if prot.beta_max is not None:
         beta = beta.clamp(max=prot.beta_max)
     if prot.log_alfa_min is not None:
         log_alfa = log_alfa.clamp(min=prot.log_alfa_min)
-    return y[..., :cf], y[..., cf:2 * cf], beta.double(), log_alfa
+    return y[..., :cf], y[..., cf:2 * cf], (beta.double() if prot.reloj_64 else beta), log_alfa
 
 
 # ----------------------------------------------------------------------------------------------------------------
@@ -183,9 +192,12 @@ def candidate_lists_bruteforce(ids_rows, C):
 # a3-a8: candidate attention (forward; autograd gives the backward)
 # ----------------------------------------------------------------------------------------------------------------
 
-def candidates(phi, V, Qc, Kc, Bt, log_alfa, sig, w_suf, gamma, sh):
+def candidates(phi, V, Qc, Kc, Bt, log_alfa, sig, w_suf, gamma, sh, prot=None):
     """Candidate attention of all tables in bucket-sorted space (estable:204-272, group A: exact mask and the fp64
-    clock difference of _TiempoRelativo estable:101-118).
+    clock difference of _TiempoRelativo estable:101-118). Without reloj_64 the clock term is formed as
+    (log alfa_k + rate B_k) - rate B_q in the clock's own (fp32) type (estable:266-267, nucleo:815-817); without
+    mascara_exacta the invalid keys of the window score -1e9 and the softmax runs over the whole window, so they take
+    weight when every valid score sinks toward -1e9 (estable:121-133, nucleo:819-823).
 
     Each row (b, tau) is stably sorted by bucket, prefixed by one block of C empty slots and cut into blocks of C. A
     query at sorted rank s scores the keys of its own block and of the block before; a key is valid when it has the
@@ -229,8 +241,18 @@ def candidates(phi, V, Qc, Kc, Bt, log_alfa, sig, w_suf, gamma, sh):
     ell = suffix_len(flatq(pfq).unsqueeze(2), flatq(pfk).unsqueeze(1))            # (W, C, 2C)
     sc = sc + w_suf[ell]
     rate = (gamma / C).repeat(B).view(BT, 1, 1, 1).expand(BT, R - 1, 1, 1).reshape(-1, 1, 1)
-    dt = (flatq(Bk).squeeze(-1).unsqueeze(1) - flatq(Bq).squeeze(-1).unsqueeze(2)).to(torch.float32)
-    sc = sc + flatq(lak).squeeze(-1).unsqueeze(1) + dt * rate
+    if prot is None or prot.reloj_64:
+        dt = (flatq(Bk).squeeze(-1).unsqueeze(1) - flatq(Bq).squeeze(-1).unsqueeze(2)).to(torch.float32)
+        sc = sc + flatq(lak).squeeze(-1).unsqueeze(1) + dt * rate
+    else:
+        # formed on each sorted row before it is cut into windows, as the reference does (estable:266-267): the two
+        # large sums that make d gamma (sum ds B_k - sum ds B_q) then accumulate in the reference's order
+        rate_row = (gamma / C).repeat(B).unsqueeze(1)                            # (BT, 1)
+        B_row = srt(Bt.unsqueeze(-1)).reshape(BT, S)
+        la_row = srt(log_alfa.unsqueeze(-1)).reshape(BT, S)
+        _, keyk = qk((la_row + rate_row * B_row).view(BT, R, C, 1))
+        qq, _ = qk((rate_row * B_row).view(BT, R, C, 1))
+        sc = sc + flatq(keyk).squeeze(-1).unsqueeze(1) - flatq(qq).squeeze(-1).unsqueeze(2)
 
     ii = torch.arange(C).unsqueeze(1)
     jj = torch.arange(2 * C)
@@ -240,9 +262,7 @@ def candidates(phi, V, Qc, Kc, Bt, log_alfa, sig, w_suf, gamma, sh):
     valid = (flatq(idq).squeeze(-1).unsqueeze(2) == flatq(idk).squeeze(-1).unsqueeze(1)) \
         & flatq(rk).squeeze(-1).unsqueeze(1) & band
     hay = valid.any(-1, keepdim=True)
-    mx = sc.detach().masked_fill(~valid, float('-inf')).amax(-1, keepdim=True)
-    ref = torch.where(hay, mx, torch.zeros_like(mx))
-    att = torch.softmax((sc - ref).masked_fill(~valid, PROHIBIDO), dim=-1) * hay
+    att, mx = masked_softmax(sc, valid, hay, prot)
     out = torch.bmm(att, flatq(vk))                                              # (W, C, d)
 
     # back to text order, summed over the tables (the forward of _DesordenarSumar, nucleo:116-133)
@@ -255,13 +275,26 @@ def candidates(phi, V, Qc, Kc, Bt, log_alfa, sig, w_suf, gamma, sh):
     return salida, sen
 
 
-def candidates_at(phi, V, Qc, Kc, Bt, log_alfa, sig, w_suf, gamma, sh, ids, queries):
+def masked_softmax(sc, valid, hay, prot):
+    """(att, the per-row max score) over the last dimension (estable:121-138). Exact mask: the max over the valid
+    scores is subtracted first and invalid keys weigh exactly 0. Without mascara_exacta (v89): invalid keys score
+    -1e9 and the softmax and the max run over every key."""
+    if prot is None or prot.mascara_exacta:
+        mx = sc.detach().masked_fill(~valid, float('-inf')).amax(-1, keepdim=True)
+        ref = torch.where(hay, mx, torch.zeros_like(mx))
+        return torch.softmax((sc - ref).masked_fill(~valid, PROHIBIDO), dim=-1) * hay, mx
+    scm = sc.masked_fill(~valid, max(PROHIBIDO, torch.finfo(sc.dtype).min))
+    return torch.softmax(scm, dim=-1) * hay, scm.detach().amax(-1, keepdim=True)
+
+
+def candidates_at(phi, V, Qc, Kc, Bt, log_alfa, sig, w_suf, gamma, sh, ids, queries, prot=None):
     """The candidate attention of selected queries only, one query at a time (estable:204-272 restated per query, for
     shapes where the sorted-window form above would not fit in memory). ids (B, L, T): the bucket ids; queries
     (nq, 2) int64: (b, t) pairs. A query's candidates in table tau are the <= C most recent earlier positions with
     its bucket (the set the sorted window nucleo:809-812 keeps), found from a stable sort of each (b, tau) row.
     Returns salida (nq, d) summed over tables and the per-table signals (nq, T, 3) = (hay, valid max, max weight);
-    autograd reaches every input through the gathers."""
+    autograd reaches every input through the gathers. prot: as in candidates(), except that the C candidates are the
+    whole window here, so v89's fill leaks only into empty slots (the block window's other keys are not formed)."""
     B, L, P = phi.shape
     T, C, cf, K = sh.T, sh.C, sh.cf, sh.K
     ids = np.asarray(ids)
@@ -291,12 +324,14 @@ def candidates_at(phi, V, Qc, Kc, Bt, log_alfa, sig, w_suf, gamma, sh, ids, quer
     sc = sc + (Qc[bq, tq].unsqueeze(1).unsqueeze(1) * Kc[bk, pk]).sum(-1) * cf ** -0.5
     ell = suffix_len(Pf[bq, tq].unsqueeze(1).unsqueeze(1), Pf[bk, pk])
     sc = sc + w_suf[ell]
-    dt = (Bt[bk, pk] - Bt[bq, tq].view(nq, 1, 1)).to(torch.float32)
-    sc = sc + log_alfa[bk, pk] + dt * (gamma / C).view(1, T, 1)
+    rate = (gamma / C).view(1, T, 1)
+    if prot is None or prot.reloj_64:
+        dt = (Bt[bk, pk] - Bt[bq, tq].view(nq, 1, 1)).to(torch.float32)
+        sc = sc + log_alfa[bk, pk] + dt * rate
+    else:
+        sc = sc + (log_alfa[bk, pk] + rate * Bt[bk, pk]) - rate * Bt[bq, tq].view(nq, 1, 1)
     hay = vk.any(-1, keepdim=True)
-    mx = sc.detach().masked_fill(~vk, float('-inf')).amax(-1, keepdim=True)
-    ref = torch.where(hay, mx, torch.zeros_like(mx))
-    att = torch.softmax((sc - ref).masked_fill(~vk, PROHIBIDO), dim=-1) * hay
+    att, mx = masked_softmax(sc, vk, hay, prot)
     salida = (att.unsqueeze(-1) * V[bk, pk]).sum(2).sum(1)
     sen = torch.cat([hay.float(), torch.where(hay, mx, torch.full_like(mx, PROHIBIDO)).float(),
                      att.detach().amax(-1, keepdim=True).float()], dim=-1)
@@ -446,12 +481,13 @@ def combine(p, acc, h, sh, prot):
 
 
 def layer_forward(p, E, h, x, sh, prot=Prot()):
-    """h' = CapaASRNEstable.forward(E, h, x) (estable:407-421)."""
+    """h' = CapaASRNEstable.forward(E, h, x) (estable:407-421); with Prot.ninguna() the core layer's
+    (nucleo.CapaASRN.forward, nucleo:880-885)."""
     sig = firmas(x) if x is not None else E.float() @ p['r_firma'].float()
     Qc, Kc, beta, log_alfa = context(p, h, sh, prot)
     Bt = beta.cumsum(1)
     phi, V = phi_and_values(p, E)
-    salida, sen = candidates(phi, V, Qc, Kc, Bt, log_alfa, sig, p['w_sufijo'], p['gamma'], sh)
+    salida, sen = candidates(phi, V, Qc, Kc, Bt, log_alfa, sig, p['w_sufijo'], p['gamma'], sh, prot)
     acc = gate_signals(salida, sen, sh.T, sh.Tc)
     acc.update(repetition(p, sig, beta, Bt, log_alfa, sh, prot))
     return combine(p, acc, h, sh, prot)

@@ -39,9 +39,17 @@ def shape_of(params, meta):
     return shape_from_params(params, meta['d'], n_bits=kw.get('n_bits', 14), **extra)
 
 
+def nucleo(meta):
+    """Whether a fixture was written by the unprotected core layer (nucleo.CapaASRN, asrn.ASRNCoreLayer)."""
+    return meta['extra'].get('clase') == 'nucleo'
+
+
 def prot(meta):
-    """The oracle's protections for a fixture: group A, plus group B (estable:72-77) for a 'textos_largos' case."""
+    """The oracle's protections for a fixture: group A, plus group B (estable:72-77) for a 'textos_largos' case, none
+    for a core-layer case."""
     from oracle.layer import Prot
+    if nucleo(meta):
+        return Prot.ninguna()
     if meta['extra'].get('prot') == 'textos_largos':
         return Prot(tope_puerta=10.0, kappa_min=1.0 / (4 * meta['extra']['largo']))
     return Prot()
@@ -50,6 +58,8 @@ def prot(meta):
 def protecciones(meta):
     """The HIP layer's Protecciones for a fixture (the same choice as prot)."""
     from asrn_amd.capa import Protecciones
+    if nucleo(meta):
+        return Protecciones.ninguna()
     if meta['extra'].get('prot') == 'textos_largos':
         return Protecciones.textos_largos(meta['extra']['largo'])
     return Protecciones()
@@ -63,3 +73,9 @@ def cpu_autocast(meta):
     if meta['extra'].get('autocast') == 'bf16':
         return torch.autocast('cpu', dtype=torch.bfloat16)
     return contextlib.nullcontext()
+
+
+def stage_input(g, k):
+    """A candidate-stage input of a fixture: the stage output of that name, except the clock when the fixture ran its
+    candidate stage on a moved clock (acc.Bt)."""
+    return g['acc.Bt'] if k == 'Bt' and 'acc.Bt' in g else g[k]

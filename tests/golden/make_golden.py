@@ -3,7 +3,8 @@
 The reference (KIROKOWA/ASRN, pure Python on PyTorch) is imported here, in the build container only, for the parts
 of its hot path that no closed form or definition pins: the full composition of CapaASRNEstable.forward and its
 gradients (asrn/estable.py:407-421), its candidate-attention stage with its gradients (estable:204-272), and its
-repetition stage (estable:304-321) with the reference's own rounding order. Each fixture holds only data: the
+repetition stage (estable:304-321) with the reference's own rounding order; and the same for the unprotected core
+layer (asrn/nucleo.py:574-886, CapaASRN = asrn.ASRNCoreLayer). Each fixture holds only data: the
 inputs, the layer's state_dict, every intermediate the hot path produces and the gradients. Nothing from the
 reference itself is stored.
 
@@ -35,6 +36,17 @@ CASES = [
     # bf16 autocast on the CPU (the reference's own bf16 case, tests/test_nucleo.py:476: d 64, default tables,
     # B 2, L 160): the layer and its stages under torch.autocast('cpu', bfloat16), and the fp32 layer beside it
     ('j_bf16_d64_L160', dict(), 64, 2, 160, 12, {'autocast': 'bf16'}),
+    # the unprotected core layer (asrn.ASRNCoreLayer = nucleo.CapaASRN, v89 numerics: the fp32 clock with the score's
+    # clock term formed as (log alfa_k + rate B_k) - rate B_q, the -1e9 fill instead of the exact mask, no clamps) on
+    # ordinary inputs, and with gamma = 1e9, where every valid score of a query sinks below -1e9 and the fill leaks
+    # weight to invalid keys (the case the protected layer exists for, estable:20-24)
+    ('k_nucleo_d64_L150', dict(), 64, 2, 150, 12, {'clase': 'nucleo'}),
+    ('l_nucleo_c16_nb4_L120', dict(chunk=16, n_bits=4), 32, 2, 120, 9, {'clase': 'nucleo'}),
+    ('m_nucleo_gamma_huge', dict(chunk=16, n_bits=3), 32, 1, 96, 7, {'clase': 'nucleo', 'gamma_fill': 1e9}),
+    # the candidate stage with the clock moved by a constant (acc.Bt = Bt + 4e5): only clock differences enter the
+    # scores, but the core layer's fp32 form (log alfa_k + rate B_k) - rate B_q rounds at ulp(rate B) ~ 1e-3 there,
+    # which tells it apart from the difference form
+    ('n_nucleo_reloj_desplazado', dict(chunk=16, n_bits=4), 32, 2, 120, 9, {'clase': 'nucleo', 'reloj_extra': 4e5}),
 ]
 
 
@@ -51,7 +63,10 @@ def build(ref_root, only=()):
             continue
         torch.manual_seed(0)
         prot = est.Protecciones.textos_largos(extra['largo']) if extra.get('prot') == 'textos_largos' else None
-        capa = est.CapaASRNEstable(d, protecciones=prot, **kw)
+        if extra.get('clase') == 'nucleo':
+            capa = v89.CapaASRN(d, **kw)
+        else:
+            capa = est.CapaASRNEstable(d, protecciones=prot, **kw)
         with torch.no_grad():
             g = torch.Generator().manual_seed(1)
             for n, p in capa.named_parameters():
@@ -107,9 +122,13 @@ def build(ref_root, only=()):
         out.update(sig=sig, Qc=Qc, Kc=Kc, beta=beta, log_alfa=la, Bt=Bt, phi=phi, V=Vv, ids=ids,
                    orden=orden, claves=claves, orden_k=ok, repetido=rep.to(torch.uint8))
 
-        # candidate stage with its own gradients: phi and V enter as leaves
+        # candidate stage with its own gradients: phi and V enter as leaves (the clock moved by reloj_extra when given,
+        # kept as acc.Bt)
+        Bt_acc = Bt + extra['reloj_extra'] if 'reloj_extra' in extra else Bt
+        if 'reloj_extra' in extra:
+            out['acc.Bt'] = Bt_acc
         leaves = {k: t.clone().requires_grad_() for k, t in
-                  dict(phi=phi, V=Vv, Qc=Qc, Kc=Kc, Bt=Bt, log_alfa=la).items()}
+                  dict(phi=phi, V=Vv, Qc=Qc, Kc=Kc, Bt=Bt_acc, log_alfa=la).items()}
         orig = capa._phi_y_valores
         capa._phi_y_valores = lambda _E: (leaves['phi'], leaves['V'])
         capa.zero_grad()

@@ -98,6 +98,11 @@ SAMPLER_CASES = [
     dict(V=1000, T=0.8, k=0, p=0.0, pena=1.0, ventana=64, nb=0, nq=0),
     dict(V=10000, T=0.9, k=100, p=0.95, pena=1.2, ventana=32, nb=2, nq=3),
     dict(V=70000, T=0.9, k=100, p=0.95, pena=1.2, ventana=32, nb=2, nq=3),
+    # the whole-row branch: V past the register rows with no top-k cut, and more tokens kept at the top-k cut than
+    # the LDS candidate list holds (4,096)
+    dict(V=50304, T=0.9, k=0, p=0.9, pena=1.1, ventana=64, nb=3, nq=4),
+    dict(V=20000, T=1.0, k=5000, p=1.0, pena=1.0, ventana=64, nb=0, nq=0),
+    dict(V=30000, T=0.8, k=4500, p=0.7, pena=1.3, ventana=16, nb=2, nq=0),
     # contexts with more distinct successors than the inline lists hold: the bans and the quote mask probe every token
     dict(V=20, T=0.7, k=0, p=1.0, pena=1.0, ventana=64, nb=1, nq=2),
     dict(V=50, T=1.0, k=5, p=0.9, pena=1.0, ventana=64, nb=1, nq=2),

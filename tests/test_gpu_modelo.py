@@ -313,3 +313,58 @@ def test_entrenar_writes_and_resumes():
                                  registro=lineas.append, semilla=5)
         assert [h['paso'] for h in hist if 'perdida' in h] == [1, 2, 3, 4]
         assert any('resuming from step 2' in s for s in lineas)
+
+
+def test_configs3_model_step_bf16():
+    """the whole d = 768 LM (V 50,304, 12 local blocks, an ASRN layer after every second one: 6 layers, tied
+    head), B 8 x N 2,048, bf16 autocast over fp32 weights, fused AdamW, clipping at 1.0. From the same weights and
+    AdamW state, PasoGrafado's replayed step computes its eager step's loss, gradient norm and every parameter's
+    gradient to 1e-3 relative (both brought back to the same state after each step); two replays from one state are
+    bit-identical; every loss is finite; and the loss falls over 5 steps on one batch."""
+    kw = dict(V=50304, d=768, n_capas=12, largo_cada=2, semilla=0)
+    B, N = 8, 2048
+    say('configs[3] model step, bf16', kw, B, N)
+    m1 = asrn_amd.crear_modelo(**kw).to(DEV).train()
+    assert len(m1.largos) == 6
+    m2 = copy.deepcopy(m1)
+    o1 = asrn_amd.crear_optimizador(m1, lr=1e-3, capturable=True)
+    o2 = asrn_amd.crear_optimizador(m2, lr=1e-3, capturable=True)
+    ansioso = asrn_amd.PasoGrafado(m1, o1, B, N, precision='bf16', grabar=False)
+    grafo = asrn_amd.PasoGrafado(m2, o2, B, N, precision='bf16', calentar=2)
+    w = synth.tokens(4 * B, N + 1, kw['V'], frac=0.15, span=(8, 128), zipf=1.1, seed=21).to(DEV)
+    lotes = [(w[B * i:B * i + B, :-1].contiguous(), w[B * i:B * i + B, 1:].contiguous()) for i in range(4)]
+    for i, (x, y) in enumerate(lotes):             # 2 side-stream steps, the capture, a replay
+        a = [float(v) for v in ansioso(x, y, lr=1e-3)]
+        b = [float(v) for v in grafo(x, y, lr=1e-3)]
+        torch.cuda.synchronize()
+        peor = _peor_grad(m1, m2)
+        print(i, 'eager', a, 'graph', b, 'worst gradient difference', peor, flush=True)
+        assert all(torch.isfinite(torch.tensor(a[:2]))) and a[2] == b[2] == 0.0
+        assert abs(a[0] - b[0]) <= 1e-3 * abs(a[0]) and abs(a[1] - b[1]) <= 1e-3 * abs(a[1])
+        assert peor[0] <= 1e-3, peor
+        _sincronizar(m2, o2, m1, o1)
+        torch.randn(1 << 20, device=DEV).sum().item()
+    assert grafo.grafo is not None
+    del ansioso, o1, m1
+    torch.cuda.empty_cache()
+    # two replays from one state
+    pesos = [p.detach().clone() for p in m2.parameters()]
+    estado = [{k: v.clone() for k, v in o2.state[p].items()} for p in m2.parameters()]
+    res = []
+    for _ in range(2):
+        with torch.no_grad():
+            for p, q, st in zip(m2.parameters(), pesos, estado):
+                p.copy_(q)
+                for k, v in st.items():
+                    o2.state[p][k].copy_(v)
+        perdida, norma, _ = grafo(*lotes[0], lr=1e-3)
+        torch.cuda.synchronize()
+        res.append((float(perdida), float(norma), [p.detach().clone() for p in m2.parameters()]))
+    assert res[0][:2] == res[1][:2]
+    assert all(torch.equal(u, v) for u, v in zip(res[0][2], res[1][2]))
+    del res, pesos, estado
+    # the loss falls on one batch
+    perdidas = [float(grafo(*lotes[1], lr=1e-3)[0]) for _ in range(5)]
+    print('losses on one batch', perdidas, flush=True)
+    assert all(torch.isfinite(torch.tensor(perdidas)))
+    assert perdidas[-1] < perdidas[0]

@@ -91,7 +91,7 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert lib.asrn_scan_workspace(32, 4096) >= 32 * 16 * 12
     assert lib.asrn_scan_workspace(1 << 20, 1 << 20) == -1
     assert lib.asrn_hawkes_bwd_workspace(8, 4096, 4) >= 2 * 8 * 4096 * 4 * 4 + lib.asrn_scan_workspace(32, 4096)
-    assert lib.asrn_scan_fwd(N, N, N, 2, 4096, N, 0, N) != 0
+    assert lib.asrn_scan_fwd(N, N, N, 2, 8192, N, 0, N) != 0           # multi-chunk: chunk totals needed
     assert 'workspace' in _err(lib)
     # the scan without a workspace: its static scratch is 4 MiB; larger scans are refused before any device work
     assert lib.asrn_scan_static_scratch_bytes() == 4 << 20

@@ -18,11 +18,14 @@ def all_queries(B, L):
 @pytest.mark.parametrize('name', fixtures.names(False))
 def test_candidates_at_equals_golden(name):
     g, p, m = fixtures.load(name)
+    if fixtures.nucleo(m) and 'gamma_fill' in m['extra']:
+        pytest.skip("v89's fill leaks weight to the invalid keys of its block window, which the per-query form does "
+                    'not build (the sorted-window form reproduces it: tests/test_oracle_golden.py)')
     sh = fixtures.shape_of(p, m)
     B, L = g['x'].shape
     ids = O.bucket_ids(g['phi'], sh.T, sh.nb).numpy()
-    salida, sen = O.candidates_at(g['phi'], g['V'], g['Qc'], g['Kc'], g['Bt'], g['log_alfa'], g['sig'],
-                                  p['w_sufijo'], p['gamma'], sh, ids, all_queries(B, L))
+    salida, sen = O.candidates_at(g['phi'], g['V'], g['Qc'], g['Kc'], fixtures.stage_input(g, 'Bt'), g['log_alfa'],
+                                  g['sig'], p['w_sufijo'], p['gamma'], sh, ids, all_queries(B, L), fixtures.prot(m))
     ref = g['acc.salida'].reshape(B * L, -1)
     assert (salida - ref).abs().max() <= 1e-5 * (ref.abs().max() + 1e-6)
     assert torch.equal(sen[:, :, 0].sum(1).view(B, L, 1), g['acc.peso_total'])

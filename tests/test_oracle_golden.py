@@ -44,19 +44,19 @@ def test_producers(name):
         assert a.dtype == g[k].dtype, (k, a.dtype, g[k].dtype)
     for a, k in ((Qc, 'Qc'), (Kc, 'Kc'), (beta, 'beta'), (la, 'log_alfa')):
         close(a, g[k], 1e-6, k)
-    assert beta.dtype == torch.float64
+    assert beta.dtype == (torch.float32 if fixtures.nucleo(m) else torch.float64)
 
 
 @pytest.mark.parametrize('name', CASES)
 def test_candidate_stage_forward_and_gradients(name):
     g, p, m = fixtures.load(name)
     sh = fixtures.shape_of(p, m)
-    leaves = {k: g[k].clone().requires_grad_() for k in ('phi', 'V', 'Qc', 'Kc', 'Bt', 'log_alfa')}
+    leaves = {k: fixtures.stage_input(g, k).clone().requires_grad_() for k in ('phi', 'V', 'Qc', 'Kc', 'Bt', 'log_alfa')}
     w = p['w_sufijo'].clone().requires_grad_()
     gam = p['gamma'].clone().requires_grad_()
     with fixtures.cpu_autocast(m):
         salida, sen = O.candidates(leaves['phi'], leaves['V'], leaves['Qc'], leaves['Kc'], leaves['Bt'],
-                                   leaves['log_alfa'], g['sig'], w, gam, sh)
+                                   leaves['log_alfa'], g['sig'], w, gam, sh, fixtures.prot(m))
         acc = O.gate_signals(salida, sen, sh.T, sh.Tc)
     assert salida.dtype == g['acc.salida'].dtype
     for k in ('salida', 'pico'):
@@ -126,3 +126,31 @@ def test_whole_layer_forward_and_gradients(name):
         if ('g.' + k) in g:
             assert t.grad is not None, k
             close(t.grad, g['g.' + k], 1e-4, 'grad ' + k)
+
+
+def test_core_layer_mistakes_fail_the_fixtures():
+    """Planted mistakes in the oracle's core-layer mode fail the reference's core fixtures: the protected layer's clock
+    difference instead of v89's (log alfa_k + rate B_k) - rate B_q (the offset-clock fixture: salida and every gradient
+    off by ~1e-4, d gamma by ~3e-3), and the exact mask instead of v89's -1e9 fill (the gamma = 1e9 fixture, where the
+    fill leaks weight to invalid keys: salida off by ~0.4)."""
+    import dataclasses
+
+    def stage_error(name, prot):
+        g, p, m = fixtures.load(name)
+        sh = fixtures.shape_of(p, m)
+        leaves = {k: fixtures.stage_input(g, k).clone().requires_grad_()
+                  for k in ('phi', 'V', 'Qc', 'Kc', 'Bt', 'log_alfa')}
+        gam = p['gamma'].clone().requires_grad_()
+        salida, _ = O.candidates(leaves['phi'], leaves['V'], leaves['Qc'], leaves['Kc'], leaves['Bt'],
+                                 leaves['log_alfa'], g['sig'], p['w_sufijo'], gam, sh, prot)
+        (salida * g['acc.gs']).sum().backward()
+        e_s = ((salida - g['acc.salida']).abs().max() / g['acc.salida'].abs().max()).item()
+        e_g = ((gam.grad - g['acc.g_gamma']).abs().max() / g['acc.g_gamma'].abs().max()).item()
+        return e_s, e_g
+
+    core = O.Prot.ninguna()
+    assert stage_error('n_nucleo_reloj_desplazado', core) == (0.0, 0.0)
+    e_s, e_g = stage_error('n_nucleo_reloj_desplazado', dataclasses.replace(core, reloj_64=True))
+    assert e_s > 3e-5 and e_g > 1e-3, (e_s, e_g)
+    assert stage_error('m_nucleo_gamma_huge', core)[0] == 0.0
+    assert stage_error('m_nucleo_gamma_huge', dataclasses.replace(core, mascara_exacta=True))[0] > 0.1

@@ -36,16 +36,31 @@ def scan_static(a, b):
 
 
 def test_static_scan_equals_workspace_scan_twice():
-    print('[case] asrn_scan_fwd_static vs asrn_scan_fwd: (32, 70000) then (5, 3000)', flush=True)
+    print('[case] asrn_scan_fwd_static vs asrn_scan_fwd: (32, 70000) then (5, 30000)', flush=True)
     g = torch.Generator().manual_seed(0)
-    for rows, N in ((32, 70000), (5, 3000)):
+    for rows, N in ((32, 70000), (5, 30000)):
         a = torch.rand(rows, N, generator=g).to(DEV)
         b = torch.randn(rows, N, generator=g).to(DEV)
-        assert _lib.query('asrn_scan_workspace', rows, N) > 0          # a multi-chunk scan: the scratch is used
+        assert _lib.query('asrn_scan_workspace', rows, N) > 0          # multi-chunk scans: the scratch is used
         ref = scan_with_workspace(a, b)
         got = scan_static(a, b)
         torch.cuda.synchronize()
         assert torch.equal(got, ref), (rows, N)
+
+
+def test_static_scan_takes_one_launch_rows_without_scratch():
+    """Rows of 1,025 to 4,096 run as one launch (a workgroup a row) and need no chunk totals: the static entry point
+    takes them at any row count, also where the workspace bound would exceed its scratch."""
+    print('[case] asrn_scan_fwd_static, (32768, 4096): one launch, no scratch', flush=True)
+    rows, N = 32768, 4096
+    assert _lib.query('asrn_scan_workspace', rows, N) > _lib.query('asrn_scan_static_scratch_bytes')
+    g = torch.Generator(device=DEV).manual_seed(1)
+    a = torch.rand(rows, N, generator=g, device=DEV)
+    b = torch.randn(rows, N, generator=g, device=DEV)
+    ref = scan_with_workspace(a, b)
+    got = scan_static(a, b)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
 
 
 def test_static_scan_refuses_sizes_beyond_its_scratch():
