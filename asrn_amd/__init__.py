@@ -2,7 +2,8 @@
 model, training and checkpoint API around it.
 
 The public names mirror the reference package (KIROKOWA/ASRN, asrn/__init__.py:41-97):
-  - the layer: ASRNLayer / CapaASRNEstable, Protecciones / Protections, convertir / convert, firmas_de_piezas, escaneo;
+  - the layer: ASRNLayer / CapaASRNEstable, ASRNCoreLayer / CapaASRN (the unprotected core layer, v89 numerics),
+    Protecciones / Protections, convertir / convert, firmas_de_piezas, escaneo;
   - the model: ModeloASRN / ASRNModel, BloqueLocal / LocalBlock, ConfigASRN / ASRNConfig, TALLAS,
     crear_modelo / create_model, crear_desde_config / create_from_config;
   - training: crear_optimizador, tasa_aprendizaje, PasoGrafado, entrenar / train, evaluar / evaluate;
@@ -16,7 +17,8 @@ from . import ops, synth
 from ._lib import ASRNHipError, LIB_PATH
 from ._lib import load as cargar_biblioteca
 from .archivo import cargar, guardar
-from .capa import ASRNLayer, CapaASRNEstable, Protecciones, Protections, convertir, firmas_de_piezas, ngramas
+from .capa import (ASRNCoreLayer, ASRNLayer, CapaASRN, CapaASRNEstable, Protecciones, Protections, convertir,
+                   firmas_de_piezas, ngramas)
 from .entrenamiento import (MULT_SUFIJO_Y_PUERTA, PESOS_SUFIJO_Y_PUERTA, PasoGrafado, crear_optimizador, entrenar,
                             evaluar, tasa_aprendizaje)
 from .escritura import EscritorCapa, LayerWriter
@@ -32,7 +34,7 @@ train, evaluate, save, load, generate = entrenar, evaluar, guardar, cargar, escr
 ModelWriter = EscritorModelo
 load_library = cargar_biblioteca
 
-__all__ = ['ASRNLayer', 'CapaASRNEstable', 'Protecciones', 'Protections', 'convertir', 'convert', 'firmas_de_piezas',
+__all__ = ['ASRNLayer', 'CapaASRNEstable', 'ASRNCoreLayer', 'CapaASRN', 'Protecciones', 'Protections', 'convertir', 'convert', 'firmas_de_piezas',
            'ngramas', 'escaneo', 'ModeloASRN', 'ASRNModel', 'BloqueLocal', 'LocalBlock', 'ConfigASRN', 'ASRNConfig',
            'TALLAS', 'crear_modelo', 'create_model', 'crear_desde_config', 'create_from_config', 'crear_optimizador',
            'tasa_aprendizaje', 'PasoGrafado', 'entrenar', 'train', 'evaluar', 'evaluate', 'guardar', 'save',

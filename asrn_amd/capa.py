@@ -19,6 +19,7 @@ from . import ops
 from .lineal import _rows, column_sums, lineal, weight_grad
 
 PROHIBIDO = -1e9          # the "not allowed" score (asrn/nucleo.py:86)
+ANCHO_FUSIONADO = 1024    # widest layer the fused context and gate kernels take; wider ones use PyTorch ops there
 
 
 @dataclasses.dataclass(frozen=True)
@@ -99,17 +100,14 @@ class CapaASRNEstable(nn.Module):
         if not E.is_cuda:
             raise RuntimeError('asrn_amd.ASRNLayer runs on the GPU only (HIP kernels for gfx950): move the layer and '
                                'its inputs to a cuda device')
-        if not (p.mascara_exacta and p.reloj_64):
-            raise ValueError('asrn_amd.ASRNLayer implements the protected layer (exact mask and 64-bit clock); '
-                             'Protecciones.ninguna() is not supported')
         if not 1 <= self.n_bits <= 14:
             raise ValueError(f'n_bits={self.n_bits}: the HIP bucket sort supports 1..14 bits per table')
         if not 1 <= self.chunk <= 64 or self.n_tablas * self.chunk > 256:
             raise ValueError(f'chunk={self.chunk}, n_tablas={self.n_tablas}: the HIP candidate kernels support 1..64 '
                              'candidates per table and n_tablas * chunk <= 256')
         d = E.shape[-1]
-        if d % 4 or d > 1024:
-            raise ValueError(f'd={d}: the HIP candidate kernels need d % 4 == 0 and d <= 1024')
+        if d % 4:
+            raise ValueError(f'd={d}: the HIP candidate kernels read rows as float4: d must be a multiple of 4')
         if self.n_tablas * self.n_bits + self.confirmar > 256 or self.sufijo > 16 or self.n_tablas > 32:
             raise ValueError('n_tablas*n_bits + confirmar must be <= 256, sufijo <= 16, n_tablas <= 32')
 
@@ -201,6 +199,8 @@ class CapaASRNEstable(nn.Module):
                 -math.inf if p.log_alfa_min is None else float(p.log_alfa_min))
         cf = self.confirmar
         Wq = torch.cat([self.cq.weight, self.ck.weight]) if pesos is None else pesos['Wq']
+        if h.shape[-1] > ANCHO_FUSIONADO:
+            return self._contexto_ancho(h, Wq, con_h)
         if not torch.is_autocast_enabled(h.device.type) and h.shape[-1] <= 512 and 2 * cf <= 32:
             # fp32: the projection's input gradient formed inside the context backward (no GEMM, no dhh buffer)
             y, beta, log_alfa, h_puerta = ops.ContextProj.apply(h, self.ln_ctx.weight, self.ln_ctx.bias,
@@ -211,6 +211,36 @@ class CapaASRNEstable(nn.Module):
             y = lineal(_a_autocast(hh32), Wq)
         Qc, Kc = _Split2.apply(y, cf)
         return (Qc, Kc, beta, log_alfa, h_puerta) if con_h else (Qc, Kc, beta, log_alfa)
+
+    def fugas(self):
+        """The number of (query, table) pairs of the last forward whose best valid score lay within reach of the -1e9
+        fill (without mascara_exacta; None otherwise). There the reference's unprotected layer gives the invalid keys
+        of its block window weight (asrn/estable.py:20-24, asrn/nucleo.py:337-339, 813) and its output depends on how
+        it cuts each sorted row into blocks; this layer only ever weighs the valid candidates, so its output there
+        differs from the reference's. Everywhere else the two agree. Reading it waits for the GPU."""
+        f = getattr(self, '_fuga', None)
+        return None if f is None else int(f.item())
+
+    def _contexto_ancho(self, h, Wq, con_h):
+        """_contexto for widths past the fused context kernels (d > 1024), as PyTorch ops on the GPU, with the same
+        math (asrn/estable.py:153-194): LayerNorm in fp32, Qc and Kc from its output in the autocast dtype, the clock
+        projection in true fp32 (no TF32: a sum of products), softplus / logsigmoid and the clamps."""
+        p = self.protecciones
+        hh32 = F.layer_norm(h.float(), (h.shape[-1],), self.ln_ctx.weight.float(), self.ln_ctx.bias.float(),
+                            self.ln_ctx.eps)
+        y = lineal(_a_autocast(hh32), Wq)
+        with torch.autocast(device_type=h.device.type, enabled=False):
+            w = self.w_reloj.float()
+            u = torch.stack([(hh32 * w[0]).sum(-1), (hh32 * w[1]).sum(-1)], -1) + self.b_reloj.float()
+        beta = F.softplus(u[..., 0])
+        log_alfa = F.logsigmoid(u[..., 1]) + math.log(2)
+        if p.beta_max is not None:
+            beta = beta.clamp(max=p.beta_max)
+        if p.log_alfa_min is not None:
+            log_alfa = log_alfa.clamp(min=p.log_alfa_min)
+        Qc, Kc = _Split2.apply(y, self.confirmar)
+        out = (Qc, Kc, beta.double(), log_alfa)
+        return out + (h,) if con_h else out
 
     def _kappas(self):
         k, kr = self.log_kappa.exp(), self.log_kappa_racha.exp()
@@ -234,7 +264,12 @@ class CapaASRNEstable(nn.Module):
         before the candidate kernels, after the producers and the bucket sort (the point where the context inputs
         must be ready); cubetas: what _cubetas returned, when it already ran."""
         phi, filas, order, win, rank = self._cubetas(E, partes, pesos) if cubetas is None else cubetas
-        shape = dict(T=self.n_tablas, Tc=self.tablas_contexto, C=self.chunk, K=self.sufijo, v_shift=1)
+        p = self.protecciones
+        shape = dict(T=self.n_tablas, Tc=self.tablas_contexto, C=self.chunk, K=self.sufijo, v_shift=1,
+                     reloj32=not p.reloj_64)
+        if not p.mascara_exacta:           # the reference's -1e9 fill: count where it would leak (fugas())
+            self._fuga = torch.zeros(1, dtype=torch.int32, device=E.device)
+            shape['fuga'] = self._fuga
         if esperar is not None:
             esperar()
         suma, sen = ops.Candidates.apply(phi, filas, Qc, Kc, Bt, log_alfa, self.w_sufijo, self.gamma, sig, order,
@@ -271,11 +306,41 @@ class CapaASRNEstable(nn.Module):
         else:
             aporte = _ConPeso.apply(lineal(acc['salida'], w.detach()), gemelo)
         aporte = self.drop(aporte)
+        if h.shape[-1] > ANCHO_FUSIONADO:
+            return self._compuerta_ancha(h, aporte, acc)
         meta = (self.n_tablas, self.tablas_contexto, self.racha_paso,
                 -1.0 if p.mejor_max is None else float(p.mejor_max), 0.0 if p.tope_puerta is None else float(p.tope_puerta))
         return ops.Gate.apply(h, aporte, acc['senales'], acc['vistos'], acc['hawkes'], acc['racha'], self.g.weight,
                                self.g.bias, self.g_conf.weight, self.g_conf.bias, self.w_vistos, self.u_hawkes,
                                self.d_racha, meta)
+
+    def _compuerta_ancha(self, h, aporte, acc):
+        """The gate for widths past the fused gate kernels (d > 1024), as PyTorch ops on the GPU with the same math
+        (asrn/estable.py:376-403, asrn/nucleo.py:865-878; the division by the table count after W_o, per token):
+        h' = h + sigmoid(cap(logit)) A / max(1, peso_total), the logit in fp32."""
+        p = self.protecciones
+        sen = acc['senales']
+        pt = sen[..., 0:1]
+        mejor = torch.where(pt > 0, sen[..., 1:2], torch.zeros_like(pt))
+        if p.mejor_max is not None:
+            mejor = mejor.clamp(-p.mejor_max, p.mejor_max)
+        senales = torch.cat([pt / self.n_tablas, mejor, sen[..., 2:3] / pt.clamp(min=1),
+                             sen[..., 3:4] / self.tablas_contexto], dim=-1)
+        with torch.autocast(device_type=h.device.type, enabled=False):
+            hf = h.float()
+            logit = F.linear(hf, self.g.weight.float(), self.g.bias.float())
+            logit = logit + F.linear(senales, self.g_conf.weight.float(), self.g_conf.bias.float())
+            logit = logit + (acc['vistos'].float() * self.w_vistos.float()).sum(-1, keepdim=True)
+            logit = logit + (torch.log1p(acc['hawkes'].float()) * self.u_hawkes.float()).sum(-1, keepdim=True)
+            racha = acc['racha'].float()
+            nodos = self.d_racha.shape[0]
+            x = (torch.log1p(racha) / self.racha_paso).clamp(max=nodos - 1)
+            i = torch.nan_to_num(x.detach(), nan=0.0).floor().long().clamp(0, nodos - 2)
+            dr = self.d_racha.float()
+            logit = logit + (dr.cumsum(0)[i] + (x - i) * dr[1:][i]).unsqueeze(-1)
+            if p.tope_puerta is not None:
+                logit = p.tope_puerta * torch.tanh(logit / p.tope_puerta)
+            return hf + torch.sigmoid(logit) * (aporte.float() / pt.clamp(min=1))
 
     # --- all together -----------------------------------------------------------------------------------------------
 
@@ -310,7 +375,8 @@ class CapaASRNEstable(nn.Module):
             sig = self._firma(E.detach()) if piezas is None else firmas_de_piezas(piezas)
             w_salida = ops.SmallMatmul.apply(self.o.weight, self.v.weight)
             Qc, Kc, beta, log_alfa, h = self._contexto(h, con_h=True, pesos=pesos)
-            Bt = ops.ClockScan.apply(beta)
+            # the clock: fp64 (reloj_64), or the core layer's fp32 clock, each sum rounded to fp32 (kept in fp64)
+            Bt = ops.ClockScan.apply(beta, not self.protecciones.reloj_64)
             contexto_listo = torch.cuda.Event()
             contexto_listo.record(lado)
             if ngramas is None:
@@ -499,6 +565,28 @@ def _a_autocast(x):
 
 
 ASRNLayer = CapaASRNEstable
+
+
+class CapaASRN(CapaASRNEstable):
+    """The unprotected core ASRN layer (asrn.ASRNCoreLayer = asrn.nucleo.CapaASRN, asrn/nucleo.py:574-886): the same
+    constructor arguments (without protecciones), parameters, buffers and construction order, and the v89 numerics
+    that CapaASRNEstable computes under Protecciones.ninguna() (asrn/estable.py:68-71): an fp32 clock (the cumsum
+    rounded to fp32; the writer's step adds in fp32), the score's clock term formed as (log alfa_k + rate B_k) -
+    rate B_q, no clamps on beta, log alfa or the gate's 'mejor', no kappa floor.
+
+    Two differences, both declared: (1) the reference's -1e9 fill gives weight to invalid keys when every valid score
+    of a (query, table) sinks within ~100 of -1e9 (the leak the protected layer exists for); this layer weighs only the
+    valid candidates there and counts such pairs (fugas()). (2) Under autocast the reference computes the clock
+    projection in the 16-bit GEMM with Qc and Kc; here it stays fp32, as in the protected layer."""
+
+    def __init__(self, d, n_tablas=8, n_bits=14, afin_oculto=128, chunk=32, tablas_contexto=4, confirmar=16,
+                 sufijo=4, vistos=4, dropout=0.0, nodos_racha=16, racha_max=256):
+        super().__init__(d, Protecciones.ninguna(), n_tablas=n_tablas, n_bits=n_bits, afin_oculto=afin_oculto,
+                         chunk=chunk, tablas_contexto=tablas_contexto, confirmar=confirmar, sufijo=sufijo,
+                         vistos=vistos, dropout=dropout, nodos_racha=nodos_racha, racha_max=racha_max)
+
+
+ASRNCoreLayer = CapaASRN
 
 
 @torch.no_grad()

@@ -25,6 +25,8 @@ namespace asrn {
 constexpr int kWavesPerBlock = 1;   // a wave's slot frees when its own query ends, and 5.9 KB of LDS a workgroup
                                     // fits 27 per CU (a 4-wave workgroup's 23.6 KB fits 6: 24 waves)
 constexpr int kMaxSlots = 256;       // T * C
+constexpr float kFill = -1e9f;       // the reference's "not allowed" score (asrn/nucleo.py:86)
+constexpr float kLeakReach = 256.f;  // a table's best valid score within this of kFill is counted as a possible leak
 constexpr int kCh = kMaxSlots / kWave;
 constexpr int kRows = 8;             // rows per half-wave in flight in the feature loops
 
@@ -55,6 +57,11 @@ struct Cand {
   // its bucket ids (B, T) out, and whether tq then enters the rings
   int32_t* rings; int32_t* counts; int32_t* ids_out; int nb; int64_t tq; int insert;
   const int64_t* tq_dev;   // generation, optional: the query position read from device memory instead of tq
+  // the unprotected core layer (v89 numerics): clock32 forms each score's clock term as (log_alfa_k + rate B_k) -
+  // rate B_q in fp32 from the fp32 clock (held in Bt as fp64 values that fp32 represents exactly); leak, when given,
+  // counts the (query, table) pairs whose best valid score is within the -1e9 fill's reach, where the reference's
+  // fill gives its invalid keys weight
+  int clock32; int32_t* leak;
 };
 
 // per-wave LDS scratch: one token's candidate list (entries) and its distinct positions (uniques)
@@ -76,8 +83,9 @@ struct Scratch {
     };
   };
   uint8_t uell[kMaxSlots]; // unique: suffix-match length (query side)
-  int off[36];             // entries of table tau: [off[tau], off[tau + 1]) (T <= 32); table tau's window length
+  int off[35];             // entries of table tau: [off[tau], off[tau + 1]) (T <= 32); table tau's window length
                            // is off[tau + 1] - off[tau]
+  float bq32;              // clock32: the query's fp32 clock
   union {
     int wrank[32];         // per table: the token's sorted rank (the gather)
     float tinv[32];        // per table: 1 / softmax denominator (the forward's weights, after the gather)
@@ -500,12 +508,21 @@ __device__ __forceinline__ void unique_feature_sum(const Cand& a, int64_t b, int
   }
 }
 
+// Widths past 256 * DCH (d > 1024) run the value phases over column slabs of 256 * DCH: columns c0 .. c0 + 256 DCH - 1
+// of every row in one pass, the lanes past d reading column d - 4 (a real column; their results are not used).
+__device__ __forceinline__ int slab_col(const Cand& a, int c0, int ch, int lane) {
+  const int dd = c0 + ch * 256 + lane * 4;
+  return dd < a.d ? dd : a.d - 4;
+}
+
 // <fixed, row_u> over the d columns for every unique (rows of batch row `rows`), R rows in flight, written to
-// out[u]; the key side (w_u != nullptr) also accumulates dV += w_u row_u from the same loads.
+// out[u] (added to it when `add`: the slabs after the first); the key side (w_u != nullptr) also accumulates
+// dV += w_u row_u from the same loads. fixed holds columns c0 .. c0 + 256 DCH - 1 (zero past d).
 template <int DCH, bool B16 = false>
 __device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows, int64_t ld, int64_t self_pos,
                                                 int NU, const float4 (&fixed)[DCH], const float* w_u,
-                                                float4 (&dv)[DCH], Scratch& S, float* out) {
+                                                float4 (&dv)[DCH], Scratch& S, float* out, int c0 = 0,
+                                                bool add = false) {
   const int lane = lane_id();
   constexpr int R = DCH >= 3 ? 2 : (DCH == 2 ? 4 : 8);
   for (int u0 = 0; u0 < NU; u0 += R) {
@@ -518,10 +535,8 @@ __device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows
       const int64_t row = ok ? S.upos[u] : self_pos;
       w[r] = (ok && w_u) ? w_u[u] : 0.f;
 #pragma unroll
-      for (int ch = 0; ch < DCH; ++ch) {
-        const int dd = ch * 256 + lane * 4;
-        o[r][ch] = ld4r<B16>(rows, (uint32_t)row * (uint32_t)ld + (uint32_t)(dd < a.d ? dd : a.d - 4));
-      }
+      for (int ch = 0; ch < DCH; ++ch)
+        o[r][ch] = ld4r<B16>(rows, (uint32_t)row * (uint32_t)ld + (uint32_t)slab_col(a, c0, ch, lane));
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -532,7 +547,7 @@ __device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows
         if (w_u) fma4(dv[ch], w[r], o[r][ch]);
       }
       const float tot = wave_sum_u(p);
-      if (lane == 0 && u0 + r < NU) out[u0 + r] = tot;
+      if (lane == 0 && u0 + r < NU) out[u0 + r] = add ? out[u0 + r] + tot : tot;
     }
   }
   wave_lds_sync();
@@ -545,6 +560,9 @@ struct Entries {
   float sc[kCh];     // score
 };
 
+// The entries' scores: S.ua[u] + rate * S.ub[u] (the clock difference); with clock32, in the reference's fp32 order
+// and roundings ((base + w_suf) + (log_alfa_k + rate B_k)) - rate B_q, from S.ua = base + w_suf, S.uc = log_alfa_k and
+// S.ub = B_k (nucleo:330-332: no fused multiply-add, each product and sum rounded on its own).
 __device__ __forceinline__ void load_entries(const Cand& a, int M, const Scratch& S, Entries& E) {
   const int lane = lane_id();
 #pragma unroll
@@ -555,7 +573,11 @@ __device__ __forceinline__ void load_entries(const Cand& a, int M, const Scratch
     E.tau[c] = in ? (e & 31) : -1;
     const int u = in ? S.uid[m] : 0;
     E.u[c] = u;
-    E.sc[c] = in ? S.ua[u] + rate_of(a, e & 31) * S.ub[u] : -INFINITY;
+    const float r = rate_of(a, e & 31);
+    E.sc[c] = !in ? -INFINITY
+                  : (a.clock32 ? __fsub_rn(__fadd_rn(S.ua[u], __fadd_rn(S.uc[u], __fmul_rn(r, S.ub[u]))),
+                                           __fmul_rn(r, S.bq32))
+                               : S.ua[u] + r * S.ub[u]);
   }
 }
 
@@ -632,7 +654,7 @@ constexpr int gather_rows_in_flight() { return DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 12
 // consecutive uniques starting at `first`, one chunk every `step` (UNR rows in flight per chunk).
 template <int DCH, bool B16 = false>
 __device__ __forceinline__ void gather_values(const Cand& a, int64_t b, const Scratch& S, int NU, int first, int step,
-                                              float4 (&acc)[DCH]) {
+                                              float4 (&acc)[DCH], int c0 = 0) {
   constexpr int UNR = gather_rows_in_flight<DCH>();
   const int lane = lane_id();
   const float* Vb = rows_at<B16>(a.V, (b * a.L + a.vshift) * a.ldv);
@@ -645,10 +667,8 @@ __device__ __forceinline__ void gather_values(const Cand& a, int64_t b, const Sc
       const int64_t p = ok ? S.upos[u0 + r] : 0;   // idle lanes read position 0 (always a V row, weight 0)
       w[r] = ok ? S.uc[u0 + r] : 0.f;
 #pragma unroll
-      for (int ch = 0; ch < DCH; ++ch) {
-        const int dd = ch * 256 + lane * 4;
-        v[r][ch] = ld4r<B16>(Vb, (uint32_t)p * (uint32_t)a.ldv + (uint32_t)(dd < a.d ? dd : a.d - 4));
-      }
+      for (int ch = 0; ch < DCH; ++ch)
+        v[r][ch] = ld4r<B16>(Vb, (uint32_t)p * (uint32_t)a.ldv + (uint32_t)slab_col(a, c0, ch, lane));
     }
 #pragma unroll
     for (int r = 0; r < UNR; ++r)
@@ -692,13 +712,21 @@ __device__ __forceinline__ void unique_terms(const Cand& a, int64_t b, int64_t t
   float mine[4];
   own_suffix_of(sigb, t, a.K, mine);
   const double bq = a.Bt[tok];
+  if (a.clock32 && lane == 0 && wave == 0) S.bq32 = (float)bq;
   auto one = [&](int u) {
     const int64_t k = S.upos[u];
     const int ell = suffix_len_of(sigb, mine, t, k, a.K);
-    const float db = (float)(a.Bt[b * a.L + k] - bq);
-    S.ua[u] = (S.ua[u] + a.w_suf[ell]) + a.la[b * a.L + k];
-    S.ub[u] = db;
-    S.uc[u] = 0.f;
+    const double bk = a.Bt[b * a.L + k];
+    const float db = (float)(bk - bq);     // with the fp32 clock, the fp32 difference of the two values
+    if (a.clock32) {                       // the clock term is formed per entry (load_entries)
+      S.ua[u] = S.ua[u] + a.w_suf[ell];
+      S.ub[u] = (float)bk;
+      S.uc[u] = a.la[b * a.L + k];
+    } else {
+      S.ua[u] = (S.ua[u] + a.w_suf[ell]) + a.la[b * a.L + k];
+      S.ub[u] = db;
+      S.uc[u] = 0.f;
+    }
     if (rec) {
       reinterpret_cast<int32_t*>(rec + R.upos)[u] = (int32_t)k;
       reinterpret_cast<float*>(rec + R.ub)[u] = db;
@@ -746,6 +774,10 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
   load_entries(a, M, S, E);
   uint32_t* tmax = reinterpret_cast<uint32_t*>(S.tsum);
   if (lane < a.T) tmax[lane] = 0u;                       // below every key
+  if (a.clock32) {                                       // uc held log_alfa_k for the scores: it sums weights now
+    wave_lds_sync();
+    for (int u = lane; u < NU; u += kWave) S.uc[u] = 0.f;
+  }
   wave_lds_sync();
 #pragma unroll
   for (int c = 0; c < kCh; ++c)
@@ -772,6 +804,9 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
       has = true;
       mx = from_order_key(tmax[tg]);
       inv = 1.f / den;
+      // the reference's -1e9 fill (without the exact mask) gives its invalid keys weight exp(-1e9 - mx), which is
+      // nonzero in fp32 once mx is within ~104 of -1e9 (the fp32 spacing there is 64)
+      if (a.leak && mx <= kFill + kLeakReach) atomicAdd(a.leak, 1);
     }
     S.tinv[tg] = inv;
   }
@@ -804,15 +839,17 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
     signals_row[3] = pctx;
   }
   if constexpr (VALUES) {
-    // copy-gather over the distinct candidates: sum_u (sum_tau att) V_u
-    float4 acc[DCH];
+    // copy-gather over the distinct candidates: sum_u (sum_tau att) V_u, a slab of 256 DCH columns at a time
+    for (int c0 = 0; c0 < a.d; c0 += 256 * DCH) {
+      float4 acc[DCH];
 #pragma unroll
-    for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
-    gather_values<DCH, B16>(a, b, S, NU, 0, gather_rows_in_flight<DCH>(), acc);
+      for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
+      gather_values<DCH, B16>(a, b, S, NU, 0, gather_rows_in_flight<DCH>(), acc, c0);
 #pragma unroll
-    for (int ch = 0; ch < DCH; ++ch) {
-      const int dd = ch * 256 + lane * 4;
-      if (dd < a.d) st4r<B16>(salida_row, dd, acc[ch]);
+      for (int ch = 0; ch < DCH; ++ch) {
+        const int dd = c0 + ch * 256 + lane * 4;
+        if (dd < a.d) st4r<B16>(salida_row, dd, acc[ch]);
+      }
     }
   }
 }
@@ -863,24 +900,29 @@ __global__ __launch_bounds__(kWave * kDecodeWaves) void k_decode_attend(Cand a) 
   if (wave == 0) token_weights<DCH, false>(a, b, m_shared, NU, S, nullptr, a.signals + b * 4, nullptr);
   __syncthreads();
   constexpr int UNR = gather_rows_in_flight<DCH>();
-  float4 acc[DCH];
+  for (int c0 = 0; c0 < a.d; c0 += 256 * DCH) {          // one slab of 256 DCH columns at a time
+    float4 acc[DCH];
 #pragma unroll
-  for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
-  gather_values<DCH>(a, b, S, NU, wave * UNR, kDecodeWaves * UNR, acc);
+    for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
+    gather_values<DCH>(a, b, S, NU, wave * UNR, kDecodeWaves * UNR, acc, c0);
 #pragma unroll
-  for (int ch = 0; ch < DCH; ++ch) part[wave][ch][lane] = acc[ch];
-  __syncthreads();
-  if (wave != 0) return;
+    for (int ch = 0; ch < DCH; ++ch) part[wave][ch][lane] = acc[ch];
+    __syncthreads();
+    if (wave == 0) {
 #pragma unroll
-  for (int ch = 0; ch < DCH; ++ch) {
-    float4 s = part[0][ch][lane];
-    for (int w = 1; w < kDecodeWaves; ++w) {
-      const float4 q = part[w][ch][lane];
-      s.x += q.x; s.y += q.y; s.z += q.z; s.w += q.w;
+      for (int ch = 0; ch < DCH; ++ch) {
+        float4 s = part[0][ch][lane];
+        for (int w = 1; w < kDecodeWaves; ++w) {
+          const float4 q = part[w][ch][lane];
+          s.x += q.x; s.y += q.y; s.z += q.z; s.w += q.w;
+        }
+        const int dd = c0 + ch * 256 + lane * 4;
+        if (dd < a.d) *reinterpret_cast<float4*>(a.salida + b * a.d + dd) = s;
+      }
     }
-    const int dd = ch * 256 + lane * 4;
-    if (dd < a.d) *reinterpret_cast<float4*>(a.salida + b * a.d + dd) = s;
+    __syncthreads();                                       // part is rewritten by the next slab
   }
+  if (wave != 0) return;
   if (a.insert && lane < a.T) {
     const int id = a.ids_out[b * a.T + lane];
     const int64_t bucket = (b * a.T + lane) * ((int64_t)1 << a.nb) + id;
@@ -934,16 +976,18 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
     slot[c] = in ? (e & 31) * a.C + (S.off[(e & 31) + 1] - 1 - m) : 0;
     att[c] = in ? erow[2 * slot[c]] : 0.f;
   }
-  // dp_u = <dO_q, V_u> (ends with a wave sync)
-  float4 dO[DCH], unused[DCH];
+  // dp_u = <dO_q, V_u>, summed over the slabs of 256 DCH columns (ends with a wave sync)
+  for (int c0 = 0; c0 < a.d; c0 += 256 * DCH) {
+    float4 dO[DCH], unused[DCH];
 #pragma unroll
-  for (int ch = 0; ch < DCH; ++ch) {
-    const int dd = ch * 256 + lane * 4;
-    dO[ch] = dd < a.d ? ld4r<B16>(rows_at<B16>(a.dsal, tok * a.d), (uint32_t)dd) : zero4();
-    unused[ch] = zero4();
+    for (int ch = 0; ch < DCH; ++ch) {
+      const int dd = c0 + ch * 256 + lane * 4;
+      dO[ch] = dd < a.d ? ld4r<B16>(rows_at<B16>(a.dsal, tok * a.d), (uint32_t)dd) : zero4();
+      unused[ch] = zero4();
+    }
+    unique_row_dots<DCH, B16>(a, rows_at<B16>(a.V, (b * a.L + a.vshift) * a.ldv), a.ldv, 0, NU, dO, nullptr, unused,
+                              S, S.uc, c0, c0 > 0);
   }
-  unique_row_dots<DCH, B16>(a, rows_at<B16>(a.V, (b * a.L + a.vshift) * a.ldv), a.ldv, 0, NU, dO, nullptr, unused, S,
-                            S.uc);
 
   // per entry: att * dp (S.ua is a per-entry buffer here)
 #pragma unroll
@@ -1026,7 +1070,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
 // sum_u w_u row_u over the uniques' d-wide rows (rows of batch row b), UNR rows in flight
 template <int DCH, bool B16 = false>
 __device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows, int64_t self_pos, int NU,
-                                               const float* w_u, const Scratch& S, float4 (&acc)[DCH]) {
+                                               const float* w_u, const Scratch& S, float4 (&acc)[DCH], int c0 = 0) {
   const int lane = lane_id();
   constexpr int UNR = DCH >= 4 ? 3 : (DCH >= 2 ? 6 : 8);   // fits the key pass's register budget (6 waves at DCH 1)
 #pragma unroll
@@ -1040,10 +1084,8 @@ __device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows,
       const int64_t p = ok ? S.upos[u0 + r] : self_pos;
       w[r] = ok ? w_u[u0 + r] : 0.f;
 #pragma unroll
-      for (int ch = 0; ch < DCH; ++ch) {
-        const int dd = ch * 256 + lane * 4;
-        v[r][ch] = ld4r<B16>(rows, (uint32_t)p * (uint32_t)a.d + (uint32_t)(dd < a.d ? dd : a.d - 4));
-      }
+      for (int ch = 0; ch < DCH; ++ch)
+        v[r][ch] = ld4r<B16>(rows, (uint32_t)p * (uint32_t)a.d + (uint32_t)slab_col(a, c0, ch, lane));
     }
 #pragma unroll
     for (int r = 0; r < UNR; ++r)
@@ -1119,20 +1161,22 @@ void k_cand_bwd_k(Cand a) {
     wave_lds_sync();
   }
 
-  // dV_k = sum_u (sum_tau att) dO_u
-  float4 dv[DCH];
-  unique_row_sum<DCH, B16>(a, rows_at<B16>(a.dsal, b * a.L * a.d), k, NU, S.uc, S, dv);
-  // d phi_k, d Kc_k = sum_u (sum_tau ds) [phi_q * scale_phi ; Qc_q * scale_c]
-  float4 gk[F4];
-  unique_feature_sum<F4, FB16>(a, b, k, NU, true, S.ub, S, gk);
   // with vshift, V[k] is the projection of k + 1: its gradient goes to row k + 1, and the last position (which no
   // query sees, so dv is 0) clears row 0, the projection no V reads
   const int64_t dv_row = a.vshift ? b * a.L + (k + 1 < a.L ? k + 1 : 0) : tok;
+  // dV_k = sum_u (sum_tau att) dO_u, a slab of 256 DCH columns at a time
+  for (int c0 = 0; c0 < a.d; c0 += 256 * DCH) {
+    float4 dv[DCH];
+    unique_row_sum<DCH, B16>(a, rows_at<B16>(a.dsal, b * a.L * a.d), k, NU, S.uc, S, dv, c0);
 #pragma unroll
-  for (int ch = 0; ch < DCH; ++ch) {
-    const int dd = ch * 256 + lane * 4;
-    if (dd < a.d) st4r<B16>(a.dV, dv_row * a.ldv + dd, dv[ch]);
+    for (int ch = 0; ch < DCH; ++ch) {
+      const int dd = c0 + ch * 256 + lane * 4;
+      if (dd < a.d) st4r<B16>(a.dV, dv_row * a.ldv + dd, dv[ch]);
+    }
   }
+  // d phi_k, d Kc_k = sum_u (sum_tau ds) [phi_q * scale_phi ; Qc_q * scale_c]
+  float4 gk[F4];
+  unique_feature_sum<F4, FB16>(a, b, k, NU, true, S.ub, S, gk);
   if (half == 0) {   // P and cf are multiples of 4: a lane's 4 features lie in one of the two rows
 #pragma unroll
     for (int c = 0; c < F4; ++c) {
@@ -1192,7 +1236,7 @@ static int check_args(const Cand& a, const char* what) {
   ASRN_REQUIRE(a.B >= 0 && a.L >= 0, "%s: bad sizes", what);
   ASRN_REQUIRE(a.L < (int64_t(1) << 26), "%s: L=%lld too long (positions are packed in 26 bits)", what,
                (long long)a.L);
-  ASRN_REQUIRE(a.d >= 4 && a.d % 4 == 0 && a.d <= 1024, "%s: d=%d must be a multiple of 4 in [4, 1024]", what, a.d);
+  ASRN_REQUIRE(a.d >= 4 && a.d % 4 == 0, "%s: d=%d must be a multiple of 4, at least 4", what, a.d);
   ASRN_REQUIRE(a.C >= 1 && a.C <= 64, "%s: chunk C=%d must be in [1, 64]", what, a.C);
   ASRN_REQUIRE(a.T >= 1 && a.T <= 32 && a.T * a.C <= kMaxSlots && a.Tc >= 0 && a.Tc <= a.T,
                "%s: T=%d, C=%d, Tc=%d: needs T <= 32 and T*C <= %d", what, a.T, a.C, a.Tc, kMaxSlots);
@@ -1295,12 +1339,16 @@ extern "C" int asrn_candidates_fwd(const float* phi, const float* V, const float
                                    int64_t B, int64_t L, int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T,
                                    int32_t Tc, int32_t C, float scale_phi, float scale_c, int64_t ldv,
                                    int32_t v_shift, int64_t ldq, int32_t rows_bf16, float* salida, float* signals,
-                                   float* entries, uint8_t* lists, void* stream) {
+                                   float* entries, uint8_t* lists, int32_t clock_mode, int32_t* leak, void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, order, win, rank, B, L, d, P, cf, K, T, Tc, C,
                 scale_phi, scale_c);
   a.ldv = ldv;
   a.vshift = v_shift;
   a.ldq = ldq;
+  ASRN_REQUIRE(clock_mode == 0 || clock_mode == 1, "asrn_candidates_fwd: clock_mode=%d must be 0 (the fp64 clock's "
+               "difference) or 1 (the core layer's fp32 clock term)", clock_mode);
+  a.clock32 = clock_mode;
+  a.leak = leak;
   if (check_args(a, "asrn_candidates_fwd")) return 1;
   if (B == 0 || L == 0) return 0;
   a.salida = salida; a.signals = signals; a.ent = entries;
@@ -1363,7 +1411,7 @@ extern "C" int asrn_decode_attend(const float* phi, const float* V, const float*
                                   int64_t t, const int64_t* t_dev, int32_t d, int32_t nb, int32_t cf, int32_t K,
                                   int32_t T, int32_t Tc,
                                   int32_t C, float scale_phi, float scale_c, int32_t insert, float* salida,
-                                  float* signals, int32_t* ids, void* stream) {
+                                  float* signals, int32_t* ids, int32_t* leak, void* stream) {
   Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, nullptr, nullptr, nullptr, B, cap, d, T * nb, cf,
                 K, T, Tc, C, scale_phi, scale_c);
   if (check_args(a, "asrn_decode_attend")) return 1;
@@ -1374,5 +1422,6 @@ extern "C" int asrn_decode_attend(const float* phi, const float* V, const float*
   a.rings = rings; a.counts = counts; a.ids_out = ids; a.nb = nb; a.tq = t; a.tq_dev = t_dev;
   a.insert = insert ? 1 : 0;
   a.salida = salida; a.signals = signals;
+  a.leak = leak;
   return dispatch<LaunchDecode>(a, (hipStream_t)stream);
 }

@@ -156,6 +156,7 @@ struct Step {
   const float* kappa_r; int64_t B, stride, t; int n;
   float* racha; float* vistos; float* hawkes;
   const int64_t* t_dev;    // optional: the position read from device memory instead of t
+  int reloj32;             // the core layer's fp32 clock: Bt[t] = fp32(Bt[t-1] + beta_t), held in fp64
 };
 
 __global__ void k_repetition_step(Step a, Table tb) {
@@ -166,7 +167,9 @@ __global__ void k_repetition_step(Step a, Table tb) {
   const int64_t t = a.t_dev ? *a.t_dev : a.t;
   if (t < 0 || t >= a.stride) return;                            // outside the caches: nothing written
   const double* Btb = a.Bt + b * a.stride;
-  const double Bq = (t > 0 ? Btb[t - 1] : 0.0) + a.beta_t[b];     // the clock advances (nucleo:1826)
+  // the clock advances (nucleo:1826): in fp64, or, for the core layer, as fp32 values added in fp32
+  const double Bq = a.reloj32 ? (double)__fadd_rn(t > 0 ? (float)Btb[t - 1] : 0.f, (float)a.beta_t[b])
+                              : (t > 0 ? Btb[t - 1] : 0.0) + a.beta_t[b];
   if (j == 0) a.Bt[b * a.stride + t] = Bq;
   // key of the group of j + 1 pieces ending at t: sum_{k <= j} sig[t - k] c[k], NaN before the text (nucleo:175-186)
   double key = 0.0;
@@ -265,7 +268,7 @@ extern "C" int asrn_repetition_step(const float* sig, double* Bt, const float* l
                                     int64_t stride, int64_t t, const int64_t* t_dev, int32_t n, int64_t cap,
                                     uint64_t* tab_keys,
                                     double* tab_Bu, float* tab_A, float* racha, float* vistos, float* hawkes,
-                                    void* stream) {
+                                    int32_t reloj32, void* stream) {
   ASRN_REQUIRE(B >= 0 && n >= 1 && n <= 16 && t >= 0 && t < stride,
                "asrn_repetition_step: bad sizes B=%lld n=%d t=%lld stride=%lld", (long long)B, n, (long long)t,
                (long long)stride);
@@ -273,7 +276,8 @@ extern "C" int asrn_repetition_step(const float* sig, double* Bt, const float* l
                "asrn_repetition_step: table capacity %lld must be a power of two >= 2 (t + 1) = %lld: grow it first",
                (long long)cap, (long long)(2 * (t + 1)));
   if (B == 0) return 0;
-  Step a = {sig, Bt, log_alfa, beta_t, coef, kappa, kappa_r, B, stride, t, n, racha, vistos, hawkes, t_dev};
+  Step a = {sig, Bt, log_alfa, beta_t, coef, kappa, kappa_r, B, stride, t, n, racha, vistos, hawkes, t_dev,
+            reloj32 ? 1 : 0};
   Table tb = {tab_keys, tab_Bu, tab_A, cap};
   hipLaunchKernelGGL(k_repetition_step, dim3((unsigned)((B * n + kThreads - 1) / kThreads)), dim3(kThreads), 0,
                      (hipStream_t)stream, a, tb);

@@ -361,15 +361,17 @@ struct StreakBwd : StreakCommon {
 };
 
 // ---- clock: fp64 prefix (or suffix) sums -----------------------------------------------------------------------------
+// round32: each stored prefix sum rounded to fp32 (held in fp64) while the running sum stays fp64: the unprotected
+// layer's fp32 clock, which the reference gets from an fp32 cumsum that accumulates in double on the CPU
 struct ClockOp {
   static constexpr bool kReduce = false;
   static constexpr bool kOneLaunch = true;
   using M = Sum64;
   using Aux = NoAux;
-  const double* x; double* y; int64_t L; int reverse;
+  const double* x; double* y; int64_t L; int reverse; int round32;
   __device__ Sum64 load(int row, int64_t e, Aux&) const { return {x[row * L + (reverse ? L - 1 - e : e)]}; }
   __device__ void store(int row, int64_t e, double v, float&, const Aux&) const {
-    y[row * L + (reverse ? L - 1 - e : e)] = v;
+    y[row * L + (reverse ? L - 1 - e : e)] = round32 ? (double)(float)v : v;
   }
   __device__ void reduce(int, float) const {}
 };
@@ -451,10 +453,12 @@ extern "C" int64_t asrn_scan_workspace(int64_t rows, int64_t N) {
   return round_up(rows * nc * 8) + round_up(rows * nc * 4);
 }
 
-extern "C" int asrn_clock_scan(const double* x, double* y, int64_t B, int64_t L, int32_t reverse, void* workspace,
+extern "C" int asrn_clock_scan(const double* x, double* y, int64_t B, int64_t L, int32_t mode, void* workspace,
                                int64_t workspace_bytes, void* stream) {
   ASRN_REQUIRE(B >= 0 && L >= 0, "asrn_clock_scan: bad sizes");
-  ClockOp op{x, y, L, (int)reverse};
+  ASRN_REQUIRE(mode >= 0 && mode <= 2, "asrn_clock_scan: mode=%d must be 0 (prefix sums), 1 (suffix sums) or 2 "
+               "(prefix sums rounded to fp32)", mode);
+  ClockOp op{x, y, L, mode == 1 ? 1 : 0, mode == 2 ? 1 : 0};
   return launch_scan(op, B, L, workspace, workspace_bytes, stream, "asrn_clock_scan");
 }
 

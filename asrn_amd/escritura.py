@@ -81,6 +81,8 @@ class EscritorCapa:
         self.hawkes = ops.HawkesTable.load(partes['claves'], partes['orden_k'], partes['repetido'], partes['hawkes'],
                                            partes['Bt'], partes['log_alfa'], cap=2 * self.cap)
         self.racha = partes['racha'][:, -1].to(f32).contiguous().clone()
+        # (query, table) pairs of the steps where the unprotected layer's -1e9 fill would leak (CapaASRN.fugas)
+        self.fugas_t = torch.zeros(1, dtype=torch.int32, device=E.device)
         self.e_ult = E[:, -1]
         self.t = L0
         self._g = None
@@ -122,9 +124,13 @@ class EscritorCapa:
         kappa, kappa_r = torch._foreach_exp([capa.log_kappa, capa.log_kappa_racha])
         if capa.protecciones.kappa_min is not None:
             kappa, kappa_r = kappa.clamp(min=capa.protecciones.kappa_min), kappa_r.clamp(min=capa.protecciones.kappa_min)
-        vistos, hawkes = self.hawkes.step(c, pos, beta_t, capa.c_vistos, kappa, kappa_r, self.racha, t_max=t_max)
-        salida, sen, _ = ops.decode_attend(c, pos, self.anillos, self.cuentas, capa.w_sufijo, capa.gamma,
-                                           self._forma(), insert=not self.ajeno, t_max=t_max)
+        vistos, hawkes = self.hawkes.step(c, pos, beta_t, capa.c_vistos, kappa, kappa_r, self.racha, t_max=t_max,
+                                          reloj32=not capa.protecciones.reloj_64)
+        forma = self._forma()
+        if not capa.protecciones.mascara_exacta:          # the -1e9 fill's leak case, counted over the steps
+            forma['fuga'] = self.fugas_t
+        salida, sen, _ = ops.decode_attend(c, pos, self.anillos, self.cuentas, capa.w_sufijo, capa.gamma, forma,
+                                           insert=not self.ajeno, t_max=t_max)
         acc = {'salida': salida.unsqueeze(1).to(e_t.dtype), 'senales': sen[:, None],
                'vistos': vistos.unsqueeze(1), 'hawkes': hawkes.unsqueeze(1), 'racha': self.racha.unsqueeze(1)}
         return capa._combinar(acc, h_t.unsqueeze(1))[:, 0]

@@ -413,15 +413,18 @@ def _scan_workspace(rows, N, dev):
 
 
 class ClockScan(torch.autograd.Function):
-    """Bt = cumsum(beta, 1) in fp64; the backward is the suffix sum."""
+    """Bt = cumsum(beta, 1) in fp64; the backward is the suffix sum. reloj32: each sum rounded to fp32 (kept in an
+    fp64 tensor), the core layer's fp32 clock (asrn/nucleo.py:882: an fp32 cumsum, accumulated in double on the CPU);
+    its gradient is the same suffix sum."""
 
     @staticmethod
-    def forward(ctx, beta):
+    def forward(ctx, beta, reloj32=False):
         dev = _dev(beta)
         x = _c(beta, torch.float64)
         y = torch.empty_like(x)
         ws, wsb = _scan_workspace(x.shape[0], x.shape[1], dev)
-        call('asrn_clock_scan', ptr(x), ptr(y), x.shape[0], x.shape[1], 0, ptr(ws), wsb, stream_of(dev))
+        call('asrn_clock_scan', ptr(x), ptr(y), x.shape[0], x.shape[1], 2 if reloj32 else 0, ptr(ws), wsb,
+             stream_of(dev))
         return y
 
     @staticmethod
@@ -430,7 +433,7 @@ class ClockScan(torch.autograd.Function):
         out = torch.empty_like(g)
         ws, wsb = _scan_workspace(g.shape[0], g.shape[1], g.device)
         call('asrn_clock_scan', ptr(g), ptr(out), g.shape[0], g.shape[1], 1, ptr(ws), wsb, stream_of(g.device))
-        return out
+        return out, None
 
 
 # ---------------------------------------------------------------------------------------------------------------------
@@ -646,10 +649,13 @@ class Candidates(torch.autograd.Function):
         # each query's deduplicated candidate list, for the backward's query pass (shape['listas'] = False: none)
         listas = (torch.empty((B, L, query('asrn_candidates_record_bytes', T, C)), dtype=torch.uint8, device=dev)
                   if shape.get('listas', True) else None)
+        # the core layer (shape['reloj32']): the fp32 clock's score term; shape['fuga']: a device int32 counting the
+        # (query, table) pairs where the core layer's -1e9 fill would leak weight
+        fuga = shape.get('fuga')
         call('asrn_candidates_fwd', ptr(ins['phi']), ptr(ins['V']), ptr(ins['Qc']), ptr(ins['Kc']), ptr(ins['sig']),
              ptr(ins['Bt']), ptr(ins['la']), ptr(ins['w']), ptr(ins['g']), ptr(order), ptr(win), ptr(rank), B, L, d,
              P, cf, K, T, Tc, C, sp, sc, Vk.stride(1), vs, Qk.stride(1), mode, ptr(salida), ptr(signals),
-             ptr(ent), ptr(listas), stream_of(dev))
+             ptr(ent), ptr(listas), 1 if shape.get('reloj32') else 0, ptr(fuga), stream_of(dev))
         ctx.save_for_backward(*ins.values(), order, win, rank, ent, listas)
         ctx.meta = (B, L, P, d, cf, K, T, Tc, C, sp, sc, V.dtype, phi.dtype, Qc.dtype, Kc.dtype, log_alfa.dtype,
                     P0, cf0, vs)
@@ -754,7 +760,7 @@ def decode_attend(cache, t, rings, counts, w_suf, gamma, shape, insert, t_max=No
     call('asrn_decode_attend', ptr(phi), ptr(V), ptr(cache['Qc']), ptr(cache['Kc']), ptr(cache['sig']),
          ptr(cache['Bt']), ptr(cache['log_alfa']), ptr(w), ptr(g), ptr(rings), ptr(counts), B, cap, th, tdev, d, nb,
          cf, K, T, Tc, C, float(P) ** -0.5, float(cf) ** -0.5, 1 if insert else 0, ptr(salida), ptr(signals),
-         ptr(ids), stream_of(dev))
+         ptr(ids), ptr(shape.get('fuga')), stream_of(dev))
     return salida, signals, ids
 
 
@@ -840,10 +846,11 @@ class HawkesTable:
              ptr(new.keys), ptr(new.Bu), ptr(new.A), new.cap, stream_of(dev))
         self.keys, self.Bu, self.A, self.cap = new.keys, new.Bu, new.A, new.cap
 
-    def step(self, cache, t, beta_t, coef, kappa, kappa_r, racha, t_max=None):
+    def step(self, cache, t, beta_t, coef, kappa, kappa_r, racha, t_max=None, reloj32=False):
         """Position t: Bt[:, t] = Bt[:, t-1] + beta_t (written into cache['Bt']), vistos and hawkes (B, n); racha (B)
         is updated in place (asrn/nucleo.py:953-960, 1683-1714, 1826). t: an int, or a one-element int64 device
-        tensor holding it (then t_max: the largest position it will hold)."""
+        tensor holding it (then t_max: the largest position it will hold). reloj32: the core layer's fp32 clock (the
+        sum in fp32)."""
         dev = _dev(racha)
         th, tdev = _posicion(t, t_max)
         self.reserve(th + 1)
@@ -856,7 +863,7 @@ class HawkesTable:
                _c(kappa_r.detach(), torch.float32)]
         call('asrn_repetition_step', ptr(sig), ptr(Bt), ptr(la), ptr(ins[0]), ptr(ins[1]), ptr(ins[2]), ptr(ins[3]),
              B, stride, th, tdev, self.n, self.cap, ptr(self.keys), ptr(self.Bu), ptr(self.A), ptr(racha),
-             ptr(vistos), ptr(hawkes), stream_of(dev))
+             ptr(vistos), ptr(hawkes), 1 if reloj32 else 0, stream_of(dev))
         return vistos, hawkes
 
 

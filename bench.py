@@ -13,10 +13,14 @@ instead. The per-kernel device events (roofline, hip_aggregate, kernels) come fr
 steps, since events recorded while capturing are not replayed. Prints one JSON line with the driver's keys plus:
   roofline      the dominant HIP kernel: algorithmic bytes per launch / its mean launch time (device events recorded
                 on the stream it runs on), against MI355X's 8 TB/s
-  hip_aggregate all HIP kernels: 25,552 B/token (cfg2) x tokens / (8 TB/s x their summed time per step), the time
+  survey_headline  SURVEY.md section 8(d)'s headline: the compulsory bytes of the HIP kernels K1-K5 (7,776 B/token at
+                cfg2) over their summed kernel time per fwd+bwd (the committed rocprofv3 kernel trace, and the eager
+                pass's device events beside it), against 8 TB/s; its target is 0.5
+  hip_aggregate all HIP kernels: 24,656 B/token (cfg2) x tokens / (8 TB/s x their summed time per step), the time
                 from the committed rocprofv3 kernel trace (profiles/cfg2_kernel_times.json) where there is one
-  layer         whole-layer tokens/s and its HBM fraction at 41,552 B/token (the HIP kernels' bytes plus the GEMMs'
-                operands and results, 16,000 B/token at cfg2)
+  layer         whole-layer tokens/s and its HBM fraction at SURVEY.md 8(d)'s compulsory 25,876 B/token (cfg2; 24,436
+                at cfg3), and beside it at the implementation's own count (the HIP kernels' bytes plus the GEMMs'
+                operands and results, 39,504 B/token at cfg2)
   decode        configs[4]'s greedy generation with the whole d = 768 model (B 16): per-token latency over 1,024
                 steps against the context, 1K to 64K, and its slope
   modelo        the whole model's training step as PasoGrafado replays it: configs[3] (V 50,304, d 768, 12 local
@@ -105,6 +109,41 @@ def gemm_bytes_per_token(d, P, cf, a=4, m=64, mc=64, fused=True):
     return a * (fwd + bwd)
 
 
+# SURVEY.md section 8(d)'s compulsory bytes per token (each distinct tensor read once and written once per pass) at its
+# two layer configurations: the HIP kernels K1-K5 (hash + bucket sort, clock, n-gram sort, Hawkes/streak scans,
+# candidates; forward + backward) and the whole layer (adding the GEMM-boundary tensors)
+SURVEY_BYTES = {'cfg2': {'hip': 3340 + 4436, 'layer': 10680 + 15196},
+                'cfg3': {'hip': 2828 + 3860, 'layer': 24436}}
+# the library entry points whose kernels are K1-K5 (the clock scan runs forward and backward)
+K1_K5 = {'K1 hash + bucket sort': ['asrn_bucket_sort'], 'K2 clock': ['asrn_clock_scan'],
+         'K3 n-gram sort': ['asrn_ngram_sort'],
+         'K4 Hawkes/streak scans': ['asrn_hawkes_fwd', 'asrn_hawkes_bwd', 'asrn_streak_fwd', 'asrn_streak_bwd'],
+         'K5 candidates': ['asrn_candidates_fwd', 'asrn_candidates_bwd']}
+
+
+def survey_headline(config, tokens, per_call, steps, prof):
+    """SURVEY section 8(d)'s headline: K1-K5's compulsory bytes over their summed kernel time per fwd+bwd, against
+    8 TB/s. From the committed rocprofv3 kernel trace of this configuration (profiles/<config>_kernel_times.json,
+    'k1_k5_us_per_step') when there is one, and from the device events around each entry point in the eager pass
+    (these also hold the host's launch gaps of a host-bound step, so they read high)."""
+    b = SURVEY_BYTES.get(config)
+    if b is None:
+        return None
+    groups = {}
+    for g, names in K1_K5.items():
+        groups[g] = round(1e3 * sum(per_call[n]['total_ms'] for n in names if n in per_call) / steps, 2)
+    ev_us = sum(groups.values())
+    out = {'bytes_per_token': b['hip'], 'target_frac': 0.5,
+           'events_us_per_step': round(ev_us, 1), 'events_us_by_kernel': groups,
+           'frac_events': round(b['hip'] * tokens / (HBM_PEAK * ev_us * 1e-6), 4) if ev_us else None}
+    if prof and prof.get('k1_k5_us_per_step'):
+        us = prof['k1_k5_us_per_step']
+        out.update({'rocprof_us_per_step': us, 'rocprof_us_by_kernel': prof.get('k1_k5_us_by_kernel'),
+                    'frac': round(b['hip'] * tokens / (HBM_PEAK * us * 1e-6), 4),
+                    'source': 'rocprofv3 kernel trace, profiles/%s_kernel_times.json' % config})
+    return out
+
+
 TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'cfg2_traffic.json')
 
 
@@ -164,19 +203,20 @@ def cpu_baseline(layer_cpu, x, E, h, gy, reps=3, max_tokens=32768):
             'cpu_model': cpu_model(), 'seconds_per_step': round(t, 3)}
 
 
-KERNEL_TIMES_FILE = os.path.join(ROOT, 'profiles', 'cfg2_kernel_times.json')
+def kernel_times(config):
+    """The committed rocprofv3 kernel-trace summary of this configuration (profiles/<config>_kernel_times.json:
+    'hip_us_per_step', 'k1_k5_us_per_step', ...), or None when there is none."""
+    try:
+        with open(os.path.join(ROOT, 'profiles', f'{config}_kernel_times.json')) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
 
 
 def profiled_hip_us(config):
-    """The HIP kernels' summed time per step from the committed rocprofv3 kernel trace of this configuration
-    (profiles/cfg2_kernel_times.json), or None when there is none."""
-    if config != 'cfg2':
-        return None
-    try:
-        with open(KERNEL_TIMES_FILE) as f:
-            return json.load(f)['hip_us_per_step']
-    except (OSError, ValueError, KeyError):
-        return None
+    """The HIP kernels' summed time per step from the committed rocprofv3 kernel trace of this configuration, or None
+    when there is none."""
+    return (kernel_times(config) or {}).get('hip_us_per_step')
 
 
 DECODE = dict(B=16, V=50304, d=768, n_capas=12, contexts=(1024, 4096, 16384, 32768, 65536), frac=0.2,
@@ -470,7 +510,8 @@ def main():
     hip_ms_per_step = sum(v['total_ms'] for v in per_call.values()) / args.steps
     fused = not bf16                    # the fused hash kernels run in fp32 outside autocast
     hip_b = hip_bytes_per_token(d, P, cf, T, layer.vistos, a=2 if bf16 else 4, K=layer.sufijo, fused=fused)
-    layer_b = hip_b + gemm_bytes_per_token(d, P, cf, a=2 if bf16 else 4, fused=fused)
+    impl_b = hip_b + gemm_bytes_per_token(d, P, cf, a=2 if bf16 else 4, fused=fused)
+    layer_b = SURVEY_BYTES.get(args.config, {}).get('layer', impl_b)
 
     out = {
         'metric': METRIC, 'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps,
@@ -484,9 +525,13 @@ def main():
         'roofline': {'bound': 'hbm', 'kernel': dom, 'achieved': round(achieved / 1e9, 1), 'peak': HBM_PEAK / 1e9,
                      'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK, 4), 'traffic': measured_traffic(dom) if args.config == 'cfg2' else None,
                      'bytes_per_token': algo[dom], 'mean_launch_us': round(dom_us, 2)},
+        'survey_headline': survey_headline(args.config, tokens, per_call, args.steps, kernel_times(args.config)),
         'hip_aggregate': hip_aggregate(hip_b, tokens, hip_ms_per_step, profiled_hip_us(args.config)),
         'layer': {'tokens_per_s': round(value, 1),
-                  'bytes_per_token': layer_b, 'hbm_frac': round(layer_b * tokens / (HBM_PEAK * wall), 4)},
+                  'bytes_per_token': layer_b, 'hbm_frac': round(layer_b * tokens / (HBM_PEAK * wall), 4),
+                  'bytes_source': "SURVEY.md 8(d)'s compulsory whole-layer bytes",
+                  'implementation_bytes_per_token': impl_b,
+                  'implementation_hbm_frac': round(impl_b * tokens / (HBM_PEAK * wall), 4)},
         'kernels': {n: {k: round(v, 3) if isinstance(v, float) else v for k, v in s.items()}
                     for n, s in sorted(per_call.items(), key=lambda kv: -kv[1]['total_ms'])},
     }

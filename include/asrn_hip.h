@@ -68,13 +68,23 @@ int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t T, int32_t 
  *           equal those from fp32 copies.
  *   Qc, Kc rows: row t at Qc + t * ldq (and Kc + t * ldq): ldq = cf for dense rows, or the row stride when both are
  *           column blocks of one projection (ldq >= cf, a multiple of 4, rows 16-byte aligned).
- * Requires d % 4 == 0, d <= 1024, 1 <= C <= 64, P + cf <= 256, K <= 16, T <= 32, L * ldv < 2^31. */
+ *   clock_mode: 0 the protected layer's clock term above (fp64 clock, difference taken before the product); 1 the
+ *           unprotected core layer's (asrn.ASRNCoreLayer = nucleo.CapaASRN, nucleo:330-332, 815-817): Bt holds the
+ *           fp32 clock (fp32 values in fp64), and the term is (log_alfa_k + rate * B_k) - rate * B_q in fp32, each
+ *           product and sum rounded on its own, added to base + w_suf.
+ *   leak: null, or a device int32 to which the kernel adds the number of (query, table) pairs whose best valid score
+ *           is within 256 of -1e9. There the core layer's -1e9 fill (nucleo:337-339, 813) gives the invalid keys of
+ *           its block window weight (the leak estable:20-24 describes), which the exact candidate set here never
+ *           sees; everywhere else the fill and the exact mask give the same weights. The caller clears it.
+ * Requires d % 4 == 0 (widths past 1024 run the value phases over column slabs of 1024), 1 <= C <= 64,
+ * P + cf <= 256, K <= 16, T <= 32, L * ldv < 2^31. */
 int asrn_candidates_fwd(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                         const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
                         const int32_t* order, const int32_t* win, const int32_t* rank, int64_t B, int64_t L,
                         int32_t d, int32_t P, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
                         float scale_phi, float scale_c, int64_t ldv, int32_t v_shift, int64_t ldq, int32_t rows_bf16,
-                        float* salida, float* signals, float* entries, uint8_t* lists, void* stream);
+                        float* salida, float* signals, float* entries, uint8_t* lists, int32_t clock_mode,
+                        int32_t* leak, void* stream);
 
 /* Bytes of one token's record in the `lists` buffer (B*L records, 16-byte aligned): the query's deduplicated candidate
  * list (table offsets, each entry's distinct candidate, the candidates' positions, clock differences and suffix
@@ -200,9 +210,11 @@ int asrn_copy_blocks(int32_t n, const float* const* src, float* const* dst, cons
                      const int64_t* rows, const int64_t* cols, void* stream);
 
 /* ---- a9: clock --------------------------------------------------------------------------------------------------
- * Bt = cumsum(beta) over L in fp64 (asrn/estable.py:418). reverse != 0 computes the suffix sums instead (the
- * backward of the cumsum). workspace: asrn_scan_workspace(B, L) bytes. */
-int asrn_clock_scan(const double* x, double* y, int64_t B, int64_t L, int32_t reverse, void* workspace,
+ * Bt = cumsum(beta) over L in fp64 (asrn/estable.py:418). mode 0: prefix sums; 1: suffix sums (the backward of the
+ * cumsum); 2: prefix sums each rounded to fp32 (stored in fp64) with the running sum kept in fp64, the unprotected
+ * core layer's fp32 clock (asrn/nucleo.py:882, beta.cumsum(1) in fp32, which the CPU accumulates in double).
+ * workspace: asrn_scan_workspace(B, L) bytes. */
+int asrn_clock_scan(const double* x, double* y, int64_t B, int64_t L, int32_t mode, void* workspace,
                     int64_t workspace_bytes, void* stream);
 
 /* ---- a10: n-gram keys, stable key sort, repeated and seen flags -------------------------------------------------
@@ -307,13 +319,15 @@ int asrn_ring_build(const int32_t* order, const int32_t* ids_sorted, int64_t B, 
  * asrn_candidates_fwd, ids (B, T) the query's bucket ids.
  * t_dev: null, or a device int64 holding the position, which the kernel then reads (a step captured once in a HIP
  * graph and replayed as the position advances); t is then checked as the largest position it will hold, and a
- * position outside [0, cap) writes nothing. */
+ * position outside [0, cap) writes nothing.
+ * The clock term is la_k + rate * fp32(B_k - B_q) for both layers: the core layer's writer takes the difference of
+ * its fp32 clock too (asrn/nucleo.py:937). leak: as in asrn_candidates_fwd (null, or a device int32 counter). */
 int asrn_decode_attend(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                        const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
                        int32_t* rings, int32_t* counts, int64_t B, int64_t cap, int64_t t, const int64_t* t_dev,
                        int32_t d, int32_t nb, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
                        float scale_phi, float scale_c, int32_t insert, float* salida, float* signals, int32_t* ids,
-                       void* stream);
+                       int32_t* leak, void* stream);
 
 /* Hawkes memory: per (b, j) group an open-addressing table of cap slots (a power of two, >= 2x the keys it can
  * hold): tab_keys (B*n, cap) uint64 key codes, tab_Bu (B*n, cap) fp64 clock of the last occurrence, tab_A (B*n, cap)
@@ -332,11 +346,12 @@ int asrn_hawkes_table_grow(const uint64_t* old_keys, const double* old_Bu, const
  * asrn/nucleo.py:175-186), _MemoriaHawkes.paso (asrn/nucleo.py:1683-1714) and _repeticion_o1
  * (asrn/nucleo.py:953-960) for position t: Bt[:, t] = Bt[:, t-1] + beta_t (written), vistos and hawkes (B, n) out,
  * racha (B) updated in place. sig, Bt, log_alfa are (B, stride) caches; cap >= 2 (t + 1). t_dev: as for
- * asrn_decode_attend (a position outside [0, stride) writes nothing). */
+ * asrn_decode_attend (a position outside [0, stride) writes nothing). reloj32 != 0: the core layer's fp32 clock,
+ * Bt[:, t] = fp32(fp32(Bt[:, t-1]) + fp32(beta_t)) (its cache in fp32, asrn/nucleo.py:1826), stored in fp64. */
 int asrn_repetition_step(const float* sig, double* Bt, const float* log_alfa, const double* beta_t,
                          const double* coef, const float* kappa, const float* kappa_r, int64_t B, int64_t stride,
                          int64_t t, const int64_t* t_dev, int32_t n, int64_t cap, uint64_t* tab_keys, double* tab_Bu,
-                         float* tab_A, float* racha, float* vistos, float* hawkes, void* stream);
+                         float* tab_A, float* racha, float* vistos, float* hawkes, int32_t reloj32, void* stream);
 
 /* decode_produce replaces the per-token producers of _Escritor.paso (asrn/nucleo.py:1797-1826): for the B new tokens
  * at position t (or *t_dev, as asrn_decode_attend), e, e_prev, h (B, d) fp32, pieza (B) int64, it writes into the

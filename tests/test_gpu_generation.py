@@ -201,13 +201,18 @@ def ids_agree(layer, E, sh, ref=None):
 SMALL = dict(chunk=4, n_bits=2, n_tablas=4, tablas_contexto=2)
 
 
+@pytest.mark.parametrize('clase', ['estable', 'nucleo'])
 @pytest.mark.parametrize('B,L0,n,kw', [(2, 40, 50, SMALL), (1, 2, 30, SMALL), (3, 1, 20, SMALL), (2, 300, 60, {}),
                                        (2, 64, 40, dict(chunk=16, n_bits=4))])
-def test_writer_equals_whole_text(B, L0, n, kw):
-    say('writer = whole text', B, L0, n, kw)
+def test_writer_equals_whole_text(B, L0, n, kw, clase):
+    """The writer's steps equal the whole-text layer position by position: the protected layer, and the core layer
+    (CapaASRN, v89 numerics), whose step advances its fp32 clock in fp32 and takes the clock difference (nucleo:937,
+    1826) where the whole text forms (log alfa_k + rate B_k) - rate B_q from the rounded cumsum; no leak counted."""
+    say('writer = whole text', B, L0, n, kw, clase)
     d = 64
     torch.manual_seed(0)
-    layer = synth.move_params(CapaASRNEstable(d, **kw), 0).to(DEV)
+    capa = asrn_amd.CapaASRN(d, **kw) if clase == 'nucleo' else CapaASRNEstable(d, **kw)
+    layer = synth.move_params(capa, 0).to(DEV)
     x, E, h = synth.layer_inputs(B, L0 + n, d, 12, seed=L0, frac=0.4, span=(3, 8))
     sh = O.shape_from_params({k: v.cpu() for k, v in layer.state_dict().items()}, d, n_bits=layer.n_bits,
                              C=layer.chunk)
@@ -219,6 +224,8 @@ def test_writer_equals_whole_text(B, L0, n, kw):
     assert_close(y0, y[:, :L0], 'prompt')
     assert_close(ys, y[:, L0:], 'steps')
     assert esc.cap >= L0 + n
+    if clase == 'nucleo':
+        assert layer.fugas() == 0 and int(esc.fugas_t.item()) == 0
 
 
 # the generation step's fallback branch (not asrn_decode_produce): widths past the fused producer's limits

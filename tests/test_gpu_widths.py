@@ -12,6 +12,10 @@ time.
 - the candidate stage at cfg3's shape (B 4, N 65,536, d 512) fed bf16 phi, Qc, Kc and value rows (the kernels' form
   that cfg3 runs: every row read as bf16 and widened exactly), checked query by query against the oracle's per-query
   restatement given the same values in fp32.
+- widths past 1,024 (the candidate kernels' value phases over column slabs of 1,024; the context producer and the
+  gate as PyTorch ops on the GPU): fp32 layers at d = 1,536 and 2,048 against the oracle per parameter, the bf16 rule
+  at d = 2,048, the generation step at d = 2,048 against the whole text, and the named size '1b' (d 2,048)
+  forward and backward.
 
 A bucket id is the sign of a hash output, so a value within rounding of 0 can land in the other bucket on the GPU and
 on the CPU. The bucket-id flips between the HIP phi and the oracle's are counted and printed; when there are any, the
@@ -245,3 +249,76 @@ def test_candidates_cfg3_shape_bf16_rows_sampled_vs_oracle():
         close(lv[k].grad, ol[k].grad, 'grad ' + k)
     close(w.grad, wo.grad, 'grad w_sufijo')
     close(gam.grad, go_.grad, 'grad gamma')
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# widths past 1,024: the candidate kernels' value phases over column slabs of 1,024; the context producer and the gate
+# as PyTorch ops on the GPU
+# ---------------------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize('B,L,d,V', [(1, 600, 1536, 300), (1, 512, 2048, 500)])
+def test_layer_fp32_past_1024_vs_oracle(B, L, d, V):
+    """d = 1,536 (one full slab and a half one) and 2,048 (two slabs): the output and every gradient against the
+    oracle, each on its own."""
+    say('layer fp32 past 1024 vs oracle, per parameter', B, L, d, V)
+    whole_layer_fp32(B, L, d, V, seed=d, zipf=1.1, frac=0.2, span=(16, 64))
+
+
+def test_layer_bf16_2048_vs_oracle_rule():
+    B, L, d, V = 1, 512, 2048, 1000
+    say('layer bf16 d 2048 vs oracle rule', B, L, d, V)
+    torch.manual_seed(d)
+    layer_cpu = synth.move_params(CapaASRNEstable(d), d)
+    x, E, h = synth.layer_inputs(B, L, d, V, seed=d + 5, frac=0.2, span=(16, 64), zipf=1.1)
+    gy = torch.randn(B, L, d, generator=torch.Generator().manual_seed(d + 6))
+    p = leaves_of(layer_cpu)
+    sh = O.shape_from_params(p, d)
+    y, gg = run_hip(copy.deepcopy(layer_cpu).to(DEV), E, h, x, gy, bf16=True)
+    y32, g32 = run_oracle(p, E, h, x, gy, sh)
+    y16, g16 = run_oracle(p, E, h, x, gy, sh, bf16=True)
+    bf16_rule(y, y16, y32, 'y')
+    for k in g32:
+        bf16_rule(gg[k], g16[k], g32[k], 'grad ' + k)
+
+
+def test_writer_d2048_equals_whole_text():
+    """The generation step at d = 2,048 (the writer's PyTorch producers, the decode attention over two slabs, the
+    gate as PyTorch ops) equals the whole-text layer position by position."""
+    from asrn_amd.escritura import EscritorCapa
+    B, L0, n, d = 2, 200, 40, 2048
+    say('writer d 2048 = whole text', B, L0, n, d)
+    torch.manual_seed(0)
+    layer = synth.move_params(CapaASRNEstable(d), 0).to(DEV)
+    x, E, h = synth.layer_inputs(B, L0 + n, d, 12, seed=4, frac=0.4, span=(3, 8))
+    Ed, hd, xd = E.to(DEV), h.to(DEV), x.to(DEV)
+    esc = EscritorCapa(layer, memoria_de_lo_ajeno=False)
+    with torch.no_grad():
+        y0 = esc.inicio(Ed[:, :L0], hd[:, :L0], xd[:, :L0], capacidad=L0 + n)
+        ys = torch.stack([esc.paso(Ed[:, t], hd[:, t], xd[:, t]) for t in range(L0, L0 + n)], 1)
+        y = layer(Ed, hd, xd)
+        whole, _ = layer._phi_y_valores(Ed)
+        step = torch.stack([layer._phi_y_valores(Ed[:, max(0, t - 1):t + 1])[0][:, -1] for t in range(L0 + n)], 1)
+    if not torch.equal(O.bucket_ids(whole.cpu(), 8, 14), O.bucket_ids(step.cpu(), 8, 14)):
+        pytest.skip('a bucket id differs between the step GEMM and the whole-text GEMM (sign of phi near 0)')
+    e0 = ((y0 - y[:, :L0]).abs().max() / y.abs().max()).item()
+    e1 = ((ys - y[:, L0:]).abs().max() / y.abs().max()).item()
+    print(f'  prompt {e0:.2e}, steps {e1:.2e}', flush=True)
+    assert e0 <= 1e-3 and e1 <= 1e-3
+
+
+def test_tallas_1b_forward_backward():
+    """The named size '1b' (d 2,048, 27 local blocks, 13 ASRN layers, V 32,768; 1.0 B parameters in fp32) runs a
+    forward and backward on one GPU: finite loss and gradients, and the loss equals a second forward's bit for bit."""
+    say("TALLAS['1b'] forward + backward", 1, 256)
+    m = asrn_amd.crear_desde_config('1b', semilla=0).to(DEV).train()
+    assert m.largos[0].v.weight.shape[0] == 2048
+    x = synth.tokens(1, 257, 32768, frac=0.2, span=(8, 32), zipf=1.1, seed=0).to(DEV)
+    perdida = m.perdida(x[:, :-1], x[:, 1:])
+    perdida.backward()
+    torch.cuda.synchronize()
+    print(f'  {m.num_parametros() / 1e9:.3f} B parameters, loss {float(perdida):.5f}', flush=True)
+    assert torch.isfinite(perdida)
+    for nombre, q in m.named_parameters():
+        assert q.grad is not None and torch.isfinite(q.grad).all(), nombre
+    with torch.no_grad():
+        assert float(m.perdida(x[:, :-1], x[:, 1:])) == float(perdida)

@@ -64,19 +64,19 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert 'workspace' in _err(lib)
     args = [N] * 12 + [2, 16]
     # d not a multiple of 4
-    assert lib.asrn_candidates_fwd(*args, 6, 112, 16, 4, 8, 4, 32, 0.1, 0.25, 6, 0, 16, 0, N, N, N, N, N) != 0
+    assert lib.asrn_candidates_fwd(*args, 6, 112, 16, 4, 8, 4, 32, 0.1, 0.25, 6, 0, 16, 0, N, N, N, N, 0, N, N) != 0
     assert 'd=6' in _err(lib)
     # chunk above 64
-    assert lib.asrn_candidates_fwd(*args, 64, 112, 16, 4, 8, 4, 65, 0.1, 0.25, 64, 0, 16, 0, N, N, N, N, N) != 0
+    assert lib.asrn_candidates_fwd(*args, 64, 112, 16, 4, 8, 4, 65, 0.1, 0.25, 64, 0, 16, 0, N, N, N, N, 0, N, N) != 0
     assert 'chunk' in _err(lib)
     # feature width above 256
     assert lib.asrn_candidates_bwd(*args, 64, 250, 16, 4, 8, 4, 32, 0.1, 0.25, 64, 0, 16, 0, *([N] * 11)) != 0
     assert 'P + cf' in _err(lib)
     # feature widths are read as float4 (the host pads them)
-    assert lib.asrn_candidates_fwd(*args, 64, 110, 16, 4, 8, 4, 32, 0.1, 0.25, 64, 0, 16, 0, N, N, N, N, N) != 0
+    assert lib.asrn_candidates_fwd(*args, 64, 110, 16, 4, 8, 4, 32, 0.1, 0.25, 64, 0, 16, 0, N, N, N, N, 0, N, N) != 0
     assert 'multiples of 4' in _err(lib)
     # V row stride below d
-    assert lib.asrn_candidates_fwd(*args, 64, 112, 16, 4, 8, 4, 32, 0.1, 0.25, 60, 1, 16, 0, N, N, N, N, N) != 0
+    assert lib.asrn_candidates_fwd(*args, 64, 112, 16, 4, 8, 4, 32, 0.1, 0.25, 60, 1, 16, 0, N, N, N, N, 0, N, N) != 0
     assert 'ldv' in _err(lib)
     # the candidate-list records: 16-byte multiples, sized for T * C entries and uniques
     assert lib.asrn_candidates_record_bytes(8, 32) % 16 == 0 and lib.asrn_candidates_record_bytes(8, 32) >= 11 * 256
@@ -141,11 +141,11 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert lib.asrn_ring_build(N, N, 2, 10, 8, 15, 32, N, N, N) != 0
     assert 'asrn_ring_build' in _err(lib)
     assert lib.asrn_decode_attend(*([N] * 11), 2, 100, 100, N, 64, 14, 16, 4, 8, 4, 32, 0.1, 0.25, 1, N, N, N,
-                                  N) != 0
+                                  N, N) != 0
     assert 'outside the caches' in _err(lib)
     assert lib.asrn_hawkes_table_load(*([N] * 6), 2, 100, 4, 96, N, N, N, N) != 0
     assert 'power of two' in _err(lib)
-    assert lib.asrn_repetition_step(*([N] * 7), 2, 1000, 100, N, 4, 128, *([N] * 7)) != 0
+    assert lib.asrn_repetition_step(*([N] * 7), 2, 1000, 100, N, 4, 128, *([N] * 6), 0, N) != 0
     assert 'grow it first' in _err(lib)
     assert lib.asrn_hawkes_table_grow(N, N, N, 8, 256, N, N, N, 128, N) != 0
     assert 'growing' in _err(lib)
