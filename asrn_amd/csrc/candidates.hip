@@ -18,6 +18,8 @@
 // output row, no atomics and no score recomputation: a query pass (ds = att (dp - D) with D = sum att*dp per (query,
 // table), written next to att; query-side gradients; per-query partials of d gamma and d w_suf) and a key pass
 // (key-side gradients: reads each (att, ds) pair with one 8-byte load at the slots of the queries that see the key).
+#include <type_traits>
+
 #include "common.h"
 
 namespace asrn {
@@ -62,12 +64,20 @@ struct Cand {
   // counts the (query, table) pairs whose best valid score is within the -1e9 fill's reach, where the reference's
   // fill gives its invalid keys weight
   int clock32; int32_t* leak;
+  // ceil(2^64 / L) (0 when L = 1): a token index's batch row is the high half of its 64-bit product with this
+  uint64_t Linv;
 };
+
+// i / L for 0 <= i < 2^32: the high half of i * ceil(2^64 / L) (the product exceeds i * 2^64 / L by less than
+// i / L * L / 2^64 < 2^-32 <= 1 / L, which cannot carry the quotient past its floor)
+__device__ __forceinline__ int64_t row_of(const Cand& a, int64_t i) {
+  return a.Linv ? (int64_t)__umul64hi((uint64_t)i, a.Linv) : i;
+}
 
 // per-wave LDS scratch: one token's candidate list (entries) and its distinct positions (uniques)
 constexpr int kHash = 3 * kMaxSlots / 2;   // dedupe hash slots: at most kMaxSlots distinct positions (load <= 2/3)
 
-struct Scratch {
+struct alignas(16) Scratch {
   int key[kMaxSlots];      // entry: (position << 5) | table
   uint8_t uid[kMaxSlots];  // entry -> unique (fewer than kMaxSlots = 256)
   int upos[kMaxSlots];     // unique: position
@@ -131,8 +141,8 @@ __device__ __forceinline__ int64_t token_of_wave() {
 #ifndef ASRN_SORTED_TABLE
 #define ASRN_SORTED_TABLE 0
 #endif
-struct Cand;
-__device__ __forceinline__ int64_t sorted_token_of_wave(const Cand& a);
+struct TokAt { int64_t b, t, tok; };   // batch row, position, b * L + t (tok < 0: past the end); wave-uniform
+__device__ __forceinline__ TokAt sorted_token_of_wave(const Cand& a);
 
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -208,14 +218,38 @@ __device__ __forceinline__ FeatLanes<F4> feat_lanes(const Cand& a, const float* 
   return fl;
 }
 
+// scaled: times the lane's scale (the query's own row; also zeroes the lanes past P + cf). Rows read unscaled meet
+// such a row in a product, whose dead lanes are then zero, or are summed with weights and scaled once at the end.
 template <int F4, bool FB16 = false>
-__device__ __forceinline__ void feat_row(const FeatLanes<F4>& fl, uint32_t row, float4 (&f)[F4]) {
+__device__ __forceinline__ void feat_row(const FeatLanes<F4>& fl, uint32_t row, float4 (&f)[F4], bool scaled = true) {
 #pragma unroll
   for (int c = 0; c < F4; ++c) {
     float4 v = ld4r<FB16>(fl.base[c], row * fl.stride[c]);
-    v.x *= fl.scale[c]; v.y *= fl.scale[c]; v.z *= fl.scale[c]; v.w *= fl.scale[c];
+    if (scaled) {
+      v.x *= fl.scale[c]; v.y *= fl.scale[c]; v.z *= fl.scale[c]; v.w *= fl.scale[c];
+    }
     f[c] = v;
   }
+}
+
+// Runs body(n, u0) over the chunks [u0, u0 + n) of [first, NU), one every `step`: n is NF, or the smallest of
+// N2 >= N3 that covers what is left, so a short tail does not load a full chunk of idle rows (n is a compile-time
+// constant: the row arrays stay in registers). By default N2 = NF / 2 and N3 = NF / 4; NF = 12 takes 8 and 4.
+template <int NF, int N2 = (NF % 3 == 0 ? 2 * NF / 3 : NF / 2), int N3 = (NF % 3 == 0 ? NF / 3 : NF / 4), class F>
+__device__ __forceinline__ void for_chunks(int first, int NU, int step, F&& body) {
+  for (int u0 = first; u0 < NU; u0 += step) {
+    const int rem = NU - u0;
+    if (rem > N2) body(std::integral_constant<int, NF>{}, u0);
+    else if (rem > N3) body(std::integral_constant<int, N2>{}, u0);
+    else body(std::integral_constant<int, N3>{}, u0);
+  }
+}
+
+// the sums of the two 32-lane halves land in lane 16 (lanes 0-31) and lane 48 (lanes 32-63); the other lanes hold
+// partial sums. Adds row 0 + row 1 and row 2 + row 3 of the 16-lane row sums, as readlane sums would.
+__device__ __forceinline__ float half_sums_at_16_48(float v) {
+  v = row_sum16(v);
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));  // row_bcast:15
 }
 
 template <int F4>
@@ -290,7 +324,7 @@ __device__ __forceinline__ int gather(const Cand& a, int64_t b, int64_t t, bool 
   const int lane = lane_id();
   int s = 0, n = 0;
   if (lane < a.T) {
-    const int64_t o = (b * a.L + t) * a.T + lane;
+    const uint32_t o = (uint32_t)((b * a.L + t) * a.T) + (uint32_t)lane;   // B L T < 2^31 (check_args)
     s = a.rank[o];
     const int w = a.win[o];
     n = query_window ? (w & 255) : ((w >> 8) & 255);
@@ -318,9 +352,9 @@ __device__ __forceinline__ int gather(const Cand& a, int64_t b, int64_t t, bool 
       const int i = m - S.off[lo];
       // query window: ranks s - n .. s - 1; key window: s + 1 .. s + n (in range by construction; clamped so that
       // inconsistent inputs cannot read out of bounds)
-      int64_t j = query_window ? (int64_t)S.wrank[lo] - (S.off[lo + 1] - S.off[lo]) + i : (int64_t)S.wrank[lo] + 1 + i;
-      j = j < 0 ? 0 : (j >= a.L ? a.L - 1 : j);
-      int pos = a.order[(b * a.T + lo) * a.L + j];
+      int j = query_window ? S.wrank[lo] - (S.off[lo + 1] - S.off[lo]) + i : S.wrank[lo] + 1 + i;
+      j = j < 0 ? 0 : (j >= a.L ? (int)a.L - 1 : j);
+      int pos = a.order[(uint32_t)((b * a.T) * a.L) + (uint32_t)lo * (uint32_t)a.L + (uint32_t)j];
       pos = pos < 0 ? 0 : (pos >= a.L ? (int)a.L - 1 : pos);          // a position whatever the sort left
       S.key[m] = (pos << 5) | lo;
     }
@@ -382,13 +416,14 @@ __device__ __forceinline__ int gather_rings(const Cand& a, int64_t b, int64_t t,
 // Every entry claims its position's slot in an LDS hash table (compare-and-swap, linear probing) and keeps the
 // smallest entry index there (atomic min, order-independent), so the numbering is deterministic.
 // a slot in [0, kHash): the high part of (Knuth's multiplicative hash) * kHash
-__device__ __forceinline__ uint32_t pos_hash(int pos) {
-  return (uint32_t)(((uint64_t)((uint32_t)pos * 2654435761u) * (uint64_t)kHash) >> 32);
+__device__ __forceinline__ uint32_t pos_hash(int pos, uint32_t slots) {
+  return __umulhi((uint32_t)pos * 2654435761u, slots);
 }
 
 __device__ __forceinline__ int dedupe(const Cand& a, int M, Scratch& S) {
   const int lane = lane_id();
-  for (int i = lane; i < kHash; i += kWave) {
+  const uint32_t hs = M <= kWave ? 2 * kWave : kHash;   // slots in use: load <= 1/2 for lists of up to 64 entries
+  for (int i = lane; i < (int)hs; i += kWave) {
     S.hpos[i] = -1;
     S.hfirst[i] = 0x7fffffff;
   }
@@ -400,11 +435,11 @@ __device__ __forceinline__ int dedupe(const Cand& a, int M, Scratch& S) {
     const int m = c * kWave + lane;
     if (c * kWave < M && m < M) {
       const int pos = S.key[m] >> 5;
-      uint32_t h = pos_hash(pos);
-      for (int probe = 0; probe < kHash; ++probe) {
+      uint32_t h = pos_hash(pos, hs);
+      for (uint32_t probe = 0; probe < hs; ++probe) {
         const int old = atomicCAS(&S.hpos[h], -1, pos);
         if (old == -1 || old == pos) break;
-        h = h + 1 == (uint32_t)kHash ? 0u : h + 1;
+        h = h + 1 == hs ? 0u : h + 1;
       }
       atomicMin(&S.hfirst[h], m);
       slot[c] = (int)h;
@@ -450,27 +485,102 @@ __device__ __forceinline__ void unique_bases(const Cand& a, int64_t b, int64_t s
   const int lane = lane_id(), half = lane >> 5;
   const FeatLanes<F4> fl = feat_lanes<F4, FB16>(a, rows_are_queries ? a.Qc : a.Kc, rows_are_queries);
   const uint32_t row0 = (uint32_t)(b * a.L);
-  for (int u0 = first; u0 < NU; u0 += step) {   // chunks of 2 kRows uniques
-    float4 f[kRows][F4];
+  // the fixed side's dead lanes are zero when it is the query's scaled row; key rows then need no scaling
+  const bool scale_rows = rows_are_queries;
+  for_chunks<2 * kRows>(first, NU, step, [&](auto n, int u0) {
+    constexpr int R = decltype(n)::value / 2;          // rows per half-wave
+    int pos[R];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
+    for (int r = 0; r < R; ++r) {                      // every position read before any row load
       const int u = u0 + 2 * r + half;
-      feat_row<F4, FB16>(fl, row0 + (uint32_t)(u < NU ? S.upos[u] : self_pos), f[r]);
+      pos[r] = S.upos[u < NU ? u : NU - 1];
     }
-    float p[kRows];
+    float4 f[R][F4];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) p[r] = rows_are_queries ? dot_f(f[r], fixed) : dot_f(fixed, f[r]);
+    for (int r = 0; r < R; ++r) feat_row<F4, FB16>(fl, row0 + (uint32_t)pos[r], f[r], scale_rows);
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-      float h0, h1;
-      half_sums_u(p[r], &h0, &h1);
-      const int u = u0 + 2 * r;
-      if (lane == 0) {
-        if (u < NU) S.ua[u] = h0;
-        if (u + 1 < NU) S.ua[u + 1] = h1;
-      }
+    for (int r = 0; r < R; ++r) {
+      const float h = half_sums_at_16_48(rows_are_queries ? dot_f(f[r], fixed) : dot_f(fixed, f[r]));
+      const int u = u0 + 2 * r + half;
+      if ((lane & 31) == 16 && u < NU) S.ua[u] = h;
     }
+  });
+  (void)self_pos;
+  wave_lds_sync();
+}
+
+// The base scores with P + cf <= 128 (F4 == 1): each aligned group of 8 lanes (g = lane / 8, j = lane % 8) reads one
+// candidate's [phi ; Kc] row, lane j holding features 32 k + 4 j .. + 3 of chunk k = 0..3. One load instruction then
+// covers 128 contiguous bytes of each of 8 rows, a lane's 16 products need no cross-lane step until the group's
+// 3-step DPP sum, and 16 rows cost 8 loads, 32 FMAs and 6 DPP adds per lane.
+struct Feat8 {
+  const float* base[4];   // per chunk: phi + f, conf + (f - P), or phi itself for dead lanes (f >= P + cf)
+  bool conf[4];           // the chunk's rows have conf's stride ldq instead of P
+  float scale[4];         // scale_phi, scale_c, or 0 past P + cf
+};
+template <bool FB16>
+__device__ __forceinline__ Feat8 feat8(const Cand& a, const float* conf, bool scaled) {
+  Feat8 fl;
+  const int j = lane_id() & 7;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int f = 32 * k + 4 * j;
+    const bool in_phi = f < a.P, live = f < a.P + a.cf;
+    fl.base[k] = in_phi ? rows_at<FB16>(a.phi, f) : (live ? rows_at<FB16>(conf, f - a.P) : a.phi);
+    fl.conf[k] = !in_phi && live;
+    fl.scale[k] = !live ? 0.f : (scaled ? (in_phi ? a.sp : a.sc) : 1.f);
   }
+  return fl;
+}
+template <bool FB16>
+__device__ __forceinline__ void feat8_row(const Cand& a, const Feat8& fl, uint32_t row, float4 (&f)[4], bool scaled) {
+  const uint32_t op = row * (uint32_t)a.P, oc = row * (uint32_t)a.ldq;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float4 v = ld4r<FB16>(fl.base[k], fl.conf[k] ? oc : op);
+    if (scaled) {
+      v.x *= fl.scale[k]; v.y *= fl.scale[k]; v.z *= fl.scale[k]; v.w *= fl.scale[k];
+    }
+    f[k] = v;
+  }
+}
+// the sum over each aligned group of 8 lanes, in all 8 (pairs, then quads, then the half-row mirror adds the quads)
+__device__ __forceinline__ float group8_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm 1032
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm 2301
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // half mirror
+}
+// query side of the base scores: S.ua[u] = <query's scaled [phi ; Qc], [phi_u ; Kc_u]> for the uniques of chunks of
+// 16 starting at `first`, one every `step`
+template <bool FB16>
+__device__ __forceinline__ void unique_bases8(const Cand& a, int64_t b, int64_t tok, int NU, Scratch& S, int first,
+                                              int step) {
+  const int lane = lane_id(), g = lane >> 3;
+  float4 q[4];
+  feat8_row<FB16>(a, feat8<FB16>(a, a.Qc, true), (uint32_t)tok, q, true);
+  const Feat8 fl = feat8<FB16>(a, a.Kc, false);
+  const uint32_t row0 = (uint32_t)(b * a.L);
+  for_chunks<16>(first, NU, step, [&](auto n, int u0) {
+    constexpr int RG = decltype(n)::value >= 8 ? decltype(n)::value / 8 : 1;   // row groups of 8 in flight
+    int pos[RG];
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {                     // every position read before any row load
+      const int u = u0 + 8 * r + g;
+      pos[r] = S.upos[u < NU ? u : NU - 1];
+    }
+    float4 f[RG][4];
+#pragma unroll
+    for (int r = 0; r < RG; ++r) feat8_row<FB16>(a, fl, row0 + (uint32_t)pos[r], f[r], false);
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      float p = dot4(q[0], f[r][0]);
+#pragma unroll
+      for (int k = 1; k < 4; ++k) p += dot4(q[k], f[r][k]);
+      p = group8_sum(p);
+      const int u = u0 + 8 * r + g;
+      if ((lane & 7) == 0 && u < NU) S.ua[u] = p;
+    }
+  });
   wave_lds_sync();
 }
 
@@ -484,28 +594,33 @@ __device__ __forceinline__ void unique_feature_sum(const Cand& a, int64_t b, int
   const uint32_t row0 = (uint32_t)(b * a.L);
 #pragma unroll
   for (int c = 0; c < F4; ++c) g[c] = zero4();
-  for (int u0 = 0; u0 < NU; u0 += 2 * kRows) {
-    float4 f[kRows][F4];
-    float w[kRows];
+  for_chunks<2 * kRows>(0, NU, 2 * kRows, [&](auto n, int u0) {
+    constexpr int R = decltype(n)::value / 2;          // rows per half-wave
+    int pos[R];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
+    for (int r = 0; r < R; ++r) {                      // every position read before any row load
       const int u = u0 + 2 * r + half;
-      const bool ok = u < NU;
-      feat_row<F4, FB16>(fl, row0 + (uint32_t)(ok ? S.upos[u] : self_pos), f[r]);
-      w[r] = ok ? wts[u] : 0.f;
+      pos[r] = S.upos[u < NU ? u : NU - 1];
     }
+    float4 f[R][F4];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r)
+    for (int r = 0; r < R; ++r) feat_row<F4, FB16>(fl, row0 + (uint32_t)pos[r], f[r], false);
 #pragma unroll
-      for (int c = 0; c < F4; ++c) fma4(g[c], w[r], f[r][c]);
+    for (int r = 0; r < R; ++r) {                      // the weights, read while the rows are in flight
+      const int u = u0 + 2 * r + half;
+      const float w = u < NU ? wts[u] : 0.f;
+#pragma unroll
+      for (int c = 0; c < F4; ++c) fma4(g[c], w, f[r][c]);
+    }
+  });
+#pragma unroll
+  for (int c = 0; c < F4; ++c) {   // both halves combined, then the lane's scale (zero past P + cf) once
+    g[c].x = (g[c].x + __shfl_xor(g[c].x, 32, 64)) * fl.scale[c];
+    g[c].y = (g[c].y + __shfl_xor(g[c].y, 32, 64)) * fl.scale[c];
+    g[c].z = (g[c].z + __shfl_xor(g[c].z, 32, 64)) * fl.scale[c];
+    g[c].w = (g[c].w + __shfl_xor(g[c].w, 32, 64)) * fl.scale[c];
   }
-#pragma unroll
-  for (int c = 0; c < F4; ++c) {
-    g[c].x += __shfl_xor(g[c].x, 32, 64);
-    g[c].y += __shfl_xor(g[c].y, 32, 64);
-    g[c].z += __shfl_xor(g[c].z, 32, 64);
-    g[c].w += __shfl_xor(g[c].w, 32, 64);
-  }
+  (void)self_pos;
 }
 
 // Widths past 256 * DCH (d > 1024) run the value phases over column slabs of 256 * DCH: columns c0 .. c0 + 256 DCH - 1
@@ -519,38 +634,79 @@ __device__ __forceinline__ int slab_col(const Cand& a, int c0, int ch, int lane)
 // out[u] (added to it when `add`: the slabs after the first); the key side (w_u != nullptr) also accumulates
 // dV += w_u row_u from the same loads. fixed holds columns c0 .. c0 + 256 DCH - 1 (zero past d).
 template <int DCH, bool B16 = false>
-__device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows, int64_t ld, int64_t self_pos,
-                                                int NU, const float4 (&fixed)[DCH], const float* w_u,
-                                                float4 (&dv)[DCH], Scratch& S, float* out, int c0 = 0,
+__device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows, int64_t ld, int NU,
+                                                const float4 (&fixed)[DCH], Scratch& S, float* out, int c0 = 0,
                                                 bool add = false) {
   const int lane = lane_id();
-  constexpr int R = DCH >= 3 ? 2 : (DCH == 2 ? 4 : 8);
-  for (int u0 = 0; u0 < NU; u0 += R) {
+  constexpr int NF = DCH >= 3 ? 4 : (DCH == 2 ? 4 : 8);
+  int col[DCH];
+#pragma unroll
+  for (int ch = 0; ch < DCH; ++ch) col[ch] = slab_col(a, c0, ch, lane);
+  for_chunks<NF>(0, NU, NF, [&](auto n, int u0) {
+    constexpr int R = decltype(n)::value;
+    int p[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)                        // wave-uniform rows: their offsets are scalar arithmetic
+      p[r] = __builtin_amdgcn_readfirstlane(S.upos[u0 + r < NU ? u0 + r : NU - 1]);
     float4 o[R][DCH];
-    float w[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int u = u0 + r;
-      const bool ok = u < NU;
-      const int64_t row = ok ? S.upos[u] : self_pos;
-      w[r] = (ok && w_u) ? w_u[u] : 0.f;
+      const float* row = rows_at<B16>(rows, (int64_t)(uint32_t)p[r] * ld);
 #pragma unroll
-      for (int ch = 0; ch < DCH; ++ch)
-        o[r][ch] = ld4r<B16>(rows, (uint32_t)row * (uint32_t)ld + (uint32_t)slab_col(a, c0, ch, lane));
+      for (int ch = 0; ch < DCH; ++ch) o[r][ch] = ld4r<B16>(row, (uint32_t)col[ch]);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      float p = 0.f;
+      float q = 0.f;
 #pragma unroll
-      for (int ch = 0; ch < DCH; ++ch) {
-        p += dot4(o[r][ch], fixed[ch]);
-        if (w_u) fma4(dv[ch], w[r], o[r][ch]);
-      }
-      const float tot = wave_sum_u(p);
+      for (int ch = 0; ch < DCH; ++ch) q += dot4(o[r][ch], fixed[ch]);
+      const float tot = wave_sum_u(q);
       if (lane == 0 && u0 + r < NU) out[u0 + r] = add ? out[u0 + r] + tot : tot;
     }
-  }
+  });
   wave_lds_sync();
+}
+
+// Per unique, the sums over tables of NV per-entry values, in table order: out[v][u] = the sum, tables ascending, of
+// val[v][c] over the entries c * 64 + lane of unique u (tau[c] < 0: no entry; a unique appears at most once in a
+// table). Each pass zeroes a cell per (unique, value, table) for the uniques [u0, u0 + per) in `slots` (nslot floats of
+// LDS that are dead during the call, 16-byte aligned), every entry writes its cell, then lane u adds its cells in
+// table order (the absent tables' cells add exact zeros, so the sums equal those of a table-by-table loop).
+template <int NV>
+__device__ __forceinline__ void unique_table_sums(int T, int NU, const int (&tau)[kCh], const int (&un)[kCh],
+                                                  const float (&val)[NV][kCh], float* slots, int nslot,
+                                                  float* const (&out)[NV]) {
+  const int lane = lane_id();
+  int tp = 4;                                   // cells per (unique, value): T rounded up to a power of 2, >= 4
+  while (tp < T) tp <<= 1;
+  const int per = nslot / (tp * NV);
+  wave_lds_sync();                              // the slots' earlier readers are done
+  for (int u0 = 0; u0 < NU; u0 += per) {
+    for (int i = 4 * lane; i < per * tp * NV; i += 4 * kWave) *reinterpret_cast<float4*>(slots + i) = zero4();
+    wave_lds_sync();
+#pragma unroll
+    for (int c = 0; c < kCh; ++c) {
+      const int u = un[c] - u0;
+      if (tau[c] >= 0 && u >= 0 && u < per) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) slots[(u * NV + v) * tp + tau[c]] = val[v][c];
+      }
+    }
+    wave_lds_sync();
+    for (int u = u0 + lane; u < NU && u < u0 + per; u += kWave) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const float* cell = slots + ((u - u0) * NV + v) * tp;
+        float acc = 0.f;
+        for (int t4 = 0; t4 < tp; t4 += 4) {
+          const float4 q = *reinterpret_cast<const float4*>(cell + t4);
+          acc += q.x; acc += q.y; acc += q.z; acc += q.w;
+        }
+        out[v][u] = acc;
+      }
+    }
+    wave_lds_sync();
+  }
 }
 
 // Entries of the candidate list held one per lane (entry c*64 + lane in chunk c).
@@ -565,6 +721,7 @@ struct Entries {
 // S.ub = B_k (nucleo:330-332: no fused multiply-add, each product and sum rounded on its own).
 __device__ __forceinline__ void load_entries(const Cand& a, int M, const Scratch& S, Entries& E) {
   const int lane = lane_id();
+  const float rate_l = lane < a.T ? rate_of(a, lane) : 0.f;   // one division per table, shuffled to the entries
 #pragma unroll
   for (int c = 0; c < kCh; ++c) {
     const int m = c * kWave + lane;
@@ -573,7 +730,7 @@ __device__ __forceinline__ void load_entries(const Cand& a, int M, const Scratch
     E.tau[c] = in ? (e & 31) : -1;
     const int u = in ? S.uid[m] : 0;
     E.u[c] = u;
-    const float r = rate_of(a, e & 31);
+    const float r = __shfl(rate_l, e & 31, kWave);          // every lane takes part (no divergent shuffle)
     E.sc[c] = !in ? -INFINITY
                   : (a.clock32 ? __fsub_rn(__fadd_rn(S.ua[u], __fadd_rn(S.uc[u], __fmul_rn(r, S.ub[u]))),
                                            __fmul_rn(r, S.bq32))
@@ -658,23 +815,31 @@ __device__ __forceinline__ void gather_values(const Cand& a, int64_t b, const Sc
   constexpr int UNR = gather_rows_in_flight<DCH>();
   const int lane = lane_id();
   const float* Vb = rows_at<B16>(a.V, (b * a.L + a.vshift) * a.ldv);
-  for (int u0 = first; u0 < NU; u0 += step) {
-    float4 v[UNR][DCH];
-    float w[UNR];
+  int col[DCH];
 #pragma unroll
-    for (int r = 0; r < UNR; ++r) {
-      const bool ok = u0 + r < NU;
-      const int64_t p = ok ? S.upos[u0 + r] : 0;   // idle lanes read position 0 (always a V row, weight 0)
-      w[r] = ok ? S.uc[u0 + r] : 0.f;
+  for (int ch = 0; ch < DCH; ++ch) col[ch] = slab_col(a, c0, ch, lane);
+  for_chunks<UNR>(first, NU, step, [&](auto n, int u0) {
+    constexpr int R = decltype(n)::value;
+    int p[R];
+    float w[R];
 #pragma unroll
-      for (int ch = 0; ch < DCH; ++ch)
-        v[r][ch] = ld4r<B16>(Vb, (uint32_t)p * (uint32_t)a.ldv + (uint32_t)slab_col(a, c0, ch, lane));
+    for (int r = 0; r < R; ++r) {                      // wave-uniform rows and weights: scalar offsets
+      const int u = u0 + r < NU ? u0 + r : NU - 1;
+      p[r] = __builtin_amdgcn_readfirstlane(S.upos[u]);
+      w[r] = u0 + r < NU ? S.uc[u] : 0.f;            // the same in every lane (an LDS broadcast)
+    }
+    float4 v[R][DCH];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float* row = rows_at<B16>(Vb, (int64_t)(uint32_t)p[r] * a.ldv);
+#pragma unroll
+      for (int ch = 0; ch < DCH; ++ch) v[r][ch] = ld4r<B16>(row, (uint32_t)col[ch]);
     }
 #pragma unroll
-    for (int r = 0; r < UNR; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int ch = 0; ch < DCH; ++ch) fma4(acc[ch], w[r], v[r][ch]);
-  }
+  });
 }
 
 // A query token's candidate list (gather and dedupe; the record's header and entries when it is kept): returns the
@@ -705,39 +870,47 @@ __device__ __forceinline__ void unique_terms(const Cand& a, int64_t b, int64_t t
   const int lane = lane_id();
   const int64_t tok = b * a.L + t;
   const RecLayout R = rec_layout(a.T, a.C);
-  float4 qf[F4];
-  feat_row<F4, FB16>(feat_lanes<F4, FB16>(a, a.Qc, true), (uint32_t)tok, qf);
-  unique_bases<F4, FB16>(a, b, t, NU, false, qf, S, wave * 2 * kRows, NW * 2 * kRows);
+  if constexpr (F4 == 1) {
+    unique_bases8<FB16>(a, b, tok, NU, S, wave * 2 * kRows, NW * 2 * kRows);
+  } else {
+    float4 qf[F4];
+    feat_row<F4, FB16>(feat_lanes<F4, FB16>(a, a.Qc, true), (uint32_t)tok, qf);
+    unique_bases<F4, FB16>(a, b, t, NU, false, qf, S, wave * 2 * kRows, NW * 2 * kRows);
+  }
   const float* sigb = a.sig + b * a.L;
   float mine[4];
   own_suffix_of(sigb, t, a.K, mine);
   const double bq = a.Bt[tok];
+  const float wsuf_l = lane <= a.K ? a.w_suf[lane] : 0.f;   // w_suf[x] in lane x (K <= 16), read by shuffles
   if (a.clock32 && lane == 0 && wave == 0) S.bq32 = (float)bq;
-  auto one = [&](int u) {
-    const int64_t k = S.upos[u];
+  // lanes take uniques u0 + lane (NW == 1: all 64 lanes; NW > 1: the first 2 kRows lanes of each wave's chunks);
+  // the loop is wave-uniform, so every lane takes part in the shuffle
+  const int per = NW == 1 ? kWave : 2 * kRows;
+  for (int u0 = NW == 1 ? 0 : wave * 2 * kRows; u0 < NU; u0 += NW * per) {
+    const int u = u0 + lane;
+    const bool in = lane < per && u < NU;
+    const int64_t k = S.upos[in ? u : NU - 1];
     const int ell = suffix_len_of(sigb, mine, t, k, a.K);
     const double bk = a.Bt[b * a.L + k];
+    const float la = a.la[b * a.L + k];
     const float db = (float)(bk - bq);     // with the fp32 clock, the fp32 difference of the two values
-    if (a.clock32) {                       // the clock term is formed per entry (load_entries)
-      S.ua[u] = S.ua[u] + a.w_suf[ell];
-      S.ub[u] = (float)bk;
-      S.uc[u] = a.la[b * a.L + k];
-    } else {
-      S.ua[u] = (S.ua[u] + a.w_suf[ell]) + a.la[b * a.L + k];
-      S.ub[u] = db;
-      S.uc[u] = 0.f;
+    const float ws = __shfl(wsuf_l, ell, kWave);
+    if (in) {
+      if (a.clock32) {                     // the clock term is formed per entry (load_entries)
+        S.ua[u] = S.ua[u] + ws;
+        S.ub[u] = (float)bk;
+        S.uc[u] = la;
+      } else {
+        S.ua[u] = (S.ua[u] + ws) + la;
+        S.ub[u] = db;
+        S.uc[u] = 0.f;
+      }
+      if (rec) {
+        reinterpret_cast<int32_t*>(rec + R.upos)[u] = (int32_t)k;
+        reinterpret_cast<float*>(rec + R.ub)[u] = db;
+        rec[R.uell + u] = (uint8_t)ell;
+      }
     }
-    if (rec) {
-      reinterpret_cast<int32_t*>(rec + R.upos)[u] = (int32_t)k;
-      reinterpret_cast<float*>(rec + R.ub)[u] = db;
-      rec[R.uell + u] = (uint8_t)ell;
-    }
-  };
-  if constexpr (NW == 1) {
-    for (int u = lane; u < NU; u += kWave) one(u);
-  } else {
-    for (int c0 = wave * 2 * kRows; c0 < NU; c0 += NW * 2 * kRows)
-      if (lane < 2 * kRows && c0 + lane < NU) one(c0 + lane);
   }
   wave_lds_sync();
 }
@@ -774,10 +947,6 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
   load_entries(a, M, S, E);
   uint32_t* tmax = reinterpret_cast<uint32_t*>(S.tsum);
   if (lane < a.T) tmax[lane] = 0u;                       // below every key
-  if (a.clock32) {                                       // uc held log_alfa_k for the scores: it sums weights now
-    wave_lds_sync();
-    for (int u = lane; u < NU; u += kWave) S.uc[u] = 0.f;
-  }
   wave_lds_sync();
 #pragma unroll
   for (int c = 0; c < kCh; ++c)
@@ -821,16 +990,17 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
       if (ent_rows) ent_rows[2 * (E.tau[c] * a.C + (S.off[E.tau[c] + 1] - 1 - m))] = w[c];   // entries ascend
     }
   }
-  for (int tt = 0; tt < a.T; ++tt) {                     // sum over tables per unique, in table order
+  {                                                      // per unique, the weights summed over tables (S.uc)
+    float wv[1][kCh];
 #pragma unroll
-    for (int c = 0; c < kCh; ++c)
-      if (E.tau[c] == tt) S.uc[E.u[c]] += w[c];          // uniques are distinct within a table
-    wave_lds_sync();
+    for (int c = 0; c < kCh; ++c) wv[0][c] = w[c];
+    float* const out[1] = {S.uc};
+    unique_table_sums<1>(a.T, NU, E.tau, E.u, wv, S.ua, 2 * kMaxSlots, out);   // ua and ub are dead here
   }
-  const float pt = wave_sum_u(has ? 1.f : 0.f);
+  const float pt = (float)__popcll(__ballot(has));       // has is set in lead lanes only
   const float best = wave_max_u(mx);
   const float pico = wave_sum_u(inv);                    // the largest weight of a table is exp(0) / den
-  const float pctx = wave_sum_u(has && tg >= a.T - a.Tc ? 1.f : 0.f);
+  const float pctx = (float)__popcll(__ballot(has && tg >= a.T - a.Tc));
 
   if (lane == 0) {
     signals_row[0] = pt;
@@ -856,14 +1026,14 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
 
 // RB: how V (and the backward's dO) and the features [phi ; Qc ; Kc] are stored: 0 fp32; 1 V and dO bf16; 2 all bf16
 template <int F4, int DCH, int RB>
-__global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 6 : 1) void k_cand_fwd(Cand a) {   // 6 waves per SIMD when narrow
+__global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 7 : 1) void k_cand_fwd(Cand a) {   // 7 waves per SIMD when narrow
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
-  const int64_t tok = sorted_token_of_wave(a);
-  if (tok >= a.B * a.L) return;
+  const TokAt at = sorted_token_of_wave(a);
+  if (at.tok < 0) return;
+  const int64_t tok = at.tok;
   float* salida_row = const_cast<float*>(rows_at<RB >= 1>(a.salida, tok * a.d));   // bf16 with the value rows
-  forward_token<F4, DCH, false, RB>(a, tok / a.L, tok % a.L, S, salida_row, a.signals + tok * 4,
-                                    a.ent + tok * a.T * a.C * 2);
+  forward_token<F4, DCH, false, RB>(a, at.b, at.t, S, salida_row, a.signals + tok * 4, a.ent + tok * a.T * a.C * 2);
 }
 
 // Generation step: one workgroup of kDecodeWaves waves per batch row; the query is position tq = a.tq (or *a.tq_dev)
@@ -941,10 +1111,10 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   constexpr bool B16 = RB >= 1, FB16 = RB == 2;
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
-  const int64_t tok = sorted_token_of_wave(a);
-  if (tok >= a.B * a.L) return;
+  const TokAt at = sorted_token_of_wave(a);
+  if (at.tok < 0) return;
   const int lane = lane_id(), half = lane >> 5;
-  const int64_t b = tok / a.L, t = tok % a.L;
+  const int64_t tok = at.tok, b = at.b, t = at.t;
 
   int M, NU;
   if (a.lists) {             // the forward's list: no gather, dedupe or per-candidate clock and suffix loads
@@ -978,15 +1148,14 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   }
   // dp_u = <dO_q, V_u>, summed over the slabs of 256 DCH columns (ends with a wave sync)
   for (int c0 = 0; c0 < a.d; c0 += 256 * DCH) {
-    float4 dO[DCH], unused[DCH];
+    float4 dO[DCH];
 #pragma unroll
     for (int ch = 0; ch < DCH; ++ch) {
       const int dd = c0 + ch * 256 + lane * 4;
       dO[ch] = dd < a.d ? ld4r<B16>(rows_at<B16>(a.dsal, tok * a.d), (uint32_t)dd) : zero4();
-      unused[ch] = zero4();
     }
-    unique_row_dots<DCH, B16>(a, rows_at<B16>(a.V, (b * a.L + a.vshift) * a.ldv), a.ldv, 0, NU, dO, nullptr, unused,
-                              S, S.uc, c0, c0 > 0);
+    unique_row_dots<DCH, B16>(a, rows_at<B16>(a.V, (b * a.L + a.vshift) * a.ldv), a.ldv, NU, dO, S, S.uc, c0,
+                              c0 > 0);
   }
 
   // per entry: att * dp (S.ua is a per-entry buffer here)
@@ -998,7 +1167,6 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
     if (in) S.ua[m] = att[c] * dp[c];
   }
   wave_lds_sync();
-  for (int u = lane; u < NU; u += kWave) S.uc[u] = 0.f;   // dp is in registers: uc now sums ds per unique
   const int G = lanes_per_table(a.T), tg = lane / G;
   const bool lead = lane % G == 0 && tg < a.T;
   {                                                     // D per table
@@ -1007,9 +1175,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   }
   wave_lds_sync();
   float ds[kCh];
-  float dw[17];
-#pragma unroll
-  for (int x = 0; x < 17; ++x) dw[x] = 0.f;
+  int ell[kCh];
 #pragma unroll
   for (int c = 0; c < kCh; ++c) {
     const int m = c * kWave + lane;
@@ -1019,10 +1185,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
       erow[2 * slot[c] + 1] = ds[c];
       S.ua[m] = ds[c];
     }
-    const int ell = in ? S.uell[un[c]] : -1;
-#pragma unroll
-    for (int x = 0; x < 17; ++x)
-      if (ell == x) dw[x] += ds[c];
+    ell[c] = in ? S.uell[un[c]] : -1;
   }
   wave_lds_sync();
   float* part = a.partials + tok * (a.T + a.K + 1);
@@ -1035,12 +1198,12 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
       dbq_t = -rate_of(a, tg) * sds;
     }
   }
-  // per unique: sum over tables of ds, in table order
-  for (int tt = 0; tt < a.T; ++tt) {
+  {                                                     // per unique: ds summed over tables (S.uc)
+    float dv[1][kCh];
 #pragma unroll
-    for (int c = 0; c < kCh; ++c)
-      if (tau[c] == tt) S.uc[un[c]] += ds[c];
-    wave_lds_sync();
+    for (int c = 0; c < kCh; ++c) dv[0][c] = ds[c];
+    float* const out[1] = {S.uc};
+    unique_table_sums<1>(a.T, NU, tau, un, dv, S.ua, 2 * kMaxSlots, out);   // ua and ub are dead here
   }
 
   // d phi_q, d Qc_q = sum_u (sum_tau ds) [phi_u ; Kc_u]
@@ -1058,8 +1221,12 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
             make_float4(gq[c].x * a.sc, gq[c].y * a.sc, gq[c].z * a.sc, gq[c].w * a.sc);
     }
   }
-  for (int x = 0; x <= a.K && x < 17; ++x) {
-    const float v = wave_sum_u(dw[x]);
+  for (int x = 0; x <= a.K; ++x) {                      // d w_suf[x]: the entries whose suffix match is x
+    float v = 0.f;
+#pragma unroll
+    for (int c = 0; c < kCh; ++c)
+      if (c * kWave < M) v += ell[c] == x ? ds[c] : 0.f;
+    v = wave_sum_u(v);
     if (lane == 0) part[a.T + x] = v;
   }
   float dbq = 0.f;
@@ -1072,26 +1239,36 @@ template <int DCH, bool B16 = false>
 __device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows, int64_t self_pos, int NU,
                                                const float* w_u, const Scratch& S, float4 (&acc)[DCH], int c0 = 0) {
   const int lane = lane_id();
-  constexpr int UNR = DCH >= 4 ? 3 : (DCH >= 2 ? 6 : 8);   // fits the key pass's register budget (6 waves at DCH 1)
+  constexpr int UNR = DCH >= 4 ? 4 : (DCH >= 2 ? 8 : 8);   // fits the key pass's register budget (6 waves at DCH 1)
+  int col[DCH];
 #pragma unroll
-  for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
-  for (int u0 = 0; u0 < NU; u0 += UNR) {
-    float4 v[UNR][DCH];
-    float w[UNR];
+  for (int ch = 0; ch < DCH; ++ch) {
+    acc[ch] = zero4();
+    col[ch] = slab_col(a, c0, ch, lane);
+  }
+  for_chunks<UNR>(0, NU, UNR, [&](auto n, int u0) {
+    constexpr int R = decltype(n)::value;
+    int p[R];
+    float w[R];
 #pragma unroll
-    for (int r = 0; r < UNR; ++r) {
-      const bool ok = u0 + r < NU;
-      const int64_t p = ok ? S.upos[u0 + r] : self_pos;
-      w[r] = ok ? w_u[u0 + r] : 0.f;
+    for (int r = 0; r < R; ++r) {                      // wave-uniform rows and weights: scalar offsets
+      const int u = u0 + r < NU ? u0 + r : NU - 1;
+      p[r] = __builtin_amdgcn_readfirstlane(S.upos[u]);
+      w[r] = u0 + r < NU ? w_u[u] : 0.f;             // the same in every lane (an LDS broadcast)
+    }
+    float4 v[R][DCH];
 #pragma unroll
-      for (int ch = 0; ch < DCH; ++ch)
-        v[r][ch] = ld4r<B16>(rows, (uint32_t)p * (uint32_t)a.d + (uint32_t)slab_col(a, c0, ch, lane));
+    for (int r = 0; r < R; ++r) {
+      const float* row = rows_at<B16>(rows, (int64_t)(uint32_t)p[r] * a.d);
+#pragma unroll
+      for (int ch = 0; ch < DCH; ++ch) v[r][ch] = ld4r<B16>(row, (uint32_t)col[ch]);
     }
 #pragma unroll
-    for (int r = 0; r < UNR; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int ch = 0; ch < DCH; ++ch) fma4(acc[ch], w[r], v[r][ch]);
-  }
+  });
+  (void)self_pos;
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -1104,10 +1281,10 @@ void k_cand_bwd_k(Cand a) {
   constexpr bool B16 = RB >= 1, FB16 = RB == 2;
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
-  const int64_t tok = sorted_token_of_wave(a);
-  if (tok >= a.B * a.L) return;
+  const TokAt at = sorted_token_of_wave(a);
+  if (at.tok < 0) return;
   const int lane = lane_id(), half = lane >> 5;
-  const int64_t b = tok / a.L, k = tok % a.L;
+  const int64_t tok = at.tok, b = at.b, k = at.t;
   // the query pass's d phi and dBt of this token, loaded now so their latency hides behind the gathers
   float4 dphi_q[F4];
 #pragma unroll
@@ -1119,19 +1296,10 @@ void k_cand_bwd_k(Cand a) {
 
   const int M = gather(a, b, k, false, S);
   const int NU = dedupe(a, M, S);
-  for (int u = lane; u < NU; u += kWave) {   // per unique: uc sums att, ub (free in this pass) sums ds
-    S.uc[u] = 0.f;
-    S.ub[u] = 0.f;
-  }
-  // park the prefetched d phi in LDS (S.ua is free once the dedupe hash is done) to keep registers for the gathers
-#pragma unroll
-  for (int c = 0; c < F4; ++c) {
-    const int f0 = 4 * lane + 128 * c;
-    if (half == 0 && f0 < a.P) *reinterpret_cast<float4*>(S.ua + f0) = dphi_q[c];
-  }
   float att[kCh], ds[kCh];
   int tau[kCh], un[kCh];
   float dla = 0.f, dbk = 0.f;
+  const float rate_l = lane < a.T ? rate_of(a, lane) : 0.f;   // one division per table, shuffled to the entries
 #pragma unroll
   for (int c = 0; c < kCh; ++c) {
     const int m = c * kWave + lane;
@@ -1141,24 +1309,35 @@ void k_cand_bwd_k(Cand a) {
     un[c] = in ? S.uid[m] : 0;
     att[c] = 0.f;
     ds[c] = 0.f;
+    const float rate = __shfl(rate_l, e & 31, kWave);        // every lane takes part (no divergent shuffle)
     if (in) {   // the key sits at distance m - lo + 1 before query (e >> 5) in table tau
-      const int64_t o = ((b * a.L + (e >> 5)) * a.T + (e & 31)) * a.C + (m - S.off[e & 31]);
-      const float2 w2 = *reinterpret_cast<const float2*>(a.ent + 2 * o);
+      const uint32_t o = ((uint32_t)(b * a.L + (e >> 5)) * (uint32_t)a.T + (uint32_t)(e & 31)) * (uint32_t)a.C +
+                         (uint32_t)(m - S.off[e & 31]);
+      const float2 w2 = *reinterpret_cast<const float2*>(a.ent + 2 * (uint64_t)o);
       att[c] = w2.x;
       ds[c] = w2.y;
       dla += ds[c];
-      dbk += rate_of(a, e & 31) * ds[c];
+      dbk += rate * ds[c];
     }
   }
-  wave_lds_sync();
-  for (int tt = 0; tt < a.T; ++tt) {
+  // per unique, summed over tables: att (S.uc, the dV weights) and ds (the feature weights, in the key array, which
+  // is dead once the entries are in registers)
+  float* const dsum = reinterpret_cast<float*>(S.key);
+  {
+    float v[2][kCh];
 #pragma unroll
-    for (int c = 0; c < kCh; ++c)
-      if (tau[c] == tt) {
-        S.uc[un[c]] += att[c];
-        S.ub[un[c]] += ds[c];
-      }
-    wave_lds_sync();
+    for (int c = 0; c < kCh; ++c) {
+      v[0][c] = att[c];
+      v[1][c] = ds[c];
+    }
+    float* const out[2] = {S.uc, dsum};
+    unique_table_sums<2>(a.T, NU, tau, un, v, S.ua, 2 * kMaxSlots, out);   // ua and ub are dead here
+  }
+  // park the prefetched d phi in LDS (ua is free again) to keep registers for the gathers
+#pragma unroll
+  for (int c = 0; c < F4; ++c) {
+    const int f0 = 4 * lane + 128 * c;
+    if (half == 0 && f0 < a.P) *reinterpret_cast<float4*>(S.ua + f0) = dphi_q[c];
   }
 
   // with vshift, V[k] is the projection of k + 1: its gradient goes to row k + 1, and the last position (which no
@@ -1176,7 +1355,7 @@ void k_cand_bwd_k(Cand a) {
   }
   // d phi_k, d Kc_k = sum_u (sum_tau ds) [phi_q * scale_phi ; Qc_q * scale_c]
   float4 gk[F4];
-  unique_feature_sum<F4, FB16>(a, b, k, NU, true, S.ub, S, gk);
+  unique_feature_sum<F4, FB16>(a, b, k, NU, true, dsum, S, gk);
   if (half == 0) {   // P and cf are multiples of 4: a lane's 4 features lie in one of the two rows
 #pragma unroll
     for (int c = 0; c < F4; ++c) {
@@ -1222,14 +1401,17 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_lists(Cand a, i
   }
 }
 
-__device__ __forceinline__ int64_t sorted_token_of_wave(const Cand& a) {
+// The wave's token, as wave-uniform scalars (so that no per-lane division or 64-bit index math follows from it).
+__device__ __forceinline__ TokAt sorted_token_of_wave(const Cand& a) {
   const int64_t i = token_of_wave();
-  if (!ASRN_SORTED_MAP || i >= a.B * a.L) return i;
-  const int64_t b = i / a.L, r = i - b * a.L;
+  if (i >= a.B * a.L) return {0, 0, -1};
+  const int64_t b = row_of(a, i), r = i - b * a.L;
+  if (!ASRN_SORTED_MAP) return {b, r, i};
   const int tab = ASRN_SORTED_TABLE < 0 ? a.T - 1 : (ASRN_SORTED_TABLE < a.T ? ASRN_SORTED_TABLE : 0);
-  int p = a.order[(b * a.T + tab) * a.L + r];            // a permutation of the row's positions (the bucket sort's)
-  p = p < 0 ? 0 : (p >= a.L ? (int)a.L - 1 : p);        // clamped so that inconsistent inputs stay in bounds
-  return b * a.L + p;
+  // a permutation of the row's positions (the bucket sort's), clamped so that inconsistent inputs stay in bounds
+  int p = __builtin_amdgcn_readfirstlane(a.order[(uint32_t)((b * a.T + tab) * a.L + r)]);
+  p = p < 0 ? 0 : (p >= a.L ? (int)a.L - 1 : p);
+  return {b, p, b * a.L + p};
 }
 
 static int check_args(const Cand& a, const char* what) {
@@ -1249,6 +1431,9 @@ static int check_args(const Cand& a, const char* what) {
                  "(32-bit row offsets)", what, (long long)(a.B * a.L * widest));
   }
   ASRN_REQUIRE(a.K >= 0 && a.K <= 16, "%s: suffix K=%d must be in [0, 16]", what, a.K);
+  ASRN_REQUIRE(a.B * a.L * a.T < (int64_t(1) << 31) && a.B * a.L * a.T * a.C * 2 < (int64_t(1) << 31),
+               "%s: B*L*T*C*2 = %lld must stay below 2^31 (32-bit index and entry offsets)", what,
+               (long long)(a.B * a.L * a.T * a.C * 2));
   ASRN_REQUIRE(a.ldv >= a.d && a.ldv % 4 == 0 && ((uintptr_t)a.V & 15) == 0 && (a.vshift == 0 || a.vshift == 1),
                "%s: V rows need a stride ldv >= d, a multiple of 4, a 16-byte aligned V and v_shift 0 or 1", what);
   ASRN_REQUIRE(a.L * a.ldv < (int64_t(1) << 31), "%s: L*ldv must stay below 2^31 (32-bit row offsets)", what);
@@ -1267,6 +1452,7 @@ static Cand make(const float* phi, const float* V, const float* Qc, const float*
   a.gamma = gamma; a.order = order; a.win = win; a.rank = rank;
   a.ldv = d; a.vshift = 0; a.ldq = cf;
   a.B = B; a.L = L; a.d = d; a.P = P; a.cf = cf; a.K = K; a.T = T; a.Tc = Tc; a.C = C;
+  a.Linv = L > 1 ? ~(uint64_t)0 / (uint64_t)L + 1 : 0;
   a.sp = sp; a.sc = sc;
   return a;
 }
