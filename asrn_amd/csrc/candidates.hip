@@ -235,7 +235,8 @@ __device__ __forceinline__ void feat_row(const FeatLanes<F4>& fl, uint32_t row, 
 // Runs body(n, u0) over the chunks [u0, u0 + n) of [first, NU), one every `step`: n is NF, or the smallest of
 // N2 >= N3 that covers what is left, so a short tail does not load a full chunk of idle rows (n is a compile-time
 // constant: the row arrays stay in registers). By default N2 = NF / 2 and N3 = NF / 4; NF = 12 takes 8 and 4.
-template <int NF, int N2 = (NF % 3 == 0 ? 2 * NF / 3 : NF / 2), int N3 = (NF % 3 == 0 ? NF / 3 : NF / 4), class F>
+template <int NF, int N2 = (NF % 3 == 0 ? 2 * NF / 3 : (NF >= 2 ? NF / 2 : 1)),
+          int N3 = (NF % 3 == 0 ? NF / 3 : (NF >= 4 ? NF / 4 : 1)), class F>
 __device__ __forceinline__ void for_chunks(int first, int NU, int step, F&& body) {
   for (int u0 = first; u0 < NU; u0 += step) {
     const int rem = NU - u0;
@@ -608,7 +609,8 @@ __device__ __forceinline__ void unique_feature_sum(const Cand& a, int64_t b, int
 #pragma unroll
     for (int r = 0; r < R; ++r) {                      // the weights, read while the rows are in flight
       const int u = u0 + 2 * r + half;
-      const float w = u < NU ? wts[u] : 0.f;
+      float w = wts[u < NU ? u : NU - 1];
+      w = u < NU ? w : 0.f;
 #pragma unroll
       for (int c = 0; c < F4; ++c) fma4(g[c], w, f[r][c]);
     }
@@ -633,12 +635,34 @@ __device__ __forceinline__ int slab_col(const Cand& a, int c0, int ch, int lane)
 // <fixed, row_u> over the d columns for every unique (rows of batch row `rows`), R rows in flight, written to
 // out[u] (added to it when `add`: the slabs after the first); the key side (w_u != nullptr) also accumulates
 // dV += w_u row_u from the same loads. fixed holds columns c0 .. c0 + 256 DCH - 1 (zero past d).
+// The wave totals of 8 per-lane values at once, by a transposing butterfly: at distances 32, 16 and 8 each lane keeps
+// half of its values and adds its partner's copies of them, so value (lane >> 3) & 7 is left, summed over the lanes
+// that share lane & 7 ... bits 3-5; the 8 lanes of each aligned group then add it up (group8_sum). About 30 VALU and
+// 6 LDS-pipe exchanges for 8 totals, against 8 separate wave sums.
+__device__ __forceinline__ float wave_sums8(const float (&v)[8]) {
+  const int lane = lane_id();
+  const bool h32 = lane & 32, h16 = lane & 16, h8 = lane & 8;
+  float a[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = (h32 ? v[4 + i] : v[i]) + __shfl_xor(h32 ? v[i] : v[4 + i], 32, kWave);
+  float c[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) c[i] = (h16 ? a[2 + i] : a[i]) + __shfl_xor(h16 ? a[i] : a[2 + i], 16, kWave);
+  const float send = h8 ? c[0] : c[1];
+  const float x = (h8 ? c[1] : c[0]) +
+                  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x128, 0xF, 0xF, false));  // lane ^ 8
+  return group8_sum(x);
+}
+
+// out[u] = <fixed, row_u> over the d columns for every unique (rows of batch row `rows`), 8 rows in flight, the 8 dot
+// products reduced together (wave_sums8); added to out[u] when `add` (the slabs after the first). fixed holds columns
+// c0 .. c0 + 256 DCH - 1 (zero past d).
 template <int DCH, bool B16 = false>
 __device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows, int64_t ld, int NU,
                                                 const float4 (&fixed)[DCH], Scratch& S, float* out, int c0 = 0,
                                                 bool add = false) {
   const int lane = lane_id();
-  constexpr int NF = DCH >= 3 ? 4 : (DCH == 2 ? 4 : 8);
+  constexpr int NF = DCH >= 3 ? 2 : (DCH == 2 ? 4 : 8);
   int col[DCH];
 #pragma unroll
   for (int ch = 0; ch < DCH; ++ch) col[ch] = slab_col(a, c0, ch, lane);
@@ -655,13 +679,28 @@ __device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows
 #pragma unroll
       for (int ch = 0; ch < DCH; ++ch) o[r][ch] = ld4r<B16>(row, (uint32_t)col[ch]);
     }
+    if constexpr (NF == 8) {                           // the 8 dot products reduced together
+      float q[8];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float q = 0.f;
+      for (int r = 0; r < 8; ++r) {
+        q[r] = 0.f;
+        if (r < R) {
 #pragma unroll
-      for (int ch = 0; ch < DCH; ++ch) q += dot4(o[r][ch], fixed[ch]);
-      const float tot = wave_sum_u(q);
-      if (lane == 0 && u0 + r < NU) out[u0 + r] = add ? out[u0 + r] + tot : tot;
+          for (int ch = 0; ch < DCH; ++ch) q[r] += dot4(o[r][ch], fixed[ch]);
+        }
+      }
+      const float tot = wave_sums8(q);                 // row (lane >> 3) & 7 of the chunk
+      const int u = u0 + ((lane >> 3) & 7);
+      if ((lane & 7) == 0 && ((lane >> 3) & 7) < R && u < NU) out[u] = add ? out[u] + tot : tot;
+    } else {                                           // wide rows, few in flight: one wave sum each
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float q = 0.f;
+#pragma unroll
+        for (int ch = 0; ch < DCH; ++ch) q += dot4(o[r][ch], fixed[ch]);
+        const float tot = wave_sum_u(q);
+        if (lane == 0 && u0 + r < NU) out[u0 + r] = add ? out[u0 + r] + tot : tot;
+      }
     }
   });
   wave_lds_sync();
@@ -744,7 +783,9 @@ __device__ __forceinline__ void load_entries(const Cand& a, int M, const Scratch
 //   upos    per unique u < NU: the candidate's position (int32)
 //   ub      per unique: fp32(Bt_k - Bt_q)
 //   uell    per unique: the suffix-match length (u8)
-// Every region is sized for T * C (the most entries and uniques a query can have); 16-byte aligned.
+// Every region is sized for T * C (the most entries and uniques a query can have); 16-byte aligned. (The entries' att
+// stays in the entries array only: the query pass reads it there, next to the ds it writes, which keeps those lines
+// in L2 for the key pass; a copy in the record made the key pass 6 us slower at cfg2.)
 struct RecLayout { int64_t e16, upos, ub, uell, size; };
 __host__ __device__ inline RecLayout rec_layout(int T, int C) {
   const int64_t tc = (int64_t)T * C;
@@ -1107,7 +1148,7 @@ __global__ __launch_bounds__(kWave * kDecodeWaves) void k_decode_attend(Cand a) 
 // difference and the suffix length; per table D = sum att dp, then ds = att (dp - D) per entry, kept for the key pass.
 // ---------------------------------------------------------------------------------------------------------------------
 template <int F4, int DCH, int RB>
-__global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
+__global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 7 : 1) void k_cand_bwd_q(Cand a) {
   constexpr bool B16 = RB >= 1, FB16 = RB == 2;
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
@@ -1175,7 +1216,6 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
   }
   wave_lds_sync();
   float ds[kCh];
-  int ell[kCh];
 #pragma unroll
   for (int c = 0; c < kCh; ++c) {
     const int m = c * kWave + lane;
@@ -1185,7 +1225,6 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
       erow[2 * slot[c] + 1] = ds[c];
       S.ua[m] = ds[c];
     }
-    ell[c] = in ? S.uell[un[c]] : -1;
   }
   wave_lds_sync();
   float* part = a.partials + tok * (a.T + a.K + 1);
@@ -1221,13 +1260,14 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_bwd_q(Cand a) {
             make_float4(gq[c].x * a.sc, gq[c].y * a.sc, gq[c].z * a.sc, gq[c].w * a.sc);
     }
   }
-  for (int x = 0; x <= a.K; ++x) {                      // d w_suf[x]: the entries whose suffix match is x
+  {   // d w_suf[x] = the ds of the entries whose suffix match is x = sum over the uniques u with ell_u = x of their
+      // summed ds (S.uc): lane group x strides over the uniques, then adds up in a fixed butterfly
+    const int Gx = lanes_per_table(a.K + 1), x = lane / Gx;
     float v = 0.f;
-#pragma unroll
-    for (int c = 0; c < kCh; ++c)
-      if (c * kWave < M) v += ell[c] == x ? ds[c] : 0.f;
-    v = wave_sum_u(v);
-    if (lane == 0) part[a.T + x] = v;
+    if (x <= a.K)
+      for (int u = lane % Gx; u < NU; u += Gx) v += S.uell[u] == x ? S.uc[u] : 0.f;
+    for (int m = Gx >> 1; m > 0; m >>= 1) v += __shfl_xor(v, m, kWave);
+    if (lane % Gx == 0 && x <= a.K) part[a.T + x] = v;
   }
   float dbq = 0.f;
   for (int tt = 0; tt < a.T; ++tt) dbq += readlane_f(dbq_t, tt * G);
