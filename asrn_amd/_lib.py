@@ -41,6 +41,10 @@ SIGNATURES = {
     'asrn_hawkes_bwd': (ctypes.c_int, [_P] * 8 + [_I64, _I64, _I32] + [_P] * 4 + [_I64, _P]),
     'asrn_streak_fwd': (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I32, _P, _P, _I64, _P]),
     'asrn_streak_bwd': (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P, _I64, _P]),
+    'asrn_repetition_workspace': (_I64, [_I64, _I64, _I32]),
+    'asrn_repetition_fwd': (ctypes.c_int, [_P] * 8 + [_I64, _I64, _I32] + [_P] * 4 + [_I64, _P]),
+    'asrn_repetition_bwd_workspace': (_I64, [_I64, _I64, _I32]),
+    'asrn_repetition_bwd': (ctypes.c_int, [_P] * 13 + [_I64, _I64, _I32] + [_P] * 6 + [_I64, _P]),
     'asrn_context_fwd': (ctypes.c_int, [_P] * 5 + [_I64, _I32] + [_F32] * 3 + [_P] * 5),
     'asrn_context_bwd_workspace': (_I64, [_I64, _I32]),
     'asrn_context_bwd': (ctypes.c_int, [_P] * 5 + [_I64, _I32] + [_F32] * 2 + [_P] * 2 + [_I64, _I32] + [_P] * 7

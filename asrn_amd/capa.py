@@ -285,8 +285,7 @@ class CapaASRNEstable(nn.Module):
             with torch.no_grad():
                 ngram = ops.ngram_sort(sig, self.c_vistos, self.vistos)
         claves, order, rep, rank_k, vistos = ngram
-        hawkes = ops.Hawkes.apply(Bt, log_alfa, kappa, order, rep, rank_k)
-        racha = ops.Streak.apply(beta, kappa_r, vistos)
+        hawkes, racha = ops.Repeticion.apply(Bt, log_alfa, kappa, beta, kappa_r, order, rep, rank_k, vistos)
         if partes is not None:
             partes.update(claves=claves, orden_k=order, repetido=rep)
         return {'vistos': vistos, 'hawkes': hawkes, 'racha': racha}

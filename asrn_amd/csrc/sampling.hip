@@ -2,7 +2,10 @@
 //
 // n-gram sets: per text row, an open-addressing table of 64-bit keys; a key packs the n token ids of an n-gram, w bits
 // apiece, the oldest token in the lowest bits. w is asrn_sample_bits(V), the smallest width whose all-ones field is
-// above every token id, so no key is the all-ones word that marks an empty slot. Inserting is then one 64-bit
+// above every token id, so no key is the all-ones word that marks an empty slot. When n w > 64 (4-grams of a
+// vocabulary of 65,536 or more, 5-grams of 50,304) the key is instead a 64-bit hash of the n ids (SplitMix64 steps,
+// all ones mapped to all ones minus one): two distinct n-grams then share a key with probability 2^-64 per pair, about
+// 2^-33 for a row of 65,536 n-grams. Inserting is then one 64-bit
 // compare-and-swap that claims and publishes the key at once: concurrent inserts of one n-gram meet in one slot, and
 // no thread ever waits on another. Beside it, a table of contexts (the n-gram minus its last token) holds each
 // context's distinct successors, up to kSucc of them inline with a count: a successor is appended only by the insert
@@ -85,17 +88,35 @@ __device__ __forceinline__ bool set_has(const TupleSet& s, int64_t row, uint64_t
   return slot_of(s.slots + row * s.cap, s.cap, key) >= 0;
 }
 
-// tokens x[0..n-1] packed w bits apiece, x[0] lowest
-__device__ __forceinline__ uint64_t pack(const int64_t* x, int n, int w) {
-  uint64_t k = 0;
-  for (int j = 0; j < n; ++j) k |= (uint64_t)x[j] << (w * j);
+// Keys of n-grams of a set with n tokens of w bits: a running state over the tokens, oldest first. Packed (n w <= 64):
+// the state is the key so far, token j at bit w j. Hashed: the state is a 64-bit hash chain. key_of finishes a state
+// (the context of an n-gram is its first n - 1 tokens, finished the same way for the context table).
+struct KeyForm {
+  int w;
+  bool hashed;
+  __device__ __forceinline__ uint64_t start() const { return hashed ? 0x243f6a8885a308d3ull : 0ull; }
+  __device__ __forceinline__ uint64_t step(uint64_t st, int j, int64_t x) const {
+    return hashed ? mix64(st ^ ((uint64_t)x + 0x9e3779b97f4a7c15ull)) : st | ((uint64_t)x << (w * j));
+  }
+  __device__ __forceinline__ uint64_t key_of(uint64_t st) const {
+    return hashed && st == kEmptySlot ? kEmptySlot - 1 : st;
+  }
+};
+__device__ __forceinline__ KeyForm key_form(int n, int w) { return {w, (int64_t)n * w > 64}; }
+
+// the state after tokens x[0..n-1]
+__device__ __forceinline__ uint64_t pack(const KeyForm& f, const int64_t* x, int n) {
+  uint64_t k = f.start();
+  for (int j = 0; j < n; ++j) k = f.step(k, j, x[j]);
   return k;
 }
 
 // the n-gram x[0..n-1] into row `row`'s set and, when new, its last token into its context's successors
 __device__ __forceinline__ void ngram_add(const TupleSet& s, int64_t row, const int64_t* x, int w) {
-  const uint64_t ctx = pack(x, s.n - 1, w);
-  const uint64_t key = ctx | ((uint64_t)x[s.n - 1] << (w * (s.n - 1)));
+  const KeyForm f = key_form(s.n, w);
+  const uint64_t st = pack(f, x, s.n - 1);
+  const uint64_t ctx = f.key_of(st);
+  const uint64_t key = f.key_of(f.step(st, s.n - 1, x[s.n - 1]));
   bool nuevo;
   if (slot_add(s.slots + row * s.cap, s.cap, key, &nuevo) < 0 || !nuevo) return;
   const int64_t c = slot_add(s.ctx + row * s.cap, s.cap, ctx, &nuevo);
@@ -212,7 +233,8 @@ struct SampleArgs {
 // than kSucc of them (then the caller probes every token); list[0 .. *n_list) otherwise. One thread calls it.
 __device__ __forceinline__ void successors(const TupleSet& s, int64_t b, const int64_t* text, int64_t pos, int w,
                                            int* list, int* n_list) {
-  const uint64_t ctx = pack(text + pos - (s.n - 1), s.n - 1, w);
+  const KeyForm f = key_form(s.n, w);
+  const uint64_t ctx = f.key_of(pack(f, text + pos - (s.n - 1), s.n - 1));
   const int64_t c = slot_of(s.ctx + b * s.cap, s.cap, ctx);
   if (c < 0) {
     *n_list = 0;
@@ -331,10 +353,10 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     if (nb_list >= 0) {
       if (tid < nb_list) work[blist[tid]] = ninf;
     } else {
-      const uint64_t base = pack(text + pos - (nb - 1), nb - 1, a.w);
-      const int sh = a.w * (nb - 1);
+      const KeyForm f = key_form(nb, a.w);
+      const uint64_t base = pack(f, text + pos - (nb - 1), nb - 1);
       for (int64_t v = tid; v < V; v += kSampleThreads)
-        if (set_has(a.ban, b, base | ((uint64_t)v << sh))) work[v] = ninf;
+        if (set_has(a.ban, b, f.key_of(f.step(base, nb - 1, v)))) work[v] = ninf;
     }
   }
   __syncthreads();
@@ -352,13 +374,13 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   uint32_t* qbits = a.quote_bits + b * ((V + 31) / 32);
   const bool qprobe = quote && nq_list < 0;
   if (qprobe) {
-    const uint64_t base = pack(text + pos - (nq - 1), nq - 1, a.w);
-    const int sh = a.w * (nq - 1);
+    const KeyForm f = key_form(nq, a.w);
+    const uint64_t base = pack(f, text + pos - (nq - 1), nq - 1);
     for (int64_t wd = tid; wd < (V + 31) / 32; wd += kSampleThreads) {
       uint32_t bits = 0;
       for (int i = 0; i < 32; ++i) {
         const int64_t v = wd * 32 + i;
-        if (v < V && set_has(a.quote, b, base | ((uint64_t)v << sh))) bits |= 1u << i;
+        if (v < V && set_has(a.quote, b, f.key_of(f.step(base, nq - 1, v)))) bits |= 1u << i;
       }
       qbits[wd] = bits;
     }
@@ -831,12 +853,12 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_reg(SampleArgs a) {
         }
       }
     } else {
-      const uint64_t base = pack(text + pos - (nb - 1), nb - 1, a.w);
-      const int sh = a.w * (nb - 1);
+      const KeyForm f = key_form(nb, a.w);
+      const uint64_t base = pack(f, text + pos - (nb - 1), nb - 1);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int64_t v = tok_of(r);
-        if (v < V && set_has(a.ban, b, base | ((uint64_t)v << sh))) x[r] = ninf;
+        if (v < V && set_has(a.ban, b, f.key_of(f.step(base, nb - 1, v)))) x[r] = ninf;
       }
     }
   }
@@ -859,12 +881,12 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_reg(SampleArgs a) {
         if (owned(qlist[k], &rr)) qmask |= 1ull << rr;
       }
     } else {
-      const uint64_t base = pack(text + pos - (nq - 1), nq - 1, a.w);
-      const int sh = a.w * (nq - 1);
+      const KeyForm f = key_form(nq, a.w);
+      const uint64_t base = pack(f, text + pos - (nq - 1), nq - 1);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int64_t v = tok_of(r);
-        if (v < V && set_has(a.quote, b, base | ((uint64_t)v << sh))) qmask |= 1ull << r;
+        if (v < V && set_has(a.quote, b, f.key_of(f.step(base, nq - 1, v)))) qmask |= 1ull << r;
       }
     }
   }
@@ -1067,8 +1089,7 @@ int check_set(const char* what, const TupleSet& s, int32_t w) {
   ASRN_REQUIRE(s.ctx && s.count && s.succ, "%s: a set needs its context, count and successor tables", what);
   ASRN_REQUIRE(s.cap >= 2 && (s.cap & (s.cap - 1)) == 0, "%s: the set's capacity %lld must be a power of two", what,
                (long long)s.cap);
-  ASRN_REQUIRE(s.n >= 1 && (int64_t)s.n * w <= 64, "%s: n=%d tokens of %d bits do not fit a 64-bit key", what, s.n,
-               w);
+  ASRN_REQUIRE(s.n >= 1 && w >= 1 && w <= 62, "%s: n=%d must be >= 1 and w=%d in [1, 62]", what, s.n, w);
   return 0;
 }
 

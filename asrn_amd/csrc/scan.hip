@@ -17,6 +17,7 @@
 // functor feeds (d kappa) is summed per chunk, and a third launch adds the chunk sums in a fixed order (deterministic;
 // no fences or atomics between workgroups, whose agent-scope release would write back and invalidate the L2).
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 
@@ -376,6 +377,30 @@ struct ClockOp {
   __device__ void reduce(int, float) const {}
 };
 
+// ---- two scans of one monoid and row length in the same launches ------------------------------------------------------
+// Rows [0, ra) are A's, the rest B's (a workgroup's rows are of one kind, so the branch is uniform): the repetition
+// branch's Hawkes rows (B n) and streak rows (B) share their totals, chunk and row-sum launches.
+template <class A, class B>
+struct Both {
+  static_assert(std::is_same<typename A::M, typename B::M>::value, "the two scans must compose the same monoid");
+  static constexpr bool kReduce = A::kReduce || B::kReduce;
+  static constexpr bool kOneLaunch = false;
+  using M = typename A::M;
+  struct Aux { typename A::Aux a; typename B::Aux b; };
+  A a; B b; int ra;
+  __device__ M load(int row, int64_t e, Aux& x) const {
+    return row < ra ? a.load(row, e, x.a) : b.load(row - ra, e, x.b);
+  }
+  __device__ void store(int row, int64_t e, typename M::V v, float& acc, const Aux& x) const {
+    if (row < ra) a.store(row, e, v, acc, x.a);
+    else b.store(row - ra, e, v, acc, x.b);
+  }
+  __device__ void reduce(int row, float s) const {
+    if (row < ra) a.reduce(row, s);
+    else b.reduce(row - ra, s);
+  }
+};
+
 // ---- launch ---------------------------------------------------------------------------------------------------------
 constexpr int64_t kOneChunk = (int64_t)kScanThreads * 4;   // rows up to this length take one chunk and no workspace
 constexpr int kRowThreads = 1024;
@@ -574,4 +599,60 @@ extern "C" int asrn_streak_bwd(const float* vistos, const double* beta, const fl
   op.vistos = vistos; op.beta = beta; op.kappa_r = kappa_r; op.L = L; op.n = n;
   op.racha = racha; op.dr = dracha; op.dbeta = dbeta; op.dkr = dkappa_r;
   return launch_scan(op, B, L, workspace, workspace_bytes, stream, "asrn_streak_bwd");
+}
+
+// The repetition branch's two scans in shared launches: Hawkes over B n rows and the streak over B rows, both of
+// length L (asrn_hawkes_fwd and asrn_streak_fwd in one pass; the same results).
+extern "C" int64_t asrn_repetition_workspace(int64_t B, int64_t L, int32_t n) {
+  if (B < 0 || L < 0 || n < 1) return -1;
+  return asrn_scan_workspace(B * (n + 1), L);
+}
+
+extern "C" int asrn_repetition_fwd(const int32_t* order, const uint8_t* repeated, const double* Bt,
+                                   const float* log_alfa, const float* kappa, const float* vistos, const double* beta,
+                                   const float* kappa_r, int64_t B, int64_t L, int32_t n, float* hawkes,
+                                   float* S_sorted, float* racha, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  ASRN_REQUIRE(B >= 0 && L >= 0 && n >= 1, "asrn_repetition_fwd: bad sizes");
+  Both<HawkesFwd, StreakFwd> op;
+  op.a.order = order; op.a.rep = repeated; op.a.Bt = Bt; op.a.la = log_alfa; op.a.kappa = kappa; op.a.L = L;
+  op.a.n = n; op.a.hawkes = hawkes; op.a.S_sorted = S_sorted;
+  op.b.vistos = vistos; op.b.beta = beta; op.b.kappa_r = kappa_r; op.b.L = L; op.b.n = n; op.b.racha = racha;
+  op.ra = (int)(B * n);
+  return launch_scan(op, B * (n + 1), L, workspace, workspace_bytes, stream, "asrn_repetition_fwd");
+}
+
+extern "C" int64_t asrn_repetition_bwd_workspace(int64_t B, int64_t L, int32_t n) {
+  const int64_t scan = asrn_repetition_workspace(B, L, n);
+  if (scan < 0) return -1;
+  return round_up(2 * B * L * n * (int64_t)sizeof(float)) + scan;
+}
+
+extern "C" int asrn_repetition_bwd(const int32_t* order, const uint8_t* repeated, const int32_t* rank_k,
+                                   const double* Bt, const float* log_alfa, const float* kappa, const float* S_sorted,
+                                   const float* dhawkes, const float* vistos, const double* beta,
+                                   const float* kappa_r, const float* racha, const float* dracha, int64_t B,
+                                   int64_t L, int32_t n, double* dBt, float* dlog_alfa, float* dkappa,
+                                   double* dbeta, float* dkappa_r, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  ASRN_REQUIRE(B >= 0 && L >= 0 && n >= 1, "asrn_repetition_bwd: bad sizes");
+  if (B == 0 || L == 0) return 0;
+  const int64_t need = asrn_repetition_bwd_workspace(B, L, n);
+  ASRN_REQUIRE(need >= 0, "asrn_repetition_bwd: rows x chunks must stay below 2^31");
+  ASRN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "asrn_repetition_bwd: workspace too small");
+  float* gdB = (float*)workspace;
+  float* wa = gdB + B * L * n;
+  char* scan_ws = (char*)workspace + round_up(2 * B * L * n * (int64_t)sizeof(float));
+  Both<HawkesBwd, StreakBwd> op;
+  op.a.order = order; op.a.rep = repeated; op.a.Bt = Bt; op.a.la = log_alfa; op.a.kappa = kappa; op.a.L = L;
+  op.a.n = n; op.a.S_sorted = S_sorted; op.a.dh = dhawkes; op.a.gdB = gdB; op.a.wa = wa; op.a.dkappa = dkappa;
+  op.b.vistos = vistos; op.b.beta = beta; op.b.kappa_r = kappa_r; op.b.L = L; op.b.n = n;
+  op.b.racha = racha; op.b.dr = dracha; op.b.dbeta = dbeta; op.b.dkr = dkappa_r;
+  op.ra = (int)(B * n);
+  if (launch_scan(op, B * (n + 1), L, scan_ws, need - (scan_ws - (char*)workspace), stream, "asrn_repetition_bwd"))
+    return 1;
+  const int threads = 256;
+  hipLaunchKernelGGL(k_hawkes_bwd_finish, dim3((unsigned)((B * L + threads - 1) / threads)), dim3(threads), 0,
+                     (hipStream_t)stream, rank_k, gdB, wa, log_alfa, B, L, (int)n, dBt, dlog_alfa);
+  return check_launch("asrn_repetition_bwd/finish");
 }

@@ -542,6 +542,52 @@ class Streak(torch.autograd.Function):
         return dbeta, dkr.sum().reshape(1), None
 
 
+class Repeticion(torch.autograd.Function):
+    """Hawkes and Streak in one pass (asrn_repetition_fwd/bwd: the B n Hawkes rows and the B streak rows share the
+    scans' launches): (hawkes (B, L, n), racha (B, L)), the same values and gradients as the two functions."""
+
+    @staticmethod
+    def forward(ctx, Bt, log_alfa, kappa, beta, kappa_r, order, rep, rank_k, vistos):
+        dev = _dev(Bt)
+        B, n, L = order.shape
+        Bt = _c(Bt, torch.float64)
+        la = _c(log_alfa, torch.float32)
+        kap = _c(kappa, torch.float32)
+        beta = _c(beta, torch.float64)
+        kr = _c(kappa_r, torch.float32)
+        vistos = _c(vistos, torch.float32)
+        hawkes = torch.empty((B, L, n), dtype=torch.float32, device=dev)
+        S = torch.empty((B, n, L), dtype=torch.float32, device=dev)
+        racha = torch.empty((B, L), dtype=torch.float32, device=dev)
+        wsb = query('asrn_repetition_workspace', B, L, n)
+        if wsb < 0:
+            raise RuntimeError(f'repetition scans of {B * (n + 1)} rows x {L}: too many chunks')
+        ws = torch.empty((wsb,), dtype=torch.uint8, device=dev) if wsb else None
+        call('asrn_repetition_fwd', ptr(order), ptr(rep), ptr(Bt), ptr(la), ptr(kap), ptr(vistos), ptr(beta), ptr(kr),
+             B, L, n, ptr(hawkes), ptr(S), ptr(racha), ptr(ws), wsb, stream_of(dev))
+        ctx.save_for_backward(Bt, la, kap, order, rep, rank_k, S, vistos, beta, kr, racha)
+        return hawkes, racha
+
+    @staticmethod
+    def backward(ctx, gh, gr):
+        Bt, la, kap, order, rep, rank_k, S, vistos, beta, kr, racha = ctx.saved_tensors
+        B, n, L = order.shape
+        dev = Bt.device
+        gh = torch.zeros((B, L, n), dtype=torch.float32, device=dev) if gh is None else _c(gh, torch.float32)
+        gr = torch.zeros((B, L), dtype=torch.float32, device=dev) if gr is None else _c(gr, torch.float32)
+        dBt = torch.empty((B, L), dtype=torch.float64, device=dev)
+        dla = torch.empty((B, L), dtype=torch.float32, device=dev)
+        dk = torch.empty((B, n), dtype=torch.float32, device=dev)
+        dbeta = torch.empty((B, L), dtype=torch.float64, device=dev)
+        dkr = torch.empty((B,), dtype=torch.float32, device=dev)
+        wsb = query('asrn_repetition_bwd_workspace', B, L, n)
+        ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+        call('asrn_repetition_bwd', ptr(order), ptr(rep), ptr(rank_k), ptr(Bt), ptr(la), ptr(kap), ptr(S), ptr(gh),
+             ptr(vistos), ptr(beta), ptr(kr), ptr(racha), ptr(gr), B, L, n, ptr(dBt), ptr(dla), ptr(dk), ptr(dbeta),
+             ptr(dkr), ptr(ws), wsb, stream_of(dev))
+        return dBt, dla, dk.sum(0), dbeta, dkr.sum().reshape(1), None, None, None, None
+
+
 # ---------------------------------------------------------------------------------------------------------------------
 # a13
 # ---------------------------------------------------------------------------------------------------------------------
@@ -877,16 +923,16 @@ def bits_por_pieza(V):
 
 
 class ConjuntoNgramas:
-    """Per text row, a device hash set of the n-grams seen (n token ids packed into one 64-bit key) and a table of
-    their contexts' distinct successors (the first asrn_ngram_set_successors() inline): the device side of the
-    reference's _Ngramas (asrn/nucleo.py:1857-1889). Sized for `capacidad` n-grams per row (at most half the slots in
-    use); n * bits_por_pieza(V) must be <= 64."""
+    """Per text row, a device hash set of the n-grams seen and a table of their contexts' distinct successors (the
+    first asrn_ngram_set_successors() inline): the device side of the reference's _Ngramas
+    (asrn/nucleo.py:1857-1889). A key packs the n token ids into 64 bits when n * bits_por_pieza(V) <= 64, and is a
+    64-bit hash of them otherwise (two distinct n-grams share a key with probability 2^-64 per pair). Sized for
+    `capacidad` n-grams per row (at most half the slots in use)."""
 
     def __init__(self, filas, n, V, capacidad, dev):
         w = bits_por_pieza(V)
-        if n < 1 or n * w > 64:
-            raise ValueError(f'n-gram sets pack n={n} token ids of {w} bits (V={V}) into 64 bits: n * {w} must be '
-                             '<= 64')
+        if n < 1:
+            raise ValueError(f'n-gram sets need n >= 1 (got {n})')
         self.n, self.w, self.V = n, w, V
         self.cap = _pow2_at_least(max(2 * int(capacidad), 2))
         self.slots = torch.full((filas, self.cap), -1, dtype=torch.int64, device=dev)     # all ones: empty

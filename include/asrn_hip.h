@@ -275,6 +275,25 @@ int asrn_streak_bwd(const float* vistos, const double* beta, const float* kappa_
                     const float* dracha, int64_t B, int64_t L, int32_t n, double* dbeta, float* dkappa_r,
                     void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- a11: the repetition branch's two scans in shared launches (asrn/estable.py:304-321) -----------------------
+ * asrn_hawkes_fwd and asrn_streak_fwd in one pass, the same outputs: the B n Hawkes rows and the B streak rows share
+ * the scan's launches (the totals, the chunks and, backward, the per-row sums); asrn_repetition_bwd likewise stands
+ * for asrn_hawkes_bwd and asrn_streak_bwd. Workspaces: asrn_repetition_workspace(B, L, n) bytes forward,
+ * asrn_repetition_bwd_workspace(B, L, n) backward. No reference counterpart as one call: the reference runs the two
+ * scans one after the other in _repeticion. */
+int64_t asrn_repetition_workspace(int64_t B, int64_t L, int32_t n);
+int asrn_repetition_fwd(const int32_t* order, const uint8_t* repeated, const double* Bt, const float* log_alfa,
+                        const float* kappa, const float* vistos, const double* beta, const float* kappa_r, int64_t B,
+                        int64_t L, int32_t n, float* hawkes, float* S_sorted, float* racha, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+int64_t asrn_repetition_bwd_workspace(int64_t B, int64_t L, int32_t n);
+int asrn_repetition_bwd(const int32_t* order, const uint8_t* repeated, const int32_t* rank_k, const double* Bt,
+                        const float* log_alfa, const float* kappa, const float* S_sorted, const float* dhawkes,
+                        const float* vistos, const double* beta, const float* kappa_r, const float* racha,
+                        const float* dracha, int64_t B, int64_t L, int32_t n, double* dBt, float* dlog_alfa,
+                        float* dkappa, double* dbeta, float* dkappa_r, void* workspace, int64_t workspace_bytes,
+                        void* stream);
+
 /* ---- a13: the gate consumer (asrn/estable.py:376-403, asrn/nucleo.py:865-878) -------------------------------
  * Replaces the PyTorch ops of _combinar after W_o: with A = W_o salida (B*L, d) (fp32, or bf16 when aporte_bf16),
  * r = 1 / max(1, peso_total) and

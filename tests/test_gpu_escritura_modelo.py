@@ -148,6 +148,44 @@ def test_sampler_matches_oracle(c):
             assert q[tok] > 0 and int(texto_cpu[b, p_now]) == tok
 
 
+@pytest.mark.parametrize('V,nq,nb', [(70000, 4, 2), (50304, 4, 5), (200000, 5, 4)])
+def test_sampler_hashed_ngram_keys(V, nq, nb):
+    """n-gram sets whose n token ids do not fit 64 bits (n * bits_por_pieza(V) > 64) key them by a 64-bit hash: the
+    quote mask and the bans still match the oracle's exact tuple sets, on texts built so that both act (the current
+    context repeats a quoted span and closes a banned n-gram of the generated part)."""
+    say('sampler hashed keys', V, nq, nb)
+    w = ops.bits_por_pieza(V)
+    assert nq * w > 64 or nb * w > 64
+    B, L0, gen = 2, 40, 30
+    pos = L0 + gen
+    g = torch.Generator().manual_seed(V + nq)
+    x = torch.randint(0, V, (B, pos + 2), generator=g)
+    for b in range(B):
+        x[b, pos - 8:pos] = x[b, 5:13].clone()                  # the context repeats text 5..12: a quote continues it
+        x[b, L0 + 2:L0 + 1 + nb] = x[b, pos - nb + 1:pos].clone()  # the context opens a generated n-gram: a ban
+    texto = x.to(DEV).contiguous()
+    est = _Estado(B, V, pos + 2)
+    cita = ops.ConjuntoNgramas(B, nq, V, pos + 2, DEV)
+    cita.agregar_texto(texto[:, :pos].contiguous())
+    prohibidas = ops.ConjuntoNgramas(B, nb, V, pos + 2, DEV)
+    prohibidas.agregar_texto(texto[:, L0:pos].contiguous())
+    lg = (torch.randn(B, V, generator=g) * 3).to(DEV)
+    pdev = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    ops.muestrear(lg, texto, pdev, pos + 1, L0, est.piezas, est.terminado, est.paso_fin, est.trabajo, est.bits, 0.9, 0,
+                  1.0, 1.0, 64, 77, cita=cita, prohibidas=prohibidas, prob=est.prob)
+    torch.cuda.synchronize()
+    prob = est.prob.cpu().double()
+    texto_cpu = texto.cpu()
+    for b in range(B):
+        t_b = texto_cpu[b, :pos].tolist()
+        lgr = M.frenar(lg[b].cpu().double(), t_b, L0, 1.0, 64, nb)
+        sig = M.ngramas_siguientes(t_b, nq)
+        assert len(sig) >= 1 and bool(torch.isinf(lgr).any()), 'the text must make both the quote and a ban act'
+        q = M.probabilidades(lgr, 0.9, 0, 1.0, sig)
+        assert set(torch.nonzero(prob[b] > 0).view(-1).tolist()) == set(torch.nonzero(q > 0).view(-1).tolist()), b
+        assert torch.allclose(prob[b], q, rtol=1e-4, atol=2e-6), (b, (prob[b] - q).abs().max())
+
+
 def test_sampler_distribution_and_seed():
     say('sampler chi-square')
     B, V = 512, 12

@@ -234,7 +234,15 @@ def test_clock_scan_fp32_core_layer(B, L):
     assert_close(bd.grad, g.flip(1).cumsum(1).flip(1), 'dbeta', 1e-12)
 
 
-def run_repetition_stage(g, p, sh, kappa_min=None):
+def repetition(Bt, la, kappa, beta, kappa_r, order, rep, rank_k, vistos, joint):
+    """hawkes and racha through the two autograd functions, or (joint) through ops.Repeticion, whose two scans share
+    their launches."""
+    if joint:
+        return ops.Repeticion.apply(Bt, la, kappa, beta, kappa_r, order, rep, rank_k, vistos)
+    return ops.Hawkes.apply(Bt, la, kappa, order, rep, rank_k), ops.Streak.apply(beta, kappa_r, vistos)
+
+
+def run_repetition_stage(g, p, sh, kappa_min=None, joint=False):
     """HIP hawkes/streak on the fixture's stage inputs, with gradients (the rates floored at kappa_min when the
     fixture's protections have one, as the layer's _kappas does)."""
     beta = g['beta'].to(DEV).requires_grad_()
@@ -246,18 +254,18 @@ def run_repetition_stage(g, p, sh, kappa_min=None):
     kappa, kappa_r = lk.exp(), lkr.exp()
     if kappa_min is not None:
         kappa, kappa_r = kappa.clamp(min=kappa_min), kappa_r.clamp(min=kappa_min)
-    hawkes = ops.Hawkes.apply(Bt, la, kappa, order, rep, rank_k)
-    racha = ops.Streak.apply(beta, kappa_r, vistos)
+    hawkes, racha = repetition(Bt, la, kappa, beta, kappa_r, order, rep, rank_k, vistos, joint)
     ((hawkes * g['rep.gh'].to(DEV)).sum() + (racha * g['rep.gr'].to(DEV)).sum()).backward()
     return vistos, hawkes, racha, beta.grad, Bt.grad, la.grad, lk.grad, lkr.grad
 
 
+@pytest.mark.parametrize('joint', [False, True], ids=['apart', 'joint'])
 @pytest.mark.parametrize('name', CASES)
-def test_repetition_golden(name):
-    say('repetition golden', name)
+def test_repetition_golden(name, joint):
+    say('repetition golden', name, joint)
     g, p, m = fixtures.load(name)
     sh = fixtures.shape_of(p, m)
-    vistos, hawkes, racha, gb, gB, gla, glk, glkr = run_repetition_stage(g, p, sh, fixtures.prot(m).kappa_min)
+    vistos, hawkes, racha, gb, gB, gla, glk, glkr = run_repetition_stage(g, p, sh, fixtures.prot(m).kappa_min, joint)
     assert torch.equal(vistos.cpu(), g['rep.vistos'])
     assert_close(hawkes, g['rep.hawkes'], 'hawkes')
     if m['extra'].get('kappa_r_zero'):
@@ -271,11 +279,12 @@ def test_repetition_golden(name):
     assert_close(glkr, g['rep.g_log_kappa_racha'], 'grad log_kappa_racha')
 
 
+@pytest.mark.parametrize('joint', [False, True], ids=['apart', 'joint'])
 @pytest.mark.parametrize('B,L,n,V', [(2, 1025, 4, 3), (3, 4096, 4, 4), (2, 5000, 4, 5), (1, 70000, 3, 8)])
-def test_repetition_vs_oracle_long_rows(B, L, n, V):
+def test_repetition_vs_oracle_long_rows(B, L, n, V, joint):
     """Hawkes and streak scans over rows that span many chunks (the carry between chunks and the chunk-summed d kappa)
     against the oracle's sequential scans, outputs and every gradient."""
-    say('repetition long rows', B, L, n, V)
+    say('repetition long rows', B, L, n, V, joint)
     g = torch.Generator().manual_seed(L)
     x = torch.randint(0, V, (B, L), generator=g)
     sig = O.firmas(x)
@@ -292,8 +301,8 @@ def test_repetition_vs_oracle_long_rows(B, L, n, V):
     ((ref['hawkes'] * gh).sum() + (ref['racha'] * gr).sum()).backward()
     leaves = [t.detach().to(DEV).requires_grad_() for t in (beta, Bt, la, lk, lkr)]
     _, order, rep, rank_k, vistos = ops.ngram_sort(sig.to(DEV), c.to(DEV), n)
-    hawkes = ops.Hawkes.apply(leaves[1], leaves[2], leaves[3].exp(), order, rep, rank_k)
-    racha = ops.Streak.apply(leaves[0], leaves[4].exp(), vistos)
+    hawkes, racha = repetition(leaves[1], leaves[2], leaves[3].exp(), leaves[0], leaves[4].exp(), order, rep, rank_k,
+                               vistos, joint)
     ((hawkes * gh.to(DEV)).sum() + (racha * gr.to(DEV)).sum()).backward()
     assert torch.equal(vistos.cpu(), ref['vistos'])
     assert_close(hawkes, ref['hawkes'], 'hawkes')
