@@ -10,6 +10,7 @@ shapes raise.
 """
 import dataclasses
 import math
+import os
 
 import torch
 import torch.nn as nn
@@ -404,7 +405,11 @@ _LATERAL = {}
 
 
 def _lateral(device):
-    """The second stream of a device (default priority), made once."""
+    """The second stream of a device (default priority), made once. With ASRN_ONE_STREAM=1 in the environment the
+    branches run one after the other on the current stream instead (a profiler's kernel trace then times each kernel
+    alone, without the waits of kernels that share the CUs)."""
+    if os.environ.get('ASRN_ONE_STREAM') == '1':
+        return torch.cuda.current_stream(device)
     i = torch.device(device).index
     if i is None:
         i = torch.cuda.current_device()

@@ -169,6 +169,17 @@ __device__ __forceinline__ float4 ld4r(const float* base, uint32_t off) {
     return ld4(base + off);
   }
 }
+// 4 bf16 values (8 bytes) at element `off` of a bf16 row, as two packed pairs
+__device__ __forceinline__ uint2 ld_bf16x4(const float* base, uint32_t off) {
+  return *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(base) + off);
+}
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+// acc + <x, y> over 4 bf16 pairs: exact products, fp32 sums (v_dot2c_f32_bf16)
+__device__ __forceinline__ float dot_bf16x4(uint2 x, uint2 y, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.x), __builtin_bit_cast(bf16x2, y.x), acc, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.y), __builtin_bit_cast(bf16x2, y.y), acc, false);
+}
+
 // 4 values stored at element `off` of an fp32 or bf16 (B16: rounded to nearest even, as a cast to bfloat16 does) row
 __device__ __forceinline__ uint32_t bf16_bits(float x) {
   const uint32_t u = __float_as_uint(x);
@@ -557,10 +568,20 @@ template <bool FB16>
 __device__ __forceinline__ void unique_bases8(const Cand& a, int64_t b, int64_t tok, int NU, Scratch& S, int first,
                                               int step) {
   const int lane = lane_id(), g = lane >> 3;
-  float4 q[4];
-  feat8_row<FB16>(a, feat8<FB16>(a, a.Qc, true), (uint32_t)tok, q, true);
+  const Feat8 fq = feat8<FB16>(a, a.Qc, true);
   const Feat8 fl = feat8<FB16>(a, a.Kc, false);
   const uint32_t row0 = (uint32_t)(b * a.L);
+  // fp32 rows: the query's features pre-scaled. bf16 rows: the query's stay packed, each chunk's v_dot2c products
+  // then take the chunk's scale (scale_phi, scale_c, or 0 past P + cf: a chunk lies in one of the two)
+  float4 q[4];
+  uint2 qb[4];
+  if constexpr (FB16) {
+    const uint32_t op = (uint32_t)tok * (uint32_t)a.P, oc = (uint32_t)tok * (uint32_t)a.ldq;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) qb[k] = ld_bf16x4(fq.base[k], fq.conf[k] ? oc : op);
+  } else {
+    feat8_row<FB16>(a, fq, (uint32_t)tok, q, true);
+  }
   for_chunks<16>(first, NU, step, [&](auto n, int u0) {
     constexpr int RG = decltype(n)::value >= 8 ? decltype(n)::value / 8 : 1;   // row groups of 8 in flight
     int pos[RG];
@@ -569,17 +590,38 @@ __device__ __forceinline__ void unique_bases8(const Cand& a, int64_t b, int64_t 
       const int u = u0 + 8 * r + g;
       pos[r] = S.upos[u < NU ? u : NU - 1];
     }
-    float4 f[RG][4];
+    float p[RG];
+    if constexpr (FB16) {
+      uint2 f[RG][4];
 #pragma unroll
-    for (int r = 0; r < RG; ++r) feat8_row<FB16>(a, fl, row0 + (uint32_t)pos[r], f[r], false);
+      for (int r = 0; r < RG; ++r) {
+        const uint32_t row = row0 + (uint32_t)pos[r];
+        const uint32_t op = row * (uint32_t)a.P, oc = row * (uint32_t)a.ldq;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) f[r][k] = ld_bf16x4(fl.base[k], fl.conf[k] ? oc : op);
+      }
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        p[r] = fq.scale[0] * dot_bf16x4(qb[0], f[r][0], 0.f);
+#pragma unroll
+        for (int k = 1; k < 4; ++k) p[r] += fq.scale[k] * dot_bf16x4(qb[k], f[r][k], 0.f);
+      }
+    } else {
+      float4 f[RG][4];
+#pragma unroll
+      for (int r = 0; r < RG; ++r) feat8_row<FB16>(a, fl, row0 + (uint32_t)pos[r], f[r], false);
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        p[r] = dot4(q[0], f[r][0]);
+#pragma unroll
+        for (int k = 1; k < 4; ++k) p[r] += dot4(q[k], f[r][k]);
+      }
+    }
 #pragma unroll
     for (int r = 0; r < RG; ++r) {
-      float p = dot4(q[0], f[r][0]);
-#pragma unroll
-      for (int k = 1; k < 4; ++k) p += dot4(q[k], f[r][k]);
-      p = group8_sum(p);
+      const float pr = group8_sum(p[r]);
       const int u = u0 + 8 * r + g;
-      if ((lane & 7) == 0 && u < NU) S.ua[u] = p;
+      if ((lane & 7) == 0 && u < NU) S.ua[u] = pr;
     }
   });
   wave_lds_sync();
@@ -635,73 +677,100 @@ __device__ __forceinline__ int slab_col(const Cand& a, int c0, int ch, int lane)
 // <fixed, row_u> over the d columns for every unique (rows of batch row `rows`), R rows in flight, written to
 // out[u] (added to it when `add`: the slabs after the first); the key side (w_u != nullptr) also accumulates
 // dV += w_u row_u from the same loads. fixed holds columns c0 .. c0 + 256 DCH - 1 (zero past d).
-// The wave totals of 8 per-lane values at once, by a transposing butterfly: at distances 32, 16 and 8 each lane keeps
-// half of its values and adds its partner's copies of them, so value (lane >> 3) & 7 is left, summed over the lanes
-// that share lane & 7 ... bits 3-5; the 8 lanes of each aligned group then add it up (group8_sum). About 30 VALU and
-// 6 LDS-pipe exchanges for 8 totals, against 8 separate wave sums.
-__device__ __forceinline__ float wave_sums8(const float (&v)[8]) {
+// The wave totals of N = 2, 4 or 8 per-lane values at once, by a transposing butterfly: at distances 32 (N >= 2), 16
+// (N >= 4) and 8 (N = 8) each lane keeps half of its values and adds its partner's copies of them, so one value is
+// left per lane, value (lane >> (6 - log2 N)) & (N - 1); the lanes that hold it (aligned groups of 64 / N) then add it
+// up with DPP steps. Returns that total; wave_sums_lead(N) says which lane writes value i: about 30 VALU and 6
+// LDS-pipe exchanges for 8 totals, against 8 separate wave sums.
+template <int N>
+__device__ __forceinline__ float wave_sums(const float (&v)[N]) {
+  static_assert(N == 2 || N == 4 || N == 8, "2, 4 or 8 values");
   const int lane = lane_id();
-  const bool h32 = lane & 32, h16 = lane & 16, h8 = lane & 8;
-  float a[4];
+  const bool h32 = lane & 32;
+  float a[N / 2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) a[i] = (h32 ? v[4 + i] : v[i]) + __shfl_xor(h32 ? v[i] : v[4 + i], 32, kWave);
-  float c[2];
+  for (int i = 0; i < N / 2; ++i)
+    a[i] = (h32 ? v[N / 2 + i] : v[i]) + __shfl_xor(h32 ? v[i] : v[N / 2 + i], 32, kWave);
+  if constexpr (N == 2) {                     // halves of 32: the row sums, then row 1 (3) adds row 0 (2)
+    const float x = row_sum16(a[0]);
+    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xA, 0xF, false));
+  } else {
+    const bool h16 = lane & 16;
+    float c[N / 4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) c[i] = (h16 ? a[2 + i] : a[i]) + __shfl_xor(h16 ? a[i] : a[2 + i], 16, kWave);
-  const float send = h8 ? c[0] : c[1];
-  const float x = (h8 ? c[1] : c[0]) +
-                  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x128, 0xF, 0xF, false));  // lane ^ 8
-  return group8_sum(x);
+    for (int i = 0; i < N / 4; ++i)
+      c[i] = (h16 ? a[N / 4 + i] : a[i]) + __shfl_xor(h16 ? a[i] : a[N / 4 + i], 16, kWave);
+    if constexpr (N == 4) {
+      return row_sum16(c[0]);
+    } else {
+      const bool h8 = lane & 8;
+      const float send = h8 ? c[0] : c[1];
+      const float x = (h8 ? c[1] : c[0]) +
+                      __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x128, 0xF, 0xF, false));
+      return group8_sum(x);
+    }
+  }
+}
+// the value wave_sums<N> leaves in this lane, and whether this lane is the one that writes it
+template <int N>
+__device__ __forceinline__ int wave_sums_index() { return (lane_id() >> (N == 8 ? 3 : (N == 4 ? 4 : 5))) & (N - 1); }
+template <int N>
+__device__ __forceinline__ bool wave_sums_lead() {
+  const int lane = lane_id();
+  return N == 8 ? (lane & 7) == 0 : (N == 4 ? (lane & 15) == 0 : (lane & 31) == 16);
 }
 
-// out[u] = <fixed, row_u> over the d columns for every unique (rows of batch row `rows`), 8 rows in flight, the 8 dot
-// products reduced together (wave_sums8); added to out[u] when `add` (the slabs after the first). fixed holds columns
-// c0 .. c0 + 256 DCH - 1 (zero past d).
+// out[u] = <fixed row, row_u> over columns c0 .. c0 + 256 DCH - 1 for every unique (rows of batch row `rows`), NF rows
+// in flight and their dot products reduced together (wave_sums); added to out[u] when `add` (the slabs after the
+// first). `fixed` is the fixed row's element 0 (dO of the query); past d both sides read column d - 4 and the fixed
+// side is zeroed. bf16 rows (B16) stay packed: v_dot2c_f32_bf16 takes both sides as they are stored.
 template <int DCH, bool B16 = false>
 __device__ __forceinline__ void unique_row_dots(const Cand& a, const float* rows, int64_t ld, int NU,
-                                                const float4 (&fixed)[DCH], Scratch& S, float* out, int c0 = 0,
+                                                const float* fixed, Scratch& S, float* out, int c0 = 0,
                                                 bool add = false) {
   const int lane = lane_id();
   constexpr int NF = DCH >= 3 ? 2 : (DCH == 2 ? 4 : 8);
   int col[DCH];
+  using Q = typename std::conditional<B16, uint2, float4>::type;
+  Q fq[DCH];
 #pragma unroll
-  for (int ch = 0; ch < DCH; ++ch) col[ch] = slab_col(a, c0, ch, lane);
+  for (int ch = 0; ch < DCH; ++ch) {
+    col[ch] = slab_col(a, c0, ch, lane);
+    const bool live = c0 + ch * 256 + lane * 4 < a.d;
+    if constexpr (B16) fq[ch] = live ? ld_bf16x4(fixed, (uint32_t)col[ch]) : make_uint2(0u, 0u);
+    else fq[ch] = live ? ld4(fixed + col[ch]) : zero4();
+  }
   for_chunks<NF>(0, NU, NF, [&](auto n, int u0) {
     constexpr int R = decltype(n)::value;
     int p[R];
 #pragma unroll
     for (int r = 0; r < R; ++r)                        // wave-uniform rows: their offsets are scalar arithmetic
       p[r] = __builtin_amdgcn_readfirstlane(S.upos[u0 + r < NU ? u0 + r : NU - 1]);
-    float4 o[R][DCH];
+    Q o[R][DCH];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const float* row = rows_at<B16>(rows, (int64_t)(uint32_t)p[r] * ld);
 #pragma unroll
-      for (int ch = 0; ch < DCH; ++ch) o[r][ch] = ld4r<B16>(row, (uint32_t)col[ch]);
+      for (int ch = 0; ch < DCH; ++ch) {
+        if constexpr (B16) o[r][ch] = ld_bf16x4(row, (uint32_t)col[ch]);
+        else o[r][ch] = ld4(row + col[ch]);
+      }
     }
-    if constexpr (NF == 8) {                           // the 8 dot products reduced together
-      float q[8];
+    float q[NF];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        q[r] = 0.f;
-        if (r < R) {
+    for (int r = 0; r < NF; ++r) {
+      q[r] = 0.f;
+      if (r < R) {
 #pragma unroll
-          for (int ch = 0; ch < DCH; ++ch) q[r] += dot4(o[r][ch], fixed[ch]);
+        for (int ch = 0; ch < DCH; ++ch) {
+          if constexpr (B16) q[r] = dot_bf16x4(o[r][ch], fq[ch], q[r]);
+          else q[r] += dot4(o[r][ch], fq[ch]);
         }
       }
-      const float tot = wave_sums8(q);                 // row (lane >> 3) & 7 of the chunk
-      const int u = u0 + ((lane >> 3) & 7);
-      if ((lane & 7) == 0 && ((lane >> 3) & 7) < R && u < NU) out[u] = add ? out[u] + tot : tot;
-    } else {                                           // wide rows, few in flight: one wave sum each
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float q = 0.f;
-#pragma unroll
-        for (int ch = 0; ch < DCH; ++ch) q += dot4(o[r][ch], fixed[ch]);
-        const float tot = wave_sum_u(q);
-        if (lane == 0 && u0 + r < NU) out[u0 + r] = add ? out[u0 + r] + tot : tot;
-      }
     }
+    const float tot = wave_sums<NF>(q);
+    const int r = wave_sums_index<NF>(), u = u0 + r;
+    if (wave_sums_lead<NF>() && r < R && u < NU) out[u] = add ? out[u] + tot : tot;
   });
   wave_lds_sync();
 }
@@ -1067,7 +1136,8 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
 
 // RB: how V (and the backward's dO) and the features [phi ; Qc ; Kc] are stored: 0 fp32; 1 V and dO bf16; 2 all bf16
 template <int F4, int DCH, int RB>
-__global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 7 : 1) void k_cand_fwd(Cand a) {   // 7 waves per SIMD when narrow
+__global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? (RB == 0 ? 7 : 6) : 1)
+void k_cand_fwd(Cand a) {   // 6-7 waves per SIMD when narrow
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
   const TokAt at = sorted_token_of_wave(a);
@@ -1189,14 +1259,8 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 7 :
   }
   // dp_u = <dO_q, V_u>, summed over the slabs of 256 DCH columns (ends with a wave sync)
   for (int c0 = 0; c0 < a.d; c0 += 256 * DCH) {
-    float4 dO[DCH];
-#pragma unroll
-    for (int ch = 0; ch < DCH; ++ch) {
-      const int dd = c0 + ch * 256 + lane * 4;
-      dO[ch] = dd < a.d ? ld4r<B16>(rows_at<B16>(a.dsal, tok * a.d), (uint32_t)dd) : zero4();
-    }
-    unique_row_dots<DCH, B16>(a, rows_at<B16>(a.V, (b * a.L + a.vshift) * a.ldv), a.ldv, NU, dO, S, S.uc, c0,
-                              c0 > 0);
+    unique_row_dots<DCH, B16>(a, rows_at<B16>(a.V, (b * a.L + a.vshift) * a.ldv), a.ldv, NU,
+                              rows_at<B16>(a.dsal, tok * a.d), S, S.uc, c0, c0 > 0);
   }
 
   // per entry: att * dp (S.ua is a per-entry buffer here)
@@ -1316,7 +1380,7 @@ __device__ __forceinline__ void unique_row_sum(const Cand& a, const float* rows,
 // slot for this key; per distinct query the table sums weight dO (-> dV) and [phi_q ; Qc_q] (-> d phi_k, d Kc_k).
 // ---------------------------------------------------------------------------------------------------------------------
 template <int F4, int DCH, int RB>
-__global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 6 : ((F4 == 1 && DCH != 3) ? 5 : 1))
+__global__ __launch_bounds__(kWave * kWavesPerBlock, (F4 == 1 && DCH == 1) ? 6 : ((F4 == 1 && DCH == 2) ? 5 : 1))
 void k_cand_bwd_k(Cand a) {
   constexpr bool B16 = RB >= 1, FB16 = RB == 2;
   __shared__ Scratch scratch[kWavesPerBlock];

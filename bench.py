@@ -117,7 +117,8 @@ SURVEY_BYTES = {'cfg2': {'hip': 3340 + 4436, 'layer': 10680 + 15196},
 # the library entry points whose kernels are K1-K5 (the clock scan runs forward and backward)
 K1_K5 = {'K1 hash + bucket sort': ['asrn_bucket_sort'], 'K2 clock': ['asrn_clock_scan'],
          'K3 n-gram sort': ['asrn_ngram_sort'],
-         'K4 Hawkes/streak scans': ['asrn_hawkes_fwd', 'asrn_hawkes_bwd', 'asrn_streak_fwd', 'asrn_streak_bwd'],
+         'K4 Hawkes/streak scans': ['asrn_hawkes_fwd', 'asrn_hawkes_bwd', 'asrn_streak_fwd', 'asrn_streak_bwd',
+                                    'asrn_repetition_fwd', 'asrn_repetition_bwd'],
          'K5 candidates': ['asrn_candidates_fwd', 'asrn_candidates_bwd']}
 
 
@@ -366,6 +367,128 @@ def hip_aggregate(hip_b, tokens, eager_ms, prof_us):
             'frac': round(hip_b * tokens / (HBM_PEAK * eager_ms * 1e-3), 4)}
 
 
+# kernel names (rocprofv3) of the K1-K5 groups and of the entry points whose traffic is reported
+K1_K5_KERNELS = {'K1 hash + bucket sort': ('k_bucket_',), 'K2 clock': ('ClockOp',),
+                 'K3 n-gram sort': ('k_ngram_', 'k_merge_pass'),
+                 'K4 Hawkes/streak scans': ('Hawkes', 'Streak', 'k_hawkes_'), 'K5 candidates': ('k_cand_',)}
+ENTRY_KERNELS = {'asrn_candidates_fwd': ('k_cand_fwd',), 'asrn_candidates_bwd': ('k_cand_bwd_q', 'k_cand_bwd_k'),
+                 'asrn_bucket_sort': ('k_bucket_',), 'asrn_ngram_sort': ('k_ngram_', 'k_merge_pass')}
+
+
+def _csv_rows(path):
+    import csv
+    import glob
+    files = glob.glob(os.path.join(path, '**', '*.csv'), recursive=True) if os.path.isdir(path) else [path]
+    return files, csv
+
+
+def summarize_trace(path, steps, command):
+    """A rocprofv3 --kernel-trace --stats run (its directory) of `steps` traced steps -> the per-step summary that
+    profiles/<config>_kernel_times.json holds: all kernels, the HIP library's, and K1-K5 by group and kernel."""
+    files, csv = _csv_rows(path)
+    stats = [f for f in files if f.endswith('kernel_stats.csv')]
+    if not stats:
+        raise SystemExit(f'no kernel_stats.csv under {path}')
+    rows = list(csv.DictReader(open(stats[0])))
+    per = {r['Name']: float(r['TotalDurationNs']) / 1e3 / steps for r in rows}
+    calls = {r['Name']: int(r['Calls']) / steps for r in rows}
+    groups, by_kernel = {}, {}
+    for g, keys in K1_K5_KERNELS.items():
+        ks = {n: us for n, us in per.items() if 'asrn::' in n and any(k in n for k in keys)}
+        groups[g] = round(sum(ks.values()), 2)
+        for n, us in ks.items():
+            by_kernel[n.split('(')[0]] = {'us_per_step': round(us, 2), 'launches_per_step': calls[n]}
+    return {'hip_us_per_step': round(sum(us for n, us in per.items() if 'asrn::' in n), 1),
+            'all_kernels_us_per_step': round(sum(per.values()), 1),
+            'k1_k5_us_per_step': round(sum(groups.values()), 1), 'k1_k5_us_by_kernel': groups,
+            'k1_k5_kernels': by_kernel, 'traced_steps': steps, 'source': command}
+
+
+def summarize_traffic(fetch, write, cal_fetch, cal_write, cal_bytes, command):
+    """rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE runs of the eager bench, and the same passes over a plain copy
+    of cal_bytes (bench.py --copy-calibration) -> HBM bytes per launch of the entry points in ENTRY_KERNELS."""
+    def per_kernel(path, counter):
+        files, csv = _csv_rows(path)
+        vals = {}
+        for f in files:
+            if f.endswith('counter_collection.csv'):
+                for r in csv.DictReader(open(f)):
+                    if r['Counter_Name'] == counter:
+                        vals.setdefault(r['Kernel_Name'], []).append(float(r['Counter_Value']))
+        return {k: sum(v) / len(v) for k, v in vals.items()}
+    def copy_kib(path, counter):
+        v = per_kernel(path, counter)
+        return max(v.values()) if v else None
+    f_scale = cal_bytes / 1024 / copy_kib(cal_fetch, 'FETCH_SIZE')
+    w_scale = cal_bytes / 1024 / copy_kib(cal_write, 'WRITE_SIZE')
+    fk, wk = per_kernel(fetch, 'FETCH_SIZE'), per_kernel(write, 'WRITE_SIZE')
+    out = {}
+    for e, keys in ENTRY_KERNELS.items():
+        names = [n for n in fk if 'asrn::' in n and any(k in n for k in keys)]
+        if names:
+            out[e] = int(1024 * sum(f_scale * fk[n] + w_scale * wk.get(n, 0.0) for n in names))
+    return {'calibration': {'FETCH_SIZE_KiB_scale': f_scale, 'WRITE_SIZE_KiB_scale': w_scale,
+                            'copy_bytes': cal_bytes},
+            'bytes_per_launch': out, 'source': command}
+
+
+def summarize_kernels(trace, steps, fetch, write, sq1, sq2, cal_fetch, cal_write, cal_bytes, algo_mb=None, top=30):
+    """A markdown table of the HIP kernels of one traced configuration: launches and mean time (kernel trace), VGPRs,
+    LDS and workgroup size (dispatch records), HBM bytes per launch (FETCH_SIZE / WRITE_SIZE calibrated by a copy),
+    L2 hit rate, LDS bank-conflict cycles per LDS instruction, VALU and LDS instructions per wave and the SIMDs'
+    VALU-busy fraction: SQ_ACTIVE_INST_VALU (quad-cycles, summed over the chip) over CU_NUM x the kernel's cycles
+    (GRBM_GUI_ACTIVE, which the profiler sums over the 8 XCDs)."""
+    import csv
+    def counters(path):
+        files, _ = _csv_rows(path)
+        acc = {}
+        for f in files:
+            if f.endswith('counter_collection.csv'):
+                for r in csv.DictReader(open(f)):
+                    d = acc.setdefault(r['Kernel_Name'], {'meta': r})
+                    d.setdefault(r['Counter_Name'], []).append(float(r['Counter_Value']))
+        return {k: {c: (sum(v) / len(v) if c != 'meta' else v) for c, v in d.items()} for k, d in acc.items()}
+    files, _ = _csv_rows(trace)
+    stats = list(csv.DictReader(open([f for f in files if f.endswith('kernel_stats.csv')][0])))
+    disp = {}
+    for r in csv.DictReader(open([f for f in files if f.endswith('kernel_trace.csv')][0])):
+        disp.setdefault(r['Kernel_Name'], r)
+    cf, cw = counters(cal_fetch), counters(cal_write)
+    f_scale = cal_bytes / 1024 / max(v.get('FETCH_SIZE', 0) for v in cf.values())
+    w_scale = cal_bytes / 1024 / max(v.get('WRITE_SIZE', 0) for v in cw.values())
+    F, W, S1, S2 = counters(fetch), counters(write), counters(sq1), counters(sq2)
+    rows = []
+    for r in stats:
+        n = r['Name']
+        if 'asrn::' not in n:
+            continue
+        us = float(r['AverageNs']) / 1e3
+        d = disp.get(n, {})
+        mb = (f_scale * F.get(n, {}).get('FETCH_SIZE', 0.0) + w_scale * W.get(n, {}).get('WRITE_SIZE', 0.0)) * 1024 / 1e6
+        s1, s2 = S1.get(n, {}), S2.get(n, {})
+        waves = s1.get('SQ_WAVES') or float('nan')
+        hit = s2.get('TCC_HIT_sum', 0.0)
+        miss = s2.get('TCC_MISS_sum', 0.0)
+        lds = s2.get('SQ_ACTIVE_INST_LDS') or float('nan')
+        grbm = s1.get('GRBM_GUI_ACTIVE') or float('nan')
+        rows.append((int(r['Calls']) / steps * us, n.split('(')[0][:60], int(r['Calls']) / steps, us,
+                     d.get('LDS_Block_Size', ''), d.get('Workgroup_Size_X', ''), mb,
+                     mb / 1e3 / (us * 1e-6) if us else 0.0, hit / (hit + miss) if hit + miss else float('nan'),
+                     s2.get('SQ_LDS_BANK_CONFLICT', 0.0) / lds, s1.get('SQ_INSTS_VALU', float('nan')) / waves,
+                     s1.get('SQ_INSTS_LDS', float('nan')) / waves,
+                     s1.get('SQ_ACTIVE_INST_VALU', float('nan')) / (256 * grbm / 8)))
+    rows.sort(key=lambda x: -x[0])
+    out = ['| kernel | launches/step | us | LDS B | WG | HBM MB/launch | GB/s | L2 hit | LDS conflict/inst | '
+           'VALU inst/wave | LDS inst/wave | SIMD VALU busy |', '|' + '---|' * 12]
+    for x in rows[:top]:
+        out.append(f'| `{x[1]}` | {x[2]:.1f} | {x[3]:.1f} | {x[4]} | {x[5]} | {x[6]:.1f} | {x[7]:.0f} | '
+                   f'{x[8]:.2f} | {x[9]:.2f} | {x[10]:.0f} | {x[11]:.0f} | {x[12]:.2f} |')
+    out.append('')
+    out.append(f'Copy calibration: FETCH_SIZE x {f_scale:.3f} KiB, WRITE_SIZE x {w_scale:.3f} KiB '
+               f'(a {cal_bytes}-byte device copy).')
+    return '\n'.join(out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -390,7 +513,30 @@ def main():
     ap.add_argument('--copy-calibration', type=int, default=0, metavar='BYTES',
                     help='only run a plain device-to-device copy of BYTES, 3 times: the reference point that scales '
                          'the FETCH_SIZE / WRITE_SIZE counters of a profiler run into bytes')
+    ap.add_argument('--summarize-trace', metavar='DIR', default=None,
+                    help='only summarize a rocprofv3 kernel-trace directory of --trace-steps steps into the JSON of '
+                         'profiles/<config>_kernel_times.json (printed); needs no GPU')
+    ap.add_argument('--trace-steps', type=int, default=13)
+    ap.add_argument('--summarize-traffic', nargs=5, metavar=('FETCH', 'WRITE', 'CAL_FETCH', 'CAL_WRITE', 'CAL_BYTES'),
+                    default=None, help='only turn FETCH_SIZE / WRITE_SIZE counter runs and their copy calibration '
+                                       'into the JSON of profiles/cfg2_traffic.json (printed); needs no GPU')
+    ap.add_argument('--summarize-kernels', nargs=9, default=None,
+                    metavar=('TRACE', 'FETCH', 'WRITE', 'SQ1', 'SQ2', 'CAL_FETCH', 'CAL_WRITE', 'CAL_BYTES', 'STEPS'),
+                    help='only print the markdown kernel table of a traced configuration (profiles/*_kernels.md) '
+                         'from its trace and counter runs; needs no GPU')
+    ap.add_argument('--command', default='', help='the profiler command recorded with a summary')
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(json.dumps(summarize_trace(args.summarize_trace, args.trace_steps, args.command), indent=1))
+        return
+    if args.summarize_kernels:
+        t, f, w, q1, q2, cf, cw, nb, st = args.summarize_kernels
+        print(summarize_kernels(t, int(st), f, w, q1, q2, cf, cw, int(nb)))
+        return
+    if args.summarize_traffic:
+        f, w, cf, cw, nb = args.summarize_traffic
+        print(json.dumps(summarize_traffic(f, w, cf, cw, int(nb), args.command), indent=1))
+        return
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
         print(f'bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): the ASRN hot path '
