@@ -999,13 +999,13 @@ def muestrear(lg, texto, pos, pos_max, L0, piezas, terminado, paso_fin, trabajo,
 
 def paso_bloque_ok(blq, h):
     """Whether asrn_block_step takes this block and state: mezcla 'conv', fp32 parameters and state, no autocast,
-    one LayerNorm epsilon, the block's usual feed-forward layout."""
+    one LayerNorm epsilon, the block's usual feed-forward layout, d up to 4,096."""
     dev = h.device.type
     ps = [blq.ln1.weight, blq.ln1.bias, blq.conv.weight, blq.conv.bias, blq.ln2.weight, blq.ln2.bias, blq.ff[0].weight,
           blq.ff[0].bias, blq.ff[2].weight, blq.ff[2].bias]
     return (blq.mezcla == 'conv' and h.is_cuda and h.dtype == torch.float32 and h.dim() == 2 and h.stride(1) == 1
             and not torch.is_autocast_enabled(dev) and all(p is not None and p.dtype == torch.float32 for p in ps)
-            and blq.ln1.eps == blq.ln2.eps and blq.conv.groups == 1)
+            and blq.ln1.eps == blq.ln2.eps and blq.conv.groups == 1 and h.shape[-1] <= 4096)
 
 
 def espacio_bloque(B, d, ff, dev):

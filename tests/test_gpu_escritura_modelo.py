@@ -235,11 +235,12 @@ def test_model_writer_matches_reference_writer(ajeno):
 
 
 @pytest.mark.parametrize('B,d,k,ff,L', [(16, 768, 4, 1536, 9), (20, 96, 3, 40, 5), (3, 64, 1, 128, 4),
-                                          (2, 32, 4, 64, 2)])
+                                          (2, 32, 4, 64, 2), (4, 1100, 12, 300, 14), (3, 2080, 2, 72, 3)])
 def test_block_step_equals_whole_text_block(B, d, k, ff, L):
     """asrn_block_step against BloqueLocal.forward at the last position of a short text: the ring built from the
     earlier positions' LayerNorm rows (slot t mod (k - 1)), then the step at position L - 1; 20 rows span two row
-    tiles, k = 1 has no ring, L < k starts with zeros."""
+    tiles, k = 1 has no ring, L < k starts with zeros; d = 1,100 and 2,080 hold 2 and 3 columns a thread in the row
+    kernels, k = 12 has taps past the 8 loaded ahead, and ff1's depth of 1,100 takes two rounds of loads."""
     say('block step', B, d, k, ff, L)
     torch.manual_seed(B + d)
     blq = asrn_amd.BloqueLocal(d, k, ff).to(DEV)
