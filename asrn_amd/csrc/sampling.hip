@@ -31,9 +31,11 @@ namespace {
 
 constexpr unsigned long long kEmptySlot = ~0ull;
 constexpr int kSampleThreads = 1024;
+constexpr int kTiesPerThread = 4;         // greedy: tokens at the maximum a thread keeps
 constexpr int kSampleWaves = kSampleThreads / kWave;
 constexpr int kSucc = 8;                         // successors held inline per context
 constexpr int kMaxCand = 4096;                   // tokens past the top-k cut handled in LDS
+static_assert(kTiesPerThread * kSampleThreads <= kMaxCand, "a thread's ties are parked in the candidate list");
 constexpr double kMassScale = 1099511627776.0;   // 2^40: fixed-point probability masses (sums stay below 2^63)
 
 // SplitMix64's output function (G. Steele, D. Lea, C. Flood, "Fast splittable pseudorandom number generators",
@@ -331,14 +333,21 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     if (bans) successors(a.ban, b, text, pos, a.w, blist, &nb_list);
   }
 
+  // Greedy rows (top_k = 1) take the maximum and its ties in one fused pass below. With no penalty and no bans the
+  // row needs no changes, so that pass reads the logits themselves and `work` is never written.
+  const bool greedy = a.top_k == 1 && V > 1;
+  const bool direct = greedy && a.penalty == 1.f && !bans;
+  const float* src = direct ? lg : work;
   // penalty (_frenar): the logits as they came, then the tokens of the window penalized from those same values
   float* lout = (a.logits_out && step >= 0 && step < a.steps) ? a.logits_out + (b * a.steps + step) * V : nullptr;
+  if (!direct) {
   each(lg, V, [&](int64_t v, float l) {
     work[v] = l;
     if (lout) lout[v] = l;
   });
+  }
   __syncthreads();
-  if (a.penalty != 1.f) {
+  if (!direct && a.penalty != 1.f) {
     for (int j = tid; j < a.window; j += kSampleThreads) {
       const int64_t p = pos - a.window + j;
       if (p < 0) continue;
@@ -360,7 +369,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     }
   }
   __syncthreads();
-  {
+  if (!direct) {
     float finite = 0.f;
     each(work, V, [&](int64_t, float x) { finite += (x == ninf) ? 0.f : 1.f; });
     if (block_sum(finite, red) == 0.f) {                        // nothing left: the plain logits (no penalty either)
@@ -395,34 +404,102 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     return false;
   };
   float mass_p = 0.f;
-  if (quote && (qprobe || nql > 0)) {
+  const bool need_mass = quote && (qprobe || nql > 0);
+  const float tden = fmaxf(a.temperature, 1e-6f);
+  float corte = ninf;
+  // greedy: one pass gives the quote mass at temperature 1 (a running maximum with its sums rescaled), the maximum
+  // of x / T and each thread's tokens at that maximum (the kept set), in the order the list gather below uses
+  bool listed = false;
+  int ncand = 0;
+  if (greedy) {
+    float m = ninf, sm = 0.f, cm = 0.f, lmax = ninf;
+    int cnt = 0;
+    bool nan = false;                                            // NaN logits: the passes below keep them as they did
+    int* mine = (int*)cval + tid * kTiesPerThread;              // this thread's tied tokens, ascending
+    each(src, V, [&](int64_t v, float x) {
+      if (direct && lout) lout[v] = x;
+      if (need_mass && x != ninf) {
+        const bool q = qprobe && in_quote(v);
+        if (x > m) {
+          const float sc = m == ninf ? 0.f : expf(m - x);
+          sm = sm * sc + 1.f;
+          cm = cm * sc + (q ? 1.f : 0.f);
+          m = x;
+        } else {
+          const float e = expf(x - m);
+          sm += e;
+          if (q) cm += e;
+        }
+      }
+      const float l = x / tden;
+      nan |= l != l;
+      if (l > lmax) {
+        lmax = l;
+        cnt = 0;
+      }
+      if (l == lmax) {
+        if (cnt < kTiesPerThread) mine[cnt] = (int)v;
+        ++cnt;
+      }
+    });
+    if (need_mass) {
+      const float m1 = block_max(m, red);
+      const float S1 = block_sum(m == ninf ? 0.f : sm * expf(m - m1), red);
+      float c = qprobe ? (m == ninf ? 0.f : cm * expf(m - m1)) : 0.f;
+      if (!qprobe && tid < nql) c = expf(src[qlist[tid]] - m1);
+      mass_p = block_sum(c, red) / S1;
+    }
+    corte = block_max(lmax, red);
+    const int my = lmax == corte ? cnt : 0;
+    // more ties than a thread keeps, or NaN logits (degenerate rows): the count and gather passes below
+    if (block_max(my > kTiesPerThread || nan ? 1.f : 0.f, red) == 0.f) {
+      __syncthreads();
+      cscan[tid] = my;
+      __syncthreads();
+      for (int off = 1; off < kSampleThreads; off <<= 1) {
+        const int add = tid >= off ? cscan[tid - off] : 0;
+        __syncthreads();
+        cscan[tid] += add;
+        __syncthreads();
+      }
+      ncand = cscan[kSampleThreads - 1];
+      const int o = cscan[tid] - my;
+      int t[kTiesPerThread];
+#pragma unroll
+      for (int j = 0; j < kTiesPerThread; ++j) t[j] = j < my ? mine[j] : 0;
+      __syncthreads();                                             // every thread holds its ties: cval is free
+#pragma unroll
+      for (int j = 0; j < kTiesPerThread; ++j)
+        if (j < my) {
+          ctok[o + j] = t[j];
+          cval[o + j] = corte;
+        }
+      __syncthreads();
+      listed = true;
+    }
+    __syncthreads();
+  } else if (need_mass) {
     float m = ninf;
-    each(work, V, [&](int64_t, float x) { m = fmaxf(m, x); });
+    each(src, V, [&](int64_t, float x) { m = fmaxf(m, x); });
     const float m1 = block_max(m, red);
     float s = 0.f, c = 0.f;
-    each(work, V, [&](int64_t v, float x) {
+    each(src, V, [&](int64_t v, float x) {
       const float e = expf(x - m1);
       s += e;
       if (qprobe && in_quote(v)) c += e;
     });
-    if (!qprobe && tid < nql) c = expf(work[qlist[tid]] - m1);
+    if (!qprobe && tid < nql) c = expf(src[qlist[tid]] - m1);
     const float S1 = block_sum(s, red);
     mass_p = block_sum(c, red) / S1;
   }
 
   // temperature and top-k: keep the logits >= the k-th largest
-  const float tden = fmaxf(a.temperature, 1e-6f);
-  float corte = ninf;
-  if (a.top_k == 1 && V > 1) {                                   // the k-th largest is the maximum: one pass
-    float m = ninf;
-    each(work, V, [&](int64_t, float x) { m = fmaxf(m, x / tden); });
-    corte = block_max(m, red);
-  } else if (a.top_k > 0 && (int64_t)a.top_k < V) {
+  if (!greedy && a.top_k > 0 && (int64_t)a.top_k < V) {
     uint32_t prefix = 0, mask = 0, rest = (uint32_t)a.top_k;
     for (int shift = 24; shift >= 0; shift -= 8) {
       for (int i = tid; i < 256; i += kSampleThreads) hist_n[i] = 0;
       __syncthreads();
-      each_all(work, V, [&](int64_t, float x, bool ok) {
+      each_all(src, V, [&](int64_t, float x, bool ok) {
         const uint32_t k = ok ? ordered(x / tden) : 0u;
         hist_count(hist_n, (k >> shift) & 255u, ok && (k & mask) == prefix);
       });
@@ -449,11 +526,10 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   // Few tokens past the top-k cut: they are gathered into LDS in a fixed order (thread, then stride) and the rest of
   // the decision (top-p, the softmax, the quote-mass correction, the draw) runs on them alone. More than kMaxCand
   // (ties at the cut): the full-row passes below.
-  bool lista = false;
-  int ncand = 0;
-  if (a.top_k > 0 && (int64_t)a.top_k < V) {
+  bool lista = listed;
+  if (!listed && a.top_k > 0 && (int64_t)a.top_k < V) {
     int cnt = 0;
-    each(work, V, [&](int64_t, float x) { cnt += kept_k(x / tden) ? 1 : 0; });
+    each(src, V, [&](int64_t, float x) { cnt += kept_k(x / tden) ? 1 : 0; });
     __syncthreads();
     cscan[tid] = cnt;
     __syncthreads();
@@ -467,7 +543,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     lista = ncand <= kMaxCand;
     if (lista) {
       int o = cscan[tid] - cnt;
-      each(work, V, [&](int64_t v, float x) {
+      each(src, V, [&](int64_t v, float x) {
         const float l = x / tden;
         if (kept_k(l)) {
           ctok[o] = (int)v;
@@ -555,7 +631,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
       return scaled ? p * (in_quote(ctok[i]) ? sc_q : sc_n) : p;
     };
     if (a.prob_out) {
-      each(work, V, [&](int64_t v, float) { a.prob_out[b * V + v] = 0.f; });
+      each(src, V, [&](int64_t v, float) { a.prob_out[b * V + v] = 0.f; });
       __syncthreads();
       for (int i = tid; i < ncand; i += kSampleThreads) a.prob_out[b * V + ctok[i]] = prob_i(i);
     }
@@ -611,7 +687,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   } else {
     // the kept logits' max (the row's max is always kept) and top-p over their softmax
     float mloc = ninf;
-    each(work, V, [&](int64_t, float x) {
+    each(src, V, [&](int64_t, float x) {
       const float l = x / tden;
       if (kept_k(l)) mloc = fmaxf(mloc, l);
     });
@@ -620,7 +696,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     float S3 = 1.f;
     if (a.top_p < 1.f) {
       float s = 0.f;
-      each(work, V, [&](int64_t, float x) {
+      each(src, V, [&](int64_t, float x) {
         const float l = x / tden;
         if (kept_k(l)) s += expf(l - m3);
       });
@@ -635,7 +711,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
           hist_m[i] = 0;
         }
         __syncthreads();
-        each_all(work, V, [&](int64_t, float x, bool ok) {
+        each_all(src, V, [&](int64_t, float x, bool ok) {
           const float l = x / tden;
           const bool in = ok && kept_k(l);
           const float p = in ? expf(l - m3) / S3 : 0.f;
@@ -674,7 +750,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     float S4;
     {
       float s = 0.f;
-      each(work, V, [&](int64_t, float x) {
+      each(src, V, [&](int64_t, float x) {
         float e;
         if (keep(x, &e)) s += e;
       });
@@ -684,11 +760,11 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     if (quote && (qprobe || nql > 0)) {
       float c = 0.f, e;
       if (qprobe) {
-        each(work, V, [&](int64_t v, float x) {
+        each(src, V, [&](int64_t v, float x) {
           float ee;
           if (in_quote(v) && keep(x, &ee)) c += ee / S4;
         });
-      } else if (tid < nql && keep(work[qlist[tid]], &e)) {
+      } else if (tid < nql && keep(src[qlist[tid]], &e)) {
         c = e / S4;
       }
       const float mass_q = block_sum(c, red);
@@ -704,7 +780,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
       const float p = e / S4;
       return scaled ? p * (in_quote(v) ? sc_q : sc_n) : p;
     };
-    if (a.prob_out) each(work, V, [&](int64_t v, float x) { a.prob_out[b * V + v] = prob(v, x); });
+    if (a.prob_out) each(src, V, [&](int64_t v, float x) { a.prob_out[b * V + v] = prob(v, x); });
 
     // the draw: inverse CDF over the tokens in index order, each thread a contiguous segment
     const int64_t seg = (V + kSampleThreads - 1) / kSampleThreads;
@@ -712,7 +788,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     const int64_t v1 = v0 + seg < V ? v0 + seg : V;
     float local = 0.f;
     int64_t last_pos = -1;
-    each_range(work, v0, v1, [&](int64_t v, float x) {
+    each_range(src, v0, v1, [&](int64_t v, float x) {
       const float p = prob(v, x);
       local += p;
       if (p > 0.f) last_pos = v;
@@ -738,7 +814,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
       const float inside = target - before;
       float acc = 0.f;                                             // summed from 0 in `local`'s order
       int64_t chosen = -1;
-      each_range(work, v0, v1, [&](int64_t v, float x) {
+      each_range(src, v0, v1, [&](int64_t v, float x) {
         const float p = prob(v, x);
         acc += p;
         if (p > 0.f && acc > inside) {

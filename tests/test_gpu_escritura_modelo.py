@@ -103,6 +103,10 @@ SAMPLER_CASES = [
     dict(V=50304, T=0.9, k=0, p=0.9, pena=1.1, ventana=64, nb=3, nq=4),
     dict(V=20000, T=1.0, k=5000, p=1.0, pena=1.0, ventana=64, nb=0, nq=0),
     dict(V=30000, T=0.8, k=4500, p=0.7, pena=1.3, ventana=16, nb=2, nq=0),
+    # greedy rows past the register sizes: one fused pass over the logits themselves (no penalty, no bans), and over
+    # the penalized and banned row
+    dict(V=50304, T=1.0, k=1, p=1.0, pena=1.0, ventana=64, nb=0, nq=4),
+    dict(V=50304, T=0.7, k=1, p=0.9, pena=1.2, ventana=64, nb=2, nq=3),
     # contexts with more distinct successors than the inline lists hold: the bans and the quote mask probe every token
     dict(V=20, T=0.7, k=0, p=1.0, pena=1.0, ventana=64, nb=1, nq=2),
     dict(V=50, T=1.0, k=5, p=0.9, pena=1.0, ventana=64, nb=1, nq=2),
@@ -184,6 +188,60 @@ def test_sampler_hashed_ngram_keys(V, nq, nb):
         q = M.probabilidades(lgr, 0.9, 0, 1.0, sig)
         assert set(torch.nonzero(prob[b] > 0).view(-1).tolist()) == set(torch.nonzero(q > 0).view(-1).tolist()), b
         assert torch.allclose(prob[b], q, rtol=1e-4, atol=2e-6), (b, (prob[b] - q).abs().max())
+
+
+@pytest.mark.parametrize('caso', ['ties', 'ties_quoted', 'tie_overflow', 'probe'])
+def test_sampler_greedy_large_rows(caso):
+    """Greedy rows (top_k = 1) of V = 40,000 against the oracle: tied maxima (kept together, so the draw is among
+    them), ties of which one continues a quote (the quote-mass correction splits the mass between the two groups),
+    six ties held by one thread (more than its four slots: the general count and gather passes), and a quote context
+    with more distinct successors than the inline lists hold (the mask probes every token)."""
+    say('sampler greedy', caso)
+    B, V, L0 = 2, 40000, 30
+    pos = 60
+    g = torch.Generator().manual_seed(5)
+    x = torch.randint(0, V, (B, pos + 2), generator=g)
+    nq = 2
+    if caso == 'probe':
+        for b in range(B):                                      # token 7 followed by 12 distinct tokens, then 7 again
+            x[b, 2:26:2] = 7
+            x[b, 3:27:2] = torch.arange(100, 112)
+            x[b, pos - 1] = 7
+    else:
+        x[:, pos - 1] = x[:, 10]                                # the context continues the text at 11: a quote
+    texto = x.to(DEV).contiguous()
+    cita = ops.ConjuntoNgramas(B, nq, V, pos + 2, DEV)
+    cita.agregar_texto(texto[:, :pos].contiguous())
+    lg = torch.randn(B, V, generator=g) * 3
+    top = float(lg.max()) + 1.0
+    for b in range(B):
+        sig = sorted(M.ngramas_siguientes(x[b, :pos].tolist(), nq))
+        if caso == 'ties':
+            lg[b, [17, 9000, 39999]] = top
+        elif caso == 'ties_quoted':
+            lg[b, [sig[0], 123, 31000]] = top
+        elif caso == 'tie_overflow':
+            lg[b, [300 + 1024 * j for j in range(6)] + [5]] = top
+        elif caso == 'probe':
+            assert len(sig) > ops.query('asrn_ngram_set_successors')
+            lg[b, sig[3]] = top
+    lg = lg.to(DEV)
+    est = _Estado(B, V, pos + 2)
+    pdev = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    ops.muestrear(lg, texto, pdev, pos + 1, L0, est.piezas, est.terminado, est.paso_fin, est.trabajo, est.bits, 1.0, 1,
+                  1.0, 1.0, 64, 99, cita=cita, prob=est.prob)
+    torch.cuda.synchronize()
+    prob = est.prob.cpu().double()
+    texto_cpu = texto.cpu()
+    for b in range(B):
+        t_b = texto_cpu[b, :pos].tolist()
+        q = M.probabilidades(lg[b].cpu().double(), 1.0, 1, 1.0, M.ngramas_siguientes(t_b, nq))
+        assert set(torch.nonzero(prob[b] > 0).view(-1).tolist()) == set(torch.nonzero(q > 0).view(-1).tolist()), b
+        assert torch.allclose(prob[b], q, rtol=1e-4, atol=2e-6), (b, (prob[b] - q).abs().max())
+        tok = int(est.piezas[b])
+        assert q[tok] > 0 and int(texto_cpu[b, pos]) == tok
+        if caso == 'ties_quoted':
+            assert 0 < float(q[q > 0].min()) < float(q.max())        # the two groups carry different masses
 
 
 def test_sampler_distribution_and_seed():
