@@ -81,6 +81,12 @@ class EscritorCapa:
         self.hawkes = ops.HawkesTable.load(partes['claves'], partes['orden_k'], partes['repetido'], partes['hawkes'],
                                            partes['Bt'], partes['log_alfa'], cap=2 * self.cap)
         self.racha = partes['racha'][:, -1].to(f32).contiguous().clone()
+        # both decay rates (capa._kappas' values, without autograd), once: the weights do not change while writing, so
+        # a step (and its graph) reads them instead of launching the exponential again
+        kappa, kappa_r = torch._foreach_exp([capa.log_kappa, capa.log_kappa_racha])
+        if capa.protecciones.kappa_min is not None:
+            kappa, kappa_r = kappa.clamp(min=capa.protecciones.kappa_min), kappa_r.clamp(min=capa.protecciones.kappa_min)
+        self.kappas = (kappa, kappa_r)
         # (query, table) pairs of the steps where the unprotected layer's -1e9 fill would leak (CapaASRN.fugas)
         self.fugas_t = torch.zeros(1, dtype=torch.int32, device=E.device)
         self.e_ult = E[:, -1]
@@ -120,10 +126,7 @@ class EscritorCapa:
             self._escribir('Kc', pos, Kc[:, 0])
             self._escribir('log_alfa', pos, log_alfa[:, 0])
             beta_t = beta[:, 0]
-        # both decay rates in one launch (capa._kappas' values, without autograd)
-        kappa, kappa_r = torch._foreach_exp([capa.log_kappa, capa.log_kappa_racha])
-        if capa.protecciones.kappa_min is not None:
-            kappa, kappa_r = kappa.clamp(min=capa.protecciones.kappa_min), kappa_r.clamp(min=capa.protecciones.kappa_min)
+        kappa, kappa_r = self.kappas
         vistos, hawkes = self.hawkes.step(c, pos, beta_t, capa.c_vistos, kappa, kappa_r, self.racha, t_max=t_max,
                                           reloj32=not capa.protecciones.reloj_64)
         forma = self._forma()
