@@ -20,6 +20,8 @@
 // (key-side gradients: reads each (att, ds) pair with one 8-byte load at the slots of the queries that see the key).
 #include <type_traits>
 
+#include <cstdlib>
+
 #include "common.h"
 
 namespace asrn {
@@ -66,6 +68,8 @@ struct Cand {
   int clock32; int32_t* leak;
   // ceil(2^64 / L) (0 when L = 1): a token index's batch row is the high half of its 64-bit product with this
   uint64_t Linv;
+  // > 0: the XCDs take one batch row at a time, XCD x the positions [x slice, (x + 1) slice) of it (L = 8 slice)
+  int64_t slice;
 };
 
 // i / L for 0 <= i < 2^32: the high half of i * ceil(2^64 / L) (the product exceeds i * 2^64 / L by less than
@@ -118,17 +122,24 @@ __device__ __forceinline__ float from_order_key(uint32_t k) {
 // each XCD a contiguous range of tokens instead, so one XCD's L2 serves one stretch of a batch row (at B = 8, one
 // whole row) and candidates, which are earlier positions of the same row, hit there. The tail that does not divide
 // evenly keeps the identity mapping.
-#ifndef ASRN_XCD_MAP
-#define ASRN_XCD_MAP 1
-#endif
+// When the rows of all the batch rows that run at once outgrow the chip's 256 MB last-level cache (cfg3: 4 rows of
+// 65,536 positions, 335 MB), a.slice > 0 turns the mapping row-wise instead: all eight XCDs work on one batch row at a
+// time, XCD x on the x-th eighth of it, so the rows the waves gather (earlier positions of that one row) stay in the
+// last-level cache that the XCDs share.
 constexpr int kXcds = 8;
-__device__ __forceinline__ int64_t token_of_wave() {
+__device__ __forceinline__ int64_t token_of_wave(const Cand& a) {
   const int64_t n = gridDim.x, i = blockIdx.x;
   int64_t blk = i;
-  if (ASRN_XCD_MAP) {
-    const int64_t per = n / kXcds;
-    if (i < per * kXcds) blk = (i % kXcds) * per + i / kXcds;
+  if (a.slice > 0) {
+    const int64_t x = i % kXcds, j = i / kXcds;             // the j-th wave of XCD x
+    if (i < a.B * a.L) {
+      const int64_t b = j / a.slice;
+      return b * a.L + x * a.slice + (j - b * a.slice);
+    }
+    return i;
   }
+  const int64_t per = n / kXcds;
+  if (i < per * kXcds) blk = (i % kXcds) * per + i / kXcds;
   return blk * kWavesPerBlock + (threadIdx.x >> 6);
 }
 
@@ -379,10 +390,22 @@ __device__ __forceinline__ int gather(const Cand& a, int64_t b, int64_t t, bool 
 // bucket ids come from the signs of the query's own hash outputs (written to ids_out for the ring insert).
 __device__ __forceinline__ int gather_rings(const Cand& a, int64_t b, int64_t t, Scratch& S) {
   const int lane = lane_id();
+  // the query's bucket id in each table from the signs of its phi row (strict > 0, nucleo:663): the whole row in one
+  // round of loads (element c * 64 + lane; P = T nb <= 255), then table `lane`'s nb bits out of the ballots
+  const float* ph = a.phi + (b * a.L + t) * a.P;
+  uint64_t pm[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int e = c * kWave + lane;
+    pm[c] = __ballot(e < a.P && ph[e] > 0.f);
+  }
   int id = 0, cnt = 0;
   if (lane < a.T) {
-    const float* ph = a.phi + (b * a.L + t) * a.P + lane * a.nb;
-    for (int j = 0; j < a.nb; ++j) id |= (ph[j] > 0.f ? 1 : 0) << j;     // strict > 0 (nucleo:663)
+    const int e0 = lane * a.nb, w = e0 >> 6, o = e0 & 63;
+    const uint64_t lo = w == 0 ? pm[0] : (w == 1 ? pm[1] : (w == 2 ? pm[2] : pm[3]));
+    uint64_t bits = lo >> o;
+    if (o + a.nb > 64) bits |= (w == 0 ? pm[1] : (w == 1 ? pm[2] : pm[3])) << (64 - o);   // w <= 2 here
+    id = (int)(bits & ((1ull << a.nb) - 1ull));
     a.ids_out[b * a.T + lane] = id;
     cnt = a.counts[(b * a.T + lane) * ((int64_t)1 << a.nb) + id];
   }
@@ -1485,7 +1508,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_lists(Cand a, i
                                                                        int32_t* __restrict__ ell) {
   __shared__ Scratch scratch[kWavesPerBlock];
   Scratch& S = scratch[threadIdx.x >> 6];
-  const int64_t tok = token_of_wave();
+  const int64_t tok = token_of_wave(a);
   if (tok >= a.B * a.L) return;
   const int lane = lane_id();
   const int64_t b = tok / a.L, t = tok % a.L;
@@ -1507,7 +1530,7 @@ __global__ __launch_bounds__(kWave * kWavesPerBlock) void k_cand_lists(Cand a, i
 
 // The wave's token, as wave-uniform scalars (so that no per-lane division or 64-bit index math follows from it).
 __device__ __forceinline__ TokAt sorted_token_of_wave(const Cand& a) {
-  const int64_t i = token_of_wave();
+  const int64_t i = token_of_wave(a);
   if (i >= a.B * a.L) return {0, 0, -1};
   const int64_t b = row_of(a, i), r = i - b * a.L;
   if (!ASRN_SORTED_MAP) return {b, r, i};
@@ -1580,6 +1603,21 @@ static int dispatch_rows(const Cand& a, hipStream_t st) {
     default: return Launcher<2, 4, RB>::run(a, st);
   }
 }
+// The row-wise XCD mapping (Cand::slice) for the whole-text kernels: when every batch row's gathered rows together
+// exceed half of the 256 MB last-level cache and a row splits into 8 equal slices. The environment variable
+// ASRN_ROWWISE=0 or 1 forces it off or on (read at each call; the results are the same bits either way, since every
+// wave computes its own token).
+static void set_mapping(Cand& a, int rows_bf16) {
+  const int64_t fb = rows_bf16 == 2 ? 2 : 4, vb = rows_bf16 >= 1 ? 2 : 4;
+  const int64_t bytes = a.B * a.L * ((a.P + a.cf) * fb + a.d * vb);
+  bool on = a.B > 1 && bytes > (int64_t(128) << 20);
+  if (const char* f = getenv("ASRN_ROWWISE")) {
+    if (f[0] == '0' && f[1] == 0) on = false;
+    if (f[0] == '1' && f[1] == 0) on = true;
+  }
+  a.slice = (on && a.L % kXcds == 0 && kWavesPerBlock == 1) ? a.L / kXcds : 0;
+}
+
 // rows_bf16: 0 fp32 rows; 1 V (and the backward's dO) bf16; 2 V, dO and the features bf16
 template <template <int, int, int> class Launcher>
 static int dispatch(const Cand& a, hipStream_t st, int rows_bf16 = 0) {
@@ -1645,6 +1683,7 @@ extern "C" int asrn_candidates_fwd(const float* phi, const float* V, const float
   a.lists = lists; a.rec = rec_layout(T, C).size;
   ASRN_REQUIRE(((uintptr_t)lists & 15) == 0, "asrn_candidates_fwd: lists must be 16-byte aligned");
   ASRN_REQUIRE(rows_bf16 >= 0 && rows_bf16 <= 2, "asrn_candidates_fwd: rows_bf16 must be 0, 1 or 2");
+  set_mapping(a, rows_bf16);
   return dispatch<LaunchFwd>(a, (hipStream_t)stream, rows_bf16);
 }
 
@@ -1672,6 +1711,7 @@ extern "C" int asrn_candidates_bwd(const float* phi, const float* V, const float
   a.dla = dlog_alfa; a.partials = partials;
   ASRN_REQUIRE(rows_bf16 >= 0 && rows_bf16 <= 2, "asrn_candidates_bwd: rows_bf16 must be 0, 1 or 2");
   ASRN_REQUIRE(((uintptr_t)dsalida & 15) == 0, "asrn_candidates_bwd: dsalida must be 16-byte aligned");
+  set_mapping(a, rows_bf16);
   return dispatch<LaunchBwd>(a, (hipStream_t)stream, rows_bf16);
 }
 

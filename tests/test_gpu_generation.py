@@ -83,7 +83,7 @@ def test_ring_build_vs_oracle(B, n, T, nb, C, V):
 
 @pytest.mark.parametrize('B,t0,steps,d,C,nb,T,V', [(2, 300, 24, 64, 32, 14, 8, 6), (3, 100, 40, 96, 4, 2, 4, 5),
                                                    (2, 1, 30, 256, 16, 4, 8, 4), (1, 500, 8, 1024, 8, 3, 8, 7),
-                                                   (16, 2000, 4, 768, 32, 14, 8, 50)])
+                                                   (16, 2000, 4, 768, 32, 14, 8, 50), (2, 200, 6, 64, 8, 14, 16, 6)])
 def test_decode_attend_vs_oracle(B, t0, steps, d, C, nb, T, V):
     say('decode attend', B, t0, steps, d, C, nb, T)
     L = t0 + steps

@@ -4,6 +4,7 @@ Bit-exact: bucket ids, sorted orders, candidate lists, suffix-match lengths, n-g
 and seen flags, integer streaks. Within the north-star tolerance (1e-3 relative at fp32): outputs and gradients of
 the candidate attention, the Hawkes and streak scans, the clock, and the whole layer. Each test prints the case it
 runs before touching the device."""
+import os
 import math
 
 import numpy as np
@@ -442,6 +443,27 @@ def test_candidates_cfg2_full_size():
     check_signals(sen, acc)
     for k in rg:
         assert_close(grads[k], rg[k], 'grad ' + k)
+
+
+@pytest.mark.parametrize('B,L,d', [(3, 1504, 256), (2, 808, 96), (1, 64, 64)])
+def test_candidates_rowwise_xcd_mapping_bit_identical(B, L, d):
+    """The row-wise XCD mapping (all XCDs on one batch row at a time, which the kernels take by themselves when the
+    rows outgrow the last-level cache, as at cfg3) forced on and off with ASRN_ROWWISE: the same bits, forward and
+    backward, since every wave computes its own token whatever order the waves take them in."""
+    say('candidates row-wise mapping', B, L, d)
+    sig, stage, w_suf, gamma, gs = random_stage(B, L, d, 40, seed=L + d)
+    sh = O.Shape(d=d)
+    runs = []
+    try:
+        for flag in ('1', '0'):
+            os.environ['ASRN_ROWWISE'] = flag
+            runs.append(run_candidates(stage, sig, w_suf, gamma, sh, gs))
+    finally:
+        os.environ.pop('ASRN_ROWWISE', None)
+    (s1, e1, g1), (s0, e0, g0) = runs
+    assert torch.equal(s1, s0) and torch.equal(e1, e0)
+    for k in g0:
+        assert torch.equal(g1[k], g0[k]), k
 
 
 @pytest.mark.parametrize('B,L,d,T,nb,C', [(2, 900, 96, 4, 6, 16), (2, 1500, 64, 8, 3, 32), (1, 1, 64, 8, 14, 32),
