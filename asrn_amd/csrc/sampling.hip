@@ -24,6 +24,9 @@
 //   the stop token (nucleo:2026-2028); then the token is written into the text and its n-grams into the sets
 //   (_Ngramas.agregar, nucleo:1872-1875).
 // Every reduction runs in a fixed order: the same inputs and seed give the same token.
+#include <climits>
+#include <cstdint>
+
 #include "common.h"
 
 namespace asrn {
@@ -164,6 +167,61 @@ __device__ __forceinline__ float block_max(float v, Red& r) {
 #pragma unroll
   for (int i = 1; i < kSampleWaves; ++i) s = fmaxf(s, r.f[i]);
   return s;
+}
+
+__device__ __forceinline__ uint32_t block_isum(uint32_t v, Red& r, unsigned int* slot) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  __syncthreads();
+  if (threadIdx.x == 0) *slot = 0u;
+  __syncthreads();
+  if (lane_id() == 0 && v != 0u) atomicAdd(slot, v);
+  __syncthreads();
+  return *slot;
+}
+
+// The top-p cut's ties, as the reference's rule gives them (_muestrear: the row sorted descending, a token kept while
+// the mass before it stays below top_p; ties in token order, a stable sort's): of the m tokens whose probability
+// equals the boundary value tau, the first K by token index stay, K = how many j = 0, 1, ... have acc + j m_tau <
+// target in the masses' fixed point (acc: the mass above tau, m_tau: tau's own mass), at least 1. Returns K, or 0 when
+// all m stay.
+__device__ __forceinline__ unsigned long long top_p_ties_kept(unsigned long long acc, double target, float tau,
+                                                              unsigned int m) {
+  const unsigned long long mt = (unsigned long long)rint((double)tau * kMassScale);
+  const unsigned long long tg = (unsigned long long)target;
+  if (mt == 0ull || m == 0u) return 0ull;
+  const unsigned long long need = tg > acc ? tg - acc : 0ull;
+  // K = ceil(need / mt) (both below 2^41: the quotient in double, then corrected to the exact ceiling)
+  unsigned long long K = (unsigned long long)ceil((double)need / (double)mt);
+  while (K > 0ull && (K - 1ull) * mt >= need) --K;
+  while (K * mt < need) ++K;
+  if (K == 0ull) K = 1ull;
+  return K >= (unsigned long long)m ? 0ull : K;
+}
+
+// the largest token index among the first K tied tokens: the least v with K ties at or below it, by bisection over
+// [0, V) with count_below(v) = the workgroup's count of tied tokens below index v (every thread calls this together)
+template <class F>
+__device__ int64_t top_p_tie_limit(unsigned long long K, int64_t V, F&& count_below) {
+  if (K == 0ull) return INT64_MAX;
+  int64_t lo = 0, hi = V - 1;
+  while (lo < hi) {
+    const int64_t mid = lo + (hi - lo) / 2;
+    if ((unsigned long long)count_below(mid + 1) >= K) hi = mid; else lo = mid + 1;
+  }
+  return lo;
+}
+
+// this thread's count of the row's tokens below index lim whose kept probability (x / T at or above the top-k cut,
+// softmax over the kept) equals tau; out of line, as only a top-p cut through tied tokens needs it
+__device__ __noinline__ uint32_t ties_below(const float* row, int64_t V, int64_t lim, float tden, float corte, float m3,
+                                            float S3, float tau) {
+  uint32_t c = 0u;
+  for (int64_t v = threadIdx.x; v < V && v < lim; v += kSampleThreads) {
+    const float l = row[v] / tden;
+    if (!(l < corte) && expf(l - m3) / S3 == tau) ++c;
+  }
+  return c;
 }
 
 // histogram adds aggregated over the wavefront: one LDS atomic per distinct bin among the valid lanes (every lane of
@@ -314,6 +372,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   __shared__ int ctok[kMaxCand];
   __shared__ float cval[kMaxCand];
   __shared__ int cscan[kSampleThreads];
+  __shared__ unsigned long long tie_acc;
+  __shared__ unsigned int tie_cnt;
+  int64_t tie_max = INT64_MAX;                // top-p: the largest token index kept at the boundary probability
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.x;
   const int64_t pos = *a.pos_dev;
@@ -599,10 +660,23 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
         __syncthreads();
       }
       if (found) tau = __uint_as_float(prefix);
+      const unsigned int m_tie = tau >= 0.f ? hist_n[sel[0]] : 0u;
+      if (m_tie > 1u) {                           // tied tokens at the boundary: the first K by token index stay
+        if (tid == 0) tie_acc = acc;
+        __syncthreads();
+        const unsigned long long above = tie_acc;
+        tie_max = top_p_tie_limit(top_p_ties_kept(above, target, tau, m_tie), V, [&](int64_t v) {
+          uint32_t c = 0u;
+          for (int i = tid; i < ncand; i += kSampleThreads)
+            c += (expf(cval[i] - m3) / S3 == tau && ctok[i] < v) ? 1u : 0u;
+          return block_isum(c, red, &tie_cnt);
+        });
+      }
     }
     auto keep_i = [&](int i, float* e) {
       *e = expf(cval[i] - m3);
-      return tau < 0.f || (*e / S3) >= tau;
+      const float p = *e / S3;
+      return tau < 0.f || p > tau || (p == tau && ctok[i] <= tie_max);
     };
     float s4 = 0.f;
     for (int i = tid; i < ncand; i += kSampleThreads) {
@@ -738,21 +812,31 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
         __syncthreads();
       }
       if (found) tau = __uint_as_float(prefix);
+      const unsigned int m_tie = tau >= 0.f ? hist_n[sel[0]] : 0u;
+      if (m_tie > 1u) {                           // tied tokens at the boundary: the first K by token index stay
+        if (tid == 0) tie_acc = acc;
+        __syncthreads();
+        const unsigned long long above = tie_acc;
+        tie_max = top_p_tie_limit(top_p_ties_kept(above, target, tau, m_tie), V, [&](int64_t lim) {
+          return block_isum(ties_below(src, V, lim, tden, corte, m3, S3, tau), red, &tie_cnt);
+        });
+      }
     }
 
     // final probabilities: softmax over what is kept, then the quote-mass correction
-    auto keep = [&](float x, float* e) {
+    auto keep = [&](int64_t v, float x, float* e) {
       const float l = x / tden;
       if (!kept_k(l)) return false;
       *e = expf(l - m3);
-      return tau < 0.f || (*e / S3) >= tau;
+      const float p = *e / S3;
+      return tau < 0.f || p > tau || (p == tau && v <= tie_max);
     };
     float S4;
     {
       float s = 0.f;
-      each(src, V, [&](int64_t, float x) {
+      each(src, V, [&](int64_t v, float x) {
         float e;
-        if (keep(x, &e)) s += e;
+        if (keep(v, x, &e)) s += e;
       });
       S4 = block_sum(s, red);
     }
@@ -762,9 +846,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
       if (qprobe) {
         each(src, V, [&](int64_t v, float x) {
           float ee;
-          if (in_quote(v) && keep(x, &ee)) c += ee / S4;
+          if (in_quote(v) && keep(v, x, &ee)) c += ee / S4;
         });
-      } else if (tid < nql && keep(src[qlist[tid]], &e)) {
+      } else if (tid < nql && keep(qlist[tid], src[qlist[tid]], &e)) {
         c = e / S4;
       }
       const float mass_q = block_sum(c, red);
@@ -776,7 +860,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     const bool scaled = sc_q != 1.f || sc_n != 1.f;
     auto prob = [&](int64_t v, float x) {
       float e;
-      if (!keep(x, &e)) return 0.f;
+      if (!keep(v, x, &e)) return 0.f;
       const float p = e / S4;
       return scaled ? p * (in_quote(v) ? sc_q : sc_n) : p;
     };
@@ -847,6 +931,31 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   }
 }
 
+// k_sample_reg's tied tokens at the top-p boundary (m > 1 of them; bit r of `ties`: this thread's token r 1024 + tid):
+// their ids into wtok (free at that point), and the K-th smallest is the last one kept (more than 1,024 tied tokens:
+// all of them stay). Out of line, so that the rare case costs the common one no registers.
+template <int R>
+__device__ __noinline__ int reg_tie_max(uint32_t ties, unsigned int m, unsigned long long above, double target,
+                                        float tau, int* wtok, unsigned int* cnt, unsigned long long* res) {
+  const int tid = threadIdx.x;
+  const unsigned long long K = top_p_ties_kept(above, target, tau, m);
+  if (K == 0ull || m > (unsigned int)kSampleThreads) return INT_MAX;
+  __syncthreads();
+  if (tid == 0) *cnt = 0u;
+  __syncthreads();
+  for (int r = 0; r < R; ++r)
+    if ((ties >> r) & 1u) wtok[atomicAdd(cnt, 1u) & (kSampleThreads - 1)] = r * kSampleThreads + tid;
+  __syncthreads();
+  if (tid < (int)m) {
+    const int me = wtok[tid];
+    unsigned int rank = 0u;
+    for (unsigned int j = 0; j < m; ++j) rank += wtok[j] < me ? 1u : 0u;
+    if (rank == (unsigned int)(K - 1ull)) *res = (unsigned long long)me;
+  }
+  __syncthreads();
+  return (int)*res;
+}
+
 // The same decision with the row held in registers: thread t owns tokens t, t + 1024, ..., t + (R - 1) * 1024, loaded
 // once, so every pass after the first is arithmetic on registers (the global-memory kernel above reads the row from
 // the cache in each pass, eight loads in flight per thread). Tokens the thread does not own are reached through LDS lists (window, bans, quotes). The
@@ -863,6 +972,8 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_reg(SampleArgs a) {
   __shared__ int qlist[kSucc], blist[kSucc];
   __shared__ int nq_list, nb_list;
   __shared__ int wtok[kSampleThreads];
+  __shared__ unsigned long long tie_acc;
+  __shared__ unsigned int tie_cnt;
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.x;
   const int64_t pos = *a.pos_dev;
@@ -1072,6 +1183,20 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_reg(SampleArgs a) {
 #pragma unroll
       for (int r = 0; r < R; ++r)
         if (x[r] != ninf && !(expf(x[r] - m3) / S3 >= tau)) x[r] = ninf;
+      const unsigned int m_tie = hist_n[sel[0]];
+      if (m_tie > 1u) {                           // tied tokens at the boundary: the first K by token index stay
+        if (tid == 0) tie_acc = acc;
+        __syncthreads();
+        const unsigned long long above = tie_acc;
+        uint32_t ties = 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (x[r] != ninf && expf(x[r] - m3) / S3 == tau) ties |= 1u << r;
+        const int tie_max = reg_tie_max<R>(ties, m_tie, above, target, tau, wtok, &tie_cnt, &tie_acc);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (((ties >> r) & 1u) && tok_of(r) > (int64_t)tie_max) x[r] = ninf;
+      }
     }
   }
 

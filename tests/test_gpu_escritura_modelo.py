@@ -244,6 +244,40 @@ def test_sampler_greedy_large_rows(caso):
             assert 0 < float(q[q > 0].min()) < float(q.max())        # the two groups carry different masses
 
 
+@pytest.mark.parametrize('V,k,p,ntie', [(300, 0, 0.6, 4), (10000, 0, 0.5, 9), (20000, 0, 0.62, 6), (30000, 3000, 0.55, 5),
+                                       (3000, 40, 0.8, 7)])
+def test_sampler_top_p_ties(V, k, p, ntie):
+    """A top-p cut through tied probabilities keeps the tied tokens in token order while the mass before each stays
+    below top_p, as the reference's sort-and-cumsum does (a stable sort's order of the ties), not every tie: rows with
+    one top token and ntie tied ones after it, on the register rows (V 300, 3,000 and 10,000), the whole-row passes
+    (V 20,000, no top-k) and the candidate list (V 30,000, top-k 3,000)."""
+    say('sampler top-p ties', V, k, p, ntie)
+    B, L0 = 2, 20
+    pos = 30
+    g = torch.Generator().manual_seed(V + ntie)
+    texto = torch.randint(0, V, (B, pos + 2), generator=g).to(DEV).contiguous()
+    lg = -8.0 + 0.01 * torch.randn(B, V, generator=g)
+    for b in range(B):
+        idx = torch.randperm(V, generator=g)[:ntie + 1]
+        lg[b, idx[0]] = 2.4                                   # the top token
+        lg[b, idx[1:]] = 2.0                                  # the tied group the cut goes through
+    lg = lg.to(DEV)
+    est = _Estado(B, V, pos + 2)
+    pdev = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    ops.muestrear(lg, texto, pdev, pos + 1, L0, est.piezas, est.terminado, est.paso_fin, est.trabajo, est.bits, 1.0, k, p,
+                  1.0, 64, 5, prob=est.prob)
+    torch.cuda.synchronize()
+    prob = est.prob.cpu().double()
+    for b in range(B):
+        q = M.probabilidades(lg[b].cpu().double(), 1.0, k, p, None)
+        tied = torch.nonzero(lg[b].cpu() == 2.0).view(-1)
+        assert 0 < int((q[tied] > 0).sum()) < ntie, 'the cut must go through the tied group'
+        assert set(torch.nonzero(prob[b] > 0).view(-1).tolist()) == set(torch.nonzero(q > 0).view(-1).tolist()), b
+        assert torch.allclose(prob[b], q, rtol=1e-4, atol=2e-6), (b, (prob[b] - q).abs().max())
+        tok = int(est.piezas[b])
+        assert q[tok] > 0
+
+
 def test_sampler_distribution_and_seed():
     say('sampler chi-square')
     B, V = 512, 12
