@@ -51,7 +51,7 @@ SIGNATURES = {
                          + [_I64, _P]),
     'asrn_hidden_fwd': (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I64, _I32, _I32, _P, _P]),
     'asrn_hidden_bwd': (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I64, _I32, _I32, _P, _P, _I64, _P]),
-    'asrn_hash_fwd': (ctypes.c_int, [_P, _I64] + [_P] * 6 + [_I64, _I64] + [_I32] * 4 + [_P, _P]),
+    'asrn_hash_fwd': (ctypes.c_int, [_P, _I64] + [_P] * 6 + [_I64, _I64] + [_I32] * 4 + [_P, _P, _I32, _I32, _P]),
     'asrn_hash_bwd_workspace': (_I64, [_I64, _I64] + [_I32] * 4),
     'asrn_hash_bwd': (ctypes.c_int, [_P, _I64] + [_P] * 4 + [_I64, _I64] + [_I32] * 4 + [_P, _P, _I64, _P, _P, _I64, _P]),
     'asrn_column_sums_workspace': (_I64, [_I64, _I64]),

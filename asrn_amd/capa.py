@@ -147,7 +147,13 @@ class CapaASRNEstable(nn.Module):
         return dict(zip(('W', 'Wq', 'W2', 'b2'), out))
 
     def _phi_y_valores(self, E, pesos=None):
-        """phi (B, L, P) and the rows the candidate kernels gather for the values (asrn/nucleo.py:644-659).
+        """phi (B, L, P) and the rows the candidate kernels gather for the values (see _phi_filas)."""
+        phi, filas, _ = self._phi_filas(E, pesos)
+        return phi, filas
+
+    def _phi_filas(self, E, pesos=None, ids=False):
+        """phi (B, L, P), the rows the candidate kernels gather for the values (asrn/nucleo.py:644-659) and, with ids
+        and the fused fp32 producer, the bucket ids of phi (B*T, L) its kernel wrote with it (else None).
 
         The reference's values are V[s] = W_v E[s+1] and the layer adds W_o (sum over tables of att V). Both maps are
         linear, so the kernels gather E[s+1] itself (read in place, shifted) and the layer applies W_o W_v once to the
@@ -162,8 +168,10 @@ class CapaASRNEstable(nn.Module):
         W = (torch.cat([pal[0].weight, ctx[0].weight.view(mc, 2, d).transpose(0, 1).reshape(2 * mc, d)])
              if pesos is None else pesos['W'])
         if self._hash_fusionado(E):
-            return ops.HashProducer.apply(E, W, pal[0].bias, ctx[0].bias, pal[2].weight, pal[2].bias, ctx[2].weight,
-                                          ctx[2].bias, m, mc)
+            phi, filas, idv = ops.HashProducer.apply(E, W, pal[0].bias, ctx[0].bias, pal[2].weight, pal[2].bias,
+                                                     ctx[2].weight, ctx[2].bias, m, mc,
+                                                     self.n_tablas if ids else 0, self.n_bits)
+            return phi, filas, (idv if idv.numel() else None)
         if pesos is None or 'W2' not in pesos:
             W2 = torch.block_diag(pal[2].weight, ctx[2].weight)    # both second layers as one GEMM: phi comes whole
             b2 = torch.cat([pal[2].bias, ctx[2].bias])
@@ -188,7 +196,7 @@ class CapaASRNEstable(nn.Module):
             g = F.gelu(torch.cat([hp, _ShiftAdd.apply(za, zb, ctx[0].bias)], dim=-1))
             filas = E
         phi = lineal(g, W2, b2)
-        return phi, filas
+        return phi, filas, None
 
     def _contexto(self, h, con_h=False, pesos=None):
         """Qc, Kc (B, L, cf), beta (B, L) fp64 and log_alfa (B, L) (asrn/estable.py:153-194 with the GPU branch's clock
@@ -253,11 +261,11 @@ class CapaASRNEstable(nn.Module):
     def _cubetas(self, E, partes=None, pesos=None):
         """The hash producers and the bucket sort (asrn/estable.py:204-236): phi, the rows the values gather, and the
         sorted order, windows and ranks of every table."""
-        phi, filas = self._phi_y_valores(E, pesos)
+        phi, filas, ids = self._phi_filas(E, pesos, ids=True)
         if partes is not None:                                              # the generation step's value cache
             v = F.linear(_a_autocast(E), self.v.weight)
             partes.update(phi=phi, V=F.pad(v, (0, 0, 0, 1))[:, 1:])         # V[t] = W_v E[t+1], 0 at the end
-        _, order, _, rank, win = ops.bucket_sort(phi.detach(), self.n_tablas, self.n_bits, self.chunk)
+        _, order, _, rank, win = ops.bucket_sort(phi.detach(), self.n_tablas, self.n_bits, self.chunk, ids=ids)
         return phi, filas, order, win, rank
 
     def _acumular(self, E, Qc, Kc, Bt, log_alfa, sig, partes=None, pesos=None, esperar=None, cubetas=None):

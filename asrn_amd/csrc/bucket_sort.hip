@@ -2,7 +2,8 @@
 //
 //   k_bucket_rows<R>  one workgroup of 1024 threads per tile of up to 1024 R positions of a row: the sign hash of its
 //                     positions (their phi columns of table tau, read 4 rows x 16 columns per load instruction and
-//                     turned into ids by ballots), then a stable LSD radix sort of the ids in LDS, 7 bits per pass:
+//                     turned into ids by ballots; with no phi, the ids the fused hash producer already wrote), then a
+//                     stable LSD radix sort of the ids in LDS, 7 bits per pass:
 //                     each wave owns 64 R consecutive positions, ranks equal digits among its lanes by ballots and
 //                     across its R rounds by a per-wave count in LDS, and one exclusive scan of the (digit, wave)
 //                     counts places every group, so ties keep text order and the result equals
@@ -175,7 +176,14 @@ __global__ __launch_bounds__(kThreads) void k_bucket_rows(const float* __restric
   // sign hash: load u of a batch starting at e0 reads position e0 + 4 u + (lane >> 4), column lane & 15; its ballot
   // holds the ids of 4 positions, one per 16-lane group; lane l keeps load l >> 2's group l & 3
   uint32_t k[R];
-  {
+  if (!phi) {                                      // the hash producer wrote the ids: read them
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      const int e = seg + 64 * q + lane;
+      const uint32_t id = e < n ? (uint32_t)ids[r * L + t0 + e] : 0u;
+      k[q] = ((e < n ? id : (1u << nb) - 1u) << kPosBits) | (uint32_t)e;
+    }
+  } else {
     const float* base = phi + (b * L + t0) * stride + tau * nb;
     const int g = lane >> 4, c = lane & 15;
     // every load of a batch in flight at once: unconditional loads from clamped addresses (a load under a branch is
@@ -466,7 +474,7 @@ extern "C" int asrn_bucket_sort(const float* phi, int64_t B, int64_t L, int32_t 
                (long long)phi_stride, T * nb);
   ASRN_REQUIRE(C >= 1 && C <= 255, "asrn_bucket_sort: window C=%d must be in [1, 255]", C);
   if (B == 0 || L == 0) return 0;
-  ASRN_REQUIRE(phi && ids && order && ids_sorted && rank && win, "asrn_bucket_sort: null pointer");
+  ASRN_REQUIRE(ids && order && ids_sorted && rank && win, "asrn_bucket_sort: null pointer");
   const int64_t need = asrn_bucket_sort_workspace(B, L, T);
   ASRN_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
                "asrn_bucket_sort: workspace %lld bytes < %lld needed", (long long)workspace_bytes, (long long)need);

@@ -35,6 +35,7 @@ struct PhiArgs {
   float* part;                         // per workgroup: [dW2w | dW2c | db2w | db2c | db_word | db_ctx]
   int64_t B, L;
   int m, mc, Pw, Pc;
+  int32_t* ids; int T, nb;             // forward, optional: the bucket ids (B T, L) of the T tables of nb columns
 };
 
 __device__ __forceinline__ float gelu_e(float x) { return 0.5f * x * (1.f + erff(x * 0.70710678118654752f)); }
@@ -131,6 +132,7 @@ __global__ __launch_bounds__(kFwdThreads) void k_phi_fwd(PhiArgs a) {
   __shared__ __align__(16) float gs[kFwdTok * kGldF];
   __shared__ float wsw[kPhiMax * kWldF];
   __shared__ float wsc[kPhiMax * kWldF];
+  __shared__ unsigned long long smask[2][kFwdTok];  // with a.ids: each token's positive columns of each MLP
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t N = a.B * a.L, t0 = (int64_t)blockIdx.x * kFwdTok;
   const int h = a.m + a.mc, h4 = h / 4, P = a.Pw + a.Pc;
@@ -200,6 +202,42 @@ __global__ __launch_bounds__(kFwdThreads) void k_phi_fwd(PhiArgs a) {
     for (int q = 0; q < 4; ++q) {
       const int64_t row = t0 + tb * 16 + k4 * 4 + q;
       if (row < N && cw < pn) a.phi[row * P + (part ? a.Pw : 0) + cw] = acc[nt][q] + bias[nt];
+    }
+  }
+  if (a.ids) {
+    // the sign hash (strict > 0, nucleo:661-664) of the values just stored, so that the bucket sort reads T ids per
+    // token instead of its phi row: ballot (nt, q) holds token k4 4 + q's columns nt 16 + r16 in lanes 16 k4 + r16
+    unsigned long long mine[4] = {0ull, 0ull, 0ull, 0ull};
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const unsigned long long bal = __ballot(nt * 16 + r16 < pn && acc[nt][q] + bias[nt] > 0.f);
+        mine[q] |= ((bal >> (16 * k4)) & 0xFFFFull) << (16 * nt);
+      }
+    if (r16 == 0) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) smask[part][tb * 16 + k4 * 4 + q] = mine[q];
+    }
+    __syncthreads();
+    // table tau's id: bits j of columns tau nb + j of the row [word | context]; one (token, table) per thread, the
+    // tokens of a table consecutive (coalesced stores)
+    for (int e = tid; e < kFwdTok * a.T; e += kFwdThreads) {
+      const int tk = e % kFwdTok, tau = e / kFwdTok;
+      const int64_t row = t0 + tk;
+      if (row >= N) continue;
+      // the row's P = Pw + Pc sign bits as 128: lo holds columns 0-63, hi 64-127 (Pw <= 64)
+      const unsigned long long w = smask[0][tk], c = smask[1][tk];
+      const unsigned long long lo = a.Pw < 64 ? w | (c << a.Pw) : w;
+      const unsigned long long hi = a.Pw == 0 ? c : (a.Pw < 64 ? c >> (64 - a.Pw) : c);
+      const int c0 = tau * a.nb;
+      unsigned long long bits;
+      if (c0 >= 64) bits = hi >> (c0 - 64);
+      else if (c0 == 0) bits = lo;
+      else bits = (lo >> c0) | (hi << (64 - c0));
+      const uint32_t id = (uint32_t)(bits & ((1ull << a.nb) - 1ull));
+      const int64_t b = row / a.L, l = row - b * a.L;
+      a.ids[(b * a.T + tau) * a.L + l] = (int32_t)id;
     }
   }
 }
@@ -421,11 +459,15 @@ using namespace asrn;
 extern "C" int asrn_hash_fwd(const float* y, int64_t ldy, const float* b_word, const float* b_ctx,
                              const float* w2_word, const float* b2_word, const float* w2_ctx, const float* b2_ctx,
                              int64_t B, int64_t L, int32_t m, int32_t mc, int32_t p_word, int32_t p_ctx, float* phi,
-                             void* stream) {
+                             int32_t* ids, int32_t T, int32_t nb, void* stream) {
   PhiArgs a = {};
   a.y = y; a.ldy = ldy; a.bp = b_word; a.bc = b_ctx; a.Ww = w2_word; a.bw = b2_word; a.Wc = w2_ctx; a.bc2 = b2_ctx;
   a.phi = phi; a.B = B; a.L = L; a.m = m; a.mc = mc; a.Pw = p_word; a.Pc = p_ctx;
+  a.ids = ids; a.T = T; a.nb = nb;
   if (phi_check(a, "asrn_hash_fwd")) return 1;
+  ASRN_REQUIRE(!ids || (T >= 1 && T <= 32 && nb >= 1 && nb <= 14 && T * nb == p_word + p_ctx),
+               "asrn_hash_fwd: bucket ids need T in [1, 32], nb in [1, 14] and T * nb = p_word + p_ctx (T=%d nb=%d, "
+               "%d columns)", T, nb, p_word + p_ctx);
   const int64_t n = B * L;
   if (n == 0) return 0;
   hipLaunchKernelGGL(k_phi_fwd, dim3((unsigned)((n + kFwdTok - 1) / kFwdTok)), dim3(kFwdThreads), 0,

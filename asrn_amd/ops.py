@@ -49,13 +49,19 @@ def _pad4(t):
 # a1 + a2
 # ---------------------------------------------------------------------------------------------------------------------
 
-def bucket_sort(phi, T, nb, C):
+def bucket_sort(phi, T, nb, C, ids=None):
     """phi (B, L, P) fp32 -> ids (B*T, L), order (B*T, L), ids_sorted (B*T, L), rank (B, L, T) and the recent-mates
-    index win (B, L, T) = min(C, mates before) | min(C, mates after) << 8, all int32."""
+    index win (B, L, T) = min(C, mates before) | min(C, mates after) << 8, all int32. ids: the bucket ids the fused
+    hash producer already wrote (HashProducer with T, nb): the sort reads them instead of hashing phi again."""
     dev = _dev(phi)
-    phi = _c(phi, torch.float32)
     B, L, P = phi.shape
-    ids = torch.empty((B * T, L), dtype=I32, device=dev)
+    if ids is not None:
+        if ids.dtype != I32 or tuple(ids.shape) != (B * T, L) or not ids.is_contiguous() or ids.device != dev:
+            raise ValueError('bucket_sort: ids must be a contiguous (B*T, L) int32 tensor on the device of phi')
+        phi = None
+    else:
+        phi = _c(phi, torch.float32)
+        ids = torch.empty((B * T, L), dtype=I32, device=dev)
     # every entry of order, ids_sorted, rank and win is written by the sort (no fill); the candidate kernels clamp
     # the positions they read from order
     buf = torch.empty((4, B * T * L), dtype=I32, device=dev)
@@ -63,8 +69,8 @@ def bucket_sort(phi, T, nb, C):
     rank, win = buf[2].view(B, L, T), buf[3].view(B, L, T)
     wsb = query('asrn_bucket_sort_workspace', B, L, T)
     ws = torch.empty((wsb,), dtype=torch.uint8, device=dev) if wsb else None
-    call('asrn_bucket_sort', ptr(phi), B, L, T, nb, P, C, ptr(ids), ptr(order), ptr(ids_s), ptr(rank), ptr(win),
-         ptr(ws), wsb, stream_of(dev))
+    call('asrn_bucket_sort', ptr(phi) if phi is not None else None, B, L, T, nb, P, C, ptr(ids), ptr(order),
+         ptr(ids_s), ptr(rank), ptr(win), ptr(ws), wsb, stream_of(dev))
     return ids, order, ids_s, rank, win
 
 
@@ -289,10 +295,12 @@ class HashProducer(torch.autograd.Function):
     (W's rows [W_p (m) | W_a (mc) | W_b (mc)]), then the hidden layer and both second layers in asrn_hash_fwd (the
     second layers on the matrix cores as the two diagonal blocks they are). Also returns E itself (fp32, an alias) as
     the rows the candidate kernels gather. Backward: asrn_hash_bwd writes dy and every second-layer and bias gradient;
-    dE = dE_rows + dy W in one GEMM with beta = 1; dW by token slabs. fp32 only."""
+    dE = dE_rows + dy W in one GEMM with beta = 1; dW by token slabs. fp32 only. With T > 0 (and T nb = Pw + Pc) the
+    kernel also writes the bucket ids (B*T, L) of the phi it stores, returned third (empty otherwise), for
+    bucket_sort(..., ids=)."""
 
     @staticmethod
-    def forward(ctx, E, W, b_word, b_ctx, W2w, b2w, W2c, b2c, m, mc):
+    def forward(ctx, E, W, b_word, b_ctx, W2w, b2w, W2c, b2c, m, mc, T=0, nb=0):
         dev = _dev(E, W)
         B, L, d = E.shape
         n = W.shape[0]
@@ -308,14 +316,18 @@ class HashProducer(torch.autograd.Function):
         else:
             y = torch.nn.functional.linear(E, W)
         phi = torch.empty((B, L, Pw + Pc), dtype=torch.float32, device=dev)
-        call('asrn_hash_fwd', ptr(y), n, *[ptr(t) for t in ps], B, L, m, mc, Pw, Pc, ptr(phi), stream_of(dev))
+        con_ids = T > 0 and T * nb == Pw + Pc
+        ids = torch.empty((B * T, L) if con_ids else (0,), dtype=I32, device=dev)
+        call('asrn_hash_fwd', ptr(y), n, *[ptr(t) for t in ps], B, L, m, mc, Pw, Pc, ptr(phi),
+             ptr(ids) if con_ids else None, T if con_ids else 0, nb if con_ids else 0, stream_of(dev))
         ctx.save_for_backward(E, W, y, ps[0], ps[1], ps[2], ps[4])
         ctx.meta = (m, mc, Pw, Pc)
         ctx.set_materialize_grads(False)
-        return phi, E.view_as(E)
+        ctx.mark_non_differentiable(ids)
+        return phi, E.view_as(E), ids
 
     @staticmethod
-    def backward(ctx, dphi, drows):
+    def backward(ctx, dphi, drows, dids):
         E, W, y, bw, bc, W2w, W2c = ctx.saved_tensors
         m, mc, Pw, Pc = ctx.meta
         B, L, n = y.shape
@@ -341,7 +353,7 @@ class HashProducer(torch.autograd.Function):
                 dE = _c(drows, torch.float32) if drows.dtype != torch.float32 or not drows.is_contiguous() else drows
                 dE.view(B * L, d).addmm_(dy2, W)
         dW = weight_grad(dy2, E.view(B * L, d)) if ctx.needs_input_grad[1] else None
-        return (dE, dW, dbw, dbc, dW2w.view(Pw, m), db2w, dW2c.view(Pc, mc), db2c, None, None)
+        return (dE, dW, dbw, dbc, dW2w.view(Pw, m), db2w, dW2c.view(Pc, mc), db2c, None, None, None, None)
 
 
 # products of more multiply-adds than this go to the library GEMM: the one-tile-per-workgroup kernel wins only while

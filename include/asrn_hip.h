@@ -29,8 +29,9 @@ int32_t asrn_hip_abi_version(void);
 /* ---- a1 + a2: sign hash and stable bucket sort ------------------------------------------------------------------
  * Replaces CapaASRN._ids (asrn/nucleo.py:661-664), `ids.argsort(dim=-1, stable=True)` and `torch.gather(ids, 1,
  * orden)` (asrn/estable.py:282-283, 288-291).
- *   phi        (B, L, phi_stride) fp32; table tau reads columns [tau*nb, tau*nb + nb)
- *   ids        (B*T, L) int32 out: bucket id of each position, text order
+ *   phi        (B, L, phi_stride) fp32; table tau reads columns [tau*nb, tau*nb + nb); or null, and then ids is
+ *              an input: the bucket ids asrn_hash_fwd wrote with its phi (the sign hash already done)
+ *   ids        (B*T, L) int32 out (in when phi is null): bucket id of each position, text order
  *   order      (B*T, L) int32 out: sorted rank -> text position (stable: ties keep text order)
  *   ids_sorted (B*T, L) int32 out: ids[order]
  *   rank       (B, L, T) int32 out: text position -> sorted rank, per table
@@ -174,10 +175,14 @@ int asrn_hidden_bwd(const float* y, int64_t ldy, const float* b_word, const floa
  * dparams = [dW2w (Pw*m) | dW2c (Pc*mc) | db2w (Pw) | db2c (Pc) | db_word (m) | db_ctx (mc)], summed over the tokens
  * in a fixed order. The second layers run on the matrix cores. m, mc multiples of 4 in [4, 64] with (m + mc) / 4
  * dividing 256; Pw, Pc in [1, 64]; y, dy rows and the first-layer biases 16-byte aligned.
+ * hash_fwd with ids non-null also writes the sign hash of the phi it stores (CapaASRN._ids, asrn/nucleo.py:661-664):
+ * ids (B*T, L) int32, table tau's id from the signs (strict > 0) of columns [tau*nb, tau*nb + nb), for
+ * asrn_bucket_sort with a null phi; T*nb = Pw + Pc, 1 <= T <= 32, 1 <= nb <= 14.
  * workspace: asrn_hash_bwd_workspace(...) bytes, 256-byte aligned. */
 int asrn_hash_fwd(const float* y, int64_t ldy, const float* b_word, const float* b_ctx, const float* w2_word,
                   const float* b2_word, const float* w2_ctx, const float* b2_ctx, int64_t B, int64_t L, int32_t m,
-                  int32_t mc, int32_t p_word, int32_t p_ctx, float* phi, void* stream);
+                  int32_t mc, int32_t p_word, int32_t p_ctx, float* phi, int32_t* ids, int32_t T, int32_t nb,
+                  void* stream);
 int64_t asrn_hash_bwd_workspace(int64_t B, int64_t L, int32_t m, int32_t mc, int32_t p_word, int32_t p_ctx);
 int asrn_hash_bwd(const float* y, int64_t ldy, const float* b_word, const float* b_ctx, const float* w2_word,
                   const float* w2_ctx, int64_t B, int64_t L, int32_t m, int32_t mc, int32_t p_word, int32_t p_ctx,

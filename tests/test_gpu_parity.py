@@ -648,6 +648,33 @@ def test_hash_producer_vs_oracle(B, L, d, kw, rows_grad):
         assert_close(named[k].grad, leaves[k].grad, 'grad ' + k)
 
 
+@pytest.mark.parametrize('B,L,T,nb,m,mc', [(2, 1500, 8, 14, 64, 64), (3, 700, 5, 14, 32, 32), (1, 65, 3, 6, 8, 8),
+                                           (1, 5000, 8, 14, 64, 64)])
+def test_hash_producer_bucket_ids(B, L, T, nb, m, mc):
+    """The bucket ids the fused hash kernel writes with phi equal the sign hash the bucket sort takes of that phi,
+    bit for bit, and the sort fed those ids gives the same order, ranks and windows: tables inside either MLP's
+    columns, a table across the word/context boundary (T 5, nb 14: columns 28-41 around 35), a few tokens (the small
+    GEMM), and rows that take the sort's one-launch (700), chunked (1,500) and merge (5,000) paths."""
+    say('hash producer bucket ids', B, L, T, nb, m, mc)
+    d, C = 64, 32
+    P = T * nb
+    Pw, Pc = P // 2, P - P // 2
+    g = torch.Generator().manual_seed(L + T)
+    r = lambda *s: torch.randn(*s, generator=g).to(DEV)
+    E = r(B, L, d)
+    args = (r(m + 2 * mc, d) * 0.2, r(m) * 0.1, r(mc) * 0.1, r(Pw, m) * 0.3, r(Pw) * 0.1, r(Pc, mc) * 0.3,
+            r(Pc) * 0.1)
+    with torch.no_grad():
+        phi, _, ids = ops.HashProducer.apply(E, *args, m, mc, T, nb)
+        ref = ops.bucket_sort(phi, T, nb, C)
+        got = ops.bucket_sort(phi, T, nb, C, ids=ids.clone())
+    assert torch.equal(ids, ref[0])
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+    pos = (phi > 0).float().mean().item()
+    assert 0.2 < pos < 0.8                                   # both signs occur
+
+
 # ---------------------------------------------------------------------------------------------------------------------
 # a0: the context producer
 # ---------------------------------------------------------------------------------------------------------------------

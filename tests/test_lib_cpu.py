@@ -114,16 +114,19 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert lib.asrn_hidden_bwd(N, 100, N, N, 2, 16, 64, 64, N, N, 448, N) != 0
     assert 'row stride' in _err(lib)
     # fused hash MLPs: hidden widths, the first layers' row stride, the backward's workspace
-    assert lib.asrn_hash_fwd(N, 192, *([N] * 6), 2, 16, 6, 64, 56, 56, N, N) != 0
+    assert lib.asrn_hash_fwd(N, 192, *([N] * 6), 2, 16, 6, 64, 56, 56, N, N, 0, 0, N) != 0
     assert 'm=6' in _err(lib)
-    assert lib.asrn_hash_fwd(N, 192, *([N] * 6), 2, 16, 64, 64, 56, 65, N, N) != 0
+    assert lib.asrn_hash_fwd(N, 192, *([N] * 6), 2, 16, 64, 64, 56, 65, N, N, 0, 0, N) != 0
     assert 'Pc=65' in _err(lib)
-    assert lib.asrn_hash_fwd(N, 100, *([N] * 6), 2, 16, 64, 64, 56, 56, N, N) != 0
+    assert lib.asrn_hash_fwd(N, 100, *([N] * 6), 2, 16, 64, 64, 56, 56, N, N, 0, 0, N) != 0
     assert 'row stride' in _err(lib)
     assert lib.asrn_hash_bwd_workspace(8, 4096, 64, 64, 56, 56) >= 128 * (56 * 64 * 2 + 56 * 2 + 128) * 4
     assert lib.asrn_hash_bwd(N, 192, N, N, N, N, 8, 4096, 64, 64, 56, 56, N, N, 192, N, N, 0, N) != 0
     assert 'workspace' in _err(lib)
-    assert lib.asrn_hash_fwd(N, 192, *([N] * 6), 0, 16, 64, 64, 56, 56, N, N) == 0      # no tokens: no launch
+    assert lib.asrn_hash_fwd(N, 192, *([N] * 6), 0, 16, 64, 64, 56, 56, N, N, 0, 0, N) == 0      # no tokens: no launch
+    # bucket ids from the hash kernel: T * nb must cover phi's columns exactly
+    assert lib.asrn_hash_fwd(N, 192, *([N] * 6), 2, 16, 64, 64, 56, 56, N, 16, 8, 13, N) != 0
+    assert 'bucket ids' in _err(lib)
     # column sums: a stride below the width; long columns need the slab workspace, short ones none
     assert lib.asrn_column_sums(N, 0, 16, 13, 12, N, N, 0, N) != 0
     assert 'bad sizes' in _err(lib)
