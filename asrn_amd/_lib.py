@@ -59,6 +59,7 @@ SIGNATURES = {
     'asrn_small_gemm': (ctypes.c_int, [_P, _I64, _I32, _P, _I64, _I32, _P, _I64, _I32, _I32, _I32, _P]),
     'asrn_copy_blocks': (ctypes.c_int, [_I32] + [_P] * 7),
     'asrn_gate_fwd': (ctypes.c_int, [_P, _P, _I32] + [_P] * 11 + [_I64] + [_I32] * 5 + [_F32] * 3 + [_P] * 3),
+    'asrn_gate_step': (ctypes.c_int, [_P] * 14 + [_I64] + [_I32] * 5 + [_F32] * 3 + [_P] * 3),
     'asrn_gate_bwd_workspace': (_I64, [_I64, _I32]),
     'asrn_gate_bwd': (ctypes.c_int, [_P, _P, _I32] + [_P] * 11 + [_I64] + [_I32] * 5 + [_F32] * 3 + [_P] * 8
                       + [_I64, _P]),

@@ -322,6 +322,20 @@ class CapaASRNEstable(nn.Module):
                                self.g.bias, self.g_conf.weight, self.g_conf.bias, self.w_vistos, self.u_hawkes,
                                self.d_racha, meta)
 
+    def _combinar_paso(self, salida, h, sen, vistos, hawkes, racha):
+        """The generation step's _combinar for B tokens, h and salida (B, d): W_o and the gate in one kernel
+        (ops.gate_step), or None where that does not apply (16-bit or wide layers, autograd, an active dropout), and
+        then _combinar runs."""
+        if (torch.is_grad_enabled() or h.dtype != torch.float32 or salida.dtype != torch.float32
+                or torch.is_autocast_enabled(h.device.type) or h.shape[-1] > ANCHO_FUSIONADO or h.shape[-1] % 4
+                or (self.drop.training and self.drop.p > 0) or self.o.weight.dtype != torch.float32):
+            return None
+        p = self.protecciones
+        meta = (self.n_tablas, self.tablas_contexto, self.racha_paso,
+                -1.0 if p.mejor_max is None else float(p.mejor_max), 0.0 if p.tope_puerta is None else float(p.tope_puerta))
+        return ops.gate_step(h, salida, self.o.weight, sen, vistos, hawkes, racha, self.g.weight, self.g.bias,
+                             self.g_conf.weight, self.g_conf.bias, self.w_vistos, self.u_hawkes, self.d_racha, meta)
+
     def _compuerta_ancha(self, h, aporte, acc):
         """The gate for widths past the fused gate kernels (d > 1024), as PyTorch ops on the GPU with the same math
         (asrn/estable.py:376-403, asrn/nucleo.py:865-878; the division by the table count after W_o, per token):

@@ -304,6 +304,103 @@ __global__ __launch_bounds__(kGateThreads) void k_gate_bwd(GateArgs a) {
   }
 }
 
+// The generation step's W_o and gate in one launch (fp32, a few tokens): workgroup (nt, rt) owns output columns
+// [16 nt, 16 nt + 16) of tokens [16 rt, 16 rt + 16). It forms the 16 x 16 tile of A = salida W_o^T on the matrix cores
+// (v_mfma_f32_16x16x4f32) over the whole depth, each wave a quarter of it with all its loads in one round, and every
+// token's logit (h . w_g as the fused gate forms it, and the small part from one thread per token), so that
+// h' = h + sigmoid(cap(logit)) r A leaves for the tile's columns: the library GEMM and its A round trip through HBM
+// are gone, and 48 workgroups (d = 768) share what was one workgroup's gate.
+constexpr int kStepTok = 16;
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4v ld4_rows(const float* m, int64_t row, int64_t nrows, int64_t ld, int k, int kend) {
+  f4v v = {0.f, 0.f, 0.f, 0.f};
+  if (row >= nrows) return v;
+  const float* p = m + row * ld + k;
+  if (k + 4 <= kend) return *(const f4v*)p;
+  if (k + 0 < kend) v.x = p[0];
+  if (k + 1 < kend) v.y = p[1];
+  if (k + 2 < kend) v.z = p[2];
+  if (k + 3 < kend) v.w = p[3];
+  return v;
+}
+
+template <int D4, int U>
+__global__ __launch_bounds__(kGateThreads) void k_gate_step(GateArgs a, const float* __restrict__ salida,
+                                                            const float* __restrict__ wo) {
+  __shared__ float tile[kGateWaves][kStepTok * kStepTok];
+  __shared__ float feat[kStepTok][kFeatStride];
+  __shared__ TokenInfo info[kStepTok];
+  __shared__ float P[kGateCols];
+  __shared__ float vh[2][kStepTok * kGateMaxN];
+  __shared__ float hdot[kStepTok];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int d = a.d, d4 = d >> 2;
+  const int n0 = blockIdx.x * kStepTok;
+  const int64_t t0 = (int64_t)blockIdx.y * kStepTok;
+  const int nt = a.BL - t0 < kStepTok ? (int)(a.BL - t0) : kStepTok;
+  // the small parameters and the tile's seen and Hawkes rows
+  stage_small_params(a, P);
+  for (int i = tid; i < nt * a.n; i += kGateThreads) {
+    vh[0][i] = a.vistos[t0 * a.n + i];
+    vh[1][i] = a.hawkes[t0 * a.n + i];
+  }
+  // A's tile: wave w sums depth [w per, (w + 1) per) in one round of U steps of 16 columns
+  const int per = ((d + kGateWaves - 1) / kGateWaves + 15) & ~15;
+  const int wb = wave * per, we = wb + per < d ? wb + per : d;
+  const int i16 = lane & 15, q4 = lane >> 4;
+  f4v acc = {0.f, 0.f, 0.f, 0.f};
+  for (int k = wb; k < we; k += 16 * U) {
+    f4v x[U], w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = k + 16 * u + 4 * q4;
+      x[u] = ld4_rows(salida, t0 + i16, a.BL, d, kk, we);
+      w[u] = ld4_rows(wo, n0 + i16, d, d, kk, we);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].x, w[u].x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].y, w[u].y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].z, w[u].z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].w, w[u].w, acc, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) tile[wave][(4 * q4 + q) * kStepTok + i16] = acc[q];   // rows 4 (l / 16) + q, col l % 16
+  // h . w_g per token, as the fused gate forms it (float4 lanes, then the wave sum): wave w takes tokens w + 4 j
+  for (int j = 0; j < kStepTok / kGateWaves; ++j) {
+    const int tl = wave + kGateWaves * j;
+    const int64_t t = t0 + tl;
+    float dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < D4; ++k) {
+      const int q = lane + kWave * k;
+      if (tl < nt && q < d4) {
+        const float4 hv = ((const float4*)(a.h + t * d))[q];
+        const float4 w = ((const float4*)a.wg)[q];
+        dot += hv.x * w.x + hv.y * w.y + hv.z * w.z + hv.w * w.w;
+      }
+    }
+    dot = wave_sum_u(dot);
+    if (lane == 0) hdot[tl] = dot;
+  }
+  __syncthreads();
+  if (tid < nt) token_features(a, t0 + tid, P, vh[0] + tid * a.n, vh[1] + tid * a.n, feat[tid], &info[tid]);
+  __syncthreads();
+  const int tl = tid / kStepTok, c = tid % kStepTok;
+  const int64_t t = t0 + tl;
+  const int col = n0 + c;
+  if (tl < nt && col < d) {
+    const int e = tl * kStepTok + c;
+    const float A = ((tile[0][e] + tile[1][e]) + tile[2][e]) + tile[3][e];
+    const float logit = hdot[tl] + info[tl].small;
+    if (blockIdx.x == 0 && c == 0) a.logit[t] = logit;
+    const float sr = info[tl].r / (1.f + expf(-capped(logit, a.tope)));
+    a.out[t * d + col] = a.h[t * d + col] + sr * A;
+  }
+}
+
 static int gate_check(const GateArgs& a, const char* what) {
   ASRN_REQUIRE(a.BL >= 0, "%s: bad sizes", what);
   ASRN_REQUIRE(a.d > 0 && a.d % 4 == 0 && a.d <= 4 * kGateMaxD4 * kWave, "%s: d=%d must be a multiple of 4, <= %d",
@@ -344,6 +441,43 @@ extern "C" int asrn_gate_fwd(const float* h, const void* aporte, int32_t aporte_
     default: hipLaunchKernelGGL(k_gate_fwd<4>, grid, block, 0, st, a); break;
   }
   return check_launch("asrn_gate_fwd");
+}
+
+extern "C" int asrn_gate_step(const float* h, const float* salida, const float* w_o, const float* signals,
+                              const float* vistos, const float* hawkes, const float* racha, const float* w_g,
+                              const float* b_g, const float* w_conf, const float* b_conf, const float* w_vistos,
+                              const float* u_hawkes, const float* d_racha, int64_t BL, int32_t d, int32_t n,
+                              int32_t nodes, int32_t T, int32_t Tc, float racha_paso, float mejor_max, float tope,
+                              float* logit, float* out, void* stream) {
+  GateArgs a{};
+  a.h = h; a.A = nullptr; a.sig = signals; a.vistos = vistos; a.hawkes = hawkes;
+  a.racha = racha; a.wg = w_g; a.bg = b_g; a.wc = w_conf; a.bc = b_conf; a.wv = w_vistos; a.uh = u_hawkes;
+  a.dr = d_racha; a.BL = BL; a.d = d; a.n = n; a.nodes = nodes; a.T = T; a.Tc = Tc; a.paso = racha_paso;
+  a.mejor_max = mejor_max; a.tope = tope; a.logit = logit; a.out = out;
+  if (gate_check(a, "asrn_gate_step")) return 1;
+  ASRN_REQUIRE(n <= kGateMaxN, "asrn_gate_step: n=%d above %d", n, kGateMaxN);
+  ASRN_REQUIRE(BL <= (int64_t(1) << 20), "asrn_gate_step: %lld tokens: the step's few tokens only", (long long)BL);
+  for (const void* p : {(const void*)h, (const void*)salida, (const void*)w_o, (const void*)w_g, (const void*)out})
+    ASRN_REQUIRE(((uintptr_t)p & 15) == 0, "asrn_gate_step: rows are read as float4: 16-byte alignment");
+  if (BL == 0) return 0;
+  const dim3 grid((unsigned)((d + kStepTok - 1) / kStepTok), (unsigned)((BL + kStepTok - 1) / kStepTok));
+  const dim3 block(kGateThreads);
+  hipStream_t st = (hipStream_t)stream;
+  const int per = ((d + kGateWaves - 1) / kGateWaves + 15) & ~15;   // a wave's depth, <= 256
+  auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, st, a, salida, w_o); };
+  const int d4c = (d + 4 * kWave - 1) / (4 * kWave);
+  if (per <= 16 * 8) {
+    switch (d4c) {
+      case 1: launch(k_gate_step<1, 8>); break;
+      default: launch(k_gate_step<2, 8>); break;
+    }
+  } else {
+    switch (d4c) {
+      case 3: launch(k_gate_step<3, 16>); break;
+      default: launch(k_gate_step<4, 16>); break;
+    }
+  }
+  return check_launch("asrn_gate_step");
 }
 
 extern "C" int64_t asrn_gate_bwd_workspace(int64_t BL, int32_t d) {

@@ -134,6 +134,10 @@ class EscritorCapa:
             forma['fuga'] = self.fugas_t
         salida, sen, _ = ops.decode_attend(c, pos, self.anillos, self.cuentas, capa.w_sufijo, capa.gamma, forma,
                                            insert=not self.ajeno, t_max=t_max)
+        if e_t.dtype == torch.float32:
+            y = capa._combinar_paso(salida, h_t, sen, vistos, hawkes, self.racha)   # W_o and the gate, one kernel
+            if y is not None:
+                return y
         acc = {'salida': salida.unsqueeze(1).to(e_t.dtype), 'senales': sen[:, None],
                'vistos': vistos.unsqueeze(1), 'hawkes': hawkes.unsqueeze(1), 'racha': self.racha.unsqueeze(1)}
         return capa._combinar(acc, h_t.unsqueeze(1))[:, 0]

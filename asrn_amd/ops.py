@@ -607,6 +607,23 @@ class Repeticion(torch.autograd.Function):
 GATE_COLS = 64        # the small parameters' block of asrn_gate_bwd's dparams
 
 
+def gate_step(h, salida, w_o, signals, vistos, hawkes, racha, wg, bg, wc, bc, wv, uh, dr, meta):
+    """The generation step's W_o product and gate in one kernel (asrn_gate_step), no autograd: h, salida (B, d)
+    fp32, w_o (d, d) -> h' = h + sigmoid(cap(logit)) W_o salida / max(1, peso_total) (B, d), as Gate.apply gives it
+    from A = W_o salida. meta as for Gate."""
+    T, Tc, paso, mejor_max, tope = meta
+    dev = _dev(h, salida)
+    B, d = h.shape
+    n, nodes = vistos.shape[-1], dr.shape[0]
+    ins = [_c(t, torch.float32) for t in (h, salida, w_o, signals, vistos, hawkes, racha)]
+    params = [_c(p, torch.float32).reshape(-1) for p in (wg, bg, wc, bc, wv, uh, dr)]
+    logit = torch.empty((B,), dtype=torch.float32, device=dev)
+    out = torch.empty((B, d), dtype=torch.float32, device=dev)
+    call('asrn_gate_step', *[ptr(t) for t in ins], *[ptr(p) for p in params], B, d, n, nodes, T, Tc, paso, mejor_max,
+         tope, ptr(logit), ptr(out), stream_of(dev))
+    return out
+
+
 class Gate(torch.autograd.Function):
     """h' = h + sigmoid(cap(logit)) A / max(1, peso_total), A = W_o salida, with the logit of _combinar
     (asrn/estable.py:376-403) and the streak response (asrn/nucleo.py:865-878), fused in asrn_gate_fwd/bwd.

@@ -244,7 +244,8 @@ def decode_bench(dev, steps, warmup, seed=0, contexts=None):
     m = asrn_amd.crear_modelo(V, d=cfg['d'], n_capas=cfg['n_capas'], largo_cada=2, semilla=seed).to(dev).eval()
     rows, kern = [], {}
     w = max(warmup, 2)
-    nombres = ['asrn_sample', 'asrn_decode_produce', 'asrn_repetition_step', 'asrn_decode_attend', 'asrn_gate_fwd']
+    nombres = ['asrn_sample', 'asrn_decode_produce', 'asrn_repetition_step', 'asrn_decode_attend', 'asrn_gate_step',
+               'asrn_block_step']
     with torch.no_grad():
         for ctx in contexts:
             x = synth.tokens(B, ctx, V, frac=cfg['frac'], span=cfg['span'], zipf=cfg['zipf'], seed=seed + ctx).to(dev)

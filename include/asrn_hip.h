@@ -318,6 +318,16 @@ int asrn_gate_fwd(const float* h, const void* aporte, int32_t aporte_bf16, const
                   const float* b_conf, const float* w_vistos, const float* u_hawkes, const float* d_racha, int64_t BL,
                   int32_t d, int32_t n, int32_t nodes, int32_t T, int32_t Tc, float racha_paso, float mejor_max,
                   float tope, float* logit, float* out, void* stream);
+/* gate_step: the generation step's W_o product and gate in one launch, for a few fp32 tokens (replaces
+ * _combinar's `self.o(salida)` and the gate after it, asrn/estable.py:376-403, in _Escritor.paso, asrn/nucleo.py:
+ * 1797-1854): A = salida W_o^T with salida (BL, d) the step's attention output and w_o (d, d) = o.weight, then out and
+ * logit exactly as gate_fwd gives them from A (its per-token logit and factor, computed alike). BL <= 2^20; h, salida,
+ * w_o, w_g and out 16-byte aligned. */
+int asrn_gate_step(const float* h, const float* salida, const float* w_o, const float* signals, const float* vistos,
+                   const float* hawkes, const float* racha, const float* w_g, const float* b_g, const float* w_conf,
+                   const float* b_conf, const float* w_vistos, const float* u_hawkes, const float* d_racha, int64_t BL,
+                   int32_t d, int32_t n, int32_t nodes, int32_t T, int32_t Tc, float racha_paso, float mejor_max,
+                   float tope, float* logit, float* out, void* stream);
 int64_t asrn_gate_bwd_workspace(int64_t BL, int32_t d);
 int asrn_gate_bwd(const float* h, const void* aporte, int32_t aporte_bf16, const float* signals, const float* vistos,
                   const float* hawkes, const float* racha, const float* w_g, const float* b_g, const float* w_conf,

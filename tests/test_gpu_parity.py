@@ -783,6 +783,45 @@ def test_gate_vs_oracle(tope, bf16):
     for k in p:
         assert_close(pm[k].grad, pr[k].grad, 'grad ' + k, tol)
 
+
+@pytest.mark.parametrize('B,d,tope', [(16, 768, None), (40, 256, 10.0), (3, 96, None), (5, 1024, None), (16, 512, 3.0)])
+def test_gate_step_vs_oracle(B, d, tope):
+    """The generation step's W_o product and gate in one kernel (asrn_gate_step: 16 x 16 tiles of W_o salida on the
+    matrix cores, the logit recomputed by every column tile) against the oracle's combine in fp64, the edge rows as in
+    test_gate_vs_oracle; 40 tokens take three row tiles, 96 and 1024 the narrowest and widest depths."""
+    say('gate step', B, d, tope)
+    n, T, Tc = 4, 8, 4
+    sh = O.Shape(d=d, T=T, Tc=Tc, n=n)
+    prot = O.Prot(tope_puerta=tope)
+    g = torch.Generator().manual_seed(B + d)
+    p = {'g.weight': torch.randn(1, d, generator=g) * 0.1, 'g.bias': torch.randn(1, generator=g),
+         'g_conf.weight': torch.randn(1, 4, generator=g) * 0.5, 'g_conf.bias': torch.randn(1, generator=g),
+         'w_vistos': torch.randn(n, generator=g), 'u_hawkes': torch.randn(n, generator=g),
+         'd_racha': torch.randn(sh.nodos, generator=g) * 0.3, 'o.weight': torch.randn(d, d, generator=g) * 0.1}
+    pt = torch.randint(0, T + 1, (B, 1, 1), generator=g).float()
+    mejor = torch.randn(B, 1, 1, generator=g) * 3
+    mejor[::7] = 2e4
+    mejor = torch.where(pt > 0, mejor, torch.full_like(mejor, -1e9))
+    pico = torch.rand(B, 1, 1, generator=g) * pt
+    ctx = torch.minimum(pt, torch.randint(0, Tc + 1, (B, 1, 1), generator=g).float())
+    top = math.log1p(sh.racha_max) * 1.3
+    h = torch.randn(B, 1, d, generator=g)
+    salida = torch.randn(B, 1, d, generator=g) * 2
+    hawkes = torch.rand(B, 1, n, generator=g) * 5
+    racha = torch.expm1(torch.rand(B, 1, generator=g) * top)
+    vistos = (torch.rand(B, 1, n, generator=g) < 0.5).float()
+    acc = {'salida': salida.double(), 'peso_total': pt.double(), 'mejor': mejor.double(), 'pico': pico.double(),
+           'peso_ctx': ctx.double(), 'vistos': vistos.double(), 'hawkes': hawkes.double(), 'racha': racha.double()}
+    yo = O.combine({k: v.double() for k, v in p.items()}, acc, h.double(), sh, prot)[:, 0]
+    sen = torch.cat([pt, mejor, pico, ctx], -1)[:, 0].to(DEV)
+    meta = (T, Tc, sh.racha_paso, float(prot.mejor_max), 0.0 if tope is None else tope)
+    with torch.no_grad():
+        y = ops.gate_step(h[:, 0].to(DEV), salida[:, 0].to(DEV), p['o.weight'].to(DEV), sen, vistos[:, 0].to(DEV),
+                          hawkes[:, 0].to(DEV), racha[:, 0].to(DEV), *[p[k].to(DEV) for k in (
+                              'g.weight', 'g.bias', 'g_conf.weight', 'g_conf.bias', 'w_vistos', 'u_hawkes', 'd_racha')],
+                          meta)
+    assert_close(y, yo, 'out')
+
 # ---------------------------------------------------------------------------------------------------------------------
 # the whole layer
 # ---------------------------------------------------------------------------------------------------------------------
