@@ -202,6 +202,23 @@ __global__ void k_repetition_step(Step a, Table tb) {
   }
 }
 
+// The generation loop step's embedding rows: e_t = emb[ids] (the model's nn.Embedding on the chosen tokens,
+// nucleo:1805) and e_prev = emb[text[:, pos - 1]] (the previous position's token, the context MLP's second input), so
+// that the loop keeps no copy of the last step's row. Ids outside [0, V) are clamped (the sampler never makes one).
+__global__ void k_embed_step(const float* __restrict__ emb, int64_t V, int d4, const int64_t* __restrict__ ids,
+                             const int64_t* __restrict__ text, int64_t ld_text, const int64_t* __restrict__ pos_p,
+                             int64_t B, float* __restrict__ e_t, float* __restrict__ e_prev) {
+  const int64_t b = blockIdx.y;
+  const int q = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B || q >= d4) return;
+  const int64_t p = *pos_p;
+  int64_t i = ids[b], j = p >= 1 ? text[b * ld_text + p - 1] : i;
+  i = i < 0 ? 0 : (i >= V ? V - 1 : i);
+  j = j < 0 ? 0 : (j >= V ? V - 1 : j);
+  ((float4*)e_t)[b * d4 + q] = ((const float4*)emb)[i * d4 + q];
+  ((float4*)e_prev)[b * d4 + q] = ((const float4*)emb)[j * d4 + q];
+}
+
 static bool pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
 }  // namespace asrn
@@ -261,6 +278,21 @@ extern "C" int asrn_hawkes_table_grow(const uint64_t* old_keys, const double* ol
   hipLaunchKernelGGL(k_hawkes_grow, dim3((unsigned)((groups * old_cap + kThreads - 1) / kThreads)), dim3(kThreads), 0,
                      st, from, to, groups);
   return check_launch("asrn_hawkes_table_grow");
+}
+
+extern "C" int asrn_embed_step(const float* emb, int64_t V, int32_t d, const int64_t* ids, const int64_t* text,
+                               int64_t ld_text, const int64_t* pos, int64_t B, float* e_t, float* e_prev,
+                               void* stream) {
+  ASRN_REQUIRE(V >= 1 && d >= 4 && d % 4 == 0 && B >= 0 && B <= 65535 && ld_text >= 1,
+               "asrn_embed_step: bad sizes V=%lld d=%d B=%lld", (long long)V, d, (long long)B);
+  ASRN_REQUIRE(emb && ids && text && pos && e_t && e_prev, "asrn_embed_step: null pointer");
+  for (const void* q : {(const void*)emb, (const void*)e_t, (const void*)e_prev})
+    ASRN_REQUIRE(((uintptr_t)q & 15) == 0, "asrn_embed_step: rows are copied as float4: 16-byte alignment");
+  if (B == 0) return 0;
+  const int d4 = d / 4;
+  hipLaunchKernelGGL(k_embed_step, dim3((unsigned)((d4 + 255) / 256), (unsigned)B), dim3(256), 0,
+                     (hipStream_t)stream, emb, V, d4, ids, text, ld_text, pos, B, e_t, e_prev);
+  return check_launch("asrn_embed_step");
 }
 
 extern "C" int asrn_repetition_step(const float* sig, double* Bt, const float* log_alfa, const double* beta_t,

@@ -615,7 +615,15 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
       __syncthreads();
     }
   }
-  if (lista) {
+  if (lista && ncand == 1 && !a.prob_out) {
+    // one token kept (a greedy row's maximum): its probability is 1 whatever the top-p cut and the quote correction,
+    // so the draw picks it
+    if (tid == 0) {
+      pick[0] = ctok[0];
+      pick[1] = -1;
+    }
+    __syncthreads();
+  } else if (lista) {
     float m = ninf;
     for (int i = tid; i < ncand; i += kSampleThreads) m = fmaxf(m, cval[i]);
     const float m3 = block_max(m, red);

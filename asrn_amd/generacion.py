@@ -105,10 +105,18 @@ class EscritorModelo:
         h = h + c
         return h + blq.ff(blq.ln2(h))
 
-    def _cuerpo(self, pieza, pos, t_max):
-        """The token ids pieza (B,) at position pos (a one-element device tensor, at most t_max) -> logits (B, V)."""
+    def _cuerpo(self, pieza, pos, t_max, texto=None, out=None):
+        """The token ids pieza (B,) at position pos (a one-element device tensor, at most t_max) -> logits (B, V).
+        texto: the loop's text (B, >= pos) holding the previous tokens: the previous row is looked up from it
+        (asrn_embed_step, with this step's) instead of being copied from the last step, and e_ult is then not kept.
+        out: a (B, V) fp32 buffer the head's product writes into."""
         m = self.m
-        e_t = m.emb(pieza)
+        emb = m.emb.weight
+        if (texto is not None and torch.is_tensor(pos) and emb.dtype == torch.float32 and emb.is_contiguous()
+                and m.emb.padding_idx is None and m.emb.max_norm is None):
+            e_t, e_prev = ops.embed_step(emb, pieza, texto, pos)
+        else:
+            e_t, e_prev = m.emb(pieza), None
         h = e_t
         capas = iter(self.capas)
         k = 0
@@ -116,9 +124,14 @@ class EscritorModelo:
             h = self._bloque(i, blq, h, k, pos)
             k += blq.mezcla == 'memoria'
             if i in m.pos_largo:
-                h = next(capas)._cuerpo(e_t, self.e_ult, h, pieza, pos, t_max=t_max)
-        self.e_ult.copy_(e_t)
-        return m.head(m.ln_f(h))
+                h = next(capas)._cuerpo(e_t, self.e_ult if e_prev is None else e_prev, h, pieza, pos, t_max=t_max)
+        if e_prev is None:
+            self.e_ult.copy_(e_t)
+        x = m.ln_f(h)
+        if (out is not None and m.head.bias is None and x.dtype == out.dtype == m.head.weight.dtype
+                and not torch.is_autocast_enabled(x.device.type)):
+            return torch.mm(x, m.head.weight.t(), out=out)
+        return m.head(x)
 
     def reservar(self, posiciones):
         """Caches and tables sized for `posiciones` positions (what a captured step must not outgrow)."""
@@ -180,7 +193,9 @@ class _Bucle:
 
     def _paso_completo(self):
         self.elegir()
-        self.lg.copy_(self.esc._cuerpo(self.piezas, self.esc.pos, self.esc.cap - 1))
+        lg = self.esc._cuerpo(self.piezas, self.esc.pos, self.esc.cap - 1, texto=self.texto, out=self.lg)
+        if lg.data_ptr() != self.lg.data_ptr():
+            self.lg.copy_(lg)
         self.esc.pos.add_(1)
 
     def paso(self, k):

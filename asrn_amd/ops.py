@@ -853,6 +853,22 @@ def decode_produce_ok(capa, e):
             and pal[2].out_features + ctx[2].out_features <= 256)
 
 
+def embed_step(emb, pieza, texto, pos):
+    """The loop step's embedding rows (asrn_embed_step): e_t = emb[pieza] and e_prev = emb[texto[:, pos - 1]], both
+    (B, d) fp32; pos a one-element int64 device tensor >= 1."""
+    dev = _dev(emb)
+    V, d = emb.shape
+    B = pieza.shape[0]
+    if emb.dtype != torch.float32 or not emb.is_contiguous() or texto.dtype != torch.int64 or texto.stride(1) != 1:
+        raise ValueError('embed_step: a contiguous fp32 table and an int64 text with unit column stride')
+    ids = _c(pieza, torch.int64)
+    e_t = torch.empty((B, d), dtype=torch.float32, device=dev)
+    e_prev = torch.empty((B, d), dtype=torch.float32, device=dev)
+    call('asrn_embed_step', ptr(emb), V, d, ptr(ids), ptr(texto), texto.stride(0), ptr(pos), B, ptr(e_t), ptr(e_prev),
+         stream_of(dev))
+    return e_t, e_prev
+
+
 def decode_produce(capa, cache, e, e_prev, h, pieza, t, t_max=None):
     """The generation step's producers for the new tokens at position t (asrn_decode_produce): V[t-1], phi[t], Qc[t],
     Kc[t], log_alfa[t] and sig[t] written into the caches; returns beta (B,) fp64. t: an int, or a one-element int64

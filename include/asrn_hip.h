@@ -387,6 +387,12 @@ int asrn_repetition_step(const float* sig, double* Bt, const float* log_alfa, co
                          int64_t t, const int64_t* t_dev, int32_t n, int64_t cap, uint64_t* tab_keys, double* tab_Bu,
                          float* tab_A, float* racha, float* vistos, float* hawkes, int32_t reloj32, void* stream);
 
+/* embed_step: the generation loop step's embedding rows, no counterpart in the reference's FFI (its loop looks the
+ * rows up with nn.Embedding, asrn/nucleo.py:1805, and keeps the previous one): e_t = emb[ids] and e_prev =
+ * emb[text[:, *pos - 1]] (B, d) fp32, emb (V, d); *pos (a device int64) >= 1; rows 16-byte aligned. */
+int asrn_embed_step(const float* emb, int64_t V, int32_t d, const int64_t* ids, const int64_t* text, int64_t ld_text,
+                    const int64_t* pos, int64_t B, float* e_t, float* e_prev, void* stream);
+
 /* decode_produce replaces the per-token producers of _Escritor.paso (asrn/nucleo.py:1797-1826): for the B new tokens
  * at position t (or *t_dev, as asrn_decode_attend), e, e_prev, h (B, d) fp32, pieza (B) int64, it writes into the
  * (B, cap, .) caches V[t-1] = W_v e (asrn/nucleo.py:683), phi[t] = the hash MLPs on [e; e_prev] (asrn/nucleo.py:644-659),
