@@ -16,7 +16,7 @@ steps, since events recorded while capturing are not replayed. Prints one JSON l
   survey_headline  SURVEY.md section 8(d)'s headline: the compulsory bytes of the HIP kernels K1-K5 (7,776 B/token at
                 cfg2) over their summed kernel time per fwd+bwd (the committed rocprofv3 kernel trace, and the eager
                 pass's device events beside it), against 8 TB/s; its target is 0.5
-  hip_aggregate all HIP kernels: 24,656 B/token (cfg2) x tokens / (8 TB/s x their summed time per step), the time
+  hip_aggregate all HIP kernels: 24,240 B/token (cfg2) x tokens / (8 TB/s x their summed time per step), the time
                 from the committed rocprofv3 kernel trace (profiles/cfg2_kernel_times.json) where there is one
   layer         whole-layer tokens/s and its HBM fraction at SURVEY.md 8(d)'s compulsory 25,876 B/token (cfg2; 24,436
                 at cfg3), and beside it at the implementation's own count (the HIP kernels' bytes plus the GEMMs'
@@ -84,16 +84,17 @@ def hash_bytes(P, m=64, mc=64):
 
 
 def hip_bytes_per_token(d, P, cf, T, n=4, a=4, m=64, mc=64, K=4, fused=True):
-    """All HIP kernels of one fwd+bwd, each distinct tensor read once and written once: hash + bucket sort (phi in, ids
-    and order out), clock 16 + 16, n-gram sort 28, Hawkes/streak scans 60 + 100, candidates, gate, context producer,
-    the hash MLPs (fused: hash_bytes; else the hidden layer and its bias column sums), and the column sums of the
+    """All HIP kernels of one fwd+bwd, each distinct tensor read once and written once: sign hash + bucket sort (fused:
+    the hash kernel writes the ids, the sort reads them and writes the order; else the sort reads phi and writes ids
+    and order), clock 16 + 16, n-gram sort 28, Hawkes/streak scans 60 + 100, candidates, gate, context producer, the
+    hash MLPs (fused: hash_bytes; else the hidden layer and its bias column sums), and the column sums of the
     candidates' per-token partials (the weight gradients' slab sums scale with the weights, not the tokens, and are
     left out).
-    cfg2 fp32 (fused): 512 + 32 + 28 + 160 + 7,044 + 8,324 + 5,304 + 3,200 + 52 = 24,656."""
+    cfg2 fp32 (fused): 96 + 32 + 28 + 160 + 7,044 + 8,324 + 5,304 + 3,200 + 52 = 24,240."""
     cand = algorithmic_bytes(d, P, cf, T, a)
     colsums = 4 * (T + K + 1) + (0 if fused else 4 * (m + mc) + 4 * P)
     mlp = sum(hash_bytes(P, m, mc)) if fused else sum(hidden_bytes(m, mc))
-    return (P * a + 8 * T + 32 + 28 + 160 + sum(cand.values()) + sum(gate_bytes(d, n, a))
+    return ((4 * T if fused else P * a) + 8 * T + 32 + 28 + 160 + sum(cand.values()) + sum(gate_bytes(d, n, a))
             + sum(context_bytes(d, cf, proj=fused)) + mlp + colsums)
 
 
@@ -490,6 +491,71 @@ def summarize_kernels(trace, steps, fetch, write, sq1, sq2, cal_fetch, cal_write
     return '\n'.join(out)
 
 
+def _short(name):
+    """A kernel's name without its namespace noise and argument list."""
+    return name.replace('(anonymous namespace)::', '').split('(')[0].replace('void ', '')
+
+
+def summarize_decode(trace, fetch, write, cal_fetch, cal_write, cal_bytes, steps=64):
+    """The decode leg's per-step kernels: from a rocprofv3 --kernel-trace of bench.py --decode-only, the last `steps`
+    intervals from one k_sample launch to the next (graph replays): each kernel's (and grid's) launches per step and
+    mean time; from --pmc FETCH_SIZE and WRITE_SIZE runs of the same command (optional), the HBM bytes per dispatch of
+    that kernel and grid (calibrated by a copy, as summarize_traffic does), and the rate they make over the traced mean
+    time. A markdown table."""
+    import csv
+    import collections
+    files, _ = _csv_rows(trace)
+    rows = list(csv.DictReader(open([f for f in files if f.endswith('kernel_trace.csv')][0])))
+    rows.sort(key=lambda r: int(r['Start_Timestamp']))
+    ks = [i for i, r in enumerate(rows) if 'k_sample' in r['Kernel_Name']]
+    spans = [(ks[j], ks[j + 1]) for j in range(len(ks) - 1)][-steps:]
+    dur, cnt, tot, kern = collections.defaultdict(list), collections.Counter(), [], []
+
+    def grid(r):
+        return int(r['Grid_Size_X']) * int(r.get('Grid_Size_Y') or 1) * int(r.get('Grid_Size_Z') or 1)
+
+    for a, b in spans:
+        tot.append((int(rows[b]['Start_Timestamp']) - int(rows[a]['Start_Timestamp'])) / 1e3)
+        kern.append(sum(int(r['End_Timestamp']) - int(r['Start_Timestamp']) for r in rows[a:b]) / 1e3)
+        for r in rows[a:b]:
+            key = (_short(r['Kernel_Name']), grid(r))
+            dur[key].append((int(r['End_Timestamp']) - int(r['Start_Timestamp'])) / 1e3)
+            cnt[key] += 1
+
+    def per_dispatch(path, counter):
+        if not path:
+            return {}
+        fs, _ = _csv_rows(path)
+        vals = collections.defaultdict(list)
+        for f in fs:
+            if f.endswith('counter_collection.csv'):
+                for r in csv.DictReader(open(f)):
+                    if r['Counter_Name'] == counter:
+                        vals[(_short(r['Kernel_Name']), int(r.get('Grid_Size') or 0))].append(float(r['Counter_Value']))
+        return {k: sum(v) / len(v) for k, v in vals.items()}
+
+    scale = {}
+    if cal_fetch and cal_write:
+        cf, cw = per_dispatch(cal_fetch, 'FETCH_SIZE'), per_dispatch(cal_write, 'WRITE_SIZE')
+        scale = {'f': cal_bytes / 1024 / max(cf.values()), 'w': cal_bytes / 1024 / max(cw.values())}
+    F, W = per_dispatch(fetch, 'FETCH_SIZE'), per_dispatch(write, 'WRITE_SIZE')
+    n_steps = len(spans)
+    out = [f'{n_steps} steps: {sum(kern) / n_steps:.1f} us of kernel time and {sum(tot) / n_steps:.1f} us from one token '
+           f'choice to the next per step, {sum(cnt.values()) / n_steps:.0f} kernels per step.', '',
+           '| kernel | grid (threads) | launches/step | us/step | mean us | HBM KB/dispatch | GB/s |',
+           '|---|---|---|---|---|---|---|']
+    for key in sorted(dur, key=lambda k: -sum(dur[k])):
+        n, g = key
+        mean = sum(dur[key]) / len(dur[key])
+        kb = rate = ''
+        if scale and key in F:
+            b = 1024 * (scale['f'] * F[key] + scale['w'] * W.get(key, 0.0))
+            kb, rate = f'{b / 1e3:.0f}', f'{b / 1e3 / mean:.0f}'
+        out.append(f'| `{n[:60]}` | {g} | {cnt[key] / n_steps:.1f} | {sum(dur[key]) / n_steps:.1f} | {mean:.2f} | '
+                   f'{kb} | {rate} |')
+    return '\n'.join(out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -518,6 +584,10 @@ def main():
                     help='only summarize a rocprofv3 kernel-trace directory of --trace-steps steps into the JSON of '
                          'profiles/<config>_kernel_times.json (printed); needs no GPU')
     ap.add_argument('--trace-steps', type=int, default=13)
+    ap.add_argument('--summarize-decode', nargs=6, default=None,
+                    metavar=('TRACE', 'FETCH', 'WRITE', 'CAL_FETCH', 'CAL_WRITE', 'CAL_BYTES'),
+                    help="only summarize the decode leg's kernel trace and its FETCH_SIZE / WRITE_SIZE runs ('-' for "
+                         'none) into a markdown table of the per-step kernels')
     ap.add_argument('--summarize-traffic', nargs=5, metavar=('FETCH', 'WRITE', 'CAL_FETCH', 'CAL_WRITE', 'CAL_BYTES'),
                     default=None, help='only turn FETCH_SIZE / WRITE_SIZE counter runs and their copy calibration '
                                        'into the JSON of profiles/cfg2_traffic.json (printed); needs no GPU')
@@ -527,6 +597,11 @@ def main():
                          'from its trace and counter runs; needs no GPU')
     ap.add_argument('--command', default='', help='the profiler command recorded with a summary')
     args = ap.parse_args()
+    if args.summarize_decode:
+        t, f, w, cf, cw, nb = args.summarize_decode
+        print(summarize_decode(t, f if f != '-' else None, w if w != '-' else None, cf if cf != '-' else None,
+                               cw if cw != '-' else None, int(nb)))
+        return
     if args.summarize_trace:
         print(json.dumps(summarize_trace(args.summarize_trace, args.trace_steps, args.command), indent=1))
         return
