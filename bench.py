@@ -20,7 +20,7 @@ steps, since events recorded while capturing are not replayed. Prints one JSON l
                 from the committed rocprofv3 kernel trace (profiles/cfg2_kernel_times.json) where there is one
   layer         whole-layer tokens/s and its HBM fraction at SURVEY.md 8(d)'s compulsory 25,876 B/token (cfg2; 24,436
                 at cfg3), and beside it at the implementation's own count (the HIP kernels' bytes plus the GEMMs'
-                operands and results, 39,504 B/token at cfg2)
+                operands and results, 39,088 B/token at cfg2)
   decode        configs[4]'s greedy generation with the whole d = 768 model (B 16): per-token latency over 1,024
                 steps against the context, 1K to 64K, and its slope
   modelo        the whole model's training step as PasoGrafado replays it: configs[3] (V 50,304, d 768, 12 local
