@@ -177,19 +177,19 @@ __device__ __forceinline__ f4 load4(const float* m, int64_t row, int64_t nrows, 
   return v;
 }
 
-// One 16 x 16 output tile over one depth split; each wavefront a quarter of the split, U steps of 16 columns of
-// loads issued ahead of their products. With g.bias the workgroup owns the whole depth (splits == 1) and writes
-// GELU(sum + bias).
-template <int U>
-__global__ __launch_bounds__(kGemvThreads) void k_part(Part g) {
-  __shared__ float tile[kGemvWaves][kTile * kTile];
+// One 16 x 16 output tile over one depth split; each of the NW wavefronts an NW-th of the split, U steps of 16 columns
+// of loads issued ahead of their products. With g.bias the workgroup owns the whole depth (splits == 1) and writes
+// GELU(sum + bias); it then runs eight wavefronts, so that twice the loads are in flight on its CU.
+template <int U, int NW>
+__global__ __launch_bounds__(NW * kWave) void k_part(Part g) {
+  __shared__ float tile[NW][kTile * kTile];
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int nt = blockIdx.x, s = blockIdx.y, rt = blockIdx.z;
   const int n0 = nt * kTile, r0 = rt * kTile;
   // this workgroup's depth range, then this wave's quarter of it, in steps of 16
   const int per_split = ((g.K + g.splits - 1) / g.splits + 15) & ~15;
   const int kb = s * per_split, ke = kb + per_split < g.K ? kb + per_split : g.K;
-  const int per_wave = ((ke - kb + kGemvWaves - 1) / kGemvWaves + 15) & ~15;
+  const int per_wave = ((ke - kb + NW - 1) / NW + 15) & ~15;
   const int wb = kb + wave * per_wave, we = wb + per_wave < ke ? wb + per_wave : ke;
   f4 acc = {0.f, 0.f, 0.f, 0.f};
   const int i16 = lane & 15, q4 = lane >> 4;
@@ -213,10 +213,13 @@ __global__ __launch_bounds__(kGemvThreads) void k_part(Part g) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) tile[wave][(4 * q4 + q) * kTile + i16] = acc[q];
   __syncthreads();
-  const int e = threadIdx.x;                          // 256 threads: one output element each
+  const int e = threadIdx.x;                          // the first 256 threads: one output element each
+  if (e >= kTile * kTile) return;
   const int b = r0 + e / kTile, n = n0 + e % kTile;
   if (b < g.B && n < g.N) {
-    const float y = ((tile[0][e] + tile[1][e]) + tile[2][e]) + tile[3][e];
+    float y = tile[0][e];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) y += tile[w][e];
     if (g.bias)
       g.part[(int64_t)b * g.N + n] = gelu_erf(y + g.bias[n]);
     else
@@ -234,16 +237,16 @@ int splits_for(int N, int K) {
 int launch_part(Part g, hipStream_t st, const char* what) {
   const dim3 grid((unsigned)((g.N + kTile - 1) / kTile), (unsigned)g.splits, (unsigned)((g.B + kTile - 1) / kTile));
   if (g.bias) {
-    // the whole depth in one workgroup: a wavefront's quarter in rounds of up to 16 steps of 16 columns
-    const int per_wave = ((g.K + kGemvWaves - 1) / kGemvWaves + 15) & ~15;
-    if (per_wave <= 16 * 8)
-      hipLaunchKernelGGL(k_part<8>, grid, dim3(kGemvThreads), 0, st, g);
-    else if (per_wave <= 16 * 12)
-      hipLaunchKernelGGL(k_part<12>, grid, dim3(kGemvThreads), 0, st, g);
+    // the whole depth in one workgroup of 8 wavefronts: a wavefront's eighth in rounds of up to 12 steps of 16
+    const int per_wave = ((g.K + 8 - 1) / 8 + 15) & ~15;
+    if (per_wave <= 16 * 4)
+      hipLaunchKernelGGL((k_part<4, 8>), grid, dim3(8 * kWave), 0, st, g);
+    else if (per_wave <= 16 * 8)
+      hipLaunchKernelGGL((k_part<8, 8>), grid, dim3(8 * kWave), 0, st, g);
     else
-      hipLaunchKernelGGL(k_part<16>, grid, dim3(kGemvThreads), 0, st, g);
+      hipLaunchKernelGGL((k_part<12, 8>), grid, dim3(8 * kWave), 0, st, g);
   } else {
-    hipLaunchKernelGGL(k_part<4>, grid, dim3(kGemvThreads), 0, st, g);
+    hipLaunchKernelGGL((k_part<4, kGemvWaves>), grid, dim3(kGemvThreads), 0, st, g);
   }
   return check_launch(what);
 }
