@@ -23,6 +23,7 @@
 #include <cstdlib>
 
 #include "common.h"
+#include "repetition.h"
 
 namespace asrn {
 
@@ -70,6 +71,9 @@ struct Cand {
   uint64_t Linv;
   // > 0: the XCDs take one batch row at a time, XCD x the positions [x slice, (x + 1) slice) of it (L = 8 slice)
   int64_t slice;
+  // generation with the repetition step in the same launch (asrn_decode_attend_repeat): the step's arguments; the
+  // query's clock is then formed from Bt[t - 1] and the step's beta (clock_at) instead of read from Bt[t]
+  Step rep; Table rep_tab;
 };
 
 // i / L for 0 <= i < 2^32: the high half of i * ceil(2^64 / L) (the product exceeds i * 2^64 / L by less than
@@ -997,7 +1001,8 @@ __device__ __forceinline__ int token_list(const Cand& a, int64_t b, int64_t t, S
 // The uniques' score terms: S.ua = base + w_suf[ell] + log_alfa_k, S.ub = fp32(Bt_k - Bt_q), S.uc = 0 (and the
 // record's per-unique fields). NW = 1: the whole wave does every unique. NW > 1: wave `wave` of NW does the chunks of
 // 2 kRows uniques wave, wave + NW, ... (its bases and then their other terms, so no other wave's results are read).
-template <int F4, int NW, bool FB16 = false>
+// STEP_CLOCK: Bt_q is formed from Bt[t - 1] and the repetition step's beta (a.rep), which writes Bt[t] concurrently.
+template <int F4, int NW, bool FB16 = false, bool STEP_CLOCK = false>
 __device__ __forceinline__ void unique_terms(const Cand& a, int64_t b, int64_t t, int NU, Scratch& S, uint8_t* rec,
                                              int wave) {
   const int lane = lane_id();
@@ -1013,7 +1018,7 @@ __device__ __forceinline__ void unique_terms(const Cand& a, int64_t b, int64_t t
   const float* sigb = a.sig + b * a.L;
   float mine[4];
   own_suffix_of(sigb, t, a.K, mine);
-  const double bq = a.Bt[tok];
+  const double bq = STEP_CLOCK ? clock_at(a.Bt + b * a.L, t, a.rep.beta_t[b], a.rep.reloj32) : a.Bt[tok];
   const float wsuf_l = lane <= a.K ? a.w_suf[lane] : 0.f;   // w_suf[x] in lane x (K <= 16), read by shuffles
   if (a.clock32 && lane == 0 && wave == 0) S.bq32 = (float)bq;
   // lanes take uniques u0 + lane (NW == 1: all 64 lanes; NW > 1: the first 2 kRows lanes of each wave's chunks);
@@ -1177,13 +1182,23 @@ void k_cand_fwd(Cand a) {   // 6-7 waves per SIMD when narrow
 // wave), and wave 0 adds the waves' sums in wave order.
 // With a.insert, tq then enters its bucket's ring in every table at slot count % C, overwriting the oldest (reference
 // nucleo:1610-1618): only wave 0 touches batch row b's rings, and its ring reads were consumed before.
+// REP: the workgroups past the B batch rows run the repetition step (a.rep), one thread per (row, n-gram length). It
+// writes Bt[tq], the Hawkes tables, the streak and its own outputs, none of which the attention reads (the candidates'
+// positions are below tq, and the query's clock is formed as the step forms it), and reads nothing the attention
+// writes.
 constexpr int kDecodeWaves = 8;
 
-template <int F4, int DCH>
+template <int F4, int DCH, bool REP>
 __global__ __launch_bounds__(kWave * kDecodeWaves) void k_decode_attend(Cand a) {
   __shared__ Scratch S;
   __shared__ float4 part[kDecodeWaves][DCH][kWave];
   __shared__ int nu_shared;
+  if (REP && blockIdx.x >= a.B) {
+    const int64_t e = (int64_t)(blockIdx.x - a.B) * blockDim.x + threadIdx.x;
+    const int64_t t = step_pos(a.rep);
+    if (e < a.rep.B * a.rep.n && t >= 0 && t < a.rep.stride) repetition_row(a.rep, a.rep_tab, e, t);
+    return;
+  }
   const int64_t b = blockIdx.x;
   const int64_t tq = a.tq_dev ? *a.tq_dev : a.tq;
   if (b >= a.B || tq < 0 || tq >= a.L) return;            // the same for every wave of the workgroup
@@ -1199,7 +1214,7 @@ __global__ __launch_bounds__(kWave * kDecodeWaves) void k_decode_attend(Cand a) 
   }
   __syncthreads();
   const int NU = nu_shared;
-  unique_terms<F4, kDecodeWaves>(a, b, tq, NU, S, nullptr, wave);
+  unique_terms<F4, kDecodeWaves, false, REP>(a, b, tq, NU, S, nullptr, wave);
   __syncthreads();
   if (wave == 0) token_weights<DCH, false>(a, b, m_shared, NU, S, nullptr, a.signals + b * 4, nullptr);
   __syncthreads();
@@ -1640,8 +1655,13 @@ struct LaunchDecode {                              // the generation caches are 
   static int run(const Cand& a, hipStream_t st) {
     if constexpr (RB != 0) {
       return fail("asrn_decode_attend: fp32 caches only");
+    } else if (a.rep.beta_t) {                     // with the repetition step's workgroups after the B rows
+      const int64_t threads = kWave * kDecodeWaves, extra = (a.rep.B * a.rep.n + threads - 1) / threads;
+      hipLaunchKernelGGL((k_decode_attend<F4, DCH, true>), dim3((unsigned)(a.B + extra)), dim3(threads), 0, st, a);
+      return check_launch("asrn_decode_attend_repeat");
     } else {
-      hipLaunchKernelGGL((k_decode_attend<F4, DCH>), dim3((unsigned)a.B), dim3(kWave * kDecodeWaves), 0, st, a);
+      hipLaunchKernelGGL((k_decode_attend<F4, DCH, false>), dim3((unsigned)a.B), dim3(kWave * kDecodeWaves), 0, st,
+                         a);
       return check_launch("asrn_decode_attend");
     }
   }
@@ -1735,6 +1755,25 @@ extern "C" int asrn_candidate_lists(const float* sig, const int32_t* order, cons
 }
 
 // a14: the generation step's candidate attention over the per-bucket rings (see k_decode_attend)
+static int decode_setup(Cand& a, const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
+                        const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
+                        int32_t* rings, int32_t* counts, int64_t B, int64_t cap, int64_t t, const int64_t* t_dev,
+                        int32_t d, int32_t nb, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
+                        float scale_phi, float scale_c, int32_t insert, float* salida, float* signals, int32_t* ids,
+                        int32_t* leak, const char* what) {
+  a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, nullptr, nullptr, nullptr, B, cap, d, T * nb, cf, K, T,
+           Tc, C, scale_phi, scale_c);
+  if (check_args(a, what)) return 1;
+  ASRN_REQUIRE(nb >= 1 && nb <= 14, "%s: nb=%d must be in [1, 14]", what, nb);
+  ASRN_REQUIRE(t >= 0 && t < cap, "%s: position t=%lld outside the caches (capacity %lld)", what, (long long)t,
+               (long long)cap);
+  a.rings = rings; a.counts = counts; a.ids_out = ids; a.nb = nb; a.tq = t; a.tq_dev = t_dev;
+  a.insert = insert ? 1 : 0;
+  a.salida = salida; a.signals = signals;
+  a.leak = leak;
+  return 0;
+}
+
 extern "C" int asrn_decode_attend(const float* phi, const float* V, const float* Qc, const float* Kc,
                                   const float* sig, const double* Bt, const float* log_alfa, const float* w_suf,
                                   const float* gamma, int32_t* rings, int32_t* counts, int64_t B, int64_t cap,
@@ -1742,16 +1781,37 @@ extern "C" int asrn_decode_attend(const float* phi, const float* V, const float*
                                   int32_t T, int32_t Tc,
                                   int32_t C, float scale_phi, float scale_c, int32_t insert, float* salida,
                                   float* signals, int32_t* ids, int32_t* leak, void* stream) {
-  Cand a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, nullptr, nullptr, nullptr, B, cap, d, T * nb, cf,
-                K, T, Tc, C, scale_phi, scale_c);
-  if (check_args(a, "asrn_decode_attend")) return 1;
-  ASRN_REQUIRE(nb >= 1 && nb <= 14, "asrn_decode_attend: nb=%d must be in [1, 14]", nb);
-  ASRN_REQUIRE(t >= 0 && t < cap, "asrn_decode_attend: position t=%lld outside the caches (capacity %lld)",
-               (long long)t, (long long)cap);
+  Cand a;
+  if (decode_setup(a, phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, rings, counts, B, cap, t, t_dev, d, nb, cf, K,
+                   T, Tc, C, scale_phi, scale_c, insert, salida, signals, ids, leak, "asrn_decode_attend"))
+    return 1;
   if (B == 0) return 0;
-  a.rings = rings; a.counts = counts; a.ids_out = ids; a.nb = nb; a.tq = t; a.tq_dev = t_dev;
-  a.insert = insert ? 1 : 0;
-  a.salida = salida; a.signals = signals;
-  a.leak = leak;
+  return dispatch<LaunchDecode>(a, (hipStream_t)stream);
+}
+
+extern "C" int asrn_decode_attend_repeat(const float* phi, const float* V, const float* Qc, const float* Kc,
+                                         const float* sig, double* Bt, const float* log_alfa, const float* w_suf,
+                                         const float* gamma, int32_t* rings, int32_t* counts, int64_t B, int64_t cap,
+                                         int64_t t, const int64_t* t_dev, int32_t d, int32_t nb, int32_t cf,
+                                         int32_t K, int32_t T, int32_t Tc, int32_t C, float scale_phi, float scale_c,
+                                         int32_t insert, float* salida, float* signals, int32_t* ids, int32_t* leak,
+                                         const double* beta_t, const double* coef, const float* kappa,
+                                         const float* kappa_r, int32_t n, int64_t tab_cap, uint64_t* tab_keys,
+                                         double* tab_Bu, float* tab_A, float* racha, float* vistos, float* hawkes,
+                                         int32_t reloj32, void* stream) {
+  Cand a;
+  if (decode_setup(a, phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, rings, counts, B, cap, t, t_dev, d, nb, cf, K,
+                   T, Tc, C, scale_phi, scale_c, insert, salida, signals, ids, leak, "asrn_decode_attend_repeat"))
+    return 1;
+  ASRN_REQUIRE(n >= 1 && n <= 16, "asrn_decode_attend_repeat: n=%d must be in [1, 16]", n);
+  ASRN_REQUIRE(tab_cap > 0 && (tab_cap & (tab_cap - 1)) == 0 && tab_cap >= 2 * (t + 1),
+               "asrn_decode_attend_repeat: table capacity %lld must be a power of two >= 2 (t + 1) = %lld: grow it "
+               "first", (long long)tab_cap, (long long)(2 * (t + 1)));
+  ASRN_REQUIRE(beta_t && coef && kappa && kappa_r && tab_keys && tab_Bu && tab_A && racha && vistos && hawkes,
+               "asrn_decode_attend_repeat: null pointer");
+  if (B == 0) return 0;
+  a.rep = {sig, Bt, log_alfa, beta_t, coef, kappa, kappa_r, B, cap, t, n, racha, vistos, hawkes, t_dev,
+           reloj32 ? 1 : 0};
+  a.rep_tab = {tab_keys, tab_Bu, tab_A, tab_cap};
   return dispatch<LaunchDecode>(a, (hipStream_t)stream);
 }

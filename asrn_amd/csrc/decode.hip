@@ -15,26 +15,13 @@
 // one thread per (row, j): no two threads touch one table, and no atomics are needed; the bulk load of a prompt
 // inserts distinct keys per table and claims slots with compare-and-swap.
 //
-// Built with -ffp-contract=off: the n-gram keys round each fp64 multiply and add separately, and the streak's
-// exp(-kappa_r beta) racha + 1 is a multiply then an add, as in the reference.
-#include "common.h"
+// The step itself (repetition.h) rounds every multiply and add explicitly; the file is also built with
+// -ffp-contract=off, so the prompt's bulk load forms its A values the same way.
+#include "repetition.h"
 
 namespace asrn {
 
-constexpr uint64_t kEmpty = ~0ull;          // no non-NaN key has this code
 constexpr int kThreads = 256;
-
-__device__ __forceinline__ uint64_t table_code(double x) {
-  if (x == 0.0) x = 0.0;
-  const uint64_t u = (uint64_t)__double_as_longlong(x);
-  return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
-}
-
-__device__ __forceinline__ uint64_t mix64(uint64_t z) {     // the splitmix64 finalizer
-  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
-  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-  return z ^ (z >> 31);
-}
 
 __global__ void k_fill_i32(int32_t* __restrict__ p, int64_t n, int32_t v) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
@@ -77,31 +64,7 @@ __global__ void k_ring_build(const int32_t* __restrict__ order, const int32_t* _
   if (place >= count - C) rings[bucket * C + place % C] = order[row * n + i];
 }
 
-// ---- Hawkes tables -------------------------------------------------------------------------------------------------
-struct Table {
-  uint64_t* keys; double* Bu; float* A; int64_t cap;   // (groups, cap) each
-};
-
-// slot of `code` in group g's table: the key's slot, or the empty slot where it goes; -1 if the table is full
-__device__ __forceinline__ int64_t probe(const Table& tb, int64_t g, uint64_t code, bool* found) {
-  const uint64_t* k = tb.keys + g * tb.cap;
-  const int64_t mask = tb.cap - 1;
-  int64_t s = (int64_t)(mix64(code) & (uint64_t)mask);
-  for (int64_t n = 0; n < tb.cap; ++n, s = (s + 1) & mask) {
-    const uint64_t v = k[s];
-    if (v == code) {
-      *found = true;
-      return s;
-    }
-    if (v == kEmpty) {
-      *found = false;
-      return s;
-    }
-  }
-  *found = false;
-  return -1;
-}
-
+// ---- Hawkes tables (Table and probe: repetition.h) ------------------------------------------------------------------
 // insert a key that is not in the table yet (concurrent inserts of distinct keys): returns its slot
 __device__ __forceinline__ int64_t claim(const Table& tb, int64_t g, uint64_t code) {
   unsigned long long* k = reinterpret_cast<unsigned long long*>(tb.keys + g * tb.cap);
@@ -150,56 +113,13 @@ __global__ void k_hawkes_grow(Table from, Table to, int64_t groups) {
 }
 
 // ---- the step: clock, n-gram keys, Hawkes, streak ------------------------------------------------------------------
-// thread per (b, j). Caches are (B, stride) rows: sig, Bt (position t written here), log_alfa (position t given).
-struct Step {
-  const float* sig; double* Bt; const float* la; const double* beta_t; const double* coef; const float* kappa;
-  const float* kappa_r; int64_t B, stride, t; int n;
-  float* racha; float* vistos; float* hawkes;
-  const int64_t* t_dev;    // optional: the position read from device memory instead of t
-  int reloj32;             // the core layer's fp32 clock: Bt[t] = fp32(Bt[t-1] + beta_t), held in fp64
-};
-
+// thread per (b, j)
 __global__ void k_repetition_step(Step a, Table tb) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= a.B * a.n) return;
-  const int64_t b = e / a.n;
-  const int j = (int)(e % a.n);
-  const int64_t t = a.t_dev ? *a.t_dev : a.t;
+  const int64_t t = step_pos(a);
   if (t < 0 || t >= a.stride) return;                            // outside the caches: nothing written
-  const double* Btb = a.Bt + b * a.stride;
-  // the clock advances (nucleo:1826): in fp64, or, for the core layer, as fp32 values added in fp32
-  const double Bq = a.reloj32 ? (double)__fadd_rn(t > 0 ? (float)Btb[t - 1] : 0.f, (float)a.beta_t[b])
-                              : (t > 0 ? Btb[t - 1] : 0.0) + a.beta_t[b];
-  if (j == 0) a.Bt[b * a.stride + t] = Bq;
-  // key of the group of j + 1 pieces ending at t: sum_{k <= j} sig[t - k] c[k], NaN before the text (nucleo:175-186)
-  double key = 0.0;
-  for (int k = 0; k <= j; ++k) {
-    const double s = t - k >= 0 ? (double)a.sig[b * a.stride + t - k] : __longlong_as_double(0x7ff8000000000000ll);
-    key = __dadd_rn(key, __dmul_rn(s, a.coef[k]));
-  }
-  float visto = 0.f, lam = 0.f;
-  if (key == key) {
-    bool found = false;
-    const int64_t s = probe(tb, e, table_code(key), &found);
-    if (s >= 0) {
-      const int64_t o = e * tb.cap + s;
-      if (found) {
-        const float dB = (float)(Bq - tb.Bu[o]);                  // the difference in the clock's type
-        lam = expf(-a.kappa[j] * dB) * tb.A[o];
-        visto = 1.f;
-      } else {
-        tb.keys[o] = table_code(key);
-      }
-      tb.Bu[o] = Bq;
-      tb.A[o] = lam + expf(a.la[b * a.stride + t]);
-    }
-  }
-  a.vistos[e] = visto;
-  a.hawkes[e] = lam;
-  if (j == a.n - 1) {                                             // racha = r (exp(-kappa_r beta) racha + 1)
-    const float g = expf(-a.kappa_r[0] * (float)a.beta_t[b]) * a.racha[b];
-    a.racha[b] = visto * (g + 1.f);
-  }
+  repetition_row(a, tb, e, t);
 }
 
 // The generation loop step's embedding rows: e_t = emb[ids] (the model's nn.Embedding on the chosen tokens,

@@ -11,10 +11,11 @@ EscritorCapa(capa, memoria_de_lo_ajeno) keeps, per layer:
 inicio() runs the layer over the prompt (its ordinary forward) and builds that state; paso() processes one new token:
 asrn_decode_produce writes the token's V, phi, Qc, Kc, log_alfa and signature rows into the caches and returns its
 beta (fp32 layers within its widths; otherwise the layer's own producers, PyTorch GEMMs, write those rows);
-asrn_repetition_step advances the clock and does the n-gram keys, the Hawkes lookup/update and the streak;
-asrn_decode_attend scores the T*C ring candidates (exact softmax, copy-gather) and inserts the token into the rings
-when every position may become a key; the gate is the layer's fused gate kernel after the W_o GEMM. Every step reads
-a fixed amount, T*C candidates, whatever the text length.
+asrn_decode_attend_repeat then runs, in one launch, the repetition step (the clock advance, the n-gram keys, the
+Hawkes lookup/update and the streak) and the attention, which scores the T*C ring candidates (exact softmax,
+copy-gather) and inserts the token into the rings when every position may become a key; the gate is the layer's fused
+gate kernel with W_o (or the W_o GEMM and the gate kernel). Every step reads a fixed amount, T*C candidates, whatever
+the text length.
 
 memoria_de_lo_ajeno=True (the reference default): the keys are only prompt positions k with k + 1 < L0 (their V rows
 are values of prompt tokens), so the rings hold positions 0..L0-2 and never change. False: every earlier position is
@@ -127,13 +128,13 @@ class EscritorCapa:
             self._escribir('log_alfa', pos, log_alfa[:, 0])
             beta_t = beta[:, 0]
         kappa, kappa_r = self.kappas
-        vistos, hawkes = self.hawkes.step(c, pos, beta_t, capa.c_vistos, kappa, kappa_r, self.racha, t_max=t_max,
-                                          reloj32=not capa.protecciones.reloj_64)
         forma = self._forma()
         if not capa.protecciones.mascara_exacta:          # the -1e9 fill's leak case, counted over the steps
             forma['fuga'] = self.fugas_t
-        salida, sen, _ = ops.decode_attend(c, pos, self.anillos, self.cuentas, capa.w_sufijo, capa.gamma, forma,
-                                           insert=not self.ajeno, t_max=t_max)
+        # the repetition step (clock, Hawkes, streak) and the attention in one launch
+        salida, sen, _, vistos, hawkes = ops.decode_attend_repeat(
+            c, pos, self.anillos, self.cuentas, capa.w_sufijo, capa.gamma, forma, not self.ajeno, self.hawkes, beta_t,
+            capa.c_vistos, kappa, kappa_r, self.racha, t_max=t_max, reloj32=not capa.protecciones.reloj_64)
         if e_t.dtype == torch.float32:
             y = capa._combinar_paso(salida, h_t, sen, vistos, hawkes, self.racha)   # W_o and the gate, one kernel
             if y is not None:

@@ -839,6 +839,38 @@ def decode_attend(cache, t, rings, counts, w_suf, gamma, shape, insert, t_max=No
     return salida, signals, ids
 
 
+def decode_attend_repeat(cache, t, rings, counts, w_suf, gamma, shape, insert, tabla, beta_t, coef, kappa, kappa_r,
+                         racha, t_max=None, reloj32=False):
+    """decode_attend and tabla.step (the repetition step: clock, Hawkes, streak) for position t in one launch
+    (asrn_decode_attend_repeat), with the same outputs, bit for bit, as the two calls in the order step, attend:
+    returns salida (B, d), signals (B, 4), the bucket ids (B, T), vistos and hawkes (B, n); Bt[:, t], the Hawkes tables
+    and racha are updated in place as tabla.step does."""
+    T, Tc, C, K, nb = shape['T'], shape['Tc'], shape['C'], shape['K'], shape['nb']
+    phi, V = cache['phi'], cache['V']
+    dev = _dev(phi)
+    B, cap, P = phi.shape
+    d, cf = V.shape[-1], cache['Qc'].shape[-1]
+    if P != T * nb:
+        raise ValueError(f'phi has {P} features, expected T * nb = {T * nb}')
+    th, tdev = _posicion(t, t_max)
+    tabla.reserve(th + 1)
+    salida = torch.empty((B, d), dtype=torch.float32, device=dev)
+    signals = torch.empty((B, 4), dtype=torch.float32, device=dev)
+    ids = torch.empty((B, T), dtype=I32, device=dev)
+    vistos = torch.empty((B, tabla.n), dtype=torch.float32, device=dev)
+    hawkes = torch.empty((B, tabla.n), dtype=torch.float32, device=dev)
+    # the converted inputs are held until the launch (a freed copy's memory could be reused by the next one)
+    ins = [_c(w_suf.detach(), torch.float32), _c(gamma.detach(), torch.float32), _c(beta_t, torch.float64),
+           _c(coef, torch.float64), _c(kappa.detach(), torch.float32), _c(kappa_r.detach(), torch.float32)]
+    call('asrn_decode_attend_repeat', ptr(phi), ptr(V), ptr(cache['Qc']), ptr(cache['Kc']), ptr(cache['sig']),
+         ptr(cache['Bt']), ptr(cache['log_alfa']), ptr(ins[0]), ptr(ins[1]), ptr(rings), ptr(counts), B, cap, th, tdev,
+         d, nb, cf, K, T, Tc, C, float(P) ** -0.5, float(cf) ** -0.5, 1 if insert else 0, ptr(salida), ptr(signals),
+         ptr(ids), ptr(shape.get('fuga')), ptr(ins[2]), ptr(ins[3]), ptr(ins[4]), ptr(ins[5]), tabla.n, tabla.cap,
+         ptr(tabla.keys), ptr(tabla.Bu), ptr(tabla.A), ptr(racha), ptr(vistos), ptr(hawkes), 1 if reloj32 else 0,
+         stream_of(dev))
+    return salida, signals, ids, vistos, hawkes
+
+
 def decode_produce_ok(capa, e):
     """Whether asrn_decode_produce covers this layer and input: fp32 (no autocast) and the widths it takes."""
     pal, ctx = capa.afin_palabra, capa.afin_contexto

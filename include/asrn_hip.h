@@ -387,6 +387,21 @@ int asrn_repetition_step(const float* sig, double* Bt, const float* log_alfa, co
                          int64_t t, const int64_t* t_dev, int32_t n, int64_t cap, uint64_t* tab_keys, double* tab_Bu,
                          float* tab_A, float* racha, float* vistos, float* hawkes, int32_t reloj32, void* stream);
 
+/* decode_attend_repeat: asrn_decode_attend and asrn_repetition_step for one position in a single launch, no
+ * counterpart in the reference's FFI (its step runs _repeticion_o1 and the attention one after the other,
+ * asrn/nucleo.py:1826-1850). The first arguments are asrn_decode_attend's, the rest asrn_repetition_step's (sig, Bt,
+ * log_alfa, B, t and t_dev shared; the caches' capacity cap is the step's stride; the Hawkes tables' capacity is
+ * tab_cap). The outputs are those of the two calls made in that order, bit for bit: the attention forms the query's
+ * clock Bt[t] = Bt[t-1] + beta_t as the step does instead of reading what the step writes. */
+int asrn_decode_attend_repeat(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
+                              double* Bt, const float* log_alfa, const float* w_suf, const float* gamma, int32_t* rings,
+                              int32_t* counts, int64_t B, int64_t cap, int64_t t, const int64_t* t_dev, int32_t d,
+                              int32_t nb, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C, float scale_phi,
+                              float scale_c, int32_t insert, float* salida, float* signals, int32_t* ids,
+                              int32_t* leak, const double* beta_t, const double* coef, const float* kappa,
+                              const float* kappa_r, int32_t n, int64_t tab_cap, uint64_t* tab_keys, double* tab_Bu,
+                              float* tab_A, float* racha, float* vistos, float* hawkes, int32_t reloj32, void* stream);
+
 /* embed_step: the generation loop step's embedding rows, no counterpart in the reference's FFI (its loop looks the
  * rows up with nn.Embedding, asrn/nucleo.py:1805, and keeps the previous one): e_t = emb[ids] and e_prev =
  * emb[text[:, *pos - 1]] (B, d) fp32, emb (V, d); *pos (a device int64) >= 1; rows 16-byte aligned. */

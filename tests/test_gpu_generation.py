@@ -175,6 +175,74 @@ def test_hawkes_table_vs_oracle(B, L0, steps, V, n):
     assert tab.cap > cap0 or 2 * L <= cap0                 # the tables grew when they had to
 
 
+def table_contents(tab):
+    """Each group's (key, Bu, A) ordered by key code, empty slots zeroed: the prompt's load and a growth place
+    colliding keys by concurrent compare-and-swap, so two tables with the same contents may differ slot by slot."""
+    keys, idx = torch.sort(tab.keys, dim=1)
+    held = keys != -1                                      # Bu and A are only defined where a key is stored
+    return (keys, torch.where(held, tab.Bu.gather(1, idx), torch.zeros((), dtype=tab.Bu.dtype, device=DEV)),
+            torch.where(held, tab.A.gather(1, idx), torch.zeros((), dtype=tab.A.dtype, device=DEV)))
+
+
+@pytest.mark.parametrize('B,t0,steps,d,C,nb,T,V,n,reloj32,dev_pos', [
+    (2, 300, 24, 64, 32, 14, 8, 6, 4, False, False), (3, 40, 30, 96, 4, 2, 4, 5, 4, True, True),
+    (16, 500, 6, 768, 32, 14, 8, 50, 4, False, True), (2, 1, 20, 64, 8, 3, 8, 4, 6, True, False)])
+def test_decode_attend_repeat_equals_two_calls(B, t0, steps, d, C, nb, T, V, n, reloj32, dev_pos):
+    """asrn_decode_attend_repeat (the repetition step in the attention's launch) against asrn_repetition_step then
+    asrn_decode_attend on a copy of the same state, bit for bit, step after step: the attention's outputs and ids, the
+    step's vistos and hawkes, the clock cache, the streak, the rings and counts and the Hawkes tables (which also
+    grow on the way in the t0 = 1 case)."""
+    say('decode attend + repetition = two calls', B, t0, steps, d, C, nb, T, n, reloj32, dev_pos)
+    L = t0 + steps
+    cf, K, Tc = 16, 4, T // 2
+    x, phi, g = token_phi(B, L, V, T, nb, seed=t0 + d + n)
+    beta = torch.rand(B, L, generator=g, dtype=torch.float64) * 1.5
+    Bt = beta.cumsum(1)
+    if reloj32:                                            # the core layer's clock holds fp32 values
+        Bt = Bt.float().double()
+    la = torch.randn(B, L, generator=g) * 0.3
+    coef = torch.rand(n, generator=g, dtype=torch.float64) + 0.5
+    kappa = (torch.rand(n, generator=g) * 0.3 + 0.01).to(DEV)
+    kappa_r = (torch.rand(1, generator=g) * 0.1 + 0.01).to(DEV)
+    w_suf = (torch.randn(K + 1, generator=g) * 0.5).to(DEV)
+    gamma = (torch.rand(T, generator=g) * 2).to(DEV)
+    cache = dict(phi=phi, V=torch.randn(B, L, d, generator=g), Qc=torch.randn(B, L, cf, generator=g),
+                 Kc=torch.randn(B, L, cf, generator=g), sig=x.float(), Bt=torch.zeros(B, L, dtype=torch.float64),
+                 log_alfa=la)
+    cache['Bt'][:, :t0] = Bt[:, :t0]
+    sig_d = x.float().to(DEV)
+    keys, order, rep, rank_k, _ = ops.ngram_sort(sig_d[:, :t0], coef.to(DEV), n)
+    hk = ops.Hawkes.apply(Bt[:, :t0].to(DEV), la[:, :t0].to(DEV), kappa, order, rep, rank_k)
+    states = []
+    for _ in range(2):
+        tab = ops.HawkesTable.load(keys, order, rep, hk, Bt[:, :t0].to(DEV), la[:, :t0].to(DEV))
+        rings, counts = ops.ring_build(phi[:, :t0].to(DEV), T, nb, C)
+        states.append(dict(cache={k: v.to(DEV).contiguous() for k, v in cache.items()}, tab=tab, rings=rings,
+                           counts=counts, racha=torch.rand(B, generator=torch.Generator().manual_seed(3)).to(DEV)))
+    sep, fus = states
+    shape = dict(T=T, Tc=Tc, C=C, K=K, nb=nb)
+    for t in range(t0, L):
+        pos = torch.full((1,), t, dtype=torch.int64, device=DEV) if dev_pos else t
+        t_max = L - 1 if dev_pos else None
+        bt = beta[:, t].to(DEV)
+        v1, h1 = sep['tab'].step(sep['cache'], pos, bt, coef.to(DEV), kappa, kappa_r, sep['racha'], t_max=t_max,
+                                 reloj32=reloj32)
+        s1, g1, i1 = ops.decode_attend(sep['cache'], pos, sep['rings'], sep['counts'], w_suf, gamma, shape,
+                                       insert=True, t_max=t_max)
+        s2, g2, i2, v2, h2 = ops.decode_attend_repeat(fus['cache'], pos, fus['rings'], fus['counts'], w_suf, gamma,
+                                                      shape, True, fus['tab'], bt, coef.to(DEV), kappa, kappa_r,
+                                                      fus['racha'], t_max=t_max, reloj32=reloj32)
+        for a_, b_, what in ((s1, s2, 'salida'), (g1, g2, 'signals'), (i1, i2, 'ids'), (v1, v2, 'vistos'),
+                             (h1, h2, 'hawkes'), (sep['racha'], fus['racha'], 'racha'),
+                             (sep['cache']['Bt'], fus['cache']['Bt'], 'Bt'), (sep['rings'], fus['rings'], 'rings'),
+                             (sep['counts'], fus['counts'], 'counts')):
+            assert torch.equal(a_, b_), f'{what} t={t}'
+        assert sep['tab'].cap == fus['tab'].cap
+        for a_, b_, what in zip(table_contents(sep['tab']), table_contents(fus['tab']), ('keys', 'Bu', 'A')):
+            assert torch.equal(a_, b_), f'table {what} t={t}'
+    assert fus['tab'].cap >= 2 * L
+
+
 # ---------------------------------------------------------------------------------------------------------------------
 # the layer written step by step
 # ---------------------------------------------------------------------------------------------------------------------

@@ -152,6 +152,17 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert 'grow it first' in _err(lib)
     assert lib.asrn_hawkes_table_grow(N, N, N, 8, 256, N, N, N, 128, N) != 0
     assert 'growing' in _err(lib)
+    # the fused attention + repetition step: the attention's checks, then the step's n and table capacity
+    att = [2, 100, 50, N, 64, 14, 16, 4, 8, 4, 32, 0.1, 0.25, 1, N, N, N, N]
+    assert lib.asrn_decode_attend_repeat(*([N] * 11), 2, 100, 100, *att[3:], *([N] * 4), 4, 128, *([N] * 6), 0,
+                                         N) != 0
+    assert 'outside the caches' in _err(lib)
+    assert lib.asrn_decode_attend_repeat(*([N] * 11), *att, *([N] * 4), 0, 128, *([N] * 6), 0, N) != 0
+    assert 'n=0' in _err(lib)
+    assert lib.asrn_decode_attend_repeat(*([N] * 11), *att, *([N] * 4), 4, 64, *([N] * 6), 0, N) != 0
+    assert 'grow it first' in _err(lib)
+    assert lib.asrn_decode_attend_repeat(*([N] * 11), *att, *([N] * 4), 4, 128, *([N] * 6), 0, N) != 0
+    assert 'null pointer' in _err(lib)
     # the step's producers: width, position, workspace
     prod = [N] * 4
     w = [N] * 9
