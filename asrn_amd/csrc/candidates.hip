@@ -397,13 +397,16 @@ __device__ __forceinline__ int gather_rings(const Cand& a, int64_t b, int64_t t,
   // the query's bucket id in each table from the signs of its phi row (strict > 0, nucleo:663): the whole row in one
   // round of loads (element c * 64 + lane; P = T nb <= 255), then table `lane`'s nb bits out of the ballots
   const float* ph = a.phi + (b * a.L + t) * a.P;
+  float hv[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {                   // unconditional loads (lanes past P read element P - 1), so all
+    const int e = c * kWave + lane;               // four are in flight before the first ballot waits
+    hv[c] = ph[e < a.P ? e : a.P - 1];
+  }
   uint64_t pm[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int e = c * kWave + lane;
-    pm[c] = __ballot(e < a.P && ph[e] > 0.f);
-  }
-  int id = 0, cnt = 0;
+  for (int c = 0; c < 4; ++c) pm[c] = __ballot(c * kWave + lane < a.P && hv[c] > 0.f);
+  int id = 0;
   if (lane < a.T) {
     const int e0 = lane * a.nb, w = e0 >> 6, o = e0 & 63;
     const uint64_t lo = w == 0 ? pm[0] : (w == 1 ? pm[1] : (w == 2 ? pm[2] : pm[3]));
@@ -411,9 +414,24 @@ __device__ __forceinline__ int gather_rings(const Cand& a, int64_t b, int64_t t,
     if (o + a.nb > 64) bits |= (w == 0 ? pm[1] : (w == 1 ? pm[2] : pm[3])) << (64 - o);   // w <= 2 here
     id = (int)(bits & ((1ull << a.nb) - 1ull));
     a.ids_out[b * a.T + lane] = id;
-    cnt = a.counts[(b * a.T + lane) * ((int64_t)1 << a.nb) + id];
   }
+  // one round of loads: each bucket's count and every slot of its ring, whose addresses need only the ids; the slots
+  // go to LDS (the dedupe's hash array, dead until dedupe clears it) and each entry then takes its slot oldest first
+  const int cnt = lane < a.T ? a.counts[(b * a.T + lane) * ((int64_t)1 << a.nb) + id] : 0;
   const int slots = a.T * a.C;
+  static_assert(kHash >= kMaxSlots, "the ring slots are staged in the dedupe's hash array");
+  int raw[kCh];
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const int sl = c * kWave + lane;
+    const int tau = sl < slots ? sl / a.C : 0;
+    const int idt = __shfl(id, tau, 64);
+    raw[c] = sl < slots ? a.rings[((b * a.T + tau) * ((int64_t)1 << a.nb) + idt) * a.C + (sl - tau * a.C)] : -1;
+  }
+#pragma unroll
+  for (int c = 0; c < kCh; ++c)
+    if (c * kWave + lane < slots) S.hpos[c * kWave + lane] = raw[c];
+  wave_lds_sync();
   int pos[kCh], tt[kCh];
   bool ok[kCh];
 #pragma unroll
@@ -421,12 +439,12 @@ __device__ __forceinline__ int gather_rings(const Cand& a, int64_t b, int64_t t,
     const int sl = c * kWave + lane;
     const int tau = sl < slots ? sl / a.C : 0;
     const int i = sl - tau * a.C;
-    const int idt = __shfl(id, tau, 64), ct = __shfl(cnt, tau, 64);
+    const int ct = __shfl(cnt, tau, 64);
     const int n = ct < a.C ? ct : a.C;              // filled slots
     const int start = ct < a.C ? 0 : ct % a.C;     // the oldest entry
     const bool v = sl < slots && i < n;
-    const int slot = (start + i) % a.C;
-    int p = v ? a.rings[((b * a.T + tau) * ((int64_t)1 << a.nb) + idt) * a.C + slot] : -1;
+    const int slot = start + i < a.C ? start + i : start + i - a.C;
+    const int p = v ? S.hpos[tau * a.C + slot] : -1;
     ok[c] = v && p >= 0 && p < t;
     tt[c] = tau;
     pos[c] = ok[c] ? p : 0;

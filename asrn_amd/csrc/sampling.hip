@@ -89,6 +89,23 @@ __device__ __forceinline__ int64_t slot_add(unsigned long long* t, int64_t cap, 
   return -1;
 }
 
+// the slot holding `key` (*found) or the empty slot where it goes; -1 if the table is full (plain loads: for the one
+// thread that owns a row's tables)
+__device__ __forceinline__ int64_t slot_find(const unsigned long long* t, int64_t cap, uint64_t key, bool* found) {
+  const uint64_t m = (uint64_t)cap - 1;
+  uint64_t i = mix64(key) & m;
+  for (int64_t p = 0; p < cap; ++p) {
+    const unsigned long long v = t[i];
+    if (v == key || v == kEmptySlot) {
+      *found = v == key;
+      return (int64_t)i;
+    }
+    i = (i + 1) & m;
+  }
+  *found = false;
+  return -1;
+}
+
 __device__ __forceinline__ bool set_has(const TupleSet& s, int64_t row, uint64_t key) {
   return slot_of(s.slots + row * s.cap, s.cap, key) >= 0;
 }
@@ -129,6 +146,40 @@ __device__ __forceinline__ void ngram_add(const TupleSet& s, int64_t row, const 
   const int64_t e = row * s.cap + c;
   const int k = atomicAdd(s.count + e, 1);
   if (k < kSucc) s.succ[e * kSucc + k] = (int32_t)x[s.n - 1];
+}
+
+// Where the context text[pos - n + 1 .. pos - 1] sits in row b's context table: its slot (or the empty slot where it
+// goes; -1 when not probed or the table is full), whether it is there, and its successor count. The step's lookup
+// finds it and the step's insert of the n-gram ending at pos, whose context it is, reuses it: only the thread that
+// does both touches row b's tables during the step.
+struct CtxAt {
+  int64_t slot = -1;
+  bool found = false;
+  int count = 0;
+};
+
+// ngram_add for the generation step's new n-gram x[0..n-1] (x[n-1] the token just written), by the one thread that owns
+// row `row`'s tables during the step: plain loads and stores instead of atomics, and the context's place from the
+// step's lookup (`at`; probed here when the lookup did not run). The tables end as ngram_add leaves them.
+__device__ __forceinline__ void ngram_put(const TupleSet& s, int64_t row, const int64_t* x, int w, CtxAt at) {
+  const KeyForm f = key_form(s.n, w);
+  const uint64_t st = pack(f, x, s.n - 1);
+  const uint64_t ctx = f.key_of(st);
+  const uint64_t key = f.key_of(f.step(st, s.n - 1, x[s.n - 1]));
+  unsigned long long* slots = s.slots + row * s.cap;
+  bool found;
+  const int64_t i = slot_find(slots, s.cap, key, &found);
+  if (i < 0 || found) return;
+  slots[i] = key;
+  if (at.slot < 0) {
+    at.slot = slot_find(s.ctx + row * s.cap, s.cap, ctx, &at.found);
+    if (at.slot < 0) return;
+    at.count = at.found ? s.count[row * s.cap + at.slot] : 0;
+  }
+  const int64_t e = row * s.cap + at.slot;
+  if (!at.found) s.ctx[e] = ctx;
+  s.count[e] = at.count + 1;
+  if (at.count < kSucc) s.succ[e * kSucc + at.count] = (int32_t)x[s.n - 1];
 }
 
 __global__ void k_set_build(const int64_t* __restrict__ x, int64_t ldx, int64_t rows, int64_t L, TupleSet s, int w) {
@@ -287,21 +338,36 @@ struct SampleArgs {
   int32_t top_k, window;
   int64_t stop_token;
   uint64_t seed;
+  int32_t greedy_parts;        // k_greedy_part ran before: its slices' results are in each row's `work`
 };
+
+// The greedy pre-pass (a greedy row with no penalty, no recorded logits and no probabilities out): kGreedySlices
+// workgroups per row, each over a contiguous slice of V / kGreedySlices logits, find the maximum of x / T there, how
+// many tokens reach it, the smallest of them and whether any x / T is NaN, so that the row's one workgroup in k_sample
+// combines kGreedySlices results instead of reading the row: one CU per row makes that pass VALU-bound (about 60
+// instructions a token, 50,304 tokens). A row with one finite maximum then takes it (its probability is 1, whatever
+// the top-p cut and the quote correction); ties, NaN or an all -inf row run the full pass as before.
+constexpr int kGreedySlices = 16;
+constexpr int kGreedyThreads = 256;
 
 // The successors of the context text[pos - n + 1 .. pos - 1] in row b's set: *n_list < 0 when the context has more
 // than kSucc of them (then the caller probes every token); list[0 .. *n_list) otherwise. One thread calls it.
 __device__ __forceinline__ void successors(const TupleSet& s, int64_t b, const int64_t* text, int64_t pos, int w,
-                                           int* list, int* n_list) {
+                                           int* list, int* n_list, CtxAt* at) {
   const KeyForm f = key_form(s.n, w);
   const uint64_t ctx = f.key_of(pack(f, text + pos - (s.n - 1), s.n - 1));
-  const int64_t c = slot_of(s.ctx + b * s.cap, s.cap, ctx);
-  if (c < 0) {
+  bool found;
+  const int64_t c = slot_find(s.ctx + b * s.cap, s.cap, ctx, &found);
+  at->slot = c;
+  at->found = found;
+  at->count = 0;
+  if (c < 0 || !found) {
     *n_list = 0;
     return;
   }
   const int64_t e = b * s.cap + c;
   const int k = s.count[e];
+  at->count = k;
   if (k > kSucc) {
     *n_list = -1;
     return;
@@ -360,6 +426,75 @@ __device__ __forceinline__ void each_range(const float* row, int64_t v0, int64_t
   }
 }
 
+__global__ __launch_bounds__(kGreedyThreads) void k_greedy_part(SampleArgs a) {
+  __shared__ float wl[kGreedyThreads / kWave];
+  __shared__ int wc[kGreedyThreads / kWave], wf[kGreedyThreads / kWave], wn[kGreedyThreads / kWave];
+  const int64_t b = blockIdx.x;                                 // row b, slice blockIdx.y
+  const int64_t pos = *a.pos_dev;
+  if (pos < 0 || pos > a.pos_max) return;                       // as k_sample: nothing is touched
+  const int64_t V = a.V;
+  const int64_t per = (V + kGreedySlices - 1) / kGreedySlices;
+  const int64_t v0 = (int64_t)blockIdx.y * per, v1 = v0 + per < V ? v0 + per : V;
+  const float* lg = a.lg + b * a.ldl;
+  const float tden = fmaxf(a.temperature, 1e-6f);
+  float lmax = -INFINITY;
+  int cnt = 0, first = INT_MAX, nan = 0;
+  for (int64_t base = v0 + threadIdx.x; base < v1; base += 4 * kGreedyThreads) {
+    float t[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t v = base + j * kGreedyThreads;
+      t[j] = v < v1 ? lg[v] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {                               // this thread's tokens in increasing order
+      const int64_t v = base + j * kGreedyThreads;
+      if (v >= v1) continue;
+      const float l = t[j] / tden;
+      nan |= l != l;
+      if (l > lmax) {
+        lmax = l;
+        cnt = 0;
+        first = (int)v;
+      }
+      if (l == lmax) ++cnt;
+    }
+  }
+  const float L = wave_max_u(lmax);
+  int c = lmax == L ? cnt : 0, f = lmax == L ? first : INT_MAX;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    c += __shfl_xor(c, m, 64);
+    f = min(f, __shfl_xor(f, m, 64));
+    nan |= __shfl_xor(nan, m, 64);
+  }
+  const int w = threadIdx.x / kWave;
+  if (lane_id() == 0) {
+    wl[w] = L;
+    wc[w] = c;
+    wf[w] = f;
+    wn[w] = nan;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float Lb = wl[0];
+    for (int i = 1; i < kGreedyThreads / kWave; ++i) Lb = fmaxf(Lb, wl[i]);
+    int C = 0, F = INT_MAX, N = 0;
+    for (int i = 0; i < kGreedyThreads / kWave; ++i) {
+      if (wl[i] == Lb) {
+        C += wc[i];
+        F = min(F, wf[i]);
+      }
+      N |= wn[i];
+    }
+    float* out = a.work + b * V + 4 * (int64_t)blockIdx.y;
+    out[0] = Lb;
+    reinterpret_cast<int*>(out)[1] = C;
+    reinterpret_cast<int*>(out)[2] = F;
+    reinterpret_cast<int*>(out)[3] = N;
+  }
+}
+
 __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   __shared__ Red red;
   __shared__ unsigned int hist_n[256];
@@ -388,10 +523,11 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   const int nq = a.quote.n, nb = a.ban.n;
   const bool quote = a.quote.slots && pos >= nq;
   const bool bans = a.ban.slots && pos - a.L0 >= nb;
+  CtxAt qat, bat;                                               // thread 0's: reused by the insert at the end
   if (tid == 0) {
     nq_list = nb_list = 0;
-    if (quote) successors(a.quote, b, text, pos, a.w, qlist, &nq_list);
-    if (bans) successors(a.ban, b, text, pos, a.w, blist, &nb_list);
+    if (quote) successors(a.quote, b, text, pos, a.w, qlist, &nq_list, &qat);
+    if (bans) successors(a.ban, b, text, pos, a.w, blist, &nb_list, &bat);
   }
 
   // Greedy rows (top_k = 1) take the maximum and its ties in one fused pass below. With no penalty and no bans the
@@ -399,6 +535,29 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   const bool greedy = a.top_k == 1 && V > 1;
   const bool direct = greedy && a.penalty == 1.f && !bans;
   const float* src = direct ? lg : work;
+  // the greedy pre-pass's slices (in `work`, which a direct row does not otherwise use): one finite maximum is taken
+  // as the row's one kept token, with no pass over the row here
+  bool fast = false;
+  if (direct && a.greedy_parts) {
+    if (tid == 0) {
+      const float* p = work;
+      const int* ip = reinterpret_cast<const int*>(work);
+      float L = p[0];
+      for (int i = 1; i < kGreedySlices; ++i) L = fmaxf(L, p[4 * i]);
+      int C = 0, F = INT_MAX, N = 0;
+      for (int i = 0; i < kGreedySlices; ++i) {
+        if (p[4 * i] == L) {
+          C += ip[4 * i + 1];
+          F = min(F, ip[4 * i + 2]);
+        }
+        N |= ip[4 * i + 3];
+      }
+      pick[0] = N == 0 && C == 1 && L != -INFINITY ? F : -1;
+    }
+    __syncthreads();
+    fast = pick[0] >= 0;
+    if (fast && tid == 0) ctok[0] = pick[0];
+  }
   // penalty (_frenar): the logits as they came, then the tokens of the window penalized from those same values
   float* lout = (a.logits_out && step >= 0 && step < a.steps) ? a.logits_out + (b * a.steps + step) * V : nullptr;
   if (!direct) {
@@ -442,7 +601,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
 
   // quote mask and its mass at temperature 1 (_conservar_cita's p1)
   uint32_t* qbits = a.quote_bits + b * ((V + 31) / 32);
-  const bool qprobe = quote && nq_list < 0;
+  const bool qprobe = quote && nq_list < 0 && !fast;
   if (qprobe) {
     const KeyForm f = key_form(nq, a.w);
     const uint64_t base = pack(f, text + pos - (nq - 1), nq - 1);
@@ -470,9 +629,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
   float corte = ninf;
   // greedy: one pass gives the quote mass at temperature 1 (a running maximum with its sums rescaled), the maximum
   // of x / T and each thread's tokens at that maximum (the kept set), in the order the list gather below uses
-  bool listed = false;
-  int ncand = 0;
-  if (greedy) {
+  bool listed = fast;
+  int ncand = fast ? 1 : 0;
+  if (greedy && !fast) {
     float m = ninf, sm = 0.f, cm = 0.f, lmax = ninf;
     int cnt = 0;
     bool nan = false;                                            // NaN logits: the passes below keep them as they did
@@ -539,7 +698,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
       listed = true;
     }
     __syncthreads();
-  } else if (need_mass) {
+  } else if (!greedy && need_mass) {
     float m = ninf;
     each(src, V, [&](int64_t, float x) { m = fmaxf(m, x); });
     const float m1 = block_max(m, red);
@@ -934,8 +1093,8 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     }
     text[pos] = tok;
     a.tokens[b] = tok;
-    if (a.quote.slots && pos + 1 >= nq) ngram_add(a.quote, b, text + pos - (nq - 1), a.w);
-    if (a.ban.slots && pos + 1 - a.L0 >= nb) ngram_add(a.ban, b, text + pos - (nb - 1), a.w);
+    if (a.quote.slots && pos + 1 >= nq) ngram_put(a.quote, b, text + pos - (nq - 1), a.w, qat);
+    if (a.ban.slots && pos + 1 - a.L0 >= nb) ngram_put(a.ban, b, text + pos - (nb - 1), a.w, bat);
   }
 }
 
@@ -994,10 +1153,11 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_reg(SampleArgs a) {
   const int nq = a.quote.n, nb = a.ban.n;
   const bool quote = a.quote.slots && pos >= nq;
   const bool bans = a.ban.slots && pos - a.L0 >= nb;
+  CtxAt qat, bat;                                               // thread 0's: reused by the insert at the end
   if (tid == 0) {
     nq_list = nb_list = 0;
-    if (quote) successors(a.quote, b, text, pos, a.w, qlist, &nq_list);
-    if (bans) successors(a.ban, b, text, pos, a.w, blist, &nb_list);
+    if (quote) successors(a.quote, b, text, pos, a.w, qlist, &nq_list, &qat);
+    if (bans) successors(a.ban, b, text, pos, a.w, blist, &nb_list, &bat);
   }
   auto tok_of = [&](int r) { return (int64_t)r * kSampleThreads + tid; };
   // the slot of token v when this thread owns it
@@ -1288,8 +1448,8 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_reg(SampleArgs a) {
     }
     text[pos] = tok;
     a.tokens[b] = tok;
-    if (a.quote.slots && pos + 1 >= nq) ngram_add(a.quote, b, text + pos - (nq - 1), a.w);
-    if (a.ban.slots && pos + 1 - a.L0 >= nb) ngram_add(a.ban, b, text + pos - (nb - 1), a.w);
+    if (a.quote.slots && pos + 1 >= nq) ngram_put(a.quote, b, text + pos - (nq - 1), a.w, qat);
+    if (a.ban.slots && pos + 1 - a.L0 >= nb) ngram_put(a.ban, b, text + pos - (nb - 1), a.w, bat);
   }
 }
 
@@ -1383,6 +1543,12 @@ extern "C" int asrn_sample(const float* lg, int64_t ldl, float* work, uint32_t* 
   a.seed = seed;
   const dim3 grid((unsigned)B), block(kSampleThreads);
   const hipStream_t st = (hipStream_t)stream;
+  static_assert(4 * kGreedySlices <= 16 * kSampleThreads, "the slices' results fit a row of the scratch");
+  a.greedy_parts = V > 16 * kSampleThreads && top_k == 1 && penalty == 1.f && !logits_out && !prob_out;
+  if (a.greedy_parts) {
+    hipLaunchKernelGGL(k_greedy_part, dim3((unsigned)B, kGreedySlices), dim3(kGreedyThreads), 0, st, a);
+    if (int rc = check_launch("asrn_sample (greedy pre-pass)")) return rc;
+  }
   // rows up to 16 Ki tokens in registers (R tokens per thread: R = 16 is what fits 128 VGPRs, the budget of a
   // 1,024-thread workgroup), longer rows from global memory
   if (V <= 4 * kSampleThreads)

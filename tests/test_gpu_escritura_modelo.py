@@ -244,6 +244,71 @@ def test_sampler_greedy_large_rows(caso):
             assert 0 < float(q[q > 0].min()) < float(q.max())        # the two groups carry different masses
 
 
+def _set_contents(s):
+    """An n-gram set's contents per row, independent of where colliding keys landed: its keys, and per context its
+    successor count and inline successors (as a set: the prompt's build appends them in no fixed order)."""
+    slots, ctx, count, succ = (t.cpu() for t in (s.slots, s.ctx, s.count, s.succ))
+    out = []
+    for r in range(slots.shape[0]):
+        keys = sorted(int(k) for k in slots[r] if int(k) != -1)
+        ctxs = {}
+        for c in torch.nonzero(ctx[r] != -1).view(-1).tolist():
+            k = int(count[r, c])
+            ctxs[int(ctx[r, c])] = (k, sorted(succ[r, c, :min(k, succ.shape[2])].tolist()))
+        out.append((keys, ctxs))
+    return out
+
+
+@pytest.mark.parametrize('caso', ['unique', 'ties', 'nan', 'neg_inf'])
+def test_sampler_greedy_prepass(caso):
+    """Greedy rows past the register sizes with no penalty, bans, recorded logits or probabilities out go through the
+    greedy pre-pass (k_greedy_part, 16 slices a row) and, with one finite maximum, take its token with no pass of
+    their own. Over 6 steps each token equals the one the same call makes with probabilities out (the full pass),
+    with the maxima placed in every slice, tied maxima (the full pass draws among them), a NaN logit and an all -inf
+    row; the quote set, filled by the steps' single-thread inserts, then holds what a set built from the generated
+    text holds."""
+    say('sampler greedy pre-pass', caso)
+    B, V, L0, nq, steps = 4, 50304, 40, 3, 6
+    pos0 = 80
+    g = torch.Generator().manual_seed(11)
+    x = torch.randint(0, 50, (B, pos0 + steps + 1), generator=g)   # a small alphabet: contexts repeat, quotes act
+    sets, ests, textos = [], [], []
+    for _ in range(2):
+        textos.append(x.to(DEV).contiguous())
+        s = ops.ConjuntoNgramas(B, nq, V, pos0 + steps + 1, DEV)
+        s.agregar_texto(textos[-1][:, :pos0].contiguous())
+        sets.append(s)
+        ests.append(_Estado(B, V, pos0 + steps + 1))
+    per = (V + 15) // 16
+    for k in range(steps):
+        pos = pos0 + k
+        lg = torch.randn(B, V, generator=g) * 3
+        for b in range(B):
+            if caso == 'unique':                               # the maximum in slice (4 k + b) mod 16, at its ends too
+                sl = (4 * k + b) % 16
+                lg[b, [sl * per, sl * per + per // 2, min(V - 1, sl * per + per - 1)][b % 3]] = 50.0
+            elif caso == 'ties':
+                lg[b, [b * 7, V - 1 - k * 13]] = 50.0
+            elif caso == 'nan' and b % 2 == 0:
+                lg[b, 1000 + k] = float('nan')
+            elif caso == 'neg_inf' and b == 1:
+                lg[b] = -float('inf')
+        lg = lg.to(DEV)
+        pdev = torch.tensor([pos], dtype=torch.int64, device=DEV)
+        for i in range(2):
+            e = ests[i]
+            ops.muestrear(lg, textos[i], pdev, pos0 + steps, L0, e.piezas, e.terminado, e.paso_fin, e.trabajo, e.bits,
+                          1.0, 1, 1.0, 1.0, 64, 5 + k, cita=sets[i], prob=e.prob if i == 1 else None)
+        torch.cuda.synchronize()
+        assert torch.equal(ests[0].piezas, ests[1].piezas), (k, ests[0].piezas.tolist(), ests[1].piezas.tolist())
+        if caso == 'unique':
+            assert torch.equal(ests[0].piezas.cpu(), lg.cpu().argmax(1)), k
+    assert torch.equal(textos[0], textos[1])
+    whole = ops.ConjuntoNgramas(B, nq, V, pos0 + steps + 1, DEV)
+    whole.agregar_texto(textos[0][:, :pos0 + steps].contiguous())
+    assert _set_contents(sets[0]) == _set_contents(sets[1]) == _set_contents(whole)
+
+
 @pytest.mark.parametrize('V,k,p,ntie', [(300, 0, 0.6, 4), (10000, 0, 0.5, 9), (20000, 0, 0.62, 6), (30000, 3000, 0.55, 5),
                                        (3000, 40, 0.8, 7)])
 def test_sampler_top_p_ties(V, k, p, ntie):
