@@ -83,7 +83,20 @@ __device__ __forceinline__ float split_sum(const float* p, int splits, int64_t s
 
 constexpr int kMaxTaps = 8;                  // ring taps a thread loads ahead of the statistics (k - 1 <= 8)
 
-__global__ __launch_bounds__(kPrepThreads) void k_prep_mix(const float* h, int64_t ldh, const float* ring,
+// A block whose last kernel was left to the next block's first (asrn_block_step_ex with finish = 0): its second
+// feed-forward product's partials and what k_finish_res would add them to
+struct Pending {
+  const float* part;  // (splits, B, d), null: no pending block
+  int splits;
+  const float* bias; const float* h1; const float* z;
+  float* ring;        // its ring (B, d, km1) takes z at slot pos mod km1
+  int km1;
+  float* out;         // its output, written here
+};
+
+// With pv.part: the row is the pending block's output h1 + (sum of the splits + bias), formed as k_finish_res forms
+// it, written to pv.out, and the pending block's z enters its ring (k_finish_res's work, one row per workgroup).
+__global__ __launch_bounds__(kPrepThreads) void k_prep_mix(const float* h, int64_t ldh, Pending pv, const float* ring,
                                                            const int64_t* pos_p, const float* w, const float* bia,
                                                            float eps, int d, int k, float* z, float* x1) {
   __shared__ float red[kPrepWaves];
@@ -91,16 +104,32 @@ __global__ __launch_bounds__(kPrepThreads) void k_prep_mix(const float* h, int64
   const int tid = threadIdx.x;
   const float* row = h + b * ldh;
   const int km1 = k - 1;
-  const int first = km1 > 0 ? (int)(*pos_p % km1) : 0;     // the slot of tap 0; tap i is at (first + i) mod (k - 1)
+  const int64_t pos = *pos_p;
+  const int first = km1 > 0 ? (int)(pos % km1) : 0;        // the slot of tap 0; tap i is at (first + i) mod (k - 1)
   auto slot = [&](int i) { return first + i < km1 ? first + i : first + i - km1; };
   // the row and, for k <= 9, its ring taps, loaded together before the statistics
   float v[kRowVals], tap[kRowVals][kMaxTaps];
 #pragma unroll
   for (int j = 0; j < kRowVals; ++j) {
     const int c = tid + j * kPrepThreads;
-    v[j] = c < d ? row[c] : 0.f;
+    if (pv.part)
+      v[j] = c < d ? pv.h1[b * d + c] + (split_sum(pv.part + b * d + c, pv.splits, gridDim.x * (int64_t)d) +
+                                         pv.bias[c])
+                   : 0.f;
+    else
+      v[j] = c < d ? row[c] : 0.f;
 #pragma unroll
     for (int i = 0; i < kMaxTaps; ++i) tap[j][i] = (c < d && i < km1) ? ring[(b * d + c) * km1 + slot(i)] : 0.f;
+  }
+  if (pv.part) {
+    const int ps = pv.km1 > 0 ? (int)(pos % pv.km1) : 0;
+#pragma unroll
+    for (int j = 0; j < kRowVals; ++j) {
+      const int c = tid + j * kPrepThreads;
+      if (c >= d) continue;
+      pv.out[b * d + c] = v[j];
+      if (pv.km1 > 0) pv.ring[(b * d + c) * pv.km1 + ps] = pv.z[b * d + c];
+    }
   }
   float m, r;
   row_stats(v, d, eps, red, &m, &r);
@@ -262,37 +291,76 @@ extern "C" int64_t asrn_block_step_workspace(int64_t B, int32_t d, int32_t ff) {
   return 4 * B * ((int64_t)kMaxSplits * d + (int64_t)ff + (int64_t)splits_for(d, ff) * d);
 }
 
+namespace asrn {
+namespace {
+
+int block_step(const float* h, int64_t ldh, const float* prev_h1, const float* prev_b2, const float* prev_z,
+               float* prev_ring, int32_t prev_k, int32_t prev_ff, float* prev_out, float* ring, const int64_t* pos,
+               int64_t B, int32_t d, int32_t k, int32_t ff, const float* ln1_w, const float* ln1_b,
+               const float* conv_w, const float* conv_b, const float* ln2_w, const float* ln2_b, const float* w1,
+               const float* b1, const float* w2, const float* b2, float eps, float* z, float* x1, float* h1, float* x2,
+               float* out, int32_t finish, void* workspace, int64_t workspace_bytes, hipStream_t st,
+               const char* what) {
+  ASRN_REQUIRE(B >= 1 && B <= (int64_t(1) << 20) && d >= 1 && k >= 1 && ff >= 1 && (prev_h1 || ldh >= d),
+               "%s: bad sizes B=%lld d=%d k=%d ff=%d", what, (long long)B, d, k, ff);
+  ASRN_REQUIRE((int64_t)d * k <= (int64_t(1) << 30) && ff <= (1 << 30), "%s: sizes too large", what);
+  ASRN_REQUIRE(d <= kRowVals * kPrepThreads, "%s: d=%d above %d", what, d, kRowVals * kPrepThreads);
+  ASRN_REQUIRE((h || prev_h1) && pos && ln1_w && ln1_b && conv_w && conv_b && ln2_w && ln2_b && w1 && b1 && w2 &&
+               b2 && z && x1 && h1 && x2 && out && (k == 1 || ring), "%s: null pointer", what);
+  ASRN_REQUIRE(!prev_h1 || (prev_b2 && prev_z && prev_out && prev_k >= 1 && prev_ff >= 1 && prev_ff <= (1 << 30) &&
+                            (prev_k == 1 || prev_ring)),
+               "%s: a pending block needs its b2, z, out, k >= 1, ff >= 1 and (k > 1) its ring", what);
+  const int64_t need = asrn_block_step_workspace(B, d, prev_h1 && prev_ff > ff ? prev_ff : ff);
+  ASRN_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+               "%s: workspace of %lld bytes needed (asrn_block_step_workspace)", what, (long long)need);
+  const int s1 = splits_for(d, d * k), s3 = splits_for(d, ff);
+  float* p1 = (float*)workspace;
+  float* hid = p1 + (int64_t)kMaxSplits * B * d;
+  float* p3 = hid + (int64_t)B * ff;
+  Pending pv = {};
+  if (prev_h1)   // the pending block's partials, where its call (same workspace, same B and d) left them
+    pv = Pending{hid + (int64_t)B * prev_ff, splits_for(d, prev_ff), prev_b2, prev_h1, prev_z, prev_ring, prev_k - 1,
+                 prev_out};
+  hipLaunchKernelGGL(k_prep_mix, dim3((unsigned)B), dim3(kPrepThreads), 0, st, prev_h1 ? prev_out : h,
+                     prev_h1 ? (int64_t)d : ldh, pv, ring, pos, ln1_w, ln1_b, eps, d, k, z, x1);
+  if (int rc = check_launch(what)) return rc;
+  if (int rc = launch_part(Part{x1, conv_w, p1, nullptr, (int)B, d * k, d, s1}, st, what)) return rc;
+  // the residual input h: the pending block's output, which k_prep_mix wrote, or h itself
+  hipLaunchKernelGGL(k_finish_mix, dim3((unsigned)B), dim3(kPrepThreads), 0, st, p1, s1, B, conv_b,
+                     prev_h1 ? prev_out : h, prev_h1 ? (int64_t)d : ldh, ln2_w, ln2_b, eps, d, h1, x2);
+  if (int rc = check_launch(what)) return rc;
+  if (int rc = launch_part(Part{x2, w1, hid, b1, (int)B, d, ff, 1}, st, what)) return rc;
+  if (int rc = launch_part(Part{hid, w2, p3, nullptr, (int)B, ff, d, s3}, st, what)) return rc;
+  if (!finish) return 0;                           // k_finish_res's work left to the next block's k_prep_mix
+  hipLaunchKernelGGL(k_finish_res, dim3((unsigned)B), dim3(kPrepThreads), 0, st, p3, s3, B, b2, h1, z, pos, d, k - 1,
+                     ring, out);
+  return check_launch(what);
+}
+
+}  // namespace
+}  // namespace asrn
+
 extern "C" int asrn_block_step(const float* h, int64_t ldh, float* ring, const int64_t* pos, int64_t B, int32_t d,
                                int32_t k, int32_t ff, const float* ln1_w, const float* ln1_b, const float* conv_w,
                                const float* conv_b, const float* ln2_w, const float* ln2_b, const float* w1,
                                const float* b1, const float* w2, const float* b2, float eps, float* z, float* x1,
                                float* h1, float* x2, float* out, void* workspace, int64_t workspace_bytes,
                                void* stream) {
-  ASRN_REQUIRE(B >= 1 && B <= (int64_t(1) << 20) && d >= 1 && k >= 1 && ff >= 1 && ldh >= d,
-               "asrn_block_step: bad sizes B=%lld d=%d k=%d ff=%d", (long long)B, d, k, ff);
-  ASRN_REQUIRE((int64_t)d * k <= (int64_t(1) << 30) && ff <= (1 << 30), "asrn_block_step: sizes too large");
-  ASRN_REQUIRE(d <= kRowVals * kPrepThreads, "asrn_block_step: d=%d above %d", d, kRowVals * kPrepThreads);
-  ASRN_REQUIRE(h && pos && ln1_w && ln1_b && conv_w && conv_b && ln2_w && ln2_b && w1 && b1 && w2 && b2 && z && x1 &&
-               h1 && x2 && out && (k == 1 || ring), "asrn_block_step: null pointer");
-  ASRN_REQUIRE(workspace != nullptr && workspace_bytes >= asrn_block_step_workspace(B, d, ff),
-               "asrn_block_step: workspace of %lld bytes needed (asrn_block_step_workspace)",
-               (long long)asrn_block_step_workspace(B, d, ff));
-  const hipStream_t st = (hipStream_t)stream;
-  const int s1 = splits_for(d, d * k), s3 = splits_for(d, ff);
-  float* p1 = (float*)workspace;
-  float* hid = p1 + (int64_t)kMaxSplits * B * d;
-  float* p3 = hid + (int64_t)B * ff;
-  hipLaunchKernelGGL(k_prep_mix, dim3((unsigned)B), dim3(kPrepThreads), 0, st, h, ldh, ring, pos, ln1_w, ln1_b, eps, d,
-                     k, z, x1);
-  if (int rc = check_launch("asrn_block_step (prep)")) return rc;
-  if (int rc = launch_part(Part{x1, conv_w, p1, nullptr, (int)B, d * k, d, s1}, st, "asrn_block_step (conv)"))
-    return rc;
-  hipLaunchKernelGGL(k_finish_mix, dim3((unsigned)B), dim3(kPrepThreads), 0, st, p1, s1, B, conv_b, h, ldh, ln2_w,
-                     ln2_b, eps, d, h1, x2);
-  if (int rc = check_launch("asrn_block_step (mix)")) return rc;
-  if (int rc = launch_part(Part{x2, w1, hid, b1, (int)B, d, ff, 1}, st, "asrn_block_step (ff1)")) return rc;
-  if (int rc = launch_part(Part{hid, w2, p3, nullptr, (int)B, ff, d, s3}, st, "asrn_block_step (ff2)")) return rc;
-  hipLaunchKernelGGL(k_finish_res, dim3((unsigned)B), dim3(kPrepThreads), 0, st, p3, s3, B, b2, h1, z, pos, d, k - 1,
-                     ring, out);
-  return check_launch("asrn_block_step (residual)");
+  ASRN_REQUIRE(h, "asrn_block_step: null pointer");
+  return block_step(h, ldh, nullptr, nullptr, nullptr, nullptr, 0, 0, nullptr, ring, pos, B, d, k, ff, ln1_w, ln1_b,
+                    conv_w, conv_b, ln2_w, ln2_b, w1, b1, w2, b2, eps, z, x1, h1, x2, out, 1, workspace,
+                    workspace_bytes, (hipStream_t)stream, "asrn_block_step");
+}
+
+extern "C" int asrn_block_step_ex(const float* h, int64_t ldh, const float* prev_h1, const float* prev_b2,
+                                  const float* prev_z, float* prev_ring, int32_t prev_k, int32_t prev_ff,
+                                  float* prev_out, float* ring, const int64_t* pos, int64_t B, int32_t d, int32_t k,
+                                  int32_t ff, const float* ln1_w, const float* ln1_b, const float* conv_w,
+                                  const float* conv_b, const float* ln2_w, const float* ln2_b, const float* w1,
+                                  const float* b1, const float* w2, const float* b2, float eps, float* z, float* x1,
+                                  float* h1, float* x2, float* out, int32_t finish, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  return block_step(h, ldh, prev_h1, prev_b2, prev_z, prev_ring, prev_k, prev_ff, prev_out, ring, pos, B, d, k, ff,
+                    ln1_w, ln1_b, conv_w, conv_b, ln2_w, ln2_b, w1, b1, w2, b2, eps, z, x1, h1, x2, out, finish,
+                    workspace, workspace_bytes, (hipStream_t)stream, "asrn_block_step_ex");
 }

@@ -80,14 +80,16 @@ class EscritorModelo:
         self.pos = torch.full((1,), L0, dtype=torch.int64, device=x0.device)
         return m.head(m.ln_f(h[:, -1]))
 
-    def _bloque(self, i, blq, h, mem_i, pos):
-        """Block i's step on the new token's state h (B, d) at position pos: three fused kernels for 'conv' blocks in
-        fp32 (asrn_block_step, the window a ring), else PyTorch ops on a window that shifts by one row."""
+    def _bloque(self, i, blq, h, mem_i, pos, previo=None, terminar=True):
+        """Block i's step on the new token's state h (B, d) at position pos: six fused kernels for 'conv' blocks in
+        fp32 (asrn_block_step, the window a ring), else PyTorch ops on a window that shifts by one row. previo and
+        terminar (fused blocks): the pending block before this one and whether to leave this one pending, as
+        ops.paso_bloque takes them."""
         if self.fusion[i]:
-            if not ops.paso_bloque_ok(blq, h):
+            if not ops.paso_bloque_ok(blq, h if previo is None else previo.out):
                 raise ValueError('EscritorModelo: the prompt ran the fused block step (fp32, no autocast); every step '
                                  'must run the same way')
-            return ops.paso_bloque(blq, h, self.anillos[i], pos, self.espacio)
+            return ops.paso_bloque(blq, h, self.anillos[i], pos, self.espacio, previo=previo, terminar=terminar)
         z = blq.ln1(h)
         ventana = torch.cat([self.ventanas[i], z.unsqueeze(-1)], dim=-1)            # (B, d, k)
         if blq.mezcla == 'conv':
@@ -120,8 +122,13 @@ class EscritorModelo:
         h = e_t
         capas = iter(self.capas)
         k = 0
+        pendiente = None
+        nb = len(m.bloques)
         for i, blq in enumerate(m.bloques):
-            h = self._bloque(i, blq, h, k, pos)
+            # two fused blocks in a row: the first's last launch is done by the second's first
+            encadenar = self.fusion[i] and i not in m.pos_largo and i + 1 < nb and self.fusion[i + 1]
+            r = self._bloque(i, blq, h, k, pos, previo=pendiente, terminar=not encadenar)
+            pendiente, h = (r, None) if encadenar else (None, r)
             k += blq.mezcla == 'memoria'
             if i in m.pos_largo:
                 h = next(capas)._cuerpo(e_t, self.e_ult if e_prev is None else e_prev, h, pieza, pos, t_max=t_max)

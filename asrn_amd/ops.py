@@ -1091,9 +1091,23 @@ def espacio_bloque(B, d, ff, dev):
     return torch.empty(int(query('asrn_block_step_workspace', B, d, ff)), dtype=torch.uint8, device=dev)
 
 
-def paso_bloque(blq, h, anillo, pos, espacio):
+class BloquePendiente:
+    """A block step whose last launch was left to the next block's first (paso_bloque(..., terminar=False)): `out` is
+    the (B, d) buffer its output will be written into, and it must be passed as `previo` to the next paso_bloque call,
+    with the same workspace, before anything reads `out`."""
+
+    def __init__(self, out, h1, b2, z, anillo, k, ff):
+        self.out, self.h1, self.b2, self.z, self.anillo, self.k, self.ff = out, h1, b2, z, anillo, k, ff
+
+
+def paso_bloque(blq, h, anillo, pos, espacio, previo=None, terminar=True):
     """The block's step for rows h (B, d) at position pos (a one-element int64 device tensor): returns (B, d); the ring
-    anillo (B, d, k - 1) of LayerNorm1 rows (position t at slot t mod (k - 1)) takes this position's row."""
+    anillo (B, d, k - 1) of LayerNorm1 rows (position t at slot t mod (k - 1)) takes this position's row.
+    previo: a BloquePendiente, the block just before this one, whose output is this block's input (h is then None):
+    this block's first kernel finishes it (asrn_block_step_ex). terminar=False: returns this block as a
+    BloquePendiente instead of its output, for the next block to finish."""
+    if previo is not None:
+        h = previo.out
     dev = _dev(h)
     B, d = h.shape
     k = blq.k
@@ -1104,10 +1118,20 @@ def paso_bloque(blq, h, anillo, pos, espacio):
                                    blq.ln2.bias, blq.ff[0].weight, blq.ff[0].bias, blq.ff[2].weight, blq.ff[2].bias)]
     z, h1, x2, out = (torch.empty((B, d), dtype=torch.float32, device=dev) for _ in range(4))
     x1 = torch.empty((B, d * k), dtype=torch.float32, device=dev)
-    call('asrn_block_step', ptr(h), h.stride(0), ptr(anillo), ptr(pos), B, d, k, ff, *[ptr(w) for w in ws],
-         float(blq.ln1.eps), ptr(z), ptr(x1), ptr(h1), ptr(x2), ptr(out), ptr(espacio), espacio.numel(),
-         stream_of(dev))
-    return out
+    if previo is None and terminar:
+        call('asrn_block_step', ptr(h), h.stride(0), ptr(anillo), ptr(pos), B, d, k, ff, *[ptr(w) for w in ws],
+             float(blq.ln1.eps), ptr(z), ptr(x1), ptr(h1), ptr(x2), ptr(out), ptr(espacio), espacio.numel(),
+             stream_of(dev))
+        return out
+    pv = previo
+    call('asrn_block_step_ex', None if pv else ptr(h), h.stride(0), ptr(pv.h1) if pv else None,
+         ptr(pv.b2) if pv else None, ptr(pv.z) if pv else None, ptr(pv.anillo) if pv else None, pv.k if pv else 0,
+         pv.ff if pv else 0, ptr(pv.out) if pv else None, ptr(anillo), ptr(pos), B, d, k, ff, *[ptr(w) for w in ws],
+         float(blq.ln1.eps), ptr(z), ptr(x1), ptr(h1), ptr(x2), ptr(out), 1 if terminar else 0, ptr(espacio),
+         espacio.numel(), stream_of(dev))
+    if terminar:
+        return out
+    return BloquePendiente(out, h1, ws[9], z, anillo, k, ff)
 
 
 # ---------------------------------------------------------------------------------------------------------------------

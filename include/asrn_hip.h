@@ -475,6 +475,21 @@ int asrn_block_step(const float* h, int64_t ldh, float* ring, const int64_t* pos
                     const float* ln2_w, const float* ln2_b, const float* w1, const float* b1, const float* w2,
                     const float* b2, float eps, float* z, float* x1, float* h1, float* x2, float* out,
                     void* workspace, int64_t workspace_bytes, void* stream);
+/* block_step_ex: asrn_block_step for two blocks that follow each other (no layer between them), no counterpart in the
+ * reference's FFI: the first block's last launch (its output and its ring's new row) is done by the second block's
+ * first. finish = 0 leaves this block's output unfinished: out and the ring's row at pos are not written, and the
+ * second feed-forward product's partials stay in the workspace. A call with prev_h1 != NULL then takes the input
+ * from that pending block (the previous call, with this same workspace, B and d): its output prev_h1 + partials +
+ * prev_b2 (in asrn_block_step's order) is formed here, written to prev_out (B, d) and used as h (h and ldh are then
+ * ignored), and prev_z enters prev_ring at slot pos mod (prev_k - 1); prev_ff is its feed-forward width. Every
+ * pending block must be taken by the next call. workspace: asrn_block_step_workspace(B, d, max(ff, prev_ff)). */
+int asrn_block_step_ex(const float* h, int64_t ldh, const float* prev_h1, const float* prev_b2, const float* prev_z,
+                       float* prev_ring, int32_t prev_k, int32_t prev_ff, float* prev_out, float* ring,
+                       const int64_t* pos, int64_t B, int32_t d, int32_t k, int32_t ff, const float* ln1_w,
+                       const float* ln1_b, const float* conv_w, const float* conv_b, const float* ln2_w,
+                       const float* ln2_b, const float* w1, const float* b1, const float* w2, const float* b2,
+                       float eps, float* z, float* x1, float* h1, float* x2, float* out, int32_t finish,
+                       void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- the model's loss: cross-entropy ---------------------------------------------------------------------------
  * Replaces F.cross_entropy(logits.float().reshape(-1, V), y.reshape(-1), ignore_index) of ModeloASRN.perdida and the

@@ -425,6 +425,44 @@ def test_block_step_equals_whole_text_block(B, d, k, ff, L):
             assert torch.allclose(anillo[:, :, (L - 1) % (k - 1)], blq.ln1(h[:, -1]), atol=1e-5)
 
 
+@pytest.mark.parametrize('B,d,ks,ffs', [(16, 768, (4, 4, 4), (1536, 1536, 1536)), (20, 96, (4, 1, 3), (40, 200, 64)),
+                                         (3, 2080, (2, 12, 1), (72, 300, 48))])
+def test_block_step_chained_equals_separate(B, d, ks, ffs):
+    """Three blocks in a row with each one's last launch done by the next one's first (asrn_block_step_ex: finish = 0,
+    then the pending block taken as the input) against three asrn_block_step calls, bit for bit: every block's output
+    and ring. The blocks differ in k (k = 1: no ring) and in the feed-forward width (the pending partials sit where
+    the previous call's width put them)."""
+    say('block step chained', B, d, ks, ffs)
+    torch.manual_seed(B + d)
+    blqs = []
+    with torch.no_grad():
+        for k, ff in zip(ks, ffs):
+            blq = asrn_amd.BloqueLocal(d, k, ff).to(DEV)
+            for p in blq.parameters():
+                p.add_(torch.randn_like(p) * 0.1)
+            blqs.append(blq)
+        h = torch.randn(B, d, device=DEV)
+        anillos = [torch.randn(B, d, k - 1, device=DEV) if k > 1 else None for k in ks]
+        anillos2 = [a.clone() if a is not None else None for a in anillos]
+        pos = torch.tensor([7], dtype=torch.int64, device=DEV)
+        espacio = ops.espacio_bloque(B, d, max(ffs), DEV)
+        x, outs = h, []
+        for blq, a in zip(blqs, anillos):
+            x = ops.paso_bloque(blq, x, a, pos, espacio)
+            outs.append(x)
+        pend, outs2 = None, []
+        for i, (blq, a) in enumerate(zip(blqs, anillos2)):
+            r = ops.paso_bloque(blq, h if i == 0 else None, a, pos, espacio, previo=pend, terminar=i == len(blqs) - 1)
+            if pend is not None:
+                outs2.append(pend.out)
+            pend = r if i < len(blqs) - 1 else None
+        outs2.append(r)
+        torch.cuda.synchronize()
+        for i in range(len(blqs)):
+            assert torch.equal(outs[i], outs2[i]), i
+            assert (anillos[i] is None) or torch.equal(anillos[i], anillos2[i]), i
+
+
 @pytest.mark.parametrize('mezcla', ['conv', 'memoria'])
 def test_escribir_equals_whole_text(mezcla):
     """tests/test_nucleo.py:105-115: the logits of every step equal the model on the whole written text."""

@@ -152,6 +152,16 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert 'grow it first' in _err(lib)
     assert lib.asrn_hawkes_table_grow(N, N, N, 8, 256, N, N, N, 128, N) != 0
     assert 'growing' in _err(lib)
+    # the chained block step: a pending block needs its parts; the workspace covers the wider of the two widths
+    P1 = ctypes.c_void_p(16)                                   # a non-null pointer never dereferenced on these paths
+    blk = [P1] * 10
+    assert lib.asrn_block_step_ex(N, 0, P1, N, P1, P1, 4, 64, P1, P1, P1, 2, 64, 4, 64, *blk, 1e-5, *([P1] * 5), 1,
+                                  P1, 1 << 30, N) != 0
+    assert 'pending block' in _err(lib)
+    need = lib.asrn_block_step_workspace(2, 64, 512)
+    assert lib.asrn_block_step_ex(N, 0, P1, P1, P1, P1, 4, 512, P1, P1, P1, 2, 64, 4, 64, *blk, 1e-5, *([P1] * 5), 1,
+                                  P1, need - 4, N) != 0
+    assert 'workspace' in _err(lib)
     # the fused attention + repetition step: the attention's checks, then the step's n and table capacity
     att = [2, 100, 50, N, 64, 14, 16, 4, 8, 4, 32, 0.1, 0.25, 1, N, N, N, N]
     assert lib.asrn_decode_attend_repeat(*([N] * 11), 2, 100, 100, *att[3:], *([N] * 4), 4, 128, *([N] * 6), 0,
