@@ -107,11 +107,13 @@ __global__ __launch_bounds__(kPrepThreads) void k_prep_mix(const float* h, int64
   const int64_t pos = *pos_p;
   const int first = km1 > 0 ? (int)(pos % km1) : 0;        // the slot of tap 0; tap i is at (first + i) mod (k - 1)
   auto slot = [&](int i) { return first + i < km1 ? first + i : first + i - km1; };
-  // the row and, for k <= 9, its ring taps, loaded together before the statistics
-  float v[kRowVals], tap[kRowVals][kMaxTaps];
+  // the row, the LayerNorm's weights and, for k <= 9, the ring taps, loaded together before the statistics
+  float v[kRowVals], tap[kRowVals][kMaxTaps], lw[kRowVals], lb[kRowVals];
 #pragma unroll
   for (int j = 0; j < kRowVals; ++j) {
     const int c = tid + j * kPrepThreads;
+    lw[j] = c < d ? w[c] : 0.f;
+    lb[j] = c < d ? bia[c] : 0.f;
     if (pv.part)
       v[j] = c < d ? pv.h1[b * d + c] + (split_sum(pv.part + b * d + c, pv.splits, gridDim.x * (int64_t)d) +
                                          pv.bias[c])
@@ -137,7 +139,7 @@ __global__ __launch_bounds__(kPrepThreads) void k_prep_mix(const float* h, int64
   for (int j = 0; j < kRowVals; ++j) {
     const int c = tid + j * kPrepThreads;
     if (c >= d) continue;
-    const float zc = (v[j] - m) * r * w[c] + bia[c];
+    const float zc = (v[j] - m) * r * lw[j] + lb[j];
     z[b * d + c] = zc;
     float* xr = x1 + (b * d + c) * k;
 #pragma unroll
@@ -156,10 +158,12 @@ __global__ __launch_bounds__(kPrepThreads) void k_finish_mix(const float* part, 
   __shared__ float red[kPrepWaves];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
-  float v[kRowVals];
+  float v[kRowVals], lw[kRowVals], lb[kRowVals];
 #pragma unroll
-  for (int j = 0; j < kRowVals; ++j) {
+  for (int j = 0; j < kRowVals; ++j) {             // the LayerNorm's weights loaded with the row
     const int c = tid + j * kPrepThreads;
+    lw[j] = c < d ? w2[c] : 0.f;
+    lb[j] = c < d ? b2[c] : 0.f;
     v[j] = c < d ? h[b * ldh + c] + gelu_erf(split_sum(part + b * d + c, splits, B * d) + bias[c]) : 0.f;
     if (c < d) h1[b * d + c] = v[j];
   }
@@ -168,7 +172,7 @@ __global__ __launch_bounds__(kPrepThreads) void k_finish_mix(const float* part, 
 #pragma unroll
   for (int j = 0; j < kRowVals; ++j) {
     const int c = tid + j * kPrepThreads;
-    if (c < d) x2[b * d + c] = (v[j] - m) * r * w2[c] + b2[c];
+    if (c < d) x2[b * d + c] = (v[j] - m) * r * lw[j] + lb[j];
   }
 }
 

@@ -52,8 +52,11 @@ __device__ __forceinline__ int kind_rows(const ProdArgs& a, int k) {
   return k == 0 ? a.d : (k == 1 ? a.m : (k <= 3 ? a.mc : a.cf));
 }
 
-// LayerNorm of the staged rows x[tok][.] (d4 float4 each) in place: wave w takes tokens w, w + 4, ...
-__device__ __forceinline__ void layer_norm_rows(const ProdArgs& a, float4* xs, int ntok, int d4) {
+// LayerNorm of the staged rows x[tok][.] (d4 float4 each) in place: wave w takes tokens w, w + 4, ...; lw and lb the
+// lane's columns lane + 64 k of the weights, loaded beforehand
+template <int D4>
+__device__ __forceinline__ void layer_norm_rows(const ProdArgs& a, float4* xs, int ntok, int d4, const float4 (&lw)[D4],
+                                                const float4 (&lb)[D4]) {
   const int lane = lane_id(), wave = threadIdx.x >> 6;
   const float inv_d = 1.f / (float)a.d;
   for (int j = wave; j < ntok; j += kProdWaves) {
@@ -67,8 +70,11 @@ __device__ __forceinline__ void layer_norm_rows(const ProdArgs& a, float4* xs, i
       v += dot4(c, c);
     }
     const float rstd = rsqrtf(wave_sum_u(v) * inv_d + a.eps);
-    for (int q = lane; q < d4; q += kWave) {
-      const float4 w = ((const float4*)a.lnw)[q], b = ((const float4*)a.lnb)[q];
+#pragma unroll
+    for (int k = 0; k < D4; ++k) {
+      const int q = lane + kWave * k;
+      if (q >= d4) continue;
+      const float4 w = lw[k], b = lb[k];
       x[q] = make_float4((x[q].x - mean) * rstd * w.x + b.x, (x[q].y - mean) * rstd * w.y + b.y,
                          (x[q].z - mean) * rstd * w.z + b.z, (x[q].w - mean) * rstd * w.w + b.w);
     }
@@ -92,20 +98,17 @@ __global__ __launch_bounds__(kProdThreads) void k_produce_rows(ProdArgs a) {
   const int nrows = kind_rows(a, k);
   const int64_t b0 = (int64_t)blockIdx.y * kProdTok;
   const int ntok = a.B - b0 < kProdTok ? (int)(a.B - b0) : kProdTok;
-  // stage the input vectors
-  const float* src = k == 3 ? a.e_prev : (k >= 4 ? a.h : a.e);
-  for (int i = threadIdx.x; i < ntok * d4; i += kProdThreads) {
-    const int j = i / d4, q = i - j * d4;
-    xs[j * d4 + q] = ((const float4*)(src + (b0 + j) * a.d))[q];
-  }
-  __syncthreads();
-  if (k >= 4) {
-    layer_norm_rows(a, xs, ntok, d4);
-    __syncthreads();
-  }
-  // wave w dots row w of the block with every token
+  // wave w dots row w of the block with every token: the row, and for the LayerNorm kinds the LayerNorm's weights,
+  // are loaded first (they do not depend on the inputs staged next)
   const int r = blk * kProdRows + wave;
-  float4 w[D4];
+  float4 w[D4], lw[D4], lb[D4];
+#pragma unroll
+  for (int kk = 0; kk < D4; ++kk) {
+    const int q = lane + kWave * kk;
+    const bool in = k >= 4 && q < d4;
+    lw[kk] = in ? ((const float4*)a.lnw)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    lb[kk] = in ? ((const float4*)a.lnb)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   {
     const float* row = k == 0 ? a.wv + (int64_t)r * a.d
                      : (k == 1 ? a.ww + (int64_t)r * a.d
@@ -117,6 +120,17 @@ __global__ __launch_bounds__(kProdThreads) void k_produce_rows(ProdArgs a) {
       const int q = lane + kWave * kk;
       w[kk] = r < nrows && q < d4 ? ((const float4*)row)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+  }
+  // stage the input vectors
+  const float* src = k == 3 ? a.e_prev : (k >= 4 ? a.h : a.e);
+  for (int i = threadIdx.x; i < ntok * d4; i += kProdThreads) {
+    const int j = i / d4, q = i - j * d4;
+    xs[j * d4 + q] = ((const float4*)(src + (b0 + j) * a.d))[q];
+  }
+  __syncthreads();
+  if (k >= 4) {
+    layer_norm_rows(a, xs, ntok, d4, lw, lb);
+    __syncthreads();
   }
   for (int j = 0; j < ntok; ++j) {
     const int64_t b = b0 + j;

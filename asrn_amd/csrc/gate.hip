@@ -101,12 +101,11 @@ __device__ __forceinline__ void stage_token_rows(const GateArgs& a, int64_t t0, 
   }
 }
 
-// phase 1: token t's features into f (LDS row), its info into ti; P the staged small parameters, vis and haw the
-// token's staged rows
-__device__ void token_features(const GateArgs& a, int64_t t, const float* P, const float* vis, const float* haw,
-                               float* f, TokenInfo* ti) {
+// phase 1: a token's features into f (LDS row), its info into ti, from its signals g (peso_total, mejor, pico,
+// peso_ctx) and streak ra; P the staged small parameters, vis and haw the token's staged rows
+__device__ void token_features_of(const GateArgs& a, float4 g, float ra, const float* P, const float* vis,
+                                  const float* haw, float* f, TokenInfo* ti) {
   const int n = a.n, S = 6 + 2 * n + a.nodes;
-  const float4 g = ((const float4*)a.sig)[t];     // peso_total, mejor, pico, peso_ctx
   const float pt = g.x;
   float mejor = pt > 0.f ? g.y : 0.f;
   if (a.mejor_max >= 0.f) mejor = fminf(fmaxf(mejor, -a.mejor_max), a.mejor_max);
@@ -121,7 +120,6 @@ __device__ void token_features(const GateArgs& a, int64_t t, const float* P, con
     f[6 + n + j] = log1pf(haw[j]);
   }
   const float top = (float)(a.nodes - 1);
-  const float ra = a.racha[t];
   const float xr = log1pf(ra) / a.paso;
   const float x = fminf(xr, top);
   float fi = x != x ? 0.f : floorf(x);
@@ -134,6 +132,12 @@ __device__ void token_features(const GateArgs& a, int64_t t, const float* P, con
   ti->small = small;
   ti->dxdr = xr <= top ? 1.f / ((1.f + ra) * a.paso) : 0.f;
   ti->i = i;
+}
+
+// the same for token t, its signals and streak read here
+__device__ void token_features(const GateArgs& a, int64_t t, const float* P, const float* vis, const float* haw,
+                               float* f, TokenInfo* ti) {
+  token_features_of(a, ((const float4*)a.sig)[t], a.racha[t], P, vis, haw, f, ti);
 }
 
 __device__ __forceinline__ float capped(float l, float tope) { return tope > 0.f ? tope * tanhf(l / tope) : l; }
@@ -325,10 +329,14 @@ __device__ __forceinline__ f4v ld4_rows(const float* m, int64_t row, int64_t nro
   return v;
 }
 
+constexpr int kStepWaves = 8;                // a workgroup's waves, each an eighth of the depth in one round of loads
+constexpr int kStepThreads = kStepWaves * kWave;
+constexpr int kStepTokPerWave = kStepTok / kStepWaves;   // tokens whose h . w_g a wave forms
+
 template <int D4, int U>
-__global__ __launch_bounds__(kGateThreads) void k_gate_step(GateArgs a, const float* __restrict__ salida,
+__global__ __launch_bounds__(kStepThreads) void k_gate_step(GateArgs a, const float* __restrict__ salida,
                                                             const float* __restrict__ wo) {
-  __shared__ float tile[kGateWaves][kStepTok * kStepTok];
+  __shared__ float tile[kStepWaves][kStepTok * kStepTok];
   __shared__ float feat[kStepTok][kFeatStride];
   __shared__ TokenInfo info[kStepTok];
   __shared__ float P[kGateCols];
@@ -339,65 +347,83 @@ __global__ __launch_bounds__(kGateThreads) void k_gate_step(GateArgs a, const fl
   const int n0 = blockIdx.x * kStepTok;
   const int64_t t0 = (int64_t)blockIdx.y * kStepTok;
   const int nt = a.BL - t0 < kStepTok ? (int)(a.BL - t0) : kStepTok;
-  // the small parameters and the tile's seen and Hawkes rows
-  stage_small_params(a, P);
-  for (int i = tid; i < nt * a.n; i += kGateThreads) {
-    vh[0][i] = a.vistos[t0 * a.n + i];
-    vh[1][i] = a.hawkes[t0 * a.n + i];
-  }
-  // A's tile: wave w sums depth [w per, (w + 1) per) in one round of U steps of 16 columns
-  const int per = ((d + kGateWaves - 1) / kGateWaves + 15) & ~15;
+  // Every load first, so that the kernel waits for memory once: the product's operands (wave w: depth [w per,
+  // (w + 1) per) in U steps of 16 columns), the h . w_g operands (wave w: tokens w + kStepWaves j), the small
+  // parameters, the tokens' seen and Hawkes rows, signals and streaks, and the h values the epilogue adds to.
+  const int per = ((d + kStepWaves - 1) / kStepWaves + 15) & ~15;
   const int wb = wave * per, we = wb + per < d ? wb + per : d;
   const int i16 = lane & 15, q4 = lane >> 4;
-  f4v acc = {0.f, 0.f, 0.f, 0.f};
-  for (int k = wb; k < we; k += 16 * U) {
-    f4v x[U], w[U];
+  f4v x[U], w[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kk = k + 16 * u + 4 * q4;
-      x[u] = ld4_rows(salida, t0 + i16, a.BL, d, kk, we);
-      w[u] = ld4_rows(wo, n0 + i16, d, d, kk, we);
-    }
+  for (int u = 0; u < U; ++u) {
+    const int kk = wb + 16 * u + 4 * q4;
+    x[u] = ld4_rows(salida, t0 + i16, a.BL, d, kk, we);
+    w[u] = ld4_rows(wo, n0 + i16, d, d, kk, we);
+  }
+  float4 hv[kStepTokPerWave][D4], wg[D4];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].x, w[u].x, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].y, w[u].y, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].z, w[u].z, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].w, w[u].w, acc, 0, 0, 0);
+  for (int k = 0; k < D4; ++k) {
+    const int q = lane + kWave * k;
+    wg[k] = q < d4 ? ((const float4*)a.wg)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < kStepTokPerWave; ++j) {
+      const int tl = wave + kStepWaves * j;
+      hv[j][k] = tl < nt && q < d4 ? ((const float4*)(a.h + (t0 + tl) * d))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
-#pragma unroll
-  for (int q = 0; q < 4; ++q) tile[wave][(4 * q4 + q) * kStepTok + i16] = acc[q];   // rows 4 (l / 16) + q, col l % 16
-  // h . w_g per token, as the fused gate forms it (float4 lanes, then the wave sum): wave w takes tokens w + 4 j
-  for (int j = 0; j < kStepTok / kGateWaves; ++j) {
-    const int tl = wave + kGateWaves * j;
-    const int64_t t = t0 + tl;
-    float dot = 0.f;
-#pragma unroll
-    for (int k = 0; k < D4; ++k) {
-      const int q = lane + kWave * k;
-      if (tl < nt && q < d4) {
-        const float4 hv = ((const float4*)(a.h + t * d))[q];
-        const float4 w = ((const float4*)a.wg)[q];
-        dot += hv.x * w.x + hv.y * w.y + hv.z * w.z + hv.w * w.w;
-      }
-    }
-    dot = wave_sum_u(dot);
-    if (lane == 0) hdot[tl] = dot;
+  const int S = 6 + 2 * a.n + a.nodes;
+  const float pv = tid < S ? small_param(a, tid) : 0.f;
+  const bool vin = tid < nt * a.n;                          // nt n <= kStepTok kGateMaxN < kStepThreads
+  const float vv = vin ? a.vistos[t0 * a.n + tid] : 0.f, hw = vin ? a.hawkes[t0 * a.n + tid] : 0.f;
+  float4 sg = make_float4(0.f, 0.f, 0.f, 0.f);
+  float ra = 0.f;
+  if (tid < nt) {
+    sg = ((const float4*)a.sig)[t0 + tid];
+    ra = a.racha[t0 + tid];
   }
-  __syncthreads();
-  if (tid < nt) token_features(a, t0 + tid, P, vh[0] + tid * a.n, vh[1] + tid * a.n, feat[tid], &info[tid]);
-  __syncthreads();
-  const int tl = tid / kStepTok, c = tid % kStepTok;
+  const int tl = tid / kStepTok, c = tid % kStepTok;        // the epilogue's element of the tile
   const int64_t t = t0 + tl;
   const int col = n0 + c;
-  if (tl < nt && col < d) {
+  const bool mine = tid < kStepTok * kStepTok && tl < nt && col < d;
+  const float hx = mine ? a.h[t * d + col] : 0.f;
+  // the tile: rows 4 (l / 16) + q, column l % 16 of each wave's partial
+  f4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].x, w[u].x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].y, w[u].y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].z, w[u].z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].w, w[u].w, acc, 0, 0, 0);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) tile[wave][(4 * q4 + q) * kStepTok + i16] = acc[q];
+  // h . w_g per token, as the fused gate forms it (float4 lanes, then the wave sum)
+#pragma unroll
+  for (int j = 0; j < kStepTokPerWave; ++j) {
+    float dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < D4; ++k)
+      dot += hv[j][k].x * wg[k].x + hv[j][k].y * wg[k].y + hv[j][k].z * wg[k].z + hv[j][k].w * wg[k].w;
+    dot = wave_sum_u(dot);
+    if (lane == 0) hdot[wave + kStepWaves * j] = dot;
+  }
+  if (tid < S) P[tid] = pv;
+  if (vin) {
+    vh[0][tid] = vv;
+    vh[1][tid] = hw;
+  }
+  __syncthreads();
+  if (tid < nt) token_features_of(a, sg, ra, P, vh[0] + tid * a.n, vh[1] + tid * a.n, feat[tid], &info[tid]);
+  __syncthreads();
+  if (mine) {
     const int e = tl * kStepTok + c;
-    const float A = ((tile[0][e] + tile[1][e]) + tile[2][e]) + tile[3][e];
+    float A = tile[0][e];
+#pragma unroll
+    for (int i = 1; i < kStepWaves; ++i) A += tile[i][e];
     const float logit = hdot[tl] + info[tl].small;
     if (blockIdx.x == 0 && c == 0) a.logit[t] = logit;
     const float sr = info[tl].r / (1.f + expf(-capped(logit, a.tope)));
-    a.out[t * d + col] = a.h[t * d + col] + sr * A;
+    a.out[t * d + col] = hx + sr * A;
   }
 }
 
@@ -461,21 +487,18 @@ extern "C" int asrn_gate_step(const float* h, const float* salida, const float* 
     ASRN_REQUIRE(((uintptr_t)p & 15) == 0, "asrn_gate_step: rows are read as float4: 16-byte alignment");
   if (BL == 0) return 0;
   const dim3 grid((unsigned)((d + kStepTok - 1) / kStepTok), (unsigned)((BL + kStepTok - 1) / kStepTok));
-  const dim3 block(kGateThreads);
+  const dim3 block(kStepThreads);
   hipStream_t st = (hipStream_t)stream;
-  const int per = ((d + kGateWaves - 1) / kGateWaves + 15) & ~15;   // a wave's depth, <= 256
+  const int per = ((d + kStepWaves - 1) / kStepWaves + 15) & ~15;   // a wave's depth
+  // the kernels make one pass of U steps: 16 U covers per for every d <= 1024 with the U picked below
+  ASRN_REQUIRE(per <= 16 * 8, "asrn_gate_step: d=%d: a wave's depth %d above 128", d, per);
   auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, st, a, salida, w_o); };
-  const int d4c = (d + 4 * kWave - 1) / (4 * kWave);
-  if (per <= 16 * 8) {
-    switch (d4c) {
-      case 1: launch(k_gate_step<1, 8>); break;
-      default: launch(k_gate_step<2, 8>); break;
-    }
-  } else {
-    switch (d4c) {
-      case 3: launch(k_gate_step<3, 16>); break;
-      default: launch(k_gate_step<4, 16>); break;
-    }
+  switch ((d + 4 * kWave - 1) / (4 * kWave)) {              // float4 columns a lane holds of h; U steps of 16
+    case 1: per <= 16 ? launch(k_gate_step<1, 1>) : (per <= 32 ? launch(k_gate_step<1, 2>) : launch(k_gate_step<1, 4>));
+            break;
+    case 2: launch(k_gate_step<2, 4>); break;
+    case 3: launch(k_gate_step<3, 6>); break;
+    default: launch(k_gate_step<4, 8>); break;
   }
   return check_launch("asrn_gate_step");
 }
