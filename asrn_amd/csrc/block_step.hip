@@ -53,15 +53,16 @@ constexpr int kRowVals = 4;                 // row values a thread holds: rows u
 
 // mean and 1/sqrt(var + eps) of a row of width d whose column tid + j * kPrepThreads is v[j] in thread tid (two-pass
 // variance; every thread gets the results)
-__device__ void row_stats(const float (&v)[kRowVals], int d, float eps, float* red, float* mean, float* rstd) {
+template <int R>
+__device__ void row_stats(const float (&v)[R], int d, float eps, float* red, float* mean, float* rstd) {
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < kRowVals; ++j)
+  for (int j = 0; j < R; ++j)
     if ((int)threadIdx.x + j * kPrepThreads < d) s += v[j];
   const float m = block_total(s, red) / (float)d;
   float q = 0.f;
 #pragma unroll
-  for (int j = 0; j < kRowVals; ++j)
+  for (int j = 0; j < R; ++j)
     if ((int)threadIdx.x + j * kPrepThreads < d) {
       const float t = v[j] - m;
       q += t * t;
@@ -70,14 +71,23 @@ __device__ void row_stats(const float (&v)[kRowVals], int d, float eps, float* r
   *rstd = rsqrtf(block_total(q, red) / (float)d + eps);
 }
 
-// the sum over `splits` partial rows (split stride `stride`) at one column, all loads in flight together
-__device__ __forceinline__ float split_sum(const float* p, int splits, int64_t stride) {
-  float v[kMaxSplits];
+// The row kernels below hold R columns a thread (column tid + j kPrepThreads, R = ceil(d / kPrepThreads)) and issue
+// every load before its first use as unconditional loads: columns past d read column d - 1, and splits past `splits`
+// re-read the last one, real addresses whose values are not used (a guarded load becomes a branch the compiler does
+// not schedule across, and each such load then waits on its own).
+
+// the S (>= splits) partial values of one column, split stride `stride`
+template <int S>
+__device__ __forceinline__ void split_loads(const float* p, int splits, int64_t stride, float (&v)[S]) {
 #pragma unroll
-  for (int s = 0; s < kMaxSplits; ++s) v[s] = s < splits ? p[s * stride] : 0.f;
+  for (int s = 0; s < S; ++s) v[s] = p[(int64_t)(s < splits ? s : splits - 1) * stride];
+}
+// their sum in split order (the splits past `splits` add nothing)
+template <int S>
+__device__ __forceinline__ float split_total(const float (&v)[S], int splits) {
   float y = 0.f;
 #pragma unroll
-  for (int s = 0; s < kMaxSplits; ++s) y += v[s];
+  for (int s = 0; s < S; ++s) y += s < splits ? v[s] : 0.f;
   return y;
 }
 
@@ -94,49 +104,61 @@ struct Pending {
   float* out;         // its output, written here
 };
 
-// With pv.part: the row is the pending block's output h1 + (sum of the splits + bias), formed as k_finish_res forms
-// it, written to pv.out, and the pending block's z enters its ring (k_finish_res's work, one row per workgroup).
+// With PEND: the row is the pending block's output h1 + (sum of the splits + bias), formed as k_finish_res forms it,
+// written to pv.out, and the pending block's z enters its ring (k_finish_res's work, one row per workgroup).
+template <int R, int S, bool PEND>
 __global__ __launch_bounds__(kPrepThreads) void k_prep_mix(const float* h, int64_t ldh, Pending pv, const float* ring,
                                                            const int64_t* pos_p, const float* w, const float* bia,
                                                            float eps, int d, int k, float* z, float* x1) {
   __shared__ float red[kPrepWaves];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
-  const float* row = h + b * ldh;
   const int km1 = k - 1;
   const int64_t pos = *pos_p;
   const int first = km1 > 0 ? (int)(pos % km1) : 0;        // the slot of tap 0; tap i is at (first + i) mod (k - 1)
   auto slot = [&](int i) { return first + i < km1 ? first + i : first + i - km1; };
-  // the row, the LayerNorm's weights and, for k <= 9, the ring taps, loaded together before the statistics
-  float v[kRowVals], tap[kRowVals][kMaxTaps], lw[kRowVals], lb[kRowVals];
+  // the row (or the pending block's parts), the LayerNorm's weights and, for k <= 9, the ring taps
+  float x[R], lw[R], lb[R], tap[R][kMaxTaps], sp[R][S], pb[R], zp[R];
 #pragma unroll
-  for (int j = 0; j < kRowVals; ++j) {
-    const int c = tid + j * kPrepThreads;
-    lw[j] = c < d ? w[c] : 0.f;
-    lb[j] = c < d ? bia[c] : 0.f;
-    if (pv.part)
-      v[j] = c < d ? pv.h1[b * d + c] + (split_sum(pv.part + b * d + c, pv.splits, gridDim.x * (int64_t)d) +
-                                         pv.bias[c])
-                   : 0.f;
-    else
-      v[j] = c < d ? row[c] : 0.f;
+  for (int j = 0; j < R; ++j) {
+    const int c = tid + j * kPrepThreads, cc = c < d ? c : d - 1;
+    lw[j] = w[cc];
+    lb[j] = bia[cc];
+    if constexpr (PEND) {
+      x[j] = pv.h1[b * d + cc];
+      split_loads<S>(pv.part + b * d + cc, pv.splits, gridDim.x * (int64_t)d, sp[j]);
+      pb[j] = pv.bias[cc];
+      zp[j] = pv.km1 > 0 ? pv.z[b * d + cc] : 0.f;
+    } else {
+      x[j] = h[b * ldh + cc];
+    }
+    if (km1 > 0) {
 #pragma unroll
-    for (int i = 0; i < kMaxTaps; ++i) tap[j][i] = (c < d && i < km1) ? ring[(b * d + c) * km1 + slot(i)] : 0.f;
+      for (int i = 0; i < kMaxTaps; ++i) tap[j][i] = ring[(b * d + cc) * km1 + slot(i < km1 ? i : km1 - 1)];
+    }
   }
-  if (pv.part) {
+  float v[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    if constexpr (PEND)
+      v[j] = x[j] + (split_total<S>(sp[j], pv.splits) + pb[j]);
+    else
+      v[j] = x[j];
+  }
+  if constexpr (PEND) {
     const int ps = pv.km1 > 0 ? (int)(pos % pv.km1) : 0;
 #pragma unroll
-    for (int j = 0; j < kRowVals; ++j) {
+    for (int j = 0; j < R; ++j) {
       const int c = tid + j * kPrepThreads;
       if (c >= d) continue;
       pv.out[b * d + c] = v[j];
-      if (pv.km1 > 0) pv.ring[(b * d + c) * pv.km1 + ps] = pv.z[b * d + c];
+      if (pv.km1 > 0) pv.ring[(b * d + c) * pv.km1 + ps] = zp[j];
     }
   }
   float m, r;
-  row_stats(v, d, eps, red, &m, &r);
+  row_stats<R>(v, d, eps, red, &m, &r);
 #pragma unroll
-  for (int j = 0; j < kRowVals; ++j) {
+  for (int j = 0; j < R; ++j) {
     const int c = tid + j * kPrepThreads;
     if (c >= d) continue;
     const float zc = (v[j] - m) * r * lw[j] + lb[j];
@@ -151,6 +173,7 @@ __global__ __launch_bounds__(kPrepThreads) void k_prep_mix(const float* h, int64
 }
 
 // h1 = h + GELU(sum of the splits + bias), then X2 = LayerNorm2(h1), one row per workgroup
+template <int R, int S>
 __global__ __launch_bounds__(kPrepThreads) void k_finish_mix(const float* part, int splits, int64_t B,
                                                              const float* bias, const float* h, int64_t ldh,
                                                              const float* w2, const float* b2, float eps, int d,
@@ -158,34 +181,56 @@ __global__ __launch_bounds__(kPrepThreads) void k_finish_mix(const float* part, 
   __shared__ float red[kPrepWaves];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
-  float v[kRowVals], lw[kRowVals], lb[kRowVals];
+  float x[R], lw[R], lb[R], bs[R], sp[R][S];
 #pragma unroll
-  for (int j = 0; j < kRowVals; ++j) {             // the LayerNorm's weights loaded with the row
+  for (int j = 0; j < R; ++j) {
+    const int c = tid + j * kPrepThreads, cc = c < d ? c : d - 1;
+    lw[j] = w2[cc];
+    lb[j] = b2[cc];
+    x[j] = h[b * ldh + cc];
+    bs[j] = bias[cc];
+    split_loads<S>(part + b * d + cc, splits, B * d, sp[j]);
+  }
+  float v[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
     const int c = tid + j * kPrepThreads;
-    lw[j] = c < d ? w2[c] : 0.f;
-    lb[j] = c < d ? b2[c] : 0.f;
-    v[j] = c < d ? h[b * ldh + c] + gelu_erf(split_sum(part + b * d + c, splits, B * d) + bias[c]) : 0.f;
+    v[j] = x[j] + gelu_erf(split_total<S>(sp[j], splits) + bs[j]);
     if (c < d) h1[b * d + c] = v[j];
   }
   float m, r;
-  row_stats(v, d, eps, red, &m, &r);
+  row_stats<R>(v, d, eps, red, &m, &r);
 #pragma unroll
-  for (int j = 0; j < kRowVals; ++j) {
+  for (int j = 0; j < R; ++j) {
     const int c = tid + j * kPrepThreads;
     if (c < d) x2[b * d + c] = (v[j] - m) * r * lw[j] + lb[j];
   }
 }
 
 // out = h1 + sum of the splits + bias; z enters the ring, one row per workgroup
+template <int R, int S>
 __global__ __launch_bounds__(kPrepThreads) void k_finish_res(const float* part, int splits, int64_t B,
                                                              const float* bias, const float* h1, const float* z,
                                                              const int64_t* pos_p, int d, int km1, float* ring,
                                                              float* out) {
   const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x;
   const int slot = km1 > 0 ? (int)(*pos_p % km1) : 0;
-  for (int c = threadIdx.x; c < d; c += kPrepThreads) {
-    out[b * d + c] = h1[b * d + c] + (split_sum(part + b * d + c, splits, B * d) + bias[c]);
-    if (km1 > 0) ring[(b * d + c) * km1 + slot] = z[b * d + c];
+  float x[R], bs[R], zv[R], sp[R][S];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int c = tid + j * kPrepThreads, cc = c < d ? c : d - 1;
+    x[j] = h1[b * d + cc];
+    bs[j] = bias[cc];
+    zv[j] = km1 > 0 ? z[b * d + cc] : 0.f;
+    split_loads<S>(part + b * d + cc, splits, B * d, sp[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int c = tid + j * kPrepThreads;
+    if (c >= d) continue;
+    out[b * d + c] = x[j] + (split_total<S>(sp[j], splits) + bs[j]);
+    if (km1 > 0) ring[(b * d + c) * km1 + slot] = zv[j];
   }
 }
 
@@ -260,6 +305,43 @@ __global__ __launch_bounds__(NW * kWave) void k_part(Part g) {
   }
 }
 
+// the row kernels' instances: R columns a thread (ceil(d / kPrepThreads)) and S loads for at most S splits
+using PrepFn = void (*)(const float*, int64_t, Pending, const float*, const int64_t*, const float*, const float*, float,
+                        int, int, float*, float*);
+using MixFn = void (*)(const float*, int, int64_t, const float*, const float*, int64_t, const float*, const float*,
+                       float, int, float*, float*);
+using ResFn = void (*)(const float*, int, int64_t, const float*, const float*, const float*, const int64_t*, int, int,
+                       float*, float*);
+
+int split_cap(int splits) { return splits <= 4 ? 4 : (splits <= 8 ? 8 : 16); }
+
+template <int R>
+PrepFn prep_fn_r(bool pend, int S) {
+  if (!pend) return k_prep_mix<R, 4, false>;
+  return S == 4 ? k_prep_mix<R, 4, true> : (S == 8 ? k_prep_mix<R, 8, true> : k_prep_mix<R, 16, true>);
+}
+PrepFn prep_fn(int R, bool pend, int splits) {
+  const int S = split_cap(splits);
+  return R == 1 ? prep_fn_r<1>(pend, S) : (R == 2 ? prep_fn_r<2>(pend, S) : (R == 3 ? prep_fn_r<3>(pend, S)
+                                                                              : prep_fn_r<4>(pend, S)));
+}
+template <int R>
+MixFn mix_fn_r(int S) {
+  return S == 4 ? k_finish_mix<R, 4> : (S == 8 ? k_finish_mix<R, 8> : k_finish_mix<R, 16>);
+}
+MixFn mix_fn(int R, int splits) {
+  const int S = split_cap(splits);
+  return R == 1 ? mix_fn_r<1>(S) : (R == 2 ? mix_fn_r<2>(S) : (R == 3 ? mix_fn_r<3>(S) : mix_fn_r<4>(S)));
+}
+template <int R>
+ResFn res_fn_r(int S) {
+  return S == 4 ? k_finish_res<R, 4> : (S == 8 ? k_finish_res<R, 8> : k_finish_res<R, 16>);
+}
+ResFn res_fn(int R, int splits) {
+  const int S = split_cap(splits);
+  return R == 1 ? res_fn_r<1>(S) : (R == 2 ? res_fn_r<2>(S) : (R == 3 ? res_fn_r<3>(S) : res_fn_r<4>(S)));
+}
+
 // depth splits: each wavefront's share at most 64 columns (one round of loads), at most kMaxSplits
 int splits_for(int N, int K) {
   (void)N;
@@ -325,18 +407,19 @@ int block_step(const float* h, int64_t ldh, const float* prev_h1, const float* p
   if (prev_h1)   // the pending block's partials, where its call (same workspace, same B and d) left them
     pv = Pending{hid + (int64_t)B * prev_ff, splits_for(d, prev_ff), prev_b2, prev_h1, prev_z, prev_ring, prev_k - 1,
                  prev_out};
-  hipLaunchKernelGGL(k_prep_mix, dim3((unsigned)B), dim3(kPrepThreads), 0, st, prev_h1 ? prev_out : h,
-                     prev_h1 ? (int64_t)d : ldh, pv, ring, pos, ln1_w, ln1_b, eps, d, k, z, x1);
+  const int R = (d + kPrepThreads - 1) / kPrepThreads;
+  hipLaunchKernelGGL(prep_fn(R, prev_h1 != nullptr, pv.splits), dim3((unsigned)B), dim3(kPrepThreads), 0, st,
+                     prev_h1 ? prev_out : h, prev_h1 ? (int64_t)d : ldh, pv, ring, pos, ln1_w, ln1_b, eps, d, k, z, x1);
   if (int rc = check_launch(what)) return rc;
   if (int rc = launch_part(Part{x1, conv_w, p1, nullptr, (int)B, d * k, d, s1}, st, what)) return rc;
   // the residual input h: the pending block's output, which k_prep_mix wrote, or h itself
-  hipLaunchKernelGGL(k_finish_mix, dim3((unsigned)B), dim3(kPrepThreads), 0, st, p1, s1, B, conv_b,
+  hipLaunchKernelGGL(mix_fn(R, s1), dim3((unsigned)B), dim3(kPrepThreads), 0, st, p1, s1, B, conv_b,
                      prev_h1 ? prev_out : h, prev_h1 ? (int64_t)d : ldh, ln2_w, ln2_b, eps, d, h1, x2);
   if (int rc = check_launch(what)) return rc;
   if (int rc = launch_part(Part{x2, w1, hid, b1, (int)B, d, ff, 1}, st, what)) return rc;
   if (int rc = launch_part(Part{hid, w2, p3, nullptr, (int)B, ff, d, s3}, st, what)) return rc;
   if (!finish) return 0;                           // k_finish_res's work left to the next block's k_prep_mix
-  hipLaunchKernelGGL(k_finish_res, dim3((unsigned)B), dim3(kPrepThreads), 0, st, p3, s3, B, b2, h1, z, pos, d, k - 1,
+  hipLaunchKernelGGL(res_fn(R, s3), dim3((unsigned)B), dim3(kPrepThreads), 0, st, p3, s3, B, b2, h1, z, pos, d, k - 1,
                      ring, out);
   return check_launch(what);
 }

@@ -43,6 +43,11 @@ struct ProdArgs {
   double* beta; float* y;                                   // beta (B); y (B, m + 2 mc): the first layers' products
 };
 
+constexpr int kMaxLayers = 8;          // layers one batched launch takes
+struct ProdBatch {                     // every layer's arguments (the same sizes and position in each)
+  ProdArgs l[kMaxLayers];
+};
+
 __device__ __forceinline__ int64_t prod_pos(const ProdArgs& a) { return a.t_dev ? *a.t_dev : a.t; }
 
 __device__ __forceinline__ float dot4(float4 a, float4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
@@ -81,16 +86,17 @@ __device__ __forceinline__ void layer_norm_rows(const ProdArgs& a, float4* xs, i
   }
 }
 
+// the products of the rows of kinds [k_lo, k_hi) (blockIdx.x: a block of kProdRows rows of one kind; blockIdx.y: a
+// group of kProdTok tokens)
 template <int D4>
-__global__ __launch_bounds__(kProdThreads) void k_produce_rows(ProdArgs a) {
-  __shared__ float4 xs[kProdTok * kProdMaxD4 * kWave];
+__device__ __forceinline__ void rows_body(const ProdArgs& a, int k_lo, int k_hi, float4* xs) {
   const int64_t t = prod_pos(a);
   if (t < 1 || t >= a.cap) return;                          // the same for the whole grid
   const int lane = lane_id(), wave = threadIdx.x >> 6;
   const int d4 = a.d >> 2;
   // which kind and block
-  int k = 0, blk = blockIdx.x;
-  for (; k < 5; ++k) {
+  int k = k_lo, blk = blockIdx.x;
+  for (; k < k_hi - 1; ++k) {
     const int nb = (kind_rows(a, k) + kProdRows - 1) / kProdRows;
     if (blk < nb) break;
     blk -= nb;
@@ -155,37 +161,52 @@ __global__ __launch_bounds__(kProdThreads) void k_produce_rows(ProdArgs a) {
   }
 }
 
+template <int D4>
+__global__ __launch_bounds__(kProdThreads) void k_produce_rows(ProdArgs a) {
+  __shared__ float4 xs[kProdTok * kProdMaxD4 * kWave];
+  rows_body<D4>(a, 0, 6, xs);
+}
+
+// every layer's rows that act on e_t and e_prev (kinds 0-3), layer blockIdx.z
+template <int D4>
+__global__ __launch_bounds__(kProdThreads) void k_produce_rows_e(ProdBatch pb) {
+  __shared__ float4 xs[kProdTok * kProdMaxD4 * kWave];
+  rows_body<D4>(pb.l[blockIdx.z], 0, 4, xs);
+}
+
 __device__ __forceinline__ float gelu_exact(float x) { return 0.5f * x * (1.f + erff(x * 0.70710678118654752f)); }
 __device__ __forceinline__ float softplus_p(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 __device__ __forceinline__ float logsigmoid_p(float x) { return fminf(x, 0.f) - log1pf(expf(-fabsf(x))); }
 
-// one token per workgroup: hidden units, both second layers, the clock, the token id
-__global__ __launch_bounds__(kProdThreads) void k_produce_token(ProdArgs a) {
-  __shared__ float g[2 * kProdMax];
+// one token per workgroup (row b): with E, the hidden units, both second layers and the token id; with H, the clock
+template <bool E, bool H>
+__device__ __forceinline__ void token_body(const ProdArgs& a, int64_t b, float* g) {
   const int64_t t = prod_pos(a);
   if (t < 1 || t >= a.cap) return;
-  const int64_t b = blockIdx.x;
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
-  const int n1 = a.m + 2 * a.mc;
-  const float* yb = a.y + b * n1;
-  if (tid < a.m) g[tid] = gelu_exact(yb[tid] + a.bw[tid]);
-  else if (tid < a.m + a.mc) {
-    const int j = tid - a.m;
-    g[tid] = gelu_exact((yb[a.m + j] + a.bc[j]) + yb[a.m + a.mc + j]);
+  if constexpr (E) {
+    const int n1 = a.m + 2 * a.mc;
+    const float* yb = a.y + b * n1;
+    if (tid < a.m) g[tid] = gelu_exact(yb[tid] + a.bw[tid]);
+    else if (tid < a.m + a.mc) {
+      const int j = tid - a.m;
+      g[tid] = gelu_exact((yb[a.m + j] + a.bc[j]) + yb[a.m + a.mc + j]);
+    }
+    __syncthreads();
+    const int P = a.Pw + a.Pc;
+    if (tid < a.Pw) {
+      float s = 0.f;
+      for (int j = 0; j < a.m; ++j) s += a.w2w[tid * a.m + j] * g[j];
+      a.phi[(b * a.cap + t) * P + tid] = s + a.b2w[tid];
+    } else if (tid < P) {
+      const int o = tid - a.Pw;
+      float s = 0.f;
+      for (int j = 0; j < a.mc; ++j) s += a.w2c[o * a.mc + j] * g[a.m + j];
+      a.phi[(b * a.cap + t) * P + tid] = s + a.b2c[o];
+    }
+    if (tid == kProdThreads - 1) a.sig[b * a.cap + t] = (float)a.pieza[b];
   }
-  __syncthreads();
-  const int P = a.Pw + a.Pc;
-  if (tid < a.Pw) {
-    float s = 0.f;
-    for (int j = 0; j < a.m; ++j) s += a.w2w[tid * a.m + j] * g[j];
-    a.phi[(b * a.cap + t) * P + tid] = s + a.b2w[tid];
-  } else if (tid < P) {
-    const int o = tid - a.Pw;
-    float s = 0.f;
-    for (int j = 0; j < a.mc; ++j) s += a.w2c[o * a.mc + j] * g[a.m + j];
-    a.phi[(b * a.cap + t) * P + tid] = s + a.b2c[o];
-  }
-  if (wave == kProdWaves - 1) {                             // the clock: LayerNorm of h_t and its two projections
+  if (H && wave == kProdWaves - 1) {                        // the clock: LayerNorm of h_t and its two projections
     const int d4 = a.d >> 2;
     const float inv_d = 1.f / (float)a.d;
     const float4* x = (const float4*)(a.h + b * a.d);
@@ -213,7 +234,117 @@ __global__ __launch_bounds__(kProdThreads) void k_produce_token(ProdArgs a) {
       if (a.beta_max >= 0.f) be = fminf(be, a.beta_max);
       a.beta[b] = (double)be;
       a.la[b * a.cap + t] = fmaxf(logsigmoid_p(u1) + 0.69314718055994530942f, a.la_min);
-      a.sig[b * a.cap + t] = (float)a.pieza[b];
+    }
+  }
+}
+
+__global__ __launch_bounds__(kProdThreads) void k_produce_token(ProdArgs a) {
+  __shared__ float g[2 * kProdMax];
+  token_body<true, true>(a, blockIdx.x, g);
+}
+
+// every layer's hidden units, second layers and token id (layer blockIdx.y)
+__global__ __launch_bounds__(kProdThreads) void k_produce_token_e(ProdBatch pb) {
+  __shared__ float g[2 * kProdMax];
+  token_body<true, false>(pb.l[blockIdx.y], blockIdx.x, g);
+}
+
+// The rows that act on the layer input h_t, one token per workgroup of kHWaves waves: hh = LayerNorm(h_t), each wave
+// forming it for itself; Qc = cq hh and Kc = ck hh, rows r = w, w + (kHWaves - 1), ... of the 2 cf by wave w, kHChunk
+// rows in flight; the clock from w_reloj hh + b_reloj by the last wave. The sums are those of the two-kernel producer
+// in the same order (layer_norm_rows, the rows' products, the clock), so the outputs are the same bits. Every load of
+// the first chunk is issued before the row's statistics.
+constexpr int kHWaves = 16;
+constexpr int kHChunk = 4;
+
+template <int D4>
+__global__ __launch_bounds__(kHWaves * kWave) void k_produce_h(ProdArgs a) {
+  const int64_t t = prod_pos(a);
+  if (t < 1 || t >= a.cap) return;
+  const int64_t b = blockIdx.x;
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const int d4 = a.d >> 2;
+  const float inv_d = 1.f / (float)a.d;
+  const bool clk = wave == kHWaves - 1;
+  const int nr = 2 * a.cf;
+  // rows past 2 cf read row 0 and lanes past d read column d - 4: every load is an unconditional float4 (a guarded
+  // one is split by the compiler into four predicated loads), and those values are never used
+  auto row_of = [&](int r) {
+    r = r < nr ? r : 0;
+    return r < a.cf ? a.wq + (int64_t)r * a.d : a.wk + (int64_t)(r - a.cf) * a.d;
+  };
+  float4 x[D4], lw[D4], lb[D4], w[kHChunk][D4];
+#pragma unroll
+  for (int k = 0; k < D4; ++k) {
+    const int q = lane + kWave * k < d4 ? lane + kWave * k : d4 - 1;
+    x[k] = ((const float4*)(a.h + b * a.d))[q];
+    lw[k] = ((const float4*)a.lnw)[q];
+    lb[k] = ((const float4*)a.lnb)[q];
+#pragma unroll
+    for (int i = 0; i < kHChunk; ++i) {
+      const float* row = clk ? a.wr + (int64_t)(i & 1) * a.d : row_of(wave + (kHWaves - 1) * i);
+      w[i][k] = ((const float4*)row)[q];
+    }
+  }
+  // hh, as layer_norm_rows forms it
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < D4; ++k)
+    if (lane + kWave * k < d4) s += (x[k].x + x[k].y) + (x[k].z + x[k].w);
+  const float mean = wave_sum_u(s) * inv_d;
+  float v = 0.f;
+#pragma unroll
+  for (int k = 0; k < D4; ++k) {
+    if (lane + kWave * k >= d4) continue;
+    const float4 c = make_float4(x[k].x - mean, x[k].y - mean, x[k].z - mean, x[k].w - mean);
+    v += dot4(c, c);
+  }
+  const float rstd = rsqrtf(wave_sum_u(v) * inv_d + a.eps);
+  float4 hh[D4];
+#pragma unroll
+  for (int k = 0; k < D4; ++k)
+    hh[k] = make_float4((x[k].x - mean) * rstd * lw[k].x + lb[k].x, (x[k].y - mean) * rstd * lw[k].y + lb[k].y,
+                        (x[k].z - mean) * rstd * lw[k].z + lb[k].z, (x[k].w - mean) * rstd * lw[k].w + lb[k].w);
+  if (clk) {                                                // the clock
+    float u0 = 0.f, u1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < D4; ++k) {
+      if (lane + kWave * k >= d4) continue;
+      u0 += dot4(hh[k], w[0][k]);
+      u1 += dot4(hh[k], w[1][k]);
+    }
+    u0 = wave_sum_u(u0) + a.br[0];
+    u1 = wave_sum_u(u1) + a.br[1];
+    if (lane == 0) {
+      float be = softplus_p(u0);
+      if (a.beta_max >= 0.f) be = fminf(be, a.beta_max);
+      a.beta[b] = (double)be;
+      a.la[b * a.cap + t] = fmaxf(logsigmoid_p(u1) + 0.69314718055994530942f, a.la_min);
+    }
+    return;
+  }
+  for (int i0 = 0;; i0 += kHChunk) {                        // Qc and Kc, kHChunk rows of this wave at a time
+    if (wave + (kHWaves - 1) * i0 >= nr) break;             // wave-uniform
+    if (i0 > 0) {
+#pragma unroll
+      for (int i = 0; i < kHChunk; ++i) {
+        const float* row = row_of(wave + (kHWaves - 1) * (i0 + i));
+#pragma unroll
+        for (int k = 0; k < D4; ++k) w[i][k] = ((const float4*)row)[lane + kWave * k < d4 ? lane + kWave * k : d4 - 1];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kHChunk; ++i) {
+      const int r = wave + (kHWaves - 1) * (i0 + i);
+      float p = 0.f;
+#pragma unroll
+      for (int k = 0; k < D4; ++k)
+        if (lane + kWave * k < d4) p += dot4(w[i][k], hh[k]);
+      const float sr = wave_sum_u(p);
+      if (lane == 0 && r < nr) {
+        if (r < a.cf) a.Qc[(b * a.cap + t) * a.cf + r] = sr;
+        else a.Kc[(b * a.cap + t) * a.cf + r - a.cf] = sr;
+      }
     }
   }
 }
@@ -276,4 +407,99 @@ extern "C" int asrn_decode_produce(const float* e, const float* e_prev, const fl
   if (check_launch("asrn_decode_produce/rows")) return 1;
   hipLaunchKernelGGL(k_produce_token, dim3((unsigned)B), dim3(kProdThreads), 0, st, a);
   return check_launch("asrn_decode_produce/token");
+}
+
+extern "C" int64_t asrn_decode_produce_e_workspace(int32_t L, int64_t B, int32_t m, int32_t mc) {
+  if (L < 0 || B < 0 || m < 0 || mc < 0) return -1;
+  return (int64_t)L * B * (int64_t)(m + 2 * mc) * (int64_t)sizeof(float);
+}
+
+extern "C" int asrn_decode_produce_e(int32_t L, const float* e, const float* e_prev, const int64_t* pieza, int64_t B,
+                                     int32_t d, const float* const* w_v, const float* const* w_word,
+                                     const float* const* w_ctx, const float* const* b_word, const float* const* b_ctx,
+                                     const float* const* w2_word, const float* const* b2_word,
+                                     const float* const* w2_ctx, const float* const* b2_ctx, int32_t m, int32_t mc,
+                                     int32_t p_word, int32_t p_ctx, float* const* phi, float* const* V,
+                                     float* const* sig, int64_t cap, int64_t t, const int64_t* t_dev, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
+  ASRN_REQUIRE(L >= 1 && L <= kMaxLayers, "asrn_decode_produce_e: L=%d layers must be in [1, %d]", L, kMaxLayers);
+  ASRN_REQUIRE(B >= 0 && B <= 65535 && d > 0 && d % 4 == 0 && d <= 4 * kProdMaxD4 * kWave,
+               "asrn_decode_produce_e: B=%lld, d=%d: d a positive multiple of 4, <= %d", (long long)B, d,
+               4 * kProdMaxD4 * kWave);
+  ASRN_REQUIRE(m >= 1 && mc >= 1 && m <= kProdMax && mc <= kProdMax && p_word >= 1 && p_ctx >= 1 &&
+                   p_word + p_ctx <= kProdThreads,
+               "asrn_decode_produce_e: m=%d, mc=%d must be in [1, %d], Pw + Pc=%d in [2, %d]", m, mc, kProdMax,
+               p_word + p_ctx, kProdThreads);
+  ASRN_REQUIRE(t >= 1 && t < cap, "asrn_decode_produce_e: position t=%lld outside [1, capacity %lld)", (long long)t,
+               (long long)cap);
+  ASRN_REQUIRE(e && e_prev && pieza && w_v && w_word && w_ctx && b_word && b_ctx && w2_word && b2_word && w2_ctx &&
+                   b2_ctx && phi && V && sig,
+               "asrn_decode_produce_e: null pointer");
+  const int64_t need = asrn_decode_produce_e_workspace(L, B, m, mc);
+  ASRN_REQUIRE(workspace != nullptr && workspace_bytes >= need, "asrn_decode_produce_e: workspace of %lld bytes, "
+               "needs %lld", (long long)workspace_bytes, (long long)need);
+  ProdBatch pb = {};
+  for (int l = 0; l < L; ++l) {
+    ASRN_REQUIRE(w_v[l] && w_word[l] && w_ctx[l] && b_word[l] && b_ctx[l] && w2_word[l] && b2_word[l] && w2_ctx[l] &&
+                     b2_ctx[l] && phi[l] && V[l] && sig[l],
+                 "asrn_decode_produce_e: layer %d: null pointer", l);
+    for (const void* p : {(const void*)w_v[l], (const void*)w_word[l], (const void*)w_ctx[l]})
+      ASRN_REQUIRE(((uintptr_t)p & 15) == 0, "asrn_decode_produce_e: layer %d: rows are read as float4: 16-byte "
+                   "alignment", l);
+    ProdArgs& a = pb.l[l];
+    a.e = e; a.e_prev = e_prev; a.pieza = pieza; a.B = B; a.d = d;
+    a.wv = w_v[l]; a.ww = w_word[l]; a.wc = w_ctx[l]; a.bw = b_word[l]; a.bc = b_ctx[l];
+    a.w2w = w2_word[l]; a.b2w = b2_word[l]; a.w2c = w2_ctx[l]; a.b2c = b2_ctx[l];
+    a.m = m; a.mc = mc; a.Pw = p_word; a.Pc = p_ctx;
+    a.phi = phi[l]; a.V = V[l]; a.sig = sig[l]; a.cap = cap; a.t = t; a.t_dev = t_dev;
+    a.y = (float*)workspace + (int64_t)l * B * (m + 2 * mc);
+  }
+  for (const void* p : {(const void*)e, (const void*)e_prev})
+    ASRN_REQUIRE(((uintptr_t)p & 15) == 0, "asrn_decode_produce_e: rows are read as float4: 16-byte alignment");
+  if (B == 0) return 0;
+  int blocks = 0;
+  for (int k = 0; k < 4; ++k) blocks += (kind_rows_host(d, m, mc, 1, k) + kProdRows - 1) / kProdRows;
+  const dim3 grid((unsigned)blocks, (unsigned)((B + kProdTok - 1) / kProdTok), (unsigned)L);
+  hipStream_t st = (hipStream_t)stream;
+  switch ((d + 4 * kWave - 1) / (4 * kWave)) {
+    case 1: hipLaunchKernelGGL(k_produce_rows_e<1>, grid, dim3(kProdThreads), 0, st, pb); break;
+    case 2: hipLaunchKernelGGL(k_produce_rows_e<2>, grid, dim3(kProdThreads), 0, st, pb); break;
+    case 3: hipLaunchKernelGGL(k_produce_rows_e<3>, grid, dim3(kProdThreads), 0, st, pb); break;
+    default: hipLaunchKernelGGL(k_produce_rows_e<4>, grid, dim3(kProdThreads), 0, st, pb); break;
+  }
+  if (check_launch("asrn_decode_produce_e/rows")) return 1;
+  hipLaunchKernelGGL(k_produce_token_e, dim3((unsigned)B, (unsigned)L), dim3(kProdThreads), 0, st, pb);
+  return check_launch("asrn_decode_produce_e/token");
+}
+
+extern "C" int asrn_decode_produce_h(const float* h, int64_t B, int32_t d, const float* ln_w, const float* ln_b,
+                                     float eps, const float* w_reloj, const float* b_reloj, float beta_max,
+                                     float log_alfa_min, const float* w_cq, const float* w_ck, int32_t cf, float* Qc,
+                                     float* Kc, float* log_alfa, int64_t cap, int64_t t, const int64_t* t_dev,
+                                     double* beta, void* stream) {
+  ASRN_REQUIRE(B >= 0 && d > 0 && d % 4 == 0 && d <= 4 * kProdMaxD4 * kWave,
+               "asrn_decode_produce_h: d=%d must be a positive multiple of 4, <= %d", d, 4 * kProdMaxD4 * kWave);
+  ASRN_REQUIRE(cf >= 1 && cf <= kProdMax, "asrn_decode_produce_h: cf=%d must be in [1, %d]", cf, kProdMax);
+  ASRN_REQUIRE(eps > 0.f, "asrn_decode_produce_h: eps must be positive");
+  ASRN_REQUIRE(t >= 1 && t < cap, "asrn_decode_produce_h: position t=%lld outside [1, capacity %lld)", (long long)t,
+               (long long)cap);
+  ASRN_REQUIRE(h && ln_w && ln_b && w_reloj && b_reloj && w_cq && w_ck && Qc && Kc && log_alfa && beta,
+               "asrn_decode_produce_h: null pointer");
+  for (const void* p : {(const void*)h, (const void*)ln_w, (const void*)ln_b, (const void*)w_reloj,
+                        (const void*)w_cq, (const void*)w_ck})
+    ASRN_REQUIRE(((uintptr_t)p & 15) == 0, "asrn_decode_produce_h: the rows are read as float4: 16-byte alignment");
+  if (B == 0) return 0;
+  ProdArgs a = {};
+  a.h = h; a.B = B; a.d = d; a.lnw = ln_w; a.lnb = ln_b; a.eps = eps; a.wr = w_reloj; a.br = b_reloj;
+  a.beta_max = beta_max; a.la_min = log_alfa_min; a.wq = w_cq; a.wk = w_ck; a.cf = cf;
+  a.Qc = Qc; a.Kc = Kc; a.la = log_alfa; a.cap = cap; a.t = t; a.t_dev = t_dev; a.beta = beta;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)B), block(kHWaves * kWave);
+  switch ((d + 4 * kWave - 1) / (4 * kWave)) {
+    case 1: hipLaunchKernelGGL(k_produce_h<1>, grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL(k_produce_h<2>, grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL(k_produce_h<3>, grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL(k_produce_h<4>, grid, block, 0, st, a); break;
+  }
+  return check_launch("asrn_decode_produce_h");
 }

@@ -360,15 +360,16 @@ __global__ __launch_bounds__(kStepThreads) void k_gate_step(GateArgs a, const fl
     x[u] = ld4_rows(salida, t0 + i16, a.BL, d, kk, we);
     w[u] = ld4_rows(wo, n0 + i16, d, d, kk, we);
   }
+  // (unconditional float4 loads: tokens past nt read token 0 and lanes past d column d - 4, values never used)
   float4 hv[kStepTokPerWave][D4], wg[D4];
 #pragma unroll
   for (int k = 0; k < D4; ++k) {
-    const int q = lane + kWave * k;
-    wg[k] = q < d4 ? ((const float4*)a.wg)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const int q = lane + kWave * k < d4 ? lane + kWave * k : d4 - 1;
+    wg[k] = ((const float4*)a.wg)[q];
 #pragma unroll
     for (int j = 0; j < kStepTokPerWave; ++j) {
       const int tl = wave + kStepWaves * j;
-      hv[j][k] = tl < nt && q < d4 ? ((const float4*)(a.h + (t0 + tl) * d))[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      hv[j][k] = ((const float4*)(a.h + (t0 + (tl < nt ? tl : 0)) * d))[q];
     }
   }
   const int S = 6 + 2 * a.n + a.nodes;
@@ -403,7 +404,8 @@ __global__ __launch_bounds__(kStepThreads) void k_gate_step(GateArgs a, const fl
     float dot = 0.f;
 #pragma unroll
     for (int k = 0; k < D4; ++k)
-      dot += hv[j][k].x * wg[k].x + hv[j][k].y * wg[k].y + hv[j][k].z * wg[k].z + hv[j][k].w * wg[k].w;
+      if (lane + kWave * k < d4)
+        dot += hv[j][k].x * wg[k].x + hv[j][k].y * wg[k].y + hv[j][k].z * wg[k].z + hv[j][k].w * wg[k].w;
     dot = wave_sum_u(dot);
     if (lane == 0) hdot[wave + kStepWaves * j] = dot;
   }

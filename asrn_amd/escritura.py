@@ -108,12 +108,15 @@ class EscritorCapa:
         else:
             c[:, pos] = valor
 
-    def _cuerpo(self, e_t, e_ult, h_t, pieza_t, pos, t_max=None):
+    def _cuerpo(self, e_t, e_ult, h_t, pieza_t, pos, t_max=None, producido=False):
         """One step's work at position pos (an int, or a one-element device buffer holding it, t_max its largest value) ->
-        the layer's output (B, d) (the layer part of asrn/nucleo.py:1797-1854)."""
+        the layer's output (B, d) (the layer part of asrn/nucleo.py:1797-1854). producido: the rows that act on e_t
+        (V, phi, sig) are already in the caches (ops.decode_produce_e, for every layer of a model at once)."""
         capa = self.capa
         c = self.cache
-        if ops.decode_produce_ok(capa, e_t):
+        if producido:
+            beta_t = ops.decode_produce_h(capa, c, h_t, pos, t_max=t_max)
+        elif ops.decode_produce_ok(capa, e_t):
             # fp32: the token's V, phi, Qc, Kc, log_alfa and id rows in two kernels (asrn_decode_produce)
             beta_t = ops.decode_produce(capa, c, e_t, e_ult, h_t, pieza_t, pos, t_max=t_max)
         else:

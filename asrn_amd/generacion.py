@@ -120,6 +120,12 @@ class EscritorModelo:
         else:
             e_t, e_prev = m.emb(pieza), None
         h = e_t
+        e_ant = self.e_ult if e_prev is None else e_prev
+        # every ASRN layer's rows that act on the embedding rows, in one launch pair before the first block
+        ls, cs = [c.capa for c in self.capas], [c.cache for c in self.capas]
+        producido = bool(ls) and torch.is_tensor(pos) and ops.decode_produce_e_ok(ls, cs, e_t)
+        if producido:
+            ops.decode_produce_e(ls, cs, e_t, e_ant, pieza, pos, t_max=t_max)
         capas = iter(self.capas)
         k = 0
         pendiente = None
@@ -131,7 +137,7 @@ class EscritorModelo:
             pendiente, h = (r, None) if encadenar else (None, r)
             k += blq.mezcla == 'memoria'
             if i in m.pos_largo:
-                h = next(capas)._cuerpo(e_t, self.e_ult if e_prev is None else e_prev, h, pieza, pos, t_max=t_max)
+                h = next(capas)._cuerpo(e_t, e_ant, h, pieza, pos, t_max=t_max, producido=producido)
         if e_prev is None:
             self.e_ult.copy_(e_t)
         x = m.ln_f(h)

@@ -930,6 +930,62 @@ def decode_produce(capa, cache, e, e_prev, h, pieza, t, t_max=None):
     return beta
 
 
+def _formas_productor(capa):
+    pal, ctx = capa.afin_palabra, capa.afin_contexto
+    return pal[0].out_features, ctx[0].out_features, pal[2].out_features, ctx[2].out_features
+
+
+def decode_produce_e_ok(capas, caches, e):
+    """Whether asrn_decode_produce_e takes these layers together: each one decode_produce_ok, at most 8 of them, with
+    the same widths and cache capacity."""
+    return (1 <= len(capas) <= 8 and all(decode_produce_ok(c, e) for c in capas)
+            and len({_formas_productor(c) for c in capas}) == 1 and len({c['phi'].shape[1] for c in caches}) == 1)
+
+
+def decode_produce_e(capas, caches, e, e_prev, pieza, t, t_max=None):
+    """The part of the generation step's producers that acts on the new tokens' embedding rows, for every layer at
+    once (asrn_decode_produce_e): V[t-1], phi[t] and sig[t] of each layer written into its caches (capas and caches
+    in the same order; decode_produce_e_ok holds). t: as decode_produce's."""
+    dev = _dev(e)
+    B, d = e.shape
+    L = len(capas)
+    m, mc, Pw, Pc = _formas_productor(capas[0])
+    cap = caches[0]['phi'].shape[1]
+    wsb = query('asrn_decode_produce_e_workspace', L, B, m, mc)
+    ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=dev)
+    th, tdev = _posicion(t, t_max)
+    ins = [_c(e, torch.float32), _c(e_prev, torch.float32), _c(pieza, torch.int64)]
+    arr = lambda ts: (ctypes.c_void_p * L)(*[t_.data_ptr() for t_ in ts])
+    pal = [c.afin_palabra for c in capas]
+    ctx = [c.afin_contexto for c in capas]
+    call('asrn_decode_produce_e', L, ptr(ins[0]), ptr(ins[1]), ptr(ins[2]), B, d, arr([c.v.weight for c in capas]),
+         arr([p[0].weight for p in pal]), arr([x[0].weight for x in ctx]), arr([p[0].bias for p in pal]),
+         arr([x[0].bias for x in ctx]), arr([p[2].weight for p in pal]), arr([p[2].bias for p in pal]),
+         arr([x[2].weight for x in ctx]), arr([x[2].bias for x in ctx]), m, mc, Pw, Pc,
+         arr([c_['phi'] for c_ in caches]), arr([c_['V'] for c_ in caches]), arr([c_['sig'] for c_ in caches]), cap, th,
+         tdev, ptr(ws), wsb, stream_of(dev))
+
+
+def decode_produce_h(capa, cache, h, t, t_max=None):
+    """The part of the generation step's producers that acts on the layer input h (asrn_decode_produce_h): Qc[t],
+    Kc[t] and log_alfa[t] written into the caches; returns beta (B,) fp64. With decode_produce_e, the same bits as
+    decode_produce."""
+    dev = _dev(h)
+    B, d = h.shape
+    cap = cache['phi'].shape[1]
+    p = capa.protecciones
+    beta_max = -1.0 if p.beta_max is None else float(p.beta_max)
+    la_min = -math.inf if p.log_alfa_min is None else float(p.log_alfa_min)
+    beta = torch.empty((B,), dtype=torch.float64, device=dev)
+    th, tdev = _posicion(t, t_max)
+    hh = _c(h, torch.float32)
+    call('asrn_decode_produce_h', ptr(hh), B, d, ptr(capa.ln_ctx.weight), ptr(capa.ln_ctx.bias),
+         float(capa.ln_ctx.eps), ptr(capa.w_reloj), ptr(capa.b_reloj), beta_max, la_min, ptr(capa.cq.weight),
+         ptr(capa.ck.weight), capa.confirmar, ptr(cache['Qc']), ptr(cache['Kc']), ptr(cache['log_alfa']), cap, th, tdev,
+         ptr(beta), stream_of(dev))
+    return beta
+
+
 def _pow2_at_least(x):
     c = 1
     while c < x:

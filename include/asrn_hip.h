@@ -425,6 +425,26 @@ int asrn_decode_produce(const float* e, const float* e_prev, const float* h, con
                         float* Qc, float* Kc, float* sig, float* log_alfa, int64_t cap, int64_t t,
                         const int64_t* t_dev, double* beta, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* decode_produce_e and decode_produce_h: asrn_decode_produce split by what the rows depend on, no counterpart in the
+ * reference's FFI (its step runs each layer's producers in turn, asrn/nucleo.py:1797-1826). decode_produce_e writes,
+ * for L layers at once (their pointers in host arrays of L; the layers share d, m, mc, p_word, p_ctx, the caches'
+ * capacity cap and the position), what depends only on the new tokens' embedding rows e and e_prev and their ids:
+ * V[t-1], phi[t] and sig[t]; the step can run it once, before its first layer. decode_produce_h then writes one
+ * layer's Qc[t], Kc[t] and log_alfa[t] and its beta from that layer's input h. Together they write what
+ * asrn_decode_produce writes, the same bits. workspace: asrn_decode_produce_e_workspace(L, B, m, mc) bytes. */
+int64_t asrn_decode_produce_e_workspace(int32_t L, int64_t B, int32_t m, int32_t mc);
+int asrn_decode_produce_e(int32_t L, const float* e, const float* e_prev, const int64_t* pieza, int64_t B, int32_t d,
+                          const float* const* w_v, const float* const* w_word, const float* const* w_ctx,
+                          const float* const* b_word, const float* const* b_ctx, const float* const* w2_word,
+                          const float* const* b2_word, const float* const* w2_ctx, const float* const* b2_ctx,
+                          int32_t m, int32_t mc, int32_t p_word, int32_t p_ctx, float* const* phi, float* const* V,
+                          float* const* sig, int64_t cap, int64_t t, const int64_t* t_dev, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+int asrn_decode_produce_h(const float* h, int64_t B, int32_t d, const float* ln_w, const float* ln_b, float eps,
+                          const float* w_reloj, const float* b_reloj, float beta_max, float log_alfa_min,
+                          const float* w_cq, const float* w_ck, int32_t cf, float* Qc, float* Kc, float* log_alfa,
+                          int64_t cap, int64_t t, const int64_t* t_dev, double* beta, void* stream);
+
 /* ---- generation loop: n-gram sets and the per-token choice ------------------------------------------------------
  * The host side of escribir (asrn/nucleo.py:1965-2043) moved onto the device. The n-gram sets replace _Ngramas
  * (asrn/nucleo.py:1857-1889: Python dicts of token tuples, updated on the host after every token): per text row, an

@@ -392,3 +392,38 @@ def test_decode_produce_matches_the_ops(B, d, kw):
             rows = [t - 1, t] if k == 'V' else [t]
             keep = [i for i in range(cache[k].shape[1]) if i not in rows]
             assert torch.equal(cache[k][:, keep], esc.cache[k][:, keep]), k
+
+
+@pytest.mark.parametrize('B,d,kw,L', [(16, 768, {}, 3), (3, 64, SMALL, 2), (2, 32, dict(confirmar=8, n_tablas=5, n_bits=4), 1)])
+def test_decode_produce_split_equals_whole(B, d, kw, L):
+    """asrn_decode_produce_e for L layers at once, then asrn_decode_produce_h for each layer, write what
+    asrn_decode_produce writes layer by layer, bit for bit: every cache (V at t - 1; phi, Qc, Kc, log_alfa, sig at t;
+    nothing else) and beta, through a device-held position as the captured model step passes it."""
+    say('decode produce split', B, d, kw, L)
+    capas, caches, hs = [], [], []
+    x, E, h = synth.layer_inputs(B, 40, d, 9, seed=3)
+    Ed, xd = E.to(DEV), x.to(DEV)
+    for l in range(L):
+        torch.manual_seed(10 + l)
+        layer = synth.move_params(CapaASRNEstable(d, **kw), 10 + l).to(DEV)
+        esc = EscritorCapa(layer, memoria_de_lo_ajeno=False)
+        hl = (h + 0.3 * l).to(DEV)
+        esc.inicio(Ed[:, :30], hl[:, :30], xd[:, :30], capacidad=40)
+        capas.append(layer)
+        caches.append(esc.cache)
+        hs.append(hl[:, 30].contiguous())
+    t = 30
+    e_t, e_prev = Ed[:, t].contiguous(), Ed[:, t - 1].contiguous()
+    pos = torch.full((1,), t, dtype=torch.int64, device=DEV)
+    whole = [{k: v.clone() for k, v in c.items()} for c in caches]
+    split = [{k: v.clone() for k, v in c.items()} for c in caches]
+    assert ops.decode_produce_e_ok(capas, split, e_t)
+    betas_w = [ops.decode_produce(capas[l], whole[l], e_t, e_prev, hs[l], xd[:, t], pos, t_max=t) for l in range(L)]
+    ops.decode_produce_e(capas, split, e_t, e_prev, xd[:, t], pos, t_max=t)
+    betas_s = [ops.decode_produce_h(capas[l], split[l], hs[l], pos, t_max=t) for l in range(L)]
+    torch.cuda.synchronize()
+    for l in range(L):
+        assert torch.equal(betas_w[l], betas_s[l]), l
+        for k in whole[l]:
+            assert torch.equal(whole[l][k], split[l][k]), (l, k)
+        assert not torch.equal(whole[l]['phi'], caches[l]['phi'])     # the step wrote something
