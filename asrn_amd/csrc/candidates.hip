@@ -343,6 +343,40 @@ __device__ __forceinline__ int suffix_len_of(const float* __restrict__ sigb, con
   return ell;
 }
 
+// What a unique's score terms read from memory, by its position k: the tokens before it (its suffix, K <= 4), its clock
+// and its log_alfa; loaded ahead of their use (unique_terms)
+struct UniqueAt {
+  int64_t k;
+  float s[4];
+  double bk;
+  float la;
+};
+// unique u's (u < NU; past NU, the last unique's; with no uniques, position self_pos's, never used)
+__device__ __forceinline__ UniqueAt unique_at(const Cand& a, int64_t b, const Scratch& S, int NU, int u,
+                                              const float* __restrict__ sigb, int64_t self_pos) {
+  UniqueAt x;
+  x.k = NU > 0 ? S.upos[u < NU ? u : NU - 1] : self_pos;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t io = x.k - 1 - j;
+    x.s[j] = sigb[io >= 0 ? io : 0];
+  }
+  x.bk = a.Bt[b * a.L + x.k];
+  x.la = a.la[b * a.L + x.k];
+  return x;
+}
+// suffix_len_of for K <= 4 on the loaded tokens (the same comparisons)
+__device__ __forceinline__ int suffix_len4(const UniqueAt& x, const float (&mine)[4], int64_t self_pos, int K) {
+  int ell = 0;
+  bool run = true;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    run = run && j < K && x.k - 1 - j >= 0 && self_pos - 1 - j >= 0 && x.s[j] == mine[j];
+    ell += run ? 1 : 0;
+  }
+  return ell;
+}
+
 // Packs every table's window of token (b, t) into S.key and the table segments into S.off. query_window: the
 // `win & 255` sorted ranks before the token's; otherwise (the key pass) the `win >> 8` after it. The segment offsets
 // are a prefix sum of the window lengths, so entry m finds its table by a binary search over T offsets and one round
@@ -1026,6 +1060,30 @@ __device__ __forceinline__ void unique_terms(const Cand& a, int64_t b, int64_t t
   const int lane = lane_id();
   const int64_t tok = b * a.L + t;
   const RecLayout R = rec_layout(a.T, a.C);
+  // Lanes take uniques u0 + lane (NW == 1: all 64 lanes; NW > 1: the first 2 kRows lanes of each wave's chunks); the
+  // loop below is wave-uniform, so every lane takes part in the shuffle. With NW > 1 (the generation step, where each
+  // wave has chunks to spare registers for), what the terms read that depends only on the uniques' positions is loaded
+  // before the base scores' rows, so that both are in flight together: this lane's unique in the wave's first NPRE
+  // chunks. (With NW = 1 those registers would spill: the whole-text kernels run at their register limit.)
+  constexpr int NPRE = NW == 1 ? 0 : 2;
+  constexpr int PRE = NPRE > 0 ? NPRE : 1;
+  const int per = NW == 1 ? kWave : 2 * kRows;
+  const int ustart = NW == 1 ? 0 : wave * 2 * kRows;
+  const float* sigb = a.sig + b * a.L;
+  float mine[4];
+  double bq;
+  float wsuf_l;                                             // w_suf[x] in lane x (K <= 16), read by shuffles
+  auto own_terms = [&]() {                                  // the query's own suffix and clock
+    own_suffix_of(sigb, t, a.K, mine);
+    bq = STEP_CLOCK ? clock_at(a.Bt + b * a.L, t, a.rep.beta_t[b], a.rep.reloj32) : a.Bt[tok];
+    wsuf_l = lane <= a.K ? a.w_suf[lane] : 0.f;
+  };
+  UniqueAt pre[PRE];
+  if constexpr (NPRE > 0) {
+    own_terms();
+#pragma unroll
+    for (int i = 0; i < NPRE; ++i) pre[i] = unique_at(a, b, S, NU, ustart + i * NW * per + lane, sigb, t);
+  }
   if constexpr (F4 == 1) {
     unique_bases8<FB16>(a, b, tok, NU, S, wave * 2 * kRows, NW * 2 * kRows);
   } else {
@@ -1033,22 +1091,35 @@ __device__ __forceinline__ void unique_terms(const Cand& a, int64_t b, int64_t t
     feat_row<F4, FB16>(feat_lanes<F4, FB16>(a, a.Qc, true), (uint32_t)tok, qf);
     unique_bases<F4, FB16>(a, b, t, NU, false, qf, S, wave * 2 * kRows, NW * 2 * kRows);
   }
-  const float* sigb = a.sig + b * a.L;
-  float mine[4];
-  own_suffix_of(sigb, t, a.K, mine);
-  const double bq = STEP_CLOCK ? clock_at(a.Bt + b * a.L, t, a.rep.beta_t[b], a.rep.reloj32) : a.Bt[tok];
-  const float wsuf_l = lane <= a.K ? a.w_suf[lane] : 0.f;   // w_suf[x] in lane x (K <= 16), read by shuffles
+  if constexpr (NPRE == 0) own_terms();
   if (a.clock32 && lane == 0 && wave == 0) S.bq32 = (float)bq;
-  // lanes take uniques u0 + lane (NW == 1: all 64 lanes; NW > 1: the first 2 kRows lanes of each wave's chunks);
-  // the loop is wave-uniform, so every lane takes part in the shuffle
-  const int per = NW == 1 ? kWave : 2 * kRows;
-  for (int u0 = NW == 1 ? 0 : wave * 2 * kRows; u0 < NU; u0 += NW * per) {
+  int i = 0;
+  for (int u0 = ustart; u0 < NU; u0 += NW * per, ++i) {
     const int u = u0 + lane;
     const bool in = lane < per && u < NU;
-    const int64_t k = S.upos[in ? u : NU - 1];
-    const int ell = suffix_len_of(sigb, mine, t, k, a.K);
-    const double bk = a.Bt[b * a.L + k];
-    const float la = a.la[b * a.L + k];
+    int64_t k;
+    int ell;
+    double bk;
+    float la;
+    if constexpr (NPRE > 0) {
+      UniqueAt x;
+      if (i < NPRE) {
+#pragma unroll
+        for (int c = 0; c < NPRE; ++c)                  // a register copy, no indexing by i
+          if (c == i) x = pre[c];
+      } else {
+        x = unique_at(a, b, S, NU, u, sigb, t);
+      }
+      k = x.k;
+      ell = a.K <= 4 ? suffix_len4(x, mine, t, a.K) : suffix_len_of(sigb, mine, t, k, a.K);
+      bk = x.bk;
+      la = x.la;
+    } else {
+      k = S.upos[in ? u : NU - 1];
+      ell = suffix_len_of(sigb, mine, t, k, a.K);
+      bk = a.Bt[b * a.L + k];
+      la = a.la[b * a.L + k];
+    }
     const float db = (float)(bk - bq);     // with the fp32 clock, the fp32 difference of the two values
     const float ws = __shfl(wsuf_l, ell, kWave);
     if (in) {
