@@ -35,11 +35,15 @@ struct GateArgs {
   const float* dout; float* dh; void* dA; float* dhawkes; float* dracha; float* partial;   // backward
 };
 
-__device__ __forceinline__ float4 load_a4(const void* p, int bf16, int64_t q) {
-  if (!bf16) return ((const float4*)p)[q];
-  const uint2 u = ((const uint2*)p)[q];   // four bf16, element 0 in the low half
-  return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
-                     __uint_as_float(u.y & 0xffff0000u));
+template <bool B16>
+__device__ __forceinline__ float4 load_a4t(const void* p, int64_t q) {
+  if constexpr (!B16) {
+    return ((const float4*)p)[q];
+  } else {
+    const uint2 u = ((const uint2*)p)[q];   // four bf16, element 0 in the low half
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xffff0000u));
+  }
 }
 
 // fp32 -> bf16 bits, round to nearest even (NaN stays a quiet NaN)
@@ -84,22 +88,7 @@ __device__ __forceinline__ float small_param(const GateArgs& a, int c) {
   return a.dr[c - 6 - 2 * n];
 }
 
-// the packed small parameters into LDS, one thread each, so that phase 1's sum reads them without a chain of global
-// loads (a short input, the generation step's few tokens, waits on that chain alone); S <= kGateCols
-__device__ __forceinline__ void stage_small_params(const GateArgs& a, float* P) {
-  if (threadIdx.x < 6 + 2 * a.n + a.nodes) P[threadIdx.x] = small_param(a, threadIdx.x);
-}
-
 constexpr int kGateMaxN = (kGateCols - 8) / 2;   // tables, at most (6 + 2 n + nodes <= kGateCols, nodes >= 2)
-
-// the workgroup's seen flags and Hawkes intensities (n per token, rows in token order) into LDS, all threads loading
-__device__ __forceinline__ void stage_token_rows(const GateArgs& a, int64_t t0, float* vis, float* haw) {
-  const int64_t nt = a.BL - t0 < kGateTok ? a.BL - t0 : kGateTok;
-  for (int64_t i = threadIdx.x; i < nt * a.n; i += kGateThreads) {
-    vis[i] = a.vistos[t0 * a.n + i];
-    haw[i] = a.hawkes[t0 * a.n + i];
-  }
-}
 
 // phase 1: a token's features into f (LDS row), its info into ti, from its signals g (peso_total, mejor, pico,
 // peso_ctx) and streak ra; P the staged small parameters, vis and haw the token's staged rows
@@ -140,9 +129,45 @@ __device__ void token_features(const GateArgs& a, int64_t t, const float* P, con
   token_features_of(a, ((const float4*)a.sig)[t], a.racha[t], P, vis, haw, f, ti);
 }
 
+// Phase 1 of the whole-text gate kernels with every load in one round: the small parameters, the workgroup's seen and
+// Hawkes rows, and each token's signals and streak (one thread per token), as unconditional loads from clamped
+// indices (a guarded load becomes a branch the compiler waits at), then the LDS staging and the features.
+__device__ __forceinline__ void gate_prologue(const GateArgs& a, int64_t t0, float* P, float* vis, float* haw,
+                                              float (*feat)[kFeatStride], TokenInfo* info) {
+  constexpr int kRowLoads = (kGateTok * kGateMaxN + kGateThreads - 1) / kGateThreads;
+  const int tid = threadIdx.x;
+  const int64_t nt = a.BL - t0 < kGateTok ? a.BL - t0 : kGateTok;
+  const int S = 6 + 2 * a.n + a.nodes, nr = (int)nt * a.n;
+  const float pv = small_param(a, tid < S ? tid : S - 1);
+  float vv[kRowLoads], hw[kRowLoads];
+#pragma unroll
+  for (int r = 0; r < kRowLoads; ++r) {
+    const int i = tid + r * kGateThreads, ic = i < nr ? i : nr - 1;
+    vv[r] = a.vistos[t0 * a.n + ic];
+    hw[r] = a.hawkes[t0 * a.n + ic];
+  }
+  const int64_t tt = t0 + (tid < nt ? tid : nt - 1);
+  const float4 sg = ((const float4*)a.sig)[tt];
+  const float ra = a.racha[tt];
+  if (tid < S) P[tid] = pv;
+#pragma unroll
+  for (int r = 0; r < kRowLoads; ++r) {
+    const int i = tid + r * kGateThreads;
+    if (i < nr) {
+      vis[i] = vv[r];
+      haw[i] = hw[r];
+    }
+  }
+  __syncthreads();
+  if (tid < nt) token_features_of(a, sg, ra, P, vis + tid * a.n, haw + tid * a.n, feat[tid], &info[tid]);
+  __syncthreads();
+}
+
 __device__ __forceinline__ float capped(float l, float tope) { return tope > 0.f ? tope * tanhf(l / tope) : l; }
 
-template <int D4>
+// AB16: A (the W_o product) in bf16. A batch's rows are loaded unconditionally from clamped indices (tokens past BL
+// read the last token, columns past d the last column; those values are not used), so each batch is one round.
+template <int D4, bool AB16>
 __global__ __launch_bounds__(kGateThreads) void k_gate_fwd(GateArgs a) {
   __shared__ float feat[kGateTok][kFeatStride];
   __shared__ TokenInfo info[kGateTok];
@@ -151,33 +176,35 @@ __global__ __launch_bounds__(kGateThreads) void k_gate_fwd(GateArgs a) {
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int d4 = a.d >> 2;
   const int64_t t0 = (int64_t)blockIdx.x * kGateTok;
-  stage_small_params(a, P);
-  stage_token_rows(a, t0, vh[0], vh[1]);
-  __syncthreads();
-  if (threadIdx.x < kGateTok && t0 + threadIdx.x < a.BL)
-    token_features(a, t0 + threadIdx.x, P, vh[0] + threadIdx.x * a.n, vh[1] + threadIdx.x * a.n, feat[threadIdx.x],
-                   &info[threadIdx.x]);
-  __syncthreads();
-  for (int b = 0; b < kGateTokPerWave; b += kGateBatch) {
-    float4 hv[kGateBatch][D4], av[kGateBatch][D4];
-    float dot[kGateBatch];
+  gate_prologue(a, t0, P, vh[0], vh[1], feat, info);
+  constexpr int kB = D4 == 1 ? kGateBatch : 2;           // a batch's rows are all live at once: fewer past d 256
+  float4 w[D4];
 #pragma unroll
-    for (int u = 0; u < kGateBatch; ++u) {
-      const int64_t t = t0 + wave + kGateWaves * (b + u);
-      dot[u] = 0.f;
+  for (int k = 0; k < D4; ++k) w[k] = ((const float4*)a.wg)[lane + kWave * k < d4 ? lane + kWave * k : d4 - 1];
+  for (int b = 0; b < kGateTokPerWave; b += kB) {
+    float4 hv[kB][D4], av[kB][D4];
+    float dot[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const int64_t t = t0 + wave + kGateWaves * (b + u), tc = t < a.BL ? t : a.BL - 1;
 #pragma unroll
       for (int k = 0; k < D4; ++k) {
-        const int q = lane + kWave * k;
-        if (t < a.BL && q < d4) {
-          hv[u][k] = ((const float4*)(a.h + t * a.d))[q];
-          av[u][k] = load_a4(a.A, a.a_bf16, t * d4 + q);
-          const float4 w = ((const float4*)a.wg)[q];
-          dot[u] += hv[u][k].x * w.x + hv[u][k].y * w.y + hv[u][k].z * w.z + hv[u][k].w * w.w;
-        }
+        const int q = lane + kWave * k, qc = q < d4 ? q : d4 - 1;
+        hv[u][k] = ((const float4*)(a.h + tc * a.d))[qc];
+        av[u][k] = load_a4t<AB16>(a.A, tc * d4 + qc);
       }
     }
 #pragma unroll
-    for (int u = 0; u < kGateBatch; ++u) {
+    for (int u = 0; u < kB; ++u) {
+      const int64_t t = t0 + wave + kGateWaves * (b + u);
+      dot[u] = 0.f;
+#pragma unroll
+      for (int k = 0; k < D4; ++k)
+        if (t < a.BL && lane + kWave * k < d4)
+          dot[u] += hv[u][k].x * w[k].x + hv[u][k].y * w[k].y + hv[u][k].z * w[k].z + hv[u][k].w * w[k].w;
+    }
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
       const int tl = wave + kGateWaves * (b + u);
       const int64_t t = t0 + tl;
       if (t >= a.BL) break;
@@ -196,7 +223,7 @@ __global__ __launch_bounds__(kGateThreads) void k_gate_fwd(GateArgs a) {
   }
 }
 
-template <int D4>
+template <int D4, bool AB16>
 __global__ __launch_bounds__(kGateThreads) void k_gate_bwd(GateArgs a) {
   __shared__ float feat[kGateTok][kFeatStride];
   __shared__ TokenInfo info[kGateTok];
@@ -208,41 +235,43 @@ __global__ __launch_bounds__(kGateThreads) void k_gate_bwd(GateArgs a) {
   const int64_t t0 = (int64_t)blockIdx.x * kGateTok;
   __shared__ float P[kGateCols];
   __shared__ float vh[2][kGateTok * kGateMaxN];
-  stage_small_params(a, P);
-  stage_token_rows(a, t0, vh[0], vh[1]);
-  __syncthreads();
-  if (threadIdx.x < kGateTok) {
-    dl[threadIdx.x] = 0.f;
-    if (t0 + threadIdx.x < a.BL)
-      token_features(a, t0 + threadIdx.x, P, vh[0] + threadIdx.x * n, vh[1] + threadIdx.x * n, feat[threadIdx.x],
-                     &info[threadIdx.x]);
+  if (threadIdx.x < kGateTok) dl[threadIdx.x] = 0.f;         // ordered before its use by the prologue's barriers
+  gate_prologue(a, t0, P, vh[0], vh[1], feat, info);
+  // a batch's rows are all live at once: 4 tokens a batch at d <= 256, 2 past it (register pressure)
+  constexpr int kB = D4 == 1 ? kGateBatch : 2;
+  float4 gw[D4], w[D4];
+#pragma unroll
+  for (int k = 0; k < D4; ++k) {
+    gw[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    w[k] = ((const float4*)a.wg)[lane + kWave * k < d4 ? lane + kWave * k : d4 - 1];
   }
-  __syncthreads();
-  float4 gw[D4];
+  for (int b = 0; b < kGateTokPerWave; b += kB) {
+    float4 gv[kB][D4], hv[kB][D4], av[kB][D4];
+    float ga[kB], lg[kB];
 #pragma unroll
-  for (int k = 0; k < D4; ++k) gw[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int b = 0; b < kGateTokPerWave; b += kGateBatch) {
-    float4 gv[kGateBatch][D4], hv[kGateBatch][D4], av[kGateBatch][D4];
-    float ga[kGateBatch], lg[kGateBatch];
-#pragma unroll
-    for (int u = 0; u < kGateBatch; ++u) {
-      const int64_t t = t0 + wave * kGateTokPerWave + b + u;
-      ga[u] = 0.f;
-      lg[u] = t < a.BL ? a.logit[t] : 0.f;
+    for (int u = 0; u < kB; ++u) {                         // the batch's loads, unconditional (clamped indices)
+      const int64_t t = t0 + wave * kGateTokPerWave + b + u, tc = t < a.BL ? t : a.BL - 1;
+      lg[u] = a.logit[tc];
 #pragma unroll
       for (int k = 0; k < D4; ++k) {
-        const int q = lane + kWave * k;
-        if (t < a.BL && q < d4) {
-          gv[u][k] = ((const float4*)(a.dout + t * a.d))[q];
-          hv[u][k] = ((const float4*)(a.h + t * a.d))[q];
-          av[u][k] = load_a4(a.A, a.a_bf16, t * d4 + q);
-          ga[u] += gv[u][k].x * av[u][k].x + gv[u][k].y * av[u][k].y + gv[u][k].z * av[u][k].z +
-                   gv[u][k].w * av[u][k].w;
-        }
+        const int q = lane + kWave * k, qc = q < d4 ? q : d4 - 1;
+        gv[u][k] = ((const float4*)(a.dout + tc * a.d))[qc];
+        hv[u][k] = ((const float4*)(a.h + tc * a.d))[qc];
+        av[u][k] = load_a4t<AB16>(a.A, tc * d4 + qc);
       }
     }
 #pragma unroll
-    for (int u = 0; u < kGateBatch; ++u) {
+    for (int u = 0; u < kB; ++u) {
+      const int64_t t = t0 + wave * kGateTokPerWave + b + u;
+      ga[u] = 0.f;
+#pragma unroll
+      for (int k = 0; k < D4; ++k)
+        if (t < a.BL && lane + kWave * k < d4)
+          ga[u] += gv[u][k].x * av[u][k].x + gv[u][k].y * av[u][k].y + gv[u][k].z * av[u][k].z +
+                   gv[u][k].w * av[u][k].w;
+    }
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
       const int tl = wave * kGateTokPerWave + b + u;
       const int64_t t = t0 + tl;
       if (t >= a.BL) break;
@@ -261,9 +290,8 @@ __global__ __launch_bounds__(kGateThreads) void k_gate_bwd(GateArgs a) {
       for (int k = 0; k < D4; ++k) {
         const int q = lane + kWave * k;
         if (q < d4) {
-          const float4 w = ((const float4*)a.wg)[q];
-          ((float4*)(a.dh + t * a.d))[q] = make_float4(gv[u][k].x + dlogit * w.x, gv[u][k].y + dlogit * w.y,
-                                                       gv[u][k].z + dlogit * w.z, gv[u][k].w + dlogit * w.w);
+          ((float4*)(a.dh + t * a.d))[q] = make_float4(gv[u][k].x + dlogit * w[k].x, gv[u][k].y + dlogit * w[k].y,
+                                                       gv[u][k].z + dlogit * w[k].z, gv[u][k].w + dlogit * w[k].w);
           store_a4(a.dA, a.a_bf16, t * d4 + q,
                    make_float4(gv[u][k].x * sr, gv[u][k].y * sr, gv[u][k].z * sr, gv[u][k].w * sr));
           gw[k].x += dlogit * hv[u][k].x;
@@ -463,10 +491,10 @@ extern "C" int asrn_gate_fwd(const float* h, const void* aporte, int32_t aporte_
   const dim3 grid((unsigned)gate_groups(BL)), block(kGateThreads);
   hipStream_t st = (hipStream_t)stream;
   switch ((d + 4 * kWave - 1) / (4 * kWave)) {
-    case 1: hipLaunchKernelGGL(k_gate_fwd<1>, grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL(k_gate_fwd<2>, grid, block, 0, st, a); break;
-    case 3: hipLaunchKernelGGL(k_gate_fwd<3>, grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL(k_gate_fwd<4>, grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((a.a_bf16 ? k_gate_fwd<1, true> : k_gate_fwd<1, false>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((a.a_bf16 ? k_gate_fwd<2, true> : k_gate_fwd<2, false>), grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((a.a_bf16 ? k_gate_fwd<3, true> : k_gate_fwd<3, false>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((a.a_bf16 ? k_gate_fwd<4, true> : k_gate_fwd<4, false>), grid, block, 0, st, a); break;
   }
   return check_launch("asrn_gate_fwd");
 }
@@ -529,11 +557,12 @@ extern "C" int asrn_gate_bwd(const float* h, const void* aporte, int32_t aporte_
   const int groups = (int)gate_groups(BL);
   const int cols = d + kGateCols;
   hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)groups), block(kGateThreads);
   switch ((d + 4 * kWave - 1) / (4 * kWave)) {
-    case 1: hipLaunchKernelGGL(k_gate_bwd<1>, dim3(groups), dim3(kGateThreads), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(k_gate_bwd<2>, dim3(groups), dim3(kGateThreads), 0, st, a); break;
-    case 3: hipLaunchKernelGGL(k_gate_bwd<3>, dim3(groups), dim3(kGateThreads), 0, st, a); break;
-    default: hipLaunchKernelGGL(k_gate_bwd<4>, dim3(groups), dim3(kGateThreads), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((a.a_bf16 ? k_gate_bwd<1, true> : k_gate_bwd<1, false>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((a.a_bf16 ? k_gate_bwd<2, true> : k_gate_bwd<2, false>), grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((a.a_bf16 ? k_gate_bwd<3, true> : k_gate_bwd<3, false>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((a.a_bf16 ? k_gate_bwd<4, true> : k_gate_bwd<4, false>), grid, block, 0, st, a); break;
   }
   if (check_launch("asrn_gate_bwd")) return 1;
   return group_sums((const float*)workspace, groups, cols, dparams, st);
