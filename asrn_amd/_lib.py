@@ -96,6 +96,9 @@ SIGNATURES = {
                               + [_I64, _I64, _P, _P, _I64, _P]),
     'asrn_decode_produce_h': (ctypes.c_int, [_P, _I64, _I32, _P, _P, _F32, _P, _P, _F32, _F32, _P, _P, _I32, _P, _P, _P,
                                              _I64, _I64, _P, _P, _P]),
+    'asrn_decode_produce_h_ex': (ctypes.c_int, [_P] * 5 + [_I32, _I32, _P, _P, _P, _I64, _I64, _I32, _P, _P, _F32, _P,
+                                                      _P, _F32, _F32, _P, _P, _I32, _P, _P, _P, _I64, _I64, _P, _P,
+                                                      _P]),
     'asrn_decode_produce': (ctypes.c_int, [_P] * 4 + [_I64, _I32] + [_P] * 9 + [_I32] * 4 + [_P, _P, _F32, _P, _P, _F32,
                                                                                               _F32, _P, _P, _I32]
                             + [_P] * 6 + [_I64, _I64, _P, _P, _P, _I64, _P]),

@@ -22,7 +22,7 @@
 //
 // The row kernels hold their row in registers (up to kRowVals values a thread), so that the LayerNorm statistics and
 // the outputs need no second read of what they loaded or wrote.
-#include "common.h"
+#include "block_pending.h"
 
 namespace asrn {
 namespace {
@@ -32,7 +32,6 @@ constexpr int kGemvWaves = 4;
 constexpr int kGemvThreads = kGemvWaves * kWave;
 constexpr int kPrepThreads = 1024;
 constexpr int kPrepWaves = kPrepThreads / kWave;
-constexpr int kMaxSplits = 16;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
@@ -72,37 +71,9 @@ __device__ void row_stats(const float (&v)[R], int d, float eps, float* red, flo
 }
 
 // The row kernels below hold R columns a thread (column tid + j kPrepThreads, R = ceil(d / kPrepThreads)) and issue
-// every load before its first use as unconditional loads: columns past d read column d - 1, and splits past `splits`
-// re-read the last one, real addresses whose values are not used (a guarded load becomes a branch the compiler does
-// not schedule across, and each such load then waits on its own).
-
-// the S (>= splits) partial values of one column, split stride `stride`
-template <int S>
-__device__ __forceinline__ void split_loads(const float* p, int splits, int64_t stride, float (&v)[S]) {
-#pragma unroll
-  for (int s = 0; s < S; ++s) v[s] = p[(int64_t)(s < splits ? s : splits - 1) * stride];
-}
-// their sum in split order (the splits past `splits` add nothing)
-template <int S>
-__device__ __forceinline__ float split_total(const float (&v)[S], int splits) {
-  float y = 0.f;
-#pragma unroll
-  for (int s = 0; s < S; ++s) y += s < splits ? v[s] : 0.f;
-  return y;
-}
+// every load before its first use as unconditional loads (split_loads).
 
 constexpr int kMaxTaps = 8;                  // ring taps a thread loads ahead of the statistics (k - 1 <= 8)
-
-// A block whose last kernel was left to the next block's first (asrn_block_step_ex with finish = 0): its second
-// feed-forward product's partials and what k_finish_res would add them to
-struct Pending {
-  const float* part;  // (splits, B, d), null: no pending block
-  int splits;
-  const float* bias; const float* h1; const float* z;
-  float* ring;        // its ring (B, d, km1) takes z at slot pos mod km1
-  int km1;
-  float* out;         // its output, written here
-};
 
 // With PEND: the row is the pending block's output h1 + (sum of the splits + bias), formed as k_finish_res forms it,
 // written to pv.out, and the pending block's z enters its ring (k_finish_res's work, one row per workgroup).
@@ -313,8 +284,6 @@ using MixFn = void (*)(const float*, int, int64_t, const float*, const float*, i
 using ResFn = void (*)(const float*, int, int64_t, const float*, const float*, const float*, const int64_t*, int, int,
                        float*, float*);
 
-int split_cap(int splits) { return splits <= 4 ? 4 : (splits <= 8 ? 8 : 16); }
-
 template <int R>
 PrepFn prep_fn_r(bool pend, int S) {
   if (!pend) return k_prep_mix<R, 4, false>;
@@ -342,13 +311,6 @@ ResFn res_fn(int R, int splits) {
   return R == 1 ? res_fn_r<1>(S) : (R == 2 ? res_fn_r<2>(S) : (R == 3 ? res_fn_r<3>(S) : res_fn_r<4>(S)));
 }
 
-// depth splits: each wavefront's share at most 64 columns (one round of loads), at most kMaxSplits
-int splits_for(int N, int K) {
-  (void)N;
-  int s = (K + 4 * 64 - 1) / (4 * 64);
-  return s < 1 ? 1 : (s > kMaxSplits ? kMaxSplits : s);
-}
-
 int launch_part(Part g, hipStream_t st, const char* what) {
   const dim3 grid((unsigned)((g.N + kTile - 1) / kTile), (unsigned)g.splits, (unsigned)((g.B + kTile - 1) / kTile));
   if (g.bias) {
@@ -374,7 +336,7 @@ using namespace asrn;
 extern "C" int64_t asrn_block_step_workspace(int64_t B, int32_t d, int32_t ff) {
   // the conv and second feed-forward products' partials, (splits, B, N) floats each (the first sized for the most
   // splits), and the hidden layer (B, ff)
-  return 4 * B * ((int64_t)kMaxSplits * d + (int64_t)ff + (int64_t)splits_for(d, ff) * d);
+  return 4 * block_workspace_floats(B, d, ff);
 }
 
 namespace asrn {
@@ -399,14 +361,14 @@ int block_step(const float* h, int64_t ldh, const float* prev_h1, const float* p
   const int64_t need = asrn_block_step_workspace(B, d, prev_h1 && prev_ff > ff ? prev_ff : ff);
   ASRN_REQUIRE(workspace != nullptr && workspace_bytes >= need,
                "%s: workspace of %lld bytes needed (asrn_block_step_workspace)", what, (long long)need);
-  const int s1 = splits_for(d, d * k), s3 = splits_for(d, ff);
+  const int s1 = splits_for(d * k), s3 = splits_for(ff);
   float* p1 = (float*)workspace;
-  float* hid = p1 + (int64_t)kMaxSplits * B * d;
-  float* p3 = hid + (int64_t)B * ff;
+  float* hid = block_hidden(workspace, B, d);
+  float* p3 = block_second_parts(workspace, B, d, ff);
   Pending pv = {};
   if (prev_h1)   // the pending block's partials, where its call (same workspace, same B and d) left them
-    pv = Pending{hid + (int64_t)B * prev_ff, splits_for(d, prev_ff), prev_b2, prev_h1, prev_z, prev_ring, prev_k - 1,
-                 prev_out};
+    pv = Pending{block_second_parts(workspace, B, d, prev_ff), splits_for(prev_ff), prev_b2, prev_h1, prev_z,
+                 prev_ring, prev_k - 1, prev_out};
   const int R = (d + kPrepThreads - 1) / kPrepThreads;
   hipLaunchKernelGGL(prep_fn(R, prev_h1 != nullptr, pv.splits), dim3((unsigned)B), dim3(kPrepThreads), 0, st,
                      prev_h1 ? prev_out : h, prev_h1 ? (int64_t)d : ldh, pv, ring, pos, ln1_w, ln1_b, eps, d, k, z, x1);

@@ -19,7 +19,7 @@
 // B = 16: about 1080 workgroups; 16 tokens and 16 rows per workgroup took 31 us, this 8). The second takes one token per workgroup: the hidden units,
 // both second layers and the clock. Every sum runs in a fixed order. The position is t, or *t_dev (a step replayed
 // from a graph); a position outside [1, cap) writes nothing.
-#include "common.h"
+#include "block_pending.h"
 
 namespace asrn {
 
@@ -254,16 +254,32 @@ __global__ __launch_bounds__(kProdThreads) void k_produce_token_e(ProdBatch pb) 
 // rows in flight; the clock from w_reloj hh + b_reloj by the last wave. The sums are those of the two-kernel producer
 // in the same order (layer_norm_rows, the rows' products, the clock), so the outputs are the same bits. Every load of
 // the first chunk is issued before the row's statistics.
+// PEND: h_t is the output of a local block step left pending (block_pending.h), formed here first: thread c sums
+// column c as the block step's k_finish_res does, writes it to pv.out and the block's z into its ring (slot *pend_pos
+// mod k - 1), and stages it in LDS for the waves' LayerNorm. Those loads are issued before the weight rows', so the
+// sum waits only on them (the load counter counts in order); the block's output is formed whatever the position.
 constexpr int kHWaves = 16;
 constexpr int kHChunk = 4;
 
-template <int D4>
-__global__ __launch_bounds__(kHWaves * kWave) void k_produce_h(ProdArgs a) {
+template <int D4, int S, bool PEND>
+__global__ __launch_bounds__(kHWaves * kWave) void k_produce_h(ProdArgs a, Pending pv, const int64_t* pend_pos) {
+  __shared__ float row_s[PEND ? 4 * kProdMaxD4 * kWave : 1];
   const int64_t t = prod_pos(a);
-  if (t < 1 || t >= a.cap) return;
+  const bool live = t >= 1 && t < a.cap;
+  if (!PEND && !live) return;
   const int64_t b = blockIdx.x;
   const int lane = lane_id(), wave = threadIdx.x >> 6;
   const int d4 = a.d >> 2;
+  float pv_x = 0.f, pv_b = 0.f, pv_z = 0.f, pv_p[S];
+  const int c = threadIdx.x, cc = c < a.d ? c : a.d - 1;   // d <= 4 kProdMaxD4 kWave = the workgroup's threads
+  int slot = 0;
+  if constexpr (PEND) {
+    slot = pv.km1 > 0 ? (int)(*pend_pos % pv.km1) : 0;
+    pv_x = pv.h1[b * a.d + cc];
+    split_loads<S>(pv.part + b * a.d + cc, pv.splits, gridDim.x * (int64_t)a.d, pv_p);
+    pv_b = pv.bias[cc];
+    pv_z = pv.km1 > 0 ? pv.z[b * a.d + cc] : 0.f;
+  }
   const float inv_d = 1.f / (float)a.d;
   const bool clk = wave == kHWaves - 1;
   const int nr = 2 * a.cf;
@@ -277,7 +293,7 @@ __global__ __launch_bounds__(kHWaves * kWave) void k_produce_h(ProdArgs a) {
 #pragma unroll
   for (int k = 0; k < D4; ++k) {
     const int q = lane + kWave * k < d4 ? lane + kWave * k : d4 - 1;
-    x[k] = ((const float4*)(a.h + b * a.d))[q];
+    if constexpr (!PEND) x[k] = ((const float4*)(a.h + b * a.d))[q];
     lw[k] = ((const float4*)a.lnw)[q];
     lb[k] = ((const float4*)a.lnb)[q];
 #pragma unroll
@@ -285,6 +301,19 @@ __global__ __launch_bounds__(kHWaves * kWave) void k_produce_h(ProdArgs a) {
       const float* row = clk ? a.wr + (int64_t)(i & 1) * a.d : row_of(wave + (kHWaves - 1) * i);
       w[i][k] = ((const float4*)row)[q];
     }
+  }
+  if constexpr (PEND) {
+    const float v = pv_x + (split_total<S>(pv_p, pv.splits) + pv_b);
+    if (c < a.d) {
+      pv.out[b * a.d + c] = v;
+      if (pv.km1 > 0) pv.ring[(b * a.d + c) * pv.km1 + slot] = pv_z;
+      row_s[c] = v;
+    }
+    __syncthreads();
+    if (!live) return;
+#pragma unroll
+    for (int k = 0; k < D4; ++k)
+      x[k] = reinterpret_cast<const float4*>(row_s)[lane + kWave * k < d4 ? lane + kWave * k : d4 - 1];
   }
   // hh, as layer_norm_rows forms it
   float s = 0.f;
@@ -472,34 +501,89 @@ extern "C" int asrn_decode_produce_e(int32_t L, const float* e, const float* e_p
   return check_launch("asrn_decode_produce_e/token");
 }
 
-extern "C" int asrn_decode_produce_h(const float* h, int64_t B, int32_t d, const float* ln_w, const float* ln_b,
-                                     float eps, const float* w_reloj, const float* b_reloj, float beta_max,
-                                     float log_alfa_min, const float* w_cq, const float* w_ck, int32_t cf, float* Qc,
-                                     float* Kc, float* log_alfa, int64_t cap, int64_t t, const int64_t* t_dev,
-                                     double* beta, void* stream) {
-  ASRN_REQUIRE(B >= 0 && d > 0 && d % 4 == 0 && d <= 4 * kProdMaxD4 * kWave,
-               "asrn_decode_produce_h: d=%d must be a positive multiple of 4, <= %d", d, 4 * kProdMaxD4 * kWave);
-  ASRN_REQUIRE(cf >= 1 && cf <= kProdMax, "asrn_decode_produce_h: cf=%d must be in [1, %d]", cf, kProdMax);
-  ASRN_REQUIRE(eps > 0.f, "asrn_decode_produce_h: eps must be positive");
-  ASRN_REQUIRE(t >= 1 && t < cap, "asrn_decode_produce_h: position t=%lld outside [1, capacity %lld)", (long long)t,
+namespace asrn {
+namespace {
+
+using ProduceH = void (*)(ProdArgs, Pending, const int64_t*);
+
+template <int D4>
+ProduceH produce_h_fn(bool pend, int S) {
+  if (!pend) return k_produce_h<D4, 1, false>;
+  return S == 4 ? k_produce_h<D4, 4, true> : (S == 8 ? k_produce_h<D4, 8, true> : k_produce_h<D4, 16, true>);
+}
+
+int produce_h(const float* h, const float* prev_h1, const float* prev_b2, const float* prev_z, float* prev_ring,
+              int32_t prev_k, int32_t prev_ff, float* prev_out, const int64_t* prev_pos, void* workspace,
+              int64_t workspace_bytes, int64_t B, int32_t d, const float* ln_w, const float* ln_b, float eps,
+              const float* w_reloj, const float* b_reloj, float beta_max, float log_alfa_min, const float* w_cq,
+              const float* w_ck, int32_t cf, float* Qc, float* Kc, float* log_alfa, int64_t cap, int64_t t,
+              const int64_t* t_dev, double* beta, hipStream_t st, const char* what) {
+  ASRN_REQUIRE(B >= 0 && B <= (int64_t(1) << 20) && d > 0 && d % 4 == 0 && d <= 4 * kProdMaxD4 * kWave,
+               "%s: d=%d must be a positive multiple of 4, <= %d (B=%lld)", what, d, 4 * kProdMaxD4 * kWave,
+               (long long)B);
+  ASRN_REQUIRE(cf >= 1 && cf <= kProdMax, "%s: cf=%d must be in [1, %d]", what, cf, kProdMax);
+  ASRN_REQUIRE(eps > 0.f, "%s: eps must be positive", what);
+  ASRN_REQUIRE(t >= 1 && t < cap, "%s: position t=%lld outside [1, capacity %lld)", what, (long long)t,
                (long long)cap);
-  ASRN_REQUIRE(h && ln_w && ln_b && w_reloj && b_reloj && w_cq && w_ck && Qc && Kc && log_alfa && beta,
-               "asrn_decode_produce_h: null pointer");
-  for (const void* p : {(const void*)h, (const void*)ln_w, (const void*)ln_b, (const void*)w_reloj,
-                        (const void*)w_cq, (const void*)w_ck})
-    ASRN_REQUIRE(((uintptr_t)p & 15) == 0, "asrn_decode_produce_h: the rows are read as float4: 16-byte alignment");
+  ASRN_REQUIRE((h || prev_h1) && ln_w && ln_b && w_reloj && b_reloj && w_cq && w_ck && Qc && Kc && log_alfa && beta,
+               "%s: null pointer", what);
+  for (const void* p : {(const void*)(prev_h1 ? prev_out : h), (const void*)ln_w, (const void*)ln_b,
+                        (const void*)w_reloj, (const void*)w_cq, (const void*)w_ck})
+    ASRN_REQUIRE(((uintptr_t)p & 15) == 0, "%s: the rows are read as float4: 16-byte alignment", what);
+  Pending pv = {};
+  if (prev_h1) {
+    ASRN_REQUIRE(prev_b2 && prev_z && prev_out && prev_pos && prev_k >= 1 && prev_ff >= 1 && prev_ff <= (1 << 30) &&
+                     (prev_k == 1 || prev_ring),
+                 "%s: a pending block needs its b2, z, out, position, k >= 1, ff >= 1 and (k > 1) its ring", what);
+    const int64_t need = 4 * block_workspace_floats(B, d, prev_ff);
+    ASRN_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+                 "%s: the pending block's workspace of %lld bytes needed (asrn_block_step_workspace)", what,
+                 (long long)need);
+    // its partials, where its block step call (same workspace, same B and d) left them
+    pv = Pending{block_second_parts(workspace, B, d, prev_ff), splits_for(prev_ff), prev_b2, prev_h1, prev_z,
+                 prev_ring, prev_k - 1, prev_out};
+  }
   if (B == 0) return 0;
   ProdArgs a = {};
   a.h = h; a.B = B; a.d = d; a.lnw = ln_w; a.lnb = ln_b; a.eps = eps; a.wr = w_reloj; a.br = b_reloj;
   a.beta_max = beta_max; a.la_min = log_alfa_min; a.wq = w_cq; a.wk = w_ck; a.cf = cf;
   a.Qc = Qc; a.Kc = Kc; a.la = log_alfa; a.cap = cap; a.t = t; a.t_dev = t_dev; a.beta = beta;
-  hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((unsigned)B), block(kHWaves * kWave);
+  const bool pend = prev_h1 != nullptr;
+  const int S = split_cap(pv.splits);
+  ProduceH fn;
   switch ((d + 4 * kWave - 1) / (4 * kWave)) {
-    case 1: hipLaunchKernelGGL(k_produce_h<1>, grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL(k_produce_h<2>, grid, block, 0, st, a); break;
-    case 3: hipLaunchKernelGGL(k_produce_h<3>, grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL(k_produce_h<4>, grid, block, 0, st, a); break;
+    case 1: fn = produce_h_fn<1>(pend, S); break;
+    case 2: fn = produce_h_fn<2>(pend, S); break;
+    case 3: fn = produce_h_fn<3>(pend, S); break;
+    default: fn = produce_h_fn<4>(pend, S); break;
   }
-  return check_launch("asrn_decode_produce_h");
+  hipLaunchKernelGGL(fn, dim3((unsigned)B), dim3(kHWaves * kWave), 0, st, a, pv, prev_pos);
+  return check_launch(what);
+}
+
+}  // namespace
+}  // namespace asrn
+
+extern "C" int asrn_decode_produce_h(const float* h, int64_t B, int32_t d, const float* ln_w, const float* ln_b,
+                                     float eps, const float* w_reloj, const float* b_reloj, float beta_max,
+                                     float log_alfa_min, const float* w_cq, const float* w_ck, int32_t cf, float* Qc,
+                                     float* Kc, float* log_alfa, int64_t cap, int64_t t, const int64_t* t_dev,
+                                     double* beta, void* stream) {
+  ASRN_REQUIRE(h, "asrn_decode_produce_h: null pointer");
+  return produce_h(h, nullptr, nullptr, nullptr, nullptr, 0, 0, nullptr, nullptr, nullptr, 0, B, d, ln_w, ln_b, eps,
+                   w_reloj, b_reloj, beta_max, log_alfa_min, w_cq, w_ck, cf, Qc, Kc, log_alfa, cap, t, t_dev, beta,
+                   (hipStream_t)stream, "asrn_decode_produce_h");
+}
+
+extern "C" int asrn_decode_produce_h_ex(const float* h, const float* prev_h1, const float* prev_b2,
+                                        const float* prev_z, float* prev_ring, int32_t prev_k, int32_t prev_ff,
+                                        float* prev_out, const int64_t* prev_pos, void* workspace,
+                                        int64_t workspace_bytes, int64_t B, int32_t d, const float* ln_w,
+                                        const float* ln_b, float eps, const float* w_reloj, const float* b_reloj,
+                                        float beta_max, float log_alfa_min, const float* w_cq, const float* w_ck,
+                                        int32_t cf, float* Qc, float* Kc, float* log_alfa, int64_t cap, int64_t t,
+                                        const int64_t* t_dev, double* beta, void* stream) {
+  return produce_h(h, prev_h1, prev_b2, prev_z, prev_ring, prev_k, prev_ff, prev_out, prev_pos, workspace,
+                   workspace_bytes, B, d, ln_w, ln_b, eps, w_reloj, b_reloj, beta_max, log_alfa_min, w_cq, w_ck, cf,
+                   Qc, Kc, log_alfa, cap, t, t_dev, beta, (hipStream_t)stream, "asrn_decode_produce_h_ex");
 }

@@ -108,14 +108,20 @@ class EscritorCapa:
         else:
             c[:, pos] = valor
 
-    def _cuerpo(self, e_t, e_ult, h_t, pieza_t, pos, t_max=None, producido=False):
+    def _cuerpo(self, e_t, e_ult, h_t, pieza_t, pos, t_max=None, producido=False, previo=None):
         """One step's work at position pos (an int, or a one-element device buffer holding it, t_max its largest value) ->
         the layer's output (B, d) (the layer part of asrn/nucleo.py:1797-1854). producido: the rows that act on e_t
-        (V, phi, sig) are already in the caches (ops.decode_produce_e, for every layer of a model at once)."""
+        (V, phi, sig) are already in the caches (ops.decode_produce_e, for every layer of a model at once). previo
+        (with producido): the local block step left pending whose output is h_t (h_t is then None); the producer
+        forms it (ops.decode_produce_h)."""
         capa = self.capa
         c = self.cache
+        if previo is not None and not producido:
+            raise ValueError('EscritorCapa: a pending block step is finished by the producer of decode_produce_e')
         if producido:
-            beta_t = ops.decode_produce_h(capa, c, h_t, pos, t_max=t_max)
+            beta_t = ops.decode_produce_h(capa, c, h_t, pos, t_max=t_max, previo=previo)
+            if previo is not None:
+                h_t = previo.out
         elif ops.decode_produce_ok(capa, e_t):
             # fp32: the token's V, phi, Qc, Kc, log_alfa and id rows in two kernels (asrn_decode_produce)
             beta_t = ops.decode_produce(capa, c, e_t, e_ult, h_t, pieza_t, pos, t_max=t_max)

@@ -131,13 +131,18 @@ class EscritorModelo:
         pendiente = None
         nb = len(m.bloques)
         for i, blq in enumerate(m.bloques):
-            # two fused blocks in a row: the first's last launch is done by the second's first
-            encadenar = self.fusion[i] and i not in m.pos_largo and i + 1 < nb and self.fusion[i + 1]
+            # a fused block's last launch is done by the next kernel that reads its output: the next block's first
+            # when that is fused too, the ASRN layer's producer when one follows (with the embedding rows produced)
+            if i in m.pos_largo:
+                encadenar = self.fusion[i] and producido
+            else:
+                encadenar = self.fusion[i] and i + 1 < nb and self.fusion[i + 1]
             r = self._bloque(i, blq, h, k, pos, previo=pendiente, terminar=not encadenar)
             pendiente, h = (r, None) if encadenar else (None, r)
             k += blq.mezcla == 'memoria'
             if i in m.pos_largo:
-                h = next(capas)._cuerpo(e_t, e_ant, h, pieza, pos, t_max=t_max, producido=producido)
+                h = next(capas)._cuerpo(e_t, e_ant, h, pieza, pos, t_max=t_max, producido=producido, previo=pendiente)
+                pendiente = None
         if e_prev is None:
             self.e_ult.copy_(e_t)
         x = m.ln_f(h)

@@ -966,10 +966,13 @@ def decode_produce_e(capas, caches, e, e_prev, pieza, t, t_max=None):
          tdev, ptr(ws), wsb, stream_of(dev))
 
 
-def decode_produce_h(capa, cache, h, t, t_max=None):
+def decode_produce_h(capa, cache, h, t, t_max=None, previo=None):
     """The part of the generation step's producers that acts on the layer input h (asrn_decode_produce_h): Qc[t],
     Kc[t] and log_alfa[t] written into the caches; returns beta (B,) fp64. With decode_produce_e, the same bits as
-    decode_produce."""
+    decode_produce. previo: a BloquePendiente whose output is the layer input (h is then None): it is formed here, into
+    previo.out, as the block step's last kernel forms it (asrn_decode_produce_h_ex)."""
+    if previo is not None:
+        h = previo.out
     dev = _dev(h)
     B, d = h.shape
     cap = cache['phi'].shape[1]
@@ -978,11 +981,16 @@ def decode_produce_h(capa, cache, h, t, t_max=None):
     la_min = -math.inf if p.log_alfa_min is None else float(p.log_alfa_min)
     beta = torch.empty((B,), dtype=torch.float64, device=dev)
     th, tdev = _posicion(t, t_max)
-    hh = _c(h, torch.float32)
-    call('asrn_decode_produce_h', ptr(hh), B, d, ptr(capa.ln_ctx.weight), ptr(capa.ln_ctx.bias),
-         float(capa.ln_ctx.eps), ptr(capa.w_reloj), ptr(capa.b_reloj), beta_max, la_min, ptr(capa.cq.weight),
-         ptr(capa.ck.weight), capa.confirmar, ptr(cache['Qc']), ptr(cache['Kc']), ptr(cache['log_alfa']), cap, th, tdev,
-         ptr(beta), stream_of(dev))
+    tail = (ptr(capa.ln_ctx.weight), ptr(capa.ln_ctx.bias), float(capa.ln_ctx.eps), ptr(capa.w_reloj),
+            ptr(capa.b_reloj), beta_max, la_min, ptr(capa.cq.weight), ptr(capa.ck.weight), capa.confirmar,
+            ptr(cache['Qc']), ptr(cache['Kc']), ptr(cache['log_alfa']), cap, th, tdev, ptr(beta), stream_of(dev))
+    if previo is None:
+        hh = _c(h, torch.float32)
+        call('asrn_decode_produce_h', ptr(hh), B, d, *tail)
+        return beta
+    pv = previo
+    call('asrn_decode_produce_h_ex', None, ptr(pv.h1), ptr(pv.b2), ptr(pv.z), ptr(pv.anillo), pv.k, pv.ff, ptr(pv.out),
+         ptr(pv.pos), ptr(pv.espacio), pv.espacio.numel(), B, d, *tail)
     return beta
 
 
@@ -1150,10 +1158,11 @@ def espacio_bloque(B, d, ff, dev):
 class BloquePendiente:
     """A block step whose last launch was left to the next block's first (paso_bloque(..., terminar=False)): `out` is
     the (B, d) buffer its output will be written into, and it must be passed as `previo` to the next paso_bloque call,
-    with the same workspace, before anything reads `out`."""
+    with the same workspace, or to decode_produce_h, before anything reads `out` or uses the workspace."""
 
-    def __init__(self, out, h1, b2, z, anillo, k, ff):
+    def __init__(self, out, h1, b2, z, anillo, k, ff, pos=None, espacio=None):
         self.out, self.h1, self.b2, self.z, self.anillo, self.k, self.ff = out, h1, b2, z, anillo, k, ff
+        self.pos, self.espacio = pos, espacio      # its position and its workspace (uint8 device tensor)
 
 
 def paso_bloque(blq, h, anillo, pos, espacio, previo=None, terminar=True):
@@ -1187,7 +1196,7 @@ def paso_bloque(blq, h, anillo, pos, espacio, previo=None, terminar=True):
          espacio.numel(), stream_of(dev))
     if terminar:
         return out
-    return BloquePendiente(out, h1, ws[9], z, anillo, k, ff)
+    return BloquePendiente(out, h1, ws[9], z, anillo, k, ff, pos, espacio)
 
 
 # ---------------------------------------------------------------------------------------------------------------------

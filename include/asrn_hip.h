@@ -444,6 +444,18 @@ int asrn_decode_produce_h(const float* h, int64_t B, int32_t d, const float* ln_
                           const float* w_reloj, const float* b_reloj, float beta_max, float log_alfa_min,
                           const float* w_cq, const float* w_ck, int32_t cf, float* Qc, float* Kc, float* log_alfa,
                           int64_t cap, int64_t t, const int64_t* t_dev, double* beta, void* stream);
+/* decode_produce_h on the output of a local block step left pending (asrn_block_step_ex with finish = 0; prev_*, its
+ * arguments as asrn_block_step_ex takes them, prev_pos its position, workspace the one its call used): the layer input
+ * is that block's output, formed here (h1 + the second feed-forward product + b2, written to prev_out, its z into its
+ * ring) with the bits the block step's last kernel gives, then the producer's rows as asrn_decode_produce_h. h is
+ * then not read. No counterpart in the reference: it saves the block step's last launch before every ASRN layer. */
+int asrn_decode_produce_h_ex(const float* h, const float* prev_h1, const float* prev_b2, const float* prev_z,
+                             float* prev_ring, int32_t prev_k, int32_t prev_ff, float* prev_out,
+                             const int64_t* prev_pos, void* workspace, int64_t workspace_bytes, int64_t B, int32_t d,
+                             const float* ln_w, const float* ln_b, float eps, const float* w_reloj,
+                             const float* b_reloj, float beta_max, float log_alfa_min, const float* w_cq,
+                             const float* w_ck, int32_t cf, float* Qc, float* Kc, float* log_alfa, int64_t cap,
+                             int64_t t, const int64_t* t_dev, double* beta, void* stream);
 
 /* ---- generation loop: n-gram sets and the per-token choice ------------------------------------------------------
  * The host side of escribir (asrn/nucleo.py:1965-2043) moved onto the device. The n-gram sets replace _Ngramas

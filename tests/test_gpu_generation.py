@@ -427,3 +427,42 @@ def test_decode_produce_split_equals_whole(B, d, kw, L):
         for k in whole[l]:
             assert torch.equal(whole[l][k], split[l][k]), (l, k)
         assert not torch.equal(whole[l]['phi'], caches[l]['phi'])     # the step wrote something
+
+
+@pytest.mark.parametrize('B,d,kw,k,ff', [(16, 768, {}, 4, 1536), (3, 64, SMALL, 1, 40),
+                                         (2, 32, dict(confirmar=8, n_tablas=5, n_bits=4), 3, 4096)])
+def test_decode_produce_h_finishes_pending_block(B, d, kw, k, ff):
+    """A local block step left pending (asrn_block_step_ex, finish = 0) then finished by the layer's producer
+    (asrn_decode_produce_h_ex) against the finished block step then asrn_decode_produce_h on its output, bit for bit:
+    the block's output and ring, every cache and beta. The feed-forward widths give 6, 1 and 16 depth splits of the
+    second product (the 8-, 4- and 16-load instances); k = 1 has no ring."""
+    say('decode produce h pending', B, d, kw, k, ff)
+    x, E, h = synth.layer_inputs(B, 40, d, 9, seed=4)
+    torch.manual_seed(20)
+    layer = synth.move_params(CapaASRNEstable(d, **kw), 20).to(DEV)
+    esc = EscritorCapa(layer, memoria_de_lo_ajeno=False)
+    esc.inicio(E.to(DEV)[:, :30], h.to(DEV)[:, :30], x.to(DEV)[:, :30], capacidad=40)
+    t = 30
+    pos = torch.full((1,), t, dtype=torch.int64, device=DEV)
+    with torch.no_grad():
+        blq = asrn_amd.BloqueLocal(d, k, ff).to(DEV)
+        for p in blq.parameters():
+            p.add_(torch.randn_like(p) * 0.1)
+        hin = torch.randn(B, d, device=DEV)
+        anillo = torch.randn(B, d, k - 1, device=DEV) if k > 1 else None
+        anillo2 = anillo.clone() if k > 1 else None
+        espacio = ops.espacio_bloque(B, d, ff, DEV)
+        whole = {kk: v.clone() for kk, v in esc.cache.items()}
+        fused = {kk: v.clone() for kk, v in esc.cache.items()}
+        out = ops.paso_bloque(blq, hin, anillo, pos, espacio)
+        beta_w = ops.decode_produce_h(layer, whole, out, pos, t_max=t)
+        pend = ops.paso_bloque(blq, hin, anillo2, pos, espacio, terminar=False)
+        assert isinstance(pend, ops.BloquePendiente)
+        beta_f = ops.decode_produce_h(layer, fused, None, pos, t_max=t, previo=pend)
+        torch.cuda.synchronize()
+    assert torch.equal(out, pend.out)
+    assert k == 1 or torch.equal(anillo, anillo2)
+    assert torch.equal(beta_w, beta_f)
+    for kk in whole:
+        assert torch.equal(whole[kk], fused[kk]), kk
+    assert not torch.equal(whole['Qc'], esc.cache['Qc'])              # the step wrote something

@@ -186,6 +186,15 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert lib.asrn_decode_produce(*prod, 16, 768, *w, 64, 64, 56, 56, N, N, 1e-5, N, N, 1e4, -30.0, N, N, 16,
                                    *([N] * 6), 100, 50, N, N, N, 0, N) != 0
     assert 'workspace' in _err(lib)
+    # the producer on a pending block: the block's pointers, then its workspace (for the block's feed-forward width)
+    hx = [N, 16, 768, P1, P1, 1e-5, P1, P1, 1e4, -30.0, P1, P1, 16, P1, P1, P1, 100, 50, N, P1, N]
+    assert lib.asrn_decode_produce_h_ex(N, P1, N, P1, P1, 4, 1536, P1, P1, P1, 1 << 30, *hx[1:]) != 0
+    assert 'pending block' in _err(lib)
+    need = lib.asrn_block_step_workspace(16, 768, 1536)
+    assert lib.asrn_decode_produce_h_ex(N, P1, P1, P1, P1, 4, 1536, P1, P1, P1, need - 4, *hx[1:]) != 0
+    assert 'workspace' in _err(lib)
+    assert lib.asrn_decode_produce_h_ex(N, N, N, N, N, 0, 0, N, N, N, 0, *hx[1:]) != 0
+    assert 'null pointer' in _err(lib)
 
 
 def test_ops_refuse_cpu_tensors():
