@@ -413,3 +413,27 @@ extern "C" int asrn_block_step_ex(const float* h, int64_t ldh, const float* prev
                     ln1_w, ln1_b, conv_w, conv_b, ln2_w, ln2_b, w1, b1, w2, b2, eps, z, x1, h1, x2, out, finish,
                     workspace, workspace_bytes, (hipStream_t)stream, "asrn_block_step_ex");
 }
+
+extern "C" int asrn_block_finish_norm(const float* prev_h1, const float* prev_b2, const float* prev_z,
+                                      float* prev_ring, int32_t prev_k, int32_t prev_ff, float* prev_out,
+                                      const int64_t* pos, int64_t B, int32_t d, const float* ln_w, const float* ln_b,
+                                      float eps, float* y, void* workspace, int64_t workspace_bytes, void* stream) {
+  ASRN_REQUIRE(B >= 1 && B <= (int64_t(1) << 20) && d >= 1 && d <= kRowVals * kPrepThreads,
+               "asrn_block_finish_norm: bad sizes B=%lld d=%d (d <= %d)", (long long)B, d, kRowVals * kPrepThreads);
+  ASRN_REQUIRE(prev_h1 && prev_b2 && prev_z && prev_out && pos && ln_w && ln_b && y && prev_k >= 1 && prev_ff >= 1 &&
+                   prev_ff <= (1 << 30) && (prev_k == 1 || prev_ring),
+               "asrn_block_finish_norm: a pending block needs its h1, b2, z, out, k >= 1, ff >= 1 and (k > 1) its "
+               "ring, and the norm its weights and output (null pointer)");
+  const int64_t need = 4 * block_workspace_floats(B, d, prev_ff);
+  ASRN_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+               "asrn_block_finish_norm: the pending block's workspace of %lld bytes needed (asrn_block_step_workspace)",
+               (long long)need);
+  const Pending pv{block_second_parts(workspace, B, d, prev_ff), splits_for(prev_ff), prev_b2, prev_h1, prev_z,
+                   prev_ring, prev_k - 1, prev_out};
+  // the row kernel of a block that follows a pending one, with one tap (k = 1): its LayerNorm row is the output, and
+  // its conv operand [z] the same values at the same addresses
+  const int R = (d + kPrepThreads - 1) / kPrepThreads;
+  hipLaunchKernelGGL(prep_fn(R, true, pv.splits), dim3((unsigned)B), dim3(kPrepThreads), 0, (hipStream_t)stream,
+                     prev_out, (int64_t)d, pv, nullptr, pos, ln_w, ln_b, eps, d, 1, y, y);
+  return check_launch("asrn_block_finish_norm");
+}

@@ -76,6 +76,9 @@ class EscritorModelo:
             if i in m.pos_largo:
                 h = next(capas).inicio(E, h, x0, capacidad=self.cap)
         self.e_ult = E[:, -1].contiguous()
+        # the last block's end and the final norm in one launch (ops.norma_pendiente) when that block is fused
+        self.norma_final = bool(self.fusion) and self.fusion[-1] and ops.norma_pendiente_ok(m.ln_f, h.shape[-1],
+                                                                                              x0.device)
         self.t = L0
         self.pos = torch.full((1,), L0, dtype=torch.int64, device=x0.device)
         return m.head(m.ln_f(h[:, -1]))
@@ -132,11 +135,14 @@ class EscritorModelo:
         nb = len(m.bloques)
         for i, blq in enumerate(m.bloques):
             # a fused block's last launch is done by the next kernel that reads its output: the next block's first
-            # when that is fused too, the ASRN layer's producer when one follows (with the embedding rows produced)
+            # when that is fused too, the ASRN layer's producer when one follows (with the embedding rows produced),
+            # the final norm after the last block
             if i in m.pos_largo:
                 encadenar = self.fusion[i] and producido
+            elif i + 1 < nb:
+                encadenar = self.fusion[i] and self.fusion[i + 1]
             else:
-                encadenar = self.fusion[i] and i + 1 < nb and self.fusion[i + 1]
+                encadenar = self.fusion[i] and self.norma_final
             r = self._bloque(i, blq, h, k, pos, previo=pendiente, terminar=not encadenar)
             pendiente, h = (r, None) if encadenar else (None, r)
             k += blq.mezcla == 'memoria'
@@ -145,7 +151,7 @@ class EscritorModelo:
                 pendiente = None
         if e_prev is None:
             self.e_ult.copy_(e_t)
-        x = m.ln_f(h)
+        x = m.ln_f(h) if pendiente is None else ops.norma_pendiente(m.ln_f, pendiente)
         if (out is not None and m.head.bias is None and x.dtype == out.dtype == m.head.weight.dtype
                 and not torch.is_autocast_enabled(x.device.type)):
             return torch.mm(x, m.head.weight.t(), out=out)

@@ -1199,6 +1199,28 @@ def paso_bloque(blq, h, anillo, pos, espacio, previo=None, terminar=True):
     return BloquePendiente(out, h1, ws[9], z, anillo, k, ff, pos, espacio)
 
 
+def norma_pendiente_ok(ln, d, dev):
+    """Whether norma_pendiente takes this LayerNorm after blocks of width d on the GPU dev: fp32 affine weights of
+    that width on a GPU, outside autocast."""
+    return (isinstance(ln, torch.nn.LayerNorm) and ln.elementwise_affine and ln.bias is not None
+            and ln.weight.dtype == torch.float32 and ln.weight.is_cuda and torch.device(dev).type == 'cuda'
+            and tuple(ln.normalized_shape) == (d,) and d <= 4096 and not torch.is_autocast_enabled('cuda'))
+
+
+def norma_pendiente(ln, previo):
+    """ln(previo's output) for a BloquePendiente, its output formed first (into previo.out, its ring row too) as the
+    block step's last kernel forms it, in one launch (asrn_block_finish_norm): the last block's end and the final
+    norm of the generation step (asrn/nucleo.py:1854). The norm is the row kernels' two-pass LayerNorm (biased
+    variance)."""
+    pv = previo
+    B, d = pv.out.shape
+    y = torch.empty((B, d), dtype=torch.float32, device=pv.out.device)
+    call('asrn_block_finish_norm', ptr(pv.h1), ptr(pv.b2), ptr(pv.z), ptr(pv.anillo), pv.k, pv.ff, ptr(pv.out),
+         ptr(pv.pos), B, d, ptr(_c(ln.weight.detach())), ptr(_c(ln.bias.detach())), float(ln.eps), ptr(y),
+         ptr(pv.espacio), pv.espacio.numel(), stream_of(pv.out.device))
+    return y
+
+
 # ---------------------------------------------------------------------------------------------------------------------
 # the model's loss
 # ---------------------------------------------------------------------------------------------------------------------

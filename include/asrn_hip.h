@@ -522,6 +522,14 @@ int asrn_block_step_ex(const float* h, int64_t ldh, const float* prev_h1, const 
                        const float* ln2_b, const float* w1, const float* b1, const float* w2, const float* b2,
                        float eps, float* z, float* x1, float* h1, float* x2, float* out, int32_t finish,
                        void* workspace, int64_t workspace_bytes, void* stream);
+/* A block step left pending (asrn_block_step_ex with finish = 0; prev_*, its arguments, pos its position, workspace the
+ * one its call used) finished, then the model's final LayerNorm (ln_w, ln_b, eps; biased variance) of its output into
+ * y (B, d): the block's output (written to prev_out) and ring row with the bits its last kernel gives. No counterpart
+ * in the reference: one launch for the last block's end and the final norm (nucleo:1854). */
+int asrn_block_finish_norm(const float* prev_h1, const float* prev_b2, const float* prev_z, float* prev_ring,
+                           int32_t prev_k, int32_t prev_ff, float* prev_out, const int64_t* pos, int64_t B, int32_t d,
+                           const float* ln_w, const float* ln_b, float eps, float* y, void* workspace,
+                           int64_t workspace_bytes, void* stream);
 
 /* ---- the model's loss: cross-entropy ---------------------------------------------------------------------------
  * Replaces F.cross_entropy(logits.float().reshape(-1, V), y.reshape(-1), ignore_index) of ModeloASRN.perdida and the

@@ -463,6 +463,39 @@ def test_block_step_chained_equals_separate(B, d, ks, ffs):
             assert (anillos[i] is None) or torch.equal(anillos[i], anillos2[i]), i
 
 
+@pytest.mark.parametrize('B,d,k,ff', [(16, 768, 4, 1536), (3, 2080, 1, 300), (5, 96, 3, 4096)])
+def test_block_finish_norm_equals_block_then_layer_norm(B, d, k, ff):
+    """A block step left pending, then finished with the final LayerNorm in one launch (asrn_block_finish_norm), against
+    the finished block step then torch's LayerNorm: the block's output and ring bit for bit, the norm within 2e-6 of
+    torch's (a two-pass biased variance against torch's own reduction order). Widths past 1,024 hold several columns
+    a thread; the feed-forward widths give 6, 2 and 16 depth splits; k = 1 has no ring."""
+    say('block finish norm', B, d, k, ff)
+    torch.manual_seed(B + d + k)
+    with torch.no_grad():
+        blq = asrn_amd.BloqueLocal(d, k, ff).to(DEV)
+        for p in blq.parameters():
+            p.add_(torch.randn_like(p) * 0.1)
+        ln = torch.nn.LayerNorm(d).to(DEV)
+        ln.weight.add_(torch.randn_like(ln.weight) * 0.3)
+        ln.bias.add_(torch.randn_like(ln.bias) * 0.3)
+        h = torch.randn(B, d, device=DEV)
+        anillo = torch.randn(B, d, k - 1, device=DEV) if k > 1 else None
+        anillo2 = anillo.clone() if k > 1 else None
+        pos = torch.tensor([11], dtype=torch.int64, device=DEV)
+        espacio = ops.espacio_bloque(B, d, ff, DEV)
+        assert ops.norma_pendiente_ok(ln, d, DEV)
+        out = ops.paso_bloque(blq, h, anillo, pos, espacio)
+        y_ref = ln(out)
+        pend = ops.paso_bloque(blq, h, anillo2, pos, espacio, terminar=False)
+        y = ops.norma_pendiente(ln, pend)
+        torch.cuda.synchronize()
+    assert torch.equal(out, pend.out)
+    assert k == 1 or torch.equal(anillo, anillo2)
+    err = ((y - y_ref).abs() / (1 + y_ref.abs())).max().item()
+    print('max rel |finish_norm - layer_norm|', err, flush=True)
+    assert err < 2e-6
+
+
 @pytest.mark.parametrize('mezcla', ['conv', 'memoria'])
 def test_escribir_equals_whole_text(mezcla):
     """tests/test_nucleo.py:105-115: the logits of every step equal the model on the whole written text."""
