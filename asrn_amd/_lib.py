@@ -65,12 +65,12 @@ SIGNATURES = {
                       + [_I64, _P]),
     'asrn_ring_build': (ctypes.c_int, [_P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P]),
     'asrn_decode_attend': (ctypes.c_int, [_P] * 11 + [_I64, _I64, _I64, _P] + [_I32] * 7 + [_F32, _F32, _I32]
-                           + [_P] * 5),
+                           + [_P] * 6),
     'asrn_hawkes_table_load': (ctypes.c_int, [_P] * 6 + [_I64, _I64, _I32, _I64] + [_P] * 4),
     'asrn_hawkes_table_grow': (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _P, _P, _I64, _P]),
     'asrn_repetition_step': (ctypes.c_int, [_P] * 7 + [_I64, _I64, _I64, _P, _I32, _I64] + [_P] * 6 + [_I32, _P]),
     'asrn_decode_attend_repeat': (ctypes.c_int, [_P] * 11 + [_I64, _I64, _I64, _P] + [_I32] * 7 + [_F32, _F32, _I32]
-                                  + [_P] * 8 + [_I32, _I64] + [_P] * 6 + [_I32, _P]),
+                                  + [_P] * 8 + [_I32, _I64] + [_P] * 6 + [_I32, _P, _P]),
     'asrn_sample_bits': (_I32, [_I64]),
     'asrn_ngram_set_successors': (_I32, []),
     'asrn_ngram_set_build': (ctypes.c_int, [_P, _I64, _I64, _I64, _I32, _I32, _P, _P, _P, _P, _I64, _P]),

@@ -62,6 +62,8 @@ struct Cand {
   // its bucket ids (B, T) out, and whether tq then enters the rings
   int32_t* rings; int32_t* counts; int32_t* ids_out; int nb; int64_t tq; int insert;
   const int64_t* tq_dev;   // generation, optional: the query position read from device memory instead of tq
+  int32_t* done;           // generation, optional: per batch row, the column workgroups past their ring reads (0
+                           // between launches): the launch then splits each row's columns over several workgroups
   // the unprotected core layer (v89 numerics): clock32 forms each score's clock term as (log_alfa_k + rate B_k) -
   // rate B_q in fp32 from the fp32 clock (held in Bt as fp64 values that fp32 represents exactly); leak, when given,
   // counts the (query, table) pairs whose best valid score is within the -1e9 fill's reach, where the reference's
@@ -1144,7 +1146,7 @@ __device__ __forceinline__ void unique_terms(const Cand& a, int64_t b, int64_t t
 
 template <int DCH, bool VALUES, bool B16 = false>
 __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, int NU, Scratch& S, float* salida_row,
-                                              float* signals_row, float* ent_rows);
+                                              float* signals_row, float* ent_rows, bool count_leak = true);
 
 // One query token's candidate attention: salida row (d), the 4 gate signals and, when `ent_rows` is given, every
 // entry's weight at ent_rows[2 (tau * C + distance - 1)]. RING: candidates from the generation rings instead of the
@@ -1165,7 +1167,7 @@ __device__ __forceinline__ void forward_token(const Cand& a, int64_t b, int64_t 
 // it, S.uc holds each unique's summed weight for the caller).
 template <int DCH, bool VALUES, bool B16>
 __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, int NU, Scratch& S, float* salida_row,
-                                              float* signals_row, float* ent_rows) {
+                                              float* signals_row, float* ent_rows, bool count_leak) {
   const int lane = lane_id();
 
   // Exact masked softmax of every table at once: the per-table max through an LDS atomic max on order-preserving
@@ -1202,7 +1204,7 @@ __device__ __forceinline__ void token_weights(const Cand& a, int64_t b, int M, i
       inv = 1.f / den;
       // the reference's -1e9 fill (without the exact mask) gives its invalid keys weight exp(-1e9 - mx), which is
       // nonzero in fp32 once mx is within ~104 of -1e9 (the fp32 spacing there is 64)
-      if (a.leak && mx <= kFill + kLeakReach) atomicAdd(a.leak, 1);
+      if (count_leak && a.leak && mx <= kFill + kLeakReach) atomicAdd(a.leak, 1);
     }
     S.tinv[tg] = inv;
   }
@@ -1275,6 +1277,11 @@ void k_cand_fwd(Cand a) {   // 6-7 waves per SIMD when narrow
 // writes Bt[tq], the Hawkes tables, the streak and its own outputs, none of which the attention reads (the candidates'
 // positions are below tq, and the query's clock is formed as the step forms it), and reads nothing the attention
 // writes.
+// Column split (gridDim.y > 1, with a.done): workgroup y of a row gathers the value columns [256 DCH y, 256 DCH (y +
+// 1)) after forming the list, scores and weights as every workgroup of the row does (the same bits; only y = 0 counts
+// the leak): the value rows one CU pulls are what bound the gather. The rings change only once every workgroup of the
+// row has read them: each adds 1 to a.done[b] once its ring reads are consumed (after the workgroup's first barrier),
+// and the one that reads gridDim.y - 1 inserts tq and sets the count back to 0. Nothing waits on the count.
 constexpr int kDecodeWaves = 8;
 
 template <int F4, int DCH, bool REP>
@@ -1283,6 +1290,7 @@ __global__ __launch_bounds__(kWave * kDecodeWaves) void k_decode_attend(Cand a) 
   __shared__ float4 part[kDecodeWaves][DCH][kWave];
   __shared__ int nu_shared;
   if (REP && blockIdx.x >= a.B) {
+    if (blockIdx.y != 0) return;
     const int64_t e = (int64_t)(blockIdx.x - a.B) * blockDim.x + threadIdx.x;
     const int64_t t = step_pos(a.rep);
     if (e < a.rep.B * a.rep.n && t >= 0 && t < a.rep.stride) repetition_row(a.rep, a.rep_tab, e, t);
@@ -1302,13 +1310,16 @@ __global__ __launch_bounds__(kWave * kDecodeWaves) void k_decode_attend(Cand a) 
     }
   }
   __syncthreads();
+  const int ny = gridDim.y;
+  __shared__ int last_shared;
+  if (ny > 1 && threadIdx.x == 0) last_shared = atomicAdd(&a.done[b], 1) == ny - 1;
   const int NU = nu_shared;
   unique_terms<F4, kDecodeWaves, false, REP>(a, b, tq, NU, S, nullptr, wave);
   __syncthreads();
-  if (wave == 0) token_weights<DCH, false>(a, b, m_shared, NU, S, nullptr, a.signals + b * 4, nullptr);
+  if (wave == 0) token_weights<DCH, false>(a, b, m_shared, NU, S, nullptr, a.signals + b * 4, nullptr, blockIdx.y == 0);
   __syncthreads();
   constexpr int UNR = gather_rows_in_flight<DCH>();
-  for (int c0 = 0; c0 < a.d; c0 += 256 * DCH) {          // one slab of 256 DCH columns at a time
+  for (int c0 = 256 * DCH * blockIdx.y; c0 < a.d; c0 += 256 * DCH * ny) {   // one slab of 256 DCH columns at a time
     float4 acc[DCH];
 #pragma unroll
     for (int ch = 0; ch < DCH; ++ch) acc[ch] = zero4();
@@ -1331,7 +1342,9 @@ __global__ __launch_bounds__(kWave * kDecodeWaves) void k_decode_attend(Cand a) 
     __syncthreads();                                       // part is rewritten by the next slab
   }
   if (wave != 0) return;
-  if (a.insert && lane < a.T) {
+  const bool last = ny == 1 || last_shared;
+  if (ny > 1 && last && lane == 0) atomicExch(&a.done[b], 0);   // at the adds' coherence point
+  if (a.insert && last && lane < a.T) {
     const int id = a.ids_out[b * a.T + lane];
     const int64_t bucket = (b * a.T + lane) * ((int64_t)1 << a.nb) + id;
     const int c = a.counts[bucket];
@@ -1744,13 +1757,21 @@ struct LaunchDecode {                              // the generation caches are 
   static int run(const Cand& a, hipStream_t st) {
     if constexpr (RB != 0) {
       return fail("asrn_decode_attend: fp32 caches only");
-    } else if (a.rep.beta_t) {                     // with the repetition step's workgroups after the B rows
-      const int64_t threads = kWave * kDecodeWaves, extra = (a.rep.B * a.rep.n + threads - 1) / threads;
-      hipLaunchKernelGGL((k_decode_attend<F4, DCH, true>), dim3((unsigned)(a.B + extra)), dim3(threads), 0, st, a);
-      return check_launch("asrn_decode_attend_repeat");
     } else {
-      hipLaunchKernelGGL((k_decode_attend<F4, DCH, false>), dim3((unsigned)a.B), dim3(kWave * kDecodeWaves), 0, st,
-                         a);
+      // the columns split over DCH workgroups of 256 when a count buffer is given and the rows leave CUs idle
+      const bool split = DCH > 1 && a.done && a.B * DCH <= 256;
+      const unsigned ny = split ? DCH : 1;
+      const int64_t threads = kWave * kDecodeWaves;
+      if (a.rep.beta_t) {                          // with the repetition step's workgroups after the B rows
+        const int64_t extra = (a.rep.B * a.rep.n + threads - 1) / threads;
+        const dim3 grid((unsigned)(a.B + extra), ny);
+        if (split) hipLaunchKernelGGL((k_decode_attend<F4, 1, true>), grid, dim3(threads), 0, st, a);
+        else hipLaunchKernelGGL((k_decode_attend<F4, DCH, true>), grid, dim3(threads), 0, st, a);
+        return check_launch("asrn_decode_attend_repeat");
+      }
+      const dim3 grid((unsigned)a.B, ny);
+      if (split) hipLaunchKernelGGL((k_decode_attend<F4, 1, false>), grid, dim3(threads), 0, st, a);
+      else hipLaunchKernelGGL((k_decode_attend<F4, DCH, false>), grid, dim3(threads), 0, st, a);
       return check_launch("asrn_decode_attend");
     }
   }
@@ -1849,7 +1870,7 @@ static int decode_setup(Cand& a, const float* phi, const float* V, const float* 
                         int32_t* rings, int32_t* counts, int64_t B, int64_t cap, int64_t t, const int64_t* t_dev,
                         int32_t d, int32_t nb, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
                         float scale_phi, float scale_c, int32_t insert, float* salida, float* signals, int32_t* ids,
-                        int32_t* leak, const char* what) {
+                        int32_t* leak, int32_t* done, const char* what) {
   a = make(phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, nullptr, nullptr, nullptr, B, cap, d, T * nb, cf, K, T,
            Tc, C, scale_phi, scale_c);
   if (check_args(a, what)) return 1;
@@ -1860,6 +1881,7 @@ static int decode_setup(Cand& a, const float* phi, const float* V, const float* 
   a.insert = insert ? 1 : 0;
   a.salida = salida; a.signals = signals;
   a.leak = leak;
+  a.done = done;
   return 0;
 }
 
@@ -1869,10 +1891,10 @@ extern "C" int asrn_decode_attend(const float* phi, const float* V, const float*
                                   int64_t t, const int64_t* t_dev, int32_t d, int32_t nb, int32_t cf, int32_t K,
                                   int32_t T, int32_t Tc,
                                   int32_t C, float scale_phi, float scale_c, int32_t insert, float* salida,
-                                  float* signals, int32_t* ids, int32_t* leak, void* stream) {
+                                  float* signals, int32_t* ids, int32_t* leak, int32_t* done, void* stream) {
   Cand a;
   if (decode_setup(a, phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, rings, counts, B, cap, t, t_dev, d, nb, cf, K,
-                   T, Tc, C, scale_phi, scale_c, insert, salida, signals, ids, leak, "asrn_decode_attend"))
+                   T, Tc, C, scale_phi, scale_c, insert, salida, signals, ids, leak, done, "asrn_decode_attend"))
     return 1;
   if (B == 0) return 0;
   return dispatch<LaunchDecode>(a, (hipStream_t)stream);
@@ -1887,10 +1909,10 @@ extern "C" int asrn_decode_attend_repeat(const float* phi, const float* V, const
                                          const double* beta_t, const double* coef, const float* kappa,
                                          const float* kappa_r, int32_t n, int64_t tab_cap, uint64_t* tab_keys,
                                          double* tab_Bu, float* tab_A, float* racha, float* vistos, float* hawkes,
-                                         int32_t reloj32, void* stream) {
+                                         int32_t reloj32, int32_t* done, void* stream) {
   Cand a;
   if (decode_setup(a, phi, V, Qc, Kc, sig, Bt, log_alfa, w_suf, gamma, rings, counts, B, cap, t, t_dev, d, nb, cf, K,
-                   T, Tc, C, scale_phi, scale_c, insert, salida, signals, ids, leak, "asrn_decode_attend_repeat"))
+                   T, Tc, C, scale_phi, scale_c, insert, salida, signals, ids, leak, done, "asrn_decode_attend_repeat"))
     return 1;
   ASRN_REQUIRE(n >= 1 && n <= 16, "asrn_decode_attend_repeat: n=%d must be in [1, 16]", n);
   ASRN_REQUIRE(tab_cap > 0 && (tab_cap & (tab_cap - 1)) == 0 && tab_cap >= 2 * (t + 1),

@@ -79,6 +79,8 @@ class EscritorCapa:
         n = L0 - 1 if self.ajeno else L0
         self.anillos, self.cuentas = ops.ring_build(partes['phi'][:, :n].to(f32).contiguous(), capa.n_tablas,
                                                     capa.n_bits, capa.chunk)
+        # the attention's per-row count of column workgroups past their ring reads (zero between launches)
+        self.hechos = torch.zeros(self.cuentas.shape[0] // capa.n_tablas, dtype=torch.int32, device=self.cuentas.device)
         self.hawkes = ops.HawkesTable.load(partes['claves'], partes['orden_k'], partes['repetido'], partes['hawkes'],
                                            partes['Bt'], partes['log_alfa'], cap=2 * self.cap)
         self.racha = partes['racha'][:, -1].to(f32).contiguous().clone()
@@ -143,7 +145,8 @@ class EscritorCapa:
         # the repetition step (clock, Hawkes, streak) and the attention in one launch
         salida, sen, _, vistos, hawkes = ops.decode_attend_repeat(
             c, pos, self.anillos, self.cuentas, capa.w_sufijo, capa.gamma, forma, not self.ajeno, self.hawkes, beta_t,
-            capa.c_vistos, kappa, kappa_r, self.racha, t_max=t_max, reloj32=not capa.protecciones.reloj_64)
+            capa.c_vistos, kappa, kappa_r, self.racha, t_max=t_max, reloj32=not capa.protecciones.reloj_64,
+            hechos=self.hechos)
         if e_t.dtype == torch.float32:
             y = capa._combinar_paso(salida, h_t, sen, vistos, hawkes, self.racha)   # W_o and the gate, one kernel
             if y is not None:

@@ -814,11 +814,12 @@ def _posicion(t, t_max):
     return int(t), None
 
 
-def decode_attend(cache, t, rings, counts, w_suf, gamma, shape, insert, t_max=None):
+def decode_attend(cache, t, rings, counts, w_suf, gamma, shape, insert, t_max=None, hechos=None):
     """The step's candidate attention for position t of the caches (dict of (B, cap, .) tensors phi, V, Qc, Kc, sig,
     Bt, log_alfa) over the rings; with insert, t then enters the rings. Returns salida (B, d), signals (B, 4) and
     the bucket ids (B, T). t: an int, or a one-element int64 device tensor holding it (then t_max: the largest
-    position it will hold)."""
+    position it will hold). hechos: a (B,) int32 device tensor of zeros kept by the caller across calls (the launch
+    leaves it zero); with it, a row's value columns are gathered by several workgroups when B leaves CUs idle."""
     T, Tc, C, K, nb = shape['T'], shape['Tc'], shape['C'], shape['K'], shape['nb']
     phi, V = cache['phi'], cache['V']
     dev = _dev(phi)
@@ -835,16 +836,16 @@ def decode_attend(cache, t, rings, counts, w_suf, gamma, shape, insert, t_max=No
     call('asrn_decode_attend', ptr(phi), ptr(V), ptr(cache['Qc']), ptr(cache['Kc']), ptr(cache['sig']),
          ptr(cache['Bt']), ptr(cache['log_alfa']), ptr(w), ptr(g), ptr(rings), ptr(counts), B, cap, th, tdev, d, nb,
          cf, K, T, Tc, C, float(P) ** -0.5, float(cf) ** -0.5, 1 if insert else 0, ptr(salida), ptr(signals),
-         ptr(ids), ptr(shape.get('fuga')), stream_of(dev))
+         ptr(ids), ptr(shape.get('fuga')), ptr(hechos), stream_of(dev))
     return salida, signals, ids
 
 
 def decode_attend_repeat(cache, t, rings, counts, w_suf, gamma, shape, insert, tabla, beta_t, coef, kappa, kappa_r,
-                         racha, t_max=None, reloj32=False):
+                         racha, t_max=None, reloj32=False, hechos=None):
     """decode_attend and tabla.step (the repetition step: clock, Hawkes, streak) for position t in one launch
-    (asrn_decode_attend_repeat), with the same outputs, bit for bit, as the two calls in the order step, attend:
-    returns salida (B, d), signals (B, 4), the bucket ids (B, T), vistos and hawkes (B, n); Bt[:, t], the Hawkes tables
-    and racha are updated in place as tabla.step does."""
+    (asrn_decode_attend_repeat), with the same outputs, bit for bit, as the two calls in the order step, attend (with
+    the same hechos, as decode_attend takes it): returns salida (B, d), signals (B, 4), the bucket ids (B, T), vistos
+    and hawkes (B, n); Bt[:, t], the Hawkes tables and racha are updated in place as tabla.step does."""
     T, Tc, C, K, nb = shape['T'], shape['Tc'], shape['C'], shape['K'], shape['nb']
     phi, V = cache['phi'], cache['V']
     dev = _dev(phi)
@@ -867,7 +868,7 @@ def decode_attend_repeat(cache, t, rings, counts, w_suf, gamma, shape, insert, t
          d, nb, cf, K, T, Tc, C, float(P) ** -0.5, float(cf) ** -0.5, 1 if insert else 0, ptr(salida), ptr(signals),
          ptr(ids), ptr(shape.get('fuga')), ptr(ins[2]), ptr(ins[3]), ptr(ins[4]), ptr(ins[5]), tabla.n, tabla.cap,
          ptr(tabla.keys), ptr(tabla.Bu), ptr(tabla.A), ptr(racha), ptr(vistos), ptr(hawkes), 1 if reloj32 else 0,
-         stream_of(dev))
+         ptr(hechos), stream_of(dev))
     return salida, signals, ids, vistos, hawkes
 
 

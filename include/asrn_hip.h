@@ -355,13 +355,17 @@ int asrn_ring_build(const int32_t* order, const int32_t* ids_sorted, int64_t B, 
  * graph and replayed as the position advances); t is then checked as the largest position it will hold, and a
  * position outside [0, cap) writes nothing.
  * The clock term is la_k + rate * fp32(B_k - B_q) for both layers: the core layer's writer takes the difference of
- * its fp32 clock too (asrn/nucleo.py:937). leak: as in asrn_candidates_fwd (null, or a device int32 counter). */
+ * its fp32 clock too (asrn/nucleo.py:937). leak: as in asrn_candidates_fwd (null, or a device int32 counter).
+ * done: null, or a device int32 (B) holding zeros, kept by the caller across calls (each launch leaves it zero): with
+ * it, when B ceil(d / 256) <= 256, each row's value columns are gathered by ceil(d / 256) workgroups (a row's value
+ * rows are what one CU's share of bandwidth bounds), the last of them to finish reading the rings inserting t. The
+ * outputs are the same but for the order of the value sums. Calls sharing one done buffer must not overlap. */
 int asrn_decode_attend(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                        const double* Bt, const float* log_alfa, const float* w_suf, const float* gamma,
                        int32_t* rings, int32_t* counts, int64_t B, int64_t cap, int64_t t, const int64_t* t_dev,
                        int32_t d, int32_t nb, int32_t cf, int32_t K, int32_t T, int32_t Tc, int32_t C,
                        float scale_phi, float scale_c, int32_t insert, float* salida, float* signals, int32_t* ids,
-                       int32_t* leak, void* stream);
+                       int32_t* leak, int32_t* done, void* stream);
 
 /* Hawkes memory: per (b, j) group an open-addressing table of cap slots (a power of two, >= 2x the keys it can
  * hold): tab_keys (B*n, cap) uint64 key codes, tab_Bu (B*n, cap) fp64 clock of the last occurrence, tab_A (B*n, cap)
@@ -392,7 +396,8 @@ int asrn_repetition_step(const float* sig, double* Bt, const float* log_alfa, co
  * asrn/nucleo.py:1826-1850). The first arguments are asrn_decode_attend's, the rest asrn_repetition_step's (sig, Bt,
  * log_alfa, B, t and t_dev shared; the caches' capacity cap is the step's stride; the Hawkes tables' capacity is
  * tab_cap). The outputs are those of the two calls made in that order, bit for bit: the attention forms the query's
- * clock Bt[t] = Bt[t-1] + beta_t as the step does instead of reading what the step writes. */
+ * clock Bt[t] = Bt[t-1] + beta_t as the step does instead of reading what the step writes. done: as for
+ * asrn_decode_attend (the same bits as that call with the same done). */
 int asrn_decode_attend_repeat(const float* phi, const float* V, const float* Qc, const float* Kc, const float* sig,
                               double* Bt, const float* log_alfa, const float* w_suf, const float* gamma, int32_t* rings,
                               int32_t* counts, int64_t B, int64_t cap, int64_t t, const int64_t* t_dev, int32_t d,
@@ -400,7 +405,8 @@ int asrn_decode_attend_repeat(const float* phi, const float* V, const float* Qc,
                               float scale_c, int32_t insert, float* salida, float* signals, int32_t* ids,
                               int32_t* leak, const double* beta_t, const double* coef, const float* kappa,
                               const float* kappa_r, int32_t n, int64_t tab_cap, uint64_t* tab_keys, double* tab_Bu,
-                              float* tab_A, float* racha, float* vistos, float* hawkes, int32_t reloj32, void* stream);
+                              float* tab_A, float* racha, float* vistos, float* hawkes, int32_t reloj32, int32_t* done,
+                              void* stream);
 
 /* embed_step: the generation loop step's embedding rows, no counterpart in the reference's FFI (its loop looks the
  * rows up with nn.Embedding, asrn/nucleo.py:1805, and keeps the previous one): e_t = emb[ids] and e_prev =

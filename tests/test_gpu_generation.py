@@ -81,11 +81,15 @@ def test_ring_build_vs_oracle(B, n, T, nb, C, V):
 # the step's candidate attention, with inserts
 # ---------------------------------------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize('B,t0,steps,d,C,nb,T,V', [(2, 300, 24, 64, 32, 14, 8, 6), (3, 100, 40, 96, 4, 2, 4, 5),
-                                                   (2, 1, 30, 256, 16, 4, 8, 4), (1, 500, 8, 1024, 8, 3, 8, 7),
-                                                   (16, 2000, 4, 768, 32, 14, 8, 50), (2, 200, 6, 64, 8, 14, 16, 6)])
-def test_decode_attend_vs_oracle(B, t0, steps, d, C, nb, T, V):
-    say('decode attend', B, t0, steps, d, C, nb, T)
+@pytest.mark.parametrize('B,t0,steps,d,C,nb,T,V,split', [
+    (2, 300, 24, 64, 32, 14, 8, 6, True), (3, 100, 40, 96, 4, 2, 4, 5, True), (2, 1, 30, 256, 16, 4, 8, 4, True),
+    (1, 500, 8, 1024, 8, 3, 8, 7, True), (16, 2000, 4, 768, 32, 14, 8, 50, True), (2, 200, 6, 64, 8, 14, 16, 6, True),
+    (16, 2000, 4, 768, 32, 14, 8, 50, False), (3, 60, 30, 520, 4, 2, 4, 5, True)])
+def test_decode_attend_vs_oracle(B, t0, steps, d, C, nb, T, V, split):
+    """The step's attention against the oracle, step after step, and the rings after each insert. split: with the
+    per-row count buffer, so that d > 256 runs each row's value columns on several workgroups (the last of a row to
+    finish its ring reads inserting); the buffer is back to zero after every launch."""
+    say('decode attend', B, t0, steps, d, C, nb, T, split)
     L = t0 + steps
     cf, K, Tc = 16, 4, T // 2
     x, phi, g = token_phi(B, L, V, T, nb, seed=t0 + d)
@@ -102,9 +106,11 @@ def test_decode_attend_vs_oracle(B, t0, steps, d, C, nb, T, V):
     rings = torch.from_numpy(ring.reshape(B * T, 2 ** nb, C)).to(DEV)
     counts = torch.from_numpy(count.reshape(B * T, 2 ** nb).astype(np.int32)).to(DEV)
     shape = dict(T=T, Tc=Tc, C=C, K=K, nb=nb)
+    hechos = torch.zeros(B, dtype=torch.int32, device=DEV) if split else None
     for t in range(t0, L):
         sal, sen, got_ids = ops.decode_attend(dcache, t, rings, counts, w_suf.to(DEV), gamma.to(DEV), shape,
-                                              insert=True)
+                                              insert=True, hechos=hechos)
+        assert hechos is None or not hechos.any(), t
         ref_sal, ref_sen = G.attend(G.ring_positions(ring, ids[:, t]), t, cache['phi'], cache['V'], cache['Qc'],
                                     cache['Kc'], cache['sig'], cache['Bt'], cache['log_alfa'], w_suf, gamma, sh)
         assert np.array_equal(got_ids.cpu().numpy(), ids[:, t]), t
@@ -221,6 +227,7 @@ def test_decode_attend_repeat_equals_two_calls(B, t0, steps, d, C, nb, T, V, n, 
                            counts=counts, racha=torch.rand(B, generator=torch.Generator().manual_seed(3)).to(DEV)))
     sep, fus = states
     shape = dict(T=T, Tc=Tc, C=C, K=K, nb=nb)
+    hechos = [torch.zeros(B, dtype=torch.int32, device=DEV) for _ in range(2)]   # d > 256: the column split
     for t in range(t0, L):
         pos = torch.full((1,), t, dtype=torch.int64, device=DEV) if dev_pos else t
         t_max = L - 1 if dev_pos else None
@@ -228,10 +235,10 @@ def test_decode_attend_repeat_equals_two_calls(B, t0, steps, d, C, nb, T, V, n, 
         v1, h1 = sep['tab'].step(sep['cache'], pos, bt, coef.to(DEV), kappa, kappa_r, sep['racha'], t_max=t_max,
                                  reloj32=reloj32)
         s1, g1, i1 = ops.decode_attend(sep['cache'], pos, sep['rings'], sep['counts'], w_suf, gamma, shape,
-                                       insert=True, t_max=t_max)
+                                       insert=True, t_max=t_max, hechos=hechos[0])
         s2, g2, i2, v2, h2 = ops.decode_attend_repeat(fus['cache'], pos, fus['rings'], fus['counts'], w_suf, gamma,
                                                       shape, True, fus['tab'], bt, coef.to(DEV), kappa, kappa_r,
-                                                      fus['racha'], t_max=t_max, reloj32=reloj32)
+                                                      fus['racha'], t_max=t_max, reloj32=reloj32, hechos=hechos[1])
         for a_, b_, what in ((s1, s2, 'salida'), (g1, g2, 'signals'), (i1, i2, 'ids'), (v1, v2, 'vistos'),
                              (h1, h2, 'hawkes'), (sep['racha'], fus['racha'], 'racha'),
                              (sep['cache']['Bt'], fus['cache']['Bt'], 'Bt'), (sep['rings'], fus['rings'], 'rings'),

@@ -144,11 +144,11 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert lib.asrn_ring_build(N, N, 2, 10, 8, 15, 32, N, N, N) != 0
     assert 'asrn_ring_build' in _err(lib)
     assert lib.asrn_decode_attend(*([N] * 11), 2, 100, 100, N, 64, 14, 16, 4, 8, 4, 32, 0.1, 0.25, 1, N, N, N,
-                                  N, N) != 0
+                                  N, N, N) != 0
     assert 'outside the caches' in _err(lib)
     assert lib.asrn_hawkes_table_load(*([N] * 6), 2, 100, 4, 96, N, N, N, N) != 0
     assert 'power of two' in _err(lib)
-    assert lib.asrn_repetition_step(*([N] * 7), 2, 1000, 100, N, 4, 128, *([N] * 6), 0, N) != 0
+    assert lib.asrn_repetition_step(*([N] * 7), 2, 1000, 100, N, 4, 128, *([N] * 6), 0, N, N) != 0
     assert 'grow it first' in _err(lib)
     assert lib.asrn_hawkes_table_grow(N, N, N, 8, 256, N, N, N, 128, N) != 0
     assert 'growing' in _err(lib)
@@ -164,14 +164,14 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert 'workspace' in _err(lib)
     # the fused attention + repetition step: the attention's checks, then the step's n and table capacity
     att = [2, 100, 50, N, 64, 14, 16, 4, 8, 4, 32, 0.1, 0.25, 1, N, N, N, N]
-    assert lib.asrn_decode_attend_repeat(*([N] * 11), 2, 100, 100, *att[3:], *([N] * 4), 4, 128, *([N] * 6), 0,
+    assert lib.asrn_decode_attend_repeat(*([N] * 11), 2, 100, 100, *att[3:], *([N] * 4), 4, 128, *([N] * 6), 0, N,
                                          N) != 0
     assert 'outside the caches' in _err(lib)
-    assert lib.asrn_decode_attend_repeat(*([N] * 11), *att, *([N] * 4), 0, 128, *([N] * 6), 0, N) != 0
+    assert lib.asrn_decode_attend_repeat(*([N] * 11), *att, *([N] * 4), 0, 128, *([N] * 6), 0, N, N) != 0
     assert 'n=0' in _err(lib)
-    assert lib.asrn_decode_attend_repeat(*([N] * 11), *att, *([N] * 4), 4, 64, *([N] * 6), 0, N) != 0
+    assert lib.asrn_decode_attend_repeat(*([N] * 11), *att, *([N] * 4), 4, 64, *([N] * 6), 0, N, N) != 0
     assert 'grow it first' in _err(lib)
-    assert lib.asrn_decode_attend_repeat(*([N] * 11), *att, *([N] * 4), 4, 128, *([N] * 6), 0, N) != 0
+    assert lib.asrn_decode_attend_repeat(*([N] * 11), *att, *([N] * 4), 4, 128, *([N] * 6), 0, N, N) != 0
     assert 'null pointer' in _err(lib)
     # the step's producers: width, position, workspace
     prod = [N] * 4
