@@ -90,7 +90,7 @@ SIGNATURES = {
     'asrn_block_step_ex': (ctypes.c_int, [_P, _I64] + [_P] * 4 + [_I32, _I32] + [_P] * 3 + [_I64, _I32, _I32, _I32]
                            + [_P] * 10 + [_F32] + [_P] * 5 + [_I32, _P, _I64, _P]),
     'asrn_block_finish_norm': (ctypes.c_int, [_P] * 4 + [_I32, _I32, _P, _P, _I64, _I32, _P, _P, _F32, _P, _P, _I64,
-                                                     _P]),
+                                                     _P, _P, _P]),
     'asrn_embed_step': (ctypes.c_int, [_P, _I64, _I32, _P, _P, _I64, _P, _I64, _P, _P, _P]),
     'asrn_decode_produce_workspace': (ctypes.c_int64, [_I64, _I32, _I32]),
     'asrn_decode_produce_e_workspace': (_I64, [_I32, _I64, _I32, _I32]),

@@ -77,10 +77,14 @@ constexpr int kMaxTaps = 8;                  // ring taps a thread loads ahead o
 
 // With PEND: the row is the pending block's output h1 + (sum of the splits + bias), formed as k_finish_res forms it,
 // written to pv.out, and the pending block's z enters its ring (k_finish_res's work, one row per workgroup).
+// pos_next (with the count `done`, 0 between launches): the position advanced to *pos_p + 1 once every workgroup has
+// used it: each workgroup, past a barrier after its last use, adds 1 to the count, and the one that reads gridDim.x
+// - 1 stores the new position and sets the count back to 0 (nothing waits on the count).
 template <int R, int S, bool PEND>
 __global__ __launch_bounds__(kPrepThreads) void k_prep_mix(const float* h, int64_t ldh, Pending pv, const float* ring,
                                                            const int64_t* pos_p, const float* w, const float* bia,
-                                                           float eps, int d, int k, float* z, float* x1) {
+                                                           float eps, int d, int k, float* z, float* x1,
+                                                           int64_t* pos_next, int32_t* done) {
   __shared__ float red[kPrepWaves];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
@@ -140,6 +144,13 @@ __global__ __launch_bounds__(kPrepThreads) void k_prep_mix(const float* h, int64
       if (i < km1) xr[i] = tap[j][i];
     for (int i = kMaxTaps; i < km1; ++i) xr[i] = ring[(b * d + c) * km1 + slot(i)];
     xr[km1] = zc;
+  }
+  if (pos_next) {
+    __syncthreads();
+    if (tid == 0 && atomicAdd(done, 1) == (int)gridDim.x - 1) {
+      *pos_next = pos + 1;
+      atomicExch(done, 0);
+    }
   }
 }
 
@@ -278,7 +289,7 @@ __global__ __launch_bounds__(NW * kWave) void k_part(Part g) {
 
 // the row kernels' instances: R columns a thread (ceil(d / kPrepThreads)) and S loads for at most S splits
 using PrepFn = void (*)(const float*, int64_t, Pending, const float*, const int64_t*, const float*, const float*, float,
-                        int, int, float*, float*);
+                        int, int, float*, float*, int64_t*, int32_t*);
 using MixFn = void (*)(const float*, int, int64_t, const float*, const float*, int64_t, const float*, const float*,
                        float, int, float*, float*);
 using ResFn = void (*)(const float*, int, int64_t, const float*, const float*, const float*, const int64_t*, int, int,
@@ -371,7 +382,8 @@ int block_step(const float* h, int64_t ldh, const float* prev_h1, const float* p
                  prev_ring, prev_k - 1, prev_out};
   const int R = (d + kPrepThreads - 1) / kPrepThreads;
   hipLaunchKernelGGL(prep_fn(R, prev_h1 != nullptr, pv.splits), dim3((unsigned)B), dim3(kPrepThreads), 0, st,
-                     prev_h1 ? prev_out : h, prev_h1 ? (int64_t)d : ldh, pv, ring, pos, ln1_w, ln1_b, eps, d, k, z, x1);
+                     prev_h1 ? prev_out : h, prev_h1 ? (int64_t)d : ldh, pv, ring, pos, ln1_w, ln1_b, eps, d, k, z, x1,
+                     nullptr, nullptr);
   if (int rc = check_launch(what)) return rc;
   if (int rc = launch_part(Part{x1, conv_w, p1, nullptr, (int)B, d * k, d, s1}, st, what)) return rc;
   // the residual input h: the pending block's output, which k_prep_mix wrote, or h itself
@@ -417,7 +429,8 @@ extern "C" int asrn_block_step_ex(const float* h, int64_t ldh, const float* prev
 extern "C" int asrn_block_finish_norm(const float* prev_h1, const float* prev_b2, const float* prev_z,
                                       float* prev_ring, int32_t prev_k, int32_t prev_ff, float* prev_out,
                                       const int64_t* pos, int64_t B, int32_t d, const float* ln_w, const float* ln_b,
-                                      float eps, float* y, void* workspace, int64_t workspace_bytes, void* stream) {
+                                      float eps, float* y, void* workspace, int64_t workspace_bytes, int64_t* pos_next,
+                                      int32_t* done, void* stream) {
   ASRN_REQUIRE(B >= 1 && B <= (int64_t(1) << 20) && d >= 1 && d <= kRowVals * kPrepThreads,
                "asrn_block_finish_norm: bad sizes B=%lld d=%d (d <= %d)", (long long)B, d, kRowVals * kPrepThreads);
   ASRN_REQUIRE(prev_h1 && prev_b2 && prev_z && prev_out && pos && ln_w && ln_b && y && prev_k >= 1 && prev_ff >= 1 &&
@@ -428,12 +441,13 @@ extern "C" int asrn_block_finish_norm(const float* prev_h1, const float* prev_b2
   ASRN_REQUIRE(workspace != nullptr && workspace_bytes >= need,
                "asrn_block_finish_norm: the pending block's workspace of %lld bytes needed (asrn_block_step_workspace)",
                (long long)need);
+  ASRN_REQUIRE(!pos_next || done, "asrn_block_finish_norm: advancing the position needs its count (done)");
   const Pending pv{block_second_parts(workspace, B, d, prev_ff), splits_for(prev_ff), prev_b2, prev_h1, prev_z,
                    prev_ring, prev_k - 1, prev_out};
   // the row kernel of a block that follows a pending one, with one tap (k = 1): its LayerNorm row is the output, and
   // its conv operand [z] the same values at the same addresses
   const int R = (d + kPrepThreads - 1) / kPrepThreads;
   hipLaunchKernelGGL(prep_fn(R, true, pv.splits), dim3((unsigned)B), dim3(kPrepThreads), 0, (hipStream_t)stream,
-                     prev_out, (int64_t)d, pv, nullptr, pos, ln_w, ln_b, eps, d, 1, y, y);
+                     prev_out, (int64_t)d, pv, nullptr, pos, ln_w, ln_b, eps, d, 1, y, y, pos_next, done);
   return check_launch("asrn_block_finish_norm");
 }

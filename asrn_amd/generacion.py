@@ -79,6 +79,8 @@ class EscritorModelo:
         # the last block's end and the final norm in one launch (ops.norma_pendiente) when that block is fused
         self.norma_final = bool(self.fusion) and self.fusion[-1] and ops.norma_pendiente_ok(m.ln_f, h.shape[-1],
                                                                                               x0.device)
+        self.cuenta_pos = torch.zeros(1, dtype=torch.int32, device=x0.device)   # the final norm's advance count
+        self.avanzado = False
         self.t = L0
         self.pos = torch.full((1,), L0, dtype=torch.int64, device=x0.device)
         return m.head(m.ln_f(h[:, -1]))
@@ -110,11 +112,12 @@ class EscritorModelo:
         h = h + c
         return h + blq.ff(blq.ln2(h))
 
-    def _cuerpo(self, pieza, pos, t_max, texto=None, out=None):
+    def _cuerpo(self, pieza, pos, t_max, texto=None, out=None, avanzar=False):
         """The token ids pieza (B,) at position pos (a one-element device tensor, at most t_max) -> logits (B, V).
         texto: the loop's text (B, >= pos) holding the previous tokens: the previous row is looked up from it
         (asrn_embed_step, with this step's) instead of being copied from the last step, and e_ult is then not kept.
-        out: a (B, V) fp32 buffer the head's product writes into."""
+        out: a (B, V) fp32 buffer the head's product writes into. avanzar: advance pos by one in the final norm's
+        launch when it takes the last block (self.avanzado then says it did)."""
         m = self.m
         emb = m.emb.weight
         if (texto is not None and torch.is_tensor(pos) and emb.dtype == torch.float32 and emb.is_contiguous()
@@ -151,7 +154,9 @@ class EscritorModelo:
                 pendiente = None
         if e_prev is None:
             self.e_ult.copy_(e_t)
-        x = m.ln_f(h) if pendiente is None else ops.norma_pendiente(m.ln_f, pendiente)
+        self.avanzado = avanzar and pendiente is not None
+        x = m.ln_f(h) if pendiente is None else ops.norma_pendiente(
+            m.ln_f, pendiente, avance=(pos, self.cuenta_pos) if self.avanzado else None)
         if (out is not None and m.head.bias is None and x.dtype == out.dtype == m.head.weight.dtype
                 and not torch.is_autocast_enabled(x.device.type)):
             return torch.mm(x, m.head.weight.t(), out=out)
@@ -217,10 +222,12 @@ class _Bucle:
 
     def _paso_completo(self):
         self.elegir()
-        lg = self.esc._cuerpo(self.piezas, self.esc.pos, self.esc.cap - 1, texto=self.texto, out=self.lg)
+        lg = self.esc._cuerpo(self.piezas, self.esc.pos, self.esc.cap - 1, texto=self.texto, out=self.lg,
+                              avanzar=True)
         if lg.data_ptr() != self.lg.data_ptr():
             self.lg.copy_(lg)
-        self.esc.pos.add_(1)
+        if not self.esc.avanzado:                  # else the final norm's launch advanced it
+            self.esc.pos.add_(1)
 
     def paso(self, k):
         """Step k: choose token k, then (k < n - 1) run the model on it."""

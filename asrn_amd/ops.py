@@ -1208,17 +1208,19 @@ def norma_pendiente_ok(ln, d, dev):
             and tuple(ln.normalized_shape) == (d,) and d <= 4096 and not torch.is_autocast_enabled('cuda'))
 
 
-def norma_pendiente(ln, previo):
+def norma_pendiente(ln, previo, avance=None):
     """ln(previo's output) for a BloquePendiente, its output formed first (into previo.out, its ring row too) as the
     block step's last kernel forms it, in one launch (asrn_block_finish_norm): the last block's end and the final
     norm of the generation step (asrn/nucleo.py:1854). The norm is the row kernels' two-pass LayerNorm (biased
-    variance)."""
+    variance). avance: (pos, count), previo's position tensor and a one-element int32 device tensor of 0 kept across
+    calls: the same launch then advances pos by one once every workgroup has used it."""
     pv = previo
     B, d = pv.out.shape
     y = torch.empty((B, d), dtype=torch.float32, device=pv.out.device)
     call('asrn_block_finish_norm', ptr(pv.h1), ptr(pv.b2), ptr(pv.z), ptr(pv.anillo), pv.k, pv.ff, ptr(pv.out),
          ptr(pv.pos), B, d, ptr(_c(ln.weight.detach())), ptr(_c(ln.bias.detach())), float(ln.eps), ptr(y),
-         ptr(pv.espacio), pv.espacio.numel(), stream_of(pv.out.device))
+         ptr(pv.espacio), pv.espacio.numel(), ptr(avance[0]) if avance else None, ptr(avance[1]) if avance else None,
+         stream_of(pv.out.device))
     return y
 
 

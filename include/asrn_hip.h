@@ -530,12 +530,15 @@ int asrn_block_step_ex(const float* h, int64_t ldh, const float* prev_h1, const 
                        void* workspace, int64_t workspace_bytes, void* stream);
 /* A block step left pending (asrn_block_step_ex with finish = 0; prev_*, its arguments, pos its position, workspace the
  * one its call used) finished, then the model's final LayerNorm (ln_w, ln_b, eps; biased variance) of its output into
- * y (B, d): the block's output (written to prev_out) and ring row with the bits its last kernel gives. No counterpart
- * in the reference: one launch for the last block's end and the final norm (nucleo:1854). */
+ * y (B, d): the block's output (written to prev_out) and ring row with the bits its last kernel gives. pos_next: null,
+ * or where *pos + 1 is stored once every workgroup has used *pos (it may be pos itself; a generation loop step's
+ * advance), with done a device int32 holding 0, kept by the caller across calls (each launch leaves it 0); calls
+ * sharing one done must not overlap. No counterpart in the reference: one launch for the last block's end, the final
+ * norm and the position's advance (nucleo:1854). */
 int asrn_block_finish_norm(const float* prev_h1, const float* prev_b2, const float* prev_z, float* prev_ring,
                            int32_t prev_k, int32_t prev_ff, float* prev_out, const int64_t* pos, int64_t B, int32_t d,
                            const float* ln_w, const float* ln_b, float eps, float* y, void* workspace,
-                           int64_t workspace_bytes, void* stream);
+                           int64_t workspace_bytes, int64_t* pos_next, int32_t* done, void* stream);
 
 /* ---- the model's loss: cross-entropy ---------------------------------------------------------------------------
  * Replaces F.cross_entropy(logits.float().reshape(-1, V), y.reshape(-1), ignore_index) of ModeloASRN.perdida and the

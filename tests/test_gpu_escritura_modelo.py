@@ -463,13 +463,15 @@ def test_block_step_chained_equals_separate(B, d, ks, ffs):
             assert (anillos[i] is None) or torch.equal(anillos[i], anillos2[i]), i
 
 
-@pytest.mark.parametrize('B,d,k,ff', [(16, 768, 4, 1536), (3, 2080, 1, 300), (5, 96, 3, 4096)])
-def test_block_finish_norm_equals_block_then_layer_norm(B, d, k, ff):
+@pytest.mark.parametrize('B,d,k,ff,avanzar', [(16, 768, 4, 1536, True), (3, 2080, 1, 300, False),
+                                               (5, 96, 3, 4096, True)])
+def test_block_finish_norm_equals_block_then_layer_norm(B, d, k, ff, avanzar):
     """A block step left pending, then finished with the final LayerNorm in one launch (asrn_block_finish_norm), against
     the finished block step then torch's LayerNorm: the block's output and ring bit for bit, the norm within 2e-6 of
     torch's (a two-pass biased variance against torch's own reduction order). Widths past 1,024 hold several columns
-    a thread; the feed-forward widths give 6, 2 and 16 depth splits; k = 1 has no ring."""
-    say('block finish norm', B, d, k, ff)
+    a thread; the feed-forward widths give 6, 2 and 16 depth splits; k = 1 has no ring. avanzar: the same launch
+    advances the position by one (the last workgroup past its use of it), the ring row still at the old one's slot."""
+    say('block finish norm', B, d, k, ff, avanzar)
     torch.manual_seed(B + d + k)
     with torch.no_grad():
         blq = asrn_amd.BloqueLocal(d, k, ff).to(DEV)
@@ -487,8 +489,10 @@ def test_block_finish_norm_equals_block_then_layer_norm(B, d, k, ff):
         out = ops.paso_bloque(blq, h, anillo, pos, espacio)
         y_ref = ln(out)
         pend = ops.paso_bloque(blq, h, anillo2, pos, espacio, terminar=False)
-        y = ops.norma_pendiente(ln, pend)
+        cuenta = torch.zeros(1, dtype=torch.int32, device=DEV)
+        y = ops.norma_pendiente(ln, pend, avance=(pos, cuenta) if avanzar else None)
         torch.cuda.synchronize()
+    assert pos.item() == (12 if avanzar else 11) and cuenta.item() == 0
     assert torch.equal(out, pend.out)
     assert k == 1 or torch.equal(anillo, anillo2)
     err = ((y - y_ref).abs() / (1 + y_ref.abs())).max().item()

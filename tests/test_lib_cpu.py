@@ -197,13 +197,17 @@ def test_argument_checks_fail_before_any_device_work(lib):
     assert 'null pointer' in _err(lib)
     # the last block's end with the final norm: sizes, the pending block's pointers, its workspace
     assert lib.asrn_block_finish_norm(P1, P1, P1, P1, 4, 1536, P1, P1, 16, 5000, P1, P1, 1e-5, P1, P1, 1 << 30,
-                                      N) != 0
+                                      N, N, N) != 0
     assert 'd=5000' in _err(lib)
-    assert lib.asrn_block_finish_norm(P1, N, P1, P1, 4, 1536, P1, P1, 16, 768, P1, P1, 1e-5, P1, P1, 1 << 30, N) != 0
+    assert lib.asrn_block_finish_norm(P1, N, P1, P1, 4, 1536, P1, P1, 16, 768, P1, P1, 1e-5, P1, P1, 1 << 30, N, N,
+                                      N) != 0
     assert 'null pointer' in _err(lib)
     assert lib.asrn_block_finish_norm(P1, P1, P1, P1, 4, 1536, P1, P1, 16, 768, P1, P1, 1e-5, P1, P1, need - 4,
-                                      N) != 0
+                                      N, N, N) != 0
     assert 'workspace' in _err(lib)
+    assert lib.asrn_block_finish_norm(P1, P1, P1, P1, 4, 1536, P1, P1, 16, 768, P1, P1, 1e-5, P1, P1, 1 << 30, P1,
+                                      N, N) != 0
+    assert 'count' in _err(lib)
 
 
 def test_ops_refuse_cpu_tensors():
